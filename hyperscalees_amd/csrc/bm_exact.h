@@ -1,0 +1,212 @@
+// bm_exact.h -- the noiser's Box-Muller normal, reproduced bit for bit on the GPU.
+//
+// The reference draws each factor entry as (noiser.rs:448-477)
+//     k1, k2 = 24-bit unit indices of two xorshift64 steps
+//     u1 = max(k1 * 2^-24, 1e-9f);  u2 = k2 * 2^-24
+//     n  = sqrtf(-2 * logf(u1)) * cosf(TAU * u2)          (f32 throughout)
+// with logf/cosf from glibc.  glibc's results are not correctly rounded for
+// about 1% of the 2^24 possible inputs, so the device evaluates log and cos in
+// f64 with the table-driven routines below (only IEEE +, *, fma and
+// conversions, so the host compiler and hipcc produce identical bits), rounds
+// to f32, and corrects the inputs where glibc differs with a per-input
+// exception bitmap.  A bitmap word is read only when the f64 result lies close
+// to an f32 rounding midpoint ("danger" test): every glibc exception lies in
+// that zone, and outside it the correctly rounded value is glibc's value.  The
+// host builds the tables and bitmaps (bm_tables.cpp) with this same code, so
+// the danger test agrees bit for bit on host and device.
+//
+// This file is included by host C++ (g++, -ffp-contract=off) and by HIP device
+// code (hipcc, -ffp-contract=off).  Nothing here may depend on a libm routine.
+#pragma once
+#include <stdint.h>
+#include <string.h>
+
+#if defined(__HIPCC__)
+#include <hip/hip_runtime.h>
+#define HSES_HD __host__ __device__ __forceinline__
+#else
+#include <math.h>
+#define HSES_HD inline
+#endif
+
+namespace hses {
+
+// Table sizes.
+constexpr int kLogTab = 128;          // subintervals of the reduced argument z in [0.75, 1.5)
+constexpr int kCosTab = 64;           // angle grid j * 2pi / 64, j = 0..64
+constexpr int kBuckets = 256;         // danger-threshold buckets: k >> 16
+constexpr uint32_t kUnitCount = 1u << 24;
+constexpr uint32_t kBitmapWords = kUnitCount / 32;
+
+// Small per-function tables (copied into LDS by kernels).  All doubles.
+struct BmTables {
+    double log_invc[kLogTab];
+    double log_logc[kLogTab];
+    double cos_c[kCosTab + 1];
+    double cos_s[kCosTab + 1];
+    double cos_thi[kCosTab + 1];
+    double cos_tlo[kCosTab + 1];
+    double log_q[kBuckets];   // danger if |d| >= q * |e|
+    double cos_q[kBuckets];
+    float log_k0;             // glibc logf(1e-9f): the k1 == 0 case (u1 clamped)
+    float pad_[3];
+};
+
+HSES_HD uint32_t f2u(float f) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return __float_as_uint(f);
+#else
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    return u;
+#endif
+}
+HSES_HD float u2f(uint32_t u) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return __uint_as_float(u);
+#else
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+#endif
+}
+
+HSES_HD double hfma(double a, double b, double c) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return __builtin_fma(a, b, c);
+#else
+    return fma(a, b, c);
+#endif
+}
+
+HSES_HD double hrint(double x) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return __builtin_rint(x);
+#else
+    return rint(x);
+#endif
+}
+
+// Constants shared by host and device.
+constexpr double kLn2Hi = 6.93147180369123816490e-01;  // 0x3FE62E42FEE00000, 32 significant bits
+constexpr double kLn2Lo = 1.90821492927058770002e-10;  // 0x3DEA39EF35793C76
+constexpr double kTwoPiInv64 = 10.185916357881301;     // 64 / (2 pi), rounded; only picks the grid point
+constexpr float kTauF = 6.28318530717958647692f;       // std::f32::consts::TAU
+
+// Polynomial coefficients (Taylor, rounded to double).
+constexpr double kL2 = -0.5, kL3 = 1.0 / 3.0, kL4 = -0.25, kL5 = 0.2, kL6 = -1.0 / 6.0,
+                 kL7 = 1.0 / 7.0, kL8 = -0.125;
+constexpr double kC2 = -0.5, kC4 = 1.0 / 24.0, kC6 = -1.0 / 720.0, kC8 = 1.0 / 40320.0;
+constexpr double kS3 = -1.0 / 6.0, kS5 = 1.0 / 120.0, kS7 = -1.0 / 5040.0, kS9 = 1.0 / 362880.0;
+
+// The f32 argument of logf for unit index k1 (k1 == 0 is clamped to 1e-9f).
+HSES_HD float log_arg(uint32_t k1) { return k1 == 0 ? 1e-9f : (float)k1 * 0x1p-24f; }
+
+// f64 evaluation of log(x) for x = log_arg(k1), k1 >= 1 (x in [2^-24, 1)).
+// x = 2^E * z with z in [0.75, 1.5); log x = E ln2 + logc + log1p(z*invc - 1).
+HSES_HD double log_f64(float x, const double* invc_tab, const double* logc_tab) {
+    const uint32_t ix = f2u(x);
+    const uint32_t tmp = ix - 0x3f400000u;  // 0.75f
+    const int32_t E = (int32_t)tmp >> 23;
+    const uint32_t idx = (tmp >> 16) & (kLogTab - 1);
+    const uint32_t iz = ix - ((uint32_t)E << 23);
+    const double z = (double)u2f(iz);
+    const double r = hfma(z, invc_tab[idx], -1.0);
+    double p = hfma(r, kL8, kL7);
+    p = hfma(r, p, kL6);
+    p = hfma(r, p, kL5);
+    p = hfma(r, p, kL4);
+    p = hfma(r, p, kL3);
+    p = hfma(r, p, kL2);
+    const double r2 = r * r;
+    const double lp = hfma(r2, p, r);
+    const double Ed = (double)E;
+    const double hi = hfma(Ed, kLn2Hi, logc_tab[idx]);
+    const double lo = hfma(Ed, kLn2Lo, lp);
+    return hi + lo;
+}
+
+// f64 evaluation of cos(th) for th = TAU * k2 * 2^-24 (th in [0, 2pi)).
+// th = theta_j + t with theta_j = j * 2pi/64; cos th = c_j cos t - s_j sin t.
+HSES_HD double cos_f64(float th, const double* c_tab, const double* s_tab, const double* thi_tab,
+                       const double* tlo_tab) {
+    const double x = (double)th;
+    const int j = (int)hrint(x * kTwoPiInv64);
+    const double t = (x - thi_tab[j]) - tlo_tab[j];
+    const double t2 = t * t;
+    double pc = hfma(t2, kC8, kC6);
+    pc = hfma(t2, pc, kC4);
+    pc = hfma(t2, pc, kC2);
+    const double ct = hfma(t2, pc, 1.0);
+    double ps = hfma(t2, kS9, kS7);
+    ps = hfma(t2, ps, kS5);
+    ps = hfma(t2, ps, kS3);
+    const double st = hfma(t * t2, ps, t);
+    const double sj = s_tab[j] * st;
+    return hfma(c_tab[j], ct, -sj);
+}
+
+// Round y to f32 and report the danger statistics.  Returns the correctly
+// rounded f32; *g receives the neighbour across the nearest rounding midpoint
+// (the only other value glibc can return), and *danger whether y lies within
+// the bucket's midpoint window.
+HSES_HD float round_with_danger(double y, double q, float* g, bool* danger) {
+    const float f = (float)y;
+    const double fd = (double)f;
+    const double d = y - fd;
+    const uint32_t fb = f2u(f);
+    const bool up = d > 0.0;
+    const bool neg = (fb >> 31) != 0;
+    const uint32_t gb = (up != neg) ? fb + 1u : fb - 1u;
+    const float gf = u2f(gb);
+    const double e = (double)gf - fd;
+    *g = gf;
+    *danger = (d != 0.0) && (d < 0.0 ? -d : d) >= q * (e < 0.0 ? -e : e);
+    return f;
+}
+
+// ---------------------------------------------------------------------------
+// Integer stream: noise_seed, xorshift64 and GF(2) jump-ahead.
+// ---------------------------------------------------------------------------
+
+// noiser.rs:495-506; i32 widens with sign extension as Rust's `as u64` does.
+HSES_HD uint64_t noise_seed(uint64_t key, int32_t true_epoch, int32_t true_thread) {
+    uint64_t h = key ^ 0x9E3779B97F4A7C15ull;
+    h *= 0xBF58476D1CE4E5B9ull;
+    h ^= (uint64_t)(int64_t)true_epoch * 0x94D049BB133111EBull;
+    h = ((h << 17) | (h >> 47)) ^ (uint64_t)(int64_t)true_thread;
+    h ^= h >> 33;
+    h *= 0xBF58476D1CE4E5B9ull;
+    h ^= h >> 29;
+    h *= 0x94D049BB133111EBull;
+    h ^= h >> 32;
+    return h;
+}
+
+// noiser.rs:453-460
+HSES_HD uint64_t xs64(uint64_t x) {
+    x ^= x << 13;
+    x ^= x >> 7;
+    x ^= x << 17;
+    return x;
+}
+
+// y = J x over GF(2), J given by its 64 columns (column i = J e_i).
+HSES_HD uint64_t gf2_apply(const uint64_t* cols, uint64_t x) {
+    uint64_t y = 0;
+#if defined(__HIP_DEVICE_COMPILE__)
+#pragma unroll 16
+#endif
+    for (int i = 0; i < 64; ++i) y ^= (0ull - ((x >> i) & 1ull)) & cols[i];
+    return y;
+}
+
+// eggroll.rs:60-65
+HSES_HD void epoch_thread_sign(int32_t epoch, int32_t tid, int32_t noise_reuse, int32_t* te,
+                               int32_t* tt, float* sign) {
+    *te = noise_reuse == 0 ? 0 : epoch / noise_reuse;
+    *tt = tid / 2;
+    *sign = (tid % 2 == 0) ? 1.0f : -1.0f;
+}
+
+}  // namespace hses

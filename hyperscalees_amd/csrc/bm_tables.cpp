@@ -1,0 +1,218 @@
+// bm_tables.cpp -- host construction of the exact Box-Muller tables.
+//
+// The device evaluates log/cos with the f64 routines of bm_exact.h and needs:
+//   * the small interpolation tables (log: 1/c and -log(1/c) per subinterval;
+//     cos: cos, sin and a two-part angle per grid point);
+//   * per-input exception bitmaps: bit k is set where glibc's logf/cosf differ
+//     from the f32 rounding of the f64 routine;
+//   * per-bucket danger coefficients q so that every exception satisfies the
+//     danger predicate of round_with_danger().
+// glibc is the parity target because the reference's f32::ln / f32::cos lower
+// to glibc logf / cosf on linux-gnu (noiser.rs:470-477).
+#include <math.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cstdio>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "runtime.h"
+
+namespace hses {
+
+namespace {
+
+void build_small(BmTables* t) {
+    // log: 128 subintervals of the bit window [0.75f, 1.5f).
+    for (int i = 0; i < kLogTab; ++i) {
+        long double lo, w;
+        if (i < 64) {
+            lo = 0.75L + (long double)i * 0x1p-8L;
+            w = 0x1p-8L;
+        } else {
+            lo = 1.0L + (long double)(i - 64) * 0x1p-7L;
+            w = 0x1p-7L;
+        }
+        if (i == 63 || i == 64) {
+            // z - 1 is exact next to 1: keep the full relative precision of log1p.
+            t->log_invc[i] = 1.0;
+            t->log_logc[i] = 0.0;
+            continue;
+        }
+        const long double c = lo + w / 2;
+        const double invc = (double)(1.0L / c);
+        t->log_invc[i] = invc;
+        t->log_logc[i] = (double)(-logl((long double)invc));
+    }
+    // cos: grid theta_j = j * 2pi / 64 with exact values at the quadrant points.
+    const long double pi = 3.141592653589793238462643383279502884L;
+    for (int j = 0; j <= kCosTab; ++j) {
+        const long double th = (long double)j * 2.0L * pi / (long double)kCosTab;
+        const double hi = (double)th;
+        t->cos_thi[j] = hi;
+        t->cos_tlo[j] = (double)(th - (long double)hi);
+        double c = (double)cosl(th), s = (double)sinl(th);
+        switch (j) {
+            case 0: c = 1.0; s = 0.0; break;
+            case 16: c = 0.0; s = 1.0; break;
+            case 32: c = -1.0; s = 0.0; break;
+            case 48: c = 0.0; s = -1.0; break;
+            case 64: c = 1.0; s = 0.0; break;
+            default: break;
+        }
+        t->cos_c[j] = c;
+        t->cos_s[j] = s;
+    }
+    t->log_k0 = logf(1e-9f);
+    t->pad_[0] = t->pad_[1] = t->pad_[2] = 0.0f;
+}
+
+struct Exc {
+    uint32_t k;
+    double ratio;  // |d| / |e|
+};
+
+// Evaluate one function over a slice of unit indices.  kind 0 = log, 1 = cos.
+void scan_slice(const BmTables* t, int kind, uint32_t k_lo, uint32_t k_hi, std::vector<Exc>* exc,
+                std::string* err) {
+    for (uint32_t k = k_lo; k < k_hi; ++k) {
+        double y;
+        float ref;
+        if (kind == 0) {
+            if (k == 0) continue;  // clamped argument: handled by log_k0
+            const float x = log_arg(k);
+            y = log_f64(x, t->log_invc, t->log_logc);
+            ref = logf(x);
+        } else {
+            const float th = kTauF * ((float)k * 0x1p-24f);
+            y = cos_f64(th, t->cos_c, t->cos_s, t->cos_thi, t->cos_tlo);
+            ref = cosf(th);
+        }
+        float g;
+        bool danger;
+        const float f = round_with_danger(y, 2.0, &g, &danger);
+        if (f2u(ref) == f2u(f)) continue;
+        if (f2u(ref) != f2u(g)) {
+            char buf[160];
+            snprintf(buf, sizeof buf,
+                     "%s exception at k=%u is not the midpoint neighbour (ref %a, f %a, g %a)",
+                     kind == 0 ? "log" : "cos", k, (double)ref, (double)f, (double)g);
+            *err = buf;
+            return;
+        }
+        const double fd = (double)f;
+        const double d = y - fd;
+        const double e = (double)g - fd;
+        if (d == 0.0) {
+            *err = "exception on an exactly representable f64 value";
+            return;
+        }
+        exc->push_back({k, (d < 0 ? -d : d) / (e < 0 ? -e : e)});
+    }
+}
+
+// Largest q such that the danger predicate holds for every exception of a bucket.
+double bucket_q(const BmTables* t, int kind, const std::vector<Exc>& exc_in_bucket) {
+    if (exc_in_bucket.empty()) return 2.0;  // never dangerous: ratio <= 0.5
+    double q = 2.0;
+    for (const Exc& x : exc_in_bucket) q = std::min(q, x.ratio);
+    // Step down until the exact predicate (as the device evaluates it) holds.
+    for (int it = 0; it < 64; ++it) {
+        bool ok = true;
+        for (const Exc& x : exc_in_bucket) {
+            double y;
+            if (kind == 0) {
+                y = log_f64(log_arg(x.k), t->log_invc, t->log_logc);
+            } else {
+                y = cos_f64(kTauF * ((float)x.k * 0x1p-24f), t->cos_c, t->cos_s, t->cos_thi,
+                            t->cos_tlo);
+            }
+            float g;
+            bool danger;
+            round_with_danger(y, q, &g, &danger);
+            if (!danger) {
+                ok = false;
+                break;
+            }
+        }
+        if (ok) return q;
+        q = nextafter(q, 0.0);
+        q = q * (1.0 - 1e-12);
+    }
+    return 0.0;  // always dangerous: still correct, only slower
+}
+
+}  // namespace
+
+std::string build_bm_tables(HostBmTables* out, int nthreads) {
+    build_small(&out->small);
+    out->log_exc.assign(kBitmapWords, 0u);
+    out->cos_exc.assign(kBitmapWords, 0u);
+    if (nthreads < 1) nthreads = 1;
+    for (int kind = 0; kind < 2; ++kind) {
+        std::vector<std::vector<Exc>> parts(nthreads);
+        std::vector<std::string> errs(nthreads);
+        std::vector<std::thread> th;
+        const uint32_t per = (kUnitCount + nthreads - 1) / nthreads;
+        for (int i = 0; i < nthreads; ++i) {
+            const uint32_t lo = std::min<uint64_t>((uint64_t)i * per, kUnitCount);
+            const uint32_t hi = std::min<uint64_t>((uint64_t)(i + 1) * per, kUnitCount);
+            th.emplace_back(scan_slice, &out->small, kind, lo, hi, &parts[i], &errs[i]);
+        }
+        for (auto& x : th) x.join();
+        for (auto& e : errs)
+            if (!e.empty()) return e;
+        std::vector<std::vector<Exc>> by_bucket(kBuckets);
+        uint32_t n = 0;
+        std::vector<uint32_t>& bm = kind == 0 ? out->log_exc : out->cos_exc;
+        for (auto& p : parts)
+            for (const Exc& x : p) {
+                bm[x.k >> 5] |= 1u << (x.k & 31);
+                by_bucket[x.k >> 16].push_back(x);
+                ++n;
+            }
+        double* q = kind == 0 ? out->small.log_q : out->small.cos_q;
+        for (int b = 0; b < kBuckets; ++b) q[b] = bucket_q(&out->small, kind, by_bucket[b]);
+        if (kind == 0)
+            out->n_log_exc = n;
+        else
+            out->n_cos_exc = n;
+    }
+    return std::string();
+}
+
+// ---------------------------------------------------------------------------
+// GF(2) matrices for xorshift64 jump-ahead.
+// ---------------------------------------------------------------------------
+
+Gf2 gf2_identity() {
+    Gf2 m;
+    for (int i = 0; i < 64; ++i) m.c[i] = 1ull << i;
+    return m;
+}
+
+Gf2 gf2_step() {
+    Gf2 m;
+    for (int i = 0; i < 64; ++i) m.c[i] = xs64(1ull << i);
+    return m;
+}
+
+Gf2 gf2_mul(const Gf2& A, const Gf2& B) {
+    Gf2 C;
+    for (int i = 0; i < 64; ++i) C.c[i] = gf2_apply(A.c, B.c[i]);
+    return C;
+}
+
+Gf2 gf2_pow(const Gf2& M, uint64_t n) {
+    Gf2 r = gf2_identity(), b = M;
+    while (n) {
+        if (n & 1) r = gf2_mul(r, b);
+        b = gf2_mul(b, b);
+        n >>= 1;
+    }
+    return r;
+}
+
+}  // namespace hses

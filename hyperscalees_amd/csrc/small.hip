@@ -1,0 +1,151 @@
+// small.hip -- fitness, fitness normalisation and the optimizer step.
+#include <math.h>
+
+#include "runtime.h"
+
+namespace hses {
+
+// snn_mnist.rs:180-201 (Loglik) per row, averaged over the member's rows.
+__global__ void k_member_loglik(const float* __restrict__ logits, int32_t classes,
+                                const int32_t* __restrict__ labels, int32_t n, int32_t rpm,
+                                float* __restrict__ fit) {
+    const int32_t m = blockIdx.x * blockDim.x + threadIdx.x;
+    if (m >= n) return;
+    double acc = 0.0;
+    for (int32_t s = 0; s < rpm; ++s) {
+        const int64_t row = (int64_t)m * rpm + s;
+        const float* x = logits + row * classes;
+        float mx = x[0];
+        for (int32_t c = 1; c < classes; ++c) mx = fmaxf(mx, x[c]);
+        float sum = 0.0f;
+        for (int32_t c = 0; c < classes; ++c) sum = __fadd_rn(sum, expf(__fsub_rn(x[c], mx)));
+        int32_t lab = labels[row];
+        lab = lab < 0 ? 0 : (lab >= classes ? classes - 1 : lab);
+        acc += (double)__fsub_rn(__fsub_rn(x[lab], mx), logf(sum));
+    }
+    fit[m] = (float)(acc / rpm);
+}
+
+// eggroll.rs:967-992: mean and E[x^2] over all n (double partial sums with a
+// fixed-order tree, one block), std = sqrt(var + 1e-5), out = (raw-mean)/std
+// or per-group centring with the global std.
+__global__ __launch_bounds__(1024) void k_convert_fitnesses(const float* __restrict__ raw,
+                                                           int32_t n, int32_t group,
+                                                           float* __restrict__ out,
+                                                           float* __restrict__ stats) {
+    __shared__ double s1[1024], s2[1024];
+    double a = 0.0, b = 0.0;
+    for (int32_t i = threadIdx.x; i < n; i += blockDim.x) {
+        const float v = raw[i];
+        a += (double)v;
+        b += (double)__fmul_rn(v, v);
+    }
+    s1[threadIdx.x] = a;
+    s2[threadIdx.x] = b;
+    __syncthreads();
+    for (int32_t w = blockDim.x / 2; w > 0; w >>= 1) {
+        if ((int32_t)threadIdx.x < w) {
+            s1[threadIdx.x] += s1[threadIdx.x + w];
+            s2[threadIdx.x] += s2[threadIdx.x + w];
+        }
+        __syncthreads();
+    }
+    const float mean = (float)(s1[0] / n);
+    const float msq = (float)(s2[0] / n);
+    const float var = __fsub_rn(msq, __fmul_rn(mean, mean));
+    const float sd = __fsqrt_rn(__fadd_rn(var, 1e-5f));
+    const float inv = __fdiv_rn(1.0f, sd);
+    if (threadIdx.x == 0 && stats) {
+        stats[0] = mean;
+        stats[1] = sd;
+    }
+    if (group <= 0) {
+        for (int32_t i = threadIdx.x; i < n; i += blockDim.x)
+            out[i] = __fmul_rn(__fadd_rn(raw[i], -mean), inv);
+    } else {
+        const int32_t groups = n / group;
+        for (int32_t gi = threadIdx.x; gi < groups; gi += blockDim.x) {
+            double gs = 0.0;
+            for (int32_t j = 0; j < group; ++j) gs += (double)raw[gi * group + j];
+            const float gm = (float)(gs / group);
+            for (int32_t j = 0; j < group; ++j)
+                out[gi * group + j] = __fmul_rn(__fsub_rn(raw[gi * group + j], gm), inv);
+        }
+    }
+}
+
+// noiser.rs:155-225.  kind 0: p - g*lr.  Adam/AdamW: moments, bias correction
+// (inverse factors precomputed on the host), p + (m_hat/(sqrt(v_hat)+eps))*(-lr)
+// (+ p*wd for AdamW, no lr factor, as the reference).
+__global__ void k_solver(int32_t kind, float lr, float b1, float omb1, float b2, float omb2,
+                         float eps, float wd, float i1, float i2, float* __restrict__ p,
+                         const float* __restrict__ g, float* __restrict__ m, float* __restrict__ v,
+                         int64_t len) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= len) return;
+    const float pv = p[e], gv = g[e];
+    if (kind == HSES_SGD) {
+        p[e] = __fsub_rn(pv, __fmul_rn(gv, lr));
+        return;
+    }
+    const float mn = __fadd_rn(__fmul_rn(m[e], b1), __fmul_rn(gv, omb1));
+    const float vn = __fadd_rn(__fmul_rn(v[e], b2), __fmul_rn(__fmul_rn(gv, gv), omb2));
+    m[e] = mn;
+    v[e] = vn;
+    const float mh = __fmul_rn(mn, i1), vh = __fmul_rn(vn, i2);
+    const float denom = __fadd_rn(__fsqrt_rn(vh), eps);
+    const float at = __fmul_rn(__fdiv_rn(mh, denom), -lr);
+    p[e] = (kind == HSES_ADAMW && wd != 0.0f) ? __fadd_rn(__fadd_rn(pv, at), __fmul_rn(pv, wd))
+                                               : __fadd_rn(pv, at);
+}
+
+}  // namespace hses
+
+using namespace hses;
+
+extern "C" int hses_member_loglik(const float* d_logits, int32_t classes, const int32_t* d_labels,
+                                  int32_t n, int32_t rows_per_member, float* d_fit, void* stream) {
+    HSES_REQUIRE(n >= 0 && classes >= 1 && rows_per_member >= 1, "bad sizes");
+    if (n == 0) return HSES_OK;
+    HSES_REQUIRE(d_logits && d_labels && d_fit, "NULL pointer");
+    hipLaunchKernelGGL(k_member_loglik, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream,
+                       d_logits, classes, d_labels, n, rows_per_member, d_fit);
+    HSES_CHECK_HIP(hipGetLastError());
+    return HSES_OK;
+}
+
+extern "C" int hses_convert_fitnesses(const float* d_raw, int32_t n, int32_t group_size,
+                                      float* d_out, float* d_stats, void* stream) {
+    HSES_REQUIRE(n >= 1, "n must be >= 1");
+    HSES_REQUIRE(d_raw && d_out, "NULL pointer");
+    HSES_REQUIRE(group_size >= 0, "group_size must be >= 0");
+    HSES_REQUIRE(group_size == 0 || n % group_size == 0, "n must be a multiple of group_size");
+    hipLaunchKernelGGL(k_convert_fitnesses, dim3(1), dim3(1024), 0, (hipStream_t)stream, d_raw, n,
+                       group_size, d_out, d_stats);
+    HSES_CHECK_HIP(hipGetLastError());
+    return HSES_OK;
+}
+
+extern "C" int hses_solver_step(int32_t kind, float lr, float beta1, float beta2, float eps,
+                                float wd, int32_t step_t, float* d_param, const float* d_grad,
+                                float* d_m, float* d_v, int64_t len, void* stream) {
+    HSES_REQUIRE(kind >= HSES_SGD && kind <= HSES_ADAMW, "unknown solver");
+    HSES_REQUIRE(len >= 0, "negative length");
+    if (len == 0) return HSES_OK;
+    HSES_REQUIRE(d_param && d_grad, "NULL pointer");
+    float i1 = 1.0f, i2 = 1.0f;
+    if (kind != HSES_SGD) {
+        HSES_REQUIRE(d_m && d_v, "Adam moments are NULL");
+        HSES_REQUIRE(step_t >= 1, "step_t must be >= 1 for Adam");
+        const float t = (float)step_t;
+        i1 = 1.0f / (1.0f - powf(beta1, t));
+        i2 = 1.0f / (1.0f - powf(beta2, t));
+    }
+    const int64_t blocks = (len + 255) / 256;
+    HSES_REQUIRE(blocks < (1ll << 31), "grid too large");
+    hipLaunchKernelGGL(k_solver, dim3(blocks), dim3(256), 0, (hipStream_t)stream, kind, lr, beta1,
+                       1.0f - beta1, beta2, 1.0f - beta2, eps, wd, i1, i2, d_param, d_grad, d_m,
+                       d_v, len);
+    HSES_CHECK_HIP(hipGetLastError());
+    return HSES_OK;
+}

@@ -1,0 +1,177 @@
+"""Torch-tensor wrappers over the libhses entry points.
+
+PyTorch supplies device memory and the current stream; every computation runs
+in libhses.so.  Each wrapper validates that its tensors are contiguous device
+tensors of the expected dtype before calling the C ABI.
+"""
+import ctypes
+
+import torch
+
+from . import _lib
+from ._lib import FMT_BF16, FMT_BITS, FMT_F32, FMT_U8, MATH_BF16, MATH_F32  # noqa: F401
+
+_FMT_DTYPE = {FMT_F32: torch.float32, FMT_BF16: torch.bfloat16, FMT_U8: torch.uint8,
+              FMT_BITS: torch.int64}
+
+
+def _p(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _dev(t, dtype, name):
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor")
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    return t
+
+
+def fmt_width(fmt, width):
+    """Storage units per row of `width` activations in format `fmt`."""
+    return (width + 63) // 64 if fmt == FMT_BITS else width
+
+
+def init(device=0):
+    _lib.call("hses_init", device)
+
+
+def bm_stats():
+    out = (ctypes.c_uint32 * 2)()
+    _lib.call("hses_bm_stats", out)
+    return int(out[0]), int(out[1])
+
+
+def noise_seed(key, true_epoch, true_thread):
+    return int(_lib.load().hses_noise_seed(key & (2**64 - 1), true_epoch, true_thread))
+
+
+def bm_eval(k_lo, n, device="cuda"):
+    """Device Box-Muller halves for unit indices [k_lo, k_lo+n)."""
+    lg = torch.empty(n, dtype=torch.float32, device=device)
+    rad = torch.empty_like(lg)
+    cs = torch.empty_like(lg)
+    _lib.call("hses_bm_eval", k_lo, n, _p(lg), _p(rad), _p(cs), _stream())
+    return lg, rad, cs
+
+
+def lora_factors(base_sigma, key, rank, epoch, noise_reuse, tids, a, b, device="cuda"):
+    """batched_lora_noise: tids is an int tensor/sequence or (tid_lo, n)."""
+    if isinstance(tids, tuple):
+        tid_lo, n = tids
+        d_tids = None
+    else:
+        d_tids = torch.as_tensor(tids, dtype=torch.int32, device=device).contiguous()
+        tid_lo, n = 0, d_tids.numel()
+    A = torch.empty((n, a, rank), dtype=torch.float32, device=device)
+    B = torch.empty((n, b, rank), dtype=torch.float32, device=device)
+    _lib.call("hses_lora_factors", base_sigma, key & (2**64 - 1), rank, epoch, noise_reuse,
+              tid_lo, _p(d_tids), n, a, b, _p(A), _p(B), _stream())
+    return A, B
+
+
+def nonlora_noise(base_sigma, key, epoch, noise_reuse, tids, a, b, device="cuda"):
+    if isinstance(tids, tuple):
+        tid_lo, n = tids
+        d_tids = None
+    else:
+        d_tids = torch.as_tensor(tids, dtype=torch.int32, device=device).contiguous()
+        tid_lo, n = 0, d_tids.numel()
+    out = torch.empty((n, a, b), dtype=torch.float32, device=device)
+    _lib.call("hses_nonlora_noise", base_sigma, key & (2**64 - 1), epoch, noise_reuse, tid_lo,
+              _p(d_tids), n, a, b, _p(out), _stream())
+    return out
+
+
+def poisson_encode(p, T, seeds=(0, 0, 0, 0), fmt=FMT_F32, out=None):
+    """(rows, in_dim) probabilities -> (T, rows, width) spikes in `fmt`."""
+    _dev(p, torch.float32, "p")
+    rows, in_dim = p.shape
+    units = fmt_width(fmt, in_dim)
+    if out is None:
+        out = torch.empty((T, rows, units), dtype=_FMT_DTYPE[fmt], device=p.device)
+    s0, s1, s2, s3 = (int(s) & 0xFFFFFFFF for s in seeds)
+    _lib.call("hses_poisson_encode", _p(p), rows, in_dim, in_dim, T, s0, s1, s2, s3, _p(out),
+              fmt, units, _stream())
+    return out
+
+
+def lif_scan(cur, tau_m, v_th, v0=None, fmt=FMT_F32, want_v=False):
+    """cur (T, rows, h) fp32 -> spikes (T, rows, width) in `fmt` [, v_final (rows, h)]."""
+    _dev(cur, torch.float32, "cur")
+    T, rows, h = cur.shape
+    if v0 is not None:
+        _dev(v0, torch.float32, "v0")
+    units = fmt_width(fmt, h)
+    spk = torch.empty((T, rows, units), dtype=_FMT_DTYPE[fmt], device=cur.device)
+    v_out = torch.empty((rows, h), dtype=torch.float32, device=cur.device) if want_v else None
+    _lib.call("hses_lif_scan", _p(cur), _p(v0), T, rows, h, h, tau_m, v_th, _p(spk), fmt, units,
+              _p(v_out), _stream())
+    return (spk, v_out) if want_v else spk
+
+
+def perturbed_linear(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n, rows_per_member,
+                     x_fmt=FMT_F32, x_width=None, n_time=1, math=MATH_F32, out=None):
+    """Batched do_mm.  x is (n_time, n*rows_per_member, units) in x_fmt (or 2-D
+    when n_time == 1); returns y (n_time, n*rows_per_member, a) fp32."""
+    a, b = W.shape
+    _dev(W, torch.float32, "W")
+    _dev(x, _FMT_DTYPE[x_fmt], "x")
+    units = fmt_width(x_fmt, b)
+    M = n * rows_per_member
+    if x.shape[-1] != units or x.numel() != n_time * M * units:
+        raise ValueError(f"x has shape {tuple(x.shape)}, expected ({n_time}, {M}, {units})")
+    if out is None:
+        out = torch.empty((n_time, M, a), dtype=torch.float32, device=W.device)
+    _lib.call("hses_perturbed_linear", _p(x), x_fmt, units, M * units, n_time, _p(W), a, b,
+              key & (2**64 - 1), rank, sigma, epoch, noise_reuse, tid_lo, n, rows_per_member,
+              _p(out), a, M * a, math, _stream())
+    return out if n_time > 1 or x.dim() == 3 else out[0]
+
+
+def es_update(fit, tid_lo, key, rank, sigma, epoch, noise_reuse, a, b, scale, out=None):
+    """scale * sum_m fit[m] A_m B_m^T (factors regenerated in-kernel)."""
+    _dev(fit, torch.float32, "fit")
+    n = fit.numel()
+    lib = _lib.load()
+    wbytes = lib.hses_es_update_workspace(a, b, rank, n)
+    work = torch.empty(max(int(wbytes), 1), dtype=torch.uint8, device=fit.device)
+    if out is None:
+        out = torch.empty((a, b), dtype=torch.float32, device=fit.device)
+    _lib.call("hses_es_update", _p(fit), n, tid_lo, key & (2**64 - 1), rank, sigma, epoch,
+              noise_reuse, a, b, scale, _p(out), _p(work), int(wbytes), _stream())
+    return out
+
+
+def member_loglik(logits, labels, n, rows_per_member):
+    _dev(logits, torch.float32, "logits")
+    _dev(labels, torch.int32, "labels")
+    fit = torch.empty(n, dtype=torch.float32, device=logits.device)
+    _lib.call("hses_member_loglik", _p(logits), logits.shape[-1], _p(labels), n, rows_per_member,
+              _p(fit), _stream())
+    return fit
+
+
+def convert_fitnesses(raw, group_size=0):
+    _dev(raw, torch.float32, "raw")
+    out = torch.empty_like(raw)
+    stats = torch.empty(2, dtype=torch.float32, device=raw.device)
+    _lib.call("hses_convert_fitnesses", _p(raw), raw.numel(), group_size, _p(out), _p(stats),
+              _stream())
+    return out, stats
+
+
+def solver_step(kind, lr, param, grad, m=None, v=None, step_t=1, beta1=0.9, beta2=0.999,
+                eps=1e-8, wd=0.0):
+    """In-place Solver::update of one parameter tensor."""
+    _dev(param, torch.float32, "param")
+    _dev(grad, torch.float32, "grad")
+    _lib.call("hses_solver_step", kind, lr, beta1, beta2, eps, wd, step_t, _p(param), _p(grad),
+              _p(m), _p(v), param.numel(), _stream())
+    return param

@@ -1,0 +1,168 @@
+/*
+ * hses.h -- C ABI of the MI355X-native EggRoll hot path (libhses.so).
+ *
+ * Each entry point replaces one function of the reference's Rust surface
+ * (hyperscalees-noiser / hyperscalees-kernels / the oxide launch layer);
+ * the reference function is cited next to it (paths relative to the
+ * reference repository root).  Conventions:
+ *   - every call returns an hses_status; on failure hses_last_error() holds a
+ *     message (thread-local).  Arguments are validated before any launch, so
+ *     a rejected call has no side effect;
+ *   - pointers named d_* are device pointers the caller owns; nothing is
+ *     allocated per call except where a function says so;
+ *   - `stream` is a hipStream_t passed as void* (NULL = default stream); all
+ *     work is enqueued on it asynchronously, as the oxide launch layer
+ *     enqueues on the cubecl stream (burn_impl/hyperscalees/src/oxide.rs:105-146);
+ *   - results do not depend on the launch configuration.
+ */
+#ifndef HSES_H
+#define HSES_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    HSES_OK = 0,
+    HSES_ERR_INVALID_ARG = 1,
+    HSES_ERR_UNSUPPORTED = 2,
+    HSES_ERR_HIP = 3,
+    HSES_ERR_INTERNAL = 4
+} hses_status;
+
+/* Spike/activation storage formats. */
+typedef enum {
+    HSES_FMT_F32 = 0,  /* 0.0f / 1.0f, the reference's layout                  */
+    HSES_FMT_BF16 = 1, /* 0 / 1 as bfloat16                                      */
+    HSES_FMT_U8 = 2,   /* 0 / 1 bytes                                            */
+    HSES_FMT_BITS = 3  /* bit-packed: a row is ceil(width/64) uint64 words, bit  */
+                       /* c%64 of word c/64 is column c; pad bits are zero       */
+} hses_fmt;
+
+/* Arithmetic of the perturbed matrix products. */
+typedef enum {
+    HSES_MATH_F32 = 0, /* fp32 MFMA, fp32 operands                               */
+    HSES_MATH_BF16 = 1 /* bf16 MFMA (operands rounded to bf16), fp32 accumulate  */
+} hses_math;
+
+/* Solver kinds (burn_impl/hyperscalees-noiser/src/noiser.rs:43-92). */
+typedef enum { HSES_SGD = 0, HSES_ADAM = 1, HSES_ADAMW = 2 } hses_solver;
+
+/* ---- runtime ---------------------------------------------------------- */
+
+/* Initialise device `device` (builds the Box-Muller correction tables and
+ * uploads them).  Called implicitly by the first launch on a device. */
+int hses_init(int device);
+/* Copies the last error message of this thread into buf (NUL-terminated). */
+int hses_last_error(char *buf, size_t len);
+const char *hses_version(void);
+/* Statistics of the Box-Muller correction tables of the current device:
+ * out[0]=#logf exceptions, out[1]=#cosf exceptions. */
+int hses_bm_stats(uint32_t out[2]);
+
+/* ---- noise stream ---------------------------------------------------- */
+
+/* noise_seed (burn_impl/hyperscalees-noiser/src/noiser.rs:495-506).  Host only. */
+uint64_t hses_noise_seed(uint64_t key, int32_t true_epoch, int32_t true_thread);
+
+/* Exhaustive evaluation of the device Box-Muller halves for unit indices
+ * [k_lo, k_lo+n): d_log[i] = logf(max(k*2^-24,1e-9)), d_radius[i] =
+ * sqrtf(-2*d_log[i]), d_cos[i] = cosf(TAU*k*2^-24) (noiser.rs:470-477).
+ * Any output may be NULL.  Test entry point. */
+int hses_bm_eval(uint32_t k_lo, uint32_t n, float *d_log, float *d_radius, float *d_cos,
+                 void *stream);
+
+/* batched_lora_noise (burn_impl/hyperscalees-noiser/src/eggroll.rs:116-227):
+ * member i has thread id tids[i] (device array) or, if d_tids is NULL,
+ * tid_lo + i.  Writes A (n,a,r) = sign*base_sigma*normals rows [b,a+b) and
+ * B (n,b,r) = normals rows [0,b) of the member's stream, bit-exact. */
+int hses_lora_factors(float base_sigma, uint64_t key, int32_t rank, int32_t epoch,
+                      int32_t noise_reuse, int32_t tid_lo, const int32_t *d_tids, int32_t n,
+                      int32_t a, int32_t b, float *d_A, float *d_B, void *stream);
+
+/* get_nonlora_update_params (eggroll.rs:312-324) for n members:
+ * d_out (n, a, b) = sign*base_sigma*normals, bit-exact. */
+int hses_nonlora_noise(float base_sigma, uint64_t key, int32_t epoch, int32_t noise_reuse,
+                       int32_t tid_lo, const int32_t *d_tids, int32_t n, int32_t a, int32_t b,
+                       float *d_out, void *stream);
+
+/* ---- spiking kernels ------------------------------------------------- */
+
+/* poisson_encode_fused (burn_impl/hyperscalees-kernels/src/poisson_encode_fused_oxide.rs:61-106,
+ * host wrapper burn_impl/hyperscalees/src/oxide.rs:573-625) for any T >= 1:
+ * spike[t][row][col] = u_t < p[row][col], u from the per-element xorshift32
+ * stream.  p rows are p_stride floats apart; output rows are out_stride
+ * elements apart (words for HSES_FMT_BITS); time planes are rows*out_stride
+ * apart. */
+int hses_poisson_encode(const float *d_p, int64_t rows, int32_t in_dim, int64_t p_stride,
+                        int32_t T, uint32_t s0, uint32_t s1, uint32_t s2, uint32_t s3,
+                        void *d_out, int32_t fmt, int64_t out_stride, void *stream);
+
+/* run_lif (burn_impl/hyperscalees-models/src/snn.rs:53-97) / lif_fused
+ * (burn_impl/hyperscalees-kernels/src/lif_fused_oxide.rs:37-70, host oxide.rs:489-543):
+ * cur (T, rows, h) fp32 with row stride cur_stride; v0 (rows, h) or NULL (zeros);
+ * spikes (T, rows, h) in `fmt` with row stride spk_stride; optional final
+ * membrane d_v_out (rows, h) with row stride h. */
+int hses_lif_scan(const float *d_cur, const float *d_v0, int32_t T, int64_t rows, int32_t h,
+                  int64_t cur_stride, float tau_m, float v_th, void *d_spikes, int32_t fmt,
+                  int64_t spk_stride, float *d_v_out, void *stream);
+
+/* ---- perturbed forward ----------------------------------------------- */
+
+/* Batched EggRoll do_mm (eggroll.rs:419-446; batched form snn.rs:665-685):
+ * for member m (thread id tid_lo+m) and each of its `rows_per_member` rows,
+ *     y = x W^T + (x B_m) A_m^T,   (A_m, B_m) = get_lora_update_params(...)
+ * generated in-kernel.  x is (n*rows_per_member, b) in x_fmt (F32, BF16 or
+ * BITS) with row stride x_stride (elements, or words for BITS); W (a, b)
+ * fp32 row-major; y (n*rows_per_member, a) fp32 with row stride y_stride.
+ * Member m's rows are rows [m*rows_per_member, (m+1)*rows_per_member); for
+ * time-major activations (T, M, b) pass rows_per_member = slots and
+ * n_time = T with plane strides x_plane / y_plane (rows of member m at time
+ * t are t*plane + m*slots + s).  sigma=0 or rank=0 gives the clean x W^T. */
+int hses_perturbed_linear(const void *d_x, int32_t x_fmt, int64_t x_stride, int64_t x_plane,
+                          int32_t n_time, const float *d_W, int32_t a, int32_t b,
+                          uint64_t key, int32_t rank, float sigma, int32_t epoch,
+                          int32_t noise_reuse, int32_t tid_lo, int32_t n, int32_t rows_per_member,
+                          float *d_y, int64_t y_stride, int64_t y_plane, int32_t math,
+                          void *stream);
+
+/* ---- ES update ------------------------------------------------------- */
+
+/* EggRoll ES gradient of one MM parameter (eggroll.rs:353-404 _simple_lora_update +
+ * _do_update; chunked form eggroll.rs:579-702; pair einsum eggroll.rs:778-915):
+ *     d_grad (a, b) = scale * sum_m f[m] * A_m B_m^T
+ * over members m in [0, n) with thread ids tid_lo+m, factors regenerated
+ * in-kernel.  do_updates uses scale = -sqrt(N)/N (N = population size).
+ * Deterministic: a fixed split-K partition and a fixed-order second-stage
+ * reduction, no atomics.  d_work must hold hses_es_update_workspace(...)
+ * bytes. */
+size_t hses_es_update_workspace(int32_t a, int32_t b, int32_t rank, int32_t n);
+int hses_es_update(const float *d_f, int32_t n, int32_t tid_lo, uint64_t key, int32_t rank,
+                   float sigma, int32_t epoch, int32_t noise_reuse, int32_t a, int32_t b,
+                   float scale, float *d_grad, void *d_work, size_t work_bytes, void *stream);
+
+/* ---- fitness, z-score, solver ----------------------------------------- */
+
+/* fitness_from_logits_reward(Loglik) (burn_impl/hyperscalees-envs/src/snn_mnist.rs:180-201)
+ * averaged over each member's rows: d_fit[m] = mean_s log_softmax(logits[m*rows+s])[label]. */
+int hses_member_loglik(const float *d_logits, int32_t classes, const int32_t *d_labels,
+                       int32_t n, int32_t rows_per_member, float *d_fit, void *stream);
+
+/* convert_fitnesses (eggroll.rs:967-992): global (group_size 0) or per-group
+ * z-score with the global std.  d_stats (optional) receives {mean, std}. */
+int hses_convert_fitnesses(const float *d_raw, int32_t n, int32_t group_size, float *d_out,
+                           float *d_stats, void *stream);
+
+/* Solver::update for one parameter (noiser.rs:155-225).  step_t is the
+ * already-incremented global step.  m, v are updated in place (ignored for SGD). */
+int hses_solver_step(int32_t kind, float lr, float beta1, float beta2, float eps, float wd,
+                     int32_t step_t, float *d_param, const float *d_grad, float *d_m, float *d_v,
+                     int64_t len, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

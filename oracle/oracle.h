@@ -1,0 +1,159 @@
+/*
+ * oracle.h -- CPU restatement of the reference's EggRoll SNN hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load this library, and only as the checker
+ * (or as the timed CPU baseline).  The product path (hyperscalees_amd) never
+ * links, loads or calls it.
+ *
+ * Every function restates a reference function in plain C; the reference
+ * file:line it follows is cited next to it (paths relative to the reference
+ * repository root).  Numeric rules (same as the reference CPU backend):
+ *   - f32 everywhere the reference uses f32;
+ *   - glibc logf/cosf and IEEE sqrtf for Box-Muller (Rust f32::ln / f32::cos
+ *     lower to libm on linux-gnu);
+ *   - no FMA contraction (the library is compiled with -ffp-contract=off);
+ *   - matrix products accumulate in f32 in ascending-k order, one rounding per
+ *     tensor the reference materialises (x@W^T, x@B, (x@B)@A^T, base+noise).
+ *     Functions whose name ends in _f64 accumulate in double instead and are
+ *     the "reference of the reference" used for tolerance checks.
+ *
+ * Pinning status of each function is listed in oracle/README.md.
+ */
+#ifndef HSES_ORACLE_H
+#define HSES_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- noise stream (burn_impl/hyperscalees-noiser/src/noiser.rs:437-506) ---- */
+uint64_t or_noise_seed(uint64_t key, int32_t true_epoch, int32_t true_thread);
+void or_epoch_thread_sign(int32_t epoch, int32_t thread_id, int32_t noise_reuse,
+                          int32_t *true_epoch, int32_t *true_thread, float *sign);
+uint64_t or_xorshift64_step(uint64_t x);
+/* Fill out[0..n) with the DeterministicNoise::standard_normal stream of `seed`. */
+void or_standard_normals(uint64_t seed, float *out, int64_t n);
+/* The two factors of one Box-Muller draw for a 24-bit unit index k. */
+float or_bm_radius(uint32_t k1);
+float or_bm_cos(uint32_t k2);
+float or_unit_from_u64(uint64_t x);
+/* Bulk evaluation over unit indices [k_lo, k_lo+n): logf(u1), radius, cos (checker for the
+ * exhaustive device test). */
+void or_bm_eval(uint32_t k_lo, uint32_t n, float *lg, float *rad, float *cs);
+
+/* ---- EggRoll factors (burn_impl/hyperscalees-noiser/src/eggroll.rs:86-227, 312-324) ---- */
+void or_get_lora_update_params(float base_sigma, uint64_t key, int32_t rank,
+                               int32_t epoch, int32_t thread_id, int32_t a, int32_t b,
+                               int32_t noise_reuse, float *A /* a*r */, float *B /* b*r */);
+void or_batched_lora_noise(float base_sigma, uint64_t key, int32_t rank,
+                           const int32_t *tids, int32_t n, int32_t epoch, int32_t noise_reuse,
+                           int32_t a, int32_t b, float *A /* n*a*r */, float *B /* n*b*r */);
+void or_get_nonlora_update_params(float base_sigma, uint64_t key, int32_t epoch,
+                                  int32_t thread_id, int32_t a, int32_t b, int32_t noise_reuse,
+                                  float *out /* a*b */);
+float or_base_sigma(float sigma, int32_t rank);
+
+/* ---- forward (eggroll.rs:419-477, snn.rs:665-685) ---- */
+/* y(m,n) = x(m,k) @ w(n,k)^T, f32 accumulation in ascending k. */
+void or_matmul_abt(const float *x, int32_t m, int32_t k, const float *w, int32_t n, float *y);
+/* Same product, double accumulation, one rounding at the end. */
+void or_matmul_abt_f64(const float *x, int32_t m, int32_t k, const float *w, int32_t n, float *y);
+/* do_mm for one member: y = x@W^T + (x@B)@A^T  (iterinfo present) or x@W^T. */
+void or_do_mm(const float *x, int32_t rows, const float *W, int32_t a, int32_t b,
+              const float *A /* a*r or NULL */, const float *B /* b*r or NULL */, int32_t r,
+              float *y);
+/* do_Tmm for one member: W is (b_in=a, out=b) in the reference's (a,b) naming:
+ * y = x@W + (x@A)@B^T, x is (rows, a), y is (rows, b). */
+void or_do_Tmm(const float *x, int32_t rows, const float *W, int32_t a, int32_t b,
+               const float *A, const float *B, int32_t r, float *y);
+
+/* ---- SNN pieces (snn.rs:53-97; poisson_encode_fused_oxide.rs:35-106) ---- */
+void or_lif_scan(const float *cur /* T*M*h */, const float *v0 /* M*h or NULL */,
+                 int32_t T, int64_t M, int32_t h, float tau_m, float v_th,
+                 float *spikes /* T*M*h */, float *v_out /* M*h or NULL */);
+void or_poisson_encode(const float *p /* M*in */, int64_t M, int32_t in_dim, int32_t T,
+                       uint32_t s0, uint32_t s1, uint32_t s2, uint32_t s3,
+                       float *spikes /* T*M*in */);
+/* rate(M,h) = mean over T of spikes(T,M,h)  (snn.rs:274) */
+void or_mean_rate(const float *spikes, int32_t T, int64_t M, int32_t h, float *rate);
+
+/* ---- fitness / z-score (snn_mnist.rs:180-201; eggroll.rs:967-992) ---- */
+void or_loglik(const float *logits, int64_t rows, int32_t classes, const int32_t *labels,
+               float *out);
+void or_convert_fitnesses(const float *raw, int32_t n, int32_t group_size, float *out,
+                          float *mean_out, float *std_out);
+
+/* ---- ES update (eggroll.rs:331-404, 550-702, 726-915) ---- */
+/* simple_lora_update: (1/N) sum_i f_i A_i B_i^T, f32 accumulation in member order. */
+void or_simple_lora_update(float sigma, uint64_t key, int32_t rank, int32_t noise_reuse,
+                           const float *scores, const int32_t *epochs, const int32_t *tids,
+                           int32_t n, int32_t a, int32_t b, float *g);
+/* do_update_with(map_class=1): returns -sqrt(N) * simple_lora_update. */
+void or_do_update_lora(float sigma, uint64_t key, int32_t rank, int32_t noise_reuse,
+                       const float *scores, const int32_t *epochs, const int32_t *tids,
+                       int32_t n, int32_t a, int32_t b, float *grad);
+/* do_update_with(map_class=0) */
+void or_do_update_full(float sigma, uint64_t key, int32_t noise_reuse, int32_t freeze_nonlora,
+                       const float *scores, const int32_t *epochs, const int32_t *tids,
+                       int32_t n, int32_t a, int32_t b, float *grad);
+/* Double-accumulated sum_i f_i A_i B_i^T over n members (no scaling). */
+void or_lora_einsum_f64(float base_sigma, uint64_t key, int32_t rank, int32_t noise_reuse,
+                        int32_t epoch, const float *scores, const int32_t *tids, int32_t n,
+                        int32_t a, int32_t b, double *g);
+/* accumulated_update (eggroll.rs:579-702), LoRA parameters only: -sum_k einsum_k/sqrt(batch). */
+void or_accumulated_lora_grad(float sigma, uint64_t key, int32_t rank, int32_t noise_reuse,
+                              int32_t epoch, const float *conv_full, const int32_t *tids,
+                              int32_t accumulate, int32_t chunk, int32_t a, int32_t b,
+                              float *grad);
+/* lora_einsum_raw / lora_einsum_ones on (n,r,*) layouts (eggroll.rs:726-748). */
+void or_lora_einsum_raw(const float *a_t, const float *b_t, const float *scores, int32_t n,
+                        int32_t r, int32_t a, int32_t b, float *g);
+void or_lora_einsum_ones(const float *a_t, const float *b_t, int32_t n, int32_t r, int32_t a,
+                         int32_t b, float *g);
+/* combine_affine_grads (eggroll.rs:902-915) */
+void or_combine_affine(const float *grad_acc, const float *ones_acc, int64_t len, float mean,
+                       float std, int32_t batch, float *out);
+
+/* ---- Solver (noiser.rs:155-244) ---- */
+enum { OR_SGD = 0, OR_ADAM = 1, OR_ADAMW = 2 };
+/* One step for one parameter tensor.  step_t is the already-incremented global step. */
+void or_solver_step(int32_t kind, float lr, float beta1, float beta2, float eps, float wd,
+                    int32_t step_t, const float *p, const float *g, float *m, float *v,
+                    int64_t len, float *p_out);
+float or_clip_global_norm_scale(const float *const *grads, const int64_t *lens, int32_t n,
+                                float max_norm);
+
+/* ---- whole SNN-MLP ES step (the composition the hot path implements) ---- */
+typedef struct {
+    int32_t n_layers;       /* number of perturbed linear layers (hidden + readout) */
+    const int32_t *dims;    /* n_layers+1 widths: in, h1, ..., classes */
+    int32_t T;              /* Poisson / LIF time steps */
+    int32_t rows;           /* samples per member (B) */
+    float tau_m, v_th;
+    float sigma;
+    int32_t rank;
+    int32_t noise_reuse;
+    int32_t epoch;
+    uint32_t poisson_seed[4];
+} or_snn_cfg;
+
+/* Forward for members [m_lo, m_hi) of the population.  probs is (n_members*rows, in)
+ * row-major (member-major rows), labels (n_members*rows).  Writes the raw member
+ * fitness (mean log-likelihood over the member's rows) into fit[m - m_lo].
+ * tid of member m is m (thread ids are the member indices).  nthreads>1 uses OpenMP. */
+void or_snn_forward_members(const or_snn_cfg *cfg, const float *const *W, const uint64_t *keys,
+                            const float *probs, const int32_t *labels, int32_t m_lo,
+                            int32_t m_hi, int32_t nthreads, float *fit);
+/* Double-accumulated ES gradient of one layer for members [0,n): -sqrt(n)*(1/n)*sum f A B^T
+ * computed from z-scored fitness.  nthreads>1 parallelises over output rows. */
+void or_lora_grad_f64(float sigma, uint64_t key, int32_t rank, int32_t noise_reuse,
+                      int32_t epoch, const float *fit, int32_t n, int32_t a, int32_t b,
+                      int32_t nthreads, float *grad);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

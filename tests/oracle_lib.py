@@ -1,0 +1,169 @@
+"""ctypes binding of the CPU oracle (oracle/liboracle.so), test infrastructure only."""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ORACLE_DIR = os.path.join(ROOT, "oracle")
+LIB = os.path.join(ORACLE_DIR, "_build", "liboracle.so")
+
+_lib = None
+f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+f64p = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
+i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
+c_i32, c_i64, c_u32, c_u64, c_f32 = (ctypes.c_int32, ctypes.c_int64, ctypes.c_uint32,
+                                     ctypes.c_uint64, ctypes.c_float)
+
+
+class SnnCfg(ctypes.Structure):
+    _fields_ = [("n_layers", c_i32), ("dims", ctypes.POINTER(c_i32)), ("T", c_i32),
+                ("rows", c_i32), ("tau_m", c_f32), ("v_th", c_f32), ("sigma", c_f32),
+                ("rank", c_i32), ("noise_reuse", c_i32), ("epoch", c_i32),
+                ("poisson_seed", c_u32 * 4)]
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", ORACLE_DIR], check=True)
+
+
+def load():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB):
+        build()
+    L = ctypes.CDLL(LIB)
+    sig = {
+        "or_noise_seed": (c_u64, [c_u64, c_i32, c_i32]),
+        "or_xorshift64_step": (c_u64, [c_u64]),
+        "or_unit_from_u64": (c_f32, [c_u64]),
+        "or_bm_radius": (c_f32, [c_u32]),
+        "or_bm_cos": (c_f32, [c_u32]),
+        "or_bm_eval": (None, [c_u32, c_u32, f32p, f32p, f32p]),
+        "or_base_sigma": (c_f32, [c_f32, c_i32]),
+        "or_standard_normals": (None, [c_u64, f32p, c_i64]),
+        "or_get_lora_update_params": (None, [c_f32, c_u64, c_i32, c_i32, c_i32, c_i32, c_i32,
+                                             c_i32, f32p, f32p]),
+        "or_batched_lora_noise": (None, [c_f32, c_u64, c_i32, i32p, c_i32, c_i32, c_i32, c_i32,
+                                         c_i32, f32p, f32p]),
+        "or_get_nonlora_update_params": (None, [c_f32, c_u64, c_i32, c_i32, c_i32, c_i32, c_i32,
+                                                f32p]),
+        "or_matmul_abt": (None, [f32p, c_i32, c_i32, f32p, c_i32, f32p]),
+        "or_matmul_abt_f64": (None, [f32p, c_i32, c_i32, f32p, c_i32, f32p]),
+        "or_do_mm": (None, [f32p, c_i32, f32p, c_i32, c_i32, ctypes.c_void_p, ctypes.c_void_p,
+                            c_i32, f32p]),
+        "or_do_Tmm": (None, [f32p, c_i32, f32p, c_i32, c_i32, ctypes.c_void_p, ctypes.c_void_p,
+                             c_i32, f32p]),
+        "or_lif_scan": (None, [f32p, ctypes.c_void_p, c_i32, c_i64, c_i32, c_f32, c_f32, f32p,
+                               ctypes.c_void_p]),
+        "or_poisson_encode": (None, [f32p, c_i64, c_i32, c_i32, c_u32, c_u32, c_u32, c_u32,
+                                     f32p]),
+        "or_mean_rate": (None, [f32p, c_i32, c_i64, c_i32, f32p]),
+        "or_loglik": (None, [f32p, c_i64, c_i32, i32p, f32p]),
+        "or_convert_fitnesses": (None, [f32p, c_i32, c_i32, f32p, ctypes.POINTER(c_f32),
+                                        ctypes.POINTER(c_f32)]),
+        "or_simple_lora_update": (None, [c_f32, c_u64, c_i32, c_i32, f32p, i32p, i32p, c_i32,
+                                         c_i32, c_i32, f32p]),
+        "or_do_update_lora": (None, [c_f32, c_u64, c_i32, c_i32, f32p, i32p, i32p, c_i32, c_i32,
+                                     c_i32, f32p]),
+        "or_do_update_full": (None, [c_f32, c_u64, c_i32, c_i32, f32p, i32p, i32p, c_i32, c_i32,
+                                     c_i32, f32p]),
+        "or_lora_einsum_f64": (None, [c_f32, c_u64, c_i32, c_i32, c_i32, f32p, i32p, c_i32,
+                                      c_i32, c_i32, f64p]),
+        "or_accumulated_lora_grad": (None, [c_f32, c_u64, c_i32, c_i32, c_i32, f32p, i32p, c_i32,
+                                            c_i32, c_i32, c_i32, f32p]),
+        "or_lora_einsum_raw": (None, [f32p, f32p, f32p, c_i32, c_i32, c_i32, c_i32, f32p]),
+        "or_lora_einsum_ones": (None, [f32p, f32p, c_i32, c_i32, c_i32, c_i32, f32p]),
+        "or_combine_affine": (None, [f32p, f32p, c_i64, c_f32, c_f32, c_i32, f32p]),
+        "or_solver_step": (None, [c_i32, c_f32, c_f32, c_f32, c_f32, c_f32, c_i32, f32p, f32p,
+                                  f32p, f32p, c_i64, f32p]),
+        "or_snn_forward_members": (None, [ctypes.POINTER(SnnCfg), ctypes.c_void_p,
+                                          ctypes.c_void_p, f32p, i32p, c_i32, c_i32, c_i32,
+                                          f32p]),
+        "or_lora_grad_f64": (None, [c_f32, c_u64, c_i32, c_i32, c_i32, f32p, c_i32, c_i32, c_i32,
+                                    c_i32, f32p]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+# ---- numpy conveniences ------------------------------------------------------
+
+def lora_factors(base_sigma, key, rank, epoch, tids, a, b, noise_reuse=0):
+    L = load()
+    tids = np.ascontiguousarray(tids, dtype=np.int32)
+    n = tids.size
+    A = np.zeros((n, a, rank), np.float32)
+    B = np.zeros((n, b, rank), np.float32)
+    L.or_batched_lora_noise(base_sigma, key & (2**64 - 1), rank, tids, n, epoch, noise_reuse, a,
+                            b, A, B)
+    return A, B
+
+
+def do_mm(x, W, A=None, B=None):
+    L = load()
+    x = np.ascontiguousarray(x, np.float32)
+    W = np.ascontiguousarray(W, np.float32)
+    rows, b = x.shape
+    a = W.shape[0]
+    y = np.zeros((rows, a), np.float32)
+    r = 0 if A is None else A.shape[1]
+    Ap = None if A is None else np.ascontiguousarray(A, np.float32)
+    Bp = None if B is None else np.ascontiguousarray(B, np.float32)
+    L.or_do_mm(x, rows, W, a, b, None if Ap is None else Ap.ctypes.data,
+               None if Bp is None else Bp.ctypes.data, r, y)
+    return y
+
+
+def lif(cur, tau_m, v_th, v0=None):
+    L = load()
+    cur = np.ascontiguousarray(cur, np.float32)
+    T, M, h = cur.shape
+    spk = np.zeros_like(cur)
+    v = np.zeros((M, h), np.float32)
+    v0p = None if v0 is None else np.ascontiguousarray(v0, np.float32).ctypes.data
+    L.or_lif_scan(cur, v0p, T, M, h, tau_m, v_th, spk, v.ctypes.data)
+    return spk, v
+
+
+def poisson(p, T, seeds=(0, 0, 0, 0)):
+    L = load()
+    p = np.ascontiguousarray(p, np.float32)
+    M, d = p.shape
+    out = np.zeros((T, M, d), np.float32)
+    L.or_poisson_encode(p, M, d, T, *[int(s) & 0xFFFFFFFF for s in seeds], out)
+    return out
+
+
+def loglik(logits, labels):
+    L = load()
+    logits = np.ascontiguousarray(logits, np.float32)
+    rows, c = logits.shape
+    out = np.zeros(rows, np.float32)
+    L.or_loglik(logits, rows, c, np.ascontiguousarray(labels, np.int32), out)
+    return out
+
+
+def convert_fitnesses(raw, group_size=0):
+    L = load()
+    raw = np.ascontiguousarray(raw, np.float32)
+    out = np.zeros_like(raw)
+    m, s = c_f32(), c_f32()
+    L.or_convert_fitnesses(raw, raw.size, group_size, out, ctypes.byref(m), ctypes.byref(s))
+    return out, m.value, s.value
+
+
+def lora_grad_f64(sigma, key, rank, epoch, fit, a, b, noise_reuse=0, nthreads=8):
+    """-sqrt(N)/N * sum_i f_i A_i B_i^T, double accumulation, tids 0..N-1."""
+    L = load()
+    fit = np.ascontiguousarray(fit, np.float32)
+    g = np.zeros((a, b), np.float32)
+    L.or_lora_grad_f64(sigma, key & (2**64 - 1), rank, noise_reuse, epoch, fit, fit.size, a, b,
+                       nthreads, g)
+    return g

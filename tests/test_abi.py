@@ -1,0 +1,82 @@
+"""CPU checks of the C ABI: libhses.so loads, exports every entry point that
+include/hses.h declares, and rejects bad arguments before touching a GPU."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from hyperscalees_amd import _lib
+from tests import oracle_lib as O
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    txt = open(os.path.join(ROOT, "include", "hses.h")).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return sorted(set(re.findall(r"\b(hses_[a-z0-9_]+)\s*\(", txt)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    syms = declared_symbols()
+    assert len(syms) >= 15
+    for s in syms:
+        assert hasattr(lib, s), f"libhses.so does not export {s}"
+    assert set(syms) == set(_lib.PROTOTYPES), "ctypes prototypes out of sync with hses.h"
+
+
+def test_version_string():
+    assert b"gfx950" in _lib.load().hses_version()
+
+
+def test_noise_seed_matches_oracle():
+    lib = _lib.load()
+    for k, e, t in [(0, 0, 0), (42, 1, 2), (2**64 - 1, -3, 17), (0x9E3779B97F4A7C15 * 3 % 2**64, 0, 4095)]:
+        assert lib.hses_noise_seed(k, e, t) == O.load().or_noise_seed(k, e, t)
+
+
+def _expect_invalid(name, *args):
+    rc = getattr(_lib.load(), name)(*args)
+    assert rc == _lib.HSES_ERR_INVALID_ARG, (name, rc)
+    assert _lib.last_error(), "no error message"
+
+
+NULL = None
+
+
+def test_validation_rejects_bad_arguments_without_a_gpu():
+    _expect_invalid("hses_bm_eval", 2**24 - 4, 8, NULL, NULL, NULL, NULL)
+    _expect_invalid("hses_lora_factors", 0.1, 1, 4, 0, -1, 0, NULL, 2, 3, 4, NULL, NULL, NULL)
+    _expect_invalid("hses_lora_factors", 0.1, 1, 4, 0, 0, 0, NULL, 2, 3, 4, NULL, NULL, NULL)
+    _expect_invalid("hses_poisson_encode", NULL, -1, 784, 784, 8, 0, 0, 0, 0, NULL, 0, 784, NULL)
+    _expect_invalid("hses_poisson_encode", ctypes.c_void_p(16), 4, 784, 700, 8, 0, 0, 0, 0,
+                    ctypes.c_void_p(16), 0, 784, NULL)
+    _expect_invalid("hses_poisson_encode", ctypes.c_void_p(16), 4, 784, 784, 8, 0, 0, 0, 0,
+                    ctypes.c_void_p(16), 3, 12, NULL)  # 784 bits need 13 words
+    _expect_invalid("hses_poisson_encode", ctypes.c_void_p(16), 4, 784, 784, 8, 0, 0, 0, 0,
+                    ctypes.c_void_p(16), 9, 784, NULL)
+    _expect_invalid("hses_poisson_encode", ctypes.c_void_p(16), 2**23, 1024, 1024, 8, 0, 0, 0, 0,
+                    ctypes.c_void_p(16), 0, 1024, NULL)  # flat index beyond u32
+    _expect_invalid("hses_lif_scan", ctypes.c_void_p(16), NULL, 8, 4, 128, 128, 0.0, 1.0,
+                    ctypes.c_void_p(16), 0, 128, NULL, NULL)
+    _expect_invalid("hses_lif_scan", ctypes.c_void_p(16), NULL, 8, 4, 128, 100, 10.0, 1.0,
+                    ctypes.c_void_p(16), 0, 128, NULL, NULL)
+    _expect_invalid("hses_convert_fitnesses", NULL, 0, 0, NULL, NULL, NULL)
+    _expect_invalid("hses_convert_fitnesses", ctypes.c_void_p(16), 10, 3, ctypes.c_void_p(16),
+                    NULL, NULL)
+    _expect_invalid("hses_solver_step", 7, 0.1, 0.9, 0.999, 1e-8, 0.0, 1, ctypes.c_void_p(16),
+                    ctypes.c_void_p(16), NULL, NULL, 4, NULL)
+    _expect_invalid("hses_solver_step", 1, 0.1, 0.9, 0.999, 1e-8, 0.0, 0, ctypes.c_void_p(16),
+                    ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16), 4, NULL)
+    _expect_invalid("hses_member_loglik", NULL, 0, NULL, 4, 2, NULL, NULL)
+
+
+def test_empty_inputs_are_no_ops_without_a_gpu():
+    lib = _lib.load()
+    assert lib.hses_poisson_encode(NULL, 0, 784, 784, 8, 0, 0, 0, 0, NULL, 0, 784, NULL) == 0
+    assert lib.hses_lif_scan(NULL, NULL, 8, 0, 128, 128, 10.0, 1.0, NULL, 0, 128, NULL, NULL) == 0
+    assert lib.hses_lora_factors(0.1, 1, 4, 0, 0, 0, NULL, 0, 3, 4, NULL, NULL, NULL) == 0
+    assert lib.hses_solver_step(0, 0.1, 0.9, 0.999, 1e-8, 0.0, 1, NULL, NULL, NULL, NULL, 0,
+                                NULL) == 0

@@ -1,0 +1,126 @@
+"""GPU parity of the Poisson and LIF kernels (bit-exact) and of the fitness,
+z-score and solver kernels (tolerance) against the oracle."""
+import numpy as np
+import pytest
+import torch
+
+from hyperscalees_amd._lib import ADAM, ADAMW, FMT_BF16, FMT_BITS, FMT_F32, FMT_U8, SGD
+from tests import oracle_lib as O
+
+pytestmark = pytest.mark.gpu
+
+
+def sparse_intensities(rng, rows, d, zero_frac=0.7):
+    p = rng.random((rows, d)).astype(np.float32)
+    p[rng.random((rows, d)) < zero_frac] = 0.0
+    return p
+
+
+def unpack_bits(words, width):
+    w = words.cpu().numpy().view(np.uint64)
+    bits = ((w[..., None] >> np.arange(64, dtype=np.uint64)) & np.uint64(1)).astype(np.float32)
+    return bits.reshape(*w.shape[:-1], -1)[..., :width]
+
+
+@pytest.mark.parametrize("rows,d,T", [(64, 784, 8), (37, 100, 16), (5, 1, 3), (256, 784, 16)])
+def test_poisson_bit_exact_all_formats(hses_gpu, rows, d, T):
+    rng = np.random.default_rng(rows * 7 + d)
+    p = sparse_intensities(rng, rows, d)
+    p[0, :min(d, 4)] = [0.0, 1.0, 0.5, 2.0][:min(d, 4)]
+    seeds = (11, 22, 33, 44)
+    ref = O.poisson(p, T, seeds)
+    pt = torch.from_numpy(p).cuda()
+    got = hses_gpu.poisson_encode(pt, T, seeds, FMT_F32)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(got.cpu().numpy(), ref)
+    bf = hses_gpu.poisson_encode(pt, T, seeds, FMT_BF16)
+    np.testing.assert_array_equal(bf.float().cpu().numpy(), ref)
+    u8 = hses_gpu.poisson_encode(pt, T, seeds, FMT_U8)
+    np.testing.assert_array_equal(u8.cpu().numpy().astype(np.float32), ref)
+    bits = hses_gpu.poisson_encode(pt, T, seeds, FMT_BITS)
+    np.testing.assert_array_equal(unpack_bits(bits, d), ref)
+
+
+def test_poisson_threshold_dense_p_sweep(hses_gpu):
+    # Every representable neighbourhood of many thresholds: p on a fine grid
+    # plus its f32 neighbours, checked against the f32-division formula.
+    base = np.linspace(0, 1, 4001, dtype=np.float32)
+    p = np.concatenate([base, np.nextafter(base, 2), np.nextafter(base, -1)]).astype(np.float32)
+    p = np.tile(p, 4)[: (p.size * 4 // 100) * 100].reshape(-1, 100)
+    ref = O.poisson(p, 12, (1, 2, 3, 5))
+    got = hses_gpu.poisson_encode(torch.from_numpy(p).cuda(), 12, (1, 2, 3, 5))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(got.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("T,M,h,tau,vth", [(8, 64, 128, 10.0, 1.0), (16, 33, 100, 20.0, 0.3),
+                                           (5, 3, 1, 10.0, -1e9), (16, 512, 128, 10.0, 1.0)])
+def test_lif_bit_exact(hses_gpu, T, M, h, tau, vth):
+    rng = np.random.default_rng(T * 1000 + h)
+    cur = (rng.standard_normal((T, M, h)) * 1.5 + 0.4).astype(np.float32)
+    v0 = (rng.standard_normal((M, h)) * 0.3).astype(np.float32)
+    ref_s, ref_v = O.lif(cur, tau, vth, v0)
+    ct = torch.from_numpy(cur).cuda()
+    vt = torch.from_numpy(v0).cuda()
+    s, v = hses_gpu.lif_scan(ct, tau, vth, v0=vt, fmt=FMT_F32, want_v=True)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(s.cpu().numpy(), ref_s)
+    np.testing.assert_array_equal(v.cpu().numpy().view(np.uint32), ref_v.view(np.uint32))
+    bits = hses_gpu.lif_scan(ct, tau, vth, v0=vt, fmt=FMT_BITS)
+    np.testing.assert_array_equal(unpack_bits(bits, h), ref_s)
+    bf = hses_gpu.lif_scan(ct, tau, vth, v0=vt, fmt=FMT_BF16)
+    np.testing.assert_array_equal(bf.float().cpu().numpy(), ref_s)
+    u8 = hses_gpu.lif_scan(ct, tau, vth, v0=vt, fmt=FMT_U8)
+    np.testing.assert_array_equal(u8.cpu().numpy().astype(np.float32), ref_s)
+
+
+def test_lif_zero_v0_default(hses_gpu):
+    cur = np.full((6, 2, 3), 2.0, np.float32)
+    ref_s, _ = O.lif(cur, 10.0, 1.0)
+    s = hses_gpu.lif_scan(torch.from_numpy(cur).cuda(), 10.0, 1.0)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(s.cpu().numpy(), ref_s)
+
+
+def test_member_loglik(hses_gpu):
+    rng = np.random.default_rng(5)
+    n, rpm, c = 40, 16, 10
+    logits = (rng.standard_normal((n * rpm, c)) * 3).astype(np.float32)
+    labels = rng.integers(0, c, n * rpm).astype(np.int32)
+    ref = O.loglik(logits, labels).reshape(n, rpm).astype(np.float64).mean(1)
+    got = hses_gpu.member_loglik(torch.from_numpy(logits).cuda(), torch.from_numpy(labels).cuda(),
+                                 n, rpm)
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(got.cpu().numpy(), ref, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("group", [0, 4])
+def test_convert_fitnesses(hses_gpu, group):
+    raw = np.random.default_rng(9).standard_normal(8192).astype(np.float32) * 3 + 1
+    ref, m, s = O.convert_fitnesses(raw, group)
+    out, stats = hses_gpu.convert_fitnesses(torch.from_numpy(raw).cuda(), group)
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(out.cpu().numpy(), ref, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(stats.cpu().numpy(), [m, s], rtol=1e-6)
+
+
+@pytest.mark.parametrize("kind", [SGD, ADAM, ADAMW])
+def test_solver_step(hses_gpu, kind):
+    rng = np.random.default_rng(kind)
+    n = 1000
+    p = rng.standard_normal(n).astype(np.float32)
+    m = rng.standard_normal(n).astype(np.float32) * 0.1
+    v = np.abs(rng.standard_normal(n).astype(np.float32)) * 0.01
+    for step in (1, 2, 7):
+        g = rng.standard_normal(n).astype(np.float32)
+        ref = np.zeros_like(p)
+        rm, rv = m.copy(), v.copy()
+        O.load().or_solver_step(kind, 0.01, 0.9, 0.999, 1e-8, 1e-4, step, p, g, rm, rv, n, ref)
+        pt, mt, vt = (torch.from_numpy(a.copy()).cuda() for a in (p, m, v))
+        hses_gpu.solver_step(kind, 0.01, pt, torch.from_numpy(g).cuda(), mt, vt, step_t=step,
+                             wd=1e-4)
+        torch.cuda.synchronize()
+        np.testing.assert_allclose(pt.cpu().numpy(), ref, rtol=1e-6, atol=1e-7)
+        if kind != SGD:
+            np.testing.assert_allclose(mt.cpu().numpy(), rm, rtol=1e-6, atol=1e-8)
+        p, m, v = ref, rm, rv
