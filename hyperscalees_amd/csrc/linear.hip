@@ -1,9 +1,320 @@
-// linear.hip -- perturbed forward (placeholder until the MFMA kernel lands).
+// linear.hip -- batched EggRoll perturbed forward  y = x W^T + (x B_m) A_m^T.
+//
+// Reference: do_mm_impl (burn_impl/hyperscalees-noiser/src/eggroll.rs:419-446)
+// and its batched form lora_linear_batched (burn_impl/hyperscalees-models/src/snn.rs:665-685).
+//
+// k_linear_small (this file) serves ranks whose noise columns fit beside a
+// 64-wide output tile (members_per_tile * r <= 64): C1 (r=4), C2 (r=1).
+// A workgroup owns 64 consecutive member-major rows and 64 output columns:
+//   1. generates B_m (all K rows) and the tile's rows of A_m for the members
+//      its rows belong to, straight into LDS (never to HBM);
+//   2. runs the K loop with MFMA over [W_tile^T | B_m...] (x tile and W tile
+//      staged through LDS, B_m resident), giving x W^T and x B_m together;
+//   3. adds (x B_m) A_m^T in the epilogue (r multiply-adds per output).
+// Larger ranks go to k_linear_pair (linear_pair.hip).
+#include <math.h>
+
+#include "linear_common.h"
+#include "mfma.h"
+#include "noise_dev.h"
 #include "runtime.h"
+
+namespace hses {
+
+constexpr int K1_BM = 64, K1_CT = 64, K1_BK = 32, K1_THREADS = 256, K1_NEMAX = 64;
+
+template <int MATH>
+struct K1Layout {
+    using T = typename MathT<MATH>::T;
+    static constexpr int PAD = MathT<MATH>::PAD;
+    static constexpr int XP = K1_BK + PAD;  // pitch of the x and W tiles
+    size_t off_x, off_w, off_b, off_a, off_xb, bytes;
+    __host__ __device__ K1Layout(int ne_real, int ne, int bpitch, int nm_max, int r) {
+        size_t o = align16(sizeof(BmTables));
+        off_x = o;
+        o = align16(o + (size_t)K1_BM * XP * sizeof(T));
+        off_w = o;
+        o = align16(o + (size_t)K1_CT * XP * sizeof(T));
+        off_b = o;
+        o = align16(o + (size_t)ne_real * bpitch * sizeof(T));
+        off_a = o;
+        o = align16(o + (size_t)nm_max * K1_CT * r * sizeof(float));
+        off_xb = o;
+        o = align16(o + (size_t)K1_BM * ne * sizeof(float));
+        bytes = o;
+    }
+};
+
+template <int MATH, int XFMT>
+__global__ __launch_bounds__(K1_THREADS) void k_linear_small(LinParams P) {
+    using T = typename MathT<MATH>::T;
+    using L = K1Layout<MATH>;
+    constexpr int XP = L::XP;
+    extern __shared__ __align__(16) unsigned char smem[];
+    const L lay(P.ne_real, P.ne, P.bpitch, P.nm_max, P.r);
+    BmTables* tabs = reinterpret_cast<BmTables*>(smem);
+    T* Xs = reinterpret_cast<T*>(smem + lay.off_x);
+    T* Ws = reinterpret_cast<T*>(smem + lay.off_w);
+    T* Bs = reinterpret_cast<T*>(smem + lay.off_b);
+    float* As = reinterpret_cast<float*>(smem + lay.off_a);
+    float* XB = reinterpret_cast<float*>(smem + lay.off_xb);
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int64_t L0 = (int64_t)blockIdx.x * K1_BM;
+    const int32_t o0 = blockIdx.y * K1_CT;
+    const int32_t ct = min(K1_CT, P.a - o0);
+    const int32_t R = P.R, r = P.r, b = P.b;
+    const int32_t m_first = (int32_t)(L0 / R);
+    const int32_t m_last = (int32_t)((min(L0 + K1_BM, P.total) - 1) / R);
+    const int32_t nm = m_last - m_first + 1;
+    const bool noisy = P.ne > 0;
+
+    // ---- 1. factors of the tile's members into LDS -------------------------
+    if (noisy) {
+        load_bm_tables(tabs, P.tables);
+        for (int i = tid; i < P.ne_real * P.bpitch; i += K1_THREADS) Bs[i] = MathT<MATH>::zero();
+        __syncthreads();
+        const NoiseCtx ctx{tabs, P.log_exc, P.cos_exc};
+        const int32_t rc = P.rc;
+        const int32_t nqB = (b + rc - 1) / rc;
+        const int32_t qA0 = (b + o0) / rc, qA1 = (b + o0 + ct + rc - 1) / rc;
+        const int32_t q2 = max(qA0, nqB);
+        const int32_t per = nqB + max(0, qA1 - q2);
+        for (int item = tid; item < nm * per; item += K1_THREADS) {
+            const int32_t lm = item / per, qi = item % per;
+            const int32_t q = qi < nqB ? qi : q2 + (qi - nqB);
+            float sign;
+            const uint64_t seed = member_seed(P.key, P.epoch, P.nreuse, P.tid_lo + m_first + lm, &sign);
+            const float sc = sign * P.bs;
+            uint64_t s = row_start_state(seed, q, P.jump);
+            for (int32_t jj = 0; jj < rc; ++jj) {
+                const int32_t j = q * rc + jj;
+                if (j >= P.a + b) break;
+                for (int32_t c = 0; c < r; ++c) {
+                    const float v = bm_normal(s, ctx);
+                    if (j < b) {
+                        Bs[(size_t)(lm * r + c) * P.bpitch + j] = MathT<MATH>::cvt(v);
+                    } else {
+                        const int32_t o = j - b - o0;
+                        if (o >= 0 && o < ct) As[((size_t)lm * K1_CT + o) * r + c] = v * sc;
+                    }
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- 2. K loop ----------------------------------------------------------
+    f32x4 accb[K1_CT / 16], accx[K1_NEMAX / 16];
+#pragma unroll
+    for (int i = 0; i < K1_CT / 16; ++i) accb[i] = f32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < K1_NEMAX / 16; ++i) accx[i] = f32x4{0, 0, 0, 0};
+    const int ne_tiles = P.ne / 16;
+    const int srow = tid >> 2, sk = (tid & 3) * 8;  // staging: 64 rows x 4 segments of 8
+    const int64_t Lrow = L0 + srow;
+    const bool rvalid = Lrow < P.total;
+    const int64_t xoff = rvalid ? phys_row(P, Lrow, P.x_stride, P.x_plane) : 0;
+    const int32_t wcol = o0 + srow;
+    const int mrow = wave * 16 + (lane & 15), kg = lane >> 4;
+
+    for (int32_t k0 = 0; k0 < b; k0 += K1_BK) {
+        T xv[8], wv[8];
+        load_x_seg<MATH, XFMT>(P.x, xoff, rvalid, k0 + sk, b, xv);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int32_t k = k0 + sk + i;
+            wv[i] = MathT<MATH>::cvt((wcol < P.a && k < b) ? P.W[(int64_t)wcol * b + k] : 0.0f);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            Xs[srow * XP + sk + i] = xv[i];
+            Ws[srow * XP + sk + i] = wv[i];
+        }
+        __syncthreads();
+        if constexpr (MATH == HSES_MATH_F32) {
+#pragma unroll
+            for (int ks = 0; ks < K1_BK; ks += 4) {
+                const float af = Xs[mrow * XP + ks + kg];
+#pragma unroll
+                for (int nt = 0; nt < K1_CT / 16; ++nt)
+                    if (nt * 16 < ct) accb[nt] = mfma_f32(af, Ws[(nt * 16 + (lane & 15)) * XP + ks + kg], accb[nt]);
+#pragma unroll
+                for (int ne = 0; ne < K1_NEMAX / 16; ++ne)
+                    if (ne < ne_tiles) {
+                        const int br = ne * 16 + (lane & 15);
+                        const float bf = br < P.ne_real ? Bs[(size_t)br * P.bpitch + k0 + ks + kg] : 0.0f;
+                        accx[ne] = mfma_f32(af, bf, accx[ne]);
+                    }
+            }
+        } else {
+            const u16x8 af = lds_u16x8(&Xs[mrow * XP + kg * 8]);
+#pragma unroll
+            for (int nt = 0; nt < K1_CT / 16; ++nt)
+                if (nt * 16 < ct) accb[nt] = mfma_bf16(af, lds_u16x8(&Ws[(nt * 16 + (lane & 15)) * XP + kg * 8]), accb[nt]);
+#pragma unroll
+            for (int ne = 0; ne < K1_NEMAX / 16; ++ne)
+                if (ne < ne_tiles) {
+                    const int br = ne * 16 + (lane & 15);
+                    const u16x8 bf = br < P.ne_real ? lds_u16x8(&Bs[(size_t)br * P.bpitch + k0 + kg * 8])
+                                                    : u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+                    accx[ne] = mfma_bf16(af, bf, accx[ne]);
+                }
+        }
+        __syncthreads();
+    }
+
+    // ---- 3. epilogue: y = x W^T + (x B_m) A_m^T ------------------------------
+    if (noisy) {
+#pragma unroll
+        for (int ne = 0; ne < K1_NEMAX / 16; ++ne)
+            if (ne < ne_tiles) {
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                    XB[(wave * 16 + 4 * kg + v) * P.ne + ne * 16 + (lane & 15)] = accx[ne][v];
+            }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int nt = 0; nt < K1_CT / 16; ++nt) {
+        const int col = nt * 16 + (lane & 15);
+        if (nt * 16 >= ct || col >= ct) continue;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int row = wave * 16 + 4 * kg + v;
+            const int64_t Lr = L0 + row;
+            if (Lr >= P.total) continue;
+            float yv = accb[nt][v];
+            if (noisy) {
+                const int32_t lm = (int32_t)(Lr / R) - m_first;
+                const float* xb = XB + row * P.ne + lm * r;
+                const float* ar = As + ((size_t)lm * K1_CT + col) * r;
+                float z = 0.0f;
+                for (int32_t c = 0; c < r; ++c) z = __fadd_rn(z, __fmul_rn(xb[c], ar[c]));
+                yv = __fadd_rn(yv, z);
+            }
+            P.y[phys_row(P, Lr, P.y_stride, P.y_plane) + o0 + col] = yv;
+        }
+    }
+}
+
+template <int MATH>
+static size_t k1_lds_bytes(const LinParams& P) {
+    return K1Layout<MATH>(P.ne_real, P.ne, P.bpitch, P.nm_max, P.r).bytes;
+}
+
+template <int MATH, int XFMT>
+static int launch_small(const LinParams& P, size_t lds, hipStream_t s) {
+    auto kern = k_linear_small<MATH, XFMT>;
+    if (lds > 64 * 1024)
+        HSES_CHECK_HIP(hipFuncSetAttribute((const void*)kern,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    const int64_t row_tiles = (P.total + K1_BM - 1) / K1_BM;
+    const int col_tiles = (P.a + K1_CT - 1) / K1_CT;
+    hipLaunchKernelGGL(kern, dim3((uint32_t)row_tiles, col_tiles), dim3(K1_THREADS), lds, s, P);
+    HSES_CHECK_HIP(hipGetLastError());
+    return HSES_OK;
+}
+
+int launch_linear_small(LinParams& P, DeviceState* st, hipStream_t s) {
+    // Members a 64-row tile can touch.
+    int32_t nm_max;
+    if (P.R % K1_BM == 0)
+        nm_max = 1;
+    else if (K1_BM % P.R == 0)
+        nm_max = K1_BM / P.R;
+    else
+        nm_max = (K1_BM - 1) / P.R + 2;
+    nm_max = std::min(nm_max, P.n);
+    const bool noisy = P.r > 0 && P.bs != 0.0f;
+    P.nm_max = nm_max;
+    P.ne_real = noisy ? nm_max * P.r : 0;
+    P.ne = (P.ne_real + 15) / 16 * 16;
+    if (P.ne > K1_NEMAX) return HSES_ERR_UNSUPPORTED;
+    P.rc = noisy ? std::max(1, 32 / P.r) : 1;
+    P.bpitch = (P.b + K1_BK - 1) / K1_BK * K1_BK + (P.math == HSES_MATH_F32 ? 4 : 8);
+    const size_t lds = P.math == HSES_MATH_F32 ? k1_lds_bytes<HSES_MATH_F32>(P)
+                                               : k1_lds_bytes<HSES_MATH_BF16>(P);
+    if (lds > st->max_lds) return HSES_ERR_UNSUPPORTED;
+    if (noisy) {
+        const int64_t chunks = (P.a + P.b + P.rc - 1) / P.rc;
+        int rc = get_jump_table(st, (int64_t)P.rc * P.r, chunks, &P.jump);
+        if (rc) return rc;
+    }
+    const int key = P.math * 4 + P.x_fmt;
+    switch (key) {
+        case HSES_MATH_F32 * 4 + HSES_FMT_F32: return launch_small<HSES_MATH_F32, HSES_FMT_F32>(P, lds, s);
+        case HSES_MATH_F32 * 4 + HSES_FMT_BF16: return launch_small<HSES_MATH_F32, HSES_FMT_BF16>(P, lds, s);
+        case HSES_MATH_F32 * 4 + HSES_FMT_BITS: return launch_small<HSES_MATH_F32, HSES_FMT_BITS>(P, lds, s);
+        case HSES_MATH_BF16 * 4 + HSES_FMT_F32: return launch_small<HSES_MATH_BF16, HSES_FMT_F32>(P, lds, s);
+        case HSES_MATH_BF16 * 4 + HSES_FMT_BF16: return launch_small<HSES_MATH_BF16, HSES_FMT_BF16>(P, lds, s);
+        case HSES_MATH_BF16 * 4 + HSES_FMT_BITS: return launch_small<HSES_MATH_BF16, HSES_FMT_BITS>(P, lds, s);
+        default: return set_error(HSES_ERR_INVALID_ARG, "unsupported x format");
+    }
+}
+
+}  // namespace hses
+
 using namespace hses;
-extern "C" int hses_perturbed_linear(const void*, int32_t, int64_t, int64_t, int32_t, const float*,
-                                     int32_t, int32_t, uint64_t, int32_t, float, int32_t, int32_t,
-                                     int32_t, int32_t, int32_t, float*, int64_t, int64_t, int32_t,
-                                     void*) {
-    return set_error(HSES_ERR_UNSUPPORTED, "hses_perturbed_linear: not built yet");
+
+extern "C" int hses_perturbed_linear(const void* d_x, int32_t x_fmt, int64_t x_stride,
+                                     int64_t x_plane, int32_t n_time, const float* d_W, int32_t a,
+                                     int32_t b, uint64_t key, int32_t rank, float sigma,
+                                     int32_t epoch, int32_t noise_reuse, int32_t tid_lo, int32_t n,
+                                     int32_t rows_per_member, float* d_y, int64_t y_stride,
+                                     int64_t y_plane, int32_t math, void* stream) {
+    HSES_REQUIRE(x_fmt == HSES_FMT_F32 || x_fmt == HSES_FMT_BF16 || x_fmt == HSES_FMT_BITS,
+                 "x_fmt must be F32, BF16 or BITS");
+    HSES_REQUIRE(math == HSES_MATH_F32 || math == HSES_MATH_BF16, "unknown math mode");
+    HSES_REQUIRE(a >= 1 && b >= 1, "a and b must be >= 1");
+    HSES_REQUIRE(n >= 0 && rank >= 0 && n_time >= 1 && rows_per_member >= 1, "bad sizes");
+    HSES_REQUIRE(noise_reuse >= 0, "noise_reuse must be >= 0");
+    if (n == 0) return HSES_OK;
+    HSES_REQUIRE(d_x && d_W && d_y, "NULL pointer");
+    const int64_t units = x_fmt == HSES_FMT_BITS ? (b + 63) / 64 : b;
+    const int64_t M = (int64_t)n * rows_per_member;
+    HSES_REQUIRE(x_stride >= units, "x_stride smaller than a row");
+    HSES_REQUIRE(y_stride >= a, "y_stride smaller than a row");
+    HSES_REQUIRE(n_time == 1 || (x_plane >= M * x_stride && y_plane >= M * y_stride),
+                 "time planes overlap");
+    HSES_REQUIRE((int64_t)tid_lo + n - 1 <= INT32_MAX && tid_lo >= 0, "thread id range");
+    HSES_REQUIRE(M * n_time < (1ll << 40), "too many rows");
+    DeviceState* st;
+    int rc = get_state(&st);
+    if (rc) return rc;
+    LinParams P{};
+    P.x = d_x;
+    P.x_fmt = x_fmt;
+    P.x_stride = x_stride;
+    P.x_plane = x_plane;
+    P.n_time = n_time;
+    P.rpm = rows_per_member;
+    P.W = d_W;
+    P.a = a;
+    P.b = b;
+    P.key = key;
+    P.r = (sigma != 0.0f) ? rank : 0;
+    P.bs = rank > 0 ? sigma / sqrtf((float)rank) : 0.0f;  // eggroll.rs:433
+    P.epoch = epoch;
+    P.nreuse = noise_reuse;
+    P.tid_lo = tid_lo;
+    P.n = n;
+    P.y = d_y;
+    P.y_stride = y_stride;
+    P.y_plane = y_plane;
+    P.math = math;
+    P.R = n_time * rows_per_member;
+    P.total = (int64_t)n * P.R;
+    P.tables = st->d_tables;
+    P.log_exc = st->d_log_exc;
+    P.cos_exc = st->d_cos_exc;
+    hipStream_t s = (hipStream_t)stream;
+    rc = launch_linear_pair(P, st, s);
+    if (rc != HSES_ERR_UNSUPPORTED) return rc;
+    rc = launch_linear_small(P, st, s);
+    if (rc == HSES_ERR_UNSUPPORTED)
+        return set_error(HSES_ERR_UNSUPPORTED,
+                         "hses_perturbed_linear: no kernel for this rank/shape (members per "
+                         "64-row tile x rank must be <= 64, or rank a multiple of 16)");
+    return rc;
 }

@@ -1,0 +1,106 @@
+// linear_common.h -- parameters and helpers shared by the perturbed-forward kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/hses.h"
+#include "bm_exact.h"
+#include "mfma.h"
+
+namespace hses {
+
+struct DeviceState;
+
+__host__ __device__ constexpr size_t align16(size_t x) { return (x + 15) & ~(size_t)15; }
+
+template <int MATH>
+struct MathT;
+template <>
+struct MathT<HSES_MATH_F32> {
+    using T = float;
+    static constexpr int PAD = 4;
+    __device__ static T zero() { return 0.0f; }
+    __device__ static T one() { return 1.0f; }
+    __device__ static T cvt(float v) { return v; }
+};
+template <>
+struct MathT<HSES_MATH_BF16> {
+    using T = uint16_t;
+    static constexpr int PAD = 8;
+    __device__ static T zero() { return 0; }
+    __device__ static T one() { return 0x3f80; }
+    __device__ static T cvt(float v) { return f2bf(v); }
+};
+
+// Everything a perturbed-forward launch needs (passed by value).
+struct LinParams {
+    const void* x;
+    int32_t x_fmt;
+    int64_t x_stride, x_plane;
+    int32_t n_time, rpm;
+    const float* W;
+    int32_t a, b;
+    uint64_t key;
+    int32_t r;
+    float bs;
+    int32_t epoch, nreuse, tid_lo, n;
+    float* y;
+    int64_t y_stride, y_plane;
+    int32_t math;
+    int32_t R;      // rows per member = n_time * rpm
+    int64_t total;  // n * R
+    // kernel-specific tiling
+    int32_t nm_max, ne_real, ne, rc, bpitch;
+    const BmTables* tables;
+    const uint32_t* log_exc;
+    const uint32_t* cos_exc;
+    const uint64_t* jump;
+};
+
+// Physical offset (in units) of member-major logical row L: member m = L / R,
+// time t and slot s inside the member; element (t, m*rpm + s).
+__device__ __forceinline__ int64_t phys_row(const LinParams& P, int64_t L, int64_t stride,
+                                            int64_t plane) {
+    const int64_t m = L / P.R;
+    const int32_t rem = (int32_t)(L - m * P.R);
+    const int32_t t = rem / P.rpm;
+    const int32_t s = rem - t * P.rpm;
+    return t * plane + (m * P.rpm + s) * stride;
+}
+
+// Eight consecutive activations x[row][k0..k0+8) converted to the MFMA type.
+// k0 is a multiple of 8; columns >= b read as zero.
+template <int MATH, int XFMT>
+__device__ __forceinline__ void load_x_seg(const void* x, int64_t off, bool valid, int32_t k0,
+                                           int32_t b, typename MathT<MATH>::T out[8]) {
+    using M = MathT<MATH>;
+    if constexpr (XFMT == HSES_FMT_BITS) {
+        uint32_t byte = 0;
+        if (valid && k0 < b) {
+            const uint64_t w = static_cast<const uint64_t*>(x)[off + (k0 >> 6)];
+            byte = (uint32_t)(w >> (k0 & 63)) & 0xffu;
+            if (b - k0 < 8) byte &= (1u << (b - k0)) - 1u;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) out[i] = ((byte >> i) & 1u) ? M::one() : M::zero();
+    } else if constexpr (XFMT == HSES_FMT_BF16) {
+        const uint16_t* p = static_cast<const uint16_t*>(x) + off;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint16_t h = (valid && k0 + i < b) ? p[k0 + i] : (uint16_t)0;
+            if constexpr (MATH == HSES_MATH_BF16)
+                out[i] = h;
+            else
+                out[i] = bf2f(h);
+        }
+    } else {
+        const float* p = static_cast<const float*>(x) + off;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) out[i] = M::cvt((valid && k0 + i < b) ? p[k0 + i] : 0.0f);
+    }
+}
+
+int launch_linear_small(LinParams& P, DeviceState* st, hipStream_t s);
+int launch_linear_pair(LinParams& P, DeviceState* st, hipStream_t s);
+
+}  // namespace hses

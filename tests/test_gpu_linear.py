@@ -1,0 +1,122 @@
+"""GPU parity of the batched perturbed forward (do_mm / lora_linear_batched).
+
+Reference: y_m = x_m W^T + (x_m B_m) A_m^T with the oracle's bit-exact factors,
+evaluated in float64 by brute force (eggroll.rs:419-446, snn.rs:665-685).
+Tolerances: fp32 math rel 1e-5 of the output scale; bf16 math compared with
+the same product on bf16-rounded W/B (rel 2e-3), and with the fp32 result
+within rel 2e-2 (the bf16-path bar)."""
+import numpy as np
+import pytest
+import torch
+
+from hyperscalees_amd._lib import FMT_BF16, FMT_BITS, FMT_F32, MATH_BF16, MATH_F32
+from tests import oracle_lib as O
+
+pytestmark = pytest.mark.gpu
+KEY = 0x9E3779B97F4A7C15
+
+
+def bf16_round(a):
+    t = torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(torch.bfloat16)
+    return t.to(torch.float32).numpy()
+
+
+def ref_forward(x3, W, A, B, rpm):
+    """x3 (T, n*rpm, b) -> (T, n*rpm, a) in float64."""
+    x3 = x3.astype(np.float64)
+    y = x3 @ W.astype(np.float64).T
+    n = A.shape[0]
+    for m in range(n):
+        xs = x3[:, m * rpm:(m + 1) * rpm, :]
+        y[:, m * rpm:(m + 1) * rpm, :] += (xs @ B[m].astype(np.float64)) @ A[m].astype(np.float64).T
+    return y
+
+
+def pack_bits(x3):
+    T, M, b = x3.shape
+    words = (b + 63) // 64
+    padded = np.zeros((T, M, words * 64), np.uint64)
+    padded[..., :b] = x3.astype(np.uint64)
+    w = (padded.reshape(T, M, words, 64) << np.arange(64, dtype=np.uint64)).sum(-1, dtype=np.uint64)
+    return torch.from_numpy(w.view(np.int64)).cuda()
+
+
+def run(hses_gpu, x3, W, r, sigma, n, rpm, tid_lo=0, fmt=FMT_F32, math=MATH_F32, epoch=0, nreuse=0):
+    T, M, b = x3.shape
+    if fmt == FMT_F32:
+        xt = torch.from_numpy(np.ascontiguousarray(x3, np.float32)).cuda()
+    elif fmt == FMT_BF16:
+        xt = torch.from_numpy(np.ascontiguousarray(x3, np.float32)).to(torch.bfloat16).cuda()
+    else:
+        xt = pack_bits(x3)
+    y = hses_gpu.perturbed_linear(xt, torch.from_numpy(W).cuda(), KEY, r, sigma, epoch, nreuse,
+                                  tid_lo, n, rpm, x_fmt=fmt, n_time=T, math=math)
+    torch.cuda.synchronize()
+    return y.cpu().numpy().reshape(T, M, -1)
+
+
+def factors(sigma, r, n, tid_lo, a, b, epoch=0, nreuse=0):
+    bs = O.load().or_base_sigma(sigma, r)
+    return O.lora_factors(bs, KEY, r, epoch, np.arange(tid_lo, tid_lo + n), a, b, noise_reuse=nreuse)
+
+
+def assert_close(y, ref, rel):
+    scale = np.abs(ref).max()
+    err = np.abs(y - ref).max()
+    assert err <= rel * scale, f"max err {err:.3e} > {rel:.1e} * {scale:.3e}"
+
+
+@pytest.mark.parametrize("n,rpm,T,a,b,r,tid_lo", [
+    (16, 16, 1, 1024, 1024, 1, 0),      # C2 layer shape, 16 members
+    (3, 64, 8, 128, 784, 4, 0),         # C1 fc1, time-major, 3 members
+    (5, 5, 3, 10, 100, 4, 3),           # members straddle tiles, odd tid_lo, ragged a/b
+    (7, 9, 1, 70, 33, 2, 1),
+    (4, 64, 1, 10, 128, 4, 6),          # C1 readout
+])
+def test_perturbed_linear_f32(hses_gpu, n, rpm, T, a, b, r, tid_lo):
+    rng = np.random.default_rng(n * 100 + b)
+    x3 = rng.standard_normal((T, n * rpm, b)).astype(np.float32)
+    W = (rng.standard_normal((a, b)) / np.sqrt(b)).astype(np.float32)
+    A, B = factors(0.02 * 10, r, n, tid_lo, a, b)
+    y = run(hses_gpu, x3, W, r, 0.2, n, rpm, tid_lo)
+    assert_close(y, ref_forward(x3, W, A, B, rpm), 1e-5)
+
+
+def test_perturbed_linear_spike_formats_agree(hses_gpu):
+    # Binary inputs are exact in every format: F32, BF16 and packed bits give
+    # the same bits for the same math mode.
+    rng = np.random.default_rng(7)
+    n, rpm, T, a, b, r = 4, 16, 4, 128, 784, 4
+    x3 = (rng.random((T, n * rpm, b)) < 0.2).astype(np.float32)
+    W = (rng.standard_normal((a, b)) / 28).astype(np.float32)
+    A, B = factors(0.02, r, n, 0, a, b)
+    ref = ref_forward(x3, W, A, B, rpm)
+    for math in (MATH_F32, MATH_BF16):
+        ys = [run(hses_gpu, x3, W, r, 0.02, n, rpm, fmt=f, math=math)
+              for f in (FMT_F32, FMT_BF16, FMT_BITS)]
+        np.testing.assert_array_equal(ys[0], ys[1])
+        np.testing.assert_array_equal(ys[0], ys[2])
+        if math == MATH_F32:
+            assert_close(ys[0], ref, 1e-5)
+        else:
+            refb = ref_forward(x3, bf16_round(W), A, bf16_round(B), rpm)
+            assert_close(ys[0], refb, 2e-3)
+            assert_close(ys[0], ref, 2e-2)
+
+
+def test_clean_path_is_plain_product(hses_gpu):
+    rng = np.random.default_rng(3)
+    x3 = rng.standard_normal((1, 40, 50)).astype(np.float32)
+    W = rng.standard_normal((30, 50)).astype(np.float32)
+    y = run(hses_gpu, x3, W, 4, 0.0, 8, 5)
+    assert_close(y, x3.astype(np.float64) @ W.T.astype(np.float64), 1e-5)
+
+
+def test_noise_reuse_epoch(hses_gpu):
+    rng = np.random.default_rng(4)
+    n, rpm, a, b, r = 6, 8, 16, 24, 2
+    x3 = rng.standard_normal((1, n * rpm, b)).astype(np.float32)
+    W = rng.standard_normal((a, b)).astype(np.float32)
+    A, B = factors(0.5, r, n, 0, a, b, epoch=5, nreuse=2)
+    y = run(hses_gpu, x3, W, r, 0.5, n, rpm, epoch=5, nreuse=2)
+    assert_close(y, ref_forward(x3, W, A, B, rpm), 1e-5)
