@@ -135,17 +135,21 @@ def perturbed_linear(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n, rows
     return out if n_time > 1 or x.dim() == 3 else out[0]
 
 
-def es_update(fit, tid_lo, key, rank, sigma, epoch, noise_reuse, a, b, scale, out=None):
-    """scale * sum_m fit[m] A_m B_m^T (factors regenerated in-kernel)."""
+def es_update(fit, tid_lo, key, rank, sigma, epoch, noise_reuse, a, b, scale, out=None,
+              accumulate=False, work=None):
+    """scale * sum_m fit[m] A_m B_m^T (factors regenerated in-kernel); adds into
+    `out` when accumulate is set."""
     _dev(fit, torch.float32, "fit")
     n = fit.numel()
     lib = _lib.load()
-    wbytes = lib.hses_es_update_workspace(a, b, rank, n)
-    work = torch.empty(max(int(wbytes), 1), dtype=torch.uint8, device=fit.device)
+    wbytes = int(lib.hses_es_update_workspace(a, b, rank, n))
+    if work is None or work.numel() < wbytes:
+        work = torch.empty(max(wbytes, 1), dtype=torch.uint8, device=fit.device)
     if out is None:
-        out = torch.empty((a, b), dtype=torch.float32, device=fit.device)
+        out = torch.zeros((a, b), dtype=torch.float32, device=fit.device)
     _lib.call("hses_es_update", _p(fit), n, tid_lo, key & (2**64 - 1), rank, sigma, epoch,
-              noise_reuse, a, b, scale, _p(out), _p(work), int(wbytes), _stream())
+              noise_reuse, a, b, scale, int(bool(accumulate)), _p(out), _p(work), wbytes,
+              _stream())
     return out
 
 

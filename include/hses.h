@@ -137,12 +137,14 @@ int hses_perturbed_linear(const void *d_x, int32_t x_fmt, int64_t x_stride, int6
  * over members m in [0, n) with thread ids tid_lo+m, factors regenerated
  * in-kernel.  do_updates uses scale = -sqrt(N)/N (N = population size).
  * Deterministic: a fixed split-K partition and a fixed-order second-stage
- * reduction, no atomics.  d_work must hold hses_es_update_workspace(...)
- * bytes. */
+ * reduction, no atomics.  accumulate != 0 adds into d_grad (the K-chunk
+ * loop of accumulated_update) instead of overwriting it.  d_work must hold
+ * hses_es_update_workspace(...) bytes. */
 size_t hses_es_update_workspace(int32_t a, int32_t b, int32_t rank, int32_t n);
 int hses_es_update(const float *d_f, int32_t n, int32_t tid_lo, uint64_t key, int32_t rank,
                    float sigma, int32_t epoch, int32_t noise_reuse, int32_t a, int32_t b,
-                   float scale, float *d_grad, void *d_work, size_t work_bytes, void *stream);
+                   float scale, int32_t accumulate, float *d_grad, void *d_work,
+                   size_t work_bytes, void *stream);
 
 /* ---- fitness, z-score, solver ----------------------------------------- */
 
