@@ -257,12 +257,24 @@ int launch_linear_small(LinParams& P, DeviceState* st, hipStream_t s) {
 
 using namespace hses;
 
+extern "C" size_t hses_perturbed_linear_workspace(int32_t a, int32_t b, int32_t rank, int32_t n,
+                                                  int32_t rows_per_member, int32_t n_time,
+                                                  int32_t math) {
+    if (a < 1 || b < 1 || n < 1 || rank < 16 || rank % 16 || rank > 128 || a > 128 ||
+        math != HSES_MATH_BF16)
+        return 0;  // served by k_linear_small, which needs no workspace
+    DeviceState* st;
+    if (get_state(&st)) return 0;
+    return linear_pair_workspace(st, a, b, rank, n);
+}
+
 extern "C" int hses_perturbed_linear(const void* d_x, int32_t x_fmt, int64_t x_stride,
                                      int64_t x_plane, int32_t n_time, const float* d_W, int32_t a,
                                      int32_t b, uint64_t key, int32_t rank, float sigma,
                                      int32_t epoch, int32_t noise_reuse, int32_t tid_lo, int32_t n,
                                      int32_t rows_per_member, float* d_y, int64_t y_stride,
-                                     int64_t y_plane, int32_t math, void* stream) {
+                                     int64_t y_plane, int32_t math, void* d_work,
+                                     size_t work_bytes, void* stream) {
     HSES_REQUIRE(x_fmt == HSES_FMT_F32 || x_fmt == HSES_FMT_BF16 || x_fmt == HSES_FMT_BITS,
                  "x_fmt must be F32, BF16 or BITS");
     HSES_REQUIRE(math == HSES_MATH_F32 || math == HSES_MATH_BF16, "unknown math mode");
@@ -309,7 +321,7 @@ extern "C" int hses_perturbed_linear(const void* d_x, int32_t x_fmt, int64_t x_s
     P.log_exc = st->d_log_exc;
     P.cos_exc = st->d_cos_exc;
     hipStream_t s = (hipStream_t)stream;
-    rc = launch_linear_pair(P, st, s);
+    rc = launch_linear_pair(P, st, s, d_work, work_bytes);
     if (rc != HSES_ERR_UNSUPPORTED) return rc;
     rc = launch_linear_small(P, st, s);
     if (rc == HSES_ERR_UNSUPPORTED)

@@ -101,6 +101,7 @@ __device__ __forceinline__ void load_x_seg(const void* x, int64_t off, bool vali
 }
 
 int launch_linear_small(LinParams& P, DeviceState* st, hipStream_t s);
-int launch_linear_pair(LinParams& P, DeviceState* st, hipStream_t s);
+int launch_linear_pair(LinParams& P, DeviceState* st, hipStream_t s, void* work, size_t work_bytes);
+size_t linear_pair_workspace(const DeviceState* st, int32_t a, int32_t b, int32_t r, int32_t n);
 
 }  // namespace hses

@@ -33,6 +33,19 @@ def _dev(t, dtype, name):
     return t
 
 
+_WORK = {}
+
+
+def _workspace(nbytes, device):
+    """A cached device workspace of at least nbytes (one per device and stream)."""
+    key = (str(device), torch.cuda.current_stream().cuda_stream)
+    buf = _WORK.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+        _WORK[key] = buf
+    return buf
+
+
 def fmt_width(fmt, width):
     """Storage units per row of `width` activations in format `fmt`."""
     return (width + 63) // 64 if fmt == FMT_BITS else width
@@ -129,9 +142,12 @@ def perturbed_linear(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n, rows
         raise ValueError(f"x has shape {tuple(x.shape)}, expected ({n_time}, {M}, {units})")
     if out is None:
         out = torch.empty((n_time, M, a), dtype=torch.float32, device=W.device)
+    wbytes = int(_lib.load().hses_perturbed_linear_workspace(a, b, rank, n, rows_per_member,
+                                                              n_time, math))
+    work = _workspace(wbytes, W.device)
     _lib.call("hses_perturbed_linear", _p(x), x_fmt, units, M * units, n_time, _p(W), a, b,
               key & (2**64 - 1), rank, sigma, epoch, noise_reuse, tid_lo, n, rows_per_member,
-              _p(out), a, M * a, math, _stream())
+              _p(out), a, M * a, math, _p(work), wbytes, _stream())
     return out if n_time > 1 or x.dim() == 3 else out[0]
 
 
@@ -144,7 +160,7 @@ def es_update(fit, tid_lo, key, rank, sigma, epoch, noise_reuse, a, b, scale, ou
     lib = _lib.load()
     wbytes = int(lib.hses_es_update_workspace(a, b, rank, n))
     if work is None or work.numel() < wbytes:
-        work = torch.empty(max(wbytes, 1), dtype=torch.uint8, device=fit.device)
+        work = _workspace(wbytes, fit.device)
     if out is None:
         out = torch.zeros((a, b), dtype=torch.float32, device=fit.device)
     _lib.call("hses_es_update", _p(fit), n, tid_lo, key & (2**64 - 1), rank, sigma, epoch,

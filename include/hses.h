@@ -121,13 +121,19 @@ int hses_lif_scan(const float *d_cur, const float *d_v0, int32_t T, int64_t rows
  * Member m's rows are rows [m*rows_per_member, (m+1)*rows_per_member); for
  * time-major activations (T, M, b) pass rows_per_member = slots and
  * n_time = T with plane strides x_plane / y_plane (rows of member m at time
- * t are t*plane + m*slots + s).  sigma=0 or rank=0 gives the clean x W^T. */
+ * t are t*plane + m*slots + s).  sigma=0 or rank=0 gives the clean x W^T.
+ * d_work must hold hses_perturbed_linear_workspace(...) bytes (a bf16 copy of W
+ * and, for large ranks, one per-workgroup staging slot for a pair's B factor;
+ * the (n, b, r) factor tensor itself is never materialised).  Large ranks
+ * (r a multiple of 16, r <= 128, a <= 128) need math = HSES_MATH_BF16. */
+size_t hses_perturbed_linear_workspace(int32_t a, int32_t b, int32_t rank, int32_t n,
+                                       int32_t rows_per_member, int32_t n_time, int32_t math);
 int hses_perturbed_linear(const void *d_x, int32_t x_fmt, int64_t x_stride, int64_t x_plane,
                           int32_t n_time, const float *d_W, int32_t a, int32_t b,
                           uint64_t key, int32_t rank, float sigma, int32_t epoch,
                           int32_t noise_reuse, int32_t tid_lo, int32_t n, int32_t rows_per_member,
                           float *d_y, int64_t y_stride, int64_t y_plane, int32_t math,
-                          void *stream);
+                          void *d_work, size_t work_bytes, void *stream);
 
 /* ---- ES update ------------------------------------------------------- */
 

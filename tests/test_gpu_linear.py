@@ -120,3 +120,44 @@ def test_noise_reuse_epoch(hses_gpu):
     A, B = factors(0.5, r, n, 0, a, b, epoch=5, nreuse=2)
     y = run(hses_gpu, x3, W, r, 0.5, n, rpm, epoch=5, nreuse=2)
     assert_close(y, ref_forward(x3, W, A, B, rpm), 1e-5)
+
+
+def ref_forward_bf16(x3, W, A, B, rpm):
+    """The bf16 pair kernel's arithmetic: bf16 W, B, A and a bf16 rounding of
+    (sign * x B) before the second product; float64 accumulation otherwise."""
+    Wb, Bb, Ab = bf16_round(W), bf16_round(B), bf16_round(A)
+    x64 = x3.astype(np.float64)
+    y = x64 @ Wb.astype(np.float64).T
+    n = A.shape[0]
+    for m in range(n):
+        xs = x64[:, m * rpm:(m + 1) * rpm, :]
+        xb = (xs @ Bb[m].astype(np.float64)).astype(np.float32)
+        y[:, m * rpm:(m + 1) * rpm, :] += bf16_round(xb).astype(np.float64) @ Ab[m].astype(np.float64).T
+    return y
+
+
+@pytest.mark.parametrize("n,rpm,T,a,b,r,tid_lo,fmt", [
+    (4, 64, 16, 128, 784, 128, 0, FMT_BITS),   # C3 fc1 (two pairs)
+    (3, 64, 16, 128, 128, 128, 1, FMT_BITS),   # C3 fc2, partial pairs at both ends
+    (4, 64, 1, 10, 128, 128, 0, FMT_F32),      # C3 readout on rates
+    (2, 40, 3, 96, 200, 64, 0, FMT_BF16),      # rows not a multiple of the block
+    (5, 7, 2, 33, 50, 16, 2, FMT_F32),
+])
+def test_perturbed_linear_pair_kernel(hses_gpu, n, rpm, T, a, b, r, tid_lo, fmt):
+    rng = np.random.default_rng(n * 1000 + a + r)
+    if fmt == FMT_BITS:
+        x3 = (rng.random((T, n * rpm, b)) < 0.2).astype(np.float32)
+    else:
+        x3 = (rng.integers(0, 17, (T, n * rpm, b)) / 16.0).astype(np.float32)  # rates, exact in bf16
+    W = (rng.standard_normal((a, b)) / np.sqrt(b)).astype(np.float32)
+    A, B = factors(0.2, r, n, tid_lo, a, b)
+    y = run(hses_gpu, x3, W, r, 0.2, n, rpm, tid_lo, fmt=fmt, math=MATH_BF16)
+    assert_close(y, ref_forward_bf16(x3, W, A, B, rpm), 2e-3)
+    assert_close(y, ref_forward(x3, W, A, B, rpm), 2e-2)
+
+
+def test_device_properties(hses_gpu):
+    p = torch.cuda.get_device_properties(0)
+    print("device", p.name, "CUs", p.multi_processor_count,
+          "smem/block", getattr(p, "shared_memory_per_block", None),
+          "smem/mp", getattr(p, "shared_memory_per_multiprocessor", None))
