@@ -29,8 +29,9 @@ PROTOTYPES = {
                                          c_i32, c_i32, c_vp, c_vp, c_vp]),
     "hses_nonlora_noise": (ctypes.c_int, [c_f32, c_u64, c_i32, c_i32, c_i32, c_vp, c_i32, c_i32,
                                           c_i32, c_vp, c_vp]),
-    "hses_poisson_encode": (ctypes.c_int, [c_vp, c_i64, c_i32, c_i64, c_i32, c_u32, c_u32, c_u32,
-                                           c_u32, c_vp, c_i32, c_i64, c_vp]),
+    "hses_poisson_encode": (ctypes.c_int, [c_vp, c_i64, c_vp, c_i64, c_i32, c_i64, c_i32, c_u32, c_u32,
+                                           c_u32, c_u32, c_vp, c_i32, c_i64, c_vp]),
+    "hses_spike_rate": (ctypes.c_int, [c_vp, c_i32, c_i64, c_i32, c_i64, c_i32, c_vp, c_vp]),
     "hses_lif_scan": (ctypes.c_int, [c_vp, c_vp, c_i32, c_i64, c_i32, c_i64, c_f32, c_f32, c_vp,
                                      c_i32, c_i64, c_vp, c_vp]),
     "hses_perturbed_linear": (ctypes.c_int, [c_vp, c_i32, c_i64, c_i64, c_i32, c_vp, c_i32, c_i32,

@@ -27,7 +27,8 @@ __device__ __forceinline__ uint32_t poisson_threshold(float p) {
 }
 
 template <int FMT>
-__global__ __launch_bounds__(256) void k_poisson(const float* __restrict__ p, int64_t rows,
+__global__ __launch_bounds__(256) void k_poisson(const float* __restrict__ p, int64_t p_rows,
+                                                 const int32_t* __restrict__ prow, int64_t rows,
                                                  int32_t in_dim, int64_t p_stride, int32_t T,
                                                  uint32_t mix, void* __restrict__ out,
                                                  int64_t out_stride) {
@@ -41,7 +42,8 @@ __global__ __launch_bounds__(256) void k_poisson(const float* __restrict__ p, in
     const bool valid = col < in_dim;
     uint32_t K = 0, x = 0;
     if (valid) {
-        K = poisson_threshold(p[row * p_stride + col]);
+        const int64_t src = prow ? (int64_t)prow[row] : row;
+        K = (src >= 0 && src < p_rows) ? poisson_threshold(p[src * p_stride + col]) : 0u;
         const uint32_t idx = (uint32_t)(row * in_dim + col);
         x = 1000000007u * idx + mix + 0x9E3779B9u;
     }
@@ -83,24 +85,78 @@ __global__ __launch_bounds__(256) void k_lif(const float* __restrict__ cur,
     if (valid && v_out) v_out[row * h + col] = v;
 }
 
+// snn.rs:274: spikes.mean_dim(0) -- the count of spikes over T divided by T.
+template <int FMT>
+__global__ __launch_bounds__(256) void k_spike_rate(const void* __restrict__ spk, int64_t stride,
+                                                    int32_t T, int64_t rows, int32_t h,
+                                                    float* __restrict__ rate) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= rows * h) return;
+    const int64_t row = e / h;
+    const int32_t c = (int32_t)(e % h);
+    const int64_t plane = rows * stride;
+    int32_t cnt = 0;
+    for (int32_t t = 0; t < T; ++t) {
+        const int64_t base = t * plane + row * stride;
+        if constexpr (FMT == HSES_FMT_BITS)
+            cnt += (int32_t)((static_cast<const uint64_t*>(spk)[base + (c >> 6)] >> (c & 63)) & 1ull);
+        else if constexpr (FMT == HSES_FMT_F32)
+            cnt += static_cast<const float*>(spk)[base + c] != 0.0f;
+        else if constexpr (FMT == HSES_FMT_BF16)
+            cnt += static_cast<const uint16_t*>(spk)[base + c] != 0;
+        else
+            cnt += static_cast<const uint8_t*>(spk)[base + c] != 0;
+    }
+    rate[e] = __fdiv_rn((float)cnt, (float)T);
+}
+
 }  // namespace hses
 
 using namespace hses;
+
+extern "C" int hses_spike_rate(const void* d_spikes, int32_t fmt, int64_t spk_stride, int32_t T,
+                               int64_t rows, int32_t h, float* d_rate, void* stream) {
+    HSES_REQUIRE(fmt >= HSES_FMT_F32 && fmt <= HSES_FMT_BITS, "unknown spike format");
+    HSES_REQUIRE(rows >= 0 && h >= 0 && T >= 1, "bad sizes");
+    if (rows == 0 || h == 0) return HSES_OK;
+    HSES_REQUIRE(d_spikes && d_rate, "NULL pointer");
+    HSES_REQUIRE(spk_stride >= fmt_row_units(fmt, h), "spk_stride too small for format");
+    const int64_t blocks = (rows * h + 255) / 256;
+    HSES_REQUIRE(blocks < (1ll << 31), "grid too large");
+    hipStream_t s = (hipStream_t)stream;
+    switch (fmt) {
+        case HSES_FMT_F32:
+            hipLaunchKernelGGL(k_spike_rate<HSES_FMT_F32>, dim3(blocks), dim3(256), 0, s, d_spikes, spk_stride, T, rows, h, d_rate);
+            break;
+        case HSES_FMT_BF16:
+            hipLaunchKernelGGL(k_spike_rate<HSES_FMT_BF16>, dim3(blocks), dim3(256), 0, s, d_spikes, spk_stride, T, rows, h, d_rate);
+            break;
+        case HSES_FMT_U8:
+            hipLaunchKernelGGL(k_spike_rate<HSES_FMT_U8>, dim3(blocks), dim3(256), 0, s, d_spikes, spk_stride, T, rows, h, d_rate);
+            break;
+        default:
+            hipLaunchKernelGGL(k_spike_rate<HSES_FMT_BITS>, dim3(blocks), dim3(256), 0, s, d_spikes, spk_stride, T, rows, h, d_rate);
+            break;
+    }
+    HSES_CHECK_HIP(hipGetLastError());
+    return HSES_OK;
+}
 
 static int64_t wave_blocks(int64_t rows, int32_t width) {
     const int64_t waves = rows * ((width + 63) / 64);
     return (waves + 3) / 4;  // 4 waves per 256-thread block
 }
 
-extern "C" int hses_poisson_encode(const float* d_p, int64_t rows, int32_t in_dim,
-                                   int64_t p_stride, int32_t T, uint32_t s0, uint32_t s1,
-                                   uint32_t s2, uint32_t s3, void* d_out, int32_t fmt,
+extern "C" int hses_poisson_encode(const float* d_p, int64_t p_rows, const int32_t* d_rows, int64_t rows,
+                                   int32_t in_dim, int64_t p_stride, int32_t T, uint32_t s0,
+                                   uint32_t s1, uint32_t s2, uint32_t s3, void* d_out, int32_t fmt,
                                    int64_t out_stride, void* stream) {
     HSES_REQUIRE(rows >= 0 && in_dim >= 0 && T >= 0, "negative size");
     HSES_REQUIRE(fmt >= HSES_FMT_F32 && fmt <= HSES_FMT_BITS, "unknown spike format");
     if (rows == 0 || in_dim == 0 || T == 0) return HSES_OK;
     HSES_REQUIRE(d_p && d_out, "NULL pointer");
     HSES_REQUIRE(p_stride >= in_dim, "p_stride < in_dim");
+    HSES_REQUIRE(d_rows || p_rows >= rows, "p_rows < rows without a row index");
     HSES_REQUIRE(out_stride >= fmt_row_units(fmt, in_dim), "out_stride too small for format");
     // The reference seeds with the flat index as u32 (poisson_encode_fused_oxide.rs:68-83).
     HSES_REQUIRE(rows * in_dim <= (int64_t)UINT32_MAX, "rows*in_dim exceeds the u32 index range");
@@ -110,20 +166,20 @@ extern "C" int hses_poisson_encode(const float* d_p, int64_t rows, int32_t in_di
     hipStream_t s = (hipStream_t)stream;
     switch (fmt) {
         case HSES_FMT_F32:
-            hipLaunchKernelGGL(k_poisson<HSES_FMT_F32>, dim3(blocks), dim3(256), 0, s, d_p, rows,
-                               in_dim, p_stride, T, mix, d_out, out_stride);
+            hipLaunchKernelGGL(k_poisson<HSES_FMT_F32>, dim3(blocks), dim3(256), 0, s, d_p, p_rows, d_rows,
+                               rows, in_dim, p_stride, T, mix, d_out, out_stride);
             break;
         case HSES_FMT_BF16:
-            hipLaunchKernelGGL(k_poisson<HSES_FMT_BF16>, dim3(blocks), dim3(256), 0, s, d_p, rows,
-                               in_dim, p_stride, T, mix, d_out, out_stride);
+            hipLaunchKernelGGL(k_poisson<HSES_FMT_BF16>, dim3(blocks), dim3(256), 0, s, d_p, p_rows, d_rows,
+                               rows, in_dim, p_stride, T, mix, d_out, out_stride);
             break;
         case HSES_FMT_U8:
-            hipLaunchKernelGGL(k_poisson<HSES_FMT_U8>, dim3(blocks), dim3(256), 0, s, d_p, rows,
-                               in_dim, p_stride, T, mix, d_out, out_stride);
+            hipLaunchKernelGGL(k_poisson<HSES_FMT_U8>, dim3(blocks), dim3(256), 0, s, d_p, p_rows, d_rows,
+                               rows, in_dim, p_stride, T, mix, d_out, out_stride);
             break;
         default:
-            hipLaunchKernelGGL(k_poisson<HSES_FMT_BITS>, dim3(blocks), dim3(256), 0, s, d_p, rows,
-                               in_dim, p_stride, T, mix, d_out, out_stride);
+            hipLaunchKernelGGL(k_poisson<HSES_FMT_BITS>, dim3(blocks), dim3(256), 0, s, d_p, p_rows, d_rows,
+                               rows, in_dim, p_stride, T, mix, d_out, out_stride);
             break;
     }
     HSES_CHECK_HIP(hipGetLastError());

@@ -102,27 +102,44 @@ def nonlora_noise(base_sigma, key, epoch, noise_reuse, tids, a, b, device="cuda"
     return out
 
 
-def poisson_encode(p, T, seeds=(0, 0, 0, 0), fmt=FMT_F32, out=None):
-    """(rows, in_dim) probabilities -> (T, rows, width) spikes in `fmt`."""
+def poisson_encode(p, T, seeds=(0, 0, 0, 0), fmt=FMT_F32, out=None, rows_index=None):
+    """(rows, in_dim) probabilities -> (T, rows, width) spikes in `fmt`.  With
+    rows_index (int32, length R) output row i encodes p[rows_index[i]]."""
     _dev(p, torch.float32, "p")
-    rows, in_dim = p.shape
+    prow, in_dim = p.shape
+    rows = prow
+    if rows_index is not None:
+        _dev(rows_index, torch.int32, "rows_index")
+        rows = rows_index.numel()
     units = fmt_width(fmt, in_dim)
     if out is None:
         out = torch.empty((T, rows, units), dtype=_FMT_DTYPE[fmt], device=p.device)
     s0, s1, s2, s3 = (int(s) & 0xFFFFFFFF for s in seeds)
-    _lib.call("hses_poisson_encode", _p(p), rows, in_dim, in_dim, T, s0, s1, s2, s3, _p(out),
-              fmt, units, _stream())
+    _lib.call("hses_poisson_encode", _p(p), prow, _p(rows_index), rows, in_dim, in_dim, T, s0, s1, s2,
+              s3, _p(out), fmt, units, _stream())
     return out
 
 
-def lif_scan(cur, tau_m, v_th, v0=None, fmt=FMT_F32, want_v=False):
+def spike_rate(spikes, fmt, h, out=None):
+    """(T, rows, units) spikes in `fmt` -> (rows, h) fp32 mean over T."""
+    _dev(spikes, _FMT_DTYPE[fmt], "spikes")
+    T, rows, units = spikes.shape
+    if out is None:
+        out = torch.empty((rows, h), dtype=torch.float32, device=spikes.device)
+    _lib.call("hses_spike_rate", _p(spikes), fmt, units, T, rows, h, _p(out), _stream())
+    return out
+
+
+def lif_scan(cur, tau_m, v_th, v0=None, fmt=FMT_F32, want_v=False, out=None):
     """cur (T, rows, h) fp32 -> spikes (T, rows, width) in `fmt` [, v_final (rows, h)]."""
     _dev(cur, torch.float32, "cur")
     T, rows, h = cur.shape
     if v0 is not None:
         _dev(v0, torch.float32, "v0")
     units = fmt_width(fmt, h)
-    spk = torch.empty((T, rows, units), dtype=_FMT_DTYPE[fmt], device=cur.device)
+    spk = out if out is not None else torch.empty((T, rows, units), dtype=_FMT_DTYPE[fmt],
+                                                  device=cur.device)
+    _dev(spk, _FMT_DTYPE[fmt], "spikes")
     v_out = torch.empty((rows, h), dtype=torch.float32, device=cur.device) if want_v else None
     _lib.call("hses_lif_scan", _p(cur), _p(v0), T, rows, h, h, tau_m, v_th, _p(spk), fmt, units,
               _p(v_out), _stream())
@@ -142,6 +159,9 @@ def perturbed_linear(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n, rows
         raise ValueError(f"x has shape {tuple(x.shape)}, expected ({n_time}, {M}, {units})")
     if out is None:
         out = torch.empty((n_time, M, a), dtype=torch.float32, device=W.device)
+    _dev(out, torch.float32, "out")
+    if out.numel() != n_time * M * a:
+        raise ValueError("out has the wrong size")
     wbytes = int(_lib.load().hses_perturbed_linear_workspace(a, b, rank, n, rows_per_member,
                                                               n_time, math))
     work = _workspace(wbytes, W.device)

@@ -1,0 +1,174 @@
+"""SNN-MLP EggRoll ES step on the GPU, composed from the libhses kernels.
+
+One step (the per-chunk body of accumulate_train.rs:770-938 with the whole
+population in one chunk, and the deterministic noiser stream):
+  1. Poisson-encode each member's samples into bit-packed spike trains
+     (poisson_encode_fused_oxide.rs:61-106);
+  2. hidden layers: perturbed linear (eggroll.rs:419-446, snn.rs:665-685)
+     then the LIF scan (snn.rs:53-97), spikes kept bit-packed;
+  3. readout on the mean rate (snn.rs:274-280), log-likelihood fitness
+     averaged over the member's samples (snn_mnist.rs:180-201);
+  4. z-score (eggroll.rs:967-992), ES gradient per layer
+     (eggroll.rs:353-404) and one solver step (noiser.rs:155-225).
+The model is the reference SnnModel generalised to any number of hidden LIF
+layers (the JAX model is depth-generic); every layer is an MM parameter with
+its own base key (i+1)*0x9E3779B97F4A7C15 (accumulate_train.rs:603-608).
+"""
+import math
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+from . import kernels as K
+from ._lib import ADAMW, FMT_BITS, FMT_F32, MATH_BF16, SGD
+
+KEY_MUL = 0x9E3779B97F4A7C15
+
+
+def layer_keys(n_layers):
+    return [((i + 1) * KEY_MUL) % 2**64 for i in range(n_layers)]
+
+
+@dataclass
+class SnnConfig:
+    dims: tuple = (784, 128, 128, 128, 10)
+    T: int = 16
+    rows: int = 64                 # samples per member
+    n: int = 8192                  # population size N
+    rank: int = 128
+    sigma: float = 0.02
+    tau_m: float = 10.0            # leak 1/tau = 0.1, i.e. decay 0.9
+    v_th: float = 1.0
+    noise_reuse: int = 0
+    math: int = MATH_BF16
+    solver: int = ADAMW
+    lr: float = 0.01
+    beta1: float = 0.9
+    beta2: float = 0.999
+    eps: float = 1e-8
+    weight_decay: float = 1e-4
+    poisson_seed: tuple = (0, 0, 0, 0)
+    keys: list = field(default_factory=list)
+
+    def __post_init__(self):
+        if not self.keys:
+            self.keys = layer_keys(len(self.dims) - 1)
+
+
+def sample_index(seed, n, rows, pool_size):
+    """Per-(member, slot) pool index: splitmix64(seed, member*rows+slot) mod pool."""
+    c = (np.arange(n * rows, dtype=np.uint64) + np.uint64(seed) * np.uint64(0x9E3779B97F4A7C15))
+    z = c + np.uint64(0x9E3779B97F4A7C15)
+    z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+    z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+    z = z ^ (z >> np.uint64(31))
+    return (z % np.uint64(pool_size)).astype(np.int32)
+
+
+def synthetic_pool(pool_size, in_dim, classes, seed=0, zero_frac=0.7):
+    """Sparse intensity vectors (70% exact zeros, rest U(0,1)) and uniform labels."""
+    rng = np.random.default_rng(seed)
+    x = rng.random((pool_size, in_dim), dtype=np.float32)
+    x[rng.random((pool_size, in_dim)) < zero_frac] = 0.0
+    y = rng.integers(0, classes, pool_size).astype(np.int32)
+    return x, y
+
+
+# With W ~ N(0, 1/fan_in), v_th = 1 and leak 0.1 the hidden layers fire at
+# ~1e-6.  Per-layer gains (12, 18, 20 for the hidden layers, 10 for the
+# readout) keep every hidden layer of the 784-128-128-128-10 model at 7-9%
+# firing so the spikes carry information.  The gains change no arithmetic cost.
+ACTIVE_GAIN = (12.0, 18.0, 20.0, 10.0)
+
+
+def init_weights(dims, seed=0, gain=1.0):
+    """W_l ~ N(0, gain_l^2/fan_in) (Mm::new, common.rs:113-121, has gain 1), from
+    a seeded fixture RNG.  `gain` is a scalar or one value per layer."""
+    rng = np.random.default_rng(seed + 1)
+    L = len(dims) - 1
+    gains = list(gain) if isinstance(gain, (tuple, list)) else [gain] * L
+    if len(gains) != L:
+        gains = (gains + [gains[-1]] * L)[:L]
+    return [(gains[i] * rng.standard_normal((dims[i + 1], dims[i])) / np.sqrt(dims[i])).astype(np.float32)
+            for i in range(L)]
+
+
+class SnnEs:
+    """Device-resident SNN-MLP population evaluation and ES update."""
+
+    def __init__(self, cfg, weights, pool, pool_labels, index, device="cuda"):
+        self.cfg = cfg
+        c = cfg
+        self.dev = device
+        self.W = [torch.as_tensor(w, dtype=torch.float32).to(device).contiguous() for w in weights]
+        self.pool = torch.as_tensor(pool, dtype=torch.float32).to(device).contiguous()
+        idx = torch.as_tensor(index, dtype=torch.int32).to(device).contiguous()
+        self.index = idx
+        self.labels = torch.as_tensor(pool_labels, dtype=torch.int32).to(device)[idx.long()].contiguous()
+        M = c.n * c.rows
+        self.M = M
+        L = len(c.dims) - 1
+        self.L = L
+        # bit-packed spikes of the input and of every hidden layer
+        self.spk = [torch.empty((c.T, M, K.fmt_width(FMT_BITS, d)), dtype=torch.int64, device=device)
+                    for d in c.dims[:-1]]
+        hmax = max(c.dims[1:-1]) if L > 1 else 1
+        self.cur = torch.empty((c.T, M, hmax), dtype=torch.float32, device=device)
+        self.rate = torch.empty((M, c.dims[-2]), dtype=torch.float32, device=device)
+        self.logits = torch.empty((M, c.dims[-1]), dtype=torch.float32, device=device)
+        self.grads = [torch.zeros_like(w) for w in self.W]
+        self.m = [torch.zeros_like(w) for w in self.W]
+        self.v = [torch.zeros_like(w) for w in self.W]
+        self.step_t = 0
+
+    # -- forward -------------------------------------------------------------
+    def poisson(self):
+        c = self.cfg
+        K.poisson_encode(self.pool, c.T, c.poisson_seed, FMT_BITS, out=self.spk[0],
+                         rows_index=self.index)
+
+    def hidden_layer(self, l, epoch):
+        c = self.cfg
+        a = c.dims[l + 1]
+        cur = self.cur[:, :, :a] if a == self.cur.shape[2] else \
+            self.cur.view(-1)[: c.T * self.M * a].view(c.T, self.M, a)
+        K.perturbed_linear(self.spk[l], self.W[l], c.keys[l], c.rank, c.sigma, epoch,
+                           c.noise_reuse, 0, c.n, c.rows, x_fmt=FMT_BITS, n_time=c.T,
+                           math=c.math, out=cur)
+        K.lif_scan(cur, c.tau_m, c.v_th, fmt=FMT_BITS, out=self.spk[l + 1])
+
+    def readout(self, epoch):
+        c = self.cfg
+        K.spike_rate(self.spk[self.L - 1], FMT_BITS, c.dims[-2], out=self.rate)
+        K.perturbed_linear(self.rate, self.W[-1], c.keys[-1], c.rank, c.sigma, epoch,
+                           c.noise_reuse, 0, c.n, c.rows, x_fmt=FMT_F32, n_time=1, math=c.math,
+                           out=self.logits.view(1, self.M, -1))
+        return K.member_loglik(self.logits, self.labels, c.n, c.rows)
+
+    def forward(self, epoch=0):
+        """Raw fitness of every member (N,)."""
+        self.poisson()
+        for l in range(self.L - 1):
+            self.hidden_layer(l, epoch)
+        return self.readout(epoch)
+
+    # -- update --------------------------------------------------------------
+    def update(self, raw_fit, epoch=0):
+        c = self.cfg
+        z, _ = K.convert_fitnesses(raw_fit)
+        scale = np.float32(-math.sqrt(c.n) / c.n)   # -g * sqrt(N) with g = (1/N) sum (eggroll.rs:403)
+        self.step_t += 1
+        for l in range(self.L):
+            a, b = self.W[l].shape
+            K.es_update(z, 0, c.keys[l], c.rank, c.sigma, epoch, c.noise_reuse, a, b, scale,
+                        out=self.grads[l])
+            K.solver_step(c.solver, c.lr, self.W[l], self.grads[l], self.m[l], self.v[l],
+                          step_t=self.step_t, beta1=c.beta1, beta2=c.beta2, eps=c.eps,
+                          wd=c.weight_decay if c.solver == ADAMW else 0.0)
+        return z
+
+    def step(self, epoch=0):
+        fit = self.forward(epoch)
+        self.update(fit, epoch)
+        return fit

@@ -96,10 +96,21 @@ int hses_nonlora_noise(float base_sigma, uint64_t key, int32_t epoch, int32_t no
  * spike[t][row][col] = u_t < p[row][col], u from the per-element xorshift32
  * stream.  p rows are p_stride floats apart; output rows are out_stride
  * elements apart (words for HSES_FMT_BITS); time planes are rows*out_stride
- * apart. */
-int hses_poisson_encode(const float *d_p, int64_t rows, int32_t in_dim, int64_t p_stride,
-                        int32_t T, uint32_t s0, uint32_t s1, uint32_t s2, uint32_t s3,
-                        void *d_out, int32_t fmt, int64_t out_stride, void *stream);
+ * apart.  If d_rows is not NULL, output row i encodes input row d_rows[i]
+ * (the batch gather train_img.select(0, idx) of accumulate_train.rs:726-735);
+ * an index outside [0, p_rows) encodes as an all-zero row.  Without d_rows,
+ * p_rows must be >= rows.  The stream index is always the output position
+ * i*in_dim + col. */
+int hses_poisson_encode(const float *d_p, int64_t p_rows, const int32_t *d_rows, int64_t rows,
+                        int32_t in_dim,
+                        int64_t p_stride, int32_t T, uint32_t s0, uint32_t s1, uint32_t s2,
+                        uint32_t s3, void *d_out, int32_t fmt, int64_t out_stride, void *stream);
+
+/* Mean firing rate over time (snn.rs:274, spikes.mean_dim(0)):
+ * d_rate[row][c] = (number of spikes of (row, c) over T) / T, spikes in `fmt`
+ * with row stride spk_stride (units) and time planes rows*spk_stride apart. */
+int hses_spike_rate(const void *d_spikes, int32_t fmt, int64_t spk_stride, int32_t T,
+                    int64_t rows, int32_t h, float *d_rate, void *stream);
 
 /* run_lif (burn_impl/hyperscalees-models/src/snn.rs:53-97) / lif_fused
  * (burn_impl/hyperscalees-kernels/src/lif_fused_oxide.rs:37-70, host oxide.rs:489-543):

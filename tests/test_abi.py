@@ -50,14 +50,14 @@ def test_validation_rejects_bad_arguments_without_a_gpu():
     _expect_invalid("hses_bm_eval", 2**24 - 4, 8, NULL, NULL, NULL, NULL)
     _expect_invalid("hses_lora_factors", 0.1, 1, 4, 0, -1, 0, NULL, 2, 3, 4, NULL, NULL, NULL)
     _expect_invalid("hses_lora_factors", 0.1, 1, 4, 0, 0, 0, NULL, 2, 3, 4, NULL, NULL, NULL)
-    _expect_invalid("hses_poisson_encode", NULL, -1, 784, 784, 8, 0, 0, 0, 0, NULL, 0, 784, NULL)
-    _expect_invalid("hses_poisson_encode", ctypes.c_void_p(16), 4, 784, 700, 8, 0, 0, 0, 0,
+    _expect_invalid("hses_poisson_encode", NULL, 0, NULL, -1, 784, 784, 8, 0, 0, 0, 0, NULL, 0, 784, NULL)
+    _expect_invalid("hses_poisson_encode", ctypes.c_void_p(16), 4, NULL, 4, 784, 700, 8, 0, 0, 0, 0,
                     ctypes.c_void_p(16), 0, 784, NULL)
-    _expect_invalid("hses_poisson_encode", ctypes.c_void_p(16), 4, 784, 784, 8, 0, 0, 0, 0,
+    _expect_invalid("hses_poisson_encode", ctypes.c_void_p(16), 4, NULL, 4, 784, 784, 8, 0, 0, 0, 0,
                     ctypes.c_void_p(16), 3, 12, NULL)  # 784 bits need 13 words
-    _expect_invalid("hses_poisson_encode", ctypes.c_void_p(16), 4, 784, 784, 8, 0, 0, 0, 0,
+    _expect_invalid("hses_poisson_encode", ctypes.c_void_p(16), 4, NULL, 4, 784, 784, 8, 0, 0, 0, 0,
                     ctypes.c_void_p(16), 9, 784, NULL)
-    _expect_invalid("hses_poisson_encode", ctypes.c_void_p(16), 2**23, 1024, 1024, 8, 0, 0, 0, 0,
+    _expect_invalid("hses_poisson_encode", ctypes.c_void_p(16), 2**23, NULL, 2**23, 1024, 1024, 8, 0, 0, 0, 0,
                     ctypes.c_void_p(16), 0, 1024, NULL)  # flat index beyond u32
     _expect_invalid("hses_lif_scan", ctypes.c_void_p(16), NULL, 8, 4, 128, 128, 0.0, 1.0,
                     ctypes.c_void_p(16), 0, 128, NULL, NULL)
@@ -71,11 +71,20 @@ def test_validation_rejects_bad_arguments_without_a_gpu():
     _expect_invalid("hses_solver_step", 1, 0.1, 0.9, 0.999, 1e-8, 0.0, 0, ctypes.c_void_p(16),
                     ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16), 4, NULL)
     _expect_invalid("hses_member_loglik", NULL, 0, NULL, 4, 2, NULL, NULL)
+    _expect_invalid("hses_poisson_encode", ctypes.c_void_p(16), 3, NULL, 4, 784, 784, 8, 0, 0, 0,
+                    0, ctypes.c_void_p(16), 0, 784, NULL)  # p has fewer rows than the output
+    _expect_invalid("hses_spike_rate", ctypes.c_void_p(16), 3, 1, 16, 4, 128, ctypes.c_void_p(16),
+                    NULL)  # 128 bits need 2 words
+    _expect_invalid("hses_perturbed_linear", ctypes.c_void_p(16), 5, 784, 0, 1,
+                    ctypes.c_void_p(16), 128, 784, 1, 4, 0.02, 0, 0, 0, 4, 8,
+                    ctypes.c_void_p(16), 128, 0, 0, NULL, 0, NULL)
+    _expect_invalid("hses_es_update", ctypes.c_void_p(16), 8, 0, 1, 4, 0.02, 0, 0, 16, 16, 1.0,
+                    0, ctypes.c_void_p(16), NULL, 0, NULL)
 
 
 def test_empty_inputs_are_no_ops_without_a_gpu():
     lib = _lib.load()
-    assert lib.hses_poisson_encode(NULL, 0, 784, 784, 8, 0, 0, 0, 0, NULL, 0, 784, NULL) == 0
+    assert lib.hses_poisson_encode(NULL, 0, NULL, 0, 784, 784, 8, 0, 0, 0, 0, NULL, 0, 784, NULL) == 0
     assert lib.hses_lif_scan(NULL, NULL, 8, 0, 128, 128, 10.0, 1.0, NULL, 0, 128, NULL, NULL) == 0
     assert lib.hses_lora_factors(0.1, 1, 4, 0, 0, 0, NULL, 0, 3, 4, NULL, NULL, NULL) == 0
     assert lib.hses_solver_step(0, 0.1, 0.9, 0.999, 1e-8, 0.0, 1, NULL, NULL, NULL, NULL, 0,
