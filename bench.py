@@ -1,0 +1,199 @@
+"""Benchmark of the EggRoll SNN-MLP hot path on one MI355X.
+
+Metric: perturbed member-evals/sec + ES-update GB/s, SNN-MLP
+N=8192 r=128.  One step = one full ES step of the population:
+Poisson encode -> 3 perturbed hidden layers with LIF -> rate readout ->
+log-likelihood fitness -> z-score -> ES gradient of the 4 layers -> AdamW.
+`value` = N / (time per step): member evaluations per second including the
+update.  Inputs are synthetic and resident in HBM before timing starts.
+
+Prints one JSON line.  --gpus N > 1 is refused: this build runs on one GPU.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "perturbed member-evals/sec + ES-update GB/s, SNN-MLP N=8192 r=128"
+PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
+PEAK_FP32_TFLOPS = 157.3      # MI355X dense fp32 MFMA
+PEAK_HBM_GBPS = 8000.0
+
+
+def layer_flops(cfg, l):
+    """Algorithmic forward FLOPs of layer l: 2Mba + 2Mbr + 2Mra."""
+    b, a = cfg.dims[l], cfg.dims[l + 1]
+    M = cfg.n * cfg.rows * (cfg.T if l < len(cfg.dims) - 2 else 1)
+    return 2 * M * b * a + 2 * M * b * cfg.rank + 2 * M * cfg.rank * a
+
+
+def update_bytes(cfg):
+    """ES-update bytes, materialized-factor convention: sum_l N r (a+b) 4 + 2 a b 4."""
+    tot = 0
+    for l in range(len(cfg.dims) - 1):
+        b, a = cfg.dims[l], cfg.dims[l + 1]
+        tot += cfg.n * cfg.rank * (a + b) * 4 + 2 * a * b * 4
+    return tot
+
+
+def cpu_baseline(cfg, pool, labels, idx, W, members, threads):
+    """The oracle (C restatement of the reference CPU path) on `members` members,
+    forward + their share of the ES update, extrapolated linearly in N."""
+    from tests import oracle_lib as O
+    L = O.load()
+    dims = np.array(cfg.dims, np.int32)
+    c = O.SnnCfg()
+    c.n_layers = len(cfg.dims) - 1
+    c.dims = dims.ctypes.data_as(O.ctypes.POINTER(O.c_i32))
+    c.T, c.rows, c.tau_m, c.v_th, c.sigma = cfg.T, cfg.rows, cfg.tau_m, cfg.v_th, cfg.sigma
+    c.rank, c.noise_reuse, c.epoch = cfg.rank, cfg.noise_reuse, 0
+    for i in range(4):
+        c.poisson_seed[i] = cfg.poisson_seed[i]
+    R = members * cfg.rows
+    probs = np.ascontiguousarray(pool[idx[:R]], np.float32)
+    lab = np.ascontiguousarray(labels[idx[:R]], np.int32)
+    Ws = [np.ascontiguousarray(w) for w in W]
+    Wp = (O.ctypes.c_void_p * len(Ws))(*[w.ctypes.data for w in Ws])
+    keys = (O.c_u64 * len(cfg.keys))(*cfg.keys)
+    fit = np.zeros(members, np.float32)
+    t0 = time.perf_counter()
+    L.or_snn_forward_members(O.ctypes.byref(c), Wp, keys, probs, lab, 0, members, threads, fit)
+    t1 = time.perf_counter()
+    z, _, _ = O.convert_fitnesses(fit)
+    for l in range(len(cfg.dims) - 1):
+        a, b = cfg.dims[l + 1], cfg.dims[l]
+        O.lora_grad_f64(cfg.sigma, cfg.keys[l], cfg.rank, 0, z, a, b, nthreads=threads)
+    t2 = time.perf_counter()
+    per_member = (t2 - t0) / members
+    return {"value": 1.0 / per_member, "unit": "member-evals/s", "cores": threads,
+            "kind": "port",
+            "sample": (f"C3 ES step (forward + ES-update share) for {members} of {cfg.n} members "
+                       f"on {threads} host threads, extrapolated linearly in N; "
+                       f"fwd {t1 - t0:.2f}s, update {t2 - t1:.2f}s"),
+            "seconds": round(t2 - t0, 2)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--population", type=int, default=8192)
+    ap.add_argument("--cpu-members", type=int, default=32)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one GPU "
+              "(the population shards by member across GPUs; see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from hyperscalees_amd import kernels as K
+    from hyperscalees_amd import snn
+
+    cfg = snn.SnnConfig(n=args.population, poisson_seed=(1, 2, 3, 4))
+    pool_size = 60000
+    pool, labels = snn.synthetic_pool(pool_size, cfg.dims[0], cfg.dims[-1], seed=0)
+    idx = snn.sample_index(0, cfg.n, cfg.rows, pool_size)
+    W = snn.init_weights(cfg.dims, 0, gain=snn.ACTIVE_GAIN)
+    K.init(0)
+    es = snn.SnnEs(cfg, W, pool, labels, idx)
+    L = len(cfg.dims) - 1
+
+    for i in range(args.warmup):
+        es.step(epoch=i)
+    torch.cuda.synchronize()
+
+    ev = lambda: torch.cuda.Event(enable_timing=True)
+    marks = []
+    t0 = time.perf_counter()
+    for s in range(args.steps):
+        e = [ev() for _ in range(2 * L + 4)]
+        e[0].record()
+        es.poisson()
+        e[1].record()
+        for l in range(L - 1):
+            es.hidden_layer(l, s)
+            e[2 + l].record()
+        fit = es.readout(s)
+        e[L + 1].record()
+        es.update(fit, s)
+        e[L + 2].record()
+        marks.append(e)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms_per_step = (t1 - t0) * 1000.0 / args.steps
+
+    def span(e, i, j):
+        return e[i].elapsed_time(e[j])
+    t_poisson = np.mean([span(e, 0, 1) for e in marks])
+    t_hidden = [np.mean([span(e, 1 + l, 2 + l) for e in marks]) for l in range(L - 1)]
+    t_readout = np.mean([span(e, L, L + 1) for e in marks])
+    t_fwd = np.mean([span(e, 0, L + 1) for e in marks])
+    t_upd = np.mean([span(e, L + 1, L + 2) for e in marks])
+
+    # Dominant kernel: fc1's perturbed forward (x[W^T|B] + (xB)A^T, bf16 MFMA),
+    # timed alone with events on the launch stream (the LIF scan excluded).
+    fc1_ms = []
+    for s in range(3):
+        e0, e1 = ev(), ev()
+        e0.record()
+        K.perturbed_linear(es.spk[0], es.W[0], cfg.keys[0], cfg.rank, cfg.sigma, s,
+                           cfg.noise_reuse, 0, cfg.n, cfg.rows, x_fmt=K.FMT_BITS, n_time=cfg.T,
+                           math=cfg.math, out=es.cur)
+        e1.record()
+        torch.cuda.synchronize()
+        fc1_ms.append(e0.elapsed_time(e1))
+    fc1_ms = float(np.median(fc1_ms))
+    fc1_flops = layer_flops(cfg, 0)
+    achieved = fc1_flops / (fc1_ms * 1e-3) / 1e12
+
+    fwd_flops = sum(layer_flops(cfg, l) for l in range(L))
+    out = {
+        "metric": METRIC,
+        "value": round(cfg.n / (ms_per_step * 1e-3), 1),
+        "unit": "member-evals/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16 forward MFMA (fp32 accumulate), fp32 ES update",
+        "data": "synthetic",
+        "config": {
+            "workload": ("C3: SNN-MLP 784-128-128-128-10, LIF decay 0.9 v_th 1.0, Poisson T=16, "
+                         "N=8192, r=128, 64 samples/member from a 60000x784 pool (70% zeros), "
+                         "full ES step (forward + fitness + z-score + ES update + AdamW)"),
+            "population": cfg.n, "rank": cfg.rank, "T": cfg.T, "samples_per_member": cfg.rows,
+            "parallelism": "single GPU",
+        },
+        "fwd_member_evals_per_s": round(cfg.n / (t_fwd * 1e-3), 1),
+        "es_update_GBps": round(update_bytes(cfg) / (t_upd * 1e-3) / 1e9, 2),
+        "phase_ms": {"poisson": round(float(t_poisson), 3),
+                     "hidden_layers": [round(float(x), 3) for x in t_hidden],
+                     "readout_fitness": round(float(t_readout), 3),
+                     "forward": round(float(t_fwd), 3), "es_update": round(float(t_upd), 3)},
+        "fwd_tflops": round(fwd_flops / (t_fwd * 1e-3) / 1e12, 1),
+        "roofline": {"kernel": "k_linear_pair (fc1: x[W^T|B] + (xB)A^T, T=16 x 524288 rows)",
+                     "bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": None, "launch_ms": round(fc1_ms, 3),
+                     "algorithmic_flop_per_launch": fc1_flops},
+    }
+    if not args.no_cpu_baseline:
+        threads = min(os.cpu_count() or 1, 16)
+        out["cpu_baseline"] = cpu_baseline(cfg, pool, labels, idx, W, args.cpu_members, threads)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()
