@@ -1,0 +1,51 @@
+"""One tiny EggRoll ES step of the SNN-MLP on cuda:0, checked against the CPU
+oracle (the oracle is only the checker here; every computation runs in
+libhses.so).  Raises AssertionError on a mismatch."""
+import math
+
+import numpy as np
+import torch
+
+from . import kernels as K
+from . import snn
+from ._lib import MATH_F32, SGD
+
+
+def run_smoke():
+    from tests import oracle_lib as O   # checker only
+
+    if not torch.cuda.is_available():
+        raise RuntimeError("smoke() needs a GPU")
+    K.init(0)
+    cfg = snn.SnnConfig(dims=(784, 64, 64, 10), T=8, rows=8, n=16, rank=4, sigma=0.02,
+                        math=MATH_F32, solver=SGD, lr=0.05, poisson_seed=(3, 1, 4, 1))
+    pool, labels = snn.synthetic_pool(500, cfg.dims[0], cfg.dims[-1], seed=1)
+    idx = snn.sample_index(1, cfg.n, cfg.rows, 500)
+    W = snn.init_weights(cfg.dims, 1, gain=snn.ACTIVE_GAIN)
+    es = snn.SnnEs(cfg, W, pool, labels, idx)
+
+    # Poisson spikes: bit-exact
+    es.poisson()
+    torch.cuda.synchronize()
+    words = es.spk[0].cpu().numpy().view(np.uint64)
+    bits = ((words[..., None] >> np.arange(64, dtype=np.uint64)) & np.uint64(1)).astype(np.float32)
+    got = bits.reshape(cfg.T, cfg.n * cfg.rows, -1)[..., : cfg.dims[0]]
+    ref = O.poisson(pool[idx], cfg.T, cfg.poisson_seed)
+    assert np.array_equal(got, ref), "Poisson spikes differ from the oracle"
+
+    # full step: fitness, then the ES gradient on the GPU's fitness
+    fit = es.forward(0)
+    torch.cuda.synchronize()
+    fit_gpu = fit.cpu().numpy()
+    assert np.all(np.isfinite(fit_gpu))
+    es.update(fit, 0)
+    torch.cuda.synchronize()
+    z, _, _ = O.convert_fitnesses(fit_gpu)
+    for l in range(es.L):
+        a, b = W[l].shape
+        g_ref = O.lora_grad_f64(cfg.sigma, cfg.keys[l], cfg.rank, 0, z, a, b, nthreads=4)
+        g = es.grads[l].cpu().numpy()
+        err = float(np.abs(g - g_ref).max())
+        assert err <= 1e-5 * float(np.abs(g_ref).max()), f"layer {l} ES gradient err {err}"
+    print(f"smoke ok: N={cfg.n} r={cfg.rank} fitness mean {fit_gpu.mean():.4f}, "
+          f"gradients within 1e-5 of the oracle", flush=True)
