@@ -46,9 +46,9 @@ struct BmTables {
     double cos_s[kCosTab + 1];
     double cos_thi[kCosTab + 1];
     double cos_tlo[kCosTab + 1];
-    double log_q[kBuckets];   // danger if |d| >= q * |e|
-    double cos_q[kBuckets];
-    float log_k0;             // glibc logf(1e-9f): the k1 == 0 case (u1 clamped)
+    uint32_t log_t[kBuckets];  // danger window half-widths in units of 2^-29 f32 ulp
+    uint32_t cos_t[kBuckets];
+    float log_k0;              // glibc logf(1e-9f): the k1 == 0 case (u1 clamped)
     float pad_[3];
 };
 
@@ -100,7 +100,10 @@ constexpr double kC2 = -0.5, kC4 = 1.0 / 24.0, kC6 = -1.0 / 720.0, kC8 = 1.0 / 4
 constexpr double kS3 = -1.0 / 6.0, kS5 = 1.0 / 120.0, kS7 = -1.0 / 5040.0, kS9 = 1.0 / 362880.0;
 
 // The f32 argument of logf for unit index k1 (k1 == 0 is clamped to 1e-9f).
-HSES_HD float log_arg(uint32_t k1) { return k1 == 0 ? 1e-9f : (float)k1 * 0x1p-24f; }
+HSES_HD float log_arg(uint32_t k1) { return k1 == 0 ? 1e-9f : (float)(int32_t)k1 * 0x1p-24f; }
+
+// The f32 angle TAU * (k2 * 2^-24) of noiser.rs:475-476.
+HSES_HD float cos_arg(uint32_t k2) { return kTauF * ((float)(int32_t)k2 * 0x1p-24f); }
 
 // f64 evaluation of log(x) for x = log_arg(k1), k1 >= 1 (x in [2^-24, 1)).
 // x = 2^E * z with z in [0.75, 1.5); log x = E ln2 + logc + log1p(z*invc - 1).
@@ -146,23 +149,33 @@ HSES_HD double cos_f64(float th, const double* c_tab, const double* s_tab, const
     return hfma(c_tab[j], ct, -sj);
 }
 
-// Round y to f32 and report the danger statistics.  Returns the correctly
-// rounded f32; *g receives the neighbour across the nearest rounding midpoint
-// (the only other value glibc can return), and *danger whether y lies within
-// the bucket's midpoint window.
-HSES_HD float round_with_danger(double y, double q, float* g, bool* danger) {
-    const float f = (float)y;
+HSES_HD uint64_t d2u(double d) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return __double_as_longlong(d);
+#else
+    uint64_t u;
+    memcpy(&u, &d, 8);
+    return u;
+#endif
+}
+
+// Rounding y (a normal-range f64) to f32 keeps the top 23 of its 52 mantissa
+// bits; the low 29 bits R (the low word's bits 0..28) decide the rounding,
+// with the midpoint at R = 2^28.  |R - 2^28| is the distance to the nearest
+// rounding midpoint in units of 2^-29 f32 ulp.
+HSES_HD uint32_t rem29(double y) { return (uint32_t)d2u(y) & 0x1FFFFFFFu; }
+
+// Inside the window of half-width t around the midpoint (one unsigned compare).
+HSES_HD bool in_danger(double y, uint32_t t) {
+    return rem29(y) - (0x10000000u - t) < 2u * t;
+}
+
+// The other f32 candidate for y: the neighbour of f = RN32(y) across the
+// nearest rounding midpoint (the only other value glibc's logf/cosf return).
+HSES_HD float other_candidate(float f, double y) {
     const double fd = (double)f;
-    const double d = y - fd;
-    const uint32_t fb = f2u(f);
-    const bool up = d > 0.0;
-    const bool neg = (fb >> 31) != 0;
-    const uint32_t gb = (up != neg) ? fb + 1u : fb - 1u;
-    const float gf = u2f(gb);
-    const double e = (double)gf - fd;
-    *g = gf;
-    *danger = (d != 0.0) && (d < 0.0 ? -d : d) >= q * (e < 0.0 ? -e : e);
-    return f;
+    const bool f_larger = (fd < 0.0 ? -fd : fd) > (y < 0.0 ? -y : y);
+    return u2f(f_larger ? f2u(f) - 1u : f2u(f) + 1u);
 }
 
 // ---------------------------------------------------------------------------

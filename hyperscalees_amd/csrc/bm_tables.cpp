@@ -5,8 +5,8 @@
 //     cos: cos, sin and a two-part angle per grid point);
 //   * per-input exception bitmaps: bit k is set where glibc's logf/cosf differ
 //     from the f32 rounding of the f64 routine;
-//   * per-bucket danger coefficients q so that every exception satisfies the
-//     danger predicate of round_with_danger().
+//   * per-bucket danger window half-widths t (in 2^-29 f32 ulp) so that every
+//     exception satisfies in_danger(y, t).
 // glibc is the parity target because the reference's f32::ln / f32::cos lower
 // to glibc logf / cosf on linux-gnu (noiser.rs:470-477).
 #include <math.h>
@@ -71,7 +71,7 @@ void build_small(BmTables* t) {
 
 struct Exc {
     uint32_t k;
-    double ratio;  // |d| / |e|
+    uint32_t dist;  // |R - 2^28|: distance to the rounding midpoint in 2^-29 ulp
 };
 
 // Evaluate one function over a slice of unit indices.  kind 0 = log, 1 = cos.
@@ -86,14 +86,13 @@ void scan_slice(const BmTables* t, int kind, uint32_t k_lo, uint32_t k_hi, std::
             y = log_f64(x, t->log_invc, t->log_logc);
             ref = logf(x);
         } else {
-            const float th = kTauF * ((float)k * 0x1p-24f);
+            const float th = cos_arg(k);
             y = cos_f64(th, t->cos_c, t->cos_s, t->cos_thi, t->cos_tlo);
             ref = cosf(th);
         }
-        float g;
-        bool danger;
-        const float f = round_with_danger(y, 2.0, &g, &danger);
+        const float f = (float)y;
         if (f2u(ref) == f2u(f)) continue;
+        const float g = other_candidate(f, y);
         if (f2u(ref) != f2u(g)) {
             char buf[160];
             snprintf(buf, sizeof buf,
@@ -102,46 +101,16 @@ void scan_slice(const BmTables* t, int kind, uint32_t k_lo, uint32_t k_hi, std::
             *err = buf;
             return;
         }
-        const double fd = (double)f;
-        const double d = y - fd;
-        const double e = (double)g - fd;
-        if (d == 0.0) {
-            *err = "exception on an exactly representable f64 value";
-            return;
-        }
-        exc->push_back({k, (d < 0 ? -d : d) / (e < 0 ? -e : e)});
+        const uint32_t R = rem29(y);
+        exc->push_back({k, R >= 0x10000000u ? R - 0x10000000u : 0x10000000u - R});
     }
 }
 
-// Largest q such that the danger predicate holds for every exception of a bucket.
-double bucket_q(const BmTables* t, int kind, const std::vector<Exc>& exc_in_bucket) {
-    if (exc_in_bucket.empty()) return 2.0;  // never dangerous: ratio <= 0.5
-    double q = 2.0;
-    for (const Exc& x : exc_in_bucket) q = std::min(q, x.ratio);
-    // Step down until the exact predicate (as the device evaluates it) holds.
-    for (int it = 0; it < 64; ++it) {
-        bool ok = true;
-        for (const Exc& x : exc_in_bucket) {
-            double y;
-            if (kind == 0) {
-                y = log_f64(log_arg(x.k), t->log_invc, t->log_logc);
-            } else {
-                y = cos_f64(kTauF * ((float)x.k * 0x1p-24f), t->cos_c, t->cos_s, t->cos_thi,
-                            t->cos_tlo);
-            }
-            float g;
-            bool danger;
-            round_with_danger(y, q, &g, &danger);
-            if (!danger) {
-                ok = false;
-                break;
-            }
-        }
-        if (ok) return q;
-        q = nextafter(q, 0.0);
-        q = q * (1.0 - 1e-12);
-    }
-    return 0.0;  // always dangerous: still correct, only slower
+// Smallest window that puts every exception of a bucket in danger.
+uint32_t bucket_t(const std::vector<Exc>& exc_in_bucket) {
+    uint32_t t = 0;
+    for (const Exc& x : exc_in_bucket) t = std::max(t, x.dist + 1u);
+    return t;
 }
 
 }  // namespace
@@ -173,8 +142,19 @@ std::string build_bm_tables(HostBmTables* out, int nthreads) {
                 by_bucket[x.k >> 16].push_back(x);
                 ++n;
             }
-        double* q = kind == 0 ? out->small.log_q : out->small.cos_q;
-        for (int b = 0; b < kBuckets; ++b) q[b] = bucket_q(&out->small, kind, by_bucket[b]);
+        uint32_t* tw = kind == 0 ? out->small.log_t : out->small.cos_t;
+        for (int b = 0; b < kBuckets; ++b) {
+            tw[b] = bucket_t(by_bucket[b]);
+            if (tw[b] > 0x10000000u) return "danger window wider than half an ulp";
+            // every exception must test as dangerous with the bucket's window
+            for (const Exc& x : by_bucket[b]) {
+                const double y = kind == 0
+                                      ? log_f64(log_arg(x.k), out->small.log_invc, out->small.log_logc)
+                                      : cos_f64(cos_arg(x.k), out->small.cos_c, out->small.cos_s,
+                                                out->small.cos_thi, out->small.cos_tlo);
+                if (!in_danger(y, tw[b])) return "exception outside its danger window";
+            }
+        }
         if (kind == 0)
             out->n_log_exc = n;
         else

@@ -102,15 +102,16 @@ __global__ __launch_bounds__(U_THREADS) void k_es_partial(UpdParams P) {
         for (int32_t ch = 0; ch < chunks; ++ch) {
             const int32_t c0 = ch * U_CW;
             const int32_t cn = min(cw, r - c0);
-            // rc > 1 only when r <= 16 (one chunk): an item is rc rows x r normals.
-            for (int32_t i = 0; i < nrows; ++i) {
-                for (int32_t c = 0; c < cn; ++c) {
-                    const float v = bm_normal(st, ctx);
-                    dst[(first + i) * U_PITCH + c] = is_a ? v * P.bs : v;
-                }
-                // The last k-step reads whole groups of 4 columns: clear the tail.
+            // rc > 1 only when r <= 16 (one chunk): the item's rows are contiguous
+            // in the stream, so one run of nrows * r normals covers them.
+            const float scl = is_a ? P.bs : 1.0f;
+            bm_run(st, nrows * cn, ctx, [&](int32_t i, float v) {
+                const int32_t row = first + i / cn, c = i % cn;
+                dst[row * U_PITCH + c] = is_a ? v * scl : v;
+            });
+            // The last k-step reads whole groups of 4 columns: clear the tail.
+            for (int32_t i = 0; i < nrows; ++i)
                 for (int32_t c = cn; c < ((cn + 3) & ~3); ++c) dst[(first + i) * U_PITCH + c] = 0.0f;
-            }
             __syncthreads();
             // acc += (w * Ahat[:, c]) B[:, c]^T over this chunk (k-steps of 4).
             for (int32_t ks = 0; ks < cn; ks += 4) {

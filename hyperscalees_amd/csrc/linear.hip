@@ -87,19 +87,16 @@ __global__ __launch_bounds__(K1_THREADS) void k_linear_small(LinParams P) {
             const uint64_t seed = member_seed(P.key, P.epoch, P.nreuse, P.tid_lo + m_first + lm, &sign);
             const float sc = sign * P.bs;
             uint64_t s = row_start_state(seed, q, P.jump);
-            for (int32_t jj = 0; jj < rc; ++jj) {
-                const int32_t j = q * rc + jj;
-                if (j >= P.a + b) break;
-                for (int32_t c = 0; c < r; ++c) {
-                    const float v = bm_normal(s, ctx);
-                    if (j < b) {
-                        Bs[(size_t)(lm * r + c) * P.bpitch + j] = MathT<MATH>::cvt(v);
-                    } else {
-                        const int32_t o = j - b - o0;
-                        if (o >= 0 && o < ct) As[((size_t)lm * K1_CT + o) * r + c] = v * sc;
-                    }
+            const int32_t rows_here = min(rc, P.a + b - q * rc);
+            bm_run(s, rows_here * r, ctx, [&](int32_t i, float v) {
+                const int32_t j = q * rc + i / r, c = i % r;
+                if (j < b) {
+                    Bs[(size_t)(lm * r + c) * P.bpitch + j] = MathT<MATH>::cvt(v);
+                } else {
+                    const int32_t o = j - b - o0;
+                    if (o >= 0 && o < ct) As[((size_t)lm * K1_CT + o) * r + c] = v * sc;
                 }
-            }
+            });
         }
     }
     __syncthreads();

@@ -109,10 +109,10 @@ __global__ __launch_bounds__(K2_THREADS) void k_linear_pair(LinParams P, K2Extra
             for (int32_t j = tid; j < a + b; j += K2_THREADS) {
                 uint64_t s = row_start_state(seed, j, P.jump);
                 if (j < b) {
-                    for (int32_t c = 0; c < r; ++c) slot[(size_t)c * E.bpitch + j] = f2bf(bm_normal(s, ctx));
+                    bm_run(s, r, ctx, [&](int32_t c, float v) { slot[(size_t)c * E.bpitch + j] = f2bf(v); });
                 } else {
                     uint16_t* dst = As + (size_t)(j - b) * lay.apitch;
-                    for (int32_t c = 0; c < r; ++c) dst[c] = f2bf(bm_normal(s, ctx) * P.bs);
+                    bm_run(s, r, ctx, [&](int32_t c, float v) { dst[c] = f2bf(v * P.bs); });
                     for (int32_t c = r; c < ((r + 31) & ~31); ++c) dst[c] = 0;
                 }
             }

@@ -19,7 +19,7 @@ __global__ void k_bm_eval(uint32_t k_lo, uint32_t n, float* lg, float* rad, floa
         if (lg || rad) {
             const float L = bm_logf(k, t, le);
             if (lg) lg[i] = L;
-            if (rad) rad[i] = __builtin_sqrtf(-2.0f * L);
+            if (rad) rad[i] = sqrt_rn(-2.0f * L);
         }
         if (cs) cs[i] = bm_cosf(k, t, ce);
     }
@@ -47,11 +47,11 @@ __global__ void k_stream_rows(float bs, uint64_t key, int32_t L, int32_t epoch, 
     const NoiseCtx ctx{&t, le, ce};
     if (j < b) {
         float* dst = B + ((int64_t)m * b + j) * L;
-        for (int32_t c = 0; c < L; ++c) dst[c] = bm_normal(s, ctx);
+        bm_run(s, L, ctx, [&](int32_t c, float v) { dst[c] = v; });
     } else {
         const float sc = sign * bs;
         float* dst = A + ((int64_t)m * a + (j - b)) * L;
-        for (int32_t c = 0; c < L; ++c) dst[c] = bm_normal(s, ctx) * sc;
+        bm_run(s, L, ctx, [&](int32_t c, float v) { dst[c] = v * sc; });
     }
 }
 

@@ -6,6 +6,10 @@
 // each thread whole rows: the state at the start of row j is
 // M^(2Lj) s0 = T1[j/16] (T0[j%16] s0), two GF(2) products with matrices from
 // the per-L jump table, after which the thread steps sequentially.
+//
+// Normals are produced in batches (bm_normals<G>): the G log and G cos
+// evaluations are independent, so their f64 latency overlaps, and every
+// exception-bitmap load the batch needs is issued before the first is used.
 #pragma once
 #include <hip/hip_runtime.h>
 
@@ -21,50 +25,104 @@ __device__ __forceinline__ void load_bm_tables(BmTables* lds, const BmTables* g)
     for (int i = threadIdx.x; i < words; i += blockDim.x) dst[i] = src[i];
 }
 
-__device__ __forceinline__ bool bit_set(const uint32_t* bm, uint32_t k) {
-    return (bm[k >> 5] >> (k & 31)) & 1u;
-}
-
-// glibc logf(max(k1 * 2^-24, 1e-9f)), bit-exact.
-__device__ __forceinline__ float bm_logf(uint32_t k1, const BmTables& t, const uint32_t* exc) {
-    const float x = log_arg(k1);
-    const double y = log_f64(x, t.log_invc, t.log_logc);
-    float g;
-    bool danger;
-    float f = round_with_danger(y, t.log_q[k1 >> 16], &g, &danger);
-    if (danger && bit_set(exc, k1)) f = g;
-    return k1 == 0 ? t.log_k0 : f;
-}
-
-// sqrtf(-2 * logf(u1)): the radius of noiser.rs:474.
-__device__ __forceinline__ float bm_radius(uint32_t k1, const BmTables& t, const uint32_t* exc) {
-    return __builtin_sqrtf(-2.0f * bm_logf(k1, t, exc));
-}
-
-// glibc cosf(TAU * k2 * 2^-24), bit-exact (noiser.rs:475-476).
-__device__ __forceinline__ float bm_cosf(uint32_t k2, const BmTables& t, const uint32_t* exc) {
-    const float th = kTauF * ((float)k2 * 0x1p-24f);
-    const double y = cos_f64(th, t.cos_c, t.cos_s, t.cos_thi, t.cos_tlo);
-    float g;
-    bool danger;
-    float f = round_with_danger(y, t.cos_q[k2 >> 16], &g, &danger);
-    if (danger && bit_set(exc, k2)) f = g;
-    return f;
-}
-
 struct NoiseCtx {
     const BmTables* t;     // LDS copy
     const uint32_t* log_exc;
     const uint32_t* cos_exc;
 };
 
-// DeterministicNoise::standard_normal (noiser.rs:470-477).
+// Correctly rounded f32 square root for a positive normal s: hardware
+// estimate plus the one-ulp correction from the two residuals.
+__device__ __forceinline__ float sqrt_rn(float s) {
+    const float r = __builtin_amdgcn_sqrtf(s);
+    const float rd = __uint_as_float(__float_as_uint(r) - 1u);
+    const float ru = __uint_as_float(__float_as_uint(r) + 1u);
+    float q = __builtin_fmaf(-rd, r, s) <= 0.0f ? rd : r;
+    q = __builtin_fmaf(-ru, r, s) > 0.0f ? ru : q;
+    return q;
+}
+
+// glibc logf(max(k1 * 2^-24, 1e-9f)), bit-exact (single value).
+__device__ __forceinline__ float bm_logf(uint32_t k1, const BmTables& t, const uint32_t* exc) {
+    const double y = log_f64(log_arg(k1), t.log_invc, t.log_logc);
+    float f = (float)y;
+    if (in_danger(y, t.log_t[k1 >> 16]) && ((exc[k1 >> 5] >> (k1 & 31)) & 1u))
+        f = other_candidate(f, y);
+    return k1 == 0 ? t.log_k0 : f;
+}
+
+// glibc cosf(TAU * k2 * 2^-24), bit-exact (single value).
+__device__ __forceinline__ float bm_cosf(uint32_t k2, const BmTables& t, const uint32_t* exc) {
+    const double y = cos_f64(cos_arg(k2), t.cos_c, t.cos_s, t.cos_thi, t.cos_tlo);
+    float f = (float)y;
+    if (in_danger(y, t.cos_t[k2 >> 16]) && ((exc[k2 >> 5] >> (k2 & 31)) & 1u))
+        f = other_candidate(f, y);
+    return f;
+}
+
+// sqrtf(-2 * logf(u1)): the radius of noiser.rs:474.
+__device__ __forceinline__ float bm_radius(uint32_t k1, const BmTables& t, const uint32_t* exc) {
+    return sqrt_rn(-2.0f * bm_logf(k1, t, exc));
+}
+
+// G consecutive DeterministicNoise::standard_normal draws (noiser.rs:470-477).
+template <int G>
+__device__ __forceinline__ void bm_normals(uint64_t& s, float* out, const NoiseCtx& c) {
+    const BmTables& t = *c.t;
+    uint32_t k1[G], k2[G];
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+        s = xs64(s);
+        k1[i] = (uint32_t)(s >> 40);
+        s = xs64(s);
+        k2[i] = (uint32_t)(s >> 40);
+    }
+    double yl[G], yc[G];
+    float fl[G], fc[G];
+    bool dl[G], dc[G];
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+        yl[i] = log_f64(log_arg(k1[i]), t.log_invc, t.log_logc);
+        yc[i] = cos_f64(cos_arg(k2[i]), t.cos_c, t.cos_s, t.cos_thi, t.cos_tlo);
+        fl[i] = (float)yl[i];
+        fc[i] = (float)yc[i];
+        dl[i] = in_danger(yl[i], t.log_t[k1[i] >> 16]);
+        dc[i] = in_danger(yc[i], t.cos_t[k2[i] >> 16]);
+    }
+    uint32_t wl[G], wc[G];
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+        wl[i] = dl[i] ? c.log_exc[k1[i] >> 5] : 0u;
+        wc[i] = dc[i] ? c.cos_exc[k2[i] >> 5] : 0u;
+    }
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+        if ((wl[i] >> (k1[i] & 31)) & 1u) fl[i] = other_candidate(fl[i], yl[i]);
+        if ((wc[i] >> (k2[i] & 31)) & 1u) fc[i] = other_candidate(fc[i], yc[i]);
+        const float L = k1[i] == 0 ? t.log_k0 : fl[i];
+        out[i] = sqrt_rn(-2.0f * L) * fc[i];
+    }
+}
+
+// One normal (used where a single draw is needed).
 __device__ __forceinline__ float bm_normal(uint64_t& s, const NoiseCtx& c) {
-    s = xs64(s);
-    const uint32_t k1 = (uint32_t)(s >> 40);
-    s = xs64(s);
-    const uint32_t k2 = (uint32_t)(s >> 40);
-    return bm_radius(k1, *c.t, c.log_exc) * bm_cosf(k2, *c.t, c.cos_exc);
+    float v;
+    bm_normals<1>(s, &v, c);
+    return v;
+}
+
+// `count` consecutive normals of one stream; sink(i, value) receives normal i.
+// Batches of 4 (a tail of 1-3 handled singly).
+template <typename Sink>
+__device__ __forceinline__ void bm_run(uint64_t& s, int32_t count, const NoiseCtx& c, Sink sink) {
+    int32_t i = 0;
+    for (; i + 4 <= count; i += 4) {
+        float v[4];
+        bm_normals<4>(s, v, c);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sink(i + j, v[j]);
+    }
+    for (; i < count; ++i) sink(i, bm_normal(s, c));
 }
 
 // State before the first normal of row j of a stream with s0 = seed | 1.
