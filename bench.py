@@ -139,15 +139,21 @@ def main():
     t_fwd = np.mean([span(e, 0, L + 1) for e in marks])
     t_upd = np.mean([span(e, L + 1, L + 2) for e in marks])
 
-    # Dominant kernel: fc1's perturbed forward (x[W^T|B] + (xB)A^T, bf16 MFMA),
-    # timed alone with events on the launch stream (the LIF scan excluded).
+    # Dominant kernel: fc1's perturbed forward (x[W^T|B] + (xB)A^T, bf16 MFMA;
+    # with the LIF fused into its epilogue when the step runs fused), timed
+    # alone with events on the launch stream.
     fc1_ms = []
     for s in range(3):
         e0, e1 = ev(), ev()
         e0.record()
-        K.perturbed_linear(es.spk[0], es.W[0], cfg.keys[0], cfg.rank, cfg.sigma, s,
-                           cfg.noise_reuse, 0, cfg.n, cfg.rows, x_fmt=K.FMT_BITS, n_time=cfg.T,
-                           math=cfg.math, out=es.cur)
+        if es.fused:
+            K.perturbed_linear_lif(es.spk[0], es.W[0], cfg.keys[0], cfg.rank, cfg.sigma, s,
+                                   cfg.noise_reuse, 0, cfg.n, cfg.rows, cfg.T, cfg.tau_m,
+                                   cfg.v_th, spikes=es.spk[1])
+        else:
+            K.perturbed_linear(es.spk[0], es.W[0], cfg.keys[0], cfg.rank, cfg.sigma, s,
+                               cfg.noise_reuse, 0, cfg.n, cfg.rows, x_fmt=K.FMT_BITS,
+                               n_time=cfg.T, math=cfg.math, out=es.cur)
         e1.record()
         torch.cuda.synchronize()
         fc1_ms.append(e0.elapsed_time(e1))
@@ -183,7 +189,8 @@ def main():
                      "readout_fitness": round(float(t_readout), 3),
                      "forward": round(float(t_fwd), 3), "es_update": round(float(t_upd), 3)},
         "fwd_tflops": round(fwd_flops / (t_fwd * 1e-3) / 1e12, 1),
-        "roofline": {"kernel": "k_linear_pair (fc1: x[W^T|B] + (xB)A^T, T=16 x 524288 rows)",
+        "roofline": {"kernel": ("k_linear_pair (fc1: x[W^T|B] + (xB)A^T, T=16 x 524288 rows"
+                                + (", LIF fused)" if es.fused else ")")),
                      "bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": None, "launch_ms": round(fc1_ms, 3),

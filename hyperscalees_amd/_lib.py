@@ -38,6 +38,10 @@ PROTOTYPES = {
                                              c_u64, c_i32, c_f32, c_i32, c_i32, c_i32, c_i32,
                                              c_i32, c_vp, c_i64, c_i64, c_i32, c_vp, c_size,
                                              c_vp]),
+    "hses_perturbed_linear_lif": (ctypes.c_int, [c_vp, c_i32, c_i64, c_i64, c_i32, c_vp, c_i32,
+                                                 c_i32, c_u64, c_i32, c_f32, c_i32, c_i32, c_i32,
+                                                 c_i32, c_i32, c_f32, c_f32, c_vp, c_i64, c_i64,
+                                                 c_vp, c_i64, c_vp, c_size, c_vp]),
     "hses_perturbed_linear_workspace": (c_size, [c_i32, c_i32, c_i32, c_i32, c_i32, c_i32,
                                                  c_i32]),
     "hses_es_update_workspace": (c_size, [c_i32, c_i32, c_i32, c_i32]),

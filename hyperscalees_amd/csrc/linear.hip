@@ -265,6 +265,54 @@ extern "C" size_t hses_perturbed_linear_workspace(int32_t a, int32_t b, int32_t 
     return linear_pair_workspace(st, a, b, rank, n);
 }
 
+// Validation and parameter block shared by the two forward entry points.
+static int make_params(LinParams* P, const void* d_x, int32_t x_fmt, int64_t x_stride,
+                       int64_t x_plane, int32_t n_time, const float* d_W, int32_t a, int32_t b,
+                       uint64_t key, int32_t rank, float sigma, int32_t epoch, int32_t noise_reuse,
+                       int32_t tid_lo, int32_t n, int32_t rows_per_member, int32_t math,
+                       DeviceState** st) {
+    HSES_REQUIRE(x_fmt == HSES_FMT_F32 || x_fmt == HSES_FMT_BF16 || x_fmt == HSES_FMT_BITS,
+                 "x_fmt must be F32, BF16 or BITS");
+    HSES_REQUIRE(math == HSES_MATH_F32 || math == HSES_MATH_BF16, "unknown math mode");
+    HSES_REQUIRE(a >= 1 && b >= 1, "a and b must be >= 1");
+    HSES_REQUIRE(n >= 0 && rank >= 0 && n_time >= 1 && rows_per_member >= 1, "bad sizes");
+    HSES_REQUIRE(noise_reuse >= 0, "noise_reuse must be >= 0");
+    HSES_REQUIRE((int64_t)tid_lo + n - 1 <= INT32_MAX && tid_lo >= 0, "thread id range");
+    if (n == 0) return HSES_OK;
+    HSES_REQUIRE(d_x && d_W, "NULL pointer");
+    const int64_t units = x_fmt == HSES_FMT_BITS ? (b + 63) / 64 : b;
+    const int64_t M = (int64_t)n * rows_per_member;
+    HSES_REQUIRE(x_stride >= units, "x_stride smaller than a row");
+    HSES_REQUIRE(n_time == 1 || x_plane >= M * x_stride, "time planes overlap");
+    HSES_REQUIRE(M * n_time < (1ll << 40), "too many rows");
+    int rc = get_state(st);
+    if (rc) return rc;
+    *P = LinParams{};
+    P->x = d_x;
+    P->x_fmt = x_fmt;
+    P->x_stride = x_stride;
+    P->x_plane = x_plane;
+    P->n_time = n_time;
+    P->rpm = rows_per_member;
+    P->W = d_W;
+    P->a = a;
+    P->b = b;
+    P->key = key;
+    P->r = (sigma != 0.0f) ? rank : 0;
+    P->bs = rank > 0 ? sigma / sqrtf((float)rank) : 0.0f;  // eggroll.rs:433
+    P->epoch = epoch;
+    P->nreuse = noise_reuse;
+    P->tid_lo = tid_lo;
+    P->n = n;
+    P->math = math;
+    P->R = n_time * rows_per_member;
+    P->total = (int64_t)n * P->R;
+    P->tables = (*st)->d_tables;
+    P->log_exc = (*st)->d_log_exc;
+    P->cos_exc = (*st)->d_cos_exc;
+    return HSES_OK;
+}
+
 extern "C" int hses_perturbed_linear(const void* d_x, int32_t x_fmt, int64_t x_stride,
                                      int64_t x_plane, int32_t n_time, const float* d_W, int32_t a,
                                      int32_t b, uint64_t key, int32_t rank, float sigma,
@@ -272,51 +320,18 @@ extern "C" int hses_perturbed_linear(const void* d_x, int32_t x_fmt, int64_t x_s
                                      int32_t rows_per_member, float* d_y, int64_t y_stride,
                                      int64_t y_plane, int32_t math, void* d_work,
                                      size_t work_bytes, void* stream) {
-    HSES_REQUIRE(x_fmt == HSES_FMT_F32 || x_fmt == HSES_FMT_BF16 || x_fmt == HSES_FMT_BITS,
-                 "x_fmt must be F32, BF16 or BITS");
-    HSES_REQUIRE(math == HSES_MATH_F32 || math == HSES_MATH_BF16, "unknown math mode");
-    HSES_REQUIRE(a >= 1 && b >= 1, "a and b must be >= 1");
-    HSES_REQUIRE(n >= 0 && rank >= 0 && n_time >= 1 && rows_per_member >= 1, "bad sizes");
-    HSES_REQUIRE(noise_reuse >= 0, "noise_reuse must be >= 0");
-    if (n == 0) return HSES_OK;
-    HSES_REQUIRE(d_x && d_W && d_y, "NULL pointer");
-    const int64_t units = x_fmt == HSES_FMT_BITS ? (b + 63) / 64 : b;
-    const int64_t M = (int64_t)n * rows_per_member;
-    HSES_REQUIRE(x_stride >= units, "x_stride smaller than a row");
+    LinParams P;
+    DeviceState* st = nullptr;
+    int rc = make_params(&P, d_x, x_fmt, x_stride, x_plane, n_time, d_W, a, b, key, rank, sigma,
+                         epoch, noise_reuse, tid_lo, n, rows_per_member, math, &st);
+    if (rc || n == 0) return rc;
+    HSES_REQUIRE(d_y, "NULL pointer");
     HSES_REQUIRE(y_stride >= a, "y_stride smaller than a row");
-    HSES_REQUIRE(n_time == 1 || (x_plane >= M * x_stride && y_plane >= M * y_stride),
+    HSES_REQUIRE(n_time == 1 || y_plane >= (int64_t)n * rows_per_member * y_stride,
                  "time planes overlap");
-    HSES_REQUIRE((int64_t)tid_lo + n - 1 <= INT32_MAX && tid_lo >= 0, "thread id range");
-    HSES_REQUIRE(M * n_time < (1ll << 40), "too many rows");
-    DeviceState* st;
-    int rc = get_state(&st);
-    if (rc) return rc;
-    LinParams P{};
-    P.x = d_x;
-    P.x_fmt = x_fmt;
-    P.x_stride = x_stride;
-    P.x_plane = x_plane;
-    P.n_time = n_time;
-    P.rpm = rows_per_member;
-    P.W = d_W;
-    P.a = a;
-    P.b = b;
-    P.key = key;
-    P.r = (sigma != 0.0f) ? rank : 0;
-    P.bs = rank > 0 ? sigma / sqrtf((float)rank) : 0.0f;  // eggroll.rs:433
-    P.epoch = epoch;
-    P.nreuse = noise_reuse;
-    P.tid_lo = tid_lo;
-    P.n = n;
     P.y = d_y;
     P.y_stride = y_stride;
     P.y_plane = y_plane;
-    P.math = math;
-    P.R = n_time * rows_per_member;
-    P.total = (int64_t)n * P.R;
-    P.tables = st->d_tables;
-    P.log_exc = st->d_log_exc;
-    P.cos_exc = st->d_cos_exc;
     hipStream_t s = (hipStream_t)stream;
     rc = launch_linear_pair(P, st, s, d_work, work_bytes);
     if (rc != HSES_ERR_UNSUPPORTED) return rc;
@@ -325,5 +340,37 @@ extern "C" int hses_perturbed_linear(const void* d_x, int32_t x_fmt, int64_t x_s
         return set_error(HSES_ERR_UNSUPPORTED,
                          "hses_perturbed_linear: no kernel for this rank/shape (members per "
                          "64-row tile x rank must be <= 64, or rank a multiple of 16)");
+    return rc;
+}
+
+extern "C" int hses_perturbed_linear_lif(const void* d_x, int32_t x_fmt, int64_t x_stride,
+                                         int64_t x_plane, int32_t n_time, const float* d_W,
+                                         int32_t a, int32_t b, uint64_t key, int32_t rank,
+                                         float sigma, int32_t epoch, int32_t noise_reuse,
+                                         int32_t tid_lo, int32_t n, int32_t rows_per_member,
+                                         float tau_m, float v_th, uint64_t* d_spikes,
+                                         int64_t spk_stride, int64_t spk_plane, float* d_rate,
+                                         int64_t rate_stride, void* d_work, size_t work_bytes,
+                                         void* stream) {
+    HSES_REQUIRE(tau_m != 0.0f, "tau_m must be non-zero");
+    LinParams P;
+    DeviceState* st = nullptr;
+    int rc = make_params(&P, d_x, x_fmt, x_stride, x_plane, n_time, d_W, a, b, key, rank, sigma,
+                         epoch, noise_reuse, tid_lo, n, rows_per_member, HSES_MATH_BF16, &st);
+    if (rc || n == 0) return rc;
+    HSES_REQUIRE(d_spikes || d_rate, "spikes and rate are both NULL");
+    const int64_t M = (int64_t)n * rows_per_member;
+    HSES_REQUIRE(!d_spikes || spk_stride >= (a + 63) / 64, "spk_stride smaller than a row");
+    HSES_REQUIRE(!d_spikes || n_time == 1 || spk_plane >= M * spk_stride, "time planes overlap");
+    HSES_REQUIRE(!d_rate || rate_stride >= a, "rate_stride smaller than a row");
+    HSES_REQUIRE(P.r > 0, "the fused kernel needs rank > 0 and sigma != 0");
+    HSES_REQUIRE(n_time <= 64 && (n_time & (n_time - 1)) == 0, "n_time must be a power of two <= 64");
+    HSES_REQUIRE(x_fmt == HSES_FMT_BITS, "the fused kernel takes bit-packed spikes (x_fmt BITS)");
+    LifOut lif{d_spikes, spk_stride, spk_plane, d_rate, rate_stride,
+               1.0f / tau_m /* snn.rs:59: dt / tau_m with dt = 1 */, v_th};
+    rc = launch_linear_pair(P, st, (hipStream_t)stream, d_work, work_bytes, &lif);
+    if (rc == HSES_ERR_UNSUPPORTED)
+        return set_error(HSES_ERR_UNSUPPORTED,
+                         "hses_perturbed_linear_lif: needs rank a multiple of 16 <= 128 and a <= 128");
     return rc;
 }

@@ -100,8 +100,18 @@ __device__ __forceinline__ void load_x_seg(const void* x, int64_t off, bool vali
     }
 }
 
+// Fused LIF output of the large-rank kernel (see hses_perturbed_linear_lif).
+struct LifOut {
+    void* spk;  // bit-packed spikes (T, M, words) or NULL
+    int64_t spk_stride, spk_plane;
+    float* rate;  // (M, a) spike rates or NULL
+    int64_t rate_stride;
+    float leak, v_th;
+};
+
 int launch_linear_small(LinParams& P, DeviceState* st, hipStream_t s);
-int launch_linear_pair(LinParams& P, DeviceState* st, hipStream_t s, void* work, size_t work_bytes);
+int launch_linear_pair(LinParams& P, DeviceState* st, hipStream_t s, void* work, size_t work_bytes,
+                       const LifOut* lif = nullptr);
 size_t linear_pair_workspace(const DeviceState* st, int32_t a, int32_t b, int32_t r, int32_t n);
 
 }  // namespace hses

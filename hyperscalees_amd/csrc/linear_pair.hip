@@ -11,14 +11,25 @@
 //      staging slot of the caller's workspace (bf16, k-contiguous per rank
 //      column; 200 KB at b = 784, more than LDS holds), each factor row by
 //      one thread continuing its row of the stream;
-//   2. for each 256-row block of the pair's rows: C = X [W^T | B] with
-//      bf16 MFMA (8 waves as 4 row groups x {base, xB}); binary activations
-//      arrive bit-packed and are expanded in LDS;
+//   2. for each 256-row block of the pair's rows: C = X [W^T | B] with bf16
+//      MFMA.  Eight waves tile the block as 4 row groups x 2 column halves;
+//      a wave owns 64 rows x (64 W columns + 64 B columns).  W/B tiles of 64 k
+//      are double-buffered in LDS with the next tile prefetched into
+//      registers during the current tile's MFMAs (one barrier per tile).
+//      Bit-packed activations stay packed in LDS (one 64-bit word per row and
+//      tile) and are expanded straight into MFMA operand registers;
 //   3. epilogue: y = base + (sign_m xB) A^T with a second MFMA over K = r,
-//      stored as fp32.
+//      then either stored as fp32 or (fused LIF) transposed through LDS so
+//      each lane holds one output column's whole time series, run through
+//      the LIF update, and written as ballot-packed spike words and/or
+//      spike rates; the fp32 currents never reach HBM.
+// Rows inside a member are taken slot-major (q = s * T + t), so the T time
+// steps of one (member, slot) are consecutive rows of one wave's row group.
 // The (n, b, r) factor tensor is never materialised: at most one B per
 // workgroup exists at any time.
 #include <math.h>
+
+#include <type_traits>
 
 #include "linear_common.h"
 #include "mfma.h"
@@ -27,74 +38,254 @@
 
 namespace hses {
 
-constexpr int K2_THREADS = 512, K2_RB = 256, K2_BK = 32, K2_AMAX = 128, K2_RMAX = 128;
-constexpr int K2_XP = K2_BK + 8;  // bf16 tile pitch (elements)
+constexpr int K2_THREADS = 512, K2_RB = 256, K2_BK = 64, K2_NMAX = 128;
+constexpr int K2_TP = K2_BK + 8;          // W/B tile pitch in bf16 elements (144 B)
+constexpr int K2_COLS = 2 * K2_NMAX;      // staged columns per tile: W rows | B columns
+constexpr int K2_LP = 20;                 // LIF transpose pitch (floats) per column
+enum { EPI_Y = 0, EPI_LIF = 1 };
 
 struct K2Layout {
-    size_t off_a, off_xbits, off_x, off_w, off_b, off_xb, bytes;
-    int32_t apitch, xbpitch, words;
-    __host__ __device__ K2Layout(int r, int b) {
+    size_t off_a, off_xbits, off_wb, bytes;
+    int32_t apitch, words, kp;
+    __host__ __device__ K2Layout(int r, int b, bool bits) {
         // the second product steps K (= r) by 32: pad rows to a multiple of 32
         apitch = (r + 31) / 32 * 32 + 8;
-        xbpitch = apitch;
         words = (b + 63) / 64;
+        kp = words * 64;
         size_t o = align16(sizeof(BmTables));
         off_a = o;
-        o = align16(o + (size_t)K2_AMAX * apitch * 2);
-        const size_t stage0 = o;
+        o = align16(o + (size_t)K2_NMAX * apitch * 2);
         off_xbits = o;
-        o = align16(o + (size_t)K2_RB * words * 8);
-        off_x = o;
-        o = align16(o + (size_t)K2_RB * K2_XP * 2);
-        off_w = o;
-        o = align16(o + (size_t)K2_AMAX * K2_XP * 2);
-        off_b = o;
-        o = align16(o + (size_t)K2_RMAX * K2_XP * 2);
-        off_xb = stage0;  // xB staging reuses the K-loop buffers
-        const size_t xb_end = align16(stage0 + (size_t)K2_RB * xbpitch * 2);
-        bytes = o > xb_end ? o : xb_end;
+        if (bits) o = align16(o + (size_t)K2_RB * words * 8);
+        off_wb = o;
+        const size_t wb = (size_t)2 * K2_COLS * K2_TP * 2;  // two tile buffers
+        const size_t xbs = (size_t)K2_RB * apitch * 2;      // epilogue alias
+        bytes = o + (wb > xbs ? wb : xbs);
     }
 };
 
-struct K2Extra {
-    uint16_t* slots;        // [grid][r][bpitch] bf16
-    const uint16_t* wbf;    // W as bf16 (a, b)
-    int32_t bpitch;         // k pitch of a slot (multiple of 8)
-    int32_t pair_lo, n_pairs;
+struct K2Args {
+    const void* x;
+    int64_t x_stride, x_plane;
+    const uint16_t* wbf;  // W as bf16, (a, kp), zero for k >= b
+    uint16_t* slots;      // per workgroup (r, kp) bf16 staging of B^T
+    float* y;
+    int64_t y_stride, y_plane;
+    uint64_t key;
+    const BmTables* tables;
+    const uint32_t* log_exc;
+    const uint32_t* cos_exc;
+    const uint64_t* jump;
+    uint64_t* spk;  // fused LIF: spike words (T, M, words), or NULL
+    int64_t spk_stride, spk_plane;
+    float* rate;    // fused LIF: spike counts / T (M, a), or NULL
+    int64_t rate_stride;
+    int32_t a, b, r, R, rpm, T, n, tid_lo, pair_lo, n_pairs, epoch, nreuse;
+    float bs, leak, v_th;
 };
 
-__global__ void k_w_to_bf16(const float* __restrict__ W, int64_t len, uint16_t* __restrict__ out) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < len) out[i] = f2bf(W[i]);
+// Rows of a block are addressed relative to the block start L0 = m0 * R + q0:
+// row L0 + i belongs to member m0 or m0 + 1 (a block never leaves its pair),
+// so a conditional subtraction replaces 64-bit division.
+struct RowCursor {
+    int32_t m0, q0;
+    __device__ __forceinline__ void at(int32_t i, int32_t R, int32_t* m, int32_t* q) const {
+        int32_t qq = q0 + i, mm = m0;
+        if (qq >= R) {
+            qq -= R;
+            ++mm;
+        }
+        *m = mm;
+        *q = qq;
+    }
+};
+
+// Physical element offset of row q (slot-major: q = s * T + t) of member m.
+__device__ __forceinline__ int64_t k2_phys(int32_t m, int32_t q, int32_t rpm, int32_t T,
+                                           int64_t stride, int64_t plane) {
+    const int32_t s = (int32_t)((uint32_t)q / (uint32_t)T);
+    const int32_t t = q - s * T;
+    return t * plane + ((int64_t)m * rpm + s) * stride;
 }
 
+// W (a, b) fp32 -> (a, kp) bf16 with zero columns [b, kp).
+__global__ void k_w_to_bf16(const float* __restrict__ W, int32_t a, int32_t b, int32_t kp,
+                            uint16_t* __restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)a * kp) return;
+    const int32_t row = (int32_t)(i / kp), k = (int32_t)(i % kp);
+    out[i] = k < b ? f2bf(W[(int64_t)row * b + k]) : (uint16_t)0;
+}
+
+// Eight bits of x (bit e = column k0 + e) as an MFMA operand of 0.0 / 1.0 bf16.
+// Dword q holds elements 2q (low half) and 2q+1 (high half):
+// y = byte | byte << 15 puts bit 2q at 2q and bit 2q+1 at 16 + 2q, and the
+// multiply by 0x3F80 >> 2q moves both to their half-word as bf16 1.0.
+__device__ __forceinline__ u16x8 expand_bits(uint32_t byte) {
+    const uint32_t y = byte | (byte << 15);
+    uint32_t d[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) d[q] = __umul24(y & (0x10001u << (2 * q)), 0x3F80u >> (2 * q));
+    u16x8 v;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        v[2 * q] = (uint16_t)d[q];
+        v[2 * q + 1] = (uint16_t)(d[q] >> 16);
+    }
+    return v;
+}
+
+// Eight activations of one row from a dense format, as bf16.
 template <int XFMT>
-__global__ __launch_bounds__(K2_THREADS) void k_linear_pair(LinParams P, K2Extra E) {
+__device__ __forceinline__ u16x8 dense_frag(const void* x, int64_t off, bool valid, int32_t k0,
+                                            int32_t b) {
+    u16x8 v;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const bool ok = valid && k0 + e < b;
+        if constexpr (XFMT == HSES_FMT_F32)
+            v[e] = ok ? f2bf(static_cast<const float*>(x)[off + k0 + e]) : (uint16_t)0;
+        else if constexpr (XFMT == HSES_FMT_BF16)
+            v[e] = ok ? static_cast<const uint16_t*>(x)[off + k0 + e] : (uint16_t)0;
+        else
+            v[e] = ok ? f2bf((float)static_cast<const uint8_t*>(x)[off + k0 + e]) : (uint16_t)0;
+    }
+    return v;
+}
+
+// Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
+// Lane L of (lo, hi) <- the wave-uniform 64-bit value w (v_writelane with an
+// inline-constant lane: one scalar operand, no lane masks).
+template <int L>
+__device__ __forceinline__ void put_lane(uint32_t& lo, uint32_t& hi, uint64_t w) {
+    asm volatile("v_writelane_b32 %0, %1, %2" : "+v"(lo) : "s"((uint32_t)w), "n"(L));
+    asm volatile("v_writelane_b32 %0, %1, %2" : "+v"(hi) : "s"((uint32_t)(w >> 32)), "n"(L));
+}
+
+// Fused LIF on a wave's 64 rows x 64 output columns of currents (acc[i][j]:
+// rows 16i + 4kg + v, columns 64h + 16j + li).  Per 16-row tile the currents
+// go through a per-wave LDS scratch S[column][row] so lane l holds column
+// 64h + l for 16 consecutive rows; the row group's rows are whole T-step
+// series (T divides 64, slot-major rows), scanned in order with the update of
+// hses_lif_scan (snn.rs:53-97) from v = 0.  Spikes of row u are ballot-packed
+// into the 64-bit word of columns [64h, 64h + 64) held by lane u.  T is a
+// template parameter so series boundaries are static.
+template <int T>
+__device__ __forceinline__ void lif_epilogue(const K2Args& P, const f32x4 (&acc)[4][8], float* S,
+                                             const RowCursor& cur_rows, int wr, int h, int lane,
+                                             int li, int kg, int32_t nvalid) {
+    static_assert(T >= 1 && T <= 64 && (T & (T - 1)) == 0, "T must be a power of two <= 64");
+    __syncthreads();  // every wave has finished reading XBs, which S aliases
+    const bool col_ok = h * 64 + lane < P.a;
+    uint32_t wlo = 0, whi = 0;  // lane u: spike word of row u (low / high half)
+    float vm = 0.0f;
+    int32_t cnt = 0;
+    static_for<0, 4>([&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            *reinterpret_cast<f32x4*>(&S[(16 * j + li) * K2_LP + 4 * kg]) = acc[i][j];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        f32x4 c4[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) c4[q] = *reinterpret_cast<const f32x4*>(&S[lane * K2_LP + 4 * q]);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        static_for<0, 16>([&](auto uc) {
+            constexpr int u = decltype(uc)::value;
+            constexpr int rr = 16 * i + u;  // row inside the row group; time step rr % T
+            if constexpr (rr % T == 0) {
+                vm = 0.0f;
+                cnt = 0;
+            }
+            const float c = c4[u >> 2][u & 3];
+            // snn.rs:61-63: charged = v + ((-v) + c) * leak; each op rounds.
+            const float charged = __fadd_rn(vm, __fmul_rn(__fadd_rn(-vm, c), P.leak));
+            const bool spike = charged >= P.v_th;
+            vm = __fmul_rn(charged, __fadd_rn(spike ? -1.0f : -0.0f, 1.0f));
+            cnt += spike ? 1 : 0;
+            put_lane<rr>(wlo, whi, __builtin_amdgcn_ballot_w64(spike && col_ok));
+            if constexpr (rr % T == T - 1) {
+                // spike rate of the series: count / T (exact: T is a power of two)
+                const int32_t row = wr * 64 + rr;
+                if (P.rate && row < nvalid && col_ok) {
+                    int32_t m, q;
+                    cur_rows.at(row, P.R, &m, &q);
+                    P.rate[((int64_t)m * P.rpm + q / T) * P.rate_stride + h * 64 + lane] =
+                        (float)cnt * (1.0f / T);
+                }
+            }
+        });
+    });
+    if (P.spk && h * 64 < P.a) {
+        const int32_t row = wr * 64 + lane;
+        if (row < nvalid) {
+            int32_t m, q;
+            cur_rows.at(row, P.R, &m, &q);
+            P.spk[k2_phys(m, q, P.rpm, T, P.spk_stride, P.spk_plane) + h] =
+                ((uint64_t)whi << 32) | wlo;
+        }
+    }
+}
+
+__device__ __forceinline__ uint4 mask4(uint4 v, uint32_t m) {
+    return uint4{v.x & m, v.y & m, v.z & m, v.w & m};
+}
+
+// EPI: EPI_Y stores y; EPI_LIF + T (a power of two <= 64) runs the fused LIF.
+template <int XFMT, int EPI, int LT = 1>
+__global__ __launch_bounds__(K2_THREADS) void k_linear_pair(const K2Args P) {
+    constexpr bool BITS = XFMT == HSES_FMT_BITS;
     extern __shared__ __align__(16) unsigned char smem[];
-    const K2Layout lay(P.r, P.b);
+    const K2Layout lay(P.r, P.b, BITS);
     BmTables* tabs = reinterpret_cast<BmTables*>(smem);
     uint16_t* As = reinterpret_cast<uint16_t*>(smem + lay.off_a);
     uint64_t* Xbits = reinterpret_cast<uint64_t*>(smem + lay.off_xbits);
-    uint16_t* Xs = reinterpret_cast<uint16_t*>(smem + lay.off_x);
-    uint16_t* Ws = reinterpret_cast<uint16_t*>(smem + lay.off_w);
-    uint16_t* Bts = reinterpret_cast<uint16_t*>(smem + lay.off_b);
-    uint16_t* XBs = reinterpret_cast<uint16_t*>(smem + lay.off_xb);
+    const uint32_t* Xbits32 = reinterpret_cast<const uint32_t*>(smem + lay.off_xbits);
+    uint16_t* WB = reinterpret_cast<uint16_t*>(smem + lay.off_wb);  // [2][K2_COLS][K2_TP]
+    uint16_t* XBs = WB;                                               // [K2_RB][apitch]
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
     const int li = lane & 15, kg = lane >> 4;
-    const int32_t r = P.r, a = P.a, b = P.b, R = P.R;
-    uint16_t* slot = E.slots + (size_t)blockIdx.x * r * E.bpitch;
-    const int wr = wave >> 1;        // row group: rows [64*wr, 64*wr+64) of the block
-    const int wc = wave & 1;         // 0: base columns (x W^T), 1: xB columns
-    const int ncols = wc == 0 ? a : r;
-    const int ntile = (ncols + 15) / 16;
+    const int wr = wave >> 1, h = wave & 1;
+    const int32_t r = P.r, a = P.a, b = P.b, kp = lay.kp, nkt = lay.words, R = P.R;
+    const int32_t rp32 = (r + 31) & ~31;
+    uint16_t* slot = P.slots + (size_t)blockIdx.x * r * kp;
 
     load_bm_tables(tabs, P.tables);
+    // generation never writes k >= b: zero the slot's padding once
+    for (int32_t i = tid; i < r * (kp - b); i += K2_THREADS) {
+        const int32_t c = i / (kp - b), k = b + i % (kp - b);
+        slot[(size_t)c * kp + k] = 0;
+    }
+    __threadfence_block();
     __syncthreads();
     const NoiseCtx ctx{tabs, P.log_exc, P.cos_exc};
 
-    for (int32_t pi = blockIdx.x; pi < E.n_pairs; pi += gridDim.x) {
-        const int32_t pair = E.pair_lo + pi;
+    // Tile loader: thread -> (staged column, 32-k half).  Columns [0, 128) are
+    // W rows, [128, 256) rank columns of B; absent ones load a valid row and
+    // are staged as zeros (a select, so the loads stay unconditional).
+    const int lcol = tid >> 1, lk = (tid & 1) * 32;
+    const bool lvalid = lcol < K2_NMAX ? lcol < a : lcol - K2_NMAX < r;
+    const uint16_t* lsrc = lcol < K2_NMAX ? P.wbf + (size_t)min(lcol, a - 1) * kp + lk
+                                          : slot + (size_t)min(lcol - K2_NMAX, r - 1) * kp + lk;
+    const uint32_t lmask = lvalid ? 0xffffffffu : 0u;
+    uint16_t* ldst = WB + lcol * K2_TP + lk;
+
+    for (int32_t pi = blockIdx.x; pi < P.n_pairs; pi += gridDim.x) {
+        const int32_t pair = P.pair_lo + pi;
         // Members of this pair inside the launch: m_lo .. m_hi (local indices).
         const int32_t m_even = 2 * pair - P.tid_lo;
         const int32_t m_lo = max(m_even, 0), m_hi = min(m_even + 1, P.n - 1);
@@ -109,17 +300,12 @@ __global__ __launch_bounds__(K2_THREADS) void k_linear_pair(LinParams P, K2Extra
             for (int32_t j = tid; j < a + b; j += K2_THREADS) {
                 uint64_t s = row_start_state(seed, j, P.jump);
                 if (j < b) {
-                    bm_run(s, r, ctx, [&](int32_t c, float v) { slot[(size_t)c * E.bpitch + j] = f2bf(v); });
+                    bm_run(s, r, ctx, [&](int32_t c, float v) { slot[(size_t)c * kp + j] = f2bf(v); });
                 } else {
                     uint16_t* dst = As + (size_t)(j - b) * lay.apitch;
                     bm_run(s, r, ctx, [&](int32_t c, float v) { dst[c] = f2bf(v * P.bs); });
-                    for (int32_t c = r; c < ((r + 31) & ~31); ++c) dst[c] = 0;
+                    for (int32_t c = r; c < rp32; ++c) dst[c] = 0;
                 }
-            }
-            // zero the k-padding of the slot so the last K tile reads zeros
-            for (int32_t i = tid; i < r * (E.bpitch - b); i += K2_THREADS) {
-                const int32_t c = i / (E.bpitch - b), k = b + i % (E.bpitch - b);
-                slot[(size_t)c * E.bpitch + k] = 0;
             }
             __threadfence_block();
             __syncthreads();
@@ -133,132 +319,138 @@ __global__ __launch_bounds__(K2_THREADS) void k_linear_pair(LinParams P, K2Extra
 #pragma unroll
                 for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0, 0, 0, 0};
 
-            if constexpr (XFMT == HSES_FMT_BITS) {
-                // Whole bit rows of the block into LDS once.
-                for (int32_t i = tid; i < K2_RB * lay.words; i += K2_THREADS) {
-                    const int32_t row = i / lay.words, w = i % lay.words;
-                    const int64_t Lr = L0 + row;
-                    Xbits[i] = Lr < row_hi
-                                   ? static_cast<const uint64_t*>(P.x)[phys_row(P, Lr, P.x_stride, P.x_plane) + w]
+            RowCursor cur_rows;
+            cur_rows.m0 = (int32_t)(L0 / R);
+            cur_rows.q0 = (int32_t)(L0 - (int64_t)cur_rows.m0 * R);
+            const int32_t nvalid = (int32_t)min<int64_t>(row_hi - L0, K2_RB);
+            int64_t xoff[4];
+            bool xval[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int32_t row = wr * 64 + i * 16 + li;
+                xval[i] = row < nvalid;
+                int32_t m, q;
+                cur_rows.at(row, R, &m, &q);
+                xoff[i] = (!BITS && xval[i]) ? k2_phys(m, q, P.rpm, P.T, P.x_stride, P.x_plane) : 0;
+            }
+            if constexpr (BITS) {
+                // the block's bit rows, one word per tile
+                for (int32_t i = tid; i < K2_RB * nkt; i += K2_THREADS) {
+                    const int32_t row = i / nkt, w = i - row * nkt;
+                    int32_t m, q;
+                    cur_rows.at(row, R, &m, &q);
+                    Xbits[i] = row < nvalid
+                                   ? static_cast<const uint64_t*>(P.x)[k2_phys(m, q, P.rpm, P.T, P.x_stride, P.x_plane) + w]
                                    : 0ull;
                 }
-                __syncthreads();
             }
-            const int srow = tid >> 1, sk = (tid & 1) * 16;  // x staging: 256 rows x 2 x 16
-            const int64_t Ls = L0 + srow;
-            const bool svalid = Ls < row_hi;
-            const int64_t xoff = (XFMT != HSES_FMT_BITS && svalid) ? phys_row(P, Ls, P.x_stride, P.x_plane) : 0;
-
-            for (int32_t k0 = 0; k0 < b; k0 += K2_BK) {
-                // x tile (256 x 32) as bf16
-                if constexpr (XFMT == HSES_FMT_BITS) {
-                    const int32_t k = k0 + sk;
-                    uint32_t bits = (uint32_t)(Xbits[srow * lay.words + (k >> 6)] >> (k & 63)) & 0xffffu;
-                    if (b - k < 16) bits &= b - k > 0 ? (1u << (b - k)) - 1u : 0u;
-                    u16x8 v0, v1;
+            // tile 0 -> buffer 0
+            uint4 pf[4];
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) {
-                        v0[i] = ((bits >> i) & 1u) ? (uint16_t)0x3f80 : (uint16_t)0;
-                        v1[i] = ((bits >> (i + 8)) & 1u) ? (uint16_t)0x3f80 : (uint16_t)0;
-                    }
-                    *reinterpret_cast<u16x8*>(&Xs[srow * K2_XP + sk]) = v0;
-                    *reinterpret_cast<u16x8*>(&Xs[srow * K2_XP + sk + 8]) = v1;
-                } else {
-                    uint16_t v[16];
-                    load_x_seg<HSES_MATH_BF16, XFMT>(P.x, xoff, svalid, k0 + sk, b, v);
-                    load_x_seg<HSES_MATH_BF16, XFMT>(P.x, xoff, svalid, k0 + sk + 8, b, v + 8);
+            for (int q = 0; q < 4; ++q) pf[q] = reinterpret_cast<const uint4*>(lsrc)[q];
 #pragma unroll
-                    for (int i = 0; i < 16; ++i) Xs[srow * K2_XP + sk + i] = v[i];
-                }
-                // W tile (a x 32) and B tile (r x 32), 8 elements per thread
-                for (int32_t i = tid; i < (K2_AMAX + K2_RMAX) * 4; i += K2_THREADS) {
-                    const int32_t row = i >> 2, seg = (i & 3) * 8;
-                    u16x8 v = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
-                    if (row < K2_AMAX) {
-                        if (row < a) {
-                            const uint16_t* src = E.wbf + (size_t)row * b + k0 + seg;
-#pragma unroll
-                            for (int e = 0; e < 8; ++e) v[e] = (k0 + seg + e < b) ? src[e] : (uint16_t)0;
-                        }
-                        *reinterpret_cast<u16x8*>(&Ws[row * K2_XP + seg]) = v;
-                    } else {
-                        const int32_t c = row - K2_AMAX;
-                        if (c < r) v = *reinterpret_cast<const u16x8*>(slot + (size_t)c * E.bpitch + k0 + seg);
-                        *reinterpret_cast<u16x8*>(&Bts[c * K2_XP + seg]) = v;
-                    }
-                }
-                __syncthreads();
-                const uint16_t* Bop = wc == 0 ? Ws : Bts;
-                u16x8 af[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) af[i] = lds_u16x8(&Xs[(wr * 64 + i * 16 + li) * K2_XP + kg * 8]);
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    if (j >= ntile) break;
-                    const u16x8 bf = lds_u16x8(&Bop[(j * 16 + li) * K2_XP + kg * 8]);
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) acc[i][j] = mfma_bf16(af[i], bf, acc[i][j]);
-                }
-                __syncthreads();
-            }
-
-            // xB waves: sign_m * xB -> LDS as bf16 [row][c]
-            if (wc == 1) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) {
-                        const int row = wr * 64 + i * 16 + 4 * kg + v;
-                        const int64_t Lr = L0 + row;
-                        const int32_t m = (int32_t)(Lr / R);
-                        const float sgn = ((P.tid_lo + m) & 1) ? -1.0f : 1.0f;
-#pragma unroll
-                        for (int j = 0; j < 8; ++j) {
-                            if (j < ntile)
-                                XBs[row * lay.xbpitch + j * 16 + li] = f2bf(sgn * acc[i][j][v]);
-                            else if (j * 16 < ((r + 31) & ~31))
-                                XBs[row * lay.xbpitch + j * 16 + li] = 0;  // K tail of the 2nd product
-                        }
-                    }
-            }
+            for (int q = 0; q < 4; ++q) reinterpret_cast<uint4*>(ldst)[q] = mask4(pf[q], lmask);
             __syncthreads();
-            // base waves: acc += (sign xB) A^T  (K = r), then store y
-            if (wc == 0) {
-                for (int32_t c0 = 0; c0 < r; c0 += 32) {
-                    u16x8 xf[4];
+
+            for (int32_t kt = 0; kt < nkt; ++kt) {
+                const int cur = kt & 1;
+                const bool more = kt + 1 < nkt;
+                if (more) {
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) xf[i] = lds_u16x8(&XBs[(wr * 64 + i * 16 + li) * lay.xbpitch + c0 + kg * 8]);
+                    for (int q = 0; q < 4; ++q) pf[q] = reinterpret_cast<const uint4*>(lsrc + (kt + 1) * K2_BK)[q];
+                }
+                const uint16_t* tb = WB + cur * (K2_COLS * K2_TP);
+#pragma unroll
+                for (int s = 0; s < 2; ++s) {
+                    u16x8 xa[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        if constexpr (BITS) {
+                            const uint32_t w = Xbits32[(wr * 64 + i * 16 + li) * (2 * nkt) + 2 * kt + s];
+                            xa[i] = expand_bits((w >> (8 * kg)) & 0xffu);
+                        } else {
+                            xa[i] = dense_frag<XFMT>(P.x, xoff[i], xval[i], kt * K2_BK + s * 32 + kg * 8, b);
+                        }
+                    }
+                    // absent columns are staged as zeros: no guards, straight-line MFMAs
 #pragma unroll
                     for (int j = 0; j < 8; ++j) {
-                        if (j >= ntile) break;
-                        const u16x8 af2 = lds_u16x8(&As[(j * 16 + li) * lay.apitch + c0 + kg * 8]);
+                        const int col = (j < 4 ? 0 : K2_NMAX) + h * 64 + (j & 3) * 16 + li;
+                        const u16x8 bw = lds_u16x8(tb + col * K2_TP + s * 32 + kg * 8);
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) acc[i][j] = mfma_bf16(xf[i], af2, acc[i][j]);
+                        for (int i = 0; i < 4; ++i) acc[i][j] = mfma_bf16(xa[i], bw, acc[i][j]);
                     }
                 }
+                if (more) {
+                    uint16_t* nb = ldst + (cur ^ 1) * (K2_COLS * K2_TP);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) reinterpret_cast<uint4*>(nb)[q] = mask4(pf[q], lmask);
+                }
+                __syncthreads();
+            }
+
+            // xB -> LDS as bf16 [row][c], sign of the row's member applied
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int row = wr * 64 + i * 16 + 4 * kg + v;
+                    int32_t m, q;
+                    cur_rows.at(row, R, &m, &q);
+                    const float sgn = ((P.tid_lo + m) & 1) ? -1.0f : 1.0f;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int c = h * 64 + j * 16 + li;
+                        if (h * 64 + j * 16 < r) XBs[row * lay.apitch + c] = f2bf(sgn * acc[i][4 + j][v]);
+                    }
+                }
+            if (rp32 != r) {  // K tail of the second product
+                for (int32_t i = tid; i < K2_RB * 16; i += K2_THREADS)
+                    XBs[(i >> 4) * lay.apitch + r + (i & 15)] = 0;
+            }
+            __syncthreads();
+            // acc += (sign xB) A^T over K = r
+            for (int32_t c0 = 0; c0 < rp32; c0 += 32) {
+                u16x8 xf[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    xf[i] = lds_u16x8(&XBs[(wr * 64 + i * 16 + li) * lay.apitch + c0 + kg * 8]);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if (h * 64 + j * 16 >= a) continue;
+                    const u16x8 af = lds_u16x8(&As[(h * 64 + j * 16 + li) * lay.apitch + c0 + kg * 8]);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[i][j] = mfma_bf16(xf[i], af, acc[i][j]);
+                }
+            }
+            if constexpr (EPI == EPI_Y) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
 #pragma unroll
                     for (int v = 0; v < 4; ++v) {
-                        const int row = wr * 64 + i * 16 + 4 * kg + v;
-                        const int64_t Lr = L0 + row;
-                        if (Lr >= row_hi) continue;
-                        float* yrow = P.y + phys_row(P, Lr, P.y_stride, P.y_plane);
+                        const int32_t row = wr * 64 + i * 16 + 4 * kg + v;
+                        if (row >= nvalid) continue;
+                        int32_t m, q;
+                        cur_rows.at(row, R, &m, &q);
+                        float* yrow = P.y + k2_phys(m, q, P.rpm, P.T, P.y_stride, P.y_plane);
 #pragma unroll
-                        for (int j = 0; j < 8; ++j) {
-                            const int col = j * 16 + li;
-                            if (j < ntile && col < a) yrow[col] = acc[i][j][v];
+                        for (int j = 0; j < 4; ++j) {
+                            const int col = h * 64 + j * 16 + li;
+                            if (col < a) yrow[col] = acc[i][j][v];
                         }
                     }
+            } else {
+                lif_epilogue<LT>(P, acc, reinterpret_cast<float*>(WB) + wave * (64 * K2_LP), cur_rows,
+                             wr, h, lane, li, kg, nvalid);
             }
-            __syncthreads();
+            __syncthreads();  // XBs aliases the tile buffers; Xbits is restaged
         }
     }
 }
 
 static bool pair_kernel_applies(const LinParams& P) {
-    return P.math == HSES_MATH_BF16 && P.r >= 16 && P.r <= K2_RMAX && P.r % 16 == 0 &&
-           P.a <= K2_AMAX;
+    return P.math == HSES_MATH_BF16 && P.r >= 16 && P.r <= K2_NMAX && P.r % 16 == 0 &&
+           P.a <= K2_NMAX;
 }
 
 static int32_t pair_grid(const DeviceState* st, int32_t n_pairs) {
@@ -270,45 +462,94 @@ static void pair_range(int32_t tid_lo, int32_t n, int32_t* lo, int32_t* cnt) {
     *cnt = (tid_lo + n - 1) / 2 - *lo + 1;
 }
 
+static size_t pair_workspace_bytes(int32_t grid, int32_t a, int32_t b, int32_t r) {
+    const size_t kp = (size_t)(b + 63) / 64 * 64;
+    return align16((size_t)a * kp * 2) + (size_t)grid * r * kp * 2;
+}
+
 size_t linear_pair_workspace(const DeviceState* st, int32_t a, int32_t b, int32_t r, int32_t n) {
     int32_t lo, cnt;
     pair_range(0, n, &lo, &cnt);
-    const int32_t grid = pair_grid(st, cnt + 1);
-    const int32_t bpitch = (b + K2_BK - 1) / K2_BK * K2_BK + 8;
-    return align16((size_t)a * b * 2) + (size_t)grid * r * bpitch * 2;
+    return pair_workspace_bytes(pair_grid(st, cnt + 1), a, b, r);
 }
 
-int launch_linear_pair(LinParams& P, DeviceState* st, hipStream_t s, void* work, size_t work_bytes) {
+int launch_linear_pair(LinParams& P, DeviceState* st, hipStream_t s, void* work, size_t work_bytes,
+                       const LifOut* lif) {
     if (P.r == 0 || !pair_kernel_applies(P)) return HSES_ERR_UNSUPPORTED;
-    const K2Layout lay(P.r, P.b);
+    if (lif && (P.n_time > 64 || (P.n_time & (P.n_time - 1)) != 0 || P.x_fmt != HSES_FMT_BITS))
+        return HSES_ERR_UNSUPPORTED;
+    const bool bits = P.x_fmt == HSES_FMT_BITS;
+    const K2Layout lay(P.r, P.b, bits);
     if (lay.bytes > st->max_lds) return HSES_ERR_UNSUPPORTED;
-    K2Extra E{};
-    pair_range(P.tid_lo, P.n, &E.pair_lo, &E.n_pairs);
-    E.bpitch = (P.b + K2_BK - 1) / K2_BK * K2_BK + 8;
-    const int32_t grid = pair_grid(st, E.n_pairs);
-    const size_t need = align16((size_t)P.a * P.b * 2) + (size_t)grid * P.r * E.bpitch * 2;
+    K2Args A{};
+    pair_range(P.tid_lo, P.n, &A.pair_lo, &A.n_pairs);
+    const int32_t grid = pair_grid(st, A.n_pairs);
+    const size_t need = pair_workspace_bytes(grid, P.a, P.b, P.r);
     if (!work || work_bytes < need)
         return set_error(HSES_ERR_INVALID_ARG, "hses_perturbed_linear: workspace too small");
     uint16_t* wbf = static_cast<uint16_t*>(work);
-    E.wbf = wbf;
-    E.slots = reinterpret_cast<uint16_t*>(static_cast<char*>(work) + align16((size_t)P.a * P.b * 2));
+    A.wbf = wbf;
+    A.slots = reinterpret_cast<uint16_t*>(static_cast<char*>(work) + align16((size_t)P.a * lay.kp * 2));
     int rc = get_jump_table(st, P.r, (int64_t)P.a + P.b, &P.jump);
     if (rc) return rc;
-    const int64_t wl = (int64_t)P.a * P.b;
-    hipLaunchKernelGGL(k_w_to_bf16, dim3((uint32_t)((wl + 255) / 256)), dim3(256), 0, s, P.W, wl, wbf);
+    A.x = P.x;
+    A.x_stride = P.x_stride;
+    A.x_plane = P.x_plane;
+    A.y = P.y;
+    A.y_stride = P.y_stride;
+    A.y_plane = P.y_plane;
+    A.key = P.key;
+    A.tables = P.tables;
+    A.log_exc = P.log_exc;
+    A.cos_exc = P.cos_exc;
+    A.jump = P.jump;
+    A.a = P.a;
+    A.b = P.b;
+    A.r = P.r;
+    A.R = P.R;
+    A.rpm = P.rpm;
+    A.T = P.n_time;
+    if (lif) {
+        A.spk = static_cast<uint64_t*>(lif->spk);
+        A.spk_stride = lif->spk_stride;
+        A.spk_plane = lif->spk_plane;
+        A.rate = lif->rate;
+        A.rate_stride = lif->rate_stride;
+        A.leak = lif->leak;
+        A.v_th = lif->v_th;
+    }
+    A.n = P.n;
+    A.tid_lo = P.tid_lo;
+    A.epoch = P.epoch;
+    A.nreuse = P.nreuse;
+    A.bs = P.bs;
+    const int64_t wl = (int64_t)P.a * lay.kp;
+    hipLaunchKernelGGL(k_w_to_bf16, dim3((uint32_t)((wl + 255) / 256)), dim3(256), 0, s, P.W, P.a,
+                       P.b, lay.kp, wbf);
     HSES_CHECK_HIP(hipGetLastError());
     auto launch = [&](auto kern) -> int {
         if (lay.bytes > 64 * 1024)
             HSES_CHECK_HIP(hipFuncSetAttribute((const void*)kern,
                                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lay.bytes));
-        hipLaunchKernelGGL(kern, dim3(grid), dim3(K2_THREADS), lay.bytes, s, P, E);
+        hipLaunchKernelGGL(kern, dim3(grid), dim3(K2_THREADS), lay.bytes, s, A);
         HSES_CHECK_HIP(hipGetLastError());
         return HSES_OK;
     };
+    if (lif) {
+        switch (P.n_time) {
+            case 1: return launch(k_linear_pair<HSES_FMT_BITS, EPI_LIF, 1>);
+            case 2: return launch(k_linear_pair<HSES_FMT_BITS, EPI_LIF, 2>);
+            case 4: return launch(k_linear_pair<HSES_FMT_BITS, EPI_LIF, 4>);
+            case 8: return launch(k_linear_pair<HSES_FMT_BITS, EPI_LIF, 8>);
+            case 16: return launch(k_linear_pair<HSES_FMT_BITS, EPI_LIF, 16>);
+            case 32: return launch(k_linear_pair<HSES_FMT_BITS, EPI_LIF, 32>);
+            default: return launch(k_linear_pair<HSES_FMT_BITS, EPI_LIF, 64>);
+        }
+    }
     switch (P.x_fmt) {
-        case HSES_FMT_F32: return launch(k_linear_pair<HSES_FMT_F32>);
-        case HSES_FMT_BF16: return launch(k_linear_pair<HSES_FMT_BF16>);
-        default: return launch(k_linear_pair<HSES_FMT_BITS>);
+        case HSES_FMT_F32: return launch(k_linear_pair<HSES_FMT_F32, EPI_Y>);
+        case HSES_FMT_BF16: return launch(k_linear_pair<HSES_FMT_BF16, EPI_Y>);
+        default: return launch(k_linear_pair<HSES_FMT_BITS, EPI_Y>);
     }
 }
 

@@ -171,6 +171,41 @@ def perturbed_linear(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n, rows
     return out if n_time > 1 or x.dim() == 3 else out[0]
 
 
+def perturbed_linear_lif(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n,
+                         rows_per_member, n_time, tau_m, v_th, spikes=None, rate=None,
+                         want_spikes=True, want_rate=False):
+    """Perturbed forward fused with LIF.  x is bit-packed (n_time, M, words(b));
+    returns (spikes (n_time, M, words(a)) int64 or None, rate (M, a) or None)."""
+    a, b = W.shape
+    _dev(W, torch.float32, "W")
+    _dev(x, _FMT_DTYPE[FMT_BITS], "x")
+    units = fmt_width(FMT_BITS, b)
+    M = n * rows_per_member
+    if x.shape[-1] != units or x.numel() != n_time * M * units:
+        raise ValueError(f"x has shape {tuple(x.shape)}, expected ({n_time}, {M}, {units})")
+    wa = fmt_width(FMT_BITS, a)
+    if want_spikes and spikes is None:
+        spikes = torch.empty((n_time, M, wa), dtype=torch.int64, device=W.device)
+    if want_rate and rate is None:
+        rate = torch.empty((M, a), dtype=torch.float32, device=W.device)
+    if spikes is not None:
+        _dev(spikes, torch.int64, "spikes")
+        if spikes.numel() != n_time * M * wa:
+            raise ValueError("spikes has the wrong size")
+    if rate is not None:
+        _dev(rate, torch.float32, "rate")
+        if rate.numel() != M * a:
+            raise ValueError("rate has the wrong size")
+    wbytes = int(_lib.load().hses_perturbed_linear_workspace(a, b, rank, n, rows_per_member,
+                                                              n_time, MATH_BF16))
+    work = _workspace(wbytes, W.device)
+    _lib.call("hses_perturbed_linear_lif", _p(x), FMT_BITS, units, M * units, n_time, _p(W), a,
+              b, key & (2**64 - 1), rank, sigma, epoch, noise_reuse, tid_lo, n, rows_per_member,
+              tau_m, v_th, _p(spikes) if spikes is not None else None, wa, M * wa,
+              _p(rate) if rate is not None else None, a, _p(work), wbytes, _stream())
+    return spikes, rate
+
+
 def es_update(fit, tid_lo, key, rank, sigma, epoch, noise_reuse, a, b, scale, out=None,
               accumulate=False, work=None):
     """scale * sum_m fit[m] A_m B_m^T (factors regenerated in-kernel); adds into

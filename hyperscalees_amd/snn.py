@@ -97,7 +97,7 @@ def init_weights(dims, seed=0, gain=1.0):
 class SnnEs:
     """Device-resident SNN-MLP population evaluation and ES update."""
 
-    def __init__(self, cfg, weights, pool, pool_labels, index, device="cuda"):
+    def __init__(self, cfg, weights, pool, pool_labels, index, device="cuda", fused=None):
         self.cfg = cfg
         c = cfg
         self.dev = device
@@ -114,7 +114,14 @@ class SnnEs:
         self.spk = [torch.empty((c.T, M, K.fmt_width(FMT_BITS, d)), dtype=torch.int64, device=device)
                     for d in c.dims[:-1]]
         hmax = max(c.dims[1:-1]) if L > 1 else 1
-        self.cur = torch.empty((c.T, M, hmax), dtype=torch.float32, device=device)
+        # Hidden layers run as one fused forward+LIF kernel when the
+        # large-rank kernel applies; the fp32 currents then never exist.
+        can_fuse = (c.math == MATH_BF16 and c.sigma != 0.0 and c.rank % 16 == 0
+                    and 16 <= c.rank <= 128 and hmax <= 128 and c.T <= 64
+                    and (c.T & (c.T - 1)) == 0)
+        self.fused = can_fuse if fused is None else (bool(fused) and can_fuse)
+        self.cur = None if self.fused else \
+            torch.empty((c.T, M, hmax), dtype=torch.float32, device=device)
         self.rate = torch.empty((M, c.dims[-2]), dtype=torch.float32, device=device)
         self.logits = torch.empty((M, c.dims[-1]), dtype=torch.float32, device=device)
         self.grads = [torch.zeros_like(w) for w in self.W]
@@ -131,6 +138,14 @@ class SnnEs:
     def hidden_layer(self, l, epoch):
         c = self.cfg
         a = c.dims[l + 1]
+        if self.fused:
+            last = l == self.L - 2  # feeds the readout: only its spike rates are used
+            K.perturbed_linear_lif(self.spk[l], self.W[l], c.keys[l], c.rank, c.sigma, epoch,
+                                   c.noise_reuse, 0, c.n, c.rows, c.T, c.tau_m, c.v_th,
+                                   spikes=None if last else self.spk[l + 1],
+                                   rate=self.rate if last else None,
+                                   want_spikes=not last, want_rate=last)
+            return
         cur = self.cur[:, :, :a] if a == self.cur.shape[2] else \
             self.cur.view(-1)[: c.T * self.M * a].view(c.T, self.M, a)
         K.perturbed_linear(self.spk[l], self.W[l], c.keys[l], c.rank, c.sigma, epoch,
@@ -140,7 +155,8 @@ class SnnEs:
 
     def readout(self, epoch):
         c = self.cfg
-        K.spike_rate(self.spk[self.L - 1], FMT_BITS, c.dims[-2], out=self.rate)
+        if not self.fused:
+            K.spike_rate(self.spk[self.L - 1], FMT_BITS, c.dims[-2], out=self.rate)
         K.perturbed_linear(self.rate, self.W[-1], c.keys[-1], c.rank, c.sigma, epoch,
                            c.noise_reuse, 0, c.n, c.rows, x_fmt=FMT_F32, n_time=1, math=c.math,
                            out=self.logits.view(1, self.M, -1))

@@ -146,6 +146,28 @@ int hses_perturbed_linear(const void *d_x, int32_t x_fmt, int64_t x_stride, int6
                           float *d_y, int64_t y_stride, int64_t y_plane, int32_t math,
                           void *d_work, size_t work_bytes, void *stream);
 
+/* Perturbed forward fused with the LIF layer that consumes it
+ * (forward_batched_lora_half_with_lif, snn.rs:544-595: lora_linear_batched
+ * then run_lif, snn.rs:53-97; kernel lif_fused_oxide.rs:37-70).  The currents
+ * are exactly those hses_perturbed_linear computes for the same arguments
+ * (bf16 math) and never reach memory: every (member, slot, output) series over
+ * n_time steps is run through hses_lif_scan's update from v0 = 0, giving
+ *   d_spikes (n_time, n*rows_per_member, ceil(a/64)) bit-packed words with row
+ *            stride spk_stride and time planes spk_plane apart, or NULL;
+ *   d_rate   (n*rows_per_member, a) spike count / n_time with row stride
+ *            rate_stride (snn.rs:274, mean over time), or NULL.
+ * x must be bit-packed (HSES_FMT_BITS); n_time a power of two <= 64; rank a
+ * multiple of 16 <= 128, a <= 128, sigma != 0.  d_work as for
+ * hses_perturbed_linear (same workspace size query). */
+int hses_perturbed_linear_lif(const void *d_x, int32_t x_fmt, int64_t x_stride, int64_t x_plane,
+                              int32_t n_time, const float *d_W, int32_t a, int32_t b,
+                              uint64_t key, int32_t rank, float sigma, int32_t epoch,
+                              int32_t noise_reuse, int32_t tid_lo, int32_t n,
+                              int32_t rows_per_member, float tau_m, float v_th,
+                              uint64_t *d_spikes, int64_t spk_stride, int64_t spk_plane,
+                              float *d_rate, int64_t rate_stride, void *d_work,
+                              size_t work_bytes, void *stream);
+
 /* ---- ES update ------------------------------------------------------- */
 
 /* EggRoll ES gradient of one MM parameter (eggroll.rs:353-404 _simple_lora_update +

@@ -156,8 +156,55 @@ def test_perturbed_linear_pair_kernel(hses_gpu, n, rpm, T, a, b, r, tid_lo, fmt)
     assert_close(y, ref_forward(x3, W, A, B, rpm), 2e-2)
 
 
+def test_pair_kernel_many_pairs_per_workgroup(hses_gpu):
+    """More pairs than workgroups: each persistent workgroup reuses its B
+    staging slot and LDS for several pairs in a row."""
+    n, rpm, T, a, b, r = 600, 2, 1, 32, 96, 32
+    rng = np.random.default_rng(5)
+    x3 = (rng.random((T, n * rpm, b)) < 0.3).astype(np.float32)
+    W = (rng.standard_normal((a, b)) / np.sqrt(b)).astype(np.float32)
+    A, B = factors(0.2, r, n, 0, a, b)
+    y = run(hses_gpu, x3, W, r, 0.2, n, rpm, 0, fmt=FMT_BITS, math=MATH_BF16)
+    assert_close(y, ref_forward_bf16(x3, W, A, B, rpm), 2e-3)
+
+
 def test_device_properties(hses_gpu):
     p = torch.cuda.get_device_properties(0)
     print("device", p.name, "CUs", p.multi_processor_count,
           "smem/block", getattr(p, "shared_memory_per_block", None),
           "smem/mp", getattr(p, "shared_memory_per_multiprocessor", None))
+
+
+@pytest.mark.parametrize("n,rpm,T,a,b,r,tid_lo", [
+    (4, 64, 16, 128, 784, 128, 0),   # C3 fc1
+    (3, 64, 16, 128, 128, 128, 1),   # C3 fc2/fc3 shape, partial pairs at both ends
+    (5, 12, 8, 100, 200, 64, 0),     # partial spike word (a = 100), r = 64
+    (4, 3, 1, 64, 96, 16, 0),        # T = 1
+    (2, 5, 32, 70, 130, 48, 1),      # T = 32, r % 32 == 16
+    (600, 1, 4, 32, 64, 32, 0),      # more pairs than workgroups
+])
+def test_fused_lif_matches_unfused(hses_gpu, n, rpm, T, a, b, r, tid_lo):
+    """hses_perturbed_linear_lif == hses_lif_scan(hses_perturbed_linear(...))
+    bit for bit (spikes), and its rates == hses_spike_rate of those spikes.
+    The unfused currents are pinned against the oracle by the tests above."""
+    rng = np.random.default_rng(n * 7 + T)
+    x3 = (rng.random((T, n * rpm, b)) < 0.3).astype(np.float32)
+    W = (rng.standard_normal((a, b)) * (6.0 / np.sqrt(b))).astype(np.float32)
+    xb = pack_bits(x3)
+    Wt = torch.from_numpy(W).cuda()
+    tau, vth = 10.0, (1.0 if T > 4 else 0.25)  # short series need a lower threshold to spike
+    y = hses_gpu.perturbed_linear(xb, Wt, KEY, r, 0.2, 3, 0, tid_lo, n, rpm, x_fmt=FMT_BITS,
+                                  n_time=T, math=MATH_BF16)
+    spk_ref = hses_gpu.lif_scan(y.view(T, n * rpm, a), tau, vth, fmt=FMT_BITS)
+    rate_ref = hses_gpu.spike_rate(spk_ref, FMT_BITS, a)
+    spk, rate = hses_gpu.perturbed_linear_lif(xb, Wt, KEY, r, 0.2, 3, 0, tid_lo, n, rpm, T, tau,
+                                              vth, want_rate=True)
+    torch.cuda.synchronize()
+    assert torch.equal(spk, spk_ref)
+    assert torch.equal(rate, rate_ref)
+    mean = float(rate.mean())
+    assert 0.005 < mean < 0.95, mean
+    # spikes only: same words
+    spk2, none = hses_gpu.perturbed_linear_lif(xb, Wt, KEY, r, 0.2, 3, 0, tid_lo, n, rpm, T, tau,
+                                               vth)
+    assert none is None and torch.equal(spk2, spk_ref)

@@ -26,11 +26,11 @@ def unpack(words, width):
     return bits.reshape(*w.shape[:-1], -1)[..., :width]
 
 
-def make(cfg, pool_size=3000, seed=0):
+def make(cfg, pool_size=3000, seed=0, fused=False):
     pool, labels = snn.synthetic_pool(pool_size, cfg.dims[0], cfg.dims[-1], seed)
     idx = snn.sample_index(seed, cfg.n, cfg.rows, pool_size)
     W = snn.init_weights(cfg.dims, seed, gain=snn.ACTIVE_GAIN)
-    return snn.SnnEs(cfg, W, pool, labels, idx), pool, labels, idx, W
+    return snn.SnnEs(cfg, W, pool, labels, idx, fused=fused), pool, labels, idx, W
 
 
 def oracle_layer(x_tm, W, cfg, l):
@@ -155,3 +155,20 @@ def test_c3_shape_bf16_step(hses_gpu):
     l = 1
     g = O.lora_grad_f64(cfg.sigma, cfg.keys[l], cfg.rank, 0, z, 128, 128)
     assert np.allclose(es.grads[l].cpu().numpy(), g, rtol=0, atol=1e-5 * np.abs(g).max())
+
+
+def test_c3_fused_forward_equals_unfused(hses_gpu):
+    # The fused forward+LIF path computes the same currents and the same LIF
+    # update in-kernel, so spikes, rates and fitness are identical bit for bit.
+    cfg = snn.SnnConfig(**C3_SMALL)
+    es_u, *_ = make(cfg, fused=False)
+    es_f, *_ = make(cfg, fused=True)
+    assert es_f.fused and not es_u.fused
+    fit_u = es_u.forward(0)
+    fit_f = es_f.forward(0)
+    torch.cuda.synchronize()
+    for l in range(1, es_u.L - 1):
+        assert torch.equal(es_u.spk[l], es_f.spk[l]), f"layer {l} spikes"
+    assert torch.equal(es_u.rate, es_f.rate)
+    assert torch.equal(fit_u, fit_f)
+    assert float(es_f.rate.mean()) > 0.005
