@@ -38,7 +38,14 @@ constexpr int kBuckets = 256;         // danger-threshold buckets: k >> 16
 constexpr uint32_t kUnitCount = 1u << 24;
 constexpr uint32_t kBitmapWords = kUnitCount / 32;
 
-// Small per-function tables (copied into LDS by kernels).  All doubles.
+// Danger window of one bucket: rem29(y) in [2^28 - t, 2^28 + t) for a
+// half-width t (units of 2^-29 f32 ulp), stored as lo = 2^28 - t and w = 2t so
+// the test is one subtraction and one unsigned compare.
+struct DangerWin {
+    uint32_t lo, w;
+};
+
+// Small per-function tables (copied into LDS by kernels).
 struct BmTables {
     double log_invc[kLogTab];
     double log_logc[kLogTab];
@@ -46,8 +53,8 @@ struct BmTables {
     double cos_s[kCosTab + 1];
     double cos_thi[kCosTab + 1];
     double cos_tlo[kCosTab + 1];
-    uint32_t log_t[kBuckets];  // danger window half-widths in units of 2^-29 f32 ulp
-    uint32_t cos_t[kBuckets];
+    DangerWin log_dw[kBuckets];
+    DangerWin cos_dw[kBuckets];
     float log_k0;              // glibc logf(1e-9f): the k1 == 0 case (u1 clamped)
     float pad_[3];
 };
@@ -79,6 +86,19 @@ HSES_HD double hfma(double a, double b, double c) {
 #endif
 }
 
+// fma with a compile-time constant addend.  On the device the constant sits in
+// a scalar register pair as the third operand of v_fma_f64 (the two-address
+// v_fmac form would copy it into the destination first).
+HSES_HD double hfma_k(double a, double b, double c) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    double d;
+    asm("v_fma_f64 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "s"(c));
+    return d;
+#else
+    return fma(a, b, c);
+#endif
+}
+
 HSES_HD double hrint(double x) {
 #if defined(__HIP_DEVICE_COMPILE__)
     return __builtin_rint(x);
@@ -93,11 +113,20 @@ constexpr double kLn2Lo = 1.90821492927058770002e-10;  // 0x3DEA39EF35793C76
 constexpr double kTwoPiInv64 = 10.185916357881301;     // 64 / (2 pi), rounded; only picks the grid point
 constexpr float kTauF = 6.28318530717958647692f;       // std::f32::consts::TAU
 
-// Polynomial coefficients (Taylor, rounded to double).
-constexpr double kL2 = -0.5, kL3 = 1.0 / 3.0, kL4 = -0.25, kL5 = 0.2, kL6 = -1.0 / 6.0,
-                 kL7 = 1.0 / 7.0, kL8 = -0.125;
-constexpr double kC2 = -0.5, kC4 = 1.0 / 24.0, kC6 = -1.0 / 720.0, kC8 = 1.0 / 40320.0;
-constexpr double kS3 = -1.0 / 6.0, kS5 = 1.0 / 120.0, kS7 = -1.0 / 5040.0, kS9 = 1.0 / 362880.0;
+// Polynomial coefficients (Taylor, rounded to double).  The degrees only set
+// how often the f64 value lands near an f32 rounding midpoint: every input
+// where glibc differs from RN32 of these routines is an exception in the
+// bitmaps (checked over all 2^24 inputs when the tables are built), so
+// correctness does not depend on them.  Truncation errors: log1p to r^3,
+// |r| <= 2^-8: < 2^-34 absolute, about 2^-10 f32 ulp where |log x| >= 2^-8
+// (relative on the two c = 1 subintervals); cos to t^4 and sin to t^5,
+// |t| <= pi/64: < 2^-35 absolute against |cos| >= 2^-4.4 off the quadrant
+// points, where c_j = 0 and only the (relative) sin series counts.  Both stay
+// far inside glibc's own error (danger windows of ~0.3 ulp), so the
+// exception bitmaps and danger rates barely change with the degree.
+constexpr double kL2 = -0.5, kL3 = 1.0 / 3.0;
+constexpr double kC2 = -0.5, kC4 = 1.0 / 24.0;
+constexpr double kS3 = -1.0 / 6.0, kS5 = 1.0 / 120.0;
 
 // The f32 argument of logf for unit index k1 (k1 == 0 is clamped to 1e-9f).
 HSES_HD float log_arg(uint32_t k1) { return k1 == 0 ? 1e-9f : (float)(int32_t)k1 * 0x1p-24f; }
@@ -115,12 +144,7 @@ HSES_HD double log_f64(float x, const double* invc_tab, const double* logc_tab) 
     const uint32_t iz = ix - ((uint32_t)E << 23);
     const double z = (double)u2f(iz);
     const double r = hfma(z, invc_tab[idx], -1.0);
-    double p = hfma(r, kL8, kL7);
-    p = hfma(r, p, kL6);
-    p = hfma(r, p, kL5);
-    p = hfma(r, p, kL4);
-    p = hfma(r, p, kL3);
-    p = hfma(r, p, kL2);
+    const double p = hfma_k(r, kL3, kL2);
     const double r2 = r * r;
     const double lp = hfma(r2, p, r);
     const double Ed = (double)E;
@@ -137,13 +161,9 @@ HSES_HD double cos_f64(float th, const double* c_tab, const double* s_tab, const
     const int j = (int)hrint(x * kTwoPiInv64);
     const double t = (x - thi_tab[j]) - tlo_tab[j];
     const double t2 = t * t;
-    double pc = hfma(t2, kC8, kC6);
-    pc = hfma(t2, pc, kC4);
-    pc = hfma(t2, pc, kC2);
+    const double pc = hfma_k(t2, kC4, kC2);
     const double ct = hfma(t2, pc, 1.0);
-    double ps = hfma(t2, kS9, kS7);
-    ps = hfma(t2, ps, kS5);
-    ps = hfma(t2, ps, kS3);
+    const double ps = hfma_k(t2, kS5, kS3);
     const double st = hfma(t * t2, ps, t);
     const double sj = s_tab[j] * st;
     return hfma(c_tab[j], ct, -sj);
@@ -165,17 +185,18 @@ HSES_HD uint64_t d2u(double d) {
 // rounding midpoint in units of 2^-29 f32 ulp.
 HSES_HD uint32_t rem29(double y) { return (uint32_t)d2u(y) & 0x1FFFFFFFu; }
 
-// Inside the window of half-width t around the midpoint (one unsigned compare).
-HSES_HD bool in_danger(double y, uint32_t t) {
-    return rem29(y) - (0x10000000u - t) < 2u * t;
-}
+// Inside the bucket's window around the midpoint (one unsigned compare).
+HSES_HD bool in_danger_r(uint32_t R, DangerWin d) { return R - d.lo < d.w; }
+HSES_HD bool in_danger(double y, DangerWin d) { return in_danger_r(rem29(y), d); }
 
 // The other f32 candidate for y: the neighbour of f = RN32(y) across the
 // nearest rounding midpoint (the only other value glibc's logf/cosf return).
-HSES_HD float other_candidate(float f, double y) {
-    const double fd = (double)f;
-    const bool f_larger = (fd < 0.0 ? -fd : fd) > (y < 0.0 ? -y : y);
-    return u2f(f_larger ? f2u(f) - 1u : f2u(f) + 1u);
+// R = rem29(y) > 2^28 means y was rounded up in magnitude (|f| > |y|), so the
+// other candidate is one step toward zero; otherwise one step away.  (An
+// exact tie, R = 2^28, would be misjudged when it rounds down; the table
+// builder checks this rule against glibc for every exception.)
+HSES_HD float other_candidate(float f, uint32_t R) {
+    return u2f(R > 0x10000000u ? f2u(f) - 1u : f2u(f) + 1u);
 }
 
 // ---------------------------------------------------------------------------

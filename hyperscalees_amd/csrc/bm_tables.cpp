@@ -92,7 +92,7 @@ void scan_slice(const BmTables* t, int kind, uint32_t k_lo, uint32_t k_hi, std::
         }
         const float f = (float)y;
         if (f2u(ref) == f2u(f)) continue;
-        const float g = other_candidate(f, y);
+        const float g = other_candidate(f, rem29(y));
         if (f2u(ref) != f2u(g)) {
             char buf[160];
             snprintf(buf, sizeof buf,
@@ -142,10 +142,11 @@ std::string build_bm_tables(HostBmTables* out, int nthreads) {
                 by_bucket[x.k >> 16].push_back(x);
                 ++n;
             }
-        uint32_t* tw = kind == 0 ? out->small.log_t : out->small.cos_t;
+        DangerWin* tw = kind == 0 ? out->small.log_dw : out->small.cos_dw;
         for (int b = 0; b < kBuckets; ++b) {
-            tw[b] = bucket_t(by_bucket[b]);
-            if (tw[b] > 0x10000000u) return "danger window wider than half an ulp";
+            const uint32_t t = bucket_t(by_bucket[b]);
+            if (t > 0x10000000u) return "danger window wider than half an ulp";
+            tw[b] = DangerWin{0x10000000u - t, 2u * t};
             // every exception must test as dangerous with the bucket's window
             for (const Exc& x : by_bucket[b]) {
                 const double y = kind == 0

@@ -162,12 +162,17 @@ __device__ __forceinline__ void static_for(F&& f) {
     }
 }
 
-// Lane L of (lo, hi) <- the wave-uniform 64-bit value w (v_writelane with an
-// inline-constant lane: one scalar operand, no lane masks).
+// v_writelane_b32 through the compiler intrinsic, so the hazard recognizer
+// inserts the wait states between the SGPR write (the ballot's compare) and
+// its read by the lane write.
+extern "C" __device__ int32_t hses_writelane_i32(int32_t src, int32_t lane, int32_t old)
+    __asm("llvm.amdgcn.writelane.i32");
+
+// Lane L of (lo, hi) <- the wave-uniform 64-bit value w (no lane masks).
 template <int L>
 __device__ __forceinline__ void put_lane(uint32_t& lo, uint32_t& hi, uint64_t w) {
-    asm volatile("v_writelane_b32 %0, %1, %2" : "+v"(lo) : "s"((uint32_t)w), "n"(L));
-    asm volatile("v_writelane_b32 %0, %1, %2" : "+v"(hi) : "s"((uint32_t)(w >> 32)), "n"(L));
+    lo = (uint32_t)hses_writelane_i32((int32_t)(uint32_t)w, L, (int32_t)lo);
+    hi = (uint32_t)hses_writelane_i32((int32_t)(uint32_t)(w >> 32), L, (int32_t)hi);
 }
 
 // Fused LIF on a wave's 64 rows x 64 output columns of currents (acc[i][j]:

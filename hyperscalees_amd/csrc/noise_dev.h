@@ -46,8 +46,8 @@ __device__ __forceinline__ float sqrt_rn(float s) {
 __device__ __forceinline__ float bm_logf(uint32_t k1, const BmTables& t, const uint32_t* exc) {
     const double y = log_f64(log_arg(k1), t.log_invc, t.log_logc);
     float f = (float)y;
-    if (in_danger(y, t.log_t[k1 >> 16]) && ((exc[k1 >> 5] >> (k1 & 31)) & 1u))
-        f = other_candidate(f, y);
+    if (in_danger(y, t.log_dw[k1 >> 16]) && ((exc[k1 >> 5] >> (k1 & 31)) & 1u))
+        f = other_candidate(f, rem29(y));
     return k1 == 0 ? t.log_k0 : f;
 }
 
@@ -55,14 +55,23 @@ __device__ __forceinline__ float bm_logf(uint32_t k1, const BmTables& t, const u
 __device__ __forceinline__ float bm_cosf(uint32_t k2, const BmTables& t, const uint32_t* exc) {
     const double y = cos_f64(cos_arg(k2), t.cos_c, t.cos_s, t.cos_thi, t.cos_tlo);
     float f = (float)y;
-    if (in_danger(y, t.cos_t[k2 >> 16]) && ((exc[k2 >> 5] >> (k2 & 31)) & 1u))
-        f = other_candidate(f, y);
+    if (in_danger(y, t.cos_dw[k2 >> 16]) && ((exc[k2 >> 5] >> (k2 & 31)) & 1u))
+        f = other_candidate(f, rem29(y));
     return f;
 }
 
 // sqrtf(-2 * logf(u1)): the radius of noiser.rs:474.
 __device__ __forceinline__ float bm_radius(uint32_t k1, const BmTables& t, const uint32_t* exc) {
     return sqrt_rn(-2.0f * bm_logf(k1, t, exc));
+}
+
+// The 24-bit unit index (x >> 40) of a state, as a 32-bit value.  Written as
+// an opaque shift of the high word: otherwise the compiler folds the
+// truncation away and converts a 64-bit integer to float (a long sequence).
+__device__ __forceinline__ uint32_t unit_index(uint64_t x) {
+    uint32_t k;
+    asm("v_lshrrev_b32 %0, 8, %1" : "=v"(k) : "v"((uint32_t)(x >> 32)));
+    return k;
 }
 
 // G consecutive DeterministicNoise::standard_normal draws (noiser.rs:470-477).
@@ -73,21 +82,23 @@ __device__ __forceinline__ void bm_normals(uint64_t& s, float* out, const NoiseC
 #pragma unroll
     for (int i = 0; i < G; ++i) {
         s = xs64(s);
-        k1[i] = (uint32_t)(s >> 40);
+        k1[i] = unit_index(s);
         s = xs64(s);
-        k2[i] = (uint32_t)(s >> 40);
+        k2[i] = unit_index(s);
     }
-    double yl[G], yc[G];
+    uint32_t rl[G], rc[G];
     float fl[G], fc[G];
     bool dl[G], dc[G];
 #pragma unroll
     for (int i = 0; i < G; ++i) {
-        yl[i] = log_f64(log_arg(k1[i]), t.log_invc, t.log_logc);
-        yc[i] = cos_f64(cos_arg(k2[i]), t.cos_c, t.cos_s, t.cos_thi, t.cos_tlo);
-        fl[i] = (float)yl[i];
-        fc[i] = (float)yc[i];
-        dl[i] = in_danger(yl[i], t.log_t[k1[i] >> 16]);
-        dc[i] = in_danger(yc[i], t.cos_t[k2[i] >> 16]);
+        const double yl = log_f64(log_arg(k1[i]), t.log_invc, t.log_logc);
+        const double yc = cos_f64(cos_arg(k2[i]), t.cos_c, t.cos_s, t.cos_thi, t.cos_tlo);
+        fl[i] = (float)yl;
+        fc[i] = (float)yc;
+        rl[i] = rem29(yl);
+        rc[i] = rem29(yc);
+        dl[i] = in_danger_r(rl[i], t.log_dw[k1[i] >> 16]);
+        dc[i] = in_danger_r(rc[i], t.cos_dw[k2[i] >> 16]);
     }
     uint32_t wl[G], wc[G];
 #pragma unroll
@@ -97,8 +108,8 @@ __device__ __forceinline__ void bm_normals(uint64_t& s, float* out, const NoiseC
     }
 #pragma unroll
     for (int i = 0; i < G; ++i) {
-        if ((wl[i] >> (k1[i] & 31)) & 1u) fl[i] = other_candidate(fl[i], yl[i]);
-        if ((wc[i] >> (k2[i] & 31)) & 1u) fc[i] = other_candidate(fc[i], yc[i]);
+        if ((wl[i] >> (k1[i] & 31)) & 1u) fl[i] = other_candidate(fl[i], rl[i]);
+        if ((wc[i] >> (k2[i] & 31)) & 1u) fc[i] = other_candidate(fc[i], rc[i]);
         const float L = k1[i] == 0 ? t.log_k0 : fl[i];
         out[i] = sqrt_rn(-2.0f * L) * fc[i];
     }
