@@ -229,7 +229,7 @@ HSES_HD uint64_t xs64(uint64_t x) {
 HSES_HD uint64_t gf2_apply(const uint64_t* cols, uint64_t x) {
     uint64_t y = 0;
 #if defined(__HIP_DEVICE_COMPILE__)
-#pragma unroll 16
+#pragma unroll 4
 #endif
     for (int i = 0; i < 64; ++i) y ^= (0ull - ((x >> i) & 1ull)) & cols[i];
     return y;

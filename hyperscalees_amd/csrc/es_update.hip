@@ -10,11 +10,19 @@
 // its own signed weight):  g = scale * sum_p sum_c (w_p Ahat_p[:,c]) B_p[:,c]^T,
 // i.e. an (a x b) output with K = pairs * r.
 //
-// Stage 1 (k_es_partial): grid = (b tiles, a tiles, splits).  A workgroup owns
-// a 128x128 output tile and a fixed contiguous range of pairs; for each pair it
-// regenerates the tile's rows of Ahat and B into LDS, rank-chunk by
-// rank-chunk (each thread continues its own row's stream), and accumulates
-// with fp32 MFMA.  The partial tile goes to the workspace.
+// Stage 1: a workgroup owns an output tile and a fixed contiguous range of
+// pairs; for each pair it regenerates the tile's rows of Ahat and B into LDS,
+// rank-chunk by rank-chunk (each thread continues its own row's stream), and
+// accumulates with fp32 MFMA.  The partial tile goes to the workspace.
+//   k_es_rows (r >= 32): one thread per generated row.  A tile spans up to 128
+//     rows of a and up to 384 columns of b, with blockDim = the tile's row
+//     count rounded up to a wave, so every generating thread is busy and a
+//     pair's A rows are regenerated once per b tile (C3 fc1: 3 tiles instead
+//     of 7).  Rank chunks are double-buffered in LDS (one barrier per chunk)
+//     and the generation of the next chunk is interleaved with the MFMAs of
+//     the current one.
+//   k_es_partial (r < 32): 128x128 tiles, 256 threads; several short stream
+//     rows per thread.
 // Stage 2 (k_es_reduce): each output element sums its partials in split
 // order in double, scales, and stores (or adds).  The split count depends on
 // the problem shape only, so the result is independent of the device.
@@ -44,6 +52,8 @@ struct UpdParams {
     const uint32_t* cos_exc;
     const uint64_t* jump;  // row length r
 };
+
+__host__ __device__ constexpr size_t align_up16(size_t x) { return (x + 15) & ~(size_t)15; }
 
 __host__ __device__ inline int32_t split_begin(int32_t n_pairs, int32_t splits, int32_t s) {
     return (int32_t)(((int64_t)n_pairs * s) / splits);
@@ -145,6 +155,156 @@ __global__ __launch_bounds__(U_THREADS) void k_es_partial(UpdParams P) {
         }
 }
 
+// ---- k_es_rows ---------------------------------------------------------------
+
+constexpr int R_CT = 3;          // 16-column tiles per wave (at most)
+constexpr int R_MAXT = 512;      // threads (rows) per workgroup
+
+struct RowTiles {
+    int32_t at, bt;              // tile extent
+    int32_t o_base, q_base;      // origin of blockIdx (0, 0)
+};
+
+// NRT: 16-row tiles of a (a tile of at <= 16 * NRT rows); CT: 16-column tiles
+// per wave.  Both compile-time, so the MFMA block is branch-free: absent
+// tiles of a wave compute on clamped rows and are not stored.
+template <int NRT, int CT>
+__global__ __launch_bounds__(R_MAXT) void k_es_rows(UpdParams P, RowTiles G) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    BmTables* tabs = reinterpret_cast<BmTables*>(smem);
+    const int32_t at = G.at, bt = G.bt, rows = at + bt;
+    float* buf0 = reinterpret_cast<float*>(smem + align_up16(sizeof(BmTables)));
+    // floats per buffer: As rows, Bs rows, then rows of the idle threads
+    const int32_t bufsz = (int32_t)blockDim.x * U_PITCH;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nw = blockDim.x >> 6;
+    const int32_t q0 = G.q_base + blockIdx.x * bt, o0 = G.o_base + blockIdx.y * at;
+    const int32_t s = blockIdx.z;
+    const int32_t p_begin = P.pair_lo + split_begin(P.n_pairs, P.splits, s);
+    const int32_t p_end = P.pair_lo + split_begin(P.n_pairs, P.splits, s + 1);
+    const int32_t r = P.r;
+    const int32_t chunks = (r + U_CW - 1) / U_CW;
+
+    load_bm_tables(tabs, P.tables);
+    for (int i = tid; i < 2 * bufsz; i += blockDim.x) buf0[i] = 0.0f;
+    __syncthreads();
+    const NoiseCtx ctx{tabs, P.log_exc, P.cos_exc};
+
+    // This thread's stream row: A rows [0, at) first, then B rows.  Threads
+    // past the tile's rows generate a copy of row 0 into their own LDS row
+    // (never read), which keeps the generation free of divergent branches.
+    const bool is_a = tid < at;
+    const int32_t srow = is_a ? P.b + o0 + tid : tid < rows ? q0 + (tid - at) : q0;
+    const float scl = is_a ? P.bs : 1.0f;
+    const int32_t grow = tid;  // LDS row written by this thread
+
+    // MFMA ownership: column tiles wave, wave + nw, ... (at most CT).
+    const int32_t nct = (bt + 15) >> 4;
+    const int kg = lane >> 4, li = lane & 15;
+    int32_t aoff[NRT], boff[CT];  // LDS offsets of this lane's operand rows
+#pragma unroll
+    for (int i = 0; i < NRT; ++i) aoff[i] = min(i * 16 + li, at - 1) * U_PITCH + kg;
+#pragma unroll
+    for (int j = 0; j < CT; ++j)
+        boff[j] = (at + min(min(wave + j * nw, nct - 1) * 16 + li, bt - 1)) * U_PITCH + kg;
+    f32x4 acc[NRT][CT];
+#pragma unroll
+    for (int i = 0; i < NRT; ++i)
+#pragma unroll
+        for (int j = 0; j < CT; ++j) acc[i][j] = f32x4{0, 0, 0, 0};
+    // acc += (w * Ahat[:, ks..ks+4)) B[:, ks..ks+4)^T from buffer X.
+    auto mfma_step = [&](const float* X, int32_t ks, float w) {
+        float af[NRT], bf[CT];
+#pragma unroll
+        for (int i = 0; i < NRT; ++i) af[i] = w * X[aoff[i] + ks];
+#pragma unroll
+        for (int j = 0; j < CT; ++j) bf[j] = X[boff[j] + ks];
+#pragma unroll
+        for (int i = 0; i < NRT; ++i)
+#pragma unroll
+            for (int j = 0; j < CT; ++j) acc[i][j] = mfma_f32(af[i], bf[j], acc[i][j]);
+    };
+
+    // Software pipeline over work items u = (pair, rank chunk): while a wave
+    // runs the MFMAs of item u from buffer u & 1 it generates item u + 1 into
+    // the other buffer, four normals per k-step, so the matrix cores of one
+    // wave overlap the VALU generation of the other waves on the SIMD.
+    const int32_t n_items = (p_end - p_begin) * chunks;
+    uint64_t st = 0;
+    auto start_pair = [&](int32_t p) {
+        int32_t te, tt;
+        float sg;
+        epoch_thread_sign(P.epoch, 2 * p, P.nreuse, &te, &tt, &sg);
+        st = row_start_state(noise_seed(P.key, te, tt), srow, P.jump);
+    };
+    auto pair_weight = [&](int32_t p) {
+        const int32_t me = 2 * p - P.tid_lo, mo = me + 1;
+        const float fe = (me >= 0 && me < P.n) ? P.f[me] : 0.0f;
+        const float fo = (mo >= 0 && mo < P.n) ? P.f[mo] : 0.0f;
+        return fe - fo;
+    };
+    // Generation of normals [c, c + cnt) (cnt <= 4) of the current chunk.
+    auto gen4 = [&](float* dst, int32_t c, int32_t cnt) {
+        if (cnt == 4) {
+#pragma unroll
+            for (int h = 0; h < 4; h += 2) {
+                float v[2];
+                bm_normals<2>(st, v, ctx);
+                dst[c + h] = v[0] * scl;
+                dst[c + h + 1] = v[1] * scl;
+            }
+        } else {
+            for (int32_t e = 0; e < cnt; ++e) dst[c + e] = bm_normal(st, ctx) * scl;
+            for (int32_t e = cnt; e < 4; ++e) dst[c + e] = 0.0f;  // k padding of the last step
+        }
+    };
+    if (n_items > 0) {
+        start_pair(p_begin);
+        float* dst = buf0 + grow * U_PITCH;
+        const int32_t cn = min(U_CW, r);
+        for (int32_t c = 0; c < cn; c += 4) gen4(dst, c, min(4, cn - c));
+    }
+    __syncthreads();
+    for (int32_t u = 0; u < n_items; ++u) {
+        const int32_t p = p_begin + u / chunks, ch = u % chunks;
+        const float w = pair_weight(p);
+        const int32_t cn = min(U_CW, r - ch * U_CW);
+        const bool has_next = u + 1 < n_items;
+        const int32_t nch = (ch + 1 == chunks) ? 0 : ch + 1;
+        const int32_t ncn = min(U_CW, r - nch * U_CW);
+        if (has_next && nch == 0) start_pair(p + 1);
+        const float* X = buf0 + (u & 1) * bufsz;
+        float* nxt = buf0 + ((u + 1) & 1) * bufsz + grow * U_PITCH;
+        // k-step ks, then four normals of the next chunk: the matrix cores of
+        // one wave overlap the generation of the other waves on the SIMD
+#pragma unroll 1
+        for (int32_t ks = 0; ks < U_CW; ks += 4) {
+            if (ks < cn) mfma_step(X, ks, w);
+            if (has_next && ks < ncn) gen4(nxt, ks, min(4, ncn - ks));
+        }
+        __syncthreads();
+    }
+
+    // Partial tile -> workspace [s][a][b].
+    float* out = P.work + (size_t)s * P.a * P.b;
+#pragma unroll
+    for (int j = 0; j < CT; ++j) {
+        const int32_t ct = wave + j * nw;
+        if (ct >= nct) continue;
+        const int32_t col = ct * 16 + li;
+        if (col >= bt) continue;
+#pragma unroll
+        for (int i = 0; i < NRT; ++i) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int32_t row = i * 16 + 4 * kg + v;
+                if (row < at) out[(size_t)(o0 + row) * P.b + q0 + col] = acc[i][j][v];
+            }
+        }
+    }
+}
+
 __global__ void k_es_reduce(const float* __restrict__ work, int32_t splits, int64_t len, float scale,
                             int32_t accumulate, float* __restrict__ g) {
     const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -164,6 +324,44 @@ static int32_t es_splits(int32_t a, int32_t b, int32_t n_pairs) {
     return (int32_t)std::max<int64_t>(s, 1);
 }
 
+// k_es_rows tiling of an (a, b) output: a-tiles of up to 128 rows; b-tiles as
+// wide as fits 512 rows per workgroup with at most R_CT column tiles per wave.
+static int32_t rows_bt_max(int32_t at) {
+    int32_t bt = std::min(384, R_MAXT - at) / 16 * 16;
+    while (bt > 16) {
+        const int32_t nct = (bt + 15) / 16, nw = (at + bt + 63) / 64;
+        if ((nct + nw - 1) / nw <= R_CT) break;
+        bt -= 16;
+    }
+    return bt;
+}
+
+static int32_t rows_tiles(int32_t a, int32_t b) {
+    int32_t t = 0;
+    for (int32_t o0 = 0; o0 < a; o0 += 128) {
+        const int32_t at = std::min(128, a - o0), btm = rows_bt_max(at);
+        t += (b + btm - 1) / btm;
+    }
+    return t;
+}
+
+// Split count of k_es_rows: about 512 workgroups over the tiles of at least
+// 256 threads, at least 8 pairs per split.  Shape-only, so results do not
+// depend on the device.
+static int32_t rows_splits(int32_t a, int32_t b, int32_t n_pairs) {
+    int32_t big = 0;
+    for (int32_t o0 = 0; o0 < a; o0 += 128) {
+        const int32_t at = std::min(128, a - o0), btm = rows_bt_max(at);
+        big += b / btm;
+        if (b % btm && at + b % btm > 256) ++big;
+    }
+    int64_t s = 512 / std::max(1, big);
+    s = std::min<int64_t>(s, std::max<int32_t>(1, n_pairs / 8));
+    return (int32_t)std::max<int64_t>(1, std::min<int64_t>(s, 512));
+}
+
+static bool use_rows_kernel(int32_t rank) { return rank >= U_CW; }
+
 static void pair_range(int32_t tid_lo, int32_t n, int32_t* lo, int32_t* cnt) {
     *lo = tid_lo / 2;
     *cnt = (tid_lo + n - 1) / 2 - *lo + 1;
@@ -178,7 +376,8 @@ extern "C" size_t hses_es_update_workspace(int32_t a, int32_t b, int32_t rank, i
     int32_t lo, cnt;
     pair_range(0, n, &lo, &cnt);
     // tid_lo parity can add one pair; size for the larger count.
-    return (size_t)es_splits(a, b, cnt + 1) * a * b * sizeof(float);
+    const int32_t splits = use_rows_kernel(rank) ? rows_splits(a, b, cnt + 1) : es_splits(a, b, cnt + 1);
+    return (size_t)splits * a * b * sizeof(float);
 }
 
 extern "C" int hses_es_update(const float* d_f, int32_t n, int32_t tid_lo, uint64_t key,
@@ -193,7 +392,8 @@ extern "C" int hses_es_update(const float* d_f, int32_t n, int32_t tid_lo, uint6
     int32_t pair_lo, n_pairs;
     pair_range(tid_lo, n, &pair_lo, &n_pairs);
     const bool empty = n == 0 || rank == 0 || sigma == 0.0f;
-    P.splits = empty ? 1 : es_splits(a, b, n_pairs);
+    const bool rows_k = use_rows_kernel(rank);
+    P.splits = empty ? 1 : rows_k ? rows_splits(a, b, n_pairs) : es_splits(a, b, n_pairs);
     const size_t need = (size_t)P.splits * a * b * sizeof(float);
     if (!empty) {
         HSES_REQUIRE(d_f, "fitness is NULL");
@@ -230,9 +430,42 @@ extern "C" int hses_es_update(const float* d_f, int32_t n, int32_t tid_lo, uint6
     P.cos_exc = st->d_cos_exc;
     rc = get_jump_table(st, rank, (int64_t)a + b, &P.jump);
     if (rc) return rc;
-    dim3 grid((b + U_TB - 1) / U_TB, (a + U_TA - 1) / U_TA, P.splits);
-    hipLaunchKernelGGL(k_es_partial, grid, dim3(U_THREADS), 0, s, P);
-    HSES_CHECK_HIP(hipGetLastError());
+    if (rows_k) {
+        // One launch per (a-tile, full / remainder b-tile) group.
+        for (int32_t o0 = 0; o0 < a; o0 += 128) {
+            const int32_t at = std::min(128, a - o0), btm = rows_bt_max(at);
+            const int32_t nfull = b / btm, rem = b % btm;
+            for (int g = 0; g < 2; ++g) {
+                const int32_t bt = g == 0 ? btm : rem, cnt = g == 0 ? nfull : (rem ? 1 : 0);
+                if (cnt == 0) continue;
+                RowTiles G{at, bt, o0, g == 0 ? 0 : nfull * btm};
+                const int32_t threads = (at + bt + 63) / 64 * 64;
+                const size_t lds = align_up16(sizeof(BmTables)) + (size_t)2 * threads * U_PITCH * 4;
+                const int32_t nw = threads / 64, nct = (bt + 15) / 16;
+                const int32_t ct = (nct + nw - 1) / nw;
+                auto launch = [&](auto kern) -> int {
+                    if (lds > 64 * 1024)
+                        HSES_CHECK_HIP(hipFuncSetAttribute(
+                            (const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+                    hipLaunchKernelGGL(kern, dim3(cnt, 1, P.splits), dim3(threads), lds, s, P, G);
+                    HSES_CHECK_HIP(hipGetLastError());
+                    return HSES_OK;
+                };
+                int lrc;
+                if (at <= 16)
+                    lrc = ct == 1 ? launch(k_es_rows<1, 1>) : ct == 2 ? launch(k_es_rows<1, 2>)
+                                                                : launch(k_es_rows<1, 3>);
+                else
+                    lrc = ct == 1 ? launch(k_es_rows<8, 1>) : ct == 2 ? launch(k_es_rows<8, 2>)
+                                                                : launch(k_es_rows<8, 3>);
+                if (lrc) return lrc;
+            }
+        }
+    } else {
+        dim3 grid((b + U_TB - 1) / U_TB, (a + U_TA - 1) / U_TA, P.splits);
+        hipLaunchKernelGGL(k_es_partial, grid, dim3(U_THREADS), 0, s, P);
+        HSES_CHECK_HIP(hipGetLastError());
+    }
     const int64_t len = (int64_t)a * b;
     hipLaunchKernelGGL(k_es_reduce, dim3((uint32_t)((len + 255) / 256)), dim3(256), 0, s, P.work,
                        P.splits, len, scale, accumulate, d_grad);
