@@ -9,21 +9,19 @@
 
 namespace hses {
 
-// Largest m in [0, 2^23] such that m == 0 or RN32(m / 8388609) < p.  The
-// reference compares u = ((v >> 9) + 1) / 8388609 (f32 division) with p
-// (poisson_encode_fused_oxide.rs:44-52); since RN32(m / D) is non-decreasing
-// in m, `u < p` is exactly `(v >> 9) + 1 <= K(p)`.  floor(p*D) is exact in
-// f64 and the rounding of m/D moves the crossing by less than one step, so
-// only three candidates need the (correctly rounded) f32 division.
+// K(p) = the number of m in [1, 2^23] with RN32(m / D) < p, D = 8388609.
+// The reference compares u = ((v >> 9) + 1) / D (f32 division) with p
+// (poisson_encode_fused_oxide.rs:44-52); RN32(m / D) is non-decreasing in m,
+// so `u < p` is exactly `(v >> 9) < K(p)`.  RN32(q) < p iff q lies below the
+// midpoint between p and its predecessor (q = m / D is never exactly that
+// dyadic midpoint: D is odd), so K = floor(mid * D), clamped to 2^23.  mid
+// (25 significant bits) and mid * D (49 bits) are exact in f64.
 __device__ __forceinline__ uint32_t poisson_threshold(float p) {
     if (!(p > 0.0f)) return 0u;  // p <= 0 or NaN: never fires
-    const double pd = (double)p * 8388609.0;
-    const double fl = __builtin_floor(pd);
-    const uint32_t m0 = fl >= 8388608.0 ? 8388608u : (uint32_t)fl;
-    auto lt = [p](uint32_t m) { return (float)m / 8388609.0f < p; };
-    if (m0 < 8388608u && lt(m0 + 1u)) return m0 + 1u;
-    if (m0 >= 1u && lt(m0)) return m0;
-    return m0 >= 1u ? m0 - 1u : 0u;
+    const float pp = __uint_as_float(__float_as_uint(p) - 1u);  // predecessor (Inf -> FLT_MAX)
+    const double mid = ((double)pp + (double)p) * 0.5;
+    const double t = mid * 8388609.0;
+    return t >= 8388608.0 ? 8388608u : (uint32_t)t;  // t > 0 and never an integer
 }
 
 template <int FMT>
@@ -52,8 +50,57 @@ __global__ __launch_bounds__(256) void k_poisson(const float* __restrict__ p, in
         x ^= x << 13;
         x ^= x >> 17;
         x ^= x << 5;
-        const bool spike = valid && ((x >> 9) + 1u) <= K;
+        const bool spike = valid && (x >> 9) < K;
         store_spike<FMT>(out, t * plane + row * out_stride, word, col, valid, spike);
+    }
+}
+
+// Bit-packed Poisson (the SNN input path): one wave per row, looping over the
+// row's 64-column words.  For each word the T ballot words are gathered into
+// lanes 0..T-1 (v_writelane) and written by one store instruction.
+extern "C" __device__ int32_t hses_poisson_writelane(int32_t src, int32_t lane, int32_t old)
+    __asm("llvm.amdgcn.writelane.i32");
+
+constexpr int P_ROWS_PER_BLOCK = 4;
+
+// TT: T as a compile-time constant (fully unrolled time loop), or 0 (runtime T).
+template <int TT>
+__global__ __launch_bounds__(64 * P_ROWS_PER_BLOCK) void k_poisson_bits(
+    const float* __restrict__ p, int64_t p_rows, const int32_t* __restrict__ prow, int64_t rows,
+    int32_t in_dim, int64_t p_stride, int32_t T_rt, uint32_t mix, uint64_t* __restrict__ out,
+    int64_t out_stride) {
+    const int32_t T = TT ? TT : T_rt;
+    const int64_t row = (int64_t)blockIdx.x * P_ROWS_PER_BLOCK + (threadIdx.x >> 6);
+    const int32_t lane = threadIdx.x & 63;
+    if (row >= rows) return;  // whole wave exits together
+    const int32_t words = (in_dim + 63) >> 6;
+    const int64_t src = prow ? (int64_t)prow[row] : row;
+    const bool src_ok = src >= 0 && src < p_rows;
+    const float* prow_p = p + (src_ok ? src : 0) * p_stride;
+    const uint32_t idx0 = (uint32_t)(row * in_dim);  // flat index of the row's first element
+    const int64_t plane = rows * out_stride;
+    uint64_t* orow = out + row * out_stride + (int64_t)lane * plane;
+    // probabilities of the next word are loaded while the current one is encoded
+    float pn = (src_ok && lane < in_dim) ? prow_p[lane] : 0.0f;
+    for (int32_t word = 0; word < words; ++word) {
+        const int32_t col = word * 64 + lane;
+        const float pc = pn;
+        const int32_t ncol = col + 64;
+        pn = (src_ok && ncol < in_dim) ? prow_p[ncol] : 0.0f;
+        const uint32_t K = col < in_dim ? poisson_threshold(pc) : 0u;
+        uint32_t x = 1000000007u * (idx0 + (uint32_t)col) + mix + 0x9E3779B9u;
+        uint32_t wlo = 0, whi = 0;  // lane t: the word of time step t
+#pragma unroll
+        for (int32_t t = 0; t < (TT ? TT : 64); ++t) {
+            if (!TT && t >= T) break;
+            x ^= x << 13;
+            x ^= x >> 17;
+            x ^= x << 5;
+            const uint64_t bits = __ballot((x >> 9) < K);  // K = 0 on invalid lanes
+            wlo = (uint32_t)hses_poisson_writelane((int32_t)(uint32_t)bits, t, (int32_t)wlo);
+            whi = (uint32_t)hses_poisson_writelane((int32_t)(uint32_t)(bits >> 32), t, (int32_t)whi);
+        }
+        if (lane < T) orow[word] = ((uint64_t)whi << 32) | wlo;
     }
 }
 
@@ -178,8 +225,23 @@ extern "C" int hses_poisson_encode(const float* d_p, int64_t p_rows, const int32
                                rows, in_dim, p_stride, T, mix, d_out, out_stride);
             break;
         default:
-            hipLaunchKernelGGL(k_poisson<HSES_FMT_BITS>, dim3(blocks), dim3(256), 0, s, d_p, p_rows, d_rows,
-                               rows, in_dim, p_stride, T, mix, d_out, out_stride);
+            if (T <= 64) {
+                const dim3 g((uint32_t)((rows + P_ROWS_PER_BLOCK - 1) / P_ROWS_PER_BLOCK));
+                const dim3 b(64 * P_ROWS_PER_BLOCK);
+                uint64_t* o = static_cast<uint64_t*>(d_out);
+                if (T == 16)
+                    hipLaunchKernelGGL(k_poisson_bits<16>, g, b, 0, s, d_p, p_rows, d_rows, rows,
+                                       in_dim, p_stride, T, mix, o, out_stride);
+                else if (T == 8)
+                    hipLaunchKernelGGL(k_poisson_bits<8>, g, b, 0, s, d_p, p_rows, d_rows, rows,
+                                       in_dim, p_stride, T, mix, o, out_stride);
+                else
+                    hipLaunchKernelGGL(k_poisson_bits<0>, g, b, 0, s, d_p, p_rows, d_rows, rows,
+                                       in_dim, p_stride, T, mix, o, out_stride);
+            }
+            else
+                hipLaunchKernelGGL(k_poisson<HSES_FMT_BITS>, dim3(blocks), dim3(256), 0, s, d_p, p_rows,
+                                   d_rows, rows, in_dim, p_stride, T, mix, d_out, out_stride);
             break;
     }
     HSES_CHECK_HIP(hipGetLastError());
