@@ -9,7 +9,7 @@
 
 namespace hses {
 
-__global__ void k_bm_eval(uint32_t k_lo, uint32_t n, float* lg, float* rad, float* cs,
+__global__ __launch_bounds__(256) void k_bm_eval(uint32_t k_lo, uint32_t n, float* lg, float* rad, float* cs,
                           const BmTables* gt, const uint32_t* le, const uint32_t* ce) {
     __shared__ BmTables t;
     load_bm_tables(&t, gt);
@@ -29,7 +29,7 @@ __global__ void k_bm_eval(uint32_t k_lo, uint32_t n, float* lg, float* rad, floa
 // [b, a+b) are A rows scaled by sign*base_sigma (eggroll.rs:86-103).  With
 // b == 0 and A == nullptr it writes a dense (a, L) noise block instead
 // (get_nonlora_update_params: all rows scaled).
-__global__ void k_stream_rows(float bs, uint64_t key, int32_t L, int32_t epoch, int32_t nreuse,
+__global__ __launch_bounds__(256) void k_stream_rows(float bs, uint64_t key, int32_t L, int32_t epoch, int32_t nreuse,
                               int32_t tid_lo, const int32_t* tids, int32_t n, int32_t a, int32_t b,
                               int32_t blocks_per_member, float* A, float* B,
                               const BmTables* gt, const uint32_t* le, const uint32_t* ce,

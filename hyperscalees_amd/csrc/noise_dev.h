@@ -74,45 +74,80 @@ __device__ __forceinline__ uint32_t unit_index(uint64_t x) {
     return k;
 }
 
-// G consecutive DeterministicNoise::standard_normal draws (noiser.rs:470-477).
+// A batch of G normals in flight.  Stage 1 steps the stream, evaluates log
+// and cos in f64, rounds to f32 and issues the exception-bitmap loads of the
+// values near a rounding midpoint; stage 2 applies the corrections and forms
+// sqrt(-2 log u1) * cos(...).  Running stage 1 of the next batch between the
+// two stages of a batch hides the bitmap loads' latency.
 template <int G>
-__device__ __forceinline__ void bm_normals(uint64_t& s, float* out, const NoiseCtx& c) {
-    const BmTables& t = *c.t;
+struct BmPending {
+    float fl[G], fc[G];
+    uint32_t rl[G], rc[G];  // remainders: direction of the correction
     uint32_t k1[G], k2[G];
+    uint32_t wl[G], wc[G];  // exception words (0 when not in danger)
+};
+
+// PIPE: loads issued by every lane (for a pipelined caller, see below);
+// otherwise only lanes in danger load (a branch skips the load when none is).
+template <int G, bool PIPE>
+__device__ __forceinline__ void bm_stage1(uint64_t& s, BmPending<G>& p, const NoiseCtx& c) {
+    const BmTables& t = *c.t;
 #pragma unroll
     for (int i = 0; i < G; ++i) {
         s = xs64(s);
-        k1[i] = unit_index(s);
+        p.k1[i] = unit_index(s);
         s = xs64(s);
-        k2[i] = unit_index(s);
+        p.k2[i] = unit_index(s);
     }
-    uint32_t rl[G], rc[G];
-    float fl[G], fc[G];
     bool dl[G], dc[G];
 #pragma unroll
     for (int i = 0; i < G; ++i) {
-        const double yl = log_f64(log_arg(k1[i]), t.log_invc, t.log_logc);
-        const double yc = cos_f64(cos_arg(k2[i]), t.cos_c, t.cos_s, t.cos_thi, t.cos_tlo);
-        fl[i] = (float)yl;
-        fc[i] = (float)yc;
-        rl[i] = rem29(yl);
-        rc[i] = rem29(yc);
-        dl[i] = in_danger_r(rl[i], t.log_dw[k1[i] >> 16]);
-        dc[i] = in_danger_r(rc[i], t.cos_dw[k2[i] >> 16]);
+        const double yl = log_f64(log_arg(p.k1[i]), t.log_invc, t.log_logc);
+        const double yc = cos_f64(cos_arg(p.k2[i]), t.cos_c, t.cos_s, t.cos_thi, t.cos_tlo);
+        p.fl[i] = (float)yl;
+        p.fc[i] = (float)yc;
+        p.rl[i] = rem29(yl);
+        p.rc[i] = rem29(yc);
+        dl[i] = in_danger_r(p.rl[i], t.log_dw[p.k1[i] >> 16]);
+        dc[i] = in_danger_r(p.rc[i], t.cos_dw[p.k2[i] >> 16]);
     }
-    uint32_t wl[G], wc[G];
+    if constexpr (PIPE) {
+        // Every lane loads (lanes out of danger read word 0, one shared cache
+        // line): no branch, so the wait before stage 2 counts exactly the
+        // loads still in flight from the batch issued after this one.
+#pragma unroll
+        for (int i = 0; i < G; ++i) {
+            p.wl[i] = c.log_exc[dl[i] ? p.k1[i] >> 5 : 0u] & (dl[i] ? ~0u : 0u);
+            p.wc[i] = c.cos_exc[dc[i] ? p.k2[i] >> 5 : 0u] & (dc[i] ? ~0u : 0u);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < G; ++i) {
+            p.wl[i] = dl[i] ? c.log_exc[p.k1[i] >> 5] : 0u;
+            p.wc[i] = dc[i] ? c.cos_exc[p.k2[i] >> 5] : 0u;
+        }
+    }
+}
+
+template <int G>
+__device__ __forceinline__ void bm_stage2(const BmPending<G>& p, float* out, const NoiseCtx& c) {
+    const BmTables& t = *c.t;
 #pragma unroll
     for (int i = 0; i < G; ++i) {
-        wl[i] = dl[i] ? c.log_exc[k1[i] >> 5] : 0u;
-        wc[i] = dc[i] ? c.cos_exc[k2[i] >> 5] : 0u;
+        float fl = p.fl[i], fc = p.fc[i];
+        if ((p.wl[i] >> (p.k1[i] & 31)) & 1u) fl = other_candidate(fl, p.rl[i]);
+        if ((p.wc[i] >> (p.k2[i] & 31)) & 1u) fc = other_candidate(fc, p.rc[i]);
+        const float L = p.k1[i] == 0 ? t.log_k0 : fl;
+        out[i] = sqrt_rn(-2.0f * L) * fc;
     }
-#pragma unroll
-    for (int i = 0; i < G; ++i) {
-        if ((wl[i] >> (k1[i] & 31)) & 1u) fl[i] = other_candidate(fl[i], rl[i]);
-        if ((wc[i] >> (k2[i] & 31)) & 1u) fc[i] = other_candidate(fc[i], rc[i]);
-        const float L = k1[i] == 0 ? t.log_k0 : fl[i];
-        out[i] = sqrt_rn(-2.0f * L) * fc[i];
-    }
+}
+
+// G consecutive DeterministicNoise::standard_normal draws (noiser.rs:470-477).
+template <int G>
+__device__ __forceinline__ void bm_normals(uint64_t& s, float* out, const NoiseCtx& c) {
+    BmPending<G> p;
+    bm_stage1<G, false>(s, p, c);
+    bm_stage2<G>(p, out, c);
 }
 
 // One normal (used where a single draw is needed).
@@ -123,15 +158,29 @@ __device__ __forceinline__ float bm_normal(uint64_t& s, const NoiseCtx& c) {
 }
 
 // `count` consecutive normals of one stream; sink(i, value) receives normal i.
-// Batches of 4 (a tail of 1-3 handled singly).
+// Batches of 4, software-pipelined (stage 1 of batch b+1 before stage 2 of
+// batch b); a tail of 1-3 is drawn singly.
 template <typename Sink>
 __device__ __forceinline__ void bm_run(uint64_t& s, int32_t count, const NoiseCtx& c, Sink sink) {
+    constexpr int G = 4;
     int32_t i = 0;
-    for (; i + 4 <= count; i += 4) {
-        float v[4];
-        bm_normals<4>(s, v, c);
+    if (count >= G) {
+        BmPending<G> p;
+        bm_stage1<G, true>(s, p, c);
+        for (; i + 2 * G <= count; i += G) {
+            BmPending<G> q;
+            bm_stage1<G, true>(s, q, c);
+            float v[G];
+            bm_stage2<G>(p, v, c);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) sink(i + j, v[j]);
+            for (int j = 0; j < G; ++j) sink(i + j, v[j]);
+            p = q;
+        }
+        float v[G];
+        bm_stage2<G>(p, v, c);
+#pragma unroll
+        for (int j = 0; j < G; ++j) sink(i + j, v[j]);
+        i += G;
     }
     for (; i < count; ++i) sink(i, bm_normal(s, c));
 }
