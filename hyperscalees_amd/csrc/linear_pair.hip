@@ -81,6 +81,7 @@ struct K2Args {
     float* rate;    // fused LIF: spike counts / T (M, a), or NULL
     int64_t rate_stride;
     int32_t a, b, r, R, rpm, T, n, tid_lo, pair_lo, n_pairs, epoch, nreuse;
+    int32_t segs;  // generation segments per stream row (jump table for row length r / segs)
     float bs, leak, v_th;
 };
 
@@ -302,14 +303,19 @@ __global__ __launch_bounds__(K2_THREADS) void k_linear_pair(const K2Args P) {
             float sg;
             epoch_thread_sign(P.epoch, 2 * pair, P.nreuse, &te, &tt, &sg);
             const uint64_t seed = noise_seed(P.key, te, tt);
-            for (int32_t j = tid; j < a + b; j += K2_THREADS) {
-                uint64_t s = row_start_state(seed, j, P.jump);
+            // Work units: segment g of stream row j (P.segs segments of r / segs
+            // normals), so small layers keep every thread generating.
+            const int32_t segs = P.segs, sl = r / segs;
+            for (int32_t u = tid; u < (a + b) * segs; u += K2_THREADS) {
+                const int32_t j = u / segs, c0 = (u - j * segs) * sl;
+                uint64_t s = row_start_state(seed, u, P.jump);
                 if (j < b) {
-                    bm_run(s, r, ctx, [&](int32_t c, float v) { slot[(size_t)c * kp + j] = f2bf(v); });
+                    bm_run(s, sl, ctx, [&](int32_t c, float v) { slot[(size_t)(c0 + c) * kp + j] = f2bf(v); });
                 } else {
-                    uint16_t* dst = As + (size_t)(j - b) * lay.apitch;
-                    bm_run(s, r, ctx, [&](int32_t c, float v) { dst[c] = f2bf(v * P.bs); });
-                    for (int32_t c = r; c < rp32; ++c) dst[c] = 0;
+                    uint16_t* dst = As + (size_t)(j - b) * lay.apitch + c0;
+                    bm_run(s, sl, ctx, [&](int32_t c, float v) { dst[c] = f2bf(v * P.bs); });
+                    if (c0 + sl == r)
+                        for (int32_t c = r; c < rp32; ++c) As[(size_t)(j - b) * lay.apitch + c] = 0;
                 }
             }
             __threadfence_block();
@@ -495,7 +501,12 @@ int launch_linear_pair(LinParams& P, DeviceState* st, hipStream_t s, void* work,
     uint16_t* wbf = static_cast<uint16_t*>(work);
     A.wbf = wbf;
     A.slots = reinterpret_cast<uint16_t*>(static_cast<char*>(work) + align16((size_t)P.a * lay.kp * 2));
-    int rc = get_jump_table(st, P.r, (int64_t)P.a + P.b, &P.jump);
+    // Split each stream row into segs pieces (row length r / segs in the jump
+    // table) when a + b rows would leave threads idle.
+    A.segs = 1;
+    while (A.segs < 4 && (int64_t)(P.a + P.b) * A.segs * 2 <= K2_THREADS && P.r % (A.segs * 8) == 0)
+        A.segs *= 2;
+    int rc = get_jump_table(st, P.r / A.segs, ((int64_t)P.a + P.b) * A.segs, &P.jump);
     if (rc) return rc;
     A.x = P.x;
     A.x_stride = P.x_stride;
