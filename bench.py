@@ -25,6 +25,10 @@ METRIC = "perturbed member-evals/sec + ES-update GB/s, SNN-MLP N=8192 r=128"
 PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
 PEAK_FP32_TFLOPS = 157.3      # MI355X dense fp32 MFMA
 PEAK_HBM_GBPS = 8000.0
+# HBM bytes per fc1 launch from two rocprofv3 PMC runs (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0,
+# factors from a 1 GiB copy) of `python3 -m hyperscalees_amd.profile_fc1`;
+# see profiles/fc1_c3_traffic.md.  Refreshed whenever the kernel changes.
+FC1_TRAFFIC_BYTES = 9.29e9
 
 
 def layer_flops(cfg, l):
@@ -86,7 +90,7 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--population", type=int, default=8192)
-    ap.add_argument("--cpu-members", type=int, default=32)
+    ap.add_argument("--cpu-members", type=int, default=8192)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -193,7 +197,8 @@ def main():
                                 + (", LIF fused)" if es.fused else ")")),
                      "bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": None, "launch_ms": round(fc1_ms, 3),
+                     "traffic": FC1_TRAFFIC_BYTES if es.fused else None,
+                     "launch_ms": round(fc1_ms, 3),
                      "algorithmic_flop_per_launch": fc1_flops},
     }
     if not args.no_cpu_baseline:

@@ -1,0 +1,47 @@
+"""Profiling target for the dominant kernel of the C3 ES step.
+
+Runs, on cuda:0 with synthetic data of the C3 shape (bench.py's workload):
+  * a device-to-device copy of a known size (1 GiB), the calibration point for
+    the FETCH_SIZE / WRITE_SIZE hardware counters;
+  * the fc1 layer of the SNN step: hses_perturbed_linear_lif (x[W^T|B] +
+    (xB)A^T fused with the LIF scan), N = 8192 members, r = 128, T = 16, 64 rows
+    per member, b = 784, a = 128.
+Each is launched --reps times.  Use under rocprofv3, e.g.
+    rocprofv3 --pmc FETCH_SIZE --output-format csv -d OUT -- python3 -m hyperscalees_amd.profile_fc1
+"""
+import argparse
+
+import torch
+
+from . import kernels as K
+from . import snn
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--reps", type=int, default=3)
+    args = ap.parse_args()
+    K.init(0)
+    cfg = snn.SnnConfig(poisson_seed=(1, 2, 3, 4))
+    M = cfg.n * cfg.rows
+    g = torch.Generator(device="cuda").manual_seed(0)
+    words_in = K.fmt_width(K.FMT_BITS, cfg.dims[0])
+    x = torch.randint(0, 2**62, (cfg.T, M, words_in), dtype=torch.int64, device="cuda", generator=g)
+    W = torch.randn(cfg.dims[1], cfg.dims[0], device="cuda", generator=g) * 0.05
+    spk = torch.empty((cfg.T, M, K.fmt_width(K.FMT_BITS, cfg.dims[1])), dtype=torch.int64,
+                      device="cuda")
+    src = torch.empty(1 << 28, dtype=torch.float32, device="cuda")  # 1 GiB
+    dst = torch.empty_like(src)
+    src.fill_(1.0)
+    torch.cuda.synchronize()
+    for _ in range(args.reps):
+        dst.copy_(src)
+    for s in range(args.reps):
+        K.perturbed_linear_lif(x, W, cfg.keys[0], cfg.rank, cfg.sigma, s, cfg.noise_reuse, 0,
+                               cfg.n, cfg.rows, cfg.T, cfg.tau_m, cfg.v_th, spikes=spk)
+    torch.cuda.synchronize()
+    print("profile_fc1: copy 1 GiB x", args.reps, "; fc1 fused x", args.reps, flush=True)
+
+
+if __name__ == "__main__":
+    main()
