@@ -230,13 +230,18 @@ __global__ __launch_bounds__(R_MAXT) void k_es_rows(UpdParams P, RowTiles G) {
     // runs the MFMAs of item u from buffer u & 1 it generates item u + 1 into
     // the other buffer, four normals per k-step, so the matrix cores of one
     // wave overlap the VALU generation of the other waves on the SIMD.
+    // The row's stream is consumed four normals at a time through a one-batch
+    // look-ahead (pend holds stage 1 of the next four normals), so the bitmap
+    // loads of a batch are in flight while the MFMAs and the next batch run.
     const int32_t n_items = (p_end - p_begin) * chunks;
     uint64_t st = 0;
+    BmPending<4> pend;
     auto start_pair = [&](int32_t p) {
         int32_t te, tt;
         float sg;
         epoch_thread_sign(P.epoch, 2 * p, P.nreuse, &te, &tt, &sg);
         st = row_start_state(noise_seed(P.key, te, tt), srow, P.jump);
+        bm_stage1<4, true>(st, pend, ctx);
     };
     auto pair_weight = [&](int32_t p) {
         const int32_t me = 2 * p - P.tid_lo, mo = me + 1;
@@ -244,20 +249,16 @@ __global__ __launch_bounds__(R_MAXT) void k_es_rows(UpdParams P, RowTiles G) {
         const float fo = (mo >= 0 && mo < P.n) ? P.f[mo] : 0.0f;
         return fe - fo;
     };
-    // Generation of normals [c, c + cnt) (cnt <= 4) of the current chunk.
+    // Normals [c, c + cnt) (cnt <= 4) of the current chunk: finish the pending
+    // batch and start the next.  Only a row's last batch can be short (r % 4),
+    // and the look-ahead past the row's end is discarded (a new pair re-seeds).
     auto gen4 = [&](float* dst, int32_t c, int32_t cnt) {
-        if (cnt == 4) {
+        const BmPending<4> cur = pend;
+        bm_stage1<4, true>(st, pend, ctx);
+        float v[4];
+        bm_stage2<4>(cur, v, ctx);
 #pragma unroll
-            for (int h = 0; h < 4; h += 2) {
-                float v[2];
-                bm_normals<2>(st, v, ctx);
-                dst[c + h] = v[0] * scl;
-                dst[c + h + 1] = v[1] * scl;
-            }
-        } else {
-            for (int32_t e = 0; e < cnt; ++e) dst[c + e] = bm_normal(st, ctx) * scl;
-            for (int32_t e = cnt; e < 4; ++e) dst[c + e] = 0.0f;  // k padding of the last step
-        }
+        for (int e = 0; e < 4; ++e) dst[c + e] = e < cnt ? v[e] * scl : 0.0f;  // k padding
     };
     if (n_items > 0) {
         start_pair(p_begin);
@@ -345,7 +346,7 @@ static int32_t rows_tiles(int32_t a, int32_t b) {
     return t;
 }
 
-// Split count of k_es_rows: about 512 workgroups over the tiles of at least
+// Split count of k_es_rows: about 1024 workgroups over the tiles of at least
 // 256 threads, at least 8 pairs per split.  Shape-only, so results do not
 // depend on the device.
 static int32_t rows_splits(int32_t a, int32_t b, int32_t n_pairs) {
@@ -355,7 +356,7 @@ static int32_t rows_splits(int32_t a, int32_t b, int32_t n_pairs) {
         big += b / btm;
         if (b % btm && at + b % btm > 256) ++big;
     }
-    int64_t s = 512 / std::max(1, big);
+    int64_t s = 1024 / std::max(1, big);
     s = std::min<int64_t>(s, std::max<int32_t>(1, n_pairs / 8));
     return (int32_t)std::max<int64_t>(1, std::min<int64_t>(s, 512));
 }
