@@ -27,6 +27,10 @@
 // steps of one (member, slot) are consecutive rows of one wave's row group.
 // The (n, b, r) factor tensor is never materialised: at most one B per
 // workgroup exists at any time.
+//
+// Two kernels share this structure.  k_linear_pair (below) takes any input
+// format; k_pair_bits (further down) is the form for bit-packed input (the
+// hidden layers of the SNN) and keeps its whole epilogue in registers.
 #include <math.h>
 
 #include <type_traits>
@@ -152,6 +156,15 @@ __device__ __forceinline__ u16x8 dense_frag(const void* x, int64_t off, bool val
             v[e] = ok ? f2bf((float)static_cast<const uint8_t*>(x)[off + k0 + e]) : (uint16_t)0;
     }
     return v;
+}
+
+// Workgroup barrier that orders LDS accesses only: global loads issued
+// before it stay in flight (a plain __syncthreads also waits for every
+// outstanding global load, which would drain the tile prefetch).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 // Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).
@@ -459,6 +472,393 @@ __global__ __launch_bounds__(K2_THREADS) void k_linear_pair(const K2Args P) {
     }
 }
 
+
+// ---- k_pair_bits: bit-packed input, epilogue in registers ----------------------
+//
+// The hidden-layer form of the pair kernel (x bit-packed, bf16 MFMA 32x32x16).
+// Eight waves of 32 rows x all 256 staged columns (128 W rows | 128 rank
+// columns of B), so every wave owns whole output rows and the epilogue needs
+// no LDS round trip:
+//   * the B columns are accumulated transposed (mfma(B, x)): lane l then holds
+//     16 rank columns of the row at MFMA position l % 32, which after the
+//     member sign and the bf16 rounding are the A-operand fragments of the
+//     second product (xB) A^T as they are (the k-group of each 16-step is
+//     chosen to match, and A is read with the same mapping);
+//   * a 32x32 accumulator gives lane l the 16 rows 8g + 4h + v (h = l / 32)
+//     of column l % 32; block rows are assigned so that those are wave rows
+//     16h + 4g + v, i.e. 16 consecutive rows.  With slot-major rows each
+//     T-step series (T <= 16) of a column sits in one lane and the LIF runs
+//     in registers; the comparison of a step, as a ballot, holds two rows x
+//     32 columns, so its 32-bit halves are the halves of spike words.
+// Each x bit row is expanded by one wave only.  The next block's bit rows and
+// first W/B tile are loaded while the epilogue runs.
+constexpr int K3_THREADS = 512, K3_RB = 256;
+// Bit-row staging: thread t handles row t / 2 and words t % 2, t % 2 + 2, ...
+// (at most K3_XPF of them: rows of up to 2 * K3_XPF words, b <= 1024; wider
+// inputs use k_linear_pair).
+constexpr int K3_XPF = 8;
+// A pitch in bf16 (r <= 128 padded to 128, plus 12 so rows 32 apart fall on
+// different LDS banks); a compile-time constant keeps the second product's
+// LDS addresses immediate offsets of one base.
+constexpr int K3_AP = K2_NMAX + 12;
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ f32x16 mfma32_bf16(const u16x8& a, const u16x8& b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+struct K3Layout {
+    size_t off_a, off_xbits, off_wb, bytes;
+    int32_t apitch, words, kp;
+    __host__ __device__ K3Layout(int r, int b) {
+        apitch = K3_AP;
+        words = (b + 63) / 64;
+        kp = words * 64;
+        size_t o = align16(sizeof(BmTables));
+        off_a = o;
+        o = align16(o + (size_t)K2_NMAX * apitch * 2);
+        off_xbits = o;
+        o = align16(o + (size_t)K3_RB * words * 8);
+        off_wb = o;
+        bytes = o + (size_t)2 * K2_COLS * K2_TP * 2;
+    }
+};
+
+// EPI_Y: store the currents; EPI_LIF: LIF with T = LT, spike words if SPK,
+// spike rates if RATE.
+template <int EPI, int LT, bool SPK, bool RATE>
+__global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
+    static_assert(LT >= 1 && LT <= 16 && (LT & (LT - 1)) == 0, "T must be a power of two <= 16");
+    extern __shared__ __align__(16) unsigned char smem[];
+    const K3Layout lay(P.r, P.b);
+    BmTables* tabs = reinterpret_cast<BmTables*>(smem);
+    uint16_t* As = reinterpret_cast<uint16_t*>(smem + lay.off_a);
+    uint64_t* Xbits = reinterpret_cast<uint64_t*>(smem + lay.off_xbits);
+    const uint32_t* Xbits32 = reinterpret_cast<const uint32_t*>(smem + lay.off_xbits);
+    uint16_t* WB = reinterpret_cast<uint16_t*>(smem + lay.off_wb);  // [2][K2_COLS][K2_TP]
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lc = lane & 31, hl = lane >> 5;  // MFMA column / k-group of this lane
+    const int32_t r = P.r, a = P.a, b = P.b, kp = lay.kp, nkt = lay.words, R = P.R;
+    const int32_t rp32 = (r + 31) & ~31;
+    uint16_t* slot = P.slots + (size_t)blockIdx.x * r * kp;
+
+    load_bm_tables(tabs, P.tables);
+    for (int32_t i = tid; i < r * (kp - b); i += K3_THREADS) {
+        const int32_t c = i / (kp - b), k = b + i % (kp - b);
+        slot[(size_t)c * kp + k] = 0;
+    }
+    __threadfence_block();
+    __syncthreads();
+    const NoiseCtx ctx{tabs, P.log_exc, P.cos_exc};
+
+    // Tile loader: thread -> (staged column, 32-k half); columns [0, 128) are
+    // W rows, [128, 256) rank columns of B; absent ones are staged as zeros.
+    const int lcol = tid >> 1, lk = (tid & 1) * 32;
+    const bool lvalid = lcol < K2_NMAX ? lcol < a : lcol - K2_NMAX < r;
+    const uint16_t* lsrc = lcol < K2_NMAX ? P.wbf + (size_t)min(lcol, a - 1) * kp + lk
+                                          : slot + (size_t)min(lcol - K2_NMAX, r - 1) * kp + lk;
+    uint16_t* ldst = WB + lcol * K2_TP + lk;
+    const uint32_t lmask = lvalid ? 0xffffffffu : 0u;
+#define K3_TILE_LOAD(kt)                                                            \
+    do {                                                                            \
+        const uint4* src_ = reinterpret_cast<const uint4*>(lsrc + (kt) * K2_BK);    \
+        pf0 = src_[0];                                                              \
+        pf1 = src_[1];                                                              \
+        pf2 = src_[2];                                                              \
+        pf3 = src_[3];                                                              \
+    } while (0)
+#define K3_TILE_STORE(buf)                                                          \
+    do {                                                                            \
+        uint4* d_ = reinterpret_cast<uint4*>(ldst + (buf) * (K2_COLS * K2_TP));     \
+        d_[0] = mask4(pf0, lmask);                                                  \
+        d_[1] = mask4(pf1, lmask);                                                  \
+        d_[2] = mask4(pf2, lmask);                                                  \
+        d_[3] = mask4(pf3, lmask);                                                  \
+    } while (0)
+    // Wave row of MFMA position p (0..31): 8g + 4h + v -> 16h + 4g + v.
+    const int xrow = 16 * ((lc >> 2) & 1) + 4 * (lc >> 3) + (lc & 3);
+    const int32_t wrow0 = wave * 32;
+    const int32_t xs_row = tid >> 1, xs_w = tid & 1;
+    // Rows [lo, hi) of the members of pair index pi.
+    auto pair_rows = [&](int32_t pi_, int64_t* lo, int64_t* hi) {
+        const int32_t m_even = 2 * (P.pair_lo + pi_) - P.tid_lo;
+        *lo = (int64_t)max(m_even, 0) * R;
+        *hi = (int64_t)(min(m_even + 1, P.n - 1) + 1) * R;
+    };
+    bool xready = false;  // the first block's bit rows are already in LDS
+
+    for (int32_t pi = blockIdx.x; pi < P.n_pairs; pi += gridDim.x) {
+        const int32_t pair = P.pair_lo + pi;
+        int64_t row_lo, row_hi;
+        pair_rows(pi, &row_lo, &row_hi);
+        const bool more_pairs = pi + (int32_t)gridDim.x < P.n_pairs;
+
+        // ---- 1. factors: A rows -> LDS (bf16, [o][c]); B rows -> slot ([c][k]) ----
+        {
+            __syncthreads();  // the previous pair's epilogue has finished reading As
+            int32_t te, tt;
+            float sg;
+            epoch_thread_sign(P.epoch, 2 * pair, P.nreuse, &te, &tt, &sg);
+            const uint64_t seed = noise_seed(P.key, te, tt);
+            const int32_t segs = P.segs, sl = r / segs;
+            for (int32_t u = tid; u < (a + b) * segs; u += K3_THREADS) {
+                const int32_t j = u / segs, c0 = (u - j * segs) * sl;
+                uint64_t s = row_start_state(seed, u, P.jump);
+                if (j < b) {
+                    bm_run(s, sl, ctx, [&](int32_t c, float v) { slot[(size_t)(c0 + c) * kp + j] = f2bf(v); });
+                } else {
+                    uint16_t* dst = As + (size_t)(j - b) * lay.apitch + c0;
+                    bm_run(s, sl, ctx, [&](int32_t c, float v) { dst[c] = f2bf(v * P.bs); });
+                    if (c0 + sl == r)
+                        for (int32_t c = r; c < rp32; ++c) As[(size_t)(j - b) * lay.apitch + c] = 0;
+                }
+            }
+            __threadfence_block();
+            __syncthreads();
+        }
+
+        // Bit rows of the block starting at L (of a pair ending at row rhi):
+        // thread t loads words t % 2 + 2q of block row t / 2.
+        // The loads are unconditional (rows past the pair's end read its last
+        // row, words past the row its last word) and the result is masked when
+        // stored, so nothing waits for them before xbits_store.
+        bool xs_ok = false;
+        auto xbits_load = [&](int64_t L, int64_t rhi, uint64_t (&v)[K3_XPF]) {
+            RowCursor cr;
+            cr.m0 = (int32_t)(L / R);
+            cr.q0 = (int32_t)(L - (int64_t)cr.m0 * R);
+            const int32_t nv = (int32_t)min<int64_t>(rhi - L, K3_RB);
+            xs_ok = xs_row < nv;
+            int32_t m, qq;
+            cr.at(min(xs_row, nv - 1), R, &m, &qq);
+            const uint64_t* src = static_cast<const uint64_t*>(P.x) +
+                                  k2_phys(m, qq, P.rpm, P.T, P.x_stride, P.x_plane);
+#pragma unroll
+            for (int q = 0; q < K3_XPF; ++q) v[q] = src[min(xs_w + 2 * q, nkt - 1)];
+        };
+        auto xbits_store = [&](const uint64_t (&v)[K3_XPF]) {
+#pragma unroll
+            for (int q = 0; q < K3_XPF; ++q) {
+                const int32_t w = xs_w + 2 * q;
+                if (w < nkt) Xbits[xs_row * nkt + w] = xs_ok ? v[q] : 0ull;
+            }
+        };
+
+        // ---- 2./3. row blocks ----------------------------------------------------
+        uint4 pf0, pf1, pf2, pf3;
+        uint64_t xpf[K3_XPF];
+        for (int64_t L0 = row_lo; L0 < row_hi; L0 += K3_RB) {
+            const bool first = L0 == row_lo;
+            const bool has_next = L0 + K3_RB < row_hi;
+            RowCursor cur_rows;
+            cur_rows.m0 = (int32_t)(L0 / R);
+            cur_rows.q0 = (int32_t)(L0 - (int64_t)cur_rows.m0 * R);
+            const int32_t nvalid = (int32_t)min<int64_t>(row_hi - L0, K3_RB);
+            if (first && !xready) {
+                xbits_load(L0, row_hi, xpf);
+                xbits_store(xpf);
+            }
+            if (first) {
+                K3_TILE_LOAD(0);
+                K3_TILE_STORE(0);
+            }
+            lds_barrier();
+            if (nkt > 1) K3_TILE_LOAD(1);
+
+            f32x16 accW[4], accB[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    accW[j][e] = 0.0f;
+                    accB[j][e] = 0.0f;
+                }
+            }
+            const uint32_t* xw = Xbits32 + (wrow0 + xrow) * (2 * nkt);
+
+            for (int32_t kt = 0; kt < nkt; ++kt) {
+                const int cur = kt & 1;
+                const uint16_t* tb = WB + cur * (K2_COLS * K2_TP) + lc * K2_TP + hl * 8;
+                const uint32_t w2[2] = {xw[2 * kt], xw[2 * kt + 1]};
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) {  // k-steps of 16: this lane's 8 k at 16ks + 8hl
+                    // all eight operand reads of the step are issued before its MFMAs
+                    u16x8 fr[8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j)
+                        fr[j] = lds_u16x8(tb + ((j < 4 ? 0 : K2_NMAX) + 32 * (j & 3)) * K2_TP + 16 * ks);
+                    const u16x8 xa = expand_bits((w2[ks >> 1] >> (8 * ((ks & 1) * 2 + hl))) & 0xffu);
+                    // keep the reads ahead of the MFMAs (the scheduler would
+                    // otherwise issue each read just before its MFMA)
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) accW[j] = mfma32_bf16(xa, fr[j], accW[j]);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) accB[j] = mfma32_bf16(fr[4 + j], xa, accB[j]);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                if (kt + 1 < nkt) {
+                    K3_TILE_STORE(cur ^ 1);
+                    if (kt + 2 < nkt) K3_TILE_LOAD(kt + 2);
+                }
+                lds_barrier();
+            }
+
+            // sign * xB as bf16: lane l holds rank columns 32j + 8g + 4hl + v of
+            // the row at MFMA position lc (the row its x operand came from).
+            uint32_t xbf[4][4][2];
+            {
+                int32_t m, q;
+                cur_rows.at(wrow0 + xrow, R, &m, &q);
+                // odd members carry -A: negate after rounding (RNE is symmetric)
+                const uint32_t sgn = ((P.tid_lo + m) & 1) ? 0x80008000u : 0u;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        xbf[j][g][0] = pack_bf16x2(accB[j][4 * g], accB[j][4 * g + 1]) ^ sgn;
+                        xbf[j][g][1] = pack_bf16x2(accB[j][4 * g + 2], accB[j][4 * g + 3]) ^ sgn;
+                    }
+            }
+            // The next block's operands land during the epilogue: its bit rows
+            // (the next pair's first block after a pair's last one) and, inside
+            // a pair, its first W/B tile.
+            // (Issued without branches: the last block of the last pair reloads
+            // its own rows and tile, which are then not stored.)
+            const bool next_pair = !has_next && more_pairs;
+            {
+                int64_t nlo = L0, nhi = row_hi;
+                if (has_next) nlo = L0 + K3_RB;
+                else if (next_pair) pair_rows(pi + (int32_t)gridDim.x, &nlo, &nhi);
+                xbits_load(nlo, nhi, xpf);
+                K3_TILE_LOAD(0);
+            }
+            // accW += (sign xB) A^T over K = r in steps of 16: step (j, t) gives
+            // k-group hl the rank columns 32j + 16t + 4hl + {0..3, 8..11}.
+            const uint16_t* abase = As + (size_t)lc * K3_AP + 4 * hl;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (32 * j >= rp32) break;
+                // the 16 A reads of this rank tile, then its 8 MFMAs (absent
+                // output tiles, 32 jo >= a, read row lc of tile 0; their columns
+                // are never stored)
+                uint2 af[2][4][2];
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+#pragma unroll
+                    for (int jo = 0; jo < 4; ++jo) {
+                        const uint16_t* ap = abase + (32 * jo < a ? 32 * jo * K3_AP : 0) + 32 * j + 16 * t;
+                        af[t][jo][0] = *reinterpret_cast<const uint2*>(ap);
+                        af[t][jo][1] = *reinterpret_cast<const uint2*>(ap + 8);
+                    }
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    const uint32_t d[4] = {xbf[j][2 * t][0], xbf[j][2 * t][1], xbf[j][2 * t + 1][0],
+                                           xbf[j][2 * t + 1][1]};
+                    const u16x8 xo = __builtin_bit_cast(u16x8, d);
+#pragma unroll
+                    for (int jo = 0; jo < 4; ++jo) {
+                        const uint32_t e[4] = {af[t][jo][0].x, af[t][jo][0].y, af[t][jo][1].x,
+                                               af[t][jo][1].y};
+                        accW[jo] = mfma32_bf16(xo, __builtin_bit_cast(u16x8, e), accW[jo]);
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+
+            // accW[jo][4g + v]: wave row 16 hl + 4g + v, column 32 jo + lc
+            if constexpr (EPI == EPI_Y) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const int32_t row = wrow0 + 16 * hl + 4 * g + v;
+                        if (row >= nvalid) continue;
+                        int32_t m, q;
+                        cur_rows.at(row, R, &m, &q);
+                        float* yrow = P.y + k2_phys(m, q, P.rpm, P.T, P.y_stride, P.y_plane);
+#pragma unroll
+                        for (int jo = 0; jo < 4; ++jo)
+                            if (32 * jo + lc < a) yrow[32 * jo + lc] = accW[jo][4 * g + v];
+                    }
+            } else {
+                // LIF (snn.rs:53-97) along each lane's rows, v = 0 at t = 0.  The
+                // reset keeps `charged` when no spike fired and gives 0 otherwise:
+                // the reference's charged * (1 - spike) differs only in the sign
+                // of a zero, which leaves every later `charged` (and spike) equal.
+                float vm[4];
+                int32_t cnt[4];
+                uint32_t wlo[2] = {0, 0}, whi[2] = {0, 0};  // lane u: spike words of wave row u
+                bool colok[4];
+#pragma unroll
+                for (int jo = 0; jo < 4; ++jo) colok[jo] = 32 * jo + lc < a;
+                static_for<0, 16>([&](auto qc) {
+                    constexpr int qq = decltype(qc)::value;  // 4g + v: time step qq % T
+                    if constexpr (qq % LT == 0) {
+#pragma unroll
+                        for (int jo = 0; jo < 4; ++jo) {
+                            vm[jo] = 0.0f;
+                            cnt[jo] = 0;
+                        }
+                    }
+                    uint64_t bal[4];
+#pragma unroll
+                    for (int jo = 0; jo < 4; ++jo) {
+                        const float c = accW[jo][qq];
+                        const float charged = __fadd_rn(vm[jo], __fmul_rn(__fadd_rn(-vm[jo], c), P.leak));
+                        const bool spike = charged >= P.v_th;
+                        vm[jo] = spike ? 0.0f : charged;
+                        if constexpr (RATE) cnt[jo] += spike ? 1 : 0;
+                        if constexpr (SPK) bal[jo] = __builtin_amdgcn_ballot_w64(spike && colok[jo]);
+                    }
+                    if constexpr (RATE && qq % LT == LT - 1) {
+                        const int32_t row = wrow0 + 16 * hl + qq;
+                        if (row < nvalid) {
+                            int32_t m, q;
+                            cur_rows.at(row, R, &m, &q);
+                            float* rp = P.rate + ((int64_t)m * P.rpm + q / LT) * P.rate_stride;
+#pragma unroll
+                            for (int jo = 0; jo < 4; ++jo)
+                                if (colok[jo]) rp[32 * jo + lc] = (float)cnt[jo] * (1.0f / LT);
+                        }
+                    }
+                    if constexpr (SPK) {
+                        // ballot bit l: column 32 jo + l % 32 of wave row 16 (l / 32) + qq
+#pragma unroll
+                        for (int hh = 0; hh < 2; ++hh) {
+                            const uint64_t b0 = bal[2 * hh], b1 = bal[2 * hh + 1];
+                            put_lane<qq>(wlo[hh], whi[hh], (b0 & 0xffffffffull) | (b1 << 32));
+                            put_lane<16 + qq>(wlo[hh], whi[hh], (b0 >> 32) | (b1 & 0xffffffff00000000ull));
+                        }
+                    }
+                });
+                if constexpr (SPK) {
+                    if (lane < 32) {
+                        const int32_t row = wrow0 + lane;
+                        if (row < nvalid) {
+                            int32_t m, q;
+                            cur_rows.at(row, R, &m, &q);
+                            uint64_t* dst = P.spk + k2_phys(m, q, P.rpm, LT, P.spk_stride, P.spk_plane);
+                            dst[0] = ((uint64_t)whi[0] << 32) | wlo[0];
+                            if (a > 64) dst[1] = ((uint64_t)whi[1] << 32) | wlo[1];
+                        }
+                    }
+                }
+            }
+            if (has_next) K3_TILE_STORE(0);
+            if (has_next || next_pair) xbits_store(xpf);
+            xready = next_pair;
+        }
+    }
+#undef K3_TILE_LOAD
+#undef K3_TILE_STORE
+}
+
 static bool pair_kernel_applies(const LinParams& P) {
     return P.math == HSES_MATH_BF16 && P.r >= 16 && P.r <= K2_NMAX && P.r % 16 == 0 &&
            P.a <= K2_NMAX;
@@ -490,8 +890,13 @@ int launch_linear_pair(LinParams& P, DeviceState* st, hipStream_t s, void* work,
     if (lif && (P.n_time > 64 || (P.n_time & (P.n_time - 1)) != 0 || P.x_fmt != HSES_FMT_BITS))
         return HSES_ERR_UNSUPPORTED;
     const bool bits = P.x_fmt == HSES_FMT_BITS;
+    // Bit-packed input with T <= 16 for the fused LIF: k_pair_bits.
+    const bool v3 = bits && (!lif || P.n_time <= 16) && P.b <= 2 * K3_XPF * 64;
     const K2Layout lay(P.r, P.b, bits);
-    if (lay.bytes > st->max_lds) return HSES_ERR_UNSUPPORTED;
+    const K3Layout lay3(P.r, P.b);
+    const size_t lds_bytes = v3 ? lay3.bytes : lay.bytes;
+    const int threads = v3 ? K3_THREADS : K2_THREADS;
+    if (lds_bytes > st->max_lds) return HSES_ERR_UNSUPPORTED;
     K2Args A{};
     pair_range(P.tid_lo, P.n, &A.pair_lo, &A.n_pairs);
     const int32_t grid = pair_grid(st, A.n_pairs);
@@ -504,7 +909,7 @@ int launch_linear_pair(LinParams& P, DeviceState* st, hipStream_t s, void* work,
     // Split each stream row into segs pieces (row length r / segs in the jump
     // table) when a + b rows would leave threads idle.
     A.segs = 1;
-    while (A.segs < 4 && (int64_t)(P.a + P.b) * A.segs * 2 <= K2_THREADS && P.r % (A.segs * 8) == 0)
+    while (A.segs < 4 && (int64_t)(P.a + P.b) * A.segs * 2 <= threads && P.r % (A.segs * 8) == 0)
         A.segs *= 2;
     int rc = get_jump_table(st, P.r / A.segs, ((int64_t)P.a + P.b) * A.segs, &P.jump);
     if (rc) return rc;
@@ -544,13 +949,30 @@ int launch_linear_pair(LinParams& P, DeviceState* st, hipStream_t s, void* work,
                        P.b, lay.kp, wbf);
     HSES_CHECK_HIP(hipGetLastError());
     auto launch = [&](auto kern) -> int {
-        if (lay.bytes > 64 * 1024)
+        if (lds_bytes > 64 * 1024)
             HSES_CHECK_HIP(hipFuncSetAttribute((const void*)kern,
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lay.bytes));
-        hipLaunchKernelGGL(kern, dim3(grid), dim3(K2_THREADS), lay.bytes, s, A);
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes));
+        hipLaunchKernelGGL(kern, dim3(grid), dim3(threads), lds_bytes, s, A);
         HSES_CHECK_HIP(hipGetLastError());
         return HSES_OK;
     };
+    if (v3) {
+        if (!lif) return launch(k_pair_bits<EPI_Y, 1, false, false>);
+        const bool spk = lif->spk != nullptr, rate = lif->rate != nullptr;
+        auto by_t = [&](auto sc, auto rc) -> int {
+            constexpr bool S = decltype(sc)::value, Q = decltype(rc)::value;
+            switch (P.n_time) {
+                case 1: return launch(k_pair_bits<EPI_LIF, 1, S, Q>);
+                case 2: return launch(k_pair_bits<EPI_LIF, 2, S, Q>);
+                case 4: return launch(k_pair_bits<EPI_LIF, 4, S, Q>);
+                case 8: return launch(k_pair_bits<EPI_LIF, 8, S, Q>);
+                default: return launch(k_pair_bits<EPI_LIF, 16, S, Q>);
+            }
+        };
+        if (spk && rate) return by_t(std::true_type{}, std::true_type{});
+        if (spk) return by_t(std::true_type{}, std::false_type{});
+        return by_t(std::false_type{}, std::true_type{});
+    }
     if (lif) {
         switch (P.n_time) {
             case 1: return launch(k_linear_pair<HSES_FMT_BITS, EPI_LIF, 1>);
