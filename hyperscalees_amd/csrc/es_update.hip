@@ -47,6 +47,7 @@ struct UpdParams {
     int32_t pair_lo, n_pairs, splits;
     int32_t rc;  // stream rows per generation item (small ranks)
     float* work;
+    const float* scale;  // k_es_rows: {S, 1/S} (device)
     const BmTables* tables;
     const uint32_t* log_exc;
     const uint32_t* cos_exc;
@@ -159,23 +160,80 @@ __global__ __launch_bounds__(U_THREADS) void k_es_partial(UpdParams P) {
 
 constexpr int R_CT = 3;          // 16-column tiles per wave (at most)
 constexpr int R_MAXT = 512;      // threads (rows) per workgroup
+// LDS row of one rank chunk: the 32 values as fp16 high parts, then the 32 low
+// parts, then padding (144 B, so the 16 rows of an operand read by a
+// quarter-wave fall on distinct banks).
+constexpr int R_HP = 72;
 
 struct RowTiles {
     int32_t at, bt;              // tile extent
     int32_t o_base, q_base;      // origin of blockIdx (0, 0)
 };
 
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4 mfma_f16(const uint4& a, const uint4& b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+// x = hi + lo with hi = RN16(x), lo = RN16(x - hi): |x - hi - lo| <= 2^-22 |x|
+// for x in fp16's normal range (the operands are scaled into it).
+__device__ __forceinline__ void split_f16x4(const float (&x)[4], uint2* hi, uint2* lo) {
+    const f16x4 h = __builtin_convertvector((f32x4){x[0], x[1], x[2], x[3]}, f16x4);
+    const f32x4 hf = __builtin_convertvector(h, f32x4);
+    const f16x4 l = __builtin_convertvector((f32x4){x[0] - hf[0], x[1] - hf[1], x[2] - hf[2],
+                                                    x[3] - hf[3]}, f16x4);
+    *hi = __builtin_bit_cast(uint2, h);
+    *lo = __builtin_bit_cast(uint2, l);
+}
+
+// Operand scale S (a power of two) of k_es_rows, and 1/S for k_es_reduce.
+// The A operand is S * (w_p * Ahat): |Ahat| <= base_sigma * 6.44 (the largest
+// Box-Muller radius, u1 >= 2^-24) and |w_p| <= 2 max|f|, so S puts the largest
+// product term near 2^15, inside fp16's range, with the low parts of every
+// value far above fp16's underflow relative to it.
+__global__ __launch_bounds__(1024) void k_es_scale(const float* __restrict__ f, int32_t n, float bs,
+                                                  float* __restrict__ out) {
+    __shared__ float red[1024];
+    float m = 0.0f;
+    for (int32_t i = threadIdx.x; i < n; i += 1024) m = fmaxf(m, fabsf(f[i]));
+    red[threadIdx.x] = m;
+    __syncthreads();
+    for (int w = 512; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + w]);
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        const float top = 2.0f * red[0] * fabsf(bs) * 6.5f;  // bound on |w_p * Ahat|
+        int e = 0;
+        if (top > 0.0f && isfinite(top)) {
+            frexpf(32768.0f / top, &e);
+            e = min(max(e - 1, -100), 100);  // 2^e <= 2^15 / top
+        }
+        out[0] = ldexpf(1.0f, e);
+        out[1] = ldexpf(1.0f, -e);
+    }
+}
+
 // NRT: 16-row tiles of a (a tile of at <= 16 * NRT rows); CT: 16-column tiles
 // per wave.  Both compile-time, so the MFMA block is branch-free: absent
 // tiles of a wave compute on clamped rows and are not stored.
+// The contraction runs as fp16 MFMAs on split operands: with x = xh + xl for
+// both sides, xh*yh + xh*yl + xl*yh (products exact in the fp32 accumulator)
+// differs from x*y by < 2^-20 |x y|, and the partial sums are S times the
+// fp32 ones (k_es_reduce divides S out).
 template <int NRT, int CT>
 __global__ __launch_bounds__(R_MAXT) void k_es_rows(UpdParams P, RowTiles G) {
+    static_assert(NRT <= 8, "the MFMA row tiles are interleaved with the 8 generation batches");
     extern __shared__ __align__(16) unsigned char smem[];
     BmTables* tabs = reinterpret_cast<BmTables*>(smem);
     const int32_t at = G.at, bt = G.bt, rows = at + bt;
-    float* buf0 = reinterpret_cast<float*>(smem + align_up16(sizeof(BmTables)));
-    // floats per buffer: As rows, Bs rows, then rows of the idle threads
-    const int32_t bufsz = (int32_t)blockDim.x * U_PITCH;
+    uint16_t* buf0 = reinterpret_cast<uint16_t*>(smem + align_up16(sizeof(BmTables)));
+    // halves per buffer: A rows, B rows, then one row shared by the idle
+    // threads (written, never read)
+    const int32_t bufsz = (rows + 1) * R_HP;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nw = blockDim.x >> 6;
@@ -187,52 +245,41 @@ __global__ __launch_bounds__(R_MAXT) void k_es_rows(UpdParams P, RowTiles G) {
     const int32_t chunks = (r + U_CW - 1) / U_CW;
 
     load_bm_tables(tabs, P.tables);
-    for (int i = tid; i < 2 * bufsz; i += blockDim.x) buf0[i] = 0.0f;
+    for (int i = tid; i < bufsz; i += blockDim.x)  // two buffers = bufsz words
+        reinterpret_cast<uint32_t*>(buf0)[i] = 0u;
     __syncthreads();
     const NoiseCtx ctx{tabs, P.log_exc, P.cos_exc};
+    const float S = P.scale[0];
 
     // This thread's stream row: A rows [0, at) first, then B rows.  Threads
-    // past the tile's rows generate a copy of row 0 into their own LDS row
-    // (never read), which keeps the generation free of divergent branches.
+    // past the tile's rows generate a copy of row 0 into one shared spare LDS
+    // row (never read), which keeps the generation free of divergent branches
+    // and the LDS footprint at the tile's rows.
     const bool is_a = tid < at;
     const int32_t srow = is_a ? P.b + o0 + tid : tid < rows ? q0 + (tid - at) : q0;
-    const float scl = is_a ? P.bs : 1.0f;
-    const int32_t grow = tid;  // LDS row written by this thread
+    const int32_t grow = min(tid, rows);  // LDS row written by this thread
 
     // MFMA ownership: column tiles wave, wave + nw, ... (at most CT).
     const int32_t nct = (bt + 15) >> 4;
     const int kg = lane >> 4, li = lane & 15;
-    int32_t aoff[NRT], boff[CT];  // LDS offsets of this lane's operand rows
+    int32_t aoff[NRT], boff[CT];  // LDS offsets (halves) of this lane's operand rows
 #pragma unroll
-    for (int i = 0; i < NRT; ++i) aoff[i] = min(i * 16 + li, at - 1) * U_PITCH + kg;
+    for (int i = 0; i < NRT; ++i) aoff[i] = min(i * 16 + li, at - 1) * R_HP + kg * 8;
 #pragma unroll
     for (int j = 0; j < CT; ++j)
-        boff[j] = (at + min(min(wave + j * nw, nct - 1) * 16 + li, bt - 1)) * U_PITCH + kg;
+        boff[j] = (at + min(min(wave + j * nw, nct - 1) * 16 + li, bt - 1)) * R_HP + kg * 8;
     f32x4 acc[NRT][CT];
 #pragma unroll
     for (int i = 0; i < NRT; ++i)
 #pragma unroll
         for (int j = 0; j < CT; ++j) acc[i][j] = f32x4{0, 0, 0, 0};
-    // acc += (w * Ahat[:, ks..ks+4)) B[:, ks..ks+4)^T from buffer X.
-    auto mfma_step = [&](const float* X, int32_t ks, float w) {
-        float af[NRT], bf[CT];
-#pragma unroll
-        for (int i = 0; i < NRT; ++i) af[i] = w * X[aoff[i] + ks];
-#pragma unroll
-        for (int j = 0; j < CT; ++j) bf[j] = X[boff[j] + ks];
-#pragma unroll
-        for (int i = 0; i < NRT; ++i)
-#pragma unroll
-            for (int j = 0; j < CT; ++j) acc[i][j] = mfma_f32(af[i], bf[j], acc[i][j]);
-    };
 
     // Software pipeline over work items u = (pair, rank chunk): while a wave
     // runs the MFMAs of item u from buffer u & 1 it generates item u + 1 into
-    // the other buffer, four normals per k-step, so the matrix cores of one
-    // wave overlap the VALU generation of the other waves on the SIMD.
-    // The row's stream is consumed four normals at a time through a one-batch
-    // look-ahead (pend holds stage 1 of the next four normals), so the bitmap
-    // loads of a batch are in flight while the MFMAs and the next batch run.
+    // the other buffer, four normals per MFMA row tile.  The row's stream is
+    // consumed four normals at a time through a one-batch look-ahead (pend
+    // holds stage 1 of the next four normals), so the bitmap loads of a batch
+    // are in flight while the MFMAs and the next batch run.
     const int32_t n_items = (p_end - p_begin) * chunks;
     uint64_t st = 0;
     BmPending<4> pend;
@@ -249,41 +296,73 @@ __global__ __launch_bounds__(R_MAXT) void k_es_rows(UpdParams P, RowTiles G) {
         const float fo = (mo >= 0 && mo < P.n) ? P.f[mo] : 0.0f;
         return fe - fo;
     };
-    // Normals [c, c + cnt) (cnt <= 4) of the current chunk: finish the pending
-    // batch and start the next.  Only a row's last batch can be short (r % 4),
-    // and the look-ahead past the row's end is discarded (a new pair re-seeds).
-    auto gen4 = [&](float* dst, int32_t c, int32_t cnt) {
+    // Normals [c, c + cnt) (cnt <= 4) of a chunk into row `dst`: finish the
+    // pending batch and start the next.  A values become S * (w * (v * bs))
+    // (the fp32 products of the reference, scaled exactly); B values stay v.
+    // Only a row's last batch can be short (r % 4), and the look-ahead past
+    // the row's end is discarded (a new pair re-seeds).
+    auto gen4 = [&](uint16_t* dst, int32_t c, int32_t cnt, float w) {
         const BmPending<4> cur = pend;
         bm_stage1<4, true>(st, pend, ctx);
         float v[4];
         bm_stage2<4>(cur, v, ctx);
+        float x[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) dst[c + e] = e < cnt ? v[e] * scl : 0.0f;  // k padding
+        for (int e = 0; e < 4; ++e) x[e] = e < cnt ? (is_a ? (v[e] * P.bs) * w * S : v[e]) : 0.0f;
+        uint2 hi, lo;
+        split_f16x4(x, &hi, &lo);
+        *reinterpret_cast<uint2*>(dst + c) = hi;
+        *reinterpret_cast<uint2*>(dst + U_CW + c) = lo;
+    };
+    // Zero columns [c, U_CW) of a short last chunk (r % 32 != 0): the MFMAs
+    // read all 32 k of a chunk.
+    auto zero_tail = [&](uint16_t* dst, int32_t c) {
+        for (; c < U_CW; c += 4) {
+            *reinterpret_cast<uint2*>(dst + c) = uint2{0, 0};
+            *reinterpret_cast<uint2*>(dst + U_CW + c) = uint2{0, 0};
+        }
     };
     if (n_items > 0) {
         start_pair(p_begin);
-        float* dst = buf0 + grow * U_PITCH;
+        uint16_t* dst = buf0 + grow * R_HP;
         const int32_t cn = min(U_CW, r);
-        for (int32_t c = 0; c < cn; c += 4) gen4(dst, c, min(4, cn - c));
+        const float w0 = pair_weight(p_begin);
+        for (int32_t c = 0; c < cn; c += 4) gen4(dst, c, min(4, cn - c), w0);
+        zero_tail(dst, (cn + 3) & ~3);
     }
     __syncthreads();
     for (int32_t u = 0; u < n_items; ++u) {
         const int32_t p = p_begin + u / chunks, ch = u % chunks;
-        const float w = pair_weight(p);
-        const int32_t cn = min(U_CW, r - ch * U_CW);
         const bool has_next = u + 1 < n_items;
         const int32_t nch = (ch + 1 == chunks) ? 0 : ch + 1;
         const int32_t ncn = min(U_CW, r - nch * U_CW);
         if (has_next && nch == 0) start_pair(p + 1);
-        const float* X = buf0 + (u & 1) * bufsz;
-        float* nxt = buf0 + ((u + 1) & 1) * bufsz + grow * U_PITCH;
-        // k-step ks, then four normals of the next chunk: the matrix cores of
-        // one wave overlap the generation of the other waves on the SIMD
-#pragma unroll 1
-        for (int32_t ks = 0; ks < U_CW; ks += 4) {
-            if (ks < cn) mfma_step(X, ks, w);
-            if (has_next && ks < ncn) gen4(nxt, ks, min(4, ncn - ks));
+        const float wn = has_next ? pair_weight(nch == 0 ? p + 1 : p) : 0.0f;
+        const uint16_t* X = buf0 + (u & 1) * bufsz;
+        uint16_t* nxt = buf0 + ((u + 1) & 1) * bufsz + grow * R_HP;
+        uint4 bh[CT], bl[CT];
+#pragma unroll
+        for (int j = 0; j < CT; ++j) {
+            bh[j] = *reinterpret_cast<const uint4*>(X + boff[j]);
+            bl[j] = *reinterpret_cast<const uint4*>(X + boff[j] + U_CW);
         }
+        // row tile i of the MFMAs, then four normals of the next chunk: the
+        // matrix cores of one wave overlap the generation of the other waves
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            if (i < NRT) {
+                const uint4 ah = *reinterpret_cast<const uint4*>(X + aoff[i]);
+                const uint4 al = *reinterpret_cast<const uint4*>(X + aoff[i] + U_CW);
+#pragma unroll
+                for (int j = 0; j < CT; ++j) {
+                    acc[i][j] = mfma_f16(ah, bh[j], acc[i][j]);
+                    acc[i][j] = mfma_f16(ah, bl[j], acc[i][j]);
+                    acc[i][j] = mfma_f16(al, bh[j], acc[i][j]);
+                }
+            }
+            if (has_next && 4 * i < ncn) gen4(nxt, 4 * i, min(4, ncn - 4 * i), wn);
+        }
+        if (has_next && ncn < U_CW) zero_tail(nxt, (ncn + 3) & ~3);
         __syncthreads();
     }
 
@@ -306,12 +385,15 @@ __global__ __launch_bounds__(R_MAXT) void k_es_rows(UpdParams P, RowTiles G) {
     }
 }
 
+// inv_s: 1/S of k_es_rows' scaled partials (a power of two), or NULL.
 __global__ void k_es_reduce(const float* __restrict__ work, int32_t splits, int64_t len, float scale,
-                            int32_t accumulate, float* __restrict__ g) {
+                            const float* __restrict__ inv_s, int32_t accumulate,
+                            float* __restrict__ g) {
     const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (e >= len) return;
     double s = 0.0;
     for (int32_t k = 0; k < splits; ++k) s += (double)work[(size_t)k * len + e];
+    if (inv_s) s *= (double)inv_s[0];
     const float v = (float)s * scale;
     g[e] = accumulate ? g[e] + v : v;
 }
@@ -378,7 +460,7 @@ extern "C" size_t hses_es_update_workspace(int32_t a, int32_t b, int32_t rank, i
     pair_range(0, n, &lo, &cnt);
     // tid_lo parity can add one pair; size for the larger count.
     const int32_t splits = use_rows_kernel(rank) ? rows_splits(a, b, cnt + 1) : es_splits(a, b, cnt + 1);
-    return (size_t)splits * a * b * sizeof(float);
+    return align_up16((size_t)splits * a * b * sizeof(float)) + 16;  // partials, then {S, 1/S}
 }
 
 extern "C" int hses_es_update(const float* d_f, int32_t n, int32_t tid_lo, uint64_t key,
@@ -395,7 +477,8 @@ extern "C" int hses_es_update(const float* d_f, int32_t n, int32_t tid_lo, uint6
     const bool empty = n == 0 || rank == 0 || sigma == 0.0f;
     const bool rows_k = use_rows_kernel(rank);
     P.splits = empty ? 1 : rows_k ? rows_splits(a, b, n_pairs) : es_splits(a, b, n_pairs);
-    const size_t need = (size_t)P.splits * a * b * sizeof(float);
+    const size_t part_bytes = align_up16((size_t)P.splits * a * b * sizeof(float));
+    const size_t need = part_bytes + 16;
     if (!empty) {
         HSES_REQUIRE(d_f, "fitness is NULL");
         HSES_REQUIRE(d_work && work_bytes >= need, "workspace too small");
@@ -426,12 +509,16 @@ extern "C" int hses_es_update(const float* d_f, int32_t n, int32_t tid_lo, uint6
     if (items > U_THREADS || (P.rc > 1 && rank > U_CW))
         return set_error(HSES_ERR_INTERNAL, "es_update tiling");
     P.work = static_cast<float*>(d_work);
+    float* d_scale = reinterpret_cast<float*>(static_cast<char*>(d_work) + part_bytes);
+    P.scale = d_scale;
     P.tables = st->d_tables;
     P.log_exc = st->d_log_exc;
     P.cos_exc = st->d_cos_exc;
     rc = get_jump_table(st, rank, (int64_t)a + b, &P.jump);
     if (rc) return rc;
     if (rows_k) {
+        hipLaunchKernelGGL(k_es_scale, dim3(1), dim3(1024), 0, s, P.f, n, P.bs, d_scale);
+        HSES_CHECK_HIP(hipGetLastError());
         // One launch per (a-tile, full / remainder b-tile) group.
         for (int32_t o0 = 0; o0 < a; o0 += 128) {
             const int32_t at = std::min(128, a - o0), btm = rows_bt_max(at);
@@ -441,7 +528,7 @@ extern "C" int hses_es_update(const float* d_f, int32_t n, int32_t tid_lo, uint6
                 if (cnt == 0) continue;
                 RowTiles G{at, bt, o0, g == 0 ? 0 : nfull * btm};
                 const int32_t threads = (at + bt + 63) / 64 * 64;
-                const size_t lds = align_up16(sizeof(BmTables)) + (size_t)2 * threads * U_PITCH * 4;
+                const size_t lds = align_up16(sizeof(BmTables)) + (size_t)2 * (at + bt + 1) * R_HP * 2;
                 const int32_t nw = threads / 64, nct = (bt + 15) / 16;
                 const int32_t ct = (nct + nw - 1) / nw;
                 auto launch = [&](auto kern) -> int {
@@ -469,7 +556,7 @@ extern "C" int hses_es_update(const float* d_f, int32_t n, int32_t tid_lo, uint6
     }
     const int64_t len = (int64_t)a * b;
     hipLaunchKernelGGL(k_es_reduce, dim3((uint32_t)((len + 255) / 256)), dim3(256), 0, s, P.work,
-                       P.splits, len, scale, accumulate, d_grad);
+                       P.splits, len, scale, rows_k ? d_scale + 1 : nullptr, accumulate, d_grad);
     HSES_CHECK_HIP(hipGetLastError());
     return HSES_OK;
 }

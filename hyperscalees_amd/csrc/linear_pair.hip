@@ -85,7 +85,8 @@ struct K2Args {
     float* rate;    // fused LIF: spike counts / T (M, a), or NULL
     int64_t rate_stride;
     int32_t a, b, r, R, rpm, T, n, tid_lo, pair_lo, n_pairs, epoch, nreuse;
-    int32_t segs;  // generation segments per stream row (jump table for row length r / segs)
+    int32_t segs;   // generation segments per stream row (jump table for row length r / segs)
+    int32_t group;  // pairs generated together (k_linear_pair; their A rows share the LDS block)
     float bs, leak, v_th;
 };
 
@@ -281,13 +282,14 @@ __global__ __launch_bounds__(K2_THREADS) void k_linear_pair(const K2Args P) {
     const int wr = wave >> 1, h = wave & 1;
     const int32_t r = P.r, a = P.a, b = P.b, kp = lay.kp, nkt = lay.words, R = P.R;
     const int32_t rp32 = (r + 31) & ~31;
-    uint16_t* slot = P.slots + (size_t)blockIdx.x * r * kp;
+    const int32_t G = P.group;
+    uint16_t* slots = P.slots + (size_t)blockIdx.x * G * r * kp;  // G slots of (r, kp)
 
     load_bm_tables(tabs, P.tables);
-    // generation never writes k >= b: zero the slot's padding once
-    for (int32_t i = tid; i < r * (kp - b); i += K2_THREADS) {
+    // generation never writes k >= b: zero the slots' padding once
+    for (int32_t i = tid; i < G * r * (kp - b); i += K2_THREADS) {
         const int32_t c = i / (kp - b), k = b + i % (kp - b);
-        slot[(size_t)c * kp + k] = 0;
+        slots[(size_t)c * kp + k] = 0;
     }
     __threadfence_block();
     __syncthreads();
@@ -298,42 +300,55 @@ __global__ __launch_bounds__(K2_THREADS) void k_linear_pair(const K2Args P) {
     // are staged as zeros (a select, so the loads stay unconditional).
     const int lcol = tid >> 1, lk = (tid & 1) * 32;
     const bool lvalid = lcol < K2_NMAX ? lcol < a : lcol - K2_NMAX < r;
-    const uint16_t* lsrc = lcol < K2_NMAX ? P.wbf + (size_t)min(lcol, a - 1) * kp + lk
-                                          : slot + (size_t)min(lcol - K2_NMAX, r - 1) * kp + lk;
+    const bool lw = lcol < K2_NMAX;
+    const size_t loff = (size_t)(lw ? min(lcol, a - 1) : min(lcol - K2_NMAX, r - 1)) * kp + lk;
     const uint32_t lmask = lvalid ? 0xffffffffu : 0u;
     uint16_t* ldst = WB + lcol * K2_TP + lk;
 
-    for (int32_t pi = blockIdx.x; pi < P.n_pairs; pi += gridDim.x) {
-        const int32_t pair = P.pair_lo + pi;
-        // Members of this pair inside the launch: m_lo .. m_hi (local indices).
-        const int32_t m_even = 2 * pair - P.tid_lo;
-        const int32_t m_lo = max(m_even, 0), m_hi = min(m_even + 1, P.n - 1);
-        const int64_t row_lo = (int64_t)m_lo * R, row_hi = (int64_t)(m_hi + 1) * R;
+    // The workgroup's pairs are blockIdx.x + i * gridDim.x; they are taken in
+    // groups of G whose factors are generated together (small layers: a + b
+    // stream rows of one pair leave most threads idle), pair g of a group
+    // using slot g and A rows [g * a, g * a + a) of the LDS block.
+    for (int32_t pi0 = blockIdx.x; pi0 < P.n_pairs; pi0 += G * (int32_t)gridDim.x) {
+        const int32_t gcnt = min(G, (P.n_pairs - pi0 + (int32_t)gridDim.x - 1) / (int32_t)gridDim.x);
 
         // ---- 1. factors: A rows -> LDS (bf16, [o][c]); B rows -> slot ([c][k]) ----
         {
-            int32_t te, tt;
-            float sg;
-            epoch_thread_sign(P.epoch, 2 * pair, P.nreuse, &te, &tt, &sg);
-            const uint64_t seed = noise_seed(P.key, te, tt);
-            // Work units: segment g of stream row j (P.segs segments of r / segs
-            // normals), so small layers keep every thread generating.
-            const int32_t segs = P.segs, sl = r / segs;
-            for (int32_t u = tid; u < (a + b) * segs; u += K2_THREADS) {
-                const int32_t j = u / segs, c0 = (u - j * segs) * sl;
-                uint64_t s = row_start_state(seed, u, P.jump);
+            __syncthreads();  // the previous group's blocks have finished with As and the slots
+            // Work units: segment of a stream row (P.segs segments of r / segs
+            // normals) of one pair of the group.
+            const int32_t segs = P.segs, sl = r / segs, upp = (a + b) * segs;
+            for (int32_t u = tid; u < gcnt * upp; u += K2_THREADS) {
+                const int32_t g = u / upp, uu = u - g * upp;
+                const int32_t j = uu / segs, c0 = (uu - j * segs) * sl;
+                int32_t te, tt;
+                float sg;
+                epoch_thread_sign(P.epoch, 2 * (P.pair_lo + pi0 + g * (int32_t)gridDim.x), P.nreuse,
+                                  &te, &tt, &sg);
+                uint64_t s = row_start_state(noise_seed(P.key, te, tt), uu, P.jump);
                 if (j < b) {
-                    bm_run(s, sl, ctx, [&](int32_t c, float v) { slot[(size_t)(c0 + c) * kp + j] = f2bf(v); });
+                    uint16_t* sg_ = slots + (size_t)g * r * kp;
+                    bm_run(s, sl, ctx, [&](int32_t c, float v) { sg_[(size_t)(c0 + c) * kp + j] = f2bf(v); });
                 } else {
-                    uint16_t* dst = As + (size_t)(j - b) * lay.apitch + c0;
-                    bm_run(s, sl, ctx, [&](int32_t c, float v) { dst[c] = f2bf(v * P.bs); });
+                    uint16_t* arow = As + (size_t)(g * a + j - b) * lay.apitch;
+                    bm_run(s, sl, ctx, [&](int32_t c, float v) { arow[c0 + c] = f2bf(v * P.bs); });
                     if (c0 + sl == r)
-                        for (int32_t c = r; c < rp32; ++c) As[(size_t)(j - b) * lay.apitch + c] = 0;
+                        for (int32_t c = r; c < rp32; ++c) arow[c] = 0;
                 }
             }
             __threadfence_block();
             __syncthreads();
         }
+
+    for (int32_t g = 0; g < gcnt; ++g) {
+        const int32_t pi = pi0 + g * (int32_t)gridDim.x;
+        const int32_t pair = P.pair_lo + pi;
+        // Members of this pair inside the launch: m_lo .. m_hi (local indices).
+        const int32_t m_even = 2 * pair - P.tid_lo;
+        const int32_t m_lo = max(m_even, 0), m_hi = min(m_even + 1, P.n - 1);
+        const int64_t row_lo = (int64_t)m_lo * R, row_hi = (int64_t)(m_hi + 1) * R;
+        const uint16_t* lsrc = (lw ? P.wbf : slots + (size_t)g * r * kp) + loff;
+        const uint16_t* Ag = As + (size_t)g * a * lay.apitch;
 
         // ---- 2./3. row blocks ----------------------------------------------------
         for (int64_t L0 = row_lo; L0 < row_hi; L0 += K2_RB) {
@@ -442,7 +457,7 @@ __global__ __launch_bounds__(K2_THREADS) void k_linear_pair(const K2Args P) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     if (h * 64 + j * 16 >= a) continue;
-                    const u16x8 af = lds_u16x8(&As[(h * 64 + j * 16 + li) * lay.apitch + c0 + kg * 8]);
+                    const u16x8 af = lds_u16x8(&Ag[(h * 64 + j * 16 + li) * lay.apitch + c0 + kg * 8]);
 #pragma unroll
                     for (int i = 0; i < 4; ++i) acc[i][j] = mfma_bf16(xf[i], af, acc[i][j]);
                 }
@@ -469,6 +484,7 @@ __global__ __launch_bounds__(K2_THREADS) void k_linear_pair(const K2Args P) {
             }
             __syncthreads();  // XBs aliases the tile buffers; Xbits is restaged
         }
+    }
     }
 }
 
@@ -873,15 +889,39 @@ static void pair_range(int32_t tid_lo, int32_t n, int32_t* lo, int32_t* cnt) {
     *cnt = (tid_lo + n - 1) / 2 - *lo + 1;
 }
 
-static size_t pair_workspace_bytes(int32_t grid, int32_t a, int32_t b, int32_t r) {
-    const size_t kp = (size_t)(b + 63) / 64 * 64;
-    return align16((size_t)a * kp * 2) + (size_t)grid * r * kp * 2;
+// Pairs whose factors k_linear_pair generates together: as many as the A block
+// of LDS (K2_NMAX rows) holds, at most 16.
+static int32_t pair_group(int32_t a) { return std::max(1, std::min(K2_NMAX / a, 16)); }
+
+// Segments per stream row for G pairs generated by `threads` threads: the
+// fewest normals per thread, counting ~12 normals' worth of work for each
+// segment's jump-ahead.
+static int32_t gen_segs(int32_t G, int32_t a, int32_t b, int32_t r, int32_t threads) {
+    int32_t best = 1;
+    int64_t best_cost = INT64_MAX;
+    for (int32_t segs = 1; segs <= 4; segs *= 2) {
+        if (r % (segs * 8)) break;
+        const int64_t units = (int64_t)G * (a + b) * segs;
+        const int64_t cost = (units + threads - 1) / threads * (r / segs + 12);
+        if (cost < best_cost) {
+            best_cost = cost;
+            best = segs;
+        }
+    }
+    return best;
 }
 
+static size_t pair_workspace_bytes(int32_t slots, int32_t a, int32_t b, int32_t r) {
+    const size_t kp = (size_t)(b + 63) / 64 * 64;
+    return align16((size_t)a * kp * 2) + (size_t)slots * r * kp * 2;
+}
+
+// Sized for k_linear_pair's grouped slots, which k_pair_bits (one slot per
+// workgroup) never exceeds.
 size_t linear_pair_workspace(const DeviceState* st, int32_t a, int32_t b, int32_t r, int32_t n) {
     int32_t lo, cnt;
     pair_range(0, n, &lo, &cnt);
-    return pair_workspace_bytes(pair_grid(st, cnt + 1), a, b, r);
+    return pair_workspace_bytes(pair_grid(st, cnt + 1) * pair_group(a), a, b, r);
 }
 
 int launch_linear_pair(LinParams& P, DeviceState* st, hipStream_t s, void* work, size_t work_bytes,
@@ -900,17 +940,16 @@ int launch_linear_pair(LinParams& P, DeviceState* st, hipStream_t s, void* work,
     K2Args A{};
     pair_range(P.tid_lo, P.n, &A.pair_lo, &A.n_pairs);
     const int32_t grid = pair_grid(st, A.n_pairs);
-    const size_t need = pair_workspace_bytes(grid, P.a, P.b, P.r);
+    A.group = v3 ? 1 : pair_group(P.a);
+    const size_t need = pair_workspace_bytes(grid * A.group, P.a, P.b, P.r);
     if (!work || work_bytes < need)
         return set_error(HSES_ERR_INVALID_ARG, "hses_perturbed_linear: workspace too small");
     uint16_t* wbf = static_cast<uint16_t*>(work);
     A.wbf = wbf;
     A.slots = reinterpret_cast<uint16_t*>(static_cast<char*>(work) + align16((size_t)P.a * lay.kp * 2));
     // Split each stream row into segs pieces (row length r / segs in the jump
-    // table) when a + b rows would leave threads idle.
-    A.segs = 1;
-    while (A.segs < 4 && (int64_t)(P.a + P.b) * A.segs * 2 <= threads && P.r % (A.segs * 8) == 0)
-        A.segs *= 2;
+    // table) when the group's a + b rows would leave threads idle.
+    A.segs = gen_segs(A.group, P.a, P.b, P.r, threads);
     int rc = get_jump_table(st, P.r / A.segs, ((int64_t)P.a + P.b) * A.segs, &P.jump);
     if (rc) return rc;
     A.x = P.x;
