@@ -55,8 +55,6 @@ struct BmTables {
     double cos_tlo[kCosTab + 1];
     DangerWin log_dw[kBuckets];
     DangerWin cos_dw[kBuckets];
-    float log_k0;              // glibc logf(1e-9f): the k1 == 0 case (u1 clamped)
-    float pad_[3];
 };
 
 HSES_HD uint32_t f2u(float f) {
@@ -99,18 +97,17 @@ HSES_HD double hfma_k(double a, double b, double c) {
 #endif
 }
 
-HSES_HD double hrint(double x) {
+HSES_HD float hfmax(float a, float b) {
 #if defined(__HIP_DEVICE_COMPILE__)
-    return __builtin_rint(x);
+    return __builtin_fmaxf(a, b);
 #else
-    return rint(x);
+    return fmaxf(a, b);
 #endif
 }
 
 // Constants shared by host and device.
 constexpr double kLn2Hi = 6.93147180369123816490e-01;  // 0x3FE62E42FEE00000, 32 significant bits
 constexpr double kLn2Lo = 1.90821492927058770002e-10;  // 0x3DEA39EF35793C76
-constexpr double kTwoPiInv64 = 10.185916357881301;     // 64 / (2 pi), rounded; only picks the grid point
 constexpr float kTauF = 6.28318530717958647692f;       // std::f32::consts::TAU
 
 // Polynomial coefficients (Taylor, rounded to double).  The degrees only set
@@ -128,13 +125,15 @@ constexpr double kL2 = -0.5, kL3 = 1.0 / 3.0;
 constexpr double kC2 = -0.5, kC4 = 1.0 / 24.0;
 constexpr double kS3 = -1.0 / 6.0, kS5 = 1.0 / 120.0;
 
-// The f32 argument of logf for unit index k1 (k1 == 0 is clamped to 1e-9f).
-HSES_HD float log_arg(uint32_t k1) { return k1 == 0 ? 1e-9f : (float)(int32_t)k1 * 0x1p-24f; }
+// The f32 argument of logf for unit index k1: max(k1 * 2^-24, 1e-9f)
+// (noiser.rs:474); only k1 == 0 is clamped, every other k1 * 2^-24 >= 2^-24.
+HSES_HD float log_arg(uint32_t k1) { return hfmax((float)(int32_t)k1 * 0x1p-24f, 1e-9f); }
 
 // The f32 angle TAU * (k2 * 2^-24) of noiser.rs:475-476.
 HSES_HD float cos_arg(uint32_t k2) { return kTauF * ((float)(int32_t)k2 * 0x1p-24f); }
 
-// f64 evaluation of log(x) for x = log_arg(k1), k1 >= 1 (x in [2^-24, 1)).
+// f64 evaluation of log(x) for x = log_arg(k1) (x in [1e-9, 1); any positive
+// normal f32 works).
 // x = 2^E * z with z in [0.75, 1.5); log x = E ln2 + logc + log1p(z*invc - 1).
 HSES_HD double log_f64(float x, const double* invc_tab, const double* logc_tab) {
     const uint32_t ix = f2u(x);
@@ -153,12 +152,15 @@ HSES_HD double log_f64(float x, const double* invc_tab, const double* logc_tab) 
     return hi + lo;
 }
 
-// f64 evaluation of cos(th) for th = TAU * k2 * 2^-24 (th in [0, 2pi)).
-// th = theta_j + t with theta_j = j * 2pi/64; cos th = c_j cos t - s_j sin t.
-HSES_HD double cos_f64(float th, const double* c_tab, const double* s_tab, const double* thi_tab,
-                       const double* tlo_tab) {
+// f64 evaluation of cos(th) for th = cos_arg(k2) = TAU * k2 * 2^-24 (th in
+// [0, 2pi)).  th = theta_j + t with theta_j = j * 2pi/64 and j = round(k2 /
+// 2^18), the grid point of the unrounded angle 2pi * k2 / 2^24 (th differs
+// from it by < 3e-8 relative, so |t| <= pi/64 * (1 + 4e-6));
+// cos th = c_j cos t - s_j sin t.
+HSES_HD double cos_f64(float th, uint32_t k2, const double* c_tab, const double* s_tab,
+                       const double* thi_tab, const double* tlo_tab) {
     const double x = (double)th;
-    const int j = (int)hrint(x * kTwoPiInv64);
+    const uint32_t j = (k2 + (1u << 17)) >> 18;
     const double t = (x - thi_tab[j]) - tlo_tab[j];
     const double t2 = t * t;
     const double pc = hfma_k(t2, kC4, kC2);

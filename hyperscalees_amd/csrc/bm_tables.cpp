@@ -65,8 +65,6 @@ void build_small(BmTables* t) {
         t->cos_c[j] = c;
         t->cos_s[j] = s;
     }
-    t->log_k0 = logf(1e-9f);
-    t->pad_[0] = t->pad_[1] = t->pad_[2] = 0.0f;
 }
 
 struct Exc {
@@ -81,13 +79,12 @@ void scan_slice(const BmTables* t, int kind, uint32_t k_lo, uint32_t k_hi, std::
         double y;
         float ref;
         if (kind == 0) {
-            if (k == 0) continue;  // clamped argument: handled by log_k0
-            const float x = log_arg(k);
+            const float x = log_arg(k);  // k == 0: the clamped 1e-9f
             y = log_f64(x, t->log_invc, t->log_logc);
             ref = logf(x);
         } else {
             const float th = cos_arg(k);
-            y = cos_f64(th, t->cos_c, t->cos_s, t->cos_thi, t->cos_tlo);
+            y = cos_f64(th, k, t->cos_c, t->cos_s, t->cos_thi, t->cos_tlo);
             ref = cosf(th);
         }
         const float f = (float)y;
@@ -151,7 +148,7 @@ std::string build_bm_tables(HostBmTables* out, int nthreads) {
             for (const Exc& x : by_bucket[b]) {
                 const double y = kind == 0
                                       ? log_f64(log_arg(x.k), out->small.log_invc, out->small.log_logc)
-                                      : cos_f64(cos_arg(x.k), out->small.cos_c, out->small.cos_s,
+                                      : cos_f64(cos_arg(x.k), x.k, out->small.cos_c, out->small.cos_s,
                                                 out->small.cos_thi, out->small.cos_tlo);
                 if (!in_danger(y, tw[b])) return "exception outside its danger window";
             }

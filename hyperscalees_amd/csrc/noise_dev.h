@@ -48,12 +48,12 @@ __device__ __forceinline__ float bm_logf(uint32_t k1, const BmTables& t, const u
     float f = (float)y;
     if (in_danger(y, t.log_dw[k1 >> 16]) && ((exc[k1 >> 5] >> (k1 & 31)) & 1u))
         f = other_candidate(f, rem29(y));
-    return k1 == 0 ? t.log_k0 : f;
+    return f;
 }
 
 // glibc cosf(TAU * k2 * 2^-24), bit-exact (single value).
 __device__ __forceinline__ float bm_cosf(uint32_t k2, const BmTables& t, const uint32_t* exc) {
-    const double y = cos_f64(cos_arg(k2), t.cos_c, t.cos_s, t.cos_thi, t.cos_tlo);
+    const double y = cos_f64(cos_arg(k2), k2, t.cos_c, t.cos_s, t.cos_thi, t.cos_tlo);
     float f = (float)y;
     if (in_danger(y, t.cos_dw[k2 >> 16]) && ((exc[k2 >> 5] >> (k2 & 31)) & 1u))
         f = other_candidate(f, rem29(y));
@@ -103,7 +103,7 @@ __device__ __forceinline__ void bm_stage1(uint64_t& s, BmPending<G>& p, const No
 #pragma unroll
     for (int i = 0; i < G; ++i) {
         const double yl = log_f64(log_arg(p.k1[i]), t.log_invc, t.log_logc);
-        const double yc = cos_f64(cos_arg(p.k2[i]), t.cos_c, t.cos_s, t.cos_thi, t.cos_tlo);
+        const double yc = cos_f64(cos_arg(p.k2[i]), p.k2[i], t.cos_c, t.cos_s, t.cos_thi, t.cos_tlo);
         p.fl[i] = (float)yl;
         p.fc[i] = (float)yc;
         p.rl[i] = rem29(yl);
@@ -137,8 +137,7 @@ __device__ __forceinline__ void bm_stage2(const BmPending<G>& p, float* out, con
         float fl = p.fl[i], fc = p.fc[i];
         if ((p.wl[i] >> (p.k1[i] & 31)) & 1u) fl = other_candidate(fl, p.rl[i]);
         if ((p.wc[i] >> (p.k2[i] & 31)) & 1u) fc = other_candidate(fc, p.rc[i]);
-        const float L = p.k1[i] == 0 ? t.log_k0 : fl;
-        out[i] = sqrt_rn(-2.0f * L) * fc;
+        out[i] = sqrt_rn(-2.0f * fl) * fc;
     }
 }
 
