@@ -37,6 +37,9 @@ constexpr int kCosTab = 64;           // angle grid j * 2pi / 64, j = 0..64
 constexpr int kBuckets = 256;         // danger-threshold buckets: k >> 16
 constexpr uint32_t kUnitCount = 1u << 24;
 constexpr uint32_t kBitmapWords = kUnitCount / 32;
+// Bitmaps are stored with 64 zero words appended: lanes without a danger test
+// read word kBitmapWords, so their loaded bits need no masking.
+constexpr uint32_t kBitmapAlloc = kBitmapWords + 64;
 
 // Danger window of one bucket: rem29(y) in [2^28 - t, 2^28 + t) for a
 // half-width t (units of 2^-29 f32 ulp), stored as lo = 2^28 - t and w = 2t so

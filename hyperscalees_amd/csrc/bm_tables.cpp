@@ -114,8 +114,8 @@ uint32_t bucket_t(const std::vector<Exc>& exc_in_bucket) {
 
 std::string build_bm_tables(HostBmTables* out, int nthreads) {
     build_small(&out->small);
-    out->log_exc.assign(kBitmapWords, 0u);
-    out->cos_exc.assign(kBitmapWords, 0u);
+    out->log_exc.assign(kBitmapAlloc, 0u);
+    out->cos_exc.assign(kBitmapAlloc, 0u);
     if (nthreads < 1) nthreads = 1;
     for (int kind = 0; kind < 2; ++kind) {
         std::vector<std::vector<Exc>> parts(nthreads);

@@ -304,6 +304,7 @@ __global__ __launch_bounds__(R_MAXT) void k_es_rows(UpdParams P, RowTiles G) {
     auto gen4 = [&](uint16_t* dst, int32_t c, int32_t cnt, float w) {
         const BmPending<4> cur = pend;
         bm_stage1<4, true>(st, pend, ctx);
+        __builtin_amdgcn_sched_barrier(0);  // next batch's loads before this batch's use
         float v[4];
         bm_stage2<4>(cur, v, ctx);
         float x[4];

@@ -112,13 +112,14 @@ __device__ __forceinline__ void bm_stage1(uint64_t& s, BmPending<G>& p, const No
         dc[i] = in_danger_r(p.rc[i], t.cos_dw[p.k2[i] >> 16]);
     }
     if constexpr (PIPE) {
-        // Every lane loads (lanes out of danger read word 0, one shared cache
-        // line): no branch, so the wait before stage 2 counts exactly the
-        // loads still in flight from the batch issued after this one.
+        // Every lane loads (lanes out of danger read the zero word past the
+        // bitmap, one shared cache line): no branch and no use of the loaded
+        // words before stage 2, so the wait there counts exactly the loads
+        // still in flight from the batch issued after this one.
 #pragma unroll
         for (int i = 0; i < G; ++i) {
-            p.wl[i] = c.log_exc[dl[i] ? p.k1[i] >> 5 : 0u] & (dl[i] ? ~0u : 0u);
-            p.wc[i] = c.cos_exc[dc[i] ? p.k2[i] >> 5 : 0u] & (dc[i] ? ~0u : 0u);
+            p.wl[i] = c.log_exc[dl[i] ? p.k1[i] >> 5 : kBitmapWords];
+            p.wc[i] = c.cos_exc[dc[i] ? p.k2[i] >> 5 : kBitmapWords];
         }
     } else {
 #pragma unroll

@@ -55,14 +55,14 @@ static int init_device_locked(int dev, DeviceState** out) {
     st->num_cus = prop.multiProcessorCount;
     st->max_lds = prop.sharedMemPerBlock;
     HSES_CHECK_HIP(hipMalloc(&st->d_tables, sizeof(BmTables)));
-    HSES_CHECK_HIP(hipMalloc(&st->d_log_exc, sizeof(uint32_t) * kBitmapWords));
-    HSES_CHECK_HIP(hipMalloc(&st->d_cos_exc, sizeof(uint32_t) * kBitmapWords));
+    HSES_CHECK_HIP(hipMalloc(&st->d_log_exc, sizeof(uint32_t) * kBitmapAlloc));
+    HSES_CHECK_HIP(hipMalloc(&st->d_cos_exc, sizeof(uint32_t) * kBitmapAlloc));
     HSES_CHECK_HIP(hipMemcpy(st->d_tables, &g_host_tables->small, sizeof(BmTables),
                              hipMemcpyHostToDevice));
     HSES_CHECK_HIP(hipMemcpy(st->d_log_exc, g_host_tables->log_exc.data(),
-                             sizeof(uint32_t) * kBitmapWords, hipMemcpyHostToDevice));
+                             sizeof(uint32_t) * kBitmapAlloc, hipMemcpyHostToDevice));
     HSES_CHECK_HIP(hipMemcpy(st->d_cos_exc, g_host_tables->cos_exc.data(),
-                             sizeof(uint32_t) * kBitmapWords, hipMemcpyHostToDevice));
+                             sizeof(uint32_t) * kBitmapAlloc, hipMemcpyHostToDevice));
     if (cur != dev) HSES_CHECK_HIP(hipSetDevice(cur));
     g_states[dev] = st;
     *out = st;

@@ -28,7 +28,7 @@ int check_hip(hipError_t e, const char* what);
 // Host-side construction of the Box-Muller tables (bm_tables.cpp).
 struct HostBmTables {
     BmTables small;
-    std::vector<uint32_t> log_exc;  // kBitmapWords
+    std::vector<uint32_t> log_exc;  // kBitmapAlloc words (zero past kBitmapWords)
     std::vector<uint32_t> cos_exc;
     uint32_t n_log_exc = 0, n_cos_exc = 0;
     uint32_t n_log_danger = 0, n_cos_danger = 0;
