@@ -28,7 +28,7 @@ PEAK_HBM_GBPS = 8000.0
 # HBM bytes per fc1 launch from two rocprofv3 PMC runs (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0,
 # factors from a 1 GiB copy) of `python3 -m hyperscalees_amd.profile_fc1`;
 # see profiles/fc1_c3_traffic.md.  Refreshed whenever the kernel changes.
-FC1_TRAFFIC_BYTES = 9.29e9
+FC1_TRAFFIC_BYTES = 9.35e9
 
 
 def layer_flops(cfg, l):
@@ -193,7 +193,7 @@ def main():
                      "readout_fitness": round(float(t_readout), 3),
                      "forward": round(float(t_fwd), 3), "es_update": round(float(t_upd), 3)},
         "fwd_tflops": round(fwd_flops / (t_fwd * 1e-3) / 1e12, 1),
-        "roofline": {"kernel": ("k_linear_pair (fc1: x[W^T|B] + (xB)A^T, T=16 x 524288 rows"
+        "roofline": {"kernel": ("k_pair_bits (fc1: x[W^T|B] + (xB)A^T, T=16 x 524288 rows"
                                 + (", LIF fused)" if es.fused else ")")),
                      "bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
