@@ -6,13 +6,19 @@
 namespace hses {
 
 // snn_mnist.rs:180-201 (Loglik) per row, averaged over the member's rows.
-__global__ void k_member_loglik(const float* __restrict__ logits, int32_t classes,
-                                const int32_t* __restrict__ labels, int32_t n, int32_t rpm,
-                                float* __restrict__ fit) {
-    const int32_t m = blockIdx.x * blockDim.x + threadIdx.x;
-    if (m >= n) return;
+// One wave per member, lane s taking rows s, s + 64, ...; the row values are
+// summed in double (exact for these magnitudes, so the tree order of the
+// cross-lane sum does not change the result).
+__global__ __launch_bounds__(256) void k_member_loglik(const float* __restrict__ logits,
+                                                       int32_t classes,
+                                                       const int32_t* __restrict__ labels,
+                                                       int32_t n, int32_t rpm,
+                                                       float* __restrict__ fit) {
+    const int32_t m = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int32_t lane = threadIdx.x & 63;
+    if (m >= n) return;  // whole wave
     double acc = 0.0;
-    for (int32_t s = 0; s < rpm; ++s) {
+    for (int32_t s = lane; s < rpm; s += 64) {
         const int64_t row = (int64_t)m * rpm + s;
         const float* x = logits + row * classes;
         float mx = x[0];
@@ -23,7 +29,9 @@ __global__ void k_member_loglik(const float* __restrict__ logits, int32_t classe
         lab = lab < 0 ? 0 : (lab >= classes ? classes - 1 : lab);
         acc += (double)__fsub_rn(__fsub_rn(x[lab], mx), logf(sum));
     }
-    fit[m] = (float)(acc / rpm);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+    if (lane == 0) fit[m] = (float)(acc / rpm);
 }
 
 // eggroll.rs:967-992: mean and E[x^2] over all n (double partial sums with a
@@ -108,7 +116,7 @@ extern "C" int hses_member_loglik(const float* d_logits, int32_t classes, const 
     HSES_REQUIRE(n >= 0 && classes >= 1 && rows_per_member >= 1, "bad sizes");
     if (n == 0) return HSES_OK;
     HSES_REQUIRE(d_logits && d_labels && d_fit, "NULL pointer");
-    hipLaunchKernelGGL(k_member_loglik, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream,
+    hipLaunchKernelGGL(k_member_loglik, dim3((n + 3) / 4), dim3(256), 0, (hipStream_t)stream,
                        d_logits, classes, d_labels, n, rows_per_member, d_fit);
     HSES_CHECK_HIP(hipGetLastError());
     return HSES_OK;

@@ -104,6 +104,116 @@ __global__ __launch_bounds__(64 * P_ROWS_PER_BLOCK) void k_poisson_bits(
     }
 }
 
+// Bit-packed Poisson for rows with many p == 0 elements (the SNN input: 70%
+// exact zeros).  One wave per row, in three phases over LDS:
+//   A. classify: K(p) = 0 never fires, K = 2^23 always fires (pattern of all
+//      ones), anything else parks its K in pat[col] and appends col to the
+//      row's active list (a ballot and a lane prefix count compact it);
+//   B. the active elements only run the xorshift32 stream (T steps each),
+//      replacing K in pat[col] with the element's T-bit time pattern;
+//   C. spike words: 64 / T consecutive words' patterns form a 64 x 64 bit
+//      matrix (lane = element of the word, bit = (word, t)); its transpose,
+//      six lane-exchange stages, leaves lane (wi, t) holding word wi of time
+//      step t, which it stores.
+// Only the zero and saturated elements skip their stream; every stream that
+// runs is the one of k_poisson_bits (poisson_encode_fused_oxide.rs:61-106).
+template <int T>
+__global__ __launch_bounds__(256) void k_poisson_sparse(
+    const float* __restrict__ p, int64_t p_rows, const int32_t* __restrict__ prow, int64_t rows,
+    int32_t in_dim, int64_t p_stride, uint32_t mix, uint64_t* __restrict__ out, int64_t out_stride) {
+    static_assert(T >= 1 && T <= 32 && (T & (T - 1)) == 0, "T must be a power of two <= 32");
+    constexpr int WPT = 64 / T;  // words per 64 x 64 transpose
+    extern __shared__ __align__(16) unsigned char psm[];
+    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int32_t words = (in_dim + 63) >> 6;
+    uint32_t* pat = reinterpret_cast<uint32_t*>(psm) + (size_t)wv * (words * 96);
+    uint16_t* list = reinterpret_cast<uint16_t*>(pat + words * 64);
+    const int64_t row = (int64_t)blockIdx.x * 4 + wv;
+    if (row >= rows) return;  // whole wave exits together
+    const int64_t src = prow ? (int64_t)prow[row] : row;
+    const bool src_ok = src >= 0 && src < p_rows;
+    const float* prow_p = p + (src_ok ? src : 0) * p_stride;
+    const uint32_t idx0 = (uint32_t)(row * in_dim);
+    constexpr uint32_t ALL = T == 32 ? 0xffffffffu : ((1u << T) - 1u);
+
+    // A. classify and compact; a batch of PB words' loads is in flight at once
+    constexpr int PB = 16;
+    int32_t cnt = 0;
+    for (int32_t w0 = 0; w0 < words; w0 += PB) {
+        float pv[PB];
+#pragma unroll
+        for (int i = 0; i < PB; ++i) {
+            const int32_t col = (w0 + i) * 64 + lane;
+            pv[i] = (src_ok && col < in_dim) ? prow_p[col] : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < PB; ++i) {
+            if (w0 + i >= words) break;
+            const int32_t col = (w0 + i) * 64 + lane;
+            const uint32_t K = col < in_dim ? poisson_threshold(pv[i]) : 0u;
+            const bool full = K >= 8388608u, act = K != 0u && !full;
+            pat[col] = full ? ALL : K;
+            const uint64_t am = __ballot(act);
+            if (act) {
+                const int32_t pos = cnt + (int32_t)__builtin_amdgcn_mbcnt_hi(
+                                              (uint32_t)(am >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)am, 0u));
+                list[pos] = (uint16_t)col;
+            }
+            cnt += (int32_t)__popcll(am);
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // B. the streams of the active elements
+    for (int32_t e = lane; e < cnt; e += 64) {
+        const uint32_t col = list[e], K = pat[col];
+        uint32_t x = 1000000007u * (idx0 + col) + mix + 0x9E3779B9u;
+        uint32_t pt = 0;
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            x ^= x << 13;
+            x ^= x >> 17;
+            x ^= x << 5;
+            pt |= ((x >> 9) < K ? 1u : 0u) << t;
+        }
+        pat[col] = pt;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // C. transpose and store
+    const int64_t plane = rows * out_stride;
+    for (int32_t w0 = 0; w0 < words; w0 += WPT) {
+        uint64_t x = 0;
+#pragma unroll
+        for (int wi = 0; wi < WPT; ++wi)
+            if (w0 + wi < words) x |= (uint64_t)pat[(w0 + wi) * 64 + lane] << (wi * T);
+        // block swap at distance d: lane r (bit d clear) takes the partner's
+        // columns c with bit d clear into c | d; the partner the mirror image
+#pragma unroll
+        for (int d = 32; d >= 1; d >>= 1) {
+            const uint64_t m0 = d == 32 ? 0x00000000ffffffffull
+                              : d == 16 ? 0x0000ffff0000ffffull
+                              : d == 8  ? 0x00ff00ff00ff00ffull
+                              : d == 4  ? 0x0f0f0f0f0f0f0f0full
+                              : d == 2  ? 0x3333333333333333ull
+                                        : 0x5555555555555555ull;
+            const uint64_t y = __shfl_xor(x, d);
+            x = (lane & d) ? ((x & ~m0) | ((y & ~m0) >> d)) : ((x & m0) | ((y & m0) << d));
+        }
+        const int32_t wi = lane / T, t = lane % T;
+        if (w0 + wi < words) out[(int64_t)t * plane + row * out_stride + w0 + wi] = x;
+    }
+}
+
+static size_t poisson_sparse_lds(int32_t in_dim) {
+    const size_t words = (size_t)(in_dim + 63) / 64;
+    return 4 * words * 96 * 4;  // 4 waves, each a u32 pattern and a u16 list entry per element
+}
+
 template <int FMT>
 __global__ __launch_bounds__(256) void k_lif(const float* __restrict__ cur,
                                              const float* __restrict__ v0, int32_t T, int64_t rows,
@@ -225,7 +335,26 @@ extern "C" int hses_poisson_encode(const float* d_p, int64_t p_rows, const int32
                                rows, in_dim, p_stride, T, mix, d_out, out_stride);
             break;
         default:
-            if (T <= 64) {
+            if (T <= 32 && (T & (T - 1)) == 0 && in_dim <= 2048) {
+                // zero-skipping kernel: T a power of two, 24 B of LDS per element (48 KiB at 2048)
+                const dim3 g((uint32_t)((rows + 3) / 4)), b(256);
+                uint64_t* o = static_cast<uint64_t*>(d_out);
+                const size_t lds = poisson_sparse_lds(in_dim);
+#define HSES_PSPARSE(TV)                                                                        \
+    case TV:                                                                                    \
+        hipLaunchKernelGGL(k_poisson_sparse<TV>, g, b, lds, s, d_p, p_rows, d_rows, rows, in_dim, \
+                           p_stride, mix, o, out_stride);                                       \
+        break;
+                switch (T) {
+                    HSES_PSPARSE(1)
+                    HSES_PSPARSE(2)
+                    HSES_PSPARSE(4)
+                    HSES_PSPARSE(8)
+                    HSES_PSPARSE(16)
+                    HSES_PSPARSE(32)
+                }
+#undef HSES_PSPARSE
+            } else if (T <= 64) {
                 const dim3 g((uint32_t)((rows + P_ROWS_PER_BLOCK - 1) / P_ROWS_PER_BLOCK));
                 const dim3 b(64 * P_ROWS_PER_BLOCK);
                 uint64_t* o = static_cast<uint64_t*>(d_out);

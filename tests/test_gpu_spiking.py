@@ -41,6 +41,31 @@ def test_poisson_bit_exact_all_formats(hses_gpu, rows, d, T):
     np.testing.assert_array_equal(unpack_bits(bits, d), ref)
 
 
+@pytest.mark.parametrize("rows,d,T,zero_frac", [
+    (9, 130, 1, 0.7), (6, 200, 2, 0.7), (11, 257, 4, 0.5), (7, 300, 32, 0.7),
+    (5, 2048, 16, 0.7), (3, 2049, 16, 0.7),   # largest zero-skipping row, first fallback row
+    (13, 784, 8, 0.0), (13, 784, 16, 1.0),     # every element active; every element zero
+])
+def test_poisson_bits_zero_skip(hses_gpu, rows, d, T, zero_frac):
+    # Bit-packed rows: zero-skipping kernel for power-of-two T (rows of all
+    # ones and all zeros included), streamed kernel beyond its row width.
+    rng = np.random.default_rng(rows * 13 + d + T)
+    p = sparse_intensities(rng, rows, d, zero_frac)
+    p[1, :] = 1.0
+    p[2, ::3] = 0.0
+    seeds = (5, 6, 7, 8)
+    ref = O.poisson(p, T, seeds)
+    bits = hses_gpu.poisson_encode(torch.from_numpy(p).cuda(), T, seeds, FMT_BITS)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(unpack_bits(bits, d), ref)
+    # gathered rows: output row i encodes p[idx[i]] seeded by its own flat index
+    idx = rng.integers(0, rows, 2 * rows).astype(np.int32)
+    got = hses_gpu.poisson_encode(torch.from_numpy(p).cuda(), T, seeds, FMT_BITS,
+                                  rows_index=torch.from_numpy(idx).cuda())
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(unpack_bits(got, d), O.poisson(p[idx], T, seeds))
+
+
 def test_poisson_threshold_dense_p_sweep(hses_gpu):
     # Every representable neighbourhood of many thresholds: p on a fine grid
     # plus its f32 neighbours, checked against the f32-division formula.
@@ -82,9 +107,10 @@ def test_lif_zero_v0_default(hses_gpu):
     np.testing.assert_array_equal(s.cpu().numpy(), ref_s)
 
 
-def test_member_loglik(hses_gpu):
-    rng = np.random.default_rng(5)
-    n, rpm, c = 40, 16, 10
+@pytest.mark.parametrize("n,rpm", [(40, 16), (9, 200), (5, 1), (6, 64)])
+def test_member_loglik(hses_gpu, n, rpm):
+    rng = np.random.default_rng(5 + rpm)
+    c = 10
     logits = (rng.standard_normal((n * rpm, c)) * 3).astype(np.float32)
     labels = rng.integers(0, c, n * rpm).astype(np.int32)
     ref = O.loglik(logits, labels).reshape(n, rpm).astype(np.float64).mean(1)
