@@ -13,6 +13,7 @@ HSES_OK, HSES_ERR_INVALID_ARG, HSES_ERR_UNSUPPORTED, HSES_ERR_HIP, HSES_ERR_INTE
 FMT_F32, FMT_BF16, FMT_U8, FMT_BITS = range(4)
 MATH_F32, MATH_BF16 = range(2)
 SGD, ADAM, ADAMW = range(3)
+REWARD_LOGLIK, REWARD_BINARY = range(2)
 
 c_i32, c_i64, c_u32, c_u64 = ctypes.c_int32, ctypes.c_int64, ctypes.c_uint32, ctypes.c_uint64
 c_f32, c_vp, c_size = ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t
@@ -48,6 +49,10 @@ PROTOTYPES = {
     "hses_es_update": (ctypes.c_int, [c_vp, c_i32, c_i32, c_u64, c_i32, c_f32, c_i32, c_i32,
                                       c_i32, c_i32, c_f32, c_i32, c_vp, c_vp, c_size, c_vp]),
     "hses_member_loglik": (ctypes.c_int, [c_vp, c_i32, c_vp, c_i32, c_i32, c_vp, c_vp]),
+    "hses_member_fitness": (ctypes.c_int, [c_vp, c_i32, c_vp, c_i32, c_i32, c_i32, c_vp, c_vp,
+                                           c_vp]),
+    "hses_fitness_moments": (ctypes.c_int, [c_vp, c_i32, c_vp, c_i32, c_vp]),
+    "hses_combine_affine": (ctypes.c_int, [c_vp, c_vp, c_vp, c_i32, c_i64, c_vp, c_vp]),
     "hses_convert_fitnesses": (ctypes.c_int, [c_vp, c_i32, c_i32, c_vp, c_vp, c_vp]),
     "hses_solver_step": (ctypes.c_int, [c_i32, c_f32, c_f32, c_f32, c_f32, c_f32, c_i32, c_vp,
                                         c_vp, c_vp, c_vp, c_i64, c_vp]),

@@ -1,52 +1,76 @@
-// small.hip -- fitness, fitness normalisation and the optimizer step.
+// small.hip -- fitness, fitness normalisation, the K-chunk affine combination and
+// the optimizer step.
 #include <math.h>
 
 #include "runtime.h"
 
 namespace hses {
 
-// snn_mnist.rs:180-201 (Loglik) per row, averaged over the member's rows.
+// snn_mnist.rs:180-201 per row, averaged over the member's rows.  Loglik:
+// log_softmax(row)[label]; Binary: 1 when the first maximal class is the label.
 // One wave per member, lane s taking rows s, s + 64, ...; the row values are
 // summed in double (exact for these magnitudes, so the tree order of the
-// cross-lane sum does not change the result).
-__global__ __launch_bounds__(256) void k_member_loglik(const float* __restrict__ logits,
-                                                       int32_t classes,
-                                                       const int32_t* __restrict__ labels,
-                                                       int32_t n, int32_t rpm,
-                                                       float* __restrict__ fit) {
+// cross-lane sum does not change the result).  `correct` (optional) counts
+// the rows whose first maximal class is the label.
+__global__ __launch_bounds__(256) void k_member_fitness(const float* __restrict__ logits,
+                                                        int32_t classes,
+                                                        const int32_t* __restrict__ labels,
+                                                        int32_t n, int32_t rpm, int32_t reward,
+                                                        float* __restrict__ fit,
+                                                        unsigned long long* __restrict__ correct) {
+    __shared__ uint32_t block_hits[4];
     const int32_t m = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int32_t lane = threadIdx.x & 63;
-    if (m >= n) return;  // whole wave
     double acc = 0.0;
-    for (int32_t s = lane; s < rpm; s += 64) {
+    uint32_t hits = 0;
+    for (int32_t s = lane; m < n && s < rpm; s += 64) {
         const int64_t row = (int64_t)m * rpm + s;
         const float* x = logits + row * classes;
+        const int32_t label = labels[row];
         float mx = x[0];
-        for (int32_t c = 1; c < classes; ++c) mx = fmaxf(mx, x[c]);
-        float sum = 0.0f;
-        for (int32_t c = 0; c < classes; ++c) sum = __fadd_rn(sum, expf(__fsub_rn(x[c], mx)));
-        int32_t lab = labels[row];
-        lab = lab < 0 ? 0 : (lab >= classes ? classes - 1 : lab);
-        acc += (double)__fsub_rn(__fsub_rn(x[lab], mx), logf(sum));
+        int32_t am = 0;
+        for (int32_t c = 1; c < classes; ++c)
+            if (x[c] > mx) {
+                mx = x[c];
+                am = c;
+            }
+        hits += am == label ? 1u : 0u;
+        if (reward == HSES_REWARD_BINARY) {
+            acc += am == label ? 1.0 : 0.0;
+        } else {
+            float sum = 0.0f;
+            for (int32_t c = 0; c < classes; ++c) sum = __fadd_rn(sum, expf(__fsub_rn(x[c], mx)));
+            const int32_t lab = label < 0 ? 0 : (label >= classes ? classes - 1 : label);
+            acc += (double)__fsub_rn(__fsub_rn(x[lab], mx), logf(sum));
+        }
     }
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
-    if (lane == 0) fit[m] = (float)(acc / rpm);
+    for (int off = 32; off > 0; off >>= 1) {
+        acc += __shfl_xor(acc, off);
+        hits += __shfl_xor(hits, off);
+    }
+    if (lane == 0) {
+        if (m < n) fit[m] = (float)(acc / rpm);
+        block_hits[threadIdx.x >> 6] = hits;
+    }
+    if (!correct) return;  // uniform over the block
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t h = block_hits[0] + block_hits[1] + block_hits[2] + block_hits[3];
+        if (h) atomicAdd(correct, (unsigned long long)h);
+    }
 }
 
-// eggroll.rs:967-992: mean and E[x^2] over all n (double partial sums with a
-// fixed-order tree, one block), std = sqrt(var + 1e-5), out = (raw-mean)/std
-// or per-group centring with the global std.
-__global__ __launch_bounds__(1024) void k_convert_fitnesses(const float* __restrict__ raw,
-                                                           int32_t n, int32_t group,
-                                                           float* __restrict__ out,
-                                                           float* __restrict__ stats) {
-    __shared__ double s1[1024], s2[1024];
+// Sum and sum of squares (in double) of v[0..n) over one 1024-thread block,
+// a fixed-order tree, so the result is deterministic.  Every thread returns
+// the totals.
+__device__ void block_moments(const float* __restrict__ v, int32_t n, double* s1, double* s2,
+                              double& a_out, double& b_out) {
     double a = 0.0, b = 0.0;
     for (int32_t i = threadIdx.x; i < n; i += blockDim.x) {
-        const float v = raw[i];
-        a += (double)v;
-        b += (double)__fmul_rn(v, v);
+        const float x = v[i];
+        a += (double)x;
+        b += (double)__fmul_rn(x, x);
     }
     s1[threadIdx.x] = a;
     s2[threadIdx.x] = b;
@@ -58,8 +82,22 @@ __global__ __launch_bounds__(1024) void k_convert_fitnesses(const float* __restr
         }
         __syncthreads();
     }
-    const float mean = (float)(s1[0] / n);
-    const float msq = (float)(s2[0] / n);
+    a_out = s1[0];
+    b_out = s2[0];
+}
+
+// eggroll.rs:967-992: mean and E[x^2] over all n (double partial sums with a
+// fixed-order tree, one block), std = sqrt(var + 1e-5), out = (raw-mean)/std
+// or per-group centring with the global std.
+__global__ __launch_bounds__(1024) void k_convert_fitnesses(const float* __restrict__ raw,
+                                                           int32_t n, int32_t group,
+                                                           float* __restrict__ out,
+                                                           float* __restrict__ stats) {
+    __shared__ double s1[1024], s2[1024];
+    double t1, t2;
+    block_moments(raw, n, s1, s2, t1, t2);
+    const float mean = (float)(t1 / n);
+    const float msq = (float)(t2 / n);
     const float var = __fsub_rn(msq, __fmul_rn(mean, mean));
     const float sd = __fsqrt_rn(__fadd_rn(var, 1e-5f));
     const float inv = __fdiv_rn(1.0f, sd);
@@ -80,6 +118,37 @@ __global__ __launch_bounds__(1024) void k_convert_fitnesses(const float* __restr
                 out[gi * group + j] = __fmul_rn(__fsub_rn(raw[gi * group + j], gm), inv);
         }
     }
+}
+
+// accumulate_train.rs:843-846: the raw-fitness sums of one chunk added to
+// (or, first chunk, written into) moments = {sum raw, sum raw^2}.
+__global__ __launch_bounds__(1024) void k_fitness_moments(const float* __restrict__ raw, int32_t n,
+                                                         double* __restrict__ moments,
+                                                         int32_t accumulate) {
+    __shared__ double s1[1024], s2[1024];
+    double t1, t2;
+    block_moments(raw, n, s1, s2, t1, t2);
+    if (threadIdx.x == 0) {
+        moments[0] = accumulate ? moments[0] + t1 : t1;
+        moments[1] = accumulate ? moments[1] + t2 : t2;
+    }
+}
+
+// combine_affine_grads (eggroll.rs:902-915) with the driver's mean and std
+// (accumulate_train.rs:940-944) taken from the device moments:
+// out = (g - o*mean) * (-1 / (std * sqrt(batch))).
+__global__ void k_combine_affine(const float* __restrict__ g, const float* __restrict__ o,
+                                 const double* __restrict__ moments, int32_t batch, int64_t len,
+                                 float* __restrict__ out) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= len) return;
+    const float fb = (float)batch;
+    const float mean = __fdiv_rn((float)moments[0], fb);
+    const float var = fmaxf(__fsub_rn(__fdiv_rn((float)moments[1], fb), __fmul_rn(mean, mean)), 0.0f);
+    const float sd = __fsqrt_rn(__fadd_rn(var, 1e-5f));
+    const float scale = __fdiv_rn(-1.0f, __fmul_rn(sd, __fsqrt_rn(fb)));
+    const float gv = g[e];
+    out[e] = __fmul_rn(o ? __fsub_rn(gv, __fmul_rn(o[e], mean)) : gv, scale);
 }
 
 // noiser.rs:155-225.  kind 0: p - g*lr.  Adam/AdamW: moments, bias correction
@@ -111,13 +180,46 @@ __global__ void k_solver(int32_t kind, float lr, float b1, float omb1, float b2,
 
 using namespace hses;
 
-extern "C" int hses_member_loglik(const float* d_logits, int32_t classes, const int32_t* d_labels,
-                                  int32_t n, int32_t rows_per_member, float* d_fit, void* stream) {
+extern "C" int hses_member_fitness(const float* d_logits, int32_t classes, const int32_t* d_labels,
+                                   int32_t n, int32_t rows_per_member, int32_t reward, float* d_fit,
+                                   unsigned long long* d_correct, void* stream) {
     HSES_REQUIRE(n >= 0 && classes >= 1 && rows_per_member >= 1, "bad sizes");
+    HSES_REQUIRE(reward == HSES_REWARD_LOGLIK || reward == HSES_REWARD_BINARY, "unknown reward");
     if (n == 0) return HSES_OK;
     HSES_REQUIRE(d_logits && d_labels && d_fit, "NULL pointer");
-    hipLaunchKernelGGL(k_member_loglik, dim3((n + 3) / 4), dim3(256), 0, (hipStream_t)stream,
-                       d_logits, classes, d_labels, n, rows_per_member, d_fit);
+    hipLaunchKernelGGL(k_member_fitness, dim3((n + 3) / 4), dim3(256), 0, (hipStream_t)stream,
+                       d_logits, classes, d_labels, n, rows_per_member, reward, d_fit, d_correct);
+    HSES_CHECK_HIP(hipGetLastError());
+    return HSES_OK;
+}
+
+extern "C" int hses_member_loglik(const float* d_logits, int32_t classes, const int32_t* d_labels,
+                                  int32_t n, int32_t rows_per_member, float* d_fit, void* stream) {
+    return hses_member_fitness(d_logits, classes, d_labels, n, rows_per_member, HSES_REWARD_LOGLIK,
+                               d_fit, nullptr, stream);
+}
+
+extern "C" int hses_fitness_moments(const float* d_raw, int32_t n, double* d_moments,
+                                    int32_t accumulate, void* stream) {
+    HSES_REQUIRE(n >= 0, "negative n");
+    HSES_REQUIRE(d_moments && (n == 0 || d_raw), "NULL pointer");
+    hipLaunchKernelGGL(k_fitness_moments, dim3(1), dim3(1024), 0, (hipStream_t)stream, d_raw, n,
+                       d_moments, accumulate);
+    HSES_CHECK_HIP(hipGetLastError());
+    return HSES_OK;
+}
+
+extern "C" int hses_combine_affine(const float* d_grad_acc, const float* d_ones_acc,
+                                   const double* d_moments, int32_t batch, int64_t len, float* d_out,
+                                   void* stream) {
+    HSES_REQUIRE(batch >= 1, "batch must be >= 1");
+    HSES_REQUIRE(len >= 0, "negative length");
+    if (len == 0) return HSES_OK;
+    HSES_REQUIRE(d_grad_acc && d_moments && d_out, "NULL pointer");
+    const int64_t blocks = (len + 255) / 256;
+    HSES_REQUIRE(blocks < (1ll << 31), "grid too large");
+    hipLaunchKernelGGL(k_combine_affine, dim3(blocks), dim3(256), 0, (hipStream_t)stream, d_grad_acc,
+                       d_ones_acc, d_moments, batch, len, d_out);
     HSES_CHECK_HIP(hipGetLastError());
     return HSES_OK;
 }

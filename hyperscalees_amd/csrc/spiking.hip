@@ -14,14 +14,15 @@ namespace hses {
 // (poisson_encode_fused_oxide.rs:44-52); RN32(m / D) is non-decreasing in m,
 // so `u < p` is exactly `(v >> 9) < K(p)`.  RN32(q) < p iff q lies below the
 // midpoint between p and its predecessor (q = m / D is never exactly that
-// dyadic midpoint: D is odd), so K = floor(mid * D), clamped to 2^23.  mid
-// (25 significant bits) and mid * D (49 bits) are exact in f64.
+// dyadic midpoint: D is odd), so K = floor(mid * D), clamped to 2^23.
+// mid * D = (pp + p) * (D / 2): the sum (25 significant bits) and its product
+// with D / 2 = 4194304.5 (24 bits) are exact in f64.  Branch-free: the value
+// computed for p <= 0 or NaN is discarded by the final select.
 __device__ __forceinline__ uint32_t poisson_threshold(float p) {
-    if (!(p > 0.0f)) return 0u;  // p <= 0 or NaN: never fires
     const float pp = __uint_as_float(__float_as_uint(p) - 1u);  // predecessor (Inf -> FLT_MAX)
-    const double mid = ((double)pp + (double)p) * 0.5;
-    const double t = mid * 8388609.0;
-    return t >= 8388608.0 ? 8388608u : (uint32_t)t;  // t > 0 and never an integer
+    const double t = ((double)pp + (double)p) * 4194304.5;
+    const uint32_t k = t >= 8388608.0 ? 8388608u : (uint32_t)t;  // t > 0 and never an integer
+    return p > 0.0f ? k : 0u;  // p <= 0 or NaN: never fires
 }
 
 template <int FMT>
@@ -104,6 +105,57 @@ __global__ __launch_bounds__(64 * P_ROWS_PER_BLOCK) void k_poisson_bits(
     }
 }
 
+// One stage (distance D <= 8) of the 64 x 64 bit transpose on a 32-bit half:
+// partner = lane ^ D by DPP, then lanes with bit D clear keep the bits of
+// mask m and take the partner's m bits shifted up by D, lanes with bit D set
+// the mirror image.  The rotate wraps only bits the select discards.
+template <int D>
+__device__ __forceinline__ uint32_t tr_stage(uint32_t w, bool set) {
+    constexpr uint32_t m = D == 8 ? 0x00FF00FFu : D == 4 ? 0x0F0F0F0Fu : D == 2 ? 0x33333333u : 0x55555555u;
+    uint32_t y;
+    if constexpr (D == 1) {
+        y = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)w, 0xB1, 0xF, 0xF, false);  // quad_perm 1,0,3,2
+    } else if constexpr (D == 2) {
+        y = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)w, 0x4E, 0xF, 0xF, false);  // quad_perm 2,3,0,1
+    } else {
+        // row_shl:D into the lanes with bit D clear, row_shr:D into the others
+        constexpr int lo_banks = D == 4 ? 0x5 : 0x3;
+        const int t = __builtin_amdgcn_update_dpp((int)w, (int)w, 0x100 + D, 0xF, lo_banks, false);
+        y = (uint32_t)__builtin_amdgcn_update_dpp(t, (int)w, 0x110 + D, 0xF, 0xF ^ lo_banks, false);
+    }
+    const uint32_t keep = set ? ~m : m;
+    const uint32_t ys = __builtin_amdgcn_alignbit(y, y, set ? D : 32 - D);
+    return (w & keep) | (ys & ~keep);
+}
+
+// Transpose of the 64 x 64 bit matrix held one row per lane (lane r: bits
+// 0-31 of row r in lo, 32-63 in hi): afterwards lane c holds column c.
+// Distance 32 is one cross-half lane swap of lo and hi; distance 16 swaps
+// 16-bit halves (byte permutes around a 16-lane swap); distances 8..1 are
+// DPP stages.
+__device__ __forceinline__ void transpose64(uint32_t& lo, uint32_t& hi, int lane) {
+    {
+        const auto r = __builtin_amdgcn_permlane32_swap(lo, hi, false, false);
+        lo = r[0];
+        hi = r[1];
+    }
+    {
+        const uint32_t u = __builtin_amdgcn_perm(hi, lo, 0x05040100u);  // low halves
+        const uint32_t v = __builtin_amdgcn_perm(hi, lo, 0x07060302u);  // high halves
+        const auto r = __builtin_amdgcn_permlane16_swap(u, v, false, false);
+        lo = __builtin_amdgcn_perm(r[1], r[0], 0x05040100u);
+        hi = __builtin_amdgcn_perm(r[1], r[0], 0x07060302u);
+    }
+    lo = tr_stage<8>(lo, lane & 8);
+    hi = tr_stage<8>(hi, lane & 8);
+    lo = tr_stage<4>(lo, lane & 4);
+    hi = tr_stage<4>(hi, lane & 4);
+    lo = tr_stage<2>(lo, lane & 2);
+    hi = tr_stage<2>(hi, lane & 2);
+    lo = tr_stage<1>(lo, lane & 1);
+    hi = tr_stage<1>(hi, lane & 1);
+}
+
 // Bit-packed Poisson for rows with many p == 0 elements (the SNN input: 70%
 // exact zeros).  One wave per row, in three phases over LDS:
 //   A. classify: K(p) = 0 never fires, K = 2^23 always fires (pattern of all
@@ -142,15 +194,18 @@ __global__ __launch_bounds__(256) void k_poisson_sparse(
     for (int32_t w0 = 0; w0 < words; w0 += PB) {
         float pv[PB];
 #pragma unroll
-        for (int i = 0; i < PB; ++i) {
+        for (int i = 0; i < PB; ++i) {  // every load in bounds, masked after
             const int32_t col = (w0 + i) * 64 + lane;
-            pv[i] = (src_ok && col < in_dim) ? prow_p[col] : 0.0f;
+            pv[i] = prow_p[col < in_dim ? col : in_dim - 1];
         }
+#pragma unroll
+        for (int i = 0; i < PB; ++i)
+            if (!src_ok || (w0 + i) * 64 + lane >= in_dim) pv[i] = 0.0f;
 #pragma unroll
         for (int i = 0; i < PB; ++i) {
             if (w0 + i >= words) break;
             const int32_t col = (w0 + i) * 64 + lane;
-            const uint32_t K = col < in_dim ? poisson_threshold(pv[i]) : 0u;
+            const uint32_t K = poisson_threshold(pv[i]);  // pv = 0 past the row: K = 0
             const bool full = K >= 8388608u, act = K != 0u && !full;
             pat[col] = full ? ALL : K;
             const uint64_t am = __ballot(act);
@@ -186,26 +241,21 @@ __global__ __launch_bounds__(256) void k_poisson_sparse(
 
     // C. transpose and store
     const int64_t plane = rows * out_stride;
+    const int32_t wi = lane / T, t = lane % T;
+    uint64_t* orow = out + (int64_t)t * plane + row * out_stride;
     for (int32_t w0 = 0; w0 < words; w0 += WPT) {
-        uint64_t x = 0;
+        uint32_t lo = 0, hi = 0;
 #pragma unroll
-        for (int wi = 0; wi < WPT; ++wi)
-            if (w0 + wi < words) x |= (uint64_t)pat[(w0 + wi) * 64 + lane] << (wi * T);
-        // block swap at distance d: lane r (bit d clear) takes the partner's
-        // columns c with bit d clear into c | d; the partner the mirror image
-#pragma unroll
-        for (int d = 32; d >= 1; d >>= 1) {
-            const uint64_t m0 = d == 32 ? 0x00000000ffffffffull
-                              : d == 16 ? 0x0000ffff0000ffffull
-                              : d == 8  ? 0x00ff00ff00ff00ffull
-                              : d == 4  ? 0x0f0f0f0f0f0f0f0full
-                              : d == 2  ? 0x3333333333333333ull
-                                        : 0x5555555555555555ull;
-            const uint64_t y = __shfl_xor(x, d);
-            x = (lane & d) ? ((x & ~m0) | ((y & ~m0) >> d)) : ((x & m0) | ((y & m0) << d));
+        for (int i = 0; i < WPT; ++i) {
+            const int32_t wr = w0 + i < words ? w0 + i : words - 1;  // in bounds, masked below
+            const uint32_t v = w0 + i < words ? pat[wr * 64 + lane] : 0u;
+            if (i * T < 32)
+                lo |= v << (i * T);
+            else
+                hi |= v << (i * T - 32);
         }
-        const int32_t wi = lane / T, t = lane % T;
-        if (w0 + wi < words) out[(int64_t)t * plane + row * out_stride + w0 + wi] = x;
+        transpose64(lo, hi, lane);
+        if (w0 + wi < words) orow[w0 + wi] = ((uint64_t)hi << 32) | lo;
     }
 }
 

@@ -9,7 +9,8 @@ import ctypes
 import torch
 
 from . import _lib
-from ._lib import FMT_BF16, FMT_BITS, FMT_F32, FMT_U8, MATH_BF16, MATH_F32  # noqa: F401
+from ._lib import (FMT_BF16, FMT_BITS, FMT_F32, FMT_U8, MATH_BF16, MATH_F32,  # noqa: F401
+                   REWARD_BINARY, REWARD_LOGLIK)
 
 _FMT_DTYPE = {FMT_F32: torch.float32, FMT_BF16: torch.bfloat16, FMT_U8: torch.uint8,
               FMT_BITS: torch.int64}
@@ -231,6 +232,45 @@ def member_loglik(logits, labels, n, rows_per_member):
     _lib.call("hses_member_loglik", _p(logits), logits.shape[-1], _p(labels), n, rows_per_member,
               _p(fit), _stream())
     return fit
+
+
+def member_fitness(logits, labels, n, rows_per_member, reward=REWARD_LOGLIK, out=None,
+                   correct=None):
+    """Per-member mean reward (Loglik or Binary); `correct` (int64, 1 element)
+    is incremented by the number of rows whose argmax is the label."""
+    _dev(logits, torch.float32, "logits")
+    _dev(labels, torch.int32, "labels")
+    if correct is not None:
+        _dev(correct, torch.int64, "correct")
+    if out is None:
+        out = torch.empty(n, dtype=torch.float32, device=logits.device)
+    _lib.call("hses_member_fitness", _p(logits), logits.shape[-1], _p(labels), n, rows_per_member,
+              reward, _p(out), _p(correct), _stream())
+    return out
+
+
+def fitness_moments(raw, moments, accumulate=False):
+    """moments (float64, 2) = / += {sum raw, sum raw^2}."""
+    _dev(raw, torch.float32, "raw")
+    _dev(moments, torch.float64, "moments")
+    _lib.call("hses_fitness_moments", _p(raw), raw.numel(), _p(moments), int(bool(accumulate)),
+              _stream())
+    return moments
+
+
+def combine_affine(grad_acc, moments, batch, ones_acc=None, out=None):
+    """(grad_acc - ones_acc*mean) * (-1/(std*sqrt(batch))) with mean/std from moments."""
+    _dev(grad_acc, torch.float32, "grad_acc")
+    _dev(moments, torch.float64, "moments")
+    if ones_acc is not None:
+        _dev(ones_acc, torch.float32, "ones_acc")
+        assert ones_acc.numel() == grad_acc.numel()
+    if out is None:
+        out = torch.empty_like(grad_acc)
+    assert out.numel() == grad_acc.numel()
+    _lib.call("hses_combine_affine", _p(grad_acc), _p(ones_acc), _p(moments), batch,
+              grad_acc.numel(), _p(out), _stream())
+    return out
 
 
 def convert_fitnesses(raw, group_size=0):

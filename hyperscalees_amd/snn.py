@@ -1,7 +1,7 @@
 """SNN-MLP EggRoll ES step on the GPU, composed from the libhses kernels.
 
-One step (the per-chunk body of accumulate_train.rs:770-938 with the whole
-population in one chunk, and the deterministic noiser stream):
+One step (the per-chunk body of accumulate_train.rs:770-938 and the
+deterministic noiser stream):
   1. Poisson-encode each member's samples into bit-packed spike trains
      (poisson_encode_fused_oxide.rs:61-106);
   2. hidden layers: perturbed linear (eggroll.rs:419-446, snn.rs:665-685)
@@ -10,6 +10,12 @@ population in one chunk, and the deterministic noiser stream):
      averaged over the member's samples (snn_mnist.rs:180-201);
   4. z-score (eggroll.rs:967-992), ES gradient per layer
      (eggroll.rs:353-404) and one solver step (noiser.rs:155-225).
+With `accumulate` K > 1 the population runs as K chunks of N/K members with
+frozen parameters, as the reference's K-chunk driver does
+(accumulate_train.rs:719-944): each chunk's raw fitness weights an ES
+gradient accumulated over the chunks, the raw-fitness sums accumulate on the
+device, and combine_affine_grads (eggroll.rs:902-915) turns the sums into the
+z-scored gradient before the one solver step.  Nothing is copied to the host.
 The model is the reference SnnModel generalised to any number of hidden LIF
 layers (the JAX model is depth-generic); every layer is an MM parameter with
 its own base key (i+1)*0x9E3779B97F4A7C15 (accumulate_train.rs:603-608).
@@ -21,7 +27,7 @@ import numpy as np
 import torch
 
 from . import kernels as K
-from ._lib import ADAMW, FMT_BITS, FMT_F32, MATH_BF16, SGD
+from ._lib import ADAMW, FMT_BITS, FMT_F32, MATH_BF16, REWARD_LOGLIK, SGD
 
 KEY_MUL = 0x9E3779B97F4A7C15
 
@@ -49,11 +55,19 @@ class SnnConfig:
     eps: float = 1e-8
     weight_decay: float = 1e-4
     poisson_seed: tuple = (0, 0, 0, 0)
+    reward: int = REWARD_LOGLIK    # fitness_from_logits_reward kind (snn_mnist.rs:175-201)
+    accumulate: int = 1            # K chunks of n / K members (accumulate_train.rs:770)
     keys: list = field(default_factory=list)
 
     def __post_init__(self):
         if not self.keys:
             self.keys = layer_keys(len(self.dims) - 1)
+        if self.accumulate < 1 or self.n % self.accumulate:
+            raise ValueError(f"n={self.n} is not a multiple of accumulate={self.accumulate}")
+
+    @property
+    def chunk(self):
+        return self.n // self.accumulate
 
 
 def sample_index(seed, n, rows, pool_size):
@@ -106,7 +120,7 @@ class SnnEs:
         idx = torch.as_tensor(index, dtype=torch.int32).to(device).contiguous()
         self.index = idx
         self.labels = torch.as_tensor(pool_labels, dtype=torch.int32).to(device)[idx.long()].contiguous()
-        M = c.n * c.rows
+        M = c.chunk * c.rows  # activation rows of one chunk
         self.M = M
         L = len(c.dims) - 1
         self.L = L
@@ -124,24 +138,38 @@ class SnnEs:
             torch.empty((c.T, M, hmax), dtype=torch.float32, device=device)
         self.rate = torch.empty((M, c.dims[-2]), dtype=torch.float32, device=device)
         self.logits = torch.empty((M, c.dims[-1]), dtype=torch.float32, device=device)
+        self.raw = torch.empty(c.n, dtype=torch.float32, device=device)
+        self.moments = torch.zeros(2, dtype=torch.float64, device=device)
+        self.correct = torch.zeros(1, dtype=torch.int64, device=device)
         self.grads = [torch.zeros_like(w) for w in self.W]
         self.m = [torch.zeros_like(w) for w in self.W]
         self.v = [torch.zeros_like(w) for w in self.W]
         self.step_t = 0
 
     # -- forward -------------------------------------------------------------
-    def poisson(self):
+    def chunk_seeds(self, lo):
+        """Poisson seeds of the chunk starting at member lo.  The kernel seeds
+        element (row, col) of a call with 1000000007*(row*in + col) + (s0^s1^s2^s3);
+        adding 1000000007 * (first row * in) to the mixed seed makes a chunk's
+        encode equal to rows lo*rows.. of a whole-population encode."""
         c = self.cfg
-        K.poisson_encode(self.pool, c.T, c.poisson_seed, FMT_BITS, out=self.spk[0],
-                         rows_index=self.index)
+        s0, s1, s2, s3 = (int(v) & 0xFFFFFFFF for v in c.poisson_seed)
+        mix = (s0 ^ s1 ^ s2 ^ s3) + 1000000007 * lo * c.rows * c.dims[0]
+        return (mix & 0xFFFFFFFF, 0, 0, 0)
 
-    def hidden_layer(self, l, epoch):
+    def poisson(self, lo=0):
+        c = self.cfg
+        rows = slice(lo * c.rows, (lo + c.chunk) * c.rows)
+        K.poisson_encode(self.pool, c.T, self.chunk_seeds(lo), FMT_BITS, out=self.spk[0],
+                         rows_index=self.index[rows])
+
+    def hidden_layer(self, l, epoch, lo=0):
         c = self.cfg
         a = c.dims[l + 1]
         if self.fused:
             last = l == self.L - 2  # feeds the readout: only its spike rates are used
             K.perturbed_linear_lif(self.spk[l], self.W[l], c.keys[l], c.rank, c.sigma, epoch,
-                                   c.noise_reuse, 0, c.n, c.rows, c.T, c.tau_m, c.v_th,
+                                   c.noise_reuse, lo, c.chunk, c.rows, c.T, c.tau_m, c.v_th,
                                    spikes=None if last else self.spk[l + 1],
                                    rate=self.rate if last else None,
                                    want_spikes=not last, want_rate=last)
@@ -149,25 +177,27 @@ class SnnEs:
         cur = self.cur[:, :, :a] if a == self.cur.shape[2] else \
             self.cur.view(-1)[: c.T * self.M * a].view(c.T, self.M, a)
         K.perturbed_linear(self.spk[l], self.W[l], c.keys[l], c.rank, c.sigma, epoch,
-                           c.noise_reuse, 0, c.n, c.rows, x_fmt=FMT_BITS, n_time=c.T,
+                           c.noise_reuse, lo, c.chunk, c.rows, x_fmt=FMT_BITS, n_time=c.T,
                            math=c.math, out=cur)
         K.lif_scan(cur, c.tau_m, c.v_th, fmt=FMT_BITS, out=self.spk[l + 1])
 
-    def readout(self, epoch):
+    def readout(self, epoch, lo=0):
         c = self.cfg
         if not self.fused:
             K.spike_rate(self.spk[self.L - 1], FMT_BITS, c.dims[-2], out=self.rate)
         K.perturbed_linear(self.rate, self.W[-1], c.keys[-1], c.rank, c.sigma, epoch,
-                           c.noise_reuse, 0, c.n, c.rows, x_fmt=FMT_F32, n_time=1, math=c.math,
-                           out=self.logits.view(1, self.M, -1))
-        return K.member_loglik(self.logits, self.labels, c.n, c.rows)
+                           c.noise_reuse, lo, c.chunk, c.rows, x_fmt=FMT_F32, n_time=1,
+                           math=c.math, out=self.logits.view(1, self.M, -1))
+        labels = self.labels[lo * c.rows:(lo + c.chunk) * c.rows]
+        return K.member_fitness(self.logits, labels, c.chunk, c.rows, c.reward,
+                                out=self.raw[lo:lo + c.chunk], correct=self.correct)
 
-    def forward(self, epoch=0):
-        """Raw fitness of every member (N,)."""
-        self.poisson()
+    def forward(self, epoch=0, lo=0):
+        """Raw fitness of the chunk of members [lo, lo + chunk) (a view of self.raw)."""
+        self.poisson(lo)
         for l in range(self.L - 1):
-            self.hidden_layer(l, epoch)
-        return self.readout(epoch)
+            self.hidden_layer(l, epoch, lo)
+        return self.readout(epoch, lo)
 
     # -- update --------------------------------------------------------------
     def update(self, raw_fit, epoch=0):
@@ -185,6 +215,41 @@ class SnnEs:
         return z
 
     def step(self, epoch=0):
-        fit = self.forward(epoch)
-        self.update(fit, epoch)
-        return fit
+        """One ES step; returns the raw fitness (N,).  self.correct counts the
+        step's rows whose argmax is the label."""
+        self.correct.zero_()
+        if self.cfg.accumulate == 1:
+            fit = self.forward(epoch)
+            self.update(fit, epoch)
+            return fit
+        return self.step_accumulate(epoch)
+
+    def step_accumulate(self, epoch=0):
+        """The K-chunk step (accumulate_train.rs:770-944) with the parameters
+        frozen over the chunks.  Per chunk: forward, raw-fitness sums, and
+        grad_acc += sum_i raw_i A_i B_i^T.  The ones sum sum_i A_i B_i^T of
+        combine_affine_grads vanishes over the noiser stream's antithetic pairs
+        (A negated for odd thread ids, B shared), also across chunk boundaries,
+        so it is only formed for an unpaired last member (odd N)."""
+        c = self.cfg
+        for k in range(c.accumulate):
+            lo = k * c.chunk
+            raw = self.forward(epoch, lo)
+            K.fitness_moments(raw, self.moments, accumulate=k > 0)
+            for l in range(self.L):
+                a, b = self.W[l].shape
+                K.es_update(raw, lo, c.keys[l], c.rank, c.sigma, epoch, c.noise_reuse, a, b,
+                            np.float32(1.0), out=self.grads[l], accumulate=k > 0)
+        one = torch.ones(1, dtype=torch.float32, device=self.dev) if c.n % 2 else None
+        self.step_t += 1
+        for l in range(self.L):
+            a, b = self.W[l].shape
+            ones = None
+            if one is not None:
+                ones = K.es_update(one, c.n - 1, c.keys[l], c.rank, c.sigma, epoch, c.noise_reuse,
+                                   a, b, np.float32(1.0))
+            K.combine_affine(self.grads[l], self.moments, c.n, ones_acc=ones, out=self.grads[l])
+            K.solver_step(c.solver, c.lr, self.W[l], self.grads[l], self.m[l], self.v[l],
+                          step_t=self.step_t, beta1=c.beta1, beta2=c.beta2, eps=c.eps,
+                          wd=c.weight_decay if c.solver == ADAMW else 0.0)
+        return self.raw

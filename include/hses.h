@@ -51,6 +51,9 @@ typedef enum {
 /* Solver kinds (burn_impl/hyperscalees-noiser/src/noiser.rs:43-92). */
 typedef enum { HSES_SGD = 0, HSES_ADAM = 1, HSES_ADAMW = 2 } hses_solver;
 
+/* Reward kinds of fitness_from_logits_reward (burn_impl/hyperscalees-envs/src/snn_mnist.rs:175-201). */
+typedef enum { HSES_REWARD_LOGLIK = 0, HSES_REWARD_BINARY = 1 } hses_reward;
+
 /* ---- runtime ---------------------------------------------------------- */
 
 /* Initialise device `device` (builds the Box-Muller correction tables and
@@ -191,6 +194,29 @@ int hses_es_update(const float *d_f, int32_t n, int32_t tid_lo, uint64_t key, in
  * averaged over each member's rows: d_fit[m] = mean_s log_softmax(logits[m*rows+s])[label]. */
 int hses_member_loglik(const float *d_logits, int32_t classes, const int32_t *d_labels,
                        int32_t n, int32_t rows_per_member, float *d_fit, void *stream);
+
+/* fitness_from_logits_reward (snn_mnist.rs:180-201) with either reward, averaged over
+ * each member's rows: Loglik log_softmax(row)[label]; Binary 1.0 when the first maximal
+ * class (argmax) is the label, else 0.0.  d_correct (optional) is incremented by the
+ * number of rows whose argmax is the label: the train-accuracy counter of the K-chunk
+ * driver (accumulate_train.rs:847-849). */
+int hses_member_fitness(const float *d_logits, int32_t classes, const int32_t *d_labels,
+                        int32_t n, int32_t rows_per_member, int32_t reward, float *d_fit,
+                        unsigned long long *d_correct, void *stream);
+
+/* The K-chunk driver's raw-fitness sums (accumulate_train.rs:843-846): d_moments[0] and
+ * d_moments[1] receive sum(raw) and sum(raw^2) of this chunk in double, overwritten
+ * (accumulate 0, first chunk) or added to (accumulate 1).  One block; deterministic. */
+int hses_fitness_moments(const float *d_raw, int32_t n, double *d_moments, int32_t accumulate,
+                         void *stream);
+
+/* combine_affine_grads (eggroll.rs:902-915) with the driver's global mean and std
+ * (accumulate_train.rs:940-944) read from d_moments over `batch` members:
+ * mean = S1/batch, var = max(S2/batch - mean^2, 0), std = sqrt(var + 1e-5),
+ * d_out = (d_grad_acc - d_ones_acc*mean) * (-1/(std*sqrt(batch))).  d_ones_acc may be
+ * NULL (an all-zero ones sum); d_out may alias d_grad_acc.  No host synchronisation. */
+int hses_combine_affine(const float *d_grad_acc, const float *d_ones_acc, const double *d_moments,
+                        int32_t batch, int64_t len, float *d_out, void *stream);
 
 /* convert_fitnesses (eggroll.rs:967-992): global (group_size 0) or per-group
  * z-score with the global std.  d_stats (optional) receives {mean, std}. */

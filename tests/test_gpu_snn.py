@@ -172,3 +172,48 @@ def test_c3_fused_forward_equals_unfused(hses_gpu):
     assert torch.equal(es_u.rate, es_f.rate)
     assert torch.equal(fit_u, fit_f)
     assert float(es_f.rate.mean()) > 0.005
+
+
+@pytest.mark.parametrize("n,K,fused", [(16, 2, False), (9, 3, False), (16, 4, True)])
+def test_k_chunk_step_equals_one_chunk(hses_gpu, n, K, fused):
+    # accumulate_train.rs:770-944: K chunks with frozen parameters, raw-weighted
+    # gradients and the affine z-score (combine_affine_grads) == the one-chunk
+    # step on z-scored fitness, the identity of eggroll.rs:1502-1568.  Chunk
+    # Poisson seeds continue the whole-population encode, so every member's
+    # fitness is bit-identical; n=9, K=3 splits pairs across chunks and leaves
+    # an unpaired last member (its ones term is the only non-zero one).
+    base = dict(C3_SMALL if fused else C1, n=n, solver=SGD, lr=0.05)
+    es1, *_ = make(snn.SnnConfig(**base), fused=fused)
+    esk, *_ = make(snn.SnnConfig(**base, accumulate=K), fused=fused)
+    W0 = [w.cpu().numpy().copy() for w in es1.W]
+    f1 = es1.step(0).clone()
+    fk = esk.step(0).clone()
+    torch.cuda.synchronize()
+    assert torch.equal(f1, fk)
+    assert int(es1.correct) == int(esk.correct) and int(esk.correct) > 0
+    for l in range(es1.L):
+        g1, gk = es1.grads[l].cpu().numpy(), esk.grads[l].cpu().numpy()
+        gmax = np.abs(g1).max()
+        assert gmax > 0 and np.abs(gk - g1).max() <= 1e-5 * gmax, f"layer {l} gradient"
+        w1, wk = es1.W[l].cpu().numpy(), esk.W[l].cpu().numpy()
+        tol = 2 * np.spacing(np.abs(W0[l])) + 1e-5 * gmax * base["lr"]
+        assert np.all(np.abs(wk - w1) <= tol), f"layer {l} parameter step"
+
+
+def test_k_chunk_step_matches_oracle_two_phase(hses_gpu):
+    # The K-chunk gradient against the oracle's two-phase accumulated_update
+    # (eggroll.rs:579-702: global z-score, per-chunk einsum, -1/sqrt(batch)) on
+    # the GPU's own raw fitness.
+    cfg = snn.SnnConfig(**dict(C1, n=12, accumulate=3))
+    es, *_ = make(cfg)
+    raw = es.step(0).cpu().numpy()
+    torch.cuda.synchronize()
+    conv, _, _ = O.convert_fitnesses(raw)
+    tids = np.arange(cfg.n, dtype=np.int32)
+    for l in range(es.L):
+        a, b = es.W[l].shape
+        ref = np.zeros((a, b), np.float32)
+        O.load().or_accumulated_lora_grad(cfg.sigma, cfg.keys[l], cfg.rank, 0, 0, conv, tids,
+                                          cfg.accumulate, cfg.chunk, a, b, ref)
+        g = es.grads[l].cpu().numpy()
+        assert np.abs(g - ref).max() <= 1e-5 * np.abs(ref).max(), f"layer {l}"

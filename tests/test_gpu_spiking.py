@@ -4,7 +4,8 @@ import numpy as np
 import pytest
 import torch
 
-from hyperscalees_amd._lib import ADAM, ADAMW, FMT_BF16, FMT_BITS, FMT_F32, FMT_U8, SGD
+from hyperscalees_amd._lib import (ADAM, ADAMW, FMT_BF16, FMT_BITS, FMT_F32, FMT_U8,
+                                   REWARD_BINARY, REWARD_LOGLIK, SGD)
 from tests import oracle_lib as O
 
 pytestmark = pytest.mark.gpu
@@ -118,6 +119,56 @@ def test_member_loglik(hses_gpu, n, rpm):
                                  n, rpm)
     torch.cuda.synchronize()
     np.testing.assert_allclose(got.cpu().numpy(), ref, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("reward", [REWARD_LOGLIK, REWARD_BINARY])
+def test_member_fitness_rewards_and_correct_count(hses_gpu, reward):
+    # fitness_from_logits_reward (snn_mnist.rs:180-201) per reward kind, member
+    # means, and the argmax == label counter (first maximal class on ties).
+    rng = np.random.default_rng(11 + reward)
+    n, rpm, c = 37, 70, 10
+    logits = np.round(rng.standard_normal((n * rpm, c)) * 2).astype(np.float32)  # many ties
+    labels = rng.integers(0, c, n * rpm).astype(np.int32)
+    hit = (logits.argmax(1) == labels)
+    if reward == REWARD_BINARY:
+        ref = hit.astype(np.float64).reshape(n, rpm).mean(1)
+    else:
+        ref = O.loglik(logits, labels).reshape(n, rpm).astype(np.float64).mean(1)
+    correct = torch.full((1,), 5, dtype=torch.int64, device="cuda")
+    got = hses_gpu.member_fitness(torch.from_numpy(logits).cuda(), torch.from_numpy(labels).cuda(),
+                                  n, rpm, reward, correct=correct)
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(got.cpu().numpy(), ref, rtol=1e-5, atol=1e-5)
+    assert int(correct) == 5 + int(hit.sum())
+
+
+def test_fitness_moments_and_combine_affine(hses_gpu):
+    # accumulate_train.rs:843-846, 940-944 and combine_affine_grads
+    # (eggroll.rs:902-915): sums over two chunks, then the affine combination
+    # against the oracle's with the driver's f32 mean/std formulas.
+    rng = np.random.default_rng(12)
+    raw = (rng.standard_normal(3000) * 2 + 0.7).astype(np.float32)
+    g = rng.standard_normal(4097).astype(np.float32)
+    o = rng.standard_normal(4097).astype(np.float32)
+    mom = torch.empty(2, dtype=torch.float64, device="cuda")
+    hses_gpu.fitness_moments(torch.from_numpy(raw[:1234]).cuda(), mom)
+    hses_gpu.fitness_moments(torch.from_numpy(raw[1234:]).cuda(), mom, accumulate=True)
+    torch.cuda.synchronize()
+    s1 = raw.astype(np.float64).sum()
+    s2 = (raw * raw).astype(np.float64).sum()
+    np.testing.assert_allclose(mom.cpu().numpy(), [s1, s2], rtol=1e-12)
+    batch = raw.size
+    mean = np.float32(np.float32(s1) / np.float32(batch))
+    var = max(np.float32(np.float32(s2) / np.float32(batch)) - mean * mean, np.float32(0))
+    std = np.float32(np.sqrt(np.float32(var + np.float32(1e-5))))
+    for ones in (o, None):
+        ref = np.zeros_like(g)
+        O.load().or_combine_affine(g, o if ones is not None else np.zeros_like(g), g.size, mean,
+                                   std, batch, ref)
+        got = hses_gpu.combine_affine(torch.from_numpy(g).cuda(), mom, batch,
+                                      ones_acc=None if ones is None else torch.from_numpy(o).cuda())
+        torch.cuda.synchronize()
+        np.testing.assert_allclose(got.cpu().numpy(), ref, rtol=2e-6, atol=1e-7)
 
 
 @pytest.mark.parametrize("group", [0, 4])
