@@ -71,6 +71,14 @@ def test_validation_rejects_bad_arguments_without_a_gpu():
     _expect_invalid("hses_solver_step", 1, 0.1, 0.9, 0.999, 1e-8, 0.0, 0, ctypes.c_void_p(16),
                     ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16), 4, NULL)
     _expect_invalid("hses_member_loglik", NULL, 0, NULL, 4, 2, NULL, NULL)
+    _expect_invalid("hses_member_fitness", ctypes.c_void_p(16), 10, ctypes.c_void_p(16), 4, 2, 2,
+                    ctypes.c_void_p(16), NULL, NULL)  # unknown reward
+    _expect_invalid("hses_member_fitness", NULL, 10, NULL, 4, 2, 0, NULL, NULL, NULL)
+    _expect_invalid("hses_fitness_moments", ctypes.c_void_p(16), 4, NULL, 0, NULL)
+    _expect_invalid("hses_combine_affine", ctypes.c_void_p(16), NULL, ctypes.c_void_p(16), 0, 4,
+                    ctypes.c_void_p(16), NULL)  # batch 0
+    _expect_invalid("hses_combine_affine", ctypes.c_void_p(16), NULL, NULL, 8, 4,
+                    ctypes.c_void_p(16), NULL)
     _expect_invalid("hses_poisson_encode", ctypes.c_void_p(16), 3, NULL, 4, 784, 784, 8, 0, 0, 0,
                     0, ctypes.c_void_p(16), 0, 784, NULL)  # p has fewer rows than the output
     _expect_invalid("hses_spike_rate", ctypes.c_void_p(16), 3, 1, 16, 4, 128, ctypes.c_void_p(16),
@@ -89,3 +97,5 @@ def test_empty_inputs_are_no_ops_without_a_gpu():
     assert lib.hses_lora_factors(0.1, 1, 4, 0, 0, 0, NULL, 0, 3, 4, NULL, NULL, NULL) == 0
     assert lib.hses_solver_step(0, 0.1, 0.9, 0.999, 1e-8, 0.0, 1, NULL, NULL, NULL, NULL, 0,
                                 NULL) == 0
+    assert lib.hses_member_fitness(NULL, 10, NULL, 0, 4, 1, NULL, NULL, NULL) == 0
+    assert lib.hses_combine_affine(NULL, NULL, NULL, 8, 0, NULL, NULL) == 0
