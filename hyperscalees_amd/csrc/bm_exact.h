@@ -230,6 +230,9 @@ HSES_HD uint64_t xs64(uint64_t x) {
     return x;
 }
 
+// Entries of a GF(2) matrix in nibble form (16 nibble positions x 16 values).
+constexpr int kJumpNib = 256;
+
 // y = J x over GF(2), J given by its 64 columns (column i = J e_i).
 HSES_HD uint64_t gf2_apply(const uint64_t* cols, uint64_t x) {
     uint64_t y = 0;

@@ -5,7 +5,8 @@
 // and 2p+2 after s0 = noise_seed(...) | 1 (noiser.rs:437-490).  Kernels give
 // each thread whole rows: the state at the start of row j is
 // M^(2Lj) s0 = T1[j/16] (T0[j%16] s0), two GF(2) products with matrices from
-// the per-L jump table, after which the thread steps sequentially.
+// the per-L jump table (each stored as 16 x 16 nibble entries, so a product
+// is 16 table reads and XORs), after which the thread steps sequentially.
 //
 // Normals are produced in batches (bm_normals<G>): the G log and G cos
 // evaluations are independent, so their f64 latency overlaps, and every
@@ -185,12 +186,26 @@ __device__ __forceinline__ void bm_run(uint64_t& s, int32_t count, const NoiseCt
     for (; i < count; ++i) sink(i, bm_normal(s, c));
 }
 
-// State before the first normal of row j of a stream with s0 = seed | 1.
+// J x over GF(2) for J in nibble form (kJumpNib entries: entry 16 i + v is
+// J (v << 4i)), so J x is the XOR of 16 entries, one per nibble of x.
+__device__ __forceinline__ uint64_t nib_apply(const uint64_t* tab, uint64_t x) {
+    const uint32_t lo = (uint32_t)x, hi = (uint32_t)(x >> 32);
+    uint64_t y0 = 0, y1 = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        y0 ^= tab[16 * i + ((lo >> (4 * i)) & 15u)];
+        y1 ^= tab[16 * (8 + i) + ((hi >> (4 * i)) & 15u)];
+    }
+    return y0 ^ y1;
+}
+
+// State before the first normal of row j of a stream with s0 = seed | 1:
+// T1[j / 16] (T0[j % 16] s0) with the nibble-form matrices of the jump table.
 __device__ __forceinline__ uint64_t row_start_state(uint64_t seed, int32_t j,
                                                      const uint64_t* jump) {
     const uint64_t s0 = seed | 1ull;
-    const uint64_t s1 = gf2_apply(jump + (size_t)(j & 15) * 64, s0);
-    return gf2_apply(jump + (size_t)(16 + (j >> 4)) * 64, s1);
+    const uint64_t s1 = nib_apply(jump + (size_t)(j & 15) * kJumpNib, s0);
+    return nib_apply(jump + (size_t)(16 + (j >> 4)) * kJumpNib, s1);
 }
 
 // Seed of member `tid` for one layer key (eggroll.rs:60-65, noiser.rs:495-506).

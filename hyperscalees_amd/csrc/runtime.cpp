@@ -87,18 +87,30 @@ int get_jump_table(DeviceState* st, int64_t row_len, int64_t rows, const uint64_
     }
     // Build (or rebuild larger) the table for this row length.
     int32_t n1 = (int32_t)std::max<int64_t>(need_n1, 64);
-    std::vector<uint64_t> host((size_t)(kJumpG + n1) * 64);
+    std::vector<uint64_t> host((size_t)(kJumpG + n1) * kJumpNib);
+    // Matrix J in nibble form: entry 16 i + v = J (v << 4i) = XOR of the
+    // columns 4i + bit over the set bits of v.
+    auto put = [&](size_t m, const Gf2& J) {
+        uint64_t* e = &host[m * kJumpNib];
+        for (int i = 0; i < 16; ++i)
+            for (int v = 0; v < 16; ++v) {
+                uint64_t y = 0;
+                for (int bit = 0; bit < 4; ++bit)
+                    if ((v >> bit) & 1) y ^= J.c[4 * i + bit];
+                e[16 * i + v] = y;
+            }
+    };
     const Gf2 M = gf2_step();
     const Gf2 row = gf2_pow(M, 2ull * (uint64_t)row_len);  // one factor row = 2L steps
     Gf2 acc = gf2_identity();
     for (int j0 = 0; j0 < kJumpG; ++j0) {
-        memcpy(&host[(size_t)j0 * 64], acc.c, sizeof(acc.c));
+        put((size_t)j0, acc);
         acc = gf2_mul(row, acc);
     }
     const Gf2 grp = acc;  // row^16
     Gf2 g = gf2_identity();
     for (int j1 = 0; j1 < n1; ++j1) {
-        memcpy(&host[(size_t)(kJumpG + j1) * 64], g.c, sizeof(g.c));
+        put((size_t)(kJumpG + j1), g);
         g = gf2_mul(grp, g);
     }
     uint64_t* d = nullptr;

@@ -52,7 +52,8 @@ struct DeviceState {
     BmTables* d_tables = nullptr;   // device copy of the small tables
     uint32_t* d_log_exc = nullptr;  // 2 MB bitmaps
     uint32_t* d_cos_exc = nullptr;
-    // Row-start jump tables, one per row length L (normals per row):
+    // Row-start jump tables, one per row length L (normals per row), each
+    // matrix in nibble form (kJumpNib entries):
     // [0,16): M^(2L*j0); [16, 16+n1): M^(2L*16*j1).
     struct Jump {
         int64_t row_len = 0;
