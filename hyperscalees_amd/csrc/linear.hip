@@ -76,25 +76,35 @@ __global__ __launch_bounds__(K1_THREADS) void k_linear_small(LinParams P) {
         __syncthreads();
         const NoiseCtx ctx{tabs, P.log_exc, P.cos_exc};
         const int32_t rc = P.rc;
-        const int32_t nqB = (b + rc - 1) / rc;
-        const int32_t qA0 = (b + o0) / rc, qA1 = (b + o0 + ct + rc - 1) / rc;
-        const int32_t q2 = max(qA0, nqB);
-        const int32_t per = nqB + max(0, qA1 - q2);
+        // Stream rows [f0, f0 + b) are the input-side operand (Bs), rows
+        // [s0, s0 + a) the output-side one (As, only this tile's columns);
+        // sign * sigma / sqrt(r) scales A of the parameter, which is the
+        // output side for do_mm and the input side for do_Tmm.
+        const int32_t f0 = P.tmm ? P.a : 0, s0 = P.tmm ? 0 : b;
+        const float one = 1.0f;
+        const int32_t qF0 = f0 / rc, qF1 = (f0 + b + rc - 1) / rc;
+        const int32_t qS0 = (s0 + o0) / rc, qS1 = (s0 + o0 + ct + rc - 1) / rc;
+        // the tile's output-side groups not already among the input side's
+        const int32_t qX0 = P.tmm ? qS0 : max(qS0, qF1);
+        const int32_t qX1 = P.tmm ? min(qS1, qF0) : qS1;
+        const int32_t nF = qF1 - qF0;
+        const int32_t per = nF + max(0, qX1 - qX0);
         for (int item = tid; item < nm * per; item += K1_THREADS) {
             const int32_t lm = item / per, qi = item % per;
-            const int32_t q = qi < nqB ? qi : q2 + (qi - nqB);
+            const int32_t q = qi < nF ? qF0 + qi : qX0 + (qi - nF);
             float sign;
             const uint64_t seed = member_seed(P.key, P.epoch, P.nreuse, P.tid_lo + m_first + lm, &sign);
             const float sc = sign * P.bs;
+            const float fsc = P.tmm ? sc : one, ssc = P.tmm ? one : sc;
             uint64_t s = row_start_state(seed, q, P.jump);
             const int32_t rows_here = min(rc, P.a + b - q * rc);
             bm_run(s, rows_here * r, ctx, [&](int32_t i, float v) {
                 const int32_t j = q * rc + i / r, c = i % r;
-                if (j < b) {
-                    Bs[(size_t)(lm * r + c) * P.bpitch + j] = MathT<MATH>::cvt(v);
+                if (j >= f0 && j < f0 + b) {
+                    Bs[(size_t)(lm * r + c) * P.bpitch + (j - f0)] = MathT<MATH>::cvt(v * fsc);
                 } else {
-                    const int32_t o = j - b - o0;
-                    if (o >= 0 && o < ct) As[((size_t)lm * K1_CT + o) * r + c] = v * sc;
+                    const int32_t o = j - s0 - o0;
+                    if (o >= 0 && o < ct) As[((size_t)lm * K1_CT + o) * r + c] = v * ssc;
                 }
             });
         }
@@ -121,7 +131,8 @@ __global__ __launch_bounds__(K1_THREADS) void k_linear_small(LinParams P) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int32_t k = k0 + sk + i;
-            wv[i] = MathT<MATH>::cvt((wcol < P.a && k < b) ? P.W[(int64_t)wcol * b + k] : 0.0f);
+            const int64_t wi = P.tmm ? (int64_t)k * P.a + wcol : (int64_t)wcol * b + k;
+            wv[i] = MathT<MATH>::cvt((wcol < P.a && k < b) ? P.W[wi] : 0.0f);
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -313,6 +324,29 @@ static int make_params(LinParams* P, const void* d_x, int32_t x_fmt, int64_t x_s
     return HSES_OK;
 }
 
+// Output checks and the kernel choice shared by do_mm and do_Tmm: the pair
+// kernels (rank a multiple of 16, output width <= 128, bf16) or else the
+// small-rank kernel.
+static int run_linear(LinParams& P, DeviceState* st, float* d_y, int64_t y_stride,
+                      int64_t y_plane, void* d_work, size_t work_bytes, void* stream,
+                      const char* name) {
+    HSES_REQUIRE(d_y, "NULL pointer");
+    HSES_REQUIRE(y_stride >= P.a, "y_stride smaller than a row");
+    HSES_REQUIRE(P.n_time == 1 || y_plane >= (int64_t)P.n * P.rpm * y_stride, "time planes overlap");
+    P.y = d_y;
+    P.y_stride = y_stride;
+    P.y_plane = y_plane;
+    hipStream_t s = (hipStream_t)stream;
+    int rc = launch_linear_pair(P, st, s, d_work, work_bytes);
+    if (rc != HSES_ERR_UNSUPPORTED) return rc;
+    rc = launch_linear_small(P, st, s);
+    if (rc == HSES_ERR_UNSUPPORTED)
+        return set_error(HSES_ERR_UNSUPPORTED,
+                         std::string(name) + ": no kernel for this rank/shape (members per 64-row "
+                         "tile x rank must be <= 64, or rank a multiple of 16)");
+    return rc;
+}
+
 extern "C" int hses_perturbed_linear(const void* d_x, int32_t x_fmt, int64_t x_stride,
                                      int64_t x_plane, int32_t n_time, const float* d_W, int32_t a,
                                      int32_t b, uint64_t key, int32_t rank, float sigma,
@@ -325,22 +359,32 @@ extern "C" int hses_perturbed_linear(const void* d_x, int32_t x_fmt, int64_t x_s
     int rc = make_params(&P, d_x, x_fmt, x_stride, x_plane, n_time, d_W, a, b, key, rank, sigma,
                          epoch, noise_reuse, tid_lo, n, rows_per_member, math, &st);
     if (rc || n == 0) return rc;
-    HSES_REQUIRE(d_y, "NULL pointer");
-    HSES_REQUIRE(y_stride >= a, "y_stride smaller than a row");
-    HSES_REQUIRE(n_time == 1 || y_plane >= (int64_t)n * rows_per_member * y_stride,
-                 "time planes overlap");
-    P.y = d_y;
-    P.y_stride = y_stride;
-    P.y_plane = y_plane;
-    hipStream_t s = (hipStream_t)stream;
-    rc = launch_linear_pair(P, st, s, d_work, work_bytes);
-    if (rc != HSES_ERR_UNSUPPORTED) return rc;
-    rc = launch_linear_small(P, st, s);
-    if (rc == HSES_ERR_UNSUPPORTED)
-        return set_error(HSES_ERR_UNSUPPORTED,
-                         "hses_perturbed_linear: no kernel for this rank/shape (members per "
-                         "64-row tile x rank must be <= 64, or rank a multiple of 16)");
-    return rc;
+    return run_linear(P, st, d_y, y_stride, y_plane, d_work, work_bytes, stream,
+                      "hses_perturbed_linear");
+}
+
+extern "C" size_t hses_perturbed_linear_t_workspace(int32_t a, int32_t b, int32_t rank, int32_t n,
+                                                    int32_t rows_per_member, int32_t n_time,
+                                                    int32_t math) {
+    return hses_perturbed_linear_workspace(b, a, rank, n, rows_per_member, n_time, math);
+}
+
+extern "C" int hses_perturbed_linear_t(const void* d_x, int32_t x_fmt, int64_t x_stride,
+                                       int64_t x_plane, int32_t n_time, const float* d_W,
+                                       int32_t a, int32_t b, uint64_t key, int32_t rank,
+                                       float sigma, int32_t epoch, int32_t noise_reuse,
+                                       int32_t tid_lo, int32_t n, int32_t rows_per_member,
+                                       float* d_y, int64_t y_stride, int64_t y_plane, int32_t math,
+                                       void* d_work, size_t work_bytes, void* stream) {
+    // The kernels' input width is the parameter's a, their output width its b.
+    LinParams P;
+    DeviceState* st = nullptr;
+    int rc = make_params(&P, d_x, x_fmt, x_stride, x_plane, n_time, d_W, b, a, key, rank, sigma,
+                         epoch, noise_reuse, tid_lo, n, rows_per_member, math, &st);
+    if (rc || n == 0) return rc;
+    P.tmm = 1;
+    return run_linear(P, st, d_y, y_stride, y_plane, d_work, work_bytes, stream,
+                      "hses_perturbed_linear_t");
 }
 
 extern "C" int hses_perturbed_linear_lif(const void* d_x, int32_t x_fmt, int64_t x_stride,

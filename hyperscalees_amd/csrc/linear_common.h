@@ -47,6 +47,11 @@ struct LinParams {
     float* y;
     int64_t y_stride, y_plane;
     int32_t math;
+    // 0: do_mm, y = x W^T + (x B) A^T with W (a, b), stream rows B then A.
+    // 1: do_Tmm, y = x W + (x A) B^T for a parameter W of shape (b, a) (x has
+    //    b columns, y has a): the first b stream rows (its B) are the output
+    //    side operand, the next a rows (its A, scaled) the input side.
+    int32_t tmm;
     int32_t R;      // rows per member = n_time * rpm
     int64_t total;  // n * R
     // kernel-specific tiling

@@ -87,7 +87,24 @@ struct K2Args {
     int32_t a, b, r, R, rpm, T, n, tid_lo, pair_lo, n_pairs, epoch, nreuse;
     int32_t segs;   // generation segments per stream row (jump table for row length r / segs)
     int32_t group;  // pairs generated together (k_linear_pair; their A rows share the LDS block)
+    int32_t tmm;    // do_Tmm stream roles (LinParams::tmm)
     float bs, leak, v_th;
+};
+
+// Stream row j of a pair's factor stream: input-side operand row (staged in
+// the slot as [c][k]) or output-side row (LDS, [o][c]), and its scale.
+// do_mm: rows [0, b) input side, [b, a + b) output side scaled by sigma/sqrt(r);
+// do_Tmm: rows [0, a) output side, [a, a + b) input side scaled.
+struct StreamRow {
+    bool in_side;
+    int32_t row;
+    float scale;
+    __device__ __forceinline__ StreamRow(const K2Args& P, int32_t j) {
+        const int32_t f0 = P.tmm ? P.a : 0;
+        in_side = j >= f0 && j < f0 + P.b;
+        row = in_side ? j - f0 : (P.tmm ? j : j - P.b);
+        scale = (in_side == (P.tmm != 0)) ? P.bs : 1.0f;
+    }
 };
 
 // Rows of a block are addressed relative to the block start L0 = m0 * R + q0:
@@ -114,13 +131,15 @@ __device__ __forceinline__ int64_t k2_phys(int32_t m, int32_t q, int32_t rpm, in
     return t * plane + ((int64_t)m * rpm + s) * stride;
 }
 
-// W (a, b) fp32 -> (a, kp) bf16 with zero columns [b, kp).
+// W (a, b) fp32 -> (a, kp) bf16 with zero columns [b, kp); with tmm the
+// parameter is stored (b, a) and is transposed on the way.
 __global__ void k_w_to_bf16(const float* __restrict__ W, int32_t a, int32_t b, int32_t kp,
-                            uint16_t* __restrict__ out) {
+                            int32_t tmm, uint16_t* __restrict__ out) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (int64_t)a * kp) return;
     const int32_t row = (int32_t)(i / kp), k = (int32_t)(i % kp);
-    out[i] = k < b ? f2bf(W[(int64_t)row * b + k]) : (uint16_t)0;
+    const int64_t src = tmm ? (int64_t)k * a + row : (int64_t)row * b + k;
+    out[i] = k < b ? f2bf(W[src]) : (uint16_t)0;
 }
 
 // Eight bits of x (bit e = column k0 + e) as an MFMA operand of 0.0 / 1.0 bf16.
@@ -326,12 +345,13 @@ __global__ __launch_bounds__(K2_THREADS) void k_linear_pair(const K2Args P) {
                 epoch_thread_sign(P.epoch, 2 * (P.pair_lo + pi0 + g * (int32_t)gridDim.x), P.nreuse,
                                   &te, &tt, &sg);
                 uint64_t s = row_start_state(noise_seed(P.key, te, tt), uu, P.jump);
-                if (j < b) {
-                    uint16_t* sg_ = slots + (size_t)g * r * kp;
-                    bm_run(s, sl, ctx, [&](int32_t c, float v) { sg_[(size_t)(c0 + c) * kp + j] = f2bf(v); });
+                const StreamRow sr(P, j);
+                if (sr.in_side) {
+                    uint16_t* sg_ = slots + (size_t)g * r * kp + sr.row;
+                    bm_run(s, sl, ctx, [&](int32_t c, float v) { sg_[(size_t)(c0 + c) * kp] = f2bf(v * sr.scale); });
                 } else {
-                    uint16_t* arow = As + (size_t)(g * a + j - b) * lay.apitch;
-                    bm_run(s, sl, ctx, [&](int32_t c, float v) { arow[c0 + c] = f2bf(v * P.bs); });
+                    uint16_t* arow = As + (size_t)(g * a + sr.row) * lay.apitch;
+                    bm_run(s, sl, ctx, [&](int32_t c, float v) { arow[c0 + c] = f2bf(v * sr.scale); });
                     if (c0 + sl == r)
                         for (int32_t c = r; c < rp32; ++c) arow[c] = 0;
                 }
@@ -624,13 +644,15 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
             for (int32_t u = tid; u < (a + b) * segs; u += K3_THREADS) {
                 const int32_t j = u / segs, c0 = (u - j * segs) * sl;
                 uint64_t s = row_start_state(seed, u, P.jump);
-                if (j < b) {
-                    bm_run(s, sl, ctx, [&](int32_t c, float v) { slot[(size_t)(c0 + c) * kp + j] = f2bf(v); });
+                const StreamRow sr(P, j);
+                if (sr.in_side) {
+                    uint16_t* dst = slot + sr.row;
+                    bm_run(s, sl, ctx, [&](int32_t c, float v) { dst[(size_t)(c0 + c) * kp] = f2bf(v * sr.scale); });
                 } else {
-                    uint16_t* dst = As + (size_t)(j - b) * lay.apitch + c0;
-                    bm_run(s, sl, ctx, [&](int32_t c, float v) { dst[c] = f2bf(v * P.bs); });
+                    uint16_t* dst = As + (size_t)sr.row * lay.apitch + c0;
+                    bm_run(s, sl, ctx, [&](int32_t c, float v) { dst[c] = f2bf(v * sr.scale); });
                     if (c0 + sl == r)
-                        for (int32_t c = r; c < rp32; ++c) As[(size_t)(j - b) * lay.apitch + c] = 0;
+                        for (int32_t c = r; c < rp32; ++c) As[(size_t)sr.row * lay.apitch + c] = 0;
                 }
             }
             __threadfence_block();
@@ -983,9 +1005,10 @@ int launch_linear_pair(LinParams& P, DeviceState* st, hipStream_t s, void* work,
     A.epoch = P.epoch;
     A.nreuse = P.nreuse;
     A.bs = P.bs;
+    A.tmm = P.tmm;
     const int64_t wl = (int64_t)P.a * lay.kp;
     hipLaunchKernelGGL(k_w_to_bf16, dim3((uint32_t)((wl + 255) / 256)), dim3(256), 0, s, P.W, P.a,
-                       P.b, lay.kp, wbf);
+                       P.b, lay.kp, P.tmm, wbf);
     HSES_CHECK_HIP(hipGetLastError());
     auto launch = [&](auto kern) -> int {
         if (lds_bytes > 64 * 1024)

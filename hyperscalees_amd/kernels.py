@@ -172,6 +172,32 @@ def perturbed_linear(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n, rows
     return out if n_time > 1 or x.dim() == 3 else out[0]
 
 
+def perturbed_linear_t(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n, rows_per_member,
+                       x_fmt=FMT_F32, n_time=1, math=MATH_F32, out=None):
+    """Batched do_Tmm: y = x W + (x A_m) B_m^T for W of shape (a, b).  x is
+    (n_time, n*rows_per_member, a) in x_fmt (or 2-D when n_time == 1);
+    returns y (n_time, n*rows_per_member, b) fp32."""
+    a, b = W.shape
+    _dev(W, torch.float32, "W")
+    _dev(x, _FMT_DTYPE[x_fmt], "x")
+    units = fmt_width(x_fmt, a)
+    M = n * rows_per_member
+    if x.shape[-1] != units or x.numel() != n_time * M * units:
+        raise ValueError(f"x has shape {tuple(x.shape)}, expected ({n_time}, {M}, {units})")
+    if out is None:
+        out = torch.empty((n_time, M, b), dtype=torch.float32, device=W.device)
+    _dev(out, torch.float32, "out")
+    if out.numel() != n_time * M * b:
+        raise ValueError("out has the wrong size")
+    wbytes = int(_lib.load().hses_perturbed_linear_t_workspace(a, b, rank, n, rows_per_member,
+                                                                n_time, math))
+    work = _workspace(wbytes, W.device)
+    _lib.call("hses_perturbed_linear_t", _p(x), x_fmt, units, M * units, n_time, _p(W), a, b,
+              key & (2**64 - 1), rank, sigma, epoch, noise_reuse, tid_lo, n, rows_per_member,
+              _p(out), b, M * b, math, _p(work), wbytes, _stream())
+    return out if n_time > 1 or x.dim() == 3 else out[0]
+
+
 def perturbed_linear_lif(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n,
                          rows_per_member, n_time, tau_m, v_th, spikes=None, rate=None,
                          want_spikes=True, want_rate=False):

@@ -149,6 +149,22 @@ int hses_perturbed_linear(const void *d_x, int32_t x_fmt, int64_t x_stride, int6
                           float *d_y, int64_t y_stride, int64_t y_plane, int32_t math,
                           void *d_work, size_t work_bytes, void *stream);
 
+/* EggRoll::do_Tmm / do_Tmm_impl (burn_impl/hyperscalees-noiser/src/eggroll.rs:450-477):
+ *     y_m = x_m W + sign_m * (sigma/sqrt(rank)) * (x_m A_m) B_m^T
+ * for a parameter W of shape (a, b), fp32 row-major: x (n*rows_per_member, a), y (.., b).
+ * A_m (a, r) and B_m (b, r) are the same factors as for do_mm on this (a, b) parameter
+ * (one stream: B rows, then A rows), regenerated in-kernel.  Arguments, layouts, strides
+ * and the workspace rule are those of hses_perturbed_linear with x rows of width a and
+ * y rows of width b; large ranks need b <= 128 (the pair kernels' output width). */
+size_t hses_perturbed_linear_t_workspace(int32_t a, int32_t b, int32_t rank, int32_t n,
+                                         int32_t rows_per_member, int32_t n_time, int32_t math);
+int hses_perturbed_linear_t(const void *d_x, int32_t x_fmt, int64_t x_stride, int64_t x_plane,
+                            int32_t n_time, const float *d_W, int32_t a, int32_t b,
+                            uint64_t key, int32_t rank, float sigma, int32_t epoch,
+                            int32_t noise_reuse, int32_t tid_lo, int32_t n,
+                            int32_t rows_per_member, float *d_y, int64_t y_stride, int64_t y_plane,
+                            int32_t math, void *d_work, size_t work_bytes, void *stream);
+
 /* Perturbed forward fused with the LIF layer that consumes it
  * (forward_batched_lora_half_with_lif, snn.rs:544-595: lora_linear_batched
  * then run_lif, snn.rs:53-97; kernel lif_fused_oxide.rs:37-70).  The currents

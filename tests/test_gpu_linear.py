@@ -208,3 +208,55 @@ def test_fused_lif_matches_unfused(hses_gpu, n, rpm, T, a, b, r, tid_lo):
     spk2, none = hses_gpu.perturbed_linear_lif(xb, Wt, KEY, r, 0.2, 3, 0, tid_lo, n, rpm, T, tau,
                                                vth)
     assert none is None and torch.equal(spk2, spk_ref)
+
+
+def ref_forward_t(x3, W, A, B, rpm):
+    """do_Tmm: x3 (T, n*rpm, a) -> (T, n*rpm, b), x W + (x A_m) B_m^T in float64."""
+    x3 = x3.astype(np.float64)
+    y = x3 @ W.astype(np.float64)
+    for m in range(A.shape[0]):
+        xs = x3[:, m * rpm:(m + 1) * rpm, :]
+        y[:, m * rpm:(m + 1) * rpm, :] += (xs @ A[m].astype(np.float64)) @ B[m].astype(np.float64).T
+    return y
+
+
+@pytest.mark.parametrize("n,rpm,T,a,b,r,tid_lo,math", [
+    (16, 16, 1, 512, 512, 1, 0, MATH_F32),     # C5-like square layer, r = 1
+    (6, 8, 1, 512, 256, 1, 3, MATH_BF16),      # C5 precision, odd first thread id
+    (5, 5, 3, 100, 10, 4, 3, MATH_F32),        # time-major, members straddle tiles, ragged
+    (7, 9, 1, 33, 70, 2, 1, MATH_F32),
+    (4, 32, 1, 96, 128, 16, 0, MATH_BF16),     # pair kernel, rank 16
+    (3, 64, 2, 784, 128, 128, 1, MATH_BF16),   # pair kernel at the C3 rank, half pairs
+])
+def test_perturbed_linear_t(hses_gpu, n, rpm, T, a, b, r, tid_lo, math):
+    # do_Tmm_impl (eggroll.rs:450-477): the same (a, b) parameter stream as
+    # do_mm, with A (scaled) on the input side and B on the output side.
+    rng = np.random.default_rng(n * 31 + a + b + r)
+    x3 = rng.standard_normal((T, n * rpm, a)).astype(np.float32)
+    W = (rng.standard_normal((a, b)) / np.sqrt(a)).astype(np.float32)
+    sigma = 0.2
+    A, B = factors(sigma, r, n, tid_lo, a, b)
+    ref = ref_forward_t(x3, W, A, B, rpm)
+    y = hses_gpu.perturbed_linear_t(torch.from_numpy(x3).cuda(), torch.from_numpy(W).cuda(), KEY,
+                                    r, sigma, 0, 0, tid_lo, n, rpm, n_time=T, math=math)
+    torch.cuda.synchronize()
+    y = y.cpu().numpy().reshape(T, n * rpm, b)
+    assert_close(y, ref, 1e-5 if math == MATH_F32 else 2e-2)
+    if math == MATH_F32:
+        # the oracle's restatement of do_Tmm_impl on member 0's rows at t = 0
+        y0 = np.zeros((rpm, b), np.float32)
+        O.load().or_do_Tmm(np.ascontiguousarray(x3[0, :rpm]), rpm, W, a, b,
+                           np.ascontiguousarray(A[0]).ctypes.data,
+                           np.ascontiguousarray(B[0]).ctypes.data, r, y0)
+        assert_close(y[0, :rpm], y0.astype(np.float64), 1e-5)
+
+
+def test_perturbed_linear_t_clean(hses_gpu):
+    # sigma = 0: the clean x W (do_Tmm_impl without iterinfo)
+    rng = np.random.default_rng(77)
+    x = rng.standard_normal((40, 65)).astype(np.float32)
+    W = rng.standard_normal((65, 33)).astype(np.float32)
+    y = hses_gpu.perturbed_linear_t(torch.from_numpy(x).cuda(), torch.from_numpy(W).cuda(), KEY,
+                                    4, 0.0, 0, 0, 0, 40, 1)
+    torch.cuda.synchronize()
+    assert_close(y.cpu().numpy(), x.astype(np.float64) @ W.astype(np.float64), 1e-5)

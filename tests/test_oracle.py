@@ -213,6 +213,23 @@ def test_do_tmm_known_answer(oracle):
     np.testing.assert_array_equal(y.ravel(), [6, 15])
 
 
+def test_do_tmm_is_do_mm_transposed(oracle):
+    # x W + (x A) B^T == do_mm(x; W^T, with B as the output-side and A as the
+    # input-side factor): ties the LoRA term of do_Tmm to the pinned do_mm.
+    # Integer-valued operands keep every product exact in f32.
+    rng = np.random.default_rng(3)
+    a, b, r, rows = 5, 4, 2, 3
+    x = rng.integers(-3, 4, (rows, a)).astype(np.float32)
+    W = rng.integers(-3, 4, (a, b)).astype(np.float32)
+    A = rng.integers(-3, 4, (a, r)).astype(np.float32)
+    B = rng.integers(-3, 4, (b, r)).astype(np.float32)
+    y = np.zeros((rows, b), np.float32)
+    oracle.or_do_Tmm(x, rows, W, a, b, A.ctypes.data, B.ctypes.data, r, y)
+    np.testing.assert_array_equal(y, O.do_mm(x, np.ascontiguousarray(W.T), B, A))
+    np.testing.assert_array_equal(y, x @ W + (x @ A) @ B.T)
+    assert not np.array_equal(y, x @ W)  # the LoRA term is not zero here
+
+
 def test_do_mm_noise_matches_brute_force():
     rng = np.random.default_rng(3)
     x = rng.standard_normal((7, 11)).astype(np.float32)
