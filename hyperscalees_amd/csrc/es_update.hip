@@ -23,9 +23,10 @@
 //     the current one.
 //   k_es_partial (r < 32): 128x128 tiles, 256 threads; several short stream
 //     rows per thread.
-// Stage 2 (k_es_reduce): each output element sums its partials in split
-// order in double, scales, and stores (or adds).  The split count depends on
-// the problem shape only, so the result is independent of the device.
+// Stage 2 (k_es_reduce): each output element sums its partials in double in
+// a fixed order (four split ranges, each in four interleaved sums), scales,
+// and stores (or adds).  The split count depends on the problem shape only,
+// so the result is independent of the device.
 #include <math.h>
 
 #include "mfma.h"
@@ -386,17 +387,38 @@ __global__ __launch_bounds__(R_MAXT) void k_es_rows(UpdParams P, RowTiles G) {
     }
 }
 
+// 64 output elements per 256-thread block: wave w sums the partials of splits
+// [w * splits / 4, (w + 1) * splits / 4) of element 64 * block + lane with four
+// interleaved double accumulators, and the four waves' sums are added in wave
+// order.  The association is fixed by the shape alone.
 // inv_s: 1/S of k_es_rows' scaled partials (a power of two), or NULL.
-__global__ void k_es_reduce(const float* __restrict__ work, int32_t splits, int64_t len, float scale,
-                            const float* __restrict__ inv_s, int32_t accumulate,
-                            float* __restrict__ g) {
-    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= len) return;
-    double s = 0.0;
-    for (int32_t k = 0; k < splits; ++k) s += (double)work[(size_t)k * len + e];
-    if (inv_s) s *= (double)inv_s[0];
-    const float v = (float)s * scale;
-    g[e] = accumulate ? g[e] + v : v;
+__global__ __launch_bounds__(256) void k_es_reduce(const float* __restrict__ work, int32_t splits,
+                                                   int64_t len, float scale,
+                                                   const float* __restrict__ inv_s,
+                                                   int32_t accumulate, float* __restrict__ g) {
+    __shared__ double part[4][64];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int64_t e = (int64_t)blockIdx.x * 64 + lane;
+    const int64_t ec = e < len ? e : len - 1;  // in bounds; discarded below
+    const int32_t k0 = (int32_t)((int64_t)splits * w / 4), k1 = (int32_t)((int64_t)splits * (w + 1) / 4);
+    const float* src = work + ec;
+    double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
+    int32_t k = k0;
+    for (; k + 4 <= k1; k += 4) {
+        s0 += (double)src[(size_t)k * len];
+        s1 += (double)src[(size_t)(k + 1) * len];
+        s2 += (double)src[(size_t)(k + 2) * len];
+        s3 += (double)src[(size_t)(k + 3) * len];
+    }
+    for (; k < k1; ++k) s0 += (double)src[(size_t)k * len];
+    part[w][lane] = (s0 + s1) + (s2 + s3);
+    __syncthreads();
+    if (w == 0 && e < len) {
+        double s = (part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]);
+        if (inv_s) s *= (double)inv_s[0];
+        const float v = (float)s * scale;
+        g[e] = accumulate ? g[e] + v : v;
+    }
 }
 
 // Split count: ~1024 workgroups in total, at least 8 pairs per split, at most 512 splits.
@@ -556,7 +578,7 @@ extern "C" int hses_es_update(const float* d_f, int32_t n, int32_t tid_lo, uint6
         HSES_CHECK_HIP(hipGetLastError());
     }
     const int64_t len = (int64_t)a * b;
-    hipLaunchKernelGGL(k_es_reduce, dim3((uint32_t)((len + 255) / 256)), dim3(256), 0, s, P.work,
+    hipLaunchKernelGGL(k_es_reduce, dim3((uint32_t)((len + 63) / 64)), dim3(256), 0, s, P.work,
                        P.splits, len, scale, rows_k ? d_scale + 1 : nullptr, accumulate, d_grad);
     HSES_CHECK_HIP(hipGetLastError());
     return HSES_OK;

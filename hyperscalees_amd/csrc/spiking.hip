@@ -280,14 +280,25 @@ __global__ __launch_bounds__(256) void k_lif(const float* __restrict__ cur,
     const bool valid = col < h;
     float v = (valid && v0) ? v0[row * h + col] : 0.0f;
     const int64_t cplane = rows * cur_stride, splane = rows * spk_stride;
-    const float* cp = cur + row * cur_stride + col;
-    for (int32_t t = 0; t < T; ++t) {
-        const float c = valid ? cp[t * cplane] : 0.0f;
-        // snn.rs:61-63: charged = v + ((-v) + c) * leak; each op rounds.
-        const float charged = __fadd_rn(v, __fmul_rn(__fadd_rn(-v, c), leak));
-        const bool spike = charged >= v_th;
-        v = __fmul_rn(charged, __fadd_rn(spike ? -1.0f : -0.0f, 1.0f));
-        store_spike<FMT>(spk, t * splane + row * spk_stride, word, col, valid, spike);
+    // lanes past the row read its last column (discarded): every load is in
+    // bounds and unconditional, so a batch of LB steps' loads is in flight at once
+    const float* cp = cur + row * cur_stride + (valid ? col : h - 1);
+    constexpr int LB = 16;
+    for (int32_t t0 = 0; t0 < T; t0 += LB) {
+        float cb[LB];
+#pragma unroll
+        for (int i = 0; i < LB; ++i) cb[i] = cp[(int64_t)min(t0 + i, T - 1) * cplane];
+#pragma unroll
+        for (int i = 0; i < LB; ++i) {
+            const int32_t t = t0 + i;
+            if (t >= T) break;  // uniform
+            const float c = valid ? cb[i] : 0.0f;
+            // snn.rs:61-63: charged = v + ((-v) + c) * leak; each op rounds.
+            const float charged = __fadd_rn(v, __fmul_rn(__fadd_rn(-v, c), leak));
+            const bool spike = charged >= v_th;
+            v = __fmul_rn(charged, __fadd_rn(spike ? -1.0f : -0.0f, 1.0f));
+            store_spike<FMT>(spk, t * splane + row * spk_stride, word, col, valid, spike);
+        }
     }
     if (valid && v_out) v_out[row * h + col] = v;
 }

@@ -1,0 +1,76 @@
+"""Standalone timing of the HBM-streaming kernels at the C3 shapes.
+
+  * LIF scan (hses_lif_scan): currents (T=16, M=524288, h=128) fp32 ->
+    bit-packed spikes, and -> fp32 spikes;
+  * Poisson encode (hses_poisson_encode): p (M=524288, 784) fp32 with 70% exact
+    zeros -> bit-packed spikes (T=16), and -> fp32 spikes for T=4.
+Each case runs --reps times after a warm-up, timed with events on the launch
+stream; the median is reported with the algorithmic bytes (inputs read once,
+outputs written once) and the fraction of the 8 TB/s HBM peak, one JSON line
+per case.  Also a profiling target:
+    rocprofv3 --kernel-trace --stats -d OUT -- python3 -m hyperscalees_amd.profile_kernels
+"""
+import argparse
+import json
+
+import torch
+
+from . import kernels as K
+
+PEAK_HBM_GBPS = 8000.0
+
+
+def timed(fn, reps):
+    fn()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        fn()
+        e1.record()
+        torch.cuda.synchronize()
+        ts.append(e0.elapsed_time(e1))
+    ts.sort()
+    return ts[len(ts) // 2]
+
+
+def report(name, ms, nbytes, **extra):
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    line = {"kernel": name, "ms": round(ms, 4), "algorithmic_bytes": int(nbytes),
+            "GBps": round(gbps, 1), "hbm_frac": round(gbps / PEAK_HBM_GBPS, 4)}
+    line.update(extra)
+    print(json.dumps(line), flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--reps", type=int, default=20)
+    args = ap.parse_args()
+    K.init(0)
+    g = torch.Generator(device="cuda").manual_seed(0)
+    T, M, h, d = 16, 8192 * 64, 128, 784
+
+    cur = torch.randn((T, M, h), device="cuda", generator=g) * 0.6 + 0.35
+    for fmt, name, out_b in ((K.FMT_BITS, "lif_scan f32 -> bits", T * M * 2 * 8),
+                             (K.FMT_F32, "lif_scan f32 -> f32", T * M * h * 4)):
+        spk = torch.empty((T, M, K.fmt_width(fmt, h)), dtype=K._FMT_DTYPE[fmt], device="cuda")
+        ms = timed(lambda: K.lif_scan(cur, 10.0, 1.0, fmt=fmt, out=spk), args.reps)
+        report(name, ms, T * M * h * 4 + out_b, shape=[T, M, h])
+    del cur, spk
+
+    p = torch.rand((M, d), device="cuda", generator=g)
+    p[torch.rand((M, d), device="cuda", generator=g) < 0.7] = 0.0
+    bits = torch.empty((T, M, K.fmt_width(K.FMT_BITS, d)), dtype=torch.int64, device="cuda")
+    ms = timed(lambda: K.poisson_encode(p, T, (1, 2, 3, 4), K.FMT_BITS, out=bits), args.reps)
+    report("poisson_encode -> bits", ms, M * d * 4 + T * M * bits.shape[2] * 8, shape=[T, M, d],
+           zero_frac=0.7)
+    T4 = 4
+    f32 = torch.empty((T4, M, d), dtype=torch.float32, device="cuda")
+    ms = timed(lambda: K.poisson_encode(p, T4, (1, 2, 3, 4), K.FMT_F32, out=f32), args.reps)
+    report("poisson_encode -> f32", ms, M * d * 4 + T4 * M * d * 4, shape=[T4, M, d],
+           zero_frac=0.7)
+
+
+if __name__ == "__main__":
+    main()
