@@ -88,6 +88,7 @@ struct K2Args {
     int32_t segs;   // generation segments per stream row (jump table for row length r / segs)
     int32_t group;  // pairs generated together (k_linear_pair; their A rows share the LDS block)
     int32_t tmm;    // do_Tmm stream roles (LinParams::tmm)
+    int32_t x_vec;  // dense x: strides keep 8-element groups 16-byte aligned
     float bs, leak, v_th;
 };
 
@@ -160,10 +161,41 @@ __device__ __forceinline__ u16x8 expand_bits(uint32_t byte) {
     return v;
 }
 
-// Eight activations of one row from a dense format, as bf16.
+// Eight activations of one row from a dense format, as bf16.  With vec
+// (strides that keep every 8-element group 16-byte aligned) a full group is
+// two (f32) or one (bf16) 16-byte loads, issued unconditionally (rows outside
+// the block address row 0) and masked after; otherwise, and for the group
+// crossing b, element by element.
 template <int XFMT>
 __device__ __forceinline__ u16x8 dense_frag(const void* x, int64_t off, bool valid, int32_t k0,
-                                            int32_t b) {
+                                            int32_t b, bool vec) {
+    if constexpr (XFMT == HSES_FMT_F32 || XFMT == HSES_FMT_BF16) {
+        if (vec && k0 + 8 <= b) {
+            uint32_t d[4];
+            if constexpr (XFMT == HSES_FMT_F32) {
+                const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(x) + off + k0);
+                const float4 lo = p[0], hi = p[1];
+                d[0] = pack_bf16x2(lo.x, lo.y);
+                d[1] = pack_bf16x2(lo.z, lo.w);
+                d[2] = pack_bf16x2(hi.x, hi.y);
+                d[3] = pack_bf16x2(hi.z, hi.w);
+            } else {
+                const uint4 q = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + off + k0);
+                d[0] = q.x;
+                d[1] = q.y;
+                d[2] = q.z;
+                d[3] = q.w;
+            }
+            const uint32_t m = valid ? 0xffffffffu : 0u;
+            u16x8 v;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                v[2 * q] = (uint16_t)(d[q] & m);
+                v[2 * q + 1] = (uint16_t)((d[q] & m) >> 16);
+            }
+            return v;
+        }
+    }
     u16x8 v;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -283,9 +315,12 @@ __device__ __forceinline__ uint4 mask4(uint4 v, uint32_t m) {
 }
 
 // EPI: EPI_Y stores y; EPI_LIF + T (a power of two <= 64) runs the fused LIF.
-template <int XFMT, int EPI, int LT = 1>
+// WJ: 16-column W tiles per wave (4 cover a <= 128; 1 suffices for a <= 16,
+// e.g. a readout, and frees the registers of the other three).
+template <int XFMT, int EPI, int LT = 1, int WJ = 4>
 __global__ __launch_bounds__(K2_THREADS) void k_linear_pair(const K2Args P) {
     constexpr bool BITS = XFMT == HSES_FMT_BITS;
+    static_assert(WJ >= 1 && WJ <= 4 && (EPI == EPI_Y || WJ == 4), "WJ < 4 only with EPI_Y");
     extern __shared__ __align__(16) unsigned char smem[];
     const K2Layout lay(P.r, P.b, BITS);
     BmTables* tabs = reinterpret_cast<BmTables*>(smem);
@@ -372,11 +407,11 @@ __global__ __launch_bounds__(K2_THREADS) void k_linear_pair(const K2Args P) {
 
         // ---- 2./3. row blocks ----------------------------------------------------
         for (int64_t L0 = row_lo; L0 < row_hi; L0 += K2_RB) {
-            f32x4 acc[4][8];
+            f32x4 acc[4][WJ + 4];  // [row group][W tiles, then 4 rank-column tiles of B]
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0, 0, 0, 0};
+                for (int j = 0; j < WJ + 4; ++j) acc[i][j] = f32x4{0, 0, 0, 0};
 
             RowCursor cur_rows;
             cur_rows.m0 = (int32_t)(L0 / R);
@@ -428,13 +463,14 @@ __global__ __launch_bounds__(K2_THREADS) void k_linear_pair(const K2Args P) {
                             const uint32_t w = Xbits32[(wr * 64 + i * 16 + li) * (2 * nkt) + 2 * kt + s];
                             xa[i] = expand_bits((w >> (8 * kg)) & 0xffu);
                         } else {
-                            xa[i] = dense_frag<XFMT>(P.x, xoff[i], xval[i], kt * K2_BK + s * 32 + kg * 8, b);
+                            xa[i] = dense_frag<XFMT>(P.x, xoff[i], xval[i], kt * K2_BK + s * 32 + kg * 8, b,
+                                                     P.x_vec != 0);
                         }
                     }
                     // absent columns are staged as zeros: no guards, straight-line MFMAs
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        const int col = (j < 4 ? 0 : K2_NMAX) + h * 64 + (j & 3) * 16 + li;
+                    for (int j = 0; j < WJ + 4; ++j) {
+                        const int col = (j < WJ ? h * 64 + j * 16 : K2_NMAX + h * 64 + (j - WJ) * 16) + li;
                         const u16x8 bw = lds_u16x8(tb + col * K2_TP + s * 32 + kg * 8);
 #pragma unroll
                         for (int i = 0; i < 4; ++i) acc[i][j] = mfma_bf16(xa[i], bw, acc[i][j]);
@@ -460,7 +496,7 @@ __global__ __launch_bounds__(K2_THREADS) void k_linear_pair(const K2Args P) {
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
                         const int c = h * 64 + j * 16 + li;
-                        if (h * 64 + j * 16 < r) XBs[row * lay.apitch + c] = f2bf(sgn * acc[i][4 + j][v]);
+                        if (h * 64 + j * 16 < r) XBs[row * lay.apitch + c] = f2bf(sgn * acc[i][WJ + j][v]);
                     }
                 }
             if (rp32 != r) {  // K tail of the second product
@@ -475,7 +511,7 @@ __global__ __launch_bounds__(K2_THREADS) void k_linear_pair(const K2Args P) {
                 for (int i = 0; i < 4; ++i)
                     xf[i] = lds_u16x8(&XBs[(wr * 64 + i * 16 + li) * lay.apitch + c0 + kg * 8]);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
+                for (int j = 0; j < WJ; ++j) {
                     if (h * 64 + j * 16 >= a) continue;
                     const u16x8 af = lds_u16x8(&Ag[(h * 64 + j * 16 + li) * lay.apitch + c0 + kg * 8]);
 #pragma unroll
@@ -493,7 +529,7 @@ __global__ __launch_bounds__(K2_THREADS) void k_linear_pair(const K2Args P) {
                         cur_rows.at(row, R, &m, &q);
                         float* yrow = P.y + k2_phys(m, q, P.rpm, P.T, P.y_stride, P.y_plane);
 #pragma unroll
-                        for (int j = 0; j < 4; ++j) {
+                        for (int j = 0; j < WJ; ++j) {
                             const int col = h * 64 + j * 16 + li;
                             if (col < a) yrow[col] = acc[i][j][v];
                         }
@@ -1006,6 +1042,13 @@ int launch_linear_pair(LinParams& P, DeviceState* st, hipStream_t s, void* work,
     A.nreuse = P.nreuse;
     A.bs = P.bs;
     A.tmm = P.tmm;
+    {
+        // 8 consecutive elements of a row start 16-byte aligned when the base,
+        // the row stride and the plane stride all keep them so
+        const int64_t g = P.x_fmt == HSES_FMT_F32 ? 4 : 8;  // elements per 16 bytes
+        A.x_vec = (reinterpret_cast<uintptr_t>(P.x) % 16 == 0) && P.x_stride % g == 0 &&
+                  P.x_plane % g == 0;
+    }
     const int64_t wl = (int64_t)P.a * lay.kp;
     hipLaunchKernelGGL(k_w_to_bf16, dim3((uint32_t)((wl + 255) / 256)), dim3(256), 0, s, P.W, P.a,
                        P.b, lay.kp, P.tmm, wbf);
@@ -1047,8 +1090,12 @@ int launch_linear_pair(LinParams& P, DeviceState* st, hipStream_t s, void* work,
         }
     }
     switch (P.x_fmt) {
-        case HSES_FMT_F32: return launch(k_linear_pair<HSES_FMT_F32, EPI_Y>);
-        case HSES_FMT_BF16: return launch(k_linear_pair<HSES_FMT_BF16, EPI_Y>);
+        case HSES_FMT_F32:
+            return P.a <= 16 ? launch(k_linear_pair<HSES_FMT_F32, EPI_Y, 1, 1>)
+                             : launch(k_linear_pair<HSES_FMT_F32, EPI_Y>);
+        case HSES_FMT_BF16:
+            return P.a <= 16 ? launch(k_linear_pair<HSES_FMT_BF16, EPI_Y, 1, 1>)
+                             : launch(k_linear_pair<HSES_FMT_BF16, EPI_Y>);
         default: return launch(k_linear_pair<HSES_FMT_BITS, EPI_Y>);
     }
 }

@@ -142,6 +142,7 @@ def ref_forward_bf16(x3, W, A, B, rpm):
     (4, 64, 1, 10, 128, 128, 0, FMT_F32),      # C3 readout on rates
     (2, 40, 3, 96, 200, 64, 0, FMT_BF16),      # rows not a multiple of the block
     (5, 7, 2, 33, 50, 16, 2, FMT_F32),
+    (3, 20, 2, 16, 96, 32, 1, FMT_BF16),       # a = 16: one W column tile per wave
 ])
 def test_perturbed_linear_pair_kernel(hses_gpu, n, rpm, T, a, b, r, tid_lo, fmt):
     rng = np.random.default_rng(n * 1000 + a + r)
@@ -227,6 +228,7 @@ def ref_forward_t(x3, W, A, B, rpm):
     (7, 9, 1, 33, 70, 2, 1, MATH_F32),
     (4, 32, 1, 96, 128, 16, 0, MATH_BF16),     # pair kernel, rank 16
     (3, 64, 2, 784, 128, 128, 1, MATH_BF16),   # pair kernel at the C3 rank, half pairs
+    (5, 8, 1, 64, 12, 16, 1, MATH_BF16),       # pair kernel, output width <= 16
 ])
 def test_perturbed_linear_t(hses_gpu, n, rpm, T, a, b, r, tid_lo, math):
     # do_Tmm_impl (eggroll.rs:450-477): the same (a, b) parameter stream as
