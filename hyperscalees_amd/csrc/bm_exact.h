@@ -34,7 +34,8 @@ namespace hses {
 // Table sizes.
 constexpr int kLogTab = 128;          // subintervals of the reduced argument z in [0.75, 1.5)
 constexpr int kCosTab = 64;           // angle grid j * 2pi / 64, j = 0..64
-constexpr int kBuckets = 256;         // danger-threshold buckets: k >> 16
+constexpr int kBucketShift = 17;      // danger-threshold buckets: k >> kBucketShift
+constexpr int kBuckets = 1 << (24 - kBucketShift);
 constexpr uint32_t kUnitCount = 1u << 24;
 constexpr uint32_t kBitmapWords = kUnitCount / 32;
 // Bitmaps are stored with 64 zero words appended: lanes without a danger test

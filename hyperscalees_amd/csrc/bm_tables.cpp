@@ -136,7 +136,7 @@ std::string build_bm_tables(HostBmTables* out, int nthreads) {
         for (auto& p : parts)
             for (const Exc& x : p) {
                 bm[x.k >> 5] |= 1u << (x.k & 31);
-                by_bucket[x.k >> 16].push_back(x);
+                by_bucket[x.k >> kBucketShift].push_back(x);
                 ++n;
             }
         DangerWin* tw = kind == 0 ? out->small.log_dw : out->small.cos_dw;

@@ -47,7 +47,7 @@ __device__ __forceinline__ float sqrt_rn(float s) {
 __device__ __forceinline__ float bm_logf(uint32_t k1, const BmTables& t, const uint32_t* exc) {
     const double y = log_f64(log_arg(k1), t.log_invc, t.log_logc);
     float f = (float)y;
-    if (in_danger(y, t.log_dw[k1 >> 16]) && ((exc[k1 >> 5] >> (k1 & 31)) & 1u))
+    if (in_danger(y, t.log_dw[k1 >> kBucketShift]) && ((exc[k1 >> 5] >> (k1 & 31)) & 1u))
         f = other_candidate(f, rem29(y));
     return f;
 }
@@ -56,7 +56,7 @@ __device__ __forceinline__ float bm_logf(uint32_t k1, const BmTables& t, const u
 __device__ __forceinline__ float bm_cosf(uint32_t k2, const BmTables& t, const uint32_t* exc) {
     const double y = cos_f64(cos_arg(k2), k2, t.cos_c, t.cos_s, t.cos_thi, t.cos_tlo);
     float f = (float)y;
-    if (in_danger(y, t.cos_dw[k2 >> 16]) && ((exc[k2 >> 5] >> (k2 & 31)) & 1u))
+    if (in_danger(y, t.cos_dw[k2 >> kBucketShift]) && ((exc[k2 >> 5] >> (k2 & 31)) & 1u))
         f = other_candidate(f, rem29(y));
     return f;
 }
@@ -109,8 +109,8 @@ __device__ __forceinline__ void bm_stage1(uint64_t& s, BmPending<G>& p, const No
         p.fc[i] = (float)yc;
         p.rl[i] = rem29(yl);
         p.rc[i] = rem29(yc);
-        dl[i] = in_danger_r(p.rl[i], t.log_dw[p.k1[i] >> 16]);
-        dc[i] = in_danger_r(p.rc[i], t.cos_dw[p.k2[i] >> 16]);
+        dl[i] = in_danger_r(p.rl[i], t.log_dw[p.k1[i] >> kBucketShift]);
+        dc[i] = in_danger_r(p.rc[i], t.cos_dw[p.k2[i] >> kBucketShift]);
     }
     if constexpr (PIPE) {
         // Every lane loads (lanes out of danger read the zero word past the
