@@ -60,6 +60,9 @@ PROTOTYPES = {
     "hses_fitness_moments": (ctypes.c_int, [c_vp, c_i32, c_vp, c_i32, c_vp]),
     "hses_combine_affine": (ctypes.c_int, [c_vp, c_vp, c_vp, c_i32, c_i64, c_vp, c_vp]),
     "hses_convert_fitnesses": (ctypes.c_int, [c_vp, c_i32, c_i32, c_vp, c_vp, c_vp]),
+    "hses_read_idx_images": (ctypes.c_int, [c_vp, c_size, c_vp, c_i64, c_vp, c_vp]),
+    "hses_read_idx_labels": (ctypes.c_int, [c_vp, c_size, c_vp, c_i64, c_vp]),
+    "hses_shuffled_indices": (ctypes.c_int, [c_i64, c_i64, c_u64, c_vp]),
     "hses_solver_step": (ctypes.c_int, [c_i32, c_f32, c_f32, c_f32, c_f32, c_f32, c_i32, c_vp,
                                         c_vp, c_vp, c_vp, c_i64, c_vp]),
 }

@@ -234,6 +234,25 @@ int hses_fitness_moments(const float *d_raw, int32_t n, double *d_moments, int32
 int hses_combine_affine(const float *d_grad_acc, const float *d_ones_acc, const double *d_moments,
                         int32_t batch, int64_t len, float *d_out, void *stream);
 
+/* ---- data path (host only: no device, no stream) ---------------------- */
+
+/* read_idx_images (burn_impl/hyperscalees-envs/src/snn_mnist.rs:57-88): an IDX images
+ * buffer, plain or gzip (leading 1f 8b), into pixels / 255 as f32, image-major.
+ * *n_images and *pixels (rows * cols) are always set; out (may be NULL: sizes only)
+ * must hold out_cap >= n_images * pixels floats.  Bad magic, a short payload, sizes
+ * beyond 2^30 elements or a corrupt gzip stream return HSES_ERR_INVALID_ARG. */
+int hses_read_idx_images(const uint8_t *data, size_t len, float *out, int64_t out_cap,
+                         int64_t *n_images, int64_t *pixels);
+/* read_idx_labels (snn_mnist.rs:90-112): an IDX labels buffer (plain or gzip) into
+ * raw bytes; *n_labels always set, out (may be NULL) must hold out_cap >= n_labels. */
+int hses_read_idx_labels(const uint8_t *data, size_t len, uint8_t *out, int64_t out_cap,
+                         int64_t *n_labels);
+/* shuffled_indices (burn_impl/hyperscalees/src/bin/accumulate_train.rs:157-174): the first
+ * `count` entries of a partial Fisher-Yates shuffle of [0, n) driven by xorshift64
+ * (13, 7, 17) from (seed ^ 0x9E3779B97F4A7C15) | 1, each draw multiplied by
+ * 0x2545F4914F6CDD1D and reduced mod (n - i).  Requires 0 <= count <= n. */
+int hses_shuffled_indices(int64_t n, int64_t count, uint64_t seed, int64_t *out);
+
 /* convert_fitnesses (eggroll.rs:967-992): global (group_size 0) or per-group
  * z-score with the global std.  d_stats (optional) receives {mean, std}. */
 int hses_convert_fitnesses(const float *d_raw, int32_t n, int32_t group_size, float *d_out,
