@@ -28,7 +28,7 @@ PEAK_HBM_GBPS = 8000.0
 # HBM bytes per fc1 launch from two rocprofv3 PMC runs (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0,
 # factors from a 1 GiB copy) of `python3 -m hyperscalees_amd.profile_fc1`;
 # see profiles/fc1_c3_traffic.md.  Refreshed whenever the kernel changes.
-FC1_TRAFFIC_BYTES = 9.35e9
+FC1_TRAFFIC_BYTES = 9.43e9
 
 
 def layer_flops(cfg, l):
