@@ -569,10 +569,18 @@ constexpr int K3_THREADS = 512, K3_RB = 256;
 // (at most K3_XPF of them: rows of up to 2 * K3_XPF words, b <= 1024; wider
 // inputs use k_linear_pair).
 constexpr int K3_XPF = 8;
-// A pitch in bf16 (r <= 128 padded to 128, plus 12 so rows 32 apart fall on
-// different LDS banks); a compile-time constant keeps the second product's
-// LDS addresses immediate offsets of one base.
-constexpr int K3_AP = K2_NMAX + 12;
+// A pitch in bf16: r <= 128 padded to 128, plus 8, so rows start 16-byte
+// aligned and the 16 rows of a quarter-wave's 16-byte reads (row stride 68
+// dwords) cover distinct banks; a compile-time constant keeps the second
+// product's LDS addresses immediate offsets of one base.
+constexpr int K3_AP = K2_NMAX + 8;
+
+// Rank column c of A is stored at column swap23(c) (bits 2 and 3 exchanged):
+// the 8 rank columns one lane feeds to a 16-deep MFMA step, {0..3, 8..11} +
+// 4 * k-group, then sit at 8 contiguous columns 8 * k-group.
+__device__ __forceinline__ int32_t swap23(int32_t c) {
+    return (c & ~12) | ((c & 4) << 1) | ((c & 8) >> 1);
+}
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
@@ -685,10 +693,10 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
                     uint16_t* dst = slot + sr.row;
                     bm_run(s, sl, ctx, [&](int32_t c, float v) { dst[(size_t)(c0 + c) * kp] = f2bf(v * sr.scale); });
                 } else {
-                    uint16_t* dst = As + (size_t)sr.row * lay.apitch + c0;
-                    bm_run(s, sl, ctx, [&](int32_t c, float v) { dst[c] = f2bf(v * sr.scale); });
-                    if (c0 + sl == r)
-                        for (int32_t c = r; c < rp32; ++c) As[(size_t)sr.row * lay.apitch + c] = 0;
+                    uint16_t* dst = As + (size_t)sr.row * lay.apitch;
+                    bm_run(s, sl, ctx, [&](int32_t c, float v) { dst[swap23(c0 + c)] = f2bf(v * sr.scale); });
+                    if (c0 + sl == r)  // r is a multiple of 16: the padding maps onto itself
+                        for (int32_t c = r; c < rp32; ++c) dst[c] = 0;
                 }
             }
             __threadfence_block();
@@ -812,22 +820,22 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
                 K3_TILE_LOAD(0);
             }
             // accW += (sign xB) A^T over K = r in steps of 16: step (j, t) gives
-            // k-group hl the rank columns 32j + 16t + 4hl + {0..3, 8..11}.
-            const uint16_t* abase = As + (size_t)lc * K3_AP + 4 * hl;
+            // k-group hl the rank columns 32j + 16t + 4hl + {0..3, 8..11}, stored
+            // (swap23) as the 8 columns 32j + 16t + 8hl.
+            const uint16_t* abase = As + (size_t)lc * K3_AP + 8 * hl;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 if (32 * j >= rp32) break;
                 // the 16 A reads of this rank tile, then its 8 MFMAs (absent
                 // output tiles, 32 jo >= a, read row lc of tile 0; their columns
                 // are never stored)
-                uint2 af[2][4][2];
+                uint4 af[2][4];
 #pragma unroll
                 for (int t = 0; t < 2; ++t)
 #pragma unroll
                     for (int jo = 0; jo < 4; ++jo) {
                         const uint16_t* ap = abase + (32 * jo < a ? 32 * jo * K3_AP : 0) + 32 * j + 16 * t;
-                        af[t][jo][0] = *reinterpret_cast<const uint2*>(ap);
-                        af[t][jo][1] = *reinterpret_cast<const uint2*>(ap + 8);
+                        af[t][jo] = *reinterpret_cast<const uint4*>(ap);
                     }
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -836,11 +844,8 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
                                            xbf[j][2 * t + 1][1]};
                     const u16x8 xo = __builtin_bit_cast(u16x8, d);
 #pragma unroll
-                    for (int jo = 0; jo < 4; ++jo) {
-                        const uint32_t e[4] = {af[t][jo][0].x, af[t][jo][0].y, af[t][jo][1].x,
-                                               af[t][jo][1].y};
-                        accW[jo] = mfma32_bf16(xo, __builtin_bit_cast(u16x8, e), accW[jo]);
-                    }
+                    for (int jo = 0; jo < 4; ++jo)
+                        accW[jo] = mfma32_bf16(xo, __builtin_bit_cast(u16x8, af[t][jo]), accW[jo]);
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }

@@ -223,7 +223,8 @@ __global__ __launch_bounds__(256) void k_poisson_sparse(
 
     // B. the streams of the active elements
     for (int32_t e = lane; e < cnt; e += 64) {
-        const uint32_t col = list[e], K = pat[col];
+        const uint32_t col = list[e];
+        const uint32_t K9 = pat[col] << 9;  // (x >> 9) < K  <=>  x < K * 2^9 for K < 2^23
         uint32_t x = 1000000007u * (idx0 + col) + mix + 0x9E3779B9u;
         uint32_t pt = 0;
 #pragma unroll
@@ -231,7 +232,7 @@ __global__ __launch_bounds__(256) void k_poisson_sparse(
             x ^= x << 13;
             x ^= x >> 17;
             x ^= x << 5;
-            pt |= ((x >> 9) < K ? 1u : 0u) << t;
+            pt |= (x < K9 ? 1u : 0u) << t;
         }
         pat[col] = pt;
     }
