@@ -60,6 +60,14 @@ PROTOTYPES = {
     "hses_fitness_moments": (ctypes.c_int, [c_vp, c_i32, c_vp, c_i32, c_vp]),
     "hses_combine_affine": (ctypes.c_int, [c_vp, c_vp, c_vp, c_i32, c_i64, c_vp, c_vp]),
     "hses_convert_fitnesses": (ctypes.c_int, [c_vp, c_i32, c_i32, c_vp, c_vp, c_vp]),
+    "hses_layer_norm": (ctypes.c_int, [c_vp, c_i64, c_i32, c_vp, c_vp, c_f32, c_vp, c_vp]),
+    "hses_group_norm": (ctypes.c_int, [c_vp, c_i64, c_i32, c_i32, c_i32, c_vp, c_vp, c_f32, c_vp,
+                                       c_vp]),
+    "hses_token_shift_mix": (ctypes.c_int, [c_vp, c_vp, c_vp, c_vp, c_i32, c_i64, c_i32, c_i32,
+                                            c_vp, c_vp]),
+    "hses_relu_sq": (ctypes.c_int, [c_vp, c_i64, c_vp]),
+    "hses_rwkv7_wkv": (ctypes.c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i32,
+                                      c_i32, c_i32, c_i32, c_vp, c_vp, c_vp]),
     "hses_read_idx_images": (ctypes.c_int, [c_vp, c_size, c_vp, c_i64, c_vp, c_vp]),
     "hses_read_idx_labels": (ctypes.c_int, [c_vp, c_size, c_vp, c_i64, c_vp]),
     "hses_shuffled_indices": (ctypes.c_int, [c_i64, c_i64, c_u64, c_vp]),

@@ -1,0 +1,260 @@
+// rwkv.hip -- RWKV-7 components of burn_impl/hyperscalees-models/src/llm.rs on the
+// GPU: layer norm, group norm, the token-shift mix of TimeMixing/ChannelMixing,
+// relu^2, and the rwkv7_inner_loop state recurrence (WKV-7), batched over
+// sequences (one sequence per population member and sample).
+//
+// Every routine keeps the reference's per-element operation order with each
+// operation rounded separately (built with -ffp-contract=off); reductions run
+// over 64-lane waves, so their association differs from the reference's.
+#include <math.h>
+
+#include "runtime.h"
+
+namespace hses {
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
+// llm.rs:66-83: y = (x - mean) / sqrt(E[x^2] - mean^2 + eps) * w + b per row.
+// One wave per row.
+__global__ __launch_bounds__(256) void k_layer_norm(const float* __restrict__ x, int64_t rows,
+                                                    int32_t C, const float* __restrict__ w,
+                                                    const float* __restrict__ b, float eps,
+                                                    float* __restrict__ y) {
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;  // whole wave
+    const float* xr = x + row * C;
+    float s = 0.0f, s2 = 0.0f;
+    for (int32_t c = lane; c < C; c += 64) {
+        const float v = xr[c];
+        s = s + v;
+        s2 = s2 + v * v;
+    }
+    const float mean = wave_sum(s) / (float)C;
+    const float var = wave_sum(s2) / (float)C - mean * mean;
+    const float sd = sqrtf(var + eps);
+    for (int32_t c = lane; c < C; c += 64) y[row * C + c] = (xr[c] - mean) / sd * w[c] + b[c];
+}
+
+// llm.rs:97-150 (GroupNorm): x (n, C, L); group g of row i is channels
+// [g C/G, (g+1) C/G) at all L positions; y = w[c] * (x - mean) / sqrt(var + eps)
+// + b[c].  One wave per (row, group).
+__global__ __launch_bounds__(256) void k_group_norm(const float* __restrict__ x, int64_t n,
+                                                    int32_t C, int32_t L, int32_t G,
+                                                    const float* __restrict__ w,
+                                                    const float* __restrict__ b, float eps,
+                                                    float* __restrict__ y) {
+    const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (item >= n * G) return;  // whole wave
+    const int64_t i = item / G;
+    const int32_t g = (int32_t)(item - i * G), inner = C / G;
+    const int64_t gsz = (int64_t)inner * L, base = (i * C + (int64_t)g * inner) * L;
+    float s = 0.0f, s2 = 0.0f;
+    for (int64_t e = lane; e < gsz; e += 64) {
+        const float v = x[base + e];
+        s = s + v;
+        s2 = s2 + v * v;
+    }
+    const float mean = wave_sum(s) / (float)gsz;
+    const float var = wave_sum(s2) / (float)gsz - mean * mean;
+    const float sd = sqrtf(var + eps);
+    for (int64_t e = lane; e < gsz; e += 64) {
+        const int32_t c = g * inner + (int32_t)(e / L);
+        y[base + e] = w[c] * ((x[base + e] - mean) / sd) + b[c];
+    }
+}
+
+// The token shift of TimeMixing / ChannelMixing (llm.rs:200-205, 360-381) for
+// n_mix mixing vectors at once: sx = [state, x[:-1]] (0 at a new start) - x,
+// out[m] = x + sx * mix[m].  x (nseq, T, C), state (nseq, C), mix (n_mix, C),
+// new_starts (nseq, T) or NULL, out (n_mix, nseq, T, C).
+__global__ void k_token_shift_mix(const float* __restrict__ x, const float* __restrict__ state,
+                                  const uint8_t* __restrict__ new_starts,
+                                  const float* __restrict__ mix, int32_t n_mix, int64_t nseq,
+                                  int32_t T, int32_t C, float* __restrict__ out) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t total = nseq * T * C;
+    if (e >= total) return;
+    const int32_t c = (int32_t)(e % C);
+    const int64_t st = e / C;  // sequence * T + t
+    const int32_t t = (int32_t)(st % T);
+    const int64_t sq = st / T;
+    float prev = t == 0 ? state[sq * C + c] : x[e - C];
+    if (new_starts && new_starts[st]) prev = 0.0f;
+    const float xv = x[e];
+    const float sx = prev - xv;
+    for (int32_t m = 0; m < n_mix; ++m) out[(int64_t)m * total + e] = xv + sx * mix[(int64_t)m * C + c];
+}
+
+// llm.rs:206: relu(x)^2, in place.
+__global__ void k_relu_sq(float* __restrict__ x, int64_t n) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= n) return;
+    const float z = x[e] > 0.0f ? x[e] : 0.0f;
+    x[e] = z * z;
+}
+
+// llm.rs:235-300 (rwkv7_inner_loop) for nseq sequences: r, w, k, v, a, b
+// (nseq, T, H, S); s_in / s_out (nseq, H, S, S); out (nseq, T, H, S);
+// new_starts (nseq, T) or NULL.  One wave per (sequence, head), S <= 64: lane i
+// holds row i of the head's state.  Per step the six vectors are staged in the
+// wave's LDS slice (decay w -> exp(-exp(w)) on the way) and read as broadcasts;
+// then sa_i = sum_j s_ij a_j, s_ij = ((s_ij w_j) + v_i k_j) + sa_i b_j,
+// out_i = sum_j s_ij r_j, all sums in ascending j.  s_out is the state after
+// the last step t < length (s_in when length == 0).
+template <int S>
+__global__ __launch_bounds__(256) void k_wkv7(const float* __restrict__ r, const float* __restrict__ w,
+                                              const float* __restrict__ k, const float* __restrict__ v,
+                                              const float* __restrict__ a, const float* __restrict__ b,
+                                              const float* __restrict__ s_in,
+                                              const uint8_t* __restrict__ new_starts, int64_t nseq,
+                                              int32_t T, int32_t H, int32_t length,
+                                              float* __restrict__ out, float* __restrict__ s_out) {
+    __shared__ __align__(16) float stage[4][6][64];
+    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t item = (int64_t)blockIdx.x * 4 + wv;
+    if (item >= nseq * H) return;  // whole wave
+    const int64_t sq = item / H;
+    const int32_t h = (int32_t)(item - sq * H);
+    const bool row_ok = lane < S;
+    const int i = row_ok ? lane : 0;
+    const int64_t sbase = (sq * H + h) * (int64_t)S * S + (int64_t)i * S;
+    float s[S];
+#pragma unroll
+    for (int j = 0; j < S; ++j) s[j] = s_in[sbase + j];
+    float (*st)[64] = stage[wv];
+    for (int32_t t = 0; t < T; ++t) {
+        if (new_starts && new_starts[sq * T + t]) {
+#pragma unroll
+            for (int j = 0; j < S; ++j) s[j] = 0.0f;
+        }
+        const int64_t o = ((sq * T + t) * H + h) * (int64_t)S;
+        if (row_ok) {
+            st[0][lane] = r[o + lane];
+            st[1][lane] = expf(-expf(w[o + lane]));
+            st[2][lane] = k[o + lane];
+            st[3][lane] = v[o + lane];
+            st[4][lane] = a[o + lane];
+            st[5][lane] = b[o + lane];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const float vi = st[3][i];
+        float sa = 0.0f;
+#pragma unroll
+        for (int j = 0; j < S; ++j) sa = sa + s[j] * st[4][j];
+#pragma unroll
+        for (int j = 0; j < S; ++j) {
+            const float t1 = s[j] * st[1][j];
+            const float t2 = vi * st[2][j];
+            const float t4 = sa * st[5][j];
+            s[j] = (t1 + t2) + t4;
+        }
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < S; ++j) acc = acc + s[j] * st[0][j];
+        if (row_ok) out[o + lane] = acc;
+        if (t == length - 1 && row_ok) {
+#pragma unroll
+            for (int j = 0; j < S; ++j) s_out[sbase + j] = s[j];
+        }
+        // the next step's staging overwrites st: every lane has read it
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    if (length <= 0 && row_ok) {
+#pragma unroll
+        for (int j = 0; j < S; ++j) s_out[sbase + j] = s_in[sbase + j];
+    }
+}
+
+}  // namespace hses
+
+using namespace hses;
+
+static uint32_t blocks_of(int64_t n, int per) { return (uint32_t)((n + per - 1) / per); }
+
+extern "C" int hses_layer_norm(const float* d_x, int64_t rows, int32_t C, const float* d_w,
+                               const float* d_b, float eps, float* d_y, void* stream) {
+    HSES_REQUIRE(rows >= 0 && C >= 1, "bad sizes");
+    if (rows == 0) return HSES_OK;
+    HSES_REQUIRE(d_x && d_w && d_b && d_y, "NULL pointer");
+    HSES_REQUIRE((rows + 3) / 4 < (1ll << 31), "grid too large");
+    hipLaunchKernelGGL(k_layer_norm, dim3(blocks_of(rows, 4)), dim3(256), 0, (hipStream_t)stream,
+                       d_x, rows, C, d_w, d_b, eps, d_y);
+    HSES_CHECK_HIP(hipGetLastError());
+    return HSES_OK;
+}
+
+extern "C" int hses_group_norm(const float* d_x, int64_t n, int32_t C, int32_t L, int32_t G,
+                               const float* d_w, const float* d_b, float eps, float* d_y,
+                               void* stream) {
+    HSES_REQUIRE(n >= 0 && C >= 1 && L >= 1 && G >= 1 && C % G == 0, "bad sizes (C % G != 0?)");
+    if (n == 0) return HSES_OK;
+    HSES_REQUIRE(d_x && d_w && d_b && d_y, "NULL pointer");
+    HSES_REQUIRE((n * G + 3) / 4 < (1ll << 31), "grid too large");
+    hipLaunchKernelGGL(k_group_norm, dim3(blocks_of(n * G, 4)), dim3(256), 0, (hipStream_t)stream,
+                       d_x, n, C, L, G, d_w, d_b, eps, d_y);
+    HSES_CHECK_HIP(hipGetLastError());
+    return HSES_OK;
+}
+
+extern "C" int hses_token_shift_mix(const float* d_x, const float* d_state,
+                                    const uint8_t* d_new_starts, const float* d_mix, int32_t n_mix,
+                                    int64_t nseq, int32_t T, int32_t C, float* d_out,
+                                    void* stream) {
+    HSES_REQUIRE(nseq >= 0 && T >= 1 && C >= 1 && n_mix >= 1, "bad sizes");
+    if (nseq == 0) return HSES_OK;
+    HSES_REQUIRE(d_x && d_state && d_mix && d_out, "NULL pointer");
+    const int64_t total = nseq * T * C;
+    HSES_REQUIRE((total + 255) / 256 < (1ll << 31), "grid too large");
+    hipLaunchKernelGGL(k_token_shift_mix, dim3(blocks_of(total, 256)), dim3(256), 0,
+                       (hipStream_t)stream, d_x, d_state, d_new_starts, d_mix, n_mix, nseq, T, C,
+                       d_out);
+    HSES_CHECK_HIP(hipGetLastError());
+    return HSES_OK;
+}
+
+extern "C" int hses_relu_sq(float* d_x, int64_t n, void* stream) {
+    HSES_REQUIRE(n >= 0, "negative size");
+    if (n == 0) return HSES_OK;
+    HSES_REQUIRE(d_x, "NULL pointer");
+    HSES_REQUIRE((n + 255) / 256 < (1ll << 31), "grid too large");
+    hipLaunchKernelGGL(k_relu_sq, dim3(blocks_of(n, 256)), dim3(256), 0, (hipStream_t)stream, d_x, n);
+    HSES_CHECK_HIP(hipGetLastError());
+    return HSES_OK;
+}
+
+extern "C" int hses_rwkv7_wkv(const float* d_r, const float* d_w, const float* d_k, const float* d_v,
+                              const float* d_a, const float* d_b, const float* d_s_in,
+                              const uint8_t* d_new_starts, int64_t nseq, int32_t T, int32_t H,
+                              int32_t S, int32_t length, float* d_out, float* d_s_out,
+                              void* stream) {
+    HSES_REQUIRE(nseq >= 0 && T >= 1 && H >= 1, "bad sizes");
+    HSES_REQUIRE(S == 16 || S == 32 || S == 64, "head size S must be 16, 32 or 64");
+    HSES_REQUIRE(length >= 0 && length <= T, "length must be in [0, T]");
+    if (nseq == 0) return HSES_OK;
+    HSES_REQUIRE(d_r && d_w && d_k && d_v && d_a && d_b && d_s_in && d_out && d_s_out, "NULL pointer");
+    HSES_REQUIRE(d_s_out != d_s_in, "s_out must not alias s_in");
+    HSES_REQUIRE((nseq * H + 3) / 4 < (1ll << 31), "grid too large");
+    const dim3 g(blocks_of(nseq * H, 4)), blk(256);
+    hipStream_t s = (hipStream_t)stream;
+    if (S == 64)
+        hipLaunchKernelGGL(k_wkv7<64>, g, blk, 0, s, d_r, d_w, d_k, d_v, d_a, d_b, d_s_in,
+                           d_new_starts, nseq, T, H, length, d_out, d_s_out);
+    else if (S == 32)
+        hipLaunchKernelGGL(k_wkv7<32>, g, blk, 0, s, d_r, d_w, d_k, d_v, d_a, d_b, d_s_in,
+                           d_new_starts, nseq, T, H, length, d_out, d_s_out);
+    else
+        hipLaunchKernelGGL(k_wkv7<16>, g, blk, 0, s, d_r, d_w, d_k, d_v, d_a, d_b, d_s_in,
+                           d_new_starts, nseq, T, H, length, d_out, d_s_out);
+    HSES_CHECK_HIP(hipGetLastError());
+    return HSES_OK;
+}

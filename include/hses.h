@@ -234,6 +234,35 @@ int hses_fitness_moments(const float *d_raw, int32_t n, double *d_moments, int32
 int hses_combine_affine(const float *d_grad_acc, const float *d_ones_acc, const double *d_moments,
                         int32_t batch, int64_t len, float *d_out, void *stream);
 
+/* ---- RWKV-7 components (burn_impl/hyperscalees-models/src/llm.rs) ------ */
+
+/* layer_norm / LayerNorm::forward (llm.rs:42-83): each of `rows` rows of C floats,
+ * y = (x - mean) / sqrt(E[x^2] - mean^2 + eps) * w + b.  y may alias x. */
+int hses_layer_norm(const float *d_x, int64_t rows, int32_t C, const float *d_w, const float *d_b,
+                    float eps, float *d_y, void *stream);
+/* GroupNorm::forward (llm.rs:97-150): x (n, C, L) (L = 1 for the rank-2 form),
+ * G groups of C/G channels x L positions; y = w[c] * (x - mean) / sqrt(var + eps) + b[c]. */
+int hses_group_norm(const float *d_x, int64_t n, int32_t C, int32_t L, int32_t G,
+                    const float *d_w, const float *d_b, float eps, float *d_y, void *stream);
+/* The token shift of TimeMixing / ChannelMixing (llm.rs:200-205, 360-381) with n_mix
+ * mixing vectors: sx = [state, x[:-1]] (0 where new_starts) - x; out[m] = x + sx * mix[m].
+ * x (nseq, T, C); state (nseq, C); new_starts (nseq, T) bytes or NULL; mix (n_mix, C);
+ * out (n_mix, nseq, T, C). */
+int hses_token_shift_mix(const float *d_x, const float *d_state, const uint8_t *d_new_starts,
+                         const float *d_mix, int32_t n_mix, int64_t nseq, int32_t T, int32_t C,
+                         float *d_out, void *stream);
+/* ChannelMixing's activation (llm.rs:206): x = relu(x)^2 in place. */
+int hses_relu_sq(float *d_x, int64_t n, void *stream);
+/* rwkv7_inner_loop (llm.rs:235-300) for nseq independent sequences: r, w, k, v, a, b
+ * (nseq, T, H, S) with w the raw decay (exp(-exp(w)) is applied here); s_in (nseq, H, S, S);
+ * new_starts (nseq, T) bytes or NULL (a set byte zeroes the state before that step);
+ * out (nseq, T, H, S); s_out (nseq, H, S, S) = the state after the last step t < length
+ * (s_in when length == 0).  S = 16, 32 or 64; s_out must not alias s_in. */
+int hses_rwkv7_wkv(const float *d_r, const float *d_w, const float *d_k, const float *d_v,
+                   const float *d_a, const float *d_b, const float *d_s_in,
+                   const uint8_t *d_new_starts, int64_t nseq, int32_t T, int32_t H, int32_t S,
+                   int32_t length, float *d_out, float *d_s_out, void *stream);
+
 /* ---- data path (host only: no device, no stream) ---------------------- */
 
 /* read_idx_images (burn_impl/hyperscalees-envs/src/snn_mnist.rs:57-88): an IDX images

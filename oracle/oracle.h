@@ -153,6 +153,19 @@ void or_lora_grad_f64(float sigma, uint64_t key, int32_t rank, int32_t noise_reu
                       int32_t epoch, const float *fit, int32_t n, int32_t a, int32_t b,
                       int32_t nthreads, float *grad);
 
+/* RWKV-7 components (oracle_rwkv.c; burn_impl/hyperscalees-models/src/llm.rs). */
+void or_layer_norm(const float *x, int64_t rows, int32_t C, const float *w, const float *b,
+                   float eps, float *y);
+void or_group_norm(const float *x, int64_t n, int32_t C, int32_t L, int32_t G, const float *w,
+                   const float *b, float eps, float *y);
+void or_rwkv7_inner_loop(const float *r, const float *w, const float *k, const float *v,
+                         const float *a, const float *b, const float *s0, int32_t T, int32_t H,
+                         int32_t S, int32_t length, const uint8_t *new_starts, float *out,
+                         float *out_s);
+void or_channel_mixing(const float *x, int32_t T, int32_t C, const float *state,
+                       const float *x_k, const float *Wk, int32_t F, const float *Wv,
+                       int32_t length, const uint8_t *new_starts, float *out, float *last);
+
 #ifdef __cplusplus
 }
 #endif

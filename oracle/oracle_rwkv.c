@@ -1,0 +1,128 @@
+/* oracle_rwkv.c -- CPU restatement of the RWKV-7 components of
+ * burn_impl/hyperscalees-models/src/llm.rs (layer_norm, GroupNorm,
+ * rwkv7_inner_loop, ChannelMixing).  Test infrastructure only, like oracle.c:
+ * it is the checker of the GPU kernels, never on the product path.
+ *
+ * Reductions (means, dot products, matmuls) accumulate in f32 in ascending
+ * index order, every operation rounded separately (built with
+ * -ffp-contract=off); Burn's own reduction order is not observable, so those
+ * sums are compared with tolerances, while the per-element arithmetic of the
+ * recurrence follows the reference's operation order exactly. */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "oracle.h"
+
+/* llm.rs:66-83: (x - mean) / sqrt(var + eps) * w + b with var = E[x^2] - E[x]^2. */
+void or_layer_norm(const float *x, int64_t rows, int32_t C, const float *w, const float *b,
+                   float eps, float *y) {
+    for (int64_t i = 0; i < rows; ++i) {
+        const float *xr = x + i * C;
+        float s = 0.0f, s2 = 0.0f;
+        for (int32_t c = 0; c < C; ++c) {
+            s = s + xr[c];
+            s2 = s2 + xr[c] * xr[c];
+        }
+        const float mean = s / (float)C;
+        const float var = s2 / (float)C - mean * mean;
+        const float sd = sqrtf(var + eps);
+        for (int32_t c = 0; c < C; ++c) y[i * C + c] = (xr[c] - mean) / sd * w[c] + b[c];
+    }
+}
+
+/* llm.rs:97-150 (GroupNorm): x (n, C, L) (L = 1 for the rank-2 form), groups of
+ * C/G channels x L positions normalised together, then gamma[c] * x + beta[c]. */
+void or_group_norm(const float *x, int64_t n, int32_t C, int32_t L, int32_t G, const float *w,
+                   const float *b, float eps, float *y) {
+    const int32_t inner = C / G;
+    const int64_t gsz = (int64_t)inner * L;
+    for (int64_t i = 0; i < n; ++i)
+        for (int32_t g = 0; g < G; ++g) {
+            const float *xg = x + (i * C + (int64_t)g * inner) * L;
+            float s = 0.0f, s2 = 0.0f;
+            for (int64_t e = 0; e < gsz; ++e) {
+                s = s + xg[e];
+                s2 = s2 + xg[e] * xg[e];
+            }
+            const float mean = s / (float)gsz;
+            const float var = s2 / (float)gsz - mean * mean;
+            const float sd = sqrtf(var + eps);
+            float *yg = y + (i * C + (int64_t)g * inner) * L;
+            for (int64_t e = 0; e < gsz; ++e) {
+                const int32_t c = g * inner + (int32_t)(e / L);
+                yg[e] = w[c] * ((xg[e] - mean) / sd) + b[c];
+            }
+        }
+}
+
+/* llm.rs:235-300 (rwkv7_inner_loop).  r, w, k, v, a, b: (T, H, S); s0: (H, S, S);
+ * new_starts: T bytes.  w -> exp(-exp(w)); per step: s = 0 on a new start,
+ * sa = s @ a, s = s * w + v @ k + sa @ b, out[t] = s @ r, out_s = s of the last
+ * step t < length (s0 when length == 0). */
+void or_rwkv7_inner_loop(const float *r, const float *w, const float *k, const float *v,
+                         const float *a, const float *b, const float *s0, int32_t T, int32_t H,
+                         int32_t S, int32_t length, const uint8_t *new_starts, float *out,
+                         float *out_s) {
+    const int64_t hs = (int64_t)S * S;
+    float *s = (float *)malloc(sizeof(float) * (size_t)(H * hs) + 4);
+    float *sa = (float *)malloc(sizeof(float) * (size_t)S + 4);
+    memcpy(s, s0, sizeof(float) * (size_t)(H * hs));
+    memcpy(out_s, s0, sizeof(float) * (size_t)(H * hs));
+    for (int32_t t = 0; t < T; ++t) {
+        if (new_starts && new_starts[t]) memset(s, 0, sizeof(float) * (size_t)(H * hs));
+        for (int32_t h = 0; h < H; ++h) {
+            const int64_t o = ((int64_t)t * H + h) * S;
+            float *sh = s + h * hs;
+            for (int32_t i = 0; i < S; ++i) {
+                float acc = 0.0f;
+                for (int32_t j = 0; j < S; ++j) acc = acc + sh[i * S + j] * a[o + j];
+                sa[i] = acc;
+            }
+            for (int32_t i = 0; i < S; ++i)
+                for (int32_t j = 0; j < S; ++j) {
+                    const float wd = expf(-expf(w[o + j]));
+                    const float t1 = sh[i * S + j] * wd;
+                    const float t2 = v[o + i] * k[o + j];
+                    const float t4 = sa[i] * b[o + j];
+                    sh[i * S + j] = (t1 + t2) + t4;
+                }
+            for (int32_t i = 0; i < S; ++i) {
+                float acc = 0.0f;
+                for (int32_t j = 0; j < S; ++j) acc = acc + sh[i * S + j] * r[o + j];
+                out[o + i] = acc;
+            }
+        }
+        if (t < length) memcpy(out_s, s, sizeof(float) * (size_t)(H * hs));
+    }
+    free(sa);
+    free(s);
+}
+
+/* llm.rs:191-213 (ChannelMixing with plain linears): x (T, C), state (C),
+ * x_k (C), Wk (F, C) key weight, Wv (C, F) value weight.
+ * sx = [state, x[:-1]] (zero on new starts) - x; xk = x + sx * x_k;
+ * out = relu(xk Wk^T)^2 Wv^T; last = x[length - 1]. */
+void or_channel_mixing(const float *x, int32_t T, int32_t C, const float *state,
+                       const float *x_k, const float *Wk, int32_t F, const float *Wv,
+                       int32_t length, const uint8_t *new_starts, float *out, float *last) {
+    float *xk = (float *)malloc(sizeof(float) * (size_t)T * C + 4);
+    float *kk = (float *)malloc(sizeof(float) * (size_t)T * F + 4);
+    for (int32_t t = 0; t < T; ++t)
+        for (int32_t c = 0; c < C; ++c) {
+            float prev = t == 0 ? state[c] : x[(int64_t)(t - 1) * C + c];
+            if (new_starts && new_starts[t]) prev = 0.0f;
+            const float sx = prev - x[(int64_t)t * C + c];
+            xk[(int64_t)t * C + c] = x[(int64_t)t * C + c] + sx * x_k[c];
+        }
+    or_matmul_abt(xk, T, C, Wk, F, kk);
+    for (int64_t e = 0; e < (int64_t)T * F; ++e) {
+        const float z = kk[e] > 0.0f ? kk[e] : 0.0f;
+        kk[e] = z * z;
+    }
+    or_matmul_abt(kk, T, F, Wv, C, out);
+    memcpy(last, x + (int64_t)(length - 1) * C, sizeof(float) * (size_t)C);
+    free(kk);
+    free(xk);
+}

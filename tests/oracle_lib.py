@@ -77,6 +77,12 @@ def load():
         "or_lora_einsum_raw": (None, [f32p, f32p, f32p, c_i32, c_i32, c_i32, c_i32, f32p]),
         "or_lora_einsum_ones": (None, [f32p, f32p, c_i32, c_i32, c_i32, c_i32, f32p]),
         "or_combine_affine": (None, [f32p, f32p, c_i64, c_f32, c_f32, c_i32, f32p]),
+        "or_layer_norm": (None, [f32p, c_i64, c_i32, f32p, f32p, c_f32, f32p]),
+        "or_group_norm": (None, [f32p, c_i64, c_i32, c_i32, c_i32, f32p, f32p, c_f32, f32p]),
+        "or_rwkv7_inner_loop": (None, [f32p, f32p, f32p, f32p, f32p, f32p, f32p, c_i32, c_i32,
+                                       c_i32, c_i32, ctypes.c_void_p, f32p, f32p]),
+        "or_channel_mixing": (None, [f32p, c_i32, c_i32, f32p, f32p, f32p, c_i32, f32p, c_i32,
+                                     ctypes.c_void_p, f32p, f32p]),
         "or_solver_step": (None, [c_i32, c_f32, c_f32, c_f32, c_f32, c_f32, c_i32, f32p, f32p,
                                   f32p, f32p, c_i64, f32p]),
         "or_snn_forward_members": (None, [ctypes.POINTER(SnnCfg), ctypes.c_void_p,
@@ -167,3 +173,46 @@ def lora_grad_f64(sigma, key, rank, epoch, fit, a, b, noise_reuse=0, nthreads=8)
     L.or_lora_grad_f64(sigma, key & (2**64 - 1), rank, noise_reuse, epoch, fit, fit.size, a, b,
                        nthreads, g)
     return g
+
+
+def _f(a):
+    return np.ascontiguousarray(a, np.float32)
+
+
+def layer_norm(x, w, b, eps=1e-5):
+    x = _f(x)
+    y = np.empty_like(x)
+    load().or_layer_norm(x, x.size // x.shape[-1], x.shape[-1], _f(w), _f(b), eps, y)
+    return y
+
+
+def group_norm(x, groups, w, b, eps=1e-5):
+    """x (n, C) or (n, C, L)."""
+    x = _f(x)
+    L = x.shape[2] if x.ndim == 3 else 1
+    y = np.empty_like(x)
+    load().or_group_norm(x, x.shape[0], x.shape[1], L, groups, _f(w), _f(b), eps, y)
+    return y
+
+
+def rwkv7_inner_loop(r, w, k, v, a, b, s0, length, new_starts=None):
+    """r..b (T, H, S), s0 (H, S, S) -> (out (T, H, S), out_s (H, S, S))."""
+    T, H, S = r.shape
+    out = np.zeros((T, H, S), np.float32)
+    out_s = np.zeros((H, S, S), np.float32)
+    ns = None if new_starts is None else np.ascontiguousarray(new_starts, np.uint8)
+    load().or_rwkv7_inner_loop(_f(r), _f(w), _f(k), _f(v), _f(a), _f(b), _f(s0), T, H, S, length,
+                               None if ns is None else ns.ctypes.data, out, out_s)
+    return out, out_s
+
+
+def channel_mixing(x, state, x_k, Wk, Wv, length, new_starts=None):
+    """x (T, C), state (C,), Wk (F, C), Wv (C, F) -> (out (T, C), last (C,))."""
+    T, C = x.shape
+    F = Wk.shape[0]
+    out = np.zeros((T, C), np.float32)
+    last = np.zeros(C, np.float32)
+    ns = None if new_starts is None else np.ascontiguousarray(new_starts, np.uint8)
+    load().or_channel_mixing(_f(x), T, C, _f(state), _f(x_k), _f(Wk), F, _f(Wv), length,
+                             None if ns is None else ns.ctypes.data, out, last)
+    return out, last

@@ -1,0 +1,108 @@
+"""GPU parity of the RWKV-7 components (llm.rs) against the oracle
+(tests/test_oracle_rwkv.py pins it on the reference's hand-computed cases).
+
+Norms and the token shift: elementwise order as the reference, reductions over
+64-lane waves (rel 1e-5).  The WKV-7 recurrence: per-element order as the
+reference and ascending-j sums, with the device's exp (rel 1e-4 of the output
+scale over 32 steps).  ChannelMixing: fp32 MFMA linears (rel 1e-5)."""
+import numpy as np
+import pytest
+import torch
+
+from hyperscalees_amd import rwkv
+from tests import oracle_lib as O
+
+pytestmark = pytest.mark.gpu
+
+
+def cuda(a, dtype=torch.float32):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dtype).cuda()
+
+
+def close(got, ref, rel):
+    ref = np.asarray(ref, np.float64)
+    err = np.abs(np.asarray(got, np.float64) - ref).max()
+    assert err <= rel * max(np.abs(ref).max(), 1e-30), f"max err {err:.3e} vs scale {np.abs(ref).max():.3e}"
+
+
+@pytest.mark.parametrize("rows,C", [(2, 4), (37, 512), (5, 1000)])
+def test_layer_norm(hses_gpu, rows, C):
+    rng = np.random.default_rng(C)
+    x = (rng.standard_normal((rows, C)) * 3 + 1).astype(np.float32)
+    w, b = rng.standard_normal(C).astype(np.float32), rng.standard_normal(C).astype(np.float32)
+    got = rwkv.layer_norm(cuda(x), cuda(w), cuda(b), 1e-5)
+    torch.cuda.synchronize()
+    close(got.cpu().numpy(), O.layer_norm(x, w, b, 1e-5), 1e-5)
+
+
+@pytest.mark.parametrize("shape,G", [((2, 4, 2), 2), ((128, 512), 8), ((7, 96, 3), 4)])
+def test_group_norm(hses_gpu, shape, G):
+    rng = np.random.default_rng(G)
+    x = (rng.standard_normal(shape) * 2 - 0.5).astype(np.float32)
+    C = shape[1]
+    w, b = rng.standard_normal(C).astype(np.float32), rng.standard_normal(C).astype(np.float32)
+    got = rwkv.group_norm(cuda(x), G, cuda(w), cuda(b), 64e-5)
+    torch.cuda.synchronize()
+    close(got.cpu().numpy(), O.group_norm(x, G, w, b, 64e-5), 1e-5)
+
+
+def test_token_shift_mix(hses_gpu):
+    rng = np.random.default_rng(3)
+    nseq, T, C, n_mix = 3, 9, 40, 6
+    x = rng.standard_normal((nseq, T, C)).astype(np.float32)
+    st = rng.standard_normal((nseq, C)).astype(np.float32)
+    mix = rng.random((n_mix, C)).astype(np.float32)
+    ns = np.zeros((nseq, T), np.uint8)
+    ns[1, 4] = 1
+    got = rwkv.token_shift_mix(cuda(x), cuda(st), cuda(mix), cuda(ns, torch.uint8)).cpu().numpy()
+    prev = np.concatenate([st[:, None, :], x[:, :-1, :]], 1)
+    prev[ns.astype(bool)] = 0.0
+    sx = prev - x
+    ref = x[None] + sx[None] * mix[:, None, None, :]
+    np.testing.assert_array_equal(got, ref.astype(np.float32))  # same elementwise ops
+
+
+@pytest.mark.parametrize("nseq,T,H,S,length", [(3, 32, 2, 64, 32), (2, 17, 3, 32, 9), (4, 5, 1, 16, 0)])
+def test_wkv7_matches_oracle(hses_gpu, nseq, T, H, S, length):
+    rng = np.random.default_rng(nseq * T + S)
+    shp = (nseq, T, H, S)
+    r = rng.standard_normal(shp).astype(np.float32)
+    w = (rng.standard_normal(shp) * 0.5 - 0.6).astype(np.float32)   # decays 0.3 .. 0.9
+    k = (rng.standard_normal(shp) * 0.3).astype(np.float32)
+    v = rng.standard_normal(shp).astype(np.float32)
+    kk = rng.standard_normal(shp).astype(np.float32)
+    kk /= np.linalg.norm(kk, axis=-1, keepdims=True)
+    a_ = (-kk).astype(np.float32)                                      # a = -kk, b = kk * gate
+    b_ = (kk * rng.random(shp)).astype(np.float32)
+    s0 = (rng.standard_normal((nseq, H, S, S)) * 0.1).astype(np.float32)
+    ns = np.zeros((nseq, T), np.uint8)
+    if T > 3:
+        ns[0, 3] = 1
+    out, s_out = rwkv.wkv7(*(cuda(t) for t in (r, w, k, v, a_, b_, s0)), length,
+                           new_starts=cuda(ns, torch.uint8))
+    torch.cuda.synchronize()
+    out, s_out = out.cpu().numpy(), s_out.cpu().numpy()
+    for q in range(nseq):
+        ro, rs = O.rwkv7_inner_loop(r[q], w[q], k[q], v[q], a_[q], b_[q], s0[q], length, ns[q])
+        close(out[q], ro, 1e-4)
+        close(s_out[q], rs, 1e-4)
+
+
+@pytest.mark.parametrize("nseq,T,C,F,length", [(2, 16, 64, 256, 16), (3, 7, 40, 96, 5)])
+def test_channel_mixing_matches_oracle(hses_gpu, nseq, T, C, F, length):
+    rng = np.random.default_rng(C + F)
+    x = rng.standard_normal((nseq, T, C)).astype(np.float32)
+    st = rng.standard_normal((nseq, C)).astype(np.float32)
+    x_k = rng.random(C).astype(np.float32)
+    Wk = (rng.standard_normal((F, C)) / np.sqrt(C)).astype(np.float32)
+    Wv = (rng.standard_normal((C, F)) / np.sqrt(F)).astype(np.float32)
+    ns = np.zeros((nseq, T), np.uint8)
+    ns[-1, 2] = 1
+    out, last = rwkv.channel_mixing(cuda(x), cuda(st), cuda(x_k), cuda(Wk), cuda(Wv), length,
+                                    new_starts=cuda(ns, torch.uint8))
+    torch.cuda.synchronize()
+    out, last = out.cpu().numpy(), last.cpu().numpy()
+    for q in range(nseq):
+        ro, rl = O.channel_mixing(x[q], st[q], x_k, Wk, Wv, length, ns[q])
+        close(out[q], ro, 1e-5)
+        np.testing.assert_array_equal(last[q], rl)
