@@ -68,6 +68,11 @@ PROTOTYPES = {
     "hses_relu_sq": (ctypes.c_int, [c_vp, c_i64, c_vp]),
     "hses_rwkv7_wkv": (ctypes.c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i32,
                                       c_i32, c_i32, c_i32, c_vp, c_vp, c_vp]),
+    "hses_rwkv_act": (ctypes.c_int, [c_vp, c_i64, c_i32, c_vp]),
+    "hses_tm_gates": (ctypes.c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i32,
+                                     c_vp]),
+    "hses_tm_kk": (ctypes.c_int, [c_vp, c_vp, c_vp, c_vp, c_i64, c_i32, c_i32, c_vp, c_vp, c_vp]),
+    "hses_tm_post": (ctypes.c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i32, c_i32, c_vp]),
     "hses_read_idx_images": (ctypes.c_int, [c_vp, c_size, c_vp, c_i64, c_vp, c_vp]),
     "hses_read_idx_labels": (ctypes.c_int, [c_vp, c_size, c_vp, c_i64, c_vp]),
     "hses_shuffled_indices": (ctypes.c_int, [c_i64, c_i64, c_u64, c_vp]),

@@ -175,6 +175,83 @@ __global__ __launch_bounds__(256) void k_wkv7(const float* __restrict__ r, const
     }
 }
 
+// Activations of TimeMixing's low-rank branches, in place: kind 0 tanh
+// (w1, v1, a1 outputs), kind 1 sigmoid (g1 output).
+__global__ void k_rwkv_act(float* __restrict__ x, int64_t n, int32_t kind) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= n) return;
+    const float z = x[e];
+    x[e] = kind == 0 ? tanhf(z) : 1.0f / (1.0f + expf(-z));
+}
+
+__device__ __forceinline__ float softplus1(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
+
+// TimeMixing gates (llm.rs:388-408), per element of (rows, C):
+//   w = -softplus(-(w0 + w2o)) - 0.5 (written over w2o);
+//   a = sigmoid(a0 + a2o) (written over a2o);
+//   v2o != NULL (layers after the first): v = v + (v_first - v) * sigmoid(v0 + v2o).
+__global__ void k_tm_gates(float* __restrict__ w2o, float* __restrict__ a2o,
+                           const float* __restrict__ v2o, float* __restrict__ v,
+                           const float* __restrict__ v_first, const float* __restrict__ w0,
+                           const float* __restrict__ a0, const float* __restrict__ v0, int64_t n,
+                           int32_t C) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= n) return;
+    const int32_t c = (int32_t)(e % C);
+    w2o[e] = -softplus1(-(w0[c] + w2o[e])) - 0.5f;
+    a2o[e] = 1.0f / (1.0f + expf(-(a0[c] + a2o[e])));
+    if (v2o) {
+        const float sg = 1.0f / (1.0f + expf(-(v0[c] + v2o[e])));
+        v[e] = v[e] + (v_first[e] - v[e]) * sg;
+    }
+}
+
+// TimeMixing's kk normalisation (llm.rs:414-426) per (row, head), one wave
+// each (S <= 64 lanes): kk = k k_k / max(||k k_k||, 1e-12); a_i = -kk;
+// b_i = kk a; k = k (k_a (a - 1) + 1) in place.
+__global__ __launch_bounds__(256) void k_tm_kk(float* __restrict__ k, const float* __restrict__ k_k,
+                                               const float* __restrict__ k_a,
+                                               const float* __restrict__ a, int64_t rows,
+                                               int32_t H, int32_t S, float* __restrict__ ai,
+                                               float* __restrict__ bi) {
+    const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (item >= rows * H) return;  // whole wave
+    const int64_t row = item / H;
+    const int32_t h = (int32_t)(item - row * H), C = H * S, c = h * S + lane;
+    const bool ok = lane < S;
+    const int64_t o = row * C + c;
+    const float kv = ok ? k[o] : 0.0f;
+    const float kk2 = ok ? kv * k_k[c] : 0.0f;
+    float nrm = sqrtf(wave_sum(kk2 * kk2));
+    nrm = nrm < 1e-12f ? 1e-12f : nrm;
+    if (!ok) return;
+    const float kk = kk2 / nrm, av = a[o];
+    ai[o] = -kk;
+    bi[o] = kk * av;
+    k[o] = kv * (k_a[c] * (av - 1.0f) + 1.0f);
+}
+
+// TimeMixing's readout and gate (llm.rs:455-470) per (row, head), one wave
+// each: x = (gn + (sum_s r k r_k) v) g, with gn the group-normed recurrence
+// output.  Written over gn.
+__global__ __launch_bounds__(256) void k_tm_post(float* __restrict__ gn, const float* __restrict__ r,
+                                                 const float* __restrict__ k,
+                                                 const float* __restrict__ v,
+                                                 const float* __restrict__ g,
+                                                 const float* __restrict__ r_k, int64_t rows,
+                                                 int32_t H, int32_t S) {
+    const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (item >= rows * H) return;  // whole wave
+    const int64_t row = item / H;
+    const int32_t h = (int32_t)(item - row * H), C = H * S, c = h * S + lane;
+    const bool ok = lane < S;
+    const int64_t o = row * C + c;
+    const float sum = wave_sum(ok ? r[o] * k[o] * r_k[c] : 0.0f);
+    if (ok) gn[o] = (gn[o] + sum * v[o]) * g[o];
+}
+
 }  // namespace hses
 
 using namespace hses;
@@ -255,6 +332,58 @@ extern "C" int hses_rwkv7_wkv(const float* d_r, const float* d_w, const float* d
     else
         hipLaunchKernelGGL(k_wkv7<16>, g, blk, 0, s, d_r, d_w, d_k, d_v, d_a, d_b, d_s_in,
                            d_new_starts, nseq, T, H, length, d_out, d_s_out);
+    HSES_CHECK_HIP(hipGetLastError());
+    return HSES_OK;
+}
+
+extern "C" int hses_rwkv_act(float* d_x, int64_t n, int32_t kind, void* stream) {
+    HSES_REQUIRE(n >= 0 && (kind == 0 || kind == 1), "bad arguments (kind 0 tanh, 1 sigmoid)");
+    if (n == 0) return HSES_OK;
+    HSES_REQUIRE(d_x, "NULL pointer");
+    HSES_REQUIRE((n + 255) / 256 < (1ll << 31), "grid too large");
+    hipLaunchKernelGGL(k_rwkv_act, dim3(blocks_of(n, 256)), dim3(256), 0, (hipStream_t)stream, d_x, n,
+                       kind);
+    HSES_CHECK_HIP(hipGetLastError());
+    return HSES_OK;
+}
+
+extern "C" int hses_tm_gates(float* d_w2o, float* d_a2o, const float* d_v2o, float* d_v,
+                             const float* d_v_first, const float* d_w0, const float* d_a0,
+                             const float* d_v0, int64_t rows, int32_t C, void* stream) {
+    HSES_REQUIRE(rows >= 0 && C >= 1, "bad sizes");
+    if (rows == 0) return HSES_OK;
+    HSES_REQUIRE(d_w2o && d_a2o && d_w0 && d_a0, "NULL pointer");
+    HSES_REQUIRE(!d_v2o || (d_v && d_v_first && d_v0), "NULL pointer (v branch)");
+    const int64_t n = rows * C;
+    HSES_REQUIRE((n + 255) / 256 < (1ll << 31), "grid too large");
+    hipLaunchKernelGGL(k_tm_gates, dim3(blocks_of(n, 256)), dim3(256), 0, (hipStream_t)stream, d_w2o,
+                       d_a2o, d_v2o, d_v, d_v_first, d_w0, d_a0, d_v0, n, C);
+    HSES_CHECK_HIP(hipGetLastError());
+    return HSES_OK;
+}
+
+extern "C" int hses_tm_kk(float* d_k, const float* d_k_k, const float* d_k_a, const float* d_a,
+                          int64_t rows, int32_t H, int32_t S, float* d_ai, float* d_bi,
+                          void* stream) {
+    HSES_REQUIRE(rows >= 0 && H >= 1 && S >= 1 && S <= 64, "bad sizes (S <= 64)");
+    if (rows == 0) return HSES_OK;
+    HSES_REQUIRE(d_k && d_k_k && d_k_a && d_a && d_ai && d_bi, "NULL pointer");
+    HSES_REQUIRE((rows * H + 3) / 4 < (1ll << 31), "grid too large");
+    hipLaunchKernelGGL(k_tm_kk, dim3(blocks_of(rows * H, 4)), dim3(256), 0, (hipStream_t)stream, d_k,
+                       d_k_k, d_k_a, d_a, rows, H, S, d_ai, d_bi);
+    HSES_CHECK_HIP(hipGetLastError());
+    return HSES_OK;
+}
+
+extern "C" int hses_tm_post(float* d_gn, const float* d_r, const float* d_k, const float* d_v,
+                            const float* d_g, const float* d_r_k, int64_t rows, int32_t H,
+                            int32_t S, void* stream) {
+    HSES_REQUIRE(rows >= 0 && H >= 1 && S >= 1 && S <= 64, "bad sizes (S <= 64)");
+    if (rows == 0) return HSES_OK;
+    HSES_REQUIRE(d_gn && d_r && d_k && d_v && d_g && d_r_k, "NULL pointer");
+    HSES_REQUIRE((rows * H + 3) / 4 < (1ll << 31), "grid too large");
+    hipLaunchKernelGGL(k_tm_post, dim3(blocks_of(rows * H, 4)), dim3(256), 0, (hipStream_t)stream,
+                       d_gn, d_r, d_k, d_v, d_g, d_r_k, rows, H, S);
     HSES_CHECK_HIP(hipGetLastError());
     return HSES_OK;
 }

@@ -114,3 +114,87 @@ def channel_mixing(x, state, x_k, Wk, Wv, length, new_starts=None, es_key=None, 
     out = linear(kk, Wv, es_value, math)
     last = x[:, length - 1, :].contiguous()
     return out, last
+
+
+def linear_t(x, W, es=None, math=MATH_F32):
+    """x (nseq, T, in) @ W for W (in, out): the plain Tmm (es None) or every
+    member's perturbed do_Tmm (common.rs:156-159, eggroll.rs do_Tmm)."""
+    nseq, T, cin = x.shape
+    if es is None:
+        es = EsLinear(key=0, rank=0, sigma=0.0, n=nseq, seqs_per_member=1)
+    y = K.perturbed_linear_t(x.reshape(1, nseq * T, cin), W, es.key, es.rank, es.sigma, es.epoch,
+                             es.noise_reuse, es.tid_lo, es.n, es.seqs_per_member * T, n_time=1,
+                             math=math)
+    return y.reshape(nseq, T, W.shape[1])
+
+
+def rwkv_act_(x, kind):
+    """In place: kind 0 tanh, kind 1 sigmoid."""
+    K._dev(x, torch.float32, "x")
+    _lib.call("hses_rwkv_act", _p(x), x.numel(), kind, _stream())
+    return x
+
+
+TM_MIXES = ("x_r", "x_w", "x_k", "x_v", "x_a", "x_g")
+
+
+def time_mixing(P, x, state, v_first, H, length, layer_id, new_starts=None, es=None,
+                math=MATH_F32):
+    """TimeMixing::forward (llm.rs:348-480) on every sequence.
+
+    P maps the module's parameter names to device tensors: x_r..x_g, w0, v0,
+    a0, k_k, k_a, r_k, ln_w, ln_b (C); receptance, key, value, output (C, C)
+    Linear weights (out, in); w1, v1, a1, g1 (C, D) and w2, v2, a2, g2 (D, C)
+    Tmm weights (in, out).  es optionally maps a matrix name to its EsLinear
+    (the member's perturbation of that parameter).  x (nseq, T, C); state
+    (nseq, 1 + S, C): row 0 the previous token, rows 1.. the (H, S, S) WKV
+    state; v_first (nseq, T, C).  Returns (out, state, v_first), new tensors."""
+    es = es or {}
+    nseq, T, C = x.shape
+    S = C // H
+    if S * H != C or S > 64:
+        raise ValueError(f"C={C} is not H={H} heads of at most 64 channels")
+    if state.shape != (nseq, 1 + S, C) or v_first.shape != (nseq, T, C):
+        raise ValueError("state must be (nseq, 1 + S, C) and v_first (nseq, T, C)")
+    if not 1 <= length <= T:
+        raise ValueError("length must be in [1, T]")
+    mixes = torch.stack([P[n] for n in TM_MIXES])
+    xm = token_shift_mix(x, state[:, 0, :].contiguous(), mixes, new_starts)
+
+    def lin(i, name):
+        return linear(xm[i], P[name], es.get(name), math)
+
+    def low(inp, n1, n2, kind):
+        h = rwkv_act_(linear_t(inp, P[n1], es.get(n1), math), kind)
+        return linear_t(h, P[n2], es.get(n2), math)
+
+    r = lin(0, "receptance")
+    w = low(xm[1], "w1", "w2", 0)        # w2 output; the gate turns it into w
+    k = lin(2, "key")
+    v = lin(3, "value")
+    if layer_id == 0:
+        v_first = v.clone()
+        v2o = None
+    else:
+        v2o = low(xm[3], "v1", "v2", 0)
+    a = low(xm[4], "a1", "a2", 0)        # a2 output; the gate turns it into a
+    g = low(xm[5], "g1", "g2", 1)
+    rows = nseq * T
+    _lib.call("hses_tm_gates", _p(w), _p(a), _p(v2o), _p(v), _p(v_first), _p(P["w0"]), _p(P["a0"]),
+              _p(P["v0"]), rows, C, _stream())
+    ai = torch.empty_like(k)
+    bi = torch.empty_like(k)
+    _lib.call("hses_tm_kk", _p(k), _p(P["k_k"]), _p(P["k_a"]), _p(a), rows, H, S, _p(ai), _p(bi),
+              _stream())
+    s_in = state[:, 1:, :].reshape(nseq, H, S, S).contiguous()
+    shp = (nseq, T, H, S)
+    wkv, s_new = wkv7(r.view(shp), w.view(shp), k.view(shp), v.view(shp), ai.view(shp),
+                      bi.view(shp), s_in, length, new_starts)
+    state_out = torch.empty_like(state)
+    state_out[:, 0, :] = x[:, length - 1, :]
+    state_out[:, 1:, :] = s_new.view(nseq, S, C)
+    gn = group_norm(wkv.view(rows, C), H, P["ln_w"], P["ln_b"], 64e-5)
+    _lib.call("hses_tm_post", _p(gn), _p(r), _p(k), _p(v), _p(g), _p(P["r_k"]), rows, H, S,
+              _stream())
+    out = linear(gn.view(nseq, T, C), P["output"], es.get("output"), math)
+    return out, state_out, v_first

@@ -263,6 +263,23 @@ int hses_rwkv7_wkv(const float *d_r, const float *d_w, const float *d_k, const f
                    const uint8_t *d_new_starts, int64_t nseq, int32_t T, int32_t H, int32_t S,
                    int32_t length, float *d_out, float *d_s_out, void *stream);
 
+/* TimeMixing (llm.rs:348-480) pieces around the projections and the recurrence:
+ * hses_rwkv_act: x = tanh(x) (kind 0) or sigmoid(x) (kind 1) in place (the low-rank branches);
+ * hses_tm_gates (llm.rs:388-408), per element of (rows, C): w2o <- -softplus(-(w0 + w2o)) - 0.5,
+ *   a2o <- sigmoid(a0 + a2o), and when v2o != NULL v <- v + (v_first - v) * sigmoid(v0 + v2o);
+ * hses_tm_kk (llm.rs:414-426) per (row, head): kk = k k_k / max(||k k_k||, 1e-12), a_i = -kk,
+ *   b_i = kk a, k <- k (k_a (a - 1) + 1);
+ * hses_tm_post (llm.rs:455-470) per (row, head): gn <- (gn + (sum_s r k r_k) v) g.
+ * Head size S <= 64; C = H * S. */
+int hses_rwkv_act(float *d_x, int64_t n, int32_t kind, void *stream);
+int hses_tm_gates(float *d_w2o, float *d_a2o, const float *d_v2o, float *d_v, const float *d_v_first,
+                  const float *d_w0, const float *d_a0, const float *d_v0, int64_t rows, int32_t C,
+                  void *stream);
+int hses_tm_kk(float *d_k, const float *d_k_k, const float *d_k_a, const float *d_a, int64_t rows,
+               int32_t H, int32_t S, float *d_ai, float *d_bi, void *stream);
+int hses_tm_post(float *d_gn, const float *d_r, const float *d_k, const float *d_v, const float *d_g,
+                 const float *d_r_k, int64_t rows, int32_t H, int32_t S, void *stream);
+
 /* ---- data path (host only: no device, no stream) ---------------------- */
 
 /* read_idx_images (burn_impl/hyperscalees-envs/src/snn_mnist.rs:57-88): an IDX images

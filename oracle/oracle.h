@@ -166,6 +166,22 @@ void or_channel_mixing(const float *x, int32_t T, int32_t C, const float *state,
                        const float *x_k, const float *Wk, int32_t F, const float *Wv,
                        int32_t length, const uint8_t *new_starts, float *out, float *last);
 
+/* TimeMixing weights (llm.rs:304-342); Linear weights (out, in), Tmm weights (in, out),
+ * every low-rank width d_lora. */
+typedef struct {
+    const float *x_r, *x_w, *x_k, *x_v, *x_a, *x_g; /* (C) */
+    const float *receptance, *key, *value, *output; /* (C, C) */
+    const float *w0, *v0, *a0;                       /* (C) */
+    const float *w1, *v1, *a1, *g1;                  /* (C, d_lora) */
+    const float *w2, *v2, *a2, *g2;                  /* (d_lora, C) */
+    const float *k_k, *k_a, *r_k;                    /* (C) */
+    const float *ln_w, *ln_b;                        /* (C) */
+    int32_t d_lora;
+} or_tm_weights;
+void or_time_mixing(const or_tm_weights *P, const float *x, int32_t T, int32_t C, int32_t H,
+                    const float *state, float *v_first, int32_t length, const uint8_t *new_starts,
+                    int32_t layer_id, float *out, float *state_out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -126,3 +126,125 @@ void or_channel_mixing(const float *x, int32_t T, int32_t C, const float *state,
     free(kk);
     free(xk);
 }
+
+/* y (m, n) = x (m, k) @ w (k, n): the Tmm forward (common.rs:156-159), f32 in ascending k. */
+static void matmul_ab_f32(const float *x, int32_t m, int32_t k, const float *w, int32_t n, float *y) {
+    for (int32_t i = 0; i < m; ++i)
+        for (int32_t j = 0; j < n; ++j) {
+            float acc = 0.0f;
+            for (int32_t q = 0; q < k; ++q) acc = acc + x[(int64_t)i * k + q] * w[(int64_t)q * n + j];
+            y[(int64_t)i * n + j] = acc;
+        }
+}
+
+/* burn 0.21 (the reference's Cargo.toml:29; not vendored) defines
+ * softplus(x, beta) = log(1 + exp(beta x)) / beta, called with beta = 1, and
+ * sigmoid(x) = 1 / (1 + exp(-x)); its backends may round the latter differently
+ * in the last place, inside the parity tolerance. */
+static float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
+static float softplusf_(float x) { return logf(expf(x) + 1.0f); }
+
+/* llm.rs:348-480 (TimeMixing::forward) for one sequence with plain weights.
+ * x (T, C); state (1 + S, C): row 0 the previous token, rows 1.. the WKV state
+ * ((S, C) read as (H, S, S) by a row-major reshape); v_first (T, C) (read when
+ * layer_id > 0, written when layer_id == 0).  Outputs out (T, C) and the new
+ * state (1 + S, C).  Weights as the reference module: mixes x_r..x_g (C);
+ * Linear weights (out, in); Tmm weights (in, out). */
+void or_time_mixing(const or_tm_weights *P, const float *x, int32_t T, int32_t C, int32_t H,
+                    const float *state, float *v_first, int32_t length, const uint8_t *new_starts,
+                    int32_t layer_id, float *out, float *state_out) {
+    const int32_t S = C / H;
+    const int64_t TC = (int64_t)T * C;
+    float *mix[6];
+    for (int m = 0; m < 6; ++m) mix[m] = (float *)malloc(sizeof(float) * (size_t)TC + 4);
+    const float *mv[6] = {P->x_r, P->x_w, P->x_k, P->x_v, P->x_a, P->x_g};
+    for (int32_t t = 0; t < T; ++t)
+        for (int32_t c = 0; c < C; ++c) {
+            float prev = t == 0 ? state[c] : x[(int64_t)(t - 1) * C + c];
+            if (new_starts && new_starts[t]) prev = 0.0f;
+            const float sx = prev - x[(int64_t)t * C + c];
+            for (int m = 0; m < 6; ++m) mix[m][(int64_t)t * C + c] = x[(int64_t)t * C + c] + sx * mv[m][c];
+        }
+    float *r = (float *)malloc(sizeof(float) * (size_t)TC + 4);
+    float *w = (float *)malloc(sizeof(float) * (size_t)TC + 4);
+    float *k = (float *)malloc(sizeof(float) * (size_t)TC + 4);
+    float *v = (float *)malloc(sizeof(float) * (size_t)TC + 4);
+    float *a = (float *)malloc(sizeof(float) * (size_t)TC + 4);
+    float *g = (float *)malloc(sizeof(float) * (size_t)TC + 4);
+    float *tmp = (float *)malloc(sizeof(float) * (size_t)TC + 4);
+    const int32_t D = P->d_lora;
+    float *low = (float *)malloc(sizeof(float) * (size_t)T * D + 4);
+    or_matmul_abt(mix[0], T, C, P->receptance, C, r);
+    /* w = -softplus(-(w0 + w2(tanh(w1 xw)))) - 0.5 */
+    matmul_ab_f32(mix[1], T, C, P->w1, D, low);
+    for (int64_t e = 0; e < (int64_t)T * D; ++e) low[e] = tanhf(low[e]);
+    matmul_ab_f32(low, T, D, P->w2, C, tmp);
+    for (int64_t e = 0; e < TC; ++e) w[e] = -softplusf_(-(P->w0[e % C] + tmp[e])) - 0.5f;
+    or_matmul_abt(mix[2], T, C, P->key, C, k);
+    or_matmul_abt(mix[3], T, C, P->value, C, v);
+    if (layer_id == 0) {
+        memcpy(v_first, v, sizeof(float) * (size_t)TC);
+    } else {
+        matmul_ab_f32(mix[3], T, C, P->v1, D, low);
+        for (int64_t e = 0; e < (int64_t)T * D; ++e) low[e] = tanhf(low[e]);
+        matmul_ab_f32(low, T, D, P->v2, C, tmp);
+        for (int64_t e = 0; e < TC; ++e)
+            v[e] = v[e] + (v_first[e] - v[e]) * sigmoidf_(P->v0[e % C] + tmp[e]);
+    }
+    matmul_ab_f32(mix[4], T, C, P->a1, D, low);
+    for (int64_t e = 0; e < (int64_t)T * D; ++e) low[e] = tanhf(low[e]);
+    matmul_ab_f32(low, T, D, P->a2, C, tmp);
+    for (int64_t e = 0; e < TC; ++e) a[e] = sigmoidf_(P->a0[e % C] + tmp[e]);
+    matmul_ab_f32(mix[5], T, C, P->g1, D, low);
+    for (int64_t e = 0; e < (int64_t)T * D; ++e) low[e] = sigmoidf_(low[e]);
+    matmul_ab_f32(low, T, D, P->g2, C, g);
+    /* kk = normalize_per_head(k * k_k); k = k * (k_a * (a - 1) + 1); a_i = -kk, b_i = kk * a */
+    float *ai = (float *)malloc(sizeof(float) * (size_t)TC + 4);
+    float *bi = (float *)malloc(sizeof(float) * (size_t)TC + 4);
+    for (int32_t t = 0; t < T; ++t)
+        for (int32_t h = 0; h < H; ++h) {
+            const int64_t o = (int64_t)t * C + (int64_t)h * S;
+            float ss = 0.0f;
+            for (int32_t s = 0; s < S; ++s) {
+                const float kk2 = k[o + s] * P->k_k[h * S + s];
+                ss = ss + kk2 * kk2;
+            }
+            float nrm = sqrtf(ss);
+            nrm = nrm < 1e-12f ? 1e-12f : nrm;
+            for (int32_t s = 0; s < S; ++s) {
+                const int32_t c = h * S + s;
+                const float kk = (k[o + s] * P->k_k[c]) / nrm;
+                ai[o + s] = -kk;
+                bi[o + s] = kk * a[o + s];
+                k[o + s] = k[o + s] * (P->k_a[c] * (a[o + s] - 1.0f) + 1.0f);
+            }
+        }
+    /* the recurrence on state rows 1.. (a row-major (S, C) == (H, S, S) block) */
+    float *wkv = (float *)malloc(sizeof(float) * (size_t)TC + 4);
+    memcpy(state_out, state, sizeof(float) * (size_t)(1 + S) * C);
+    memcpy(state_out, x + (int64_t)(length - 1) * C, sizeof(float) * (size_t)C);
+    or_rwkv7_inner_loop(r, w, k, v, ai, bi, state + C, T, H, S, length, new_starts, wkv,
+                        state_out + C);
+    /* group norm per head (eps 64e-5), + readout (sum_s r k r_k) v, * g, output */
+    or_group_norm(wkv, T, C, 1, H, P->ln_w, P->ln_b, 64e-5f, tmp);
+    for (int32_t t = 0; t < T; ++t)
+        for (int32_t h = 0; h < H; ++h) {
+            const int64_t o = (int64_t)t * C + (int64_t)h * S;
+            float sum = 0.0f;
+            for (int32_t s = 0; s < S; ++s) sum = sum + r[o + s] * k[o + s] * P->r_k[h * S + s];
+            for (int32_t s = 0; s < S; ++s) tmp[o + s] = (tmp[o + s] + sum * v[o + s]) * g[o + s];
+        }
+    or_matmul_abt(tmp, T, C, P->output, C, out);
+    free(wkv);
+    free(bi);
+    free(ai);
+    free(low);
+    free(tmp);
+    free(g);
+    free(a);
+    free(v);
+    free(k);
+    free(w);
+    free(r);
+    for (int m = 0; m < 6; ++m) free(mix[m]);
+}

@@ -24,6 +24,17 @@ class SnnCfg(ctypes.Structure):
                 ("poisson_seed", c_u32 * 4)]
 
 
+TM_VECTORS = ("x_r", "x_w", "x_k", "x_v", "x_a", "x_g")
+TM_LINEAR = ("receptance", "key", "value", "output")
+TM_TMM = ("w1", "w2", "v1", "v2", "a1", "a2", "g1", "g2")
+TM_FIELDS = (TM_VECTORS + TM_LINEAR + ("w0", "v0", "a0") + ("w1", "v1", "a1", "g1")
+             + ("w2", "v2", "a2", "g2") + ("k_k", "k_a", "r_k", "ln_w", "ln_b"))
+
+
+class TmWeights(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_void_p) for name in TM_FIELDS] + [("d_lora", c_i32)]
+
+
 def build():
     subprocess.run(["make", "-s", "-C", ORACLE_DIR], check=True)
 
@@ -83,6 +94,8 @@ def load():
                                        c_i32, c_i32, ctypes.c_void_p, f32p, f32p]),
         "or_channel_mixing": (None, [f32p, c_i32, c_i32, f32p, f32p, f32p, c_i32, f32p, c_i32,
                                      ctypes.c_void_p, f32p, f32p]),
+        "or_time_mixing": (None, [ctypes.POINTER(TmWeights), f32p, c_i32, c_i32, c_i32, f32p,
+                                  f32p, c_i32, ctypes.c_void_p, c_i32, f32p, f32p]),
         "or_solver_step": (None, [c_i32, c_f32, c_f32, c_f32, c_f32, c_f32, c_i32, f32p, f32p,
                                   f32p, f32p, c_i64, f32p]),
         "or_snn_forward_members": (None, [ctypes.POINTER(SnnCfg), ctypes.c_void_p,
@@ -216,3 +229,21 @@ def channel_mixing(x, state, x_k, Wk, Wv, length, new_starts=None):
     load().or_channel_mixing(_f(x), T, C, _f(state), _f(x_k), _f(Wk), F, _f(Wv), length,
                              None if ns is None else ns.ctypes.data, out, last)
     return out, last
+
+
+def time_mixing(P, x, state, v_first, H, length, layer_id, new_starts=None):
+    """TimeMixing::forward (llm.rs:348-480) of one sequence.  P maps the
+    TM_FIELDS names to arrays (Linear weights (out, in), Tmm weights (in, out)).
+    x (T, C), state (1 + S, C), v_first (T, C) -> (out (T, C), state (1 + S, C),
+    v_first (T, C))."""
+    T, C = x.shape
+    S = C // H
+    keep = {name: _f(P[name]) for name in TM_FIELDS}
+    tw = TmWeights(*[keep[name].ctypes.data for name in TM_FIELDS], keep["w1"].shape[1])
+    vf = np.array(v_first, np.float32, copy=True).reshape(T, C)
+    out = np.zeros((T, C), np.float32)
+    st = np.zeros((1 + S, C), np.float32)
+    ns = None if new_starts is None else np.ascontiguousarray(new_starts, np.uint8)
+    load().or_time_mixing(ctypes.byref(tw), _f(x), T, C, H, _f(state), vf, length,
+                          None if ns is None else ns.ctypes.data, layer_id, out, st)
+    return out, st, vf

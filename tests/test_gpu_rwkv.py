@@ -106,3 +106,83 @@ def test_channel_mixing_matches_oracle(hses_gpu, nseq, T, C, F, length):
         ro, rl = O.channel_mixing(x[q], st[q], x_k, Wk, Wv, length, ns[q])
         close(out[q], ro, 1e-5)
         np.testing.assert_array_equal(last[q], rl)
+
+
+def tm_params(rng, C, D):
+    P = {}
+    for n in O.TM_VECTORS + ("k_a",):
+        P[n] = rng.random(C).astype(np.float32)
+    for n in ("w0", "v0", "a0", "r_k", "ln_b"):
+        P[n] = (rng.standard_normal(C) * 0.5).astype(np.float32)
+    P["k_k"] = (1 + 0.2 * rng.standard_normal(C)).astype(np.float32)
+    P["ln_w"] = (1 + 0.2 * rng.standard_normal(C)).astype(np.float32)
+    for n in O.TM_LINEAR:
+        P[n] = (rng.standard_normal((C, C)) / np.sqrt(C)).astype(np.float32)
+    for n in ("w1", "v1", "a1", "g1"):
+        P[n] = (rng.standard_normal((C, D)) / np.sqrt(C)).astype(np.float32)
+    for n in ("w2", "v2", "a2", "g2"):
+        P[n] = (rng.standard_normal((D, C)) / np.sqrt(D)).astype(np.float32)
+    return P
+
+
+@pytest.mark.parametrize("nseq,T,H,S,D,length,layer_id", [
+    (2, 8, 2, 16, 8, 8, 0),
+    (3, 7, 4, 32, 16, 5, 1),
+    (2, 4, 2, 64, 32, 4, 2),
+])
+def test_time_mixing_matches_oracle(hses_gpu, nseq, T, H, S, D, length, layer_id):
+    # fp32 linears, elementwise gates in the reference's order with the device's
+    # exp/log/tanh, the recurrence's 1e-4 bound: rel 1e-4 of each output's scale.
+    C = H * S
+    rng = np.random.default_rng(C + T + layer_id)
+    P = tm_params(rng, C, D)
+    x = rng.standard_normal((nseq, T, C)).astype(np.float32)
+    st = (rng.standard_normal((nseq, 1 + S, C)) * 0.3).astype(np.float32)
+    vf = rng.standard_normal((nseq, T, C)).astype(np.float32)
+    ns = np.zeros((nseq, T), np.uint8)
+    ns[-1, T // 2] = 1
+    Pd = {n: cuda(t) for n, t in P.items()}
+    out, so, vfo = rwkv.time_mixing(Pd, cuda(x), cuda(st), cuda(vf), H, length, layer_id,
+                                    new_starts=cuda(ns, torch.uint8))
+    torch.cuda.synchronize()
+    out, so, vfo = out.cpu().numpy(), so.cpu().numpy(), vfo.cpu().numpy()
+    for q in range(nseq):
+        ro, rs, rv = O.time_mixing(P, x[q], st[q], vf[q], H, length, layer_id, ns[q])
+        close(out[q], ro, 1e-4)
+        close(so[q, 1:], rs[1:], 1e-4)
+        np.testing.assert_array_equal(so[q, 0], rs[0])
+        if layer_id == 0:
+            close(vfo[q], rv, 1e-5)
+        else:
+            np.testing.assert_array_equal(vfo[q], vf[q])
+
+
+def test_time_mixing_perturbed_members(hses_gpu):
+    # n = 2 members of 2 sequences each, perturbing the Linear `key` and `output`
+    # and the Tmm `w1` and `g2`: member m's sequences equal the plain module with
+    # W + A_m B_m^T (the do_mm / do_Tmm identity).
+    n, spm, T, H, S, D, r, sigma = 2, 2, 5, 2, 32, 16, 2, 0.1
+    C, nseq = H * S, n * spm
+    rng = np.random.default_rng(11)
+    P = tm_params(rng, C, D)
+    x = rng.standard_normal((nseq, T, C)).astype(np.float32)
+    st = (rng.standard_normal((nseq, 1 + S, C)) * 0.3).astype(np.float32)
+    vf = np.zeros((nseq, T, C), np.float32)
+    keys = {"key": 0x1234, "output": 0x5678, "w1": 0x9ABC, "g2": 0xDEF0}
+    es = {name: rwkv.EsLinear(key=kk, rank=r, sigma=sigma, n=n, seqs_per_member=spm)
+          for name, kk in keys.items()}
+    Pd = {nm: cuda(t) for nm, t in P.items()}
+    out, so, _ = rwkv.time_mixing(Pd, cuda(x), cuda(st), cuda(vf), H, T, 0, es=es)
+    torch.cuda.synchronize()
+    out, so = out.cpu().numpy(), so.cpu().numpy()
+    bs = O.load().or_base_sigma(sigma, r)
+    for m in range(n):
+        Pm = dict(P)
+        for name, kk in keys.items():
+            a, b = P[name].shape
+            A, B = O.lora_factors(bs, kk, r, 0, [m], a, b)
+            Pm[name] = (P[name].astype(np.float64) + A[0].astype(np.float64) @ B[0].T).astype(np.float32)
+        for q in range(m * spm, (m + 1) * spm):
+            ro, rs, _ = O.time_mixing(Pm, x[q], st[q], vf[q], H, T, 0)
+            close(out[q], ro, 1e-4)
+            close(so[q, 1:], rs[1:], 1e-4)
