@@ -14,6 +14,7 @@ FMT_F32, FMT_BF16, FMT_U8, FMT_BITS = range(4)
 MATH_F32, MATH_BF16 = range(2)
 SGD, ADAM, ADAMW = range(3)
 REWARD_LOGLIK, REWARD_BINARY = range(2)
+ACT_NONE, ACT_TANH, ACT_SIGMOID, ACT_RELU_SQ = range(4)
 
 c_i32, c_i64, c_u32, c_u64 = ctypes.c_int32, ctypes.c_int64, ctypes.c_uint32, ctypes.c_uint64
 c_f32, c_vp, c_size = ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t
@@ -68,11 +69,19 @@ PROTOTYPES = {
     "hses_relu_sq": (ctypes.c_int, [c_vp, c_i64, c_vp]),
     "hses_rwkv7_wkv": (ctypes.c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i32,
                                       c_i32, c_i32, c_i32, c_vp, c_vp, c_vp]),
+    "hses_perturbed_linear_act": (ctypes.c_int, [c_vp, c_i32, c_i64, c_i64, c_i32, c_vp, c_i32,
+                                                 c_i32, c_u64, c_i32, c_f32, c_i32, c_i32, c_i32,
+                                                 c_i32, c_i32, c_vp, c_i64, c_i64, c_i32, c_i32,
+                                                 c_i32, c_vp, c_size, c_vp]),
     "hses_rwkv_act": (ctypes.c_int, [c_vp, c_i64, c_i32, c_vp]),
     "hses_tm_gates": (ctypes.c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i32,
                                      c_vp]),
     "hses_tm_kk": (ctypes.c_int, [c_vp, c_vp, c_vp, c_vp, c_i64, c_i32, c_i32, c_vp, c_vp, c_vp]),
     "hses_tm_post": (ctypes.c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i32, c_i32, c_vp]),
+    "hses_embed_layer_norm": (ctypes.c_int, [c_vp, c_i64, c_vp, c_i32, c_i32, c_vp, c_vp, c_f32,
+                                             c_vp, c_vp]),
+    "hses_add_layer_norm": (ctypes.c_int, [c_vp, c_vp, c_i64, c_i32, c_vp, c_vp, c_f32, c_vp,
+                                           c_vp]),
     "hses_read_idx_images": (ctypes.c_int, [c_vp, c_size, c_vp, c_i64, c_vp, c_vp]),
     "hses_read_idx_labels": (ctypes.c_int, [c_vp, c_size, c_vp, c_i64, c_vp]),
     "hses_shuffled_indices": (ctypes.c_int, [c_i64, c_i64, c_u64, c_vp]),

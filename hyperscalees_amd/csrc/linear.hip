@@ -18,6 +18,7 @@
 #include "mfma.h"
 #include "noise_dev.h"
 #include "runtime.h"
+#include "tile_factors.h"
 
 namespace hses {
 
@@ -75,39 +76,7 @@ __global__ __launch_bounds__(K1_THREADS) void k_linear_small(LinParams P) {
         for (int i = tid; i < P.ne_real * P.bpitch; i += K1_THREADS) Bs[i] = MathT<MATH>::zero();
         __syncthreads();
         const NoiseCtx ctx{tabs, P.log_exc, P.cos_exc};
-        const int32_t rc = P.rc;
-        // Stream rows [f0, f0 + b) are the input-side operand (Bs), rows
-        // [s0, s0 + a) the output-side one (As, only this tile's columns);
-        // sign * sigma / sqrt(r) scales A of the parameter, which is the
-        // output side for do_mm and the input side for do_Tmm.
-        const int32_t f0 = P.tmm ? P.a : 0, s0 = P.tmm ? 0 : b;
-        const float one = 1.0f;
-        const int32_t qF0 = f0 / rc, qF1 = (f0 + b + rc - 1) / rc;
-        const int32_t qS0 = (s0 + o0) / rc, qS1 = (s0 + o0 + ct + rc - 1) / rc;
-        // the tile's output-side groups not already among the input side's
-        const int32_t qX0 = P.tmm ? qS0 : max(qS0, qF1);
-        const int32_t qX1 = P.tmm ? min(qS1, qF0) : qS1;
-        const int32_t nF = qF1 - qF0;
-        const int32_t per = nF + max(0, qX1 - qX0);
-        for (int item = tid; item < nm * per; item += K1_THREADS) {
-            const int32_t lm = item / per, qi = item % per;
-            const int32_t q = qi < nF ? qF0 + qi : qX0 + (qi - nF);
-            float sign;
-            const uint64_t seed = member_seed(P.key, P.epoch, P.nreuse, P.tid_lo + m_first + lm, &sign);
-            const float sc = sign * P.bs;
-            const float fsc = P.tmm ? sc : one, ssc = P.tmm ? one : sc;
-            uint64_t s = row_start_state(seed, q, P.jump);
-            const int32_t rows_here = min(rc, P.a + b - q * rc);
-            bm_run(s, rows_here * r, ctx, [&](int32_t i, float v) {
-                const int32_t j = q * rc + i / r, c = i % r;
-                if (j >= f0 && j < f0 + b) {
-                    Bs[(size_t)(lm * r + c) * P.bpitch + (j - f0)] = MathT<MATH>::cvt(v * fsc);
-                } else {
-                    const int32_t o = j - s0 - o0;
-                    if (o >= 0 && o < ct) As[((size_t)lm * K1_CT + o) * r + c] = v * ssc;
-                }
-            });
-        }
+        gen_tile_factors<MATH>(P, ctx, m_first, nm, o0, ct, Bs, P.bpitch, As, K1_CT);
     }
     __syncthreads();
 
@@ -270,7 +239,8 @@ extern "C" size_t hses_perturbed_linear_workspace(int32_t a, int32_t b, int32_t 
                                                   int32_t math) {
     if (a < 1 || b < 1 || n < 1 || rank < 16 || rank % 16 || rank > 128 || a > 128 ||
         math != HSES_MATH_BF16)
-        return 0;  // served by k_linear_small, which needs no workspace
+        // the wide-output kernel (bf16 W) or k_linear_small (no workspace)
+        return linear_wide_workspace(a, b, rank, n, rows_per_member, n_time, math);
     DeviceState* st;
     if (get_state(&st)) return 0;
     return linear_pair_workspace(st, a, b, rank, n);
@@ -324,27 +294,58 @@ static int make_params(LinParams* P, const void* d_x, int32_t x_fmt, int64_t x_s
     return HSES_OK;
 }
 
+// The activation applied in place to y when the forward kernel did not fuse it.
+template <int ACT>
+__global__ void k_act_rows(LinParams P) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= P.total * P.a) return;
+    const int64_t L = e / P.a;
+    const int32_t c = (int32_t)(e - L * P.a);
+    float* y = P.y + phys_row(P, L, P.y_stride, P.y_plane) + c;
+    const float v = *y;
+    if constexpr (ACT == ACT_TANH) *y = tanhf(v);
+    if constexpr (ACT == ACT_SIGMOID) *y = 1.0f / (1.0f + expf(-v));
+    if constexpr (ACT == ACT_RELU_SQ) {
+        const float z = v > 0.0f ? v : 0.0f;
+        *y = z * z;
+    }
+}
+
 // Output checks and the kernel choice shared by do_mm and do_Tmm: the pair
-// kernels (rank a multiple of 16, output width <= 128, bf16) or else the
-// small-rank kernel.
+// kernels (rank a multiple of 16, output width <= 128, bf16), the wide-output
+// kernel (bf16, small rank), or else the small-rank kernel.
 static int run_linear(LinParams& P, DeviceState* st, float* d_y, int64_t y_stride,
                       int64_t y_plane, void* d_work, size_t work_bytes, void* stream,
-                      const char* name) {
+                      const char* name, int32_t act = ACT_NONE) {
     HSES_REQUIRE(d_y, "NULL pointer");
     HSES_REQUIRE(y_stride >= P.a, "y_stride smaller than a row");
     HSES_REQUIRE(P.n_time == 1 || y_plane >= (int64_t)P.n * P.rpm * y_stride, "time planes overlap");
+    HSES_REQUIRE(act >= ACT_NONE && act <= ACT_RELU_SQ, "unknown activation");
     P.y = d_y;
     P.y_stride = y_stride;
     P.y_plane = y_plane;
     hipStream_t s = (hipStream_t)stream;
     int rc = launch_linear_pair(P, st, s, d_work, work_bytes);
-    if (rc != HSES_ERR_UNSUPPORTED) return rc;
-    rc = launch_linear_small(P, st, s);
+    if (rc == HSES_ERR_UNSUPPORTED) {
+        rc = launch_linear_wide(P, st, s, d_work, work_bytes, act);
+        if (rc != HSES_ERR_UNSUPPORTED) return rc;  // activation fused
+        rc = launch_linear_small(P, st, s);
+    }
     if (rc == HSES_ERR_UNSUPPORTED)
         return set_error(HSES_ERR_UNSUPPORTED,
                          std::string(name) + ": no kernel for this rank/shape (members per 64-row "
                          "tile x rank must be <= 64, or rank a multiple of 16)");
-    return rc;
+    if (rc || act == ACT_NONE) return rc;
+    const int64_t n = P.total * P.a;
+    HSES_REQUIRE((n + 255) / 256 < (1ll << 31), "grid too large");
+    const dim3 g((uint32_t)((n + 255) / 256));
+    switch (act) {
+        case ACT_TANH: hipLaunchKernelGGL(k_act_rows<ACT_TANH>, g, dim3(256), 0, s, P); break;
+        case ACT_SIGMOID: hipLaunchKernelGGL(k_act_rows<ACT_SIGMOID>, g, dim3(256), 0, s, P); break;
+        default: hipLaunchKernelGGL(k_act_rows<ACT_RELU_SQ>, g, dim3(256), 0, s, P); break;
+    }
+    HSES_CHECK_HIP(hipGetLastError());
+    return HSES_OK;
 }
 
 extern "C" int hses_perturbed_linear(const void* d_x, int32_t x_fmt, int64_t x_stride,
@@ -417,4 +418,28 @@ extern "C" int hses_perturbed_linear_lif(const void* d_x, int32_t x_fmt, int64_t
         return set_error(HSES_ERR_UNSUPPORTED,
                          "hses_perturbed_linear_lif: needs rank a multiple of 16 <= 128 and a <= 128");
     return rc;
+}
+
+extern "C" int hses_perturbed_linear_act(const void* d_x, int32_t x_fmt, int64_t x_stride,
+                                         int64_t x_plane, int32_t n_time, const float* d_W,
+                                         int32_t a, int32_t b, uint64_t key, int32_t rank,
+                                         float sigma, int32_t epoch, int32_t noise_reuse,
+                                         int32_t tid_lo, int32_t n, int32_t rows_per_member,
+                                         float* d_y, int64_t y_stride, int64_t y_plane,
+                                         int32_t math, int32_t transposed, int32_t act,
+                                         void* d_work, size_t work_bytes, void* stream) {
+    HSES_REQUIRE(transposed == 0 || transposed == 1, "transposed must be 0 or 1");
+    LinParams P;
+    DeviceState* st = nullptr;
+    // do_Tmm: the kernels' input width is the parameter's a, their output width its b
+    int rc = transposed ? make_params(&P, d_x, x_fmt, x_stride, x_plane, n_time, d_W, b, a, key,
+                                      rank, sigma, epoch, noise_reuse, tid_lo, n, rows_per_member,
+                                      math, &st)
+                        : make_params(&P, d_x, x_fmt, x_stride, x_plane, n_time, d_W, a, b, key,
+                                      rank, sigma, epoch, noise_reuse, tid_lo, n, rows_per_member,
+                                      math, &st);
+    if (rc || n == 0) return rc;
+    P.tmm = transposed;
+    return run_linear(P, st, d_y, y_stride, y_plane, d_work, work_bytes, stream,
+                      "hses_perturbed_linear_act", act);
 }

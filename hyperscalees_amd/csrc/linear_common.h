@@ -105,6 +105,24 @@ __device__ __forceinline__ void load_x_seg(const void* x, int64_t off, bool vali
     }
 }
 
+// Eight bits of x (bit e = column k0 + e) as an MFMA operand of 0.0 / 1.0 bf16.
+// Dword q holds elements 2q (low half) and 2q+1 (high half):
+// y = byte | byte << 15 puts bit 2q at 2q and bit 2q+1 at 16 + 2q, and the
+// multiply by 0x3F80 >> 2q moves both to their half-word as bf16 1.0.
+__device__ __forceinline__ u16x8 expand_bits(uint32_t byte) {
+    const uint32_t y = byte | (byte << 15);
+    uint32_t d[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) d[q] = __umul24(y & (0x10001u << (2 * q)), 0x3F80u >> (2 * q));
+    u16x8 v;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        v[2 * q] = (uint16_t)d[q];
+        v[2 * q + 1] = (uint16_t)(d[q] >> 16);
+    }
+    return v;
+}
+
 // Fused LIF output of the large-rank kernel (see hses_perturbed_linear_lif).
 struct LifOut {
     void* spk;  // bit-packed spikes (T, M, words) or NULL
@@ -118,5 +136,18 @@ int launch_linear_small(LinParams& P, DeviceState* st, hipStream_t s);
 int launch_linear_pair(LinParams& P, DeviceState* st, hipStream_t s, void* work, size_t work_bytes,
                        const LifOut* lif = nullptr);
 size_t linear_pair_workspace(const DeviceState* st, int32_t a, int32_t b, int32_t r, int32_t n);
+// The wide small-rank kernel: 0 when it does not apply to the shape, else its
+// workspace (W as bf16, (a, kp)).
+size_t linear_wide_workspace(int32_t a, int32_t b, int32_t r, int32_t n, int32_t rows_per_member,
+                             int32_t n_time, int32_t math);
+int launch_linear_wide(LinParams& P, DeviceState* st, hipStream_t s, void* work, size_t work_bytes,
+                       int32_t act);
+// W (a, b) fp32 -> (a, kp) bf16, zero columns [b, kp); tmm: W is stored (b, a).
+void launch_w_to_bf16(const float* W, int32_t a, int32_t b, int32_t kp, int32_t tmm, uint16_t* out,
+                      hipStream_t s);
+
+// Elementwise activation fused into a forward epilogue (hses_act).
+enum { ACT_NONE = HSES_ACT_NONE, ACT_TANH = HSES_ACT_TANH, ACT_SIGMOID = HSES_ACT_SIGMOID,
+       ACT_RELU_SQ = HSES_ACT_RELU_SQ };
 
 }  // namespace hses

@@ -143,23 +143,13 @@ __global__ void k_w_to_bf16(const float* __restrict__ W, int32_t a, int32_t b, i
     out[i] = k < b ? f2bf(W[src]) : (uint16_t)0;
 }
 
-// Eight bits of x (bit e = column k0 + e) as an MFMA operand of 0.0 / 1.0 bf16.
-// Dword q holds elements 2q (low half) and 2q+1 (high half):
-// y = byte | byte << 15 puts bit 2q at 2q and bit 2q+1 at 16 + 2q, and the
-// multiply by 0x3F80 >> 2q moves both to their half-word as bf16 1.0.
-__device__ __forceinline__ u16x8 expand_bits(uint32_t byte) {
-    const uint32_t y = byte | (byte << 15);
-    uint32_t d[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) d[q] = __umul24(y & (0x10001u << (2 * q)), 0x3F80u >> (2 * q));
-    u16x8 v;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        v[2 * q] = (uint16_t)d[q];
-        v[2 * q + 1] = (uint16_t)(d[q] >> 16);
-    }
-    return v;
+void launch_w_to_bf16(const float* W, int32_t a, int32_t b, int32_t kp, int32_t tmm, uint16_t* out,
+                      hipStream_t s) {
+    const int64_t n = (int64_t)a * kp;
+    hipLaunchKernelGGL(k_w_to_bf16, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, s, W, a, b, kp,
+                       tmm, out);
 }
+
 
 // Eight activations of one row from a dense format, as bf16.  With vec
 // (strides that keep every 8-element group 16-byte aligned) a full group is

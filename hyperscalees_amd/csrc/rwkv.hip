@@ -252,6 +252,65 @@ __global__ __launch_bounds__(256) void k_tm_post(float* __restrict__ gn, const f
     if (ok) gn[o] = (gn[o] + sum * v[o]) * g[o];
 }
 
+// The LM's embedding lookup fused with ln0 (rwkv7.py:189-192, 227): row i is
+// emb[tok[i]] layer-normed.  A token outside [0, V) reads nothing and gives a
+// row of NaN.  One wave per row.
+__global__ __launch_bounds__(256) void k_embed_layer_norm(const int32_t* __restrict__ tok,
+                                                          int64_t rows,
+                                                          const float* __restrict__ emb,
+                                                          int32_t V, int32_t C,
+                                                          const float* __restrict__ w,
+                                                          const float* __restrict__ b, float eps,
+                                                          float* __restrict__ y) {
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;  // whole wave
+    const int32_t t = tok[row];
+    float* yr = y + row * C;
+    if (t < 0 || t >= V) {
+        for (int32_t c = lane; c < C; c += 64) yr[c] = __builtin_nanf("");
+        return;
+    }
+    const float* xr = emb + (int64_t)t * C;
+    float s = 0.0f, s2 = 0.0f;
+    for (int32_t c = lane; c < C; c += 64) {
+        const float v = xr[c];
+        s = s + v;
+        s2 = s2 + v * v;
+    }
+    const float mean = wave_sum(s) / (float)C;
+    const float var = wave_sum(s2) / (float)C - mean * mean;
+    const float sd = sqrtf(var + eps);
+    for (int32_t c = lane; c < C; c += 64) yr[c] = (xr[c] - mean) / sd * w[c] + b[c];
+}
+
+// The block's residual add fused with the LayerNorm that follows it
+// (rwkv7.py:243-252, 194-196): x += d in place, then y = LayerNorm(x).
+// One wave per row; each lane keeps its sums of the updated values.
+__global__ __launch_bounds__(256) void k_add_layer_norm(float* __restrict__ x,
+                                                        const float* __restrict__ d, int64_t rows,
+                                                        int32_t C, const float* __restrict__ w,
+                                                        const float* __restrict__ b, float eps,
+                                                        float* __restrict__ y) {
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;  // whole wave
+    float* xr = x + row * C;
+    const float* dr = d + row * C;
+    float s = 0.0f, s2 = 0.0f;
+    for (int32_t c = lane; c < C; c += 64) {
+        const float v = xr[c] + dr[c];
+        xr[c] = v;
+        s = s + v;
+        s2 = s2 + v * v;
+    }
+    const float mean = wave_sum(s) / (float)C;
+    const float var = wave_sum(s2) / (float)C - mean * mean;
+    const float sd = sqrtf(var + eps);
+    float* yr = y + row * C;
+    for (int32_t c = lane; c < C; c += 64) yr[c] = (xr[c] - mean) / sd * w[c] + b[c];
+}
+
 }  // namespace hses
 
 using namespace hses;
@@ -384,6 +443,33 @@ extern "C" int hses_tm_post(float* d_gn, const float* d_r, const float* d_k, con
     HSES_REQUIRE((rows * H + 3) / 4 < (1ll << 31), "grid too large");
     hipLaunchKernelGGL(k_tm_post, dim3(blocks_of(rows * H, 4)), dim3(256), 0, (hipStream_t)stream,
                        d_gn, d_r, d_k, d_v, d_g, d_r_k, rows, H, S);
+    HSES_CHECK_HIP(hipGetLastError());
+    return HSES_OK;
+}
+
+extern "C" int hses_embed_layer_norm(const int32_t* d_tokens, int64_t rows, const float* d_emb,
+                                     int32_t V, int32_t C, const float* d_w, const float* d_b,
+                                     float eps, float* d_y, void* stream) {
+    HSES_REQUIRE(rows >= 0 && V >= 1 && C >= 1, "bad sizes");
+    if (rows == 0) return HSES_OK;
+    HSES_REQUIRE(d_tokens && d_emb && d_w && d_b && d_y, "NULL pointer");
+    HSES_REQUIRE((rows + 3) / 4 < (1ll << 31), "grid too large");
+    hipLaunchKernelGGL(k_embed_layer_norm, dim3(blocks_of(rows, 4)), dim3(256), 0,
+                       (hipStream_t)stream, d_tokens, rows, d_emb, V, C, d_w, d_b, eps, d_y);
+    HSES_CHECK_HIP(hipGetLastError());
+    return HSES_OK;
+}
+
+extern "C" int hses_add_layer_norm(float* d_x, const float* d_delta, int64_t rows, int32_t C,
+                                   const float* d_w, const float* d_b, float eps, float* d_y,
+                                   void* stream) {
+    HSES_REQUIRE(rows >= 0 && C >= 1, "bad sizes");
+    if (rows == 0) return HSES_OK;
+    HSES_REQUIRE(d_x && d_delta && d_w && d_b && d_y, "NULL pointer");
+    HSES_REQUIRE(d_y != d_x && d_y != d_delta, "y must not alias x or delta");
+    HSES_REQUIRE((rows + 3) / 4 < (1ll << 31), "grid too large");
+    hipLaunchKernelGGL(k_add_layer_norm, dim3(blocks_of(rows, 4)), dim3(256), 0, (hipStream_t)stream,
+                       d_x, d_delta, rows, C, d_w, d_b, eps, d_y);
     HSES_CHECK_HIP(hipGetLastError());
     return HSES_OK;
 }

@@ -148,9 +148,10 @@ def lif_scan(cur, tau_m, v_th, v0=None, fmt=FMT_F32, want_v=False, out=None):
 
 
 def perturbed_linear(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n, rows_per_member,
-                     x_fmt=FMT_F32, x_width=None, n_time=1, math=MATH_F32, out=None):
+                     x_fmt=FMT_F32, x_width=None, n_time=1, math=MATH_F32, out=None, act=0):
     """Batched do_mm.  x is (n_time, n*rows_per_member, units) in x_fmt (or 2-D
-    when n_time == 1); returns y (n_time, n*rows_per_member, a) fp32."""
+    when n_time == 1); returns y (n_time, n*rows_per_member, a) fp32, passed
+    through the activation `act` (hses_act) when it is not 0."""
     a, b = W.shape
     _dev(W, torch.float32, "W")
     _dev(x, _FMT_DTYPE[x_fmt], "x")
@@ -166,14 +167,19 @@ def perturbed_linear(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n, rows
     wbytes = int(_lib.load().hses_perturbed_linear_workspace(a, b, rank, n, rows_per_member,
                                                               n_time, math))
     work = _workspace(wbytes, W.device)
-    _lib.call("hses_perturbed_linear", _p(x), x_fmt, units, M * units, n_time, _p(W), a, b,
-              key & (2**64 - 1), rank, sigma, epoch, noise_reuse, tid_lo, n, rows_per_member,
-              _p(out), a, M * a, math, _p(work), wbytes, _stream())
+    if act:
+        _lib.call("hses_perturbed_linear_act", _p(x), x_fmt, units, M * units, n_time, _p(W), a,
+                  b, key & (2**64 - 1), rank, sigma, epoch, noise_reuse, tid_lo, n,
+                  rows_per_member, _p(out), a, M * a, math, 0, act, _p(work), wbytes, _stream())
+    else:
+        _lib.call("hses_perturbed_linear", _p(x), x_fmt, units, M * units, n_time, _p(W), a, b,
+                  key & (2**64 - 1), rank, sigma, epoch, noise_reuse, tid_lo, n, rows_per_member,
+                  _p(out), a, M * a, math, _p(work), wbytes, _stream())
     return out if n_time > 1 or x.dim() == 3 else out[0]
 
 
 def perturbed_linear_t(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n, rows_per_member,
-                       x_fmt=FMT_F32, n_time=1, math=MATH_F32, out=None):
+                       x_fmt=FMT_F32, n_time=1, math=MATH_F32, out=None, act=0):
     """Batched do_Tmm: y = x W + (x A_m) B_m^T for W of shape (a, b).  x is
     (n_time, n*rows_per_member, a) in x_fmt (or 2-D when n_time == 1);
     returns y (n_time, n*rows_per_member, b) fp32."""
@@ -192,9 +198,14 @@ def perturbed_linear_t(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n, ro
     wbytes = int(_lib.load().hses_perturbed_linear_t_workspace(a, b, rank, n, rows_per_member,
                                                                 n_time, math))
     work = _workspace(wbytes, W.device)
-    _lib.call("hses_perturbed_linear_t", _p(x), x_fmt, units, M * units, n_time, _p(W), a, b,
-              key & (2**64 - 1), rank, sigma, epoch, noise_reuse, tid_lo, n, rows_per_member,
-              _p(out), b, M * b, math, _p(work), wbytes, _stream())
+    if act:
+        _lib.call("hses_perturbed_linear_act", _p(x), x_fmt, units, M * units, n_time, _p(W), a,
+                  b, key & (2**64 - 1), rank, sigma, epoch, noise_reuse, tid_lo, n,
+                  rows_per_member, _p(out), b, M * b, math, 1, act, _p(work), wbytes, _stream())
+    else:
+        _lib.call("hses_perturbed_linear_t", _p(x), x_fmt, units, M * units, n_time, _p(W), a,
+                  b, key & (2**64 - 1), rank, sigma, epoch, noise_reuse, tid_lo, n,
+                  rows_per_member, _p(out), b, M * b, math, _p(work), wbytes, _stream())
     return out if n_time > 1 or x.dim() == 3 else out[0]
 
 

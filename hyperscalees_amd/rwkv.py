@@ -13,7 +13,7 @@ import torch
 
 from . import _lib
 from . import kernels as K
-from ._lib import MATH_F32
+from ._lib import ACT_RELU_SQ, ACT_SIGMOID, ACT_TANH, MATH_F32
 
 
 def _stream():
@@ -92,15 +92,16 @@ class EsLinear:
     seqs_per_member: int = 1
 
 
-def linear(x, W, es=None, math=MATH_F32):
+def linear(x, W, es=None, math=MATH_F32, act=0):
     """x (nseq, T, in) @ W^T for W (out, in): the plain Linear (es None) or every
-    member's perturbed do_mm (eggroll.rs:419-446) on its own sequences."""
+    member's perturbed do_mm (eggroll.rs:419-446) on its own sequences; `act`
+    (hses_act) applies the elementwise op that follows."""
     nseq, T, cin = x.shape
     if es is None:
         es = EsLinear(key=0, rank=0, sigma=0.0, n=nseq, seqs_per_member=1)
     y = K.perturbed_linear(x.reshape(1, nseq * T, cin), W, es.key, es.rank, es.sigma, es.epoch,
                            es.noise_reuse, es.tid_lo, es.n, es.seqs_per_member * T, n_time=1,
-                           math=math)
+                           math=math, act=act)
     return y.reshape(nseq, T, W.shape[0])
 
 
@@ -110,21 +111,22 @@ def channel_mixing(x, state, x_k, Wk, Wv, length, new_starts=None, es_key=None, 
     xk = x + ([state, x[:-1]] - x) * x_k; out = relu(xk Wk^T)^2 Wv^T; last = x[length-1].
     x (nseq, T, C), state (nseq, C), Wk (F, C), Wv (C, F)."""
     xk = token_shift_mix(x, state, x_k.reshape(1, -1), new_starts)[0]
-    kk = relu_sq_(linear(xk, Wk, es_key, math))
+    kk = linear(xk, Wk, es_key, math, act=ACT_RELU_SQ)
     out = linear(kk, Wv, es_value, math)
     last = x[:, length - 1, :].contiguous()
     return out, last
 
 
-def linear_t(x, W, es=None, math=MATH_F32):
+def linear_t(x, W, es=None, math=MATH_F32, act=0):
     """x (nseq, T, in) @ W for W (in, out): the plain Tmm (es None) or every
-    member's perturbed do_Tmm (common.rs:156-159, eggroll.rs do_Tmm)."""
+    member's perturbed do_Tmm (common.rs:156-159, eggroll.rs:450-477), then
+    the activation `act` (hses_act)."""
     nseq, T, cin = x.shape
     if es is None:
         es = EsLinear(key=0, rank=0, sigma=0.0, n=nseq, seqs_per_member=1)
     y = K.perturbed_linear_t(x.reshape(1, nseq * T, cin), W, es.key, es.rank, es.sigma, es.epoch,
                              es.noise_reuse, es.tid_lo, es.n, es.seqs_per_member * T, n_time=1,
-                             math=math)
+                             math=math, act=act)
     return y.reshape(nseq, T, W.shape[1])
 
 
@@ -164,21 +166,21 @@ def time_mixing(P, x, state, v_first, H, length, layer_id, new_starts=None, es=N
     def lin(i, name):
         return linear(xm[i], P[name], es.get(name), math)
 
-    def low(inp, n1, n2, kind):
-        h = rwkv_act_(linear_t(inp, P[n1], es.get(n1), math), kind)
+    def low(inp, n1, n2, act):
+        h = linear_t(inp, P[n1], es.get(n1), math, act=act)
         return linear_t(h, P[n2], es.get(n2), math)
 
     r = lin(0, "receptance")
-    w = low(xm[1], "w1", "w2", 0)        # w2 output; the gate turns it into w
+    w = low(xm[1], "w1", "w2", ACT_TANH)  # w2 output; the gate turns it into w
     k = lin(2, "key")
     v = lin(3, "value")
     if layer_id == 0:
         v_first = v.clone()
         v2o = None
     else:
-        v2o = low(xm[3], "v1", "v2", 0)
-    a = low(xm[4], "a1", "a2", 0)        # a2 output; the gate turns it into a
-    g = low(xm[5], "g1", "g2", 1)
+        v2o = low(xm[3], "v1", "v2", ACT_TANH)
+    a = low(xm[4], "a1", "a2", ACT_TANH)  # a2 output; the gate turns it into a
+    g = low(xm[5], "g1", "g2", ACT_SIGMOID)
     rows = nseq * T
     _lib.call("hses_tm_gates", _p(w), _p(a), _p(v2o), _p(v), _p(v_first), _p(P["w0"]), _p(P["a0"]),
               _p(P["v0"]), rows, C, _stream())

@@ -54,6 +54,16 @@ typedef enum { HSES_SGD = 0, HSES_ADAM = 1, HSES_ADAMW = 2 } hses_solver;
 /* Reward kinds of fitness_from_logits_reward (burn_impl/hyperscalees-envs/src/snn_mnist.rs:175-201). */
 typedef enum { HSES_REWARD_LOGLIK = 0, HSES_REWARD_BINARY = 1 } hses_reward;
 
+/* Elementwise activations a forward can apply to its output (the op that follows a
+ * Linear / Tmm in the models: tanh and sigmoid of TimeMixing's low-rank branches,
+ * llm.rs:388-410, relu^2 of ChannelMixing, llm.rs:206). */
+typedef enum {
+    HSES_ACT_NONE = 0,
+    HSES_ACT_TANH = 1,
+    HSES_ACT_SIGMOID = 2, /* 1 / (1 + exp(-y)) */
+    HSES_ACT_RELU_SQ = 3  /* max(y, 0)^2 */
+} hses_act;
+
 /* ---- runtime ---------------------------------------------------------- */
 
 /* Initialise device `device` (builds the Box-Muller correction tables and
@@ -139,7 +149,10 @@ int hses_lif_scan(const float *d_cur, const float *d_v0, int32_t T, int64_t rows
  * d_work must hold hses_perturbed_linear_workspace(...) bytes (a bf16 copy of W
  * and, for large ranks, one per-workgroup staging slot for a pair's B factor;
  * the (n, b, r) factor tensor itself is never materialised).  Large ranks
- * (r a multiple of 16, r <= 128, a <= 128) need math = HSES_MATH_BF16. */
+ * (r a multiple of 16, r <= 128, a <= 128) need math = HSES_MATH_BF16.  With
+ * math = HSES_MATH_BF16 and small ranks (members per 128-row tile x rank <= 16)
+ * the wide-output kernel runs when the workspace holds its bf16 copy of W and x
+ * rows are 16-byte aligned; otherwise the small-rank kernel (no workspace). */
 size_t hses_perturbed_linear_workspace(int32_t a, int32_t b, int32_t rank, int32_t n,
                                        int32_t rows_per_member, int32_t n_time, int32_t math);
 int hses_perturbed_linear(const void *d_x, int32_t x_fmt, int64_t x_stride, int64_t x_plane,
@@ -164,6 +177,19 @@ int hses_perturbed_linear_t(const void *d_x, int32_t x_fmt, int64_t x_stride, in
                             int32_t noise_reuse, int32_t tid_lo, int32_t n,
                             int32_t rows_per_member, float *d_y, int64_t y_stride, int64_t y_plane,
                             int32_t math, void *d_work, size_t work_bytes, void *stream);
+
+/* hses_perturbed_linear (transposed = 0) or hses_perturbed_linear_t (transposed = 1)
+ * followed by the activation `act` (hses_act) on every output: a Linear / Tmm and the
+ * elementwise op after it (llm.rs:206, 388-410), fused into the forward's epilogue by the
+ * wide-output kernel and applied in place after it otherwise.  Workspace as for the
+ * unfused entry point of the same orientation. */
+int hses_perturbed_linear_act(const void *d_x, int32_t x_fmt, int64_t x_stride, int64_t x_plane,
+                              int32_t n_time, const float *d_W, int32_t a, int32_t b,
+                              uint64_t key, int32_t rank, float sigma, int32_t epoch,
+                              int32_t noise_reuse, int32_t tid_lo, int32_t n,
+                              int32_t rows_per_member, float *d_y, int64_t y_stride,
+                              int64_t y_plane, int32_t math, int32_t transposed, int32_t act,
+                              void *d_work, size_t work_bytes, void *stream);
 
 /* Perturbed forward fused with the LIF layer that consumes it
  * (forward_batched_lora_half_with_lif, snn.rs:544-595: lora_linear_batched
@@ -279,6 +305,18 @@ int hses_tm_kk(float *d_k, const float *d_k_k, const float *d_k_a, const float *
                int32_t H, int32_t S, float *d_ai, float *d_bi, void *stream);
 int hses_tm_post(float *d_gn, const float *d_r, const float *d_k, const float *d_v, const float *d_g,
                  const float *d_r_k, int64_t rows, int32_t H, int32_t S, void *stream);
+
+/* The RWKV-7 LM around the blocks (src/hyperscalees/models/llm/rwkv7.py:189-253):
+ * hses_embed_layer_norm: y[i] = LayerNorm(emb[tokens[i]]) with ln0's w, b (embed and
+ *   the ln0 of forward_seq; a token outside [0, V) gives a row of NaN);
+ * hses_add_layer_norm: x += delta in place, then y = LayerNorm(x) (a block's residual
+ *   add and the ln2 / next ln1 / ln_out that reads it); y must not alias x or delta.
+ * LayerNorm as hses_layer_norm. */
+int hses_embed_layer_norm(const int32_t *d_tokens, int64_t rows, const float *d_emb, int32_t V,
+                          int32_t C, const float *d_w, const float *d_b, float eps, float *d_y,
+                          void *stream);
+int hses_add_layer_norm(float *d_x, const float *d_delta, int64_t rows, int32_t C,
+                        const float *d_w, const float *d_b, float eps, float *d_y, void *stream);
 
 /* ---- data path (host only: no device, no stream) ---------------------- */
 

@@ -166,21 +166,41 @@ void or_channel_mixing(const float *x, int32_t T, int32_t C, const float *state,
                        const float *x_k, const float *Wk, int32_t F, const float *Wv,
                        int32_t length, const uint8_t *new_starts, float *out, float *last);
 
-/* TimeMixing weights (llm.rs:304-342); Linear weights (out, in), Tmm weights (in, out),
- * every low-rank width d_lora. */
+/* TimeMixing weights (llm.rs:304-342); Linear weights (out, in), Tmm weights (in, out);
+ * the low-rank widths of the decay (w1/w2), value (v1/v2), in-context rate (a1/a2) and
+ * gate (g1/g2) branches. */
 typedef struct {
     const float *x_r, *x_w, *x_k, *x_v, *x_a, *x_g; /* (C) */
     const float *receptance, *key, *value, *output; /* (C, C) */
     const float *w0, *v0, *a0;                       /* (C) */
-    const float *w1, *v1, *a1, *g1;                  /* (C, d_lora) */
-    const float *w2, *v2, *a2, *g2;                  /* (d_lora, C) */
+    const float *w1, *v1, *a1, *g1;                  /* (C, d_*) */
+    const float *w2, *v2, *a2, *g2;                  /* (d_*, C) */
     const float *k_k, *k_a, *r_k;                    /* (C) */
     const float *ln_w, *ln_b;                        /* (C) */
-    int32_t d_lora;
+    int32_t d_w, d_v, d_a, d_g;
 } or_tm_weights;
 void or_time_mixing(const or_tm_weights *P, const float *x, int32_t T, int32_t C, int32_t H,
                     const float *state, float *v_first, int32_t length, const uint8_t *new_starts,
                     int32_t layer_id, float *out, float *state_out);
+
+/* One RWKV-7 block (rwkv7.py:232-253): TimeMixing 'att', ChannelMixing 'ffn' (x_k (C),
+ * key (F, C), value (C, F)) and the LayerNorms ln1 / ln2. */
+typedef struct {
+    or_tm_weights tm;
+    const float *ffn_x_k, *ffn_key, *ffn_value;
+    const float *ln1_w, *ln1_b, *ln2_w, *ln2_b;
+} or_rwkv_block;
+/* The RWKV-7 LM (rwkv7.py:117-253): emb (V, C), ln0, blocks, ln_out, head (V, C). */
+typedef struct {
+    int32_t n_layer, C, H, F, V;
+    const float *emb, *ln0_w, *ln0_b, *ln_out_w, *ln_out_b, *head;
+    const or_rwkv_block *blocks;
+} or_rwkv_lm;
+/* embed + forward_seq + outhead (rwkv7.py:189-253) of one sequence of T tokens at full
+ * length without new starts.  state (n_layer, 2 + S, C) is read and updated in place
+ * (row 0 ChannelMixing's shift, rows 1.. TimeMixing's state); logits (T, V). */
+void or_rwkv_lm_forward(const or_rwkv_lm *P, const int32_t *tokens, int32_t T, float *state,
+                        float *logits);
 
 #ifdef __cplusplus
 }

@@ -172,32 +172,35 @@ void or_time_mixing(const or_tm_weights *P, const float *x, int32_t T, int32_t C
     float *a = (float *)malloc(sizeof(float) * (size_t)TC + 4);
     float *g = (float *)malloc(sizeof(float) * (size_t)TC + 4);
     float *tmp = (float *)malloc(sizeof(float) * (size_t)TC + 4);
-    const int32_t D = P->d_lora;
+    int32_t D = P->d_w;
+    if (P->d_v > D) D = P->d_v;
+    if (P->d_a > D) D = P->d_a;
+    if (P->d_g > D) D = P->d_g;
     float *low = (float *)malloc(sizeof(float) * (size_t)T * D + 4);
     or_matmul_abt(mix[0], T, C, P->receptance, C, r);
     /* w = -softplus(-(w0 + w2(tanh(w1 xw)))) - 0.5 */
-    matmul_ab_f32(mix[1], T, C, P->w1, D, low);
-    for (int64_t e = 0; e < (int64_t)T * D; ++e) low[e] = tanhf(low[e]);
-    matmul_ab_f32(low, T, D, P->w2, C, tmp);
+    matmul_ab_f32(mix[1], T, C, P->w1, P->d_w, low);
+    for (int64_t e = 0; e < (int64_t)T * P->d_w; ++e) low[e] = tanhf(low[e]);
+    matmul_ab_f32(low, T, P->d_w, P->w2, C, tmp);
     for (int64_t e = 0; e < TC; ++e) w[e] = -softplusf_(-(P->w0[e % C] + tmp[e])) - 0.5f;
     or_matmul_abt(mix[2], T, C, P->key, C, k);
     or_matmul_abt(mix[3], T, C, P->value, C, v);
     if (layer_id == 0) {
         memcpy(v_first, v, sizeof(float) * (size_t)TC);
     } else {
-        matmul_ab_f32(mix[3], T, C, P->v1, D, low);
-        for (int64_t e = 0; e < (int64_t)T * D; ++e) low[e] = tanhf(low[e]);
-        matmul_ab_f32(low, T, D, P->v2, C, tmp);
+        matmul_ab_f32(mix[3], T, C, P->v1, P->d_v, low);
+        for (int64_t e = 0; e < (int64_t)T * P->d_v; ++e) low[e] = tanhf(low[e]);
+        matmul_ab_f32(low, T, P->d_v, P->v2, C, tmp);
         for (int64_t e = 0; e < TC; ++e)
             v[e] = v[e] + (v_first[e] - v[e]) * sigmoidf_(P->v0[e % C] + tmp[e]);
     }
-    matmul_ab_f32(mix[4], T, C, P->a1, D, low);
-    for (int64_t e = 0; e < (int64_t)T * D; ++e) low[e] = tanhf(low[e]);
-    matmul_ab_f32(low, T, D, P->a2, C, tmp);
+    matmul_ab_f32(mix[4], T, C, P->a1, P->d_a, low);
+    for (int64_t e = 0; e < (int64_t)T * P->d_a; ++e) low[e] = tanhf(low[e]);
+    matmul_ab_f32(low, T, P->d_a, P->a2, C, tmp);
     for (int64_t e = 0; e < TC; ++e) a[e] = sigmoidf_(P->a0[e % C] + tmp[e]);
-    matmul_ab_f32(mix[5], T, C, P->g1, D, low);
-    for (int64_t e = 0; e < (int64_t)T * D; ++e) low[e] = sigmoidf_(low[e]);
-    matmul_ab_f32(low, T, D, P->g2, C, g);
+    matmul_ab_f32(mix[5], T, C, P->g1, P->d_g, low);
+    for (int64_t e = 0; e < (int64_t)T * P->d_g; ++e) low[e] = sigmoidf_(low[e]);
+    matmul_ab_f32(low, T, P->d_g, P->g2, C, g);
     /* kk = normalize_per_head(k * k_k); k = k * (k_a * (a - 1) + 1); a_i = -kk, b_i = kk * a */
     float *ai = (float *)malloc(sizeof(float) * (size_t)TC + 4);
     float *bi = (float *)malloc(sizeof(float) * (size_t)TC + 4);
@@ -247,4 +250,41 @@ void or_time_mixing(const or_tm_weights *P, const float *x, int32_t T, int32_t C
     free(w);
     free(r);
     for (int m = 0; m < 6; ++m) free(mix[m]);
+}
+
+/* rwkv7.py:189-253: x = ln0(emb[tokens]); per block x += att(ln1(x)), x += ffn(ln2(x))
+ * with v_first carried from block 0; logits = ln_out(x) head^T.  LayerNorm eps 1e-5
+ * (rwkv7.py:32). */
+void or_rwkv_lm_forward(const or_rwkv_lm *P, const int32_t *tokens, int32_t T, float *state,
+                        float *logits) {
+    const int32_t C = P->C, H = P->H, S = C / H;
+    const int64_t TC = (int64_t)T * C, SR = (int64_t)(2 + S) * C;
+    float *x = (float *)malloc(sizeof(float) * (size_t)TC + 4);
+    float *h = (float *)malloc(sizeof(float) * (size_t)TC + 4);
+    float *d = (float *)malloc(sizeof(float) * (size_t)TC + 4);
+    float *vf = (float *)calloc((size_t)TC + 1, sizeof(float));
+    float *st = (float *)malloc(sizeof(float) * (size_t)(1 + S) * C + 4);
+    for (int32_t t = 0; t < T; ++t)
+        memcpy(x + (int64_t)t * C, P->emb + (int64_t)tokens[t] * C, sizeof(float) * (size_t)C);
+    or_layer_norm(x, T, C, P->ln0_w, P->ln0_b, 1e-5f, h);
+    memcpy(x, h, sizeof(float) * (size_t)TC);
+    for (int32_t l = 0; l < P->n_layer; ++l) {
+        const or_rwkv_block *B = &P->blocks[l];
+        float *sl = state + (int64_t)l * SR;
+        or_layer_norm(x, T, C, B->ln1_w, B->ln1_b, 1e-5f, h);
+        or_time_mixing(&B->tm, h, T, C, H, sl + C, vf, T, NULL, l, d, st);
+        memcpy(sl + C, st, sizeof(float) * (size_t)(1 + S) * C);
+        for (int64_t e = 0; e < TC; ++e) x[e] = x[e] + d[e];
+        or_layer_norm(x, T, C, B->ln2_w, B->ln2_b, 1e-5f, h);
+        or_channel_mixing(h, T, C, sl, B->ffn_x_k, B->ffn_key, P->F, B->ffn_value, T, NULL, d, st);
+        memcpy(sl, st, sizeof(float) * (size_t)C);
+        for (int64_t e = 0; e < TC; ++e) x[e] = x[e] + d[e];
+    }
+    or_layer_norm(x, T, C, P->ln_out_w, P->ln_out_b, 1e-5f, h);
+    or_matmul_abt(h, T, C, P->head, P->V, logits);
+    free(st);
+    free(vf);
+    free(d);
+    free(h);
+    free(x);
 }

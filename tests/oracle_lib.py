@@ -32,7 +32,21 @@ TM_FIELDS = (TM_VECTORS + TM_LINEAR + ("w0", "v0", "a0") + ("w1", "v1", "a1", "g
 
 
 class TmWeights(ctypes.Structure):
-    _fields_ = [(name, ctypes.c_void_p) for name in TM_FIELDS] + [("d_lora", c_i32)]
+    _fields_ = ([(name, ctypes.c_void_p) for name in TM_FIELDS]
+                + [("d_w", c_i32), ("d_v", c_i32), ("d_a", c_i32), ("d_g", c_i32)])
+
+
+class RwkvBlock(ctypes.Structure):
+    _fields_ = [("tm", TmWeights)] + [(n, ctypes.c_void_p) for n in
+                                      ("ffn_x_k", "ffn_key", "ffn_value", "ln1_w", "ln1_b",
+                                       "ln2_w", "ln2_b")]
+
+
+class RwkvLm(ctypes.Structure):
+    _fields_ = ([(n, c_i32) for n in ("n_layer", "C", "H", "F", "V")]
+                + [(n, ctypes.c_void_p) for n in ("emb", "ln0_w", "ln0_b", "ln_out_w", "ln_out_b",
+                                                  "head")]
+                + [("blocks", ctypes.POINTER(RwkvBlock))])
 
 
 def build():
@@ -96,6 +110,7 @@ def load():
                                      ctypes.c_void_p, f32p, f32p]),
         "or_time_mixing": (None, [ctypes.POINTER(TmWeights), f32p, c_i32, c_i32, c_i32, f32p,
                                   f32p, c_i32, ctypes.c_void_p, c_i32, f32p, f32p]),
+        "or_rwkv_lm_forward": (None, [ctypes.POINTER(RwkvLm), i32p, c_i32, f32p, f32p]),
         "or_solver_step": (None, [c_i32, c_f32, c_f32, c_f32, c_f32, c_f32, c_i32, f32p, f32p,
                                   f32p, f32p, c_i64, f32p]),
         "or_snn_forward_members": (None, [ctypes.POINTER(SnnCfg), ctypes.c_void_p,
@@ -231,6 +246,11 @@ def channel_mixing(x, state, x_k, Wk, Wv, length, new_starts=None):
     return out, last
 
 
+def _tm_struct(keep):
+    return TmWeights(*[keep[name].ctypes.data for name in TM_FIELDS],
+                     *[keep[name].shape[1] for name in ("w1", "v1", "a1", "g1")])
+
+
 def time_mixing(P, x, state, v_first, H, length, layer_id, new_starts=None):
     """TimeMixing::forward (llm.rs:348-480) of one sequence.  P maps the
     TM_FIELDS names to arrays (Linear weights (out, in), Tmm weights (in, out)).
@@ -239,7 +259,7 @@ def time_mixing(P, x, state, v_first, H, length, layer_id, new_starts=None):
     T, C = x.shape
     S = C // H
     keep = {name: _f(P[name]) for name in TM_FIELDS}
-    tw = TmWeights(*[keep[name].ctypes.data for name in TM_FIELDS], keep["w1"].shape[1])
+    tw = _tm_struct(keep)
     vf = np.array(v_first, np.float32, copy=True).reshape(T, C)
     out = np.zeros((T, C), np.float32)
     st = np.zeros((1 + S, C), np.float32)
@@ -247,3 +267,30 @@ def time_mixing(P, x, state, v_first, H, length, layer_id, new_starts=None):
     load().or_time_mixing(ctypes.byref(tw), _f(x), T, C, H, _f(state), vf, length,
                           None if ns is None else ns.ctypes.data, layer_id, out, st)
     return out, st, vf
+
+
+def rwkv_lm_forward(P, tokens, H, state=None):
+    """The RWKV-7 LM (rwkv7.py:189-253) on one sequence.  P: emb (V, C), ln0_w,
+    ln0_b, ln_out_w, ln_out_b, head (V, C) and `blocks`, a list of dicts with the
+    TimeMixing names, ffn_x_k, ffn_key (F, C), ffn_value (C, F), ln1_w, ln1_b,
+    ln2_w, ln2_b.  Returns (logits (T, V), state (n_layer, 2 + S, C))."""
+    tokens = np.ascontiguousarray(tokens, np.int32)
+    V, C = P["emb"].shape
+    L = len(P["blocks"])
+    S = C // H
+    F = P["blocks"][0]["ffn_key"].shape[0]
+    keep = {n: _f(P[n]) for n in ("emb", "ln0_w", "ln0_b", "ln_out_w", "ln_out_b", "head")}
+    bkeep = [{n: _f(v) for n, v in b.items()} for b in P["blocks"]]
+    blocks = (RwkvBlock * L)()
+    for l, b in enumerate(bkeep):
+        blocks[l].tm = _tm_struct(b)
+        for n in ("ffn_x_k", "ffn_key", "ffn_value", "ln1_w", "ln1_b", "ln2_w", "ln2_b"):
+            setattr(blocks[l], n, b[n].ctypes.data)
+    lm = RwkvLm(L, C, H, F, V, *[keep[n].ctypes.data for n in ("emb", "ln0_w", "ln0_b",
+                                                               "ln_out_w", "ln_out_b", "head")],
+                blocks)
+    st = (np.zeros((L, 2 + S, C), np.float32) if state is None
+          else np.array(state, np.float32, copy=True))
+    logits = np.zeros((tokens.size, V), np.float32)
+    load().or_rwkv_lm_forward(ctypes.byref(lm), tokens, tokens.size, st, logits)
+    return logits, st

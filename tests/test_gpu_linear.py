@@ -262,3 +262,62 @@ def test_perturbed_linear_t_clean(hses_gpu):
                                     4, 0.0, 0, 0, 0, 40, 1)
     torch.cuda.synchronize()
     assert_close(y.cpu().numpy(), x.astype(np.float64) @ W.astype(np.float64), 1e-5)
+
+
+# -- the wide-output small-rank kernel (bf16 math, members x rank <= 16 per 128-row tile) --
+
+@pytest.mark.parametrize("n,rpm,T,a,b,r,tid_lo,fmt", [
+    (4, 128, 1, 512, 512, 1, 0, FMT_F32),      # C5 square layer, one member per tile
+    (3, 128, 1, 2048, 512, 1, 1, FMT_F32),     # C5 ChannelMixing key, odd first member
+    (2, 128, 1, 512, 2048, 1, 0, FMT_BF16),    # C5 ChannelMixing value, bf16 activations
+    (6, 64, 1, 300, 256, 2, 3, FMT_F32),       # two members per tile, ragged output width
+    (5, 100, 1, 130, 96, 1, 0, FMT_F32),       # members straddle tiles (three per tile)
+    (4, 32, 2, 256, 200, 4, 2, FMT_F32),       # time-major planes, four members per tile
+    (3, 64, 1, 192, 300, 2, 0, FMT_BITS),      # bit-packed input, K not a multiple of 64
+])
+def test_wide_kernel(hses_gpu, n, rpm, T, a, b, r, tid_lo, fmt):
+    rng = np.random.default_rng(n * 7 + a + b + r)
+    if fmt == FMT_BITS:
+        x3 = (rng.random((T, n * rpm, b)) < 0.3).astype(np.float32)
+    else:
+        x3 = rng.standard_normal((T, n * rpm, b)).astype(np.float32)
+    W = (rng.standard_normal((a, b)) / np.sqrt(b)).astype(np.float32)
+    sigma = 0.2
+    A, B = factors(sigma, r, n, tid_lo, a, b)
+    y = run(hses_gpu, x3, W, r, sigma, n, rpm, tid_lo, fmt=fmt, math=MATH_BF16)
+    xb = bf16_round(x3)
+    assert_close(y, ref_forward(xb, bf16_round(W), A, bf16_round(B), rpm), 2e-3)
+    assert_close(y, ref_forward(x3, W, A, B, rpm), 2e-2)
+
+
+@pytest.mark.parametrize("a,b,act", [(512, 32, 1), (96, 512, 2), (512, 512, 3), (256, 64, 0)])
+def test_wide_kernel_transposed_and_activations(hses_gpu, a, b, act):
+    # do_Tmm on a parameter W (a, b): y = act(x W + (x A_m) B_m^T), bf16 math
+    from hyperscalees_amd._lib import ACT_RELU_SQ, ACT_SIGMOID, ACT_TANH
+    n, rpm, r, tid_lo, sigma = 4, 128, 1, 1, 0.3
+    rng = np.random.default_rng(a + b + act)
+    x = rng.standard_normal((n * rpm, a)).astype(np.float32)
+    W = (rng.standard_normal((a, b)) / np.sqrt(a)).astype(np.float32)
+    A, B = factors(sigma, r, n, tid_lo, a, b)
+    y = hses_gpu.perturbed_linear_t(torch.from_numpy(x).cuda(), torch.from_numpy(W).cuda(), KEY, r,
+                                    sigma, 0, 0, tid_lo, n, rpm, math=MATH_BF16, act=act)
+    torch.cuda.synchronize()
+    ref = ref_forward_t(bf16_round(x)[None], bf16_round(W), bf16_round(A), B, rpm)[0]
+    f = {0: lambda v: v, ACT_TANH: np.tanh, ACT_SIGMOID: lambda v: 1 / (1 + np.exp(-v)),
+         ACT_RELU_SQ: lambda v: np.maximum(v, 0) ** 2}[act]
+    assert_close(y.cpu().numpy(), f(ref), 2e-3)
+
+
+def test_linear_activation_unfused_path_matches(hses_gpu):
+    # fp32 math runs k_linear_small and applies the activation afterwards
+    from hyperscalees_amd._lib import ACT_RELU_SQ
+    n, rpm, a, b, r = 3, 16, 40, 24, 2
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((n * rpm, b)).astype(np.float32)
+    W = (rng.standard_normal((a, b)) / np.sqrt(b)).astype(np.float32)
+    A, B = factors(0.2, r, n, 0, a, b)
+    y = hses_gpu.perturbed_linear(torch.from_numpy(x).cuda(), torch.from_numpy(W).cuda(), KEY, r,
+                                  0.2, 0, 0, 0, n, rpm, act=ACT_RELU_SQ)
+    torch.cuda.synchronize()
+    ref = np.maximum(ref_forward(x[None], W, A, B, rpm)[0], 0) ** 2
+    assert_close(y.cpu().numpy(), ref, 1e-5)

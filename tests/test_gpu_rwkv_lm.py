@@ -1,0 +1,123 @@
+"""GPU parity of the RWKV-7 LM ES step (hyperscalees_amd.rwkv_lm) against the
+oracle's LM forward (rwkv7.py:189-253; pinned in tests/test_oracle_rwkv.py) on
+each member's materialised parameters W + A_m B_m^T, the log-likelihood
+fitness, and the ES gradient and SGD step of every MM parameter.
+
+fp32 linears: rel 1e-4 of the logits' scale through two blocks (the WKV-7
+recurrence's bound); bf16 linears (the C5 precision): rel 2e-2."""
+import numpy as np
+import pytest
+import torch
+
+from hyperscalees_amd import rwkv_lm
+from hyperscalees_amd._lib import MATH_BF16, MATH_F32, SGD
+from tests import oracle_lib as O
+
+pytestmark = pytest.mark.gpu
+
+SMALL = dict(n_layer=2, d_model=64, head_size=32, vocab=50, ffn_mult=4, seq_len=8, n=4, rank=1,
+             sigma=0.05, math=MATH_F32, solver=SGD, lr=0.1, init_std=0.2, widths=(16, 8, 16, 32))
+
+
+def member_params(params, es, m):
+    """The oracle's parameter dict of member m: W + A_m B_m^T for every MM parameter."""
+    c = es.cfg
+    bs = O.load().or_base_sigma(c.sigma, c.rank)
+    P = {k: v for k, v in params.items() if k != "blocks"}
+    P["blocks"] = []
+    for l, B in enumerate(params["blocks"]):
+        Bm = dict(B)
+        for name in rwkv_lm.TM_MATRICES + rwkv_lm.FFN_MATRICES:
+            a, b = B[name].shape
+            A, Bf = O.lora_factors(bs, es.keys[(l, name)], c.rank, 0, [m], a, b)
+            Bm[name] = (B[name].astype(np.float64) + A[0].astype(np.float64) @ Bf[0].T.astype(np.float64)).astype(np.float32)
+        P["blocks"].append(Bm)
+    return P
+
+
+def close(got, ref, rel):
+    ref = np.asarray(ref, np.float64)
+    err = np.abs(np.asarray(got, np.float64) - ref).max()
+    assert err <= rel * np.abs(ref).max(), f"max err {err:.3e} vs scale {np.abs(ref).max():.3e}"
+
+
+def log_softmax(z):
+    z = z.astype(np.float64)
+    m = z.max(-1, keepdims=True)
+    return z - m - np.log(np.exp(z - m).sum(-1, keepdims=True))
+
+
+@pytest.mark.parametrize("math,spm,rel", [(MATH_F32, 1, 1e-4), (MATH_F32, 2, 1e-4),
+                                          (MATH_BF16, 1, 2e-2)])
+def test_lm_members_match_oracle(hses_gpu, math, spm, rel):
+    cfg = rwkv_lm.RwkvLmConfig(**dict(SMALL, math=math, seqs_per_member=spm))
+    params = rwkv_lm.init_params(cfg, seed=3)
+    es = rwkv_lm.RwkvLmEs(cfg, params)
+    H = cfg.d_model // cfg.head_size
+    rng = np.random.default_rng(4)
+    nseq, T = cfg.n * spm, cfg.seq_len
+    tok = rng.integers(0, cfg.vocab, (nseq, T + 1)).astype(np.int32)
+    tok_d = torch.from_numpy(tok).cuda()
+    lg = es.logits(tok_d[:, :-1].contiguous()).cpu().numpy().reshape(nseq, T, cfg.vocab)
+    fit = es.forward(tok_d).cpu().numpy()
+    torch.cuda.synchronize()
+    for m in range(cfg.n):
+        Pm = member_params(params, es, m)
+        lls = []
+        for q in range(m * spm, (m + 1) * spm):
+            ref, _ = O.rwkv_lm_forward(Pm, tok[q, :-1], H)
+            close(lg[q], ref, rel)
+            lls.append(log_softmax(ref)[np.arange(T), tok[q, 1:]])
+        np.testing.assert_allclose(fit[m], np.mean(lls), rtol=10 * rel, atol=10 * rel)
+
+
+def test_lm_plain_forward_matches_oracle(hses_gpu):
+    cfg = rwkv_lm.RwkvLmConfig(**dict(SMALL, n_layer=3, n=3))
+    params = rwkv_lm.init_params(cfg, seed=5)
+    es = rwkv_lm.RwkvLmEs(cfg, params)
+    rng = np.random.default_rng(6)
+    tok = rng.integers(0, cfg.vocab, (3, 11)).astype(np.int32)     # T != seq_len
+    lg = es.logits(torch.from_numpy(tok).cuda(), perturb=False).cpu().numpy().reshape(3, 11, -1)
+    for q in range(3):
+        ref, _ = O.rwkv_lm_forward(params, tok[q], cfg.d_model // cfg.head_size)
+        close(lg[q], ref, 1e-4)
+
+
+def test_lm_es_step_gradients_and_sgd(hses_gpu):
+    cfg = rwkv_lm.RwkvLmConfig(**dict(SMALL, n=6))
+    params = rwkv_lm.init_params(cfg, seed=7)
+    es = rwkv_lm.RwkvLmEs(cfg, params)
+    rng = np.random.default_rng(8)
+    tok = torch.from_numpy(rng.integers(0, cfg.vocab, (cfg.n, cfg.seq_len + 1)).astype(np.int32)).cuda()
+    before = {ln: es.blocks[ln[0]][ln[1]].cpu().numpy().copy() for ln in es.keys}
+    vec_before = es.blocks[1]["x_r"].cpu().numpy().copy()
+    fit = es.step(tok, epoch=0)
+    torch.cuda.synchronize()
+    z, _, _ = O.convert_fitnesses(fit.cpu().numpy())
+    for (l, name), key in es.keys.items():
+        a, b = before[(l, name)].shape
+        g = O.lora_grad_f64(cfg.sigma, key, cfg.rank, 0, z, a, b)
+        g_gpu = es.grads[(l, name)].cpu().numpy()
+        assert np.abs(g_gpu - g).max() <= 1e-5 * np.abs(g).max(), (l, name)
+        p_ref = before[(l, name)] - g * np.float32(cfg.lr)
+        ulp = np.spacing(np.abs(p_ref).astype(np.float32))
+        tol = 2 * ulp + 1e-5 * np.abs(g).max() * cfg.lr
+        assert np.all(np.abs(es.blocks[l][name].cpu().numpy() - p_ref) <= tol), (l, name)
+    # full-rank vectors are frozen (freeze_nonlora)
+    np.testing.assert_array_equal(es.blocks[1]["x_r"].cpu().numpy(), vec_before)
+
+
+def test_embed_layer_norm_out_of_range_token_gives_nan(hses_gpu):
+    from hyperscalees_amd import _lib, kernels as K
+    C, V = 64, 10
+    emb = torch.randn(V, C, device="cuda")
+    w = torch.ones(C, device="cuda")
+    b = torch.zeros(C, device="cuda")
+    tok = torch.tensor([0, 9, 10, -1, 3], dtype=torch.int32, device="cuda")
+    y = torch.empty(5, C, device="cuda")
+    _lib.call("hses_embed_layer_norm", K._p(tok), 5, K._p(emb), V, C, K._p(w), K._p(b), 1e-5,
+              K._p(y), K._stream())
+    y = y.cpu().numpy()
+    assert np.isfinite(y[[0, 1, 4]]).all() and np.isnan(y[[2, 3]]).all()
+    ref = O.layer_norm(emb.cpu().numpy()[[0, 9, 3]], np.ones(C), np.zeros(C))
+    close(y[[0, 1, 4]], ref, 1e-5)

@@ -273,3 +273,97 @@ def test_time_mixing_length_and_new_starts():
     ref = ((prev * x).sum(-1))[:, None] * x        # (sum r k r_k) v with r = prev, k = v = x
     np.testing.assert_allclose(out, ref, rtol=1e-5, atol=1e-6)
     np.testing.assert_array_equal(st[0], x[2])
+
+
+# -- the RWKV-7 LM (rwkv7.py:189-253) ------------------------------------------
+
+def lm_params(rng, L, C, F, V, D=8, zero_out=False):
+    P = {"emb": rng.standard_normal((V, C)).astype(np.float32),
+         "head": (rng.standard_normal((V, C)) / np.sqrt(C)).astype(np.float32),
+         "ln0_w": (1 + 0.1 * rng.standard_normal(C)).astype(np.float32),
+         "ln0_b": (0.1 * rng.standard_normal(C)).astype(np.float32),
+         "ln_out_w": (1 + 0.1 * rng.standard_normal(C)).astype(np.float32),
+         "ln_out_b": (0.1 * rng.standard_normal(C)).astype(np.float32), "blocks": []}
+    for _ in range(L):
+        B = tm_zero(C, D)
+        for n in O.TM_VECTORS + ("w0", "v0", "a0", "k_a", "r_k", "ln_b"):
+            B[n] = (rng.random(C) * 0.5).astype(np.float32)
+        B["k_k"] = (1 + 0.1 * rng.standard_normal(C)).astype(np.float32)
+        B["ln_w"] = (1 + 0.1 * rng.standard_normal(C)).astype(np.float32)
+        for n in O.TM_LINEAR:
+            B[n] = (rng.standard_normal((C, C)) / np.sqrt(C)).astype(np.float32)
+        for n in ("w1", "v1", "a1", "g1"):
+            B[n] = (rng.standard_normal((C, D)) / np.sqrt(C)).astype(np.float32)
+        for n in ("w2", "v2", "a2", "g2"):
+            B[n] = (rng.standard_normal((D, C)) / np.sqrt(D)).astype(np.float32)
+        B["ffn_x_k"] = rng.random(C).astype(np.float32)
+        B["ffn_key"] = (rng.standard_normal((F, C)) / np.sqrt(C)).astype(np.float32)
+        B["ffn_value"] = (rng.standard_normal((C, F)) / np.sqrt(F)).astype(np.float32)
+        for n in ("ln1_w", "ln2_w"):
+            B[n] = (1 + 0.1 * rng.standard_normal(C)).astype(np.float32)
+        for n in ("ln1_b", "ln2_b"):
+            B[n] = (0.1 * rng.standard_normal(C)).astype(np.float32)
+        if zero_out:
+            B["output"][:] = 0
+            B["ffn_value"][:] = 0
+        P["blocks"].append(B)
+    return P
+
+
+def test_lm_with_silent_blocks_is_embedding_norm_head():
+    # output = ffn value = 0: every block adds 0, so logits = ln_out(ln0(emb[tok])) head^T,
+    # and each block's state rows 0 / 1 hold ln2 / ln1 of the last residual row.
+    L, C, F, V, H, T = 2, 16, 32, 11, 2, 6
+    rng = np.random.default_rng(6)
+    P = lm_params(rng, L, C, F, V, zero_out=True)
+    tok = rng.integers(0, V, T)
+    logits, st = O.rwkv_lm_forward(P, tok, H)
+    f = np.float64
+
+    def ln(x, w, b):
+        m = x.mean(-1, keepdims=True)
+        return (x - m) / np.sqrt(x.var(-1, keepdims=True) + 1e-5) * w + b
+    x = ln(P["emb"][tok].astype(f), P["ln0_w"], P["ln0_b"])
+    ref = ln(x, P["ln_out_w"], P["ln_out_b"]) @ P["head"].T.astype(f)
+    np.testing.assert_allclose(logits, ref, rtol=1e-4, atol=1e-4)
+    for l, B in enumerate(P["blocks"]):
+        np.testing.assert_allclose(st[l, 0], ln(x[-1], B["ln2_w"], B["ln2_b"]), rtol=1e-4, atol=1e-5)
+        np.testing.assert_allclose(st[l, 1], ln(x[-1], B["ln1_w"], B["ln1_b"]), rtol=1e-4, atol=1e-5)
+
+
+def test_lm_state_carry_equals_one_pass():
+    # the model is recurrent: running tokens [0, T1) and then [T1, T) from the carried
+    # state gives the one-pass logits and state, bit for bit (every op is per token
+    # or in token order).
+    L, C, F, V, H, T, T1 = 2, 16, 32, 13, 2, 9, 4
+    rng = np.random.default_rng(7)
+    P = lm_params(rng, L, C, F, V)
+    tok = rng.integers(0, V, T)
+    full, st_full = O.rwkv_lm_forward(P, tok, H)
+    a, st_a = O.rwkv_lm_forward(P, tok[:T1], H)
+    b, st_b = O.rwkv_lm_forward(P, tok[T1:], H, st_a)
+    np.testing.assert_array_equal(np.vstack([a, b]), full)
+    np.testing.assert_array_equal(st_b, st_full)
+
+
+def test_lm_one_block_wiring():
+    # one block from the pinned components: x0 = ln0(emb); x1 = x0 + att(ln1 x0);
+    # x2 = x1 + ffn(ln2 x1); logits = ln_out(x2) head^T; state rows [ffn last, att state]
+    L, C, F, V, H, T = 1, 16, 32, 7, 4, 5
+    rng = np.random.default_rng(8)
+    P = lm_params(rng, L, C, F, V)
+    tok = rng.integers(0, V, T)
+    st0 = (rng.standard_normal((1, 2 + C // H, C)) * 0.3).astype(np.float32)
+    logits, st = O.rwkv_lm_forward(P, tok, H, st0)
+    B = P["blocks"][0]
+    x0 = O.layer_norm(P["emb"][tok], P["ln0_w"], P["ln0_b"])
+    att, st_att, _ = O.time_mixing(B, O.layer_norm(x0, B["ln1_w"], B["ln1_b"]), st0[0, 1:],
+                                   np.zeros((T, C)), H, T, 0)
+    x1 = x0 + att
+    h2 = O.layer_norm(x1, B["ln2_w"], B["ln2_b"])
+    ffn, last = O.channel_mixing(h2, st0[0, 0], B["ffn_x_k"], B["ffn_key"], B["ffn_value"], T)
+    x2 = x1 + ffn
+    ref = O.layer_norm(x2, P["ln_out_w"], P["ln_out_b"]) @ P["head"].T
+    np.testing.assert_allclose(logits, ref, rtol=1e-5, atol=1e-5)
+    np.testing.assert_array_equal(st[0, 0], last)
+    np.testing.assert_array_equal(st[0, 1:], st_att)
