@@ -21,8 +21,9 @@
 //     of 7).  Rank chunks are double-buffered in LDS (one barrier per chunk)
 //     and the generation of the next chunk is interleaved with the MFMAs of
 //     the current one.
-//   k_es_partial (r < 32): 128x128 tiles, 256 threads; several short stream
-//     rows per thread.
+//   k_es_partial (r < 32): 128x128 tiles, 256 threads; a k-chunk of 32 columns
+//     holds 32 / r pairs (the pair weight folded into A at generation), so
+//     every thread generates a run of stream rows of one pair per chunk.
 // Stage 2 (k_es_reduce): each output element sums its partials in double in
 // a fixed order (four split ranges, each in four interleaved sums), scales,
 // and stores (or adds).  The split count depends on the problem shape only,
@@ -78,17 +79,13 @@ __global__ __launch_bounds__(U_THREADS) void k_es_partial(UpdParams P) {
     __syncthreads();
     const NoiseCtx ctx{&tabs, P.log_exc, P.cos_exc};
 
-    // Generation items: RC consecutive stream rows each; A rows first.
+    // A chunk holds pc = 32 / r pairs (its k-columns: pair-major, then rank
+    // column); each generation item is rc consecutive stream rows (rows of one
+    // factor) of one pair, A rows first.
     const int32_t r = P.r, rc = P.rc;
+    const int32_t pc = U_CW / r;
     const int32_t itemsA = (at + rc - 1) / rc, itemsB = (bt + rc - 1) / rc;
-    const bool has_item = tid < itemsA + itemsB;
-    const bool is_a = tid < itemsA;
-    const int32_t first = is_a ? tid * rc : (tid - itemsA) * rc;       // local row
-    const int32_t nrows = has_item ? min(rc, (is_a ? at : bt) - first) : 0;
-    const int32_t srow = is_a ? P.b + o0 + first : q0 + first;          // stream row
-    float* dst = is_a ? As : Bs;
-    const int32_t cw = min(r, U_CW);
-    const int32_t chunks = (r + U_CW - 1) / U_CW;
+    const int32_t per_pair = itemsA + itemsB;
 
     f32x4 acc[4][4];
 #pragma unroll
@@ -98,47 +95,53 @@ __global__ __launch_bounds__(U_THREADS) void k_es_partial(UpdParams P) {
     const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;  // wave quadrant
     const int kg = lane >> 4, li = lane & 15;
 
-    for (int32_t p = p_begin; p < p_end; ++p) {
-        // Pair weight from the members of pair p inside [tid_lo, tid_lo+n).
-        const int32_t me = 2 * p - P.tid_lo, mo = me + 1;
-        const float fe = (me >= 0 && me < P.n) ? P.f[me] : 0.0f;
-        const float fo = (mo >= 0 && mo < P.n) ? P.f[mo] : 0.0f;
-        const float w = fe - fo;
-        uint64_t st = 0;
-        if (has_item) {
+    for (int32_t p0 = p_begin; p0 < p_end; p0 += pc) {
+        const int32_t np = min(pc, p_end - p0);
+        const int32_t kc = np * r;  // k-columns of this chunk
+        for (int32_t item = tid; item < np * per_pair; item += U_THREADS) {
+            const int32_t pl = item / per_pair, it = item - pl * per_pair;
+            const int32_t p = p0 + pl;
+            const bool is_a = it < itemsA;
+            const int32_t first = (is_a ? it : it - itemsA) * rc;  // local row
+            const int32_t nrows = min(rc, (is_a ? at : bt) - first);
+            const int32_t srow = is_a ? P.b + o0 + first : q0 + first;  // stream row
+            float* dst = is_a ? As : Bs;
+            // Pair weight from the members of pair p inside [tid_lo, tid_lo+n).
+            const int32_t me = 2 * p - P.tid_lo, mo = me + 1;
+            const float fe = (me >= 0 && me < P.n) ? P.f[me] : 0.0f;
+            const float fo = (mo >= 0 && mo < P.n) ? P.f[mo] : 0.0f;
+            const float w = fe - fo;
             int32_t te, tt;
             float sg;
             epoch_thread_sign(P.epoch, 2 * p, P.nreuse, &te, &tt, &sg);
-            st = row_start_state(noise_seed(P.key, te, tt), srow, P.jump);
-        }
-        for (int32_t ch = 0; ch < chunks; ++ch) {
-            const int32_t c0 = ch * U_CW;
-            const int32_t cn = min(cw, r - c0);
-            // rc > 1 only when r <= 16 (one chunk): the item's rows are contiguous
-            // in the stream, so one run of nrows * r normals covers them.
+            uint64_t st = row_start_state(noise_seed(P.key, te, tt), srow, P.jump);
             const float scl = is_a ? P.bs : 1.0f;
-            bm_run(st, nrows * cn, ctx, [&](int32_t i, float v) {
-                const int32_t row = first + i / cn, c = i % cn;
-                dst[row * U_PITCH + c] = is_a ? v * scl : v;
+            // the item's rows are contiguous in the stream: one run of nrows * r normals
+            bm_run(st, nrows * r, ctx, [&](int32_t i, float v) {
+                const int32_t row = first + i / r, c = i % r;
+                dst[row * U_PITCH + pl * r + c] = is_a ? (v * scl) * w : v;
             });
-            // The last k-step reads whole groups of 4 columns: clear the tail.
-            for (int32_t i = 0; i < nrows; ++i)
-                for (int32_t c = cn; c < ((cn + 3) & ~3); ++c) dst[(first + i) * U_PITCH + c] = 0.0f;
-            __syncthreads();
-            // acc += (w * Ahat[:, c]) B[:, c]^T over this chunk (k-steps of 4).
-            for (int32_t ks = 0; ks < cn; ks += 4) {
-                float af[4], bf[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) af[i] = w * As[(wm + i * 16 + li) * U_PITCH + ks + kg];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) bf[j] = Bs[(wn + j * 16 + li) * U_PITCH + ks + kg];
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) acc[i][j] = mfma_f32(af[i], bf[j], acc[i][j]);
-            }
-            __syncthreads();
         }
+        // The last k-step reads whole groups of 4 columns: clear the tail.
+        const int32_t kc4 = (kc + 3) & ~3;
+        for (int32_t i = tid; i < (U_TA + U_TB) * (kc4 - kc); i += U_THREADS) {
+            const int32_t row = i / (kc4 - kc), c = kc + i % (kc4 - kc);
+            (row < U_TA ? As : Bs)[(row < U_TA ? row : row - U_TA) * U_PITCH + c] = 0.0f;
+        }
+        __syncthreads();
+        // acc += (w Ahat[:, k]) B[:, k]^T over this chunk (k-steps of 4).
+        for (int32_t ks = 0; ks < kc; ks += 4) {
+            float af[4], bf[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) af[i] = As[(wm + i * 16 + li) * U_PITCH + ks + kg];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) bf[j] = Bs[(wn + j * 16 + li) * U_PITCH + ks + kg];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = mfma_f32(af[i], bf[j], acc[i][j]);
+        }
+        __syncthreads();
     }
 
     // Partial tile -> workspace [s][a][b].
@@ -421,11 +424,12 @@ __global__ __launch_bounds__(256) void k_es_reduce(const float* __restrict__ wor
     }
 }
 
-// Split count: ~1024 workgroups in total, at least 8 pairs per split, at most 512 splits.
-static int32_t es_splits(int32_t a, int32_t b, int32_t n_pairs) {
+// Split count: ~1024 workgroups in total, at least max(8, 32 / r) pairs (one
+// k-chunk) per split, at most 512 splits.
+static int32_t es_splits(int32_t a, int32_t b, int32_t n_pairs, int32_t rank) {
     const int64_t tiles = (int64_t)((a + U_TA - 1) / U_TA) * ((b + U_TB - 1) / U_TB);
     int64_t s = std::max<int64_t>(1, 1024 / std::max<int64_t>(tiles, 1));
-    s = std::min<int64_t>(s, std::max<int32_t>(1, n_pairs / 8));
+    s = std::min<int64_t>(s, std::max<int32_t>(1, n_pairs / std::max(8, U_CW / rank)));
     s = std::min<int64_t>(s, 512);
     return (int32_t)std::max<int64_t>(s, 1);
 }
@@ -482,7 +486,7 @@ extern "C" size_t hses_es_update_workspace(int32_t a, int32_t b, int32_t rank, i
     int32_t lo, cnt;
     pair_range(0, n, &lo, &cnt);
     // tid_lo parity can add one pair; size for the larger count.
-    const int32_t splits = use_rows_kernel(rank) ? rows_splits(a, b, cnt + 1) : es_splits(a, b, cnt + 1);
+    const int32_t splits = use_rows_kernel(rank) ? rows_splits(a, b, cnt + 1) : es_splits(a, b, cnt + 1, rank);
     return align_up16((size_t)splits * a * b * sizeof(float)) + 16;  // partials, then {S, 1/S}
 }
 
@@ -499,7 +503,7 @@ extern "C" int hses_es_update(const float* d_f, int32_t n, int32_t tid_lo, uint6
     pair_range(tid_lo, n, &pair_lo, &n_pairs);
     const bool empty = n == 0 || rank == 0 || sigma == 0.0f;
     const bool rows_k = use_rows_kernel(rank);
-    P.splits = empty ? 1 : rows_k ? rows_splits(a, b, n_pairs) : es_splits(a, b, n_pairs);
+    P.splits = empty ? 1 : rows_k ? rows_splits(a, b, n_pairs) : es_splits(a, b, n_pairs, rank);
     const size_t part_bytes = align_up16((size_t)P.splits * a * b * sizeof(float));
     const size_t need = part_bytes + 16;
     if (!empty) {
@@ -527,10 +531,6 @@ extern "C" int hses_es_update(const float* d_f, int32_t n, int32_t tid_lo, uint6
     P.pair_lo = pair_lo;
     P.n_pairs = n_pairs;
     P.rc = rank >= U_CW ? 1 : std::max(1, U_CW / rank);
-    // Items must cover a tile's rows with the block's threads.
-    const int32_t items = (U_TA + P.rc - 1) / P.rc + (U_TB + P.rc - 1) / P.rc;
-    if (items > U_THREADS || (P.rc > 1 && rank > U_CW))
-        return set_error(HSES_ERR_INTERNAL, "es_update tiling");
     P.work = static_cast<float*>(d_work);
     float* d_scale = reinterpret_cast<float*>(static_cast<char*>(d_work) + part_bytes);
     P.scale = d_scale;

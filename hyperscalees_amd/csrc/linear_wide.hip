@@ -4,19 +4,21 @@
 //   do_Tmm (eggroll.rs:450-477):  y = x W + (x A_m) B_m^T,
 // with an optional elementwise activation fused into the epilogue.
 //
-// A workgroup of 4 waves owns a 128-row x 128-column output tile (rows are
-// member-major, a tile touches at most a few members; the members' noise
-// columns, nm * r <= 16, ride along as one extra 16-wide operand):
+// A workgroup of 8 waves owns a 128-row tile of the output and sweeps its
+// 256-column tiles (rows are member-major, a row tile touches at most a few
+// members; their noise columns, nm * r <= 16, ride along as one extra
+// 16-wide operand):
 //   1. W is converted once per call to bf16 (a, kp) in the workspace; the
-//      tile's members' input-side factors (K x r each) and output-side factor
-//      rows (128 x r) are generated from the noiser stream into LDS;
-//   2. K loop in steps of 64: x (fp32, bf16 or bit-packed) and W tiles are prefetched into
-//      registers one step ahead, stored to LDS as bf16, and each wave
+//      row tile's members' input-side factors (K x r each) and output-side
+//      factors (a x r each) are generated once from the noiser stream into LDS;
+//   2. one pipeline over (column tile, K step of 64): x (fp32, bf16 or
+//      bit-packed) and W tiles are prefetched into registers one step ahead,
+//      also across column tiles, stored to LDS as bf16, and each wave
 //      accumulates its 64 x 64 sub-tile with 32x32x16 MFMAs (fp32
-//      accumulation) plus a 32-row slice of x B_m with 16x16x32 MFMAs;
-//   3. epilogue: y = acc + (x B_m) A_m^T (r multiply-adds), activation, store.
-// Tiles are ordered so that the column tiles of one row tile run on one XCD
-// (workgroup i goes to XCD i mod 8), where they share its L2 copy of x.
+//      accumulation); during the first column tile each wave also forms a
+//      16-row slice of x B_m with 16x16x32 MFMAs;
+//   3. after a column tile's last K step: y = acc + (x B_m) A_m^T (r
+//      multiply-adds), activation, store, and the accumulators restart.
 #include <math.h>
 
 #include "linear_common.h"
@@ -27,7 +29,7 @@
 
 namespace hses {
 
-constexpr int KW_BM = 128, KW_BN = 128, KW_BK = 64, KW_THREADS = 256;
+constexpr int KW_BM = 128, KW_BN = 256, KW_BK = 64, KW_THREADS = 512;
 constexpr int KW_XP = KW_BK + 8;  // LDS pitch of the x and W tiles (bf16 elements, 144 B)
 constexpr int KW_NE = 16;         // noise columns (members x rank) per tile
 
@@ -39,8 +41,8 @@ __device__ __forceinline__ f32x16w mfma32w(const u16x8& a, const u16x8& b, f32x1
 }
 
 struct KWLayout {
-    size_t off_x, off_w, off_b, off_a, bytes;
-    __host__ __device__ KWLayout(int ne_real, int bpitch, int nm_max, int r, bool noisy) {
+    size_t off_x, off_w, off_b, off_a, off_xb, bytes;
+    __host__ __device__ KWLayout(int ne_real, int bpitch, int nm_max, int r, int a, bool noisy) {
         size_t o = noisy ? align16(sizeof(BmTables)) : 0;
         off_x = o;
         o = align16(o + (size_t)KW_BM * KW_XP * 2);
@@ -49,7 +51,9 @@ struct KWLayout {
         off_b = o;
         o = align16(o + (size_t)ne_real * bpitch * 2);
         off_a = o;
-        o = align16(o + (size_t)nm_max * KW_BN * r * 4);
+        o = align16(o + (noisy ? (size_t)nm_max * a * r * 4 : 0));
+        off_xb = o;
+        o = align16(o + (noisy ? (size_t)KW_BM * KW_NE * 4 : 0));
         bytes = o;
     }
 };
@@ -67,52 +71,47 @@ __device__ __forceinline__ float act_apply(float v) {
 
 template <int XFMT, int ACT>
 __global__ __launch_bounds__(KW_THREADS) void k_linear_wide(LinParams P, const uint16_t* __restrict__ Wb,
-                                                            int32_t kp, int32_t col_tiles,
-                                                            int32_t ntiles, int32_t per_xcd) {
+                                                            int32_t kp, int32_t col_tiles) {
     extern __shared__ __align__(16) unsigned char smem[];
     const bool noisy = P.ne_real > 0;
-    const KWLayout lay(P.ne_real, P.bpitch, P.nm_max, P.r, noisy);
+    const KWLayout lay(P.ne_real, P.bpitch, P.nm_max, P.r, P.a, noisy);
     BmTables* tabs = reinterpret_cast<BmTables*>(smem);
     uint16_t* Xs = reinterpret_cast<uint16_t*>(smem + lay.off_x);
     uint16_t* Ws = reinterpret_cast<uint16_t*>(smem + lay.off_w);
     uint16_t* Bs = reinterpret_cast<uint16_t*>(smem + lay.off_b);
     float* As = reinterpret_cast<float*>(smem + lay.off_a);
-    float* XB = reinterpret_cast<float*>(smem + lay.off_x);  // reuses the x tile after the K loop
+    float* XB = reinterpret_cast<float*>(smem + lay.off_xb);
 
-    const int32_t bid = blockIdx.x;
-    const int32_t t = (bid & 7) * per_xcd + (bid >> 3);
-    if (t >= ntiles) return;  // whole workgroup, before any barrier
-    const int64_t L0 = (int64_t)(t / col_tiles) * KW_BM;
-    const int32_t o0 = (t % col_tiles) * KW_BN;
-    const int32_t ct = min(KW_BN, P.a - o0);
+    const int64_t L0 = (int64_t)blockIdx.x * KW_BM;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int wr = wave >> 1, wc = wave & 1, lc = lane & 31, hl = lane >> 5;
-    const int32_t b = P.b, R = P.R;
+    const int wr = wave >> 2, wc = wave & 3, lc = lane & 31, hl = lane >> 5;
+    const int32_t b = P.b, R = P.R, a = P.a;
     const int32_t nkt = (b + KW_BK - 1) / KW_BK;
     const bool flat = P.n_time == 1;  // physical row = logical row
     const int32_t m_first = (int32_t)(L0 / R);
     const int32_t m_last = (int32_t)((min(L0 + KW_BM, P.total) - 1) / R);
 
     // ---- staging: x rows and W columns this thread loads ----------------------
-    // F32: 8 rows (step 16) x 4 k; BF16: 4 rows (step 32) x 8 k; BITS: one row,
-    // 32 k (half of the row's 64-bit word of this K step).
+    // F32: 4 rows (step 32) x 4 k; BF16: 2 rows (step 64) x 8 k; BITS (threads
+    // below 256): one row, 32 k (half of the row's 64-bit word of this K step).
     constexpr bool BITS = XFMT == HSES_FMT_BITS;
-    constexpr int XR = XFMT == HSES_FMT_F32 ? 8 : (BITS ? 1 : 4);
-    constexpr int XSTEP = XFMT == HSES_FMT_F32 ? 16 : 32;
+    constexpr int XR = XFMT == HSES_FMT_F32 ? 4 : (BITS ? 1 : 2);
+    constexpr int XSTEP = XFMT == HSES_FMT_F32 ? 32 : 64;
     const int xseg = XFMT == HSES_FMT_F32 ? (tid & 15) * 4 : (BITS ? (tid & 1) * 32 : (tid & 7) * 8);
-    const int xrow0 = XFMT == HSES_FMT_F32 ? tid >> 4 : (BITS ? tid >> 1 : tid >> 3);
+    const int xrow0 = XFMT == HSES_FMT_F32 ? tid >> 4 : (BITS ? (tid & 255) >> 1 : tid >> 3);
+    const bool xload = !BITS || tid < 2 * KW_BM;
     int64_t xoff[XR];
 #pragma unroll
     for (int i = 0; i < XR; ++i) {
         const int64_t Lr = L0 + xrow0 + XSTEP * i;
-        xoff[i] = Lr < P.total ? (flat ? Lr * P.x_stride : phys_row(P, Lr, P.x_stride, P.x_plane)) : -1;
+        xoff[i] = (xload && Lr < P.total) ? (flat ? Lr * P.x_stride : phys_row(P, Lr, P.x_stride, P.x_plane)) : -1;
     }
-    const int wseg = (tid & 7) * 8, wcol0 = tid >> 3;  // W: 4 columns (step 32) x 8 k
-    uint4 xr_[XFMT == HSES_FMT_F32 ? 8 : 4];
+    const int wseg = (tid & 7) * 8, wcol0 = tid >> 3;  // W: 4 columns (step 64) x 8 k
+    uint4 xr_[XR];
     uint32_t xbits = 0;
     uint4 wr_[4];
 
-    auto load_tiles = [&](int32_t kt) {
+    auto load_tiles = [&](int32_t ct_i, int32_t kt) {
         const int32_t k = kt * KW_BK + xseg;
         if constexpr (BITS) {
             // bits past column b are masked off (the ABI does not require them zero)
@@ -124,58 +123,59 @@ __global__ __launch_bounds__(KW_THREADS) void k_linear_wide(LinParams P, const u
         } else if constexpr (XFMT == HSES_FMT_F32) {
             const float* xp = static_cast<const float*>(P.x);
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
+            for (int i = 0; i < XR; ++i)
                 xr_[i] = (xoff[i] >= 0 && k < b) ? *reinterpret_cast<const uint4*>(xp + xoff[i] + k)
                                                  : uint4{0, 0, 0, 0};
         } else {
             const uint16_t* xp = static_cast<const uint16_t*>(P.x);
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < XR; ++i)
                 xr_[i] = (xoff[i] >= 0 && k < b) ? *reinterpret_cast<const uint4*>(xp + xoff[i] + k)
                                                  : uint4{0, 0, 0, 0};
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int32_t col = o0 + wcol0 + 32 * i;
-            wr_[i] = col < P.a ? *reinterpret_cast<const uint4*>(Wb + (int64_t)col * kp + kt * KW_BK + wseg)
-                               : uint4{0, 0, 0, 0};
+            const int32_t col = ct_i * KW_BN + wcol0 + 64 * i;
+            wr_[i] = col < a ? *reinterpret_cast<const uint4*>(Wb + (int64_t)col * kp + kt * KW_BK + wseg)
+                             : uint4{0, 0, 0, 0};
         }
     };
     auto store_tiles = [&]() {
         if constexpr (BITS) {
+            if (xload) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-                *reinterpret_cast<u16x8*>(Xs + xrow0 * KW_XP + xseg + 8 * q) =
-                    expand_bits((xbits >> (8 * q)) & 0xffu);
+                for (int q = 0; q < 4; ++q)
+                    *reinterpret_cast<u16x8*>(Xs + xrow0 * KW_XP + xseg + 8 * q) =
+                        expand_bits((xbits >> (8 * q)) & 0xffu);
+            }
         } else if constexpr (XFMT == HSES_FMT_F32) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
+            for (int i = 0; i < XR; ++i) {
                 const uint2 v{pack_bf16x2(__uint_as_float(xr_[i].x), __uint_as_float(xr_[i].y)),
                               pack_bf16x2(__uint_as_float(xr_[i].z), __uint_as_float(xr_[i].w))};
-                *reinterpret_cast<uint2*>(Xs + (xrow0 + 16 * i) * KW_XP + xseg) = v;
+                *reinterpret_cast<uint2*>(Xs + (xrow0 + XSTEP * i) * KW_XP + xseg) = v;
             }
         } else {
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                *reinterpret_cast<uint4*>(Xs + (xrow0 + 32 * i) * KW_XP + xseg) = xr_[i];
+            for (int i = 0; i < XR; ++i)
+                *reinterpret_cast<uint4*>(Xs + (xrow0 + XSTEP * i) * KW_XP + xseg) = xr_[i];
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            *reinterpret_cast<uint4*>(Ws + (wcol0 + 32 * i) * KW_XP + wseg) = wr_[i];
+            *reinterpret_cast<uint4*>(Ws + (wcol0 + 64 * i) * KW_XP + wseg) = wr_[i];
     };
 
-    // ---- 1. factors of the tile's members into LDS ---------------------------
+    // ---- 1. factors of the row tile's members into LDS -------------------------
     if (noisy) {
         load_bm_tables(tabs, P.tables);
         for (int i = tid; i < P.ne_real * P.bpitch; i += KW_THREADS) Bs[i] = 0;
         __syncthreads();
         const NoiseCtx ctx{tabs, P.log_exc, P.cos_exc};
-        gen_tile_factors<HSES_MATH_BF16>(P, ctx, m_first, m_last - m_first + 1, o0, ct, Bs,
-                                         P.bpitch, As, KW_BN);
+        gen_tile_factors<HSES_MATH_BF16>(P, ctx, m_first, m_last - m_first + 1, 0, a, Bs,
+                                         P.bpitch, As, a);
     }
 
-    // ---- 2. K loop -------------------------------------------------------------
-    load_tiles(0);  // after the generation, whose registers it would otherwise share
+    // ---- 2. one pipeline over (column tile, K step) -----------------------------
     f32x16w acc[2][2];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -183,15 +183,22 @@ __global__ __launch_bounds__(KW_THREADS) void k_linear_wide(LinParams P, const u
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
-    f32x4 accx[2] = {f32x4{0, 0, 0, 0}, f32x4{0, 0, 0, 0}};
-    const int xb_row = wr * 64 + wc * 32 + (lane & 15);  // x B rows of this wave: +0, +16
+    f32x4 accx = f32x4{0, 0, 0, 0};
+    const int xb_row = wave * 16 + (lane & 15);  // the 16 x B rows of this wave
     const int xb_e = lane & 15, xb_kg = lane >> 4;
     const bool xb_on = noisy && xb_e < P.ne_real;
+    const int32_t r = P.r;
 
-    for (int32_t kt = 0; kt < nkt; ++kt) {
+    load_tiles(0, 0);  // after the generation, whose registers it would otherwise share
+    int32_t ct_i = 0, kt = 0;
+    const int32_t nsteps = col_tiles * nkt;
+    for (int32_t step = 0; step < nsteps; ++step) {
         store_tiles();
         __syncthreads();
-        if (kt + 1 < nkt) load_tiles(kt + 1);
+        if (step + 1 < nsteps) {
+            const bool same = kt + 1 < nkt;
+            load_tiles(same ? ct_i : ct_i + 1, same ? kt + 1 : 0);
+        }
 #pragma unroll
         for (int ks = 0; ks < KW_BK / 16; ++ks) {
             const int kk = ks * 16 + hl * 8;
@@ -204,57 +211,70 @@ __global__ __launch_bounds__(KW_THREADS) void k_linear_wide(LinParams P, const u
             acc[1][0] = mfma32w(a1, b0, acc[1][0]);
             acc[1][1] = mfma32w(a1, b1, acc[1][1]);
         }
-        if (noisy) {
+        if (noisy && ct_i == 0) {
 #pragma unroll
             for (int k32 = 0; k32 < KW_BK / 32; ++k32) {
                 const int kk = k32 * 32 + xb_kg * 8;
                 const u16x8 bx = xb_on ? lds_u16x8(Bs + xb_e * P.bpitch + kt * KW_BK + kk)
                                        : u16x8{0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll
-                for (int s = 0; s < 2; ++s)
-                    accx[s] = mfma_bf16(lds_u16x8(Xs + (xb_row + 16 * s) * KW_XP + kk), bx, accx[s]);
+                accx = mfma_bf16(lds_u16x8(Xs + xb_row * KW_XP + kk), bx, accx);
             }
         }
         __syncthreads();
-    }
+        if (kt + 1 < nkt) {
+            ++kt;
+            continue;
+        }
 
-    // ---- 3. epilogue -------------------------------------------------------------
-    if (noisy) {
-        // 16x16 layout: lane l holds D[4 (l / 16) + v][l % 16]
+        // ---- 3. epilogue of column tile ct_i ---------------------------------------
+        if (noisy && ct_i == 0) {
+            // 16x16 layout: lane l holds D[4 (l / 16) + v][l % 16]
 #pragma unroll
-        for (int s = 0; s < 2; ++s)
-#pragma unroll
-            for (int v = 0; v < 4; ++v)
-                XB[(wr * 64 + wc * 32 + 16 * s + 4 * xb_kg + v) * KW_NE + xb_e] = accx[s][v];
-        __syncthreads();
-    }
-    const int32_t r = P.r;
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            // 32x32 layout: lane l holds D[8 (e / 4) + 4 (l / 32) + e % 4][l % 32]
-            const int row = wr * 64 + 32 * i + 8 * (e >> 2) + 4 * hl + (e & 3);
-            const int64_t Lr = L0 + row;
-            if (Lr >= P.total) continue;
-            int32_t lm = 0;
-            if (noisy && P.nm_max > 1) lm = (int32_t)((Lr - (int64_t)m_first * R) / R);
-            float* yrow = P.y + (flat ? Lr * P.y_stride : phys_row(P, Lr, P.y_stride, P.y_plane)) + o0;
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int col = wc * 64 + 32 * j + lc;
-                if (col >= ct) continue;
-                float v = acc[i][j][e];
-                if (noisy) {
-                    const float* xb = XB + row * KW_NE + lm * r;
-                    const float* ar = As + ((size_t)lm * KW_BN + col) * r;
-                    float z = 0.0f;
-                    for (int32_t c = 0; c < r; ++c) z = __fadd_rn(z, __fmul_rn(xb[c], ar[c]));
-                    v = __fadd_rn(v, z);
-                }
-                yrow[col] = act_apply<ACT>(v);
-            }
+            for (int v = 0; v < 4; ++v) XB[(wave * 16 + 4 * xb_kg + v) * KW_NE + xb_e] = accx[v];
+            __syncthreads();
         }
+        const int32_t o0 = ct_i * KW_BN;
+        const int32_t ct = min(KW_BN, a - o0);
+        // The row addresses below are the same for every column tile; computing
+        // them here (the empty asm hides that) keeps the compiler from holding
+        // all 32 of them in registers across the whole pipeline.
+        int32_t rbase = wr * 64 + 4 * hl;
+        asm volatile("" : "+v"(rbase));
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                // 32x32 layout: lane l holds D[8 (e / 4) + 4 (l / 32) + e % 4][l % 32]
+                const int row = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
+                const int64_t Lr = L0 + row;
+                if (Lr >= P.total) continue;
+                int32_t lm = 0;
+                if (noisy && P.nm_max > 1) lm = (int32_t)((Lr - (int64_t)m_first * R) / R);
+                float* yrow = P.y + (flat ? Lr * P.y_stride : phys_row(P, Lr, P.y_stride, P.y_plane)) + o0;
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int col = wc * 64 + 32 * j + lc;
+                    if (col >= ct) continue;
+                    float v = acc[i][j][e];
+                    if (noisy) {
+                        const float* xb = XB + row * KW_NE + lm * r;
+                        const float* ar = As + ((size_t)lm * a + o0 + col) * r;
+                        float z = 0.0f;
+                        for (int32_t c = 0; c < r; ++c) z = __fadd_rn(z, __fmul_rn(xb[c], ar[c]));
+                        v = __fadd_rn(v, z);
+                    }
+                    yrow[col] = act_apply<ACT>(v);
+                }
+            }
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+        ++ct_i;
+        kt = 0;
+    }
 }
 
 static int32_t wide_nm_max(int32_t R, int32_t n) {
@@ -301,8 +321,8 @@ int launch_linear_wide(LinParams& P, DeviceState* st, hipStream_t s, void* work,
     P.ne = KW_NE;
     P.bpitch = kp + 8;
     // about one jump and a few normals per thread: groups of rc stream rows
-    P.rc = noisy ? std::max(1, std::min(32 / P.r, (P.b + std::min(P.a, KW_BN)) / KW_THREADS)) : 1;
-    const KWLayout lay(P.ne_real, P.bpitch, nm_max, P.r, noisy);
+    P.rc = noisy ? std::max(1, std::min(32 / P.r, (P.b + P.a) / KW_THREADS)) : 1;
+    const KWLayout lay(P.ne_real, P.bpitch, nm_max, P.r, P.a, noisy);
     if (lay.bytes > st->max_lds) return HSES_ERR_UNSUPPORTED;
     if (noisy) {
         const int64_t chunks = (P.a + P.b + P.rc - 1) / P.rc;
@@ -314,16 +334,14 @@ int launch_linear_wide(LinParams& P, DeviceState* st, hipStream_t s, void* work,
     HSES_CHECK_HIP(hipGetLastError());
     const int64_t row_tiles = (P.total + KW_BM - 1) / KW_BM;
     const int32_t col_tiles = (P.a + KW_BN - 1) / KW_BN;
-    const int64_t ntiles = row_tiles * col_tiles;
-    if (ntiles > INT32_MAX / 2) return set_error(HSES_ERR_INVALID_ARG, "too many output tiles");
-    const int32_t per_xcd = (int32_t)((ntiles + 7) / 8);
+    if (row_tiles > INT32_MAX / 2) return set_error(HSES_ERR_INVALID_ARG, "too many output rows");
     auto launch = [&](auto kern) -> int {
         if (lay.bytes > 64 * 1024)
             HSES_CHECK_HIP(hipFuncSetAttribute((const void*)kern,
                                                hipFuncAttributeMaxDynamicSharedMemorySize,
                                                (int)lay.bytes));
-        hipLaunchKernelGGL(kern, dim3((uint32_t)(8 * per_xcd)), dim3(KW_THREADS), lay.bytes, s, P,
-                           (const uint16_t*)wb, kp, col_tiles, (int32_t)ntiles, per_xcd);
+        hipLaunchKernelGGL(kern, dim3((uint32_t)row_tiles), dim3(KW_THREADS), lay.bytes, s, P,
+                           (const uint16_t*)wb, kp, col_tiles);
         HSES_CHECK_HIP(hipGetLastError());
         return HSES_OK;
     };
