@@ -7,6 +7,11 @@ log-likelihood fitness -> z-score -> ES gradient of the 4 layers -> AdamW.
 `value` = N / (time per step): member evaluations per second including the
 update.  Inputs are synthetic and resident in HBM before timing starts.
 
+With --workload c5 it measures the RWKV-7 LM configuration instead:
+one step = one ES step of N=2048 members at r=1, each scoring the next-token
+log-likelihood of its own 128-token sequence (bf16 MFMA linears), then the
+z-score and the ES update of every matrix.
+
 Prints one JSON line.  --gpus N > 1 is refused: this build runs on one GPU.
 """
 import argparse
@@ -84,6 +89,99 @@ def cpu_baseline(cfg, pool, labels, idx, W, members, threads):
             "seconds": round(t2 - t0, 2)}
 
 
+def bench_c5(args):
+    """The C5 workload: RWKV-7 LM (4 layers, d=512, vocab 256), N=2048, r=1."""
+    import torch
+    from hyperscalees_amd import kernels as K
+    from hyperscalees_amd import rwkv, rwkv_lm
+    from hyperscalees_amd._lib import ACT_RELU_SQ
+
+    n = args.population if args.population != 8192 else 2048
+    cfg = rwkv_lm.RwkvLmConfig(n=n)
+    params = rwkv_lm.init_params(cfg, seed=0)
+    K.init(0)
+    es = rwkv_lm.RwkvLmEs(cfg, params)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0)
+    tok = torch.randint(0, cfg.vocab, (cfg.n, cfg.seq_len + 1), dtype=torch.int32, device="cuda",
+                        generator=g)
+    for i in range(args.warmup):
+        es.step(tok, epoch=i)
+    torch.cuda.synchronize()
+    ev = lambda: torch.cuda.Event(enable_timing=True)
+    marks = []
+    t0 = time.perf_counter()
+    for s_ in range(args.steps):
+        e = [ev() for _ in range(3)]
+        e[0].record()
+        fit = es.forward(tok, epoch=s_)
+        e[1].record()
+        es.update(fit, s_)
+        e[2].record()
+        marks.append(e)
+    torch.cuda.synchronize()
+    ms_per_step = (time.perf_counter() - t0) * 1000.0 / args.steps
+    t_fwd = float(np.mean([e[0].elapsed_time(e[1]) for e in marks]))
+    t_upd = float(np.mean([e[1].elapsed_time(e[2]) for e in marks]))
+
+    # Dominant single launch: ChannelMixing key of layer 0 (x (N*T, 512) -> relu^2 (N*T, 2048)),
+    # timed alone with events on the launch stream.
+    B0 = es.blocks[0]
+    C, F, T = cfg.d_model, cfg.ffn_mult * cfg.d_model, cfg.seq_len
+    x = torch.randn((cfg.n, T, C), device="cuda", generator=g)
+    ek = es._es(0, 0, 0, cfg.n)["ffn_key"]
+    lk = []
+    for _ in range(3):
+        e0, e1 = ev(), ev()
+        e0.record()
+        rwkv.linear(x, B0["ffn_key"], ek, cfg.math, act=ACT_RELU_SQ)
+        e1.record()
+        torch.cuda.synchronize()
+        lk.append(e0.elapsed_time(e1))
+    lk_ms = float(np.median(lk))
+    rows = cfg.n * T
+    lk_flops = 2 * rows * C * F + 2 * rows * cfg.rank * (C + F)
+    achieved = lk_flops / (lk_ms * 1e-3) / 1e12
+    out = {
+        "metric": "perturbed member-evals/sec, RWKV-7 LM N=2048 r=1 (configs[4])",
+        "value": round(cfg.n / (ms_per_step * 1e-3), 1),
+        "unit": "member-evals/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16 MFMA linears (fp32 accumulate), fp32 activations and recurrence",
+        "data": "synthetic",
+        "config": {"workload": ("C5: RWKV-7 LM, 4 layers, d=512, head 64, vocab 256, 128-token "
+                                "uniform random sequences, N=2048 members x 1 sequence, r=1, "
+                                "init N(0, 0.02), fitness = mean next-token log-likelihood, full "
+                                "ES step (forward + fitness + z-score + ES update + SGD)"),
+                   "population": cfg.n, "rank": cfg.rank, "seq_len": T,
+                   "parallelism": "single GPU"},
+        "phase_ms": {"forward": round(t_fwd, 3), "es_update": round(t_upd, 3)},
+        "fwd_tflops": round(rwkv_lm.forward_flops(cfg) / (t_fwd * 1e-3) / 1e12, 1),
+        "roofline": {"kernel": "k_linear_wide<F32, RELU_SQ> (ChannelMixing key, 262144 x 512 -> 2048)",
+                     "bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": None, "launch_ms": round(lk_ms, 3),
+                     "algorithmic_flop_per_launch": lk_flops},
+    }
+    if not args.no_cpu_baseline:
+        from tests import oracle_lib as O
+        ns = 16
+        tk = tok[:ns].cpu().numpy()
+        t0 = time.perf_counter()
+        for q in range(ns):
+            O.rwkv_lm_forward(params, tk[q, :-1], C // cfg.head_size)
+        dt = time.perf_counter() - t0
+        out["cpu_baseline"] = {
+            "value": round(ns / dt, 4), "unit": "member-evals/s", "cores": 1, "kind": "port",
+            "sample": (f"oracle LM forward of {ns} members' {T}-token sequences (base weights; the "
+                       f"rank-1 terms and the update share are under 1% of its FLOPs), "
+                       f"{dt:.2f}s on 1 host thread"),
+            "seconds": round(dt, 2)}
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -92,11 +190,15 @@ def main():
     ap.add_argument("--population", type=int, default=8192)
     ap.add_argument("--cpu-members", type=int, default=8192)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--workload", choices=("c3", "c5"), default="c3")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one GPU "
               "(the population shards by member across GPUs; see DESIGN.md)", file=sys.stderr)
         sys.exit(2)
+    if args.workload == "c5":
+        bench_c5(args)
+        return
 
     import torch
     from hyperscalees_amd import kernels as K
