@@ -65,14 +65,14 @@ PROTOTYPES = {
     "hses_group_norm": (ctypes.c_int, [c_vp, c_i64, c_i32, c_i32, c_i32, c_vp, c_vp, c_f32, c_vp,
                                        c_vp]),
     "hses_token_shift_mix": (ctypes.c_int, [c_vp, c_vp, c_vp, c_vp, c_i32, c_i64, c_i32, c_i32,
-                                            c_vp, c_vp]),
+                                            c_vp, c_i32, c_vp]),
     "hses_relu_sq": (ctypes.c_int, [c_vp, c_i64, c_vp]),
     "hses_rwkv7_wkv": (ctypes.c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i32,
                                       c_i32, c_i32, c_i32, c_vp, c_vp, c_vp]),
     "hses_perturbed_linear_act": (ctypes.c_int, [c_vp, c_i32, c_i64, c_i64, c_i32, c_vp, c_i32,
                                                  c_i32, c_u64, c_i32, c_f32, c_i32, c_i32, c_i32,
                                                  c_i32, c_i32, c_vp, c_i64, c_i64, c_i32, c_i32,
-                                                 c_i32, c_vp, c_size, c_vp]),
+                                                 c_i32, c_i32, c_vp, c_size, c_vp]),
     "hses_rwkv_act": (ctypes.c_int, [c_vp, c_i64, c_i32, c_vp]),
     "hses_tm_gates": (ctypes.c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i32,
                                      c_vp]),

@@ -316,7 +316,7 @@ __global__ void k_act_rows(LinParams P) {
 // kernel (bf16, small rank), or else the small-rank kernel.
 static int run_linear(LinParams& P, DeviceState* st, float* d_y, int64_t y_stride,
                       int64_t y_plane, void* d_work, size_t work_bytes, void* stream,
-                      const char* name, int32_t act = ACT_NONE) {
+                      const char* name, int32_t act = ACT_NONE, int32_t y_fmt = HSES_FMT_F32) {
     HSES_REQUIRE(d_y, "NULL pointer");
     HSES_REQUIRE(y_stride >= P.a, "y_stride smaller than a row");
     HSES_REQUIRE(P.n_time == 1 || y_plane >= (int64_t)P.n * P.rpm * y_stride, "time planes overlap");
@@ -325,10 +325,16 @@ static int run_linear(LinParams& P, DeviceState* st, float* d_y, int64_t y_strid
     P.y_stride = y_stride;
     P.y_plane = y_plane;
     hipStream_t s = (hipStream_t)stream;
-    int rc = launch_linear_pair(P, st, s, d_work, work_bytes);
+    HSES_REQUIRE(y_fmt == HSES_FMT_F32 || y_fmt == HSES_FMT_BF16, "y_fmt must be F32 or BF16");
+    int rc = y_fmt == HSES_FMT_F32 ? launch_linear_pair(P, st, s, d_work, work_bytes)
+                                   : HSES_ERR_UNSUPPORTED;
     if (rc == HSES_ERR_UNSUPPORTED) {
-        rc = launch_linear_wide(P, st, s, d_work, work_bytes, act);
+        rc = launch_linear_wide(P, st, s, d_work, work_bytes, act, y_fmt);
         if (rc != HSES_ERR_UNSUPPORTED) return rc;  // activation fused
+        if (y_fmt != HSES_FMT_F32)
+            return set_error(HSES_ERR_UNSUPPORTED,
+                             std::string(name) + ": bf16 output needs the wide-output kernel (bf16 "
+                             "math, members per 128-row tile x rank <= 16, aligned x rows)");
         rc = launch_linear_small(P, st, s);
     }
     if (rc == HSES_ERR_UNSUPPORTED)
@@ -425,9 +431,10 @@ extern "C" int hses_perturbed_linear_act(const void* d_x, int32_t x_fmt, int64_t
                                          int32_t a, int32_t b, uint64_t key, int32_t rank,
                                          float sigma, int32_t epoch, int32_t noise_reuse,
                                          int32_t tid_lo, int32_t n, int32_t rows_per_member,
-                                         float* d_y, int64_t y_stride, int64_t y_plane,
+                                         void* d_y, int64_t y_stride, int64_t y_plane,
                                          int32_t math, int32_t transposed, int32_t act,
-                                         void* d_work, size_t work_bytes, void* stream) {
+                                         int32_t y_fmt, void* d_work, size_t work_bytes,
+                                         void* stream) {
     HSES_REQUIRE(transposed == 0 || transposed == 1, "transposed must be 0 or 1");
     LinParams P;
     DeviceState* st = nullptr;
@@ -440,6 +447,6 @@ extern "C" int hses_perturbed_linear_act(const void* d_x, int32_t x_fmt, int64_t
                                       math, &st);
     if (rc || n == 0) return rc;
     P.tmm = transposed;
-    return run_linear(P, st, d_y, y_stride, y_plane, d_work, work_bytes, stream,
-                      "hses_perturbed_linear_act", act);
+    return run_linear(P, st, static_cast<float*>(d_y), y_stride, y_plane, d_work, work_bytes,
+                      stream, "hses_perturbed_linear_act", act, y_fmt);
 }

@@ -141,7 +141,7 @@ size_t linear_pair_workspace(const DeviceState* st, int32_t a, int32_t b, int32_
 size_t linear_wide_workspace(int32_t a, int32_t b, int32_t r, int32_t n, int32_t rows_per_member,
                              int32_t n_time, int32_t math);
 int launch_linear_wide(LinParams& P, DeviceState* st, hipStream_t s, void* work, size_t work_bytes,
-                       int32_t act);
+                       int32_t act, int32_t y_fmt = HSES_FMT_F32);
 // W (a, b) fp32 -> (a, kp) bf16, zero columns [b, kp); tmm: W is stored (b, a).
 void launch_w_to_bf16(const float* W, int32_t a, int32_t b, int32_t kp, int32_t tmm, uint16_t* out,
                       hipStream_t s);

@@ -2,7 +2,8 @@
 // small rank, on bf16 MFMA:
 //   do_mm  (eggroll.rs:419-446):  y = x W^T + (x B_m) A_m^T,
 //   do_Tmm (eggroll.rs:450-477):  y = x W + (x A_m) B_m^T,
-// with an optional elementwise activation fused into the epilogue.
+// with an optional elementwise activation fused into the epilogue and an fp32
+// or bf16 output.
 //
 // A workgroup of 8 waves owns a 128-row tile of the output and sweeps its
 // 256-column tiles (rows are member-major, a row tile touches at most a few
@@ -69,7 +70,7 @@ __device__ __forceinline__ float act_apply(float v) {
     return v;
 }
 
-template <int XFMT, int ACT>
+template <int XFMT, int ACT, bool YBF16>
 __global__ __launch_bounds__(KW_THREADS) void k_linear_wide(LinParams P, const uint16_t* __restrict__ Wb,
                                                             int32_t kp, int32_t col_tiles) {
     extern __shared__ __align__(16) unsigned char smem[];
@@ -250,7 +251,7 @@ __global__ __launch_bounds__(KW_THREADS) void k_linear_wide(LinParams P, const u
                 if (Lr >= P.total) continue;
                 int32_t lm = 0;
                 if (noisy && P.nm_max > 1) lm = (int32_t)((Lr - (int64_t)m_first * R) / R);
-                float* yrow = P.y + (flat ? Lr * P.y_stride : phys_row(P, Lr, P.y_stride, P.y_plane)) + o0;
+                const int64_t yoff = (flat ? Lr * P.y_stride : phys_row(P, Lr, P.y_stride, P.y_plane)) + o0;
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
                     const int col = wc * 64 + 32 * j + lc;
@@ -263,7 +264,10 @@ __global__ __launch_bounds__(KW_THREADS) void k_linear_wide(LinParams P, const u
                         for (int32_t c = 0; c < r; ++c) z = __fadd_rn(z, __fmul_rn(xb[c], ar[c]));
                         v = __fadd_rn(v, z);
                     }
-                    yrow[col] = act_apply<ACT>(v);
+                    if constexpr (YBF16)
+                        reinterpret_cast<uint16_t*>(P.y)[yoff + col] = f2bf(act_apply<ACT>(v));
+                    else
+                        P.y[yoff + col] = act_apply<ACT>(v);
                 }
             }
 #pragma unroll
@@ -299,7 +303,7 @@ size_t linear_wide_workspace(int32_t a, int32_t b, int32_t r, int32_t n, int32_t
 }
 
 int launch_linear_wide(LinParams& P, DeviceState* st, hipStream_t s, void* work, size_t work_bytes,
-                       int32_t act) {
+                       int32_t act, int32_t y_fmt) {
     if (P.math != HSES_MATH_BF16) return HSES_ERR_UNSUPPORTED;
     if (P.x_fmt == HSES_FMT_BITS) {
         if (reinterpret_cast<uintptr_t>(P.x) % 8) return HSES_ERR_UNSUPPORTED;
@@ -345,8 +349,10 @@ int launch_linear_wide(LinParams& P, DeviceState* st, hipStream_t s, void* work,
         HSES_CHECK_HIP(hipGetLastError());
         return HSES_OK;
     };
-#define KW_CASE(F, A) \
-    if (P.x_fmt == F && act == A) return launch(k_linear_wide<F, A>);
+    const bool ybf = y_fmt == HSES_FMT_BF16;
+#define KW_CASE(F, A)                                                          \
+    if (P.x_fmt == F && act == A)                                              \
+        return ybf ? launch(k_linear_wide<F, A, true>) : launch(k_linear_wide<F, A, false>);
     KW_CASE(HSES_FMT_F32, ACT_NONE)
     KW_CASE(HSES_FMT_F32, ACT_TANH)
     KW_CASE(HSES_FMT_F32, ACT_SIGMOID)
@@ -355,9 +361,10 @@ int launch_linear_wide(LinParams& P, DeviceState* st, hipStream_t s, void* work,
     KW_CASE(HSES_FMT_BF16, ACT_TANH)
     KW_CASE(HSES_FMT_BF16, ACT_SIGMOID)
     KW_CASE(HSES_FMT_BF16, ACT_RELU_SQ)
-    KW_CASE(HSES_FMT_BITS, ACT_NONE)
 #undef KW_CASE
-    if (P.x_fmt == HSES_FMT_BITS) return HSES_ERR_UNSUPPORTED;  // activations: unfused path
+    if (P.x_fmt == HSES_FMT_BITS && act == ACT_NONE && !ybf)
+        return launch(k_linear_wide<HSES_FMT_BITS, ACT_NONE, false>);
+    if (P.x_fmt == HSES_FMT_BITS) return HSES_ERR_UNSUPPORTED;  // other forms: unfused path
     return set_error(HSES_ERR_INVALID_ARG, "unknown activation");
 }
 

@@ -12,6 +12,13 @@
 
 namespace hses {
 
+// Round-to-nearest-even f32 -> bf16 bits (the rounding the bf16 MFMA operands get).
+__device__ __forceinline__ uint16_t f2bf_rne(float f) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    return (uint16_t)__builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){f, 0.0f}, bf16x2_t));
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
@@ -73,10 +80,11 @@ __global__ __launch_bounds__(256) void k_group_norm(const float* __restrict__ x,
 // n_mix mixing vectors at once: sx = [state, x[:-1]] (0 at a new start) - x,
 // out[m] = x + sx * mix[m].  x (nseq, T, C), state (nseq, C), mix (n_mix, C),
 // new_starts (nseq, T) or NULL, out (n_mix, nseq, T, C).
+template <bool BF16OUT>
 __global__ void k_token_shift_mix(const float* __restrict__ x, const float* __restrict__ state,
                                   const uint8_t* __restrict__ new_starts,
                                   const float* __restrict__ mix, int32_t n_mix, int64_t nseq,
-                                  int32_t T, int32_t C, float* __restrict__ out) {
+                                  int32_t T, int32_t C, void* __restrict__ out) {
     const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t total = nseq * T * C;
     if (e >= total) return;
@@ -88,7 +96,13 @@ __global__ void k_token_shift_mix(const float* __restrict__ x, const float* __re
     if (new_starts && new_starts[st]) prev = 0.0f;
     const float xv = x[e];
     const float sx = prev - xv;
-    for (int32_t m = 0; m < n_mix; ++m) out[(int64_t)m * total + e] = xv + sx * mix[(int64_t)m * C + c];
+    for (int32_t m = 0; m < n_mix; ++m) {
+        const float v = xv + sx * mix[(int64_t)m * C + c];
+        if constexpr (BF16OUT)
+            static_cast<uint16_t*>(out)[(int64_t)m * total + e] = f2bf_rne(v);
+        else
+            static_cast<float*>(out)[(int64_t)m * total + e] = v;
+    }
 }
 
 // llm.rs:206: relu(x)^2, in place.
@@ -344,16 +358,17 @@ extern "C" int hses_group_norm(const float* d_x, int64_t n, int32_t C, int32_t L
 
 extern "C" int hses_token_shift_mix(const float* d_x, const float* d_state,
                                     const uint8_t* d_new_starts, const float* d_mix, int32_t n_mix,
-                                    int64_t nseq, int32_t T, int32_t C, float* d_out,
-                                    void* stream) {
+                                    int64_t nseq, int32_t T, int32_t C, void* d_out,
+                                    int32_t out_fmt, void* stream) {
     HSES_REQUIRE(nseq >= 0 && T >= 1 && C >= 1 && n_mix >= 1, "bad sizes");
+    HSES_REQUIRE(out_fmt == HSES_FMT_F32 || out_fmt == HSES_FMT_BF16, "out_fmt must be F32 or BF16");
     if (nseq == 0) return HSES_OK;
     HSES_REQUIRE(d_x && d_state && d_mix && d_out, "NULL pointer");
     const int64_t total = nseq * T * C;
     HSES_REQUIRE((total + 255) / 256 < (1ll << 31), "grid too large");
-    hipLaunchKernelGGL(k_token_shift_mix, dim3(blocks_of(total, 256)), dim3(256), 0,
-                       (hipStream_t)stream, d_x, d_state, d_new_starts, d_mix, n_mix, nseq, T, C,
-                       d_out);
+    hipLaunchKernelGGL(out_fmt == HSES_FMT_BF16 ? k_token_shift_mix<true> : k_token_shift_mix<false>,
+                       dim3(blocks_of(total, 256)), dim3(256), 0, (hipStream_t)stream, d_x, d_state,
+                       d_new_starts, d_mix, n_mix, nseq, T, C, d_out);
     HSES_CHECK_HIP(hipGetLastError());
     return HSES_OK;
 }

@@ -148,10 +148,11 @@ def lif_scan(cur, tau_m, v_th, v0=None, fmt=FMT_F32, want_v=False, out=None):
 
 
 def perturbed_linear(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n, rows_per_member,
-                     x_fmt=FMT_F32, x_width=None, n_time=1, math=MATH_F32, out=None, act=0):
+                     x_fmt=FMT_F32, x_width=None, n_time=1, math=MATH_F32, out=None, act=0,
+                     out_bf16=False):
     """Batched do_mm.  x is (n_time, n*rows_per_member, units) in x_fmt (or 2-D
-    when n_time == 1); returns y (n_time, n*rows_per_member, a) fp32, passed
-    through the activation `act` (hses_act) when it is not 0."""
+    when n_time == 1); returns y (n_time, n*rows_per_member, a) fp32 (bf16 with
+    out_bf16), passed through the activation `act` (hses_act) when it is not 0."""
     a, b = W.shape
     _dev(W, torch.float32, "W")
     _dev(x, _FMT_DTYPE[x_fmt], "x")
@@ -159,18 +160,20 @@ def perturbed_linear(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n, rows
     M = n * rows_per_member
     if x.shape[-1] != units or x.numel() != n_time * M * units:
         raise ValueError(f"x has shape {tuple(x.shape)}, expected ({n_time}, {M}, {units})")
+    ydt = torch.bfloat16 if out_bf16 else torch.float32
     if out is None:
-        out = torch.empty((n_time, M, a), dtype=torch.float32, device=W.device)
-    _dev(out, torch.float32, "out")
+        out = torch.empty((n_time, M, a), dtype=ydt, device=W.device)
+    _dev(out, ydt, "out")
     if out.numel() != n_time * M * a:
         raise ValueError("out has the wrong size")
     wbytes = int(_lib.load().hses_perturbed_linear_workspace(a, b, rank, n, rows_per_member,
                                                               n_time, math))
     work = _workspace(wbytes, W.device)
-    if act:
+    if act or out_bf16:
         _lib.call("hses_perturbed_linear_act", _p(x), x_fmt, units, M * units, n_time, _p(W), a,
                   b, key & (2**64 - 1), rank, sigma, epoch, noise_reuse, tid_lo, n,
-                  rows_per_member, _p(out), a, M * a, math, 0, act, _p(work), wbytes, _stream())
+                  rows_per_member, _p(out), a, M * a, math, 0, act,
+                  FMT_BF16 if out_bf16 else FMT_F32, _p(work), wbytes, _stream())
     else:
         _lib.call("hses_perturbed_linear", _p(x), x_fmt, units, M * units, n_time, _p(W), a, b,
                   key & (2**64 - 1), rank, sigma, epoch, noise_reuse, tid_lo, n, rows_per_member,
@@ -179,7 +182,7 @@ def perturbed_linear(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n, rows
 
 
 def perturbed_linear_t(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n, rows_per_member,
-                       x_fmt=FMT_F32, n_time=1, math=MATH_F32, out=None, act=0):
+                       x_fmt=FMT_F32, n_time=1, math=MATH_F32, out=None, act=0, out_bf16=False):
     """Batched do_Tmm: y = x W + (x A_m) B_m^T for W of shape (a, b).  x is
     (n_time, n*rows_per_member, a) in x_fmt (or 2-D when n_time == 1);
     returns y (n_time, n*rows_per_member, b) fp32."""
@@ -190,18 +193,20 @@ def perturbed_linear_t(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n, ro
     M = n * rows_per_member
     if x.shape[-1] != units or x.numel() != n_time * M * units:
         raise ValueError(f"x has shape {tuple(x.shape)}, expected ({n_time}, {M}, {units})")
+    ydt = torch.bfloat16 if out_bf16 else torch.float32
     if out is None:
-        out = torch.empty((n_time, M, b), dtype=torch.float32, device=W.device)
-    _dev(out, torch.float32, "out")
+        out = torch.empty((n_time, M, b), dtype=ydt, device=W.device)
+    _dev(out, ydt, "out")
     if out.numel() != n_time * M * b:
         raise ValueError("out has the wrong size")
     wbytes = int(_lib.load().hses_perturbed_linear_t_workspace(a, b, rank, n, rows_per_member,
                                                                 n_time, math))
     work = _workspace(wbytes, W.device)
-    if act:
+    if act or out_bf16:
         _lib.call("hses_perturbed_linear_act", _p(x), x_fmt, units, M * units, n_time, _p(W), a,
                   b, key & (2**64 - 1), rank, sigma, epoch, noise_reuse, tid_lo, n,
-                  rows_per_member, _p(out), b, M * b, math, 1, act, _p(work), wbytes, _stream())
+                  rows_per_member, _p(out), b, M * b, math, 1, act,
+                  FMT_BF16 if out_bf16 else FMT_F32, _p(work), wbytes, _stream())
     else:
         _lib.call("hses_perturbed_linear_t", _p(x), x_fmt, units, M * units, n_time, _p(W), a,
                   b, key & (2**64 - 1), rank, sigma, epoch, noise_reuse, tid_lo, n,

@@ -13,7 +13,7 @@ import torch
 
 from . import _lib
 from . import kernels as K
-from ._lib import ACT_RELU_SQ, ACT_SIGMOID, ACT_TANH, MATH_F32
+from ._lib import ACT_RELU_SQ, ACT_SIGMOID, ACT_TANH, FMT_BF16, FMT_F32, MATH_BF16, MATH_F32
 
 
 def _stream():
@@ -43,17 +43,20 @@ def group_norm(x, groups, w, b, eps=1e-5, out=None):
     return out
 
 
-def token_shift_mix(x, state, mixes, new_starts=None, out=None):
+def token_shift_mix(x, state, mixes, new_starts=None, out=None, bf16=False):
     """x (nseq, T, C), state (nseq, C), mixes (n_mix, C) -> (n_mix, nseq, T, C):
-    x + ([state, x[:-1]] (0 at new starts) - x) * mix."""
+    x + ([state, x[:-1]] (0 at new starts) - x) * mix, in fp32 or (bf16) rounded
+    to bfloat16 for a bf16-math forward."""
     K._dev(x, torch.float32, "x")
     nseq, T, C = x.shape
     n_mix = mixes.shape[0]
     if new_starts is not None:
         K._dev(new_starts, torch.uint8, "new_starts")
-    out = torch.empty((n_mix, nseq, T, C), dtype=torch.float32, device=x.device) if out is None else out
+    dt = torch.bfloat16 if bf16 else torch.float32
+    out = torch.empty((n_mix, nseq, T, C), dtype=dt, device=x.device) if out is None else out
+    K._dev(out, dt, "out")
     _lib.call("hses_token_shift_mix", _p(x), _p(state), _p(new_starts), _p(mixes), n_mix, nseq, T, C,
-              _p(out), _stream())
+              _p(out), FMT_BF16 if bf16 else FMT_F32, _stream())
     return out
 
 
@@ -92,16 +95,20 @@ class EsLinear:
     seqs_per_member: int = 1
 
 
-def linear(x, W, es=None, math=MATH_F32, act=0):
-    """x (nseq, T, in) @ W^T for W (out, in): the plain Linear (es None) or every
-    member's perturbed do_mm (eggroll.rs:419-446) on its own sequences; `act`
-    (hses_act) applies the elementwise op that follows."""
+def _fmt(x):
+    return FMT_BF16 if x.dtype == torch.bfloat16 else FMT_F32
+
+
+def linear(x, W, es=None, math=MATH_F32, act=0, out_bf16=False):
+    """x (nseq, T, in) (fp32 or bf16) @ W^T for W (out, in): the plain Linear (es
+    None) or every member's perturbed do_mm (eggroll.rs:419-446) on its own
+    sequences; `act` (hses_act) applies the elementwise op that follows."""
     nseq, T, cin = x.shape
     if es is None:
         es = EsLinear(key=0, rank=0, sigma=0.0, n=nseq, seqs_per_member=1)
     y = K.perturbed_linear(x.reshape(1, nseq * T, cin), W, es.key, es.rank, es.sigma, es.epoch,
                            es.noise_reuse, es.tid_lo, es.n, es.seqs_per_member * T, n_time=1,
-                           math=math, act=act)
+                           math=math, act=act, x_fmt=_fmt(x), out_bf16=out_bf16)
     return y.reshape(nseq, T, W.shape[0])
 
 
@@ -110,14 +117,17 @@ def channel_mixing(x, state, x_k, Wk, Wv, length, new_starts=None, es_key=None, 
     """ChannelMixing::forward (llm.rs:191-213) on every sequence:
     xk = x + ([state, x[:-1]] - x) * x_k; out = relu(xk Wk^T)^2 Wv^T; last = x[length-1].
     x (nseq, T, C), state (nseq, C), Wk (F, C), Wv (C, F)."""
-    xk = token_shift_mix(x, state, x_k.reshape(1, -1), new_starts)[0]
-    kk = linear(xk, Wk, es_key, math, act=ACT_RELU_SQ)
+    # with bf16 math the intermediates only feed the next bf16 product, which
+    # would round them the same way: store them as bf16
+    bf = math == MATH_BF16
+    xk = token_shift_mix(x, state, x_k.reshape(1, -1), new_starts, bf16=bf)[0]
+    kk = linear(xk, Wk, es_key, math, act=ACT_RELU_SQ, out_bf16=bf)
     out = linear(kk, Wv, es_value, math)
     last = x[:, length - 1, :].contiguous()
     return out, last
 
 
-def linear_t(x, W, es=None, math=MATH_F32, act=0):
+def linear_t(x, W, es=None, math=MATH_F32, act=0, out_bf16=False):
     """x (nseq, T, in) @ W for W (in, out): the plain Tmm (es None) or every
     member's perturbed do_Tmm (common.rs:156-159, eggroll.rs:450-477), then
     the activation `act` (hses_act)."""
@@ -126,7 +136,7 @@ def linear_t(x, W, es=None, math=MATH_F32, act=0):
         es = EsLinear(key=0, rank=0, sigma=0.0, n=nseq, seqs_per_member=1)
     y = K.perturbed_linear_t(x.reshape(1, nseq * T, cin), W, es.key, es.rank, es.sigma, es.epoch,
                              es.noise_reuse, es.tid_lo, es.n, es.seqs_per_member * T, n_time=1,
-                             math=math, act=act)
+                             math=math, act=act, x_fmt=_fmt(x), out_bf16=out_bf16)
     return y.reshape(nseq, T, W.shape[1])
 
 
@@ -161,13 +171,14 @@ def time_mixing(P, x, state, v_first, H, length, layer_id, new_starts=None, es=N
     if not 1 <= length <= T:
         raise ValueError("length must be in [1, T]")
     mixes = torch.stack([P[n] for n in TM_MIXES])
-    xm = token_shift_mix(x, state[:, 0, :].contiguous(), mixes, new_starts)
+    bf = math == MATH_BF16  # bf16-only consumers get bf16 inputs (the same rounding)
+    xm = token_shift_mix(x, state[:, 0, :].contiguous(), mixes, new_starts, bf16=bf)
 
     def lin(i, name):
         return linear(xm[i], P[name], es.get(name), math)
 
     def low(inp, n1, n2, act):
-        h = linear_t(inp, P[n1], es.get(n1), math, act=act)
+        h = linear_t(inp, P[n1], es.get(n1), math, act=act, out_bf16=bf)
         return linear_t(h, P[n2], es.get(n2), math)
 
     r = lin(0, "receptance")

@@ -181,15 +181,18 @@ int hses_perturbed_linear_t(const void *d_x, int32_t x_fmt, int64_t x_stride, in
 /* hses_perturbed_linear (transposed = 0) or hses_perturbed_linear_t (transposed = 1)
  * followed by the activation `act` (hses_act) on every output: a Linear / Tmm and the
  * elementwise op after it (llm.rs:206, 388-410), fused into the forward's epilogue by the
- * wide-output kernel and applied in place after it otherwise.  Workspace as for the
- * unfused entry point of the same orientation. */
+ * wide-output kernel and applied in place after it otherwise.  y_fmt HSES_FMT_F32, or
+ * HSES_FMT_BF16 (rounded to nearest even; for an output only a bf16-math forward reads,
+ * which rounds the same way) when the wide-output kernel serves the call
+ * (HSES_ERR_UNSUPPORTED otherwise).  Workspace as for the unfused entry point of the same
+ * orientation. */
 int hses_perturbed_linear_act(const void *d_x, int32_t x_fmt, int64_t x_stride, int64_t x_plane,
                               int32_t n_time, const float *d_W, int32_t a, int32_t b,
                               uint64_t key, int32_t rank, float sigma, int32_t epoch,
                               int32_t noise_reuse, int32_t tid_lo, int32_t n,
-                              int32_t rows_per_member, float *d_y, int64_t y_stride,
+                              int32_t rows_per_member, void *d_y, int64_t y_stride,
                               int64_t y_plane, int32_t math, int32_t transposed, int32_t act,
-                              void *d_work, size_t work_bytes, void *stream);
+                              int32_t y_fmt, void *d_work, size_t work_bytes, void *stream);
 
 /* Perturbed forward fused with the LIF layer that consumes it
  * (forward_batched_lora_half_with_lif, snn.rs:544-595: lora_linear_batched
@@ -273,10 +276,11 @@ int hses_group_norm(const float *d_x, int64_t n, int32_t C, int32_t L, int32_t G
 /* The token shift of TimeMixing / ChannelMixing (llm.rs:200-205, 360-381) with n_mix
  * mixing vectors: sx = [state, x[:-1]] (0 where new_starts) - x; out[m] = x + sx * mix[m].
  * x (nseq, T, C); state (nseq, C); new_starts (nseq, T) bytes or NULL; mix (n_mix, C);
- * out (n_mix, nseq, T, C). */
+ * out (n_mix, nseq, T, C) in out_fmt: HSES_FMT_F32, or HSES_FMT_BF16 (each value rounded to
+ * nearest even, what a bf16-math forward does to its input). */
 int hses_token_shift_mix(const float *d_x, const float *d_state, const uint8_t *d_new_starts,
                          const float *d_mix, int32_t n_mix, int64_t nseq, int32_t T, int32_t C,
-                         float *d_out, void *stream);
+                         void *d_out, int32_t out_fmt, void *stream);
 /* ChannelMixing's activation (llm.rs:206): x = relu(x)^2 in place. */
 int hses_relu_sq(float *d_x, int64_t n, void *stream);
 /* rwkv7_inner_loop (llm.rs:235-300) for nseq independent sequences: r, w, k, v, a, b

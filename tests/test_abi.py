@@ -90,10 +90,12 @@ def test_validation_rejects_bad_arguments_without_a_gpu():
                     0, ctypes.c_void_p(16), NULL, 0, NULL)
     _expect_invalid("hses_perturbed_linear_act", ctypes.c_void_p(16), 0, 512, 0, 1,
                     ctypes.c_void_p(16), 512, 512, 1, 1, 0.02, 0, 0, 0, 4, 128,
-                    ctypes.c_void_p(16), 512, 0, 1, 2, 0, NULL, 0, NULL)  # transposed 2
+                    ctypes.c_void_p(16), 512, 0, 1, 2, 0, 0, NULL, 0, NULL)  # transposed 2
     _expect_invalid("hses_perturbed_linear_act", ctypes.c_void_p(16), 7, 512, 0, 1,
                     ctypes.c_void_p(16), 512, 512, 1, 1, 0.02, 0, 0, 0, 4, 128,
-                    ctypes.c_void_p(16), 512, 0, 1, 0, 1, NULL, 0, NULL)  # unknown x format
+                    ctypes.c_void_p(16), 512, 0, 1, 0, 1, 0, NULL, 0, NULL)  # unknown x format
+    _expect_invalid("hses_token_shift_mix", ctypes.c_void_p(16), ctypes.c_void_p(16), NULL,
+                    ctypes.c_void_p(16), 6, 2, 4, 8, ctypes.c_void_p(16), 3, NULL)  # out_fmt U8
     _expect_invalid("hses_tm_kk", ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
                     ctypes.c_void_p(16), 4, 2, 65, ctypes.c_void_p(16), ctypes.c_void_p(16), NULL)
     _expect_invalid("hses_add_layer_norm", ctypes.c_void_p(16), ctypes.c_void_p(32), 4, 8,

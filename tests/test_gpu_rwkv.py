@@ -186,3 +186,27 @@ def test_time_mixing_perturbed_members(hses_gpu):
             ro, rs, _ = O.time_mixing(Pm, x[q], st[q], vf[q], H, T, 0)
             close(out[q], ro, 1e-4)
             close(so[q, 1:], rs[1:], 1e-4)
+
+
+def test_bf16_intermediates_are_exact(hses_gpu):
+    # With bf16 math the forward rounds its input to bf16 (nearest even) before the
+    # MFMAs, so a bf16 token-shift output and a bf16 linear output feed the next
+    # product with exactly the values the fp32 path would: the results are equal.
+    from hyperscalees_amd._lib import ACT_RELU_SQ, MATH_BF16
+    rng = np.random.default_rng(21)
+    nseq, T, C, F = 4, 128, 64, 256
+    x = cuda(rng.standard_normal((nseq, T, C)))
+    st = cuda(rng.standard_normal((nseq, C)))
+    mixes = cuda(rng.random((6, C)))
+    o32 = rwkv.token_shift_mix(x, st, mixes)
+    o16 = rwkv.token_shift_mix(x, st, mixes, bf16=True)
+    assert torch.equal(o32.to(torch.bfloat16), o16)
+    W = cuda(rng.standard_normal((F, C)) / 8)
+    es = rwkv.EsLinear(key=0x77, rank=1, sigma=0.1, n=nseq, seqs_per_member=1)
+    y32 = rwkv.linear(o32[1], W, es, MATH_BF16, act=ACT_RELU_SQ)
+    y16 = rwkv.linear(o16[1], W, es, MATH_BF16, act=ACT_RELU_SQ)
+    assert torch.equal(y32, y16)
+    yb = rwkv.linear(o16[1], W, es, MATH_BF16, act=ACT_RELU_SQ, out_bf16=True)
+    assert torch.equal(y32.to(torch.bfloat16), yb)
+    W2 = cuda(rng.standard_normal((C, F)) / 16)
+    assert torch.equal(rwkv.linear(y32, W2, es, MATH_BF16), rwkv.linear(yb, W2, es, MATH_BF16))
