@@ -71,7 +71,7 @@ __device__ __forceinline__ float act_apply(float v) {
 }
 
 template <int XFMT, int ACT, bool YBF16>
-__global__ __launch_bounds__(KW_THREADS) void k_linear_wide(LinParams P, const uint16_t* __restrict__ Wb,
+__global__ __launch_bounds__(KW_THREADS, 4) void k_linear_wide(LinParams P, const uint16_t* __restrict__ Wb,
                                                             int32_t kp, int32_t col_tiles) {
     extern __shared__ __align__(16) unsigned char smem[];
     const bool noisy = P.ne_real > 0;
