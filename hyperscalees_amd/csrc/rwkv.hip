@@ -121,14 +121,28 @@ __global__ void k_relu_sq(float* __restrict__ x, int64_t n) {
 // then sa_i = sum_j s_ij a_j, s_ij = ((s_ij w_j) + v_i k_j) + sa_i b_j,
 // out_i = sum_j s_ij r_j, all sums in ascending j.  s_out is the state after
 // the last step t < length (s_in when length == 0).
-template <int S>
+// With POST the output row is TimeMixing's next three steps instead
+// (llm.rs:455-470): y = (GroupNorm_head(out) + (sum_s r k r_k) v) g, with
+// the group statistics and the readout sum formed exactly as k_group_norm and
+// k_tm_post form them (the same per-lane terms and wave reductions), so the
+// result equals the unfused chain bit for bit.
+struct WkvPost {
+    const float* g;
+    const float* ln_w;
+    const float* ln_b;
+    const float* r_k;
+    float eps;
+};
+
+template <int S, bool POST>
 __global__ __launch_bounds__(256) void k_wkv7(const float* __restrict__ r, const float* __restrict__ w,
                                               const float* __restrict__ k, const float* __restrict__ v,
                                               const float* __restrict__ a, const float* __restrict__ b,
                                               const float* __restrict__ s_in,
                                               const uint8_t* __restrict__ new_starts, int64_t nseq,
                                               int32_t T, int32_t H, int32_t length,
-                                              float* __restrict__ out, float* __restrict__ s_out) {
+                                              float* __restrict__ out, float* __restrict__ s_out,
+                                              WkvPost post) {
     __shared__ __align__(16) float stage[4][6][64];
     const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int64_t item = (int64_t)blockIdx.x * 4 + wv;
@@ -173,7 +187,20 @@ __global__ __launch_bounds__(256) void k_wkv7(const float* __restrict__ r, const
         float acc = 0.0f;
 #pragma unroll
         for (int j = 0; j < S; ++j) acc = acc + s[j] * st[0][j];
-        if (row_ok) out[o + lane] = acc;
+        if constexpr (POST) {
+            const float x1 = row_ok ? acc : 0.0f;
+            const float mean = wave_sum(0.0f + x1) / (float)S;
+            const float var = wave_sum(0.0f + x1 * x1) / (float)S - mean * mean;
+            const float sd = sqrtf(var + post.eps);
+            const int32_t c = h * S + i;
+            const float rk = wave_sum(row_ok ? st[0][i] * st[2][i] * post.r_k[c] : 0.0f);
+            if (row_ok) {
+                const float gn = post.ln_w[c] * ((acc - mean) / sd) + post.ln_b[c];
+                out[o + lane] = (gn + rk * vi) * post.g[o + lane];
+            }
+        } else {
+            if (row_ok) out[o + lane] = acc;
+        }
         if (t == length - 1 && row_ok) {
 #pragma unroll
             for (int j = 0; j < S; ++j) s_out[sbase + j] = s[j];
@@ -383,6 +410,27 @@ extern "C" int hses_relu_sq(float* d_x, int64_t n, void* stream) {
     return HSES_OK;
 }
 
+template <bool POST>
+static int launch_wkv7(const float* d_r, const float* d_w, const float* d_k, const float* d_v,
+                       const float* d_a, const float* d_b, const float* d_s_in,
+                       const uint8_t* d_new_starts, int64_t nseq, int32_t T, int32_t H, int32_t S,
+                       int32_t length, float* d_out, float* d_s_out, WkvPost post, void* stream) {
+    HSES_REQUIRE((nseq * H + 3) / 4 < (1ll << 31), "grid too large");
+    const dim3 g(blocks_of(nseq * H, 4)), blk(256);
+    hipStream_t s = (hipStream_t)stream;
+    if (S == 64)
+        hipLaunchKernelGGL((k_wkv7<64, POST>), g, blk, 0, s, d_r, d_w, d_k, d_v, d_a, d_b, d_s_in,
+                           d_new_starts, nseq, T, H, length, d_out, d_s_out, post);
+    else if (S == 32)
+        hipLaunchKernelGGL((k_wkv7<32, POST>), g, blk, 0, s, d_r, d_w, d_k, d_v, d_a, d_b, d_s_in,
+                           d_new_starts, nseq, T, H, length, d_out, d_s_out, post);
+    else
+        hipLaunchKernelGGL((k_wkv7<16, POST>), g, blk, 0, s, d_r, d_w, d_k, d_v, d_a, d_b, d_s_in,
+                           d_new_starts, nseq, T, H, length, d_out, d_s_out, post);
+    HSES_CHECK_HIP(hipGetLastError());
+    return HSES_OK;
+}
+
 extern "C" int hses_rwkv7_wkv(const float* d_r, const float* d_w, const float* d_k, const float* d_v,
                               const float* d_a, const float* d_b, const float* d_s_in,
                               const uint8_t* d_new_starts, int64_t nseq, int32_t T, int32_t H,
@@ -394,20 +442,28 @@ extern "C" int hses_rwkv7_wkv(const float* d_r, const float* d_w, const float* d
     if (nseq == 0) return HSES_OK;
     HSES_REQUIRE(d_r && d_w && d_k && d_v && d_a && d_b && d_s_in && d_out && d_s_out, "NULL pointer");
     HSES_REQUIRE(d_s_out != d_s_in, "s_out must not alias s_in");
-    HSES_REQUIRE((nseq * H + 3) / 4 < (1ll << 31), "grid too large");
-    const dim3 g(blocks_of(nseq * H, 4)), blk(256);
-    hipStream_t s = (hipStream_t)stream;
-    if (S == 64)
-        hipLaunchKernelGGL(k_wkv7<64>, g, blk, 0, s, d_r, d_w, d_k, d_v, d_a, d_b, d_s_in,
-                           d_new_starts, nseq, T, H, length, d_out, d_s_out);
-    else if (S == 32)
-        hipLaunchKernelGGL(k_wkv7<32>, g, blk, 0, s, d_r, d_w, d_k, d_v, d_a, d_b, d_s_in,
-                           d_new_starts, nseq, T, H, length, d_out, d_s_out);
-    else
-        hipLaunchKernelGGL(k_wkv7<16>, g, blk, 0, s, d_r, d_w, d_k, d_v, d_a, d_b, d_s_in,
-                           d_new_starts, nseq, T, H, length, d_out, d_s_out);
-    HSES_CHECK_HIP(hipGetLastError());
-    return HSES_OK;
+    return launch_wkv7<false>(d_r, d_w, d_k, d_v, d_a, d_b, d_s_in, d_new_starts, nseq, T, H, S,
+                              length, d_out, d_s_out, WkvPost{}, stream);
+}
+
+extern "C" int hses_tm_wkv_post(const float* d_r, const float* d_w, const float* d_k,
+                                const float* d_v, const float* d_a, const float* d_b,
+                                const float* d_s_in, const uint8_t* d_new_starts, int64_t nseq,
+                                int32_t T, int32_t H, int32_t S, int32_t length, const float* d_g,
+                                const float* d_ln_w, const float* d_ln_b, float eps,
+                                const float* d_r_k, float* d_out, float* d_s_out, void* stream) {
+    HSES_REQUIRE(nseq >= 0 && T >= 1 && H >= 1, "bad sizes");
+    HSES_REQUIRE(S == 16 || S == 32 || S == 64, "head size S must be 16, 32 or 64");
+    HSES_REQUIRE(length >= 0 && length <= T, "length must be in [0, T]");
+    if (nseq == 0) return HSES_OK;
+    HSES_REQUIRE(d_r && d_w && d_k && d_v && d_a && d_b && d_s_in && d_out && d_s_out && d_g &&
+                     d_ln_w && d_ln_b && d_r_k,
+                 "NULL pointer");
+    HSES_REQUIRE(d_s_out != d_s_in, "s_out must not alias s_in");
+    HSES_REQUIRE(d_out != d_r && d_out != d_k && d_out != d_v, "out must not alias r, k or v");
+    return launch_wkv7<true>(d_r, d_w, d_k, d_v, d_a, d_b, d_s_in, d_new_starts, nseq, T, H, S,
+                             length, d_out, d_s_out, WkvPost{d_g, d_ln_w, d_ln_b, d_r_k, eps},
+                             stream);
 }
 
 extern "C" int hses_rwkv_act(float* d_x, int64_t n, int32_t kind, void* stream) {

@@ -200,14 +200,16 @@ def time_mixing(P, x, state, v_first, H, length, layer_id, new_starts=None, es=N
     _lib.call("hses_tm_kk", _p(k), _p(P["k_k"]), _p(P["k_a"]), _p(a), rows, H, S, _p(ai), _p(bi),
               _stream())
     s_in = state[:, 1:, :].reshape(nseq, H, S, S).contiguous()
-    shp = (nseq, T, H, S)
-    wkv, s_new = wkv7(r.view(shp), w.view(shp), k.view(shp), v.view(shp), ai.view(shp),
-                      bi.view(shp), s_in, length, new_starts)
+    # the recurrence with ln_x, the readout and the gate fused into its output
+    gn = torch.empty_like(r)
+    s_new = torch.empty_like(s_in)
+    if new_starts is not None:
+        K._dev(new_starts, torch.uint8, "new_starts")
+    _lib.call("hses_tm_wkv_post", _p(r), _p(w), _p(k), _p(v), _p(ai), _p(bi), _p(s_in),
+              _p(new_starts), nseq, T, H, S, length, _p(g), _p(P["ln_w"]), _p(P["ln_b"]), 64e-5,
+              _p(P["r_k"]), _p(gn), _p(s_new), _stream())
     state_out = torch.empty_like(state)
     state_out[:, 0, :] = x[:, length - 1, :]
     state_out[:, 1:, :] = s_new.view(nseq, S, C)
-    gn = group_norm(wkv.view(rows, C), H, P["ln_w"], P["ln_b"], 64e-5)
-    _lib.call("hses_tm_post", _p(gn), _p(r), _p(k), _p(v), _p(g), _p(P["r_k"]), rows, H, S,
-              _stream())
     out = linear(gn.view(nseq, T, C), P["output"], es.get("output"), math)
     return out, state_out, v_first

@@ -210,3 +210,35 @@ def test_bf16_intermediates_are_exact(hses_gpu):
     assert torch.equal(y32.to(torch.bfloat16), yb)
     W2 = cuda(rng.standard_normal((C, F)) / 16)
     assert torch.equal(rwkv.linear(y32, W2, es, MATH_BF16), rwkv.linear(yb, W2, es, MATH_BF16))
+
+
+@pytest.mark.parametrize("S", [64, 32, 16])
+def test_fused_wkv_post_equals_chain(hses_gpu, S):
+    # hses_tm_wkv_post == hses_rwkv7_wkv -> hses_group_norm(G = H) -> hses_tm_post, bit for bit
+    from hyperscalees_amd import _lib, kernels as K
+    nseq, T, H, length = 3, 9, 2, 7
+    C = H * S
+    rng = np.random.default_rng(S)
+    shp = (nseq, T, H, S)
+    r, k, v, g = (cuda(rng.standard_normal(shp)) for _ in range(4))
+    w = cuda(rng.standard_normal(shp) * 0.5 - 0.6)
+    kk = rng.standard_normal(shp)
+    kk /= np.linalg.norm(kk, axis=-1, keepdims=True)
+    a_, b_ = cuda(-kk), cuda(kk * rng.random(shp))
+    s0 = cuda(rng.standard_normal((nseq, H, S, S)) * 0.1)
+    ln_w, ln_b, r_k = (cuda(rng.standard_normal(C)) for _ in range(3))
+    ns = np.zeros((nseq, T), np.uint8)
+    ns[1, 4] = 1
+    nsd = cuda(ns, torch.uint8)
+    wkv, s_a = rwkv.wkv7(r, w, k, v, a_, b_, s0, length, new_starts=nsd)
+    gn = rwkv.group_norm(wkv.view(nseq * T, C), H, ln_w, ln_b, 64e-5)
+    _lib.call("hses_tm_post", K._p(gn), K._p(r), K._p(k), K._p(v), K._p(g), K._p(r_k), nseq * T,
+              H, S, K._stream())
+    out = torch.empty_like(r)
+    s_b = torch.empty_like(s0)
+    _lib.call("hses_tm_wkv_post", K._p(r), K._p(w), K._p(k), K._p(v), K._p(a_), K._p(b_), K._p(s0),
+              K._p(nsd), nseq, T, H, S, length, K._p(g), K._p(ln_w), K._p(ln_b), 64e-5, K._p(r_k),
+              K._p(out), K._p(s_b), K._stream())
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(nseq * T, C), gn)
+    assert torch.equal(s_a, s_b)
