@@ -124,17 +124,17 @@ def bench_c5(args):
     t_fwd = float(np.mean([e[0].elapsed_time(e[1]) for e in marks]))
     t_upd = float(np.mean([e[1].elapsed_time(e[2]) for e in marks]))
 
-    # Dominant single launch: ChannelMixing key of layer 0 (x (N*T, 512) -> relu^2 (N*T, 2048)),
-    # timed alone with events on the launch stream.
+    # Dominant single launch: ChannelMixing key of layer 0 (x (N*T, 512) -> relu^2 (N*T, 2048),
+    # bf16 in and out as in the step), timed alone with events on the launch stream.
     B0 = es.blocks[0]
     C, F, T = cfg.d_model, cfg.ffn_mult * cfg.d_model, cfg.seq_len
-    x = torch.randn((cfg.n, T, C), device="cuda", generator=g)
+    x = torch.randn((cfg.n, T, C), device="cuda", generator=g).to(torch.bfloat16)
     ek = es._es(0, 0, 0, cfg.n)["ffn_key"]
     lk = []
     for _ in range(3):
         e0, e1 = ev(), ev()
         e0.record()
-        rwkv.linear(x, B0["ffn_key"], ek, cfg.math, act=ACT_RELU_SQ)
+        rwkv.linear(x, B0["ffn_key"], ek, cfg.math, act=ACT_RELU_SQ, out_bf16=True)
         e1.record()
         torch.cuda.synchronize()
         lk.append(e0.elapsed_time(e1))
@@ -159,7 +159,8 @@ def bench_c5(args):
                    "parallelism": "single GPU"},
         "phase_ms": {"forward": round(t_fwd, 3), "es_update": round(t_upd, 3)},
         "fwd_tflops": round(rwkv_lm.forward_flops(cfg) / (t_fwd * 1e-3) / 1e12, 1),
-        "roofline": {"kernel": "k_linear_wide<F32, RELU_SQ> (ChannelMixing key, 262144 x 512 -> 2048)",
+        "roofline": {"kernel": ("k_linear_wide<BF16 x, RELU_SQ, bf16 y> (ChannelMixing key, "
+                                "262144 x 512 -> 2048)"),
                      "bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": None, "launch_ms": round(lk_ms, 3),
