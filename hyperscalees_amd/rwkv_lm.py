@@ -141,10 +141,13 @@ class RwkvLmEs:
                                     seqs_per_member=c.seqs_per_member)
                 for name in TM_MATRICES + FFN_MATRICES}
 
-    def logits(self, tokens, epoch=0, tid_lo=0, perturb=True):
+    def logits(self, tokens, epoch=0, tid_lo=0, perturb=True, state=None):
         """tokens (n * seqs_per_member, T) int32 on the device -> logits
         (n * seqs_per_member * T, V) fp32; every member's sequences run with its
-        perturbed MM parameters (perturb False: the plain model)."""
+        perturbed MM parameters (perturb False: the plain model).  With `state`
+        (n_layer, sequences, 2 + S, C) -- per layer row 0 the ChannelMixing shift,
+        rows 1.. TimeMixing's state (rwkv7.py:182-187) -- the sequences continue
+        from it and (logits, new state) is returned."""
         c = self.cfg
         nseq, T = tokens.shape
         n = nseq // c.seqs_per_member
@@ -159,26 +162,36 @@ class RwkvLmEs:
                   K._p(self.P["ln0_w"]), K._p(self.P["ln0_b"]), 1e-5, K._p(x), K._stream())
         B0 = self.blocks[0]
         rwkv.layer_norm(x, B0["ln1_w"], B0["ln1_b"], 1e-5, out=h)
+        carry = state is not None
+        if carry:
+            if state.shape != (c.n_layer, nseq, 2 + c.head_size, C):
+                raise ValueError("state must be (n_layer, sequences, 2 + S, C)")
+            new_state = torch.empty_like(state)
         if T == c.seq_len and nseq == self.state0.shape[0]:
-            state, vf = self.state0, self.vf0
+            zero, vf = self.state0, self.vf0
         else:
-            state = torch.zeros((nseq, 2 + c.head_size, C), dtype=torch.float32, device=self.dev)
+            zero = torch.zeros((nseq, 2 + c.head_size, C), dtype=torch.float32, device=self.dev)
             vf = torch.zeros((nseq, T, C), dtype=torch.float32, device=self.dev)
         for l, B in enumerate(self.blocks):
+            st = state[l] if carry else zero
             es = self._es(l, epoch, tid_lo, n) if perturb else {}
-            d, _, vf = rwkv.time_mixing(B, h.view(nseq, T, C), state[:, 1:, :], vf, H, T, l,
-                                        es=es, math=c.math)
+            d, st_tm, vf = rwkv.time_mixing(B, h.view(nseq, T, C), st[:, 1:, :], vf, H, T, l,
+                                            es=es, math=c.math)
             _lib.call("hses_add_layer_norm", K._p(x), K._p(d), rows, C, K._p(B["ln2_w"]),
                       K._p(B["ln2_b"]), 1e-5, K._p(h), K._stream())
-            d, _ = rwkv.channel_mixing(h.view(nseq, T, C), state[:, 0, :].contiguous(),
-                                       B["ffn_x_k"], B["ffn_key"], B["ffn_value"], T,
-                                       es_key=es.get("ffn_key"), es_value=es.get("ffn_value"),
-                                       math=c.math)
+            d, last = rwkv.channel_mixing(h.view(nseq, T, C), st[:, 0, :].contiguous(),
+                                          B["ffn_x_k"], B["ffn_key"], B["ffn_value"], T,
+                                          es_key=es.get("ffn_key"), es_value=es.get("ffn_value"),
+                                          math=c.math)
+            if carry:
+                new_state[l][:, 1:, :] = st_tm
+                new_state[l][:, 0, :] = last
             nxt = self.blocks[l + 1] if l + 1 < len(self.blocks) else None
             w_, b_ = (nxt["ln1_w"], nxt["ln1_b"]) if nxt else (self.P["ln_out_w"], self.P["ln_out_b"])
             _lib.call("hses_add_layer_norm", K._p(x), K._p(d), rows, C, K._p(w_), K._p(b_), 1e-5,
                       K._p(h), K._stream())
-        return rwkv.linear(h.view(1, rows, C), self.P["head"], None, c.math).view(rows, V)
+        lg = rwkv.linear(h.view(1, rows, C), self.P["head"], None, c.math).view(rows, V)
+        return (lg, new_state) if carry else lg
 
     def forward(self, tokens, epoch=0, tid_lo=0):
         """tokens (n * seqs_per_member, T + 1) int32: inputs are the first T ids,

@@ -121,3 +121,26 @@ def test_embed_layer_norm_out_of_range_token_gives_nan(hses_gpu):
     assert np.isfinite(y[[0, 1, 4]]).all() and np.isnan(y[[2, 3]]).all()
     ref = O.layer_norm(emb.cpu().numpy()[[0, 9, 3]], np.ones(C), np.zeros(C))
     close(y[[0, 1, 4]], ref, 1e-5)
+
+
+def test_lm_full_width_state_carry_is_exact(hses_gpu):
+    # The C5 model at full width and depth (4 layers, d=512, 8 heads of 64, FFN 2048, bf16
+    # products, r=1 perturbed members): the LM is recurrent and every kernel computes a
+    # token's row independently of the others, so running 128 tokens equals running 64 and
+    # then 64 from the carried state, bit for bit (logits and final state).
+    cfg = rwkv_lm.RwkvLmConfig(n=64)
+    params = rwkv_lm.init_params(cfg, seed=11)
+    es = rwkv_lm.RwkvLmEs(cfg, params)
+    S, C = cfg.head_size, cfg.d_model
+    rng = np.random.default_rng(12)
+    tok = torch.from_numpy(rng.integers(0, cfg.vocab, (cfg.n, 128)).astype(np.int32)).cuda()
+    st0 = torch.zeros((cfg.n_layer, cfg.n, 2 + S, C), device="cuda")
+    full, st_full = es.logits(tok, epoch=3, state=st0)
+    a, st_a = es.logits(tok[:, :64].contiguous(), epoch=3, state=st0)
+    b, st_b = es.logits(tok[:, 64:].contiguous(), epoch=3, state=st_a)
+    torch.cuda.synchronize()
+    V = cfg.vocab
+    joined = torch.cat([a.view(cfg.n, 64, V), b.view(cfg.n, 64, V)], dim=1)
+    assert torch.equal(full.view(cfg.n, 128, V), joined)
+    assert torch.equal(st_full, st_b)
+    assert torch.isfinite(full).all()
