@@ -352,6 +352,42 @@ __global__ __launch_bounds__(256) void k_add_layer_norm(float* __restrict__ x,
     for (int32_t c = lane; c < C; c += 64) yr[c] = (xr[c] - mean) / sd * w[c] + b[c];
 }
 
+// k_tm_gates and k_tm_kk in one pass, per (row, head), one wave each: the
+// same per-element operations (a stays in registers instead of memory), so the
+// outputs equal the two-kernel chain bit for bit.
+__global__ __launch_bounds__(256) void k_tm_gates_kk(
+    float* __restrict__ w2o, const float* __restrict__ a2o, const float* __restrict__ v2o,
+    float* __restrict__ v, const float* __restrict__ v_first, const float* __restrict__ w0,
+    const float* __restrict__ a0, const float* __restrict__ v0, float* __restrict__ k,
+    const float* __restrict__ k_k, const float* __restrict__ k_a, int64_t rows, int32_t H,
+    int32_t S, float* __restrict__ ai, float* __restrict__ bi) {
+    const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (item >= rows * H) return;  // whole wave
+    const int64_t row = item / H;
+    const int32_t h = (int32_t)(item - row * H), C = H * S, c = h * S + lane;
+    const bool ok = lane < S;
+    const int64_t o = row * C + c;
+    float av = 0.0f, kv = 0.0f;
+    if (ok) {
+        w2o[o] = -softplus1(-(w0[c] + w2o[o])) - 0.5f;
+        av = 1.0f / (1.0f + expf(-(a0[c] + a2o[o])));
+        if (v2o) {
+            const float sg = 1.0f / (1.0f + expf(-(v0[c] + v2o[o])));
+            v[o] = v[o] + (v_first[o] - v[o]) * sg;
+        }
+        kv = k[o];
+    }
+    const float kk2 = ok ? kv * k_k[c] : 0.0f;
+    float nrm = sqrtf(wave_sum(kk2 * kk2));
+    nrm = nrm < 1e-12f ? 1e-12f : nrm;
+    if (!ok) return;
+    const float kk = kk2 / nrm;
+    ai[o] = -kk;
+    bi[o] = kk * av;
+    k[o] = kv * (k_a[c] * (av - 1.0f) + 1.0f);
+}
+
 }  // namespace hses
 
 using namespace hses;
@@ -541,6 +577,24 @@ extern "C" int hses_add_layer_norm(float* d_x, const float* d_delta, int64_t row
     HSES_REQUIRE((rows + 3) / 4 < (1ll << 31), "grid too large");
     hipLaunchKernelGGL(k_add_layer_norm, dim3(blocks_of(rows, 4)), dim3(256), 0, (hipStream_t)stream,
                        d_x, d_delta, rows, C, d_w, d_b, eps, d_y);
+    HSES_CHECK_HIP(hipGetLastError());
+    return HSES_OK;
+}
+
+extern "C" int hses_tm_gates_kk(float* d_w2o, const float* d_a2o, const float* d_v2o, float* d_v,
+                                const float* d_v_first, const float* d_w0, const float* d_a0,
+                                const float* d_v0, float* d_k, const float* d_k_k,
+                                const float* d_k_a, int64_t rows, int32_t H, int32_t S,
+                                float* d_ai, float* d_bi, void* stream) {
+    HSES_REQUIRE(rows >= 0 && H >= 1 && S >= 1 && S <= 64, "bad sizes (S <= 64)");
+    if (rows == 0) return HSES_OK;
+    HSES_REQUIRE(d_w2o && d_a2o && d_w0 && d_a0 && d_k && d_k_k && d_k_a && d_ai && d_bi,
+                 "NULL pointer");
+    HSES_REQUIRE(!d_v2o || (d_v && d_v_first && d_v0), "NULL pointer (v branch)");
+    HSES_REQUIRE((rows * H + 3) / 4 < (1ll << 31), "grid too large");
+    hipLaunchKernelGGL(k_tm_gates_kk, dim3(blocks_of(rows * H, 4)), dim3(256), 0,
+                       (hipStream_t)stream, d_w2o, d_a2o, d_v2o, d_v, d_v_first, d_w0, d_a0, d_v0,
+                       d_k, d_k_k, d_k_a, rows, H, S, d_ai, d_bi);
     HSES_CHECK_HIP(hipGetLastError());
     return HSES_OK;
 }

@@ -193,12 +193,12 @@ def time_mixing(P, x, state, v_first, H, length, layer_id, new_starts=None, es=N
     a = low(xm[4], "a1", "a2", ACT_TANH)  # a2 output; the gate turns it into a
     g = low(xm[5], "g1", "g2", ACT_SIGMOID)
     rows = nseq * T
-    _lib.call("hses_tm_gates", _p(w), _p(a), _p(v2o), _p(v), _p(v_first), _p(P["w0"]), _p(P["a0"]),
-              _p(P["v0"]), rows, C, _stream())
     ai = torch.empty_like(k)
     bi = torch.empty_like(k)
-    _lib.call("hses_tm_kk", _p(k), _p(P["k_k"]), _p(P["k_a"]), _p(a), rows, H, S, _p(ai), _p(bi),
-              _stream())
+    # gates (w, a, value blend) and the kk normalisation / k update in one pass
+    _lib.call("hses_tm_gates_kk", _p(w), _p(a), _p(v2o), _p(v), _p(v_first), _p(P["w0"]),
+              _p(P["a0"]), _p(P["v0"]), _p(k), _p(P["k_k"]), _p(P["k_a"]), rows, H, S, _p(ai),
+              _p(bi), _stream())
     s_in = state[:, 1:, :].reshape(nseq, H, S, S).contiguous()
     # the recurrence with ln_x, the readout and the gate fused into its output
     gn = torch.empty_like(r)

@@ -320,6 +320,12 @@ int hses_tm_kk(float *d_k, const float *d_k_k, const float *d_k_a, const float *
                int32_t H, int32_t S, float *d_ai, float *d_bi, void *stream);
 int hses_tm_post(float *d_gn, const float *d_r, const float *d_k, const float *d_v, const float *d_g,
                  const float *d_r_k, int64_t rows, int32_t H, int32_t S, void *stream);
+/* hses_tm_gates then hses_tm_kk in one pass (llm.rs:388-426), equal to the two calls bit for
+ * bit; the in-context rate a stays in registers (a2o is only read). */
+int hses_tm_gates_kk(float *d_w2o, const float *d_a2o, const float *d_v2o, float *d_v,
+                     const float *d_v_first, const float *d_w0, const float *d_a0, const float *d_v0,
+                     float *d_k, const float *d_k_k, const float *d_k_a, int64_t rows, int32_t H,
+                     int32_t S, float *d_ai, float *d_bi, void *stream);
 
 /* The RWKV-7 LM around the blocks (src/hyperscalees/models/llm/rwkv7.py:189-253):
  * hses_embed_layer_norm: y[i] = LayerNorm(emb[tokens[i]]) with ln0's w, b (embed and

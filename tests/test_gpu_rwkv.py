@@ -242,3 +242,31 @@ def test_fused_wkv_post_equals_chain(hses_gpu, S):
     torch.cuda.synchronize()
     assert torch.equal(out.view(nseq * T, C), gn)
     assert torch.equal(s_a, s_b)
+
+
+@pytest.mark.parametrize("S,with_v", [(64, True), (32, False)])
+def test_gates_kk_equals_chain(hses_gpu, S, with_v):
+    # hses_tm_gates_kk == hses_tm_gates -> hses_tm_kk, bit for bit
+    from hyperscalees_amd import _lib, kernels as K
+    rows, H = 37, 3
+    C = H * S
+    rng = np.random.default_rng(S + with_v)
+    w2o, a2o, v2o, v, vf, k = (rng.standard_normal((rows, C)).astype(np.float32) for _ in range(6))
+    w0, a0, v0, k_k, k_a = (rng.standard_normal(C).astype(np.float32) for _ in range(5))
+    d = {n: cuda(x) for n, x in dict(w2o=w2o, a2o=a2o, v2o=v2o, v=v, vf=vf, k=k, w0=w0, a0=a0,
+                                       v0=v0, k_k=k_k, k_a=k_a).items()}
+    e = {n: t.clone() for n, t in d.items()}
+    v2 = d["v2o"] if with_v else None
+    ai1, bi1, ai2, bi2 = (torch.empty((rows, C), device="cuda") for _ in range(4))
+    _lib.call("hses_tm_gates", K._p(d["w2o"]), K._p(d["a2o"]), K._p(v2), K._p(d["v"]), K._p(d["vf"]),
+              K._p(d["w0"]), K._p(d["a0"]), K._p(d["v0"]), rows, C, K._stream())
+    _lib.call("hses_tm_kk", K._p(d["k"]), K._p(d["k_k"]), K._p(d["k_a"]), K._p(d["a2o"]), rows, H, S,
+              K._p(ai1), K._p(bi1), K._stream())
+    v2e = e["v2o"] if with_v else None
+    _lib.call("hses_tm_gates_kk", K._p(e["w2o"]), K._p(e["a2o"]), K._p(v2e), K._p(e["v"]),
+              K._p(e["vf"]), K._p(e["w0"]), K._p(e["a0"]), K._p(e["v0"]), K._p(e["k"]),
+              K._p(e["k_k"]), K._p(e["k_a"]), rows, H, S, K._p(ai2), K._p(bi2), K._stream())
+    torch.cuda.synchronize()
+    for n in ("w2o", "v", "k"):
+        assert torch.equal(d[n], e[n]), n
+    assert torch.equal(ai1, ai2) and torch.equal(bi1, bi2)
