@@ -156,20 +156,36 @@ __global__ __launch_bounds__(256) void k_wkv7(const float* __restrict__ r, const
 #pragma unroll
     for (int j = 0; j < S; ++j) s[j] = s_in[sbase + j];
     float (*st)[64] = stage[wv];
+    // this lane's elements of the step's six vectors (and the gate g with POST),
+    // loaded one step ahead so their latency overlaps the previous step's work
+    float nr = 0.0f, nw = 0.0f, nk = 0.0f, nv = 0.0f, na = 0.0f, nb = 0.0f, ng = 0.0f;
+    auto fetch = [&](int32_t t) {
+        const int64_t o = ((sq * T + t) * H + h) * (int64_t)S + i;
+        nr = r[o];
+        nw = w[o];
+        nk = k[o];
+        nv = v[o];
+        na = a[o];
+        nb = b[o];
+        if constexpr (POST) ng = post.g[o];
+    };
+    fetch(0);
     for (int32_t t = 0; t < T; ++t) {
         if (new_starts && new_starts[sq * T + t]) {
 #pragma unroll
             for (int j = 0; j < S; ++j) s[j] = 0.0f;
         }
         const int64_t o = ((sq * T + t) * H + h) * (int64_t)S;
+        const float gcur = ng;
         if (row_ok) {
-            st[0][lane] = r[o + lane];
-            st[1][lane] = expf(-expf(w[o + lane]));
-            st[2][lane] = k[o + lane];
-            st[3][lane] = v[o + lane];
-            st[4][lane] = a[o + lane];
-            st[5][lane] = b[o + lane];
+            st[0][lane] = nr;
+            st[1][lane] = expf(-expf(nw));
+            st[2][lane] = nk;
+            st[3][lane] = nv;
+            st[4][lane] = na;
+            st[5][lane] = nb;
         }
+        if (t + 1 < T) fetch(t + 1);
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -196,7 +212,7 @@ __global__ __launch_bounds__(256) void k_wkv7(const float* __restrict__ r, const
             const float rk = wave_sum(row_ok ? st[0][i] * st[2][i] * post.r_k[c] : 0.0f);
             if (row_ok) {
                 const float gn = post.ln_w[c] * ((acc - mean) / sd) + post.ln_b[c];
-                out[o + lane] = (gn + rk * vi) * post.g[o + lane];
+                out[o + lane] = (gn + rk * vi) * gcur;
             }
         } else {
             if (row_ok) out[o + lane] = acc;
