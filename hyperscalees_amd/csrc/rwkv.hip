@@ -105,6 +105,42 @@ __global__ void k_token_shift_mix(const float* __restrict__ x, const float* __re
     }
 }
 
+// The same for C % 4 == 0, four consecutive channels of one row per thread
+// (16-byte loads, 16- or 8-byte stores, one row computation per four values).
+template <bool BF16OUT>
+__global__ void k_token_shift_mix4(const float* __restrict__ x, const float* __restrict__ state,
+                                   const uint8_t* __restrict__ new_starts,
+                                   const float* __restrict__ mix, int32_t n_mix, int64_t nseq,
+                                   int32_t T, int32_t C, void* __restrict__ out) {
+    const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t total = nseq * T * C;
+    const int64_t e = q * 4;
+    if (e >= total) return;
+    const int32_t c4 = C >> 2;
+    const int64_t st = q / c4;  // sequence * T + t
+    const int32_t c = (int32_t)(q - st * c4) * 4;
+    const int32_t t = (int32_t)(st % T);
+    const int64_t sq = st / T;
+    const float4 xv = *reinterpret_cast<const float4*>(x + e);
+    float4 pv = t == 0 ? *reinterpret_cast<const float4*>(state + sq * C + c)
+                       : *reinterpret_cast<const float4*>(x + e - C);
+    if (new_starts && new_starts[st]) pv = float4{0.0f, 0.0f, 0.0f, 0.0f};
+    const float sx0 = pv.x - xv.x, sx1 = pv.y - xv.y, sx2 = pv.z - xv.z, sx3 = pv.w - xv.w;
+    for (int32_t m = 0; m < n_mix; ++m) {
+        const float4 mv = *reinterpret_cast<const float4*>(mix + (int64_t)m * C + c);
+        const float v0 = xv.x + sx0 * mv.x, v1 = xv.y + sx1 * mv.y;
+        const float v2 = xv.z + sx2 * mv.z, v3 = xv.w + sx3 * mv.w;
+        if constexpr (BF16OUT) {
+            const uint2 pk{(uint32_t)f2bf_rne(v0) | ((uint32_t)f2bf_rne(v1) << 16),
+                           (uint32_t)f2bf_rne(v2) | ((uint32_t)f2bf_rne(v3) << 16)};
+            *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + (int64_t)m * total + e) = pk;
+        } else {
+            *reinterpret_cast<float4*>(static_cast<float*>(out) + (int64_t)m * total + e) =
+                float4{v0, v1, v2, v3};
+        }
+    }
+}
+
 // llm.rs:206: relu(x)^2, in place.
 __global__ void k_relu_sq(float* __restrict__ x, int64_t n) {
     const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -445,9 +481,19 @@ extern "C" int hses_token_shift_mix(const float* d_x, const float* d_state,
     HSES_REQUIRE(d_x && d_state && d_mix && d_out, "NULL pointer");
     const int64_t total = nseq * T * C;
     HSES_REQUIRE((total + 255) / 256 < (1ll << 31), "grid too large");
-    hipLaunchKernelGGL(out_fmt == HSES_FMT_BF16 ? k_token_shift_mix<true> : k_token_shift_mix<false>,
-                       dim3(blocks_of(total, 256)), dim3(256), 0, (hipStream_t)stream, d_x, d_state,
-                       d_new_starts, d_mix, n_mix, nseq, T, C, d_out);
+    const bool bf = out_fmt == HSES_FMT_BF16;
+    const bool vec = C % 4 == 0 && reinterpret_cast<uintptr_t>(d_x) % 16 == 0 &&
+                     reinterpret_cast<uintptr_t>(d_state) % 16 == 0 &&
+                     reinterpret_cast<uintptr_t>(d_mix) % 16 == 0 &&
+                     reinterpret_cast<uintptr_t>(d_out) % 16 == 0;
+    if (vec)
+        hipLaunchKernelGGL(bf ? k_token_shift_mix4<true> : k_token_shift_mix4<false>,
+                           dim3(blocks_of(total / 4, 256)), dim3(256), 0, (hipStream_t)stream, d_x,
+                           d_state, d_new_starts, d_mix, n_mix, nseq, T, C, d_out);
+    else
+        hipLaunchKernelGGL(bf ? k_token_shift_mix<true> : k_token_shift_mix<false>,
+                           dim3(blocks_of(total, 256)), dim3(256), 0, (hipStream_t)stream, d_x,
+                           d_state, d_new_starts, d_mix, n_mix, nseq, T, C, d_out);
     HSES_CHECK_HIP(hipGetLastError());
     return HSES_OK;
 }

@@ -46,9 +46,10 @@ def test_group_norm(hses_gpu, shape, G):
     close(got.cpu().numpy(), O.group_norm(x, G, w, b, 64e-5), 1e-5)
 
 
-def test_token_shift_mix(hses_gpu):
+@pytest.mark.parametrize("C", [40, 38])   # four-channel vector path, scalar path
+def test_token_shift_mix(hses_gpu, C):
     rng = np.random.default_rng(3)
-    nseq, T, C, n_mix = 3, 9, 40, 6
+    nseq, T, n_mix = 3, 9, 6
     x = rng.standard_normal((nseq, T, C)).astype(np.float32)
     st = rng.standard_normal((nseq, C)).astype(np.float32)
     mix = rng.random((n_mix, C)).astype(np.float32)
@@ -60,6 +61,8 @@ def test_token_shift_mix(hses_gpu):
     sx = prev - x
     ref = x[None] + sx[None] * mix[:, None, None, :]
     np.testing.assert_array_equal(got, ref.astype(np.float32))  # same elementwise ops
+    got16 = rwkv.token_shift_mix(cuda(x), cuda(st), cuda(mix), cuda(ns, torch.uint8), bf16=True)
+    assert torch.equal(got16, torch.from_numpy(ref.astype(np.float32)).cuda().to(torch.bfloat16))
 
 
 @pytest.mark.parametrize("nseq,T,H,S,length", [(3, 32, 2, 64, 32), (2, 17, 3, 32, 9), (4, 5, 1, 16, 0)])
