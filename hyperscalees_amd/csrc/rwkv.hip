@@ -404,6 +404,50 @@ __global__ __launch_bounds__(256) void k_add_layer_norm(float* __restrict__ x,
     for (int32_t c = lane; c < C; c += 64) yr[c] = (xr[c] - mean) / sd * w[c] + b[c];
 }
 
+// k_add_layer_norm for C = 256 NV: lane l holds channels 256 j + 4 l .. + 3
+// (j < NV) in registers, read and written with 16-byte accesses.
+template <int NV>
+__global__ __launch_bounds__(256) void k_add_layer_norm4(float* __restrict__ x,
+                                                         const float* __restrict__ d, int64_t rows,
+                                                         const float* __restrict__ w,
+                                                         const float* __restrict__ b, float eps,
+                                                         float* __restrict__ y) {
+    constexpr int C = 256 * NV;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;  // whole wave
+    float4* xr = reinterpret_cast<float4*>(x + row * C);
+    const float4* dr = reinterpret_cast<const float4*>(d + row * C);
+    float4 v[NV];
+    float s = 0.0f, s2 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const float4 a = xr[64 * j + lane], e = dr[64 * j + lane];
+        v[j] = float4{a.x + e.x, a.y + e.y, a.z + e.z, a.w + e.w};
+        xr[64 * j + lane] = v[j];
+        s = s + v[j].x;
+        s = s + v[j].y;
+        s = s + v[j].z;
+        s = s + v[j].w;
+        s2 = s2 + v[j].x * v[j].x;
+        s2 = s2 + v[j].y * v[j].y;
+        s2 = s2 + v[j].z * v[j].z;
+        s2 = s2 + v[j].w * v[j].w;
+    }
+    const float mean = wave_sum(s) / (float)C;
+    const float var = wave_sum(s2) / (float)C - mean * mean;
+    const float sd = sqrtf(var + eps);
+    float4* yr = reinterpret_cast<float4*>(y + row * C);
+    const float4* w4 = reinterpret_cast<const float4*>(w);
+    const float4* b4 = reinterpret_cast<const float4*>(b);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const float4 ww = w4[64 * j + lane], bb = b4[64 * j + lane];
+        yr[64 * j + lane] = float4{(v[j].x - mean) / sd * ww.x + bb.x, (v[j].y - mean) / sd * ww.y + bb.y,
+                                   (v[j].z - mean) / sd * ww.z + bb.z, (v[j].w - mean) / sd * ww.w + bb.w};
+    }
+}
+
 // k_tm_gates and k_tm_kk in one pass, per (row, head), one wave each: the
 // same per-element operations (a stays in registers instead of memory), so the
 // outputs equal the two-kernel chain bit for bit.
@@ -637,8 +681,19 @@ extern "C" int hses_add_layer_norm(float* d_x, const float* d_delta, int64_t row
     HSES_REQUIRE(d_x && d_delta && d_w && d_b && d_y, "NULL pointer");
     HSES_REQUIRE(d_y != d_x && d_y != d_delta, "y must not alias x or delta");
     HSES_REQUIRE((rows + 3) / 4 < (1ll << 31), "grid too large");
-    hipLaunchKernelGGL(k_add_layer_norm, dim3(blocks_of(rows, 4)), dim3(256), 0, (hipStream_t)stream,
-                       d_x, d_delta, rows, C, d_w, d_b, eps, d_y);
+    const bool al = reinterpret_cast<uintptr_t>(d_x) % 16 == 0 && reinterpret_cast<uintptr_t>(d_delta) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(d_w) % 16 == 0 && reinterpret_cast<uintptr_t>(d_b) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(d_y) % 16 == 0;
+    const dim3 g(blocks_of(rows, 4)), blk(256);
+    hipStream_t s = (hipStream_t)stream;
+    if (al && C == 256)
+        hipLaunchKernelGGL(k_add_layer_norm4<1>, g, blk, 0, s, d_x, d_delta, rows, d_w, d_b, eps, d_y);
+    else if (al && C == 512)
+        hipLaunchKernelGGL(k_add_layer_norm4<2>, g, blk, 0, s, d_x, d_delta, rows, d_w, d_b, eps, d_y);
+    else if (al && C == 1024)
+        hipLaunchKernelGGL(k_add_layer_norm4<4>, g, blk, 0, s, d_x, d_delta, rows, d_w, d_b, eps, d_y);
+    else
+        hipLaunchKernelGGL(k_add_layer_norm, g, blk, 0, s, d_x, d_delta, rows, C, d_w, d_b, eps, d_y);
     HSES_CHECK_HIP(hipGetLastError());
     return HSES_OK;
 }

@@ -113,7 +113,7 @@ def linear(x, W, es=None, math=MATH_F32, act=0, out_bf16=False):
 
 
 def channel_mixing(x, state, x_k, Wk, Wv, length, new_starts=None, es_key=None, es_value=None,
-                   math=MATH_F32):
+                   math=MATH_F32, want_last=True):
     """ChannelMixing::forward (llm.rs:191-213) on every sequence:
     xk = x + ([state, x[:-1]] - x) * x_k; out = relu(xk Wk^T)^2 Wv^T; last = x[length-1].
     x (nseq, T, C), state (nseq, C), Wk (F, C), Wv (C, F)."""
@@ -123,7 +123,7 @@ def channel_mixing(x, state, x_k, Wk, Wv, length, new_starts=None, es_key=None, 
     xk = token_shift_mix(x, state, x_k.reshape(1, -1), new_starts, bf16=bf)[0]
     kk = linear(xk, Wk, es_key, math, act=ACT_RELU_SQ, out_bf16=bf)
     out = linear(kk, Wv, es_value, math)
-    last = x[:, length - 1, :].contiguous()
+    last = x[:, length - 1, :].contiguous() if want_last else None
     return out, last
 
 
@@ -151,7 +151,7 @@ TM_MIXES = ("x_r", "x_w", "x_k", "x_v", "x_a", "x_g")
 
 
 def time_mixing(P, x, state, v_first, H, length, layer_id, new_starts=None, es=None,
-                math=MATH_F32):
+                math=MATH_F32, want_state=True):
     """TimeMixing::forward (llm.rs:348-480) on every sequence.
 
     P maps the module's parameter names to device tensors: x_r..x_g, w0, v0,
@@ -208,8 +208,10 @@ def time_mixing(P, x, state, v_first, H, length, layer_id, new_starts=None, es=N
     _lib.call("hses_tm_wkv_post", _p(r), _p(w), _p(k), _p(v), _p(ai), _p(bi), _p(s_in),
               _p(new_starts), nseq, T, H, S, length, _p(g), _p(P["ln_w"]), _p(P["ln_b"]), 64e-5,
               _p(P["r_k"]), _p(gn), _p(s_new), _stream())
-    state_out = torch.empty_like(state)
-    state_out[:, 0, :] = x[:, length - 1, :]
-    state_out[:, 1:, :] = s_new.view(nseq, S, C)
+    state_out = None
+    if want_state:
+        state_out = torch.empty_like(state)
+        state_out[:, 0, :] = x[:, length - 1, :]
+        state_out[:, 1:, :] = s_new.view(nseq, S, C)
     out = linear(gn.view(nseq, T, C), P["output"], es.get("output"), math)
     return out, state_out, v_first

@@ -176,13 +176,13 @@ class RwkvLmEs:
             st = state[l] if carry else zero
             es = self._es(l, epoch, tid_lo, n) if perturb else {}
             d, st_tm, vf = rwkv.time_mixing(B, h.view(nseq, T, C), st[:, 1:, :], vf, H, T, l,
-                                            es=es, math=c.math)
+                                            es=es, math=c.math, want_state=carry)
             _lib.call("hses_add_layer_norm", K._p(x), K._p(d), rows, C, K._p(B["ln2_w"]),
                       K._p(B["ln2_b"]), 1e-5, K._p(h), K._stream())
             d, last = rwkv.channel_mixing(h.view(nseq, T, C), st[:, 0, :].contiguous(),
                                           B["ffn_x_k"], B["ffn_key"], B["ffn_value"], T,
                                           es_key=es.get("ffn_key"), es_value=es.get("ffn_value"),
-                                          math=c.math)
+                                          math=c.math, want_last=carry)
             if carry:
                 new_state[l][:, 1:, :] = st_tm
                 new_state[l][:, 0, :] = last

@@ -273,3 +273,21 @@ def test_gates_kk_equals_chain(hses_gpu, S, with_v):
     for n in ("w2o", "v", "k"):
         assert torch.equal(d[n], e[n]), n
     assert torch.equal(ai1, ai2) and torch.equal(bi1, bi2)
+
+
+@pytest.mark.parametrize("C", [512, 256, 40])   # vector paths and the scalar path
+def test_add_layer_norm(hses_gpu, C):
+    from hyperscalees_amd import _lib, kernels as K
+    rows = 70
+    rng = np.random.default_rng(C)
+    x = rng.standard_normal((rows, C)).astype(np.float32) * 2 + 0.5
+    dl = rng.standard_normal((rows, C)).astype(np.float32)
+    w, b = rng.standard_normal(C).astype(np.float32), rng.standard_normal(C).astype(np.float32)
+    xd, dd, y = cuda(x), cuda(dl), torch.empty((rows, C), device="cuda")
+    wd, bd = cuda(w), cuda(b)   # held: a temporary's memory could be handed to the next tensor
+    _lib.call("hses_add_layer_norm", K._p(xd), K._p(dd), rows, C, K._p(wd), K._p(bd), 1e-5,
+              K._p(y), K._stream())
+    torch.cuda.synchronize()
+    s = x + dl
+    np.testing.assert_array_equal(xd.cpu().numpy(), s)       # the residual, one fp32 add
+    close(y.cpu().numpy(), O.layer_norm(s, w, b, 1e-5), 1e-5)
