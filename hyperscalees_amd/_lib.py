@@ -75,7 +75,7 @@ PROTOTYPES = {
                                                  c_i32, c_i32, c_vp, c_size, c_vp]),
     "hses_tm_wkv_post": (ctypes.c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64,
                                         c_i32, c_i32, c_i32, c_i32, c_vp, c_vp, c_vp, c_f32, c_vp,
-                                        c_vp, c_vp, c_vp]),
+                                        c_vp, c_i32, c_vp, c_vp]),
     "hses_tm_gates_kk": (ctypes.c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
                                         c_vp, c_i64, c_i32, c_i32, c_vp, c_vp, c_vp]),
     "hses_rwkv_act": (ctypes.c_int, [c_vp, c_i64, c_i32, c_vp]),

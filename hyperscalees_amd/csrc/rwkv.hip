@@ -168,6 +168,7 @@ struct WkvPost {
     const float* ln_b;
     const float* r_k;
     float eps;
+    int32_t bf16_out;  // write the output rows as bf16 (nearest even)
 };
 
 template <int S, bool POST>
@@ -248,7 +249,11 @@ __global__ __launch_bounds__(256) void k_wkv7(const float* __restrict__ r, const
             const float rk = wave_sum(row_ok ? st[0][i] * st[2][i] * post.r_k[c] : 0.0f);
             if (row_ok) {
                 const float gn = post.ln_w[c] * ((acc - mean) / sd) + post.ln_b[c];
-                out[o + lane] = (gn + rk * vi) * gcur;
+                const float y = (gn + rk * vi) * gcur;
+                if (post.bf16_out)
+                    reinterpret_cast<uint16_t*>(out)[o + lane] = f2bf_rne(y);
+                else
+                    out[o + lane] = y;
             }
         } else {
             if (row_ok) out[o + lane] = acc;
@@ -593,7 +598,9 @@ extern "C" int hses_tm_wkv_post(const float* d_r, const float* d_w, const float*
                                 const float* d_s_in, const uint8_t* d_new_starts, int64_t nseq,
                                 int32_t T, int32_t H, int32_t S, int32_t length, const float* d_g,
                                 const float* d_ln_w, const float* d_ln_b, float eps,
-                                const float* d_r_k, float* d_out, float* d_s_out, void* stream) {
+                                const float* d_r_k, void* d_out, int32_t out_fmt, float* d_s_out,
+                                void* stream) {
+    HSES_REQUIRE(out_fmt == HSES_FMT_F32 || out_fmt == HSES_FMT_BF16, "out_fmt must be F32 or BF16");
     HSES_REQUIRE(nseq >= 0 && T >= 1 && H >= 1, "bad sizes");
     HSES_REQUIRE(S == 16 || S == 32 || S == 64, "head size S must be 16, 32 or 64");
     HSES_REQUIRE(length >= 0 && length <= T, "length must be in [0, T]");
@@ -604,7 +611,8 @@ extern "C" int hses_tm_wkv_post(const float* d_r, const float* d_w, const float*
     HSES_REQUIRE(d_s_out != d_s_in, "s_out must not alias s_in");
     HSES_REQUIRE(d_out != d_r && d_out != d_k && d_out != d_v, "out must not alias r, k or v");
     return launch_wkv7<true>(d_r, d_w, d_k, d_v, d_a, d_b, d_s_in, d_new_starts, nseq, T, H, S,
-                             length, d_out, d_s_out, WkvPost{d_g, d_ln_w, d_ln_b, d_r_k, eps},
+                             length, static_cast<float*>(d_out), d_s_out,
+                             WkvPost{d_g, d_ln_w, d_ln_b, d_r_k, eps, out_fmt == HSES_FMT_BF16},
                              stream);
 }
 

@@ -201,13 +201,13 @@ def time_mixing(P, x, state, v_first, H, length, layer_id, new_starts=None, es=N
               _p(bi), _stream())
     s_in = state[:, 1:, :].reshape(nseq, H, S, S).contiguous()
     # the recurrence with ln_x, the readout and the gate fused into its output
-    gn = torch.empty_like(r)
+    gn = torch.empty(r.shape, dtype=torch.bfloat16 if bf else torch.float32, device=r.device)
     s_new = torch.empty_like(s_in)
     if new_starts is not None:
         K._dev(new_starts, torch.uint8, "new_starts")
     _lib.call("hses_tm_wkv_post", _p(r), _p(w), _p(k), _p(v), _p(ai), _p(bi), _p(s_in),
               _p(new_starts), nseq, T, H, S, length, _p(g), _p(P["ln_w"]), _p(P["ln_b"]), 64e-5,
-              _p(P["r_k"]), _p(gn), _p(s_new), _stream())
+              _p(P["r_k"]), _p(gn), FMT_BF16 if bf else FMT_F32, _p(s_new), _stream())
     state_out = None
     if want_state:
         state_out = torch.empty_like(state)

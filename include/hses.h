@@ -296,13 +296,15 @@ int hses_rwkv7_wkv(const float *d_r, const float *d_w, const float *d_k, const f
 /* hses_rwkv7_wkv followed by the rest of TimeMixing's per-head algebra (llm.rs:455-470):
  * out = (GroupNorm_head(wkv; ln_w, ln_b, eps) + (sum_s r k r_k) v) * g, formed exactly as
  * hses_group_norm (G = H, L = 1) and hses_tm_post form it (bit-identical to that chain),
- * without writing the recurrence output.  g (nseq, T, H*S); ln_w, ln_b, r_k (H*S); out must
- * not alias r, k or v. */
+ * without writing the recurrence output.  g (nseq, T, H*S); ln_w, ln_b, r_k (H*S); out in
+ * out_fmt (HSES_FMT_F32, or HSES_FMT_BF16 rounded to nearest even for a bf16-math output
+ * projection) must not alias r, k or v. */
 int hses_tm_wkv_post(const float *d_r, const float *d_w, const float *d_k, const float *d_v,
                      const float *d_a, const float *d_b, const float *d_s_in,
                      const uint8_t *d_new_starts, int64_t nseq, int32_t T, int32_t H, int32_t S,
                      int32_t length, const float *d_g, const float *d_ln_w, const float *d_ln_b,
-                     float eps, const float *d_r_k, float *d_out, float *d_s_out, void *stream);
+                     float eps, const float *d_r_k, void *d_out, int32_t out_fmt, float *d_s_out,
+                     void *stream);
 
 /* TimeMixing (llm.rs:348-480) pieces around the projections and the recurrence:
  * hses_rwkv_act: x = tanh(x) (kind 0) or sigmoid(x) (kind 1) in place (the low-rank branches);

@@ -241,10 +241,16 @@ def test_fused_wkv_post_equals_chain(hses_gpu, S):
     s_b = torch.empty_like(s0)
     _lib.call("hses_tm_wkv_post", K._p(r), K._p(w), K._p(k), K._p(v), K._p(a_), K._p(b_), K._p(s0),
               K._p(nsd), nseq, T, H, S, length, K._p(g), K._p(ln_w), K._p(ln_b), 64e-5, K._p(r_k),
-              K._p(out), K._p(s_b), K._stream())
+              K._p(out), 0, K._p(s_b), K._stream())
+    out16 = torch.empty(r.shape, dtype=torch.bfloat16, device="cuda")
+    s_c = torch.empty_like(s0)
+    _lib.call("hses_tm_wkv_post", K._p(r), K._p(w), K._p(k), K._p(v), K._p(a_), K._p(b_), K._p(s0),
+              K._p(nsd), nseq, T, H, S, length, K._p(g), K._p(ln_w), K._p(ln_b), 64e-5, K._p(r_k),
+              K._p(out16), 1, K._p(s_c), K._stream())
     torch.cuda.synchronize()
     assert torch.equal(out.view(nseq * T, C), gn)
     assert torch.equal(s_a, s_b)
+    assert torch.equal(out16, out.to(torch.bfloat16))
 
 
 @pytest.mark.parametrize("S,with_v", [(64, True), (32, False)])
