@@ -6,7 +6,7 @@
 // or bf16 output.
 //
 // A workgroup of 8 waves owns a 128-row tile of the output and sweeps its
-// 256-column tiles (rows are member-major, a row tile touches at most a few
+// 256-column tiles (64 or 128 for outputs that narrow) (rows are member-major, a row tile touches at most a few
 // members; their noise columns, nm * r <= 16, ride along as one extra
 // 16-wide operand):
 //   1. W is converted once per call to bf16 (a, kp) in the workspace; the
@@ -22,6 +22,8 @@
 //      multiply-adds), activation, store, and the accumulators restart.
 #include <math.h>
 
+#include <type_traits>
+
 #include "linear_common.h"
 #include "mfma.h"
 #include "noise_dev.h"
@@ -30,7 +32,7 @@
 
 namespace hses {
 
-constexpr int KW_BM = 128, KW_BN = 256, KW_BK = 64, KW_THREADS = 512;
+constexpr int KW_BM = 128, KW_BN = 256, KW_BK = 64, KW_THREADS = 512;  // KW_BN: widest pass
 constexpr int KW_XP = KW_BK + 8;  // LDS pitch of the x and W tiles (bf16 elements, 144 B)
 constexpr int KW_NE = 16;         // noise columns (members x rank) per tile
 
@@ -70,7 +72,9 @@ __device__ __forceinline__ float act_apply(float v) {
     return v;
 }
 
-template <int XFMT, int ACT, bool YBF16>
+// BN: columns per pass (256, or 128 / 64 for narrow outputs).  The 8 waves
+// form WR x WC (rows x columns); each wave owns WI x WJ blocks of 32 x 32.
+template <int XFMT, int ACT, bool YBF16, int BN>
 __global__ __launch_bounds__(KW_THREADS, 4) void k_linear_wide(LinParams P, const uint16_t* __restrict__ Wb,
                                                             int32_t kp, int32_t col_tiles) {
     extern __shared__ __align__(16) unsigned char smem[];
@@ -85,7 +89,11 @@ __global__ __launch_bounds__(KW_THREADS, 4) void k_linear_wide(LinParams P, cons
 
     const int64_t L0 = (int64_t)blockIdx.x * KW_BM;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int wr = wave >> 2, wc = wave & 3, lc = lane & 31, hl = lane >> 5;
+    constexpr int WC = BN == 256 ? 4 : 2, WR = 8 / WC;
+    constexpr int WI = KW_BM / (32 * WR), WJ = BN / (32 * WC);
+    constexpr int WROWS = KW_BM / WR, WCOLS = BN / WC;
+    constexpr int NW = BN / 64;  // W uint4 loads per thread per K step
+    const int wr = wave / WC, wc = wave % WC, lc = lane & 31, hl = lane >> 5;
     const int32_t b = P.b, R = P.R, a = P.a;
     const int32_t nkt = (b + KW_BK - 1) / KW_BK;
     const bool flat = P.n_time == 1;  // physical row = logical row
@@ -107,10 +115,10 @@ __global__ __launch_bounds__(KW_THREADS, 4) void k_linear_wide(LinParams P, cons
         const int64_t Lr = L0 + xrow0 + XSTEP * i;
         xoff[i] = (xload && Lr < P.total) ? (flat ? Lr * P.x_stride : phys_row(P, Lr, P.x_stride, P.x_plane)) : -1;
     }
-    const int wseg = (tid & 7) * 8, wcol0 = tid >> 3;  // W: 4 columns (step 64) x 8 k
+    const int wseg = (tid & 7) * 8, wcol0 = tid >> 3;  // W: NW columns (step 64) x 8 k
     uint4 xr_[XR];
     uint32_t xbits = 0;
-    uint4 wr_[4];
+    uint4 wr_[NW];
 
     auto load_tiles = [&](int32_t ct_i, int32_t kt) {
         const int32_t k = kt * KW_BK + xseg;
@@ -135,8 +143,8 @@ __global__ __launch_bounds__(KW_THREADS, 4) void k_linear_wide(LinParams P, cons
                                                  : uint4{0, 0, 0, 0};
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int32_t col = ct_i * KW_BN + wcol0 + 64 * i;
+        for (int i = 0; i < NW; ++i) {
+            const int32_t col = ct_i * BN + wcol0 + 64 * i;
             wr_[i] = col < a ? *reinterpret_cast<const uint4*>(Wb + (int64_t)col * kp + kt * KW_BK + wseg)
                              : uint4{0, 0, 0, 0};
         }
@@ -162,7 +170,7 @@ __global__ __launch_bounds__(KW_THREADS, 4) void k_linear_wide(LinParams P, cons
                 *reinterpret_cast<uint4*>(Xs + (xrow0 + XSTEP * i) * KW_XP + xseg) = xr_[i];
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < NW; ++i)
             *reinterpret_cast<uint4*>(Ws + (wcol0 + 64 * i) * KW_XP + wseg) = wr_[i];
     };
 
@@ -177,11 +185,11 @@ __global__ __launch_bounds__(KW_THREADS, 4) void k_linear_wide(LinParams P, cons
     }
 
     // ---- 2. one pipeline over (column tile, K step) -----------------------------
-    f32x16w acc[2][2];
+    f32x16w acc[WI][WJ];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < WI; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < WJ; ++j)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
     f32x4 accx = f32x4{0, 0, 0, 0};
@@ -203,14 +211,15 @@ __global__ __launch_bounds__(KW_THREADS, 4) void k_linear_wide(LinParams P, cons
 #pragma unroll
         for (int ks = 0; ks < KW_BK / 16; ++ks) {
             const int kk = ks * 16 + hl * 8;
-            const u16x8 a0 = lds_u16x8(Xs + (wr * 64 + lc) * KW_XP + kk);
-            const u16x8 a1 = lds_u16x8(Xs + (wr * 64 + 32 + lc) * KW_XP + kk);
-            const u16x8 b0 = lds_u16x8(Ws + (wc * 64 + lc) * KW_XP + kk);
-            const u16x8 b1 = lds_u16x8(Ws + (wc * 64 + 32 + lc) * KW_XP + kk);
-            acc[0][0] = mfma32w(a0, b0, acc[0][0]);
-            acc[0][1] = mfma32w(a0, b1, acc[0][1]);
-            acc[1][0] = mfma32w(a1, b0, acc[1][0]);
-            acc[1][1] = mfma32w(a1, b1, acc[1][1]);
+            u16x8 af[WI], bf[WJ];
+#pragma unroll
+            for (int i = 0; i < WI; ++i) af[i] = lds_u16x8(Xs + (wr * WROWS + 32 * i + lc) * KW_XP + kk);
+#pragma unroll
+            for (int j = 0; j < WJ; ++j) bf[j] = lds_u16x8(Ws + (wc * WCOLS + 32 * j + lc) * KW_XP + kk);
+#pragma unroll
+            for (int i = 0; i < WI; ++i)
+#pragma unroll
+                for (int j = 0; j < WJ; ++j) acc[i][j] = mfma32w(af[i], bf[j], acc[i][j]);
         }
         if (noisy && ct_i == 0) {
 #pragma unroll
@@ -234,15 +243,15 @@ __global__ __launch_bounds__(KW_THREADS, 4) void k_linear_wide(LinParams P, cons
             for (int v = 0; v < 4; ++v) XB[(wave * 16 + 4 * xb_kg + v) * KW_NE + xb_e] = accx[v];
             __syncthreads();
         }
-        const int32_t o0 = ct_i * KW_BN;
-        const int32_t ct = min(KW_BN, a - o0);
+        const int32_t o0 = ct_i * BN;
+        const int32_t ct = min(BN, a - o0);
         // The row addresses below are the same for every column tile; computing
         // them here (the empty asm hides that) keeps the compiler from holding
         // all 32 of them in registers across the whole pipeline.
-        int32_t rbase = wr * 64 + 4 * hl;
+        int32_t rbase = wr * WROWS + 4 * hl;
         asm volatile("" : "+v"(rbase));
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < WI; ++i)
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 // 32x32 layout: lane l holds D[8 (e / 4) + 4 (l / 32) + e % 4][l % 32]
@@ -253,8 +262,8 @@ __global__ __launch_bounds__(KW_THREADS, 4) void k_linear_wide(LinParams P, cons
                 if (noisy && P.nm_max > 1) lm = (int32_t)((Lr - (int64_t)m_first * R) / R);
                 const int64_t yoff = (flat ? Lr * P.y_stride : phys_row(P, Lr, P.y_stride, P.y_plane)) + o0;
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const int col = wc * 64 + 32 * j + lc;
+                for (int j = 0; j < WJ; ++j) {
+                    const int col = wc * WCOLS + 32 * j + lc;
                     if (col >= ct) continue;
                     float v = acc[i][j][e];
                     if (noisy) {
@@ -271,9 +280,9 @@ __global__ __launch_bounds__(KW_THREADS, 4) void k_linear_wide(LinParams P, cons
                 }
             }
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < WI; ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
+            for (int j = 0; j < WJ; ++j)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
         ++ct_i;
@@ -337,7 +346,8 @@ int launch_linear_wide(LinParams& P, DeviceState* st, hipStream_t s, void* work,
     launch_w_to_bf16(P.W, P.a, P.b, kp, P.tmm, wb, s);
     HSES_CHECK_HIP(hipGetLastError());
     const int64_t row_tiles = (P.total + KW_BM - 1) / KW_BM;
-    const int32_t col_tiles = (P.a + KW_BN - 1) / KW_BN;
+    const int32_t bn = P.a <= 64 ? 64 : P.a <= 128 ? 128 : KW_BN;
+    const int32_t col_tiles = (P.a + bn - 1) / bn;
     if (row_tiles > INT32_MAX / 2) return set_error(HSES_ERR_INVALID_ARG, "too many output rows");
     auto launch = [&](auto kern) -> int {
         if (lay.bytes > 64 * 1024)
@@ -350,9 +360,20 @@ int launch_linear_wide(LinParams& P, DeviceState* st, hipStream_t s, void* work,
         return HSES_OK;
     };
     const bool ybf = y_fmt == HSES_FMT_BF16;
-#define KW_CASE(F, A)                                                          \
-    if (P.x_fmt == F && act == A)                                              \
-        return ybf ? launch(k_linear_wide<F, A, true>) : launch(k_linear_wide<F, A, false>);
+    auto by_bn = [&](auto f, auto act_c, auto ybf_c) -> int {
+        constexpr int F = decltype(f)::value, A = decltype(act_c)::value;
+        constexpr bool Y = decltype(ybf_c)::value;
+        if (bn == 64) return launch(k_linear_wide<F, A, Y, 64>);
+        if (bn == 128) return launch(k_linear_wide<F, A, Y, 128>);
+        return launch(k_linear_wide<F, A, Y, KW_BN>);
+    };
+    using std::integral_constant;
+#define KW_CASE(F, A)                                                                         \
+    if (P.x_fmt == F && act == A)                                                             \
+        return ybf ? by_bn(integral_constant<int, F>{}, integral_constant<int, A>{},          \
+                           integral_constant<bool, true>{})                                   \
+                   : by_bn(integral_constant<int, F>{}, integral_constant<int, A>{},          \
+                           integral_constant<bool, false>{});
     KW_CASE(HSES_FMT_F32, ACT_NONE)
     KW_CASE(HSES_FMT_F32, ACT_TANH)
     KW_CASE(HSES_FMT_F32, ACT_SIGMOID)
@@ -363,7 +384,8 @@ int launch_linear_wide(LinParams& P, DeviceState* st, hipStream_t s, void* work,
     KW_CASE(HSES_FMT_BF16, ACT_RELU_SQ)
 #undef KW_CASE
     if (P.x_fmt == HSES_FMT_BITS && act == ACT_NONE && !ybf)
-        return launch(k_linear_wide<HSES_FMT_BITS, ACT_NONE, false>);
+        return by_bn(integral_constant<int, HSES_FMT_BITS>{}, integral_constant<int, ACT_NONE>{},
+                     integral_constant<bool, false>{});
     if (P.x_fmt == HSES_FMT_BITS) return HSES_ERR_UNSUPPORTED;  // other forms: unfused path
     return set_error(HSES_ERR_INVALID_ARG, "unknown activation");
 }
