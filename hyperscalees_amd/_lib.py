@@ -78,6 +78,8 @@ PROTOTYPES = {
                                         c_vp, c_i32, c_vp, c_vp]),
     "hses_tm_gates_kk": (ctypes.c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
                                         c_vp, c_i64, c_i32, c_i32, c_vp, c_vp, c_vp]),
+    "hses_tm_fused": (ctypes.c_int, [c_vp] * 14 + [c_i64, c_i32, c_i32, c_i32, c_i32, c_vp, c_vp,
+                                                   c_vp, c_f32, c_vp, c_vp, c_i32, c_vp, c_vp]),
     "hses_rwkv_act": (ctypes.c_int, [c_vp, c_i64, c_i32, c_vp]),
     "hses_tm_gates": (ctypes.c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i32,
                                      c_vp]),

@@ -171,7 +171,24 @@ struct WkvPost {
     int32_t bf16_out;  // write the output rows as bf16 (nearest even)
 };
 
-template <int S, bool POST>
+// With GATES (and POST) the step's vectors are formed in the staging from
+// TimeMixing's raw projections exactly as k_tm_gates_kk forms them: w is the
+// decay branch's w2 output, a the rate branch's a2 output, k and v the raw key
+// and value, and the per-head kk norm is a wave sum, so nothing between the
+// projections and the output goes through memory.
+struct WkvGates {
+    const float* v2o;      // value branch's v2 output, NULL at the first layer
+    const float* v_first;  // (with v2o)
+    const float* w0;
+    const float* a0;
+    const float* v0;
+    const float* k_k;
+    const float* k_a;
+};
+
+__device__ __forceinline__ float softplus1(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
+
+template <int S, bool POST, bool GATES>
 __global__ __launch_bounds__(256) void k_wkv7(const float* __restrict__ r, const float* __restrict__ w,
                                               const float* __restrict__ k, const float* __restrict__ v,
                                               const float* __restrict__ a, const float* __restrict__ b,
@@ -179,7 +196,7 @@ __global__ __launch_bounds__(256) void k_wkv7(const float* __restrict__ r, const
                                               const uint8_t* __restrict__ new_starts, int64_t nseq,
                                               int32_t T, int32_t H, int32_t length,
                                               float* __restrict__ out, float* __restrict__ s_out,
-                                              WkvPost post) {
+                                              WkvPost post, WkvGates gt) {
     __shared__ __align__(16) float stage[4][6][64];
     const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int64_t item = (int64_t)blockIdx.x * 4 + wv;
@@ -196,6 +213,16 @@ __global__ __launch_bounds__(256) void k_wkv7(const float* __restrict__ r, const
     // this lane's elements of the step's six vectors (and the gate g with POST),
     // loaded one step ahead so their latency overlaps the previous step's work
     float nr = 0.0f, nw = 0.0f, nk = 0.0f, nv = 0.0f, na = 0.0f, nb = 0.0f, ng = 0.0f;
+    float nv2 = 0.0f, nvf = 0.0f;
+    const int32_t cc = h * S + i;  // this lane's channel
+    float w0c = 0.0f, a0c = 0.0f, v0c = 0.0f, kkc = 0.0f, kac = 0.0f;
+    if constexpr (GATES) {
+        w0c = gt.w0[cc];
+        a0c = gt.a0[cc];
+        v0c = gt.v2o ? gt.v0[cc] : 0.0f;
+        kkc = gt.k_k[cc];
+        kac = gt.k_a[cc];
+    }
     auto fetch = [&](int32_t t) {
         const int64_t o = ((sq * T + t) * H + h) * (int64_t)S + i;
         nr = r[o];
@@ -203,7 +230,14 @@ __global__ __launch_bounds__(256) void k_wkv7(const float* __restrict__ r, const
         nk = k[o];
         nv = v[o];
         na = a[o];
-        nb = b[o];
+        if constexpr (GATES) {
+            if (gt.v2o) {
+                nv2 = gt.v2o[o];
+                nvf = gt.v_first[o];
+            }
+        } else {
+            nb = b[o];
+        }
         if constexpr (POST) ng = post.g[o];
     };
     fetch(0);
@@ -214,7 +248,28 @@ __global__ __launch_bounds__(256) void k_wkv7(const float* __restrict__ r, const
         }
         const int64_t o = ((sq * T + t) * H + h) * (int64_t)S;
         const float gcur = ng;
-        if (row_ok) {
+        if constexpr (GATES) {
+            // k_tm_gates_kk's per-element algebra (same operations, same wave sum)
+            const float wv = -softplus1(-(w0c + nw)) - 0.5f;
+            const float av = 1.0f / (1.0f + expf(-(a0c + na)));
+            float vv = nv;
+            if (gt.v2o) {
+                const float sg = 1.0f / (1.0f + expf(-(v0c + nv2)));
+                vv = vv + (nvf - vv) * sg;
+            }
+            const float kk2 = row_ok ? nk * kkc : 0.0f;
+            float nrm = sqrtf(wave_sum(kk2 * kk2));
+            nrm = nrm < 1e-12f ? 1e-12f : nrm;
+            const float kk = kk2 / nrm;
+            if (row_ok) {
+                st[0][lane] = nr;
+                st[1][lane] = expf(-expf(wv));
+                st[2][lane] = nk * (kac * (av - 1.0f) + 1.0f);
+                st[3][lane] = vv;
+                st[4][lane] = -kk;
+                st[5][lane] = kk * av;
+            }
+        } else if (row_ok) {
             st[0][lane] = nr;
             st[1][lane] = expf(-expf(nw));
             st[2][lane] = nk;
@@ -282,7 +337,6 @@ __global__ void k_rwkv_act(float* __restrict__ x, int64_t n, int32_t kind) {
     x[e] = kind == 0 ? tanhf(z) : 1.0f / (1.0f + expf(-z));
 }
 
-__device__ __forceinline__ float softplus1(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
 
 // TimeMixing gates (llm.rs:388-408), per element of (rows, C):
 //   w = -softplus(-(w0 + w2o)) - 0.5 (written over w2o);
@@ -557,23 +611,24 @@ extern "C" int hses_relu_sq(float* d_x, int64_t n, void* stream) {
     return HSES_OK;
 }
 
-template <bool POST>
+template <bool POST, bool GATES = false>
 static int launch_wkv7(const float* d_r, const float* d_w, const float* d_k, const float* d_v,
                        const float* d_a, const float* d_b, const float* d_s_in,
                        const uint8_t* d_new_starts, int64_t nseq, int32_t T, int32_t H, int32_t S,
-                       int32_t length, float* d_out, float* d_s_out, WkvPost post, void* stream) {
+                       int32_t length, float* d_out, float* d_s_out, WkvPost post, void* stream,
+                       WkvGates gt = WkvGates{}) {
     HSES_REQUIRE((nseq * H + 3) / 4 < (1ll << 31), "grid too large");
     const dim3 g(blocks_of(nseq * H, 4)), blk(256);
     hipStream_t s = (hipStream_t)stream;
     if (S == 64)
-        hipLaunchKernelGGL((k_wkv7<64, POST>), g, blk, 0, s, d_r, d_w, d_k, d_v, d_a, d_b, d_s_in,
-                           d_new_starts, nseq, T, H, length, d_out, d_s_out, post);
+        hipLaunchKernelGGL((k_wkv7<64, POST, GATES>), g, blk, 0, s, d_r, d_w, d_k, d_v, d_a, d_b,
+                           d_s_in, d_new_starts, nseq, T, H, length, d_out, d_s_out, post, gt);
     else if (S == 32)
-        hipLaunchKernelGGL((k_wkv7<32, POST>), g, blk, 0, s, d_r, d_w, d_k, d_v, d_a, d_b, d_s_in,
-                           d_new_starts, nseq, T, H, length, d_out, d_s_out, post);
+        hipLaunchKernelGGL((k_wkv7<32, POST, GATES>), g, blk, 0, s, d_r, d_w, d_k, d_v, d_a, d_b,
+                           d_s_in, d_new_starts, nseq, T, H, length, d_out, d_s_out, post, gt);
     else
-        hipLaunchKernelGGL((k_wkv7<16, POST>), g, blk, 0, s, d_r, d_w, d_k, d_v, d_a, d_b, d_s_in,
-                           d_new_starts, nseq, T, H, length, d_out, d_s_out, post);
+        hipLaunchKernelGGL((k_wkv7<16, POST, GATES>), g, blk, 0, s, d_r, d_w, d_k, d_v, d_a, d_b,
+                           d_s_in, d_new_starts, nseq, T, H, length, d_out, d_s_out, post, gt);
     HSES_CHECK_HIP(hipGetLastError());
     return HSES_OK;
 }
@@ -722,4 +777,30 @@ extern "C" int hses_tm_gates_kk(float* d_w2o, const float* d_a2o, const float* d
                        d_k, d_k_k, d_k_a, rows, H, S, d_ai, d_bi);
     HSES_CHECK_HIP(hipGetLastError());
     return HSES_OK;
+}
+
+extern "C" int hses_tm_fused(const float* d_r, const float* d_w2o, const float* d_k,
+                             const float* d_v, const float* d_a2o, const float* d_v2o,
+                             const float* d_v_first, const float* d_w0, const float* d_a0,
+                             const float* d_v0, const float* d_k_k, const float* d_k_a,
+                             const float* d_s_in, const uint8_t* d_new_starts, int64_t nseq,
+                             int32_t T, int32_t H, int32_t S, int32_t length, const float* d_g,
+                             const float* d_ln_w, const float* d_ln_b, float eps,
+                             const float* d_r_k, void* d_out, int32_t out_fmt, float* d_s_out,
+                             void* stream) {
+    HSES_REQUIRE(nseq >= 0 && T >= 1 && H >= 1, "bad sizes");
+    HSES_REQUIRE(S == 16 || S == 32 || S == 64, "head size S must be 16, 32 or 64");
+    HSES_REQUIRE(length >= 0 && length <= T, "length must be in [0, T]");
+    HSES_REQUIRE(out_fmt == HSES_FMT_F32 || out_fmt == HSES_FMT_BF16, "out_fmt must be F32 or BF16");
+    if (nseq == 0) return HSES_OK;
+    HSES_REQUIRE(d_r && d_w2o && d_k && d_v && d_a2o && d_w0 && d_a0 && d_k_k && d_k_a && d_s_in &&
+                     d_out && d_s_out && d_g && d_ln_w && d_ln_b && d_r_k,
+                 "NULL pointer");
+    HSES_REQUIRE(!d_v2o || (d_v_first && d_v0), "NULL pointer (value branch)");
+    HSES_REQUIRE(d_s_out != d_s_in, "s_out must not alias s_in");
+    return launch_wkv7<true, true>(
+        d_r, d_w2o, d_k, d_v, d_a2o, nullptr, d_s_in, d_new_starts, nseq, T, H, S, length,
+        static_cast<float*>(d_out), d_s_out,
+        WkvPost{d_g, d_ln_w, d_ln_b, d_r_k, eps, out_fmt == HSES_FMT_BF16}, stream,
+        WkvGates{d_v2o, d_v_first, d_w0, d_a0, d_v0, d_k_k, d_k_a});
 }

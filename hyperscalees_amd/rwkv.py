@@ -186,26 +186,21 @@ def time_mixing(P, x, state, v_first, H, length, layer_id, new_starts=None, es=N
     k = lin(2, "key")
     v = lin(3, "value")
     if layer_id == 0:
-        v_first = v.clone()
+        v_first = v  # only read from here on
         v2o = None
     else:
         v2o = low(xm[3], "v1", "v2", ACT_TANH)
     a = low(xm[4], "a1", "a2", ACT_TANH)  # a2 output; the gate turns it into a
     g = low(xm[5], "g1", "g2", ACT_SIGMOID)
-    rows = nseq * T
-    ai = torch.empty_like(k)
-    bi = torch.empty_like(k)
-    # gates (w, a, value blend) and the kk normalisation / k update in one pass
-    _lib.call("hses_tm_gates_kk", _p(w), _p(a), _p(v2o), _p(v), _p(v_first), _p(P["w0"]),
-              _p(P["a0"]), _p(P["v0"]), _p(k), _p(P["k_k"]), _p(P["k_a"]), rows, H, S, _p(ai),
-              _p(bi), _stream())
     s_in = state[:, 1:, :].reshape(nseq, H, S, S).contiguous()
-    # the recurrence with ln_x, the readout and the gate fused into its output
+    # the gates, the kk normalisation and k update, the recurrence, ln_x, the readout and
+    # the gate in one kernel, from the raw projections
     gn = torch.empty(r.shape, dtype=torch.bfloat16 if bf else torch.float32, device=r.device)
     s_new = torch.empty_like(s_in)
     if new_starts is not None:
         K._dev(new_starts, torch.uint8, "new_starts")
-    _lib.call("hses_tm_wkv_post", _p(r), _p(w), _p(k), _p(v), _p(ai), _p(bi), _p(s_in),
+    _lib.call("hses_tm_fused", _p(r), _p(w), _p(k), _p(v), _p(a), _p(v2o), _p(v_first),
+              _p(P["w0"]), _p(P["a0"]), _p(P["v0"]), _p(P["k_k"]), _p(P["k_a"]), _p(s_in),
               _p(new_starts), nseq, T, H, S, length, _p(g), _p(P["ln_w"]), _p(P["ln_b"]), 64e-5,
               _p(P["r_k"]), _p(gn), FMT_BF16 if bf else FMT_F32, _p(s_new), _stream())
     state_out = None

@@ -306,6 +306,19 @@ int hses_tm_wkv_post(const float *d_r, const float *d_w, const float *d_k, const
                      float eps, const float *d_r_k, void *d_out, int32_t out_fmt, float *d_s_out,
                      void *stream);
 
+/* hses_tm_gates_kk followed by hses_tm_wkv_post in one kernel (llm.rs:388-470), equal to
+ * that chain bit for bit: from TimeMixing's raw projections r, k, v (nseq, T, H*S), the decay
+ * branch's w2 output w2o, the rate branch's a2 output a2o and (after the first layer) the value
+ * branch's v2 output v2o with v_first (else NULL), the gates, kk normalisation and k update are
+ * formed per step inside the recurrence; w2o, k, v and the rest are only read. */
+int hses_tm_fused(const float *d_r, const float *d_w2o, const float *d_k, const float *d_v,
+                  const float *d_a2o, const float *d_v2o, const float *d_v_first, const float *d_w0,
+                  const float *d_a0, const float *d_v0, const float *d_k_k, const float *d_k_a,
+                  const float *d_s_in, const uint8_t *d_new_starts, int64_t nseq, int32_t T,
+                  int32_t H, int32_t S, int32_t length, const float *d_g, const float *d_ln_w,
+                  const float *d_ln_b, float eps, const float *d_r_k, void *d_out, int32_t out_fmt,
+                  float *d_s_out, void *stream);
+
 /* TimeMixing (llm.rs:348-480) pieces around the projections and the recurrence:
  * hses_rwkv_act: x = tanh(x) (kind 0) or sigmoid(x) (kind 1) in place (the low-rank branches);
  * hses_tm_gates (llm.rs:388-408), per element of (rows, C): w2o <- -softplus(-(w0 + w2o)) - 0.5,

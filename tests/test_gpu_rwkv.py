@@ -297,3 +297,44 @@ def test_add_layer_norm(hses_gpu, C):
     s = x + dl
     np.testing.assert_array_equal(xd.cpu().numpy(), s)       # the residual, one fp32 add
     close(y.cpu().numpy(), O.layer_norm(s, w, b, 1e-5), 1e-5)
+
+
+@pytest.mark.parametrize("S,with_v,bf", [(64, True, False), (32, False, False), (64, True, True)])
+def test_tm_fused_equals_chain(hses_gpu, S, with_v, bf):
+    # hses_tm_fused == hses_tm_gates_kk -> hses_tm_wkv_post, bit for bit
+    from hyperscalees_amd import _lib, kernels as K
+    nseq, T, H, length = 3, 9, 2, 7
+    C = H * S
+    rng = np.random.default_rng(S + 2 * with_v + bf)
+    shp = (nseq, T, H, S)
+    raw = {n: cuda(rng.standard_normal(shp)) for n in ("r", "w2o", "k", "v", "a2o", "v2o", "vf", "g")}
+    par = {n: cuda(rng.standard_normal(C)) for n in ("w0", "a0", "v0", "k_k", "k_a", "ln_w", "ln_b", "r_k")}
+    s0 = cuda(rng.standard_normal((nseq, H, S, S)) * 0.1)
+    ns = np.zeros((nseq, T), np.uint8)
+    ns[2, 3] = 1
+    nsd = cuda(ns, torch.uint8)
+    odt = torch.bfloat16 if bf else torch.float32
+    c = {n: t.clone() for n, t in raw.items()}
+    v2 = c["v2o"] if with_v else None
+    ai, bi = torch.empty(shp, device="cuda"), torch.empty(shp, device="cuda")
+    _lib.call("hses_tm_gates_kk", K._p(c["w2o"]), K._p(c["a2o"]), K._p(v2), K._p(c["v"]),
+              K._p(c["vf"]), K._p(par["w0"]), K._p(par["a0"]), K._p(par["v0"]), K._p(c["k"]),
+              K._p(par["k_k"]), K._p(par["k_a"]), nseq * T, H, S, K._p(ai), K._p(bi), K._stream())
+    out1, s1 = torch.empty(shp, dtype=odt, device="cuda"), torch.empty_like(s0)
+    _lib.call("hses_tm_wkv_post", K._p(c["r"]), K._p(c["w2o"]), K._p(c["k"]), K._p(c["v"]),
+              K._p(ai), K._p(bi), K._p(s0), K._p(nsd), nseq, T, H, S, length, K._p(c["g"]),
+              K._p(par["ln_w"]), K._p(par["ln_b"]), 64e-5, K._p(par["r_k"]), K._p(out1), int(bf),
+              K._p(s1), K._stream())
+    f = {n: t.clone() for n, t in raw.items()}
+    v2f = f["v2o"] if with_v else None
+    out2, s2 = torch.empty(shp, dtype=odt, device="cuda"), torch.empty_like(s0)
+    _lib.call("hses_tm_fused", K._p(f["r"]), K._p(f["w2o"]), K._p(f["k"]), K._p(f["v"]),
+              K._p(f["a2o"]), K._p(v2f), K._p(f["vf"] if with_v else None), K._p(par["w0"]),
+              K._p(par["a0"]), K._p(par["v0"]), K._p(par["k_k"]), K._p(par["k_a"]), K._p(s0),
+              K._p(nsd), nseq, T, H, S, length, K._p(f["g"]), K._p(par["ln_w"]), K._p(par["ln_b"]),
+              64e-5, K._p(par["r_k"]), K._p(out2), int(bf), K._p(s2), K._stream())
+    torch.cuda.synchronize()
+    assert torch.equal(out1, out2)
+    assert torch.equal(s1, s2)
+    for n in raw:   # the fused kernel only reads its inputs
+        assert torch.equal(f[n], raw[n]), n
