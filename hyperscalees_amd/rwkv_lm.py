@@ -129,6 +129,7 @@ class RwkvLmEs:
         self.m = {ln: None for ln in self.keys}
         self.v = {ln: None for ln in self.keys}
         self.step_t = 0
+        self.streams = None
         S, C = cfg.head_size, cfg.d_model
         nseq = cfg.n * cfg.seqs_per_member
         self.state0 = torch.zeros((nseq, 2 + S, C), dtype=torch.float32, device=self.dev)
@@ -211,13 +212,27 @@ class RwkvLmEs:
         n = raw_fit.numel()
         scale = np.float32(-math.sqrt(n) / n)   # -g sqrt(N), g = (1/N) sum (eggroll.rs:403)
         self.step_t += 1
-        for (l, name), key in self.keys.items():
-            W = self.blocks[l][name]
-            a, b = W.shape
-            K.es_update(z, 0, key, c.rank, c.sigma, epoch, c.noise_reuse, a, b, scale,
-                        out=self.grads[(l, name)])
-            K.solver_step(c.solver, c.lr, W, self.grads[(l, name)], self.m[(l, name)],
-                          self.v[(l, name)], step_t=self.step_t)
+        # The parameters' updates are independent and each fills only part of the GPU
+        # at r = 1: they run round-robin on side streams (default priority, each with
+        # its own workspace), joined before the next forward.
+        if self.streams is None:
+            self.streams = [torch.cuda.Stream(device=self.dev) for _ in range(4)]
+        main = torch.cuda.current_stream()
+        ready = torch.cuda.Event()
+        ready.record(main)
+        for side in self.streams:
+            side.wait_event(ready)
+            z.record_stream(side)
+        for i, ((l, name), key) in enumerate(self.keys.items()):
+            with torch.cuda.stream(self.streams[i % len(self.streams)]):
+                W = self.blocks[l][name]
+                a, b = W.shape
+                K.es_update(z, 0, key, c.rank, c.sigma, epoch, c.noise_reuse, a, b, scale,
+                            out=self.grads[(l, name)])
+                K.solver_step(c.solver, c.lr, W, self.grads[(l, name)], self.m[(l, name)],
+                              self.v[(l, name)], step_t=self.step_t)
+        for side in self.streams:
+            main.wait_stream(side)
         return z
 
     def step(self, tokens, epoch=0):
