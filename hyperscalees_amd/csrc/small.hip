@@ -61,6 +61,66 @@ __global__ __launch_bounds__(256) void k_member_fitness(const float* __restrict_
     }
 }
 
+// The same fitness for wide rows (classes > 64, e.g. a language model's
+// vocabulary): one wave per member walks its rows in order, the lanes split a
+// row's classes (coalesced loads); the row's maximum and first maximal class,
+// and its sum of exponentials, are fixed-order wave reductions, and lane 0
+// accumulates the member's rows in double in row order.
+__global__ __launch_bounds__(256) void k_member_fitness_wide(const float* __restrict__ logits,
+                                                             int32_t classes,
+                                                             const int32_t* __restrict__ labels,
+                                                             int32_t n, int32_t rpm, int32_t reward,
+                                                             float* __restrict__ fit,
+                                                             unsigned long long* __restrict__ correct) {
+    __shared__ uint32_t block_hits[4];
+    const int32_t m = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int32_t lane = threadIdx.x & 63;
+    double acc = 0.0;
+    uint32_t hits = 0;
+    for (int32_t s = 0; m < n && s < rpm; ++s) {
+        const int64_t row = (int64_t)m * rpm + s;
+        const float* x = logits + row * classes;
+        float mx = -INFINITY;
+        int32_t am = classes;
+        for (int32_t c = lane; c < classes; c += 64)
+            if (x[c] > mx) {  // ascending c: the lane's first maximal class
+                mx = x[c];
+                am = c;
+            }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const float om = __shfl_xor(mx, off);
+            const int32_t oa = __shfl_xor(am, off);
+            if (om > mx || (om == mx && oa < am)) {
+                mx = om;
+                am = oa;
+            }
+        }
+        const int32_t label = labels[row];
+        hits += am == label ? 1u : 0u;
+        if (reward == HSES_REWARD_BINARY) {
+            acc += am == label ? 1.0 : 0.0;
+        } else {
+            float sum = 0.0f;
+            for (int32_t c = lane; c < classes; c += 64) sum = __fadd_rn(sum, expf(__fsub_rn(x[c], mx)));
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) sum = __fadd_rn(sum, __shfl_xor(sum, off));
+            const int32_t lab = label < 0 ? 0 : (label >= classes ? classes - 1 : label);
+            acc += (double)__fsub_rn(__fsub_rn(x[lab], mx), logf(sum));
+        }
+    }
+    if (lane == 0) {
+        if (m < n) fit[m] = (float)(acc / rpm);
+        block_hits[threadIdx.x >> 6] = hits;
+    }
+    if (!correct) return;  // uniform over the block
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t h = block_hits[0] + block_hits[1] + block_hits[2] + block_hits[3];
+        if (h) atomicAdd(correct, (unsigned long long)h);
+    }
+}
+
 // Sum and sum of squares (in double) of v[0..n) over one 1024-thread block,
 // a fixed-order tree, so the result is deterministic.  Every thread returns
 // the totals.
@@ -187,7 +247,8 @@ extern "C" int hses_member_fitness(const float* d_logits, int32_t classes, const
     HSES_REQUIRE(reward == HSES_REWARD_LOGLIK || reward == HSES_REWARD_BINARY, "unknown reward");
     if (n == 0) return HSES_OK;
     HSES_REQUIRE(d_logits && d_labels && d_fit, "NULL pointer");
-    hipLaunchKernelGGL(k_member_fitness, dim3((n + 3) / 4), dim3(256), 0, (hipStream_t)stream,
+    hipLaunchKernelGGL(classes > 64 ? k_member_fitness_wide : k_member_fitness, dim3((n + 3) / 4),
+                       dim3(256), 0, (hipStream_t)stream,
                        d_logits, classes, d_labels, n, rows_per_member, reward, d_fit, d_correct);
     HSES_CHECK_HIP(hipGetLastError());
     return HSES_OK;

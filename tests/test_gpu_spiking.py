@@ -122,11 +122,12 @@ def test_member_loglik(hses_gpu, n, rpm):
 
 
 @pytest.mark.parametrize("reward", [REWARD_LOGLIK, REWARD_BINARY])
-def test_member_fitness_rewards_and_correct_count(hses_gpu, reward):
+@pytest.mark.parametrize("c", [10, 256, 100])   # per-lane rows; wide rows (lanes over classes)
+def test_member_fitness_rewards_and_correct_count(hses_gpu, reward, c):
     # fitness_from_logits_reward (snn_mnist.rs:180-201) per reward kind, member
     # means, and the argmax == label counter (first maximal class on ties).
-    rng = np.random.default_rng(11 + reward)
-    n, rpm, c = 37, 70, 10
+    rng = np.random.default_rng(11 + reward + c)
+    n, rpm = 37, 70
     logits = np.round(rng.standard_normal((n * rpm, c)) * 2).astype(np.float32)  # many ties
     labels = rng.integers(0, c, n * rpm).astype(np.int32)
     hit = (logits.argmax(1) == labels)
