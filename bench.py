@@ -52,9 +52,33 @@ def update_bytes(cfg):
     return tot
 
 
+def host_cpu():
+    """(threads this process may use, logical CPUs of the host, CPU model name).
+    The thread count is the process's CPU affinity, capped by OMP_NUM_THREADS
+    when set (the box's per-GPU CPU share)."""
+    nproc = os.cpu_count() or 1
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        avail = nproc
+    cap = os.environ.get("OMP_NUM_THREADS")
+    threads = min(avail, int(cap)) if cap and cap.isdigit() and int(cap) > 0 else avail
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return threads, nproc, model
+
+
 def cpu_baseline(cfg, pool, labels, idx, W, members, threads):
     """The oracle (C restatement of the reference CPU path) on `members` members,
-    forward + their share of the ES update, extrapolated linearly in N."""
+    forward + their share of the ES update, extrapolated linearly in N when
+    members < N."""
     from tests import oracle_lib as O
     L = O.load()
     dims = np.array(cfg.dims, np.int32)
@@ -81,11 +105,13 @@ def cpu_baseline(cfg, pool, labels, idx, W, members, threads):
         O.lora_grad_f64(cfg.sigma, cfg.keys[l], cfg.rank, 0, z, a, b, nthreads=threads)
     t2 = time.perf_counter()
     per_member = (t2 - t0) / members
+    _, nproc, model = host_cpu()
+    scope = ("all N members (no extrapolation)" if members == cfg.n else
+             f"{members} of {cfg.n} members, extrapolated linearly in N")
     return {"value": 1.0 / per_member, "unit": "member-evals/s", "cores": threads,
-            "kind": "port",
-            "sample": (f"C3 ES step (forward + ES-update share) for {members} of {cfg.n} members "
-                       f"on {threads} host threads, extrapolated linearly in N; "
-                       f"fwd {t1 - t0:.2f}s, update {t2 - t1:.2f}s"),
+            "kind": "port", "host_nproc": nproc, "cpu_model": model,
+            "sample": (f"C3 ES step (forward + ES update) of {scope}, oracle (C, -O3, OpenMP) on "
+                       f"{threads} host threads; fwd {t1 - t0:.2f}s, update {t2 - t1:.2f}s"),
             "seconds": round(t2 - t0, 2)}
 
 
@@ -167,20 +193,53 @@ def bench_c5(args):
                      "algorithmic_flop_per_launch": lk_flops},
     }
     if not args.no_cpu_baseline:
-        from tests import oracle_lib as O
-        ns = 16
-        tk = tok[:ns].cpu().numpy()
-        t0 = time.perf_counter()
-        for q in range(ns):
-            O.rwkv_lm_forward(params, tk[q, :-1], C // cfg.head_size)
-        dt = time.perf_counter() - t0
-        out["cpu_baseline"] = {
-            "value": round(ns / dt, 4), "unit": "member-evals/s", "cores": 1, "kind": "port",
-            "sample": (f"oracle LM forward of {ns} members' {T}-token sequences (base weights; the "
-                       f"rank-1 terms and the update share are under 1% of its FLOPs), "
-                       f"{dt:.2f}s on 1 host thread"),
-            "seconds": round(dt, 2)}
+        out["cpu_baseline"] = cpu_baseline_c5(cfg, params, es, tok, args.cpu_members)
     print(json.dumps(out), flush=True)
+
+
+def cpu_baseline_c5(cfg, params, es, tok, members):
+    """The oracle's LM (a C restatement of the reference's forward) for a sample
+    of members, each on its own materialised parameters W + A_m B_m^T, in
+    parallel over the host threads (ctypes releases the GIL), plus the sample's
+    share of the ES update (the oracle's double-accumulated gradient of every
+    matrix over the sample's members)."""
+    from concurrent.futures import ThreadPoolExecutor
+    from tests import oracle_lib as O
+    threads, nproc, model = host_cpu()
+    ns = max(1, min(members, 4 * threads, cfg.n))
+    tk = tok[:ns].cpu().numpy()
+    H = cfg.d_model // cfg.head_size
+    bs = O.load().or_base_sigma(cfg.sigma, cfg.rank)
+    names = list(es.keys)  # (layer, matrix) of every MM parameter
+
+    def member(m):
+        P = {k: v for k, v in params.items() if k != "blocks"}
+        P["blocks"] = []
+        for l, B in enumerate(params["blocks"]):
+            Bm = dict(B)
+            for name in (nm for (l2, nm) in names if l2 == l):
+                a, b = B[name].shape
+                A, Bf = O.lora_factors(bs, es.keys[(l, name)], cfg.rank, 0, [m], a, b)
+                Bm[name] = B[name] + A[0] @ Bf[0].T
+            P["blocks"].append(Bm)
+        O.rwkv_lm_forward(P, tk[m, :-1], H)
+
+    t0 = time.perf_counter()
+    with ThreadPoolExecutor(max_workers=threads) as ex:
+        list(ex.map(member, range(ns)))
+    t1 = time.perf_counter()
+    z = np.random.default_rng(0).standard_normal(ns).astype(np.float32)
+    for (l, name) in names:
+        a, b = params["blocks"][l][name].shape
+        O.lora_grad_f64(cfg.sigma, es.keys[(l, name)], cfg.rank, 0, z, a, b, nthreads=threads)
+    t2 = time.perf_counter()
+    return {"value": round(ns / (t2 - t0), 4), "unit": "member-evals/s", "cores": threads,
+            "kind": "port", "host_nproc": nproc, "cpu_model": model,
+            "sample": (f"oracle LM forward of {ns} of {cfg.n} members ({cfg.seq_len}-token sequences, "
+                       f"each on its materialised W + A_m B_m^T) in parallel on {threads} host "
+                       f"threads, plus the ES update of every matrix over those members; fwd "
+                       f"{t1 - t0:.2f}s, update {t2 - t1:.2f}s; extrapolated linearly in N"),
+            "seconds": round(t2 - t0, 2)}
 
 
 def main():
@@ -280,7 +339,8 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16 forward MFMA (fp32 accumulate), fp32 ES update",
+        "dtype": ("bf16 forward MFMA (fp32 accumulate); ES update as fp16 split-operand MFMA "
+                  "(hi*hi + hi*lo + lo*hi, fp32 accumulate; fp32-accurate)"),
         "data": "synthetic",
         "config": {
             "workload": ("C3: SNN-MLP 784-128-128-128-10, LIF decay 0.9 v_th 1.0, Poisson T=16, "
@@ -305,7 +365,7 @@ def main():
                      "algorithmic_flop_per_launch": fc1_flops},
     }
     if not args.no_cpu_baseline:
-        threads = min(os.cpu_count() or 1, 16)
+        threads, _, _ = host_cpu()
         out["cpu_baseline"] = cpu_baseline(cfg, pool, labels, idx, W, args.cpu_members, threads)
     print(json.dumps(out), flush=True)
 

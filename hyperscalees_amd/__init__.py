@@ -3,8 +3,12 @@
 Layout:
   csrc/        HIP kernels and the C ABI of libhses.so (include/hses.h)
   _lib.py      ctypes binding (no fallback: calls raise if the library is absent)
-  kernels.py   torch-tensor wrappers over the entry points
-  noiser.py    the EggRoll noiser API (mirrors hyperscalees-noiser)
+  kernels.py   torch-tensor wrappers over the entry points (the noiser and
+               kernel-launch surface of hyperscalees-noiser / hyperscalees-kernels)
   snn.py       SNN-MLP forward and ES step built on the kernels
+  rwkv.py      RWKV-7 TimeMixing / ChannelMixing compositions
+  rwkv_lm.py   RWKV-7 LM population forward and ES step
+  data.py      IDX/MNIST reader and the batch sampler
+  build.py     compiles libhses.so in-tree
 """
 __version__ = "0.1.0"

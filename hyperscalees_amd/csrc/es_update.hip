@@ -424,6 +424,13 @@ __global__ __launch_bounds__(256) void k_es_reduce(const float* __restrict__ wor
     }
 }
 
+// g[0, len) = 0 (a kernel rather than hipMemsetAsync, so that callers may
+// capture the entry point in a graph).
+__global__ __launch_bounds__(256) void k_zero(float* __restrict__ g, int64_t len) {
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (e < len) g[e] = 0.0f;
+}
+
 // Split count: ~1024 workgroups in total, at least max(8, 32 / r) pairs (one
 // k-chunk) per split, at most 512 splits.
 static int32_t es_splits(int32_t a, int32_t b, int32_t n_pairs, int32_t rank) {
@@ -490,32 +497,42 @@ extern "C" size_t hses_es_update_workspace(int32_t a, int32_t b, int32_t rank, i
     return align_up16((size_t)splits * a * b * sizeof(float)) + 16;  // partials, then {S, 1/S}
 }
 
-extern "C" int hses_es_update(const float* d_f, int32_t n, int32_t tid_lo, uint64_t key,
-                              int32_t rank, float sigma, int32_t epoch, int32_t noise_reuse,
-                              int32_t a, int32_t b, float scale, int32_t accumulate, float* d_grad,
-                              void* d_work, size_t work_bytes, void* stream) {
-    HSES_REQUIRE(n >= 0 && a >= 1 && b >= 1 && rank >= 0, "bad sizes");
-    HSES_REQUIRE(noise_reuse >= 0, "noise_reuse must be >= 0");
-    HSES_REQUIRE(tid_lo >= 0 && (int64_t)tid_lo + n - 1 <= INT32_MAX, "thread id range");
-    HSES_REQUIRE(d_grad, "grad is NULL");
+// The ES update into a caller's partials buffer: d_work of work_bytes, or,
+// with scratch_cap > 0, at most scratch_cap bytes of it (the split count is
+// lowered until the partials fit).
+static int es_update_impl(const float* d_f, int32_t n, int32_t tid_lo, uint64_t key, int32_t rank,
+                          float sigma, int32_t epoch, int32_t noise_reuse, int32_t a, int32_t b,
+                          float scale, int32_t accumulate, float* d_grad, void* d_work,
+                          size_t work_bytes, size_t scratch_cap, DeviceState* st,
+                          hipStream_t s) {
     UpdParams P{};
     int32_t pair_lo, n_pairs;
     pair_range(tid_lo, n, &pair_lo, &n_pairs);
     const bool empty = n == 0 || rank == 0 || sigma == 0.0f;
     const bool rows_k = use_rows_kernel(rank);
     P.splits = empty ? 1 : rows_k ? rows_splits(a, b, n_pairs) : es_splits(a, b, n_pairs, rank);
-    const size_t part_bytes = align_up16((size_t)P.splits * a * b * sizeof(float));
+    const size_t elems = (size_t)a * b;
+    if (scratch_cap) {
+        const size_t fit = (scratch_cap - 16) / (elems * sizeof(float));
+        if (fit < 1)
+            return set_error(HSES_ERR_INVALID_ARG, "a * b exceeds the fixed scratch of the "
+                                                   "allocation-free ES update");
+        P.splits = (int32_t)std::min<size_t>((size_t)P.splits, fit);
+    }
+    const size_t part_bytes = align_up16((size_t)P.splits * elems * sizeof(float));
     const size_t need = part_bytes + 16;
     if (!empty) {
         HSES_REQUIRE(d_f, "fitness is NULL");
         HSES_REQUIRE(d_work && work_bytes >= need, "workspace too small");
     }
-    DeviceState* st;
-    int rc = get_state(&st);
-    if (rc) return rc;
-    hipStream_t s = (hipStream_t)stream;
+    int rc;
     if (empty) {
-        if (!accumulate) HSES_CHECK_HIP(hipMemsetAsync(d_grad, 0, sizeof(float) * a * b, s));
+        if (!accumulate) {
+            const int64_t len = (int64_t)a * b;
+            hipLaunchKernelGGL(k_zero, dim3((uint32_t)((len + 255) / 256)), dim3(256), 0, s,
+                               d_grad, len);
+            HSES_CHECK_HIP(hipGetLastError());
+        }
         return HSES_OK;
     }
     P.f = d_f;
@@ -582,4 +599,36 @@ extern "C" int hses_es_update(const float* d_f, int32_t n, int32_t tid_lo, uint6
                        P.splits, len, scale, rows_k ? d_scale + 1 : nullptr, accumulate, d_grad);
     HSES_CHECK_HIP(hipGetLastError());
     return HSES_OK;
+}
+
+static int es_update_check(int32_t n, int32_t tid_lo, int32_t rank, int32_t noise_reuse, int32_t a,
+                           int32_t b, const float* d_grad) {
+    HSES_REQUIRE(n >= 0 && a >= 1 && b >= 1 && rank >= 0, "bad sizes");
+    HSES_REQUIRE(noise_reuse >= 0, "noise_reuse must be >= 0");
+    HSES_REQUIRE(tid_lo >= 0 && (int64_t)tid_lo + n - 1 <= INT32_MAX, "thread id range");
+    HSES_REQUIRE(d_grad, "grad is NULL");
+    return HSES_OK;
+}
+
+extern "C" int hses_es_update(const float* d_f, int32_t n, int32_t tid_lo, uint64_t key,
+                              int32_t rank, float sigma, int32_t epoch, int32_t noise_reuse,
+                              int32_t a, int32_t b, float scale, int32_t accumulate, float* d_grad,
+                              void* d_work, size_t work_bytes, void* stream) {
+    int rc = es_update_check(n, tid_lo, rank, noise_reuse, a, b, d_grad);
+    if (rc) return rc;
+    const bool empty = n == 0 || rank == 0 || sigma == 0.0f;
+    if (!empty) {
+        int32_t lo, cnt;
+        pair_range(tid_lo, n, &lo, &cnt);
+        const int32_t splits = use_rows_kernel(rank) ? rows_splits(a, b, cnt)
+                                                     : es_splits(a, b, cnt, rank);
+        HSES_REQUIRE(d_f, "fitness is NULL");
+        HSES_REQUIRE(d_work && work_bytes >= align_up16((size_t)splits * a * b * sizeof(float)) + 16,
+                     "workspace too small");
+    }
+    DeviceState* st;
+    rc = get_state(&st);
+    if (rc) return rc;
+    return es_update_impl(d_f, n, tid_lo, key, rank, sigma, epoch, noise_reuse, a, b, scale,
+                          accumulate, d_grad, d_work, work_bytes, 0, st, (hipStream_t)stream);
 }

@@ -112,7 +112,11 @@ extern "C" int hses_nonlora_noise(float base_sigma, uint64_t key, int32_t epoch,
     HSES_REQUIRE(noise_reuse >= 0, "noise_reuse must be >= 0");
     if (n == 0 || a == 0 || b == 0) return HSES_OK;
     HSES_REQUIRE(d_out, "output pointer is NULL");
-    // A dense (a, b) block is an A-only stream with row length b.
-    return launch_stream_rows(base_sigma, key, b, epoch, noise_reuse, tid_lo, d_tids, n, a, 0,
-                              d_out, nullptr, stream);
+    HSES_REQUIRE((int64_t)a * b < (1ll << 31), "a * b too large");
+    // A dense (a, b) block is an A-only stream of a * b normals, written as
+    // rows of Lc normals (the largest divisor of b the jump tables cover).
+    int32_t Lc = std::min<int32_t>(b, kJumpMaxL);
+    while (b % Lc) --Lc;
+    return launch_stream_rows(base_sigma, key, Lc, epoch, noise_reuse, tid_lo, d_tids, n,
+                              (int32_t)((int64_t)a * (b / Lc)), 0, d_out, nullptr, stream);
 }

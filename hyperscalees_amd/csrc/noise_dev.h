@@ -200,12 +200,16 @@ __device__ __forceinline__ uint64_t nib_apply(const uint64_t* tab, uint64_t x) {
 }
 
 // State before the first normal of row j of a stream with s0 = seed | 1:
-// T1[j / 16] (T0[j % 16] s0) with the nibble-form matrices of the jump table.
+// T2[j / 256] T1[(j / 16) % 16] T0[j % 16] s0 with the nibble-form matrices
+// of the row length's jump-table block (T2 is skipped for j < 256, where it
+// is the identity).
 __device__ __forceinline__ uint64_t row_start_state(uint64_t seed, int32_t j,
                                                      const uint64_t* jump) {
     const uint64_t s0 = seed | 1ull;
     const uint64_t s1 = nib_apply(jump + (size_t)(j & 15) * kJumpNib, s0);
-    return nib_apply(jump + (size_t)(16 + (j >> 4)) * kJumpNib, s1);
+    uint64_t s2 = nib_apply(jump + (size_t)(16 + ((j >> 4) & 15)) * kJumpNib, s1);
+    if (j >= 256) s2 = nib_apply(jump + (size_t)(32 + (j >> 8)) * kJumpNib, s2);
+    return s2;
 }
 
 // Seed of member `tid` for one layer key (eggroll.rs:60-65, noiser.rs:495-506).

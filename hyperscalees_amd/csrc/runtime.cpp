@@ -14,6 +14,7 @@ thread_local std::string g_err;
 std::mutex g_mu;
 std::vector<DeviceState*> g_states;  // indexed by device id
 HostBmTables* g_host_tables = nullptr;
+std::vector<uint64_t>* g_host_jump = nullptr;
 }  // namespace
 
 int set_error(int code, const std::string& msg) {
@@ -45,6 +46,12 @@ static int init_device_locked(int dev, DeviceState** out) {
         }
         g_host_tables = t;
     }
+    if (!g_host_jump) {
+        unsigned hc = std::thread::hardware_concurrency();
+        auto* j = new std::vector<uint64_t>();
+        build_jump_tables(j, (int)std::min<unsigned>(hc ? hc : 1, 16u));
+        g_host_jump = j;
+    }
     int cur = 0;
     HSES_CHECK_HIP(hipGetDevice(&cur));
     if (cur != dev) HSES_CHECK_HIP(hipSetDevice(dev));
@@ -63,6 +70,9 @@ static int init_device_locked(int dev, DeviceState** out) {
                              sizeof(uint32_t) * kBitmapAlloc, hipMemcpyHostToDevice));
     HSES_CHECK_HIP(hipMemcpy(st->d_cos_exc, g_host_tables->cos_exc.data(),
                              sizeof(uint32_t) * kBitmapAlloc, hipMemcpyHostToDevice));
+    HSES_CHECK_HIP(hipMalloc(&st->d_jump, sizeof(uint64_t) * g_host_jump->size()));
+    HSES_CHECK_HIP(hipMemcpy(st->d_jump, g_host_jump->data(), sizeof(uint64_t) * g_host_jump->size(),
+                             hipMemcpyHostToDevice));
     if (cur != dev) HSES_CHECK_HIP(hipSetDevice(cur));
     g_states[dev] = st;
     *out = st;
@@ -73,62 +83,71 @@ int get_state(DeviceState** out) {
     int dev = 0;
     HSES_CHECK_HIP(hipGetDevice(&dev));
     std::lock_guard<std::mutex> lk(g_mu);
-    return init_device_locked(dev, out);
+    if (dev < 0 || dev >= (int)g_states.size() || !g_states[dev]) {
+        char buf[96];
+        snprintf(buf, sizeof buf, "hses_init(%d) has not been called for the current device", dev);
+        return set_error(HSES_ERR_INVALID_ARG, buf);
+    }
+    *out = g_states[dev];
+    return HSES_OK;
 }
 
 int get_jump_table(DeviceState* st, int64_t row_len, int64_t rows, const uint64_t** out) {
-    std::lock_guard<std::mutex> lk(g_mu);
-    const int64_t need_n1 = (rows + kJumpG - 1) / kJumpG;
-    for (auto& j : st->jumps) {
-        if (j.row_len == row_len && j.n1 >= need_n1) {
-            *out = j.d_cols;
-            return HSES_OK;
-        }
+    if (row_len < 1 || row_len > kJumpMaxL || rows > kJumpMaxRows) {
+        char buf[160];
+        snprintf(buf, sizeof buf,
+                 "noise stream rows of %lld normals x %lld rows exceed the jump tables "
+                 "(row length <= %d, rows <= %lld)",
+                 (long long)row_len, (long long)rows, kJumpMaxL, (long long)kJumpMaxRows);
+        return set_error(HSES_ERR_UNSUPPORTED, buf);
     }
-    // Build (or rebuild larger) the table for this row length.
-    int32_t n1 = (int32_t)std::max<int64_t>(need_n1, 64);
-    std::vector<uint64_t> host((size_t)(kJumpG + n1) * kJumpNib);
-    // Matrix J in nibble form: entry 16 i + v = J (v << 4i) = XOR of the
-    // columns 4i + bit over the set bits of v.
-    auto put = [&](size_t m, const Gf2& J) {
-        uint64_t* e = &host[m * kJumpNib];
-        for (int i = 0; i < 16; ++i)
-            for (int v = 0; v < 16; ++v) {
-                uint64_t y = 0;
-                for (int bit = 0; bit < 4; ++bit)
-                    if ((v >> bit) & 1) y ^= J.c[4 * i + bit];
-                e[16 * i + v] = y;
-            }
-    };
-    const Gf2 M = gf2_step();
-    const Gf2 row = gf2_pow(M, 2ull * (uint64_t)row_len);  // one factor row = 2L steps
-    Gf2 acc = gf2_identity();
-    for (int j0 = 0; j0 < kJumpG; ++j0) {
-        put((size_t)j0, acc);
-        acc = gf2_mul(row, acc);
-    }
-    const Gf2 grp = acc;  // row^16
-    Gf2 g = gf2_identity();
-    for (int j1 = 0; j1 < n1; ++j1) {
-        put((size_t)(kJumpG + j1), g);
-        g = gf2_mul(grp, g);
-    }
-    uint64_t* d = nullptr;
-    HSES_CHECK_HIP(hipMalloc(&d, host.size() * sizeof(uint64_t)));
-    HSES_CHECK_HIP(hipMemcpy(d, host.data(), host.size() * sizeof(uint64_t), hipMemcpyHostToDevice));
-    bool replaced = false;
-    for (auto& j : st->jumps) {
-        if (j.row_len == row_len) {
-            // The old table may still be read by in-flight kernels; keep it alive.
-            j.n1 = n1;
-            j.d_cols = d;
-            replaced = true;
-            break;
-        }
-    }
-    if (!replaced) st->jumps.push_back({row_len, n1, d});
-    *out = d;
+    *out = st->d_jump + (size_t)(row_len - 1) * kJumpPerL * kJumpNib;
     return HSES_OK;
+}
+
+// Nibble form of J: entry 16 i + v = J (v << 4i), the XOR of the columns
+// 4i + bit over the set bits of v.
+static void put_nibbles(uint64_t* e, const Gf2& J) {
+    for (int i = 0; i < 16; ++i)
+        for (int v = 0; v < 16; ++v) {
+            uint64_t y = 0;
+            for (int bit = 0; bit < 4; ++bit)
+                if ((v >> bit) & 1) y ^= J.c[4 * i + bit];
+            e[16 * i + v] = y;
+        }
+}
+
+void build_jump_tables(std::vector<uint64_t>* out, int nthreads) {
+    out->assign((size_t)kJumpMaxL * kJumpPerL * kJumpNib, 0);
+    const Gf2 M = gf2_step();
+    auto one_length = [&](int L) {
+        uint64_t* blk = out->data() + (size_t)(L - 1) * kJumpPerL * kJumpNib;
+        const Gf2 R = gf2_pow(M, 2ull * (uint64_t)L);  // one stream row = 2L steps
+        Gf2 acc = gf2_identity();
+        for (int j0 = 0; j0 < 16; ++j0) {
+            put_nibbles(blk + (size_t)j0 * kJumpNib, acc);
+            acc = gf2_mul(R, acc);
+        }
+        const Gf2 R16 = acc;
+        acc = gf2_identity();
+        for (int j1 = 0; j1 < 16; ++j1) {
+            put_nibbles(blk + (size_t)(16 + j1) * kJumpNib, acc);
+            acc = gf2_mul(R16, acc);
+        }
+        const Gf2 R256 = acc;
+        acc = gf2_identity();
+        for (int j2 = 0; j2 < kJumpN2; ++j2) {
+            put_nibbles(blk + (size_t)(32 + j2) * kJumpNib, acc);
+            acc = gf2_mul(R256, acc);
+        }
+    };
+    const int nt = std::max(1, nthreads);
+    std::vector<std::thread> pool;
+    for (int t = 0; t < nt; ++t)
+        pool.emplace_back([&, t] {
+            for (int L = 1 + t; L <= kJumpMaxL; L += nt) one_length(L);
+        });
+    for (auto& th : pool) th.join();
 }
 
 }  // namespace hses

@@ -46,30 +46,34 @@ Gf2 gf2_step();                          // one xorshift64 step
 Gf2 gf2_mul(const Gf2& A, const Gf2& B);  // A * B
 Gf2 gf2_pow(const Gf2& M, uint64_t n);
 
-// Per-device state.
+// Row-start jump tables.  For every row length L in [1, kJumpMaxL] (normals
+// per stream row) one block of kJumpPerL matrices in nibble form (kJumpNib
+// entries each), with R = M^(2L) the xorshift64 advance over one row:
+// [0, 16): R^j0; [16, 32): R^(16 j1); [32, 32 + kJumpN2): R^(256 j2), so the
+// start of row j < kJumpMaxRows is three table products (row_start_state).
+// Built once on the host, uploaded at hses_init, immutable afterwards.
+constexpr int kJumpMaxL = 256;
+constexpr int kJumpN2 = 64;
+constexpr int kJumpPerL = 32 + kJumpN2;
+constexpr int64_t kJumpMaxRows = 256ll * kJumpN2;
+void build_jump_tables(std::vector<uint64_t>* out, int nthreads);
+
+// Per-device state, created by hses_init.
 struct DeviceState {
     int device = -1;
     BmTables* d_tables = nullptr;   // device copy of the small tables
     uint32_t* d_log_exc = nullptr;  // 2 MB bitmaps
     uint32_t* d_cos_exc = nullptr;
-    // Row-start jump tables, one per row length L (normals per row), each
-    // matrix in nibble form (kJumpNib entries):
-    // [0,16): M^(2L*j0); [16, 16+n1): M^(2L*16*j1).
-    struct Jump {
-        int64_t row_len = 0;
-        int32_t n1 = 0;
-        uint64_t* d_cols = nullptr;
-    };
-    std::vector<Jump> jumps;
+    uint64_t* d_jump = nullptr;     // kJumpMaxL blocks of kJumpPerL nibble matrices
     int num_cus = 0;
     size_t max_lds = 0;
 };
 
-// Returns the state of the current device, initialising it on first use.
+// The state of the current device.  Fails (nothing is allocated here) when
+// hses_init has not been called for it.
 int get_state(DeviceState** out);
-// Device pointer of the jump table for row length L covering `rows` rows.
+// Device pointer of the jump-table block for row length L, checked to cover
+// `rows` rows.  Pure lookup: no allocation, no copy.
 int get_jump_table(DeviceState* st, int64_t row_len, int64_t rows, const uint64_t** out);
-
-constexpr int kJumpG = 16;  // rows per first-level jump group
 
 }  // namespace hses

@@ -798,6 +798,11 @@ extern "C" int hses_tm_fused(const float* d_r, const float* d_w2o, const float* 
                  "NULL pointer");
     HSES_REQUIRE(!d_v2o || (d_v_first && d_v0), "NULL pointer (value branch)");
     HSES_REQUIRE(d_s_out != d_s_in, "s_out must not alias s_in");
+    // Other waves still read these planes while a wave stores its output rows
+    // (a bf16 out would also write 2-byte halves into fp32 rows).
+    HSES_REQUIRE(d_out != d_r && d_out != d_k && d_out != d_v && d_out != d_w2o &&
+                     d_out != d_a2o && d_out != d_v2o && d_out != d_v_first && d_out != d_g,
+                 "out must not alias r, w, k, v, a, the value-branch inputs or g");
     return launch_wkv7<true, true>(
         d_r, d_w2o, d_k, d_v, d_a2o, nullptr, d_s_in, d_new_starts, nseq, T, H, S, length,
         static_cast<float*>(d_out), d_s_out,

@@ -28,7 +28,7 @@ import torch
 
 from . import kernels as K
 from . import rwkv
-from ._lib import MATH_BF16, REWARD_LOGLIK, SGD
+from ._lib import ADAMW, MATH_BF16, REWARD_LOGLIK, SGD
 from . import _lib
 
 TM_MATRICES = ("receptance", "key", "value", "output", "w1", "w2", "v1", "v2", "a1", "a2",
@@ -64,6 +64,10 @@ class RwkvLmConfig:
     math: int = MATH_BF16
     solver: int = SGD
     lr: float = 1e-3
+    beta1: float = 0.9             # Adam / AdamW (Solver::adam, noiser.rs:101-108)
+    beta2: float = 0.999
+    eps: float = 1e-8
+    weight_decay: float = 1e-4     # AdamW only (Solver::adamw, noiser.rs:111-119)
     init_std: float = 0.02
     widths: tuple = field(default=None)
 
@@ -126,8 +130,12 @@ class RwkvLmEs:
         self.keys = {ln: ((i + 1 + key_seed) * KEY_MUL) % 2**64
                      for i, ln in enumerate(mm_names(cfg.n_layer))}
         self.grads = {ln: torch.empty_like(self.blocks[ln[0]][ln[1]]) for ln in self.keys}
-        self.m = {ln: None for ln in self.keys}
-        self.v = {ln: None for ln in self.keys}
+        # Adam / AdamW moments m = v = 0 per parameter (Solver::init_state, noiser.rs:126-149)
+        adam = cfg.solver != SGD
+        self.m = {ln: torch.zeros_like(self.blocks[ln[0]][ln[1]]) if adam else None
+                  for ln in self.keys}
+        self.v = {ln: torch.zeros_like(self.blocks[ln[0]][ln[1]]) if adam else None
+                  for ln in self.keys}
         self.step_t = 0
         self.streams = None
         S, C = cfg.head_size, cfg.d_model
@@ -230,7 +238,9 @@ class RwkvLmEs:
                 K.es_update(z, 0, key, c.rank, c.sigma, epoch, c.noise_reuse, a, b, scale,
                             out=self.grads[(l, name)])
                 K.solver_step(c.solver, c.lr, W, self.grads[(l, name)], self.m[(l, name)],
-                              self.v[(l, name)], step_t=self.step_t)
+                              self.v[(l, name)], step_t=self.step_t, beta1=c.beta1,
+                              beta2=c.beta2, eps=c.eps,
+                              wd=c.weight_decay if c.solver == ADAMW else 0.0)
         for side in self.streams:
             main.wait_stream(side)
         return z

@@ -66,8 +66,12 @@ typedef enum {
 
 /* ---- runtime ---------------------------------------------------------- */
 
-/* Initialise device `device` (builds the Box-Muller correction tables and
- * uploads them).  Called implicitly by the first launch on a device. */
+/* Initialise device `device`: builds (once per process) the Box-Muller
+ * correction tables and the row-start jump tables of every row length
+ * 1..256, and uploads them.  Must be called for a device before any other
+ * entry point launches on it (those return HSES_ERR_INVALID_ARG otherwise);
+ * it is the only call that allocates device memory, so no launch entry point
+ * allocates or copies behind the caller's stream. */
 int hses_init(int device);
 /* Copies the last error message of this thread into buf (NUL-terminated). */
 int hses_last_error(char *buf, size_t len);

@@ -543,6 +543,8 @@ float or_clip_global_norm_scale(const float *const *grads, const int64_t *lens, 
  * (the JAX model is depth-generic: llm_experiments/snn_mnist_train_multi_gpu.py:49-98),
  * the batched LoRA forward snn.rs:665-685 per member, the rate readout and the
  * log-likelihood fitness snn_mnist.rs:180-201 averaged over the member's rows. */
+/* probs / labels are member m's own R rows; m fixes its factors and the global
+ * (row, col) index of its Poisson streams. */
 static void snn_member(const or_snn_cfg *cfg, const float *const *W, const uint64_t *keys,
                        const float *probs, const int32_t *labels, int32_t m, float *fit_out) {
     const int32_t L = cfg->n_layers, T = cfg->T, R = cfg->rows, r = cfg->rank;
@@ -560,7 +562,7 @@ static void snn_member(const or_snn_cfg *cfg, const float *const *W, const uint6
         for (int32_t c = 0; c < in0; ++c) {
             const int64_t idx = ((int64_t)m * R + s) * in0 + c;
             uint32_t xs = 1000000007u * (uint32_t)idx + mix + 0x9E3779B9u;
-            const float pv = probs[idx];
+            const float pv = probs[(int64_t)s * in0 + c];
             for (int32_t t = 0; t < T; ++t) {
                 xs ^= xs << 13;
                 xs ^= xs >> 17;
@@ -581,7 +583,7 @@ static void snn_member(const or_snn_cfg *cfg, const float *const *W, const uint6
             or_mean_rate(x, T, R, b, rate);
             or_do_mm(rate, R, W[l], a, b, A, B, r, y);
             float *ll = (float *)malloc(sizeof(float) * (size_t)R + 4);
-            or_loglik(y, R, a, labels + (int64_t)m * R, ll);
+            or_loglik(y, R, a, labels, ll);
             double s = 0.0;
             for (int32_t i = 0; i < R; ++i) s += ll[i];
             *fit_out = (float)(s / R);
@@ -604,8 +606,15 @@ void or_snn_forward_members(const or_snn_cfg *cfg, const float *const *W, const 
 #ifdef _OPENMP
 #pragma omp parallel for schedule(dynamic, 1) num_threads(nthreads > 0 ? nthreads : 1)
 #endif
-    for (int32_t m = m_lo; m < m_hi; ++m) snn_member(cfg, W, keys, probs, labels, m, &fit[m - m_lo]);
+    for (int32_t m = m_lo; m < m_hi; ++m)
+        snn_member(cfg, W, keys, probs + (int64_t)m * cfg->rows * cfg->dims[0],
+                   labels + (int64_t)m * cfg->rows, m, &fit[m - m_lo]);
     (void)nthreads;
+}
+
+void or_snn_forward_member(const or_snn_cfg *cfg, const float *const *W, const uint64_t *keys,
+                           const float *probs_m, const int32_t *labels_m, int32_t m, float *fit) {
+    snn_member(cfg, W, keys, probs_m, labels_m, m, fit);
 }
 
 void or_lora_grad_f64(float sigma, uint64_t key, int32_t rank, int32_t noise_reuse,

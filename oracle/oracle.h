@@ -147,6 +147,10 @@ typedef struct {
 void or_snn_forward_members(const or_snn_cfg *cfg, const float *const *W, const uint64_t *keys,
                             const float *probs, const int32_t *labels, int32_t m_lo,
                             int32_t m_hi, int32_t nthreads, float *fit);
+/* One member m from its own R rows of probabilities and labels (same result
+ * as or_snn_forward_members at member m). */
+void or_snn_forward_member(const or_snn_cfg *cfg, const float *const *W, const uint64_t *keys,
+                           const float *probs_m, const int32_t *labels_m, int32_t m, float *fit);
 /* Double-accumulated ES gradient of one layer for members [0,n): -sqrt(n)*(1/n)*sum f A B^T
  * computed from z-scored fitness.  nthreads>1 parallelises over output rows. */
 void or_lora_grad_f64(float sigma, uint64_t key, int32_t rank, int32_t noise_reuse,

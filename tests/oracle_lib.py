@@ -118,6 +118,9 @@ def load():
                                           f32p]),
         "or_lora_grad_f64": (None, [c_f32, c_u64, c_i32, c_i32, c_i32, f32p, c_i32, c_i32, c_i32,
                                     c_i32, f32p]),
+        "or_snn_forward_member": (None, [ctypes.POINTER(SnnCfg), ctypes.c_void_p,
+                                         ctypes.c_void_p, f32p, i32p, c_i32, f32p]),
+        "or_clip_global_norm_scale": (c_f32, [ctypes.c_void_p, ctypes.c_void_p, c_i32, c_f32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -294,3 +297,11 @@ def rwkv_lm_forward(P, tokens, H, state=None):
     logits = np.zeros((tokens.size, V), np.float32)
     load().or_rwkv_lm_forward(ctypes.byref(lm), tokens, tokens.size, st, logits)
     return logits, st
+
+
+def clip_scale(grads, max_norm):
+    """or_clip_global_norm_scale over a list of float32 arrays."""
+    gs = [np.ascontiguousarray(g, np.float32) for g in grads]
+    ptrs = (ctypes.c_void_p * max(1, len(gs)))(*[g.ctypes.data for g in gs])
+    lens = np.array([g.size for g in gs] or [0], np.int64)
+    return float(load().or_clip_global_norm_scale(ptrs, lens.ctypes.data, len(gs), max_norm))

@@ -101,6 +101,12 @@ def test_validation_rejects_bad_arguments_without_a_gpu():
     _expect_invalid("hses_add_layer_norm", ctypes.c_void_p(16), ctypes.c_void_p(32), 4, 8,
                     ctypes.c_void_p(16), ctypes.c_void_p(16), 1e-5, ctypes.c_void_p(16), NULL)
     _expect_invalid("hses_rwkv_act", ctypes.c_void_p(16), 4, 5, NULL)
+    # hses_tm_fused: the output may not alias an input plane that other waves read
+    P = [ctypes.c_void_p(4096 * (i + 1)) for i in range(24)]
+    for alias in (0, 1, 2, 3, 4, 19):  # r, w, k, v, a, g
+        _expect_invalid("hses_tm_fused", P[0], P[1], P[2], P[3], P[4], NULL, NULL, P[7], P[8],
+                        NULL, P[10], P[11], P[12], NULL, 2, 8, 2, 64, 8, P[19], P[20], P[21],
+                        64e-5, P[22], P[alias], 1, P[23], NULL)
 
 
 def test_empty_inputs_are_no_ops_without_a_gpu():

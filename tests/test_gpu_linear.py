@@ -274,6 +274,9 @@ def test_perturbed_linear_t_clean(hses_gpu):
     (5, 100, 1, 130, 96, 1, 0, FMT_F32),       # members straddle tiles (three per tile)
     (4, 32, 2, 256, 200, 4, 2, FMT_F32),       # time-major planes, four members per tile
     (3, 64, 1, 192, 300, 2, 0, FMT_BITS),      # bit-packed input, K not a multiple of 64
+    (3, 128, 1, 100, 512, 1, 0, FMT_F32),      # output width in (64, 128]: 128-column passes
+    (2, 128, 1, 100, 256, 1, 1, FMT_BF16),
+    (4, 64, 1, 64, 200, 2, 0, FMT_BF16),       # exactly 64 columns: 64-column passes
 ])
 def test_wide_kernel(hses_gpu, n, rpm, T, a, b, r, tid_lo, fmt):
     rng = np.random.default_rng(n * 7 + a + b + r)
@@ -290,7 +293,8 @@ def test_wide_kernel(hses_gpu, n, rpm, T, a, b, r, tid_lo, fmt):
     assert_close(y, ref_forward(x3, W, A, B, rpm), 2e-2)
 
 
-@pytest.mark.parametrize("a,b,act", [(512, 32, 1), (96, 512, 2), (512, 512, 3), (256, 64, 0)])
+@pytest.mark.parametrize("a,b,act", [(512, 32, 1), (96, 512, 2), (512, 512, 3), (256, 64, 0),
+                                     (512, 96, 2), (512, 120, 0)])  # C5 g1: width 96
 def test_wide_kernel_transposed_and_activations(hses_gpu, a, b, act):
     # do_Tmm on a parameter W (a, b): y = act(x W + (x A_m) B_m^T), bf16 math
     from hyperscalees_amd._lib import ACT_RELU_SQ, ACT_SIGMOID, ACT_TANH

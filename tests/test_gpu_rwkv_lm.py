@@ -10,7 +10,7 @@ import pytest
 import torch
 
 from hyperscalees_amd import rwkv_lm
-from hyperscalees_amd._lib import MATH_BF16, MATH_F32, SGD
+from hyperscalees_amd._lib import ADAM, ADAMW, MATH_BF16, MATH_F32, SGD
 from tests import oracle_lib as O
 
 pytestmark = pytest.mark.gpu
@@ -19,7 +19,7 @@ SMALL = dict(n_layer=2, d_model=64, head_size=32, vocab=50, ffn_mult=4, seq_len=
              sigma=0.05, math=MATH_F32, solver=SGD, lr=0.1, init_std=0.2, widths=(16, 8, 16, 32))
 
 
-def member_params(params, es, m):
+def member_params(params, es, m, epoch=0):
     """The oracle's parameter dict of member m: W + A_m B_m^T for every MM parameter."""
     c = es.cfg
     bs = O.load().or_base_sigma(c.sigma, c.rank)
@@ -29,7 +29,8 @@ def member_params(params, es, m):
         Bm = dict(B)
         for name in rwkv_lm.TM_MATRICES + rwkv_lm.FFN_MATRICES:
             a, b = B[name].shape
-            A, Bf = O.lora_factors(bs, es.keys[(l, name)], c.rank, 0, [m], a, b)
+            A, Bf = O.lora_factors(bs, es.keys[(l, name)], c.rank, epoch, [m], a, b,
+                                   noise_reuse=c.noise_reuse)
             Bm[name] = (B[name].astype(np.float64) + A[0].astype(np.float64) @ Bf[0].T.astype(np.float64)).astype(np.float32)
         P["blocks"].append(Bm)
     return P
@@ -107,6 +108,35 @@ def test_lm_es_step_gradients_and_sgd(hses_gpu):
     np.testing.assert_array_equal(es.blocks[1]["x_r"].cpu().numpy(), vec_before)
 
 
+@pytest.mark.parametrize("solver", [ADAM, ADAMW])
+def test_lm_es_step_adam(hses_gpu, solver):
+    # Adam / AdamW on every MM parameter: the moments start at zero and the
+    # step follows Solver::update (noiser.rs:166-214) on the step's own
+    # gradient; a second step checks that the moments carry over.
+    cfg = rwkv_lm.RwkvLmConfig(**dict(SMALL, n=6, solver=solver, lr=0.01))
+    params = rwkv_lm.init_params(cfg, seed=9)
+    es = rwkv_lm.RwkvLmEs(cfg, params)
+    rng = np.random.default_rng(10)
+    tok = torch.from_numpy(rng.integers(0, cfg.vocab, (cfg.n, cfg.seq_len + 1)).astype(np.int32)).cuda()
+    p = {ln: es.blocks[ln[0]][ln[1]].cpu().numpy().copy() for ln in es.keys}
+    m = {ln: np.zeros_like(v) for ln, v in p.items()}
+    v = {ln: np.zeros_like(x) for ln, x in p.items()}
+    wd = cfg.weight_decay if solver == ADAMW else 0.0
+    for t in (1, 2):
+        es.step(tok, epoch=t)
+        torch.cuda.synchronize()
+        for ln in es.keys:
+            g = es.grads[ln].cpu().numpy()
+            out = np.zeros_like(p[ln])
+            O.load().or_solver_step(solver, cfg.lr, cfg.beta1, cfg.beta2, cfg.eps, wd, t,
+                                    p[ln].ravel(), g.ravel(), m[ln].reshape(-1), v[ln].reshape(-1),
+                                    p[ln].size, out.reshape(-1))
+            got = es.blocks[ln[0]][ln[1]].cpu().numpy()
+            # a few ulps of the lr-sized Adam step (p + step may cancel to near zero)
+            np.testing.assert_allclose(got, out, rtol=1e-6, atol=1e-6 * cfg.lr, err_msg=str(ln))
+            p[ln] = got.copy()
+
+
 def test_embed_layer_norm_out_of_range_token_gives_nan(hses_gpu):
     from hyperscalees_amd import _lib, kernels as K
     C, V = 64, 10
@@ -144,3 +174,23 @@ def test_lm_full_width_state_carry_is_exact(hses_gpu):
     assert torch.equal(full.view(cfg.n, 128, V), joined)
     assert torch.equal(st_full, st_b)
     assert torch.isfinite(full).all()
+
+
+def test_lm_full_size_members_match_oracle(hses_gpu):
+    # C5 at its full size (N = 2048 members, 4 layers, d = 512, 128 tokens,
+    # bf16 products): sampled members' logits against the oracle LM on their
+    # materialised parameters, at the bf16 bar.
+    cfg = rwkv_lm.RwkvLmConfig()
+    params = rwkv_lm.init_params(cfg, seed=13)
+    es = rwkv_lm.RwkvLmEs(cfg, params)
+    H = cfg.d_model // cfg.head_size
+    rng = np.random.default_rng(14)
+    T = cfg.seq_len
+    tok = rng.integers(0, cfg.vocab, (cfg.n, T)).astype(np.int32)
+    lg = es.logits(torch.from_numpy(tok).cuda(), epoch=2)
+    torch.cuda.synchronize()
+    for m in (0, 1, 1023, 2047):
+        got = lg[m * T:(m + 1) * T].cpu().numpy()
+        Pm = member_params(params, es, m, epoch=2)
+        ref, _ = O.rwkv_lm_forward(Pm, tok[m], H)
+        close(got, ref, 2e-2)

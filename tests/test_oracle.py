@@ -467,3 +467,20 @@ def test_adam_first_step_closed_form(oracle):
                           np.zeros(3, np.float32), 3, out_w)
     # AdamW adds +wd*p with no lr factor (noiser.rs:208-212)
     np.testing.assert_allclose(out_w - out, 1e-4 * p, rtol=1e-3)
+
+
+def test_clip_global_norm_hand_computed(oracle):
+    # noiser.rs:231-244 (optax clip_by_global_norm): scale = max_norm / ||g||
+    # over all tensors together when the norm exceeds max_norm, else 1.
+    assert O.clip_scale([np.array([3.0, 4.0])], 1.0) == pytest.approx(0.2, rel=1e-7)
+    # the norm is global: [3] and [4] in separate tensors give the same 5
+    assert O.clip_scale([np.array([3.0]), np.array([[4.0]])], 1.0) == pytest.approx(0.2, rel=1e-7)
+    assert O.clip_scale([np.array([3.0, 4.0])], 10.0) == 1.0      # below the threshold
+    assert O.clip_scale([np.array([3.0, 4.0])], 5.0) == 1.0       # equal: strict '>'
+    assert O.clip_scale([np.zeros(7)], 0.0) == 1.0                # all zero: no division
+    assert O.clip_scale([np.zeros(3), np.zeros(2)], 1.0) == 1.0
+    # squares, not absolute values: ||[1, -1, 1, -1]|| = 2
+    assert O.clip_scale([np.array([1.0, -1.0, 1.0, -1.0])], 1.0) == pytest.approx(0.5, rel=1e-7)
+    g = np.random.default_rng(5).standard_normal(1000)
+    assert O.clip_scale([g[:300], g[300:]], 1.0) == pytest.approx(1.0 / np.linalg.norm(g),
+                                                                   rel=1e-6)
