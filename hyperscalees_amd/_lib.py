@@ -55,6 +55,8 @@ PROTOTYPES = {
     "hses_es_update_workspace": (c_size, [c_i32, c_i32, c_i32, c_i32]),
     "hses_es_update": (ctypes.c_int, [c_vp, c_i32, c_i32, c_u64, c_i32, c_f32, c_i32, c_i32,
                                       c_i32, c_i32, c_f32, c_i32, c_vp, c_vp, c_size, c_vp]),
+    "hses_es_update_noalloc": (ctypes.c_int, [c_vp, c_i32, c_i32, c_u64, c_i32, c_f32, c_i32,
+                                              c_i32, c_i32, c_i32, c_f32, c_i32, c_vp, c_vp]),
     "hses_member_loglik": (ctypes.c_int, [c_vp, c_i32, c_vp, c_i32, c_i32, c_vp, c_vp]),
     "hses_member_fitness": (ctypes.c_int, [c_vp, c_i32, c_vp, c_i32, c_i32, c_i32, c_vp, c_vp,
                                            c_vp]),

@@ -632,3 +632,44 @@ extern "C" int hses_es_update(const float* d_f, int32_t n, int32_t tid_lo, uint6
     return es_update_impl(d_f, n, tid_lo, key, rank, sigma, epoch, noise_reuse, a, b, scale,
                           accumulate, d_grad, d_work, work_bytes, 0, st, (hipStream_t)stream);
 }
+
+// ---- the allocation-free variant ---------------------------------------------
+//
+// The split-K partials and the operand scale live in this file-scope device
+// array instead of a caller workspace.  Each device holds its own copy for
+// the life of the process; its address on a device is looked up once, at
+// hses_init, and kept in that device's state (the array's name in host code is
+// not a device address).  Every call on a device shares the array, so calls
+// that overlap on one device (other streams, other threads) race.  Nothing in
+// it has to start at zero: every split stores its whole partial tile and the
+// scale kernel stores both words it owns.
+namespace hses {
+
+static __device__ __align__(256) unsigned char scratch[kEsScratchBytes];
+
+int es_scratch_setup(DeviceState* st) {
+    void* ptr = nullptr;
+    HSES_CHECK_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    st->es_scratch = ptr;
+    return HSES_OK;
+}
+
+}  // namespace hses
+
+extern "C" int hses_es_update_noalloc(const float* d_f, int32_t n, int32_t tid_lo, uint64_t key,
+                                      int32_t rank, float sigma, int32_t epoch,
+                                      int32_t noise_reuse, int32_t a, int32_t b, float scale,
+                                      int32_t accumulate, float* d_grad, void* stream) {
+    int rc = es_update_check(n, tid_lo, rank, noise_reuse, a, b, d_grad);
+    if (rc) return rc;
+    HSES_REQUIRE((size_t)a * b * sizeof(float) + 16 <= kEsScratchBytes,
+                 "a * b exceeds the fixed scratch of the allocation-free ES update "
+                 "(at most (kEsScratchBytes - 16) / 4 elements)");
+    DeviceState* st;
+    rc = get_state(&st);
+    if (rc) return rc;
+    HSES_REQUIRE(st->es_scratch, "scratch address of this device is missing");
+    return es_update_impl(d_f, n, tid_lo, key, rank, sigma, epoch, noise_reuse, a, b, scale,
+                          accumulate, d_grad, st->es_scratch, kEsScratchBytes, kEsScratchBytes, st,
+                          (hipStream_t)stream);
+}

@@ -73,6 +73,10 @@ static int init_device_locked(int dev, DeviceState** out) {
     HSES_CHECK_HIP(hipMalloc(&st->d_jump, sizeof(uint64_t) * g_host_jump->size()));
     HSES_CHECK_HIP(hipMemcpy(st->d_jump, g_host_jump->data(), sizeof(uint64_t) * g_host_jump->size(),
                              hipMemcpyHostToDevice));
+    {
+        const int src = es_scratch_setup(st);  // with `dev` current
+        if (src) return src;
+    }
     if (cur != dev) HSES_CHECK_HIP(hipSetDevice(cur));
     g_states[dev] = st;
     *out = st;

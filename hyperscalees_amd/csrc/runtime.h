@@ -65,9 +65,16 @@ struct DeviceState {
     uint32_t* d_log_exc = nullptr;  // 2 MB bitmaps
     uint32_t* d_cos_exc = nullptr;
     uint64_t* d_jump = nullptr;     // kJumpMaxL blocks of kJumpPerL nibble matrices
+    void* es_scratch = nullptr;     // this device's address of es_update.hip's scratch array
     int num_cus = 0;
     size_t max_lds = 0;
 };
+
+// Size of the file-scope scratch array of the allocation-free ES update
+// (es_update.hip), and its per-device address lookup, run by hses_init with
+// the device current.
+constexpr size_t kEsScratchBytes = 32u << 20;
+int es_scratch_setup(DeviceState* st);
 
 // The state of the current device.  Fails (nothing is allocated here) when
 // hses_init has not been called for it.

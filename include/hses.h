@@ -236,6 +236,17 @@ int hses_es_update(const float *d_f, int32_t n, int32_t tid_lo, uint64_t key, in
                    float sigma, int32_t epoch, int32_t noise_reuse, int32_t a, int32_t b,
                    float scale, int32_t accumulate, float *d_grad, void *d_work,
                    size_t work_bytes, void *stream);
+/* No counterpart in the reference: hses_es_update for callers that cannot
+ * allocate (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments and result (to fp32 rounding: the split count
+ * may be lower) without the workspace: the split-K partials live in a fixed
+ * 32 MiB device array of the library, one per GPU, kept until the process
+ * ends.  Rejects a * b > (32 MiB - 16) / 4 elements with HSES_ERR_INVALID_ARG.
+ * Calls share the array, so calls that overlap on one GPU race. */
+int hses_es_update_noalloc(const float *d_f, int32_t n, int32_t tid_lo, uint64_t key,
+                           int32_t rank, float sigma, int32_t epoch, int32_t noise_reuse,
+                           int32_t a, int32_t b, float scale, int32_t accumulate, float *d_grad,
+                           void *stream);
 
 /* ---- fitness, z-score, solver ----------------------------------------- */
 

@@ -101,6 +101,9 @@ def test_validation_rejects_bad_arguments_without_a_gpu():
     _expect_invalid("hses_add_layer_norm", ctypes.c_void_p(16), ctypes.c_void_p(32), 4, 8,
                     ctypes.c_void_p(16), ctypes.c_void_p(16), 1e-5, ctypes.c_void_p(16), NULL)
     _expect_invalid("hses_rwkv_act", ctypes.c_void_p(16), 4, 5, NULL)
+    # the allocation-free ES update: one a x b partial must fit its fixed 32 MiB scratch
+    _expect_invalid("hses_es_update_noalloc", ctypes.c_void_p(16), 8, 0, 1, 4, 0.02, 0, 0,
+                    2048, 4096, 1.0, 0, ctypes.c_void_p(16), NULL)
     # hses_tm_fused: the output may not alias an input plane that other waves read
     P = [ctypes.c_void_p(4096 * (i + 1)) for i in range(24)]
     for alias in (0, 1, 2, 3, 4, 19):  # r, w, k, v, a, g
