@@ -75,7 +75,7 @@ def host_cpu():
     return threads, nproc, model
 
 
-def cpu_baseline(cfg, pool, labels, idx, W, members, threads):
+def cpu_baseline(cfg, pool, labels, idx, W, members, threads, label="C3"):
     """The oracle (C restatement of the reference CPU path) on `members` members,
     forward + their share of the ES update, extrapolated linearly in N when
     members < N."""
@@ -110,7 +110,7 @@ def cpu_baseline(cfg, pool, labels, idx, W, members, threads):
              f"{members} of {cfg.n} members, extrapolated linearly in N")
     return {"value": 1.0 / per_member, "unit": "member-evals/s", "cores": threads,
             "kind": "port", "host_nproc": nproc, "cpu_model": model,
-            "sample": (f"C3 ES step (forward + ES update) of {scope}, oracle (C, -O3, OpenMP) on "
+            "sample": (f"{label} ES step (forward + ES update) of {scope}, oracle (C, -O3, OpenMP) on "
                        f"{threads} host threads; fwd {t1 - t0:.2f}s, update {t2 - t1:.2f}s"),
             "seconds": round(t2 - t0, 2)}
 
@@ -242,6 +242,167 @@ def cpu_baseline_c5(cfg, params, es, tok, members):
             "seconds": round(t2 - t0, 2)}
 
 
+def _events(n):
+    import torch
+    return [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+
+
+def _time_launch(fn, reps=5):
+    """Median duration (ms) of fn's launches, HIP events on the launch stream."""
+    import torch
+    ts = []
+    for _ in range(reps):
+        e0, e1 = _events(2)
+        e0.record()
+        fn()
+        e1.record()
+        torch.cuda.synchronize()
+        ts.append(e0.elapsed_time(e1))
+    return float(np.median(ts))
+
+
+def _timed_steps(step, steps, warmup):
+    import torch
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s_ in range(steps):
+        step(s_)
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1000.0 / steps
+
+
+def bench_c1(args):
+    """SNN-MLP 784-128-128-128-10, T=8, N=256, r=4, sigma 0.02, fp32; every
+    member evaluates the same 64 synthetic inputs.  One step = the full ES step."""
+    import torch
+    from hyperscalees_amd import kernels as K
+    from hyperscalees_amd import snn
+    from hyperscalees_amd._lib import MATH_F32, SGD
+    cfg = snn.SnnConfig(T=8, rows=64, n=256, rank=4, sigma=0.02, math=MATH_F32, solver=SGD,
+                        lr=0.05, poisson_seed=(1, 2, 3, 4))
+    pool, labels = snn.synthetic_pool(64, cfg.dims[0], cfg.dims[-1], seed=0)
+    idx = np.tile(np.arange(64, dtype=np.int32), cfg.n)  # the same 64 inputs for every member
+    W = snn.init_weights(cfg.dims, 0, gain=snn.ACTIVE_GAIN)
+    K.init(0)
+    es = snn.SnnEs(cfg, W, pool, labels, idx)
+    ms = _timed_steps(lambda i: es.step(epoch=i), args.steps, args.warmup)
+    # dominant kernel: fc1's perturbed forward (k_linear_small, fp32 MFMA)
+    fc1 = lambda: K.perturbed_linear(es.spk[0], es.W[0], cfg.keys[0], cfg.rank, cfg.sigma, 0,
+                                     cfg.noise_reuse, 0, cfg.n, cfg.rows, x_fmt=K.FMT_BITS,
+                                     n_time=cfg.T, math=cfg.math, out=es.cur)
+    fc1_ms = _time_launch(fc1)
+    fl = layer_flops(cfg, 0)
+    achieved = fl / (fc1_ms * 1e-3) / 1e12
+    out = {
+        "metric": "perturbed member-evals/sec, SNN-MLP N=256 r=4 T=8 fp32 (configs[0])",
+        "value": round(cfg.n / (ms * 1e-3), 1), "unit": "member-evals/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp32 (fp32 MFMA forward and ES update)", "data": "synthetic",
+        "config": {"workload": ("C1: SNN-MLP 784-128-128-128-10, LIF decay 0.9 v_th 1.0, Poisson "
+                                "T=8, N=256, r=4, sigma 0.02, the same 64 inputs (70% zeros) for "
+                                "every member, full ES step (forward + fitness + z-score + ES "
+                                "update + SGD)"),
+                   "population": cfg.n, "rank": cfg.rank, "T": cfg.T, "parallelism": "single GPU"},
+        "fwd_flop_per_step": sum(layer_flops(cfg, l) for l in range(len(cfg.dims) - 1)),
+        "roofline": {"kernel": "k_linear_small<F32 math, BITS x> (fc1, 8 x 16384 rows, 784 -> 128)",
+                     "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP32_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_TFLOPS, 4),
+                     "traffic": None, "launch_ms": round(fc1_ms, 4),
+                     "algorithmic_flop_per_launch": fl},
+    }
+    if not args.no_cpu_baseline:
+        threads, _, _ = host_cpu()
+        out["cpu_baseline"] = cpu_baseline(cfg, pool, labels, idx, W, cfg.n, threads, label="C1")
+    print(json.dumps(out), flush=True)
+
+
+def bench_c2(args):
+    """one EggRoll layer W 1024x1024 fp32, N=4096, r=1, 16 rows per member,
+    x ~ N(0,1); one step = the perturbed forward, then the ES update on z-scored
+    N(0,1) fitness (noise from seed 0: the layer key of layer 0)."""
+    import torch
+    from hyperscalees_amd import kernels as K
+    from hyperscalees_amd._lib import MATH_F32
+    n, rpm, a, b, r, sigma = 4096, 16, 1024, 1024, 1, 0.02
+    key = 0x9E3779B97F4A7C15
+    K.init(0)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0)
+    W = (torch.randn((a, b), device="cuda", generator=g) / 32.0).contiguous()
+    x = torch.randn((n * rpm, b), device="cuda", generator=g)
+    fit = torch.randn(n, device="cuda", generator=g)
+    y = torch.empty((n * rpm, a), device="cuda")
+    grad = torch.empty((a, b), device="cuda")
+    scale = np.float32(-math.sqrt(n) / n)
+
+    def step(i):
+        K.perturbed_linear(x, W, key, r, sigma, i, 0, 0, n, rpm, math=MATH_F32, out=y)
+        z, _ = K.convert_fitnesses(fit)
+        K.es_update(z, 0, key, r, sigma, i, 0, a, b, scale, out=grad)
+
+    ms = _timed_steps(step, args.steps, args.warmup)
+    fwd_ms = _time_launch(lambda: K.perturbed_linear(x, W, key, r, sigma, 0, 0, 0, n, rpm,
+                                                     math=MATH_F32, out=y))
+    z, _ = K.convert_fitnesses(fit)
+    upd_ms = _time_launch(lambda: K.es_update(z, 0, key, r, sigma, 0, 0, a, b, scale, out=grad))
+    M = n * rpm
+    fwd_fl = 2 * M * b * a + 2 * M * b * r + 2 * M * r * a
+    upd_fl = 2 * a * b * n * r
+    achieved = fwd_fl / (fwd_ms * 1e-3) / 1e12
+    out = {
+        "metric": "perturbed member-evals/sec, EggRoll layer 1024x1024 N=4096 r=1 fp32 (configs[1])",
+        "value": round(n / (ms * 1e-3), 1), "unit": "member-evals/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp32 (fp32 MFMA forward and ES update)", "data": "synthetic",
+        "config": {"workload": ("C2: W 1024x1024 ~ N(0, 1/32^2), N=4096, r=1, 16 rows per member, "
+                                "x ~ N(0,1); perturbed forward + z-score of N(0,1) fitness + ES "
+                                "update"),
+                   "population": n, "rank": r, "parallelism": "single GPU"},
+        "phase_ms": {"forward": round(fwd_ms, 4), "es_update": round(upd_ms, 4)},
+        "es_update_tflops": round(upd_fl / (upd_ms * 1e-3) / 1e12, 2),
+        "roofline": {"kernel": "k_linear_small<F32 math, F32 x> (65536 x 1024 -> 1024, r=1)",
+                     "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP32_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_TFLOPS, 4),
+                     "traffic": None, "launch_ms": round(fwd_ms, 4),
+                     "algorithmic_flop_per_launch": fwd_fl},
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline_c2(W.cpu().numpy(), x.cpu().numpy(),
+                                              z.cpu().numpy(), n, rpm, r, sigma, key)
+    print(json.dumps(out), flush=True)
+
+
+def cpu_baseline_c2(W, x, z, n, rpm, r, sigma, key):
+    """The oracle's do_mm for every member (its factors from the noiser stream),
+    in parallel over the host threads, then the double-accumulated ES update."""
+    from concurrent.futures import ThreadPoolExecutor
+    from tests import oracle_lib as O
+    threads, nproc, model = host_cpu()
+    a, b = W.shape
+    bs = O.load().or_base_sigma(sigma, r)
+
+    def member(m):
+        A, B = O.lora_factors(bs, key, r, 0, [m], a, b)
+        O.do_mm(np.ascontiguousarray(x[m * rpm:(m + 1) * rpm]), W, A[0], B[0])
+
+    t0 = time.perf_counter()
+    with ThreadPoolExecutor(max_workers=threads) as ex:
+        list(ex.map(member, range(n)))
+    t1 = time.perf_counter()
+    O.lora_grad_f64(sigma, key, r, 0, z, a, b, nthreads=threads)
+    t2 = time.perf_counter()
+    return {"value": round(n / (t2 - t0), 2), "unit": "member-evals/s", "cores": threads,
+            "kind": "port", "host_nproc": nproc, "cpu_model": model,
+            "sample": (f"C2 step of all {n} members (no extrapolation): oracle do_mm per member in "
+                       f"parallel on {threads} host threads, then the ES update; fwd "
+                       f"{t1 - t0:.2f}s, update {t2 - t1:.2f}s"),
+            "seconds": round(t2 - t0, 2)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -250,14 +411,14 @@ def main():
     ap.add_argument("--population", type=int, default=8192)
     ap.add_argument("--cpu-members", type=int, default=8192)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=("c3", "c5"), default="c3")
+    ap.add_argument("--workload", choices=("c1", "c2", "c3", "c5"), default="c3")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one GPU "
               "(the population shards by member across GPUs; see DESIGN.md)", file=sys.stderr)
         sys.exit(2)
-    if args.workload == "c5":
-        bench_c5(args)
+    if args.workload in ("c1", "c2", "c5"):
+        {"c1": bench_c1, "c2": bench_c2, "c5": bench_c5}[args.workload](args)
         return
 
     import torch

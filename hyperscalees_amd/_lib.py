@@ -57,6 +57,14 @@ PROTOTYPES = {
                                       c_i32, c_i32, c_f32, c_i32, c_vp, c_vp, c_size, c_vp]),
     "hses_es_update_noalloc": (ctypes.c_int, [c_vp, c_i32, c_i32, c_u64, c_i32, c_f32, c_i32,
                                               c_i32, c_i32, c_i32, c_f32, c_i32, c_vp, c_vp]),
+    "hses_noisy_standard": (ctypes.c_int, [c_vp, c_i32, c_i32, c_u64, c_f32, c_i32, c_i32, c_i32,
+                                           c_vp, c_i32, c_vp, c_vp]),
+    "hses_full_update_workspace": (c_size, [c_i32, c_i32, c_i32]),
+    "hses_full_update": (ctypes.c_int, [c_vp, c_i32, c_i32, c_u64, c_f32, c_i32, c_i32, c_i32,
+                                        c_i32, c_f32, c_i32, c_vp, c_vp, c_size, c_vp]),
+    "hses_solver_step_scaled": (ctypes.c_int, [c_i32, c_f32, c_f32, c_f32, c_f32, c_f32, c_i32,
+                                               c_vp, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp]),
+    "hses_clip_global_norm": (ctypes.c_int, [c_vp, c_vp, c_i32, c_f32, c_vp, c_vp, c_vp]),
     "hses_member_loglik": (ctypes.c_int, [c_vp, c_i32, c_vp, c_i32, c_i32, c_vp, c_vp]),
     "hses_member_fitness": (ctypes.c_int, [c_vp, c_i32, c_vp, c_i32, c_i32, c_i32, c_vp, c_vp,
                                            c_vp]),

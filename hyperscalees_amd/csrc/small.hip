@@ -214,13 +214,15 @@ __global__ void k_combine_affine(const float* __restrict__ g, const float* __res
 // noiser.rs:155-225.  kind 0: p - g*lr.  Adam/AdamW: moments, bias correction
 // (inverse factors precomputed on the host), p + (m_hat/(sqrt(v_hat)+eps))*(-lr)
 // (+ p*wd for AdamW, no lr factor, as the reference).
+// With gscale (TrustRegion, noiser.rs:215-222) the gradient is first
+// multiplied by the clip factor *gscale, as clip_grads_global_norm does.
 __global__ void k_solver(int32_t kind, float lr, float b1, float omb1, float b2, float omb2,
                          float eps, float wd, float i1, float i2, float* __restrict__ p,
                          const float* __restrict__ g, float* __restrict__ m, float* __restrict__ v,
-                         int64_t len) {
+                         int64_t len, const float* __restrict__ gscale) {
     const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (e >= len) return;
-    const float pv = p[e], gv = g[e];
+    const float pv = p[e], gv = gscale ? __fmul_rn(g[e], gscale[0]) : g[e];
     if (kind == HSES_SGD) {
         p[e] = __fsub_rn(pv, __fmul_rn(gv, lr));
         return;
@@ -236,9 +238,70 @@ __global__ void k_solver(int32_t kind, float lr, float b1, float omb1, float b2,
                                                : __fadd_rn(pv, at);
 }
 
+// clip_grads_global_norm (noiser.rs:231-244), stage 1: kClipBlocks partial
+// sums of g*g (the f32 square, accumulated in double) over a fixed partition
+// of one tensor; each block sums its range with a fixed stride and a fixed
+// tree, so the result depends on the length only.
+constexpr int kClipBlocks = 64;
+__global__ __launch_bounds__(256) void k_sq_partial(const float* __restrict__ g, int64_t len,
+                                                    double* __restrict__ part) {
+    __shared__ double red[256];
+    const int64_t per = (len + kClipBlocks - 1) / kClipBlocks;
+    const int64_t lo = (int64_t)blockIdx.x * per, hi = min(len, lo + per);
+    double s = 0.0;
+    for (int64_t e = lo + threadIdx.x; e < hi; e += 256) {
+        const float v = g[e];
+        s += (double)__fmul_rn(v, v);
+    }
+    red[threadIdx.x] = s;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) part[blockIdx.x] = red[0];
+}
+
+// Stage 2: per tensor the partials in order (double, then f32 as the
+// reference's per-tensor sum), the tensors' sums added in f32 in order, and
+// scale = max_norm / ||g|| when ||g|| > max_norm and ||g|| > 0, else 1.
+__global__ void k_clip_scale(const double* __restrict__ part, int32_t n, float max_norm,
+                             float* __restrict__ scale) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    float sq = 0.0f;
+    for (int32_t i = 0; i < n; ++i) {
+        double s = 0.0;
+        for (int b = 0; b < kClipBlocks; ++b) s += part[(int64_t)i * kClipBlocks + b];
+        sq = __fadd_rn(sq, (float)s);
+    }
+    const float gn = __fsqrt_rn(sq);
+    scale[0] = (gn > max_norm && gn > 0.0f) ? __fdiv_rn(max_norm, gn) : 1.0f;
+}
+
 }  // namespace hses
 
 using namespace hses;
+
+extern "C" int hses_clip_global_norm(const float* const* h_grads, const int64_t* h_lens,
+                                     int32_t n, float max_norm, double* d_work, float* d_scale,
+                                     void* stream) {
+    HSES_REQUIRE(n >= 1 && h_grads && h_lens, "need at least one gradient tensor");
+    HSES_REQUIRE(max_norm >= 0.0f, "max_norm must be >= 0");
+    HSES_REQUIRE(d_work && d_scale, "NULL pointer");
+    for (int32_t i = 0; i < n; ++i) {
+        HSES_REQUIRE(h_lens[i] >= 0, "negative length");
+        HSES_REQUIRE(h_lens[i] == 0 || h_grads[i], "NULL gradient");
+    }
+    hipStream_t s = (hipStream_t)stream;
+    for (int32_t i = 0; i < n; ++i) {
+        hipLaunchKernelGGL(k_sq_partial, dim3(kClipBlocks), dim3(256), 0, s, h_grads[i], h_lens[i],
+                           d_work + (int64_t)i * kClipBlocks);
+        HSES_CHECK_HIP(hipGetLastError());
+    }
+    hipLaunchKernelGGL(k_clip_scale, dim3(1), dim3(64), 0, s, d_work, n, max_norm, d_scale);
+    HSES_CHECK_HIP(hipGetLastError());
+    return HSES_OK;
+}
 
 extern "C" int hses_member_fitness(const float* d_logits, int32_t classes, const int32_t* d_labels,
                                    int32_t n, int32_t rows_per_member, int32_t reward, float* d_fit,
@@ -297,9 +360,10 @@ extern "C" int hses_convert_fitnesses(const float* d_raw, int32_t n, int32_t gro
     return HSES_OK;
 }
 
-extern "C" int hses_solver_step(int32_t kind, float lr, float beta1, float beta2, float eps,
-                                float wd, int32_t step_t, float* d_param, const float* d_grad,
-                                float* d_m, float* d_v, int64_t len, void* stream) {
+extern "C" int hses_solver_step_scaled(int32_t kind, float lr, float beta1, float beta2,
+                                       float eps, float wd, int32_t step_t, float* d_param,
+                                       const float* d_grad, float* d_m, float* d_v, int64_t len,
+                                       const float* d_gscale, void* stream) {
     HSES_REQUIRE(kind >= HSES_SGD && kind <= HSES_ADAMW, "unknown solver");
     HSES_REQUIRE(len >= 0, "negative length");
     if (len == 0) return HSES_OK;
@@ -316,7 +380,14 @@ extern "C" int hses_solver_step(int32_t kind, float lr, float beta1, float beta2
     HSES_REQUIRE(blocks < (1ll << 31), "grid too large");
     hipLaunchKernelGGL(k_solver, dim3(blocks), dim3(256), 0, (hipStream_t)stream, kind, lr, beta1,
                        1.0f - beta1, beta2, 1.0f - beta2, eps, wd, i1, i2, d_param, d_grad, d_m,
-                       d_v, len);
+                       d_v, len, d_gscale);
     HSES_CHECK_HIP(hipGetLastError());
     return HSES_OK;
+}
+
+extern "C" int hses_solver_step(int32_t kind, float lr, float beta1, float beta2, float eps,
+                                float wd, int32_t step_t, float* d_param, const float* d_grad,
+                                float* d_m, float* d_v, int64_t len, void* stream) {
+    return hses_solver_step_scaled(kind, lr, beta1, beta2, eps, wd, step_t, d_param, d_grad, d_m,
+                                   d_v, len, nullptr, stream);
 }

@@ -325,10 +325,65 @@ def convert_fitnesses(raw, group_size=0):
 
 
 def solver_step(kind, lr, param, grad, m=None, v=None, step_t=1, beta1=0.9, beta2=0.999,
-                eps=1e-8, wd=0.0):
-    """In-place Solver::update of one parameter tensor."""
+                eps=1e-8, wd=0.0, gscale=None):
+    """In-place Solver::update of one parameter tensor; with gscale (a device
+    float32 scalar, e.g. from clip_global_norm) on grad * gscale."""
     _dev(param, torch.float32, "param")
     _dev(grad, torch.float32, "grad")
-    _lib.call("hses_solver_step", kind, lr, beta1, beta2, eps, wd, step_t, _p(param), _p(grad),
-              _p(m), _p(v), param.numel(), _stream())
+    if gscale is None:
+        _lib.call("hses_solver_step", kind, lr, beta1, beta2, eps, wd, step_t, _p(param),
+                  _p(grad), _p(m), _p(v), param.numel(), _stream())
+    else:
+        _dev(gscale, torch.float32, "gscale")
+        _lib.call("hses_solver_step_scaled", kind, lr, beta1, beta2, eps, wd, step_t, _p(param),
+                  _p(grad), _p(m), _p(v), param.numel(), _p(gscale), _stream())
     return param
+
+
+def clip_global_norm(grads, max_norm, out=None):
+    """clip_grads_global_norm's factor over a list of gradient tensors: a
+    device float32 scalar, max_norm / ||g|| or 1."""
+    if not grads:
+        raise ValueError("need at least one gradient tensor")
+    for g in grads:
+        _dev(g, torch.float32, "grad")
+    dev = grads[0].device
+    work = torch.empty(64 * len(grads), dtype=torch.float64, device=dev)
+    if out is None:
+        out = torch.empty(1, dtype=torch.float32, device=dev)
+    ptrs = (ctypes.c_void_p * len(grads))(*[g.data_ptr() for g in grads])
+    lens = (ctypes.c_int64 * len(grads))(*[g.numel() for g in grads])
+    _lib.call("hses_clip_global_norm", ptrs, lens, len(grads), max_norm, _p(work), _p(out),
+              _stream())
+    return out
+
+
+def noisy_standard(param, key, sigma, epoch, noise_reuse, tids):
+    """get_noisy_standard for n members: (n, a, b) = param + sign*sigma*noise.
+    tids is an int sequence/tensor or (tid_lo, n)."""
+    _dev(param, torch.float32, "param")
+    a, b = param.shape
+    if isinstance(tids, tuple):
+        tid_lo, n = tids
+        d_tids = None
+    else:
+        d_tids = torch.as_tensor(tids, dtype=torch.int32, device=param.device).contiguous()
+        tid_lo, n = 0, d_tids.numel()
+    out = torch.empty((n, a, b), dtype=torch.float32, device=param.device)
+    _lib.call("hses_noisy_standard", _p(param), a, b, key & (2**64 - 1), sigma, epoch,
+              noise_reuse, tid_lo, _p(d_tids), n, _p(out), _stream())
+    return out
+
+
+def full_update(fit, tid_lo, key, sigma, epoch, noise_reuse, a, b, scale, out=None,
+                accumulate=False):
+    """_simple_full_update of a dense (a, b) parameter: scale * sum_m fit[m] noise_m."""
+    _dev(fit, torch.float32, "fit")
+    n = fit.numel()
+    wbytes = int(_lib.load().hses_full_update_workspace(a, b, n))
+    work = _workspace(wbytes, fit.device)
+    if out is None:
+        out = torch.empty((a, b), dtype=torch.float32, device=fit.device)
+    _lib.call("hses_full_update", _p(fit), n, tid_lo, key & (2**64 - 1), sigma, epoch, noise_reuse,
+              a, b, scale, int(bool(accumulate)), _p(out), _p(work), wbytes, _stream())
+    return out

@@ -57,6 +57,7 @@ class SnnConfig:
     poisson_seed: tuple = (0, 0, 0, 0)
     reward: int = REWARD_LOGLIK    # fitness_from_logits_reward kind (snn_mnist.rs:175-201)
     accumulate: int = 1            # K chunks of n / K members (accumulate_train.rs:770)
+    max_norm: float = 0.0          # > 0: Solver::TrustRegion, clip by global norm (noiser.rs:215-244)
     keys: list = field(default_factory=list)
 
     def __post_init__(self):
@@ -200,18 +201,34 @@ class SnnEs:
         return self.readout(epoch, lo)
 
     # -- update --------------------------------------------------------------
+    def _solve(self, l, gscale):
+        c = self.cfg
+        K.solver_step(c.solver, c.lr, self.W[l], self.grads[l], self.m[l], self.v[l],
+                      step_t=self.step_t, beta1=c.beta1, beta2=c.beta2, eps=c.eps,
+                      wd=c.weight_decay if c.solver == ADAMW else 0.0, gscale=gscale)
+
+    def _clip(self):
+        """TrustRegion's clip factor over all layers' gradients, or None."""
+        if self.cfg.max_norm <= 0.0:
+            return None
+        return K.clip_global_norm(self.grads, self.cfg.max_norm)
+
     def update(self, raw_fit, epoch=0):
         c = self.cfg
         z, _ = K.convert_fitnesses(raw_fit)
         scale = np.float32(-math.sqrt(c.n) / c.n)   # -g * sqrt(N) with g = (1/N) sum (eggroll.rs:403)
         self.step_t += 1
+        clip = c.max_norm > 0.0  # the global norm needs every gradient before any step
         for l in range(self.L):
             a, b = self.W[l].shape
             K.es_update(z, 0, c.keys[l], c.rank, c.sigma, epoch, c.noise_reuse, a, b, scale,
                         out=self.grads[l])
-            K.solver_step(c.solver, c.lr, self.W[l], self.grads[l], self.m[l], self.v[l],
-                          step_t=self.step_t, beta1=c.beta1, beta2=c.beta2, eps=c.eps,
-                          wd=c.weight_decay if c.solver == ADAMW else 0.0)
+            if not clip:
+                self._solve(l, None)
+        if clip:
+            gscale = self._clip()
+            for l in range(self.L):
+                self._solve(l, gscale)
         return z
 
     def step(self, epoch=0):
@@ -249,7 +266,7 @@ class SnnEs:
                 ones = K.es_update(one, c.n - 1, c.keys[l], c.rank, c.sigma, epoch, c.noise_reuse,
                                    a, b, np.float32(1.0))
             K.combine_affine(self.grads[l], self.moments, c.n, ones_acc=ones, out=self.grads[l])
-            K.solver_step(c.solver, c.lr, self.W[l], self.grads[l], self.m[l], self.v[l],
-                          step_t=self.step_t, beta1=c.beta1, beta2=c.beta2, eps=c.eps,
-                          wd=c.weight_decay if c.solver == ADAMW else 0.0)
+        gscale = self._clip()
+        for l in range(self.L):
+            self._solve(l, gscale)
         return self.raw

@@ -106,6 +106,28 @@ int hses_nonlora_noise(float base_sigma, uint64_t key, int32_t epoch, int32_t no
                        int32_t tid_lo, const int32_t *d_tids, int32_t n, int32_t a, int32_t b,
                        float *d_out, void *stream);
 
+/* get_noisy_standard_impl (eggroll.rs:480-503) for the dense (PARAM-class)
+ * parameters of n members: d_out (n, a, b) = param + sign*sigma*normals of
+ * each member's stream (noiser sigma, not divided by sqrt(rank)), bit-exact.
+ * The clean path (iterinfo None) and freeze_nonlora are the caller's copy of
+ * param. */
+int hses_noisy_standard(const float *d_param, int32_t a, int32_t b, uint64_t key, float sigma,
+                        int32_t epoch, int32_t noise_reuse, int32_t tid_lo, const int32_t *d_tids,
+                        int32_t n, float *d_out, void *stream);
+
+/* _simple_full_update + _do_update for a dense parameter (eggroll.rs:331-350,
+ * 384-404): d_grad (a, b) = scale * sum_m f[m] * sign_m*sigma*normals_m over
+ * members m in [0, n) with thread ids tid_lo+m (do_updates: scale =
+ * -sqrt(N)/N).  Each member's f32 term is accumulated in double over a fixed
+ * split of the pairs and reduced in a fixed order (deterministic, no
+ * atomics).  accumulate != 0 adds into d_grad.  a*b <= 524288.  d_work must
+ * hold hses_full_update_workspace(a, b, n) bytes. */
+size_t hses_full_update_workspace(int32_t a, int32_t b, int32_t n);
+int hses_full_update(const float *d_f, int32_t n, int32_t tid_lo, uint64_t key, float sigma,
+                     int32_t epoch, int32_t noise_reuse, int32_t a, int32_t b, float scale,
+                     int32_t accumulate, float *d_grad, void *d_work, size_t work_bytes,
+                     void *stream);
+
 /* ---- spiking kernels ------------------------------------------------- */
 
 /* poisson_encode_fused (burn_impl/hyperscalees-kernels/src/poisson_encode_fused_oxide.rs:61-106,
@@ -398,6 +420,21 @@ int hses_convert_fitnesses(const float *d_raw, int32_t n, int32_t group_size, fl
 int hses_solver_step(int32_t kind, float lr, float beta1, float beta2, float eps, float wd,
                      int32_t step_t, float *d_param, const float *d_grad, float *d_m, float *d_v,
                      int64_t len, void *stream);
+/* The same step on the gradient multiplied by the device scalar *d_gscale
+ * (NULL: 1): Solver::TrustRegion (noiser.rs:215-222) with the factor of
+ * hses_clip_global_norm. */
+int hses_solver_step_scaled(int32_t kind, float lr, float beta1, float beta2, float eps, float wd,
+                            int32_t step_t, float *d_param, const float *d_grad, float *d_m,
+                            float *d_v, int64_t len, const float *d_gscale, void *stream);
+
+/* clip_grads_global_norm (noiser.rs:231-244), the factor only: over the n
+ * gradient tensors h_grads[i] (device pointers in a host array) of h_lens[i]
+ * floats, ||g|| = sqrt(sum_i sum g^2) and *d_scale = max_norm / ||g|| when
+ * ||g|| > max_norm and ||g|| > 0, else 1.  Each tensor's sum of squares is a
+ * fixed-order double reduction (f32 squares) rounded to f32; the tensors'
+ * sums are added in f32 in order.  d_work holds 64 * n doubles. */
+int hses_clip_global_norm(const float *const *h_grads, const int64_t *h_lens, int32_t n,
+                          float max_norm, double *d_work, float *d_scale, void *stream);
 
 #ifdef __cplusplus
 }

@@ -101,6 +101,14 @@ def test_validation_rejects_bad_arguments_without_a_gpu():
     _expect_invalid("hses_add_layer_norm", ctypes.c_void_p(16), ctypes.c_void_p(32), 4, 8,
                     ctypes.c_void_p(16), ctypes.c_void_p(16), 1e-5, ctypes.c_void_p(16), NULL)
     _expect_invalid("hses_rwkv_act", ctypes.c_void_p(16), 4, 5, NULL)
+    _expect_invalid("hses_full_update", ctypes.c_void_p(16), 8, 0, 1, 0.02, 0, 0, 1024, 1024,
+                    1.0, 0, ctypes.c_void_p(16), ctypes.c_void_p(16), 1 << 30, NULL)  # a*b > 2^19
+    _expect_invalid("hses_noisy_standard", ctypes.c_void_p(16), -1, 4, 1, 0.02, 0, 0, 0, NULL, 2,
+                    ctypes.c_void_p(16), NULL)
+    _expect_invalid("hses_clip_global_norm", NULL, NULL, 0, 1.0, ctypes.c_void_p(16),
+                    ctypes.c_void_p(16), NULL)
+    _expect_invalid("hses_solver_step_scaled", 9, 0.1, 0.9, 0.999, 1e-8, 0.0, 1,
+                    ctypes.c_void_p(16), ctypes.c_void_p(16), NULL, NULL, 4, NULL, NULL)
     # the allocation-free ES update: one a x b partial must fit its fixed 32 MiB scratch
     _expect_invalid("hses_es_update_noalloc", ctypes.c_void_p(16), 8, 0, 1, 4, 0.02, 0, 0,
                     2048, 4096, 1.0, 0, ctypes.c_void_p(16), NULL)

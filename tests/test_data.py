@@ -100,6 +100,31 @@ def test_shuffled_indices_first_draw_parity():
         assert data.shuffled_indices(2, 1, seed)[0] == expect
 
 
+def py_shuffled_indices(n, count, seed):
+    """accumulate_train.rs:157-174 in Python integers: xorshift64 (13, 7, 17)
+    from (seed ^ 0x9E3779B97F4A7C15) | 1, each draw times 0x2545F4914F6CDD1D
+    (wrapping u64), partial Fisher-Yates swap of i with i + draw % (n - i)."""
+    m64 = 2**64 - 1
+    state = ((seed ^ 0x9E3779B97F4A7C15) | 1) & m64
+    idx = list(range(n))
+    for i in range(count):
+        state ^= (state << 13) & m64
+        state ^= state >> 7
+        state ^= (state << 17) & m64
+        draw = (state * 0x2545F4914F6CDD1D) & m64
+        j = i + draw % (n - i)
+        idx[i], idx[j] = idx[j], idx[i]
+    return idx[:count]
+
+
+@pytest.mark.parametrize("n,count,seed", [(60000, 100, 0), (60000, 100, 42 ^ KEY),
+                                          (1000, 1000, 12345), (7, 7, 2**64 - 1),
+                                          (2**20, 100, 0xDEADBEEF), (3, 2, 5)])
+def test_shuffled_indices_match_python_restatement(n, count, seed):
+    np.testing.assert_array_equal(data.shuffled_indices(n, count, seed),
+                                  py_shuffled_indices(n, count, seed))
+
+
 def test_shuffled_indices_first_index_uniform():
     n = 7
     counts = np.bincount([data.shuffled_indices(n, 1, s)[0] for s in range(7000)], minlength=n)
