@@ -273,6 +273,106 @@ def _timed_steps(step, steps, warmup):
     return (time.perf_counter() - t0) * 1000.0 / steps
 
 
+def bench_c4(args):
+    """the spiking self-attention transformer (d_model 64, 4 heads, 2
+    blocks, 64 tokens, LIF on Q/K/V) at N=1024, r=8, fp32.  One step = the
+    population forward (Poisson-encoded tokens of a random 256-way vocabulary,
+    one sequence per member), log-likelihood fitness, z-score, do_updates of
+    every leaf and AdamW."""
+    import torch
+    from hyperscalees_amd import kernels as K
+    from hyperscalees_amd import snn_attention as sa
+    cfg = sa.SaConfig()
+    K.init(0)
+    P = sa.init_params(cfg, 0)
+    vocab = sa.synthetic_vocab(cfg, 0)
+    es = sa.SpikingAttentionEs(cfg, P, vocab)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0)
+    tok = torch.randint(0, cfg.vocab, (cfg.n, cfg.ntok), dtype=torch.int32, device="cuda", generator=g)
+    lab = torch.randint(0, cfg.classes, (cfg.n,), dtype=torch.int32, device="cuda", generator=g)
+    ms = _timed_steps(lambda i: es.step(tok, lab, epoch=i), args.steps, args.warmup)
+    fwd_ms = _time_launch(lambda: es.forward(tok, lab, epoch=0), reps=3)
+    # dominant kernel: the attention competition of one block (all members and heads)
+    att_ms = _time_launch(lambda: es.attention_block(0, 0), reps=3)
+    att = lambda: K._lib.call("hses_sa_attention", K._p(es.Q), K._p(es.Kt), K._p(es.V),
+                              cfg.d_model, cfg.n, cfg.ntok, cfg.heads, cfg.head_dim,
+                              K._p(es.th["beta"]), K._p(es.th["attn_th"]), cfg.g_inh, cfg.tau_m,
+                              cfg.n_iter, K._p(es.O), K._stream())
+    core_ms = _time_launch(att, reps=5)
+    # algorithmic work of the competition: n_iter LIF steps over R x R key
+    # neurons per (member, head) plus the scores and A V products (fp32 VALU)
+    R, hd = cfg.ntok, cfg.head_dim
+    core_flop = cfg.n * cfg.heads * (2 * R * R * hd * 2 + cfg.n_iter * R * R * 6)
+    achieved = core_flop / (core_ms * 1e-3) / 1e12
+    peak_vector_fp32 = 157.3  # MI355X fp32 vector (FMA) peak, TFLOP/s
+    fl = sa.forward_flops(cfg)
+    out = {
+        "metric": "perturbed member-evals/sec, spiking self-attention N=1024 r=8 fp32 (configs[3])",
+        "value": round(cfg.n / (ms * 1e-3), 1), "unit": "member-evals/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp32 (fp32 MFMA projections, fp32 VALU spiking stages, fp32 ES update)",
+        "data": "synthetic",
+        "config": {"workload": ("C4: spiking self-attention transformer (snn_self_attention_heads), "
+                                "d_model 64, 4 heads, 2 blocks, 64 tokens of a random 256-way "
+                                "vocabulary (16-value intensity vectors, Poisson T=8), LIF on Q/K/V, "
+                                "N=1024 members x 1 sequence, r=8, sigma 0.02; full ES step "
+                                "(forward + fitness + z-score + ES update of every leaf + AdamW)"),
+                   "population": cfg.n, "rank": cfg.rank, "tokens": cfg.ntok,
+                   "parallelism": "single GPU"},
+        "phase_ms": {"forward": round(fwd_ms, 4), "attention_block": round(att_ms, 4)},
+        "fwd_flop": fl,
+        "roofline": {"kernel": "k_sa_attention (row_softmax_lif over 1024 members x 4 heads x 64 rows)",
+                     "bound": "valu", "achieved": round(achieved, 2), "peak": peak_vector_fp32,
+                     "unit": "TFLOP/s", "frac": round(achieved / peak_vector_fp32, 4),
+                     "traffic": None, "launch_ms": round(core_ms, 4),
+                     "algorithmic_flop_per_launch": core_flop},
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline_c4(cfg, P, es, tr_spikes(es, tok, lab), args.cpu_members)
+    print(json.dumps(out), flush=True)
+
+
+def tr_spikes(es, tok, lab):
+    """The population's input spikes (T, M, tin) on the host."""
+    tr = {}
+    es.forward(tok, lab, epoch=0, trace=tr)
+    return tr["spk"].cpu().numpy()
+
+
+def cpu_baseline_c4(cfg, P, es, spk, members):
+    """The oracle's member forward (C restatement of the JAX model) on each
+    sampled member's materialised parameters, in parallel over the host threads,
+    plus the sample's share of the ES update of every leaf."""
+    from concurrent.futures import ThreadPoolExecutor
+    from tests import oracle_lib as O
+    threads, nproc, model = host_cpu()
+    ns = max(1, min(members, 8 * threads, cfg.n))
+    R = cfg.ntok
+
+    def member(m):
+        Pm = O.sa_member_params(P, es.keys, es.leaves, cfg.sigma, cfg.rank, m)
+        O.sa_forward_member(cfg, Pm, spk[:, m * R:(m + 1) * R])
+
+    t0 = time.perf_counter()
+    with ThreadPoolExecutor(max_workers=threads) as ex:
+        list(ex.map(member, range(ns)))
+    t1 = time.perf_counter()
+    z = np.random.default_rng(0).standard_normal(ns).astype(np.float32)
+    for name, (a, b), cls in es.leaves:
+        if cls == 1:
+            O.lora_grad_f64(cfg.sigma, es.keys[name], cfg.rank, 0, z, a, b, nthreads=threads)
+    t2 = time.perf_counter()
+    return {"value": round(ns / (t2 - t0), 3), "unit": "member-evals/s", "cores": threads,
+            "kind": "port", "host_nproc": nproc, "cpu_model": model,
+            "sample": (f"oracle forward of {ns} of {cfg.n} members (each on its materialised "
+                       f"parameters) in parallel on {threads} host threads, plus the ES update of "
+                       f"every MM leaf over those members; fwd {t1 - t0:.2f}s, update "
+                       f"{t2 - t1:.2f}s; extrapolated linearly in N"),
+            "seconds": round(t2 - t0, 2)}
+
+
 def bench_c1(args):
     """SNN-MLP 784-128-128-128-10, T=8, N=256, r=4, sigma 0.02, fp32; every
     member evaluates the same 64 synthetic inputs.  One step = the full ES step."""
@@ -411,14 +511,14 @@ def main():
     ap.add_argument("--population", type=int, default=8192)
     ap.add_argument("--cpu-members", type=int, default=8192)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=("c1", "c2", "c3", "c5"), default="c3")
+    ap.add_argument("--workload", choices=("c1", "c2", "c3", "c4", "c5"), default="c3")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one GPU "
               "(the population shards by member across GPUs; see DESIGN.md)", file=sys.stderr)
         sys.exit(2)
-    if args.workload in ("c1", "c2", "c5"):
-        {"c1": bench_c1, "c2": bench_c2, "c5": bench_c5}[args.workload](args)
+    if args.workload in ("c1", "c2", "c4", "c5"):
+        {"c1": bench_c1, "c2": bench_c2, "c4": bench_c4, "c5": bench_c5}[args.workload](args)
         return
 
     import torch

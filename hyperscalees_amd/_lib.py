@@ -65,6 +65,15 @@ PROTOTYPES = {
     "hses_solver_step_scaled": (ctypes.c_int, [c_i32, c_f32, c_f32, c_f32, c_f32, c_f32, c_i32,
                                                c_vp, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp]),
     "hses_clip_global_norm": (ctypes.c_int, [c_vp, c_vp, c_i32, c_f32, c_vp, c_vp, c_vp]),
+    "hses_softplus": (ctypes.c_int, [c_vp, c_i64, c_vp, c_vp]),
+    "hses_sa_encode": (ctypes.c_int, [c_vp, c_vp, c_vp, c_i32, c_i64, c_i32, c_i32, c_vp, c_vp,
+                                      c_vp, c_f32, c_vp, c_i32, c_vp, c_vp]),
+    "hses_sa_attention": (ctypes.c_int, [c_vp, c_vp, c_vp, c_i32, c_i64, c_i32, c_i32, c_i32,
+                                         c_vp, c_vp, c_f32, c_f32, c_i32, c_vp, c_vp]),
+    "hses_sa_ffn_spike": (ctypes.c_int, [c_vp, c_i64, c_i32, c_i32, c_vp, c_vp, c_vp]),
+    "hses_add_inplace": (ctypes.c_int, [c_vp, c_vp, c_i64, c_vp]),
+    "hses_sa_pool": (ctypes.c_int, [c_vp, c_i64, c_i32, c_i32, c_vp, c_vp]),
+    "hses_scale_rows": (ctypes.c_int, [c_vp, c_i64, c_i32, c_vp, c_vp]),
     "hses_member_loglik": (ctypes.c_int, [c_vp, c_i32, c_vp, c_i32, c_i32, c_vp, c_vp]),
     "hses_member_fitness": (ctypes.c_int, [c_vp, c_i32, c_vp, c_i32, c_i32, c_i32, c_vp, c_vp,
                                            c_vp]),

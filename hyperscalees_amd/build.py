@@ -16,7 +16,8 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libhses.so")
 SOURCES = ["runtime.cpp", "bm_tables.cpp", "data.cpp", "noise.hip", "spiking.hip", "small.hip",
-           "linear.hip", "linear_pair.hip", "linear_wide.hip", "es_update.hip", "rwkv.hip"]
+           "linear.hip", "linear_pair.hip", "linear_wide.hip", "es_update.hip", "rwkv.hip",
+           "attention.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

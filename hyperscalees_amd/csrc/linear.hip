@@ -311,6 +311,91 @@ __global__ void k_act_rows(LinParams P) {
     }
 }
 
+// Few rows per member (readouts on pooled rows): one wave per member.  The
+// wave generates the member's factor rows into LDS (B rows [0, b), A rows
+// [b, a+b) scaled by sign * base_sigma), then per row of the member forms
+// xb = x B (lanes over the rank) and y = x W^T + xb A^T (lanes over outputs),
+// every sum in index order with f32 accumulation.  fp32 math, do_mm
+// orientation, F32 or BF16 activations.
+constexpr int KR_MAXF = 16384;  // (a + b) * r + b floats of LDS per member
+__global__ __launch_bounds__(64) void k_linear_rows(LinParams P) {
+    extern __shared__ float smem[];
+    __shared__ BmTables tabs;
+    const int lane = threadIdx.x;
+    const int32_t m = blockIdx.x;
+    const int32_t r = P.r, a = P.a, b = P.b;
+    float* Bs = smem;                     // (b, r)
+    float* As = smem + (size_t)b * r;     // (a, r)
+    float* xs = As + (size_t)a * r;       // (b) current row
+    float* xb = xs + b;                   // (r)
+    if (r > 0) {
+        load_bm_tables(&tabs, P.tables);
+        __syncthreads();
+        const NoiseCtx ctx{&tabs, P.log_exc, P.cos_exc};
+        float sign;
+        const uint64_t seed = member_seed(P.key, P.epoch, P.nreuse, P.tid_lo + m, &sign);
+        const float sc = sign * P.bs;
+        for (int32_t j = lane; j < a + b; j += 64) {
+            uint64_t s = row_start_state(seed, j, P.jump);
+            if (j < b) {
+                float* dst = Bs + (size_t)j * r;
+                bm_run(s, r, ctx, [&](int32_t c, float v) { dst[c] = v; });
+            } else {
+                float* dst = As + (size_t)(j - b) * r;
+                bm_run(s, r, ctx, [&](int32_t c, float v) { dst[c] = v * sc; });
+            }
+        }
+    }
+    __syncthreads();
+    for (int32_t q = 0; q < P.R; ++q) {
+        const int64_t L = (int64_t)m * P.R + q;
+        const int64_t xo = phys_row(P, L, P.x_stride, P.x_plane);
+        for (int32_t k = lane; k < b; k += 64) {
+            if (P.x_fmt == HSES_FMT_F32) {
+                xs[k] = static_cast<const float*>(P.x)[xo + k];
+            } else {
+                const uint32_t u = static_cast<const uint16_t*>(P.x)[xo + k];
+                xs[k] = __builtin_bit_cast(float, u << 16);
+            }
+        }
+        __syncthreads();
+        if (lane < r) {
+            float s = 0.0f;
+            for (int32_t k = 0; k < b; ++k) s = s + xs[k] * Bs[(size_t)k * r + lane];
+            xb[lane] = s;
+        }
+        __syncthreads();
+        float* y = P.y + phys_row(P, L, P.y_stride, P.y_plane);
+        for (int32_t o = lane; o < a; o += 64) {
+            const float* w = P.W + (size_t)o * b;
+            float base = 0.0f;
+            for (int32_t k = 0; k < b; ++k) base = base + xs[k] * w[k];
+            float lo = 0.0f;
+            for (int32_t c = 0; c < r; ++c) lo = lo + xb[c] * As[(size_t)o * r + c];
+            y[o] = r > 0 ? base + lo : base;
+        }
+        __syncthreads();
+    }
+}
+
+static int launch_linear_rows(LinParams& P, DeviceState* st, hipStream_t s) {
+    if (P.math != HSES_MATH_F32 || P.tmm || P.x_fmt == HSES_FMT_BITS || P.r > 64)
+        return HSES_ERR_UNSUPPORTED;
+    const size_t nf = (size_t)(P.a + P.b) * P.r + P.b + 64;
+    if (nf > KR_MAXF) return HSES_ERR_UNSUPPORTED;
+    if (P.r > 0) {
+        int rc = get_jump_table(st, P.r, (int64_t)P.a + P.b, &P.jump);
+        if (rc) return rc;
+    }
+    const size_t lds = nf * sizeof(float);
+    if (lds > 48 * 1024)
+        HSES_CHECK_HIP(hipFuncSetAttribute((const void*)k_linear_rows,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    hipLaunchKernelGGL(k_linear_rows, dim3((uint32_t)P.n), dim3(64), lds, s, P);
+    HSES_CHECK_HIP(hipGetLastError());
+    return HSES_OK;
+}
+
 // Output checks and the kernel choice shared by do_mm and do_Tmm: the pair
 // kernels (rank a multiple of 16, output width <= 128, bf16), the wide-output
 // kernel (bf16, small rank), or else the small-rank kernel.
@@ -336,11 +421,13 @@ static int run_linear(LinParams& P, DeviceState* st, float* d_y, int64_t y_strid
                              std::string(name) + ": bf16 output needs the wide-output kernel (bf16 "
                              "math, members per 128-row tile x rank <= 16, aligned x rows)");
         rc = launch_linear_small(P, st, s);
+        if (rc == HSES_ERR_UNSUPPORTED && P.R <= 16) rc = launch_linear_rows(P, st, s);
     }
     if (rc == HSES_ERR_UNSUPPORTED)
         return set_error(HSES_ERR_UNSUPPORTED,
                          std::string(name) + ": no kernel for this rank/shape (members per 64-row "
-                         "tile x rank must be <= 64, or rank a multiple of 16)");
+                         "tile x rank must be <= 64, or rank a multiple of 16, or at most 16 fp32 "
+                         "rows per member with (a + b) x rank <= 16000)");
     if (rc || act == ACT_NONE) return rc;
     const int64_t n = P.total * P.a;
     HSES_REQUIRE((n + 255) / 256 < (1ll << 31), "grid too large");

@@ -436,6 +436,54 @@ int hses_solver_step_scaled(int32_t kind, float lr, float beta1, float beta2, fl
 int hses_clip_global_norm(const float *const *h_grads, const int64_t *h_lens, int32_t n,
                           float max_norm, double *d_work, float *d_scale, void *stream);
 
+/* ---- spiking self-attention transformer (C4) -------------------------- */
+/* The model of src/hyperscalees/models/snn_self_attention_heads.py batched over
+ * a population: member m owns rows [m R, (m+1) R) of every (rows, C) plane
+ * (R = tokens per member); per-member scalars (thresholds, beta, gains) are
+ * device arrays of n floats.  Its perturbed projections are
+ * hses_perturbed_linear calls (one per MM leaf, heads written into column
+ * blocks through y_stride); its Parameter leaves are perturbed with
+ * hses_noisy_standard. */
+
+/* jax.nn.softplus (the models' positive-threshold map, snn_self_attention_heads.py:43-44):
+ * y = max(x, 0) + log1p(exp(-|x|)). */
+int hses_softplus(const float *d_x, int64_t n, float *d_y, void *stream);
+
+/* The input encoders (_rate, snn_self_attention_heads.py:33-40, 168-175):
+ * X = (rate(cq) + rate(ck) + rate(cv)) / 3 + pos, rate = mean over T of the LIF
+ * spikes (snn_attention.py:41-61, v0 = 0) of the time-major (T, M, d)
+ * projection currents with member m's threshold th_*[m].  pos is (R, d)
+ * (pos_per_member 0) or (M, d). */
+int hses_sa_encode(const float *d_cq, const float *d_ck, const float *d_cv, int32_t T, int64_t M,
+                   int32_t d, int32_t rows_per_member, const float *d_th_q, const float *d_th_k,
+                   const float *d_th_v, float tau_m, const float *d_pos, int32_t pos_per_member,
+                   float *d_X, void *stream);
+
+/* The attention of multihead_attention_once (snn_self_attention_heads.py:47-73)
+ * for every member and head: head h of a row is columns [h hd, (h+1) hd) of q, k,
+ * v and out ((n R, ld) fp32); A = row_softmax_lif(beta[m] (Q K^T))
+ * (snn_self_attention.py:45-80: n_iter LIF steps of the key neurons on
+ * h / (max |h| + 1e-6) - g_inh * sum(count), p = count / (sum count + 1e-6),
+ * threshold vth[m]), out = A V.  R <= 64, hd <= 64. */
+int hses_sa_attention(const float *d_q, const float *d_k, const float *d_v, int32_t ld, int64_t n,
+                      int32_t R, int32_t H, int32_t hd, const float *d_beta, const float *d_vth,
+                      float g_inh, float tau_m, int32_t n_iter, float *d_out, void *stream);
+
+/* ffn_once's lif_single (snn_self_attention_heads.py:79-83): per row,
+ * act = (c / max(max |c|, 1e-6) >= vth[m]) as 0/1 fp32. */
+int hses_sa_ffn_spike(const float *d_c, int64_t M, int32_t d, int32_t rows_per_member,
+                      const float *d_vth, float *d_act, void *stream);
+
+/* x += y (the blocks' residual adds, snn_self_attention_heads.py:186-187). */
+int hses_add_inplace(float *d_x, const float *d_y, int64_t n, void *stream);
+
+/* jnp.mean(X, axis=0) per member (snn_self_attention_heads.py:189):
+ * out (n, d) = sum of the member's R rows / R, in row order. */
+int hses_sa_pool(const float *d_X, int64_t n, int32_t R, int32_t d, float *d_out, void *stream);
+
+/* y[r, :] *= s[r] (logits * out_gain per member, snn_self_attention_heads.py:191-192). */
+int hses_scale_rows(float *d_y, int64_t rows, int32_t cols, const float *d_s, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

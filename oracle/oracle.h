@@ -206,6 +206,38 @@ typedef struct {
 void or_rwkv_lm_forward(const or_rwkv_lm *P, const int32_t *tokens, int32_t T, float *state,
                         float *logits);
 
+/* Spiking self-attention transformer, C4 (oracle_attn.c;
+ * src/hyperscalees/models/snn_self_attention_heads.py). */
+#define OR_SA_MAX_HEADS 8
+typedef struct {
+    int32_t T, ntok, tin, d_model, heads, blocks, classes, n_iter;
+    float tau_m, g_inh;
+} or_sa_cfg;
+typedef struct {
+    const float *q[OR_SA_MAX_HEADS], *k[OR_SA_MAX_HEADS], *v[OR_SA_MAX_HEADS]; /* (hd, d) */
+    const float *o, *ff1, *ff2;                                             /* (d, d)  */
+    float ff_th;                                                            /* raw     */
+} or_sa_block;
+typedef struct {
+    const float *in_q, *in_k, *in_v; /* (d, tin) */
+    const float *pos;                /* (ntok, d) */
+    const or_sa_block *blocks;
+    const float *out;                /* (classes, d) */
+    float out_gain, beta, q_th, k_th, v_th, attn_th; /* raw Parameter leaves */
+} or_sa_params;
+float or_sa_softplus(float x);
+void or_sa_encode(const float *cq, const float *ck, const float *cv, int32_t T, int32_t R,
+                  int32_t d, float th_q, float th_k, float th_v, float tau_m, const float *pos,
+                  float *X);
+void or_sa_row_softmax_lif(const float *h, int32_t n, float vth, float g_inh, float tau_m,
+                           int32_t n_iter, float *p);
+void or_sa_attention_head(const float *q, const float *k, const float *v, int32_t R, int32_t hd,
+                          int32_t ld, float beta, float vth, float g_inh, float tau_m,
+                          int32_t n_iter, float *out);
+void or_sa_ffn_spike(const float *c, int32_t R, int32_t d, float vth, float *act);
+void or_sa_forward_member(const or_sa_cfg *cfg, const or_sa_params *P, const float *x,
+                          float *logits);
+
 #ifdef __cplusplus
 }
 #endif

@@ -49,6 +49,25 @@ class RwkvLm(ctypes.Structure):
                 + [("blocks", ctypes.POINTER(RwkvBlock))])
 
 
+SA_MAX_HEADS = 8
+
+
+class SaCfg(ctypes.Structure):
+    _fields_ = [(n, c_i32) for n in ("T", "ntok", "tin", "d_model", "heads", "blocks", "classes",
+                                      "n_iter")] + [("tau_m", c_f32), ("g_inh", c_f32)]
+
+
+class SaBlock(ctypes.Structure):
+    _fields_ = ([(n, ctypes.c_void_p * SA_MAX_HEADS) for n in ("q", "k", "v")]
+                + [(n, ctypes.c_void_p) for n in ("o", "ff1", "ff2")] + [("ff_th", c_f32)])
+
+
+class SaParams(ctypes.Structure):
+    _fields_ = ([(n, ctypes.c_void_p) for n in ("in_q", "in_k", "in_v", "pos")]
+                + [("blocks", ctypes.POINTER(SaBlock)), ("out", ctypes.c_void_p)]
+                + [(n, c_f32) for n in ("out_gain", "beta", "q_th", "k_th", "v_th", "attn_th")])
+
+
 def build():
     subprocess.run(["make", "-s", "-C", ORACLE_DIR], check=True)
 
@@ -120,6 +139,16 @@ def load():
                                     c_i32, f32p]),
         "or_snn_forward_member": (None, [ctypes.POINTER(SnnCfg), ctypes.c_void_p,
                                          ctypes.c_void_p, f32p, i32p, c_i32, f32p]),
+        "or_sa_softplus": (c_f32, [c_f32]),
+        "or_sa_encode": (None, [f32p, f32p, f32p, c_i32, c_i32, c_i32, c_f32, c_f32, c_f32, c_f32,
+                                f32p, f32p]),
+        "or_sa_row_softmax_lif": (None, [f32p, c_i32, c_f32, c_f32, c_f32, c_i32, f32p]),
+        "or_sa_attention_head": (None, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, c_i32,
+                                        c_i32, c_i32, c_f32, c_f32, c_f32, c_f32, c_i32,
+                                        ctypes.c_void_p]),
+        "or_sa_ffn_spike": (None, [f32p, c_i32, c_i32, c_f32, f32p]),
+        "or_sa_forward_member": (None, [ctypes.POINTER(SaCfg), ctypes.POINTER(SaParams), f32p,
+                                        f32p]),
         "or_clip_global_norm_scale": (c_f32, [ctypes.c_void_p, ctypes.c_void_p, c_i32, c_f32]),
     }
     for name, (res, args) in sig.items():
@@ -305,3 +334,60 @@ def clip_scale(grads, max_norm):
     ptrs = (ctypes.c_void_p * max(1, len(gs)))(*[g.ctypes.data for g in gs])
     lens = np.array([g.size for g in gs] or [0], np.int64)
     return float(load().or_clip_global_norm_scale(ptrs, lens.ctypes.data, len(gs), max_norm))
+
+
+# ---- spiking self-attention (C4) ---------------------------------------------
+
+def sa_cfg(c):
+    """SaCfg from a hyperscalees_amd.snn_attention.SaConfig-like object."""
+    out = SaCfg()
+    for f in ("T", "ntok", "tin", "d_model", "heads", "blocks", "classes", "n_iter"):
+        setattr(out, f, int(getattr(c, f)))
+    out.tau_m, out.g_inh = float(c.tau_m), float(c.g_inh)
+    return out
+
+
+def sa_forward_member(c, P, x):
+    """or_sa_forward_member on a member's parameter dict P (leaf name -> f32
+    array, already perturbed) and its input spikes x (T, ntok, tin)."""
+    keep = {k: np.ascontiguousarray(v, np.float32) for k, v in P.items()}
+    blocks = (SaBlock * c.blocks)()
+    for b in range(c.blocks):
+        for kind in "qkv":
+            arr = getattr(blocks[b], kind)
+            for h in range(c.heads):
+                arr[h] = keep[f"b{b}_{kind}{h}"].ctypes.data
+        blocks[b].o = keep[f"b{b}_o"].ctypes.data
+        blocks[b].ff1 = keep[f"b{b}_ff1"].ctypes.data
+        blocks[b].ff2 = keep[f"b{b}_ff2"].ctypes.data
+        blocks[b].ff_th = float(keep[f"b{b}_ff_th"].ravel()[0])
+    sp = SaParams()
+    for n, key in (("in_q", "in_q"), ("in_k", "in_k"), ("in_v", "in_v"), ("pos", "pos_emb"),
+                   ("out", "out")):
+        setattr(sp, n, keep[key].ctypes.data)
+    sp.blocks = blocks
+    for n in ("out_gain", "beta", "q_th", "k_th", "v_th", "attn_th"):
+        setattr(sp, n, float(keep[n].ravel()[0]))
+    logits = np.zeros(c.classes, np.float32)
+    cfg = sa_cfg(c)
+    load().or_sa_forward_member(ctypes.byref(cfg), ctypes.byref(sp),
+                                np.ascontiguousarray(x, np.float32), logits)
+    return logits
+
+
+def sa_member_params(P, keys, leaves, sigma, rank, m, epoch=0, noise_reuse=0):
+    """Member m's parameters: W + A_m B_m^T (float64 product, rounded to f32) for
+    MM leaves, param + sign*sigma*noise for Parameter leaves."""
+    L = load()
+    bs = L.or_base_sigma(sigma, rank)
+    out = {}
+    for name, (a, b), cls in leaves:
+        if cls == 1:
+            A, B = lora_factors(bs, keys[name], rank, epoch, [m], a, b, noise_reuse=noise_reuse)
+            out[name] = (P[name].astype(np.float64)
+                         + A[0].astype(np.float64) @ B[0].T.astype(np.float64)).astype(np.float32)
+        else:
+            nz = np.zeros(a * b, np.float32)
+            L.or_get_nonlora_update_params(sigma, keys[name], epoch, m, a, b, noise_reuse, nz)
+            out[name] = P[name] + nz.reshape(a, b)
+    return out

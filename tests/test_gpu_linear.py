@@ -325,3 +325,20 @@ def test_linear_activation_unfused_path_matches(hses_gpu):
     torch.cuda.synchronize()
     ref = np.maximum(ref_forward(x[None], W, A, B, rpm)[0], 0) ** 2
     assert_close(y.cpu().numpy(), ref, 1e-5)
+
+
+@pytest.mark.parametrize("n,rpm,T,a,b,r,tid_lo,fmt", [
+    (1024, 1, 1, 10, 64, 8, 0, FMT_F32),     # C4 readout on pooled rows
+    (300, 2, 1, 70, 33, 8, 3, FMT_F32),      # output wider than a wave, odd first member
+    (130, 1, 2, 20, 100, 12, 0, FMT_BF16),   # time planes, bf16 activations
+])
+def test_rows_kernel_few_rows_per_member(hses_gpu, n, rpm, T, a, b, r, tid_lo, fmt):
+    # more members per 64-row tile than the small-rank kernel stages: one wave per member
+    rng = np.random.default_rng(n + a)
+    x3 = rng.standard_normal((T, n * rpm, b)).astype(np.float32)
+    if fmt == FMT_BF16:
+        x3 = bf16_round(x3)
+    W = (rng.standard_normal((a, b)) / np.sqrt(b)).astype(np.float32)
+    A, B = factors(0.2, r, n, tid_lo, a, b)
+    y = run(hses_gpu, x3, W, r, 0.2, n, rpm, tid_lo, fmt=fmt, math=MATH_F32)
+    assert_close(y, ref_forward(x3, W, A, B, rpm), 1e-5)
