@@ -237,6 +237,8 @@ using namespace hses;
 extern "C" size_t hses_perturbed_linear_workspace(int32_t a, int32_t b, int32_t rank, int32_t n,
                                                   int32_t rows_per_member, int32_t n_time,
                                                   int32_t math) {
+    if (math == HSES_MATH_F32)  // the fp32 GEMM's factor rows (k_linear_small needs none)
+        return linear_f32_workspace(a, b, rank, n, rows_per_member, n_time, math);
     if (a < 1 || b < 1 || n < 1 || rank < 16 || rank % 16 || rank > 128 || a > 128 ||
         math != HSES_MATH_BF16)
         // the wide-output kernel (bf16 W) or k_linear_small (no workspace)
@@ -420,7 +422,8 @@ static int run_linear(LinParams& P, DeviceState* st, float* d_y, int64_t y_strid
             return set_error(HSES_ERR_UNSUPPORTED,
                              std::string(name) + ": bf16 output needs the wide-output kernel (bf16 "
                              "math, members per 128-row tile x rank <= 16, aligned x rows)");
-        rc = launch_linear_small(P, st, s);
+        rc = launch_linear_f32(P, st, s, d_work, work_bytes);
+        if (rc == HSES_ERR_UNSUPPORTED) rc = launch_linear_small(P, st, s);
         if (rc == HSES_ERR_UNSUPPORTED && P.R <= 16) rc = launch_linear_rows(P, st, s);
     }
     if (rc == HSES_ERR_UNSUPPORTED)

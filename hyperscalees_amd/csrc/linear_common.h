@@ -133,6 +133,11 @@ struct LifOut {
 };
 
 int launch_linear_small(LinParams& P, DeviceState* st, hipStream_t s);
+// fp32 math, do_mm, rank <= 16: the members' A_m / B_m rows into the workspace,
+// then an fp32 MFMA GEMM with x B_m and (x B_m) A_m^T fused (linear_f32.hip).
+int launch_linear_f32(LinParams& P, DeviceState* st, hipStream_t s, void* work, size_t work_bytes);
+size_t linear_f32_workspace(int32_t a, int32_t b, int32_t r, int32_t n, int32_t rows_per_member,
+                            int32_t n_time, int32_t math);
 int launch_linear_pair(LinParams& P, DeviceState* st, hipStream_t s, void* work, size_t work_bytes,
                        const LifOut* lif = nullptr);
 size_t linear_pair_workspace(const DeviceState* st, int32_t a, int32_t b, int32_t r, int32_t n);

@@ -159,11 +159,11 @@ __device__ __forceinline__ float bm_normal(uint64_t& s, const NoiseCtx& c) {
 }
 
 // `count` consecutive normals of one stream; sink(i, value) receives normal i.
-// Batches of 4, software-pipelined (stage 1 of batch b+1 before stage 2 of
-// batch b); a tail of 1-3 is drawn singly.
-template <typename Sink>
+// Batches of G (4 by default), software-pipelined (stage 1 of batch b+1
+// before stage 2 of batch b); a tail of 1..G-1 is drawn singly.  A larger G
+// keeps more loads and f64 chains in flight where registers allow.
+template <int G = 4, typename Sink>
 __device__ __forceinline__ void bm_run(uint64_t& s, int32_t count, const NoiseCtx& c, Sink sink) {
-    constexpr int G = 4;
     int32_t i = 0;
     if (count >= G) {
         BmPending<G> p;

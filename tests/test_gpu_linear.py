@@ -82,6 +82,28 @@ def test_perturbed_linear_f32(hses_gpu, n, rpm, T, a, b, r, tid_lo):
     assert_close(y, ref_forward(x3, W, A, B, rpm), 1e-5)
 
 
+@pytest.mark.parametrize("n,rpm,T,a,b,r,tid_lo,fmt", [
+    (4, 48, 1, 300, 100, 16, 5, FMT_F32),    # rank 16, four members per tile, three column tiles
+    (6, 40, 2, 96, 300, 3, 2, FMT_BITS),     # rank 3 (padded to 4), bit-packed, time-major
+    (5, 64, 1, 64, 77, 5, 1, FMT_BF16),      # rank 5 (padded to 8), unaligned bf16 rows
+    (9, 16, 1, 40, 1000, 1, 0, FMT_F32),     # rank 1, 64-column tile, eight members per tile
+    (3, 200, 1, 130, 64, 8, 7, FMT_F32),     # members straddle tiles, 128 + 2 columns
+])
+def test_fp32_gemm_kernel(hses_gpu, n, rpm, T, a, b, r, tid_lo, fmt):
+    # the fp32 MFMA GEMM with x B_m fused and the members' factors drawn up front
+    rng = np.random.default_rng(n * 31 + a + b + r)
+    if fmt == FMT_BITS:
+        x3 = (rng.random((T, n * rpm, b)) < 0.3).astype(np.float32)
+    else:
+        x3 = rng.standard_normal((T, n * rpm, b)).astype(np.float32)
+        if fmt == FMT_BF16:
+            x3 = bf16_round(x3)
+    W = (rng.standard_normal((a, b)) / np.sqrt(b)).astype(np.float32)
+    A, B = factors(0.2, r, n, tid_lo, a, b)
+    y = run(hses_gpu, x3, W, r, 0.2, n, rpm, tid_lo, fmt=fmt, math=MATH_F32)
+    assert_close(y, ref_forward(x3, W, A, B, rpm), 1e-5)
+
+
 def test_perturbed_linear_spike_formats_agree(hses_gpu):
     # Binary inputs are exact in every format: F32, BF16 and packed bits give
     # the same bits for the same math mode.
