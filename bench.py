@@ -388,7 +388,7 @@ def bench_c1(args):
     K.init(0)
     es = snn.SnnEs(cfg, W, pool, labels, idx)
     ms = _timed_steps(lambda i: es.step(epoch=i), args.steps, args.warmup)
-    # dominant kernel: fc1's perturbed forward (k_linear_small, fp32 MFMA)
+    # dominant kernel: fc1's perturbed forward (k_factors + k_gemm_f32, fp32 MFMA)
     fc1 = lambda: K.perturbed_linear(es.spk[0], es.W[0], cfg.keys[0], cfg.rank, cfg.sigma, 0,
                                      cfg.noise_reuse, 0, cfg.n, cfg.rows, x_fmt=K.FMT_BITS,
                                      n_time=cfg.T, math=cfg.math, out=es.cur)
@@ -407,7 +407,8 @@ def bench_c1(args):
                                 "update + SGD)"),
                    "population": cfg.n, "rank": cfg.rank, "T": cfg.T, "parallelism": "single GPU"},
         "fwd_flop_per_step": sum(layer_flops(cfg, l) for l in range(len(cfg.dims) - 1)),
-        "roofline": {"kernel": "k_linear_small<F32 math, BITS x> (fc1, 8 x 16384 rows, 784 -> 128)",
+        "roofline": {"kernel": ("k_factors + k_gemm_f32<BITS x, 128 columns, rank 4> (fc1, 8 x 16384 "
+                                "rows, 784 -> 128)"),
                      "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP32_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_TFLOPS, 4),
                      "traffic": None, "launch_ms": round(fc1_ms, 4),
@@ -464,7 +465,8 @@ def bench_c2(args):
                    "population": n, "rank": r, "parallelism": "single GPU"},
         "phase_ms": {"forward": round(fwd_ms, 4), "es_update": round(upd_ms, 4)},
         "es_update_tflops": round(upd_fl / (upd_ms * 1e-3) / 1e12, 2),
-        "roofline": {"kernel": "k_linear_small<F32 math, F32 x> (65536 x 1024 -> 1024, r=1)",
+        "roofline": {"kernel": ("k_factors + k_gemm_f32<F32 x, 128 columns, rank 1> (65536 x 1024 "
+                                "-> 1024)"),
                      "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP32_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_TFLOPS, 4),
                      "traffic": None, "launch_ms": round(fwd_ms, 4),
@@ -576,7 +578,8 @@ def main():
         if es.fused:
             K.perturbed_linear_lif(es.spk[0], es.W[0], cfg.keys[0], cfg.rank, cfg.sigma, s,
                                    cfg.noise_reuse, 0, cfg.n, cfg.rows, cfg.T, cfg.tau_m,
-                                   cfg.v_th, spikes=es.spk[1])
+                                   cfg.v_th, spikes=es.spk[1],
+                                   rec=es.rec[0] if es.rec else None)
         else:
             K.perturbed_linear(es.spk[0], es.W[0], cfg.keys[0], cfg.rank, cfg.sigma, s,
                                cfg.noise_reuse, 0, cfg.n, cfg.rows, x_fmt=K.FMT_BITS,

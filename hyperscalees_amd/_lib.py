@@ -46,6 +46,16 @@ PROTOTYPES = {
                                                  c_vp, c_i64, c_vp, c_size, c_vp]),
     "hses_perturbed_linear_workspace": (c_size, [c_i32, c_i32, c_i32, c_i32, c_i32, c_i32,
                                                  c_i32]),
+    "hses_factor_record_bytes": (c_size, [c_i32, c_i32, c_i32, c_i32, c_i32]),
+    "hses_perturbed_linear_rec": (ctypes.c_int, [c_vp, c_i32, c_i64, c_i64, c_i32, c_vp, c_i32,
+                                                 c_i32, c_u64, c_i32, c_f32, c_i32, c_i32, c_i32,
+                                                 c_i32, c_i32, c_vp, c_i64, c_i64, c_i32, c_vp,
+                                                 c_size, c_vp, c_size, c_vp]),
+    "hses_perturbed_linear_lif_rec": (ctypes.c_int, [c_vp, c_i32, c_i64, c_i64, c_i32, c_vp,
+                                                     c_i32, c_i32, c_u64, c_i32, c_f32, c_i32,
+                                                     c_i32, c_i32, c_i32, c_i32, c_f32, c_f32,
+                                                     c_vp, c_i64, c_i64, c_vp, c_i64, c_vp,
+                                                     c_size, c_vp, c_size, c_vp]),
     "hses_perturbed_linear_t": (ctypes.c_int, [c_vp, c_i32, c_i64, c_i64, c_i32, c_vp, c_i32,
                                                c_i32, c_u64, c_i32, c_f32, c_i32, c_i32, c_i32,
                                                c_i32, c_i32, c_vp, c_i64, c_i64, c_i32, c_vp,
@@ -55,6 +65,8 @@ PROTOTYPES = {
     "hses_es_update_workspace": (c_size, [c_i32, c_i32, c_i32, c_i32]),
     "hses_es_update": (ctypes.c_int, [c_vp, c_i32, c_i32, c_u64, c_i32, c_f32, c_i32, c_i32,
                                       c_i32, c_i32, c_f32, c_i32, c_vp, c_vp, c_size, c_vp]),
+    "hses_es_update_rec": (ctypes.c_int, [c_vp, c_i32, c_i32, c_vp, c_size, c_i32, c_f32, c_i32,
+                                          c_i32, c_f32, c_i32, c_vp, c_vp, c_size, c_vp]),
     "hses_es_update_noalloc": (ctypes.c_int, [c_vp, c_i32, c_i32, c_u64, c_i32, c_f32, c_i32,
                                               c_i32, c_i32, c_i32, c_f32, c_i32, c_vp, c_vp]),
     "hses_noisy_standard": (ctypes.c_int, [c_vp, c_i32, c_i32, c_u64, c_f32, c_i32, c_i32, c_i32,

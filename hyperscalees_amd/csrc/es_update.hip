@@ -30,6 +30,8 @@
 // so the result is independent of the device.
 #include <math.h>
 
+#include <type_traits>
+
 #include "mfma.h"
 #include "noise_dev.h"
 #include "runtime.h"
@@ -54,6 +56,9 @@ struct UpdParams {
     const uint32_t* log_exc;
     const uint32_t* cos_exc;
     const uint64_t* jump;  // row length r
+    // k_es_rows<.., true>: the forward's factor record, pair pair_lo + i's raw
+    // normal of stream row j, rank c at rec[(i * r + c) * (a + b) + j]
+    const float* rec;
 };
 
 __host__ __device__ constexpr size_t align_up16(size_t x) { return (x + 15) & ~(size_t)15; }
@@ -228,7 +233,11 @@ __global__ __launch_bounds__(1024) void k_es_scale(const float* __restrict__ f, 
 // both sides, xh*yh + xh*yl + xl*yh (products exact in the fp32 accumulator)
 // differs from x*y by < 2^-20 |x y|, and the partial sums are S times the
 // fp32 ones (k_es_reduce divides S out).
-template <int NRT, int CT>
+// REC: the normals come from the factor record instead of the generator; the
+// next item's 32 values of this thread's row are loaded while the MFMAs of
+// the current item run and converted after them, so the operands, their
+// order and the result are those of the generating form.
+template <int NRT, int CT, bool REC>
 __global__ __launch_bounds__(R_MAXT) void k_es_rows(UpdParams P, RowTiles G) {
     static_assert(NRT <= 8, "the MFMA row tiles are interleaved with the 8 generation batches");
     extern __shared__ __align__(16) unsigned char smem[];
@@ -248,7 +257,7 @@ __global__ __launch_bounds__(R_MAXT) void k_es_rows(UpdParams P, RowTiles G) {
     const int32_t r = P.r;
     const int32_t chunks = (r + U_CW - 1) / U_CW;
 
-    load_bm_tables(tabs, P.tables);
+    if constexpr (!REC) load_bm_tables(tabs, P.tables);
     for (int i = tid; i < bufsz; i += blockDim.x)  // two buffers = bufsz words
         reinterpret_cast<uint32_t*>(buf0)[i] = 0u;
     __syncthreads();
@@ -327,13 +336,41 @@ __global__ __launch_bounds__(R_MAXT) void k_es_rows(UpdParams P, RowTiles G) {
             *reinterpret_cast<uint2*>(dst + U_CW + c) = uint2{0, 0};
         }
     };
+    // The record form: values of item (p, ch) of this thread's row into pv,
+    // then (after the MFMAs) into the LDS row as gen4 would have.
+    float pv[U_CW];
+    const int64_t rstride = (int64_t)P.a + P.b;  // floats between a row's ranks
+    auto load_item = [&](int32_t p, int32_t ch) {
+        const float* src = P.rec + ((int64_t)(p - P.pair_lo) * r + ch * U_CW) * rstride + srow;
+        const int32_t cn = min(U_CW, r - ch * U_CW);
+#pragma unroll
+        for (int c = 0; c < U_CW; ++c) pv[c] = c < cn ? src[c * rstride] : 0.0f;
+    };
+    auto store_item = [&](uint16_t* dst, int32_t cn, float w) {
+#pragma unroll
+        for (int c = 0; c < U_CW; c += 4) {
+            float x[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                x[e] = c + e < cn ? (is_a ? (pv[c + e] * P.bs) * w * S : pv[c + e]) : 0.0f;
+            uint2 hi, lo;
+            split_f16x4(x, &hi, &lo);
+            *reinterpret_cast<uint2*>(dst + c) = hi;
+            *reinterpret_cast<uint2*>(dst + U_CW + c) = lo;
+        }
+    };
     if (n_items > 0) {
-        start_pair(p_begin);
         uint16_t* dst = buf0 + grow * R_HP;
         const int32_t cn = min(U_CW, r);
         const float w0 = pair_weight(p_begin);
-        for (int32_t c = 0; c < cn; c += 4) gen4(dst, c, min(4, cn - c), w0);
-        zero_tail(dst, (cn + 3) & ~3);
+        if constexpr (REC) {
+            load_item(p_begin, 0);
+            store_item(dst, cn, w0);
+        } else {
+            start_pair(p_begin);
+            for (int32_t c = 0; c < cn; c += 4) gen4(dst, c, min(4, cn - c), w0);
+            zero_tail(dst, (cn + 3) & ~3);
+        }
     }
     __syncthreads();
     for (int32_t u = 0; u < n_items; ++u) {
@@ -341,7 +378,11 @@ __global__ __launch_bounds__(R_MAXT) void k_es_rows(UpdParams P, RowTiles G) {
         const bool has_next = u + 1 < n_items;
         const int32_t nch = (ch + 1 == chunks) ? 0 : ch + 1;
         const int32_t ncn = min(U_CW, r - nch * U_CW);
-        if (has_next && nch == 0) start_pair(p + 1);
+        if constexpr (REC) {
+            if (has_next) load_item(nch == 0 ? p + 1 : p, nch);
+        } else {
+            if (has_next && nch == 0) start_pair(p + 1);
+        }
         const float wn = has_next ? pair_weight(nch == 0 ? p + 1 : p) : 0.0f;
         const uint16_t* X = buf0 + (u & 1) * bufsz;
         uint16_t* nxt = buf0 + ((u + 1) & 1) * bufsz + grow * R_HP;
@@ -365,9 +406,14 @@ __global__ __launch_bounds__(R_MAXT) void k_es_rows(UpdParams P, RowTiles G) {
                     acc[i][j] = mfma_f16(al, bh[j], acc[i][j]);
                 }
             }
-            if (has_next && 4 * i < ncn) gen4(nxt, 4 * i, min(4, ncn - 4 * i), wn);
+            if constexpr (!REC)
+                if (has_next && 4 * i < ncn) gen4(nxt, 4 * i, min(4, ncn - 4 * i), wn);
         }
-        if (has_next && ncn < U_CW) zero_tail(nxt, (ncn + 3) & ~3);
+        if constexpr (REC) {
+            if (has_next) store_item(nxt, ncn, wn);
+        } else {
+            if (has_next && ncn < U_CW) zero_tail(nxt, (ncn + 3) & ~3);
+        }
         __syncthreads();
     }
 
@@ -504,7 +550,7 @@ static int es_update_impl(const float* d_f, int32_t n, int32_t tid_lo, uint64_t 
                           float sigma, int32_t epoch, int32_t noise_reuse, int32_t a, int32_t b,
                           float scale, int32_t accumulate, float* d_grad, void* d_work,
                           size_t work_bytes, size_t scratch_cap, DeviceState* st,
-                          hipStream_t s) {
+                          hipStream_t s, const float* rec = nullptr) {
     UpdParams P{};
     int32_t pair_lo, n_pairs;
     pair_range(tid_lo, n, &pair_lo, &n_pairs);
@@ -554,8 +600,13 @@ static int es_update_impl(const float* d_f, int32_t n, int32_t tid_lo, uint64_t 
     P.tables = st->d_tables;
     P.log_exc = st->d_log_exc;
     P.cos_exc = st->d_cos_exc;
-    rc = get_jump_table(st, rank, (int64_t)a + b, &P.jump);
-    if (rc) return rc;
+    P.rec = rec;
+    if (rec) {
+        HSES_REQUIRE(rows_k, "the factor record update needs rank >= 32");
+    } else {
+        rc = get_jump_table(st, rank, (int64_t)a + b, &P.jump);
+        if (rc) return rc;
+    }
     if (rows_k) {
         hipLaunchKernelGGL(k_es_scale, dim3(1), dim3(1024), 0, s, P.f, n, P.bs, d_scale);
         HSES_CHECK_HIP(hipGetLastError());
@@ -579,13 +630,15 @@ static int es_update_impl(const float* d_f, int32_t n, int32_t tid_lo, uint64_t 
                     HSES_CHECK_HIP(hipGetLastError());
                     return HSES_OK;
                 };
-                int lrc;
-                if (at <= 16)
-                    lrc = ct == 1 ? launch(k_es_rows<1, 1>) : ct == 2 ? launch(k_es_rows<1, 2>)
-                                                                : launch(k_es_rows<1, 3>);
-                else
-                    lrc = ct == 1 ? launch(k_es_rows<8, 1>) : ct == 2 ? launch(k_es_rows<8, 2>)
-                                                                : launch(k_es_rows<8, 3>);
+                auto by_src = [&](auto recc) -> int {
+                    constexpr bool RC = decltype(recc)::value;
+                    if (at <= 16)
+                        return ct == 1 ? launch(k_es_rows<1, 1, RC>)
+                               : ct == 2 ? launch(k_es_rows<1, 2, RC>) : launch(k_es_rows<1, 3, RC>);
+                    return ct == 1 ? launch(k_es_rows<8, 1, RC>)
+                           : ct == 2 ? launch(k_es_rows<8, 2, RC>) : launch(k_es_rows<8, 3, RC>);
+                };
+                const int lrc = rec ? by_src(std::true_type{}) : by_src(std::false_type{});
                 if (lrc) return lrc;
             }
         }
@@ -631,6 +684,36 @@ extern "C" int hses_es_update(const float* d_f, int32_t n, int32_t tid_lo, uint6
     if (rc) return rc;
     return es_update_impl(d_f, n, tid_lo, key, rank, sigma, epoch, noise_reuse, a, b, scale,
                           accumulate, d_grad, d_work, work_bytes, 0, st, (hipStream_t)stream);
+}
+
+// The ES update from the forward's factor record (hses_perturbed_linear_rec /
+// hses_perturbed_linear_lif_rec with the same tid_lo and n): the same
+// operands, tiles and order as hses_es_update, so the same result, without
+// drawing the normals again.
+extern "C" int hses_es_update_rec(const float* d_f, int32_t n, int32_t tid_lo, const float* d_rec,
+                                  size_t rec_bytes, int32_t rank, float sigma, int32_t a,
+                                  int32_t b, float scale, int32_t accumulate, float* d_grad,
+                                  void* d_work, size_t work_bytes, void* stream) {
+    int rc = es_update_check(n, tid_lo, rank, 0, a, b, d_grad);
+    if (rc) return rc;
+    const bool empty = n == 0 || rank == 0 || sigma == 0.0f;
+    if (!empty) {
+        HSES_REQUIRE(rank >= 32, "the factor record update needs rank >= 32");
+        HSES_REQUIRE(d_rec, "factor record is NULL");
+        int32_t lo, cnt;
+        pair_range(tid_lo, n, &lo, &cnt);
+        HSES_REQUIRE(rec_bytes >= (size_t)cnt * (size_t)(a + b) * rank * sizeof(float),
+                     "factor record smaller than hses_factor_record_bytes");
+        HSES_REQUIRE(d_f, "fitness is NULL");
+        HSES_REQUIRE(d_work && work_bytes >= align_up16((size_t)rows_splits(a, b, cnt) * a * b *
+                                                        sizeof(float)) + 16,
+                     "workspace too small");
+    }
+    DeviceState* st;
+    rc = get_state(&st);
+    if (rc) return rc;
+    return es_update_impl(d_f, n, tid_lo, 0, rank, sigma, 0, 0, a, b, scale, accumulate, d_grad,
+                          d_work, work_bytes, 0, st, (hipStream_t)stream, d_rec);
 }
 
 // ---- the allocation-free variant ---------------------------------------------

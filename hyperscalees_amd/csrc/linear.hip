@@ -484,21 +484,80 @@ extern "C" int hses_perturbed_linear_t(const void* d_x, int32_t x_fmt, int64_t x
                       "hses_perturbed_linear_t");
 }
 
-extern "C" int hses_perturbed_linear_lif(const void* d_x, int32_t x_fmt, int64_t x_stride,
+// ---- factor record --------------------------------------------------------------
+// The pair kernels can keep every pair's raw normals (B rows [0, b), A rows
+// [b, a + b) of the stream, before any scale) for the ES update of the same
+// parameter, which then reads them instead of drawing them again.
+
+static int64_t record_pairs(int32_t tid_lo, int32_t n) {
+    return n <= 0 ? 0 : (int64_t)(tid_lo + n - 1) / 2 - tid_lo / 2 + 1;
+}
+
+extern "C" size_t hses_factor_record_bytes(int32_t a, int32_t b, int32_t rank, int32_t tid_lo,
+                                           int32_t n) {
+    if (a < 1 || b < 1 || rank < 1 || tid_lo < 0 || n < 1) return 0;
+    return (size_t)record_pairs(tid_lo, n) * (size_t)(a + b) * rank * sizeof(float);
+}
+
+static int check_record(const LinParams& P, const float* d_rec, size_t rec_bytes, const char* name) {
+    HSES_REQUIRE(d_rec, "factor record is NULL");
+    HSES_REQUIRE(P.r >= 32 && P.r % 16 == 0 && P.r <= 128,
+                 std::string(name) + ": the factor record needs rank a multiple of 16 in "
+                                     "[32, 128] and sigma != 0");
+    HSES_REQUIRE(rec_bytes >= hses_factor_record_bytes(P.a, P.b, P.r, P.tid_lo, P.n),
+                 std::string(name) + ": factor record smaller than hses_factor_record_bytes");
+    return HSES_OK;
+}
+
+extern "C" int hses_perturbed_linear_rec(const void* d_x, int32_t x_fmt, int64_t x_stride,
                                          int64_t x_plane, int32_t n_time, const float* d_W,
                                          int32_t a, int32_t b, uint64_t key, int32_t rank,
                                          float sigma, int32_t epoch, int32_t noise_reuse,
                                          int32_t tid_lo, int32_t n, int32_t rows_per_member,
-                                         float tau_m, float v_th, uint64_t* d_spikes,
-                                         int64_t spk_stride, int64_t spk_plane, float* d_rate,
-                                         int64_t rate_stride, void* d_work, size_t work_bytes,
-                                         void* stream) {
+                                         float* d_y, int64_t y_stride, int64_t y_plane,
+                                         int32_t math, void* d_work, size_t work_bytes,
+                                         float* d_rec, size_t rec_bytes, void* stream) {
+    LinParams P;
+    DeviceState* st = nullptr;
+    int rc = make_params(&P, d_x, x_fmt, x_stride, x_plane, n_time, d_W, a, b, key, rank, sigma,
+                         epoch, noise_reuse, tid_lo, n, rows_per_member, math, &st);
+    if (rc || n == 0) return rc;
+    rc = check_record(P, d_rec, rec_bytes, "hses_perturbed_linear_rec");
+    if (rc) return rc;
+    HSES_REQUIRE(d_y, "NULL pointer");
+    HSES_REQUIRE(y_stride >= a, "y_stride smaller than a row");
+    HSES_REQUIRE(n_time == 1 || y_plane >= (int64_t)n * rows_per_member * y_stride,
+                 "time planes overlap");
+    P.y = d_y;
+    P.y_stride = y_stride;
+    P.y_plane = y_plane;
+    P.rec = d_rec;
+    rc = launch_linear_pair(P, st, (hipStream_t)stream, d_work, work_bytes);
+    if (rc == HSES_ERR_UNSUPPORTED)
+        return set_error(HSES_ERR_UNSUPPORTED,
+                         "hses_perturbed_linear_rec: the factor record needs the pair kernels "
+                         "(bf16 math, a <= 128)");
+    return rc;
+}
+
+static int linear_lif_impl(const void* d_x, int32_t x_fmt, int64_t x_stride, int64_t x_plane,
+                           int32_t n_time, const float* d_W, int32_t a, int32_t b, uint64_t key,
+                           int32_t rank, float sigma, int32_t epoch, int32_t noise_reuse,
+                           int32_t tid_lo, int32_t n, int32_t rows_per_member, float tau_m,
+                           float v_th, uint64_t* d_spikes, int64_t spk_stride, int64_t spk_plane,
+                           float* d_rate, int64_t rate_stride, void* d_work, size_t work_bytes,
+                           float* d_rec, size_t rec_bytes, void* stream) {
     HSES_REQUIRE(tau_m != 0.0f, "tau_m must be non-zero");
     LinParams P;
     DeviceState* st = nullptr;
     int rc = make_params(&P, d_x, x_fmt, x_stride, x_plane, n_time, d_W, a, b, key, rank, sigma,
                          epoch, noise_reuse, tid_lo, n, rows_per_member, HSES_MATH_BF16, &st);
     if (rc || n == 0) return rc;
+    if (d_rec || rec_bytes) {
+        rc = check_record(P, d_rec, rec_bytes, "hses_perturbed_linear_lif_rec");
+        if (rc) return rc;
+        P.rec = d_rec;
+    }
     HSES_REQUIRE(d_spikes || d_rate, "spikes and rate are both NULL");
     const int64_t M = (int64_t)n * rows_per_member;
     HSES_REQUIRE(!d_spikes || spk_stride >= (a + 63) / 64, "spk_stride smaller than a row");
@@ -514,6 +573,37 @@ extern "C" int hses_perturbed_linear_lif(const void* d_x, int32_t x_fmt, int64_t
         return set_error(HSES_ERR_UNSUPPORTED,
                          "hses_perturbed_linear_lif: needs rank a multiple of 16 <= 128 and a <= 128");
     return rc;
+}
+
+extern "C" int hses_perturbed_linear_lif(const void* d_x, int32_t x_fmt, int64_t x_stride,
+                                         int64_t x_plane, int32_t n_time, const float* d_W,
+                                         int32_t a, int32_t b, uint64_t key, int32_t rank,
+                                         float sigma, int32_t epoch, int32_t noise_reuse,
+                                         int32_t tid_lo, int32_t n, int32_t rows_per_member,
+                                         float tau_m, float v_th, uint64_t* d_spikes,
+                                         int64_t spk_stride, int64_t spk_plane, float* d_rate,
+                                         int64_t rate_stride, void* d_work, size_t work_bytes,
+                                         void* stream) {
+    return linear_lif_impl(d_x, x_fmt, x_stride, x_plane, n_time, d_W, a, b, key, rank, sigma,
+                           epoch, noise_reuse, tid_lo, n, rows_per_member, tau_m, v_th, d_spikes,
+                           spk_stride, spk_plane, d_rate, rate_stride, d_work, work_bytes, nullptr,
+                           0, stream);
+}
+
+extern "C" int hses_perturbed_linear_lif_rec(const void* d_x, int32_t x_fmt, int64_t x_stride,
+                                             int64_t x_plane, int32_t n_time, const float* d_W,
+                                             int32_t a, int32_t b, uint64_t key, int32_t rank,
+                                             float sigma, int32_t epoch, int32_t noise_reuse,
+                                             int32_t tid_lo, int32_t n, int32_t rows_per_member,
+                                             float tau_m, float v_th, uint64_t* d_spikes,
+                                             int64_t spk_stride, int64_t spk_plane, float* d_rate,
+                                             int64_t rate_stride, void* d_work, size_t work_bytes,
+                                             float* d_rec, size_t rec_bytes, void* stream) {
+    HSES_REQUIRE(d_rec, "factor record is NULL");
+    return linear_lif_impl(d_x, x_fmt, x_stride, x_plane, n_time, d_W, a, b, key, rank, sigma,
+                           epoch, noise_reuse, tid_lo, n, rows_per_member, tau_m, v_th, d_spikes,
+                           spk_stride, spk_plane, d_rate, rate_stride, d_work, work_bytes, d_rec,
+                           rec_bytes, stream);
 }
 
 extern "C" int hses_perturbed_linear_act(const void* d_x, int32_t x_fmt, int64_t x_stride,

@@ -60,6 +60,7 @@ struct LinParams {
     const uint32_t* log_exc;
     const uint32_t* cos_exc;
     const uint64_t* jump;
+    float* rec;  // factor record (pair kernels, do_mm), or NULL
 };
 
 // Physical offset (in units) of member-major logical row L: member m = L / R,

@@ -90,7 +90,24 @@ struct K2Args {
     int32_t tmm;    // do_Tmm stream roles (LinParams::tmm)
     int32_t x_vec;  // dense x: strides keep 8-element groups 16-byte aligned
     float bs, leak, v_th;
+    // Factor record (do_mm), or NULL: pair pair_lo + i's raw normals (before
+    // any scale) at rec[(i * r + c) * (a + b) + j] for stream row j, rank c.
+    float* rec;
 };
+
+// bm_run that also stores each raw normal i at rp[i * pitch] when rp is set
+// (the factor record; one branch per row, not per normal).
+template <typename Sink>
+__device__ __forceinline__ void bm_rec_run(uint64_t& s, int32_t count, const NoiseCtx& ctx,
+                                           float* rp, int32_t pitch, Sink sink) {
+    if (rp)
+        bm_run(s, count, ctx, [&](int32_t i, float v) {
+            rp[(size_t)i * pitch] = v;
+            sink(i, v);
+        });
+    else
+        bm_run(s, count, ctx, sink);
+}
 
 // Stream row j of a pair's factor stream: input-side operand row (staged in
 // the slot as [c][k]) or output-side row (LDS, [o][c]), and its scale.
@@ -371,12 +388,16 @@ __global__ __launch_bounds__(K2_THREADS) void k_linear_pair(const K2Args P) {
                                   &te, &tt, &sg);
                 uint64_t s = row_start_state(noise_seed(P.key, te, tt), uu, P.jump);
                 const StreamRow sr(P, j);
+                float* rp = P.rec ? P.rec + ((size_t)(pi0 + g * (int32_t)gridDim.x) * r + c0) * (a + b) + j
+                                  : nullptr;
                 if (sr.in_side) {
                     uint16_t* sg_ = slots + (size_t)g * r * kp + sr.row;
-                    bm_run(s, sl, ctx, [&](int32_t c, float v) { sg_[(size_t)(c0 + c) * kp] = f2bf(v * sr.scale); });
+                    bm_rec_run(s, sl, ctx, rp, a + b,
+                               [&](int32_t c, float v) { sg_[(size_t)(c0 + c) * kp] = f2bf(v * sr.scale); });
                 } else {
                     uint16_t* arow = As + (size_t)(g * a + sr.row) * lay.apitch;
-                    bm_run(s, sl, ctx, [&](int32_t c, float v) { arow[c0 + c] = f2bf(v * sr.scale); });
+                    bm_rec_run(s, sl, ctx, rp, a + b,
+                               [&](int32_t c, float v) { arow[c0 + c] = f2bf(v * sr.scale); });
                     if (c0 + sl == r)
                         for (int32_t c = r; c < rp32; ++c) arow[c] = 0;
                 }
@@ -679,12 +700,15 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
                 const int32_t j = u / segs, c0 = (u - j * segs) * sl;
                 uint64_t s = row_start_state(seed, u, P.jump);
                 const StreamRow sr(P, j);
+                float* rp = P.rec ? P.rec + ((size_t)pi * r + c0) * (a + b) + j : nullptr;
                 if (sr.in_side) {
                     uint16_t* dst = slot + sr.row;
-                    bm_run(s, sl, ctx, [&](int32_t c, float v) { dst[(size_t)(c0 + c) * kp] = f2bf(v * sr.scale); });
+                    bm_rec_run(s, sl, ctx, rp, a + b,
+                               [&](int32_t c, float v) { dst[(size_t)(c0 + c) * kp] = f2bf(v * sr.scale); });
                 } else {
                     uint16_t* dst = As + (size_t)sr.row * lay.apitch;
-                    bm_run(s, sl, ctx, [&](int32_t c, float v) { dst[swap23(c0 + c)] = f2bf(v * sr.scale); });
+                    bm_rec_run(s, sl, ctx, rp, a + b,
+                               [&](int32_t c, float v) { dst[swap23(c0 + c)] = f2bf(v * sr.scale); });
                     if (c0 + sl == r)  // r is a multiple of 16: the padding maps onto itself
                         for (int32_t c = r; c < rp32; ++c) dst[c] = 0;
                 }
@@ -1037,6 +1061,7 @@ int launch_linear_pair(LinParams& P, DeviceState* st, hipStream_t s, void* work,
     A.nreuse = P.nreuse;
     A.bs = P.bs;
     A.tmm = P.tmm;
+    A.rec = P.rec;
     {
         // 8 consecutive elements of a row start 16-byte aligned when the base,
         // the row stride and the plane stride all keep them so

@@ -147,12 +147,27 @@ def lif_scan(cur, tau_m, v_th, v0=None, fmt=FMT_F32, want_v=False, out=None):
     return (spk, v_out) if want_v else spk
 
 
+def factor_record(a, b, rank, tid_lo, n, device="cuda"):
+    """A factor record buffer for the members [tid_lo, tid_lo + n) of an (a, b)
+    parameter (hses_factor_record_bytes)."""
+    nbytes = int(_lib.load().hses_factor_record_bytes(a, b, rank, tid_lo, n))
+    if nbytes == 0:
+        raise ValueError("no factor record for this shape")
+    return torch.empty(nbytes // 4, dtype=torch.float32, device=device)
+
+
+def _rec_arg(rec):
+    _dev(rec, torch.float32, "rec")
+    return _p(rec), rec.numel() * 4
+
+
 def perturbed_linear(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n, rows_per_member,
                      x_fmt=FMT_F32, x_width=None, n_time=1, math=MATH_F32, out=None, act=0,
-                     out_bf16=False):
+                     out_bf16=False, rec=None):
     """Batched do_mm.  x is (n_time, n*rows_per_member, units) in x_fmt (or 2-D
     when n_time == 1); returns y (n_time, n*rows_per_member, a) fp32 (bf16 with
-    out_bf16), passed through the activation `act` (hses_act) when it is not 0."""
+    out_bf16), passed through the activation `act` (hses_act) when it is not 0.
+    With `rec` (factor_record) the pairs' normals are also kept there."""
     a, b = W.shape
     _dev(W, torch.float32, "W")
     _dev(x, _FMT_DTYPE[x_fmt], "x")
@@ -169,7 +184,14 @@ def perturbed_linear(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n, rows
     wbytes = int(_lib.load().hses_perturbed_linear_workspace(a, b, rank, n, rows_per_member,
                                                               n_time, math))
     work = _workspace(wbytes, W.device)
-    if act or out_bf16:
+    if rec is not None:
+        if act or out_bf16:
+            raise ValueError("the factor record is kept by the plain fp32-output forward only")
+        _lib.call("hses_perturbed_linear_rec", _p(x), x_fmt, units, M * units, n_time, _p(W), a,
+                  b, key & (2**64 - 1), rank, sigma, epoch, noise_reuse, tid_lo, n,
+                  rows_per_member, _p(out), a, M * a, math, _p(work), wbytes, *_rec_arg(rec),
+                  _stream())
+    elif act or out_bf16:
         _lib.call("hses_perturbed_linear_act", _p(x), x_fmt, units, M * units, n_time, _p(W), a,
                   b, key & (2**64 - 1), rank, sigma, epoch, noise_reuse, tid_lo, n,
                   rows_per_member, _p(out), a, M * a, math, 0, act,
@@ -216,9 +238,10 @@ def perturbed_linear_t(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n, ro
 
 def perturbed_linear_lif(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n,
                          rows_per_member, n_time, tau_m, v_th, spikes=None, rate=None,
-                         want_spikes=True, want_rate=False):
+                         want_spikes=True, want_rate=False, rec=None):
     """Perturbed forward fused with LIF.  x is bit-packed (n_time, M, words(b));
-    returns (spikes (n_time, M, words(a)) int64 or None, rate (M, a) or None)."""
+    returns (spikes (n_time, M, words(a)) int64 or None, rate (M, a) or None).
+    With `rec` (factor_record) the pairs' normals are also kept there."""
     a, b = W.shape
     _dev(W, torch.float32, "W")
     _dev(x, _FMT_DTYPE[FMT_BITS], "x")
@@ -242,10 +265,14 @@ def perturbed_linear_lif(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n,
     wbytes = int(_lib.load().hses_perturbed_linear_workspace(a, b, rank, n, rows_per_member,
                                                               n_time, MATH_BF16))
     work = _workspace(wbytes, W.device)
-    _lib.call("hses_perturbed_linear_lif", _p(x), FMT_BITS, units, M * units, n_time, _p(W), a,
-              b, key & (2**64 - 1), rank, sigma, epoch, noise_reuse, tid_lo, n, rows_per_member,
-              tau_m, v_th, _p(spikes) if spikes is not None else None, wa, M * wa,
-              _p(rate) if rate is not None else None, a, _p(work), wbytes, _stream())
+    args = (_p(x), FMT_BITS, units, M * units, n_time, _p(W), a, b, key & (2**64 - 1), rank,
+            sigma, epoch, noise_reuse, tid_lo, n, rows_per_member, tau_m, v_th,
+            _p(spikes) if spikes is not None else None, wa, M * wa,
+            _p(rate) if rate is not None else None, a, _p(work), wbytes)
+    if rec is None:
+        _lib.call("hses_perturbed_linear_lif", *args, _stream())
+    else:
+        _lib.call("hses_perturbed_linear_lif_rec", *args, *_rec_arg(rec), _stream())
     return spikes, rate
 
 
@@ -264,6 +291,23 @@ def es_update(fit, tid_lo, key, rank, sigma, epoch, noise_reuse, a, b, scale, ou
     _lib.call("hses_es_update", _p(fit), n, tid_lo, key & (2**64 - 1), rank, sigma, epoch,
               noise_reuse, a, b, scale, int(bool(accumulate)), _p(out), _p(work), wbytes,
               _stream())
+    return out
+
+
+def es_update_rec(fit, tid_lo, rec, rank, sigma, a, b, scale, out=None, accumulate=False,
+                  work=None):
+    """es_update from the factor record a forward over the same members kept
+    (the same result as es_update, without drawing the normals again)."""
+    _dev(fit, torch.float32, "fit")
+    n = fit.numel()
+    lib = _lib.load()
+    wbytes = int(lib.hses_es_update_workspace(a, b, rank, n))
+    if work is None or work.numel() < wbytes:
+        work = _workspace(wbytes, fit.device)
+    if out is None:
+        out = torch.zeros((a, b), dtype=torch.float32, device=fit.device)
+    _lib.call("hses_es_update_rec", _p(fit), n, tid_lo, *_rec_arg(rec), rank, sigma, a, b, scale,
+              int(bool(accumulate)), _p(out), _p(work), wbytes, _stream())
     return out
 
 

@@ -112,7 +112,8 @@ def init_weights(dims, seed=0, gain=1.0):
 class SnnEs:
     """Device-resident SNN-MLP population evaluation and ES update."""
 
-    def __init__(self, cfg, weights, pool, pool_labels, index, device="cuda", fused=None):
+    def __init__(self, cfg, weights, pool, pool_labels, index, device="cuda", fused=None,
+                 record=None):
         self.cfg = cfg
         c = cfg
         self.dev = device
@@ -146,6 +147,22 @@ class SnnEs:
         self.m = [torch.zeros_like(w) for w in self.W]
         self.v = [torch.zeros_like(w) for w in self.W]
         self.step_t = 0
+        # Factor records: the fused forward keeps every pair's normals so the
+        # ES update reads them instead of drawing them again (rank >= 32; the
+        # readout runs on the same pair kernels).  Sized for a chunk starting
+        # at an even or an odd member.
+        can_record = self.fused and c.rank >= 32 and c.dims[-1] <= 128
+        self.record = can_record if record is None else (bool(record) and can_record)
+        self.rec = None
+        if self.record:
+            self.rec = []
+            for w in self.W:
+                a, b = w.shape
+                n_odd = c.chunk if c.accumulate > 1 and c.chunk % 2 else 0
+                nbytes = max(K._lib.load().hses_factor_record_bytes(a, b, c.rank, t, c.chunk)
+                             for t in (0, n_odd))
+                self.rec.append(torch.empty(nbytes // 4, dtype=torch.float32, device=device))
+        self._rec_at = [None] * L  # per layer: (epoch, lo) of the forward its record holds
 
     # -- forward -------------------------------------------------------------
     def chunk_seeds(self, lo):
@@ -173,7 +190,10 @@ class SnnEs:
                                    c.noise_reuse, lo, c.chunk, c.rows, c.T, c.tau_m, c.v_th,
                                    spikes=None if last else self.spk[l + 1],
                                    rate=self.rate if last else None,
-                                   want_spikes=not last, want_rate=last)
+                                   want_spikes=not last, want_rate=last,
+                                   rec=self.rec[l] if self.rec else None)
+            if self.rec:
+                self._rec_at[l] = (epoch, lo)
             return
         cur = self.cur[:, :, :a] if a == self.cur.shape[2] else \
             self.cur.view(-1)[: c.T * self.M * a].view(c.T, self.M, a)
@@ -188,7 +208,10 @@ class SnnEs:
             K.spike_rate(self.spk[self.L - 1], FMT_BITS, c.dims[-2], out=self.rate)
         K.perturbed_linear(self.rate, self.W[-1], c.keys[-1], c.rank, c.sigma, epoch,
                            c.noise_reuse, lo, c.chunk, c.rows, x_fmt=FMT_F32, n_time=1,
-                           math=c.math, out=self.logits.view(1, self.M, -1))
+                           math=c.math, out=self.logits.view(1, self.M, -1),
+                           rec=self.rec[-1] if self.rec else None)
+        if self.rec:
+            self._rec_at[-1] = (epoch, lo)
         labels = self.labels[lo * c.rows:(lo + c.chunk) * c.rows]
         return K.member_fitness(self.logits, labels, c.chunk, c.rows, c.reward,
                                 out=self.raw[lo:lo + c.chunk], correct=self.correct)
@@ -199,6 +222,18 @@ class SnnEs:
         for l in range(self.L - 1):
             self.hidden_layer(l, epoch, lo)
         return self.readout(epoch, lo)
+
+    def _grad(self, l, fit, lo, epoch, scale, accumulate=False):
+        """grads[l] (+)= scale * sum_m fit[m] A_m B_m^T over members [lo, lo + len(fit)),
+        from the factor records when they hold this epoch's chunk."""
+        c = self.cfg
+        a, b = self.W[l].shape
+        if self.rec is not None and self._rec_at[l] == (epoch, lo) and fit.numel() == c.chunk:
+            K.es_update_rec(fit, lo, self.rec[l], c.rank, c.sigma, a, b, scale,
+                            out=self.grads[l], accumulate=accumulate)
+        else:
+            K.es_update(fit, lo, c.keys[l], c.rank, c.sigma, epoch, c.noise_reuse, a, b, scale,
+                        out=self.grads[l], accumulate=accumulate)
 
     # -- update --------------------------------------------------------------
     def _solve(self, l, gscale):
@@ -220,9 +255,7 @@ class SnnEs:
         self.step_t += 1
         clip = c.max_norm > 0.0  # the global norm needs every gradient before any step
         for l in range(self.L):
-            a, b = self.W[l].shape
-            K.es_update(z, 0, c.keys[l], c.rank, c.sigma, epoch, c.noise_reuse, a, b, scale,
-                        out=self.grads[l])
+            self._grad(l, z, 0, epoch, scale)
             if not clip:
                 self._solve(l, None)
         if clip:
@@ -254,9 +287,7 @@ class SnnEs:
             raw = self.forward(epoch, lo)
             K.fitness_moments(raw, self.moments, accumulate=k > 0)
             for l in range(self.L):
-                a, b = self.W[l].shape
-                K.es_update(raw, lo, c.keys[l], c.rank, c.sigma, epoch, c.noise_reuse, a, b,
-                            np.float32(1.0), out=self.grads[l], accumulate=k > 0)
+                self._grad(l, raw, lo, epoch, np.float32(1.0), accumulate=k > 0)
         one = torch.ones(1, dtype=torch.float32, device=self.dev) if c.n % 2 else None
         self.step_t += 1
         for l in range(self.L):

@@ -242,6 +242,44 @@ int hses_perturbed_linear_lif(const void *d_x, int32_t x_fmt, int64_t x_stride, 
                               float *d_rate, int64_t rate_stride, void *d_work,
                               size_t work_bytes, void *stream);
 
+/* ---- factor record -------------------------------------------------------
+ * The update of a parameter needs the same per-member factors as its forward:
+ * the reference draws them for the forward (do_mm, eggroll.rs:419-446) and again
+ * as materialised (n, a, r) / (n, b, r) tensors for the update
+ * (get_lora_update_params / batched_lora_noise inside _simple_lora_update,
+ * eggroll.rs:353-404).  A factor record keeps the normals the forward draws so
+ * the update reads them instead: one block per antithetic pair p of the
+ * members [tid_lo, tid_lo + n) (pairs tid_lo / 2 .. (tid_lo + n - 1) / 2), the
+ * raw normal of stream row j (B rows [0, b), then A rows) and rank c at
+ *   rec[((p - tid_lo / 2) * rank + c) * (a + b) + j]   (fp32, before any scale).
+ * Rank a multiple of 16 in [32, 128], sigma != 0, do_mm only. */
+
+/* Bytes of the record of members [tid_lo, tid_lo + n) of an (a, b) parameter. */
+size_t hses_factor_record_bytes(int32_t a, int32_t b, int32_t rank, int32_t tid_lo, int32_t n);
+
+/* hses_perturbed_linear (bf16 math, a <= 128: the pair kernels) that also
+ * writes the factor record of its members to d_rec (rec_bytes >=
+ * hses_factor_record_bytes).  y is identical to hses_perturbed_linear's. */
+int hses_perturbed_linear_rec(const void *d_x, int32_t x_fmt, int64_t x_stride, int64_t x_plane,
+                              int32_t n_time, const float *d_W, int32_t a, int32_t b,
+                              uint64_t key, int32_t rank, float sigma, int32_t epoch,
+                              int32_t noise_reuse, int32_t tid_lo, int32_t n,
+                              int32_t rows_per_member, float *d_y, int64_t y_stride,
+                              int64_t y_plane, int32_t math, void *d_work, size_t work_bytes,
+                              float *d_rec, size_t rec_bytes, void *stream);
+
+/* hses_perturbed_linear_lif that also writes the factor record of its members;
+ * spikes and rates are identical to hses_perturbed_linear_lif's. */
+int hses_perturbed_linear_lif_rec(const void *d_x, int32_t x_fmt, int64_t x_stride,
+                                  int64_t x_plane, int32_t n_time, const float *d_W, int32_t a,
+                                  int32_t b, uint64_t key, int32_t rank, float sigma,
+                                  int32_t epoch, int32_t noise_reuse, int32_t tid_lo, int32_t n,
+                                  int32_t rows_per_member, float tau_m, float v_th,
+                                  uint64_t *d_spikes, int64_t spk_stride, int64_t spk_plane,
+                                  float *d_rate, int64_t rate_stride, void *d_work,
+                                  size_t work_bytes, float *d_rec, size_t rec_bytes,
+                                  void *stream);
+
 /* ---- ES update ------------------------------------------------------- */
 
 /* EggRoll ES gradient of one MM parameter (eggroll.rs:353-404 _simple_lora_update +
@@ -269,6 +307,15 @@ int hses_es_update_noalloc(const float *d_f, int32_t n, int32_t tid_lo, uint64_t
                            int32_t rank, float sigma, int32_t epoch, int32_t noise_reuse,
                            int32_t a, int32_t b, float scale, int32_t accumulate, float *d_grad,
                            void *stream);
+
+/* hses_es_update (same reference functions) of members [tid_lo, tid_lo + n)
+ * reading their normals from the factor record a *_rec forward over the same
+ * tid_lo and n wrote (rank >= 32): the same result, bit for bit, without
+ * drawing the normals again.  Workspace: hses_es_update_workspace. */
+int hses_es_update_rec(const float *d_f, int32_t n, int32_t tid_lo, const float *d_rec,
+                       size_t rec_bytes, int32_t rank, float sigma, int32_t a, int32_t b,
+                       float scale, int32_t accumulate, float *d_grad, void *d_work,
+                       size_t work_bytes, void *stream);
 
 /* ---- fitness, z-score, solver ----------------------------------------- */
 

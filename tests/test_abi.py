@@ -120,6 +120,23 @@ def test_validation_rejects_bad_arguments_without_a_gpu():
                         64e-5, P[22], P[alias], 1, P[23], NULL)
 
 
+def test_factor_record_bytes_and_validation():
+    lib = _lib.load()
+    c = ctypes.c_void_p
+    # members [1, 5) span pairs 0, 1, 2; members [0, 4) pairs 0, 1
+    assert lib.hses_factor_record_bytes(10, 20, 32, 1, 4) == 3 * 30 * 32 * 4
+    assert lib.hses_factor_record_bytes(10, 20, 32, 0, 4) == 2 * 30 * 32 * 4
+    assert lib.hses_factor_record_bytes(10, 20, 32, 0, 0) == 0
+    assert lib.hses_factor_record_bytes(10, 20, 0, 0, 4) == 0
+    # update from a record: rank >= 32, a record, and one large enough
+    _expect_invalid("hses_es_update_rec", c(16), 8, 0, c(16), 1 << 20, 16, 0.02, 16, 16, 1.0, 0,
+                    c(16), c(16), 1 << 20, NULL)
+    _expect_invalid("hses_es_update_rec", c(16), 8, 0, NULL, 1 << 20, 32, 0.02, 16, 16, 1.0, 0,
+                    c(16), c(16), 1 << 20, NULL)
+    _expect_invalid("hses_es_update_rec", c(16), 8, 0, c(16), 4 * 32 * 32 * 4 - 4, 32, 0.02, 16,
+                    16, 1.0, 0, c(16), c(16), 1 << 20, NULL)
+
+
 def test_empty_inputs_are_no_ops_without_a_gpu():
     lib = _lib.load()
     assert lib.hses_poisson_encode(NULL, 0, NULL, 0, 784, 784, 8, 0, 0, 0, 0, NULL, 0, 784, NULL) == 0
