@@ -85,11 +85,24 @@ __global__ __launch_bounds__(KF_THREADS) void k_gemm_f32(LinParams P, const floa
     // without noise) is the host's, which sized the LDS.
     const int32_t bufsz = (KF_BM + BN) * KF_XP + bch;
     float* buf = reinterpret_cast<float*>(smem);
-    float* As = buf + 2 * bufsz;
+    // one staging buffer when K is a single chunk (b <= 32), else two
+    float* As = buf + (P.b > KF_BK ? 2 : 1) * bufsz;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int32_t lc = lane & 31, kh = lane >> 5;
-    const int64_t L0 = (int64_t)blockIdx.x * KF_BM;
-    const int32_t o0 = blockIdx.y * BN;
+    // Tile of this workgroup: workgroups are dealt to the 8 XCDs in turn, so
+    // XCD x gets the contiguous tile range x * nb / 8 .. with the column tiles
+    // of a row tile adjacent: the workgroups that read the same x rows run on
+    // one XCD together and share its L2.
+    int64_t L0;
+    int32_t o0;
+    {
+        const uint32_t nb = gridDim.x, g = blockIdx.x, xcd = g & 7u, j = g >> 3;
+        const uint32_t q = nb >> 3, rem = nb & 7u;
+        const uint32_t t = xcd < rem ? xcd * (q + 1) + j : rem * (q + 1) + (xcd - rem) * q + j;
+        const uint32_t ncol = (uint32_t)((P.a + BN - 1) / BN);
+        L0 = (int64_t)(t / ncol) * KF_BM;
+        o0 = (int32_t)(t % ncol) * BN;
+    }
     const int32_t ct = min(BN, P.a - o0);
     const int32_t R = P.R, r = P.r, b = P.b;
     const int64_t Llast = min<int64_t>(L0 + KF_BM, P.total) - 1;
@@ -351,7 +364,8 @@ static bool f32_plan(const LinParams& P, F32Plan* pl) {
     pl->bch = (int32_t)bch;
     const size_t a_lds = r > 0 ? (size_t)pl->nm * pl->bn * pl->rk : 0;
     if (a_lds > KF_AMAX) return false;
-    pl->lds = (2 * ((size_t)(KF_BM + pl->bn) * KF_XP + bch) + a_lds) * 4;
+    const size_t nbuf = P.b > KF_BK ? 2 : 1;  // staging buffers (k_gemm_f32)
+    pl->lds = (nbuf * ((size_t)(KF_BM + pl->bn) * KF_XP + bch) + a_lds) * 4;
     pl->rc = 1;
     pl->groups = 0;
     pl->f_bytes = 0;
@@ -414,7 +428,8 @@ int launch_linear_f32(LinParams& P, DeviceState* st, hipStream_t s, void* work, 
     if (pl.lds > st->max_lds) return HSES_ERR_UNSUPPORTED;
     if (P.r > 0 && (!work || work_bytes < pl.f_bytes)) return HSES_ERR_UNSUPPORTED;
     const int64_t row_tiles = (P.total + KF_BM - 1) / KF_BM;
-    if (row_tiles > INT32_MAX) return set_error(HSES_ERR_INVALID_ARG, "too many output rows");
+    const int64_t tiles = row_tiles * ((P.a + pl.bn - 1) / pl.bn);
+    if (tiles > INT32_MAX) return set_error(HSES_ERR_INVALID_ARG, "too many output rows");
     float* F = static_cast<float*>(work);
     if (P.r > 0) {
         int rc = get_jump_table(st, (int64_t)pl.rc * P.r, pl.groups, &P.jump);
@@ -425,7 +440,7 @@ int launch_linear_f32(LinParams& P, DeviceState* st, hipStream_t s, void* work, 
         hipLaunchKernelGGL(k_factors, dim3((uint32_t)blocks), dim3(256), 0, s, P, pl.rc, pl.groups, F);
         HSES_CHECK_HIP(hipGetLastError());
     }
-    const dim3 grid((uint32_t)row_tiles, (uint32_t)((P.a + pl.bn - 1) / pl.bn));
+    const dim3 grid((uint32_t)tiles);
     switch (P.x_fmt) {
         case HSES_FMT_BITS: return launch_gemm_bn<HSES_FMT_BITS>(P, pl, s, F, grid);
         case HSES_FMT_BF16: return launch_gemm_bn<HSES_FMT_BF16>(P, pl, s, F, grid);
