@@ -70,6 +70,26 @@ __global__ __launch_bounds__(256) void k_factors(LinParams P, int32_t rc, int32_
            [&](int32_t i, float v) { dst[i] = i >= split ? v * sc : v; });
 }
 
+// Rows of a tile: row L0 + i (i < 128) is member m_first + dm of the tile
+// with dm, its time plane and slot from 32-bit divisions of rem0 + i (the
+// 64-bit division by R happens once per workgroup).
+struct TileRows {
+    int32_t m_first, rem0;
+    __device__ __forceinline__ TileRows(const LinParams& P, int64_t L0) {
+        m_first = (int32_t)(L0 / P.R);
+        rem0 = (int32_t)(L0 - (int64_t)m_first * P.R);
+    }
+    __device__ __forceinline__ int32_t member(const LinParams& P, int32_t i) const {
+        return (rem0 + i) / P.R;
+    }
+    __device__ __forceinline__ int64_t offset(const LinParams& P, int32_t i, int64_t stride,
+                                              int64_t plane) const {
+        const int32_t rr = rem0 + i, dm = rr / P.R, rem = rr - dm * P.R;
+        const int32_t t = rem / P.rpm, s = rem - t * P.rpm;
+        return t * plane + ((int64_t)(m_first + dm) * P.rpm + s) * stride;
+    }
+};
+
 // ---- k_gemm_f32 ------------------------------------------------------------------
 // NT 32-column MFMA tiles per wave (BN = 32 NT); four waves of 32 rows.  RK is
 // the rank padded to 1, 4, 8 or 16 (the LDS copies of B_m and A_m rows hold RK
@@ -98,16 +118,18 @@ __global__ __launch_bounds__(KF_THREADS) void k_gemm_f32(LinParams P, const floa
     {
         const uint32_t nb = gridDim.x, g = blockIdx.x, xcd = g & 7u, j = g >> 3;
         const uint32_t q = nb >> 3, rem = nb & 7u;
-        const uint32_t t = xcd < rem ? xcd * (q + 1) + j : rem * (q + 1) + (xcd - rem) * q + j;
         const uint32_t ncol = (uint32_t)((P.a + BN - 1) / BN);
+        const uint32_t t = ncol == 1 ? g  // one column tile: no x rows are shared
+                           : xcd < rem ? xcd * (q + 1) + j : rem * (q + 1) + (xcd - rem) * q + j;
         L0 = (int64_t)(t / ncol) * KF_BM;
         o0 = (int32_t)(t % ncol) * BN;
     }
     const int32_t ct = min(BN, P.a - o0);
-    const int32_t R = P.R, r = P.r, b = P.b;
-    const int64_t Llast = min<int64_t>(L0 + KF_BM, P.total) - 1;
-    const int32_t m_first = (int32_t)(L0 / R);
-    const int32_t nm = (int32_t)(Llast / R) - m_first + 1;
+    const int32_t r = P.r, b = P.b;
+    const int32_t rows_here = (int32_t)min<int64_t>(KF_BM, P.total - L0);
+    const TileRows tr(P, L0);
+    const int32_t m_first = tr.m_first;
+    const int32_t nm = tr.member(P, rows_here - 1) + 1;
     const bool noisy = r > 0;
     const int64_t fpitch = (int64_t)(P.a + b) * r;  // floats of one member's factors
     const float* Fm = F + (int64_t)m_first * fpitch;
@@ -124,8 +146,8 @@ __global__ __launch_bounds__(KF_THREADS) void k_gemm_f32(LinParams P, const floa
     const int xr = tid >> 1, xk = (tid & 1) * 16;
     const int64_t Lx = L0 + xr;
     const bool xvalid = Lx < P.total;
-    const int64_t xoff = xvalid ? phys_row(P, Lx, P.x_stride, P.x_plane) : 0;
-    const int32_t xlm = xvalid ? (int32_t)(Lx / R) - m_first : 0;  // the x row's member
+    const int64_t xoff = xvalid ? tr.offset(P, xr, P.x_stride, P.x_plane) : 0;
+    const int32_t xlm = xvalid ? tr.member(P, xr) : 0;  // the x row's member in the tile
     constexpr int WPT = BN * KF_BK / KF_THREADS;  // W values per thread: 16, 8 or 4
     constexpr int WTPR = KF_BK / WPT;             // threads per W row
     const int wr = tid / WTPR, wk = (tid % WTPR) * WPT;
@@ -312,8 +334,8 @@ __global__ __launch_bounds__(KF_THREADS) void k_gemm_f32(LinParams P, const floa
         const int32_t row = wave * 32 + 8 * (e >> 2) + 4 * kh + (e & 3);
         const int64_t L = L0 + row;
         if (L >= P.total) continue;
-        const int32_t lm = (int32_t)(L / R) - m_first;
-        float* yrow = P.y + phys_row(P, L, P.y_stride, P.y_plane) + o0;
+        const int32_t lm = tr.member(P, row);
+        float* yrow = P.y + tr.offset(P, row, P.y_stride, P.y_plane) + o0;
         float xr_[RK];
 #pragma unroll
         for (int c = 0; c < RK; ++c) xr_[c] = noisy ? XBs[row * RK + c] : 0.0f;
