@@ -248,17 +248,19 @@ def _events(n):
 
 
 def _time_launch(fn, reps=5):
-    """Median duration (ms) of fn's launches, HIP events on the launch stream."""
+    """Mean duration (ms) of fn's launches: `reps` back-to-back calls between two
+    HIP events on the launch stream, after one untimed call.  The host enqueues
+    ahead of the GPU, so its per-call overhead does not show as GPU idle time."""
     import torch
-    ts = []
+    fn()
+    torch.cuda.synchronize()
+    e0, e1 = _events(2)
+    e0.record()
     for _ in range(reps):
-        e0, e1 = _events(2)
-        e0.record()
         fn()
-        e1.record()
-        torch.cuda.synchronize()
-        ts.append(e0.elapsed_time(e1))
-    return float(np.median(ts))
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
 
 
 def _timed_steps(step, steps, warmup):
@@ -591,6 +593,22 @@ def main():
     fc1_flops = layer_flops(cfg, 0)
     achieved = fc1_flops / (fc1_ms * 1e-3) / 1e12
 
+    # fc1's ES update from the factor record (HBM-bound): algorithmic bytes are
+    # the record (pairs x r x (a + b) fp32) plus the gradient written.
+    upd_roof = None
+    if es.rec is not None:
+        a1, b1 = es.W[0].shape
+        zf = torch.randn(cfg.n, device="cuda")
+        scale1 = np.float32(-math.sqrt(cfg.n) / cfg.n)
+        upd1_ms = _time_launch(lambda: K.es_update_rec(zf, 0, es.rec[0], cfg.rank, cfg.sigma, a1,
+                                                       b1, scale1, out=es.grads[0]), reps=5)
+        rec_bytes = (cfg.n // 2) * cfg.rank * (a1 + b1) * 4 + a1 * b1 * 4
+        gbs = rec_bytes / (upd1_ms * 1e-3) / 1e9
+        upd_roof = {"kernel": "k_es_rows<.., record> + k_es_reduce (fc1 ES update from the factor record)",
+                    "bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBPS,
+                    "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBPS, 4),
+                    "launch_ms": round(upd1_ms, 4), "algorithmic_bytes_per_launch": rec_bytes}
+
     fwd_flops = sum(layer_flops(cfg, l) for l in range(L))
     out = {
         "metric": METRIC,
@@ -628,6 +646,8 @@ def main():
                      "launch_ms": round(fc1_ms, 3),
                      "algorithmic_flop_per_launch": fc1_flops},
     }
+    if upd_roof is not None:
+        out["es_update_roofline"] = upd_roof
     if not args.no_cpu_baseline:
         threads, _, _ = host_cpu()
         out["cpu_baseline"] = cpu_baseline(cfg, pool, labels, idx, W, args.cpu_members, threads)
