@@ -241,8 +241,10 @@ extern "C" size_t hses_perturbed_linear_workspace(int32_t a, int32_t b, int32_t 
         return linear_f32_workspace(a, b, rank, n, rows_per_member, n_time, math);
     if (a < 1 || b < 1 || n < 1 || rank < 16 || rank % 16 || rank > 128 || a > 128 ||
         math != HSES_MATH_BF16)
-        // the wide-output kernel (bf16 W) or k_linear_small (no workspace)
-        return linear_wide_workspace(a, b, rank, n, rows_per_member, n_time, math);
+        // the bf16 GEMM (bf16 W, factor rows), the wide-output kernel (bf16 W) or
+        // k_linear_small (no workspace)
+        return std::max(linear_bf16_workspace(a, b, rank, n, rows_per_member, n_time, math),
+                        linear_wide_workspace(a, b, rank, n, rows_per_member, n_time, math));
     DeviceState* st;
     if (get_state(&st)) return 0;
     return linear_pair_workspace(st, a, b, rank, n);
@@ -416,6 +418,8 @@ static int run_linear(LinParams& P, DeviceState* st, float* d_y, int64_t y_strid
     int rc = y_fmt == HSES_FMT_F32 ? launch_linear_pair(P, st, s, d_work, work_bytes)
                                    : HSES_ERR_UNSUPPORTED;
     if (rc == HSES_ERR_UNSUPPORTED) {
+        rc = launch_linear_bf16(P, st, s, d_work, work_bytes, act, y_fmt);
+        if (rc != HSES_ERR_UNSUPPORTED) return rc;  // activation fused
         rc = launch_linear_wide(P, st, s, d_work, work_bytes, act, y_fmt);
         if (rc != HSES_ERR_UNSUPPORTED) return rc;  // activation fused
         if (y_fmt != HSES_FMT_F32)

@@ -137,6 +137,15 @@ int launch_linear_small(LinParams& P, DeviceState* st, hipStream_t s);
 // fp32 math, do_mm, rank <= 16: the members' A_m / B_m rows into the workspace,
 // then an fp32 MFMA GEMM with x B_m and (x B_m) A_m^T fused (linear_f32.hip).
 int launch_linear_f32(LinParams& P, DeviceState* st, hipStream_t s, void* work, size_t work_bytes);
+// Every member's (a + b) x r factor rows into F (n (a + b) r floats), the
+// scaled role's rows (do_mm: A; do_Tmm: the input side) times sign * sigma / sqrt(r).
+int launch_factors(LinParams& P, DeviceState* st, hipStream_t s, float* F);
+// bf16 math, outputs >= 256 wide, rank <= 4: the bf16 MFMA GEMM with x B_m
+// fused (linear_bf16.hip); its workspace, 0 when it does not apply.
+int launch_linear_bf16(LinParams& P, DeviceState* st, hipStream_t s, void* work, size_t work_bytes,
+                       int32_t act, int32_t y_fmt);
+size_t linear_bf16_workspace(int32_t a, int32_t b, int32_t r, int32_t n, int32_t rows_per_member,
+                             int32_t n_time, int32_t math);
 size_t linear_f32_workspace(int32_t a, int32_t b, int32_t r, int32_t n, int32_t rows_per_member,
                             int32_t n_time, int32_t math);
 int launch_linear_pair(LinParams& P, DeviceState* st, hipStream_t s, void* work, size_t work_bytes,
@@ -155,5 +164,25 @@ void launch_w_to_bf16(const float* W, int32_t a, int32_t b, int32_t kp, int32_t 
 // Elementwise activation fused into a forward epilogue (hses_act).
 enum { ACT_NONE = HSES_ACT_NONE, ACT_TANH = HSES_ACT_TANH, ACT_SIGMOID = HSES_ACT_SIGMOID,
        ACT_RELU_SQ = HSES_ACT_RELU_SQ };
+
+// Rows of a tile: row L0 + i (i within the tile) is member m_first + dm of the tile
+// with dm, its time plane and slot from 32-bit divisions of rem0 + i (the
+// 64-bit division by R happens once per workgroup).
+struct TileRows {
+    int32_t m_first, rem0;
+    __device__ __forceinline__ TileRows(const LinParams& P, int64_t L0) {
+        m_first = (int32_t)(L0 / P.R);
+        rem0 = (int32_t)(L0 - (int64_t)m_first * P.R);
+    }
+    __device__ __forceinline__ int32_t member(const LinParams& P, int32_t i) const {
+        return (rem0 + i) / P.R;
+    }
+    __device__ __forceinline__ int64_t offset(const LinParams& P, int32_t i, int64_t stride,
+                                              int64_t plane) const {
+        const int32_t rr = rem0 + i, dm = rr / P.R, rem = rr - dm * P.R;
+        const int32_t t = rem / P.rpm, s = rem - t * P.rpm;
+        return t * plane + ((int64_t)(m_first + dm) * P.rpm + s) * stride;
+    }
+};
 
 }  // namespace hses

@@ -47,9 +47,10 @@ __device__ __forceinline__ float x_at(const void* x, int64_t off, int32_t k) {
 }
 
 // ---- k_factors -------------------------------------------------------------------
-// F[m] = the member's (b + a) x r stream rows: rows [0, b) are B_m as drawn,
-// rows [b, a + b) are A_m scaled by sign * sigma / sqrt(r).  A thread draws
-// rows [q rc, q rc + rc) of one member after one jump to the group's start.
+// F[m] = the member's (a + b) x r stream rows as drawn, except that the
+// rows carrying sign * sigma / sqrt(r) are scaled: do_mm's A rows [b, a + b),
+// do_Tmm's input-side rows [a, a + b) (with a the output width).  A thread
+// draws rows [q rc, q rc + rc) of one member after one jump to the group's start.
 __global__ __launch_bounds__(256) void k_factors(LinParams P, int32_t rc, int32_t groups,
                                                  float* __restrict__ F) {
     __shared__ BmTables t;
@@ -65,30 +66,10 @@ __global__ __launch_bounds__(256) void k_factors(LinParams P, int32_t rc, int32_
     uint64_t s = row_start_state(seed, q, P.jump);
     const NoiseCtx ctx{&t, P.log_exc, P.cos_exc};
     float* dst = F + ((int64_t)m * rows + row0) * r;
-    const int32_t split = (P.b - row0) * r;  // normals before the first A row
+    const int32_t split = ((P.tmm ? P.a : P.b) - row0) * r;  // normals before the first scaled row
     bm_run(s, min(rc, rows - row0) * r, ctx,
            [&](int32_t i, float v) { dst[i] = i >= split ? v * sc : v; });
 }
-
-// Rows of a tile: row L0 + i (i < 128) is member m_first + dm of the tile
-// with dm, its time plane and slot from 32-bit divisions of rem0 + i (the
-// 64-bit division by R happens once per workgroup).
-struct TileRows {
-    int32_t m_first, rem0;
-    __device__ __forceinline__ TileRows(const LinParams& P, int64_t L0) {
-        m_first = (int32_t)(L0 / P.R);
-        rem0 = (int32_t)(L0 - (int64_t)m_first * P.R);
-    }
-    __device__ __forceinline__ int32_t member(const LinParams& P, int32_t i) const {
-        return (rem0 + i) / P.R;
-    }
-    __device__ __forceinline__ int64_t offset(const LinParams& P, int32_t i, int64_t stride,
-                                              int64_t plane) const {
-        const int32_t rr = rem0 + i, dm = rr / P.R, rem = rr - dm * P.R;
-        const int32_t t = rem / P.rpm, s = rem - t * P.rpm;
-        return t * plane + ((int64_t)(m_first + dm) * P.rpm + s) * stride;
-    }
-};
 
 // ---- k_gemm_f32 ------------------------------------------------------------------
 // NT 32-column MFMA tiles per wave (BN = 32 NT); four waves of 32 rows.  RK is
@@ -369,9 +350,22 @@ static int32_t f32_nm_max(int32_t R, int32_t n) {
     return std::min(nm, n);
 }
 
+// Rows per generating thread: up to 32 normals, fewer while that leaves under
+// 64k threads; at least enough for the jump tables' row count.
+static bool factor_rows(const LinParams& P, int32_t* rc_out, int32_t* groups) {
+    const int32_t r = P.r, rows = P.a + P.b;
+    int32_t rc = std::max(1, 32 / r);
+    while (rc > 1 && (int64_t)P.n * ((rows + rc - 1) / rc) < 65536) rc = std::max(1, rc / 2);
+    rc = std::max<int32_t>(rc, (int32_t)((rows + kJumpMaxRows - 1) / kJumpMaxRows));
+    if ((int64_t)rc * r > kJumpMaxL) return false;
+    *rc_out = rc;
+    *groups = (rows + rc - 1) / rc;
+    return true;
+}
+
 // The tiling of one call (shape only).
 struct F32Plan {
-    int32_t bn, rk, nm, bch, rc, groups;
+    int32_t bn, rk, nm, bch;
     size_t lds, f_bytes;
 };
 
@@ -388,22 +382,25 @@ static bool f32_plan(const LinParams& P, F32Plan* pl) {
     if (a_lds > KF_AMAX) return false;
     const size_t nbuf = P.b > KF_BK ? 2 : 1;  // staging buffers (k_gemm_f32)
     pl->lds = (nbuf * ((size_t)(KF_BM + pl->bn) * KF_XP + bch) + a_lds) * 4;
-    pl->rc = 1;
-    pl->groups = 0;
     pl->f_bytes = 0;
     if (r > 0) {
-        // rows per generating thread: up to 32 normals, fewer while that leaves
-        // under 64k threads; at least enough for the jump tables' row count
-        const int32_t rows = P.a + P.b;
-        int32_t rc = std::max(1, 32 / r);
-        while (rc > 1 && (int64_t)P.n * ((rows + rc - 1) / rc) < 65536) rc = std::max(1, rc / 2);
-        rc = std::max<int32_t>(rc, (int32_t)((rows + kJumpMaxRows - 1) / kJumpMaxRows));
-        if ((int64_t)rc * r > kJumpMaxL) return false;
-        pl->rc = rc;
-        pl->groups = (rows + rc - 1) / rc;
-        pl->f_bytes = align16((size_t)P.n * rows * r * 4);
+        int32_t rc, groups;
+        if (!factor_rows(P, &rc, &groups)) return false;
+        pl->f_bytes = align16((size_t)P.n * (P.a + P.b) * r * 4);
     }
     return true;
+}
+
+int launch_factors(LinParams& P, DeviceState* st, hipStream_t s, float* F) {
+    int32_t rc, groups;
+    if (P.r < 1 || !factor_rows(P, &rc, &groups)) return HSES_ERR_UNSUPPORTED;
+    int e = get_jump_table(st, (int64_t)rc * P.r, groups, &P.jump);
+    if (e) return e;
+    const int64_t blocks = ((int64_t)P.n * groups + 255) / 256;
+    if (blocks > INT32_MAX) return set_error(HSES_ERR_INVALID_ARG, "too many factor rows");
+    hipLaunchKernelGGL(k_factors, dim3((uint32_t)blocks), dim3(256), 0, s, P, rc, groups, F);
+    HSES_CHECK_HIP(hipGetLastError());
+    return HSES_OK;
 }
 
 size_t linear_f32_workspace(int32_t a, int32_t b, int32_t r, int32_t n, int32_t rows_per_member,
@@ -454,13 +451,8 @@ int launch_linear_f32(LinParams& P, DeviceState* st, hipStream_t s, void* work, 
     if (tiles > INT32_MAX) return set_error(HSES_ERR_INVALID_ARG, "too many output rows");
     float* F = static_cast<float*>(work);
     if (P.r > 0) {
-        int rc = get_jump_table(st, (int64_t)pl.rc * P.r, pl.groups, &P.jump);
+        const int rc = launch_factors(P, st, s, F);
         if (rc) return rc;
-        const int64_t items = (int64_t)P.n * pl.groups;
-        const int64_t blocks = (items + 255) / 256;
-        if (blocks > INT32_MAX) return set_error(HSES_ERR_INVALID_ARG, "too many factor rows");
-        hipLaunchKernelGGL(k_factors, dim3((uint32_t)blocks), dim3(256), 0, s, P, pl.rc, pl.groups, F);
-        HSES_CHECK_HIP(hipGetLastError());
     }
     const dim3 grid((uint32_t)tiles);
     switch (P.x_fmt) {

@@ -315,6 +315,46 @@ def test_wide_kernel(hses_gpu, n, rpm, T, a, b, r, tid_lo, fmt):
     assert_close(y, ref_forward(x3, W, A, B, rpm), 2e-2)
 
 
+@pytest.mark.parametrize("n,rpm,T,a,b,r,tid_lo,fmt,sigma", [
+    (4, 128, 1, 512, 512, 1, 0, FMT_BF16, 0.2),    # C5 square layer: two members per tile
+    (3, 100, 1, 300, 200, 3, 1, FMT_F32, 0.2),     # ragged output tile, K % 64 != 0, 4 members per tile
+    (2, 64, 4, 256, 128, 4, 2, FMT_F32, 0.2),      # time-major planes, rank 4
+    (2, 128, 1, 2048, 512, 1, 0, FMT_BF16, 0.2),   # ChannelMixing key width: 8 column tiles
+    (2, 128, 1, 512, 256, 1, 0, FMT_F32, 0.0),     # sigma 0: the plain product
+])
+def test_bf16_gemm_kernel(hses_gpu, n, rpm, T, a, b, r, tid_lo, fmt, sigma):
+    # outputs >= 256 wide at bf16 math: the bf16 MFMA GEMM with x B_m fused
+    rng = np.random.default_rng(n * 13 + a + b + r)
+    x3 = rng.standard_normal((T, n * rpm, b)).astype(np.float32)
+    if fmt == FMT_BF16:
+        x3 = bf16_round(x3)
+    W = (rng.standard_normal((a, b)) / np.sqrt(b)).astype(np.float32)
+    A, B = factors(max(sigma, 1e-30), r, n, tid_lo, a, b)
+    if sigma == 0.0:
+        A = np.zeros_like(A)
+    y = run(hses_gpu, x3, W, r, sigma, n, rpm, tid_lo, fmt=fmt, math=MATH_BF16)
+    assert_close(y, ref_forward(bf16_round(x3), bf16_round(W), A, bf16_round(B), rpm), 2e-3)
+    assert_close(y, ref_forward(x3, W, A, B, rpm), 2e-2)
+
+
+@pytest.mark.parametrize("act", [1, 2, 3])
+def test_bf16_gemm_activation_bf16_out(hses_gpu, act):
+    from hyperscalees_amd._lib import ACT_RELU_SQ, ACT_SIGMOID, ACT_TANH
+    n, rpm, a, b, r, sigma = 3, 128, 512, 256, 1, 0.2
+    rng = np.random.default_rng(act)
+    x = bf16_round(rng.standard_normal((n * rpm, b)).astype(np.float32))
+    W = (rng.standard_normal((a, b)) / np.sqrt(b)).astype(np.float32)
+    A, B = factors(sigma, r, n, 0, a, b)
+    y = hses_gpu.perturbed_linear(torch.from_numpy(x).cuda().to(torch.bfloat16),
+                                  torch.from_numpy(W).cuda(), KEY, r, sigma, 0, 0, 0, n, rpm,
+                                  x_fmt=FMT_BF16, math=MATH_BF16, act=act, out_bf16=True)
+    torch.cuda.synchronize()
+    ref = ref_forward(x[None], bf16_round(W), A, bf16_round(B), rpm)[0]
+    f = {ACT_TANH: np.tanh, ACT_SIGMOID: lambda v: 1 / (1 + np.exp(-v)),
+         ACT_RELU_SQ: lambda v: np.maximum(v, 0) ** 2}[act]
+    assert_close(y.float().cpu().numpy(), f(ref), 6e-3)   # plus the bf16 rounding of y
+
+
 @pytest.mark.parametrize("a,b,act", [(512, 32, 1), (96, 512, 2), (512, 512, 3), (256, 64, 0),
                                      (512, 96, 2), (512, 120, 0)])  # C5 g1: width 96
 def test_wide_kernel_transposed_and_activations(hses_gpu, a, b, act):
