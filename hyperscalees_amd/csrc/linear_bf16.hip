@@ -110,7 +110,6 @@ __global__ __launch_bounds__(KB_THREADS) void k_gemm_bf16(LinParams P, const uin
     const int xr = tid >> 1, xk = (tid & 1) * 32;
     const bool xvalid = xr < rows_here;
     const int64_t xoff = xvalid ? tr.offset(P, xr, P.x_stride, P.x_plane) : 0;
-    const int32_t xlm = xvalid ? tr.member(P, xr) : 0;
     const int32_t wrow = o0 + xr;
     const bool wvalid = wrow < a;
     const uint16_t* wsrc = Wb + (int64_t)(wvalid ? wrow : 0) * kp + xk;
@@ -205,7 +204,12 @@ __global__ __launch_bounds__(KB_THREADS) void k_gemm_bf16(LinParams P, const uin
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
-    float xb[RK];  // x B_m of row xr over this thread's half of each step
+    // x B_m from the MFMA x operands: the two waves that share rows 64 wr ..
+    // take one 32-row block each (block wc), so every SIMD does the same share;
+    // lane (lc, hl) holds k 16 ks + 8 hl .. + 8 of row xbr
+    const int32_t xbr = wr * 64 + 32 * wc + lc;
+    const int32_t xbm = xbr < rows_here ? tr.member(P, xbr) : 0;  // its member in the tile
+    float xb[RK];
 #pragma unroll
     for (int c = 0; c < RK; ++c) xb[c] = 0.0f;
 
@@ -232,23 +236,28 @@ __global__ __launch_bounds__(KB_THREADS) void k_gemm_bf16(LinParams P, const uin
             for (int i = 0; i < 2; ++i)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) acc[i][j] = mfma32b(bf[j], af[i], acc[i][j]);
-        }
-        if (noisy) {
-            // x B_m over this thread's 32 k as 16 bf16-pair dot products per rank column
-            const uint16_t* xs = X + xr * KB_P + xk;
-            const uint32_t* bs = Bc + cur * bch + (xlm * (KB_BK / 2) + xk / 2) * RK;
+            if (noisy) {
+                // the factor's bf16 pairs of these 8 k: [lm][pair][c]
+                const uint4* bs = reinterpret_cast<const uint4*>(
+                    Bc + cur * bch + (xbm * (KB_BK / 2) + ks * 8 + hl * 4) * RK);
+                const uint4 xw = __builtin_bit_cast(uint4, wc ? af[1] : af[0]);
+                const uint32_t xp[4] = {xw.x, xw.y, xw.z, xw.w};
+                if constexpr (RK == 1) {
+                    const uint4 q = bs[0];  // pairs u = 0..3
+                    xb[0] = dot2_bf16(xp[0], q.x, xb[0]);
+                    xb[0] = dot2_bf16(xp[1], q.y, xb[0]);
+                    xb[0] = dot2_bf16(xp[2], q.z, xb[0]);
+                    xb[0] = dot2_bf16(xp[3], q.w, xb[0]);
+                } else {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const uint4 x4 = *reinterpret_cast<const uint4*>(xs + 8 * q);
-                const uint32_t xp[4] = {x4.x, x4.y, x4.z, x4.w};
-                uint32_t bb[4 * RK];
-#pragma unroll
-                for (int g = 0; g < RK; ++g)
-                    *reinterpret_cast<uint4*>(bb + 4 * g) = reinterpret_cast<const uint4*>(bs + 4 * q * RK)[g];
-#pragma unroll
-                for (int u = 0; u < 4; ++u)
-#pragma unroll
-                    for (int c = 0; c < RK; ++c) xb[c] = dot2_bf16(xp[u], bb[u * RK + c], xb[c]);
+                    for (int u = 0; u < 4; ++u) {
+                        const uint4 q = bs[u];  // rank columns 0..3 of pair u
+                        xb[0] = dot2_bf16(xp[u], q.x, xb[0]);
+                        xb[1] = dot2_bf16(xp[u], q.y, xb[1]);
+                        xb[2] = dot2_bf16(xp[u], q.z, xb[2]);
+                        xb[3] = dot2_bf16(xp[u], q.w, xb[3]);
+                    }
+                }
             }
         }
         if (kt + 1 < nkt) store_step(cur ^ 1);
@@ -260,8 +269,8 @@ __global__ __launch_bounds__(KB_THREADS) void k_gemm_bf16(LinParams P, const uin
     if (noisy) {
 #pragma unroll
         for (int c = 0; c < RK; ++c) {
-            const float v = xb[c] + __shfl_xor(xb[c], 1);  // the row's two halves
-            if (xk == 0) XBs[xr * RK + c] = v;
+            const float v = xb[c] + __shfl_xor(xb[c], 32);  // the two k groups
+            if (hl == 0) XBs[xbr * RK + c] = v;
         }
         __syncthreads();
     }
@@ -270,7 +279,7 @@ __global__ __launch_bounds__(KB_THREADS) void k_gemm_bf16(LinParams P, const uin
     // 32-row block and column 8 (e / 4) + 4 hl + e % 4 of the 32-column tile:
     // each lane owns two rows and stores four consecutive columns at a time.
     const bool flat = P.n_time == 1;
-    auto store_all = [&](auto actc, auto ybc) {
+    auto store_all = [&](auto actc, auto ybc) __attribute__((always_inline)) {
         constexpr int ACT = decltype(actc)::value;
         constexpr bool YB = decltype(ybc)::value;
 #pragma unroll
@@ -283,6 +292,52 @@ __global__ __launch_bounds__(KB_THREADS) void k_gemm_bf16(LinParams P, const uin
             float xr_[RK];
 #pragma unroll
             for (int c = 0; c < RK; ++c) xr_[c] = noisy ? XBs[row * RK + c] : 0.0f;
+            if constexpr (YB) {
+                if (vec_y == 2 && o0 + KB_BN <= a) {
+                    // lanes l and l + 32 hold columns 8 g + 0..3 and 8 g + 4..7: after a
+                    // swap of the upper half-lanes of group g with the lower of group
+                    // g + 1, lane l holds the 8 columns of group g and lane l + 32 those
+                    // of g + 1: one 16-byte store each
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+#pragma unroll
+                        for (int g = 0; g < 4; g += 2) {
+                            uint32_t w[2][2];
+#pragma unroll
+                            for (int h = 0; h < 2; ++h) {
+                                const int32_t c0 = wc * 128 + 32 * j + 8 * (g + h) + 4 * hl;
+                                float v[4];
+#pragma unroll
+                                for (int u = 0; u < 4; ++u) v[u] = acc[i][j][4 * (g + h) + u];
+                                if (noisy) {
+                                    const float* ar = As + ((size_t)lm * KB_BN + c0) * RK;
+#pragma unroll
+                                    for (int u = 0; u < 4; ++u) {
+                                        float z = 0.0f;
+#pragma unroll
+                                        for (int c = 0; c < RK; ++c)
+                                            z = __fadd_rn(z, __fmul_rn(xr_[c], ar[u * RK + c]));
+                                        v[u] = __fadd_rn(v[u], z);
+                                    }
+                                }
+#pragma unroll
+                                for (int u = 0; u < 4; ++u) v[u] = act_value<ACT>(v[u]);
+                                w[h][0] = pack_bf16x2(v[0], v[1]);
+                                w[h][1] = pack_bf16x2(v[2], v[3]);
+                            }
+#pragma unroll
+                            for (int q = 0; q < 2; ++q) {
+                                const auto sw = __builtin_amdgcn_permlane32_swap(w[0][q], w[1][q], false, false);
+                                w[0][q] = sw[0];
+                                w[1][q] = sw[1];
+                            }
+                            const int32_t cs = wc * 128 + 32 * j + 8 * (g + hl);
+                            *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(P.y) + yoff + cs) =
+                                uint4{w[0][0], w[0][1], w[1][0], w[1][1]};
+                        }
+                    continue;
+                }
+            }
 #pragma unroll
             for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -326,7 +381,7 @@ __global__ __launch_bounds__(KB_THREADS) void k_gemm_bf16(LinParams P, const uin
     using T1 = std::integral_constant<int, ACT_TANH>;
     using T2 = std::integral_constant<int, ACT_SIGMOID>;
     using T3 = std::integral_constant<int, ACT_RELU_SQ>;
-    auto by_act = [&](auto ybc) {
+    auto by_act = [&](auto ybc) __attribute__((always_inline)) {
         switch (act) {
             case ACT_TANH: store_all(T1{}, ybc); break;
             case ACT_SIGMOID: store_all(T2{}, ybc); break;
@@ -398,10 +453,13 @@ int launch_linear_bf16(LinParams& P, DeviceState* st, hipStream_t s, void* work,
     uint16_t* Wb = static_cast<uint16_t*>(work);
     float* F = reinterpret_cast<float*>(static_cast<char*>(work) + pl.w_bytes);
     // four consecutive outputs per store (16 bytes fp32, 8 bytes bf16) when every
-    // row start keeps them aligned
+    // row start keeps them aligned (vec_y 1); bf16 rows 16-byte aligned: eight (2)
     const int64_t ybytes = y_fmt == HSES_FMT_BF16 ? 2 : 4;
-    const int32_t vec_y = reinterpret_cast<uintptr_t>(P.y) % (4 * ybytes) == 0 && P.y_stride % 4 == 0 &&
-                          (P.n_time == 1 || P.y_plane % 4 == 0);
+    int32_t vec_y = reinterpret_cast<uintptr_t>(P.y) % (4 * ybytes) == 0 && P.y_stride % 4 == 0 &&
+                    (P.n_time == 1 || P.y_plane % 4 == 0);
+    if (vec_y && ybytes == 2 && reinterpret_cast<uintptr_t>(P.y) % 16 == 0 && P.y_stride % 8 == 0 &&
+        (P.n_time == 1 || P.y_plane % 8 == 0))
+        vec_y = 2;
     launch_w_to_bf16(P.W, P.a, P.b, pl.kp, P.tmm, Wb, s);
     HSES_CHECK_HIP(hipGetLastError());
     LinParams Q = P;
