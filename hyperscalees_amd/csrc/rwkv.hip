@@ -155,7 +155,10 @@ __global__ void k_relu_sq(float* __restrict__ x, int64_t n) {
 // holds row i of the head's state.  Per step the six vectors are staged in the
 // wave's LDS slice (decay w -> exp(-exp(w)) on the way) and read as broadcasts;
 // then sa_i = sum_j s_ij a_j, s_ij = ((s_ij w_j) + v_i k_j) + sa_i b_j,
-// out_i = sum_j s_ij r_j, all sums in ascending j.  s_out is the state after
+// out_i = sum_j s_ij r_j, all sums in ascending j, each multiply-add fused
+// (one rounding where the reference rounds the product and the sum: at most
+// an ulp per operation apart; the kernel is bound by these vector operations,
+// 5 per state element and step instead of 9).  s_out is the state after
 // the last step t < length (s_in when length == 0).
 // With POST the output row is TimeMixing's next three steps instead
 // (llm.rs:455-470): y = (GroupNorm_head(out) + (sum_s r k r_k) v) g, with
@@ -284,17 +287,13 @@ __global__ __launch_bounds__(256) void k_wkv7(const float* __restrict__ r, const
         const float vi = st[3][i];
         float sa = 0.0f;
 #pragma unroll
-        for (int j = 0; j < S; ++j) sa = sa + s[j] * st[4][j];
+        for (int j = 0; j < S; ++j) sa = __builtin_fmaf(s[j], st[4][j], sa);
 #pragma unroll
-        for (int j = 0; j < S; ++j) {
-            const float t1 = s[j] * st[1][j];
-            const float t2 = vi * st[2][j];
-            const float t4 = sa * st[5][j];
-            s[j] = (t1 + t2) + t4;
-        }
+        for (int j = 0; j < S; ++j)
+            s[j] = __builtin_fmaf(sa, st[5][j], __builtin_fmaf(vi, st[2][j], s[j] * st[1][j]));
         float acc = 0.0f;
 #pragma unroll
-        for (int j = 0; j < S; ++j) acc = acc + s[j] * st[0][j];
+        for (int j = 0; j < S; ++j) acc = __builtin_fmaf(s[j], st[0][j], acc);
         if constexpr (POST) {
             const float x1 = row_ok ? acc : 0.0f;
             const float mean = wave_sum(0.0f + x1) / (float)S;
