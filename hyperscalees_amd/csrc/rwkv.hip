@@ -5,7 +5,11 @@
 //
 // Every routine keeps the reference's per-element operation order with each
 // operation rounded separately (built with -ffp-contract=off); reductions run
-// over 64-lane waves, so their association differs from the reference's.
+// over 64-lane waves, so their association differs from the reference's.  Two
+// exceptions, both in TimeMixing's per-step work, which the recurrence kernel
+// does for every element and step: the state update's multiply-adds are fused,
+// and the gates use the hardware's exp2 / log2 / reciprocal / reciprocal-root
+// instructions (about an ulp each) in place of libm-accurate routines.
 #include <math.h>
 
 #include "runtime.h"
@@ -19,10 +23,45 @@ __device__ __forceinline__ uint16_t f2bf_rne(float f) {
     return (uint16_t)__builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){f, 0.0f}, bf16x2_t));
 }
 
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+
+// Sum over the 64 lanes of a wave, the same bits in every lane (each exchange
+// pairs lanes symmetrically and the adds commute): within rows of 16 lanes by
+// DPP (quad swaps, then the half-row and row mirrors), across rows by the
+// permlane16 and permlane32 swaps.  No LDS traffic.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-    return v;
+    v += dpp_f<0xB1>(v);   // quad_perm 1,0,3,2
+    v += dpp_f<0x4E>(v);   // quad_perm 2,3,0,1
+    v += dpp_f<0x141>(v);  // row_half_mirror: the other quad of the half-row
+    v += dpp_f<0x140>(v);  // row_mirror: the other half-row
+    const uint32_t u = __float_as_uint(v);
+    const auto p16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    v = __uint_as_float(p16[0]) + __uint_as_float(p16[1]);  // rows 0+1 | 2+3
+    const uint32_t w = __float_as_uint(v);
+    const auto p32 = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+    return __uint_as_float(p32[0]) + __uint_as_float(p32[1]);
+}
+
+// TimeMixing's gate algebra on the hardware's transcendental instructions.
+// Every kernel that forms a gate calls these, so the fused and unfused paths
+// agree bit for bit.
+__device__ __forceinline__ float exp_hw(float x) {
+    return __builtin_amdgcn_exp2f(x * 1.44269504088896341f);
+}
+__device__ __forceinline__ float sigmoid_hw(float z) { return __builtin_amdgcn_rcpf(1.0f + exp_hw(-z)); }
+// ln(1 + e^x), x itself above 20
+__device__ __forceinline__ float softplus_hw(float x) {
+    return x > 20.0f ? x : 0.693147180559945309f * __builtin_amdgcn_logf(1.0f + exp_hw(x));
+}
+// the recurrence's decay exp(-exp(w))
+__device__ __forceinline__ float decay_hw(float w) { return exp_hw(-exp_hw(w)); }
+// 1 / max(sqrt(ss), 1e-12): the kk normalisation
+__device__ __forceinline__ float inv_norm_hw(float ss) {
+    const float n = __builtin_amdgcn_sqrtf(ss);
+    return __builtin_amdgcn_rcpf(n < 1e-12f ? 1e-12f : n);
 }
 
 // llm.rs:66-83: y = (x - mean) / sqrt(E[x^2] - mean^2 + eps) * w + b per row.
@@ -69,10 +108,10 @@ __global__ __launch_bounds__(256) void k_group_norm(const float* __restrict__ x,
     }
     const float mean = wave_sum(s) / (float)gsz;
     const float var = wave_sum(s2) / (float)gsz - mean * mean;
-    const float sd = sqrtf(var + eps);
+    const float isd = __builtin_amdgcn_rsqf(var + eps);  // as the fused TimeMixing output forms it
     for (int64_t e = lane; e < gsz; e += 64) {
         const int32_t c = g * inner + (int32_t)(e / L);
-        y[base + e] = w[c] * ((x[base + e] - mean) / sd) + b[c];
+        y[base + e] = w[c] * ((x[base + e] - mean) * isd) + b[c];
     }
 }
 
@@ -153,8 +192,8 @@ __global__ void k_relu_sq(float* __restrict__ x, int64_t n) {
 // (nseq, T, H, S); s_in / s_out (nseq, H, S, S); out (nseq, T, H, S);
 // new_starts (nseq, T) or NULL.  One wave per (sequence, head), S <= 64: lane i
 // holds row i of the head's state.  Per step the six vectors are staged in the
-// wave's LDS slice (decay w -> exp(-exp(w)) on the way) and read as broadcasts;
-// then sa_i = sum_j s_ij a_j, s_ij = ((s_ij w_j) + v_i k_j) + sa_i b_j,
+// wave's LDS slice (decay w -> exp(-exp(w)) on the way, by the hardware's exp2)
+// and read as broadcasts; then sa_i = sum_j s_ij a_j, s_ij = ((s_ij w_j) + v_i k_j) + sa_i b_j,
 // out_i = sum_j s_ij r_j, all sums in ascending j, each multiply-add fused
 // (one rounding where the reference rounds the product and the sum: at most
 // an ulp per operation apart; the kernel is bound by these vector operations,
@@ -189,8 +228,6 @@ struct WkvGates {
     const float* k_a;
 };
 
-__device__ __forceinline__ float softplus1(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
-
 template <int S, bool POST, bool GATES>
 __global__ __launch_bounds__(256) void k_wkv7(const float* __restrict__ r, const float* __restrict__ w,
                                               const float* __restrict__ k, const float* __restrict__ v,
@@ -217,6 +254,7 @@ __global__ __launch_bounds__(256) void k_wkv7(const float* __restrict__ r, const
     // loaded one step ahead so their latency overlaps the previous step's work
     float nr = 0.0f, nw = 0.0f, nk = 0.0f, nv = 0.0f, na = 0.0f, nb = 0.0f, ng = 0.0f;
     float nv2 = 0.0f, nvf = 0.0f;
+    uint8_t nns = 0;  // the step's new-start flag
     const int32_t cc = h * S + i;  // this lane's channel
     float w0c = 0.0f, a0c = 0.0f, v0c = 0.0f, kkc = 0.0f, kac = 0.0f;
     if constexpr (GATES) {
@@ -228,6 +266,7 @@ __global__ __launch_bounds__(256) void k_wkv7(const float* __restrict__ r, const
     }
     auto fetch = [&](int32_t t) {
         const int64_t o = ((sq * T + t) * H + h) * (int64_t)S + i;
+        if (new_starts) nns = new_starts[sq * T + t];
         nr = r[o];
         nw = w[o];
         nk = k[o];
@@ -245,7 +284,7 @@ __global__ __launch_bounds__(256) void k_wkv7(const float* __restrict__ r, const
     };
     fetch(0);
     for (int32_t t = 0; t < T; ++t) {
-        if (new_starts && new_starts[sq * T + t]) {
+        if (nns) {
 #pragma unroll
             for (int j = 0; j < S; ++j) s[j] = 0.0f;
         }
@@ -253,20 +292,18 @@ __global__ __launch_bounds__(256) void k_wkv7(const float* __restrict__ r, const
         const float gcur = ng;
         if constexpr (GATES) {
             // k_tm_gates_kk's per-element algebra (same operations, same wave sum)
-            const float wv = -softplus1(-(w0c + nw)) - 0.5f;
-            const float av = 1.0f / (1.0f + expf(-(a0c + na)));
+            const float wv = -softplus_hw(-(w0c + nw)) - 0.5f;
+            const float av = sigmoid_hw(a0c + na);
             float vv = nv;
             if (gt.v2o) {
-                const float sg = 1.0f / (1.0f + expf(-(v0c + nv2)));
+                const float sg = sigmoid_hw(v0c + nv2);
                 vv = vv + (nvf - vv) * sg;
             }
             const float kk2 = row_ok ? nk * kkc : 0.0f;
-            float nrm = sqrtf(wave_sum(kk2 * kk2));
-            nrm = nrm < 1e-12f ? 1e-12f : nrm;
-            const float kk = kk2 / nrm;
+            const float kk = kk2 * inv_norm_hw(wave_sum(kk2 * kk2));
             if (row_ok) {
                 st[0][lane] = nr;
-                st[1][lane] = expf(-expf(wv));
+                st[1][lane] = decay_hw(wv);
                 st[2][lane] = nk * (kac * (av - 1.0f) + 1.0f);
                 st[3][lane] = vv;
                 st[4][lane] = -kk;
@@ -274,7 +311,7 @@ __global__ __launch_bounds__(256) void k_wkv7(const float* __restrict__ r, const
             }
         } else if (row_ok) {
             st[0][lane] = nr;
-            st[1][lane] = expf(-expf(nw));
+            st[1][lane] = decay_hw(nw);
             st[2][lane] = nk;
             st[3][lane] = nv;
             st[4][lane] = na;
@@ -298,11 +335,11 @@ __global__ __launch_bounds__(256) void k_wkv7(const float* __restrict__ r, const
             const float x1 = row_ok ? acc : 0.0f;
             const float mean = wave_sum(0.0f + x1) / (float)S;
             const float var = wave_sum(0.0f + x1 * x1) / (float)S - mean * mean;
-            const float sd = sqrtf(var + post.eps);
+            const float isd = __builtin_amdgcn_rsqf(var + post.eps);
             const int32_t c = h * S + i;
             const float rk = wave_sum(row_ok ? st[0][i] * st[2][i] * post.r_k[c] : 0.0f);
             if (row_ok) {
-                const float gn = post.ln_w[c] * ((acc - mean) / sd) + post.ln_b[c];
+                const float gn = post.ln_w[c] * ((acc - mean) * isd) + post.ln_b[c];
                 const float y = (gn + rk * vi) * gcur;
                 if (post.bf16_out)
                     reinterpret_cast<uint16_t*>(out)[o + lane] = f2bf_rne(y);
@@ -349,10 +386,10 @@ __global__ void k_tm_gates(float* __restrict__ w2o, float* __restrict__ a2o,
     const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (e >= n) return;
     const int32_t c = (int32_t)(e % C);
-    w2o[e] = -softplus1(-(w0[c] + w2o[e])) - 0.5f;
-    a2o[e] = 1.0f / (1.0f + expf(-(a0[c] + a2o[e])));
+    w2o[e] = -softplus_hw(-(w0[c] + w2o[e])) - 0.5f;
+    a2o[e] = sigmoid_hw(a0[c] + a2o[e]);
     if (v2o) {
-        const float sg = 1.0f / (1.0f + expf(-(v0[c] + v2o[e])));
+        const float sg = sigmoid_hw(v0[c] + v2o[e]);
         v[e] = v[e] + (v_first[e] - v[e]) * sg;
     }
 }
@@ -374,10 +411,9 @@ __global__ __launch_bounds__(256) void k_tm_kk(float* __restrict__ k, const floa
     const int64_t o = row * C + c;
     const float kv = ok ? k[o] : 0.0f;
     const float kk2 = ok ? kv * k_k[c] : 0.0f;
-    float nrm = sqrtf(wave_sum(kk2 * kk2));
-    nrm = nrm < 1e-12f ? 1e-12f : nrm;
+    const float inv = inv_norm_hw(wave_sum(kk2 * kk2));
     if (!ok) return;
-    const float kk = kk2 / nrm, av = a[o];
+    const float kk = kk2 * inv, av = a[o];
     ai[o] = -kk;
     bi[o] = kk * av;
     k[o] = kv * (k_a[c] * (av - 1.0f) + 1.0f);
@@ -524,19 +560,18 @@ __global__ __launch_bounds__(256) void k_tm_gates_kk(
     const int64_t o = row * C + c;
     float av = 0.0f, kv = 0.0f;
     if (ok) {
-        w2o[o] = -softplus1(-(w0[c] + w2o[o])) - 0.5f;
-        av = 1.0f / (1.0f + expf(-(a0[c] + a2o[o])));
+        w2o[o] = -softplus_hw(-(w0[c] + w2o[o])) - 0.5f;
+        av = sigmoid_hw(a0[c] + a2o[o]);
         if (v2o) {
-            const float sg = 1.0f / (1.0f + expf(-(v0[c] + v2o[o])));
+            const float sg = sigmoid_hw(v0[c] + v2o[o]);
             v[o] = v[o] + (v_first[o] - v[o]) * sg;
         }
         kv = k[o];
     }
     const float kk2 = ok ? kv * k_k[c] : 0.0f;
-    float nrm = sqrtf(wave_sum(kk2 * kk2));
-    nrm = nrm < 1e-12f ? 1e-12f : nrm;
+    const float inv = inv_norm_hw(wave_sum(kk2 * kk2));
     if (!ok) return;
-    const float kk = kk2 / nrm;
+    const float kk = kk2 * inv;
     ai[o] = -kk;
     bi[o] = kk * av;
     k[o] = kv * (k_a[c] * (av - 1.0f) + 1.0f);
