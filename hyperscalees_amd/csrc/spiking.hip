@@ -304,6 +304,96 @@ __global__ __launch_bounds__(256) void k_lif(const float* __restrict__ cur,
     if (valid && v_out) v_out[row * h + col] = v;
 }
 
+// The LIF scan with 16-byte loads, for rows of a multiple of 64 columns: a
+// dword per lane caps a load stream near half the HBM peak on gfx950, a dwordx4
+// per lane does not.  Loads and the per-lane spike stores are non-temporal
+// (streamed data, read or written once).  Each 16-lane row of the wave owns one 64-column word
+// (lane j of it columns 4j .. 4j+3), so a wave scans four (row, word) items.
+// BITS: every lane forms the nibble of its four spikes, shifted to its place in
+// the word; ORs over the half-row (quad swaps, half-row mirror) leave the low
+// and high 32 bits in lanes 0..7 and 8..15, a row mirror brings the high half
+// to lane 0, which stores the word.  The arithmetic is k_lif's, element by
+// element, so the outputs are identical.
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+
+template <int FMT>
+__global__ __launch_bounds__(256) void k_lif4(const float* __restrict__ cur,
+                                              const float* __restrict__ v0, int32_t T, int64_t rows,
+                                              int32_t h, int64_t cur_stride, float leak, float v_th,
+                                              void* __restrict__ spk, int64_t spk_stride,
+                                              float* __restrict__ v_out) {
+    const int32_t words = h >> 6;
+    const int64_t items = rows * words;
+    const int32_t lane = threadIdx.x & 63, g = lane & 15;
+    const int64_t item0 = (((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6) * 4;
+    if (item0 >= items) return;  // whole wave
+    const int64_t it = item0 + (lane >> 4);
+    const bool valid = it < items;  // uniform over the 16-lane row
+    const int64_t itc = valid ? it : items - 1;
+    const int64_t row = itc / words;
+    const int32_t word = (int32_t)(itc - row * words);
+    const int32_t col = word * 64 + 4 * g;
+    float4 v = (valid && v0) ? *reinterpret_cast<const float4*>(v0 + row * h + col)
+                             : float4{0.0f, 0.0f, 0.0f, 0.0f};
+    const int64_t cplane = rows * cur_stride, splane = rows * spk_stride;
+    const float4* cp = reinterpret_cast<const float4*>(cur + row * cur_stride + col);
+    const int64_t cp4 = cplane / 4;
+    auto step = [&](float& vv, float c) {
+        // snn.rs:61-63: charged = v + ((-v) + c) * leak; each op rounds.
+        const float charged = __fadd_rn(vv, __fmul_rn(__fadd_rn(-vv, c), leak));
+        const bool spike = charged >= v_th;
+        vv = __fmul_rn(charged, __fadd_rn(spike ? -1.0f : -0.0f, 1.0f));
+        return spike;
+    };
+    constexpr int LB = 16;
+    for (int32_t t0 = 0; t0 < T; t0 += LB) {
+        float4 cb[LB];
+#pragma unroll
+        for (int i = 0; i < LB; ++i) {
+            const f32x4v q = __builtin_nontemporal_load(
+                reinterpret_cast<const f32x4v*>(cp + (int64_t)min(t0 + i, T - 1) * cp4));
+            cb[i] = float4{q.x, q.y, q.z, q.w};
+        }
+#pragma unroll
+        for (int i = 0; i < LB; ++i) {
+            const int32_t t = t0 + i;
+            if (t >= T) break;  // uniform
+            const bool s0 = step(v.x, cb[i].x), s1 = step(v.y, cb[i].y);
+            const bool s2 = step(v.z, cb[i].z), s3 = step(v.w, cb[i].w);
+            const int64_t base = t * splane + row * spk_stride;
+            if constexpr (FMT == HSES_FMT_BITS) {
+                const uint32_t nib = (uint32_t)s0 | ((uint32_t)s1 << 1) | ((uint32_t)s2 << 2) |
+                                     ((uint32_t)s3 << 3);
+                int32_t w = (int32_t)(nib << (4 * (g & 7)));
+                w |= __builtin_amdgcn_mov_dpp(w, 0xB1, 0xF, 0xF, true);   // quad_perm 1,0,3,2
+                w |= __builtin_amdgcn_mov_dpp(w, 0x4E, 0xF, 0xF, true);   // quad_perm 2,3,0,1
+                w |= __builtin_amdgcn_mov_dpp(w, 0x141, 0xF, 0xF, true);  // row_half_mirror
+                const int32_t hi = __builtin_amdgcn_mov_dpp(w, 0x140, 0xF, 0xF, true);  // row_mirror
+                if (valid && g == 0)
+                    static_cast<uint64_t*>(spk)[base + word] = ((uint64_t)(uint32_t)hi << 32) | (uint32_t)w;
+            } else if constexpr (FMT == HSES_FMT_F32) {
+                if (valid)
+                    __builtin_nontemporal_store(
+                        f32x4v{s0 ? 1.0f : 0.0f, s1 ? 1.0f : 0.0f, s2 ? 1.0f : 0.0f, s3 ? 1.0f : 0.0f},
+                        reinterpret_cast<f32x4v*>(static_cast<float*>(spk) + base + col));
+            } else if constexpr (FMT == HSES_FMT_BF16) {
+                if (valid)
+                    __builtin_nontemporal_store(
+                        u32x2v{(s0 ? 0x3f80u : 0u) | (s1 ? 0x3f800000u : 0u),
+                               (s2 ? 0x3f80u : 0u) | (s3 ? 0x3f800000u : 0u)},
+                        reinterpret_cast<u32x2v*>(static_cast<uint16_t*>(spk) + base + col));
+            } else {
+                if (valid)
+                    __builtin_nontemporal_store(
+                        (uint32_t)s0 | ((uint32_t)s1 << 8) | ((uint32_t)s2 << 16) | ((uint32_t)s3 << 24),
+                        reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(spk) + base + col));
+            }
+        }
+    }
+    if (valid && v_out) *reinterpret_cast<float4*>(v_out + row * h + col) = v;
+}
+
 // snn.rs:274: spikes.mean_dim(0) -- the count of spikes over T divided by T.
 template <int FMT>
 __global__ __launch_bounds__(256) void k_spike_rate(const void* __restrict__ spk, int64_t stride,
@@ -456,6 +546,34 @@ extern "C" int hses_lif_scan(const float* d_cur, const float* d_v0, int32_t T, i
     // snn.rs:59: leak_scale = dt / tau_m with dt = 1, one f32 division.
     const float leak = 1.0f / tau_m;
     hipStream_t s = (hipStream_t)stream;
+    // 16-byte loads (k_lif4) when rows are whole 64-column words and every
+    // row start keeps the vector accesses aligned
+    const auto al = [](const void* q, uintptr_t a) { return reinterpret_cast<uintptr_t>(q) % a == 0; };
+    const int64_t ub = fmt_unit_bytes(fmt);
+    if (h % 64 == 0 && cur_stride % 4 == 0 && al(d_cur, 16) && al(d_v0, 16) && al(d_v_out, 16) &&
+        (fmt == HSES_FMT_BITS || (spk_stride % 4 == 0 && al(d_spikes, 4 * ub)))) {
+        const int64_t blocks4 = (rows * (h / 64) + 15) / 16;  // 4 items per wave, 4 waves per block
+        switch (fmt) {
+            case HSES_FMT_F32:
+                hipLaunchKernelGGL(k_lif4<HSES_FMT_F32>, dim3(blocks4), dim3(256), 0, s, d_cur, d_v0, T,
+                                   rows, h, cur_stride, leak, v_th, d_spikes, spk_stride, d_v_out);
+                break;
+            case HSES_FMT_BF16:
+                hipLaunchKernelGGL(k_lif4<HSES_FMT_BF16>, dim3(blocks4), dim3(256), 0, s, d_cur, d_v0,
+                                   T, rows, h, cur_stride, leak, v_th, d_spikes, spk_stride, d_v_out);
+                break;
+            case HSES_FMT_U8:
+                hipLaunchKernelGGL(k_lif4<HSES_FMT_U8>, dim3(blocks4), dim3(256), 0, s, d_cur, d_v0, T,
+                                   rows, h, cur_stride, leak, v_th, d_spikes, spk_stride, d_v_out);
+                break;
+            default:
+                hipLaunchKernelGGL(k_lif4<HSES_FMT_BITS>, dim3(blocks4), dim3(256), 0, s, d_cur, d_v0,
+                                   T, rows, h, cur_stride, leak, v_th, d_spikes, spk_stride, d_v_out);
+                break;
+        }
+        HSES_CHECK_HIP(hipGetLastError());
+        return HSES_OK;
+    }
     switch (fmt) {
         case HSES_FMT_F32:
             hipLaunchKernelGGL(k_lif<HSES_FMT_F32>, dim3(blocks), dim3(256), 0, s, d_cur, d_v0, T,

@@ -3,7 +3,9 @@
   * LIF scan (hses_lif_scan): currents (T=16, M=524288, h=128) fp32 ->
     bit-packed spikes, and -> fp32 spikes;
   * Poisson encode (hses_poisson_encode): p (M=524288, 784) fp32 with 70% exact
-    zeros -> bit-packed spikes (T=16), and -> fp32 spikes for T=4.
+    zeros -> bit-packed spikes (T=16), and -> fp32 spikes for T=4;
+  * torch's device copy of the LIF input (a reference point for the bandwidth
+    a plain read + write stream reaches).
 Each case runs --reps times after a warm-up, timed with events on the launch
 stream; the median is reported with the algorithmic bytes (inputs read once,
 outputs written once) and the fraction of the 8 TB/s HBM peak, one JSON line
@@ -52,6 +54,13 @@ def main():
     T, M, h, d = 16, 8192 * 64, 128, 784
 
     cur = torch.randn((T, M, h), device="cuda", generator=g) * 0.6 + 0.35
+    # reference point: torch's device copy of the same 4.3 GB (read + write)
+    cpy = torch.empty_like(cur)
+    ms = timed(lambda: cpy.copy_(cur), args.reps)
+    report("device copy (torch)", ms, 2 * cur.numel() * 4, shape=[T, M, h])
+    del cpy
+    ms = timed(lambda: cur.sum(), args.reps)
+    report("device read (torch sum)", ms, cur.numel() * 4, shape=[T, M, h])
     for fmt, name, out_b in ((K.FMT_BITS, "lif_scan f32 -> bits", T * M * 2 * 8),
                              (K.FMT_F32, "lif_scan f32 -> f32", T * M * h * 4)):
         spk = torch.empty((T, M, K.fmt_width(fmt, h)), dtype=K._FMT_DTYPE[fmt], device="cuda")

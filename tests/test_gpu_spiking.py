@@ -79,8 +79,13 @@ def test_poisson_threshold_dense_p_sweep(hses_gpu):
     np.testing.assert_array_equal(got.cpu().numpy(), ref)
 
 
+# Rows of a multiple of 64 columns take the 16-byte-load kernel (four
+# (row, word) items per wave; 7 and 15 items leave a partial last wave), others
+# the one-column-per-lane kernel; T = 37 and 20 scan several 16-step chunks.
 @pytest.mark.parametrize("T,M,h,tau,vth", [(8, 64, 128, 10.0, 1.0), (16, 33, 100, 20.0, 0.3),
-                                           (5, 3, 1, 10.0, -1e9), (16, 512, 128, 10.0, 1.0)])
+                                           (5, 3, 1, 10.0, -1e9), (16, 512, 128, 10.0, 1.0),
+                                           (37, 5000, 128, 10.0, 1.0), (20, 3000, 200, 5.0, 0.5),
+                                           (12, 7, 64, 4.0, 0.8), (9, 5, 192, 10.0, 1.0)])
 def test_lif_bit_exact(hses_gpu, T, M, h, tau, vth):
     rng = np.random.default_rng(T * 1000 + h)
     cur = (rng.standard_normal((T, M, h)) * 1.5 + 0.4).astype(np.float32)
