@@ -157,6 +157,26 @@ class SpikingAttentionEs:
         self.step_t = 0
 
     # -- pieces ---------------------------------------------------------------
+    def _side_streams(self):
+        if self.streams is None:
+            self.streams = [torch.cuda.Stream(device=self.dev) for _ in range(4)]
+        return self.streams
+
+    def _fan_out(self, calls):
+        """Independent launches round-robin on the side streams (default priority,
+        a workspace per stream), joined into the current stream afterwards."""
+        main = torch.cuda.current_stream()
+        ready = torch.cuda.Event()
+        ready.record(main)
+        sides = self._side_streams()
+        for side in sides:
+            side.wait_event(ready)
+        for i, fn in enumerate(calls):
+            with torch.cuda.stream(sides[i % len(sides)]):
+                fn()
+        for side in sides:
+            main.wait_stream(side)
+
     def _linear(self, x, x_stride, x_plane, n_time, name, rpm, n, y, y_off, y_stride, y_plane,
                 epoch):
         """Perturbed do_mm of MM leaf `name` over the population (fp32 math), rows
@@ -191,9 +211,10 @@ class SpikingAttentionEs:
         """Poisson spikes, the three encoder projections and their LIF rates -> X."""
         c = self.cfg
         R, d, M = c.ntok, c.d_model, self.M
-        for i, name in enumerate(("in_q", "in_k", "in_v")):
-            self._linear(self.spk, c.tin, M * c.tin, c.T, name, R, c.n, self.cur[i], 0, d, M * d,
-                         epoch)
+        self._fan_out([
+            (lambda i=i, name=name: self._linear(self.spk, c.tin, M * c.tin, c.T, name, R, c.n,
+                                                 self.cur[i], 0, d, M * d, epoch))
+            for i, name in enumerate(("in_q", "in_k", "in_v"))])
         _lib.call("hses_sa_encode", K._p(self.cur[0]), K._p(self.cur[1]), K._p(self.cur[2]), c.T,
                   M, d, R, K._p(self.th["q_th"]), K._p(self.th["k_th"]), K._p(self.th["v_th"]),
                   c.tau_m, K._p(self.noisy["pos_emb"]), 1, K._p(self.X), K._stream())
@@ -201,9 +222,12 @@ class SpikingAttentionEs:
     def attention_block(self, b, epoch, trace=None):
         c = self.cfg
         R, d, M, hd = c.ntok, c.d_model, self.M, c.head_dim
-        for kind, buf in (("q", self.Q), ("k", self.Kt), ("v", self.V)):
-            for h in range(c.heads):
-                self._linear(self.X, d, 0, 1, f"b{b}_{kind}{h}", R, c.n, buf, h * hd, d, 0, epoch)
+        # the 3 x heads projections are independent
+        self._fan_out([
+            (lambda kind=kind, buf=buf, h=h: self._linear(self.X, d, 0, 1, f"b{b}_{kind}{h}", R,
+                                                          c.n, buf, h * hd, d, 0, epoch))
+            for kind, buf in (("q", self.Q), ("k", self.Kt), ("v", self.V))
+            for h in range(c.heads)])
         _lib.call("hses_sa_attention", K._p(self.Q), K._p(self.Kt), K._p(self.V), d, c.n, R,
                   c.heads, hd, K._p(self.th["beta"]), K._p(self.th["attn_th"]), c.g_inh, c.tau_m,
                   c.n_iter, K._p(self.O), K._stream())
@@ -271,12 +295,10 @@ class SpikingAttentionEs:
         # The leaves' updates are independent and each is a few tens of microseconds
         # on a small part of the GPU: they run round-robin on side streams (default
         # priority, each with its own workspace), joined before the next forward.
-        if self.streams is None:
-            self.streams = [torch.cuda.Stream(device=self.dev) for _ in range(4)]
         main = torch.cuda.current_stream()
         ready = torch.cuda.Event()
         ready.record(main)
-        for side in self.streams:
+        for side in self._side_streams():
             side.wait_event(ready)
             z.record_stream(side)
         for i, (name, (a, b), cls) in enumerate(self.leaves):
