@@ -16,6 +16,39 @@ from . import kernels as K
 from ._lib import ACT_RELU_SQ, ACT_SIGMOID, ACT_TANH, FMT_BF16, FMT_F32, MATH_BF16, MATH_F32
 
 
+_SIDE = {}  # device index -> side streams (default priority)
+
+
+def _side_streams(dev):
+    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    if key not in _SIDE:
+        _SIDE[key] = [torch.cuda.Stream(device=dev) for _ in range(4)]
+    return _SIDE[key]
+
+
+def _fan_out(jobs, inputs):
+    """Run independent launches round-robin on side streams, joined into the
+    current stream.  `inputs` (made on the current stream) is recorded on the
+    side streams and every job's output on the current stream, so the caching
+    allocator reuses neither block before the stream that reads it is done."""
+    main = torch.cuda.current_stream()
+    ready = torch.cuda.Event()
+    ready.record(main)
+    sides = _side_streams(inputs.device)
+    for side in sides:
+        side.wait_event(ready)
+        inputs.record_stream(side)
+    out = {}
+    for i, (name, fn) in enumerate(jobs.items()):
+        with torch.cuda.stream(sides[i % len(sides)]):
+            out[name] = fn()
+    for side in sides:
+        main.wait_stream(side)
+    for t in out.values():
+        t.record_stream(main)
+    return out
+
+
 def _stream():
     return K._stream()
 
@@ -181,17 +214,22 @@ def time_mixing(P, x, state, v_first, H, length, layer_id, new_starts=None, es=N
         h = linear_t(inp, P[n1], es.get(n1), math, act=act, out_bf16=bf)
         return linear_t(h, P[n2], es.get(n2), math)
 
-    r = lin(0, "receptance")
-    w = low(xm[1], "w1", "w2", ACT_TANH)  # w2 output; the gate turns it into w
-    k = lin(2, "key")
-    v = lin(3, "value")
+    # the projections and the low-rank branches only read the mixes: they run
+    # side by side (the write-bound narrow products overlap the wide ones)
+    jobs = {"r": lambda: lin(0, "receptance"), "k": lambda: lin(2, "key"),
+            "v": lambda: lin(3, "value"),
+            "g": lambda: low(xm[5], "g1", "g2", ACT_SIGMOID),
+            "w": lambda: low(xm[1], "w1", "w2", ACT_TANH),   # w2 output; the gate makes w
+            "a": lambda: low(xm[4], "a1", "a2", ACT_TANH)}   # a2 output; the gate makes a
+    if layer_id != 0:
+        jobs["v2o"] = lambda: low(xm[3], "v1", "v2", ACT_TANH)
+    res = _fan_out(jobs, xm)
+    r, w, k, v, a, g = (res[n] for n in ("r", "w", "k", "v", "a", "g"))
     if layer_id == 0:
         v_first = v  # only read from here on
         v2o = None
     else:
-        v2o = low(xm[3], "v1", "v2", ACT_TANH)
-    a = low(xm[4], "a1", "a2", ACT_TANH)  # a2 output; the gate turns it into a
-    g = low(xm[5], "g1", "g2", ACT_SIGMOID)
+        v2o = res["v2o"]
     s_in = state[:, 1:, :].reshape(nseq, H, S, S).contiguous()
     # the gates, the kk normalisation and k update, the recurrence, ln_x, the readout and
     # the gate in one kernel, from the raw projections
