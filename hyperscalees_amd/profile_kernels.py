@@ -5,7 +5,10 @@
   * Poisson encode (hses_poisson_encode): p (M=524288, 784) fp32 with 70% exact
     zeros -> bit-packed spikes (T=16), and -> fp32 spikes for T=4;
   * torch's device copy of the LIF input (a reference point for the bandwidth
-    a plain read + write stream reaches).
+    a plain read + write stream reaches);
+  * the exact normal generator (hses_lora_factors) over every pair's factors
+    of C3 fc1 (4096 pairs x (128 + 784) stream rows x 128 ranks = 478 M
+    normals): normals per second, the bound of the factor-drawing kernels.
 Each case runs --reps times after a warm-up, timed with events on the launch
 stream; the median is reported with the algorithmic bytes (inputs read once,
 outputs written once) and the fraction of the 8 TB/s HBM peak, one JSON line
@@ -79,6 +82,13 @@ def main():
     ms = timed(lambda: K.poisson_encode(p, T4, (1, 2, 3, 4), K.FMT_F32, out=f32), args.reps)
     report("poisson_encode -> f32", ms, M * d * 4 + T4 * M * d * 4, shape=[T4, M, d],
            zero_frac=0.7)
+    del p, bits, f32
+
+    pairs, a, b, r = 4096, 128, 784, 128
+    ms = timed(lambda: K.lora_factors(0.01, 12345, r, 0, 0, (0, pairs), a, b), args.reps)
+    normals = pairs * (a + b) * r
+    report("lora_factors (exact normals)", ms, normals * 4, shape=[pairs, a + b, r],
+           g_normals_per_s=round(normals / (ms * 1e-3) / 1e9, 1))
 
 
 if __name__ == "__main__":
