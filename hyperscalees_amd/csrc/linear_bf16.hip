@@ -35,6 +35,20 @@ constexpr int KB_BUF = KB_BM * KB_P;   // bf16 elements of one x (or W) buffer
 constexpr int KB_RMAX = 4;
 constexpr int KB_BPT = 2;              // input-side factor values staged per thread and step
 
+// The direct-to-LDS pipeline (bf16 x, K a multiple of 64): K steps of 64 in
+// two LDS stages, the next step's loads in flight during a step.  A stage holds
+// x and W as 8-row blocks of 1 KB: row r of a block at r * 128 bytes, its k
+// chunk c (8 bf16) in slot c ^ r, so one global_load_lds_dwordx4 fills a block
+// from eight whole 128-byte rows (lane p: row p / 8, chunk (p % 8) ^ (p / 8))
+// and the MFMA operand reads of eight lanes (eight rows, one chunk) hit
+// distinct banks.  Then the input-side factor values of the step (fp32,
+// [member][64 k], one more load).
+constexpr int DL_BK = 64, DL_NS = 2;
+constexpr int DL_XB = KB_BM * DL_BK * 2;          // bytes of x per stage
+constexpr int DL_WB = KB_BN * DL_BK * 2;          // bytes of W per stage
+constexpr int DL_FB = 1024;                       // bytes of factor values per stage
+constexpr int DL_SB = DL_XB + DL_WB + DL_FB;      // 66560 bytes per stage
+
 typedef float f32x16b __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x2b __attribute__((ext_vector_type(2)));
 
@@ -60,19 +74,42 @@ __device__ __forceinline__ float act_value(float v) {
     return v;
 }
 
+// 32 bytes of a pipeline stage's factor values (two 16-byte LDS reads and
+// their wait).  LDS reads the compiler does not see: it would otherwise wait
+// for every stage load in flight (it cannot tell the stages apart); the
+// stage's own loads are complete by the pipeline's explicit vmcnt wait and
+// barrier.
+__device__ __forceinline__ void lds_f8_dl(const float* p, float4& lo, float4& hi) {
+    asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %2 offset:16\n\ts_waitcnt lgkmcnt(0)"
+                 : "=&v"(lo), "=&v"(hi)
+                 : "v"((uint32_t)reinterpret_cast<uintptr_t>(p))
+                 : "memory");
+}
+
+// s_waitcnt vmcnt(N) (expcnt and lgkmcnt not waited for), gfx9 encoding
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 // RK: rank padded to 1 or 4 (zeros past r).  bch: words of one step's staged
 // input-side factor rows, as bf16 pairs of consecutive k ([lm][32][RK], 0
-// without noise).
-template <int XFMT, int RK>
+// without noise).  DL: the direct-to-LDS pipeline (bf16 x, rank
+// 0 or 1, b % 64 == 0); otherwise x and W go through registers, one 64-wide
+// step ahead.
+template <int XFMT, int RK, bool DL>
 __global__ __launch_bounds__(KB_THREADS) void k_gemm_bf16(LinParams P, const uint16_t* __restrict__ Wb,
                                                           int32_t kp, const float* __restrict__ F,
                                                           int32_t bch, int32_t act, int32_t ybf16,
                                                           int32_t vec_y) {
+    static_assert(!DL || XFMT == HSES_FMT_BF16, "the direct-to-LDS pipeline takes bf16 x");
     extern __shared__ __align__(16) unsigned char smem[];
-    uint16_t* Xs = reinterpret_cast<uint16_t*>(smem);   // [2][256][KB_P]
+    uint16_t* Xs = reinterpret_cast<uint16_t*>(smem);   // [2][256][KB_P]; DL: [DL_NS][DL_SB] bytes
     uint16_t* Ws = Xs + 2 * KB_BUF;                      // [2][256][KB_P]
     uint32_t* Bc = reinterpret_cast<uint32_t*>(Ws + 2 * KB_BUF);  // [2][bch] bf16 pairs
-    float* As = reinterpret_cast<float*>(Bc + 2 * bch);  // [lm][256][RK]
+    float* As = DL ? reinterpret_cast<float*>(smem + DL_NS * DL_SB)
+                   : reinterpret_cast<float*>(Bc + 2 * bch);  // [lm][256][RK]
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lc = lane & 31, hl = lane >> 5;
@@ -106,97 +143,7 @@ __global__ __launch_bounds__(KB_THREADS) void k_gemm_bf16(LinParams P, const uin
         }
     }
 
-    // ---- staging: thread -> x row tid / 2 and W row tid / 2, 32 k each ----------
-    const int xr = tid >> 1, xk = (tid & 1) * 32;
-    const bool xvalid = xr < rows_here;
-    const int64_t xoff = xvalid ? tr.offset(P, xr, P.x_stride, P.x_plane) : 0;
-    const int32_t wrow = o0 + xr;
-    const bool wvalid = wrow < a;
-    const uint16_t* wsrc = Wb + (int64_t)(wvalid ? wrow : 0) * kp + xk;
-    constexpr int XU = XFMT == HSES_FMT_F32 ? 8 : 4;  // 16-byte loads of x per thread and step
-    constexpr int XE = XFMT == HSES_FMT_F32 ? 4 : 8;  // elements per 16-byte load
-    uint4 xv[XU], wv[4];
-    uint32_t bv[KB_BPT];
-    // staged factor words of this thread: (member, k pair, rank column), the
-    // source of the pair's first k at step 0 (a step adds 64 rows)
-    const float* bsrc[KB_BPT];
-    int32_t bk2[KB_BPT];
-    bool bon[KB_BPT];
-#pragma unroll
-    for (int j = 0; j < KB_BPT; ++j) {
-        const int32_t e = tid + KB_THREADS * j;  // [lm][kp][c]
-        const int32_t c = e % RK, kp2 = (e / RK) % (KB_BK / 2), lm = e / (RK * (KB_BK / 2));
-        bon[j] = noisy && e < bch && lm < nm && c < r;
-        bk2[j] = 2 * kp2;
-        bsrc[j] = Fm + (bon[j] ? lm * fpitch + (int64_t)(in_off + 2 * kp2) * r + c : 0);
-    }
-    auto load_step = [&](int32_t kt) {
-        const int32_t k0 = kt * KB_BK + xk;
-        // whole steps load unconditionally; the last, partial one masks
-        if (xvalid && k0 + 32 <= b) {
-#pragma unroll
-            for (int q = 0; q < XU; ++q) {
-                if constexpr (XFMT == HSES_FMT_F32)
-                    xv[q] = reinterpret_cast<const uint4*>(static_cast<const float*>(P.x) + xoff + k0)[q];
-                else
-                    xv[q] = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(P.x) + xoff + k0)[q];
-            }
-        } else {
-#pragma unroll
-            for (int q = 0; q < XU; ++q) {
-                const bool ok = xvalid && k0 + XE * q < b;
-                if constexpr (XFMT == HSES_FMT_F32)
-                    xv[q] = ok ? reinterpret_cast<const uint4*>(static_cast<const float*>(P.x) + xoff + k0)[q]
-                               : uint4{0, 0, 0, 0};
-                else
-                    xv[q] = ok ? reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(P.x) + xoff + k0)[q]
-                               : uint4{0, 0, 0, 0};
-            }
-        }
-        if (wvalid) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) wv[q] = reinterpret_cast<const uint4*>(wsrc + kt * KB_BK)[q];
-        } else {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) wv[q] = uint4{0, 0, 0, 0};
-        }
-        if (noisy) {
-#pragma unroll
-            for (int j = 0; j < KB_BPT; ++j) {
-                const bool ok = bon[j] && kt * KB_BK + bk2[j] < b;  // b is even: both k of the pair
-                const float* p = bsrc[j] + (int64_t)kt * KB_BK * r;
-                bv[j] = ok ? pack_bf16x2(p[0], p[r]) : 0u;
-            }
-        }
-    };
-    auto store_step = [&](int buf) {
-        uint16_t* xd = Xs + buf * KB_BUF + xr * KB_P + xk;
-        if constexpr (XFMT == HSES_FMT_F32) {
-#pragma unroll
-            for (int q = 0; q < XU; q += 2) {
-                const uint4 lo = xv[q], hi = xv[q + 1];
-                *reinterpret_cast<uint4*>(xd + 4 * q) = uint4{
-                    pack_bf16x2(__uint_as_float(lo.x), __uint_as_float(lo.y)),
-                    pack_bf16x2(__uint_as_float(lo.z), __uint_as_float(lo.w)),
-                    pack_bf16x2(__uint_as_float(hi.x), __uint_as_float(hi.y)),
-                    pack_bf16x2(__uint_as_float(hi.z), __uint_as_float(hi.w))};
-            }
-        } else {
-#pragma unroll
-            for (int q = 0; q < XU; ++q) *reinterpret_cast<uint4*>(xd + 8 * q) = xv[q];
-        }
-        uint16_t* wd = Ws + buf * KB_BUF + xr * KB_P + xk;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) *reinterpret_cast<uint4*>(wd + 8 * q) = wv[q];
-        if (noisy) {
-#pragma unroll
-            for (int j = 0; j < KB_BPT; ++j) {
-                const int32_t e = tid + KB_THREADS * j;
-                if (e < bch) Bc[buf * bch + e] = bv[j];
-            }
-        }
-    };
-
+    // ---- staging and the K loop ---------------------------------------------------
     f32x16b acc[2][4];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -213,55 +160,247 @@ __global__ __launch_bounds__(KB_THREADS) void k_gemm_bf16(LinParams P, const uin
 #pragma unroll
     for (int c = 0; c < RK; ++c) xb[c] = 0.0f;
 
-    const int32_t nkt = (b + KB_BK - 1) / KB_BK;
-    load_step(0);
-    store_step(0);
-    __syncthreads();
-    for (int32_t kt = 0; kt < nkt; ++kt) {
-        const int cur = kt & 1;
-        if (kt + 1 < nkt) load_step(kt + 1);
-        const uint16_t* X = Xs + cur * KB_BUF;
-        const uint16_t* W = Ws + cur * KB_BUF;
+    if constexpr (DL) {
+        // ---- direct-to-LDS pipeline ------------------------------------------------
+        // As is in LDS before any stage load is issued: the barrier's fence
+        // waits for its stores, with no stage load in flight yet
+        __syncthreads();
+        unsigned char* stg = smem;
+        const int dr = lane >> 3, dc = (lane & 7) ^ (lane >> 3);  // row in the 8-row block, k chunk
+        const uint16_t* xsrc[4];
+        const uint16_t* wsrc[4];
 #pragma unroll
-        for (int ks = 0; ks < KB_BK / 16; ++ks) {
-            const int kk = ks * 16 + hl * 8;
-            u16x8 af[2], bf[4];
+        for (int h = 0; h < 4; ++h) {
+            // wave w fills blocks 4w .. 4w + 3 of x and of W; rows past the tile
+            // read row 0 (finite values in rows and columns that are never stored)
+            const int32_t R = 32 * wave + 8 * h + dr;
+            xsrc[h] = static_cast<const uint16_t*>(P.x) +
+                      tr.offset(P, R < rows_here ? R : 0, P.x_stride, P.x_plane) + dc * 8;
+            wsrc[h] = Wb + (int64_t)(o0 + R < a ? o0 + R : 0) * kp + dc * 8;
+        }
+        // factor values: lane p holds member p / 16, floats (p % 16) * 4 .. of the
+        // step's 64 k (every wave loads them: the same bytes)
+        const bool f_on = noisy && lane < nm * 16;
+        const float* fsrc = Fm + (f_on ? (int64_t)(lane >> 4) * fpitch + in_off + (lane & 15) * 4 : 0);
+        auto issue = [&](int32_t st) {
+            unsigned char* base = stg + (st & 1) * DL_SB;
 #pragma unroll
-            for (int i = 0; i < 2; ++i) af[i] = lds_u16x8(X + (wr * 64 + 32 * i + lc) * KB_P + kk);
+            for (int h = 0; h < 4; ++h)
+                __builtin_amdgcn_global_load_lds(xsrc[h] + st * DL_BK, base + (4 * wave + h) * 1024, 16, 0, 0);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) bf[j] = lds_u16x8(W + (wc * 128 + 32 * j + lc) * KB_P + kk);
-            // D = W x^T: a lane's accumulator holds one output row (its x row)
-            // and runs of four consecutive output columns
+            for (int h = 0; h < 4; ++h)
+                __builtin_amdgcn_global_load_lds(wsrc[h] + st * DL_BK, base + DL_XB + (4 * wave + h) * 1024,
+                                                 16, 0, 0);
+            if (noisy && f_on)
+                __builtin_amdgcn_global_load_lds(fsrc + (int64_t)st * DL_BK, base + DL_XB + DL_WB, 16, 0, 0);
+        };
+        const int32_t nkt = b / DL_BK;
+        issue(0);
+        // operand byte offsets (block and row); the chunk slot depends on the slice
+        int32_t aoff[2], boff[4];
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < 2; ++i) aoff[i] = (8 * wr + 4 * i + (lc >> 3)) * 1024 + (lc & 7) * 128;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] = mfma32b(bf[j], af[i], acc[i][j]);
+        for (int j = 0; j < 4; ++j) boff[j] = DL_XB + (16 * wc + 4 * j + (lc >> 3)) * 1024 + (lc & 7) * 128;
+        for (int32_t kt = 0; kt < nkt; ++kt) {
+            vm_wait<0>();  // this wave's loads of stage kt (the only ones in flight)
+            // every wave's loads of stage kt are in LDS, and every wave is done
+            // with stage kt - 1, whose buffer the load of stage kt + 1 reuses
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);  // nothing of this step moves above the wait
+            if (kt + 1 < nkt) issue(kt + 1);
+            const unsigned char* base = stg + (kt & 1) * DL_SB;
+            const float* Fs = reinterpret_cast<const float*>(base + DL_XB + DL_WB);
+            // operand fragments one 16-wide k slice ahead: the reads of slice
+            // ks + 1 are in flight while slice ks's MFMAs run
+            auto frag = [&](int ks, u16x8 (&fa)[2], u16x8 (&fb)[4]) {
+                const int32_t cx = ((2 * ks + hl) ^ (lc & 7)) << 4;  // this lane's k chunk slot
+#pragma unroll
+                for (int i = 0; i < 2; ++i) fa[i] = *reinterpret_cast<const u16x8*>(base + aoff[i] + cx);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) fb[j] = *reinterpret_cast<const u16x8*>(base + boff[j] + cx);
+            };
+            // the factor values of k 16 ks + 8 hl .. + 8 of row xbr (the read
+            // waits for the fragments already issued too)
+            auto fvals = [&](int ks, float4 (&fv)[2]) {
+                lds_f8_dl(Fs + xbm * DL_BK + 16 * ks + 8 * hl, fv[0], fv[1]);
+            };
+            auto slice = [&](const u16x8 (&fa)[2], const u16x8 (&fb)[4], const float4 (&fv)[2]) {
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) acc[i][j] = mfma32b(fb[j], fa[i], acc[i][j]);
+                if (noisy) {
+                    // pairs of consecutive k: the factor rounded to bf16 as the
+                    // register pipeline stages it
+                    const uint4 x0 = __builtin_bit_cast(uint4, fa[0]), x1 = __builtin_bit_cast(uint4, fa[1]);
+                    xb[0] = dot2_bf16(wc ? x1.x : x0.x, pack_bf16x2(fv[0].x, fv[0].y), xb[0]);
+                    xb[0] = dot2_bf16(wc ? x1.y : x0.y, pack_bf16x2(fv[0].z, fv[0].w), xb[0]);
+                    xb[0] = dot2_bf16(wc ? x1.z : x0.z, pack_bf16x2(fv[1].x, fv[1].y), xb[0]);
+                    xb[0] = dot2_bf16(wc ? x1.w : x0.w, pack_bf16x2(fv[1].z, fv[1].w), xb[0]);
+                }
+            };
+            static_assert(DL_BK == 64 && RK == 1, "four 16-wide k slices per stage, rank 1");
+            u16x8 a0[2], b0[4], a1[2], b1[4];
+            float4 f0[2], f1[2];
+            frag(0, a0, b0);
+            if (noisy) fvals(0, f0);
+            frag(1, a1, b1);
+            slice(a0, b0, f0);
+            if (noisy) fvals(1, f1);
+            frag(2, a0, b0);
+            slice(a1, b1, f1);
+            if (noisy) fvals(2, f0);
+            frag(3, a1, b1);
+            slice(a0, b0, f0);
+            if (noisy) fvals(3, f1);
+            slice(a1, b1, f1);
+        }
+        // the epilogue reuses stage 0 for x B_m: every wave is past its last read
+        __syncthreads();
+    } else {
+        // ---- staging: thread -> x row tid / 2 and W row tid / 2, 32 k each ----------
+        const int xr = tid >> 1, xk = (tid & 1) * 32;
+        const bool xvalid = xr < rows_here;
+        const int64_t xoff = xvalid ? tr.offset(P, xr, P.x_stride, P.x_plane) : 0;
+        const int32_t wrow = o0 + xr;
+        const bool wvalid = wrow < a;
+        const uint16_t* wsrc = Wb + (int64_t)(wvalid ? wrow : 0) * kp + xk;
+        constexpr int XU = XFMT == HSES_FMT_F32 ? 8 : 4;  // 16-byte loads of x per thread and step
+        constexpr int XE = XFMT == HSES_FMT_F32 ? 4 : 8;  // elements per 16-byte load
+        uint4 xv[XU], wv[4];
+        uint32_t bv[KB_BPT];
+        // staged factor words of this thread: (member, k pair, rank column), the
+        // source of the pair's first k at step 0 (a step adds 64 rows)
+        const float* bsrc[KB_BPT];
+        int32_t bk2[KB_BPT];
+        bool bon[KB_BPT];
+    #pragma unroll
+        for (int j = 0; j < KB_BPT; ++j) {
+            const int32_t e = tid + KB_THREADS * j;  // [lm][kp][c]
+            const int32_t c = e % RK, kp2 = (e / RK) % (KB_BK / 2), lm = e / (RK * (KB_BK / 2));
+            bon[j] = noisy && e < bch && lm < nm && c < r;
+            bk2[j] = 2 * kp2;
+            bsrc[j] = Fm + (bon[j] ? lm * fpitch + (int64_t)(in_off + 2 * kp2) * r + c : 0);
+        }
+        auto load_step = [&](int32_t kt) {
+            const int32_t k0 = kt * KB_BK + xk;
+            // whole steps load unconditionally; the last, partial one masks
+            if (xvalid && k0 + 32 <= b) {
+    #pragma unroll
+                for (int q = 0; q < XU; ++q) {
+                    if constexpr (XFMT == HSES_FMT_F32)
+                        xv[q] = reinterpret_cast<const uint4*>(static_cast<const float*>(P.x) + xoff + k0)[q];
+                    else
+                        xv[q] = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(P.x) + xoff + k0)[q];
+                }
+            } else {
+    #pragma unroll
+                for (int q = 0; q < XU; ++q) {
+                    const bool ok = xvalid && k0 + XE * q < b;
+                    if constexpr (XFMT == HSES_FMT_F32)
+                        xv[q] = ok ? reinterpret_cast<const uint4*>(static_cast<const float*>(P.x) + xoff + k0)[q]
+                                   : uint4{0, 0, 0, 0};
+                    else
+                        xv[q] = ok ? reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(P.x) + xoff + k0)[q]
+                                   : uint4{0, 0, 0, 0};
+                }
+            }
+            if (wvalid) {
+    #pragma unroll
+                for (int q = 0; q < 4; ++q) wv[q] = reinterpret_cast<const uint4*>(wsrc + kt * KB_BK)[q];
+            } else {
+    #pragma unroll
+                for (int q = 0; q < 4; ++q) wv[q] = uint4{0, 0, 0, 0};
+            }
             if (noisy) {
-                // the factor's bf16 pairs of these 8 k: [lm][pair][c]
-                const uint4* bs = reinterpret_cast<const uint4*>(
-                    Bc + cur * bch + (xbm * (KB_BK / 2) + ks * 8 + hl * 4) * RK);
-                const uint4 xw = __builtin_bit_cast(uint4, wc ? af[1] : af[0]);
-                const uint32_t xp[4] = {xw.x, xw.y, xw.z, xw.w};
-                if constexpr (RK == 1) {
-                    const uint4 q = bs[0];  // pairs u = 0..3
-                    xb[0] = dot2_bf16(xp[0], q.x, xb[0]);
-                    xb[0] = dot2_bf16(xp[1], q.y, xb[0]);
-                    xb[0] = dot2_bf16(xp[2], q.z, xb[0]);
-                    xb[0] = dot2_bf16(xp[3], q.w, xb[0]);
-                } else {
-#pragma unroll
-                    for (int u = 0; u < 4; ++u) {
-                        const uint4 q = bs[u];  // rank columns 0..3 of pair u
-                        xb[0] = dot2_bf16(xp[u], q.x, xb[0]);
-                        xb[1] = dot2_bf16(xp[u], q.y, xb[1]);
-                        xb[2] = dot2_bf16(xp[u], q.z, xb[2]);
-                        xb[3] = dot2_bf16(xp[u], q.w, xb[3]);
+    #pragma unroll
+                for (int j = 0; j < KB_BPT; ++j) {
+                    const bool ok = bon[j] && kt * KB_BK + bk2[j] < b;  // b is even: both k of the pair
+                    const float* p = bsrc[j] + (int64_t)kt * KB_BK * r;
+                    bv[j] = ok ? pack_bf16x2(p[0], p[r]) : 0u;
+                }
+            }
+        };
+        auto store_step = [&](int buf) {
+            uint16_t* xd = Xs + buf * KB_BUF + xr * KB_P + xk;
+            if constexpr (XFMT == HSES_FMT_F32) {
+    #pragma unroll
+                for (int q = 0; q < XU; q += 2) {
+                    const uint4 lo = xv[q], hi = xv[q + 1];
+                    *reinterpret_cast<uint4*>(xd + 4 * q) = uint4{
+                        pack_bf16x2(__uint_as_float(lo.x), __uint_as_float(lo.y)),
+                        pack_bf16x2(__uint_as_float(lo.z), __uint_as_float(lo.w)),
+                        pack_bf16x2(__uint_as_float(hi.x), __uint_as_float(hi.y)),
+                        pack_bf16x2(__uint_as_float(hi.z), __uint_as_float(hi.w))};
+                }
+            } else {
+    #pragma unroll
+                for (int q = 0; q < XU; ++q) *reinterpret_cast<uint4*>(xd + 8 * q) = xv[q];
+            }
+            uint16_t* wd = Ws + buf * KB_BUF + xr * KB_P + xk;
+    #pragma unroll
+            for (int q = 0; q < 4; ++q) *reinterpret_cast<uint4*>(wd + 8 * q) = wv[q];
+            if (noisy) {
+    #pragma unroll
+                for (int j = 0; j < KB_BPT; ++j) {
+                    const int32_t e = tid + KB_THREADS * j;
+                    if (e < bch) Bc[buf * bch + e] = bv[j];
+                }
+            }
+        };
+
+        const int32_t nkt = (b + KB_BK - 1) / KB_BK;
+        load_step(0);
+        store_step(0);
+        __syncthreads();
+        for (int32_t kt = 0; kt < nkt; ++kt) {
+            const int cur = kt & 1;
+            if (kt + 1 < nkt) load_step(kt + 1);
+            const uint16_t* X = Xs + cur * KB_BUF;
+            const uint16_t* W = Ws + cur * KB_BUF;
+    #pragma unroll
+            for (int ks = 0; ks < KB_BK / 16; ++ks) {
+                const int kk = ks * 16 + hl * 8;
+                u16x8 af[2], bf[4];
+    #pragma unroll
+                for (int i = 0; i < 2; ++i) af[i] = lds_u16x8(X + (wr * 64 + 32 * i + lc) * KB_P + kk);
+    #pragma unroll
+                for (int j = 0; j < 4; ++j) bf[j] = lds_u16x8(W + (wc * 128 + 32 * j + lc) * KB_P + kk);
+                // D = W x^T: a lane's accumulator holds one output row (its x row)
+                // and runs of four consecutive output columns
+    #pragma unroll
+                for (int i = 0; i < 2; ++i)
+    #pragma unroll
+                    for (int j = 0; j < 4; ++j) acc[i][j] = mfma32b(bf[j], af[i], acc[i][j]);
+                if (noisy) {
+                    // the factor's bf16 pairs of these 8 k: [lm][pair][c]
+                    const uint4* bs = reinterpret_cast<const uint4*>(
+                        Bc + cur * bch + (xbm * (KB_BK / 2) + ks * 8 + hl * 4) * RK);
+                    const uint4 xw = __builtin_bit_cast(uint4, wc ? af[1] : af[0]);
+                    const uint32_t xp[4] = {xw.x, xw.y, xw.z, xw.w};
+                    if constexpr (RK == 1) {
+                        const uint4 q = bs[0];  // pairs u = 0..3
+                        xb[0] = dot2_bf16(xp[0], q.x, xb[0]);
+                        xb[0] = dot2_bf16(xp[1], q.y, xb[0]);
+                        xb[0] = dot2_bf16(xp[2], q.z, xb[0]);
+                        xb[0] = dot2_bf16(xp[3], q.w, xb[0]);
+                    } else {
+    #pragma unroll
+                        for (int u = 0; u < 4; ++u) {
+                            const uint4 q = bs[u];  // rank columns 0..3 of pair u
+                            xb[0] = dot2_bf16(xp[u], q.x, xb[0]);
+                            xb[1] = dot2_bf16(xp[u], q.y, xb[1]);
+                            xb[2] = dot2_bf16(xp[u], q.z, xb[2]);
+                            xb[3] = dot2_bf16(xp[u], q.w, xb[3]);
+                        }
                     }
                 }
             }
+            if (kt + 1 < nkt) store_step(cur ^ 1);
+            __syncthreads();
         }
-        if (kt + 1 < nkt) store_step(cur ^ 1);
-        __syncthreads();
+
     }
 
     // ---- epilogue: y = act(x W^T + (x B_m) A_m^T) ---------------------------------
@@ -409,10 +548,12 @@ static int32_t bf16_kp(int32_t b) { return (b + KB_BK - 1) / KB_BK * KB_BK; }
 
 struct Bf16Plan {
     int32_t rk, nm, bch, kp;
+    bool dl;  // the direct-to-LDS pipeline
     size_t lds, w_bytes, f_bytes;
 };
 
-static bool bf16_plan(int32_t a, int32_t b, int32_t r, int32_t n, int32_t R, Bf16Plan* pl) {
+static bool bf16_plan(int32_t a, int32_t b, int32_t r, int32_t n, int32_t R, bool bf16_x, int32_t in_off,
+                      Bf16Plan* pl) {
     if (a < KB_BN || b < 1 || n < 1 || r < 0 || r > KB_RMAX || b % 8) return false;
     pl->rk = bf16_rk(r);
     pl->nm = bf16_nm_max(R, n);
@@ -422,6 +563,11 @@ static bool bf16_plan(int32_t a, int32_t b, int32_t r, int32_t n, int32_t R, Bf1
     pl->bch = (int32_t)bch;
     const size_t a_lds = r > 0 ? (size_t)pl->nm * KB_BN * pl->rk : 0;
     pl->lds = (size_t)4 * KB_BUF * 2 + (2 * bch + a_lds) * 4;
+    // direct-to-LDS: bf16 x, whole 64-wide K steps, rank 0 or 1 (the factor
+    // values of a step contiguous per member, 16-byte aligned, at most 1 KB)
+    pl->dl = bf16_x && b % DL_BK == 0 && pl->rk == 1 &&
+             (r == 0 || (pl->nm <= 4 && ((int64_t)(a + b) * r) % 4 == 0 && ((int64_t)in_off * r) % 4 == 0));
+    if (pl->dl) pl->lds = (size_t)DL_NS * DL_SB + a_lds * 4;
     pl->w_bytes = align16((size_t)a * pl->kp * 2);
     pl->f_bytes = r > 0 ? align16((size_t)n * (a + b) * r * 4) : 0;
     return true;
@@ -431,7 +577,7 @@ size_t linear_bf16_workspace(int32_t a, int32_t b, int32_t r, int32_t n, int32_t
                              int32_t n_time, int32_t math) {
     if (math != HSES_MATH_BF16 || (int64_t)rows_per_member * n_time > INT32_MAX) return 0;
     Bf16Plan pl;
-    if (!bf16_plan(a, b, r, n, rows_per_member * n_time, &pl)) return 0;
+    if (!bf16_plan(a, b, r, n, rows_per_member * n_time, false, 0, &pl)) return 0;
     return pl.w_bytes + pl.f_bytes;
 }
 
@@ -441,7 +587,9 @@ int launch_linear_bf16(LinParams& P, DeviceState* st, hipStream_t s, void* work,
     if (P.x_fmt != HSES_FMT_F32 && P.x_fmt != HSES_FMT_BF16) return HSES_ERR_UNSUPPORTED;
     const int32_t r = (P.r > 0 && P.bs != 0.0f) ? P.r : 0;
     Bf16Plan pl;
-    if (!bf16_plan(P.a, P.b, r, P.n, P.R, &pl) || pl.lds > st->max_lds) return HSES_ERR_UNSUPPORTED;
+    if (!bf16_plan(P.a, P.b, r, P.n, P.R, P.x_fmt == HSES_FMT_BF16, P.tmm ? P.a : 0, &pl) ||
+        pl.lds > st->max_lds)
+        return HSES_ERR_UNSUPPORTED;
     // 16-byte loads of 8 (bf16) or 4 (fp32) elements: aligned rows, whole groups
     const int64_t vec = P.x_fmt == HSES_FMT_F32 ? 4 : 8;
     if (reinterpret_cast<uintptr_t>(P.x) % 16 || P.x_stride % vec || (P.n_time > 1 && P.x_plane % vec))
@@ -480,10 +628,11 @@ int launch_linear_bf16(LinParams& P, DeviceState* st, hipStream_t s, void* work,
     auto by_rk = [&](auto fmt) -> int {
         constexpr int X = decltype(fmt)::value;
         switch (pl.rk) {
-            case 1: return launch(k_gemm_bf16<X, 1>);
-            default: return launch(k_gemm_bf16<X, 4>);
+            case 1: return launch(k_gemm_bf16<X, 1, false>);
+            default: return launch(k_gemm_bf16<X, 4, false>);
         }
     };
+    if (pl.dl) return launch(k_gemm_bf16<HSES_FMT_BF16, 1, true>);
     return P.x_fmt == HSES_FMT_F32 ? by_rk(std::integral_constant<int, HSES_FMT_F32>{})
                                    : by_rk(std::integral_constant<int, HSES_FMT_BF16>{});
 }

@@ -337,6 +337,29 @@ def test_bf16_gemm_kernel(hses_gpu, n, rpm, T, a, b, r, tid_lo, fmt, sigma):
     assert_close(y, ref_forward(x3, W, A, B, rpm), 2e-2)
 
 
+@pytest.mark.parametrize("n,rpm,T,a,b,r,tid_lo,sigma", [
+    (4, 128, 1, 512, 512, 1, 0, 0.2),     # C5 square layer
+    (2, 128, 1, 2048, 512, 1, 0, 0.2),    # ChannelMixing key width
+    (2, 128, 1, 512, 2048, 1, 0, 0.2),    # ChannelMixing value: 64 K steps
+    (3, 128, 1, 512, 32, 1, 1, 0.2),      # one K step (w2 / a2 / v2)
+    (3, 128, 1, 512, 96, 1, 0, 0.2),      # three K steps (g2)
+    (3, 100, 1, 300, 64, 1, 2, 0.2),      # ragged rows and output width
+    (2, 64, 4, 256, 128, 4, 2, 0.2),      # time-major planes, rank 4
+    (6, 64, 1, 256, 160, 4, 0, 0.2),      # rank 4, four members per tile (register path)
+    (2, 128, 1, 512, 256, 1, 0, 0.0),     # sigma 0
+])
+def test_bf16_gemm_bf16_x_equals_f32_x(hses_gpu, n, rpm, T, a, b, r, tid_lo, sigma):
+    # bf16 x takes the direct-to-LDS pipeline where it applies, fp32 x holding
+    # the same (bf16-representable) values the register pipeline: the same
+    # operands, products and accumulation order, so the outputs are equal
+    rng = np.random.default_rng(n * 17 + a + b + r)
+    x3 = bf16_round(rng.standard_normal((T, n * rpm, b)).astype(np.float32))
+    W = (rng.standard_normal((a, b)) / np.sqrt(b)).astype(np.float32)
+    y32 = run(hses_gpu, x3, W, r, sigma, n, rpm, tid_lo, fmt=FMT_F32, math=MATH_BF16)
+    y16 = run(hses_gpu, x3, W, r, sigma, n, rpm, tid_lo, fmt=FMT_BF16, math=MATH_BF16)
+    np.testing.assert_array_equal(y16, y32)
+
+
 @pytest.mark.parametrize("act", [1, 2, 3])
 def test_bf16_gemm_activation_bf16_out(hses_gpu, act):
     from hyperscalees_amd._lib import ACT_RELU_SQ, ACT_SIGMOID, ACT_TANH
