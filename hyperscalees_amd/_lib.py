@@ -120,6 +120,8 @@ PROTOTYPES = {
                                              c_vp, c_vp]),
     "hses_add_layer_norm": (ctypes.c_int, [c_vp, c_vp, c_i64, c_i32, c_vp, c_vp, c_f32, c_vp,
                                            c_vp]),
+    "hses_add_ln_shift": (ctypes.c_int, [c_vp, c_vp, c_i64, c_i32, c_i32, c_vp, c_vp, c_f32, c_vp,
+                                         c_vp, c_vp, c_i32, c_vp, c_i32, c_vp, c_i32, c_vp]),
     "hses_read_idx_images": (ctypes.c_int, [c_vp, c_size, c_vp, c_i64, c_vp, c_vp]),
     "hses_read_idx_labels": (ctypes.c_int, [c_vp, c_size, c_vp, c_i64, c_vp]),
     "hses_shuffled_indices": (ctypes.c_int, [c_i64, c_i64, c_u64, c_vp]),

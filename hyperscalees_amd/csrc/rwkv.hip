@@ -12,6 +12,8 @@
 // instructions (about an ulp each) in place of libm-accurate routines.
 #include <math.h>
 
+#include <type_traits>
+
 #include "runtime.h"
 
 namespace hses {
@@ -542,6 +544,115 @@ __global__ __launch_bounds__(256) void k_add_layer_norm4(float* __restrict__ x,
     }
 }
 
+// A block's residual add, the LayerNorm that reads it and the next module's
+// token shift in one pass (llm.rs:66-83, 200-205, 360-381): one wave per
+// sequence walks its T rows in order, so the previous row's normalised values
+// are still in its registers when the row's mixes are formed; the next two
+// rows' x and delta are loaded ahead.  Per row the arithmetic is that of
+// k_add_layer_norm4 (ADD) followed by k_token_shift_mix4, element for element,
+// so the mixes (and x) equal the two-kernel chain's bit for bit; without ADD the
+// row is normalised as k_add_layer_norm4 normalises x + 0 and x is not written.
+// y_last (or NULL) receives the normalised row length - 1 (the next shift state).
+template <int NV, int NMIX, bool ADD, bool BF16OUT>
+__global__ __launch_bounds__(256) void k_ln_shift(float* __restrict__ x, const float* __restrict__ d,
+                                                  int64_t nseq, int32_t T,
+                                                  const float* __restrict__ w,
+                                                  const float* __restrict__ b, float eps,
+                                                  const float* __restrict__ state,
+                                                  const uint8_t* __restrict__ new_starts,
+                                                  const float* __restrict__ mix,
+                                                  void* __restrict__ out,
+                                                  float* __restrict__ y_last, int32_t length) {
+    constexpr int C = 256 * NV;
+    const int64_t q = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (q >= nseq) return;  // whole wave
+    const int64_t plane = nseq * T * C;  // elements of one mix's output
+    float4 wv[NV], bv[NV], mv[NMIX][NV], prev[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        wv[j] = reinterpret_cast<const float4*>(w)[64 * j + lane];
+        bv[j] = reinterpret_cast<const float4*>(b)[64 * j + lane];
+        prev[j] = reinterpret_cast<const float4*>(state + q * C)[64 * j + lane];
+#pragma unroll
+        for (int m = 0; m < NMIX; ++m) mv[m][j] = reinterpret_cast<const float4*>(mix + (int64_t)m * C)[64 * j + lane];
+    }
+    float4 xa[3][NV], da[3][NV];  // rows t, t + 1, t + 2
+    auto load = [&](int32_t t, float4 (&xo)[NV], float4 (&dout)[NV]) {
+        const int64_t r = q * T + (t < T ? t : T - 1);  // past the end: the last row again
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            xo[j] = reinterpret_cast<const float4*>(x + r * C)[64 * j + lane];
+            if constexpr (ADD) dout[j] = reinterpret_cast<const float4*>(d + r * C)[64 * j + lane];
+        }
+    };
+    load(0, xa[0], da[0]);
+    load(1, xa[1], da[1]);
+    for (int32_t t = 0; t < T; ++t) {
+        load(t + 2, xa[2], da[2]);
+        const int64_t r = q * T + t;
+        float4 v[NV];
+        float s = 0.0f, s2 = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const float4 a = xa[0][j];
+            if constexpr (ADD) {
+                const float4 e = da[0][j];
+                v[j] = float4{a.x + e.x, a.y + e.y, a.z + e.z, a.w + e.w};
+                reinterpret_cast<float4*>(x + r * C)[64 * j + lane] = v[j];
+            } else {
+                v[j] = float4{a.x + 0.0f, a.y + 0.0f, a.z + 0.0f, a.w + 0.0f};
+            }
+            s = s + v[j].x;
+            s = s + v[j].y;
+            s = s + v[j].z;
+            s = s + v[j].w;
+            s2 = s2 + v[j].x * v[j].x;
+            s2 = s2 + v[j].y * v[j].y;
+            s2 = s2 + v[j].z * v[j].z;
+            s2 = s2 + v[j].w * v[j].w;
+        }
+        const float mean = wave_sum(s) / (float)C;
+        const float var = wave_sum(s2) / (float)C - mean * mean;
+        const float sd = sqrtf(var + eps);
+        const bool fresh = new_starts && new_starts[r];
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const float4 ww = wv[j], bb = bv[j];
+            const float4 y{(v[j].x - mean) / sd * ww.x + bb.x, (v[j].y - mean) / sd * ww.y + bb.y,
+                           (v[j].z - mean) / sd * ww.z + bb.z, (v[j].w - mean) / sd * ww.w + bb.w};
+            if (y_last && t == length - 1) reinterpret_cast<float4*>(y_last + q * C)[64 * j + lane] = y;
+            const float4 pv = fresh ? float4{0.0f, 0.0f, 0.0f, 0.0f} : prev[j];
+            const float sx0 = pv.x - y.x, sx1 = pv.y - y.y, sx2 = pv.z - y.z, sx3 = pv.w - y.w;
+            const int64_t e = r * C + 4 * (64 * j + lane);
+#pragma unroll
+            for (int m = 0; m < NMIX; ++m) {
+                const float4 mm = mv[m][j];
+                const float v0 = y.x + sx0 * mm.x, v1 = y.y + sx1 * mm.y;
+                const float v2 = y.z + sx2 * mm.z, v3 = y.w + sx3 * mm.w;
+                if constexpr (BF16OUT) {
+                    const uint2 pk{(uint32_t)f2bf_rne(v0) | ((uint32_t)f2bf_rne(v1) << 16),
+                                   (uint32_t)f2bf_rne(v2) | ((uint32_t)f2bf_rne(v3) << 16)};
+                    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + (int64_t)m * plane + e) = pk;
+                } else {
+                    *reinterpret_cast<float4*>(static_cast<float*>(out) + (int64_t)m * plane + e) =
+                        float4{v0, v1, v2, v3};
+                }
+            }
+            prev[j] = y;
+        }
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            xa[0][j] = xa[1][j];
+            xa[1][j] = xa[2][j];
+            if constexpr (ADD) {
+                da[0][j] = da[1][j];
+                da[1][j] = da[2][j];
+            }
+        }
+    }
+}
+
 // k_tm_gates and k_tm_kk in one pass, per (row, head), one wave each: the
 // same per-element operations (a stays in registers instead of memory), so the
 // outputs equal the two-kernel chain bit for bit.
@@ -791,6 +902,51 @@ extern "C" int hses_add_layer_norm(float* d_x, const float* d_delta, int64_t row
         hipLaunchKernelGGL(k_add_layer_norm4<4>, g, blk, 0, s, d_x, d_delta, rows, d_w, d_b, eps, d_y);
     else
         hipLaunchKernelGGL(k_add_layer_norm, g, blk, 0, s, d_x, d_delta, rows, C, d_w, d_b, eps, d_y);
+    HSES_CHECK_HIP(hipGetLastError());
+    return HSES_OK;
+}
+
+extern "C" int hses_add_ln_shift(float* d_x, const float* d_delta, int64_t nseq, int32_t T, int32_t C,
+                                 const float* d_w, const float* d_b, float eps, const float* d_state,
+                                 const uint8_t* d_new_starts, const float* d_mix, int32_t n_mix,
+                                 void* d_out, int32_t out_fmt, float* d_y_last, int32_t length,
+                                 void* stream) {
+    HSES_REQUIRE(nseq >= 0 && T >= 1 && C >= 1, "bad sizes");
+    HSES_REQUIRE(out_fmt == HSES_FMT_F32 || out_fmt == HSES_FMT_BF16, "out_fmt must be F32 or BF16");
+    HSES_REQUIRE(!d_y_last || (length >= 1 && length <= T), "length must be in [1, T]");
+    if (nseq == 0) return HSES_OK;
+    HSES_REQUIRE(d_x && d_w && d_b && d_state && d_mix && d_out, "NULL pointer");
+    const auto a16 = [](const void* p) { return p == nullptr || reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    if (!((C == 256 || C == 512 || C == 1024) && (n_mix == 1 || n_mix == 6) && a16(d_x) && a16(d_delta) &&
+          a16(d_w) && a16(d_b) && a16(d_state) && a16(d_mix) && a16(d_out) && a16(d_y_last)))
+        return set_error(HSES_ERR_UNSUPPORTED,
+                         "fused add + LayerNorm + token shift: C in {256, 512, 1024}, 1 or 6 mixes, "
+                         "16-byte aligned buffers");
+    HSES_REQUIRE((nseq + 3) / 4 < (1ll << 31), "grid too large");
+    const dim3 g(blocks_of(nseq, 4)), blk(256);
+    hipStream_t s = (hipStream_t)stream;
+    const bool add = d_delta != nullptr, bf = out_fmt == HSES_FMT_BF16;
+    auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, g, blk, 0, s, d_x, d_delta, nseq, T, d_w, d_b, eps, d_state,
+                           d_new_starts, d_mix, d_out, d_y_last, length);
+    };
+    auto by_fmt = [&](auto nv, auto nm, auto ad) {
+        constexpr int NV = decltype(nv)::value, NM = decltype(nm)::value;
+        constexpr bool AD = decltype(ad)::value;
+        if (bf) go(k_ln_shift<NV, NM, AD, true>);
+        else go(k_ln_shift<NV, NM, AD, false>);
+    };
+    auto by_add = [&](auto nv, auto nm) {
+        if (add) by_fmt(nv, nm, std::true_type{});
+        else by_fmt(nv, nm, std::false_type{});
+    };
+    auto by_mix = [&](auto nv) {
+        if (n_mix == 1) by_add(nv, std::integral_constant<int, 1>{});
+        else by_add(nv, std::integral_constant<int, 6>{});
+    };
+    if (C == 256) by_mix(std::integral_constant<int, 1>{});
+    else if (C == 512) by_mix(std::integral_constant<int, 2>{});
+    else by_mix(std::integral_constant<int, 4>{});
     HSES_CHECK_HIP(hipGetLastError());
     return HSES_OK;
 }

@@ -145,19 +145,56 @@ def linear(x, W, es=None, math=MATH_F32, act=0, out_bf16=False):
     return y.reshape(nseq, T, W.shape[0])
 
 
+def add_layer_norm_shift(x, delta, w, b, eps, state, mixes, new_starts=None, bf16=False,
+                         length=None, want_last=False):
+    """A block's residual add (x += delta in place; delta None: x only read), the
+    LayerNorm y of x, and the next module's token shift of y with the mixing
+    vectors mixes (n_mix, C): returns (out (n_mix, nseq, T, C), y[:, length-1]
+    or None).  x (nseq, T, C), state (nseq, C) the previous token's y.  One fused
+    kernel where it applies (C 256 / 512 / 1024, 1 or 6 mixes), else the two
+    steps; the values are the same bit for bit."""
+    K._dev(x, torch.float32, "x")
+    nseq, T, C = x.shape
+    length = T if length is None else length
+    n_mix = mixes.shape[0]
+    dt = torch.bfloat16 if bf16 else torch.float32
+    state = state.contiguous()
+    mixes = mixes.contiguous()
+    if C in (256, 512, 1024) and n_mix in (1, 6):
+        out = torch.empty((n_mix, nseq, T, C), dtype=dt, device=x.device)
+        last = torch.empty((nseq, C), dtype=torch.float32, device=x.device) if want_last else None
+        if new_starts is not None:
+            K._dev(new_starts, torch.uint8, "new_starts")
+        _lib.call("hses_add_ln_shift", _p(x), _p(delta), nseq, T, C, _p(w), _p(b), eps, _p(state),
+                  _p(new_starts), _p(mixes), n_mix, _p(out), FMT_BF16 if bf16 else FMT_F32,
+                  _p(last), length, _stream())
+        return out, last
+    y = torch.empty_like(x)
+    if delta is None:
+        layer_norm(x, w, b, eps, out=y)
+    else:
+        _lib.call("hses_add_layer_norm", _p(x), _p(delta), nseq * T, C, _p(w), _p(b), eps, _p(y),
+                  _stream())
+    out = token_shift_mix(y, state, mixes, new_starts, bf16=bf16)
+    return out, (y[:, length - 1, :].contiguous() if want_last else None)
+
+
 def channel_mixing(x, state, x_k, Wk, Wv, length, new_starts=None, es_key=None, es_value=None,
-                   math=MATH_F32, want_last=True):
+                   math=MATH_F32, want_last=True, xk=None, last=None):
     """ChannelMixing::forward (llm.rs:191-213) on every sequence:
     xk = x + ([state, x[:-1]] - x) * x_k; out = relu(xk Wk^T)^2 Wv^T; last = x[length-1].
-    x (nseq, T, C), state (nseq, C), Wk (F, C), Wv (C, F)."""
+    x (nseq, T, C), state (nseq, C), Wk (F, C), Wv (C, F).  With xk (and last)
+    given -- the shift formed by add_layer_norm_shift -- x may be None."""
     # with bf16 math the intermediates only feed the next bf16 product, which
     # would round them the same way: store them as bf16
     bf = math == MATH_BF16
-    xk = token_shift_mix(x, state, x_k.reshape(1, -1), new_starts, bf16=bf)[0]
+    if xk is None:
+        xk = token_shift_mix(x, state, x_k.reshape(1, -1), new_starts, bf16=bf)[0]
     kk = linear(xk, Wk, es_key, math, act=ACT_RELU_SQ, out_bf16=bf)
     out = linear(kk, Wv, es_value, math)
-    last = x[:, length - 1, :].contiguous() if want_last else None
-    return out, last
+    if last is None and want_last:
+        last = x[:, length - 1, :].contiguous()
+    return out, (last if want_last else None)
 
 
 def linear_t(x, W, es=None, math=MATH_F32, act=0, out_bf16=False):
@@ -184,7 +221,7 @@ TM_MIXES = ("x_r", "x_w", "x_k", "x_v", "x_a", "x_g")
 
 
 def time_mixing(P, x, state, v_first, H, length, layer_id, new_starts=None, es=None,
-                math=MATH_F32, want_state=True):
+                math=MATH_F32, want_state=True, xm=None, x_last=None):
     """TimeMixing::forward (llm.rs:348-480) on every sequence.
 
     P maps the module's parameter names to device tensors: x_r..x_g, w0, v0,
@@ -193,9 +230,11 @@ def time_mixing(P, x, state, v_first, H, length, layer_id, new_starts=None, es=N
     Tmm weights (in, out).  es optionally maps a matrix name to its EsLinear
     (the member's perturbation of that parameter).  x (nseq, T, C); state
     (nseq, 1 + S, C): row 0 the previous token, rows 1.. the (H, S, S) WKV
-    state; v_first (nseq, T, C).  Returns (out, state, v_first), new tensors."""
+    state; v_first (nseq, T, C).  Returns (out, state, v_first), new tensors.  With
+    xm (the six mixes, (6, nseq, T, C), as add_layer_norm_shift forms them) and,
+    for want_state, x_last (x[:, length-1]) given, x may be None."""
     es = es or {}
-    nseq, T, C = x.shape
+    nseq, T, C = x.shape if xm is None else xm.shape[1:]
     S = C // H
     if S * H != C or S > 64:
         raise ValueError(f"C={C} is not H={H} heads of at most 64 channels")
@@ -203,9 +242,10 @@ def time_mixing(P, x, state, v_first, H, length, layer_id, new_starts=None, es=N
         raise ValueError("state must be (nseq, 1 + S, C) and v_first (nseq, T, C)")
     if not 1 <= length <= T:
         raise ValueError("length must be in [1, T]")
-    mixes = torch.stack([P[n] for n in TM_MIXES])
     bf = math == MATH_BF16  # bf16-only consumers get bf16 inputs (the same rounding)
-    xm = token_shift_mix(x, state[:, 0, :].contiguous(), mixes, new_starts, bf16=bf)
+    if xm is None:
+        mixes = torch.stack([P[n] for n in TM_MIXES])
+        xm = token_shift_mix(x, state[:, 0, :].contiguous(), mixes, new_starts, bf16=bf)
 
     def lin(i, name):
         return linear(xm[i], P[name], es.get(name), math)
@@ -244,7 +284,7 @@ def time_mixing(P, x, state, v_first, H, length, layer_id, new_starts=None, es=N
     state_out = None
     if want_state:
         state_out = torch.empty_like(state)
-        state_out[:, 0, :] = x[:, length - 1, :]
+        state_out[:, 0, :] = x[:, length - 1, :] if x_last is None else x_last
         state_out[:, 1:, :] = s_new.view(nseq, S, C)
     out = linear(gn.view(nseq, T, C), P["output"], es.get("output"), math)
     return out, state_out, v_first

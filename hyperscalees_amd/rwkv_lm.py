@@ -169,8 +169,8 @@ class RwkvLmEs:
         h = torch.empty_like(x)
         _lib.call("hses_embed_layer_norm", K._p(tokens), rows, K._p(self.P["emb"]), V, C,
                   K._p(self.P["ln0_w"]), K._p(self.P["ln0_b"]), 1e-5, K._p(x), K._stream())
-        B0 = self.blocks[0]
-        rwkv.layer_norm(x, B0["ln1_w"], B0["ln1_b"], 1e-5, out=h)
+        bf = c.math == MATH_BF16
+        x3 = x.view(nseq, T, C)
         carry = state is not None
         if carry:
             if state.shape != (c.n_layer, nseq, 2 + c.head_size, C):
@@ -181,24 +181,35 @@ class RwkvLmEs:
         else:
             zero = torch.zeros((nseq, 2 + c.head_size, C), dtype=torch.float32, device=self.dev)
             vf = torch.zeros((nseq, T, C), dtype=torch.float32, device=self.dev)
+        # Each LayerNorm that feeds a token shift is formed with that shift (and the
+        # residual add before it) in one pass: the normalised rows never go to memory.
+        def tm_mixes(B, delta, st):
+            mixes = torch.stack([B[nm] for nm in rwkv.TM_MIXES])
+            return rwkv.add_layer_norm_shift(x3, delta, B["ln1_w"], B["ln1_b"], 1e-5, st[:, 1, :],
+                                             mixes, bf16=bf, want_last=carry)
+
+        d = None  # block 0's ln1 reads the embedding (no residual add)
+        st = state[0] if carry else zero
+        xm, xm_last = tm_mixes(self.blocks[0], d, st)
         for l, B in enumerate(self.blocks):
-            st = state[l] if carry else zero
             es = self._es(l, epoch, tid_lo, n) if perturb else {}
-            d, st_tm, vf = rwkv.time_mixing(B, h.view(nseq, T, C), st[:, 1:, :], vf, H, T, l,
-                                            es=es, math=c.math, want_state=carry)
-            _lib.call("hses_add_layer_norm", K._p(x), K._p(d), rows, C, K._p(B["ln2_w"]),
-                      K._p(B["ln2_b"]), 1e-5, K._p(h), K._stream())
-            d, last = rwkv.channel_mixing(h.view(nseq, T, C), st[:, 0, :].contiguous(),
-                                          B["ffn_x_k"], B["ffn_key"], B["ffn_value"], T,
+            d, st_tm, vf = rwkv.time_mixing(B, None, st[:, 1:, :], vf, H, T, l, es=es, math=c.math,
+                                            want_state=carry, xm=xm, x_last=xm_last)
+            xk, xk_last = rwkv.add_layer_norm_shift(x3, d.view(nseq, T, C), B["ln2_w"], B["ln2_b"],
+                                                    1e-5, st[:, 0, :], B["ffn_x_k"].reshape(1, -1),
+                                                    bf16=bf, want_last=carry)
+            d, last = rwkv.channel_mixing(None, None, B["ffn_x_k"], B["ffn_key"], B["ffn_value"], T,
                                           es_key=es.get("ffn_key"), es_value=es.get("ffn_value"),
-                                          math=c.math, want_last=carry)
+                                          math=c.math, want_last=carry, xk=xk[0], last=xk_last)
             if carry:
                 new_state[l][:, 1:, :] = st_tm
                 new_state[l][:, 0, :] = last
-            nxt = self.blocks[l + 1] if l + 1 < len(self.blocks) else None
-            w_, b_ = (nxt["ln1_w"], nxt["ln1_b"]) if nxt else (self.P["ln_out_w"], self.P["ln_out_b"])
-            _lib.call("hses_add_layer_norm", K._p(x), K._p(d), rows, C, K._p(w_), K._p(b_), 1e-5,
-                      K._p(h), K._stream())
+            if l + 1 < len(self.blocks):
+                st = state[l + 1] if carry else zero
+                xm, xm_last = tm_mixes(self.blocks[l + 1], d.view(nseq, T, C), st)
+            else:
+                _lib.call("hses_add_layer_norm", K._p(x), K._p(d), rows, C, K._p(self.P["ln_out_w"]),
+                          K._p(self.P["ln_out_b"]), 1e-5, K._p(h), K._stream())
         lg = rwkv.linear(h.view(1, rows, C), self.P["head"], None, c.math).view(rows, V)
         return (lg, new_state) if carry else lg
 

@@ -437,6 +437,20 @@ int hses_embed_layer_norm(const int32_t *d_tokens, int64_t rows, const float *d_
                           void *stream);
 int hses_add_layer_norm(float *d_x, const float *d_delta, int64_t rows, int32_t C,
                         const float *d_w, const float *d_b, float eps, float *d_y, void *stream);
+/* A block's residual add, the LayerNorm that reads it and the next module's token shift
+ * in one pass (rwkv7.py:240-249 around llm.rs:66-83, 200-205, 360-381): x (nseq, T, C) +=
+ * delta (delta NULL: x only read), y = LayerNorm(x) with w, b, then out[m] = y + ([state,
+ * y[:-1]] (0 where new_starts) - y) * mix[m] for the n_mix mixing vectors, (n_mix, nseq, T, C)
+ * in out_fmt (HSES_FMT_F32 or HSES_FMT_BF16); state (nseq, C) the previous token's y;
+ * y_last (nseq, C) or NULL receives y at row length - 1 (the next shift state).  The values
+ * of hses_add_layer_norm followed by hses_token_shift_mix, bit for bit (without delta, of
+ * hses_add_layer_norm with a zero delta), without y in memory.  Returns
+ * HSES_ERR_UNSUPPORTED unless C is 256, 512 or 1024, n_mix is 1 or 6 and every buffer is
+ * 16-byte aligned (callers then run the two steps). */
+int hses_add_ln_shift(float *d_x, const float *d_delta, int64_t nseq, int32_t T, int32_t C,
+                      const float *d_w, const float *d_b, float eps, const float *d_state,
+                      const uint8_t *d_new_starts, const float *d_mix, int32_t n_mix, void *d_out,
+                      int32_t out_fmt, float *d_y_last, int32_t length, void *stream);
 
 /* ---- data path (host only: no device, no stream) ---------------------- */
 

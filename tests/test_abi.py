@@ -46,6 +46,21 @@ def _expect_invalid(name, *args):
 NULL = None
 
 
+def test_add_ln_shift_validation_without_a_gpu():
+    lib = _lib.load()
+    v = ctypes.c_void_p(256)  # aligned stand-ins: rejected before anything is read
+    _expect_invalid("hses_add_ln_shift", v, v, 4, 8, 512, v, v, 1e-5, v, NULL, v, 6, v, 7, NULL, 8,
+                    NULL)  # out_fmt
+    _expect_invalid("hses_add_ln_shift", v, v, 4, 8, 512, v, v, 1e-5, v, NULL, v, 6, v,
+                    _lib.FMT_BF16, v, 9, NULL)  # length past T with y_last
+    _expect_invalid("hses_add_ln_shift", NULL, v, 4, 8, 512, v, v, 1e-5, v, NULL, v, 6, v,
+                    _lib.FMT_BF16, NULL, 8, NULL)
+    for C, n_mix, x in ((64, 6, v), (512, 3, v), (512, 6, ctypes.c_void_p(260))):
+        rc = lib.hses_add_ln_shift(x, v, 4, 8, C, v, v, 1e-5, v, NULL, v, n_mix, v, _lib.FMT_BF16,
+                                   NULL, 8, NULL)
+        assert rc == _lib.HSES_ERR_UNSUPPORTED, (C, n_mix, rc)
+
+
 def test_validation_rejects_bad_arguments_without_a_gpu():
     _expect_invalid("hses_bm_eval", 2**24 - 4, 8, NULL, NULL, NULL, NULL)
     _expect_invalid("hses_lora_factors", 0.1, 1, 4, 0, -1, 0, NULL, 2, 3, 4, NULL, NULL, NULL)

@@ -281,6 +281,47 @@ def test_gates_kk_equals_chain(hses_gpu, S, with_v):
     assert torch.equal(ai1, ai2) and torch.equal(bi1, bi2)
 
 
+@pytest.mark.parametrize("C,n_mix,add,bf16", [(512, 6, True, True), (512, 1, True, True),
+                                              (256, 6, False, False), (1024, 1, True, False),
+                                              (512, 6, False, True)])
+def test_add_ln_shift_equals_chain(hses_gpu, C, n_mix, add, bf16):
+    # the fused residual add + LayerNorm + token shift == hses_add_layer_norm (a zero
+    # delta without add) then hses_token_shift_mix, bit for bit, with new starts, a
+    # carried state and the last normalised row at length < T
+    from hyperscalees_amd import _lib, kernels as K
+    from hyperscalees_amd._lib import FMT_BF16, FMT_F32
+    nseq, T, length = 5, 37, 30
+    rng = np.random.default_rng(C + n_mix + 2 * add)
+    x = rng.standard_normal((nseq, T, C)).astype(np.float32) * 2 + 0.5
+    dl = rng.standard_normal((nseq, T, C)).astype(np.float32)
+    w, b = rng.standard_normal(C).astype(np.float32), rng.standard_normal(C).astype(np.float32)
+    st = rng.standard_normal((nseq, C)).astype(np.float32)
+    mix = rng.random((n_mix, C)).astype(np.float32)
+    ns = np.zeros((nseq, T), np.uint8)
+    ns[1, 0] = ns[2, 17] = 1
+    fmt, dt = (FMT_BF16, torch.bfloat16) if bf16 else (FMT_F32, torch.float32)
+    wd, bd, sd, md, nsd = cuda(w), cuda(b), cuda(st), cuda(mix), cuda(ns, torch.uint8)
+    # the chain
+    x1, d1 = cuda(x), cuda(dl if add else np.zeros_like(dl))
+    y1 = torch.empty_like(x1)
+    _lib.call("hses_add_layer_norm", K._p(x1), K._p(d1), nseq * T, C, K._p(wd), K._p(bd), 1e-5,
+              K._p(y1), K._stream())
+    o1 = torch.empty((n_mix, nseq, T, C), dtype=dt, device="cuda")
+    _lib.call("hses_token_shift_mix", K._p(y1), K._p(sd), K._p(nsd), K._p(md), n_mix, nseq, T, C,
+              K._p(o1), fmt, K._stream())
+    # fused
+    x2, d2 = cuda(x), cuda(dl)
+    o2 = torch.empty((n_mix, nseq, T, C), dtype=dt, device="cuda")
+    last = torch.empty((nseq, C), device="cuda")
+    _lib.call("hses_add_ln_shift", K._p(x2), K._p(d2) if add else None, nseq, T, C, K._p(wd),
+              K._p(bd), 1e-5, K._p(sd), K._p(nsd), K._p(md), n_mix, K._p(o2), fmt, K._p(last),
+              length, K._stream())
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2)
+    assert torch.equal(last, y1[:, length - 1, :])
+    assert torch.equal(x2, x1 if add else cuda(x))
+
+
 @pytest.mark.parametrize("C", [512, 256, 40])   # vector paths and the scalar path
 def test_add_layer_norm(hses_gpu, C):
     from hyperscalees_amd import _lib, kernels as K
