@@ -200,7 +200,8 @@ __global__ void k_relu_sq(float* __restrict__ x, int64_t n) {
 // (one rounding where the reference rounds the product and the sum: at most
 // an ulp per operation apart; the kernel is bound by these vector operations,
 // 5 per state element and step instead of 9).  s_out is the state after
-// the last step t < length (s_in when length == 0).
+// the last step t < length (s_in when length == 0).  s_in NULL: the zero
+// state; s_out NULL: the final state is not stored.
 // With POST the output row is TimeMixing's next three steps instead
 // (llm.rs:455-470): y = (GroupNorm_head(out) + (sum_s r k r_k) v) g, with
 // the group statistics and the readout sum formed exactly as k_group_norm and
@@ -250,7 +251,7 @@ __global__ __launch_bounds__(256) void k_wkv7(const float* __restrict__ r, const
     const int64_t sbase = (sq * H + h) * (int64_t)S * S + (int64_t)i * S;
     float s[S];
 #pragma unroll
-    for (int j = 0; j < S; ++j) s[j] = s_in[sbase + j];
+    for (int j = 0; j < S; ++j) s[j] = s_in ? s_in[sbase + j] : 0.0f;
     float (*st)[64] = stage[wv];
     // this lane's elements of the step's six vectors (and the gate g with POST),
     // loaded one step ahead so their latency overlaps the previous step's work
@@ -351,7 +352,7 @@ __global__ __launch_bounds__(256) void k_wkv7(const float* __restrict__ r, const
         } else {
             if (row_ok) out[o + lane] = acc;
         }
-        if (t == length - 1 && row_ok) {
+        if (t == length - 1 && row_ok && s_out) {
 #pragma unroll
             for (int j = 0; j < S; ++j) s_out[sbase + j] = s[j];
         }
@@ -360,9 +361,9 @@ __global__ __launch_bounds__(256) void k_wkv7(const float* __restrict__ r, const
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
-    if (length <= 0 && row_ok) {
+    if (length <= 0 && row_ok && s_out) {
 #pragma unroll
-        for (int j = 0; j < S; ++j) s_out[sbase + j] = s_in[sbase + j];
+        for (int j = 0; j < S; ++j) s_out[sbase + j] = s_in ? s_in[sbase + j] : 0.0f;
     }
 }
 
@@ -787,8 +788,8 @@ extern "C" int hses_rwkv7_wkv(const float* d_r, const float* d_w, const float* d
     HSES_REQUIRE(S == 16 || S == 32 || S == 64, "head size S must be 16, 32 or 64");
     HSES_REQUIRE(length >= 0 && length <= T, "length must be in [0, T]");
     if (nseq == 0) return HSES_OK;
-    HSES_REQUIRE(d_r && d_w && d_k && d_v && d_a && d_b && d_s_in && d_out && d_s_out, "NULL pointer");
-    HSES_REQUIRE(d_s_out != d_s_in, "s_out must not alias s_in");
+    HSES_REQUIRE(d_r && d_w && d_k && d_v && d_a && d_b && d_out, "NULL pointer");
+    HSES_REQUIRE(!d_s_out || d_s_out != d_s_in, "s_out must not alias s_in");
     return launch_wkv7<false>(d_r, d_w, d_k, d_v, d_a, d_b, d_s_in, d_new_starts, nseq, T, H, S,
                               length, d_out, d_s_out, WkvPost{}, stream);
 }
@@ -805,10 +806,10 @@ extern "C" int hses_tm_wkv_post(const float* d_r, const float* d_w, const float*
     HSES_REQUIRE(S == 16 || S == 32 || S == 64, "head size S must be 16, 32 or 64");
     HSES_REQUIRE(length >= 0 && length <= T, "length must be in [0, T]");
     if (nseq == 0) return HSES_OK;
-    HSES_REQUIRE(d_r && d_w && d_k && d_v && d_a && d_b && d_s_in && d_out && d_s_out && d_g &&
+    HSES_REQUIRE(d_r && d_w && d_k && d_v && d_a && d_b && d_out && d_g &&
                      d_ln_w && d_ln_b && d_r_k,
                  "NULL pointer");
-    HSES_REQUIRE(d_s_out != d_s_in, "s_out must not alias s_in");
+    HSES_REQUIRE(!d_s_out || d_s_out != d_s_in, "s_out must not alias s_in");
     HSES_REQUIRE(d_out != d_r && d_out != d_k && d_out != d_v, "out must not alias r, k or v");
     return launch_wkv7<true>(d_r, d_w, d_k, d_v, d_a, d_b, d_s_in, d_new_starts, nseq, T, H, S,
                              length, static_cast<float*>(d_out), d_s_out,
@@ -983,11 +984,11 @@ extern "C" int hses_tm_fused(const float* d_r, const float* d_w2o, const float* 
     HSES_REQUIRE(length >= 0 && length <= T, "length must be in [0, T]");
     HSES_REQUIRE(out_fmt == HSES_FMT_F32 || out_fmt == HSES_FMT_BF16, "out_fmt must be F32 or BF16");
     if (nseq == 0) return HSES_OK;
-    HSES_REQUIRE(d_r && d_w2o && d_k && d_v && d_a2o && d_w0 && d_a0 && d_k_k && d_k_a && d_s_in &&
-                     d_out && d_s_out && d_g && d_ln_w && d_ln_b && d_r_k,
+    HSES_REQUIRE(d_r && d_w2o && d_k && d_v && d_a2o && d_w0 && d_a0 && d_k_k && d_k_a &&
+                     d_out && d_g && d_ln_w && d_ln_b && d_r_k,
                  "NULL pointer");
     HSES_REQUIRE(!d_v2o || (d_v_first && d_v0), "NULL pointer (value branch)");
-    HSES_REQUIRE(d_s_out != d_s_in, "s_out must not alias s_in");
+    HSES_REQUIRE(!d_s_out || d_s_out != d_s_in, "s_out must not alias s_in");
     // Other waves still read these planes while a wave stores its output rows
     // (a bf16 out would also write 2-byte halves into fp32 rows).
     HSES_REQUIRE(d_out != d_r && d_out != d_k && d_out != d_v && d_out != d_w2o &&

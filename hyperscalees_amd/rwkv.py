@@ -232,18 +232,21 @@ def time_mixing(P, x, state, v_first, H, length, layer_id, new_starts=None, es=N
     (nseq, 1 + S, C): row 0 the previous token, rows 1.. the (H, S, S) WKV
     state; v_first (nseq, T, C).  Returns (out, state, v_first), new tensors.  With
     xm (the six mixes, (6, nseq, T, C), as add_layer_norm_shift forms them) and,
-    for want_state, x_last (x[:, length-1]) given, x may be None."""
+    for want_state, x_last (x[:, length-1]) given, x may be None, and then state
+    may be None for the zero state (no state returned)."""
     es = es or {}
     nseq, T, C = x.shape if xm is None else xm.shape[1:]
     S = C // H
     if S * H != C or S > 64:
         raise ValueError(f"C={C} is not H={H} heads of at most 64 channels")
-    if state.shape != (nseq, 1 + S, C) or v_first.shape != (nseq, T, C):
+    if (state is not None and state.shape != (nseq, 1 + S, C)) or v_first.shape != (nseq, T, C):
         raise ValueError("state must be (nseq, 1 + S, C) and v_first (nseq, T, C)")
     if not 1 <= length <= T:
         raise ValueError("length must be in [1, T]")
     bf = math == MATH_BF16  # bf16-only consumers get bf16 inputs (the same rounding)
     if xm is None:
+        if x is None or state is None:
+            raise ValueError("x and state are needed to form the mixes")
         mixes = torch.stack([P[n] for n in TM_MIXES])
         xm = token_shift_mix(x, state[:, 0, :].contiguous(), mixes, new_starts, bf16=bf)
 
@@ -270,11 +273,12 @@ def time_mixing(P, x, state, v_first, H, length, layer_id, new_starts=None, es=N
         v2o = None
     else:
         v2o = res["v2o"]
-    s_in = state[:, 1:, :].reshape(nseq, H, S, S).contiguous()
+    # state None: the zero WKV state (the kernel starts from zeros, nothing is copied)
+    s_in = None if state is None else state[:, 1:, :].reshape(nseq, H, S, S).contiguous()
     # the gates, the kk normalisation and k update, the recurrence, ln_x, the readout and
     # the gate in one kernel, from the raw projections
     gn = torch.empty(r.shape, dtype=torch.bfloat16 if bf else torch.float32, device=r.device)
-    s_new = torch.empty_like(s_in)
+    s_new = torch.empty((nseq, H, S, S), dtype=torch.float32, device=r.device) if want_state else None
     if new_starts is not None:
         K._dev(new_starts, torch.uint8, "new_starts")
     _lib.call("hses_tm_fused", _p(r), _p(w), _p(k), _p(v), _p(a), _p(v2o), _p(v_first),
@@ -283,6 +287,8 @@ def time_mixing(P, x, state, v_first, H, length, layer_id, new_starts=None, es=N
               _p(P["r_k"]), _p(gn), FMT_BF16 if bf else FMT_F32, _p(s_new), _stream())
     state_out = None
     if want_state:
+        if state is None:
+            raise ValueError("want_state needs the incoming state")
         state_out = torch.empty_like(state)
         state_out[:, 0, :] = x[:, length - 1, :] if x_last is None else x_last
         state_out[:, 1:, :] = s_new.view(nseq, S, C)

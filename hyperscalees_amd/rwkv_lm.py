@@ -193,8 +193,9 @@ class RwkvLmEs:
         xm, xm_last = tm_mixes(self.blocks[0], d, st)
         for l, B in enumerate(self.blocks):
             es = self._es(l, epoch, tid_lo, n) if perturb else {}
-            d, st_tm, vf = rwkv.time_mixing(B, None, st[:, 1:, :], vf, H, T, l, es=es, math=c.math,
-                                            want_state=carry, xm=xm, x_last=xm_last)
+            d, st_tm, vf = rwkv.time_mixing(B, None, st[:, 1:, :] if carry else None, vf, H, T, l,
+                                            es=es, math=c.math, want_state=carry, xm=xm,
+                                            x_last=xm_last)
             xk, xk_last = rwkv.add_layer_norm_shift(x3, d.view(nseq, T, C), B["ln2_w"], B["ln2_b"],
                                                     1e-5, st[:, 0, :], B["ffn_x_k"].reshape(1, -1),
                                                     bf16=bf, want_last=carry)

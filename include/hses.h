@@ -371,7 +371,9 @@ int hses_relu_sq(float *d_x, int64_t n, void *stream);
  * (nseq, T, H, S) with w the raw decay (exp(-exp(w)) is applied here); s_in (nseq, H, S, S);
  * new_starts (nseq, T) bytes or NULL (a set byte zeroes the state before that step);
  * out (nseq, T, H, S); s_out (nseq, H, S, S) = the state after the last step t < length
- * (s_in when length == 0).  S = 16, 32 or 64; s_out must not alias s_in. */
+ * (s_in when length == 0).  S = 16, 32 or 64; s_out must not alias s_in.  s_in NULL starts
+ * from the zero state; s_out NULL does not store the final state (both, also for
+ * hses_tm_wkv_post and hses_tm_fused). */
 int hses_rwkv7_wkv(const float *d_r, const float *d_w, const float *d_k, const float *d_v,
                    const float *d_a, const float *d_b, const float *d_s_in,
                    const uint8_t *d_new_starts, int64_t nseq, int32_t T, int32_t H, int32_t S,
