@@ -56,6 +56,18 @@ PROTOTYPES = {
                                                      c_i32, c_i32, c_i32, c_i32, c_f32, c_f32,
                                                      c_vp, c_i64, c_i64, c_vp, c_i64, c_vp,
                                                      c_size, c_vp, c_size, c_vp]),
+    "hses_pair_image_bytes": (c_size, [c_i32, c_i32, c_i32, c_i32, c_i32]),
+    "hses_pair_factors": (ctypes.c_int, [c_u64, c_i32, c_f32, c_i32, c_i32, c_i32, c_i32, c_i32,
+                                         c_i32, c_vp, c_size, c_vp, c_size, c_vp]),
+    "hses_perturbed_linear_pre": (ctypes.c_int, [c_vp, c_i32, c_i64, c_i64, c_i32, c_vp, c_i32,
+                                                 c_i32, c_i32, c_f32, c_i32, c_i32, c_i32, c_vp,
+                                                 c_i64, c_i64, c_vp, c_size, c_vp, c_size, c_vp,
+                                                 c_size, c_vp]),
+    "hses_perturbed_linear_lif_pre": (ctypes.c_int, [c_vp, c_i32, c_i64, c_i64, c_i32, c_vp,
+                                                     c_i32, c_i32, c_i32, c_f32, c_i32, c_i32,
+                                                     c_i32, c_f32, c_f32, c_vp, c_i64, c_i64,
+                                                     c_vp, c_i64, c_vp, c_size, c_vp, c_size,
+                                                     c_vp, c_size, c_vp]),
     "hses_perturbed_linear_t": (ctypes.c_int, [c_vp, c_i32, c_i64, c_i64, c_i32, c_vp, c_i32,
                                                c_i32, c_u64, c_i32, c_f32, c_i32, c_i32, c_i32,
                                                c_i32, c_i32, c_vp, c_i64, c_i64, c_i32, c_vp,

@@ -550,7 +550,8 @@ static int linear_lif_impl(const void* d_x, int32_t x_fmt, int64_t x_stride, int
                            int32_t tid_lo, int32_t n, int32_t rows_per_member, float tau_m,
                            float v_th, uint64_t* d_spikes, int64_t spk_stride, int64_t spk_plane,
                            float* d_rate, int64_t rate_stride, void* d_work, size_t work_bytes,
-                           float* d_rec, size_t rec_bytes, void* stream) {
+                           float* d_rec, size_t rec_bytes, void* stream,
+                           const uint16_t* d_img = nullptr, size_t img_bytes = 0) {
     HSES_REQUIRE(tau_m != 0.0f, "tau_m must be non-zero");
     LinParams P;
     DeviceState* st = nullptr;
@@ -562,6 +563,11 @@ static int linear_lif_impl(const void* d_x, int32_t x_fmt, int64_t x_stride, int
         if (rc) return rc;
         P.rec = d_rec;
     }
+    if (d_img) {
+        HSES_REQUIRE(img_bytes >= pair_image_bytes(a, b, P.r, tid_lo, n),
+                     "hses_perturbed_linear_lif_pre: operand image smaller than "
+                     "hses_pair_image_bytes");
+    }
     HSES_REQUIRE(d_spikes || d_rate, "spikes and rate are both NULL");
     const int64_t M = (int64_t)n * rows_per_member;
     HSES_REQUIRE(!d_spikes || spk_stride >= (a + 63) / 64, "spk_stride smaller than a row");
@@ -572,10 +578,12 @@ static int linear_lif_impl(const void* d_x, int32_t x_fmt, int64_t x_stride, int
     HSES_REQUIRE(x_fmt == HSES_FMT_BITS, "the fused kernel takes bit-packed spikes (x_fmt BITS)");
     LifOut lif{d_spikes, spk_stride, spk_plane, d_rate, rate_stride,
                1.0f / tau_m /* snn.rs:59: dt / tau_m with dt = 1 */, v_th};
-    rc = launch_linear_pair(P, st, (hipStream_t)stream, d_work, work_bytes, &lif);
+    rc = launch_linear_pair(P, st, (hipStream_t)stream, d_work, work_bytes, &lif, d_img);
     if (rc == HSES_ERR_UNSUPPORTED)
         return set_error(HSES_ERR_UNSUPPORTED,
-                         "hses_perturbed_linear_lif: needs rank a multiple of 16 <= 128 and a <= 128");
+                         d_img ? "hses_perturbed_linear_lif_pre: needs rank a multiple of 16 <= 128, "
+                                 "a <= 128, n_time <= 16 and b <= 1024"
+                               : "hses_perturbed_linear_lif: needs rank a multiple of 16 <= 128 and a <= 128");
     return rc;
 }
 
@@ -608,6 +616,107 @@ extern "C" int hses_perturbed_linear_lif_rec(const void* d_x, int32_t x_fmt, int
                            epoch, noise_reuse, tid_lo, n, rows_per_member, tau_m, v_th, d_spikes,
                            spk_stride, spk_plane, d_rate, rate_stride, d_work, work_bytes, d_rec,
                            rec_bytes, stream);
+}
+
+// ---- factors drawn ahead -----------------------------------------------------
+// hses_pair_factors draws every pair's factors of a do_mm pair-kernel forward
+// into the factor record and the bf16 B operand image; the *_pre forwards
+// then read them instead of drawing, with the same operands, products and
+// order as the *_rec forwards (so the same outputs, bit for bit).  The draw
+// is a separate full-occupancy launch that a caller may put on another
+// stream or issue ahead of the forward.
+
+extern "C" size_t hses_pair_image_bytes(int32_t a, int32_t b, int32_t rank, int32_t tid_lo,
+                                        int32_t n) {
+    if (a < 1 || b < 1 || rank < 1 || tid_lo < 0 || n < 1) return 0;
+    return pair_image_bytes(a, b, rank, tid_lo, n);
+}
+
+extern "C" int hses_pair_factors(uint64_t key, int32_t rank, float sigma, int32_t epoch,
+                                 int32_t noise_reuse, int32_t tid_lo, int32_t n, int32_t a,
+                                 int32_t b, float* d_rec, size_t rec_bytes, uint16_t* d_img,
+                                 size_t img_bytes, void* stream) {
+    HSES_REQUIRE(a >= 1 && b >= 1 && n >= 0 && rank >= 0, "bad sizes");
+    HSES_REQUIRE(noise_reuse >= 0, "noise_reuse must be >= 0");
+    HSES_REQUIRE(tid_lo >= 0 && (int64_t)tid_lo + n - 1 <= INT32_MAX, "thread id range");
+    if (n == 0) return HSES_OK;
+    HSES_REQUIRE(a <= 128, "hses_pair_factors: output width a must be <= 128 (the pair kernels)");
+    DeviceState* st;
+    int rc = get_state(&st);
+    if (rc) return rc;
+    LinParams P{};
+    P.a = a;
+    P.b = b;
+    P.key = key;
+    P.r = (sigma != 0.0f) ? rank : 0;
+    P.bs = rank > 0 ? sigma / sqrtf((float)rank) : 0.0f;  // eggroll.rs:433
+    P.epoch = epoch;
+    P.nreuse = noise_reuse;
+    P.tid_lo = tid_lo;
+    P.n = n;
+    P.math = HSES_MATH_BF16;
+    P.tables = st->d_tables;
+    P.log_exc = st->d_log_exc;
+    P.cos_exc = st->d_cos_exc;
+    rc = check_record(P, d_rec, rec_bytes, "hses_pair_factors");
+    if (rc) return rc;
+    HSES_REQUIRE(d_img, "operand image is NULL");
+    HSES_REQUIRE(img_bytes >= pair_image_bytes(a, b, P.r, tid_lo, n),
+                 "hses_pair_factors: operand image smaller than hses_pair_image_bytes");
+    P.rec = d_rec;
+    return launch_pair_gen(P, st, (hipStream_t)stream, d_img);
+}
+
+extern "C" int hses_perturbed_linear_pre(const void* d_x, int32_t x_fmt, int64_t x_stride,
+                                         int64_t x_plane, int32_t n_time, const float* d_W,
+                                         int32_t a, int32_t b, int32_t rank, float sigma,
+                                         int32_t tid_lo, int32_t n, int32_t rows_per_member,
+                                         float* d_y, int64_t y_stride, int64_t y_plane,
+                                         void* d_work, size_t work_bytes, const float* d_rec,
+                                         size_t rec_bytes, const uint16_t* d_img,
+                                         size_t img_bytes, void* stream) {
+    LinParams P;
+    DeviceState* st = nullptr;
+    int rc = make_params(&P, d_x, x_fmt, x_stride, x_plane, n_time, d_W, a, b, 0, rank, sigma, 0,
+                         0, tid_lo, n, rows_per_member, HSES_MATH_BF16, &st);
+    if (rc || n == 0) return rc;
+    rc = check_record(P, d_rec, rec_bytes, "hses_perturbed_linear_pre");
+    if (rc) return rc;
+    HSES_REQUIRE(d_img, "operand image is NULL");
+    HSES_REQUIRE(img_bytes >= pair_image_bytes(a, b, P.r, tid_lo, n),
+                 "hses_perturbed_linear_pre: operand image smaller than hses_pair_image_bytes");
+    HSES_REQUIRE(d_y, "NULL pointer");
+    HSES_REQUIRE(y_stride >= a, "y_stride smaller than a row");
+    HSES_REQUIRE(n_time == 1 || y_plane >= (int64_t)n * rows_per_member * y_stride,
+                 "time planes overlap");
+    P.y = d_y;
+    P.y_stride = y_stride;
+    P.y_plane = y_plane;
+    P.rec = const_cast<float*>(d_rec);
+    rc = launch_linear_pair(P, st, (hipStream_t)stream, d_work, work_bytes, nullptr, d_img);
+    if (rc == HSES_ERR_UNSUPPORTED)
+        return set_error(HSES_ERR_UNSUPPORTED,
+                         "hses_perturbed_linear_pre: needs the pair kernels (a <= 128, rank a "
+                         "multiple of 16 in [32, 128])");
+    return rc;
+}
+
+extern "C" int hses_perturbed_linear_lif_pre(const void* d_x, int32_t x_fmt, int64_t x_stride,
+                                             int64_t x_plane, int32_t n_time, const float* d_W,
+                                             int32_t a, int32_t b, int32_t rank, float sigma,
+                                             int32_t tid_lo, int32_t n, int32_t rows_per_member,
+                                             float tau_m, float v_th, uint64_t* d_spikes,
+                                             int64_t spk_stride, int64_t spk_plane, float* d_rate,
+                                             int64_t rate_stride, void* d_work, size_t work_bytes,
+                                             const float* d_rec, size_t rec_bytes,
+                                             const uint16_t* d_img, size_t img_bytes,
+                                             void* stream) {
+    HSES_REQUIRE(d_rec, "factor record is NULL");
+    HSES_REQUIRE(d_img, "operand image is NULL");
+    return linear_lif_impl(d_x, x_fmt, x_stride, x_plane, n_time, d_W, a, b, 0, rank, sigma, 0, 0,
+                           tid_lo, n, rows_per_member, tau_m, v_th, d_spikes, spk_stride,
+                           spk_plane, d_rate, rate_stride, d_work, work_bytes,
+                           const_cast<float*>(d_rec), rec_bytes, stream, d_img, img_bytes);
 }
 
 extern "C" int hses_perturbed_linear_act(const void* d_x, int32_t x_fmt, int64_t x_stride,

@@ -148,9 +148,16 @@ size_t linear_bf16_workspace(int32_t a, int32_t b, int32_t r, int32_t n, int32_t
                              int32_t n_time, int32_t math);
 size_t linear_f32_workspace(int32_t a, int32_t b, int32_t r, int32_t n, int32_t rows_per_member,
                             int32_t n_time, int32_t math);
+// The pair kernels (rank a multiple of 16 <= 128, output width <= 128, bf16).
+// With bimg the factors were drawn ahead by launch_pair_gen: A is read from
+// P.rec, B from bimg, and the kernels draw nothing.
 int launch_linear_pair(LinParams& P, DeviceState* st, hipStream_t s, void* work, size_t work_bytes,
-                       const LifOut* lif = nullptr);
+                       const LifOut* lif = nullptr, const uint16_t* bimg = nullptr);
 size_t linear_pair_workspace(const DeviceState* st, int32_t a, int32_t b, int32_t r, int32_t n);
+// Every pair's factors of members [tid_lo, tid_lo + n) into the record P.rec
+// and the bf16 B operand image bimg (pair_image_bytes bytes).
+int launch_pair_gen(LinParams& P, DeviceState* st, hipStream_t s, uint16_t* bimg);
+size_t pair_image_bytes(int32_t a, int32_t b, int32_t r, int32_t tid_lo, int32_t n);
 // The wide small-rank kernel: 0 when it does not apply to the shape, else its
 // workspace (W as bf16, (a, kp)).
 size_t linear_wide_workspace(int32_t a, int32_t b, int32_t r, int32_t n, int32_t rows_per_member,

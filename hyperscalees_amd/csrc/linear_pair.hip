@@ -93,6 +93,10 @@ struct K2Args {
     // Factor record (do_mm), or NULL: pair pair_lo + i's raw normals (before
     // any scale) at rec[(i * r + c) * (a + b) + j] for stream row j, rank c.
     float* rec;
+    // Factors drawn ahead (PRE kernels, k_pair_gen): pair pair_lo + i's
+    // scaled input-side factor as bf16 at bimg[(i * r + c) * kp + k] (the
+    // layout of a staging slot, zero for k >= b); A comes from rec.
+    uint16_t* bimg;
 };
 
 // bm_run that also stores each raw normal i at rp[i * pitch] when rp is set
@@ -158,6 +162,42 @@ __global__ void k_w_to_bf16(const float* __restrict__ W, int32_t a, int32_t b, i
     const int32_t row = (int32_t)(i / kp), k = (int32_t)(i % kp);
     const int64_t src = tmm ? (int64_t)k * a + row : (int64_t)row * b + k;
     out[i] = k < b ? f2bf(W[src]) : (uint16_t)0;
+}
+
+// Factors of the pair kernels drawn ahead of their GEMM (the PRE kernels):
+// one thread per (pair, stream row) continues its row of the pair's stream
+// for r normals, keeps each raw normal in the factor record and, for an
+// input-side row, its scaled bf16 value in the B operand image.  Threads of
+// output-side rows also zero the image's padding columns [b, kp).  Lanes
+// take consecutive stream rows, so for each rank column a wave's record
+// stores and image stores are contiguous runs.  Full occupancy (256-thread
+// workgroups, no other work) keeps the VALU-bound generator at its rate.
+constexpr int KG_THREADS = 256;
+__global__ __launch_bounds__(KG_THREADS) void k_pair_gen(const K2Args P) {
+    __shared__ BmTables t;
+    load_bm_tables(&t, P.tables);
+    __syncthreads();
+    const uint32_t rows = (uint32_t)(P.a + P.b);
+    const uint32_t u = blockIdx.x * KG_THREADS + threadIdx.x;
+    if (u >= (uint32_t)P.n_pairs * rows) return;
+    const uint32_t pi = u / rows, j = u - pi * rows;
+    const int32_t r = P.r, kp = (P.b + 63) / 64 * 64;
+    int32_t te, tt;
+    float sg;
+    epoch_thread_sign(P.epoch, 2 * (P.pair_lo + (int32_t)pi), P.nreuse, &te, &tt, &sg);
+    uint64_t s = row_start_state(noise_seed(P.key, te, tt), (int32_t)j, P.jump);
+    const StreamRow sr(P, (int32_t)j);
+    float* rp = P.rec + (size_t)pi * r * rows + j;
+    uint16_t* img = P.bimg + (size_t)pi * r * kp;
+    uint16_t* bp = sr.in_side ? img + sr.row : nullptr;
+    const NoiseCtx ctx{&t, P.log_exc, P.cos_exc};
+    bm_run(s, r, ctx, [&](int32_t c, float v) {
+        rp[(size_t)c * rows] = v;
+        if (bp) bp[(size_t)c * kp] = f2bf(v * sr.scale);
+    });
+    if (!sr.in_side)
+        for (int32_t k = P.b + sr.row; k < kp; k += P.a)
+            for (int32_t c = 0; c < r; ++c) img[(size_t)c * kp + k] = 0;
 }
 
 void launch_w_to_bf16(const float* W, int32_t a, int32_t b, int32_t kp, int32_t tmm, uint16_t* out,
@@ -324,7 +364,9 @@ __device__ __forceinline__ uint4 mask4(uint4 v, uint32_t m) {
 // EPI: EPI_Y stores y; EPI_LIF + T (a power of two <= 64) runs the fused LIF.
 // WJ: 16-column W tiles per wave (4 cover a <= 128; 1 suffices for a <= 16,
 // e.g. a readout, and frees the registers of the other three).
-template <int XFMT, int EPI, int LT = 1, int WJ = 4>
+// PRE: the factors were drawn ahead (k_pair_gen): A rows come from the
+// record, B from the operand image, and nothing is generated.
+template <int XFMT, int EPI, int LT = 1, int WJ = 4, bool PRE = false>
 __global__ __launch_bounds__(K2_THREADS) void k_linear_pair(const K2Args P) {
     constexpr bool BITS = XFMT == HSES_FMT_BITS;
     static_assert(WJ >= 1 && WJ <= 4 && (EPI == EPI_Y || WJ == 4), "WJ < 4 only with EPI_Y");
@@ -344,16 +386,18 @@ __global__ __launch_bounds__(K2_THREADS) void k_linear_pair(const K2Args P) {
     const int32_t r = P.r, a = P.a, b = P.b, kp = lay.kp, nkt = lay.words, R = P.R;
     const int32_t rp32 = (r + 31) & ~31;
     const int32_t G = P.group;
-    uint16_t* slots = P.slots + (size_t)blockIdx.x * G * r * kp;  // G slots of (r, kp)
+    uint16_t* slots = PRE ? nullptr : P.slots + (size_t)blockIdx.x * G * r * kp;  // G slots of (r, kp)
 
-    load_bm_tables(tabs, P.tables);
-    // generation never writes k >= b: zero the slots' padding once
-    for (int32_t i = tid; i < G * r * (kp - b); i += K2_THREADS) {
-        const int32_t c = i / (kp - b), k = b + i % (kp - b);
-        slots[(size_t)c * kp + k] = 0;
+    if constexpr (!PRE) {
+        load_bm_tables(tabs, P.tables);
+        // generation never writes k >= b: zero the slots' padding once
+        for (int32_t i = tid; i < G * r * (kp - b); i += K2_THREADS) {
+            const int32_t c = i / (kp - b), k = b + i % (kp - b);
+            slots[(size_t)c * kp + k] = 0;
+        }
+        __threadfence_block();
+        __syncthreads();
     }
-    __threadfence_block();
-    __syncthreads();
     const NoiseCtx ctx{tabs, P.log_exc, P.cos_exc};
 
     // Tile loader: thread -> (staged column, 32-k half).  Columns [0, 128) are
@@ -374,7 +418,23 @@ __global__ __launch_bounds__(K2_THREADS) void k_linear_pair(const K2Args P) {
         const int32_t gcnt = min(G, (P.n_pairs - pi0 + (int32_t)gridDim.x - 1) / (int32_t)gridDim.x);
 
         // ---- 1. factors: A rows -> LDS (bf16, [o][c]); B rows -> slot ([c][k]) ----
-        {
+        if constexpr (PRE) {
+            // A^T of pair pi is rec[(pi r + c)(a + b) + aoff + o]: scale, round
+            // and place it as the generation would have
+            __syncthreads();  // the previous group's blocks have finished with As
+            const int32_t per = r * a, aoff = P.tmm ? 0 : b;
+            const float sc = P.tmm ? 1.0f : P.bs;
+            for (int32_t i = tid; i < gcnt * per; i += K2_THREADS) {
+                const int32_t g = i / per, e = i - g * per, c = e / a, o = e - c * a;
+                const size_t pi = (size_t)(pi0 + g * (int32_t)gridDim.x);
+                As[(size_t)(g * a + o) * lay.apitch + c] =
+                    f2bf(P.rec[(pi * r + c) * (a + b) + aoff + o] * sc);
+            }
+            for (int32_t i = tid; i < gcnt * a * (rp32 - r); i += K2_THREADS)
+                As[(size_t)(i / (rp32 - r)) * lay.apitch + r + i % (rp32 - r)] = 0;
+            __threadfence_block();
+            __syncthreads();
+        } else {
             __syncthreads();  // the previous group's blocks have finished with As and the slots
             // Work units: segment of a stream row (P.segs segments of r / segs
             // normals) of one pair of the group.
@@ -413,7 +473,7 @@ __global__ __launch_bounds__(K2_THREADS) void k_linear_pair(const K2Args P) {
         const int32_t m_even = 2 * pair - P.tid_lo;
         const int32_t m_lo = max(m_even, 0), m_hi = min(m_even + 1, P.n - 1);
         const int64_t row_lo = (int64_t)m_lo * R, row_hi = (int64_t)(m_hi + 1) * R;
-        const uint16_t* lsrc = (lw ? P.wbf : slots + (size_t)g * r * kp) + loff;
+        const uint16_t* lsrc = (lw ? P.wbf : PRE ? P.bimg + (size_t)pi * r * kp : slots + (size_t)g * r * kp) + loff;
         const uint16_t* Ag = As + (size_t)g * a * lay.apitch;
 
         // ---- 2./3. row blocks ----------------------------------------------------
@@ -618,8 +678,9 @@ struct K3Layout {
 };
 
 // EPI_Y: store the currents; EPI_LIF: LIF with T = LT, spike words if SPK,
-// spike rates if RATE.
-template <int EPI, int LT, bool SPK, bool RATE>
+// spike rates if RATE.  PRE: the factors were drawn ahead (k_pair_gen): A
+// comes from the record, B from the operand image, and nothing is generated.
+template <int EPI, int LT, bool SPK, bool RATE, bool PRE = false>
 __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
     static_assert(LT >= 1 && LT <= 16 && (LT & (LT - 1)) == 0, "T must be a power of two <= 16");
     extern __shared__ __align__(16) unsigned char smem[];
@@ -635,23 +696,25 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
     const int lc = lane & 31, hl = lane >> 5;  // MFMA column / k-group of this lane
     const int32_t r = P.r, a = P.a, b = P.b, kp = lay.kp, nkt = lay.words, R = P.R;
     const int32_t rp32 = (r + 31) & ~31;
-    uint16_t* slot = P.slots + (size_t)blockIdx.x * r * kp;
+    uint16_t* slot = PRE ? nullptr : P.slots + (size_t)blockIdx.x * r * kp;
 
-    load_bm_tables(tabs, P.tables);
-    for (int32_t i = tid; i < r * (kp - b); i += K3_THREADS) {
-        const int32_t c = i / (kp - b), k = b + i % (kp - b);
-        slot[(size_t)c * kp + k] = 0;
+    if constexpr (!PRE) {
+        load_bm_tables(tabs, P.tables);
+        for (int32_t i = tid; i < r * (kp - b); i += K3_THREADS) {
+            const int32_t c = i / (kp - b), k = b + i % (kp - b);
+            slot[(size_t)c * kp + k] = 0;
+        }
+        __threadfence_block();
+        __syncthreads();
     }
-    __threadfence_block();
-    __syncthreads();
     const NoiseCtx ctx{tabs, P.log_exc, P.cos_exc};
 
     // Tile loader: thread -> (staged column, 32-k half); columns [0, 128) are
     // W rows, [128, 256) rank columns of B; absent ones are staged as zeros.
     const int lcol = tid >> 1, lk = (tid & 1) * 32;
     const bool lvalid = lcol < K2_NMAX ? lcol < a : lcol - K2_NMAX < r;
-    const uint16_t* lsrc = lcol < K2_NMAX ? P.wbf + (size_t)min(lcol, a - 1) * kp + lk
-                                          : slot + (size_t)min(lcol - K2_NMAX, r - 1) * kp + lk;
+    const size_t loff = (size_t)(lcol < K2_NMAX ? min(lcol, a - 1) : min(lcol - K2_NMAX, r - 1)) * kp + lk;
+    const uint16_t* lsrc = (lcol < K2_NMAX ? P.wbf : slot) + loff;  // PRE: B part set per pair
     uint16_t* ldst = WB + lcol * K2_TP + lk;
     const uint32_t lmask = lvalid ? 0xffffffffu : 0u;
 #define K3_TILE_LOAD(kt)                                                            \
@@ -689,7 +752,33 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
         const bool more_pairs = pi + (int32_t)gridDim.x < P.n_pairs;
 
         // ---- 1. factors: A rows -> LDS (bf16, [o][c]); B rows -> slot ([c][k]) ----
-        {
+        if constexpr (PRE) {
+            if (lcol >= K2_NMAX) lsrc = P.bimg + (size_t)pi * r * kp + loff;
+            // A^T of the pair is rec[(pi r + c)(a + b) + aoff + o]: scale, round
+            // and place it (swap23 columns) as the generation would have; eight
+            // loads in flight per thread
+            __syncthreads();  // the previous pair's epilogue has finished reading As
+            const int32_t na = r * a, aoff = P.tmm ? 0 : b;
+            const float sc = P.tmm ? 1.0f : P.bs;
+            const float* ar = P.rec + (size_t)pi * r * (a + b) + aoff;
+            for (int32_t i0 = 0; i0 < na; i0 += 8 * K3_THREADS) {
+                float v[8];
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    const int32_t i = min(i0 + q * K3_THREADS + tid, na - 1);
+                    v[q] = ar[(size_t)(i / a) * (a + b) + i % a];
+                }
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    const int32_t i = i0 + q * K3_THREADS + tid;
+                    if (i < na) As[(size_t)(i % a) * K3_AP + swap23(i / a)] = f2bf(v[q] * sc);
+                }
+            }
+            for (int32_t i = tid; i < a * (rp32 - r); i += K3_THREADS)
+                As[(size_t)(i / (rp32 - r)) * K3_AP + r + i % (rp32 - r)] = 0;
+            __threadfence_block();
+            __syncthreads();
+        } else {
             __syncthreads();  // the previous pair's epilogue has finished reading As
             int32_t te, tt;
             float sg;
@@ -1001,9 +1090,48 @@ size_t linear_pair_workspace(const DeviceState* st, int32_t a, int32_t b, int32_
     return pair_workspace_bytes(pair_grid(st, cnt + 1) * pair_group(a), a, b, r);
 }
 
-int launch_linear_pair(LinParams& P, DeviceState* st, hipStream_t s, void* work, size_t work_bytes,
-                       const LifOut* lif) {
+// Every pair's factors of a launch drawn into the record and the B operand
+// image (the PRE kernels' inputs).
+int launch_pair_gen(LinParams& P, DeviceState* st, hipStream_t s, uint16_t* bimg) {
     if (P.r == 0 || !pair_kernel_applies(P)) return HSES_ERR_UNSUPPORTED;
+    K2Args A{};
+    pair_range(P.tid_lo, P.n, &A.pair_lo, &A.n_pairs);
+    const int64_t units = (int64_t)A.n_pairs * (P.a + P.b);
+    HSES_REQUIRE(units < (1ll << 31), "too many factor rows");
+    int rc = get_jump_table(st, P.r, (int64_t)P.a + P.b, &A.jump);
+    if (rc) return rc;
+    A.key = P.key;
+    A.tables = P.tables;
+    A.log_exc = P.log_exc;
+    A.cos_exc = P.cos_exc;
+    A.a = P.a;
+    A.b = P.b;
+    A.r = P.r;
+    A.epoch = P.epoch;
+    A.nreuse = P.nreuse;
+    A.bs = P.bs;
+    A.tmm = P.tmm;
+    A.rec = P.rec;
+    A.bimg = bimg;
+    hipLaunchKernelGGL(k_pair_gen, dim3((uint32_t)((units + KG_THREADS - 1) / KG_THREADS)),
+                       dim3(KG_THREADS), 0, s, A);
+    HSES_CHECK_HIP(hipGetLastError());
+    return HSES_OK;
+}
+
+size_t pair_image_bytes(int32_t a, int32_t b, int32_t r, int32_t tid_lo, int32_t n) {
+    (void)a;
+    if (n < 1 || r < 1 || b < 1 || tid_lo < 0) return 0;
+    int32_t lo, cnt;
+    pair_range(tid_lo, n, &lo, &cnt);
+    return (size_t)cnt * r * ((size_t)(b + 63) / 64 * 64) * 2;
+}
+
+int launch_linear_pair(LinParams& P, DeviceState* st, hipStream_t s, void* work, size_t work_bytes,
+                       const LifOut* lif, const uint16_t* bimg) {
+    if (P.r == 0 || !pair_kernel_applies(P)) return HSES_ERR_UNSUPPORTED;
+    const bool pre = bimg != nullptr;
+    if (pre && !P.rec) return set_error(HSES_ERR_INVALID_ARG, "factors drawn ahead need the record");
     if (lif && (P.n_time > 64 || (P.n_time & (P.n_time - 1)) != 0 || P.x_fmt != HSES_FMT_BITS))
         return HSES_ERR_UNSUPPORTED;
     const bool bits = P.x_fmt == HSES_FMT_BITS;
@@ -1018,7 +1146,7 @@ int launch_linear_pair(LinParams& P, DeviceState* st, hipStream_t s, void* work,
     pair_range(P.tid_lo, P.n, &A.pair_lo, &A.n_pairs);
     const int32_t grid = pair_grid(st, A.n_pairs);
     A.group = v3 ? 1 : pair_group(P.a);
-    const size_t need = pair_workspace_bytes(grid * A.group, P.a, P.b, P.r);
+    const size_t need = pair_workspace_bytes(pre ? 0 : grid * A.group, P.a, P.b, P.r);
     if (!work || work_bytes < need)
         return set_error(HSES_ERR_INVALID_ARG, "hses_perturbed_linear: workspace too small");
     uint16_t* wbf = static_cast<uint16_t*>(work);
@@ -1062,6 +1190,7 @@ int launch_linear_pair(LinParams& P, DeviceState* st, hipStream_t s, void* work,
     A.bs = P.bs;
     A.tmm = P.tmm;
     A.rec = P.rec;
+    A.bimg = const_cast<uint16_t*>(bimg);
     {
         // 8 consecutive elements of a row start 16-byte aligned when the base,
         // the row stride and the plane stride all keep them so
@@ -1082,21 +1211,38 @@ int launch_linear_pair(LinParams& P, DeviceState* st, hipStream_t s, void* work,
         return HSES_OK;
     };
     if (v3) {
-        if (!lif) return launch(k_pair_bits<EPI_Y, 1, false, false>);
-        const bool spk = lif->spk != nullptr, rate = lif->rate != nullptr;
-        auto by_t = [&](auto sc, auto rc) -> int {
-            constexpr bool S = decltype(sc)::value, Q = decltype(rc)::value;
-            switch (P.n_time) {
-                case 1: return launch(k_pair_bits<EPI_LIF, 1, S, Q>);
-                case 2: return launch(k_pair_bits<EPI_LIF, 2, S, Q>);
-                case 4: return launch(k_pair_bits<EPI_LIF, 4, S, Q>);
-                case 8: return launch(k_pair_bits<EPI_LIF, 8, S, Q>);
-                default: return launch(k_pair_bits<EPI_LIF, 16, S, Q>);
-            }
+        auto by_pre = [&](auto pc) -> int {
+            constexpr bool PR = decltype(pc)::value;
+            if (!lif) return launch(k_pair_bits<EPI_Y, 1, false, false, PR>);
+            const bool spk = lif->spk != nullptr, rate = lif->rate != nullptr;
+            auto by_t = [&](auto sc, auto rc) -> int {
+                constexpr bool S = decltype(sc)::value, Q = decltype(rc)::value;
+                switch (P.n_time) {
+                    case 1: return launch(k_pair_bits<EPI_LIF, 1, S, Q, PR>);
+                    case 2: return launch(k_pair_bits<EPI_LIF, 2, S, Q, PR>);
+                    case 4: return launch(k_pair_bits<EPI_LIF, 4, S, Q, PR>);
+                    case 8: return launch(k_pair_bits<EPI_LIF, 8, S, Q, PR>);
+                    default: return launch(k_pair_bits<EPI_LIF, 16, S, Q, PR>);
+                }
+            };
+            if (spk && rate) return by_t(std::true_type{}, std::true_type{});
+            if (spk) return by_t(std::true_type{}, std::false_type{});
+            return by_t(std::false_type{}, std::true_type{});
         };
-        if (spk && rate) return by_t(std::true_type{}, std::true_type{});
-        if (spk) return by_t(std::true_type{}, std::false_type{});
-        return by_t(std::false_type{}, std::true_type{});
+        return pre ? by_pre(std::true_type{}) : by_pre(std::false_type{});
+    }
+    if (pre) {
+        // dense input (the readout on spike rates) on the PRE form of k_linear_pair
+        if (lif) return HSES_ERR_UNSUPPORTED;
+        switch (P.x_fmt) {
+            case HSES_FMT_F32:
+                return P.a <= 16 ? launch(k_linear_pair<HSES_FMT_F32, EPI_Y, 1, 1, true>)
+                                 : launch(k_linear_pair<HSES_FMT_F32, EPI_Y, 1, 4, true>);
+            case HSES_FMT_BF16:
+                return P.a <= 16 ? launch(k_linear_pair<HSES_FMT_BF16, EPI_Y, 1, 1, true>)
+                                 : launch(k_linear_pair<HSES_FMT_BF16, EPI_Y, 1, 4, true>);
+            default: return HSES_ERR_UNSUPPORTED;
+        }
     }
     if (lif) {
         switch (P.n_time) {

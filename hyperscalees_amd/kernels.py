@@ -161,13 +161,36 @@ def _rec_arg(rec):
     return _p(rec), rec.numel() * 4
 
 
+def pair_image(a, b, rank, tid_lo, n, device="cuda"):
+    """A bf16 operand image buffer (stored as int16) for the factors of members
+    [tid_lo, tid_lo + n) of an (a, b) parameter (hses_pair_image_bytes)."""
+    nbytes = int(_lib.load().hses_pair_image_bytes(a, b, rank, tid_lo, n))
+    if nbytes == 0:
+        raise ValueError("no operand image for this shape")
+    return torch.empty(nbytes // 2, dtype=torch.int16, device=device)
+
+
+def _img_arg(img):
+    _dev(img, torch.int16, "img")
+    return _p(img), img.numel() * 2
+
+
+def pair_factors(key, rank, sigma, epoch, noise_reuse, tid_lo, n, a, b, rec, img):
+    """Draw every pair's factors of members [tid_lo, tid_lo + n) into the factor
+    record `rec` and the operand image `img` (hses_pair_factors); the forwards
+    given rec= and img= then read them instead of drawing."""
+    _lib.call("hses_pair_factors", key & (2**64 - 1), rank, sigma, epoch, noise_reuse, tid_lo, n,
+              a, b, *_rec_arg(rec), *_img_arg(img), _stream())
+
+
 def perturbed_linear(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n, rows_per_member,
                      x_fmt=FMT_F32, x_width=None, n_time=1, math=MATH_F32, out=None, act=0,
-                     out_bf16=False, rec=None):
+                     out_bf16=False, rec=None, img=None):
     """Batched do_mm.  x is (n_time, n*rows_per_member, units) in x_fmt (or 2-D
     when n_time == 1); returns y (n_time, n*rows_per_member, a) fp32 (bf16 with
     out_bf16), passed through the activation `act` (hses_act) when it is not 0.
-    With `rec` (factor_record) the pairs' normals are also kept there."""
+    With `rec` (factor_record) the pairs' normals are also kept there; with
+    `rec` and `img` filled by pair_factors they are read from there instead."""
     a, b = W.shape
     _dev(W, torch.float32, "W")
     _dev(x, _FMT_DTYPE[x_fmt], "x")
@@ -184,7 +207,13 @@ def perturbed_linear(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n, rows
     wbytes = int(_lib.load().hses_perturbed_linear_workspace(a, b, rank, n, rows_per_member,
                                                               n_time, math))
     work = _workspace(wbytes, W.device)
-    if rec is not None:
+    if img is not None:
+        if rec is None or act or out_bf16 or math != MATH_BF16:
+            raise ValueError("factors drawn ahead need rec, bf16 math and a plain fp32 output")
+        _lib.call("hses_perturbed_linear_pre", _p(x), x_fmt, units, M * units, n_time, _p(W), a,
+                  b, rank, sigma, tid_lo, n, rows_per_member, _p(out), a, M * a, _p(work),
+                  wbytes, *_rec_arg(rec), *_img_arg(img), _stream())
+    elif rec is not None:
         if act or out_bf16:
             raise ValueError("the factor record is kept by the plain fp32-output forward only")
         _lib.call("hses_perturbed_linear_rec", _p(x), x_fmt, units, M * units, n_time, _p(W), a,
@@ -238,10 +267,11 @@ def perturbed_linear_t(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n, ro
 
 def perturbed_linear_lif(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n,
                          rows_per_member, n_time, tau_m, v_th, spikes=None, rate=None,
-                         want_spikes=True, want_rate=False, rec=None):
+                         want_spikes=True, want_rate=False, rec=None, img=None):
     """Perturbed forward fused with LIF.  x is bit-packed (n_time, M, words(b));
     returns (spikes (n_time, M, words(a)) int64 or None, rate (M, a) or None).
-    With `rec` (factor_record) the pairs' normals are also kept there."""
+    With `rec` (factor_record) the pairs' normals are also kept there; with
+    `rec` and `img` filled by pair_factors they are read from there instead."""
     a, b = W.shape
     _dev(W, torch.float32, "W")
     _dev(x, _FMT_DTYPE[FMT_BITS], "x")
@@ -269,7 +299,15 @@ def perturbed_linear_lif(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n,
             sigma, epoch, noise_reuse, tid_lo, n, rows_per_member, tau_m, v_th,
             _p(spikes) if spikes is not None else None, wa, M * wa,
             _p(rate) if rate is not None else None, a, _p(work), wbytes)
-    if rec is None:
+    if img is not None:
+        if rec is None:
+            raise ValueError("factors drawn ahead need rec")
+        _lib.call("hses_perturbed_linear_lif_pre", _p(x), FMT_BITS, units, M * units, n_time,
+                  _p(W), a, b, rank, sigma, tid_lo, n, rows_per_member, tau_m, v_th,
+                  _p(spikes) if spikes is not None else None, wa, M * wa,
+                  _p(rate) if rate is not None else None, a, _p(work), wbytes, *_rec_arg(rec),
+                  *_img_arg(img), _stream())
+    elif rec is None:
         _lib.call("hses_perturbed_linear_lif", *args, _stream())
     else:
         _lib.call("hses_perturbed_linear_lif_rec", *args, *_rec_arg(rec), _stream())

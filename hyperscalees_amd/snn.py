@@ -113,7 +113,7 @@ class SnnEs:
     """Device-resident SNN-MLP population evaluation and ES update."""
 
     def __init__(self, cfg, weights, pool, pool_labels, index, device="cuda", fused=None,
-                 record=None):
+                 record=None, ahead=None):
         self.cfg = cfg
         c = cfg
         self.dev = device
@@ -163,6 +163,19 @@ class SnnEs:
                              for t in (0, n_odd))
                 self.rec.append(torch.empty(nbytes // 4, dtype=torch.float32, device=device))
         self._rec_at = [None] * L  # per layer: (epoch, lo) of the forward its record holds
+        # Factors drawn ahead (with a record): each layer's draw is a launch of
+        # its own (hses_pair_factors, full occupancy) and the forward reads the
+        # record and the bf16 B operand image instead of drawing.
+        self.ahead = self.record if ahead is None else (bool(ahead) and self.record)
+        self.img = None
+        if self.ahead:
+            self.img = []
+            n_odd = c.chunk if c.accumulate > 1 and c.chunk % 2 else 0
+            for w in self.W:
+                a, b = w.shape
+                nbytes = max(K._lib.load().hses_pair_image_bytes(a, b, c.rank, t, c.chunk)
+                             for t in (0, n_odd))
+                self.img.append(torch.empty(nbytes // 2, dtype=torch.int16, device=device))
 
     # -- forward -------------------------------------------------------------
     def chunk_seeds(self, lo):
@@ -186,12 +199,13 @@ class SnnEs:
         a = c.dims[l + 1]
         if self.fused:
             last = l == self.L - 2  # feeds the readout: only its spike rates are used
+            img = self._draw(l, epoch, lo)
             K.perturbed_linear_lif(self.spk[l], self.W[l], c.keys[l], c.rank, c.sigma, epoch,
                                    c.noise_reuse, lo, c.chunk, c.rows, c.T, c.tau_m, c.v_th,
                                    spikes=None if last else self.spk[l + 1],
                                    rate=self.rate if last else None,
                                    want_spikes=not last, want_rate=last,
-                                   rec=self.rec[l] if self.rec else None)
+                                   rec=self.rec[l] if self.rec else None, img=img)
             if self.rec:
                 self._rec_at[l] = (epoch, lo)
             return
@@ -206,15 +220,27 @@ class SnnEs:
         c = self.cfg
         if not self.fused:
             K.spike_rate(self.spk[self.L - 1], FMT_BITS, c.dims[-2], out=self.rate)
+        img = self._draw(self.L - 1, epoch, lo)
         K.perturbed_linear(self.rate, self.W[-1], c.keys[-1], c.rank, c.sigma, epoch,
                            c.noise_reuse, lo, c.chunk, c.rows, x_fmt=FMT_F32, n_time=1,
                            math=c.math, out=self.logits.view(1, self.M, -1),
-                           rec=self.rec[-1] if self.rec else None)
+                           rec=self.rec[-1] if self.rec else None, img=img)
         if self.rec:
             self._rec_at[-1] = (epoch, lo)
         labels = self.labels[lo * c.rows:(lo + c.chunk) * c.rows]
         return K.member_fitness(self.logits, labels, c.chunk, c.rows, c.reward,
                                 out=self.raw[lo:lo + c.chunk], correct=self.correct)
+
+    def _draw(self, l, epoch, lo):
+        """Layer l's factors of the chunk into its record and operand image
+        (factors drawn ahead), or None when the forward draws them itself."""
+        if not self.img:
+            return None
+        c = self.cfg
+        a, b = self.W[l].shape
+        K.pair_factors(c.keys[l], c.rank, c.sigma, epoch, c.noise_reuse, lo, c.chunk, a, b,
+                       self.rec[l], self.img[l])
+        return self.img[l]
 
     def forward(self, epoch=0, lo=0):
         """Raw fitness of the chunk of members [lo, lo + chunk) (a view of self.raw)."""

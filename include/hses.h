@@ -280,6 +280,47 @@ int hses_perturbed_linear_lif_rec(const void *d_x, int32_t x_fmt, int64_t x_stri
                                   size_t work_bytes, float *d_rec, size_t rec_bytes,
                                   void *stream);
 
+/* ---- factors drawn ahead ---------------------------------------------------
+ * The same forwards with the draw split off (get_lora_update_params /
+ * batched_lora_noise, eggroll.rs:116-227, as consumed by do_mm
+ * eggroll.rs:419-446 and lora_linear_batched snn.rs:665-685): hses_pair_factors
+ * draws every pair's factors of members [tid_lo, tid_lo + n) into the factor
+ * record and a bf16 operand image of the scaled B factors (pair-major, rank
+ * rows padded to a multiple of 64 inputs); the *_pre forwards read both and
+ * draw nothing.  Outputs equal the *_rec forwards' bit for bit.  The draw is
+ * its own launch, so a caller can run it on another stream or ahead of the
+ * forward (it depends on the key, epoch and members only, not on W or x).
+ * do_mm only; rank a multiple of 16 in [32, 128], sigma != 0, a <= 128. */
+
+/* Bytes of the operand image of members [tid_lo, tid_lo + n). */
+size_t hses_pair_image_bytes(int32_t a, int32_t b, int32_t rank, int32_t tid_lo, int32_t n);
+
+int hses_pair_factors(uint64_t key, int32_t rank, float sigma, int32_t epoch,
+                      int32_t noise_reuse, int32_t tid_lo, int32_t n, int32_t a, int32_t b,
+                      float *d_rec, size_t rec_bytes, uint16_t *d_img, size_t img_bytes,
+                      void *stream);
+
+/* hses_perturbed_linear_rec's y from a record and image written by
+ * hses_pair_factors with the same (a, b, rank, sigma, tid_lo, n). */
+int hses_perturbed_linear_pre(const void *d_x, int32_t x_fmt, int64_t x_stride, int64_t x_plane,
+                              int32_t n_time, const float *d_W, int32_t a, int32_t b,
+                              int32_t rank, float sigma, int32_t tid_lo, int32_t n,
+                              int32_t rows_per_member, float *d_y, int64_t y_stride,
+                              int64_t y_plane, void *d_work, size_t work_bytes,
+                              const float *d_rec, size_t rec_bytes, const uint16_t *d_img,
+                              size_t img_bytes, void *stream);
+
+/* hses_perturbed_linear_lif_rec's spikes and rates from a record and image
+ * written by hses_pair_factors (n_time <= 16, b <= 1024). */
+int hses_perturbed_linear_lif_pre(const void *d_x, int32_t x_fmt, int64_t x_stride,
+                                  int64_t x_plane, int32_t n_time, const float *d_W, int32_t a,
+                                  int32_t b, int32_t rank, float sigma, int32_t tid_lo, int32_t n,
+                                  int32_t rows_per_member, float tau_m, float v_th,
+                                  uint64_t *d_spikes, int64_t spk_stride, int64_t spk_plane,
+                                  float *d_rate, int64_t rate_stride, void *d_work,
+                                  size_t work_bytes, const float *d_rec, size_t rec_bytes,
+                                  const uint16_t *d_img, size_t img_bytes, void *stream);
+
 /* ---- ES update ------------------------------------------------------- */
 
 /* EggRoll ES gradient of one MM parameter (eggroll.rs:353-404 _simple_lora_update +
