@@ -68,6 +68,26 @@ struct K2Layout {
     }
 };
 
+// Rank column c of A is stored at column swap23(c) (bits 2 and 3 exchanged):
+// the 8 rank columns one lane feeds to a 16-deep MFMA step of k_pair_bits,
+// {0..3, 8..11} + 4 * k-group, then sit at 8 contiguous columns 8 * k-group.
+__host__ __device__ __forceinline__ int32_t swap23(int32_t c) {
+    return (c & ~12) | ((c & 4) << 1) | ((c & 8) >> 1);
+}
+
+// Operand image of one pair (factors drawn ahead, bf16): the input-side factor
+// as [c][kp] (r rows, the layout of a staging slot, zero for k >= b), then
+// the output-side factor as [o][swap23(c)] rows of K2_NMAX + 8 (a rows, zero
+// for rank columns [r, r rounded up to 32)), the layout of k_pair_bits' LDS
+// block.  Elements per pair: stride.
+struct PairImage {
+    size_t b_elems, stride;
+    __host__ __device__ PairImage(int a, int b, int r) {
+        b_elems = (size_t)r * ((b + 63) / 64 * 64);
+        stride = b_elems + (size_t)a * (K2_NMAX + 8);
+    }
+};
+
 struct K2Args {
     const void* x;
     int64_t x_stride, x_plane;
@@ -94,8 +114,7 @@ struct K2Args {
     // any scale) at rec[(i * r + c) * (a + b) + j] for stream row j, rank c.
     float* rec;
     // Factors drawn ahead (PRE kernels, k_pair_gen): pair pair_lo + i's
-    // scaled input-side factor as bf16 at bimg[(i * r + c) * kp + k] (the
-    // layout of a staging slot, zero for k >= b); A comes from rec.
+    // operand image (PairImage) at bimg + i * stride.
     uint16_t* bimg;
 };
 
@@ -166,12 +185,13 @@ __global__ void k_w_to_bf16(const float* __restrict__ W, int32_t a, int32_t b, i
 
 // Factors of the pair kernels drawn ahead of their GEMM (the PRE kernels):
 // one thread per (pair, stream row) continues its row of the pair's stream
-// for r normals, keeps each raw normal in the factor record and, for an
-// input-side row, its scaled bf16 value in the B operand image.  Threads of
-// output-side rows also zero the image's padding columns [b, kp).  Lanes
-// take consecutive stream rows, so for each rank column a wave's record
-// stores and image stores are contiguous runs.  Full occupancy (256-thread
-// workgroups, no other work) keeps the VALU-bound generator at its rate.
+// for r normals, keeps each raw normal in the factor record and its scaled
+// bf16 value in the pair's operand image (PairImage).  Threads of
+// output-side rows also zero the image's padding columns [b, kp) and their
+// row's rank padding.  Lanes take consecutive stream rows, so for each rank
+// column a wave's record stores and input-side image stores are contiguous
+// runs.  Full occupancy (256-thread workgroups, no other work) keeps the
+// VALU-bound generator at its rate.
 constexpr int KG_THREADS = 256;
 __global__ __launch_bounds__(KG_THREADS) void k_pair_gen(const K2Args P) {
     __shared__ BmTables t;
@@ -188,16 +208,21 @@ __global__ __launch_bounds__(KG_THREADS) void k_pair_gen(const K2Args P) {
     uint64_t s = row_start_state(noise_seed(P.key, te, tt), (int32_t)j, P.jump);
     const StreamRow sr(P, (int32_t)j);
     float* rp = P.rec + (size_t)pi * r * rows + j;
-    uint16_t* img = P.bimg + (size_t)pi * r * kp;
-    uint16_t* bp = sr.in_side ? img + sr.row : nullptr;
+    const PairImage im(P.a, P.b, r);
+    uint16_t* img = P.bimg + (size_t)pi * im.stride;
+    // input side: element c at bp[c * kp]; output side: at bp[swap23(c)]
+    uint16_t* bp = sr.in_side ? img + sr.row : img + im.b_elems + (size_t)sr.row * (K2_NMAX + 8);
+    const int32_t cs = sr.in_side ? kp : 0;
     const NoiseCtx ctx{&t, P.log_exc, P.cos_exc};
     bm_run(s, r, ctx, [&](int32_t c, float v) {
         rp[(size_t)c * rows] = v;
-        if (bp) bp[(size_t)c * kp] = f2bf(v * sr.scale);
+        bp[cs ? (size_t)c * kp : (size_t)swap23(c)] = f2bf(v * sr.scale);
     });
-    if (!sr.in_side)
+    if (!sr.in_side) {
+        for (int32_t c = r; c < ((r + 31) & ~31); ++c) bp[c] = 0;  // swap23 keeps 16-blocks
         for (int32_t k = P.b + sr.row; k < kp; k += P.a)
             for (int32_t c = 0; c < r; ++c) img[(size_t)c * kp + k] = 0;
+    }
 }
 
 void launch_w_to_bf16(const float* W, int32_t a, int32_t b, int32_t kp, int32_t tmm, uint16_t* out,
@@ -473,7 +498,8 @@ __global__ __launch_bounds__(K2_THREADS) void k_linear_pair(const K2Args P) {
         const int32_t m_even = 2 * pair - P.tid_lo;
         const int32_t m_lo = max(m_even, 0), m_hi = min(m_even + 1, P.n - 1);
         const int64_t row_lo = (int64_t)m_lo * R, row_hi = (int64_t)(m_hi + 1) * R;
-        const uint16_t* lsrc = (lw ? P.wbf : PRE ? P.bimg + (size_t)pi * r * kp : slots + (size_t)g * r * kp) + loff;
+        const uint16_t* lsrc =
+            (lw ? P.wbf : PRE ? P.bimg + (size_t)pi * PairImage(a, b, r).stride : slots + (size_t)g * r * kp) + loff;
         const uint16_t* Ag = As + (size_t)g * a * lay.apitch;
 
         // ---- 2./3. row blocks ----------------------------------------------------
@@ -646,12 +672,6 @@ constexpr int K3_XPF = 8;
 // product's LDS addresses immediate offsets of one base.
 constexpr int K3_AP = K2_NMAX + 8;
 
-// Rank column c of A is stored at column swap23(c) (bits 2 and 3 exchanged):
-// the 8 rank columns one lane feeds to a 16-deep MFMA step, {0..3, 8..11} +
-// 4 * k-group, then sit at 8 contiguous columns 8 * k-group.
-__device__ __forceinline__ int32_t swap23(int32_t c) {
-    return (c & ~12) | ((c & 4) << 1) | ((c & 8) >> 1);
-}
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
@@ -744,6 +764,10 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
         *hi = (int64_t)(min(m_even + 1, P.n - 1) + 1) * R;
     };
     bool xready = false;  // the first block's bit rows are already in LDS
+    // K of at most two tiles: both stay in the two LDS buffers for all of a
+    // pair's blocks (staged by its first block), so no block reloads them
+    // and the K loop needs no barrier between its tiles.
+    const bool resident = nkt <= 2;
 
     for (int32_t pi = blockIdx.x; pi < P.n_pairs; pi += gridDim.x) {
         const int32_t pair = P.pair_lo + pi;
@@ -753,29 +777,29 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
 
         // ---- 1. factors: A rows -> LDS (bf16, [o][c]); B rows -> slot ([c][k]) ----
         if constexpr (PRE) {
-            if (lcol >= K2_NMAX) lsrc = P.bimg + (size_t)pi * r * kp + loff;
-            // A^T of the pair is rec[(pi r + c)(a + b) + aoff + o]: scale, round
-            // and place it (swap23 columns) as the generation would have; eight
-            // loads in flight per thread
+            // the pair's image holds A in this block's layout: one round of
+            // 16-byte copies (a rows of K3_AP bf16, at most 5 per thread)
+            const PairImage im(a, b, r);
+            const uint16_t* img = P.bimg + (size_t)pi * im.stride;
+            if (lcol >= K2_NMAX) lsrc = img + loff;
+            const uint4* asrc = reinterpret_cast<const uint4*>(img + im.b_elems);
+            const int32_t n16 = a * (K3_AP / 8);
+            uint4 av0, av1, av2, av3, av4;
+            auto aload = [&](int q) { return asrc[min(tid + q * K3_THREADS, n16 - 1)]; };
+            auto astore = [&](int q, const uint4& v) {
+                if (tid + q * K3_THREADS < n16) reinterpret_cast<uint4*>(As)[tid + q * K3_THREADS] = v;
+            };
+            av0 = aload(0);
+            av1 = aload(1);
+            av2 = aload(2);
+            av3 = aload(3);
+            av4 = aload(4);
             __syncthreads();  // the previous pair's epilogue has finished reading As
-            const int32_t na = r * a, aoff = P.tmm ? 0 : b;
-            const float sc = P.tmm ? 1.0f : P.bs;
-            const float* ar = P.rec + (size_t)pi * r * (a + b) + aoff;
-            for (int32_t i0 = 0; i0 < na; i0 += 8 * K3_THREADS) {
-                float v[8];
-#pragma unroll
-                for (int q = 0; q < 8; ++q) {
-                    const int32_t i = min(i0 + q * K3_THREADS + tid, na - 1);
-                    v[q] = ar[(size_t)(i / a) * (a + b) + i % a];
-                }
-#pragma unroll
-                for (int q = 0; q < 8; ++q) {
-                    const int32_t i = i0 + q * K3_THREADS + tid;
-                    if (i < na) As[(size_t)(i % a) * K3_AP + swap23(i / a)] = f2bf(v[q] * sc);
-                }
-            }
-            for (int32_t i = tid; i < a * (rp32 - r); i += K3_THREADS)
-                As[(size_t)(i / (rp32 - r)) * K3_AP + r + i % (rp32 - r)] = 0;
+            astore(0, av0);
+            astore(1, av1);
+            astore(2, av2);
+            astore(3, av3);
+            astore(4, av4);
             __threadfence_block();
             __syncthreads();
         } else {
@@ -850,9 +874,13 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
             if (first) {
                 K3_TILE_LOAD(0);
                 K3_TILE_STORE(0);
+                if (resident && nkt > 1) {
+                    K3_TILE_LOAD(1);
+                    K3_TILE_STORE(1);
+                }
             }
             lds_barrier();
-            if (nkt > 1) K3_TILE_LOAD(1);
+            if (nkt > 1 && !resident) K3_TILE_LOAD(1);
 
             f32x16 accW[4], accB[4];
 #pragma unroll
@@ -886,11 +914,12 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
                     for (int j = 0; j < 4; ++j) accB[j] = mfma32_bf16(fr[4 + j], xa, accB[j]);
                     __builtin_amdgcn_sched_barrier(0);
                 }
-                if (kt + 1 < nkt) {
+                if (kt + 1 < nkt && !resident) {
                     K3_TILE_STORE(cur ^ 1);
                     if (kt + 2 < nkt) K3_TILE_LOAD(kt + 2);
                 }
-                lds_barrier();
+                // resident tiles: one barrier, before the epilogue restages Xbits
+                if (!resident || kt + 1 == nkt) lds_barrier();
             }
 
             // sign * xB as bf16: lane l holds rank columns 32j + 8g + 4hl + v of
@@ -920,7 +949,7 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
                 if (has_next) nlo = L0 + K3_RB;
                 else if (next_pair) pair_rows(pi + (int32_t)gridDim.x, &nlo, &nhi);
                 xbits_load(nlo, nhi, xpf);
-                K3_TILE_LOAD(0);
+                if (!resident) K3_TILE_LOAD(0);
             }
             // accW += (sign xB) A^T over K = r in steps of 16: step (j, t) gives
             // k-group hl the rank columns 32j + 16t + 4hl + {0..3, 8..11}, stored
@@ -1032,7 +1061,7 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
                     }
                 }
             }
-            if (has_next) K3_TILE_STORE(0);
+            if (has_next && !resident) K3_TILE_STORE(0);
             if (has_next || next_pair) xbits_store(xpf);
             xready = next_pair;
         }
@@ -1120,11 +1149,10 @@ int launch_pair_gen(LinParams& P, DeviceState* st, hipStream_t s, uint16_t* bimg
 }
 
 size_t pair_image_bytes(int32_t a, int32_t b, int32_t r, int32_t tid_lo, int32_t n) {
-    (void)a;
     if (n < 1 || r < 1 || b < 1 || tid_lo < 0) return 0;
     int32_t lo, cnt;
     pair_range(tid_lo, n, &lo, &cnt);
-    return (size_t)cnt * r * ((size_t)(b + 63) / 64 * 64) * 2;
+    return (size_t)cnt * PairImage(a, b, r).stride * 2;
 }
 
 int launch_linear_pair(LinParams& P, DeviceState* st, hipStream_t s, void* work, size_t work_bytes,

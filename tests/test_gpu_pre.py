@@ -5,7 +5,8 @@ instead of drawing.
 Pinned against the generating forwards, which the oracle pins elsewhere
 (test_gpu_linear, test_gpu_snn, test_gpu_c3_full): the record hses_pair_factors
 writes equals the one the *_rec forwards keep, the image is the bf16 rounding
-of the record's B rows with zero padding, and the *_pre forwards' spikes,
+of the record's B rows and scaled A rows in their kernel layouts with zero
+padding, and the *_pre forwards' spikes,
 rates and currents equal the *_rec forwards' bit for bit (same operands,
 products and order), also inside whole SNN steps."""
 import numpy as np
@@ -31,15 +32,31 @@ def draw(a, b, r, sigma, epoch, nreuse, tid_lo, n):
     return rec, img
 
 
-def check_image(rec, img, a, b, r, tid_lo, n):
+def swap23(c):
+    return (c & ~12) | ((c & 4) << 1) | ((c & 8) >> 1)
+
+
+def check_image(rec, img, a, b, r, sigma, tid_lo, n):
+    """Per pair: B^T as [c][kp] (bf16 of the raw normal, zero for k >= b), then
+    A as [o][swap23(c)] rows of 136 (bf16 of normal * sigma / sqrt(r), zero
+    for rank columns [r, r rounded up to 32))."""
     P = pairs_of(tid_lo, n)
     kp = (b + 63) // 64 * 64
-    assert img.numel() == P * r * kp
+    stride = r * kp + a * 136
+    assert img.numel() == P * stride
     recv = rec[: P * r * (a + b)].view(P, r, a + b)
-    im = img.view(P, r, kp)
+    im = img.view(P, stride)
+    bt = im[:, : r * kp].view(P, r, kp)
     want = recv[:, :, :b].to(torch.bfloat16).view(torch.int16)  # do_mm: B unscaled, RNE
-    assert torch.equal(im[:, :, :b], want)
-    assert not im[:, :, b:].any(), "padding columns must be zero"
+    assert torch.equal(bt[:, :, :b], want)
+    assert not bt[:, :, b:].any(), "padding columns must be zero"
+    bs = torch.tensor(np.float32(sigma) / np.sqrt(np.float32(r)), device=rec.device)
+    at = im[:, r * kp:].view(P, a, 136)
+    pos = torch.tensor([swap23(c) for c in range(r)], device=rec.device)
+    wantA = (recv[:, :, b:].transpose(1, 2) * bs).to(torch.bfloat16).view(torch.int16)
+    assert torch.equal(at[:, :, pos], wantA)
+    rp32 = (r + 31) // 32 * 32
+    assert not at[:, :, r:rp32].any(), "rank padding must be zero"
 
 
 @pytest.mark.parametrize("a,b,r,n,tid_lo,T,epoch,nreuse", [
@@ -61,7 +78,7 @@ def test_lif_pre_equals_rec(hses_gpu, a, b, r, n, tid_lo, T, epoch, nreuse):
     rec, img = draw(a, b, r, sigma, epoch, nreuse, tid_lo, n)
     torch.cuda.synchronize()
     assert torch.equal(rec, rec0), "record of the draw differs from the forward's"
-    check_image(rec, img, a, b, r, tid_lo, n)
+    check_image(rec, img, a, b, r, sigma, tid_lo, n)
     s1, q1 = K.perturbed_linear_lif(x, W, KEY, r, sigma, epoch, nreuse, tid_lo, n, rows, T, 10.0,
                                     1.0, want_spikes=True, want_rate=True, rec=rec, img=img)
     torch.cuda.synchronize()
@@ -107,7 +124,7 @@ def test_dense_pre_equals_rec(hses_gpu, a, b, r, n, tid_lo):
                             math=MATH_BF16, rec=rec, img=img)
     torch.cuda.synchronize()
     assert torch.equal(rec, rec0)
-    check_image(rec, img, a, b, r, tid_lo, n)
+    check_image(rec, img, a, b, r, sigma, tid_lo, n)
     assert torch.equal(y0, y1)
 
 
