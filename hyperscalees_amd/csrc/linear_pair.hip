@@ -883,39 +883,46 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
             if (nkt > 1 && !resident) K3_TILE_LOAD(1);
 
             f32x16 accW[4], accB[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-#pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    accW[j][e] = 0.0f;
-                    accB[j][e] = 0.0f;
-                }
-            }
             const uint32_t* xw = Xbits32 + (wrow0 + xrow) * (2 * nkt);
-
-            for (int32_t kt = 0; kt < nkt; ++kt) {
-                const int cur = kt & 1;
-                const uint16_t* tb = WB + cur * (K2_COLS * K2_TP) + lc * K2_TP + hl * 8;
+            // One K tile: four k-steps of 16 (this lane's 8 k at 16ks + 8hl),
+            // each one x expansion and 8 MFMAs whose eight operand reads are
+            // issued first (the scheduler would otherwise issue each read just
+            // before its MFMA).  ZERO: the block's first tile, whose first step
+            // starts from the zero operand instead of clearing 128 accumulator
+            // registers (8.6% of the K loop's cycles at b = 784).
+            auto k_tile = [&](int32_t kt, auto zc) {
+                constexpr bool ZERO = decltype(zc)::value;
+                const uint16_t* tb = WB + (kt & 1) * (K2_COLS * K2_TP) + lc * K2_TP + hl * 8;
                 const uint32_t w2[2] = {xw[2 * kt], xw[2 * kt + 1]};
-#pragma unroll
-                for (int ks = 0; ks < 4; ++ks) {  // k-steps of 16: this lane's 8 k at 16ks + 8hl
-                    // all eight operand reads of the step are issued before its MFMAs
+                static_for<0, 4>([&](auto kc) {
+                    constexpr int ks = decltype(kc)::value;
+                    constexpr bool z = ZERO && ks == 0;
                     u16x8 fr[8];
 #pragma unroll
                     for (int j = 0; j < 8; ++j)
                         fr[j] = lds_u16x8(tb + ((j < 4 ? 0 : K2_NMAX) + 32 * (j & 3)) * K2_TP + 16 * ks);
                     const u16x8 xa = expand_bits((w2[ks >> 1] >> (8 * ((ks & 1) * 2 + hl))) & 0xffu);
-                    // keep the reads ahead of the MFMAs (the scheduler would
-                    // otherwise issue each read just before its MFMA)
                     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) accW[j] = mfma32_bf16(xa, fr[j], accW[j]);
+                    for (int j = 0; j < 4; ++j) accW[j] = mfma32_bf16(xa, fr[j], z ? f32x16{} : accW[j]);
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) accB[j] = mfma32_bf16(fr[4 + j], xa, accB[j]);
+                    for (int j = 0; j < 4; ++j)
+                        accB[j] = mfma32_bf16(fr[4 + j], xa, z ? f32x16{} : accB[j]);
                     __builtin_amdgcn_sched_barrier(0);
-                }
+                });
+            };
+            // tile kt sits in LDS buffer kt & 1; the next one is staged from
+            // registers after it (unless the tiles are resident)
+            k_tile(0, std::true_type{});
+            if (nkt > 1 && !resident) {
+                K3_TILE_STORE(1);
+                if (nkt > 2) K3_TILE_LOAD(2);
+            }
+            if (!resident || nkt == 1) lds_barrier();
+            for (int32_t kt = 1; kt < nkt; ++kt) {
+                k_tile(kt, std::false_type{});
                 if (kt + 1 < nkt && !resident) {
-                    K3_TILE_STORE(cur ^ 1);
+                    K3_TILE_STORE((kt & 1) ^ 1);
                     if (kt + 2 < nkt) K3_TILE_LOAD(kt + 2);
                 }
                 // resident tiles: one barrier, before the epilogue restages Xbits
