@@ -30,10 +30,11 @@ METRIC = "perturbed member-evals/sec + ES-update GB/s, SNN-MLP N=8192 r=128"
 PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
 PEAK_FP32_TFLOPS = 157.3      # MI355X dense fp32 MFMA
 PEAK_HBM_GBPS = 8000.0
-# HBM bytes per fc1 launch from two rocprofv3 PMC runs (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0,
-# factors from a 1 GiB copy) of `python3 -m hyperscalees_amd.profile_fc1`;
-# see profiles/fc1_c3_traffic.md.  Refreshed whenever the kernel changes.
-FC1_TRAFFIC_BYTES = 9.43e9
+# HBM bytes per launch of fc1's GEMM on factors drawn ahead, from two rocprofv3 PMC runs
+# (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0, factors from a 1 GiB copy in the same process) of
+# `python3 -m hyperscalees_amd.profile_fc1`: 4.126 GB x 2 + 0.134 GB; see
+# profiles/fc1_c3_traffic.md.  Refreshed whenever the kernel changes.
+FC1_TRAFFIC_BYTES = 8.39e9
 
 
 def layer_flops(cfg, l):
@@ -543,41 +544,61 @@ def main():
     torch.cuda.synchronize()
 
     ev = lambda: torch.cuda.Event(enable_timing=True)
+    # Whole ES steps (es.step), consecutive epochs; stage events recorded on
+    # the stream as the stages are issued.
     marks = []
     t0 = time.perf_counter()
     for s in range(args.steps):
-        e = [ev() for _ in range(2 * L + 4)]
-        e[0].record()
-        es.poisson()
-        e[1].record()
-        for l in range(L - 1):
-            es.hidden_layer(l, s)
-            e[2 + l].record()
-        fit = es.readout(s)
-        e[L + 1].record()
-        es.update(fit, s)
-        e[L + 2].record()
-        marks.append(e)
+        evs = {}
+
+        def mark(name, evs=evs):
+            e = ev()
+            e.record()
+            evs[name] = e
+        mark("start")
+        es.step(epoch=args.warmup + s, mark=mark)
+        marks.append(evs)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     ms_per_step = (t1 - t0) * 1000.0 / args.steps
 
     def span(e, i, j):
         return e[i].elapsed_time(e[j])
-    t_poisson = np.mean([span(e, 0, 1) for e in marks])
-    t_hidden = [np.mean([span(e, 1 + l, 2 + l) for e in marks]) for l in range(L - 1)]
-    t_readout = np.mean([span(e, L, L + 1) for e in marks])
-    t_fwd = np.mean([span(e, 0, L + 1) for e in marks])
-    t_upd = np.mean([span(e, L + 1, L + 2) for e in marks])
+    stages = ["poisson"] + [f"hidden{l}" for l in range(L - 1)] + ["readout"]
+    t_poisson = np.mean([span(e, "start", "poisson") for e in marks])
+    t_hidden = [np.mean([span(e, stages[l], stages[l + 1]) for e in marks]) for l in range(L - 1)]
+    t_readout = np.mean([span(e, stages[L - 1], "readout") for e in marks])
+    t_fwd = np.mean([span(e, "start", "readout") for e in marks])
+    t_upd = np.mean([span(e, "readout", "update") for e in marks])
 
-    # Dominant kernel: fc1's perturbed forward (x[W^T|B] + (xB)A^T, bf16 MFMA;
-    # with the LIF fused into its epilogue when the step runs fused), timed
-    # alone with events on the launch stream.
+    # Dominant kernel: fc1's perturbed forward (x[W^T|B] + (xB)A^T, bf16 MFMA,
+    # LIF fused), timed alone with events on the launch stream: with factors
+    # drawn ahead, the GEMM kernel on the record and operand image (its draw,
+    # k_pair_gen, timed beside it); otherwise the kernel that draws inline.
+    a1, b1 = es.W[0].shape
+    draw = None
+    if es.ahead:
+        fc1_draw = lambda: K.pair_factors(cfg.keys[0], cfg.rank, cfg.sigma, 0, cfg.noise_reuse, 0,
+                                          cfg.n, a1, b1, es.rec[0], es.img[0])
+        draw_ms = _time_launch(fc1_draw, reps=3)
+        normals = (cfg.n // 2) * cfg.rank * (a1 + b1)
+        wbytes = normals * 4 + (cfg.n // 2) * (cfg.rank * ((b1 + 63) // 64 * 64) + a1 * 136) * 2
+        draw = {"kernel": ("k_pair_gen (fc1 factors: every pair's exact Box-Muller normals into "
+                           "the factor record and the bf16 operand image)"),
+                "bound": "valu", "launch_ms": round(draw_ms, 4), "normals_per_launch": normals,
+                "g_normals_per_s": round(normals / (draw_ms * 1e-3) / 1e9, 1),
+                "hbm_bytes_written": wbytes,
+                "hbm_frac": round(wbytes / (draw_ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
+        fc1_draw()
     fc1_ms = []
     for s in range(3):
         e0, e1 = ev(), ev()
         e0.record()
-        if es.fused:
+        if es.ahead:
+            K.perturbed_linear_lif(es.spk[0], es.W[0], cfg.keys[0], cfg.rank, cfg.sigma, 0,
+                                   cfg.noise_reuse, 0, cfg.n, cfg.rows, cfg.T, cfg.tau_m,
+                                   cfg.v_th, spikes=es.spk[1], rec=es.rec[0], img=es.img[0])
+        elif es.fused:
             K.perturbed_linear_lif(es.spk[0], es.W[0], cfg.keys[0], cfg.rank, cfg.sigma, s,
                                    cfg.noise_reuse, 0, cfg.n, cfg.rows, cfg.T, cfg.tau_m,
                                    cfg.v_th, spikes=es.spk[1],
@@ -597,7 +618,6 @@ def main():
     # the record (pairs x r x (a + b) fp32) plus the gradient written.
     upd_roof = None
     if es.rec is not None:
-        a1, b1 = es.W[0].shape
         zf = torch.randn(cfg.n, device="cuda")
         scale1 = np.float32(-math.sqrt(cfg.n) / cfg.n)
         upd1_ms = _time_launch(lambda: K.es_update_rec(zf, 0, es.rec[0], cfg.rank, cfg.sigma, a1,
@@ -638,14 +658,18 @@ def main():
                      "readout_fitness": round(float(t_readout), 3),
                      "forward": round(float(t_fwd), 3), "es_update": round(float(t_upd), 3)},
         "fwd_tflops": round(fwd_flops / (t_fwd * 1e-3) / 1e12, 1),
-        "roofline": {"kernel": ("k_pair_bits (fc1: x[W^T|B] + (xB)A^T, T=16 x 524288 rows"
+        "roofline": {"kernel": (("k_pair_bits<LIF, T=16, spikes, factors drawn ahead> (fc1 GEMM: "
+                                 if es.ahead else "k_pair_bits (fc1: ")
+                                + "x[W^T|B] + (xB)A^T, T=16 x 524288 rows"
                                 + (", LIF fused)" if es.fused else ")")),
                      "bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": FC1_TRAFFIC_BYTES if es.fused else None,
+                     "traffic": (FC1_TRAFFIC_BYTES if es.ahead else None),
                      "launch_ms": round(fc1_ms, 3),
                      "algorithmic_flop_per_launch": fc1_flops},
     }
+    if draw is not None:
+        out["draw"] = draw
     if upd_roof is not None:
         out["es_update_roofline"] = upd_roof
     if not args.no_cpu_baseline:

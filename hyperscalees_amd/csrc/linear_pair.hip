@@ -214,7 +214,7 @@ __global__ __launch_bounds__(KG_THREADS) void k_pair_gen(const K2Args P) {
     uint16_t* bp = sr.in_side ? img + sr.row : img + im.b_elems + (size_t)sr.row * (K2_NMAX + 8);
     const int32_t cs = sr.in_side ? kp : 0;
     const NoiseCtx ctx{&t, P.log_exc, P.cos_exc};
-    bm_run(s, r, ctx, [&](int32_t c, float v) {
+    bm_run2(s, r, ctx, [&](int32_t c, float v) {
         rp[(size_t)c * rows] = v;
         bp[cs ? (size_t)c * kp : (size_t)swap23(c)] = f2bf(v * sr.scale);
     });

@@ -3,10 +3,12 @@
 Runs, on cuda:0 with synthetic data of the C3 shape (bench.py's workload):
   * a device-to-device copy of a known size (1 GiB), the calibration point for
     the FETCH_SIZE / WRITE_SIZE hardware counters;
-  * the fc1 layer of the SNN step: hses_perturbed_linear_lif (x[W^T|B] +
-    (xB)A^T fused with the LIF scan), N = 8192 members, r = 128, T = 16, 64 rows
-    per member, b = 784, a = 128.
-Each is launched --reps times.  Use under rocprofv3, e.g.
+  * the fc1 layer of the SNN step as the step runs it: the factor draw
+    (hses_pair_factors, once) and then the GEMM on the drawn factors
+    (hses_perturbed_linear_lif_pre: x[W^T|B] + (xB)A^T fused with the LIF
+    scan), N = 8192 members, r = 128, T = 16, 64 rows per member, b = 784,
+    a = 128.
+The copy and the GEMM are launched --reps times.  Use under rocprofv3, e.g.
     rocprofv3 --pmc FETCH_SIZE --output-format csv -d OUT -- python3 -m hyperscalees_amd.profile_fc1
 """
 import argparse
@@ -30,6 +32,10 @@ def main():
     W = torch.randn(cfg.dims[1], cfg.dims[0], device="cuda", generator=g) * 0.05
     spk = torch.empty((cfg.T, M, K.fmt_width(K.FMT_BITS, cfg.dims[1])), dtype=torch.int64,
                       device="cuda")
+    a, b = cfg.dims[1], cfg.dims[0]
+    rec = K.factor_record(a, b, cfg.rank, 0, cfg.n)
+    img = K.pair_image(a, b, cfg.rank, 0, cfg.n)
+    K.pair_factors(cfg.keys[0], cfg.rank, cfg.sigma, 0, cfg.noise_reuse, 0, cfg.n, a, b, rec, img)
     src = torch.empty(1 << 28, dtype=torch.float32, device="cuda")  # 1 GiB
     dst = torch.empty_like(src)
     src.fill_(1.0)
@@ -37,10 +43,12 @@ def main():
     for _ in range(args.reps):
         dst.copy_(src)
     for s in range(args.reps):
-        K.perturbed_linear_lif(x, W, cfg.keys[0], cfg.rank, cfg.sigma, s, cfg.noise_reuse, 0,
-                               cfg.n, cfg.rows, cfg.T, cfg.tau_m, cfg.v_th, spikes=spk)
+        K.perturbed_linear_lif(x, W, cfg.keys[0], cfg.rank, cfg.sigma, 0, cfg.noise_reuse, 0,
+                               cfg.n, cfg.rows, cfg.T, cfg.tau_m, cfg.v_th, spikes=spk, rec=rec,
+                               img=img)
     torch.cuda.synchronize()
-    print("profile_fc1: copy 1 GiB x", args.reps, "; fc1 fused x", args.reps, flush=True)
+    print("profile_fc1: copy 1 GiB x", args.reps, "; fc1 draw x 1; fc1 GEMM x", args.reps,
+          flush=True)
 
 
 if __name__ == "__main__":

@@ -242,12 +242,19 @@ class SnnEs:
                        self.rec[l], self.img[l])
         return self.img[l]
 
-    def forward(self, epoch=0, lo=0):
-        """Raw fitness of the chunk of members [lo, lo + chunk) (a view of self.raw)."""
+    def forward(self, epoch=0, lo=0, mark=None):
+        """Raw fitness of the chunk of members [lo, lo + chunk) (a view of self.raw).
+        mark(name), when given, is called after each stage is issued (e.g. to
+        record an event on the current stream)."""
+        mark = mark or (lambda name: None)
         self.poisson(lo)
+        mark("poisson")
         for l in range(self.L - 1):
             self.hidden_layer(l, epoch, lo)
-        return self.readout(epoch, lo)
+            mark(f"hidden{l}")
+        fit = self.readout(epoch, lo)
+        mark("readout")
+        return fit
 
     def _grad(self, l, fit, lo, epoch, scale, accumulate=False):
         """grads[l] (+)= scale * sum_m fit[m] A_m B_m^T over members [lo, lo + len(fit)),
@@ -290,13 +297,15 @@ class SnnEs:
                 self._solve(l, gscale)
         return z
 
-    def step(self, epoch=0):
+    def step(self, epoch=0, mark=None):
         """One ES step; returns the raw fitness (N,).  self.correct counts the
-        step's rows whose argmax is the label."""
+        step's rows whose argmax is the label.  mark: see forward (plus "update")."""
         self.correct.zero_()
         if self.cfg.accumulate == 1:
-            fit = self.forward(epoch)
+            fit = self.forward(epoch, mark=mark)
             self.update(fit, epoch)
+            if mark:
+                mark("update")
             return fit
         return self.step_accumulate(epoch)
 

@@ -135,14 +135,19 @@ def make(cfg, ahead, seed=0, pool_size=3000):
     return snn.SnnEs(cfg, W, pool, labels, idx, fused=True, record=True, ahead=ahead)
 
 
-@pytest.mark.parametrize("extra", [dict(), dict(accumulate=2, solver=SGD, lr=0.05),
-                                   dict(n=9, solver=SGD, lr=0.05)])
-def test_snn_steps_drawn_ahead_equal_drawn_inline(hses_gpu, extra):
+@pytest.mark.parametrize("extra,epochs", [
+    (dict(), (0, 1, 2)),
+    (dict(accumulate=2, solver=SGD, lr=0.05), (0, 1, 2)),             # two chunks per step
+    (dict(n=9, solver=SGD, lr=0.05), (0, 1, 2)),
+    (dict(noise_reuse=1, solver=SGD, lr=0.05), (0, 1, 2, 3)),          # fresh noise every epoch
+    (dict(noise_reuse=1), (0, 1, 5, 6, 6)),                           # skipped / repeated epochs
+])
+def test_snn_steps_drawn_ahead_equal_drawn_inline(hses_gpu, extra, epochs):
     cfg = dict(C3_SMALL, **extra)
     es_i = make(snn.SnnConfig(**cfg), ahead=False)
     es_a = make(snn.SnnConfig(**cfg), ahead=True)
     assert es_a.img is not None and es_i.img is None
-    for epoch in range(3):
+    for epoch in epochs:
         f_i = es_i.step(epoch).clone()
         f_a = es_a.step(epoch).clone()
         torch.cuda.synchronize()
