@@ -133,8 +133,11 @@ constexpr double kS3 = -1.0 / 6.0, kS5 = 1.0 / 120.0;
 // (noiser.rs:474); only k1 == 0 is clamped, every other k1 * 2^-24 >= 2^-24.
 HSES_HD float log_arg(uint32_t k1) { return hfmax((float)(int32_t)k1 * 0x1p-24f, 1e-9f); }
 
-// The f32 angle TAU * (k2 * 2^-24) of noiser.rs:475-476.
-HSES_HD float cos_arg(uint32_t k2) { return kTauF * ((float)(int32_t)k2 * 0x1p-24f); }
+// The f32 angle TAU * (k2 * 2^-24) of noiser.rs:475-476, as one multiply:
+// k2 * 2^-24 is exact (k2 < 2^24) and so is TAU * 2^-24, so both forms round
+// the same real product once.
+constexpr float kTauLsb = kTauF * 0x1p-24f;
+HSES_HD float cos_arg(uint32_t k2) { return (float)(int32_t)k2 * kTauLsb; }
 
 // f64 evaluation of log(x) for x = log_arg(k1) (x in [1e-9, 1); any positive
 // normal f32 works).
