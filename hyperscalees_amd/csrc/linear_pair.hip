@@ -210,14 +210,30 @@ __global__ __launch_bounds__(KG_THREADS) void k_pair_gen(const K2Args P) {
     float* rp = P.rec + (size_t)pi * r * rows + j;
     const PairImage im(P.a, P.b, r);
     uint16_t* img = P.bimg + (size_t)pi * im.stride;
-    // input side: element c at bp[c * kp]; output side: at bp[swap23(c)]
+    // input side: element c at bp[c * kp]; output side: at bp[swap23(c)], where
+    // swap23 keeps every aligned run of 4 rank columns contiguous, so an
+    // output-side row stores each batch of 4 normals as one 8-byte write
     uint16_t* bp = sr.in_side ? img + sr.row : img + im.b_elems + (size_t)sr.row * (K2_NMAX + 8);
-    const int32_t cs = sr.in_side ? kp : 0;
     const NoiseCtx ctx{&t, P.log_exc, P.cos_exc};
-    bm_run2(s, r, ctx, [&](int32_t c, float v) {
+    auto one = [&](int32_t c, float v) {
         rp[(size_t)c * rows] = v;
-        bp[cs ? (size_t)c * kp : (size_t)swap23(c)] = f2bf(v * sr.scale);
-    });
+        bp[sr.in_side ? (size_t)c * kp : (size_t)swap23(c)] = f2bf(v * sr.scale);
+    };
+    bm_run2(
+        s, r, ctx,
+        [&](int32_t c0, const float (&v)[4]) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) rp[(size_t)(c0 + q) * rows] = v[q];
+            if (sr.in_side) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) bp[(size_t)(c0 + q) * kp] = f2bf(v[q] * sr.scale);
+            } else {
+                const uint2 w{pack_bf16x2(v[0] * sr.scale, v[1] * sr.scale),
+                              pack_bf16x2(v[2] * sr.scale, v[3] * sr.scale)};
+                *reinterpret_cast<uint2*>(bp + swap23(c0)) = w;
+            }
+        },
+        one);
     if (!sr.in_side) {
         for (int32_t c = r; c < ((r + 31) & ~31); ++c) bp[c] = 0;  // swap23 keeps 16-blocks
         for (int32_t k = P.b + sr.row; k < kp; k += P.a)

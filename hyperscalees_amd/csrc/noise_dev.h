@@ -191,14 +191,16 @@ __device__ __forceinline__ void bm_run(uint64_t& s, int32_t count, const NoiseCt
 // about 5% of a generator's vector instructions; the unrolled body needs about
 // ten more registers, which suits a kernel that only generates).  Stage 1
 // still runs batch after batch in stream order: the same normals.
-template <int G = 4, typename Sink>
-__device__ __forceinline__ void bm_run2(uint64_t& s, int32_t count, const NoiseCtx& c, Sink sink) {
+// batch(at, v) receives each batch's G normals [at, at + G) together (at a
+// multiple of G), sink(i, value) the tail's.
+template <int G = 4, typename Batch, typename Sink>
+__device__ __forceinline__ void bm_run2(uint64_t& s, int32_t count, const NoiseCtx& c, Batch batch,
+                                        Sink sink) {
     int32_t i = 0;
     auto finish = [&](const BmPending<G>& b, int32_t at) {
         float v[G];
         bm_stage2<G>(b, v, c);
-#pragma unroll
-        for (int j = 0; j < G; ++j) sink(at + j, v[j]);
+        batch(at, v);
     };
     if (count >= G) {
         BmPending<G> p, q;
