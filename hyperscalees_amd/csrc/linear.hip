@@ -626,6 +626,26 @@ extern "C" int hses_perturbed_linear_lif_rec(const void* d_x, int32_t x_fmt, int
 // is a separate full-occupancy launch that a caller may put on another
 // stream or issue ahead of the forward.
 
+// The record and operand image of factors drawn ahead, checked from the
+// arguments alone (before the device is touched).
+static int check_drawn(int32_t a, int32_t b, int32_t rank, float sigma, int32_t tid_lo, int32_t n,
+                       const float* d_rec, size_t rec_bytes, const void* d_img, size_t img_bytes,
+                       const char* name) {
+    const int32_t r = (sigma != 0.0f) ? rank : 0;
+    HSES_REQUIRE(a >= 1 && a <= 128,
+                 std::string(name) + ": output width a must be in [1, 128] (the pair kernels)");
+    HSES_REQUIRE(r >= 32 && r % 16 == 0 && r <= 128,
+                 std::string(name) + ": factors drawn ahead need rank a multiple of 16 in "
+                                     "[32, 128] and sigma != 0");
+    HSES_REQUIRE(d_rec, std::string(name) + ": factor record is NULL");
+    HSES_REQUIRE(rec_bytes >= hses_factor_record_bytes(a, b, r, tid_lo, n),
+                 std::string(name) + ": factor record smaller than hses_factor_record_bytes");
+    HSES_REQUIRE(d_img, std::string(name) + ": operand image is NULL");
+    HSES_REQUIRE(img_bytes >= pair_image_bytes(a, b, r, tid_lo, n),
+                 std::string(name) + ": operand image smaller than hses_pair_image_bytes");
+    return HSES_OK;
+}
+
 extern "C" size_t hses_pair_image_bytes(int32_t a, int32_t b, int32_t rank, int32_t tid_lo,
                                         int32_t n) {
     if (a < 1 || b < 1 || rank < 1 || tid_lo < 0 || n < 1) return 0;
@@ -640,16 +660,18 @@ extern "C" int hses_pair_factors(uint64_t key, int32_t rank, float sigma, int32_
     HSES_REQUIRE(noise_reuse >= 0, "noise_reuse must be >= 0");
     HSES_REQUIRE(tid_lo >= 0 && (int64_t)tid_lo + n - 1 <= INT32_MAX, "thread id range");
     if (n == 0) return HSES_OK;
-    HSES_REQUIRE(a <= 128, "hses_pair_factors: output width a must be <= 128 (the pair kernels)");
+    int rc = check_drawn(a, b, rank, sigma, tid_lo, n, d_rec, rec_bytes, d_img, img_bytes,
+                         "hses_pair_factors");
+    if (rc) return rc;
     DeviceState* st;
-    int rc = get_state(&st);
+    rc = get_state(&st);
     if (rc) return rc;
     LinParams P{};
     P.a = a;
     P.b = b;
     P.key = key;
-    P.r = (sigma != 0.0f) ? rank : 0;
-    P.bs = rank > 0 ? sigma / sqrtf((float)rank) : 0.0f;  // eggroll.rs:433
+    P.r = rank;
+    P.bs = sigma / sqrtf((float)rank);  // eggroll.rs:433
     P.epoch = epoch;
     P.nreuse = noise_reuse;
     P.tid_lo = tid_lo;
@@ -658,11 +680,6 @@ extern "C" int hses_pair_factors(uint64_t key, int32_t rank, float sigma, int32_
     P.tables = st->d_tables;
     P.log_exc = st->d_log_exc;
     P.cos_exc = st->d_cos_exc;
-    rc = check_record(P, d_rec, rec_bytes, "hses_pair_factors");
-    if (rc) return rc;
-    HSES_REQUIRE(d_img, "operand image is NULL");
-    HSES_REQUIRE(img_bytes >= pair_image_bytes(a, b, P.r, tid_lo, n),
-                 "hses_pair_factors: operand image smaller than hses_pair_image_bytes");
     P.rec = d_rec;
     return launch_pair_gen(P, st, (hipStream_t)stream, d_img);
 }
@@ -675,16 +692,16 @@ extern "C" int hses_perturbed_linear_pre(const void* d_x, int32_t x_fmt, int64_t
                                          void* d_work, size_t work_bytes, const float* d_rec,
                                          size_t rec_bytes, const uint16_t* d_img,
                                          size_t img_bytes, void* stream) {
+    if (n > 0 && tid_lo >= 0) {
+        const int rc0 = check_drawn(a, b, rank, sigma, tid_lo, n, d_rec, rec_bytes, d_img,
+                                    img_bytes, "hses_perturbed_linear_pre");
+        if (rc0) return rc0;
+    }
     LinParams P;
     DeviceState* st = nullptr;
     int rc = make_params(&P, d_x, x_fmt, x_stride, x_plane, n_time, d_W, a, b, 0, rank, sigma, 0,
                          0, tid_lo, n, rows_per_member, HSES_MATH_BF16, &st);
     if (rc || n == 0) return rc;
-    rc = check_record(P, d_rec, rec_bytes, "hses_perturbed_linear_pre");
-    if (rc) return rc;
-    HSES_REQUIRE(d_img, "operand image is NULL");
-    HSES_REQUIRE(img_bytes >= pair_image_bytes(a, b, P.r, tid_lo, n),
-                 "hses_perturbed_linear_pre: operand image smaller than hses_pair_image_bytes");
     HSES_REQUIRE(d_y, "NULL pointer");
     HSES_REQUIRE(y_stride >= a, "y_stride smaller than a row");
     HSES_REQUIRE(n_time == 1 || y_plane >= (int64_t)n * rows_per_member * y_stride,
@@ -711,8 +728,11 @@ extern "C" int hses_perturbed_linear_lif_pre(const void* d_x, int32_t x_fmt, int
                                              const float* d_rec, size_t rec_bytes,
                                              const uint16_t* d_img, size_t img_bytes,
                                              void* stream) {
-    HSES_REQUIRE(d_rec, "factor record is NULL");
-    HSES_REQUIRE(d_img, "operand image is NULL");
+    if (n > 0 && tid_lo >= 0) {
+        const int rc = check_drawn(a, b, rank, sigma, tid_lo, n, d_rec, rec_bytes, d_img,
+                                   img_bytes, "hses_perturbed_linear_lif_pre");
+        if (rc) return rc;
+    }
     return linear_lif_impl(d_x, x_fmt, x_stride, x_plane, n_time, d_W, a, b, 0, rank, sigma, 0, 0,
                            tid_lo, n, rows_per_member, tau_m, v_th, d_spikes, spk_stride,
                            spk_plane, d_rate, rate_stride, d_work, work_bytes,

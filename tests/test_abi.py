@@ -152,6 +152,36 @@ def test_factor_record_bytes_and_validation():
                     16, 1.0, 0, c(16), c(16), 1 << 20, NULL)
 
 
+def test_pair_image_bytes_and_validation():
+    lib = _lib.load()
+    c = ctypes.c_void_p
+    # per pair: B^T as rank rows of b rounded up to 64, then A as a rows of 136, bf16
+    assert lib.hses_pair_image_bytes(10, 20, 32, 1, 4) == 3 * (32 * 64 + 10 * 136) * 2
+    assert lib.hses_pair_image_bytes(128, 784, 128, 0, 8192) == 4096 * (128 * 832 + 128 * 136) * 2
+    assert lib.hses_pair_image_bytes(10, 20, 32, 0, 0) == 0
+    rec = lib.hses_factor_record_bytes(128, 784, 128, 0, 8)
+    img = lib.hses_pair_image_bytes(128, 784, 128, 0, 8)
+    draw = lambda rank, sigma, a, r_ptr, r_bytes, i_ptr, i_bytes: (
+        _expect_invalid("hses_pair_factors", 7, rank, sigma, 0, 0, 0, 8, a, 784, r_ptr, r_bytes,
+                        i_ptr, i_bytes, NULL))
+    draw(128, 0.02, 128, c(16), rec, c(16), img - 2)    # image too small
+    draw(128, 0.02, 128, c(16), rec, NULL, img)         # no image
+    draw(128, 0.02, 128, c(16), rec - 4, c(16), img)    # record too small
+    draw(128, 0.02, 128, NULL, rec, c(16), img)         # no record
+    draw(8, 0.02, 128, c(16), rec, c(16), img)          # rank below the pair kernels'
+    draw(120, 0.02, 128, c(16), rec, c(16), img)        # rank not a multiple of 16
+    draw(128, 0.0, 128, c(16), rec, c(16), img)         # sigma 0: nothing to draw
+    draw(128, 0.02, 200, c(16), 1 << 30, c(16), 1 << 30)  # output wider than 128
+    # the forwards on drawn factors check the same buffers before anything else
+    M, words = 8 * 64, 13
+    _expect_invalid("hses_perturbed_linear_lif_pre", c(16), 3, words, M * words, 16, c(16), 128,
+                    784, 128, 0.02, 0, 8, 64, 10.0, 1.0, c(16), 2, M * 2, NULL, 0, c(16),
+                    1 << 20, c(16), rec, c(16), img - 2, NULL)
+    _expect_invalid("hses_perturbed_linear_pre", c(16), 0, 784, M * 784, 1, c(16), 128, 784,
+                    128, 0.02, 0, 8, 64, c(16), 128, M * 128, c(16), 1 << 20, c(16), rec - 4,
+                    c(16), img, NULL)
+
+
 def test_empty_inputs_are_no_ops_without_a_gpu():
     lib = _lib.load()
     assert lib.hses_poisson_encode(NULL, 0, NULL, 0, 784, 784, 8, 0, 0, 0, 0, NULL, 0, 784, NULL) == 0
