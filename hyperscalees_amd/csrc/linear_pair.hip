@@ -307,6 +307,13 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// Orders a wave's own LDS accesses (the writes before, the reads after).
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+}
+
 // Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).
 template <int B, int E, typename F>
 __device__ __forceinline__ void static_for(F&& f) {
@@ -895,7 +902,13 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
                     K3_TILE_STORE(1);
                 }
             }
-            lds_barrier();
+            // resident tiles: after a pair's first block each wave reads only the
+            // bit rows it staged itself (thread t stages row t / 2), so waves order
+            // their own LDS accesses and run their blocks out of step
+            if (!resident || first)
+                lds_barrier();
+            else
+                wave_lds_sync();
             if (nkt > 1 && !resident) K3_TILE_LOAD(1);
 
             f32x16 accW[4], accB[4];
@@ -941,8 +954,11 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
                     K3_TILE_STORE((kt & 1) ^ 1);
                     if (kt + 2 < nkt) K3_TILE_LOAD(kt + 2);
                 }
-                // resident tiles: one barrier, before the epilogue restages Xbits
-                if (!resident || kt + 1 == nkt) lds_barrier();
+                // resident tiles: the epilogue restages only this wave's bit rows
+                if (!resident)
+                    lds_barrier();
+                else if (kt + 1 == nkt)
+                    wave_lds_sync();
             }
 
             // sign * xB as bf16: lane l holds rank columns 32j + 8g + 4hl + v of
