@@ -336,17 +336,18 @@ __global__ __launch_bounds__(R_MAXT) void k_es_rows(UpdParams P, RowTiles G) {
             *reinterpret_cast<uint2*>(dst + U_CW + c) = uint2{0, 0};
         }
     };
-    // The record form: values of item (p, ch) of this thread's row into pv,
-    // then (after the MFMAs) into the LDS row as gen4 would have.
-    float pv[U_CW];
+    // The record form: values of item (p, ch) of this thread's row into a
+    // register set, then (iterations later) into the LDS row as gen4 would
+    // have.
+    float pv[U_CW], pw[U_CW];
     const int64_t rstride = (int64_t)P.a + P.b;  // floats between a row's ranks
-    auto load_item = [&](int32_t p, int32_t ch) {
+    auto load_item = [&](float (&pr)[U_CW], int32_t p, int32_t ch) {
         const float* src = P.rec + ((int64_t)(p - P.pair_lo) * r + ch * U_CW) * rstride + srow;
         const int32_t cn = min(U_CW, r - ch * U_CW);
 #pragma unroll
-        for (int c = 0; c < U_CW; ++c) pv[c] = c < cn ? src[c * rstride] : 0.0f;
+        for (int c = 0; c < U_CW; ++c) pr[c] = c < cn ? src[c * rstride] : 0.0f;
     };
-    auto store_item = [&](uint16_t* dst, int32_t cn, float w) {
+    auto store_item = [&](const float (&pv)[U_CW], uint16_t* dst, int32_t cn, float w) {
 #pragma unroll
         for (int c = 0; c < U_CW; c += 4) {
             float x[4];
@@ -364,8 +365,8 @@ __global__ __launch_bounds__(R_MAXT) void k_es_rows(UpdParams P, RowTiles G) {
         const int32_t cn = min(U_CW, r);
         const float w0 = pair_weight(p_begin);
         if constexpr (REC) {
-            load_item(p_begin, 0);
-            store_item(dst, cn, w0);
+            load_item(pv, p_begin, 0);
+            store_item(pv, dst, cn, w0);
         } else {
             start_pair(p_begin);
             for (int32_t c = 0; c < cn; c += 4) gen4(dst, c, min(4, cn - c), w0);
@@ -373,27 +374,16 @@ __global__ __launch_bounds__(R_MAXT) void k_es_rows(UpdParams P, RowTiles G) {
         }
     }
     __syncthreads();
-    for (int32_t u = 0; u < n_items; ++u) {
-        const int32_t p = p_begin + u / chunks, ch = u % chunks;
-        const bool has_next = u + 1 < n_items;
-        const int32_t nch = (ch + 1 == chunks) ? 0 : ch + 1;
-        const int32_t ncn = min(U_CW, r - nch * U_CW);
-        if constexpr (REC) {
-            if (has_next) load_item(nch == 0 ? p + 1 : p, nch);
-        } else {
-            if (has_next && nch == 0) start_pair(p + 1);
-        }
-        const float wn = has_next ? pair_weight(nch == 0 ? p + 1 : p) : 0.0f;
-        const uint16_t* X = buf0 + (u & 1) * bufsz;
-        uint16_t* nxt = buf0 + ((u + 1) & 1) * bufsz + grow * R_HP;
+    // The MFMAs of item u from buffer X: row tile i, then hook(i) (the
+    // generating form draws four normals of the next chunk there: the matrix
+    // cores of one wave overlap the generation of the other waves).
+    auto mfma_item = [&](const uint16_t* X, auto hook) {
         uint4 bh[CT], bl[CT];
 #pragma unroll
         for (int j = 0; j < CT; ++j) {
             bh[j] = *reinterpret_cast<const uint4*>(X + boff[j]);
             bl[j] = *reinterpret_cast<const uint4*>(X + boff[j] + U_CW);
         }
-        // row tile i of the MFMAs, then four normals of the next chunk: the
-        // matrix cores of one wave overlap the generation of the other waves
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             if (i < NRT) {
@@ -406,15 +396,64 @@ __global__ __launch_bounds__(R_MAXT) void k_es_rows(UpdParams P, RowTiles G) {
                     acc[i][j] = mfma_f16(al, bh[j], acc[i][j]);
                 }
             }
-            if constexpr (!REC)
+            hook(i);
+        }
+    };
+    auto item_pc = [&](int32_t v, int32_t* p, int32_t* ch) {
+        *p = p_begin + v / chunks;
+        *ch = v % chunks;
+    };
+    if constexpr (REC) {
+        // Two register sets take turns (the loop unrolled by two, no copies):
+        // item u + 1's values, converted into the LDS after the MFMAs of item
+        // u, were loaded at the end of iteration u - 2, so two iterations of
+        // MFMAs cover the record's load latency.
+        int32_t pl, cl;
+        if (n_items > 1) {
+            item_pc(1, &pl, &cl);
+            load_item(pv, pl, cl);
+        }
+        if (n_items > 2) {
+            item_pc(2, &pl, &cl);
+            load_item(pw, pl, cl);
+        }
+        auto rec_iter = [&](int32_t u, float (&pr)[U_CW]) {
+            const bool has_next = u + 1 < n_items;
+            int32_t pn = 0, chn = 0;
+            if (has_next) item_pc(u + 1, &pn, &chn);
+            const int32_t ncn = min(U_CW, r - chn * U_CW);
+            const float wn = has_next ? pair_weight(pn) : 0.0f;
+            const uint16_t* X = buf0 + (u & 1) * bufsz;
+            uint16_t* nxt = buf0 + ((u + 1) & 1) * bufsz + grow * R_HP;
+            mfma_item(X, [](int) {});
+            if (has_next) store_item(pr, nxt, ncn, wn);
+            if (u + 3 < n_items) {
+                int32_t p3, c3;
+                item_pc(u + 3, &p3, &c3);
+                load_item(pr, p3, c3);
+            }
+            __syncthreads();
+        };
+        for (int32_t u = 0; u < n_items; u += 2) {
+            rec_iter(u, pv);
+            if (u + 1 < n_items) rec_iter(u + 1, pw);
+        }
+    } else {
+        for (int32_t u = 0; u < n_items; ++u) {
+            const int32_t p = p_begin + u / chunks, ch = u % chunks;
+            const bool has_next = u + 1 < n_items;
+            const int32_t nch = (ch + 1 == chunks) ? 0 : ch + 1;
+            const int32_t ncn = min(U_CW, r - nch * U_CW);
+            if (has_next && nch == 0) start_pair(p + 1);
+            const float wn = has_next ? pair_weight(nch == 0 ? p + 1 : p) : 0.0f;
+            const uint16_t* X = buf0 + (u & 1) * bufsz;
+            uint16_t* nxt = buf0 + ((u + 1) & 1) * bufsz + grow * R_HP;
+            mfma_item(X, [&](int i) {
                 if (has_next && 4 * i < ncn) gen4(nxt, 4 * i, min(4, ncn - 4 * i), wn);
-        }
-        if constexpr (REC) {
-            if (has_next) store_item(nxt, ncn, wn);
-        } else {
+            });
             if (has_next && ncn < U_CW) zero_tail(nxt, (ncn + 3) & ~3);
+            __syncthreads();
         }
-        __syncthreads();
     }
 
     // Partial tile -> workspace [s][a][b].
