@@ -298,6 +298,44 @@ __device__ __forceinline__ u16x8 dense_frag(const void* x, int64_t off, bool val
     return v;
 }
 
+// dense_frag's vector path in two parts, so that the loads of a fragment can
+// be issued a step before it is used: the raw 16 or 32 bytes at (off + k0),
+// then their bf16 form, masked when the row is absent (the same values).
+template <int XFMT>
+__device__ __forceinline__ void dense_raw(const void* x, int64_t off, int32_t k0, uint4 (&q)[2]) {
+    if constexpr (XFMT == HSES_FMT_F32) {
+        const uint4* p = reinterpret_cast<const uint4*>(static_cast<const float*>(x) + off + k0);
+        q[0] = p[0];
+        q[1] = p[1];
+    } else {
+        q[0] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + off + k0);
+    }
+}
+
+template <int XFMT>
+__device__ __forceinline__ u16x8 dense_cvt(const uint4 (&q)[2], bool valid) {
+    uint32_t d[4];
+    if constexpr (XFMT == HSES_FMT_F32) {
+        d[0] = pack_bf16x2(__uint_as_float(q[0].x), __uint_as_float(q[0].y));
+        d[1] = pack_bf16x2(__uint_as_float(q[0].z), __uint_as_float(q[0].w));
+        d[2] = pack_bf16x2(__uint_as_float(q[1].x), __uint_as_float(q[1].y));
+        d[3] = pack_bf16x2(__uint_as_float(q[1].z), __uint_as_float(q[1].w));
+    } else {
+        d[0] = q[0].x;
+        d[1] = q[0].y;
+        d[2] = q[0].z;
+        d[3] = q[0].w;
+    }
+    const uint32_t m = valid ? 0xffffffffu : 0u;
+    u16x8 v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        v[2 * e] = (uint16_t)(d[e] & m);
+        v[2 * e + 1] = (uint16_t)((d[e] & m) >> 16);
+    }
+    return v;
+}
+
 // Workgroup barrier that orders LDS accesses only: global loads issued
 // before it stay in flight (a plain __syncthreads also waits for every
 // outstanding global load, which would drain the tile prefetch).
@@ -558,13 +596,26 @@ __global__ __launch_bounds__(K2_THREADS) void k_linear_pair(const K2Args P) {
                                    : 0ull;
                 }
             }
+            // Dense x whose 8-element groups are 16-byte aligned and never
+            // cross b, narrow outputs (one W tile per wave: the registers are
+            // there): each sub-step's fragments are loaded one sub-step ahead
+            // (the barriers below order LDS only, so these loads stay in flight).
+            constexpr bool DENSE_VEC = (XFMT == HSES_FMT_F32 || XFMT == HSES_FMT_BF16) && WJ == 1;
+            const bool xpre = DENSE_VEC && P.x_vec != 0 && b % K2_BK == 0;
+            uint4 xr[4][2];
+            if constexpr (DENSE_VEC) {
+                if (xpre) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) dense_raw<XFMT>(P.x, xoff[i], kg * 8, xr[i]);
+                }
+            }
             // tile 0 -> buffer 0
             uint4 pf[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) pf[q] = reinterpret_cast<const uint4*>(lsrc)[q];
 #pragma unroll
             for (int q = 0; q < 4; ++q) reinterpret_cast<uint4*>(ldst)[q] = mask4(pf[q], lmask);
-            __syncthreads();
+            lds_barrier();
 
             for (int32_t kt = 0; kt < nkt; ++kt) {
                 const int cur = kt & 1;
@@ -582,9 +633,18 @@ __global__ __launch_bounds__(K2_THREADS) void k_linear_pair(const K2Args P) {
                         if constexpr (BITS) {
                             const uint32_t w = Xbits32[(wr * 64 + i * 16 + li) * (2 * nkt) + 2 * kt + s];
                             xa[i] = expand_bits((w >> (8 * kg)) & 0xffu);
+                        } else if (DENSE_VEC && xpre) {
+                            xa[i] = dense_cvt<XFMT>(xr[i], xval[i]);
                         } else {
                             xa[i] = dense_frag<XFMT>(P.x, xoff[i], xval[i], kt * K2_BK + s * 32 + kg * 8, b,
                                                      P.x_vec != 0);
+                        }
+                    }
+                    if constexpr (DENSE_VEC) {
+                        const int32_t k1 = kt * K2_BK + (s + 1) * 32;  // the next sub-step's k
+                        if (xpre && k1 < b) {
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) dense_raw<XFMT>(P.x, xoff[i], k1 + kg * 8, xr[i]);
                         }
                     }
                     // absent columns are staged as zeros: no guards, straight-line MFMAs
@@ -601,7 +661,7 @@ __global__ __launch_bounds__(K2_THREADS) void k_linear_pair(const K2Args P) {
 #pragma unroll
                     for (int q = 0; q < 4; ++q) reinterpret_cast<uint4*>(nb)[q] = mask4(pf[q], lmask);
                 }
-                __syncthreads();
+                lds_barrier();
             }
 
             // xB -> LDS as bf16 [row][c], sign of the row's member applied
