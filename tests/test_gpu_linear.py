@@ -165,6 +165,8 @@ def ref_forward_bf16(x3, W, A, B, rpm):
     (2, 40, 3, 96, 200, 64, 0, FMT_BF16),      # rows not a multiple of the block
     (5, 7, 2, 33, 50, 16, 2, FMT_F32),
     (3, 20, 2, 16, 96, 32, 1, FMT_BF16),       # a = 16: one W column tile per wave
+    (3, 20, 2, 16, 128, 32, 1, FMT_BF16),      # a = 16, b % 64 == 0: x loaded a sub-step ahead
+    (5, 7, 2, 12, 256, 16, 2, FMT_F32),        # same, four K tiles, rows not a multiple of the block
 ])
 def test_perturbed_linear_pair_kernel(hses_gpu, n, rpm, T, a, b, r, tid_lo, fmt):
     rng = np.random.default_rng(n * 1000 + a + r)

@@ -110,6 +110,7 @@ def test_bits_currents_pre_equal_rec(hses_gpu, a, b, r, n, tid_lo, T):
     (10, 128, 128, 6, 0),     # C3 readout on rates (pairs in groups of 12)
     (40, 96, 32, 7, 2),       # several pairs per group, four W column tiles
     (10, 128, 128, 27, 1),    # a group split over the grid, odd ends
+    (12, 256, 32, 5, 1),      # four K tiles of fp32 x loaded a sub-step ahead
 ])
 def test_dense_pre_equals_rec(hses_gpu, a, b, r, n, tid_lo):
     rng = np.random.default_rng(a * b + n)
