@@ -1037,19 +1037,7 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
                         xbf[j][g][1] = pack_bf16x2(accB[j][4 * g + 2], accB[j][4 * g + 3]) ^ sgn;
                     }
             }
-            // The next block's operands land during the epilogue: its bit rows
-            // (the next pair's first block after a pair's last one) and, inside
-            // a pair, its first W/B tile.
-            // (Issued without branches: the last block of the last pair reloads
-            // its own rows and tile, which are then not stored.)
             const bool next_pair = !has_next && more_pairs;
-            {
-                int64_t nlo = L0, nhi = row_hi;
-                if (has_next) nlo = L0 + K3_RB;
-                else if (next_pair) pair_rows(pi + (int32_t)gridDim.x, &nlo, &nhi);
-                xbits_load(nlo, nhi, xpf);
-                if (!resident) K3_TILE_LOAD(0);
-            }
             // accW += (sign xB) A^T over K = r in steps of 16: step (j, t) gives
             // k-group hl the rank columns 32j + 16t + 4hl + {0..3, 8..11}, stored
             // (swap23) as the 8 columns 32j + 16t + 8hl.
@@ -1079,6 +1067,21 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
                         accW[jo] = mfma32_bf16(xo, __builtin_bit_cast(u16x8, af[t][jo]), accW[jo]);
                 }
                 __builtin_amdgcn_sched_barrier(0);
+            }
+
+            // The next block's operands land during the LIF and the stores: its
+            // bit rows (the next pair's first block after a pair's last one) and,
+            // inside a pair, its first W/B tile.  Issued after the second
+            // product: issued before it, the wave stalled there for about as
+            // long as the product takes (fc1 GEMM 3.55 -> 3.50 ms).
+            // (Issued without branches: the last block of the last pair reloads
+            // its own rows and tile, which are then not stored.)
+            {
+                int64_t nlo = L0, nhi = row_hi;
+                if (has_next) nlo = L0 + K3_RB;
+                else if (next_pair) pair_rows(pi + (int32_t)gridDim.x, &nlo, &nhi);
+                xbits_load(nlo, nhi, xpf);
+                if (!resident) K3_TILE_LOAD(0);
             }
 
             // accW[jo][4g + v]: wave row 16 hl + 4g + v, column 32 jo + lc
