@@ -32,9 +32,11 @@ PEAK_FP32_TFLOPS = 157.3      # MI355X dense fp32 MFMA
 PEAK_HBM_GBPS = 8000.0
 # HBM bytes per launch of fc1's GEMM on factors drawn ahead, from two rocprofv3 PMC runs
 # (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0, factors from a 1 GiB copy in the same process) of
-# `python3 -m hyperscalees_amd.profile_fc1`: 4.126 GB x 2 + 0.134 GB; see
-# profiles/fc1_c3_traffic.md.  Refreshed whenever the kernel changes.
-FC1_TRAFFIC_BYTES = 8.39e9
+# `python3 -m hyperscalees_amd.profile_fc1`: 4.067 GB x 2 + 0.134 GB, measured on the kernel
+# source of commit 8b404b2; see profiles/fc1_c3_traffic.md.  Refreshed whenever the kernel
+# changes; the bench line names the source it was measured on.
+FC1_TRAFFIC_BYTES = 8.27e9
+FC1_TRAFFIC_SOURCE = "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of profile_fc1 on commit 8b404b2"
 
 
 def layer_flops(cfg, l):
@@ -186,8 +188,9 @@ def bench_c5(args):
                    "parallelism": "single GPU"},
         "phase_ms": {"forward": round(t_fwd, 3), "es_update": round(t_upd, 3)},
         "fwd_tflops": round(rwkv_lm.forward_flops(cfg) / (t_fwd * 1e-3) / 1e12, 1),
-        "roofline": {"kernel": ("k_linear_wide<BF16 x, RELU_SQ, bf16 y> (ChannelMixing key, "
-                                "262144 x 512 -> 2048)"),
+        "roofline": {"kernel": ("k_gemm_bf16<BF16 x, rank 1, relu^2, bf16 y> with its W->bf16 "
+                                "conversion and factor draw (ChannelMixing key, 262144 x 512 -> "
+                                "2048)"),
                      "bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": None, "launch_ms": round(lk_ms, 3),
@@ -665,6 +668,7 @@ def main():
                      "bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": (FC1_TRAFFIC_BYTES if es.ahead else None),
+                     "traffic_source": (FC1_TRAFFIC_SOURCE if es.ahead else None),
                      "launch_ms": round(fc1_ms, 3),
                      "algorithmic_flop_per_launch": fc1_flops},
     }

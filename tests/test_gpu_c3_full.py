@@ -16,8 +16,9 @@ input spikes, so a single spike flip does not cascade into later layers:
   reference spikes (the bf16-path bar);
 * readout: member fitness from the GPU's own rates within rel 2e-2 of the fp32
   oracle, and the whole member forward (or_snn_forward_member) within rel 5e-2;
-* ES update: the readout layer's gradient at N = 8192 against the oracle's
-  double-accumulated gradient, rel 1e-5.
+* ES update: every layer's gradient at N = 8192 (the hidden layers' from the
+  factor record the forward's draws wrote, the readout's generated) against the
+  oracle's double-accumulated gradient, rel 1e-5.
 """
 import numpy as np
 import pytest
@@ -69,6 +70,7 @@ def c3_run(hses_gpu):
     W = snn.init_weights(cfg.dims, 0, gain=snn.ACTIVE_GAIN)
     es = snn.SnnEs(cfg, W, pool, labels, idx)
     assert es.fused, "the full-size C3 step runs the fused forward + LIF kernel"
+    assert es.record and es.ahead, "the full-size C3 step draws factors ahead into the record"
     fit = es.forward(0)
     torch.cuda.synchronize()
     R = cfg.rows
@@ -79,9 +81,9 @@ def c3_run(hses_gpu):
     fit_gpu = fit.cpu().numpy().copy()
     es.update(fit, 0)
     torch.cuda.synchronize()
-    g_read = es.grads[-1].cpu().numpy()
+    grads = [g.cpu().numpy() for g in es.grads]
     return dict(cfg=cfg, pool=pool, labels=labels, idx=idx, W=W, spk=spk, rate=rate,
-                fit=fit_gpu, g_read=g_read)
+                fit=fit_gpu, grads=grads)
 
 
 def test_c3_full_input_spikes_bit_exact(c3_run):
@@ -164,12 +166,18 @@ def test_c3_full_member_forward_end_to_end(c3_run):
     print(f"end-to-end member fitness: worst rel difference {worst:.2e}")
 
 
-def test_c3_full_readout_gradient(c3_run):
-    # the fc4 ES gradient over all 8192 members against the double-accumulated
-    # oracle on the same (z-scored) fitness
+@pytest.mark.parametrize("layer", [0, 1, 2, 3])
+def test_c3_full_layer_gradient(c3_run, layer):
+    # each layer's ES gradient over all 8192 members (fc1 from 4096 pairs in 512
+    # split-K slices, the operand scale taken from max|f| over the whole
+    # population) against the double-accumulated oracle on the same z-scored
+    # fitness
     cfg = c3_run["cfg"]
     z, _, _ = O.convert_fitnesses(c3_run["fit"])
-    a, b = cfg.dims[-1], cfg.dims[-2]
-    g = O.lora_grad_f64(cfg.sigma, cfg.keys[-1], cfg.rank, 0, z, a, b, nthreads=16)
-    err = np.abs(c3_run["g_read"] - g).max()
-    assert err <= 1e-5 * np.abs(g).max(), f"readout gradient err {err:.3e} of {np.abs(g).max():.3e}"
+    a, b = cfg.dims[layer + 1], cfg.dims[layer]
+    g = O.lora_grad_f64(cfg.sigma, cfg.keys[layer], cfg.rank, 0, z, a, b, nthreads=16)
+    got = c3_run["grads"][layer]
+    assert got.shape == g.shape
+    err = np.abs(got - g).max()
+    print(f"layer {layer}: gradient max err {err:.3e} of max {np.abs(g).max():.3e}")
+    assert err <= 1e-5 * np.abs(g).max(), f"layer {layer} gradient err {err:.3e}"

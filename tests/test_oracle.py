@@ -484,3 +484,149 @@ def test_clip_global_norm_hand_computed(oracle):
     g = np.random.default_rng(5).standard_normal(1000)
     assert O.clip_scale([g[:300], g[300:]], 1.0) == pytest.approx(1.0 / np.linalg.norm(g),
                                                                    rel=1e-6)
+
+
+# ---- the ES gradient checker (eggroll.rs:353-404) -----------------------------
+
+def test_lora_grad_f64_is_scaled_einsum(oracle):
+    # or_lora_grad_f64 = -(sqrt(N)/N) * sum_i f_i A_i B_i^T over tids 0..N-1
+    # (simple_lora_update's sum, eggroll.rs:353-404, with the SGD scale -g*sqrt(N)),
+    # split over threads; must equal the pinned single-thread einsum for any split.
+    rng = np.random.default_rng(11)
+    for n, a, b, r in ((2, 3, 4, 1), (7, 5, 3, 2), (16, 6, 9, 4)):
+        fit = rng.standard_normal(n).astype(np.float32)
+        sigma, key = 0.4, 0x1234567 + n
+        bs = oracle.or_base_sigma(sigma, r)
+        ein = np.zeros((a, b), np.float64)
+        oracle.or_lora_einsum_f64(bs, key, r, 0, 3, fit, np.arange(n, dtype=np.int32), n, a, b,
+                                  ein)
+        want = (ein * (-math.sqrt(n) / n)).astype(np.float32)
+        for nt in (1, 3, 8):
+            g = O.lora_grad_f64(sigma, key, r, 3, fit, a, b, nthreads=nt)
+            np.testing.assert_allclose(g, want, rtol=1e-6, atol=1e-9)
+
+
+def test_lora_grad_f64_hand_computed_pair(oracle):
+    # N = 2, r = 1: members 0 and 1 share B and have A_1 = -A_0 (antithetic pair,
+    # eggroll.rs:60-65), so g = -(sqrt(2)/2) * (f_0 - f_1) * A_0 B_0^T.
+    sigma, key, a, b = 0.5, 99, 2, 3
+    A, B = O.lora_factors(oracle.or_base_sigma(sigma, 1), key, 1, 0, [0], a, b)
+    f0, f1 = 1.25, -0.5
+    g = O.lora_grad_f64(sigma, key, 1, 0, np.array([f0, f1], np.float32), a, b, nthreads=2)
+    outer = [[float(A[0, p, 0]) * float(B[0, q, 0]) for q in range(b)] for p in range(a)]
+    want = np.array([[-(math.sqrt(2) / 2) * (f0 - f1) * v for v in row] for row in outer])
+    np.testing.assert_allclose(g, want, rtol=1e-6)
+    # a fitness shared by both members cancels exactly
+    g0 = O.lora_grad_f64(sigma, key, 1, 0, np.array([0.7, 0.7], np.float32), a, b)
+    assert np.all(g0 == 0.0)
+
+
+# ---- whole SNN member forward (snn.rs:253-282, snn_mnist.rs:180-201) ---------
+
+def _snn_cfg(dims, T, rows, sigma, rank, tau_m=10.0, v_th=1.0, seeds=(1, 2, 3, 4), epoch=0):
+    c = O.SnnCfg()
+    d = np.array(dims, np.int32)
+    c.n_layers = len(dims) - 1
+    c.dims = d.ctypes.data_as(ctypes.POINTER(O.c_i32))
+    c.T, c.rows, c.tau_m, c.v_th, c.sigma = T, rows, tau_m, v_th, sigma
+    c.rank, c.noise_reuse, c.epoch = rank, 0, epoch
+    for i in range(4):
+        c.poisson_seed[i] = seeds[i]
+    return c, d
+
+
+def _snn_member_oracle(oracle, c, W, keys, probs_m, labels_m, m):
+    Ws = [np.ascontiguousarray(w, np.float32) for w in W]
+    Wp = (ctypes.c_void_p * len(Ws))(*[w.ctypes.data for w in Ws])
+    kk = (O.c_u64 * len(keys))(*keys)
+    out = np.zeros(1, np.float32)
+    oracle.or_snn_forward_member(ctypes.byref(c), Wp, kk, np.ascontiguousarray(probs_m, np.float32),
+                                 np.ascontiguousarray(labels_m, np.int32), m, out)
+    return float(out[0])
+
+
+def _snn_member_composed(dims, T, rows, sigma, rank, tau_m, v_th, seeds, W, keys, probs_m,
+                         labels_m, m, bs):
+    # The member's Poisson streams use the global (row, col) index: encode the
+    # m+1 members' rows with this member's rows last and keep those.
+    pad = np.zeros(((m + 1) * rows, dims[0]), np.float32)
+    pad[m * rows:] = probs_m
+    x = O.poisson(pad, T, seeds)[:, m * rows:]                 # (T, R, in)
+    hidden = []
+    for l in range(len(dims) - 2):
+        a, b = dims[l + 1], dims[l]
+        A, B = O.lora_factors(bs, keys[l], rank, 0, [m], a, b)
+        cur = O.do_mm(x.reshape(T * rows, b), W[l], A[0], B[0]).reshape(T, rows, a)
+        x, _ = O.lif(cur, tau_m, v_th)
+        hidden.append(x)
+    rate = x.sum(axis=0, dtype=np.float32) / np.float32(T)      # T a power of two: exact
+    a, b = dims[-1], dims[-2]
+    A, B = O.lora_factors(bs, keys[-1], rank, 0, [m], a, b)
+    logits = O.do_mm(rate, W[-1], A[0], B[0])
+    ll = O.loglik(logits, labels_m).astype(np.float64)
+    return float(np.float32(ll.sum() / rows)), hidden
+
+
+def test_snn_forward_member_is_composition_of_pinned_pieces(oracle):
+    dims, T, rows, sigma, rank = (12, 6, 5, 3), 8, 3, 0.3, 2
+    seeds = (5, 6, 7, 8)
+    rng = np.random.default_rng(4)
+    W = [rng.standard_normal((dims[l + 1], dims[l])).astype(np.float32) * g
+         for l, g in zip(range(3), (4.0, 6.0, 1.0))]
+    keys = [(i + 1) * 0x9E3779B97F4A7C15 & M64 for i in range(3)]
+    c, _d = _snn_cfg(dims, T, rows, sigma, rank, seeds=seeds)
+    bs = oracle.or_base_sigma(sigma, rank)
+    fits = []
+    for m in (0, 1, 6):
+        probs = rng.random((rows, dims[0])).astype(np.float32)
+        probs[rng.random(probs.shape) < 0.3] = 0.0
+        labels = rng.integers(0, dims[-1], rows).astype(np.int32)
+        got = _snn_member_oracle(oracle, c, W, keys, probs, labels, m)
+        want, hidden = _snn_member_composed(dims, T, rows, sigma, rank, 10.0, 1.0, seeds, W, keys,
+                                            probs, labels, m, bs)
+        assert got == want, (m, got, want)
+        # every hidden layer fires, so each piece of the wiring reaches the fitness
+        assert all(h.sum() > 0 for h in hidden), m
+        # the member index reaches the factors and the Poisson streams: member
+        # m+1's composition on the same rows gives another fitness
+        other, _ = _snn_member_composed(dims, T, rows, sigma, rank, 10.0, 1.0, seeds, W, keys,
+                                        probs, labels, m + 1, bs)
+        assert other != got
+        fits.append(got)
+    assert all(abs(f + math.log(3.0)) > 1e-3 for f in fits)  # not the silent-readout value
+
+
+def test_snn_forward_members_equals_per_member(oracle):
+    # or_snn_forward_members indexes member m's rows and labels and keeps the
+    # global Poisson index, for any thread count.
+    dims, T, rows, sigma, rank, n = (10, 7, 4), 4, 2, 0.2, 3, 6
+    rng = np.random.default_rng(8)
+    W = [rng.standard_normal((dims[l + 1], dims[l])).astype(np.float32) * 4.0 for l in range(2)]
+    keys = [11, 22]
+    c, _d = _snn_cfg(dims, T, rows, sigma, rank)
+    probs = rng.random((n * rows, dims[0])).astype(np.float32)
+    labels = rng.integers(0, dims[-1], n * rows).astype(np.int32)
+    per = [_snn_member_oracle(oracle, c, W, keys, probs[m * rows:(m + 1) * rows],
+                              labels[m * rows:(m + 1) * rows], m) for m in range(n)]
+    assert len(set(per)) == n  # the hidden layer fires: members differ
+    Ws = [np.ascontiguousarray(w) for w in W]
+    Wp = (ctypes.c_void_p * 2)(*[w.ctypes.data for w in Ws])
+    kk = (O.c_u64 * 2)(*keys)
+    for nt in (1, 4):
+        fit = np.zeros(n - 1, np.float32)
+        oracle.or_snn_forward_members(ctypes.byref(c), Wp, kk, probs, labels, 1, n, nt, fit)
+        np.testing.assert_array_equal(fit, np.array(per[1:], np.float32))
+
+
+def test_snn_forward_member_silent_model_closed_form(oracle):
+    # Hidden weights 0 and sigma 0: no current, no spike, rates 0, logits 0 for
+    # any readout weights, so every row's log-likelihood is -ln(classes).
+    dims, T, rows = (9, 5, 4, 10), 8, 3
+    rng = np.random.default_rng(1)
+    W = [np.zeros((5, 9), np.float32), np.zeros((4, 5), np.float32),
+         rng.standard_normal((10, 4)).astype(np.float32)]
+    c, _d = _snn_cfg(dims, T, rows, 0.0, 2)
+    probs = rng.random((rows, 9)).astype(np.float32)
+    labels = np.array([0, 3, 9], np.int32)
+    got = _snn_member_oracle(oracle, c, W, [1, 2, 3], probs, labels, 2)
+    assert got == pytest.approx(-math.log(10.0), rel=1e-6)
