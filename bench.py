@@ -600,12 +600,13 @@ def main():
         if es.ahead:
             K.perturbed_linear_lif(es.spk[0], es.W[0], cfg.keys[0], cfg.rank, cfg.sigma, 0,
                                    cfg.noise_reuse, 0, cfg.n, cfg.rows, cfg.T, cfg.tau_m,
-                                   cfg.v_th, spikes=es.spk[1], rec=es.rec[0], img=es.img[0])
+                                   cfg.v_th, spikes=es.spk[1], rec=es.rec[0], img=es.img[0],
+                                   time_inner=es.time_inner)
         elif es.fused:
             K.perturbed_linear_lif(es.spk[0], es.W[0], cfg.keys[0], cfg.rank, cfg.sigma, s,
                                    cfg.noise_reuse, 0, cfg.n, cfg.rows, cfg.T, cfg.tau_m,
                                    cfg.v_th, spikes=es.spk[1],
-                                   rec=es.rec[0] if es.rec else None)
+                                   rec=es.rec[0] if es.rec else None, time_inner=es.time_inner)
         else:
             K.perturbed_linear(es.spk[0], es.W[0], cfg.keys[0], cfg.rank, cfg.sigma, s,
                                cfg.noise_reuse, 0, cfg.n, cfg.rows, x_fmt=K.FMT_BITS,

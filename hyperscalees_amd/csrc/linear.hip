@@ -267,8 +267,8 @@ static int make_params(LinParams* P, const void* d_x, int32_t x_fmt, int64_t x_s
     HSES_REQUIRE(d_x && d_W, "NULL pointer");
     const int64_t units = x_fmt == HSES_FMT_BITS ? (b + 63) / 64 : b;
     const int64_t M = (int64_t)n * rows_per_member;
-    HSES_REQUIRE(x_stride >= units, "x_stride smaller than a row");
-    HSES_REQUIRE(n_time == 1 || x_plane >= M * x_stride, "time planes overlap");
+    HSES_REQUIRE(rows_layout_ok(units, M, n_time, x_stride, x_plane),
+                 "x rows overlap (x_stride smaller than a row, or time planes overlap)");
     HSES_REQUIRE(M * n_time < (1ll << 40), "too many rows");
     int rc = get_state(st);
     if (rc) return rc;
@@ -407,8 +407,8 @@ static int run_linear(LinParams& P, DeviceState* st, float* d_y, int64_t y_strid
                       int64_t y_plane, void* d_work, size_t work_bytes, void* stream,
                       const char* name, int32_t act = ACT_NONE, int32_t y_fmt = HSES_FMT_F32) {
     HSES_REQUIRE(d_y, "NULL pointer");
-    HSES_REQUIRE(y_stride >= P.a, "y_stride smaller than a row");
-    HSES_REQUIRE(P.n_time == 1 || y_plane >= (int64_t)P.n * P.rpm * y_stride, "time planes overlap");
+    HSES_REQUIRE(rows_layout_ok(P.a, (int64_t)P.n * P.rpm, P.n_time, y_stride, y_plane),
+                 "y rows overlap (y_stride smaller than a row, or time planes overlap)");
     HSES_REQUIRE(act >= ACT_NONE && act <= ACT_RELU_SQ, "unknown activation");
     P.y = d_y;
     P.y_stride = y_stride;
@@ -529,9 +529,8 @@ extern "C" int hses_perturbed_linear_rec(const void* d_x, int32_t x_fmt, int64_t
     rc = check_record(P, d_rec, rec_bytes, "hses_perturbed_linear_rec");
     if (rc) return rc;
     HSES_REQUIRE(d_y, "NULL pointer");
-    HSES_REQUIRE(y_stride >= a, "y_stride smaller than a row");
-    HSES_REQUIRE(n_time == 1 || y_plane >= (int64_t)n * rows_per_member * y_stride,
-                 "time planes overlap");
+    HSES_REQUIRE(rows_layout_ok(a, (int64_t)n * rows_per_member, n_time, y_stride, y_plane),
+                 "y rows overlap (y_stride smaller than a row, or time planes overlap)");
     P.y = d_y;
     P.y_stride = y_stride;
     P.y_plane = y_plane;
@@ -570,8 +569,8 @@ static int linear_lif_impl(const void* d_x, int32_t x_fmt, int64_t x_stride, int
     }
     HSES_REQUIRE(d_spikes || d_rate, "spikes and rate are both NULL");
     const int64_t M = (int64_t)n * rows_per_member;
-    HSES_REQUIRE(!d_spikes || spk_stride >= (a + 63) / 64, "spk_stride smaller than a row");
-    HSES_REQUIRE(!d_spikes || n_time == 1 || spk_plane >= M * spk_stride, "time planes overlap");
+    HSES_REQUIRE(!d_spikes || rows_layout_ok((a + 63) / 64, M, n_time, spk_stride, spk_plane),
+                 "spike rows overlap (spk_stride smaller than a row, or time planes overlap)");
     HSES_REQUIRE(!d_rate || rate_stride >= a, "rate_stride smaller than a row");
     HSES_REQUIRE(P.r > 0, "the fused kernel needs rank > 0 and sigma != 0");
     HSES_REQUIRE(n_time <= 64 && (n_time & (n_time - 1)) == 0, "n_time must be a power of two <= 64");
@@ -703,9 +702,8 @@ extern "C" int hses_perturbed_linear_pre(const void* d_x, int32_t x_fmt, int64_t
                          0, tid_lo, n, rows_per_member, HSES_MATH_BF16, &st);
     if (rc || n == 0) return rc;
     HSES_REQUIRE(d_y, "NULL pointer");
-    HSES_REQUIRE(y_stride >= a, "y_stride smaller than a row");
-    HSES_REQUIRE(n_time == 1 || y_plane >= (int64_t)n * rows_per_member * y_stride,
-                 "time planes overlap");
+    HSES_REQUIRE(rows_layout_ok(a, (int64_t)n * rows_per_member, n_time, y_stride, y_plane),
+                 "y rows overlap (y_stride smaller than a row, or time planes overlap)");
     P.y = d_y;
     P.y_stride = y_stride;
     P.y_plane = y_plane;

@@ -6,6 +6,7 @@
 #include "../../include/hses.h"
 #include "bm_exact.h"
 #include "mfma.h"
+#include "spike_fmt.h"
 
 namespace hses {
 

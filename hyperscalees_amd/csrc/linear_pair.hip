@@ -973,53 +973,71 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
 
             f32x16 accW[4], accB[4];
             const uint32_t* xw = Xbits32 + (wrow0 + xrow) * (2 * nkt);
-            // One K tile: four k-steps of 16 (this lane's 8 k at 16ks + 8hl),
-            // each one x expansion and 8 MFMAs whose eight operand reads are
-            // issued first (the scheduler would otherwise issue each read just
-            // before its MFMA).  ZERO: the block's first tile, whose first step
-            // starts from the zero operand instead of clearing 128 accumulator
-            // registers (8.6% of the K loop's cycles at b = 784).
-            auto k_tile = [&](int32_t kt, auto zc) {
-                constexpr bool ZERO = decltype(zc)::value;
-                const uint16_t* tb = WB + (kt & 1) * (K2_COLS * K2_TP) + lc * K2_TP + hl * 8;
-                const uint32_t w2[2] = {xw[2 * kt], xw[2 * kt + 1]};
-                static_for<0, 4>([&](auto kc) {
-                    constexpr int ks = decltype(kc)::value;
-                    constexpr bool z = ZERO && ks == 0;
-                    u16x8 fr[8];
-#pragma unroll
-                    for (int j = 0; j < 8; ++j)
-                        fr[j] = lds_u16x8(tb + ((j < 4 ? 0 : K2_NMAX) + 32 * (j & 3)) * K2_TP + 16 * ks);
-                    const u16x8 xa = expand_bits((w2[ks >> 1] >> (8 * ((ks & 1) * 2 + hl))) & 0xffu);
-                    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) accW[j] = mfma32_bf16(xa, fr[j], z ? f32x16{} : accW[j]);
-#pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        accB[j] = mfma32_bf16(fr[4 + j], xa, z ? f32x16{} : accB[j]);
-                    __builtin_amdgcn_sched_barrier(0);
-                });
+            // The K loop.  A K tile is four k-steps of 16 (this lane's 8 k at
+            // 16 ks + 8 hl), each an x expansion and 8 MFMAs on 8 operand
+            // fragments.  The fragment reads are rolled: right after the MFMA
+            // that consumes fragment j of a step, fragment j of the next step is
+            // read into the same registers, so each read has the following seven
+            // MFMAs to land.  Across a tile boundary (non-resident tiles) the
+            // barrier that publishes the next tile comes before the tile's last
+            // step, whose MFMAs then cover the next tile's first reads.  ZERO:
+            // the block's first tile, whose first step starts from the zero
+            // operand instead of clearing 128 accumulator registers.
+            u16x8 fr[8];
+            auto frag_ptr = [&](int32_t kt, int ks) {
+                return WB + (kt & 1) * (K2_COLS * K2_TP) + lc * K2_TP + hl * 8 + 16 * ks;
             };
-            // tile kt sits in LDS buffer kt & 1; the next one is staged from
-            // registers after it (unless the tiles are resident)
-            k_tile(0, std::true_type{});
-            if (nkt > 1 && !resident) {
-                K3_TILE_STORE(1);
-                if (nkt > 2) K3_TILE_LOAD(2);
+            auto frag_off = [](int j) { return ((j < 4 ? 0 : K2_NMAX) + 32 * (j & 3)) * K2_TP; };
+            {
+                const uint16_t* tb = frag_ptr(0, 0);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) fr[j] = lds_u16x8(tb + frag_off(j));
             }
-            if (!resident || nkt == 1) lds_barrier();
-            for (int32_t kt = 1; kt < nkt; ++kt) {
-                k_tile(kt, std::false_type{});
-                if (kt + 1 < nkt && !resident) {
-                    K3_TILE_STORE((kt & 1) ^ 1);
+            uint32_t xw0 = xw[0], xw1 = xw[1];
+            // One step: its 8 MFMAs, each followed by the read of the same
+            // fragment of the step at `nxt`.
+            auto step = [&](uint32_t w, auto kc, auto zc, const uint16_t* nxt) {
+                constexpr int ks = decltype(kc)::value;
+                constexpr bool z = decltype(zc)::value;
+                const u16x8 xa = expand_bits((w >> (8 * ((ks & 1) * 2 + hl))) & 0xffu);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    if (j < 4)
+                        accW[j] = mfma32_bf16(xa, fr[j], z ? f32x16{} : accW[j]);
+                    else
+                        accB[j - 4] = mfma32_bf16(fr[j], xa, z ? f32x16{} : accB[j - 4]);
+                    fr[j] = lds_u16x8(nxt + frag_off(j));
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            };
+            // Tile kt sits in LDS buffer kt & 1; the next one is staged from
+            // registers into the other buffer during this one (unless the tiles
+            // are resident).  The last tile's last step re-reads its own first
+            // fragments (no branch around the reads; the values are unused).
+            auto tile = [&](int32_t kt, auto zc) {
+                const bool more = kt + 1 < nkt;
+                const int32_t kn = more ? kt + 1 : kt;
+                const uint32_t w0 = xw0, w1 = xw1;
+                step(w0, std::integral_constant<int, 0>{}, zc, frag_ptr(kt, 1));
+                step(w0, std::integral_constant<int, 1>{}, std::false_type{}, frag_ptr(kt, 2));
+                if (more && !resident) {
+                    K3_TILE_STORE((kt + 1) & 1);
                     if (kt + 2 < nkt) K3_TILE_LOAD(kt + 2);
                 }
-                // resident tiles: the epilogue restages only this wave's bit rows
-                if (!resident)
-                    lds_barrier();
-                else if (kt + 1 == nkt)
-                    wave_lds_sync();
-            }
+                step(w1, std::integral_constant<int, 2>{}, std::false_type{}, frag_ptr(kt, 3));
+                if (more && !resident) lds_barrier();
+                xw0 = xw[2 * kn];
+                xw1 = xw[2 * kn + 1];
+                step(w1, std::integral_constant<int, 3>{}, std::false_type{}, frag_ptr(kn, 0));
+            };
+            tile(0, std::true_type{});
+            for (int32_t kt = 1; kt < nkt; ++kt) tile(kt, std::false_type{});
+            // resident tiles: the epilogue restages only this wave's bit rows
+            if (!resident || nkt == 1)
+                lds_barrier();
+            else
+                wave_lds_sync();
 
             // sign * xB as bf16: lane l holds rank columns 32j + 8g + 4hl + v of
             // the row at MFMA position lc (the row its x operand came from).

@@ -7,6 +7,15 @@
 
 namespace hses {
 
+// Rows of `units` elements at row * stride + t * plane (row < M, t < n_time)
+// do not overlap: time-major (planes of M rows, plane >= M * stride) or
+// time-inner (each row's n_time entries adjacent, stride >= n_time * plane).
+inline bool rows_layout_ok(int64_t units, int64_t M, int32_t n_time, int64_t stride,
+                           int64_t plane) {
+    if (n_time <= 1) return stride >= units;
+    return (stride >= units && plane >= M * stride) || (plane >= units && stride >= n_time * plane);
+}
+
 // Row length, in storage units, of a row of `width` spikes.
 inline int64_t fmt_row_units(int32_t fmt, int64_t width) {
     return fmt == HSES_FMT_BITS ? (width + 63) / 64 : width;

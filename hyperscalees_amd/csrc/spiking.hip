@@ -30,7 +30,7 @@ __global__ __launch_bounds__(256) void k_poisson(const float* __restrict__ p, in
                                                  const int32_t* __restrict__ prow, int64_t rows,
                                                  int32_t in_dim, int64_t p_stride, int32_t T,
                                                  uint32_t mix, void* __restrict__ out,
-                                                 int64_t out_stride) {
+                                                 int64_t out_stride, int64_t plane) {
     const int32_t words = (in_dim + 63) >> 6;
     const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
     const int32_t lane = threadIdx.x & 63;
@@ -46,7 +46,6 @@ __global__ __launch_bounds__(256) void k_poisson(const float* __restrict__ p, in
         const uint32_t idx = (uint32_t)(row * in_dim + col);
         x = 1000000007u * idx + mix + 0x9E3779B9u;
     }
-    const int64_t plane = rows * out_stride;
     for (int32_t t = 0; t < T; ++t) {
         x ^= x << 13;
         x ^= x >> 17;
@@ -69,7 +68,7 @@ template <int TT>
 __global__ __launch_bounds__(64 * P_ROWS_PER_BLOCK) void k_poisson_bits(
     const float* __restrict__ p, int64_t p_rows, const int32_t* __restrict__ prow, int64_t rows,
     int32_t in_dim, int64_t p_stride, int32_t T_rt, uint32_t mix, uint64_t* __restrict__ out,
-    int64_t out_stride) {
+    int64_t out_stride, int64_t plane) {
     const int32_t T = TT ? TT : T_rt;
     const int64_t row = (int64_t)blockIdx.x * P_ROWS_PER_BLOCK + (threadIdx.x >> 6);
     const int32_t lane = threadIdx.x & 63;
@@ -79,7 +78,6 @@ __global__ __launch_bounds__(64 * P_ROWS_PER_BLOCK) void k_poisson_bits(
     const bool src_ok = src >= 0 && src < p_rows;
     const float* prow_p = p + (src_ok ? src : 0) * p_stride;
     const uint32_t idx0 = (uint32_t)(row * in_dim);  // flat index of the row's first element
-    const int64_t plane = rows * out_stride;
     uint64_t* orow = out + row * out_stride + (int64_t)lane * plane;
     // probabilities of the next word are loaded while the current one is encoded
     float pn = (src_ok && lane < in_dim) ? prow_p[lane] : 0.0f;
@@ -172,7 +170,8 @@ __device__ __forceinline__ void transpose64(uint32_t& lo, uint32_t& hi, int lane
 template <int T>
 __global__ __launch_bounds__(256) void k_poisson_sparse(
     const float* __restrict__ p, int64_t p_rows, const int32_t* __restrict__ prow, int64_t rows,
-    int32_t in_dim, int64_t p_stride, uint32_t mix, uint64_t* __restrict__ out, int64_t out_stride) {
+    int32_t in_dim, int64_t p_stride, uint32_t mix, uint64_t* __restrict__ out, int64_t out_stride,
+    int64_t plane) {
     static_assert(T >= 1 && T <= 32 && (T & (T - 1)) == 0, "T must be a power of two <= 32");
     constexpr int WPT = 64 / T;  // words per 64 x 64 transpose
     extern __shared__ __align__(16) unsigned char psm[];
@@ -241,7 +240,6 @@ __global__ __launch_bounds__(256) void k_poisson_sparse(
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
     // C. transpose and store
-    const int64_t plane = rows * out_stride;
     const int32_t wi = lane / T, t = lane % T;
     uint64_t* orow = out + (int64_t)t * plane + row * out_stride;
     for (int32_t w0 = 0; w0 < words; w0 += WPT) {
@@ -456,17 +454,19 @@ static int64_t wave_blocks(int64_t rows, int32_t width) {
     return (waves + 3) / 4;  // 4 waves per 256-thread block
 }
 
-extern "C" int hses_poisson_encode(const float* d_p, int64_t p_rows, const int32_t* d_rows, int64_t rows,
-                                   int32_t in_dim, int64_t p_stride, int32_t T, uint32_t s0,
-                                   uint32_t s1, uint32_t s2, uint32_t s3, void* d_out, int32_t fmt,
-                                   int64_t out_stride, void* stream) {
+extern "C" int hses_poisson_encode_planes(const float* d_p, int64_t p_rows, const int32_t* d_rows,
+                                          int64_t rows, int32_t in_dim, int64_t p_stride, int32_t T,
+                                          uint32_t s0, uint32_t s1, uint32_t s2, uint32_t s3,
+                                          void* d_out, int32_t fmt, int64_t out_stride,
+                                          int64_t out_plane, void* stream) {
     HSES_REQUIRE(rows >= 0 && in_dim >= 0 && T >= 0, "negative size");
     HSES_REQUIRE(fmt >= HSES_FMT_F32 && fmt <= HSES_FMT_BITS, "unknown spike format");
     if (rows == 0 || in_dim == 0 || T == 0) return HSES_OK;
     HSES_REQUIRE(d_p && d_out, "NULL pointer");
     HSES_REQUIRE(p_stride >= in_dim, "p_stride < in_dim");
     HSES_REQUIRE(d_rows || p_rows >= rows, "p_rows < rows without a row index");
-    HSES_REQUIRE(out_stride >= fmt_row_units(fmt, in_dim), "out_stride too small for format");
+    HSES_REQUIRE(rows_layout_ok(fmt_row_units(fmt, in_dim), rows, T, out_stride, out_plane),
+                 "output rows overlap (out_stride too small for the format, or time planes overlap)");
     // The reference seeds with the flat index as u32 (poisson_encode_fused_oxide.rs:68-83).
     HSES_REQUIRE(rows * in_dim <= (int64_t)UINT32_MAX, "rows*in_dim exceeds the u32 index range");
     const int64_t blocks = wave_blocks(rows, in_dim);
@@ -476,15 +476,15 @@ extern "C" int hses_poisson_encode(const float* d_p, int64_t p_rows, const int32
     switch (fmt) {
         case HSES_FMT_F32:
             hipLaunchKernelGGL(k_poisson<HSES_FMT_F32>, dim3(blocks), dim3(256), 0, s, d_p, p_rows, d_rows,
-                               rows, in_dim, p_stride, T, mix, d_out, out_stride);
+                               rows, in_dim, p_stride, T, mix, d_out, out_stride, out_plane);
             break;
         case HSES_FMT_BF16:
             hipLaunchKernelGGL(k_poisson<HSES_FMT_BF16>, dim3(blocks), dim3(256), 0, s, d_p, p_rows, d_rows,
-                               rows, in_dim, p_stride, T, mix, d_out, out_stride);
+                               rows, in_dim, p_stride, T, mix, d_out, out_stride, out_plane);
             break;
         case HSES_FMT_U8:
             hipLaunchKernelGGL(k_poisson<HSES_FMT_U8>, dim3(blocks), dim3(256), 0, s, d_p, p_rows, d_rows,
-                               rows, in_dim, p_stride, T, mix, d_out, out_stride);
+                               rows, in_dim, p_stride, T, mix, d_out, out_stride, out_plane);
             break;
         default:
             if (T <= 32 && (T & (T - 1)) == 0 && in_dim <= 2048) {
@@ -495,7 +495,7 @@ extern "C" int hses_poisson_encode(const float* d_p, int64_t p_rows, const int32
 #define HSES_PSPARSE(TV)                                                                        \
     case TV:                                                                                    \
         hipLaunchKernelGGL(k_poisson_sparse<TV>, g, b, lds, s, d_p, p_rows, d_rows, rows, in_dim, \
-                           p_stride, mix, o, out_stride);                                       \
+                           p_stride, mix, o, out_stride, out_plane);                                       \
         break;
                 switch (T) {
                     HSES_PSPARSE(1)
@@ -512,21 +512,29 @@ extern "C" int hses_poisson_encode(const float* d_p, int64_t p_rows, const int32
                 uint64_t* o = static_cast<uint64_t*>(d_out);
                 if (T == 16)
                     hipLaunchKernelGGL(k_poisson_bits<16>, g, b, 0, s, d_p, p_rows, d_rows, rows,
-                                       in_dim, p_stride, T, mix, o, out_stride);
+                                       in_dim, p_stride, T, mix, o, out_stride, out_plane);
                 else if (T == 8)
                     hipLaunchKernelGGL(k_poisson_bits<8>, g, b, 0, s, d_p, p_rows, d_rows, rows,
-                                       in_dim, p_stride, T, mix, o, out_stride);
+                                       in_dim, p_stride, T, mix, o, out_stride, out_plane);
                 else
                     hipLaunchKernelGGL(k_poisson_bits<0>, g, b, 0, s, d_p, p_rows, d_rows, rows,
-                                       in_dim, p_stride, T, mix, o, out_stride);
+                                       in_dim, p_stride, T, mix, o, out_stride, out_plane);
             }
             else
                 hipLaunchKernelGGL(k_poisson<HSES_FMT_BITS>, dim3(blocks), dim3(256), 0, s, d_p, p_rows,
-                                   d_rows, rows, in_dim, p_stride, T, mix, d_out, out_stride);
+                                   d_rows, rows, in_dim, p_stride, T, mix, d_out, out_stride, out_plane);
             break;
     }
     HSES_CHECK_HIP(hipGetLastError());
     return HSES_OK;
+}
+
+extern "C" int hses_poisson_encode(const float* d_p, int64_t p_rows, const int32_t* d_rows, int64_t rows,
+                                   int32_t in_dim, int64_t p_stride, int32_t T, uint32_t s0,
+                                   uint32_t s1, uint32_t s2, uint32_t s3, void* d_out, int32_t fmt,
+                                   int64_t out_stride, void* stream) {
+    return hses_poisson_encode_planes(d_p, p_rows, d_rows, rows, in_dim, p_stride, T, s0, s1, s2, s3,
+                                      d_out, fmt, out_stride, rows * out_stride, stream);
 }
 
 extern "C" int hses_lif_scan(const float* d_cur, const float* d_v0, int32_t T, int64_t rows,

@@ -103,8 +103,10 @@ def nonlora_noise(base_sigma, key, epoch, noise_reuse, tids, a, b, device="cuda"
     return out
 
 
-def poisson_encode(p, T, seeds=(0, 0, 0, 0), fmt=FMT_F32, out=None, rows_index=None):
-    """(rows, in_dim) probabilities -> (T, rows, width) spikes in `fmt`.  With
+def poisson_encode(p, T, seeds=(0, 0, 0, 0), fmt=FMT_F32, out=None, rows_index=None,
+                   time_inner=False):
+    """(rows, in_dim) probabilities -> (T, rows, width) spikes in `fmt`, or
+    (rows, T, width) with time_inner (each row's T words adjacent).  With
     rows_index (int32, length R) output row i encodes p[rows_index[i]]."""
     _dev(p, torch.float32, "p")
     prow, in_dim = p.shape
@@ -113,11 +115,16 @@ def poisson_encode(p, T, seeds=(0, 0, 0, 0), fmt=FMT_F32, out=None, rows_index=N
         _dev(rows_index, torch.int32, "rows_index")
         rows = rows_index.numel()
     units = fmt_width(fmt, in_dim)
+    shape = (rows, T, units) if time_inner else (T, rows, units)
     if out is None:
-        out = torch.empty((T, rows, units), dtype=_FMT_DTYPE[fmt], device=p.device)
+        out = torch.empty(shape, dtype=_FMT_DTYPE[fmt], device=p.device)
+    _dev(out, _FMT_DTYPE[fmt], "out")
+    if tuple(out.shape) != shape:
+        raise ValueError(f"out has shape {tuple(out.shape)}, expected {shape}")
+    stride, plane = (T * units, units) if time_inner else (units, rows * units)
     s0, s1, s2, s3 = (int(s) & 0xFFFFFFFF for s in seeds)
-    _lib.call("hses_poisson_encode", _p(p), prow, _p(rows_index), rows, in_dim, in_dim, T, s0, s1, s2,
-              s3, _p(out), fmt, units, _stream())
+    _lib.call("hses_poisson_encode_planes", _p(p), prow, _p(rows_index), rows, in_dim, in_dim, T,
+              s0, s1, s2, s3, _p(out), fmt, stride, plane, _stream())
     return out
 
 
@@ -267,11 +274,14 @@ def perturbed_linear_t(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n, ro
 
 def perturbed_linear_lif(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n,
                          rows_per_member, n_time, tau_m, v_th, spikes=None, rate=None,
-                         want_spikes=True, want_rate=False, rec=None, img=None):
+                         want_spikes=True, want_rate=False, rec=None, img=None,
+                         time_inner=False):
     """Perturbed forward fused with LIF.  x is bit-packed (n_time, M, words(b));
     returns (spikes (n_time, M, words(a)) int64 or None, rate (M, a) or None).
-    With `rec` (factor_record) the pairs' normals are also kept there; with
-    `rec` and `img` filled by pair_factors they are read from there instead."""
+    With time_inner, x and spikes are (M, n_time, words) (each row's time steps
+    adjacent).  With `rec` (factor_record) the pairs' normals are also kept
+    there; with `rec` and `img` filled by pair_factors they are read from there
+    instead."""
     a, b = W.shape
     _dev(W, torch.float32, "W")
     _dev(x, _FMT_DTYPE[FMT_BITS], "x")
@@ -281,7 +291,8 @@ def perturbed_linear_lif(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n,
         raise ValueError(f"x has shape {tuple(x.shape)}, expected ({n_time}, {M}, {units})")
     wa = fmt_width(FMT_BITS, a)
     if want_spikes and spikes is None:
-        spikes = torch.empty((n_time, M, wa), dtype=torch.int64, device=W.device)
+        shape = (M, n_time, wa) if time_inner else (n_time, M, wa)
+        spikes = torch.empty(shape, dtype=torch.int64, device=W.device)
     if want_rate and rate is None:
         rate = torch.empty((M, a), dtype=torch.float32, device=W.device)
     if spikes is not None:
@@ -295,16 +306,22 @@ def perturbed_linear_lif(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n,
     wbytes = int(_lib.load().hses_perturbed_linear_workspace(a, b, rank, n, rows_per_member,
                                                               n_time, MATH_BF16))
     work = _workspace(wbytes, W.device)
-    args = (_p(x), FMT_BITS, units, M * units, n_time, _p(W), a, b, key & (2**64 - 1), rank,
+    if time_inner:
+        xs, xp, ss, sp = n_time * units, units, n_time * wa, wa
+        if x.dim() != 3 or x.shape[0] != M or (spikes is not None and spikes.shape[0] != M):
+            raise ValueError("time_inner x and spikes are (M, n_time, words)")
+    else:
+        xs, xp, ss, sp = units, M * units, wa, M * wa
+    args = (_p(x), FMT_BITS, xs, xp, n_time, _p(W), a, b, key & (2**64 - 1), rank,
             sigma, epoch, noise_reuse, tid_lo, n, rows_per_member, tau_m, v_th,
-            _p(spikes) if spikes is not None else None, wa, M * wa,
+            _p(spikes) if spikes is not None else None, ss, sp,
             _p(rate) if rate is not None else None, a, _p(work), wbytes)
     if img is not None:
         if rec is None:
             raise ValueError("factors drawn ahead need rec")
-        _lib.call("hses_perturbed_linear_lif_pre", _p(x), FMT_BITS, units, M * units, n_time,
+        _lib.call("hses_perturbed_linear_lif_pre", _p(x), FMT_BITS, xs, xp, n_time,
                   _p(W), a, b, rank, sigma, tid_lo, n, rows_per_member, tau_m, v_th,
-                  _p(spikes) if spikes is not None else None, wa, M * wa,
+                  _p(spikes) if spikes is not None else None, ss, sp,
                   _p(rate) if rate is not None else None, a, _p(work), wbytes, *_rec_arg(rec),
                   *_img_arg(img), _stream())
     elif rec is None:

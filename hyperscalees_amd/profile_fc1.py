@@ -28,9 +28,10 @@ def main():
     M = cfg.n * cfg.rows
     g = torch.Generator(device="cuda").manual_seed(0)
     words_in = K.fmt_width(K.FMT_BITS, cfg.dims[0])
-    x = torch.randint(0, 2**62, (cfg.T, M, words_in), dtype=torch.int64, device="cuda", generator=g)
+    # spikes in the step's time-inner layout, (M, T, words)
+    x = torch.randint(0, 2**62, (M, cfg.T, words_in), dtype=torch.int64, device="cuda", generator=g)
     W = torch.randn(cfg.dims[1], cfg.dims[0], device="cuda", generator=g) * 0.05
-    spk = torch.empty((cfg.T, M, K.fmt_width(K.FMT_BITS, cfg.dims[1])), dtype=torch.int64,
+    spk = torch.empty((M, cfg.T, K.fmt_width(K.FMT_BITS, cfg.dims[1])), dtype=torch.int64,
                       device="cuda")
     a, b = cfg.dims[1], cfg.dims[0]
     rec = K.factor_record(a, b, cfg.rank, 0, cfg.n)
@@ -45,7 +46,7 @@ def main():
     for s in range(args.reps):
         K.perturbed_linear_lif(x, W, cfg.keys[0], cfg.rank, cfg.sigma, 0, cfg.noise_reuse, 0,
                                cfg.n, cfg.rows, cfg.T, cfg.tau_m, cfg.v_th, spikes=spk, rec=rec,
-                               img=img)
+                               img=img, time_inner=True)
     torch.cuda.synchronize()
     print("profile_fc1: copy 1 GiB x", args.reps, "; fc1 draw x 1; fc1 GEMM x", args.reps,
           flush=True)

@@ -27,7 +27,7 @@ def run_smoke():
     # Poisson spikes: bit-exact
     es.poisson()
     torch.cuda.synchronize()
-    words = es.spk[0].cpu().numpy().view(np.uint64)
+    words = es.spikes_tm(0).contiguous().cpu().numpy().view(np.uint64)
     bits = ((words[..., None] >> np.arange(64, dtype=np.uint64)) & np.uint64(1)).astype(np.float32)
     got = bits.reshape(cfg.T, cfg.n * cfg.rows, -1)[..., : cfg.dims[0]]
     ref = O.poisson(pool[idx], cfg.T, cfg.poisson_seed)

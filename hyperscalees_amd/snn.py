@@ -126,9 +126,6 @@ class SnnEs:
         self.M = M
         L = len(c.dims) - 1
         self.L = L
-        # bit-packed spikes of the input and of every hidden layer
-        self.spk = [torch.empty((c.T, M, K.fmt_width(FMT_BITS, d)), dtype=torch.int64, device=device)
-                    for d in c.dims[:-1]]
         hmax = max(c.dims[1:-1]) if L > 1 else 1
         # Hidden layers run as one fused forward+LIF kernel when the
         # large-rank kernel applies; the fp32 currents then never exist.
@@ -136,6 +133,15 @@ class SnnEs:
                     and 16 <= c.rank <= 128 and hmax <= 128 and c.T <= 64
                     and (c.T & (c.T - 1)) == 0)
         self.fused = can_fuse if fused is None else (bool(fused) and can_fuse)
+        # Bit-packed spikes of the input and of every hidden layer.  The fused
+        # path keeps them time-inner, (M, T, words): a member's rows, in the
+        # kernels' slot-major row order, are then contiguous, so a 256-row
+        # block of the next layer is one contiguous read.  The unfused path
+        # (LIF scan, spike rates) keeps the time-major (T, M, words) layout.
+        self.time_inner = self.fused
+        self.spk = [torch.empty((M, c.T, K.fmt_width(FMT_BITS, d)) if self.time_inner else
+                                (c.T, M, K.fmt_width(FMT_BITS, d)), dtype=torch.int64, device=device)
+                    for d in c.dims[:-1]]
         self.cur = None if self.fused else \
             torch.empty((c.T, M, hmax), dtype=torch.float32, device=device)
         self.rate = torch.empty((M, c.dims[-2]), dtype=torch.float32, device=device)
@@ -178,6 +184,10 @@ class SnnEs:
                 self.img.append(torch.empty(nbytes // 2, dtype=torch.int16, device=device))
 
     # -- forward -------------------------------------------------------------
+    def spikes_tm(self, l):
+        """Layer l's input spikes as a time-major (T, M, words) view."""
+        return self.spk[l].transpose(0, 1) if self.time_inner else self.spk[l]
+
     def chunk_seeds(self, lo):
         """Poisson seeds of the chunk starting at member lo.  The kernel seeds
         element (row, col) of a call with 1000000007*(row*in + col) + (s0^s1^s2^s3);
@@ -192,7 +202,7 @@ class SnnEs:
         c = self.cfg
         rows = slice(lo * c.rows, (lo + c.chunk) * c.rows)
         K.poisson_encode(self.pool, c.T, self.chunk_seeds(lo), FMT_BITS, out=self.spk[0],
-                         rows_index=self.index[rows])
+                         rows_index=self.index[rows], time_inner=self.time_inner)
 
     def hidden_layer(self, l, epoch, lo=0):
         c = self.cfg
@@ -205,7 +215,8 @@ class SnnEs:
                                    spikes=None if last else self.spk[l + 1],
                                    rate=self.rate if last else None,
                                    want_spikes=not last, want_rate=last,
-                                   rec=self.rec[l] if self.rec else None, img=img)
+                                   rec=self.rec[l] if self.rec else None, img=img,
+                                   time_inner=self.time_inner)
             if self.rec:
                 self._rec_at[l] = (epoch, lo)
             return

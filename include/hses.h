@@ -145,6 +145,19 @@ int hses_poisson_encode(const float *d_p, int64_t p_rows, const int32_t *d_rows,
                         int64_t p_stride, int32_t T, uint32_t s0, uint32_t s1, uint32_t s2,
                         uint32_t s3, void *d_out, int32_t fmt, int64_t out_stride, void *stream);
 
+/* hses_poisson_encode with the time-plane stride given: spike (t, row) at
+ * t*out_plane + row*out_stride.  Besides the time-major layout above
+ * (out_plane >= rows*out_stride) it takes the time-inner layout, each row's T
+ * entries adjacent (out_plane >= the row's units, out_stride >= T*out_plane):
+ * a member's rows then lie contiguous, the layout the fused forward of the
+ * next layer reads fastest (hses_perturbed_linear_lif_pre).  The same
+ * streams and spikes as hses_poisson_encode (poisson_encode_fused_oxide.rs:35-106);
+ * only where they are stored differs. */
+int hses_poisson_encode_planes(const float *d_p, int64_t p_rows, const int32_t *d_rows,
+                               int64_t rows, int32_t in_dim, int64_t p_stride, int32_t T,
+                               uint32_t s0, uint32_t s1, uint32_t s2, uint32_t s3, void *d_out,
+                               int32_t fmt, int64_t out_stride, int64_t out_plane, void *stream);
+
 /* Mean firing rate over time (snn.rs:274, spikes.mean_dim(0)):
  * d_rate[row][c] = (number of spikes of (row, c) over T) / T, spikes in `fmt`
  * with row stride spk_stride (units) and time planes rows*spk_stride apart. */
@@ -170,8 +183,11 @@ int hses_lif_scan(const float *d_cur, const float *d_v0, int32_t T, int64_t rows
  * fp32 row-major; y (n*rows_per_member, a) fp32 with row stride y_stride.
  * Member m's rows are rows [m*rows_per_member, (m+1)*rows_per_member); for
  * time-major activations (T, M, b) pass rows_per_member = slots and
- * n_time = T with plane strides x_plane / y_plane (rows of member m at time
- * t are t*plane + m*slots + s).  sigma=0 or rank=0 gives the clean x W^T.
+ * n_time = T with plane strides x_plane / y_plane (row s of member m at time
+ * t is at t*plane + (m*slots + s)*stride).  Time-major planes (plane >=
+ * M*stride) and the time-inner layout (each row's T entries adjacent:
+ * plane >= a row, stride >= T*plane) are both accepted, for x, y and spikes.
+ * sigma=0 or rank=0 gives the clean x W^T.
  * d_work must hold hses_perturbed_linear_workspace(...) bytes (a bf16 copy of W
  * and, for large ranks, one per-workgroup staging slot for a pair's B factor;
  * the (n, b, r) factor tensor itself is never materialised).  Large ranks

@@ -76,7 +76,7 @@ def c3_run(hses_gpu):
     R = cfg.rows
     rows = np.concatenate([np.arange(m * R, (m + 1) * R) for m in MEMBERS])
     rows_t = torch.as_tensor(rows, device="cuda")
-    spk = [unpack(es.spk[l].index_select(1, rows_t), cfg.dims[l]) for l in range(es.L - 1)]
+    spk = [unpack(es.spikes_tm(l).index_select(1, rows_t), cfg.dims[l]) for l in range(es.L - 1)]
     rate = es.rate.index_select(0, rows_t).cpu().numpy()
     fit_gpu = fit.cpu().numpy().copy()
     es.update(fit, 0)

@@ -235,6 +235,40 @@ def test_fused_lif_matches_unfused(hses_gpu, n, rpm, T, a, b, r, tid_lo):
     assert none is None and torch.equal(spk2, spk_ref)
 
 
+@pytest.mark.parametrize("n,rpm,T,a,b,r,tid_lo,pre", [
+    (4, 64, 16, 128, 784, 128, 0, True),    # C3 fc1, factors drawn ahead (the step's form)
+    (3, 64, 16, 128, 128, 128, 1, True),    # C3 fc2/fc3 shape (resident tiles), partial pairs
+    (5, 12, 8, 100, 200, 64, 0, False),     # partial spike word, generating form
+    (2, 5, 32, 70, 130, 48, 1, False),      # T = 32
+])
+def test_fused_lif_time_inner_layout(hses_gpu, n, rpm, T, a, b, r, tid_lo, pre):
+    """The time-inner layout (each row's T words adjacent, (M, T, words)) gives
+    the spikes and rates of the time-major layout, bit for bit."""
+    rng = np.random.default_rng(n * 11 + T + b)
+    M = n * rpm
+    x3 = (rng.random((T, M, b)) < 0.3).astype(np.float32)
+    W = (rng.standard_normal((a, b)) * (6.0 / np.sqrt(b))).astype(np.float32)
+    xb = pack_bits(x3)
+    Wt = torch.from_numpy(W).cuda()
+    tau, vth = 10.0, 1.0
+    kw = {}
+    if pre:
+        rec = hses_gpu.factor_record(a, b, r, tid_lo, n)
+        img = hses_gpu.pair_image(a, b, r, tid_lo, n)
+        hses_gpu.pair_factors(KEY, r, 0.2, 3, 0, tid_lo, n, a, b, rec, img)
+        kw = dict(rec=rec, img=img)
+    spk_tm, rate_tm = hses_gpu.perturbed_linear_lif(xb, Wt, KEY, r, 0.2, 3, 0, tid_lo, n, rpm, T,
+                                                    tau, vth, want_rate=True, **kw)
+    x_ti = xb.transpose(0, 1).contiguous()
+    spk_ti, rate_ti = hses_gpu.perturbed_linear_lif(x_ti, Wt, KEY, r, 0.2, 3, 0, tid_lo, n, rpm, T,
+                                                    tau, vth, want_rate=True, time_inner=True, **kw)
+    torch.cuda.synchronize()
+    assert tuple(spk_ti.shape) == (M, T, spk_tm.shape[2])
+    assert torch.equal(spk_ti.transpose(0, 1), spk_tm)
+    assert torch.equal(rate_ti, rate_tm)
+    assert 0.005 < float(rate_tm.mean()) < 0.95
+
+
 def ref_forward_t(x3, W, A, B, rpm):
     """do_Tmm: x3 (T, n*rpm, a) -> (T, n*rpm, b), x W + (x A_m) B_m^T in float64."""
     x3 = x3.astype(np.float64)

@@ -76,19 +76,19 @@ def test_c1_layerwise_parity(hses_gpu):
     es.poisson()
     torch.cuda.synchronize()
     ref0 = O.poisson(pool[idx], cfg.T, cfg.poisson_seed)
-    np.testing.assert_array_equal(unpack(es.spk[0], cfg.dims[0]), ref0)
+    np.testing.assert_array_equal(unpack(es.spikes_tm(0), cfg.dims[0]), ref0)
     total = mism = 0
     for l in range(es.L - 1):
         es.hidden_layer(l, 0)
         torch.cuda.synchronize()
-        x = unpack(es.spk[l], cfg.dims[l])
+        x = unpack(es.spikes_tm(l), cfg.dims[l])
         a = cfg.dims[l + 1]
         cur_ref = oracle_layer(x, W[l], cfg, l)
         cur_gpu = es.cur.view(-1)[: cur_ref.size].view(cur_ref.shape).cpu().numpy()
         err = np.abs(cur_gpu - cur_ref).max()
         assert err <= 1e-5 * np.abs(cur_ref).max(), f"layer {l} currents err {err}"
         spk_ref, _ = O.lif(cur_ref, cfg.tau_m, cfg.v_th)
-        spk_gpu = unpack(es.spk[l + 1], a)
+        spk_gpu = unpack(es.spikes_tm(l + 1), a)
         # LIF on the GPU's own currents is bit-exact; flips come only from
         # current rounding near the threshold
         spk_own, _ = O.lif(cur_gpu, cfg.tau_m, cfg.v_th)
@@ -149,7 +149,7 @@ def test_c3_shape_bf16_step(hses_gpu):
     for l in range(es.L - 1):
         es.hidden_layer(l, 0)
         torch.cuda.synchronize()
-        x = unpack(es.spk[l], cfg.dims[l])
+        x = unpack(es.spikes_tm(l), cfg.dims[l])
         cur_ref = oracle_layer(x, W[l], cfg, l)
         cur_gpu = es.cur.view(-1)[: cur_ref.size].view(cur_ref.shape).cpu().numpy()
         err = np.abs(cur_gpu - cur_ref).max()
@@ -158,7 +158,7 @@ def test_c3_shape_bf16_step(hses_gpu):
         A, B = O.lora_factors(bs, cfg.keys[l], cfg.rank, 0, np.arange(cfg.n), a, cfg.dims[l])
         cur_bf = np.concatenate([member_currents(x[:, m * R:(m + 1) * R], W[l], A[m], B[m], True)
                                  for m in range(cfg.n)], axis=1)
-        spk_gpu = unpack(es.spk[l + 1], a)
+        spk_gpu = unpack(es.spikes_tm(l + 1), a)
         spk_bf, _ = O.lif(cur_bf.astype(np.float32), cfg.tau_m, cfg.v_th)
         spk_32, _ = O.lif(cur_ref, cfg.tau_m, cfg.v_th)
         n_ref = int(spk_32.sum())
@@ -186,7 +186,7 @@ def test_c3_fused_forward_equals_unfused(hses_gpu):
     fit_f = es_f.forward(0)
     torch.cuda.synchronize()
     for l in range(1, es_u.L - 1):
-        assert torch.equal(es_u.spk[l], es_f.spk[l]), f"layer {l} spikes"
+        assert torch.equal(es_u.spikes_tm(l), es_f.spikes_tm(l)), f"layer {l} spikes"
     assert torch.equal(es_u.rate, es_f.rate)
     assert torch.equal(fit_u, fit_f)
     assert float(es_f.rate.mean()) > 0.005

@@ -67,6 +67,34 @@ def test_poisson_bits_zero_skip(hses_gpu, rows, d, T, zero_frac):
     np.testing.assert_array_equal(unpack_bits(got, d), O.poisson(p[idx], T, seeds))
 
 
+@pytest.mark.parametrize("rows,d,T,fmt", [
+    (37, 784, 16, FMT_BITS),   # zero-skipping kernel (the C3 input)
+    (9, 300, 8, FMT_BITS),
+    (5, 130, 40, FMT_BITS),    # T not a power of two: one wave per row
+    (6, 70, 5, FMT_F32),       # element formats
+    (4, 33, 3, FMT_U8),
+])
+def test_poisson_time_inner_layout(hses_gpu, rows, d, T, fmt):
+    """hses_poisson_encode_planes with the time-inner layout (rows, T, width)
+    stores the same spikes as the time-major layout, and the time-major call
+    through it equals hses_poisson_encode."""
+    rng = np.random.default_rng(rows * 3 + d)
+    p = rng.random((rows, d)).astype(np.float32)
+    p[rng.random(p.shape) < 0.5] = 0.0
+    pt = torch.from_numpy(p).cuda()
+    seeds = (7, 8, 9, 10)
+    tm = hses_gpu.poisson_encode(pt, T, seeds, fmt)
+    ti = hses_gpu.poisson_encode(pt, T, seeds, fmt, time_inner=True)
+    torch.cuda.synchronize()
+    assert torch.equal(ti.transpose(0, 1), tm)
+    ref = O.poisson(p, T, seeds)
+    got = tm.cpu().numpy()
+    if fmt == FMT_BITS:
+        w = got.view(np.uint64)
+        got = ((w[..., None] >> np.arange(64, dtype=np.uint64)) & np.uint64(1)).reshape(T, rows, -1)[..., :d]
+    np.testing.assert_array_equal(np.asarray(got, np.float32), ref)
+
+
 def test_poisson_threshold_dense_p_sweep(hses_gpu):
     # Every representable neighbourhood of many thresholds: p on a fine grid
     # plus its f32 neighbours, checked against the f32-division formula.
