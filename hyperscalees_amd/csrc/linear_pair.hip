@@ -109,6 +109,16 @@ struct K2Args {
     int32_t group;  // pairs generated together (k_linear_pair; their A rows share the LDS block)
     int32_t tmm;    // do_Tmm stream roles (LinParams::tmm)
     int32_t x_vec;  // dense x: strides keep 8-element groups 16-byte aligned
+    // bit-packed x in the packed time-inner layout (x_plane = a row's words,
+    // x_stride = T rows of them): row L of the call lies at word L * words,
+    // so a block's bit rows are one contiguous run, 16-byte aligned
+    int32_t x_packed;
+    // k_pair_bits work units: each pair's row blocks split evenly over `split`
+    // workgroups (1, or 4 with every pair full and the grid a multiple of 32),
+    // which work on it at the same time on one XCD (workgroups are dealt to
+    // the 8 XCDs in turn), so the pair's operand image is fetched from HBM
+    // about once and re-read from that XCD's L2
+    int32_t split;
     float bs, leak, v_th;
     // Factor record (do_mm), or NULL: pair pair_lo + i's raw normals (before
     // any scale) at rec[(i * r + c) * (a + b) + j] for stream row j, rank c.
@@ -763,31 +773,69 @@ __device__ __forceinline__ f32x16 mfma32_bf16(const u16x8& a, const u16x8& b, f3
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
+// Direct-to-LDS tiles (DL): K3_DLBUF unpadded tile buffers of K2_COLS
+// columns x K2_BK k (128 bytes per column), filled by LDS DMA (each lane's
+// 16-byte chunk lands at the wave's base + 16 x lane).  A column's eight
+// 16-byte chunks are stored XOR-swizzled, chunk c at slot c ^ ((column / 2) & 7),
+// so that the 16 lanes of a fragment read (16 columns, one chunk each) cover
+// all 64 banks.
+constexpr int K3_DLBUF = 3;
+constexpr int K3_DLTILE = K2_COLS * K2_BK;  // bf16 elements per DL tile buffer
+
 struct K3Layout {
     size_t off_a, off_xbits, off_wb, bytes;
     int32_t apitch, words, kp;
-    __host__ __device__ K3Layout(int r, int b) {
+    // dl: the DL form (factors drawn ahead, so no noise tables)
+    __host__ __device__ K3Layout(int r, int b, bool dl = false) {
         apitch = K3_AP;
         words = (b + 63) / 64;
         kp = words * 64;
-        size_t o = align16(sizeof(BmTables));
+        size_t o = dl ? 0 : align16(sizeof(BmTables));
         off_a = o;
         o = align16(o + (size_t)K2_NMAX * apitch * 2);
         off_xbits = o;
         o = align16(o + (size_t)K3_RB * words * 8);
         off_wb = o;
-        bytes = o + (size_t)2 * K2_COLS * K2_TP * 2;
+        bytes = o + (dl ? (size_t)K3_DLBUF * K3_DLTILE * 2 : (size_t)2 * K2_COLS * K2_TP * 2);
     }
 };
+
+// One LDS DMA of 16 bytes per lane: lane l's 16 bytes at gptr land at LDS byte
+// address lds + 16 l (lds wave-uniform).  Written as inline assembly so that
+// the compiler's memory model does not see an LDS write that completes on the
+// vector-memory counter: its LDS fences would otherwise wait for every
+// transfer in flight, including the tile streaming two ahead.  The kernel
+// orders these transfers itself (wait_vmcnt before the barrier that
+// publishes a tile).
+__device__ __forceinline__ void lds_dma16(const void* gptr, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds)
+                 : "memory", "m0");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// s_waitcnt on the vector-memory counter only (gfx9 encoding: vmcnt in bits
+// 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
 
 // EPI_Y: store the currents; EPI_LIF: LIF with T = LT, spike words if SPK,
 // spike rates if RATE.  PRE: the factors were drawn ahead (k_pair_gen): A
 // comes from the record, B from the operand image, and nothing is generated.
-template <int EPI, int LT, bool SPK, bool RATE, bool PRE = false>
+// DL (with PRE, K of more than two tiles): the W/B tiles stream into three
+// LDS buffers by LDS DMA, two tiles ahead of the MFMAs, instead of through
+// registers; the stream runs on across blocks and pairs.
+template <int EPI, int LT, bool SPK, bool RATE, bool PRE = false, bool DL = false>
 __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
     static_assert(LT >= 1 && LT <= 16 && (LT & (LT - 1)) == 0, "T must be a power of two <= 16");
+    static_assert(!DL || PRE, "the DL tile stream needs factors drawn ahead");
     extern __shared__ __align__(16) unsigned char smem[];
-    const K3Layout lay(P.r, P.b);
+    const K3Layout lay(P.r, P.b, DL);
     BmTables* tabs = reinterpret_cast<BmTables*>(smem);
     uint16_t* As = reinterpret_cast<uint16_t*>(smem + lay.off_a);
     uint64_t* Xbits = reinterpret_cast<uint64_t*>(smem + lay.off_xbits);
@@ -820,6 +868,25 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
     const uint16_t* lsrc = (lcol < K2_NMAX ? P.wbf : slot) + loff;  // PRE: B part set per pair
     uint16_t* ldst = WB + lcol * K2_TP + lk;
     const uint32_t lmask = lvalid ? 0xffffffffu : 0u;
+    // DL: wave w's DMA instruction q fills chunk block 4w + q of a tile buffer
+    // (staged columns 32w + 8q .. 32w + 8q + 7); lane l fetches chunk
+    // (l & 7) ^ swizzle of column 32w + 8q + l / 8.  Waves 0-3 stage W rows,
+    // waves 4-7 rank columns of B; absent columns repeat the last present one
+    // (their outputs are never stored, and A is zero there).
+    int32_t dl_off[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int32_t col = 32 * wave + 8 * q + (lane >> 3);
+        const int32_t ch = (lane & 7) ^ (((8 * q + (lane >> 3)) >> 1) & 7);
+        const int32_t srow = col < K2_NMAX ? min(col, a - 1) : min(col - K2_NMAX, r - 1);
+        dl_off[q] = srow * kp + ch * 8;
+    }
+    auto dl_issue = [&](const uint16_t* src, int32_t kt, int32_t buf) {
+        const uint32_t dst = __builtin_amdgcn_readfirstlane(
+            lds_addr(WB + buf * K3_DLTILE + (4 * wave) * 512));
+#pragma unroll
+        for (int q = 0; q < 4; ++q) lds_dma16(src + dl_off[q] + kt * K2_BK, dst + q * 1024);
+    };
 #define K3_TILE_LOAD(kt)                                                            \
     do {                                                                            \
         const uint4* src_ = reinterpret_cast<const uint4*>(lsrc + (kt) * K2_BK);    \
@@ -850,13 +917,61 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
     // K of at most two tiles: both stay in the two LDS buffers for all of a
     // pair's blocks (staged by its first block), so no block reloads them
     // and the K loop needs no barrier between its tiles.
-    const bool resident = nkt <= 2;
+    const bool resident = DL ? false : nkt <= 2;
+    // DL tile stream: the buffer of the block's current tile, and whether the
+    // stream has been started (tiles 0 and 1 of the first block).
+    int32_t dl_cb = 0;
+    bool dl_primed = false;
+    const uint16_t* dl_wsrc = wave < 4 ? P.wbf : nullptr;  // waves 4-7: set per pair
+    const PairImage dl_im(a, b, r);
 
-    for (int32_t pi = blockIdx.x; pi < P.n_pairs; pi += gridDim.x) {
+    // Work unit `it` of this workgroup: pair index and part (of P.split).
+    const int32_t G = (int32_t)gridDim.x, S = P.split;
+    auto unit_of = [&](int32_t it, int32_t* pi_, int32_t* part) {
+        if (S == 1) {
+            *pi_ = (int32_t)blockIdx.x + it * G;
+            *part = 0;
+        } else {
+            const int32_t xcd = (int32_t)blockIdx.x & 7, sl = (int32_t)blockIdx.x >> 3;
+            *pi_ = it * (G / S) + xcd * (G / (8 * S)) + sl / S;
+            *part = sl % S;
+        }
+    };
+    // Rows [lo, hi) of part `part` of pair pi, and the (member, row) of lo.
+    auto unit_rows = [&](int32_t pi_, int32_t part, int64_t* lo, int64_t* hi) {
+        pair_rows(pi_, lo, hi);
+        if (S > 1) {
+            const int64_t span = (*hi - *lo) / S;  // a multiple of K3_RB (host check)
+            *lo += part * span;
+            *hi = *lo + span;
+        }
+    };
+    auto unit_cursor = [&](int32_t pi_, int32_t part) {
+        RowCursor c;
+        c.m0 = max(2 * (P.pair_lo + pi_) - P.tid_lo, 0);
+        c.q0 = 0;
+        if (S > 1) {
+            const int32_t off = part * (int32_t)((2 * (int64_t)R) / S);
+            c.m0 += off / R;
+            c.q0 = off - (off / R) * R;
+        }
+        return c;
+    };
+
+    for (int32_t it = 0;; ++it) {
+        int32_t pi, part;
+        unit_of(it, &pi, &part);
+        if (pi >= P.n_pairs) break;
         const int32_t pair = P.pair_lo + pi;
         int64_t row_lo, row_hi;
-        pair_rows(pi, &row_lo, &row_hi);
-        const bool more_pairs = pi + (int32_t)gridDim.x < P.n_pairs;
+        unit_rows(pi, part, &row_lo, &row_hi);
+        int32_t pi_n, part_n;  // this workgroup's next unit
+        unit_of(it + 1, &pi_n, &part_n);
+        const bool more_pairs = pi_n < P.n_pairs;
+        // DL: this wave's tile source for pair pi and for the next unit's pair
+        const uint16_t* dl_src = wave < 4 ? dl_wsrc : P.bimg + (size_t)pi * dl_im.stride;
+        const uint16_t* dl_src_next =
+            wave < 4 ? dl_wsrc : P.bimg + (size_t)(more_pairs ? pi_n : pi) * dl_im.stride;
 
         // ---- 1. factors: A rows -> LDS (bf16, [o][c]); B rows -> slot ([c][k]) ----
         if constexpr (PRE) {
@@ -877,14 +992,20 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
             av2 = aload(2);
             av3 = aload(3);
             av4 = aload(4);
-            __syncthreads();  // the previous pair's epilogue has finished reading As
+            // the previous pair's epilogue has finished reading As (DL: an
+            // LDS-only barrier, so the tiles streaming in stay in flight)
+            if constexpr (DL) lds_barrier(); else __syncthreads();
             astore(0, av0);
             astore(1, av1);
             astore(2, av2);
             astore(3, av3);
             astore(4, av4);
-            __threadfence_block();
-            __syncthreads();
+            if constexpr (DL) {
+                lds_barrier();
+            } else {
+                __threadfence_block();
+                __syncthreads();
+            }
         } else {
             __syncthreads();  // the previous pair's epilogue has finished reading As
             int32_t te, tt;
@@ -919,10 +1040,7 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
         // row, words past the row its last word) and the result is masked when
         // stored, so nothing waits for them before xbits_store.
         bool xs_ok = false;
-        auto xbits_load = [&](int64_t L, int64_t rhi, uint64_t (&v)[K3_XPF]) {
-            RowCursor cr;
-            cr.m0 = (int32_t)(L / R);
-            cr.q0 = (int32_t)(L - (int64_t)cr.m0 * R);
+        auto xbits_load = [&](const RowCursor& cr, int64_t L, int64_t rhi, uint64_t (&v)[K3_XPF]) {
             const int32_t nv = (int32_t)min<int64_t>(rhi - L, K3_RB);
             xs_ok = xs_row < nv;
             int32_t m, qq;
@@ -932,29 +1050,96 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
 #pragma unroll
             for (int q = 0; q < K3_XPF; ++q) v[q] = src[min(xs_w + 2 * q, nkt - 1)];
         };
+        // Every loaded register is read here on every path (the empty asm),
+        // so the compiler sees no load in flight across the block loop's back
+        // edge and does not wait for all memory at the next block's start.
+        auto consume = [](const uint64_t (&v)[K3_XPF]) {
+#pragma unroll
+            for (int q = 0; q < K3_XPF; ++q) asm volatile("" ::"v"(v[q]));
+        };
         auto xbits_store = [&](const uint64_t (&v)[K3_XPF]) {
 #pragma unroll
             for (int q = 0; q < K3_XPF; ++q) {
                 const int32_t w = xs_w + 2 * q;
                 if (w < nkt) Xbits[xs_row * nkt + w] = xs_ok ? v[q] : 0ull;
             }
+            consume(v);
+        };
+        // Packed layout (P.x_packed): the block's nv rows are the nv * nkt
+        // words from L * nkt on, stored to Xbits as they lie.  Wave w moves the
+        // 16-byte chunks of its own rows 32w .. 32w + 31 (16 nkt chunks; lane l
+        // takes chunks l + 64 q), so that with resident tiles each wave still
+        // reads only the bit rows it staged.  Loads are clamped to the valid
+        // words; words past them are stored as zero.  (The same registers as
+        // the gathered form: chunk q in v[2q], v[2q + 1].)
+        int32_t xp_nw = 0;  // valid words of the block being staged
+        const int32_t xp_c0 = 16 * nkt * wave;  // this wave's first chunk
+        auto xbits_load_packed = [&](int64_t L, int64_t rhi, uint64_t (&v)[K3_XPF]) {
+            const int32_t nv = (int32_t)min<int64_t>(rhi - L, K3_RB);
+            xp_nw = nv * nkt;
+            const uint4* src = reinterpret_cast<const uint4*>(static_cast<const uint64_t*>(P.x) + L * nkt);
+            const int32_t cmax = (xp_nw - 1) >> 1;
+#pragma unroll
+            for (int q = 0; q < K3_XPF / 2; ++q) {
+                const uint4 u = src[min(xp_c0 + lane + 64 * q, cmax)];
+                v[2 * q] = ((uint64_t)u.y << 32) | u.x;
+                v[2 * q + 1] = ((uint64_t)u.w << 32) | u.z;
+            }
+        };
+        auto xbits_store_packed = [&](const uint64_t (&v)[K3_XPF]) {
+#pragma unroll
+            for (int q = 0; q < K3_XPF / 2; ++q) {
+                const int32_t cl = lane + 64 * q, c = xp_c0 + cl;
+                if (cl < 16 * nkt) {
+                    const uint64_t lo = 2 * c < xp_nw ? v[2 * q] : 0ull;
+                    const uint64_t hi = 2 * c + 1 < xp_nw ? v[2 * q + 1] : 0ull;
+                    reinterpret_cast<uint4*>(Xbits)[c] =
+                        make_uint4((uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32));
+                }
+            }
+            consume(v);
         };
 
         // ---- 2./3. row blocks ----------------------------------------------------
         uint4 pf0, pf1, pf2, pf3;
         uint64_t xpf[K3_XPF];
+        // (member, row) of a block's first row: a pair's rows start at row 0
+        // of its first member, and a block's cursor is the previous one's
+        // advanced by K3_RB rows (no 64-bit division per block).
+        auto advance = [&](RowCursor c) {
+            c.q0 += K3_RB;
+            if (c.q0 >= R) {
+                const int32_t d = c.q0 / R;
+                c.m0 += d;
+                c.q0 -= d * R;
+            }
+            return c;
+        };
+        RowCursor cur_rows = unit_cursor(pi, part);
         for (int64_t L0 = row_lo; L0 < row_hi; L0 += K3_RB) {
             const bool first = L0 == row_lo;
             const bool has_next = L0 + K3_RB < row_hi;
-            RowCursor cur_rows;
-            cur_rows.m0 = (int32_t)(L0 / R);
-            cur_rows.q0 = (int32_t)(L0 - (int64_t)cur_rows.m0 * R);
+            if (!first) cur_rows = advance(cur_rows);
             const int32_t nvalid = (int32_t)min<int64_t>(row_hi - L0, K3_RB);
             if (first && !xready) {
-                xbits_load(L0, row_hi, xpf);
-                xbits_store(xpf);
+                if (P.x_packed) {
+                    xbits_load_packed(L0, row_hi, xpf);
+                    xbits_store_packed(xpf);
+                } else {
+                    xbits_load(cur_rows, L0, row_hi, xpf);
+                    xbits_store(xpf);
+                }
             }
-            if (first) {
+            if constexpr (DL) {
+                // the stream's first two tiles; later blocks' tiles were issued
+                // during the previous block's last two tiles
+                if (!dl_primed) {
+                    dl_issue(dl_src, 0, dl_cb);
+                    dl_issue(dl_src, 1, dl_cb == 2 ? 0 : dl_cb + 1);
+                    wait_vmcnt<4>();
+                    dl_primed = true;
+                }
+            } else if (first) {
                 K3_TILE_LOAD(0);
                 K3_TILE_STORE(0);
                 if (resident && nkt > 1) {
@@ -969,7 +1154,7 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
                 lds_barrier();
             else
                 wave_lds_sync();
-            if (nkt > 1 && !resident) K3_TILE_LOAD(1);
+            if (!DL && nkt > 1 && !resident) K3_TILE_LOAD(1);
 
             f32x16 accW[4], accB[4];
             const uint32_t* xw = Xbits32 + (wrow0 + xrow) * (2 * nkt);
@@ -984,12 +1169,22 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
             // the block's first tile, whose first step starts from the zero
             // operand instead of clearing 128 accumulator registers.
             u16x8 fr[8];
-            auto frag_ptr = [&](int32_t kt, int ks) {
-                return WB + (kt & 1) * (K2_COLS * K2_TP) + lc * K2_TP + hl * 8 + 16 * ks;
+            // Fragment base of LDS tile buffer `bsel` at k-step ks; DL buffers
+            // are unpadded and XOR-swizzled (chunk 2 ks + hl of column c at
+            // slot (2 ks + hl) ^ ((c / 2) & 7); c / 2 mod 8 is lc / 2 mod 8 for
+            // every staged column this lane reads).
+            const int32_t dl_u = hl ^ ((lc >> 1) & 7);
+            auto frag_ptr = [&](int32_t bsel, int ks) -> const uint16_t* {
+                if constexpr (DL)
+                    return WB + bsel * K3_DLTILE + lc * K2_BK + (((2 * ks) ^ dl_u) << 3);
+                else
+                    return WB + bsel * (K2_COLS * K2_TP) + lc * K2_TP + hl * 8 + 16 * ks;
             };
-            auto frag_off = [](int j) { return ((j < 4 ? 0 : K2_NMAX) + 32 * (j & 3)) * K2_TP; };
+            auto frag_off = [](int j) {
+                return ((j < 4 ? 0 : K2_NMAX) + 32 * (j & 3)) * (DL ? K2_BK : K2_TP);
+            };
             {
-                const uint16_t* tb = frag_ptr(0, 0);
+                const uint16_t* tb = frag_ptr(DL ? dl_cb : 0, 0);
 #pragma unroll
                 for (int j = 0; j < 8; ++j) fr[j] = lds_u16x8(tb + frag_off(j));
             }
@@ -1011,33 +1206,69 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
                     __builtin_amdgcn_sched_barrier(0);
                 }
             };
-            // Tile kt sits in LDS buffer kt & 1; the next one is staged from
-            // registers into the other buffer during this one (unless the tiles
-            // are resident).  The last tile's last step re-reads its own first
-            // fragments (no branch around the reads; the values are unused).
+            // Tile kt sits in LDS buffer kt & 1 (DL: dl_cb); the next one is
+            // staged into the other buffer during this one (unless the tiles are
+            // resident; DL: the tile two ahead in the stream is issued and the
+            // next one waited for).  The last tile's last step re-reads its own
+            // first fragments (no branch around the reads; the values are unused).
+            const bool dl_next_pair = !has_next && more_pairs;
+            bool dl_v2 = false;  // DL: this tile issued the stream's tile two ahead
             auto tile = [&](int32_t kt, auto zc) {
                 const bool more = kt + 1 < nkt;
                 const int32_t kn = more ? kt + 1 : kt;
+                const int32_t cb = DL ? dl_cb : (kt & 1);
+                const int32_t nb = DL ? (dl_cb == 2 ? 0 : dl_cb + 1) : ((kt + 1) & 1);
                 const uint32_t w0 = xw0, w1 = xw1;
-                step(w0, std::integral_constant<int, 0>{}, zc, frag_ptr(kt, 1));
-                step(w0, std::integral_constant<int, 1>{}, std::false_type{}, frag_ptr(kt, 2));
-                if (more && !resident) {
+                step(w0, std::integral_constant<int, 0>{}, zc, frag_ptr(cb, 1));
+                step(w0, std::integral_constant<int, 1>{}, std::false_type{}, frag_ptr(cb, 2));
+                if constexpr (DL) {
+                    int32_t t2 = kt + 2;
+                    const uint16_t* src2 = dl_src;
+                    dl_v2 = true;
+                    if (t2 >= nkt) {
+                        t2 -= nkt;
+                        if (!has_next) {
+                            src2 = dl_src_next;
+                            dl_v2 = dl_next_pair;
+                        }
+                    }
+                    if (dl_v2) dl_issue(src2, t2, nb == 2 ? 0 : nb + 1);
+                } else if (more && !resident) {
                     K3_TILE_STORE((kt + 1) & 1);
                     if (kt + 2 < nkt) K3_TILE_LOAD(kt + 2);
                 }
-                step(w1, std::integral_constant<int, 2>{}, std::false_type{}, frag_ptr(kt, 3));
-                if (more && !resident) lds_barrier();
+                step(w1, std::integral_constant<int, 2>{}, std::false_type{}, frag_ptr(cb, 3));
+                if (more && !resident) {
+                    if constexpr (DL) {
+                        // tile kt + 1 (issued two tiles ago) has landed; only the
+                        // tile just issued may still be in flight
+                        if (dl_v2)
+                            wait_vmcnt<4>();
+                        else
+                            wait_vmcnt<0>();
+                    }
+                    lds_barrier();
+                }
                 xw0 = xw[2 * kn];
                 xw1 = xw[2 * kn + 1];
-                step(w1, std::integral_constant<int, 3>{}, std::false_type{}, frag_ptr(kn, 0));
+                step(w1, std::integral_constant<int, 3>{}, std::false_type{}, frag_ptr(more ? nb : cb, 0));
+                if constexpr (DL) dl_cb = nb;
             };
             tile(0, std::true_type{});
             for (int32_t kt = 1; kt < nkt; ++kt) tile(kt, std::false_type{});
-            // resident tiles: the epilogue restages only this wave's bit rows
-            if (!resident || nkt == 1)
+            // resident tiles: the epilogue restages only this wave's bit rows.
+            // DL: the next block's first tile has landed before this barrier.
+            if (!resident || nkt == 1) {
+                if constexpr (DL) {
+                    if (dl_v2)
+                        wait_vmcnt<4>();
+                    else
+                        wait_vmcnt<0>();
+                }
                 lds_barrier();
-            else
+            } else {
                 wave_lds_sync();
+            }
 
             // sign * xB as bf16: lane l holds rank columns 32j + 8g + 4hl + v of
             // the row at MFMA position lc (the row its x operand came from).
@@ -1089,17 +1320,27 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
 
             // The next block's operands land during the LIF and the stores: its
             // bit rows (the next pair's first block after a pair's last one) and,
-            // inside a pair, its first W/B tile.  Issued after the second
-            // product: issued before it, the wave stalled there for about as
-            // long as the product takes (fc1 GEMM 3.55 -> 3.50 ms).
+            // without DL, inside a pair, its first W/B tile.  Issued after the
+            // second product: issued before it, the gathered rows stalled the
+            // wave for about as long as the product takes, and the packed rows
+            // (issued there) gained nothing while their registers spilled.
             // (Issued without branches: the last block of the last pair reloads
-            // its own rows and tile, which are then not stored.)
+            // its own rows and tile, which are then not used.)
             {
                 int64_t nlo = L0, nhi = row_hi;
-                if (has_next) nlo = L0 + K3_RB;
-                else if (next_pair) pair_rows(pi + (int32_t)gridDim.x, &nlo, &nhi);
-                xbits_load(nlo, nhi, xpf);
-                if (!resident) K3_TILE_LOAD(0);
+                RowCursor ncr = cur_rows;
+                if (has_next) {
+                    nlo = L0 + K3_RB;
+                    ncr = advance(cur_rows);
+                } else if (next_pair) {
+                    unit_rows(pi_n, part_n, &nlo, &nhi);
+                    ncr = unit_cursor(pi_n, part_n);
+                }
+                if (P.x_packed)
+                    xbits_load_packed(nlo, nhi, xpf);
+                else
+                    xbits_load(ncr, nlo, nhi, xpf);
+                if (!DL && !resident) K3_TILE_LOAD(0);
             }
 
             // accW[jo][4g + v]: wave row 16 hl + 4g + v, column 32 jo + lc
@@ -1181,8 +1422,14 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
                     }
                 }
             }
-            if (has_next && !resident) K3_TILE_STORE(0);
-            if (has_next || next_pair) xbits_store(xpf);
+            if (!DL && has_next && !resident) K3_TILE_STORE(0);
+            // stored also after the last block (the bit rows are then unused):
+            // every path consumes the loads, so no load is left in flight
+            // across the block loop's back edge
+            if (P.x_packed)
+                xbits_store_packed(xpf);
+            else
+                xbits_store(xpf);
             xready = next_pair;
         }
     }
@@ -1286,13 +1533,26 @@ int launch_linear_pair(LinParams& P, DeviceState* st, hipStream_t s, void* work,
     // Bit-packed input with T <= 16 for the fused LIF: k_pair_bits.
     const bool v3 = bits && (!lif || P.n_time <= 16) && P.b <= 2 * K3_XPF * 64;
     const K2Layout lay(P.r, P.b, bits);
-    const K3Layout lay3(P.r, P.b);
+    // factors drawn ahead and K of more than two tiles: the DL tile stream
+    const bool dl = v3 && pre && (P.b + 63) / 64 > 2 && K3Layout(P.r, P.b, true).bytes <= st->max_lds;
+    const K3Layout lay3(P.r, P.b, dl);
     const size_t lds_bytes = v3 ? lay3.bytes : lay.bytes;
     const int threads = v3 ? K3_THREADS : K2_THREADS;
     if (lds_bytes > st->max_lds) return HSES_ERR_UNSUPPORTED;
     K2Args A{};
     pair_range(P.tid_lo, P.n, &A.pair_lo, &A.n_pairs);
-    const int32_t grid = pair_grid(st, A.n_pairs);
+    int32_t grid = pair_grid(st, A.n_pairs);
+    // Pairs split over 4 workgroups of one XCD (the DL stream: drawn-ahead
+    // factors, so no per-pair generation is repeated, and K of more than two
+    // tiles; with resident tiles each part would restage them): every pair
+    // full (both members), its blocks a multiple of 4, and the grid a
+    // multiple of 32 workgroups.
+    A.split = 1;
+    if (dl && P.tid_lo % 2 == 0 && P.n % 2 == 0 && (2 * (int64_t)P.R) % (4 * K3_RB) == 0 &&
+        st->num_cus % 32 == 0 && (int64_t)A.n_pairs * 4 >= st->num_cus) {
+        A.split = 4;
+        grid = st->num_cus;
+    }
     A.group = v3 ? 1 : pair_group(P.a);
     const size_t need = pair_workspace_bytes(pre ? 0 : grid * A.group, P.a, P.b, P.r);
     if (!work || work_bytes < need)
@@ -1345,6 +1605,9 @@ int launch_linear_pair(LinParams& P, DeviceState* st, hipStream_t s, void* work,
         const int64_t g = P.x_fmt == HSES_FMT_F32 ? 4 : 8;  // elements per 16 bytes
         A.x_vec = (reinterpret_cast<uintptr_t>(P.x) % 16 == 0) && P.x_stride % g == 0 &&
                   P.x_plane % g == 0;
+        const int64_t words = (P.b + 63) / 64;
+        A.x_packed = bits && reinterpret_cast<uintptr_t>(P.x) % 16 == 0 && P.x_plane == words &&
+                     P.x_stride == (int64_t)P.n_time * words && ((int64_t)P.R * words) % 2 == 0;
     }
     const int64_t wl = (int64_t)P.a * lay.kp;
     hipLaunchKernelGGL(k_w_to_bf16, dim3((uint32_t)((wl + 255) / 256)), dim3(256), 0, s, P.W, P.a,
@@ -1359,25 +1622,27 @@ int launch_linear_pair(LinParams& P, DeviceState* st, hipStream_t s, void* work,
         return HSES_OK;
     };
     if (v3) {
-        auto by_pre = [&](auto pc) -> int {
-            constexpr bool PR = decltype(pc)::value;
-            if (!lif) return launch(k_pair_bits<EPI_Y, 1, false, false, PR>);
+        auto by_pre = [&](auto pc, auto dc) -> int {
+            constexpr bool PR = decltype(pc)::value, D = decltype(dc)::value;
+            if (!lif) return launch(k_pair_bits<EPI_Y, 1, false, false, PR, D>);
             const bool spk = lif->spk != nullptr, rate = lif->rate != nullptr;
             auto by_t = [&](auto sc, auto rc) -> int {
                 constexpr bool S = decltype(sc)::value, Q = decltype(rc)::value;
                 switch (P.n_time) {
-                    case 1: return launch(k_pair_bits<EPI_LIF, 1, S, Q, PR>);
-                    case 2: return launch(k_pair_bits<EPI_LIF, 2, S, Q, PR>);
-                    case 4: return launch(k_pair_bits<EPI_LIF, 4, S, Q, PR>);
-                    case 8: return launch(k_pair_bits<EPI_LIF, 8, S, Q, PR>);
-                    default: return launch(k_pair_bits<EPI_LIF, 16, S, Q, PR>);
+                    case 1: return launch(k_pair_bits<EPI_LIF, 1, S, Q, PR, D>);
+                    case 2: return launch(k_pair_bits<EPI_LIF, 2, S, Q, PR, D>);
+                    case 4: return launch(k_pair_bits<EPI_LIF, 4, S, Q, PR, D>);
+                    case 8: return launch(k_pair_bits<EPI_LIF, 8, S, Q, PR, D>);
+                    default: return launch(k_pair_bits<EPI_LIF, 16, S, Q, PR, D>);
                 }
             };
             if (spk && rate) return by_t(std::true_type{}, std::true_type{});
             if (spk) return by_t(std::true_type{}, std::false_type{});
             return by_t(std::false_type{}, std::true_type{});
         };
-        return pre ? by_pre(std::true_type{}) : by_pre(std::false_type{});
+        if (dl) return by_pre(std::true_type{}, std::true_type{});
+        return pre ? by_pre(std::true_type{}, std::false_type{})
+                   : by_pre(std::false_type{}, std::false_type{});
     }
     if (pre) {
         // dense input (the readout on spike rates) on the PRE form of k_linear_pair

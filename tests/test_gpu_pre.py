@@ -142,6 +142,7 @@ def make(cfg, ahead, seed=0, pool_size=3000):
     (dict(n=9, solver=SGD, lr=0.05), (0, 1, 2)),
     (dict(noise_reuse=1, solver=SGD, lr=0.05), (0, 1, 2, 3)),          # fresh noise every epoch
     (dict(noise_reuse=1), (0, 1, 5, 6, 6)),                           # skipped / repeated epochs
+    (dict(n=130, solver=SGD, lr=0.05), (0, 1)),    # 65 pairs: each pair split over 4 workgroups
 ])
 def test_snn_steps_drawn_ahead_equal_drawn_inline(hses_gpu, extra, epochs):
     cfg = dict(C3_SMALL, **extra)
