@@ -171,7 +171,7 @@ template <int T>
 __global__ __launch_bounds__(256) void k_poisson_sparse(
     const float* __restrict__ p, int64_t p_rows, const int32_t* __restrict__ prow, int64_t rows,
     int32_t in_dim, int64_t p_stride, uint32_t mix, uint64_t* __restrict__ out, int64_t out_stride,
-    int64_t plane) {
+    int64_t plane, int32_t vec) {
     static_assert(T >= 1 && T <= 32 && (T & (T - 1)) == 0, "T must be a power of two <= 32");
     constexpr int WPT = 64 / T;  // words per 64 x 64 transpose
     extern __shared__ __align__(16) unsigned char psm[];
@@ -187,43 +187,81 @@ __global__ __launch_bounds__(256) void k_poisson_sparse(
     const uint32_t idx0 = (uint32_t)(row * in_dim);
     constexpr uint32_t ALL = T == 32 ? 0xffffffffu : ((1u << T) - 1u);
 
-    // A. classify and compact; a batch of PB words' loads is in flight at once
-    constexpr int PB = 16;
+    // A. classify and compact.  Only the exact zeros and ones are decided here
+    // (p <= 0 or NaN: never fires; p >= 1: K = 2^23, every step fires, since
+    // RN32(m / D) < 1 for every m <= 2^23); an element with 0 < p < 1 parks the
+    // bits of p in its pattern slot and appends its column to the active list,
+    // and its threshold K(p) is computed in B.  With 16-byte rows (vec) each lane
+    // loads four consecutive columns at once, 256 columns per wave load.
     int32_t cnt = 0;
-    for (int32_t w0 = 0; w0 < words; w0 += PB) {
-        float pv[PB];
-#pragma unroll
-        for (int i = 0; i < PB; ++i) {  // every load in bounds, masked after
-            const int32_t col = (w0 + i) * 64 + lane;
-            pv[i] = prow_p[col < in_dim ? col : in_dim - 1];
+    auto classify = [&](int32_t col, float pv) -> uint32_t {
+        const bool full = pv >= 1.0f, act = pv > 0.0f && pv < 1.0f;
+        const uint64_t am = __ballot(act);
+        if (act) {
+            const int32_t pos = cnt + (int32_t)__builtin_amdgcn_mbcnt_hi(
+                                          (uint32_t)(am >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)am, 0u));
+            list[pos] = (uint16_t)col;
         }
+        cnt += (int32_t)__popcll(am);
+        return full ? ALL : (act ? __float_as_uint(pv) : 0u);
+    };
+    if (vec) {
+        const int32_t ncol = words * 64;  // pattern slots of the row (zero past in_dim)
+        constexpr int PB = 4;             // 1024 columns of loads in flight
+        for (int32_t c0 = 0; c0 < ncol; c0 += 256 * PB) {
+            float4 pv[PB];
 #pragma unroll
-        for (int i = 0; i < PB; ++i)
-            if (!src_ok || (w0 + i) * 64 + lane >= in_dim) pv[i] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < PB; ++i) {
-            if (w0 + i >= words) break;
-            const int32_t col = (w0 + i) * 64 + lane;
-            const uint32_t K = poisson_threshold(pv[i]);  // pv = 0 past the row: K = 0
-            const bool full = K >= 8388608u, act = K != 0u && !full;
-            pat[col] = full ? ALL : K;
-            const uint64_t am = __ballot(act);
-            if (act) {
-                const int32_t pos = cnt + (int32_t)__builtin_amdgcn_mbcnt_hi(
-                                              (uint32_t)(am >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)am, 0u));
-                list[pos] = (uint16_t)col;
+            for (int i = 0; i < PB; ++i) {  // every load in bounds, masked after
+                const int32_t col = c0 + 256 * i + 4 * lane;
+                pv[i] = reinterpret_cast<const float4*>(prow_p)[(col < in_dim ? col : in_dim - 4) >> 2];
+                if (!src_ok || col >= in_dim) pv[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             }
-            cnt += (int32_t)__popcll(am);
+#pragma unroll
+            for (int i = 0; i < PB; ++i) {
+                const int32_t col = c0 + 256 * i + 4 * lane;
+                if (c0 + 256 * i >= ncol) break;
+                uint4 pt;
+                pt.x = classify(col, pv[i].x);
+                pt.y = classify(col + 1, pv[i].y);
+                pt.z = classify(col + 2, pv[i].z);
+                pt.w = classify(col + 3, pv[i].w);
+                if (col < ncol) *reinterpret_cast<uint4*>(pat + col) = pt;
+            }
+        }
+    } else {
+        // a batch of PB words' loads is in flight at once
+        constexpr int PB = 16;
+        for (int32_t w0 = 0; w0 < words; w0 += PB) {
+            float pv[PB];
+#pragma unroll
+            for (int i = 0; i < PB; ++i) {  // every load in bounds, masked after
+                const int32_t col = (w0 + i) * 64 + lane;
+                pv[i] = prow_p[col < in_dim ? col : in_dim - 1];
+            }
+#pragma unroll
+            for (int i = 0; i < PB; ++i)
+                if (!src_ok || (w0 + i) * 64 + lane >= in_dim) pv[i] = 0.0f;
+#pragma unroll
+            for (int i = 0; i < PB; ++i) {
+                if (w0 + i >= words) break;
+                const int32_t col = (w0 + i) * 64 + lane;
+                pat[col] = classify(col, pv[i]);
+            }
         }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-    // B. the streams of the active elements
+    // B. the streams of the active elements: the exact threshold K(p), then
+    // the T steps of the element's xorshift32 stream.  Each step's bit enters
+    // at the bottom by one compare and one add-with-carry (pt + pt + carry),
+    // and the pattern is bit-reversed at the end.  K = 2^23 (p just below 1)
+    // fires every step.
     for (int32_t e = lane; e < cnt; e += 64) {
         const uint32_t col = list[e];
-        const uint32_t K9 = pat[col] << 9;  // (x >> 9) < K  <=>  x < K * 2^9 for K < 2^23
+        const uint32_t K = poisson_threshold(__uint_as_float(pat[col]));
+        const uint32_t K9 = K << 9;  // (x >> 9) < K  <=>  x < K * 2^9 for K < 2^23
         uint32_t x = 1000000007u * (idx0 + col) + mix + 0x9E3779B9u;
         uint32_t pt = 0;
 #pragma unroll
@@ -231,9 +269,13 @@ __global__ __launch_bounds__(256) void k_poisson_sparse(
             x ^= x << 13;
             x ^= x >> 17;
             x ^= x << 5;
-            pt |= (x < K9 ? 1u : 0u) << t;
+            asm("v_cmp_lt_u32 vcc, %1, %2\n\tv_addc_co_u32 %0, vcc, %0, %0, vcc"
+                : "+v"(pt)
+                : "v"(x), "v"(K9)
+                : "vcc");
         }
-        pat[col] = pt;
+        pt = __builtin_bitreverse32(pt) >> (32 - T);
+        pat[col] = K >= 8388608u ? ALL : pt;
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -492,10 +534,13 @@ extern "C" int hses_poisson_encode_planes(const float* d_p, int64_t p_rows, cons
                 const dim3 g((uint32_t)((rows + 3) / 4)), b(256);
                 uint64_t* o = static_cast<uint64_t*>(d_out);
                 const size_t lds = poisson_sparse_lds(in_dim);
+                // rows of whole 16-byte groups: four columns per lane and load
+                const int32_t vec = in_dim % 4 == 0 && p_stride % 4 == 0 &&
+                                    reinterpret_cast<uintptr_t>(d_p) % 16 == 0;
 #define HSES_PSPARSE(TV)                                                                        \
     case TV:                                                                                    \
         hipLaunchKernelGGL(k_poisson_sparse<TV>, g, b, lds, s, d_p, p_rows, d_rows, rows, in_dim, \
-                           p_stride, mix, o, out_stride, out_plane);                                       \
+                           p_stride, mix, o, out_stride, out_plane, vec);                          \
         break;
                 switch (T) {
                     HSES_PSPARSE(1)
