@@ -520,6 +520,8 @@ def main():
     ap.add_argument("--cpu-members", type=int, default=8192)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", choices=("c1", "c2", "c3", "c4", "c5"), default="c3")
+    ap.add_argument("--math", choices=("bf16", "f32x"), default="bf16",
+                    help="C3 forward arithmetic: bf16 MFMA, or fp32-accurate split fp16 operands")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one GPU "
@@ -533,7 +535,9 @@ def main():
     from hyperscalees_amd import kernels as K
     from hyperscalees_amd import snn
 
-    cfg = snn.SnnConfig(n=args.population, poisson_seed=(1, 2, 3, 4))
+    from hyperscalees_amd._lib import MATH_BF16, MATH_F32X
+    cfg = snn.SnnConfig(n=args.population, poisson_seed=(1, 2, 3, 4),
+                        math=MATH_F32X if args.math == "f32x" else MATH_BF16)
     pool_size = 60000
     pool, labels = snn.synthetic_pool(pool_size, cfg.dims[0], cfg.dims[-1], seed=0)
     idx = snn.sample_index(0, cfg.n, cfg.rows, pool_size)
@@ -581,13 +585,17 @@ def main():
     a1, b1 = es.W[0].shape
     draw = None
     if es.ahead:
+        img1 = es.img_x[0] if es.split else es.img[0]
         fc1_draw = lambda: K.pair_factors(cfg.keys[0], cfg.rank, cfg.sigma, 0, cfg.noise_reuse, 0,
-                                          cfg.n, a1, b1, es.rec[0], es.img[0])
+                                          cfg.n, a1, b1, es.rec[0], img1, split=es.split)
         draw_ms = _time_launch(fc1_draw, reps=3)
         normals = (cfg.n // 2) * cfg.rank * (a1 + b1)
-        wbytes = normals * 4 + (cfg.n // 2) * (cfg.rank * ((b1 + 63) // 64 * 64) + a1 * 136) * 2
+        parts = 2 if es.split else 1  # the split image holds high and low parts
+        wbytes = normals * 4 + parts * (cfg.n // 2) * (cfg.rank * ((b1 + 63) // 64 * 64)
+                                                       + a1 * 136) * 2
         draw = {"kernel": ("k_pair_gen (fc1 factors: every pair's exact Box-Muller normals into "
-                           "the factor record and the bf16 operand image)"),
+                           "the factor record and the "
+                           + ("split fp16 operand image)" if es.split else "bf16 operand image)")),
                 "bound": "valu", "launch_ms": round(draw_ms, 4), "normals_per_launch": normals,
                 "g_normals_per_s": round(normals / (draw_ms * 1e-3) / 1e9, 1),
                 "hbm_bytes_written": wbytes,
@@ -600,8 +608,9 @@ def main():
         if es.ahead:
             K.perturbed_linear_lif(es.spk[0], es.W[0], cfg.keys[0], cfg.rank, cfg.sigma, 0,
                                    cfg.noise_reuse, 0, cfg.n, cfg.rows, cfg.T, cfg.tau_m,
-                                   cfg.v_th, spikes=es.spk[1], rec=es.rec[0], img=es.img[0],
-                                   time_inner=es.time_inner)
+                                   cfg.v_th, spikes=es.spk[1], rec=es.rec[0],
+                                   img=img1,
+                                   time_inner=es.time_inner, math=cfg.math)
         elif es.fused:
             K.perturbed_linear_lif(es.spk[0], es.W[0], cfg.keys[0], cfg.rank, cfg.sigma, s,
                                    cfg.noise_reuse, 0, cfg.n, cfg.rows, cfg.T, cfg.tau_m,
@@ -645,8 +654,10 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": ("bf16 forward MFMA (fp32 accumulate); ES update as fp16 split-operand MFMA "
-                  "(hi*hi + hi*lo + lo*hi, fp32 accumulate; fp32-accurate)"),
+        "dtype": (("fp32-accurate forward: fp16 split-operand MFMA (hi*hi + hi*lo + lo*hi, fp32 "
+                   "accumulate)" if es.split else "bf16 forward MFMA (fp32 accumulate)")
+                  + "; ES update as fp16 split-operand MFMA (hi*hi + hi*lo + lo*hi, fp32 "
+                  "accumulate; fp32-accurate)"),
         "data": "synthetic",
         "config": {
             "workload": ("C3: SNN-MLP 784-128-128-128-10, LIF decay 0.9 v_th 1.0, Poisson T=16, "
@@ -662,14 +673,15 @@ def main():
                      "readout_fitness": round(float(t_readout), 3),
                      "forward": round(float(t_fwd), 3), "es_update": round(float(t_upd), 3)},
         "fwd_tflops": round(fwd_flops / (t_fwd * 1e-3) / 1e12, 1),
-        "roofline": {"kernel": (("k_pair_bits<LIF, T=16, spikes, factors drawn ahead> (fc1 GEMM: "
+        "roofline": {"kernel": (("k_pair_bits<LIF, T=16, spikes, factors drawn ahead"
+                                 + (", split fp16 operands" if es.split else "") + "> (fc1 GEMM: "
                                  if es.ahead else "k_pair_bits (fc1: ")
                                 + "x[W^T|B] + (xB)A^T, T=16 x 524288 rows"
                                 + (", LIF fused)" if es.fused else ")")),
                      "bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": (FC1_TRAFFIC_BYTES if es.ahead else None),
-                     "traffic_source": (FC1_TRAFFIC_SOURCE if es.ahead else None),
+                     "traffic": (FC1_TRAFFIC_BYTES if es.ahead and not es.split else None),
+                     "traffic_source": (FC1_TRAFFIC_SOURCE if es.ahead and not es.split else None),
                      "launch_ms": round(fc1_ms, 3),
                      "algorithmic_flop_per_launch": fc1_flops},
     }

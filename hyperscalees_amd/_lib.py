@@ -11,7 +11,7 @@ LIB_PATH = os.path.join(_HERE, "libhses.so")
 
 HSES_OK, HSES_ERR_INVALID_ARG, HSES_ERR_UNSUPPORTED, HSES_ERR_HIP, HSES_ERR_INTERNAL = range(5)
 FMT_F32, FMT_BF16, FMT_U8, FMT_BITS = range(4)
-MATH_F32, MATH_BF16 = range(2)
+MATH_F32, MATH_BF16, MATH_F32X = range(3)
 SGD, ADAM, ADAMW = range(3)
 REWARD_LOGLIK, REWARD_BINARY = range(2)
 ACT_NONE, ACT_TANH, ACT_SIGMOID, ACT_RELU_SQ = range(4)
@@ -71,6 +71,20 @@ PROTOTYPES = {
                                                      c_i32, c_f32, c_f32, c_vp, c_i64, c_i64,
                                                      c_vp, c_i64, c_vp, c_size, c_vp, c_size,
                                                      c_vp, c_size, c_vp]),
+    "hses_pair_image_x_bytes": (c_size, [c_i32, c_i32, c_i32, c_i32, c_i32]),
+    "hses_pair_factors_x": (ctypes.c_int, [c_u64, c_i32, c_f32, c_i32, c_i32, c_i32, c_i32, c_i32,
+                                           c_i32, c_vp, c_size, c_vp, c_size, c_vp]),
+    "hses_pair_image_x": (ctypes.c_int, [c_i32, c_i32, c_i32, c_f32, c_i32, c_i32, c_vp, c_size,
+                                         c_vp, c_size, c_vp]),
+    "hses_perturbed_linear_pre_x": (ctypes.c_int, [c_vp, c_i32, c_i64, c_i64, c_i32, c_vp, c_i32,
+                                                   c_i32, c_i32, c_f32, c_i32, c_i32, c_i32, c_vp,
+                                                   c_i64, c_i64, c_vp, c_size, c_vp, c_size, c_vp,
+                                                   c_size, c_vp]),
+    "hses_perturbed_linear_lif_pre_x": (ctypes.c_int, [c_vp, c_i32, c_i64, c_i64, c_i32, c_vp,
+                                                       c_i32, c_i32, c_i32, c_f32, c_i32, c_i32,
+                                                       c_i32, c_f32, c_f32, c_vp, c_i64, c_i64,
+                                                       c_vp, c_i64, c_vp, c_size, c_vp, c_size,
+                                                       c_vp, c_size, c_vp]),
     "hses_perturbed_linear_t": (ctypes.c_int, [c_vp, c_i32, c_i64, c_i64, c_i32, c_vp, c_i32,
                                                c_i32, c_u64, c_i32, c_f32, c_i32, c_i32, c_i32,
                                                c_i32, c_i32, c_vp, c_i64, c_i64, c_i32, c_vp,

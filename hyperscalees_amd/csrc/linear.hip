@@ -240,7 +240,7 @@ extern "C" size_t hses_perturbed_linear_workspace(int32_t a, int32_t b, int32_t 
     if (math == HSES_MATH_F32)  // the fp32 GEMM's factor rows (k_linear_small needs none)
         return linear_f32_workspace(a, b, rank, n, rows_per_member, n_time, math);
     if (a < 1 || b < 1 || n < 1 || rank < 16 || rank % 16 || rank > 128 || a > 128 ||
-        math != HSES_MATH_BF16)
+        (math != HSES_MATH_BF16 && math != HSES_MATH_F32X))
         // the bf16 GEMM (bf16 W, factor rows), the wide-output kernel (bf16 W) or
         // k_linear_small (no workspace)
         return std::max(linear_bf16_workspace(a, b, rank, n, rows_per_member, n_time, math),
@@ -550,7 +550,8 @@ static int linear_lif_impl(const void* d_x, int32_t x_fmt, int64_t x_stride, int
                            float v_th, uint64_t* d_spikes, int64_t spk_stride, int64_t spk_plane,
                            float* d_rate, int64_t rate_stride, void* d_work, size_t work_bytes,
                            float* d_rec, size_t rec_bytes, void* stream,
-                           const uint16_t* d_img = nullptr, size_t img_bytes = 0) {
+                           const uint16_t* d_img = nullptr, size_t img_bytes = 0,
+                           bool split = false) {
     HSES_REQUIRE(tau_m != 0.0f, "tau_m must be non-zero");
     LinParams P;
     DeviceState* st = nullptr;
@@ -562,11 +563,12 @@ static int linear_lif_impl(const void* d_x, int32_t x_fmt, int64_t x_stride, int
         if (rc) return rc;
         P.rec = d_rec;
     }
-    if (d_img) {
+    if (d_img && !split) {
         HSES_REQUIRE(img_bytes >= pair_image_bytes(a, b, P.r, tid_lo, n),
                      "hses_perturbed_linear_lif_pre: operand image smaller than "
                      "hses_pair_image_bytes");
     }
+    if (split) P.math = HSES_MATH_F32X;
     HSES_REQUIRE(d_spikes || d_rate, "spikes and rate are both NULL");
     const int64_t M = (int64_t)n * rows_per_member;
     HSES_REQUIRE(!d_spikes || rows_layout_ok((a + 63) / 64, M, n_time, spk_stride, spk_plane),
@@ -580,9 +582,11 @@ static int linear_lif_impl(const void* d_x, int32_t x_fmt, int64_t x_stride, int
     rc = launch_linear_pair(P, st, (hipStream_t)stream, d_work, work_bytes, &lif, d_img);
     if (rc == HSES_ERR_UNSUPPORTED)
         return set_error(HSES_ERR_UNSUPPORTED,
-                         d_img ? "hses_perturbed_linear_lif_pre: needs rank a multiple of 16 <= 128, "
-                                 "a <= 128, n_time <= 16 and b <= 1024"
-                               : "hses_perturbed_linear_lif: needs rank a multiple of 16 <= 128 and a <= 128");
+                         split ? "hses_perturbed_linear_lif_pre_x: needs rank a multiple of 16 <= 128, "
+                                 "a <= 128, n_time <= 16 and b <= 896"
+                         : d_img ? "hses_perturbed_linear_lif_pre: needs rank a multiple of 16 <= 128, "
+                                   "a <= 128, n_time <= 16 and b <= 1024"
+                                 : "hses_perturbed_linear_lif: needs rank a multiple of 16 <= 128 and a <= 128");
     return rc;
 }
 
@@ -629,7 +633,7 @@ extern "C" int hses_perturbed_linear_lif_rec(const void* d_x, int32_t x_fmt, int
 // arguments alone (before the device is touched).
 static int check_drawn(int32_t a, int32_t b, int32_t rank, float sigma, int32_t tid_lo, int32_t n,
                        const float* d_rec, size_t rec_bytes, const void* d_img, size_t img_bytes,
-                       const char* name) {
+                       const char* name, bool split = false) {
     const int32_t r = (sigma != 0.0f) ? rank : 0;
     HSES_REQUIRE(a >= 1 && a <= 128,
                  std::string(name) + ": output width a must be in [1, 128] (the pair kernels)");
@@ -640,8 +644,12 @@ static int check_drawn(int32_t a, int32_t b, int32_t rank, float sigma, int32_t 
     HSES_REQUIRE(rec_bytes >= hses_factor_record_bytes(a, b, r, tid_lo, n),
                  std::string(name) + ": factor record smaller than hses_factor_record_bytes");
     HSES_REQUIRE(d_img, std::string(name) + ": operand image is NULL");
-    HSES_REQUIRE(img_bytes >= pair_image_bytes(a, b, r, tid_lo, n),
-                 std::string(name) + ": operand image smaller than hses_pair_image_bytes");
+    if (split)
+        HSES_REQUIRE(img_bytes >= pair_image_x_bytes(a, b, r, tid_lo, n),
+                     std::string(name) + ": operand image smaller than hses_pair_image_x_bytes");
+    else
+        HSES_REQUIRE(img_bytes >= pair_image_bytes(a, b, r, tid_lo, n),
+                     std::string(name) + ": operand image smaller than hses_pair_image_bytes");
     return HSES_OK;
 }
 
@@ -651,16 +659,16 @@ extern "C" size_t hses_pair_image_bytes(int32_t a, int32_t b, int32_t rank, int3
     return pair_image_bytes(a, b, rank, tid_lo, n);
 }
 
-extern "C" int hses_pair_factors(uint64_t key, int32_t rank, float sigma, int32_t epoch,
-                                 int32_t noise_reuse, int32_t tid_lo, int32_t n, int32_t a,
-                                 int32_t b, float* d_rec, size_t rec_bytes, uint16_t* d_img,
-                                 size_t img_bytes, void* stream) {
+static int pair_factors_impl(uint64_t key, int32_t rank, float sigma, int32_t epoch,
+                             int32_t noise_reuse, int32_t tid_lo, int32_t n, int32_t a, int32_t b,
+                             float* d_rec, size_t rec_bytes, uint16_t* d_img, size_t img_bytes,
+                             void* stream, bool split) {
     HSES_REQUIRE(a >= 1 && b >= 1 && n >= 0 && rank >= 0, "bad sizes");
     HSES_REQUIRE(noise_reuse >= 0, "noise_reuse must be >= 0");
     HSES_REQUIRE(tid_lo >= 0 && (int64_t)tid_lo + n - 1 <= INT32_MAX, "thread id range");
     if (n == 0) return HSES_OK;
     int rc = check_drawn(a, b, rank, sigma, tid_lo, n, d_rec, rec_bytes, d_img, img_bytes,
-                         "hses_pair_factors");
+                         split ? "hses_pair_factors_x" : "hses_pair_factors", split);
     if (rc) return rc;
     DeviceState* st;
     rc = get_state(&st);
@@ -680,20 +688,27 @@ extern "C" int hses_pair_factors(uint64_t key, int32_t rank, float sigma, int32_
     P.log_exc = st->d_log_exc;
     P.cos_exc = st->d_cos_exc;
     P.rec = d_rec;
-    return launch_pair_gen(P, st, (hipStream_t)stream, d_img);
+    return launch_pair_gen(P, st, (hipStream_t)stream, d_img, split);
 }
 
-extern "C" int hses_perturbed_linear_pre(const void* d_x, int32_t x_fmt, int64_t x_stride,
-                                         int64_t x_plane, int32_t n_time, const float* d_W,
-                                         int32_t a, int32_t b, int32_t rank, float sigma,
-                                         int32_t tid_lo, int32_t n, int32_t rows_per_member,
-                                         float* d_y, int64_t y_stride, int64_t y_plane,
-                                         void* d_work, size_t work_bytes, const float* d_rec,
-                                         size_t rec_bytes, const uint16_t* d_img,
-                                         size_t img_bytes, void* stream) {
+extern "C" int hses_pair_factors(uint64_t key, int32_t rank, float sigma, int32_t epoch,
+                                 int32_t noise_reuse, int32_t tid_lo, int32_t n, int32_t a,
+                                 int32_t b, float* d_rec, size_t rec_bytes, uint16_t* d_img,
+                                 size_t img_bytes, void* stream) {
+    return pair_factors_impl(key, rank, sigma, epoch, noise_reuse, tid_lo, n, a, b, d_rec,
+                             rec_bytes, d_img, img_bytes, stream, false);
+}
+
+static int linear_pre_impl(const void* d_x, int32_t x_fmt, int64_t x_stride, int64_t x_plane,
+                           int32_t n_time, const float* d_W, int32_t a, int32_t b, int32_t rank,
+                           float sigma, int32_t tid_lo, int32_t n, int32_t rows_per_member,
+                           float* d_y, int64_t y_stride, int64_t y_plane, void* d_work,
+                           size_t work_bytes, const float* d_rec, size_t rec_bytes,
+                           const uint16_t* d_img, size_t img_bytes, void* stream, bool split) {
+    const char* name = split ? "hses_perturbed_linear_pre_x" : "hses_perturbed_linear_pre";
     if (n > 0 && tid_lo >= 0) {
         const int rc0 = check_drawn(a, b, rank, sigma, tid_lo, n, d_rec, rec_bytes, d_img,
-                                    img_bytes, "hses_perturbed_linear_pre");
+                                    img_bytes, name, split);
         if (rc0) return rc0;
     }
     LinParams P;
@@ -708,12 +723,28 @@ extern "C" int hses_perturbed_linear_pre(const void* d_x, int32_t x_fmt, int64_t
     P.y_stride = y_stride;
     P.y_plane = y_plane;
     P.rec = const_cast<float*>(d_rec);
+    if (split) P.math = HSES_MATH_F32X;
     rc = launch_linear_pair(P, st, (hipStream_t)stream, d_work, work_bytes, nullptr, d_img);
     if (rc == HSES_ERR_UNSUPPORTED)
         return set_error(HSES_ERR_UNSUPPORTED,
-                         "hses_perturbed_linear_pre: needs the pair kernels (a <= 128, rank a "
-                         "multiple of 16 in [32, 128])");
+                         split ? "hses_perturbed_linear_pre_x: needs bit-packed x (x_fmt BITS), "
+                                 "a <= 128, rank a multiple of 16 in [32, 128] and b <= 896"
+                               : "hses_perturbed_linear_pre: needs the pair kernels (a <= 128, rank a "
+                                 "multiple of 16 in [32, 128])");
     return rc;
+}
+
+extern "C" int hses_perturbed_linear_pre(const void* d_x, int32_t x_fmt, int64_t x_stride,
+                                         int64_t x_plane, int32_t n_time, const float* d_W,
+                                         int32_t a, int32_t b, int32_t rank, float sigma,
+                                         int32_t tid_lo, int32_t n, int32_t rows_per_member,
+                                         float* d_y, int64_t y_stride, int64_t y_plane,
+                                         void* d_work, size_t work_bytes, const float* d_rec,
+                                         size_t rec_bytes, const uint16_t* d_img,
+                                         size_t img_bytes, void* stream) {
+    return linear_pre_impl(d_x, x_fmt, x_stride, x_plane, n_time, d_W, a, b, rank, sigma, tid_lo,
+                           n, rows_per_member, d_y, y_stride, y_plane, d_work, work_bytes, d_rec,
+                           rec_bytes, d_img, img_bytes, stream, false);
 }
 
 extern "C" int hses_perturbed_linear_lif_pre(const void* d_x, int32_t x_fmt, int64_t x_stride,
@@ -735,6 +766,70 @@ extern "C" int hses_perturbed_linear_lif_pre(const void* d_x, int32_t x_fmt, int
                            tid_lo, n, rows_per_member, tau_m, v_th, d_spikes, spk_stride,
                            spk_plane, d_rate, rate_stride, d_work, work_bytes,
                            const_cast<float*>(d_rec), rec_bytes, stream, d_img, img_bytes);
+}
+
+// ---- the split (fp32-accurate) forwards -------------------------------------
+// The *_pre forwards on a split operand image (hses_pair_image_x) and W split
+// the same way, as fp16 MFMA products of high and low parts.
+
+extern "C" size_t hses_pair_image_x_bytes(int32_t a, int32_t b, int32_t rank, int32_t tid_lo,
+                                          int32_t n) {
+    if (a < 1 || b < 1 || rank < 1 || tid_lo < 0 || n < 1) return 0;
+    return pair_image_x_bytes(a, b, rank, tid_lo, n);
+}
+
+extern "C" int hses_pair_image_x(int32_t a, int32_t b, int32_t rank, float sigma, int32_t tid_lo,
+                                 int32_t n, const float* d_rec, size_t rec_bytes, uint16_t* d_img,
+                                 size_t img_bytes, void* stream) {
+    HSES_REQUIRE(a >= 1 && b >= 1 && n >= 0 && rank >= 0, "bad sizes");
+    HSES_REQUIRE(tid_lo >= 0 && (int64_t)tid_lo + n - 1 <= INT32_MAX, "thread id range");
+    if (n == 0) return HSES_OK;
+    int rc = check_drawn(a, b, rank, sigma, tid_lo, n, d_rec, rec_bytes, d_img, img_bytes,
+                         "hses_pair_image_x", true);
+    if (rc) return rc;
+    DeviceState* st;
+    rc = get_state(&st);
+    if (rc) return rc;
+    return launch_pair_image_x(d_rec, a, b, rank, sigma / sqrtf((float)rank) /* eggroll.rs:433 */,
+                               tid_lo, n, d_img, (hipStream_t)stream);
+}
+
+extern "C" int hses_pair_factors_x(uint64_t key, int32_t rank, float sigma, int32_t epoch,
+                                   int32_t noise_reuse, int32_t tid_lo, int32_t n, int32_t a,
+                                   int32_t b, float* d_rec, size_t rec_bytes, uint16_t* d_img,
+                                   size_t img_bytes, void* stream) {
+    return pair_factors_impl(key, rank, sigma, epoch, noise_reuse, tid_lo, n, a, b, d_rec,
+                             rec_bytes, d_img, img_bytes, stream, true);
+}
+
+extern "C" int hses_perturbed_linear_pre_x(const void* d_x, int32_t x_fmt, int64_t x_stride,
+                                           int64_t x_plane, int32_t n_time, const float* d_W,
+                                           int32_t a, int32_t b, int32_t rank, float sigma,
+                                           int32_t tid_lo, int32_t n, int32_t rows_per_member,
+                                           float* d_y, int64_t y_stride, int64_t y_plane,
+                                           void* d_work, size_t work_bytes, const float* d_rec,
+                                           size_t rec_bytes, const uint16_t* d_img,
+                                           size_t img_bytes, void* stream) {
+    return linear_pre_impl(d_x, x_fmt, x_stride, x_plane, n_time, d_W, a, b, rank, sigma, tid_lo,
+                           n, rows_per_member, d_y, y_stride, y_plane, d_work, work_bytes, d_rec,
+                           rec_bytes, d_img, img_bytes, stream, true);
+}
+
+extern "C" int hses_perturbed_linear_lif_pre_x(
+    const void* d_x, int32_t x_fmt, int64_t x_stride, int64_t x_plane, int32_t n_time,
+    const float* d_W, int32_t a, int32_t b, int32_t rank, float sigma, int32_t tid_lo, int32_t n,
+    int32_t rows_per_member, float tau_m, float v_th, uint64_t* d_spikes, int64_t spk_stride,
+    int64_t spk_plane, float* d_rate, int64_t rate_stride, void* d_work, size_t work_bytes,
+    const float* d_rec, size_t rec_bytes, const uint16_t* d_img, size_t img_bytes, void* stream) {
+    if (n > 0 && tid_lo >= 0) {
+        const int rc = check_drawn(a, b, rank, sigma, tid_lo, n, d_rec, rec_bytes, d_img,
+                                   img_bytes, "hses_perturbed_linear_lif_pre_x", true);
+        if (rc) return rc;
+    }
+    return linear_lif_impl(d_x, x_fmt, x_stride, x_plane, n_time, d_W, a, b, 0, rank, sigma, 0, 0,
+                           tid_lo, n, rows_per_member, tau_m, v_th, d_spikes, spk_stride,
+                           spk_plane, d_rate, rate_stride, d_work, work_bytes,
+                           const_cast<float*>(d_rec), rec_bytes, stream, d_img, img_bytes, true);
 }
 
 extern "C" int hses_perturbed_linear_act(const void* d_x, int32_t x_fmt, int64_t x_stride,

@@ -125,6 +125,22 @@ __device__ __forceinline__ u16x8 expand_bits(uint32_t byte) {
     return v;
 }
 
+// The same as fp16 1.0 / 0.0 (0x3C00 has its low ten bits clear, so the
+// multiplies by 0x3C00 >> 2q stay exact).
+__device__ __forceinline__ u16x8 expand_bits_f16(uint32_t byte) {
+    const uint32_t y = byte | (byte << 15);
+    uint32_t d[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) d[q] = __umul24(y & (0x10001u << (2 * q)), 0x3C00u >> (2 * q));
+    u16x8 v;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        v[2 * q] = (uint16_t)d[q];
+        v[2 * q + 1] = (uint16_t)(d[q] >> 16);
+    }
+    return v;
+}
+
 // Fused LIF output of the large-rank kernel (see hses_perturbed_linear_lif).
 struct LifOut {
     void* spk;  // bit-packed spikes (T, M, words) or NULL
@@ -156,9 +172,17 @@ int launch_linear_pair(LinParams& P, DeviceState* st, hipStream_t s, void* work,
                        const LifOut* lif = nullptr, const uint16_t* bimg = nullptr);
 size_t linear_pair_workspace(const DeviceState* st, int32_t a, int32_t b, int32_t r, int32_t n);
 // Every pair's factors of members [tid_lo, tid_lo + n) into the record P.rec
-// and the bf16 B operand image bimg (pair_image_bytes bytes).
-int launch_pair_gen(LinParams& P, DeviceState* st, hipStream_t s, uint16_t* bimg);
+// and the bf16 operand image bimg (pair_image_bytes bytes), or with split
+// the split operand image (pair_image_x_bytes bytes).
+int launch_pair_gen(LinParams& P, DeviceState* st, hipStream_t s, uint16_t* bimg,
+                    bool split = false);
 size_t pair_image_bytes(int32_t a, int32_t b, int32_t r, int32_t tid_lo, int32_t n);
+// The split (HSES_MATH_F32X) operand image of members [tid_lo, tid_lo + n)
+// from their factor record rec (do_mm, scale bs on the output side), and its
+// size.  launch_linear_pair with P.math = HSES_MATH_F32X takes it as bimg.
+int launch_pair_image_x(const float* rec, int32_t a, int32_t b, int32_t r, float bs, int32_t tid_lo,
+                        int32_t n, uint16_t* img, hipStream_t s);
+size_t pair_image_x_bytes(int32_t a, int32_t b, int32_t r, int32_t tid_lo, int32_t n);
 // The wide small-rank kernel: 0 when it does not apply to the shape, else its
 // workspace (W as bf16, (a, kp)).
 size_t linear_wide_workspace(int32_t a, int32_t b, int32_t r, int32_t n, int32_t rows_per_member,

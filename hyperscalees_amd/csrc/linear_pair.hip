@@ -88,6 +88,25 @@ struct PairImage {
     }
 };
 
+// Split operand image of one pair (the fp32-accurate mode, HSES_MATH_F32X):
+// each operand as a high and a low fp16 part, x = hi + lo to about 2^-22 of
+// x (hi the fp16 rounding, lo the fp16 rounding of the remainder; x in
+// {0, 1} is exact in fp16).  B_hi, B_lo as [c][kp] (zero for k >= b), then
+// A_hi, A_lo as [o][swap23(c)] rows of K2_NMAX + 8 (zero for rank columns
+// [r, r rounded up to 32)), A scaled by K3_XSCALE.  Elements per pair: stride.
+struct PairImageX {
+    size_t b_elems, a_elems, stride;
+    __host__ __device__ PairImageX(int a, int b, int r) {
+        b_elems = (size_t)r * ((b + 63) / 64 * 64);
+        a_elems = (size_t)a * (K2_NMAX + 8);
+        stride = 2 * b_elems + 2 * a_elems;
+    }
+};
+// W and A enter the split products scaled by 2^10 (B and x B unscaled), so
+// that A's low parts stay in fp16's normal range; the currents are the
+// accumulators times 2^-10 (exact).
+constexpr float K3_XSCALE = 1024.0f;
+
 struct K2Args {
     const void* x;
     int64_t x_stride, x_plane;
@@ -193,6 +212,14 @@ __global__ void k_w_to_bf16(const float* __restrict__ W, int32_t a, int32_t b, i
     out[i] = k < b ? f2bf(W[src]) : (uint16_t)0;
 }
 
+// fp32 -> fp16 high part and fp16 low part (round to nearest even both):
+// hi + lo is v to about 2^-22 of v (v - hi is exact in fp32).
+__device__ __forceinline__ void split_f16(float v, uint16_t* hi, uint16_t* lo) {
+    const _Float16 h = (_Float16)v;
+    *hi = __builtin_bit_cast(uint16_t, h);
+    *lo = __builtin_bit_cast(uint16_t, (_Float16)(v - (float)h));
+}
+
 // Factors of the pair kernels drawn ahead of their GEMM (the PRE kernels):
 // one thread per (pair, stream row) continues its row of the pair's stream
 // for r normals, keeps each raw normal in the factor record and its scaled
@@ -201,8 +228,11 @@ __global__ void k_w_to_bf16(const float* __restrict__ W, int32_t a, int32_t b, i
 // row's rank padding.  Lanes take consecutive stream rows, so for each rank
 // column a wave's record stores and input-side image stores are contiguous
 // runs.  Full occupancy (256-thread workgroups, no other work) keeps the
-// VALU-bound generator at its rate.
+// VALU-bound generator at its rate.  X: the split image (PairImageX) instead,
+// each value's fp16 high and low parts, A scaled by K3_XSCALE (the same
+// values k_pair_image_x derives from the record).
 constexpr int KG_THREADS = 256;
+template <bool X = false>
 __global__ __launch_bounds__(KG_THREADS) void k_pair_gen(const K2Args P) {
     __shared__ BmTables t;
     load_bm_tables(&t, P.tables);
@@ -219,22 +249,54 @@ __global__ __launch_bounds__(KG_THREADS) void k_pair_gen(const K2Args P) {
     const StreamRow sr(P, (int32_t)j);
     float* rp = P.rec + (size_t)pi * r * rows + j;
     const PairImage im(P.a, P.b, r);
-    uint16_t* img = P.bimg + (size_t)pi * im.stride;
+    const PairImageX imx(P.a, P.b, r);
+    uint16_t* img = P.bimg + (size_t)pi * (X ? imx.stride : im.stride);
+    const size_t b_elems = X ? imx.b_elems : im.b_elems;
+    // X: the low parts at `lo_off` elements after the high parts
+    const size_t lo_off = sr.in_side ? imx.b_elems : imx.a_elems;
     // input side: element c at bp[c * kp]; output side: at bp[swap23(c)], where
     // swap23 keeps every aligned run of 4 rank columns contiguous, so an
     // output-side row stores each batch of 4 normals as one 8-byte write
-    uint16_t* bp = sr.in_side ? img + sr.row : img + im.b_elems + (size_t)sr.row * (K2_NMAX + 8);
+    uint16_t* bp = sr.in_side ? img + sr.row : img + (X ? 2 : 1) * b_elems + (size_t)sr.row * (K2_NMAX + 8);
+    // X: A (the output side) scaled by K3_XSCALE after the sigma scale
+    const float xs = (X && !sr.in_side) ? K3_XSCALE : 1.0f;
     const NoiseCtx ctx{&t, P.log_exc, P.cos_exc};
     auto one = [&](int32_t c, float v) {
         rp[(size_t)c * rows] = v;
-        bp[sr.in_side ? (size_t)c * kp : (size_t)swap23(c)] = f2bf(v * sr.scale);
+        const size_t at = sr.in_side ? (size_t)c * kp : (size_t)swap23(c);
+        if constexpr (X) {
+            uint16_t hi, lo;
+            split_f16(v * sr.scale * xs, &hi, &lo);
+            bp[at] = hi;
+            bp[at + lo_off] = lo;
+        } else {
+            bp[at] = f2bf(v * sr.scale);
+        }
     };
     bm_run2(
         s, r, ctx,
         [&](int32_t c0, const float (&v)[4]) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) rp[(size_t)(c0 + q) * rows] = v[q];
-            if (sr.in_side) {
+            if constexpr (X) {
+                uint16_t hi[4], lo[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) split_f16(v[q] * sr.scale * xs, &hi[q], &lo[q]);
+                if (sr.in_side) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        bp[(size_t)(c0 + q) * kp] = hi[q];
+                        bp[(size_t)(c0 + q) * kp + lo_off] = lo[q];
+                    }
+                } else {
+                    const uint2 wh{(uint32_t)hi[0] | ((uint32_t)hi[1] << 16),
+                                   (uint32_t)hi[2] | ((uint32_t)hi[3] << 16)};
+                    const uint2 wl{(uint32_t)lo[0] | ((uint32_t)lo[1] << 16),
+                                   (uint32_t)lo[2] | ((uint32_t)lo[3] << 16)};
+                    *reinterpret_cast<uint2*>(bp + swap23(c0)) = wh;
+                    *reinterpret_cast<uint2*>(bp + swap23(c0) + lo_off) = wl;
+                }
+            } else if (sr.in_side) {
 #pragma unroll
                 for (int q = 0; q < 4; ++q) bp[(size_t)(c0 + q) * kp] = f2bf(v[q] * sr.scale);
             } else {
@@ -245,9 +307,15 @@ __global__ __launch_bounds__(KG_THREADS) void k_pair_gen(const K2Args P) {
         },
         one);
     if (!sr.in_side) {
-        for (int32_t c = r; c < ((r + 31) & ~31); ++c) bp[c] = 0;  // swap23 keeps 16-blocks
+        for (int32_t c = r; c < ((r + 31) & ~31); ++c) {  // swap23 keeps 16-blocks
+            bp[c] = 0;
+            if constexpr (X) bp[c + lo_off] = 0;
+        }
         for (int32_t k = P.b + sr.row; k < kp; k += P.a)
-            for (int32_t c = 0; c < r; ++c) img[(size_t)c * kp + k] = 0;
+            for (int32_t c = 0; c < r; ++c) {
+                img[(size_t)c * kp + k] = 0;
+                if constexpr (X) img[b_elems + (size_t)c * kp + k] = 0;
+            }
     }
 }
 
@@ -257,6 +325,56 @@ void launch_w_to_bf16(const float* W, int32_t a, int32_t b, int32_t kp, int32_t 
     hipLaunchKernelGGL(k_w_to_bf16, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, s, W, a, b, kp,
                        tmm, out);
 }
+
+
+// The split mode's W: (a, b) fp32 times K3_XSCALE as a high part (a, kp) and
+// then a low part (a, kp), fp16, zero columns [b, kp).
+// (do_mm only: W stored (a, b).)
+__global__ void k_w_to_f16x(const float* __restrict__ W, int32_t a, int32_t b, int32_t kp,
+                            uint16_t* __restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t n = (int64_t)a * kp;
+    if (i >= n) return;
+    const int32_t row = (int32_t)(i / kp), k = (int32_t)(i % kp);
+    uint16_t hi = 0, lo = 0;
+    if (k < b) split_f16(W[(int64_t)row * b + k] * K3_XSCALE, &hi, &lo);
+    out[i] = hi;
+    out[n + i] = lo;
+}
+
+// The split operand image (PairImageX) of every pair from the factor record
+// (the raw normals; do_mm: stream rows [0, b) are B, [b, a + b) are A and
+// carry the scale bs = sigma / sqrt(r) as the forward applies it, one fp32
+// product).  Element e of a pair: e < r kp the B element (c, k) = (e / kp,
+// e % kp), zero for k >= b; after that the A element (o, c) of a rows of
+// r rounded up to 32, zero for c >= r.
+__global__ void k_pair_image_x(const float* __restrict__ rec, int32_t a, int32_t b, int32_t r,
+                               float bs, int32_t n_pairs, uint16_t* __restrict__ img) {
+    const int32_t kp = (b + 63) / 64 * 64, rp32 = (r + 31) & ~31;
+    const int64_t per = (int64_t)r * kp + (int64_t)a * rp32;
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= per * n_pairs) return;
+    const int64_t pi = i / per;
+    const int64_t e = i - pi * per;
+    const PairImageX im(a, b, r);
+    uint16_t* dst = img + pi * im.stride;
+    const float* rp = rec + pi * r * (int64_t)(a + b);
+    uint16_t hi = 0, lo = 0;
+    if (e < (int64_t)r * kp) {
+        const int32_t c = (int32_t)(e / kp), k = (int32_t)(e % kp);
+        if (k < b) split_f16(rp[(int64_t)c * (a + b) + k], &hi, &lo);
+        dst[e] = hi;
+        dst[im.b_elems + e] = lo;
+    } else {
+        const int64_t ea = e - (int64_t)r * kp;
+        const int32_t o = (int32_t)(ea / rp32), c = (int32_t)(ea % rp32);
+        if (c < r) split_f16(rp[(int64_t)c * (a + b) + b + o] * bs * K3_XSCALE, &hi, &lo);
+        const size_t at = 2 * im.b_elems + (size_t)o * (K2_NMAX + 8) + swap23(c);
+        dst[at] = hi;
+        dst[at + im.a_elems] = lo;
+    }
+}
+
 
 
 // Eight activations of one row from a dense format, as bf16.  With vec
@@ -773,6 +891,22 @@ __device__ __forceinline__ f32x16 mfma32_bf16(const u16x8& a, const u16x8& b, f3
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ f32x16 mfma32_f16(const u16x8& a, const u16x8& b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+// Two floats as packed fp16 high parts and packed fp16 low parts (split_f16
+// on each).
+__device__ __forceinline__ void split_f16x2(float v0, float v1, uint32_t* hi, uint32_t* lo) {
+    uint16_t h0, l0, h1, l1;
+    split_f16(v0, &h0, &l0);
+    split_f16(v1, &h1, &l1);
+    *hi = (uint32_t)h0 | ((uint32_t)h1 << 16);
+    *lo = (uint32_t)l0 | ((uint32_t)l1 << 16);
+}
+
 // Direct-to-LDS tiles (DL): K3_DLBUF unpadded tile buffers of K2_COLS
 // columns x K2_BK k (128 bytes per column), filled by LDS DMA (each lane's
 // 16-byte chunk lands at the wave's base + 16 x lane).  A column's eight
@@ -785,18 +919,19 @@ constexpr int K3_DLTILE = K2_COLS * K2_BK;  // bf16 elements per DL tile buffer
 struct K3Layout {
     size_t off_a, off_xbits, off_wb, bytes;
     int32_t apitch, words, kp;
-    // dl: the DL form (factors drawn ahead, so no noise tables)
-    __host__ __device__ K3Layout(int r, int b, bool dl = false) {
+    // dl: the DL form (factors drawn ahead, so no noise tables); x: the
+    // split (fp32-accurate) form, A as high and low parts and two DL buffers
+    __host__ __device__ K3Layout(int r, int b, bool dl = false, bool x = false) {
         apitch = K3_AP;
         words = (b + 63) / 64;
         kp = words * 64;
         size_t o = dl ? 0 : align16(sizeof(BmTables));
         off_a = o;
-        o = align16(o + (size_t)K2_NMAX * apitch * 2);
+        o = align16(o + (size_t)(x ? 2 : 1) * K2_NMAX * apitch * 2);
         off_xbits = o;
         o = align16(o + (size_t)K3_RB * words * 8);
         off_wb = o;
-        bytes = o + (dl ? (size_t)K3_DLBUF * K3_DLTILE * 2 : (size_t)2 * K2_COLS * K2_TP * 2);
+        bytes = o + (dl ? (size_t)(x ? 2 : K3_DLBUF) * K3_DLTILE * 2 : (size_t)2 * K2_COLS * K2_TP * 2);
     }
 };
 
@@ -830,12 +965,20 @@ __device__ __forceinline__ void wait_vmcnt() {
 // DL (with PRE, K of more than two tiles): the W/B tiles stream into three
 // LDS buffers by LDS DMA, two tiles ahead of the MFMAs, instead of through
 // registers; the stream runs on across blocks and pairs.
-template <int EPI, int LT, bool SPK, bool RATE, bool PRE = false, bool DL = false>
+// X (with DL): the split fp16 operands of the fp32-accurate mode (P.bimg a
+// PairImageX image, P.wbf W's high then low part, scaled): each K tile is
+// taken twice, its high and its low part (two DL buffers; each transfer is
+// issued right after the barrier that frees its buffer, one tile ahead), and
+// the second product is (xB)_hi A_hi + (xB)_lo A_hi + (xB)_hi A_lo.
+template <int EPI, int LT, bool SPK, bool RATE, bool PRE = false, bool DL = false, bool X = false>
 __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
     static_assert(LT >= 1 && LT <= 16 && (LT & (LT - 1)) == 0, "T must be a power of two <= 16");
     static_assert(!DL || PRE, "the DL tile stream needs factors drawn ahead");
+    static_assert(!X || DL, "the split operands stream through DL buffers");
+    constexpr int NBUF = X ? 2 : K3_DLBUF;  // DL tile buffers
+    constexpr int DIST = NBUF - 1;          // tiles the stream runs ahead
     extern __shared__ __align__(16) unsigned char smem[];
-    const K3Layout lay(P.r, P.b, DL);
+    const K3Layout lay(P.r, P.b, DL, X);
     BmTables* tabs = reinterpret_cast<BmTables*>(smem);
     uint16_t* As = reinterpret_cast<uint16_t*>(smem + lay.off_a);
     uint64_t* Xbits = reinterpret_cast<uint64_t*>(smem + lay.off_xbits);
@@ -923,7 +1066,16 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
     int32_t dl_cb = 0;
     bool dl_primed = false;
     const uint16_t* dl_wsrc = wave < 4 ? P.wbf : nullptr;  // waves 4-7: set per pair
-    const PairImage dl_im(a, b, r);
+    const size_t dl_stride = X ? PairImageX(a, b, r).stride : PairImage(a, b, r).stride;
+    // X: a stream tile t is K tile t / 2, its high (t even) or low part
+    const int32_t dl_part = wave < 4 ? a * kp : r * kp;
+    const int32_t nt = X ? 2 * nkt : nkt;  // stream tiles per block
+    auto dl_issue_t = [&](const uint16_t* src, int32_t t, int32_t buf) {
+        if constexpr (X)
+            dl_issue(src + (t & 1) * dl_part, t >> 1, buf);
+        else
+            dl_issue(src, t, buf);
+    };
 
     // Work unit `it` of this workgroup: pair index and part (of P.split).
     const int32_t G = (int32_t)gridDim.x, S = P.split;
@@ -969,19 +1121,21 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
         unit_of(it + 1, &pi_n, &part_n);
         const bool more_pairs = pi_n < P.n_pairs;
         // DL: this wave's tile source for pair pi and for the next unit's pair
-        const uint16_t* dl_src = wave < 4 ? dl_wsrc : P.bimg + (size_t)pi * dl_im.stride;
+        const uint16_t* dl_src = wave < 4 ? dl_wsrc : P.bimg + (size_t)pi * dl_stride;
         const uint16_t* dl_src_next =
-            wave < 4 ? dl_wsrc : P.bimg + (size_t)(more_pairs ? pi_n : pi) * dl_im.stride;
+            wave < 4 ? dl_wsrc : P.bimg + (size_t)(more_pairs ? pi_n : pi) * dl_stride;
 
         // ---- 1. factors: A rows -> LDS (bf16, [o][c]); B rows -> slot ([c][k]) ----
         if constexpr (PRE) {
             // the pair's image holds A in this block's layout: one round of
             // 16-byte copies (a rows of K3_AP bf16, at most 5 per thread)
             const PairImage im(a, b, r);
-            const uint16_t* img = P.bimg + (size_t)pi * im.stride;
+            const PairImageX imx(a, b, r);
+            const uint16_t* img = P.bimg + (size_t)pi * (X ? imx.stride : im.stride);
             if (lcol >= K2_NMAX) lsrc = img + loff;
-            const uint4* asrc = reinterpret_cast<const uint4*>(img + im.b_elems);
-            const int32_t n16 = a * (K3_AP / 8);
+            // X: A's high then low part (a rows each), as they lie in the image
+            const uint4* asrc = reinterpret_cast<const uint4*>(img + (X ? 2 * imx.b_elems : im.b_elems));
+            const int32_t n16 = (X ? 2 : 1) * a * (K3_AP / 8);
             uint4 av0, av1, av2, av3, av4;
             auto aload = [&](int q) { return asrc[min(tid + q * K3_THREADS, n16 - 1)]; };
             auto astore = [&](int q, const uint4& v) {
@@ -1000,6 +1154,18 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
             astore(2, av2);
             astore(3, av3);
             astore(4, av4);
+            if constexpr (X) {  // the low part: a second round
+                av0 = aload(5);
+                av1 = aload(6);
+                av2 = aload(7);
+                av3 = aload(8);
+                av4 = aload(9);
+                astore(5, av0);
+                astore(6, av1);
+                astore(7, av2);
+                astore(8, av3);
+                astore(9, av4);
+            }
             if constexpr (DL) {
                 lds_barrier();
             } else {
@@ -1134,8 +1300,10 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
                 // the stream's first two tiles; later blocks' tiles were issued
                 // during the previous block's last two tiles
                 if (!dl_primed) {
-                    dl_issue(dl_src, 0, dl_cb);
-                    dl_issue(dl_src, 1, dl_cb == 2 ? 0 : dl_cb + 1);
+                    // X: tile 1 into the other of the two buffers (a block has
+                    // at least two stream tiles)
+                    dl_issue_t(dl_src, 0, dl_cb);
+                    dl_issue_t(dl_src, 1, dl_cb + 1 == NBUF ? 0 : dl_cb + 1);
                     wait_vmcnt<4>();
                     dl_primed = true;
                 }
@@ -1194,14 +1362,18 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
             auto step = [&](uint32_t w, auto kc, auto zc, const uint16_t* nxt) {
                 constexpr int ks = decltype(kc)::value;
                 constexpr bool z = decltype(zc)::value;
-                const u16x8 xa = expand_bits((w >> (8 * ((ks & 1) * 2 + hl))) & 0xffu);
+                const uint32_t xbyte = (w >> (8 * ((ks & 1) * 2 + hl))) & 0xffu;
+                const u16x8 xa = X ? expand_bits_f16(xbyte) : expand_bits(xbyte);
+                auto mma = [](const u16x8& p, const u16x8& q, const f32x16& c) {
+                    return X ? mfma32_f16(p, q, c) : mfma32_bf16(p, q, c);
+                };
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     if (j < 4)
-                        accW[j] = mfma32_bf16(xa, fr[j], z ? f32x16{} : accW[j]);
+                        accW[j] = mma(xa, fr[j], z ? f32x16{} : accW[j]);
                     else
-                        accB[j - 4] = mfma32_bf16(fr[j], xa, z ? f32x16{} : accB[j - 4]);
+                        accB[j - 4] = mma(fr[j], xa, z ? f32x16{} : accB[j - 4]);
                     fr[j] = lds_u16x8(nxt + frag_off(j));
                     __builtin_amdgcn_sched_barrier(0);
                 }
@@ -1212,67 +1384,89 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
             // next one waited for).  The last tile's last step re-reads its own
             // first fragments (no branch around the reads; the values are unused).
             const bool dl_next_pair = !has_next && more_pairs;
-            bool dl_v2 = false;  // DL: this tile issued the stream's tile two ahead
+            const int32_t ntb = DL ? nt : nkt;  // tiles of this block's K loop
+            // X: stream tile t (t >= ntb: the next block's, or the next unit's
+            // pair's, tile t - ntb) into buffer buf, issued right after the
+            // barrier that frees buf (the one after the last reads of the
+            // tile it held), so a transfer has four k-steps to land.
+            auto dl_issue_ahead = [&](int32_t t, int32_t buf) {
+                const uint16_t* src2 = dl_src;
+                bool v = true;
+                if (t >= ntb) {
+                    t -= ntb;
+                    if (!has_next) {
+                        src2 = dl_src_next;
+                        v = dl_next_pair;
+                    }
+                }
+                if (v) dl_issue_t(src2, t, buf);
+            };
+            bool dl_v2 = false;  // DL: this tile issued the stream's tile DIST ahead
+            // DL: tile DIST ahead in flight; the one just issued may remain so
+            // (DIST 2), or every transfer has landed (X: the only one in
+            // flight is the tile the barrier publishes)
+            auto dl_wait = [&]() {
+                if (DIST == 2 && dl_v2)
+                    wait_vmcnt<4>();
+                else
+                    wait_vmcnt<0>();
+            };
             auto tile = [&](int32_t kt, auto zc) {
-                const bool more = kt + 1 < nkt;
+                const bool more = kt + 1 < ntb;
                 const int32_t kn = more ? kt + 1 : kt;
+                const int32_t kw = X ? kn >> 1 : kn;  // x word of tile kn
                 const int32_t cb = DL ? dl_cb : (kt & 1);
-                const int32_t nb = DL ? (dl_cb == 2 ? 0 : dl_cb + 1) : ((kt + 1) & 1);
+                const int32_t nb = DL ? (dl_cb + 1 == NBUF ? 0 : dl_cb + 1) : ((kt + 1) & 1);
                 const uint32_t w0 = xw0, w1 = xw1;
                 step(w0, std::integral_constant<int, 0>{}, zc, frag_ptr(cb, 1));
                 step(w0, std::integral_constant<int, 1>{}, std::false_type{}, frag_ptr(cb, 2));
                 if constexpr (DL) {
-                    int32_t t2 = kt + 2;
-                    const uint16_t* src2 = dl_src;
-                    dl_v2 = true;
-                    if (t2 >= nkt) {
-                        t2 -= nkt;
-                        if (!has_next) {
-                            src2 = dl_src_next;
-                            dl_v2 = dl_next_pair;
+                    if constexpr (!X) {
+                        int32_t t2 = kt + DIST;
+                        const uint16_t* src2 = dl_src;
+                        dl_v2 = true;
+                        if (t2 >= ntb) {
+                            t2 -= ntb;
+                            if (!has_next) {
+                                src2 = dl_src_next;
+                                dl_v2 = dl_next_pair;
+                            }
                         }
+                        if (dl_v2) dl_issue_t(src2, t2, nb + 1 == NBUF ? 0 : nb + 1);
                     }
-                    if (dl_v2) dl_issue(src2, t2, nb == 2 ? 0 : nb + 1);
                 } else if (more && !resident) {
                     K3_TILE_STORE((kt + 1) & 1);
                     if (kt + 2 < nkt) K3_TILE_LOAD(kt + 2);
                 }
                 step(w1, std::integral_constant<int, 2>{}, std::false_type{}, frag_ptr(cb, 3));
                 if (more && !resident) {
-                    if constexpr (DL) {
-                        // tile kt + 1 (issued two tiles ago) has landed; only the
-                        // tile just issued may still be in flight
-                        if (dl_v2)
-                            wait_vmcnt<4>();
-                        else
-                            wait_vmcnt<0>();
-                    }
+                    if constexpr (DL) dl_wait();  // tile kt + 1 has landed
                     lds_barrier();
+                    if constexpr (X) dl_issue_ahead(kt + 2, cb);
                 }
-                xw0 = xw[2 * kn];
-                xw1 = xw[2 * kn + 1];
+                xw0 = xw[2 * kw];
+                xw1 = xw[2 * kw + 1];
                 step(w1, std::integral_constant<int, 3>{}, std::false_type{}, frag_ptr(more ? nb : cb, 0));
                 if constexpr (DL) dl_cb = nb;
             };
             tile(0, std::true_type{});
-            for (int32_t kt = 1; kt < nkt; ++kt) tile(kt, std::false_type{});
+            for (int32_t kt = 1; kt < ntb; ++kt) tile(kt, std::false_type{});
             // resident tiles: the epilogue restages only this wave's bit rows.
             // DL: the next block's first tile has landed before this barrier.
             if (!resident || nkt == 1) {
-                if constexpr (DL) {
-                    if (dl_v2)
-                        wait_vmcnt<4>();
-                    else
-                        wait_vmcnt<0>();
-                }
+                if constexpr (DL) dl_wait();
                 lds_barrier();
+                // X: the next block's second tile, into the last tile's buffer
+                if constexpr (X) dl_issue_ahead(ntb + 1, dl_cb == 0 ? 1 : 0);
             } else {
                 wave_lds_sync();
             }
 
             // sign * xB as bf16: lane l holds rank columns 32j + 8g + 4hl + v of
             // the row at MFMA position lc (the row its x operand came from).
+            // X: the same as fp16 high and low parts (xbf, xlo).
             uint32_t xbf[4][4][2];
+            uint32_t xlo[4][4][2];
             {
                 int32_t m, q;
                 cur_rows.at(wrow0 + xrow, R, &m, &q);
@@ -1282,8 +1476,17 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
                 for (int j = 0; j < 4; ++j)
 #pragma unroll
                     for (int g = 0; g < 4; ++g) {
-                        xbf[j][g][0] = pack_bf16x2(accB[j][4 * g], accB[j][4 * g + 1]) ^ sgn;
-                        xbf[j][g][1] = pack_bf16x2(accB[j][4 * g + 2], accB[j][4 * g + 3]) ^ sgn;
+                        if constexpr (X) {
+                            split_f16x2(accB[j][4 * g], accB[j][4 * g + 1], &xbf[j][g][0], &xlo[j][g][0]);
+                            split_f16x2(accB[j][4 * g + 2], accB[j][4 * g + 3], &xbf[j][g][1], &xlo[j][g][1]);
+                            xlo[j][g][0] ^= sgn;
+                            xlo[j][g][1] ^= sgn;
+                        } else {
+                            xbf[j][g][0] = pack_bf16x2(accB[j][4 * g], accB[j][4 * g + 1]);
+                            xbf[j][g][1] = pack_bf16x2(accB[j][4 * g + 2], accB[j][4 * g + 3]);
+                        }
+                        xbf[j][g][0] ^= sgn;
+                        xbf[j][g][1] ^= sgn;
                     }
             }
             const bool next_pair = !has_next && more_pairs;
@@ -1297,25 +1500,45 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
                 // the 16 A reads of this rank tile, then its 8 MFMAs (absent
                 // output tiles, 32 jo >= a, read row lc of tile 0; their columns
                 // are never stored)
-                uint4 af[2][4];
+                // X: (xB)_hi A_hi + (xB)_lo A_hi, then (xB)_hi A_lo (A's low part
+                // at row a of the LDS block)
 #pragma unroll
-                for (int t = 0; t < 2; ++t)
+                for (int part = 0; part < (X ? 2 : 1); ++part) {
+                    uint4 af[2][4];
 #pragma unroll
-                    for (int jo = 0; jo < 4; ++jo) {
-                        const uint16_t* ap = abase + (32 * jo < a ? 32 * jo * K3_AP : 0) + 32 * j + 16 * t;
-                        af[t][jo] = *reinterpret_cast<const uint4*>(ap);
+                    for (int t = 0; t < 2; ++t)
+#pragma unroll
+                        for (int jo = 0; jo < 4; ++jo) {
+                            const uint16_t* ap = abase + part * a * K3_AP +
+                                                 (32 * jo < a ? 32 * jo * K3_AP : 0) + 32 * j + 16 * t;
+                            af[t][jo] = *reinterpret_cast<const uint4*>(ap);
+                        }
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int t = 0; t < 2; ++t) {
+                        const uint32_t d[4] = {xbf[j][2 * t][0], xbf[j][2 * t][1], xbf[j][2 * t + 1][0],
+                                               xbf[j][2 * t + 1][1]};
+                        const u16x8 xo = __builtin_bit_cast(u16x8, d);
+#pragma unroll
+                        for (int jo = 0; jo < 4; ++jo) {
+                            if constexpr (X)
+                                accW[jo] = mfma32_f16(xo, __builtin_bit_cast(u16x8, af[t][jo]), accW[jo]);
+                            else
+                                accW[jo] = mfma32_bf16(xo, __builtin_bit_cast(u16x8, af[t][jo]), accW[jo]);
+                        }
+                        if constexpr (X) {
+                            if (part == 0) {
+                                const uint32_t e[4] = {xlo[j][2 * t][0], xlo[j][2 * t][1],
+                                                       xlo[j][2 * t + 1][0], xlo[j][2 * t + 1][1]};
+                                const u16x8 xl = __builtin_bit_cast(u16x8, e);
+#pragma unroll
+                                for (int jo = 0; jo < 4; ++jo)
+                                    accW[jo] = mfma32_f16(xl, __builtin_bit_cast(u16x8, af[t][jo]), accW[jo]);
+                            }
+                        }
                     }
-                __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                for (int t = 0; t < 2; ++t) {
-                    const uint32_t d[4] = {xbf[j][2 * t][0], xbf[j][2 * t][1], xbf[j][2 * t + 1][0],
-                                           xbf[j][2 * t + 1][1]};
-                    const u16x8 xo = __builtin_bit_cast(u16x8, d);
-#pragma unroll
-                    for (int jo = 0; jo < 4; ++jo)
-                        accW[jo] = mfma32_bf16(xo, __builtin_bit_cast(u16x8, af[t][jo]), accW[jo]);
+                    __builtin_amdgcn_sched_barrier(0);
                 }
-                __builtin_amdgcn_sched_barrier(0);
             }
 
             // The next block's operands land during the LIF and the stores: its
@@ -1356,7 +1579,9 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
                         float* yrow = P.y + k2_phys(m, q, P.rpm, P.T, P.y_stride, P.y_plane);
 #pragma unroll
                         for (int jo = 0; jo < 4; ++jo)
-                            if (32 * jo + lc < a) yrow[32 * jo + lc] = accW[jo][4 * g + v];
+                            if (32 * jo + lc < a)
+                                yrow[32 * jo + lc] = X ? accW[jo][4 * g + v] * (1.0f / K3_XSCALE)
+                                                       : accW[jo][4 * g + v];
                     }
             } else {
                 // LIF (snn.rs:53-97) along each lane's rows, v = 0 at t = 0.  The
@@ -1381,7 +1606,7 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
                     uint64_t bal[4];
 #pragma unroll
                     for (int jo = 0; jo < 4; ++jo) {
-                        const float c = accW[jo][qq];
+                        const float c = X ? accW[jo][qq] * (1.0f / K3_XSCALE) : accW[jo][qq];
                         const float charged = __fadd_rn(vm[jo], __fmul_rn(__fadd_rn(-vm[jo], c), P.leak));
                         const bool spike = charged >= P.v_th;
                         vm[jo] = spike ? 0.0f : charged;
@@ -1438,7 +1663,7 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
 }
 
 static bool pair_kernel_applies(const LinParams& P) {
-    return P.math == HSES_MATH_BF16 && P.r >= 16 && P.r <= K2_NMAX && P.r % 16 == 0 &&
+    return (P.math == HSES_MATH_BF16 || P.math == HSES_MATH_F32X) && P.r >= 16 && P.r <= K2_NMAX && P.r % 16 == 0 &&
            P.a <= K2_NMAX;
 }
 
@@ -1480,15 +1705,17 @@ static size_t pair_workspace_bytes(int32_t slots, int32_t a, int32_t b, int32_t 
 
 // Sized for k_linear_pair's grouped slots, which k_pair_bits (one slot per
 // workgroup) never exceeds.
+// Also holds the split mode's W (high and low parts).
 size_t linear_pair_workspace(const DeviceState* st, int32_t a, int32_t b, int32_t r, int32_t n) {
     int32_t lo, cnt;
     pair_range(0, n, &lo, &cnt);
-    return pair_workspace_bytes(pair_grid(st, cnt + 1) * pair_group(a), a, b, r);
+    return std::max(pair_workspace_bytes(pair_grid(st, cnt + 1) * pair_group(a), a, b, r),
+                    2 * pair_workspace_bytes(0, a, b, r));
 }
 
 // Every pair's factors of a launch drawn into the record and the B operand
 // image (the PRE kernels' inputs).
-int launch_pair_gen(LinParams& P, DeviceState* st, hipStream_t s, uint16_t* bimg) {
+int launch_pair_gen(LinParams& P, DeviceState* st, hipStream_t s, uint16_t* bimg, bool split) {
     if (P.r == 0 || !pair_kernel_applies(P)) return HSES_ERR_UNSUPPORTED;
     K2Args A{};
     pair_range(P.tid_lo, P.n, &A.pair_lo, &A.n_pairs);
@@ -1509,10 +1736,33 @@ int launch_pair_gen(LinParams& P, DeviceState* st, hipStream_t s, uint16_t* bimg
     A.tmm = P.tmm;
     A.rec = P.rec;
     A.bimg = bimg;
-    hipLaunchKernelGGL(k_pair_gen, dim3((uint32_t)((units + KG_THREADS - 1) / KG_THREADS)),
-                       dim3(KG_THREADS), 0, s, A);
+    const dim3 grid((uint32_t)((units + KG_THREADS - 1) / KG_THREADS));
+    if (split)
+        hipLaunchKernelGGL(k_pair_gen<true>, grid, dim3(KG_THREADS), 0, s, A);
+    else
+        hipLaunchKernelGGL(k_pair_gen<false>, grid, dim3(KG_THREADS), 0, s, A);
     HSES_CHECK_HIP(hipGetLastError());
     return HSES_OK;
+}
+
+int launch_pair_image_x(const float* rec, int32_t a, int32_t b, int32_t r, float bs, int32_t tid_lo,
+                        int32_t n, uint16_t* img, hipStream_t s) {
+    int32_t lo, cnt;
+    pair_range(tid_lo, n, &lo, &cnt);
+    const int32_t kp = (b + 63) / 64 * 64, rp32 = (r + 31) & ~31;
+    const int64_t total = ((int64_t)r * kp + (int64_t)a * rp32) * cnt;
+    if (total == 0) return HSES_OK;
+    hipLaunchKernelGGL(k_pair_image_x, dim3((uint32_t)((total + 255) / 256)), dim3(256), 0, s, rec,
+                       a, b, r, bs, cnt, img);
+    HSES_CHECK_HIP(hipGetLastError());
+    return HSES_OK;
+}
+
+size_t pair_image_x_bytes(int32_t a, int32_t b, int32_t r, int32_t tid_lo, int32_t n) {
+    if (n < 1 || r < 1 || b < 1 || tid_lo < 0) return 0;
+    int32_t lo, cnt;
+    pair_range(tid_lo, n, &lo, &cnt);
+    return (size_t)cnt * PairImageX(a, b, r).stride * 2;
 }
 
 size_t pair_image_bytes(int32_t a, int32_t b, int32_t r, int32_t tid_lo, int32_t n) {
@@ -1527,15 +1777,22 @@ int launch_linear_pair(LinParams& P, DeviceState* st, hipStream_t s, void* work,
     if (P.r == 0 || !pair_kernel_applies(P)) return HSES_ERR_UNSUPPORTED;
     const bool pre = bimg != nullptr;
     if (pre && !P.rec) return set_error(HSES_ERR_INVALID_ARG, "factors drawn ahead need the record");
+    // the split (fp32-accurate) mode: drawn-ahead factors (a PairImageX image),
+    // bit-packed x, do_mm, through the DL stream only
+    const bool xm = P.math == HSES_MATH_F32X;
+    if (xm && (!pre || P.x_fmt != HSES_FMT_BITS || P.tmm)) return HSES_ERR_UNSUPPORTED;
     if (lif && (P.n_time > 64 || (P.n_time & (P.n_time - 1)) != 0 || P.x_fmt != HSES_FMT_BITS))
         return HSES_ERR_UNSUPPORTED;
     const bool bits = P.x_fmt == HSES_FMT_BITS;
     // Bit-packed input with T <= 16 for the fused LIF: k_pair_bits.
     const bool v3 = bits && (!lif || P.n_time <= 16) && P.b <= 2 * K3_XPF * 64;
     const K2Layout lay(P.r, P.b, bits);
-    // factors drawn ahead and K of more than two tiles: the DL tile stream
-    const bool dl = v3 && pre && (P.b + 63) / 64 > 2 && K3Layout(P.r, P.b, true).bytes <= st->max_lds;
-    const K3Layout lay3(P.r, P.b, dl);
+    // factors drawn ahead and K of more than two tiles (any K in the split
+    // mode): the DL tile stream
+    const bool dl = v3 && pre && (xm || (P.b + 63) / 64 > 2) &&
+                    K3Layout(P.r, P.b, true, xm).bytes <= st->max_lds;
+    if (xm && !dl) return HSES_ERR_UNSUPPORTED;
+    const K3Layout lay3(P.r, P.b, dl, xm);
     const size_t lds_bytes = v3 ? lay3.bytes : lay.bytes;
     const int threads = v3 ? K3_THREADS : K2_THREADS;
     if (lds_bytes > st->max_lds) return HSES_ERR_UNSUPPORTED;
@@ -1554,7 +1811,8 @@ int launch_linear_pair(LinParams& P, DeviceState* st, hipStream_t s, void* work,
         grid = st->num_cus;
     }
     A.group = v3 ? 1 : pair_group(P.a);
-    const size_t need = pair_workspace_bytes(pre ? 0 : grid * A.group, P.a, P.b, P.r);
+    const size_t need = xm ? 2 * pair_workspace_bytes(0, P.a, P.b, P.r)
+                           : pair_workspace_bytes(pre ? 0 : grid * A.group, P.a, P.b, P.r);
     if (!work || work_bytes < need)
         return set_error(HSES_ERR_INVALID_ARG, "hses_perturbed_linear: workspace too small");
     uint16_t* wbf = static_cast<uint16_t*>(work);
@@ -1610,8 +1868,12 @@ int launch_linear_pair(LinParams& P, DeviceState* st, hipStream_t s, void* work,
                      P.x_stride == (int64_t)P.n_time * words && ((int64_t)P.R * words) % 2 == 0;
     }
     const int64_t wl = (int64_t)P.a * lay.kp;
-    hipLaunchKernelGGL(k_w_to_bf16, dim3((uint32_t)((wl + 255) / 256)), dim3(256), 0, s, P.W, P.a,
-                       P.b, lay.kp, P.tmm, wbf);
+    if (xm)
+        hipLaunchKernelGGL(k_w_to_f16x, dim3((uint32_t)((wl + 255) / 256)), dim3(256), 0, s, P.W,
+                           P.a, P.b, lay.kp, wbf);
+    else
+        hipLaunchKernelGGL(k_w_to_bf16, dim3((uint32_t)((wl + 255) / 256)), dim3(256), 0, s, P.W,
+                           P.a, P.b, lay.kp, P.tmm, wbf);
     HSES_CHECK_HIP(hipGetLastError());
     auto launch = [&](auto kern) -> int {
         if (lds_bytes > 64 * 1024)
@@ -1622,27 +1884,30 @@ int launch_linear_pair(LinParams& P, DeviceState* st, hipStream_t s, void* work,
         return HSES_OK;
     };
     if (v3) {
-        auto by_pre = [&](auto pc, auto dc) -> int {
+        auto by_pre = [&](auto pc, auto dc, auto xc) -> int {
             constexpr bool PR = decltype(pc)::value, D = decltype(dc)::value;
-            if (!lif) return launch(k_pair_bits<EPI_Y, 1, false, false, PR, D>);
+            constexpr bool XX = decltype(xc)::value;
+            if (!lif) return launch(k_pair_bits<EPI_Y, 1, false, false, PR, D, XX>);
             const bool spk = lif->spk != nullptr, rate = lif->rate != nullptr;
             auto by_t = [&](auto sc, auto rc) -> int {
                 constexpr bool S = decltype(sc)::value, Q = decltype(rc)::value;
                 switch (P.n_time) {
-                    case 1: return launch(k_pair_bits<EPI_LIF, 1, S, Q, PR, D>);
-                    case 2: return launch(k_pair_bits<EPI_LIF, 2, S, Q, PR, D>);
-                    case 4: return launch(k_pair_bits<EPI_LIF, 4, S, Q, PR, D>);
-                    case 8: return launch(k_pair_bits<EPI_LIF, 8, S, Q, PR, D>);
-                    default: return launch(k_pair_bits<EPI_LIF, 16, S, Q, PR, D>);
+                    case 1: return launch(k_pair_bits<EPI_LIF, 1, S, Q, PR, D, XX>);
+                    case 2: return launch(k_pair_bits<EPI_LIF, 2, S, Q, PR, D, XX>);
+                    case 4: return launch(k_pair_bits<EPI_LIF, 4, S, Q, PR, D, XX>);
+                    case 8: return launch(k_pair_bits<EPI_LIF, 8, S, Q, PR, D, XX>);
+                    default: return launch(k_pair_bits<EPI_LIF, 16, S, Q, PR, D, XX>);
                 }
             };
             if (spk && rate) return by_t(std::true_type{}, std::true_type{});
             if (spk) return by_t(std::true_type{}, std::false_type{});
             return by_t(std::false_type{}, std::true_type{});
         };
-        if (dl) return by_pre(std::true_type{}, std::true_type{});
-        return pre ? by_pre(std::true_type{}, std::false_type{})
-                   : by_pre(std::false_type{}, std::false_type{});
+        const std::true_type yes;
+        const std::false_type no;
+        if (xm) return by_pre(yes, yes, yes);
+        if (dl) return by_pre(yes, yes, no);
+        return pre ? by_pre(yes, no, no) : by_pre(no, no, no);
     }
     if (pre) {
         // dense input (the readout on spike rates) on the PRE form of k_linear_pair

@@ -9,7 +9,7 @@ import ctypes
 import torch
 
 from . import _lib
-from ._lib import (FMT_BF16, FMT_BITS, FMT_F32, FMT_U8, MATH_BF16, MATH_F32,  # noqa: F401
+from ._lib import (FMT_BF16, FMT_BITS, FMT_F32, FMT_U8, MATH_BF16, MATH_F32, MATH_F32X,  # noqa: F401
                    REWARD_BINARY, REWARD_LOGLIK)
 
 _FMT_DTYPE = {FMT_F32: torch.float32, FMT_BF16: torch.bfloat16, FMT_U8: torch.uint8,
@@ -182,12 +182,31 @@ def _img_arg(img):
     return _p(img), img.numel() * 2
 
 
-def pair_factors(key, rank, sigma, epoch, noise_reuse, tid_lo, n, a, b, rec, img):
+def pair_image_x(a, b, rank, tid_lo, n, device="cuda"):
+    """A split (fp16 high + low parts, stored as int16) operand image buffer for
+    the fp32-accurate forwards (hses_pair_image_x_bytes)."""
+    nbytes = int(_lib.load().hses_pair_image_x_bytes(a, b, rank, tid_lo, n))
+    if nbytes == 0:
+        raise ValueError("no operand image for this shape")
+    return torch.empty(nbytes // 2, dtype=torch.int16, device=device)
+
+
+def split_pair_image(a, b, rank, sigma, tid_lo, n, rec, img):
+    """Fill the split operand image `img` (pair_image_x) from the factor record
+    `rec` of the same members (hses_pair_image_x)."""
+    _lib.call("hses_pair_image_x", a, b, rank, sigma, tid_lo, n, *_rec_arg(rec), *_img_arg(img),
+              _stream())
+
+
+def pair_factors(key, rank, sigma, epoch, noise_reuse, tid_lo, n, a, b, rec, img, split=False):
     """Draw every pair's factors of members [tid_lo, tid_lo + n) into the factor
     record `rec` and the operand image `img` (hses_pair_factors); the forwards
-    given rec= and img= then read them instead of drawing."""
-    _lib.call("hses_pair_factors", key & (2**64 - 1), rank, sigma, epoch, noise_reuse, tid_lo, n,
-              a, b, *_rec_arg(rec), *_img_arg(img), _stream())
+    given rec= and img= then read them instead of drawing.  split: `img` is the
+    split image (pair_image_x) for the fp32-accurate forwards
+    (hses_pair_factors_x)."""
+    _lib.call("hses_pair_factors_x" if split else "hses_pair_factors", key & (2**64 - 1), rank,
+              sigma, epoch, noise_reuse, tid_lo, n, a, b, *_rec_arg(rec), *_img_arg(img),
+              _stream())
 
 
 def perturbed_linear(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n, rows_per_member,
@@ -197,7 +216,9 @@ def perturbed_linear(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n, rows
     when n_time == 1); returns y (n_time, n*rows_per_member, a) fp32 (bf16 with
     out_bf16), passed through the activation `act` (hses_act) when it is not 0.
     With `rec` (factor_record) the pairs' normals are also kept there; with
-    `rec` and `img` filled by pair_factors they are read from there instead."""
+    `rec` and `img` filled by pair_factors they are read from there instead;
+    with math=MATH_F32X, `img` is the split image (split_pair_image) and y is
+    fp32-accurate (hses_perturbed_linear_pre_x)."""
     a, b = W.shape
     _dev(W, torch.float32, "W")
     _dev(x, _FMT_DTYPE[x_fmt], "x")
@@ -215,9 +236,11 @@ def perturbed_linear(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n, rows
                                                               n_time, math))
     work = _workspace(wbytes, W.device)
     if img is not None:
-        if rec is None or act or out_bf16 or math != MATH_BF16:
-            raise ValueError("factors drawn ahead need rec, bf16 math and a plain fp32 output")
-        _lib.call("hses_perturbed_linear_pre", _p(x), x_fmt, units, M * units, n_time, _p(W), a,
+        if rec is None or act or out_bf16 or math not in (MATH_BF16, MATH_F32X):
+            raise ValueError("factors drawn ahead need rec, bf16 or split math and a plain "
+                             "fp32 output")
+        _lib.call("hses_perturbed_linear_pre_x" if math == MATH_F32X else
+                  "hses_perturbed_linear_pre", _p(x), x_fmt, units, M * units, n_time, _p(W), a,
                   b, rank, sigma, tid_lo, n, rows_per_member, _p(out), a, M * a, _p(work),
                   wbytes, *_rec_arg(rec), *_img_arg(img), _stream())
     elif rec is not None:
@@ -275,13 +298,14 @@ def perturbed_linear_t(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n, ro
 def perturbed_linear_lif(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n,
                          rows_per_member, n_time, tau_m, v_th, spikes=None, rate=None,
                          want_spikes=True, want_rate=False, rec=None, img=None,
-                         time_inner=False):
+                         time_inner=False, math=MATH_BF16):
     """Perturbed forward fused with LIF.  x is bit-packed (n_time, M, words(b));
     returns (spikes (n_time, M, words(a)) int64 or None, rate (M, a) or None).
     With time_inner, x and spikes are (M, n_time, words) (each row's time steps
     adjacent).  With `rec` (factor_record) the pairs' normals are also kept
     there; with `rec` and `img` filled by pair_factors they are read from there
-    instead."""
+    instead.  math=MATH_F32X (with `img` the split image of split_pair_image):
+    fp32-accurate currents (hses_perturbed_linear_lif_pre_x)."""
     a, b = W.shape
     _dev(W, torch.float32, "W")
     _dev(x, _FMT_DTYPE[FMT_BITS], "x")
@@ -303,8 +327,10 @@ def perturbed_linear_lif(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n,
         _dev(rate, torch.float32, "rate")
         if rate.numel() != M * a:
             raise ValueError("rate has the wrong size")
+    if math not in (MATH_BF16, MATH_F32X) or (math == MATH_F32X and img is None):
+        raise ValueError("the fused forward takes bf16 math, or split math with img")
     wbytes = int(_lib.load().hses_perturbed_linear_workspace(a, b, rank, n, rows_per_member,
-                                                              n_time, MATH_BF16))
+                                                              n_time, math))
     work = _workspace(wbytes, W.device)
     if time_inner:
         xs, xp, ss, sp = n_time * units, units, n_time * wa, wa
@@ -319,7 +345,8 @@ def perturbed_linear_lif(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n,
     if img is not None:
         if rec is None:
             raise ValueError("factors drawn ahead need rec")
-        _lib.call("hses_perturbed_linear_lif_pre", _p(x), FMT_BITS, xs, xp, n_time,
+        _lib.call("hses_perturbed_linear_lif_pre_x" if math == MATH_F32X else
+                  "hses_perturbed_linear_lif_pre", _p(x), FMT_BITS, xs, xp, n_time,
                   _p(W), a, b, rank, sigma, tid_lo, n, rows_per_member, tau_m, v_th,
                   _p(spikes) if spikes is not None else None, ss, sp,
                   _p(rate) if rate is not None else None, a, _p(work), wbytes, *_rec_arg(rec),

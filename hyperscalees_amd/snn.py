@@ -27,7 +27,7 @@ import numpy as np
 import torch
 
 from . import kernels as K
-from ._lib import ADAMW, FMT_BITS, FMT_F32, MATH_BF16, REWARD_LOGLIK, SGD
+from ._lib import ADAMW, FMT_BITS, FMT_F32, MATH_BF16, MATH_F32X, REWARD_LOGLIK, SGD
 
 KEY_MUL = 0x9E3779B97F4A7C15
 
@@ -129,7 +129,7 @@ class SnnEs:
         hmax = max(c.dims[1:-1]) if L > 1 else 1
         # Hidden layers run as one fused forward+LIF kernel when the
         # large-rank kernel applies; the fp32 currents then never exist.
-        can_fuse = (c.math == MATH_BF16 and c.sigma != 0.0 and c.rank % 16 == 0
+        can_fuse = (c.math in (MATH_BF16, MATH_F32X) and c.sigma != 0.0 and c.rank % 16 == 0
                     and 16 <= c.rank <= 128 and hmax <= 128 and c.T <= 64
                     and (c.T & (c.T - 1)) == 0)
         self.fused = can_fuse if fused is None else (bool(fused) and can_fuse)
@@ -173,8 +173,9 @@ class SnnEs:
         # its own (hses_pair_factors, full occupancy) and the forward reads the
         # record and the bf16 B operand image instead of drawing.
         self.ahead = self.record if ahead is None else (bool(ahead) and self.record)
+        self.split = c.math == MATH_F32X
         self.img = None
-        if self.ahead:
+        if self.ahead and not self.split:
             self.img = []
             n_odd = c.chunk if c.accumulate > 1 and c.chunk % 2 else 0
             for w in self.W:
@@ -182,6 +183,27 @@ class SnnEs:
                 nbytes = max(K._lib.load().hses_pair_image_bytes(a, b, c.rank, t, c.chunk)
                              for t in (0, n_odd))
                 self.img.append(torch.empty(nbytes // 2, dtype=torch.int16, device=device))
+        # The split (fp32-accurate) mode: every layer's draw writes the record
+        # and a split operand image (hses_pair_factors_x), which the forward
+        # reads in place of the bf16 image.  The last
+        # hidden layer keeps its spikes, and the readout runs on them row by
+        # row and time step by time step (rows_per_member = rows * T, one time
+        # plane), its outputs averaged over the T steps: by linearity that is
+        # the readout of the spike rate (snn.rs:274-280), whose bit-packed x
+        # the split kernels take exactly.
+        self.img_x = None
+        if self.split:
+            if not (self.ahead and self.time_inner and c.T <= 16):
+                raise ValueError("MATH_F32X needs the fused path with factors drawn ahead "
+                                 "(rank a multiple of 16 in [32, 128], widths <= 128, T <= 16)")
+            self.img_x = []
+            n_odd = c.chunk if c.accumulate > 1 and c.chunk % 2 else 0
+            for w in self.W:
+                a, b = w.shape
+                nbytes = max(K._lib.load().hses_pair_image_x_bytes(a, b, c.rank, t, c.chunk)
+                             for t in (0, n_odd))
+                self.img_x.append(torch.empty(nbytes // 2, dtype=torch.int16, device=device))
+            self.ylog = torch.empty((1, M * c.T, c.dims[-1]), dtype=torch.float32, device=device)
 
     # -- forward -------------------------------------------------------------
     def spikes_tm(self, l):
@@ -208,7 +230,9 @@ class SnnEs:
         c = self.cfg
         a = c.dims[l + 1]
         if self.fused:
-            last = l == self.L - 2  # feeds the readout: only its spike rates are used
+            # feeds the readout: only its spike rates are used (the split mode
+            # reads its spikes)
+            last = l == self.L - 2 and not self.split
             img = self._draw(l, epoch, lo)
             K.perturbed_linear_lif(self.spk[l], self.W[l], c.keys[l], c.rank, c.sigma, epoch,
                                    c.noise_reuse, lo, c.chunk, c.rows, c.T, c.tau_m, c.v_th,
@@ -216,7 +240,7 @@ class SnnEs:
                                    rate=self.rate if last else None,
                                    want_spikes=not last, want_rate=last,
                                    rec=self.rec[l] if self.rec else None, img=img,
-                                   time_inner=self.time_inner)
+                                   time_inner=self.time_inner, math=c.math)
             if self.rec:
                 self._rec_at[l] = (epoch, lo)
             return
@@ -229,6 +253,17 @@ class SnnEs:
 
     def readout(self, epoch, lo=0):
         c = self.cfg
+        if self.split:
+            img = self._draw(self.L - 1, epoch, lo)
+            x = self.spk[self.L - 1].view(1, self.M * c.T, -1)
+            K.perturbed_linear(x, self.W[-1], c.keys[-1], c.rank, c.sigma, epoch, c.noise_reuse,
+                               lo, c.chunk, c.rows * c.T, x_fmt=FMT_BITS, n_time=1,
+                               math=MATH_F32X, out=self.ylog, rec=self.rec[-1], img=img)
+            torch.mean(self.ylog.view(self.M, c.T, -1), 1, out=self.logits)
+            self._rec_at[-1] = (epoch, lo)
+            labels = self.labels[lo * c.rows:(lo + c.chunk) * c.rows]
+            return K.member_fitness(self.logits, labels, c.chunk, c.rows, c.reward,
+                                    out=self.raw[lo:lo + c.chunk], correct=self.correct)
         if not self.fused:
             K.spike_rate(self.spk[self.L - 1], FMT_BITS, c.dims[-2], out=self.rate)
         img = self._draw(self.L - 1, epoch, lo)
@@ -245,13 +280,14 @@ class SnnEs:
     def _draw(self, l, epoch, lo):
         """Layer l's factors of the chunk into its record and operand image
         (factors drawn ahead), or None when the forward draws them itself."""
-        if not self.img:
+        img = self.img_x if self.split else self.img
+        if not img:
             return None
         c = self.cfg
         a, b = self.W[l].shape
         K.pair_factors(c.keys[l], c.rank, c.sigma, epoch, c.noise_reuse, lo, c.chunk, a, b,
-                       self.rec[l], self.img[l])
-        return self.img[l]
+                       self.rec[l], img[l], split=self.split)
+        return img[l]
 
     def forward(self, epoch=0, lo=0, mark=None):
         """Raw fitness of the chunk of members [lo, lo + chunk) (a view of self.raw).

@@ -44,8 +44,11 @@ typedef enum {
 
 /* Arithmetic of the perturbed matrix products. */
 typedef enum {
-    HSES_MATH_F32 = 0, /* fp32 MFMA, fp32 operands                               */
-    HSES_MATH_BF16 = 1 /* bf16 MFMA (operands rounded to bf16), fp32 accumulate  */
+    HSES_MATH_F32 = 0,  /* fp32 MFMA, fp32 operands                              */
+    HSES_MATH_BF16 = 1, /* bf16 MFMA (operands rounded to bf16), fp32 accumulate */
+    HSES_MATH_F32X = 2  /* fp16 MFMA on split operands (each fp32 operand as an  */
+                        /* fp16 high + low part, 3 products), fp32 accumulate:  */
+                        /* fp32-accurate; the *_pre_x forwards only             */
 } hses_math;
 
 /* Solver kinds (burn_impl/hyperscalees-noiser/src/noiser.rs:43-92). */
@@ -336,6 +339,62 @@ int hses_perturbed_linear_lif_pre(const void *d_x, int32_t x_fmt, int64_t x_stri
                                   float *d_rate, int64_t rate_stride, void *d_work,
                                   size_t work_bytes, const float *d_rec, size_t rec_bytes,
                                   const uint16_t *d_img, size_t img_bytes, void *stream);
+
+/* ---- fp32-accurate forwards (HSES_MATH_F32X) -------------------------------
+ * The *_pre forwards with every operand held to fp32 accuracy: the same
+ * perturbed product x W^T + sign_m (x B_m) A_m^T that snn.rs:665-685
+ * (lora_linear_batched) and eggroll.rs:419-446 (do_mm) compute in fp32, on
+ * fp16 MFMAs.  Each fp32 operand v is split into an fp16 high part and the
+ * fp16 rounding of v - high (v to about 2^-22 of v); x is 0/1 spikes (exact).
+ * x W^T takes x W_hi + x W_lo, x B_m takes x B_hi + x B_lo, and its product
+ * with A takes (xB)_hi A_hi + (xB)_lo A_hi + (xB)_hi A_lo, all accumulated in
+ * fp32, so the currents carry fp32 rounding, not bf16's: the spikes differ
+ * from an fp32 evaluation only where a membrane potential lies within fp32
+ * summation error of the threshold.  hses_pair_factors_x draws the factors
+ * into the record and the split operand image; hses_pair_image_x builds the
+ * image from a record written by hses_pair_factors or a *_rec forward.  The
+ * *_pre_x forwards take it in place of the bf16 image.
+ * Bit-packed x (x_fmt BITS), do_mm, a <= 128, rank a multiple of 16 in
+ * [32, 128], b <= 896; workspace as hses_perturbed_linear_workspace with
+ * math = HSES_MATH_F32X (or HSES_MATH_BF16: the same size).  None of these
+ * has a counterpart in the reference's bf16-free path; they are its fp32
+ * arithmetic on this hardware's fp16 matrix cores. */
+
+/* Bytes of the split operand image of members [tid_lo, tid_lo + n). */
+size_t hses_pair_image_x_bytes(int32_t a, int32_t b, int32_t rank, int32_t tid_lo, int32_t n);
+
+/* hses_pair_factors with the split operand image in place of the bf16 one:
+ * the same record, and the image hses_pair_image_x derives from it. */
+int hses_pair_factors_x(uint64_t key, int32_t rank, float sigma, int32_t epoch,
+                        int32_t noise_reuse, int32_t tid_lo, int32_t n, int32_t a, int32_t b,
+                        float *d_rec, size_t rec_bytes, uint16_t *d_img, size_t img_bytes,
+                        void *stream);
+
+/* The split operand image from a factor record (same a, b, rank, sigma,
+ * tid_lo, n as the draw that wrote it). */
+int hses_pair_image_x(int32_t a, int32_t b, int32_t rank, float sigma, int32_t tid_lo, int32_t n,
+                      const float *d_rec, size_t rec_bytes, uint16_t *d_img, size_t img_bytes,
+                      void *stream);
+
+/* hses_perturbed_linear_pre at fp32 accuracy (d_img from hses_pair_image_x). */
+int hses_perturbed_linear_pre_x(const void *d_x, int32_t x_fmt, int64_t x_stride,
+                                int64_t x_plane, int32_t n_time, const float *d_W, int32_t a,
+                                int32_t b, int32_t rank, float sigma, int32_t tid_lo, int32_t n,
+                                int32_t rows_per_member, float *d_y, int64_t y_stride,
+                                int64_t y_plane, void *d_work, size_t work_bytes,
+                                const float *d_rec, size_t rec_bytes, const uint16_t *d_img,
+                                size_t img_bytes, void *stream);
+
+/* hses_perturbed_linear_lif_pre at fp32 accuracy (d_img from
+ * hses_pair_image_x): the LIF of snn.rs:53-97 on fp32-accurate currents. */
+int hses_perturbed_linear_lif_pre_x(const void *d_x, int32_t x_fmt, int64_t x_stride,
+                                    int64_t x_plane, int32_t n_time, const float *d_W, int32_t a,
+                                    int32_t b, int32_t rank, float sigma, int32_t tid_lo,
+                                    int32_t n, int32_t rows_per_member, float tau_m, float v_th,
+                                    uint64_t *d_spikes, int64_t spk_stride, int64_t spk_plane,
+                                    float *d_rate, int64_t rate_stride, void *d_work,
+                                    size_t work_bytes, const float *d_rec, size_t rec_bytes,
+                                    const uint16_t *d_img, size_t img_bytes, void *stream);
 
 /* ---- ES update ------------------------------------------------------- */
 
