@@ -72,6 +72,11 @@ PROTOTYPES = {
                                                      c_vp, c_i64, c_vp, c_size, c_vp, c_size,
                                                      c_vp, c_size, c_vp]),
     "hses_pair_image_x_bytes": (c_size, [c_i32, c_i32, c_i32, c_i32, c_i32]),
+    "hses_perturbed_linear_lif_counts_pre_x": (ctypes.c_int, [c_vp, c_i32, c_i64, c_i64, c_i32,
+                                                              c_vp, c_i32, c_i32, c_i32, c_f32,
+                                                              c_i32, c_i32, c_i32, c_f32, c_f32,
+                                                              c_vp, c_i64, c_vp, c_size, c_vp,
+                                                              c_size, c_vp, c_size, c_vp]),
     "hses_pair_factors_x": (ctypes.c_int, [c_u64, c_i32, c_f32, c_i32, c_i32, c_i32, c_i32, c_i32,
                                            c_i32, c_vp, c_size, c_vp, c_size, c_vp]),
     "hses_pair_image_x": (ctypes.c_int, [c_i32, c_i32, c_i32, c_f32, c_i32, c_i32, c_vp, c_size,

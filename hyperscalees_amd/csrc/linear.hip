@@ -551,7 +551,8 @@ static int linear_lif_impl(const void* d_x, int32_t x_fmt, int64_t x_stride, int
                            float* d_rate, int64_t rate_stride, void* d_work, size_t work_bytes,
                            float* d_rec, size_t rec_bytes, void* stream,
                            const uint16_t* d_img = nullptr, size_t img_bytes = 0,
-                           bool split = false) {
+                           bool split = false, uint64_t* d_counts = nullptr,
+                           int64_t counts_stride = 0) {
     HSES_REQUIRE(tau_m != 0.0f, "tau_m must be non-zero");
     LinParams P;
     DeviceState* st = nullptr;
@@ -569,7 +570,7 @@ static int linear_lif_impl(const void* d_x, int32_t x_fmt, int64_t x_stride, int
                      "hses_pair_image_bytes");
     }
     if (split) P.math = HSES_MATH_F32X;
-    HSES_REQUIRE(d_spikes || d_rate, "spikes and rate are both NULL");
+    HSES_REQUIRE(d_spikes || d_rate || d_counts, "spikes and rate are both NULL");
     const int64_t M = (int64_t)n * rows_per_member;
     HSES_REQUIRE(!d_spikes || rows_layout_ok((a + 63) / 64, M, n_time, spk_stride, spk_plane),
                  "spike rows overlap (spk_stride smaller than a row, or time planes overlap)");
@@ -578,7 +579,7 @@ static int linear_lif_impl(const void* d_x, int32_t x_fmt, int64_t x_stride, int
     HSES_REQUIRE(n_time <= 64 && (n_time & (n_time - 1)) == 0, "n_time must be a power of two <= 64");
     HSES_REQUIRE(x_fmt == HSES_FMT_BITS, "the fused kernel takes bit-packed spikes (x_fmt BITS)");
     LifOut lif{d_spikes, spk_stride, spk_plane, d_rate, rate_stride,
-               1.0f / tau_m /* snn.rs:59: dt / tau_m with dt = 1 */, v_th};
+               1.0f / tau_m /* snn.rs:59: dt / tau_m with dt = 1 */, v_th, d_counts, counts_stride};
     rc = launch_linear_pair(P, st, (hipStream_t)stream, d_work, work_bytes, &lif, d_img);
     if (rc == HSES_ERR_UNSUPPORTED)
         return set_error(HSES_ERR_UNSUPPORTED,
@@ -813,6 +814,30 @@ extern "C" int hses_perturbed_linear_pre_x(const void* d_x, int32_t x_fmt, int64
     return linear_pre_impl(d_x, x_fmt, x_stride, x_plane, n_time, d_W, a, b, rank, sigma, tid_lo,
                            n, rows_per_member, d_y, y_stride, y_plane, d_work, work_bytes, d_rec,
                            rec_bytes, d_img, img_bytes, stream, true);
+}
+
+extern "C" int hses_perturbed_linear_lif_counts_pre_x(
+    const void* d_x, int32_t x_fmt, int64_t x_stride, int64_t x_plane, int32_t n_time,
+    const float* d_W, int32_t a, int32_t b, int32_t rank, float sigma, int32_t tid_lo, int32_t n,
+    int32_t rows_per_member, float tau_m, float v_th, uint64_t* d_counts, int64_t counts_stride,
+    void* d_work, size_t work_bytes, const float* d_rec, size_t rec_bytes, const uint16_t* d_img,
+    size_t img_bytes, void* stream) {
+    if (n > 0 && tid_lo >= 0) {
+        const int rc = check_drawn(a, b, rank, sigma, tid_lo, n, d_rec, rec_bytes, d_img,
+                                   img_bytes, "hses_perturbed_linear_lif_counts_pre_x", true);
+        if (rc) return rc;
+    }
+    HSES_REQUIRE(d_counts, "count planes are NULL");
+    HSES_REQUIRE(n_time >= 1 && n_time <= 16 && (n_time & (n_time - 1)) == 0,
+                 "hses_perturbed_linear_lif_counts_pre_x: n_time must be a power of two <= 16");
+    int32_t planes = 1;
+    while ((1 << (planes - 1)) < n_time) ++planes;
+    HSES_REQUIRE(counts_stride >= (int64_t)planes * ((a + 63) / 64),
+                 "counts_stride smaller than a row's count planes");
+    return linear_lif_impl(d_x, x_fmt, x_stride, x_plane, n_time, d_W, a, b, 0, rank, sigma, 0, 0,
+                           tid_lo, n, rows_per_member, tau_m, v_th, nullptr, 0, 0, nullptr, 0,
+                           d_work, work_bytes, const_cast<float*>(d_rec), rec_bytes, stream, d_img,
+                           img_bytes, true, d_counts, counts_stride);
 }
 
 extern "C" int hses_perturbed_linear_lif_pre_x(

@@ -148,6 +148,9 @@ struct LifOut {
     float* rate;  // (M, a) spike rates or NULL
     int64_t rate_stride;
     float leak, v_th;
+    // spike-count bit planes in place of the rates (k_pair_bits only), or NULL
+    void* cpl;
+    int64_t cpl_stride;
 };
 
 int launch_linear_small(LinParams& P, DeviceState* st, hipStream_t s);

@@ -123,6 +123,11 @@ struct K2Args {
     int64_t spk_stride, spk_plane;
     float* rate;    // fused LIF: spike counts / T (M, a), or NULL
     int64_t rate_stride;
+    // fused LIF: spike-count bit planes in place of the rates, or NULL: output
+    // row (m, s) has log2(T) + 1 planes of words(a) words at cpl + (m rpm + s)
+    // cpl_stride, bit c of plane p being bit p of neuron c's count
+    uint64_t* cpl;
+    int64_t cpl_stride;
     int32_t a, b, r, R, rpm, T, n, tid_lo, pair_lo, n_pairs, epoch, nreuse;
     int32_t segs;   // generation segments per stream row (jump table for row length r / segs)
     int32_t group;  // pairs generated together (k_linear_pair; their A rows share the LDS block)
@@ -970,7 +975,10 @@ __device__ __forceinline__ void wait_vmcnt() {
 // taken twice, its high and its low part (two DL buffers; each transfer is
 // issued right after the barrier that frees its buffer, one tile ahead), and
 // the second product is (xB)_hi A_hi + (xB)_lo A_hi + (xB)_hi A_lo.
-template <int EPI, int LT, bool SPK, bool RATE, bool PRE = false, bool DL = false, bool X = false>
+// WT: output tiles of 32 columns computed (4; 1 for a <= 32, where the other
+// three would only be discarded).
+template <int EPI, int LT, bool SPK, bool RATE, bool PRE = false, bool DL = false, bool X = false,
+          int WT = 4>
 __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
     static_assert(LT >= 1 && LT <= 16 && (LT & (LT - 1)) == 0, "T must be a power of two <= 16");
     static_assert(!DL || PRE, "the DL tile stream needs factors drawn ahead");
@@ -1025,6 +1033,7 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
         dl_off[q] = srow * kp + ch * 8;
     }
     auto dl_issue = [&](const uint16_t* src, int32_t kt, int32_t buf) {
+        if (wave >= WT && wave < 4) return;  // W rows no output tile reads
         const uint32_t dst = __builtin_amdgcn_readfirstlane(
             lds_addr(WB + buf * K3_DLTILE + (4 * wave) * 512));
 #pragma unroll
@@ -1354,7 +1363,11 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
             {
                 const uint16_t* tb = frag_ptr(DL ? dl_cb : 0, 0);
 #pragma unroll
-                for (int j = 0; j < 8; ++j) fr[j] = lds_u16x8(tb + frag_off(j));
+                for (int j = 0; j < 8; ++j)
+                    if (j >= WT && j < 4)
+                        fr[j] = u16x8{};
+                    else
+                        fr[j] = lds_u16x8(tb + frag_off(j));
             }
             uint32_t xw0 = xw[0], xw1 = xw[1];
             // One step: its 8 MFMAs, each followed by the read of the same
@@ -1370,6 +1383,7 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
+                    if (j >= WT && j < 4) continue;
                     if (j < 4)
                         accW[j] = mma(xa, fr[j], z ? f32x16{} : accW[j]);
                     else
@@ -1508,7 +1522,7 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
 #pragma unroll
                     for (int t = 0; t < 2; ++t)
 #pragma unroll
-                        for (int jo = 0; jo < 4; ++jo) {
+                        for (int jo = 0; jo < WT; ++jo) {
                             const uint16_t* ap = abase + part * a * K3_AP +
                                                  (32 * jo < a ? 32 * jo * K3_AP : 0) + 32 * j + 16 * t;
                             af[t][jo] = *reinterpret_cast<const uint4*>(ap);
@@ -1520,7 +1534,7 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
                                                xbf[j][2 * t + 1][1]};
                         const u16x8 xo = __builtin_bit_cast(u16x8, d);
 #pragma unroll
-                        for (int jo = 0; jo < 4; ++jo) {
+                        for (int jo = 0; jo < WT; ++jo) {
                             if constexpr (X)
                                 accW[jo] = mfma32_f16(xo, __builtin_bit_cast(u16x8, af[t][jo]), accW[jo]);
                             else
@@ -1532,7 +1546,7 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
                                                        xlo[j][2 * t + 1][0], xlo[j][2 * t + 1][1]};
                                 const u16x8 xl = __builtin_bit_cast(u16x8, e);
 #pragma unroll
-                                for (int jo = 0; jo < 4; ++jo)
+                                for (int jo = 0; jo < WT; ++jo)
                                     accW[jo] = mfma32_f16(xl, __builtin_bit_cast(u16x8, af[t][jo]), accW[jo]);
                             }
                         }
@@ -1578,7 +1592,7 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
                         cur_rows.at(row, R, &m, &q);
                         float* yrow = P.y + k2_phys(m, q, P.rpm, P.T, P.y_stride, P.y_plane);
 #pragma unroll
-                        for (int jo = 0; jo < 4; ++jo)
+                        for (int jo = 0; jo < WT; ++jo)
                             if (32 * jo + lc < a)
                                 yrow[32 * jo + lc] = X ? accW[jo][4 * g + v] * (1.0f / K3_XSCALE)
                                                        : accW[jo][4 * g + v];
@@ -1615,7 +1629,33 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
                     }
                     if constexpr (RATE && qq % LT == LT - 1) {
                         const int32_t row = wrow0 + 16 * hl + qq;
-                        if (row < nvalid) {
+                        if (P.cpl) {
+                            // the counts' bit planes (0..LT needs log2(LT) + 1):
+                            // ballot bit l is column 32 jo + l % 32 of the row of
+                            // lane half l / 32, which lane 32 (l / 32) stores
+                            constexpr int NPL = LT == 1 ? 1 : LT == 2 ? 2 : LT == 4 ? 3 : LT == 8 ? 4 : 5;
+                            uint64_t pb[NPL][4];
+#pragma unroll
+                            for (int p = 0; p < NPL; ++p)
+#pragma unroll
+                                for (int jo = 0; jo < 4; ++jo)
+                                    pb[p][jo] = __builtin_amdgcn_ballot_w64(((cnt[jo] >> p) & 1) && colok[jo]);
+                            if (lc == 0 && row < nvalid) {
+                                int32_t m, q;
+                                cur_rows.at(row, R, &m, &q);
+                                uint64_t* dst = P.cpl + ((int64_t)m * P.rpm + q / LT) * P.cpl_stride;
+                                const int32_t words = (a + 63) >> 6;
+#pragma unroll
+                                for (int p = 0; p < NPL; ++p)
+#pragma unroll
+                                    for (int hh = 0; hh < 2; ++hh) {
+                                        const uint64_t b0 = pb[p][2 * hh], b1 = pb[p][2 * hh + 1];
+                                        const uint64_t w = hl ? (b0 >> 32) | (b1 & 0xffffffff00000000ull)
+                                                              : (b0 & 0xffffffffull) | (b1 << 32);
+                                        if (hh < words) dst[p * words + hh] = w;
+                                    }
+                            }
+                        } else if (row < nvalid) {
                             int32_t m, q;
                             cur_rows.at(row, R, &m, &q);
                             float* rp = P.rate + ((int64_t)m * P.rpm + q / LT) * P.rate_stride;
@@ -1786,6 +1826,7 @@ int launch_linear_pair(LinParams& P, DeviceState* st, hipStream_t s, void* work,
     const bool bits = P.x_fmt == HSES_FMT_BITS;
     // Bit-packed input with T <= 16 for the fused LIF: k_pair_bits.
     const bool v3 = bits && (!lif || P.n_time <= 16) && P.b <= 2 * K3_XPF * 64;
+    if (lif && lif->cpl && !v3) return HSES_ERR_UNSUPPORTED;  // count planes: k_pair_bits only
     const K2Layout lay(P.r, P.b, bits);
     // factors drawn ahead and K of more than two tiles (any K in the split
     // mode): the DL tile stream
@@ -1846,6 +1887,8 @@ int launch_linear_pair(LinParams& P, DeviceState* st, hipStream_t s, void* work,
         A.spk_plane = lif->spk_plane;
         A.rate = lif->rate;
         A.rate_stride = lif->rate_stride;
+        A.cpl = static_cast<uint64_t*>(lif->cpl);
+        A.cpl_stride = lif->cpl_stride;
         A.leak = lif->leak;
         A.v_th = lif->v_th;
     }
@@ -1887,8 +1930,13 @@ int launch_linear_pair(LinParams& P, DeviceState* st, hipStream_t s, void* work,
         auto by_pre = [&](auto pc, auto dc, auto xc) -> int {
             constexpr bool PR = decltype(pc)::value, D = decltype(dc)::value;
             constexpr bool XX = decltype(xc)::value;
-            if (!lif) return launch(k_pair_bits<EPI_Y, 1, false, false, PR, D, XX>);
-            const bool spk = lif->spk != nullptr, rate = lif->rate != nullptr;
+            if (!lif) {
+                // X with a <= 32 (the readout): one output tile
+                if constexpr (XX)
+                    if (P.a <= 32) return launch(k_pair_bits<EPI_Y, 1, false, false, PR, D, XX, 1>);
+                return launch(k_pair_bits<EPI_Y, 1, false, false, PR, D, XX>);
+            }
+            const bool spk = lif->spk != nullptr, rate = lif->rate != nullptr || lif->cpl != nullptr;
             auto by_t = [&](auto sc, auto rc) -> int {
                 constexpr bool S = decltype(sc)::value, Q = decltype(rc)::value;
                 switch (P.n_time) {

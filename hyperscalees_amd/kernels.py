@@ -358,6 +358,45 @@ def perturbed_linear_lif(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n,
     return spikes, rate
 
 
+def count_planes(n_time):
+    """Bit planes of a spike count over n_time steps (0..n_time)."""
+    return int(n_time).bit_length()
+
+
+def perturbed_linear_lif_counts_x(x, W, rank, sigma, tid_lo, n, rows_per_member, n_time, tau_m,
+                                  v_th, rec, img, counts=None, time_inner=False):
+    """The fp32-accurate fused forward + LIF on factors drawn ahead (`rec`,
+    split `img`) leaving each output row's spike count as bit planes: returns
+    counts (M, P, words(a)) int64, P = count_planes(n_time), bit c of plane p
+    being bit p of neuron c's count (hses_perturbed_linear_lif_counts_pre_x).
+    x as in perturbed_linear_lif."""
+    a, b = W.shape
+    _dev(W, torch.float32, "W")
+    _dev(x, _FMT_DTYPE[FMT_BITS], "x")
+    units = fmt_width(FMT_BITS, b)
+    M = n * rows_per_member
+    if x.shape[-1] != units or x.numel() != n_time * M * units:
+        raise ValueError(f"x has shape {tuple(x.shape)}, expected ({n_time}, {M}, {units})")
+    wa = fmt_width(FMT_BITS, a)
+    npl = count_planes(n_time)
+    if counts is None:
+        counts = torch.empty((M, npl, wa), dtype=torch.int64, device=W.device)
+    _dev(counts, torch.int64, "counts")
+    if counts.numel() != M * npl * wa:
+        raise ValueError("counts has the wrong size")
+    wbytes = int(_lib.load().hses_perturbed_linear_workspace(a, b, rank, n, rows_per_member,
+                                                              n_time, MATH_F32X))
+    work = _workspace(wbytes, W.device)
+    if time_inner:
+        xs, xp = n_time * units, units
+    else:
+        xs, xp = units, M * units
+    _lib.call("hses_perturbed_linear_lif_counts_pre_x", _p(x), FMT_BITS, xs, xp, n_time, _p(W),
+              a, b, rank, sigma, tid_lo, n, rows_per_member, tau_m, v_th, _p(counts), npl * wa,
+              _p(work), wbytes, *_rec_arg(rec), *_img_arg(img), _stream())
+    return counts
+
+
 def es_update(fit, tid_lo, key, rank, sigma, epoch, noise_reuse, a, b, scale, out=None,
               accumulate=False, work=None):
     """scale * sum_m fit[m] A_m B_m^T (factors regenerated in-kernel); adds into

@@ -185,12 +185,12 @@ class SnnEs:
                 self.img.append(torch.empty(nbytes // 2, dtype=torch.int16, device=device))
         # The split (fp32-accurate) mode: every layer's draw writes the record
         # and a split operand image (hses_pair_factors_x), which the forward
-        # reads in place of the bf16 image.  The last
-        # hidden layer keeps its spikes, and the readout runs on them row by
-        # row and time step by time step (rows_per_member = rows * T, one time
-        # plane), its outputs averaged over the T steps: by linearity that is
-        # the readout of the spike rate (snn.rs:274-280), whose bit-packed x
-        # the split kernels take exactly.
+        # reads in place of the bf16 image.  The last hidden layer leaves its
+        # spike counts as P = log2(T) + 1 bit planes, and the readout runs on
+        # the planes as P bit-packed rows per sample (rows_per_member =
+        # rows * P), its outputs combined with the weights 2^p / T: by
+        # linearity that is the readout of the spike rate (snn.rs:274-280),
+        # sum_p 2^p plane_p / T, which the split kernels take exactly.
         self.img_x = None
         if self.split:
             if not (self.ahead and self.time_inner and c.T <= 16):
@@ -203,7 +203,13 @@ class SnnEs:
                 nbytes = max(K._lib.load().hses_pair_image_x_bytes(a, b, c.rank, t, c.chunk)
                              for t in (0, n_odd))
                 self.img_x.append(torch.empty(nbytes // 2, dtype=torch.int16, device=device))
-            self.ylog = torch.empty((1, M * c.T, c.dims[-1]), dtype=torch.float32, device=device)
+            self.npl = K.count_planes(c.T)
+            self.cpl = torch.empty((M, self.npl, K.fmt_width(FMT_BITS, c.dims[-2])),
+                                   dtype=torch.int64, device=device)
+            self.ylog = torch.empty((1, M * self.npl, c.dims[-1]), dtype=torch.float32,
+                                    device=device)
+            self.plane_w = torch.tensor([2.0 ** p / c.T for p in range(self.npl)],
+                                        dtype=torch.float32, device=device).view(1, -1, 1)
 
     # -- forward -------------------------------------------------------------
     def spikes_tm(self, l):
@@ -230,10 +236,17 @@ class SnnEs:
         c = self.cfg
         a = c.dims[l + 1]
         if self.fused:
-            # feeds the readout: only its spike rates are used (the split mode
-            # reads its spikes)
-            last = l == self.L - 2 and not self.split
+            # feeds the readout: only its spike rates (split mode: spike-count
+            # planes) are used
+            last = l == self.L - 2
             img = self._draw(l, epoch, lo)
+            if last and self.split:
+                K.perturbed_linear_lif_counts_x(self.spk[l], self.W[l], c.rank, c.sigma, lo,
+                                                c.chunk, c.rows, c.T, c.tau_m, c.v_th,
+                                                self.rec[l], img, counts=self.cpl,
+                                                time_inner=self.time_inner)
+                self._rec_at[l] = (epoch, lo)
+                return
             K.perturbed_linear_lif(self.spk[l], self.W[l], c.keys[l], c.rank, c.sigma, epoch,
                                    c.noise_reuse, lo, c.chunk, c.rows, c.T, c.tau_m, c.v_th,
                                    spikes=None if last else self.spk[l + 1],
@@ -255,11 +268,11 @@ class SnnEs:
         c = self.cfg
         if self.split:
             img = self._draw(self.L - 1, epoch, lo)
-            x = self.spk[self.L - 1].view(1, self.M * c.T, -1)
+            x = self.cpl.view(1, self.M * self.npl, -1)
             K.perturbed_linear(x, self.W[-1], c.keys[-1], c.rank, c.sigma, epoch, c.noise_reuse,
-                               lo, c.chunk, c.rows * c.T, x_fmt=FMT_BITS, n_time=1,
+                               lo, c.chunk, c.rows * self.npl, x_fmt=FMT_BITS, n_time=1,
                                math=MATH_F32X, out=self.ylog, rec=self.rec[-1], img=img)
-            torch.mean(self.ylog.view(self.M, c.T, -1), 1, out=self.logits)
+            torch.sum(self.ylog.view(self.M, self.npl, -1) * self.plane_w, 1, out=self.logits)
             self._rec_at[-1] = (epoch, lo)
             labels = self.labels[lo * c.rows:(lo + c.chunk) * c.rows]
             return K.member_fitness(self.logits, labels, c.chunk, c.rows, c.reward,

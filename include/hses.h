@@ -396,6 +396,21 @@ int hses_perturbed_linear_lif_pre_x(const void *d_x, int32_t x_fmt, int64_t x_st
                                     size_t work_bytes, const float *d_rec, size_t rec_bytes,
                                     const uint16_t *d_img, size_t img_bytes, void *stream);
 
+/* hses_perturbed_linear_lif_pre_x that leaves each output row's spike count
+ * over the n_time steps as bit planes instead of spikes or rates: row
+ * (member m, sample s) holds P = log2(n_time) + 1 planes of ceil(a/64) words
+ * at d_counts + (m * rows_per_member + s) * counts_stride, bit c of plane p
+ * being bit p of neuron c's count.  rate = sum_p 2^p plane_p / n_time, so the
+ * readout of the rate (snn.rs:274-280) is sum_p (2^p / n_time) (plane_p W^T +
+ * (plane_p B) A^T): a bit-packed product over P rows per sample.  n_time a
+ * power of two <= 16, counts_stride >= P * ceil(a/64). */
+int hses_perturbed_linear_lif_counts_pre_x(
+    const void *d_x, int32_t x_fmt, int64_t x_stride, int64_t x_plane, int32_t n_time,
+    const float *d_W, int32_t a, int32_t b, int32_t rank, float sigma, int32_t tid_lo, int32_t n,
+    int32_t rows_per_member, float tau_m, float v_th, uint64_t *d_counts, int64_t counts_stride,
+    void *d_work, size_t work_bytes, const float *d_rec, size_t rec_bytes, const uint16_t *d_img,
+    size_t img_bytes, void *stream);
+
 /* ---- ES update ------------------------------------------------------- */
 
 /* EggRoll ES gradient of one MM parameter (eggroll.rs:353-404 _simple_lora_update +

@@ -8,8 +8,9 @@ accumulated in fp32.
   reference product x W^T + (x B_m) A_m^T (or_batched_lora_noise's factors):
   within 4e-6 of sum |terms| per element, and at least 50x closer than the
   bf16 path on the same inputs (so the bound tells the two apart);
-* spikes and rates (hses_perturbed_linear_lif_pre_x) equal the oracle's LIF
-  scan (snn.rs:53-97) of the split path's own currents, bit for bit (both
+* spikes and rates (hses_perturbed_linear_lif_pre_x), and the spike-count
+  bit planes (hses_perturbed_linear_lif_counts_pre_x), equal the oracle's LIF
+  scan (snn.rs:53-97) of the split path's own currents, bit for bit (the
   kernels share the accumulators; the LIF is fp32 in both);
 * the whole C3 step at N = 8192 in split mode: spike mismatches against the
   fp32 oracle (or_do_mm currents, or_lif_scan) per hidden layer, member
@@ -204,6 +205,16 @@ def test_lif_pre_x_equals_lif_of_its_currents(hses_gpu, a, b, r, n, tid_lo, rows
     assert ref_s.sum() > 0.02 * ref_s.size, "the layer is nearly silent"
     np.testing.assert_array_equal(got, ref_s)
     np.testing.assert_array_equal(rate.cpu().numpy(), ref_s.mean(0).astype(np.float32))
+    counts = K.perturbed_linear_lif_counts_x(x, Wd, r, sigma, tid_lo, n, rows, T, tau, vth, rec,
+                                             imx, time_inner=time_inner)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(decode_counts(counts, a), ref_s.sum(0))
+
+
+def decode_counts(counts, a):
+    """(M, P, words) count planes -> (M, a) counts."""
+    planes = unpack(counts, a)  # (M, P, a)
+    return sum(planes[:, p] * 2.0 ** p for p in range(planes.shape[1]))
 
 
 def test_split_rejects_unsupported(hses_gpu):
@@ -247,8 +258,9 @@ def c3x_run(hses_gpu):
     R = cfg.rows
     rows = np.concatenate([np.arange(m * R, (m + 1) * R) for m in MEMBERS])
     rows_t = torch.as_tensor(rows, device="cuda")
-    spk = [unpack(es.spikes_tm(l).index_select(1, rows_t), cfg.dims[l]) for l in range(es.L)]
-    return dict(cfg=cfg, pool=pool, labels=labels, idx=idx, W=W, spk=spk,
+    spk = [unpack(es.spikes_tm(l).index_select(1, rows_t), cfg.dims[l]) for l in range(es.L - 1)]
+    counts = decode_counts(es.cpl.index_select(0, rows_t), cfg.dims[-2])
+    return dict(cfg=cfg, pool=pool, labels=labels, idx=idx, W=W, spk=spk, counts=counts,
                 fit=fit.cpu().numpy().copy())
 
 
@@ -264,8 +276,14 @@ def test_c3_split_spikes_against_fp32_oracle(c3x_run):
             x = c3x_run["spk"][l][:, j * R:(j + 1) * R]
             cur = O.do_mm(x.reshape(-1, b), W[l], A[j], B[j]).reshape(cfg.T, R, a)
             ref, _ = O.lif(cur, cfg.tau_m, cfg.v_th)
-            got = c3x_run["spk"][l + 1][:, j * R:(j + 1) * R]
-            mism += int((got != ref).sum())
+            if l < L - 2:
+                got = c3x_run["spk"][l + 1][:, j * R:(j + 1) * R]
+                mism += int((got != ref).sum())
+            else:
+                # the last hidden layer leaves spike counts: |count difference|
+                # counts the flips that do not cancel within a (row, column)
+                got = c3x_run["counts"][j * R:(j + 1) * R]
+                mism += int(np.abs(got - ref.sum(0)).sum())
             n_ref += int(ref.sum())
         print(f"split layer {l}: {n_ref} reference spikes, {mism} mismatches against the "
               f"fp32 oracle ({mism / max(n_ref, 1):.2e})")
@@ -281,7 +299,7 @@ def test_c3_split_fitness(c3x_run):
     A, B = O.lora_factors(bs, cfg.keys[-1], cfg.rank, 0, np.array(MEMBERS), a, b)
     worst = 0.0
     for j, m in enumerate(MEMBERS):
-        rate = np.ascontiguousarray(c3x_run["spk"][-1][:, j * R:(j + 1) * R].mean(0), np.float32)
+        rate = np.ascontiguousarray(c3x_run["counts"][j * R:(j + 1) * R] / cfg.T, np.float32)
         logits = O.do_mm(rate, W[-1], A[j], B[j])
         lab = c3x_run["labels"][c3x_run["idx"][m * R:(m + 1) * R]]
         ref = float(O.loglik(logits, lab).astype(np.float64).mean())
