@@ -35,8 +35,7 @@ PEAK_HBM_GBPS = 8000.0
 # `python3 -m hyperscalees_amd.profile_fc1`: 4.067 GB x 2 + 0.134 GB, measured on the kernel
 # source of commit 8b404b2; see profiles/fc1_c3_traffic.md.  Refreshed whenever the kernel
 # changes; the bench line names the source it was measured on.
-FC1_TRAFFIC_BYTES = 8.27e9
-FC1_TRAFFIC_SOURCE = "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of profile_fc1 on commit 8b404b2"
+FC1_TRAFFIC = {}  # (math, member weights) -> (bytes per launch, source); filled once measured
 
 
 def layer_flops(cfg, l):
@@ -520,8 +519,9 @@ def main():
     ap.add_argument("--cpu-members", type=int, default=8192)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", choices=("c1", "c2", "c3", "c4", "c5"), default="c3")
-    ap.add_argument("--math", choices=("bf16", "f32x"), default="bf16",
-                    help="C3 forward arithmetic: bf16 MFMA, or fp32-accurate split fp16 operands")
+    ap.add_argument("--math", choices=("bf16", "f32x"), default="f32x",
+                    help="C3 forward arithmetic: fp32-accurate split fp16 operands (the "
+                         "reference's fp32 results), or the faster bf16 MFMA")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one GPU "
@@ -578,34 +578,65 @@ def main():
     t_fwd = np.mean([span(e, "start", "readout") for e in marks])
     t_upd = np.mean([span(e, "readout", "update") for e in marks])
 
-    # Dominant kernel: fc1's perturbed forward (x[W^T|B] + (xB)A^T, bf16 MFMA,
-    # LIF fused), timed alone with events on the launch stream: with factors
-    # drawn ahead, the GEMM kernel on the record and operand image (its draw,
-    # k_pair_gen, timed beside it); otherwise the kernel that draws inline.
+    # Dominant kernel: fc1's forward GEMM with the LIF fused, timed alone with
+    # events on the launch stream.  On member weights (the C3 step's path):
+    # k_pair_bits<.., MW> computing x W_m^T, beside the two launches that feed
+    # it, the factor draw (k_pair_gen, the record alone) and the member-weight
+    # product (k_member_weights); on the factored forward, the GEMM on the
+    # drawn factors x[W^T|B] + (xB)A^T (or the kernel that draws inline).
     a1, b1 = es.W[0].shape
+    kp1 = (b1 + 63) // 64 * 64
     draw = None
-    if es.ahead:
+    wm_info = None
+    normals = (cfg.n // 2) * cfg.rank * (a1 + b1)
+    if es.mw:
+        fc1_draw = lambda: K.pair_factors(cfg.keys[0], cfg.rank, cfg.sigma, 0, cfg.noise_reuse, 0,
+                                          cfg.n, a1, b1, es.rec[0], None)
+        draw_ms = _time_launch(fc1_draw, reps=3)
+        wbytes = normals * 4
+        nwm = K._lib.load().hses_member_weights_bytes(a1, b1, cfg.n, cfg.math) // 2
+        wm1 = es.wm[:nwm]
+        fc1_wm = lambda: K.member_weights(es.W[0], cfg.rank, cfg.sigma, 0, cfg.n, es.rec[0],
+                                          math=cfg.math, out=wm1)
+        wm_ms = _time_launch(fc1_wm, reps=3)
+        wm_bytes = nwm * 2 + normals * 4  # written + the record read
+        wm_info = {"kernel": ("k_member_weights<" + ("split" if es.split else "bf16")
+                              + "> (fc1: every member's W + sign (sigma/sqrt(r)) A B^T from the "
+                              "factor record, " + ("fp16 high and low parts"
+                                                   if es.split else "bf16") + ")"),
+                   "bound": "hbm", "launch_ms": round(wm_ms, 4),
+                   "hbm_bytes": wm_bytes, "written_bytes": nwm * 2,
+                   "achieved_GBps": round(wm_bytes / (wm_ms * 1e-3) / 1e9, 1),
+                   "frac": round(wm_bytes / (wm_ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
+                   "mfma_flop_per_launch": 2 * (cfg.n // 2) * a1 * kp1 * cfg.rank * 3}
+        fc1_draw()
+        fc1_wm()
+    elif es.ahead:
         img1 = es.img_x[0] if es.split else es.img[0]
         fc1_draw = lambda: K.pair_factors(cfg.keys[0], cfg.rank, cfg.sigma, 0, cfg.noise_reuse, 0,
                                           cfg.n, a1, b1, es.rec[0], img1, split=es.split)
         draw_ms = _time_launch(fc1_draw, reps=3)
-        normals = (cfg.n // 2) * cfg.rank * (a1 + b1)
         parts = 2 if es.split else 1  # the split image holds high and low parts
-        wbytes = normals * 4 + parts * (cfg.n // 2) * (cfg.rank * ((b1 + 63) // 64 * 64)
-                                                       + a1 * 136) * 2
+        wbytes = normals * 4 + parts * (cfg.n // 2) * (cfg.rank * kp1 + a1 * 136) * 2
+        fc1_draw()
+    if es.ahead:
         draw = {"kernel": ("k_pair_gen (fc1 factors: every pair's exact Box-Muller normals into "
-                           "the factor record and the "
-                           + ("split fp16 operand image)" if es.split else "bf16 operand image)")),
+                           "the factor record"
+                           + ("" if es.mw else (" and the split fp16 operand image" if es.split
+                                                else " and the bf16 operand image")) + ")"),
                 "bound": "valu", "launch_ms": round(draw_ms, 4), "normals_per_launch": normals,
                 "g_normals_per_s": round(normals / (draw_ms * 1e-3) / 1e9, 1),
                 "hbm_bytes_written": wbytes,
                 "hbm_frac": round(wbytes / (draw_ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
-        fc1_draw()
     fc1_ms = []
     for s in range(3):
         e0, e1 = ev(), ev()
         e0.record()
-        if es.ahead:
+        if es.mw:
+            K.perturbed_linear_lif_mw(es.spk[0], wm1, a1, b1, 0, cfg.n, cfg.rows, cfg.T,
+                                      cfg.tau_m, cfg.v_th, math=cfg.math, spikes=es.spk[1],
+                                      time_inner=es.time_inner)
+        elif es.ahead:
             K.perturbed_linear_lif(es.spk[0], es.W[0], cfg.keys[0], cfg.rank, cfg.sigma, 0,
                                    cfg.noise_reuse, 0, cfg.n, cfg.rows, cfg.T, cfg.tau_m,
                                    cfg.v_th, spikes=es.spk[1], rec=es.rec[0],
@@ -624,8 +655,20 @@ def main():
         torch.cuda.synchronize()
         fc1_ms.append(e0.elapsed_time(e1))
     fc1_ms = float(np.median(fc1_ms))
-    fc1_flops = layer_flops(cfg, 0)
+    M1 = cfg.n * cfg.rows * cfg.T
+    # algorithmic FLOPs of the kernel: x W_m^T on member weights, else the
+    # factored product (layer_flops)
+    fc1_flops = 2 * M1 * b1 * a1 if es.mw else layer_flops(cfg, 0)
+    # matrix-core FLOPs it issues: K padded to whole 64-k tiles, twice for the
+    # split operands (and the factored form's 256 staged columns and rank
+    # product)
+    if es.mw:
+        mfma_flops = 2 * M1 * kp1 * a1 * (2 if es.split else 1)
+    else:
+        mfma_flops = (2 * M1 * kp1 * (a1 + cfg.rank) * (2 if es.split else 1)
+                      + 2 * M1 * cfg.rank * a1 * (3 if es.split else 1))
     achieved = fc1_flops / (fc1_ms * 1e-3) / 1e12
+    traffic_key = ("f32x" if es.split else "bf16", bool(es.mw))
 
     # fc1's ES update from the factor record (HBM-bound): algorithmic bytes are
     # the record (pairs x r x (a + b) fp32) plus the gradient written.
@@ -673,18 +716,29 @@ def main():
                      "readout_fitness": round(float(t_readout), 3),
                      "forward": round(float(t_fwd), 3), "es_update": round(float(t_upd), 3)},
         "fwd_tflops": round(fwd_flops / (t_fwd * 1e-3) / 1e12, 1),
-        "roofline": {"kernel": (("k_pair_bits<LIF, T=16, spikes, factors drawn ahead"
-                                 + (", split fp16 operands" if es.split else "") + "> (fc1 GEMM: "
-                                 if es.ahead else "k_pair_bits (fc1: ")
-                                + "x[W^T|B] + (xB)A^T, T=16 x 524288 rows"
-                                + (", LIF fused)" if es.fused else ")")),
+        "roofline": {"kernel": (("k_pair_bits<LIF, T=16, spikes, member weights"
+                                 + (", split fp16 operands" if es.split else "")
+                                 + "> (fc1: x W_m^T, T=16 x 524288 rows, LIF fused)")
+                                if es.mw else
+                                (("k_pair_bits<LIF, T=16, spikes, factors drawn ahead"
+                                  + (", split fp16 operands" if es.split else "") + "> (fc1 GEMM: "
+                                  if es.ahead else "k_pair_bits (fc1: ")
+                                 + "x[W^T|B] + (xB)A^T, T=16 x 524288 rows"
+                                 + (", LIF fused)" if es.fused else ")"))),
                      "bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": (FC1_TRAFFIC_BYTES if es.ahead and not es.split else None),
-                     "traffic_source": (FC1_TRAFFIC_SOURCE if es.ahead and not es.split else None),
+                     "traffic": FC1_TRAFFIC.get(traffic_key, (None, None))[0],
+                     "traffic_source": FC1_TRAFFIC.get(traffic_key, (None, None))[1],
                      "launch_ms": round(fc1_ms, 3),
-                     "algorithmic_flop_per_launch": fc1_flops},
+                     "algorithmic_flop_per_launch": fc1_flops,
+                     # the matrix-core work the kernel issues (split operands:
+                     # each product twice) against the same fp16/bf16 peak
+                     "mfma_flop_per_launch": mfma_flops,
+                     "mfma_issue_frac": round(mfma_flops / (fc1_ms * 1e-3) / 1e12
+                                              / PEAK_BF16_TFLOPS, 4)},
     }
+    if wm_info is not None:
+        out["member_weights"] = wm_info
     if draw is not None:
         out["draw"] = draw
     if upd_roof is not None:

@@ -72,6 +72,16 @@ PROTOTYPES = {
                                                      c_vp, c_i64, c_vp, c_size, c_vp, c_size,
                                                      c_vp, c_size, c_vp]),
     "hses_pair_image_x_bytes": (c_size, [c_i32, c_i32, c_i32, c_i32, c_i32]),
+    "hses_member_weights_bytes": (c_size, [c_i32, c_i32, c_i32, c_i32]),
+    "hses_member_weights": (ctypes.c_int, [c_vp, c_i32, c_i32, c_i32, c_f32, c_i32, c_i32, c_vp,
+                                           c_size, c_i32, c_vp, c_size, c_vp]),
+    "hses_perturbed_linear_mw": (ctypes.c_int, [c_vp, c_i32, c_i64, c_i64, c_i32, c_i32, c_i32,
+                                                c_i32, c_i32, c_i32, c_i32, c_vp, c_size, c_vp,
+                                                c_i64, c_i64, c_vp]),
+    "hses_perturbed_linear_lif_mw": (ctypes.c_int, [c_vp, c_i32, c_i64, c_i64, c_i32, c_i32,
+                                                    c_i32, c_i32, c_i32, c_i32, c_f32, c_f32,
+                                                    c_i32, c_vp, c_size, c_vp, c_i64, c_i64, c_vp,
+                                                    c_i64, c_vp, c_i64, c_vp]),
     "hses_perturbed_linear_lif_counts_pre_x": (ctypes.c_int, [c_vp, c_i32, c_i64, c_i64, c_i32,
                                                               c_vp, c_i32, c_i32, c_i32, c_f32,
                                                               c_i32, c_i32, c_i32, c_f32, c_f32,

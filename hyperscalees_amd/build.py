@@ -17,7 +17,7 @@ BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libhses.so")
 SOURCES = ["runtime.cpp", "bm_tables.cpp", "data.cpp", "noise.hip", "spiking.hip", "small.hip",
            "linear.hip", "linear_pair.hip", "linear_wide.hip", "es_update.hip", "rwkv.hip",
-           "attention.hip", "linear_f32.hip", "linear_bf16.hip"]
+           "attention.hip", "linear_f32.hip", "linear_bf16.hip", "linear_mw.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

@@ -634,7 +634,7 @@ extern "C" int hses_perturbed_linear_lif_rec(const void* d_x, int32_t x_fmt, int
 // arguments alone (before the device is touched).
 static int check_drawn(int32_t a, int32_t b, int32_t rank, float sigma, int32_t tid_lo, int32_t n,
                        const float* d_rec, size_t rec_bytes, const void* d_img, size_t img_bytes,
-                       const char* name, bool split = false) {
+                       const char* name, bool split = false, bool img_optional = false) {
     const int32_t r = (sigma != 0.0f) ? rank : 0;
     HSES_REQUIRE(a >= 1 && a <= 128,
                  std::string(name) + ": output width a must be in [1, 128] (the pair kernels)");
@@ -644,6 +644,7 @@ static int check_drawn(int32_t a, int32_t b, int32_t rank, float sigma, int32_t 
     HSES_REQUIRE(d_rec, std::string(name) + ": factor record is NULL");
     HSES_REQUIRE(rec_bytes >= hses_factor_record_bytes(a, b, r, tid_lo, n),
                  std::string(name) + ": factor record smaller than hses_factor_record_bytes");
+    if (img_optional && !d_img && img_bytes == 0) return HSES_OK;  // the record alone
     HSES_REQUIRE(d_img, std::string(name) + ": operand image is NULL");
     if (split)
         HSES_REQUIRE(img_bytes >= pair_image_x_bytes(a, b, r, tid_lo, n),
@@ -669,7 +670,7 @@ static int pair_factors_impl(uint64_t key, int32_t rank, float sigma, int32_t ep
     HSES_REQUIRE(tid_lo >= 0 && (int64_t)tid_lo + n - 1 <= INT32_MAX, "thread id range");
     if (n == 0) return HSES_OK;
     int rc = check_drawn(a, b, rank, sigma, tid_lo, n, d_rec, rec_bytes, d_img, img_bytes,
-                         split ? "hses_pair_factors_x" : "hses_pair_factors", split);
+                         split ? "hses_pair_factors_x" : "hses_pair_factors", split, true);
     if (rc) return rc;
     DeviceState* st;
     rc = get_state(&st);
@@ -814,6 +815,126 @@ extern "C" int hses_perturbed_linear_pre_x(const void* d_x, int32_t x_fmt, int64
     return linear_pre_impl(d_x, x_fmt, x_stride, x_plane, n_time, d_W, a, b, rank, sigma, tid_lo,
                            n, rows_per_member, d_y, y_stride, y_plane, d_work, work_bytes, d_rec,
                            rec_bytes, d_img, img_bytes, stream, true);
+}
+
+// ---- member weights ------------------------------------------------------------
+// W_m = W + sign_m (sigma / sqrt(r)) A_m B_m^T of every member from the factor
+// record (hses_member_weights), then the forwards y = x W_m^T on them
+// (hses_perturbed_linear_mw, hses_perturbed_linear_lif_mw).
+
+static int check_mw_math(int32_t math, const char* name) {
+    HSES_REQUIRE(math == HSES_MATH_BF16 || math == HSES_MATH_F32X,
+                 std::string(name) + ": math must be HSES_MATH_BF16 or HSES_MATH_F32X");
+    return HSES_OK;
+}
+
+extern "C" size_t hses_member_weights_bytes(int32_t a, int32_t b, int32_t n, int32_t math) {
+    if (math != HSES_MATH_BF16 && math != HSES_MATH_F32X) return 0;
+    return member_weights_bytes(a, b, n, math == HSES_MATH_F32X);
+}
+
+extern "C" int hses_member_weights(const float* d_W, int32_t a, int32_t b, int32_t rank,
+                                   float sigma, int32_t tid_lo, int32_t n, const float* d_rec,
+                                   size_t rec_bytes, int32_t math, uint16_t* d_wm,
+                                   size_t wm_bytes, void* stream) {
+    HSES_REQUIRE(a >= 1 && b >= 1 && n >= 0 && rank >= 0, "bad sizes");
+    HSES_REQUIRE(tid_lo >= 0 && (int64_t)tid_lo + n - 1 <= INT32_MAX, "thread id range");
+    int rc = check_mw_math(math, "hses_member_weights");
+    if (rc || n == 0) return rc;
+    rc = check_drawn(a, b, rank, sigma, tid_lo, n, d_rec, rec_bytes, nullptr, 0,
+                     "hses_member_weights", false, true);
+    if (rc) return rc;
+    HSES_REQUIRE(d_W && d_wm, "NULL pointer");
+    HSES_REQUIRE(wm_bytes >= member_weights_bytes(a, b, n, math == HSES_MATH_F32X),
+                 "hses_member_weights: buffer smaller than hses_member_weights_bytes");
+    DeviceState* st;
+    rc = get_state(&st);
+    if (rc) return rc;
+    return launch_member_weights(d_W, d_rec, a, b, rank, sigma / sqrtf((float)rank) /* eggroll.rs:433 */,
+                                 tid_lo, n, math == HSES_MATH_F32X, d_wm, (hipStream_t)stream);
+}
+
+// Checks shared by the two member-weight forwards; fills P (x, sizes, the
+// weights).
+static int mw_params(LinParams* P, DeviceState** st, const void* d_x, int32_t x_fmt,
+                     int64_t x_stride, int64_t x_plane, int32_t n_time, int32_t a, int32_t b,
+                     int32_t tid_lo, int32_t n, int32_t rows_per_member, int32_t math,
+                     const uint16_t* d_wm, size_t wm_bytes, const char* name) {
+    int rc = check_mw_math(math, name);
+    if (rc) return rc;
+    HSES_REQUIRE(x_fmt == HSES_FMT_BITS, std::string(name) + ": x must be bit-packed (x_fmt BITS)");
+    HSES_REQUIRE(a >= 1 && a <= 128 && b >= 1 && b <= 1024,
+                 std::string(name) + ": needs a <= 128 and b <= 1024");
+    HSES_REQUIRE(math == HSES_MATH_F32X || b > 64,
+                 std::string(name) + ": bf16 member weights need b > 64");
+    // a stand-in W pointer: make_params checks it, the kernels read d_wm
+    rc = make_params(P, d_x, x_fmt, x_stride, x_plane, n_time, reinterpret_cast<const float*>(d_wm),
+                     a, b, 0, 0, 0.0f, 0, 0, tid_lo, n, rows_per_member, HSES_MATH_BF16, st);
+    if (rc || n == 0) return rc;
+    HSES_REQUIRE(((int64_t)n_time * rows_per_member) % 256 == 0,
+                 std::string(name) + ": rows per member (n_time x rows_per_member) must be a "
+                                     "multiple of 256");
+    HSES_REQUIRE(wm_bytes >= member_weights_bytes(a, b, n, math == HSES_MATH_F32X),
+                 std::string(name) + ": weights smaller than hses_member_weights_bytes");
+    P->math = math;
+    P->wm = d_wm;
+    P->wm_stride = (int64_t)(member_weights_bytes(a, b, 1, math == HSES_MATH_F32X) / 2);
+    return HSES_OK;
+}
+
+extern "C" int hses_perturbed_linear_mw(const void* d_x, int32_t x_fmt, int64_t x_stride,
+                                        int64_t x_plane, int32_t n_time, int32_t a, int32_t b,
+                                        int32_t tid_lo, int32_t n, int32_t rows_per_member,
+                                        int32_t math, const uint16_t* d_wm, size_t wm_bytes,
+                                        float* d_y, int64_t y_stride, int64_t y_plane,
+                                        void* stream) {
+    LinParams P;
+    DeviceState* st = nullptr;
+    int rc = mw_params(&P, &st, d_x, x_fmt, x_stride, x_plane, n_time, a, b, tid_lo, n,
+                       rows_per_member, math, d_wm, wm_bytes, "hses_perturbed_linear_mw");
+    if (rc || n == 0) return rc;
+    HSES_REQUIRE(d_y, "NULL pointer");
+    HSES_REQUIRE(rows_layout_ok(a, (int64_t)n * rows_per_member, n_time, y_stride, y_plane),
+                 "y rows overlap (y_stride smaller than a row, or time planes overlap)");
+    P.y = d_y;
+    P.y_stride = y_stride;
+    P.y_plane = y_plane;
+    rc = launch_linear_mw(P, st, (hipStream_t)stream, nullptr);
+    if (rc == HSES_ERR_UNSUPPORTED)
+        return set_error(HSES_ERR_UNSUPPORTED, "hses_perturbed_linear_mw: unsupported shape");
+    return rc;
+}
+
+extern "C" int hses_perturbed_linear_lif_mw(
+    const void* d_x, int32_t x_fmt, int64_t x_stride, int64_t x_plane, int32_t n_time, int32_t a,
+    int32_t b, int32_t tid_lo, int32_t n, int32_t rows_per_member, float tau_m, float v_th,
+    int32_t math, const uint16_t* d_wm, size_t wm_bytes, uint64_t* d_spikes, int64_t spk_stride,
+    int64_t spk_plane, float* d_rate, int64_t rate_stride, uint64_t* d_counts,
+    int64_t counts_stride, void* stream) {
+    HSES_REQUIRE(tau_m != 0.0f, "tau_m must be non-zero");
+    HSES_REQUIRE(n_time >= 1 && n_time <= 16 && (n_time & (n_time - 1)) == 0,
+                 "hses_perturbed_linear_lif_mw: n_time must be a power of two <= 16");
+    LinParams P;
+    DeviceState* st = nullptr;
+    int rc = mw_params(&P, &st, d_x, x_fmt, x_stride, x_plane, n_time, a, b, tid_lo, n,
+                       rows_per_member, math, d_wm, wm_bytes, "hses_perturbed_linear_lif_mw");
+    if (rc || n == 0) return rc;
+    HSES_REQUIRE(d_spikes || d_rate || d_counts, "spikes, rate and counts are all NULL");
+    HSES_REQUIRE(!(d_rate && d_counts), "rate and counts are exclusive");
+    const int64_t M = (int64_t)n * rows_per_member;
+    HSES_REQUIRE(!d_spikes || rows_layout_ok((a + 63) / 64, M, n_time, spk_stride, spk_plane),
+                 "spike rows overlap (spk_stride smaller than a row, or time planes overlap)");
+    HSES_REQUIRE(!d_rate || rate_stride >= a, "rate_stride smaller than a row");
+    int32_t planes = 1;
+    while ((1 << (planes - 1)) < n_time) ++planes;
+    HSES_REQUIRE(!d_counts || counts_stride >= (int64_t)planes * ((a + 63) / 64),
+                 "counts_stride smaller than a row's count planes");
+    LifOut lif{d_spikes, spk_stride, spk_plane, d_rate, rate_stride,
+               1.0f / tau_m /* snn.rs:59: dt / tau_m with dt = 1 */, v_th, d_counts, counts_stride};
+    rc = launch_linear_mw(P, st, (hipStream_t)stream, &lif);
+    if (rc == HSES_ERR_UNSUPPORTED)
+        return set_error(HSES_ERR_UNSUPPORTED, "hses_perturbed_linear_lif_mw: unsupported shape");
+    return rc;
 }
 
 extern "C" int hses_perturbed_linear_lif_counts_pre_x(

@@ -62,6 +62,9 @@ struct LinParams {
     const uint32_t* cos_exc;
     const uint64_t* jump;
     float* rec;  // factor record (pair kernels, do_mm), or NULL
+    // member weights (launch_linear_mw): member tid_lo + m's at wm + m * wm_stride
+    const uint16_t* wm;
+    int64_t wm_stride;
 };
 
 // Physical offset (in units) of member-major logical row L: member m = L / R,
@@ -186,6 +189,15 @@ size_t pair_image_bytes(int32_t a, int32_t b, int32_t r, int32_t tid_lo, int32_t
 int launch_pair_image_x(const float* rec, int32_t a, int32_t b, int32_t r, float bs, int32_t tid_lo,
                         int32_t n, uint16_t* img, hipStream_t s);
 size_t pair_image_x_bytes(int32_t a, int32_t b, int32_t r, int32_t tid_lo, int32_t n);
+// Member weights (linear_mw.hip): W_m = W + sign_m bs A_m B_m^T of members
+// [tid_lo, tid_lo + n) from their factor record, bf16 (a, kp) per member or,
+// split, the fp16 high and low parts of 1024 W_m; and the forward on them
+// (P.wm, P.wm_stride; bit-packed x, rows per member a multiple of 256).
+size_t member_weights_bytes(int32_t a, int32_t b, int32_t n, bool split);
+int launch_member_weights(const float* W, const float* rec, int32_t a, int32_t b, int32_t r,
+                          float bs, int32_t tid_lo, int32_t n, bool split, uint16_t* wm,
+                          hipStream_t s);
+int launch_linear_mw(LinParams& P, DeviceState* st, hipStream_t s, const LifOut* lif);
 // The wide small-rank kernel: 0 when it does not apply to the shape, else its
 // workspace (W as bf16, (a, kp)).
 size_t linear_wide_workspace(int32_t a, int32_t b, int32_t r, int32_t n, int32_t rows_per_member,

@@ -203,10 +203,89 @@ def pair_factors(key, rank, sigma, epoch, noise_reuse, tid_lo, n, a, b, rec, img
     record `rec` and the operand image `img` (hses_pair_factors); the forwards
     given rec= and img= then read them instead of drawing.  split: `img` is the
     split image (pair_image_x) for the fp32-accurate forwards
-    (hses_pair_factors_x)."""
+    (hses_pair_factors_x).  img=None: the record alone (member_weights'
+    input)."""
+    img_args = (None, 0) if img is None else _img_arg(img)
     _lib.call("hses_pair_factors_x" if split else "hses_pair_factors", key & (2**64 - 1), rank,
-              sigma, epoch, noise_reuse, tid_lo, n, a, b, *_rec_arg(rec), *_img_arg(img),
-              _stream())
+              sigma, epoch, noise_reuse, tid_lo, n, a, b, *_rec_arg(rec), *img_args, _stream())
+
+
+def member_weights(W, rank, sigma, tid_lo, n, rec, math=MATH_F32X, out=None):
+    """Every member's perturbed weights W + sign_m (sigma/sqrt(r)) A_m B_m^T from
+    the factor record (hses_member_weights): int16 storage of bf16 (math BF16)
+    or of fp16 high and low parts of 1024 W_m (math F32X)."""
+    a, b = W.shape
+    _dev(W, torch.float32, "W")
+    nbytes = int(_lib.load().hses_member_weights_bytes(a, b, n, math))
+    if nbytes == 0:
+        raise ValueError("no member weights for this shape / math")
+    if out is None:
+        out = torch.empty(nbytes // 2, dtype=torch.int16, device=W.device)
+    _dev(out, torch.int16, "out")
+    _lib.call("hses_member_weights", _p(W), a, b, rank, sigma, tid_lo, n, *_rec_arg(rec), math,
+              _p(out), out.numel() * 2, _stream())
+    return out
+
+
+def perturbed_linear_mw(x, wm, a, b, tid_lo, n, rows_per_member, n_time=1, math=MATH_F32X,
+                        out=None):
+    """y = x W_m^T on member weights (hses_perturbed_linear_mw); x bit-packed
+    (n_time, M, words(b)) or 2-D; returns y (n_time, M, a) fp32."""
+    _dev(x, _FMT_DTYPE[FMT_BITS], "x")
+    _dev(wm, torch.int16, "wm")
+    units = fmt_width(FMT_BITS, b)
+    M = n * rows_per_member
+    if x.shape[-1] != units or x.numel() != n_time * M * units:
+        raise ValueError(f"x has shape {tuple(x.shape)}, expected ({n_time}, {M}, {units})")
+    if out is None:
+        out = torch.empty((n_time, M, a), dtype=torch.float32, device=x.device)
+    _dev(out, torch.float32, "out")
+    if out.numel() != n_time * M * a:
+        raise ValueError("out has the wrong size")
+    _lib.call("hses_perturbed_linear_mw", _p(x), FMT_BITS, units, M * units, n_time, a, b, tid_lo,
+              n, rows_per_member, math, _p(wm), wm.numel() * 2, _p(out), a, M * a, _stream())
+    return out if n_time > 1 or x.dim() == 3 else out[0]
+
+
+def perturbed_linear_lif_mw(x, wm, a, b, tid_lo, n, rows_per_member, n_time, tau_m, v_th,
+                            math=MATH_F32X, spikes=None, rate=None, counts=None,
+                            time_inner=False):
+    """The fused forward + LIF on member weights (hses_perturbed_linear_lif_mw):
+    any of spikes (time-major (T, M, words), or (M, T, words) with time_inner),
+    rate (M, a) and counts (M, P, words) given as tensors (or True to allocate)
+    is written; returns (spikes, rate, counts)."""
+    _dev(x, _FMT_DTYPE[FMT_BITS], "x")
+    _dev(wm, torch.int16, "wm")
+    units = fmt_width(FMT_BITS, b)
+    M = n * rows_per_member
+    if x.shape[-1] != units or x.numel() != n_time * M * units:
+        raise ValueError(f"x has shape {tuple(x.shape)}, expected ({n_time}, {M}, {units})")
+    wa = fmt_width(FMT_BITS, a)
+    npl = count_planes(n_time)
+    if spikes is True:
+        spikes = torch.empty((M, n_time, wa) if time_inner else (n_time, M, wa),
+                             dtype=torch.int64, device=x.device)
+    if rate is True:
+        rate = torch.empty((M, a), dtype=torch.float32, device=x.device)
+    if counts is True:
+        counts = torch.empty((M, npl, wa), dtype=torch.int64, device=x.device)
+    for t, nm, dt, numel in ((spikes, "spikes", torch.int64, n_time * M * wa),
+                             (rate, "rate", torch.float32, M * a),
+                             (counts, "counts", torch.int64, M * npl * wa)):
+        if t is not None:
+            _dev(t, dt, nm)
+            if t.numel() != numel:
+                raise ValueError(f"{nm} has the wrong size")
+    if time_inner:
+        xs, xp, ss, sp = n_time * units, units, n_time * wa, wa
+    else:
+        xs, xp, ss, sp = units, M * units, wa, M * wa
+    _lib.call("hses_perturbed_linear_lif_mw", _p(x), FMT_BITS, xs, xp, n_time, a, b, tid_lo, n,
+              rows_per_member, tau_m, v_th, math, _p(wm), wm.numel() * 2,
+              _p(spikes) if spikes is not None else None, ss, sp,
+              _p(rate) if rate is not None else None, a,
+              _p(counts) if counts is not None else None, npl * wa, _stream())
+    return spikes, rate, counts
 
 
 def perturbed_linear(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n, rows_per_member,

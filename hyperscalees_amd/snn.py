@@ -47,7 +47,12 @@ class SnnConfig:
     tau_m: float = 10.0            # leak 1/tau = 0.1, i.e. decay 0.9
     v_th: float = 1.0
     noise_reuse: int = 0
-    math: int = MATH_BF16
+    # MATH_F32X: fp32-accurate forward (split fp16 operands; the reference's
+    # fp32 arithmetic), on the fused path with factors drawn ahead (rank a
+    # multiple of 16 in [32, 128], hidden widths <= 128, T <= 16).  MATH_BF16:
+    # the faster bf16 forward (spikes differ from fp32 near the threshold).
+    # MATH_F32: the generic fp32 kernels (small ranks).
+    math: int = MATH_F32X
     solver: int = ADAMW
     lr: float = 0.01
     beta1: float = 0.9
@@ -113,7 +118,7 @@ class SnnEs:
     """Device-resident SNN-MLP population evaluation and ES update."""
 
     def __init__(self, cfg, weights, pool, pool_labels, index, device="cuda", fused=None,
-                 record=None, ahead=None):
+                 record=None, ahead=None, member_weights=None, overlap=None):
         self.cfg = cfg
         c = cfg
         self.dev = device
@@ -174,11 +179,40 @@ class SnnEs:
         # record and the bf16 B operand image instead of drawing.
         self.ahead = self.record if ahead is None else (bool(ahead) and self.record)
         self.split = c.math == MATH_F32X
+        # Member weights (factors drawn ahead, rows per member = samples x T a
+        # multiple of 256): each hidden layer's draw writes the record alone,
+        # hses_member_weights forms every member's W + sign (sigma/sqrt(r)) A B^T
+        # from it, and the forward is x W_m^T (half the matrix work of the
+        # factored product at 1024 rows per member); the readout, with fewer
+        # rows per member, stays on the factored product.
+        can_mw = (self.ahead and (c.rows * c.T) % 256 == 0
+                  and (self.split or min(c.dims[:-2]) > 64))
+        self.mw = can_mw if member_weights is None else (bool(member_weights) and can_mw)
+        self.wm = None
+        if self.mw:
+            n_odd = c.chunk if c.accumulate > 1 and c.chunk % 2 else 0
+            nbytes = max(K._lib.load().hses_member_weights_bytes(w.shape[0], w.shape[1],
+                                                                 c.chunk + (n_odd > 0), c.math)
+                         for w in self.W[:-1])
+            self.wm = torch.empty(nbytes // 2, dtype=torch.int16, device=device)
+        # The draws (VALU-bound, independent of the activations) run on a
+        # second stream at the default priority: the first layer's as the
+        # chunk's forward starts (beside the Poisson encode), the others once
+        # the first layer's GEMM is issued, so that they share the CUs with
+        # that matrix-core-bound kernel (one draw wave per SIMD fits beside
+        # it); each layer's forward waits for its draw.
+        can_overlap = self.ahead and str(device).startswith("cuda")
+        self.overlap = can_overlap if overlap is None else (bool(overlap) and can_overlap)
+        self.side = torch.cuda.Stream(device=device) if self.overlap else None
+        self._drawn = {}  # layer -> (epoch, lo, event) of a draw issued on the side stream
         self.img = None
         if self.ahead and not self.split:
             self.img = []
             n_odd = c.chunk if c.accumulate > 1 and c.chunk % 2 else 0
-            for w in self.W:
+            for l, w in enumerate(self.W):
+                if self.mw and l < L - 1:
+                    self.img.append(None)  # member weights instead
+                    continue
                 a, b = w.shape
                 nbytes = max(K._lib.load().hses_pair_image_bytes(a, b, c.rank, t, c.chunk)
                              for t in (0, n_odd))
@@ -198,7 +232,10 @@ class SnnEs:
                                  "(rank a multiple of 16 in [32, 128], widths <= 128, T <= 16)")
             self.img_x = []
             n_odd = c.chunk if c.accumulate > 1 and c.chunk % 2 else 0
-            for w in self.W:
+            for l, w in enumerate(self.W):
+                if self.mw and l < L - 1:
+                    self.img_x.append(None)  # member weights instead
+                    continue
                 a, b = w.shape
                 nbytes = max(K._lib.load().hses_pair_image_x_bytes(a, b, c.rank, t, c.chunk)
                              for t in (0, n_odd))
@@ -240,6 +277,16 @@ class SnnEs:
             # planes) are used
             last = l == self.L - 2
             img = self._draw(l, epoch, lo)
+            if self.mw:
+                # img: the member weights of this layer
+                counts = self.cpl if last and self.split else None
+                K.perturbed_linear_lif_mw(self.spk[l], img, a, c.dims[l], lo, c.chunk, c.rows, c.T,
+                                          c.tau_m, c.v_th, math=c.math,
+                                          spikes=None if last else self.spk[l + 1],
+                                          rate=self.rate if last and not self.split else None,
+                                          counts=counts, time_inner=self.time_inner)
+                self._rec_at[l] = (epoch, lo)
+                return
             if last and self.split:
                 K.perturbed_linear_lif_counts_x(self.spk[l], self.W[l], c.rank, c.sigma, lo,
                                                 c.chunk, c.rows, c.T, c.tau_m, c.v_th,
@@ -290,23 +337,62 @@ class SnnEs:
         return K.member_fitness(self.logits, labels, c.chunk, c.rows, c.reward,
                                 out=self.raw[lo:lo + c.chunk], correct=self.correct)
 
+    def _draw_factors(self, l, epoch, lo):
+        """Layer l's factors of the chunk into its record (and, without member
+        weights, its operand image) on the current stream."""
+        c = self.cfg
+        a, b = self.W[l].shape
+        img = self.img_x if self.split else self.img
+        mw = self.mw and l < self.L - 1
+        K.pair_factors(c.keys[l], c.rank, c.sigma, epoch, c.noise_reuse, lo, c.chunk, a, b,
+                       self.rec[l], None if mw else img[l], split=self.split and not mw)
+
+    def _issue_draws(self, epoch, lo, layers):
+        """Layers' draws of the chunk on the side stream, after the work
+        issued so far on the current stream (the previous update still reads
+        the records)."""
+        start = torch.cuda.Event()
+        start.record()
+        with torch.cuda.stream(self.side):
+            self.side.wait_event(start)
+            for l in layers:
+                self._draw_factors(l, epoch, lo)
+                done = torch.cuda.Event()
+                done.record(self.side)
+                self._drawn[l] = (epoch, lo, done)
+
     def _draw(self, l, epoch, lo):
-        """Layer l's factors of the chunk into its record and operand image
-        (factors drawn ahead), or None when the forward draws them itself."""
+        """Layer l's operand of the chunk: with member weights every member's
+        W_m formed from the record, else the operand image; None when the
+        forward draws its factors itself.  The draw itself was issued on the
+        side stream (waited for here) or runs now."""
         img = self.img_x if self.split else self.img
         if not img:
             return None
+        drawn = self._drawn.pop(l, None)
+        if drawn is not None and drawn[:2] == (epoch, lo):
+            torch.cuda.current_stream().wait_event(drawn[2])
+        else:
+            self._draw_factors(l, epoch, lo)
         c = self.cfg
         a, b = self.W[l].shape
-        K.pair_factors(c.keys[l], c.rank, c.sigma, epoch, c.noise_reuse, lo, c.chunk, a, b,
-                       self.rec[l], img[l], split=self.split)
-        return img[l]
+        out = img[l]
+        if self.mw and l < self.L - 1:
+            n_wm = K._lib.load().hses_member_weights_bytes(a, b, c.chunk, c.math) // 2
+            out = K.member_weights(self.W[l], c.rank, c.sigma, lo, c.chunk, self.rec[l],
+                                   math=c.math, out=self.wm[:n_wm])
+        if self.overlap and l == 0 and drawn is not None:
+            # the other layers' draws, beside the first layer's GEMM
+            self._issue_draws(epoch, lo, range(1, self.L))
+        return out
 
     def forward(self, epoch=0, lo=0, mark=None):
         """Raw fitness of the chunk of members [lo, lo + chunk) (a view of self.raw).
         mark(name), when given, is called after each stage is issued (e.g. to
         record an event on the current stream)."""
         mark = mark or (lambda name: None)
+        if self.overlap:
+            self._issue_draws(epoch, lo, [0])
         self.poisson(lo)
         mark("poisson")
         for l in range(self.L - 1):

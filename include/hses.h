@@ -364,7 +364,9 @@ int hses_perturbed_linear_lif_pre(const void *d_x, int32_t x_fmt, int64_t x_stri
 size_t hses_pair_image_x_bytes(int32_t a, int32_t b, int32_t rank, int32_t tid_lo, int32_t n);
 
 /* hses_pair_factors with the split operand image in place of the bf16 one:
- * the same record, and the image hses_pair_image_x derives from it. */
+ * the same record, and the image hses_pair_image_x derives from it.  (Both
+ * draws take d_img = NULL with img_bytes = 0 to write the record alone, the
+ * input of hses_member_weights.) */
 int hses_pair_factors_x(uint64_t key, int32_t rank, float sigma, int32_t epoch,
                         int32_t noise_reuse, int32_t tid_lo, int32_t n, int32_t a, int32_t b,
                         float *d_rec, size_t rec_bytes, uint16_t *d_img, size_t img_bytes,
@@ -410,6 +412,45 @@ int hses_perturbed_linear_lif_counts_pre_x(
     int32_t rows_per_member, float tau_m, float v_th, uint64_t *d_counts, int64_t counts_stride,
     void *d_work, size_t work_bytes, const float *d_rec, size_t rec_bytes, const uint16_t *d_img,
     size_t img_bytes, void *stream);
+
+/* ---- member weights ------------------------------------------------------
+ * The same perturbed product formed per member instead of factored: with R
+ * rows per member, y_m = x (W + sign_m (sigma / sqrt(r)) A_m B_m^T)^T costs
+ * a b r per pair plus R b a per member, against R b (a + r) + R r a for
+ * x W^T + sign_m (x B_m) A_m^T (snn.rs:665-685, eggroll.rs:419-446); at the
+ * SNN's R = samples x T = 1024 and a = r = 128 about half.
+ * hses_member_weights forms every member's W_m from the factor record (a
+ * record written by hses_pair_factors with d_img = NULL, by either image
+ * form, or by a *_rec forward): with math = HSES_MATH_BF16 W_m in bf16,
+ * (a, ceil(b/64)*64) per member, zero past b; with HSES_MATH_F32X the fp16
+ * high and low parts of 1024 W_m, each of that shape (the product A_m B_m^T
+ * is taken on split operands in both, so only W_m's final rounding differs).
+ * The forwards read them: bit-packed x, rows per member (n_time x
+ * rows_per_member) a multiple of 256, a <= 128, b <= 1024 (b > 64 with
+ * HSES_MATH_BF16); the LIF form
+ * takes any of spikes, rates or spike-count planes (the layout of
+ * hses_perturbed_linear_lif_counts_pre_x; rates and counts exclusive).
+ * None of these has a counterpart in the reference; they are its forward
+ * reassociated for this hardware. */
+size_t hses_member_weights_bytes(int32_t a, int32_t b, int32_t n, int32_t math);
+
+int hses_member_weights(const float *d_W, int32_t a, int32_t b, int32_t rank, float sigma,
+                        int32_t tid_lo, int32_t n, const float *d_rec, size_t rec_bytes,
+                        int32_t math, uint16_t *d_wm, size_t wm_bytes, void *stream);
+
+int hses_perturbed_linear_mw(const void *d_x, int32_t x_fmt, int64_t x_stride, int64_t x_plane,
+                             int32_t n_time, int32_t a, int32_t b, int32_t tid_lo, int32_t n,
+                             int32_t rows_per_member, int32_t math, const uint16_t *d_wm,
+                             size_t wm_bytes, float *d_y, int64_t y_stride, int64_t y_plane,
+                             void *stream);
+
+int hses_perturbed_linear_lif_mw(const void *d_x, int32_t x_fmt, int64_t x_stride,
+                                 int64_t x_plane, int32_t n_time, int32_t a, int32_t b,
+                                 int32_t tid_lo, int32_t n, int32_t rows_per_member, float tau_m,
+                                 float v_th, int32_t math, const uint16_t *d_wm, size_t wm_bytes,
+                                 uint64_t *d_spikes, int64_t spk_stride, int64_t spk_plane,
+                                 float *d_rate, int64_t rate_stride, uint64_t *d_counts,
+                                 int64_t counts_stride, void *stream);
 
 /* ---- ES update ------------------------------------------------------- */
 

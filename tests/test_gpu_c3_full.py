@@ -1,7 +1,8 @@
 """The headline configuration C3 at its full size (N = 8192 members, r = 128,
 T = 16, 64 samples per member), run through the product path (bit-packed
-Poisson, fused perturbed forward + LIF, bf16 math) and checked on sampled
-members against the oracle.
+Poisson, factors drawn ahead, member weights W_m = W + A_m B_m^T formed once
+per member and the fused forward + LIF on them, bf16 math) and checked on
+sampled members against the oracle.
 
 Members are sampled at both ends of the population, on either side of pair
 255 / 256 (where the persistent forward kernel's workgroups wrap around to
@@ -10,7 +11,8 @@ input spikes, so a single spike flip does not cascade into later layers:
 
 * input spikes: bit-exact against the oracle's Poisson encode;
 * hidden layers: spikes against the LIF scan of float64 currents computed with
-  the kernel's bf16 arithmetic (bf16 W, A, B and a bf16 rounding of x B):
+  the kernel's bf16 arithmetic (x times the bf16 rounding of W_m, formed to
+  fp32 accuracy):
   mismatches <= 1e-4 of the reference spikes; against the fp32 oracle
   (or_do_mm) the mismatch rate is reported and held under 2e-2 of the
   reference spikes (the bf16-path bar);
@@ -38,12 +40,17 @@ MEMBERS = (0, 1, 510, 511, 512, 513, 2047, 4094, 4095, 8190, 8191)
 POOL = 60000
 
 
-def member_currents(x, W, A, B, bf16):
-    """Currents (T, R, a) of one member from its input spikes x (T, R, b), float64."""
+def member_currents(x, W, A, B, bf16, mw=False):
+    """Currents (T, R, a) of one member from its input spikes x (T, R, b), float64.
+    bf16: the factored kernel's arithmetic (bf16 W, A, B and a bf16 rounding of
+    x B), or with mw the member-weight kernel's (bf16 of W + A B^T)."""
     T, R, b = x.shape
     xs = x.reshape(-1, b).astype(np.float64)
     if not bf16:
         return O.do_mm(x.reshape(-1, b), W, A, B).reshape(T, R, -1).astype(np.float64)
+    if mw:
+        wm = (W.astype(np.float64) + A.astype(np.float64) @ B.astype(np.float64).T).astype(np.float32)
+        return (xs @ bf16_round(wm).astype(np.float64).T).reshape(T, R, -1)
     xb = (xs @ bf16_round(B).astype(np.float64)).astype(np.float32)
     y = xs @ bf16_round(W).astype(np.float64).T
     y += bf16_round(xb).astype(np.float64) @ bf16_round(A).astype(np.float64).T
@@ -71,6 +78,7 @@ def c3_run(hses_gpu):
     es = snn.SnnEs(cfg, W, pool, labels, idx)
     assert es.fused, "the full-size C3 step runs the fused forward + LIF kernel"
     assert es.record and es.ahead, "the full-size C3 step draws factors ahead into the record"
+    assert es.mw, "the full-size C3 step runs on member weights"
     fit = es.forward(0)
     torch.cuda.synchronize()
     R = cfg.rows
@@ -83,7 +91,7 @@ def c3_run(hses_gpu):
     torch.cuda.synchronize()
     grads = [g.cpu().numpy() for g in es.grads]
     return dict(cfg=cfg, pool=pool, labels=labels, idx=idx, W=W, spk=spk, rate=rate,
-                fit=fit_gpu, grads=grads)
+                fit=fit_gpu, grads=grads, mw=es.mw)
 
 
 def test_c3_full_input_spikes_bit_exact(c3_run):
@@ -110,7 +118,7 @@ def test_c3_full_hidden_layers_and_readout(c3_run):
         n_ref = mism_bf = mism_32 = 0
         for j, m in enumerate(MEMBERS):
             x = c3_run["spk"][l][:, j * R:(j + 1) * R]
-            cur_bf = member_currents(x, W[l], A[j], B[j], True)
+            cur_bf = member_currents(x, W[l], A[j], B[j], True, mw=c3_run["mw"])
             cur_32 = member_currents(x, W[l], A[j], B[j], False)
             err = np.abs(cur_bf - cur_32).max()
             assert err <= 2e-2 * np.abs(cur_32).max(), f"layer {l} member {m}: currents"

@@ -133,7 +133,9 @@ def make(cfg, ahead, seed=0, pool_size=3000):
     pool, labels = snn.synthetic_pool(pool_size, cfg.dims[0], cfg.dims[-1], seed)
     idx = snn.sample_index(seed, cfg.n, cfg.rows, pool_size)
     W = snn.init_weights(cfg.dims, seed, gain=snn.ACTIVE_GAIN)
-    return snn.SnnEs(cfg, W, pool, labels, idx, fused=True, record=True, ahead=ahead)
+    # the factored forward (member weights would change the arithmetic)
+    return snn.SnnEs(cfg, W, pool, labels, idx, fused=True, record=True, ahead=ahead,
+                     member_weights=False)
 
 
 @pytest.mark.parametrize("extra,epochs", [

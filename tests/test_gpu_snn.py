@@ -26,11 +26,12 @@ def unpack(words, width):
     return bits.reshape(*w.shape[:-1], -1)[..., :width]
 
 
-def make(cfg, pool_size=3000, seed=0, fused=False):
+def make(cfg, pool_size=3000, seed=0, fused=False, member_weights=None):
     pool, labels = snn.synthetic_pool(pool_size, cfg.dims[0], cfg.dims[-1], seed)
     idx = snn.sample_index(seed, cfg.n, cfg.rows, pool_size)
     W = snn.init_weights(cfg.dims, seed, gain=snn.ACTIVE_GAIN)
-    return snn.SnnEs(cfg, W, pool, labels, idx, fused=fused), pool, labels, idx, W
+    return (snn.SnnEs(cfg, W, pool, labels, idx, fused=fused, member_weights=member_weights),
+            pool, labels, idx, W)
 
 
 def oracle_layer(x_tm, W, cfg, l):
@@ -180,7 +181,7 @@ def test_c3_fused_forward_equals_unfused(hses_gpu):
     # update in-kernel, so spikes, rates and fitness are identical bit for bit.
     cfg = snn.SnnConfig(**C3_SMALL)
     es_u, *_ = make(cfg, fused=False)
-    es_f, *_ = make(cfg, fused=True)
+    es_f, *_ = make(cfg, fused=True, member_weights=False)
     assert es_f.fused and not es_u.fused
     fit_u = es_u.forward(0)
     fit_f = es_f.forward(0)
