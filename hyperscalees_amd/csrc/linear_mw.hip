@@ -20,9 +20,10 @@
 //                        odd member) and stored as bf16 or, for the
 //                        fp32-accurate mode, as the fp16 high and low parts of
 //                        1024 W_m (the split form k_pair_bits<.., X> reads).
-//   k_pair_bits<.., MW>  the hidden-layer kernel on those weights
-//                        (pair_bits.h): each block's member's W tiles stream
-//                        into LDS; no B columns, no A block, no rank product.
+//   k_mw_bits            the hidden-layer GEMM on those weights: each 256-row
+//                        block's member's W tiles stream into LDS; waves of
+//                        64 rows (every W fragment feeds two MFMAs); no B
+//                        columns, no A block, no rank product; LIF fused.
 #include "pair_bits.h"
 
 namespace hses {
@@ -229,6 +230,414 @@ __global__ __launch_bounds__(MW_THREADS, 2) void k_member_weights(
     }
 }
 
+// ---- k_mw_bits: the forward on member weights -------------------------------
+//
+// y = x W_m^T for bit-packed x, the W_m of each 256-row block's member
+// streamed from HBM (hses_member_weights' layout).  Four waves of 64 rows x
+// all output columns: each W fragment read from LDS feeds the MFMAs of both
+// of a wave's 32-row tiles, so a 32x32x16 MFMA needs half a fragment read
+// (the factored kernel's waves of 32 rows need a whole one, which with one
+// W fragment per MFMA saturates LDS bandwidth).  A wave's bit rows are staged
+// by its own threads (thread t holds block row t), so they need no workgroup
+// barrier.  W tiles (128 columns x 64 k, XOR-swizzled chunks as in
+// k_pair_bits) stream by LDS DMA into NB buffers, each transfer issued right
+// after the barrier that frees its buffer, NB - 1 tiles ahead (NB = 3 when a
+// block has at least three stream tiles, so a transfer has two tiles of
+// MFMAs to land; else 2); with X each K tile streams twice (high, then low
+// part) on the same bit rows.  The epilogue runs the LIF (or
+// stores y) in registers as k_pair_bits does, per row tile.  Two workgroups
+// share a CU (58.6 KB of LDS each at b = 784).
+constexpr int MB_THREADS = 256, MB_RB = 256;
+constexpr int MB_XPF = 16;                  // x words per row (b <= 1024)
+constexpr int MB_TILE = K2_NMAX * K2_BK;    // elements of one W tile buffer
+
+struct MbLayout {
+    size_t off_w, bytes;
+    int32_t words;
+    __host__ __device__ MbLayout(int b, int nb) {
+        words = (b + 63) / 64;
+        off_w = align16((size_t)MB_RB * words * 8);
+        bytes = off_w + (size_t)nb * MB_TILE * 2;
+    }
+};
+
+template <int EPI, int LT, bool SPK, bool RATE, bool X, int WT, int NB>
+__global__ __launch_bounds__(MB_THREADS, 2) void k_mw_bits(const K2Args P) {
+    static_assert(LT >= 1 && LT <= 16 && (LT & (LT - 1)) == 0, "T must be a power of two <= 16");
+    static_assert(NB == 2 || NB == 3, "two or three tile buffers");
+    extern __shared__ __align__(16) unsigned char smem[];
+    const MbLayout lay(P.b, NB);
+    uint64_t* Xbits = reinterpret_cast<uint64_t*>(smem);
+    const uint32_t* Xbits32 = reinterpret_cast<const uint32_t*>(smem);
+    uint16_t* WB = reinterpret_cast<uint16_t*>(smem + lay.off_w);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lc = lane & 31, hl = lane >> 5;
+    const int32_t a = P.a, nkt = lay.words, kp = nkt * 64, R = P.R;
+    const int32_t ntb = X ? 2 * nkt : nkt;  // stream tiles per block
+    const int32_t wrow0 = 64 * wave;
+    // MFMA position p of a row tile -> its row: 8g + 4h + v -> 16h + 4g + v
+    const int xrow = 16 * ((lc >> 2) & 1) + 4 * (lc >> 3) + (lc & 3);
+    const int64_t part_off = X ? (int64_t)a * kp : 0;  // X: the low part after the high part
+
+    // DMA: wave w's instruction q fills 1 KB chunk block 4w + q (staged columns
+    // 32w + 8q .. + 7): lane l fetches chunk (l & 7) ^ ((column / 2) & 7) of
+    // column 32w + 8q + l / 8; columns past a repeat row a - 1 (never stored)
+    int32_t dl_off[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int32_t col = 32 * wave + 8 * q + (lane >> 3);
+        const int32_t ch = (lane & 7) ^ (((8 * q + (lane >> 3)) >> 1) & 7);
+        dl_off[q] = min(col, a - 1) * kp + ch * 8;
+    }
+    auto dl_issue = [&](const uint16_t* src, int32_t t, int32_t buf) {
+        if (wave >= WT) return;  // W rows no output tile reads
+        const uint16_t* s = src + (X ? (t & 1) * part_off : 0) + (X ? t >> 1 : t) * K2_BK;
+        const uint32_t dst = __builtin_amdgcn_readfirstlane(lds_addr(WB + buf * MB_TILE + (4 * wave) * 512));
+#pragma unroll
+        for (int q = 0; q < 4; ++q) lds_dma16(s + dl_off[q], dst + q * 1024);
+    };
+    // fragment of staged columns 32 ct + lc at k-step ks in buffer bsel
+    const int32_t dl_u = hl ^ ((lc >> 1) & 7);
+    auto frag_ptr = [&](int32_t bsel, int ks) -> const uint16_t* {
+        return WB + bsel * MB_TILE + lc * K2_BK + (((2 * ks) ^ dl_u) << 3);
+    };
+
+    // work units: pair index and part (of P.split), as in k_pair_bits
+    const int32_t G = (int32_t)gridDim.x, S = P.split;
+    auto unit_of = [&](int32_t it, int32_t* pi_, int32_t* part) {
+        if (S == 1) {
+            *pi_ = (int32_t)blockIdx.x + it * G;
+            *part = 0;
+        } else {
+            const int32_t xcd = (int32_t)blockIdx.x & 7, sl = (int32_t)blockIdx.x >> 3;
+            *pi_ = it * (G / S) + xcd * (G / (8 * S)) + sl / S;
+            *part = sl % S;
+        }
+    };
+    auto unit_rows = [&](int32_t pi_, int32_t part, int64_t* lo, int64_t* hi) {
+        const int32_t m_even = 2 * (P.pair_lo + pi_) - P.tid_lo;
+        *lo = (int64_t)max(m_even, 0) * R;
+        *hi = (int64_t)(min(m_even + 1, P.n - 1) + 1) * R;
+        if (S > 1) {
+            const int64_t span = (*hi - *lo) / S;  // a multiple of MB_RB (host check)
+            *lo += part * span;
+            *hi = *lo + span;
+        }
+    };
+    auto unit_cursor = [&](int32_t pi_, int32_t part) {
+        RowCursor c;
+        c.m0 = max(2 * (P.pair_lo + pi_) - P.tid_lo, 0);
+        c.q0 = 0;
+        if (S > 1) {
+            const int32_t off = part * (int32_t)((2 * (int64_t)R) / S);
+            c.m0 += off / R;
+            c.q0 = off - (off / R) * R;
+        }
+        return c;
+    };
+    auto advance = [&](RowCursor c) {
+        c.q0 += MB_RB;
+        if (c.q0 >= R) {
+            const int32_t d = c.q0 / R;
+            c.m0 += d;
+            c.q0 -= d * R;
+        }
+        return c;
+    };
+
+    // bit rows: thread t holds row t of a block (its wave's rows only)
+    uint64_t xv[MB_XPF];
+    bool xv_ok = false;
+    auto xload = [&](const RowCursor& cr, int64_t L, int64_t rhi) {
+        const int32_t nv = (int32_t)min<int64_t>(rhi - L, MB_RB);
+        xv_ok = tid < nv;
+        int32_t m, q;
+        cr.at(min(tid, nv - 1), R, &m, &q);
+        const uint64_t* src = static_cast<const uint64_t*>(P.x) +
+                              k2_phys(m, q, P.rpm, P.T, P.x_stride, P.x_plane);
+#pragma unroll
+        for (int w = 0; w < MB_XPF; ++w) xv[w] = src[min(w, nkt - 1)];
+    };
+    auto xstore = [&]() {
+#pragma unroll
+        for (int w = 0; w < MB_XPF; ++w) {
+            if (w < nkt) Xbits[tid * nkt + w] = xv_ok ? xv[w] : 0ull;
+            asm volatile("" ::"v"(xv[w]));  // every load consumed on every path
+        }
+    };
+
+    int32_t dl_cb = 0;
+    bool dl_primed = false, xready = false;
+    // whether the last dl_issue_ahead issued (the tile that may stay in
+    // flight at the next wait, NB = 3)
+    bool iss_last = false;
+    auto next_buf = [](int32_t c) { return c + 1 == NB ? 0 : c + 1; };
+    // wait until the tile a barrier publishes has landed (NB = 3: the one
+    // issued after it may stay in flight)
+    auto dl_wait = [&]() {
+        if (NB == 3 && iss_last)
+            wait_vmcnt<4>();
+        else
+            wait_vmcnt<0>();
+    };
+    for (int32_t it = 0;; ++it) {
+        int32_t pi, part;
+        unit_of(it, &pi, &part);
+        if (pi >= P.n_pairs) break;
+        int64_t row_lo, row_hi;
+        unit_rows(pi, part, &row_lo, &row_hi);
+        int32_t pi_n, part_n;
+        unit_of(it + 1, &pi_n, &part_n);
+        const bool more_pairs = pi_n < P.n_pairs;
+        RowCursor cur_rows = unit_cursor(pi, part);
+        for (int64_t L0 = row_lo; L0 < row_hi; L0 += MB_RB) {
+            const bool first = L0 == row_lo;
+            const bool has_next = L0 + MB_RB < row_hi;
+            const bool next_pair = !has_next && more_pairs;
+            if (!first) cur_rows = advance(cur_rows);
+            const int32_t nvalid = (int32_t)min<int64_t>(row_hi - L0, MB_RB);
+            // this block's member's weights, and the next block's
+            int32_t mn = cur_rows.m0;
+            if (has_next)
+                mn = cur_rows.q0 + MB_RB >= R ? cur_rows.m0 + 1 : cur_rows.m0;
+            else if (more_pairs)
+                mn = unit_cursor(pi_n, part_n).m0;
+            const uint16_t* blk_src = P.wm + (size_t)cur_rows.m0 * P.wm_stride;
+            const uint16_t* nblk_src = P.wm + (size_t)mn * P.wm_stride;
+            if (first && !xready) {
+                xload(cur_rows, L0, row_hi);
+                xstore();
+            }
+            if (!dl_primed) {
+                // the stream's first NB tiles (a block has at least NB)
+                dl_issue(blk_src, 0, dl_cb);
+                dl_issue(blk_src, 1, next_buf(dl_cb));
+                if constexpr (NB == 3) {
+                    dl_issue(blk_src, 2, next_buf(next_buf(dl_cb)));
+                    wait_vmcnt<8>();
+                } else {
+                    wait_vmcnt<4>();
+                }
+                iss_last = true;
+                dl_primed = true;
+            }
+            lds_barrier();
+
+            // stream tile t (t >= ntb: the next block's tile t - ntb) into buf
+            auto dl_issue_ahead = [&](int32_t t, int32_t buf) {
+                iss_last = t < ntb || has_next || next_pair;
+                if (t < ntb)
+                    dl_issue(blk_src, t, buf);
+                else if (iss_last)
+                    dl_issue(nblk_src, t - ntb, buf);
+            };
+
+            f32x16 acc[2][WT];
+            u16x8 fr[WT];
+            {
+                const uint16_t* tb = frag_ptr(dl_cb, 0);
+#pragma unroll
+                for (int ct = 0; ct < WT; ++ct) fr[ct] = lds_u16x8(tb + 32 * ct * K2_BK);
+            }
+            const uint32_t* xw[2] = {Xbits32 + (wrow0 + xrow) * (2 * nkt),
+                                     Xbits32 + (wrow0 + 32 + xrow) * (2 * nkt)};
+            uint32_t xw0[2] = {xw[0][0], xw[1][0]}, xw1[2] = {xw[0][1], xw[1][1]};
+            // x operand of row tile rt at k-step ks from its tile word w
+            auto expand = [&](uint32_t w, int ks) {
+                const uint32_t xbyte = (w >> (8 * ((ks & 1) * 2 + hl))) & 0xffu;
+                return X ? expand_bits_f16(xbyte) : expand_bits(xbyte);
+            };
+            // the x operands of the step about to run; each step expands the
+            // next one's between its MFMAs (they do not depend on the MFMAs in
+            // flight, so they issue while the matrix core is busy)
+            u16x8 xa[2] = {expand(xw0[0], 0), expand(xw0[1], 0)};
+            // one k-step: per column tile its two MFMAs and the read of its
+            // fragment for the step at `nxt`; wn / ksn: the next step's words
+            // and k-step
+            auto step = [&](auto zc, const uint16_t* nxt, const uint32_t (&wn)[2], int ksn) {
+                constexpr bool z = decltype(zc)::value;
+                u16x8 xn[2];
+#pragma unroll
+                for (int ct = 0; ct < WT; ++ct) {
+#pragma unroll
+                    for (int rt = 0; rt < 2; ++rt) {
+                        if constexpr (X)
+                            acc[rt][ct] = mfma32_f16(xa[rt], fr[ct], z ? f32x16{} : acc[rt][ct]);
+                        else
+                            acc[rt][ct] = mfma32_bf16(xa[rt], fr[ct], z ? f32x16{} : acc[rt][ct]);
+                    }
+                    fr[ct] = lds_u16x8(nxt + 32 * ct * K2_BK);
+                    if (ct == 0) xn[0] = expand(wn[0], ksn);
+                    if (ct == (WT > 1 ? 1 : 0)) xn[1] = expand(wn[1], ksn);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                xa[0] = xn[0];
+                xa[1] = xn[1];
+            };
+            auto tile = [&](int32_t kt, auto zc) {
+                const bool more = kt + 1 < ntb;
+                const int32_t kn = more ? kt + 1 : kt;
+                const int32_t kw = X ? kn >> 1 : kn;  // x word of tile kn
+                const int32_t cb = dl_cb, nb = next_buf(dl_cb);
+                const uint32_t wa[2] = {xw0[0], xw0[1]}, wb[2] = {xw1[0], xw1[1]};
+                step(zc, frag_ptr(cb, 1), wa, 1);
+                step(std::false_type{}, frag_ptr(cb, 2), wb, 2);
+                step(std::false_type{}, frag_ptr(cb, 3), wb, 3);
+                if (more) {
+                    dl_wait();  // tile kt + 1 has landed
+                    lds_barrier();
+                    dl_issue_ahead(kt + NB, cb);
+                }
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt) {
+                    xw0[rt] = xw[rt][2 * kw];
+                    xw1[rt] = xw[rt][2 * kw + 1];
+                }
+                const uint32_t wn[2] = {xw0[0], xw0[1]};
+                step(std::false_type{}, frag_ptr(more ? nb : cb, 0), wn, 0);
+                dl_cb = nb;
+            };
+            tile(0, std::true_type{});
+            for (int32_t kt = 1; kt < ntb; ++kt) tile(kt, std::false_type{});
+            // the next block's first tile has landed; its tile NB - 1 into the
+            // last tile's buffer
+            dl_wait();
+            lds_barrier();
+            dl_issue_ahead(ntb + NB - 1, NB == 3 ? next_buf(next_buf(dl_cb)) : next_buf(dl_cb));
+
+            // the next block's bit rows land during the epilogue
+            {
+                int64_t nlo = L0, nhi = row_hi;
+                RowCursor ncr = cur_rows;
+                if (has_next) {
+                    nlo = L0 + MB_RB;
+                    ncr = advance(cur_rows);
+                } else if (next_pair) {
+                    unit_rows(pi_n, part_n, &nlo, &nhi);
+                    ncr = unit_cursor(pi_n, part_n);
+                }
+                xload(ncr, nlo, nhi);
+            }
+
+            // acc[rt][jo][4g + v]: wave row 32 rt + 16 hl + 4g + v, column 32 jo + lc
+            if constexpr (EPI == EPI_Y) {
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g)
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) {
+                            const int32_t row = wrow0 + 32 * rt + 16 * hl + 4 * g + v;
+                            if (row >= nvalid) continue;
+                            int32_t m, q;
+                            cur_rows.at(row, R, &m, &q);
+                            float* yrow = P.y + k2_phys(m, q, P.rpm, P.T, P.y_stride, P.y_plane);
+#pragma unroll
+                            for (int jo = 0; jo < WT; ++jo)
+                                if (32 * jo + lc < a)
+                                    yrow[32 * jo + lc] = X ? acc[rt][jo][4 * g + v] * (1.0f / K3_XSCALE)
+                                                           : acc[rt][jo][4 * g + v];
+                        }
+            } else {
+                // LIF (snn.rs:53-97) along each lane's rows, v = 0 at t = 0; the
+                // reset as in k_pair_bits (charged kept when no spike, else 0)
+                uint32_t wlo[2] = {0, 0}, whi[2] = {0, 0};  // lane u: spike words of wave row u
+                bool colok[WT];
+#pragma unroll
+                for (int jo = 0; jo < WT; ++jo) colok[jo] = 32 * jo + lc < a;
+                static_for<0, 2>([&](auto rc) {
+                    constexpr int rt = decltype(rc)::value;
+                    float vm[WT];
+                    int32_t cnt[WT];
+                    static_for<0, 16>([&](auto qc) {
+                        constexpr int qq = decltype(qc)::value;  // 4g + v: time step qq % T
+                        if constexpr (qq % LT == 0) {
+#pragma unroll
+                            for (int jo = 0; jo < WT; ++jo) {
+                                vm[jo] = 0.0f;
+                                cnt[jo] = 0;
+                            }
+                        }
+                        uint64_t bal[WT];
+#pragma unroll
+                        for (int jo = 0; jo < WT; ++jo) {
+                            const float c = X ? acc[rt][jo][qq] * (1.0f / K3_XSCALE) : acc[rt][jo][qq];
+                            const float charged = __fadd_rn(vm[jo], __fmul_rn(__fadd_rn(-vm[jo], c), P.leak));
+                            const bool spike = charged >= P.v_th;
+                            vm[jo] = spike ? 0.0f : charged;
+                            if constexpr (RATE) cnt[jo] += spike ? 1 : 0;
+                            if constexpr (SPK) bal[jo] = __builtin_amdgcn_ballot_w64(spike && colok[jo]);
+                        }
+                        if constexpr (RATE && qq % LT == LT - 1) {
+                            const int32_t row = wrow0 + 32 * rt + 16 * hl + qq;
+                            if (P.cpl) {
+                                // the counts' bit planes (k_pair_bits' layout)
+                                constexpr int NPL = LT == 1 ? 1 : LT == 2 ? 2 : LT == 4 ? 3 : LT == 8 ? 4 : 5;
+                                uint64_t pb[NPL][WT];
+#pragma unroll
+                                for (int p = 0; p < NPL; ++p)
+#pragma unroll
+                                    for (int jo = 0; jo < WT; ++jo)
+                                        pb[p][jo] = __builtin_amdgcn_ballot_w64(((cnt[jo] >> p) & 1) && colok[jo]);
+                                if (lc == 0 && row < nvalid) {
+                                    int32_t m, q;
+                                    cur_rows.at(row, R, &m, &q);
+                                    uint64_t* dst = P.cpl + ((int64_t)m * P.rpm + q / LT) * P.cpl_stride;
+                                    const int32_t words = (a + 63) >> 6;
+#pragma unroll
+                                    for (int p = 0; p < NPL; ++p)
+#pragma unroll
+                                        for (int hh = 0; hh < 2; ++hh) {
+                                            const uint64_t b0 = 2 * hh < WT ? pb[p][min(2 * hh, WT - 1)] : 0ull;
+                                            const uint64_t b1 = 2 * hh + 1 < WT ? pb[p][min(2 * hh + 1, WT - 1)] : 0ull;
+                                            const uint64_t w = hl ? (b0 >> 32) | (b1 & 0xffffffff00000000ull)
+                                                                  : (b0 & 0xffffffffull) | (b1 << 32);
+                                            if (hh < words) dst[p * words + hh] = w;
+                                        }
+                                }
+                            } else if (row < nvalid) {
+                                int32_t m, q;
+                                cur_rows.at(row, R, &m, &q);
+                                float* rp = P.rate + ((int64_t)m * P.rpm + q / LT) * P.rate_stride;
+#pragma unroll
+                                for (int jo = 0; jo < WT; ++jo)
+                                    if (colok[jo]) rp[32 * jo + lc] = (float)cnt[jo] * (1.0f / LT);
+                            }
+                        }
+                        if constexpr (SPK) {
+                            // ballot bit l: column 32 jo + l % 32 of wave row
+                            // 32 rt + 16 (l / 32) + qq; lane 32 rt + 16 h + qq holds it
+#pragma unroll
+                            for (int hh = 0; hh < 2; ++hh) {
+                                const uint64_t b0 = 2 * hh < WT ? bal[min(2 * hh, WT - 1)] : 0ull;
+                                const uint64_t b1 = 2 * hh + 1 < WT ? bal[min(2 * hh + 1, WT - 1)] : 0ull;
+                                put_lane<32 * rt + qq>(wlo[hh], whi[hh], (b0 & 0xffffffffull) | (b1 << 32));
+                                put_lane<32 * rt + 16 + qq>(wlo[hh], whi[hh],
+                                                            (b0 >> 32) | (b1 & 0xffffffff00000000ull));
+                            }
+                        }
+                    });
+                });
+                if constexpr (SPK) {
+                    const int32_t row = wrow0 + lane;
+                    if (row < nvalid) {
+                        int32_t m, q;
+                        cur_rows.at(row, R, &m, &q);
+                        uint64_t* dst = P.spk + k2_phys(m, q, P.rpm, LT, P.spk_stride, P.spk_plane);
+                        dst[0] = ((uint64_t)whi[0] << 32) | wlo[0];
+                        if (a > 64) dst[1] = ((uint64_t)whi[1] << 32) | wlo[1];
+                    }
+                }
+            }
+            // the next block's bit rows (this wave's own rows: a wave-level
+            // order suffices; the next block's start barrier covers it too)
+            xstore();
+            xready = next_pair;
+        }
+    }
+}
+
 size_t member_weights_bytes(int32_t a, int32_t b, int32_t n, bool split) {
     if (a < 1 || b < 1 || n < 1) return 0;
     return (size_t)n * member_stride(a, b, split) * 2;
@@ -255,29 +664,33 @@ int launch_member_weights(const float* W, const float* rec, int32_t a, int32_t b
     return HSES_OK;
 }
 
-// The forward on member weights: k_pair_bits<.., MW> over members
+// The forward on member weights: k_mw_bits over members
 // [tid_lo, tid_lo + n), bit-packed x, rows per member a multiple of K3_RB.
 int launch_linear_mw(LinParams& P, DeviceState* st, hipStream_t s, const LifOut* lif) {
     const bool xm = P.math == HSES_MATH_F32X;
-    if (P.x_fmt != HSES_FMT_BITS || P.a > K2_NMAX || P.R % K3_RB || P.b > 2 * K3_XPF * 64 ||
-        P.tmm)
+    if (P.x_fmt != HSES_FMT_BITS || P.a > K2_NMAX || P.R % MB_RB || P.b > 64 * MB_XPF || P.tmm)
         return HSES_ERR_UNSUPPORTED;
     // the two-buffer stream needs two stream tiles per block: K of more than
     // one tile, or the split form (each K tile streamed twice)
     if (!xm && P.b <= 64) return HSES_ERR_UNSUPPORTED;
     if (lif && (P.n_time > 16 || (P.n_time & (P.n_time - 1)) != 0)) return HSES_ERR_UNSUPPORTED;
-    const K3Layout lay(P.r, P.b, true, xm, true);
+    // three tile buffers when a block streams at least three tiles
+    const int32_t ntb = (xm ? 2 : 1) * ((P.b + 63) / 64);
+    const int nbuf = ntb >= 3 ? 3 : 2;
+    const MbLayout lay(P.b, nbuf);
     if (lay.bytes > st->max_lds) return HSES_ERR_UNSUPPORTED;
     K2Args A{};
     pair_range(P.tid_lo, P.n, &A.pair_lo, &A.n_pairs);
-    int32_t grid = pair_grid(st, A.n_pairs);
+    // two workgroups per CU, persistent over the pairs
+    const int32_t slots = 2 * st->num_cus;
+    int32_t grid = std::max(1, std::min(A.n_pairs, slots));
     // pairs split over 4 workgroups of one XCD, as in launch_linear_pair: the
     // member's weights are fetched about once and re-read from that XCD's L2
     A.split = 1;
-    if (P.tid_lo % 2 == 0 && P.n % 2 == 0 && (2 * (int64_t)P.R) % (4 * K3_RB) == 0 &&
-        st->num_cus % 32 == 0 && (int64_t)A.n_pairs * 4 >= st->num_cus) {
+    if (P.tid_lo % 2 == 0 && P.n % 2 == 0 && (2 * (int64_t)P.R) % (4 * MB_RB) == 0 &&
+        slots % 32 == 0 && (int64_t)A.n_pairs * 4 >= slots) {
         A.split = 4;
-        grid = st->num_cus;
+        grid = slots;
     }
     A.group = 1;
     A.x = P.x;
@@ -318,32 +731,36 @@ int launch_linear_mw(LinParams& P, DeviceState* st, hipStream_t s, const LifOut*
             HSES_CHECK_HIP(hipFuncSetAttribute((const void*)kern,
                                                hipFuncAttributeMaxDynamicSharedMemorySize,
                                                (int)lay.bytes));
-        hipLaunchKernelGGL(kern, dim3(grid), dim3(K3_THREADS), lay.bytes, s, A);
+        hipLaunchKernelGGL(kern, dim3(grid), dim3(MB_THREADS), lay.bytes, s, A);
         HSES_CHECK_HIP(hipGetLastError());
         return HSES_OK;
     };
-    auto by_math = [&](auto xc) -> int {
+    auto by_math = [&](auto xc, auto nc) -> int {
         constexpr bool XX = decltype(xc)::value;
+        constexpr int NB = decltype(nc)::value;
         if (!lif) {
-            if (P.a <= 32) return launch(k_pair_bits<EPI_Y, 1, false, false, true, true, XX, 1, true>);
-            return launch(k_pair_bits<EPI_Y, 1, false, false, true, true, XX, 4, true>);
+            if (P.a <= 32) return launch(k_mw_bits<EPI_Y, 1, false, false, XX, 1, NB>);
+            return launch(k_mw_bits<EPI_Y, 1, false, false, XX, 4, NB>);
         }
         const bool spk = lif->spk != nullptr, rate = lif->rate != nullptr || lif->cpl != nullptr;
         auto by_t = [&](auto sc, auto rc) -> int {
             constexpr bool S = decltype(sc)::value, Q = decltype(rc)::value;
             switch (P.n_time) {
-                case 1: return launch(k_pair_bits<EPI_LIF, 1, S, Q, true, true, XX, 4, true>);
-                case 2: return launch(k_pair_bits<EPI_LIF, 2, S, Q, true, true, XX, 4, true>);
-                case 4: return launch(k_pair_bits<EPI_LIF, 4, S, Q, true, true, XX, 4, true>);
-                case 8: return launch(k_pair_bits<EPI_LIF, 8, S, Q, true, true, XX, 4, true>);
-                default: return launch(k_pair_bits<EPI_LIF, 16, S, Q, true, true, XX, 4, true>);
+                case 1: return launch(k_mw_bits<EPI_LIF, 1, S, Q, XX, 4, NB>);
+                case 2: return launch(k_mw_bits<EPI_LIF, 2, S, Q, XX, 4, NB>);
+                case 4: return launch(k_mw_bits<EPI_LIF, 4, S, Q, XX, 4, NB>);
+                case 8: return launch(k_mw_bits<EPI_LIF, 8, S, Q, XX, 4, NB>);
+                default: return launch(k_mw_bits<EPI_LIF, 16, S, Q, XX, 4, NB>);
             }
         };
         if (spk && rate) return by_t(std::true_type{}, std::true_type{});
         if (spk) return by_t(std::true_type{}, std::false_type{});
         return by_t(std::false_type{}, std::true_type{});
     };
-    return xm ? by_math(std::true_type{}) : by_math(std::false_type{});
+    using nb2 = std::integral_constant<int, 2>;
+    using nb3 = std::integral_constant<int, 3>;
+    if (xm) return nbuf == 3 ? by_math(std::true_type{}, nb3{}) : by_math(std::true_type{}, nb2{});
+    return nbuf == 3 ? by_math(std::false_type{}, nb3{}) : by_math(std::false_type{}, nb2{});
 }
 
 }  // namespace hses
