@@ -2,7 +2,7 @@
 //
 // Included by linear_pair.hip (the factor draws, k_linear_pair, the pair
 // forwards and their k_pair_bits instances) and linear_mw.hip (member
-// weights and the member-weight instances of k_pair_bits), which compile
+// weights and k_mw_bits, which reuses these definitions), which compile
 // separately.  See linear_pair.hip for the design of the pair kernels.
 #pragma once
 
@@ -125,7 +125,7 @@ struct K2Args {
     // Factors drawn ahead (PRE kernels, k_pair_gen): pair pair_lo + i's
     // operand image (PairImage) at bimg + i * stride.
     uint16_t* bimg;
-    // Member weights (MW kernels): member tid_lo + m's perturbed W (the
+    // Member weights (k_mw_bits): member tid_lo + m's perturbed W (the
     // member_weights layout, (a, kp) per part) at wm + m * wm_stride.
     const uint16_t* wm;
     int64_t wm_stride;
@@ -302,19 +302,18 @@ struct K3Layout {
     size_t off_a, off_xbits, off_wb, bytes;
     int32_t apitch, words, kp;
     // dl: the DL form (factors drawn ahead, so no noise tables); x: the
-    // split (fp32-accurate) form, A as high and low parts and two DL buffers;
-    // mw: member weights (no A block, two DL buffers)
-    __host__ __device__ K3Layout(int r, int b, bool dl = false, bool x = false, bool mw = false) {
+    // split (fp32-accurate) form, A as high and low parts and two DL buffers
+    __host__ __device__ K3Layout(int r, int b, bool dl = false, bool x = false) {
         apitch = K3_AP;
         words = (b + 63) / 64;
         kp = words * 64;
         size_t o = dl ? 0 : align16(sizeof(BmTables));
         off_a = o;
-        if (!mw) o = align16(o + (size_t)(x ? 2 : 1) * K2_NMAX * apitch * 2);
+        o = align16(o + (size_t)(x ? 2 : 1) * K2_NMAX * apitch * 2);
         off_xbits = o;
         o = align16(o + (size_t)K3_RB * words * 8);
         off_wb = o;
-        bytes = o + (dl ? (size_t)(x || mw ? 2 : K3_DLBUF) * K3_DLTILE * 2
+        bytes = o + (dl ? (size_t)(x ? 2 : K3_DLBUF) * K3_DLTILE * 2
                         : (size_t)2 * K2_COLS * K2_TP * 2);
     }
 };
@@ -356,26 +355,19 @@ __device__ __forceinline__ void wait_vmcnt() {
 // the second product is (xB)_hi A_hi + (xB)_lo A_hi + (xB)_hi A_lo.
 // WT: output tiles of 32 columns computed (4; 1 for a <= 32, where the other
 // three would only be discarded).
-// MW (with DL): member weights.  Each member's perturbed weights W_m = W +
-// sign_m (sigma / sqrt(r)) A_m B_m^T were formed ahead (member_weights.hip;
-// with X as high and low parts), so the K loop is y = x W_m^T alone: the W
-// tiles of the block's member stream in, and there is no x B_m, no A block
-// and no rank product in the epilogue.  A row block never spans two members
-// (rows per member a multiple of K3_RB).
 template <int EPI, int LT, bool SPK, bool RATE, bool PRE = false, bool DL = false, bool X = false,
-          int WT = 4, bool MW = false>
+          int WT = 4>
 __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
     static_assert(LT >= 1 && LT <= 16 && (LT & (LT - 1)) == 0, "T must be a power of two <= 16");
     static_assert(!DL || PRE, "the DL tile stream needs factors drawn ahead");
     static_assert(!X || DL, "the split operands stream through DL buffers");
-    static_assert(!MW || DL, "member weights stream through DL buffers");
     // two DL buffers, each transfer issued right after the barrier that frees
-    // its buffer (X, MW); or three, two tiles ahead
-    constexpr bool EARLY = X || MW;
+    // its buffer (X); or three, two tiles ahead
+    constexpr bool EARLY = X;
     constexpr int NBUF = EARLY ? 2 : K3_DLBUF;  // DL tile buffers
     constexpr int DIST = NBUF - 1;              // tiles the stream runs ahead
     extern __shared__ __align__(16) unsigned char smem[];
-    const K3Layout lay(P.r, P.b, DL, X, MW);
+    const K3Layout lay(P.r, P.b, DL, X);
     BmTables* tabs = reinterpret_cast<BmTables*>(smem);
     uint16_t* As = reinterpret_cast<uint16_t*>(smem + lay.off_a);
     uint64_t* Xbits = reinterpret_cast<uint64_t*>(smem + lay.off_xbits);
@@ -423,7 +415,6 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
     }
     auto dl_issue = [&](const uint16_t* src, int32_t kt, int32_t buf) {
         if (wave >= WT && wave < 4) return;  // W rows no output tile reads
-        if (MW && wave >= 4) return;         // no B columns
         const uint32_t dst = __builtin_amdgcn_readfirstlane(
             lds_addr(WB + buf * K3_DLTILE + (4 * wave) * 512));
 #pragma unroll
@@ -520,16 +511,12 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
         unit_of(it + 1, &pi_n, &part_n);
         const bool more_pairs = pi_n < P.n_pairs;
         // DL: this wave's tile source for pair pi and for the next unit's pair
-        // (MW: waves 0-3 set theirs per block; waves 4-7 stage nothing)
-        const uint16_t* dl_src =
-            wave < 4 || MW ? dl_wsrc : P.bimg + (size_t)pi * dl_stride;
+        const uint16_t* dl_src = wave < 4 ? dl_wsrc : P.bimg + (size_t)pi * dl_stride;
         const uint16_t* dl_src_next =
-            wave < 4 || MW ? dl_wsrc : P.bimg + (size_t)(more_pairs ? pi_n : pi) * dl_stride;
+            wave < 4 ? dl_wsrc : P.bimg + (size_t)(more_pairs ? pi_n : pi) * dl_stride;
 
         // ---- 1. factors: A rows -> LDS (bf16, [o][c]); B rows -> slot ([c][k]) ----
-        if constexpr (MW) {
-            // no factors: the member weights hold them
-        } else if constexpr (PRE) {
+        if constexpr (PRE) {
             // the pair's image holds A in this block's layout: one round of
             // 16-byte copies (a rows of K3_AP bf16, at most 5 per thread)
             const PairImage im(a, b, r);
@@ -691,21 +678,9 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
             if (!first) cur_rows = advance(cur_rows);
             const int32_t nvalid = (int32_t)min<int64_t>(row_hi - L0, K3_RB);
             // DL: this wave's tile source for this block and for the next
-            // block (the next unit's first block after the unit's last); MW:
-            // the blocks' members' weights
+            // block (the next unit's first block after the unit's last)
             const uint16_t* blk_src = dl_src;
             const uint16_t* nblk_src = has_next ? dl_src : dl_src_next;
-            if constexpr (MW) {
-                if (wave < 4) {
-                    int32_t mn;
-                    if (has_next)
-                        mn = cur_rows.q0 + K3_RB >= R ? cur_rows.m0 + 1 : cur_rows.m0;
-                    else
-                        mn = more_pairs ? unit_cursor(pi_n, part_n).m0 : cur_rows.m0;
-                    blk_src = P.wm + (size_t)cur_rows.m0 * P.wm_stride;
-                    nblk_src = P.wm + (size_t)mn * P.wm_stride;
-                }
-            }
             if (first && !xready) {
                 if (P.x_packed) {
                     xbits_load_packed(L0, row_hi, xpf);
@@ -774,7 +749,7 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
                 const uint16_t* tb = frag_ptr(DL ? dl_cb : 0, 0);
 #pragma unroll
                 for (int j = 0; j < 8; ++j)
-                    if ((j >= WT && j < 4) || (MW && j >= 4))
+                    if (j >= WT && j < 4)
                         fr[j] = u16x8{};
                     else
                         fr[j] = lds_u16x8(tb + frag_off(j));
@@ -794,7 +769,6 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     if (j >= WT && j < 4) continue;
-                    if (MW && j >= 4) continue;
                     if (j < 4)
                         accW[j] = mma(xa, fr[j], z ? f32x16{} : accW[j]);
                     else
@@ -879,7 +853,7 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
             if (!resident || nkt == 1) {
                 if constexpr (DL) dl_wait();
                 lds_barrier();
-                // X, MW: the next block's second tile, into the last tile's buffer
+                // X: the next block's second tile, into the last tile's buffer
                 if constexpr (EARLY) dl_issue_ahead(ntb + 1, dl_cb == 0 ? 1 : 0);
             } else {
                 wave_lds_sync();
@@ -888,9 +862,7 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
             const bool next_pair = !has_next && more_pairs;
             // sign * xB as bf16: lane l holds rank columns 32j + 8g + 4hl + v of
             // the row at MFMA position lc (the row its x operand came from).
-            // X: the same as fp16 high and low parts (xbf, xlo).  (MW: no rank
-            // product.)
-            if constexpr (!MW) {
+            // X: the same as fp16 high and low parts (xbf, xlo).
             uint32_t xbf[4][4][2];
             uint32_t xlo[4][4][2];
             {
@@ -965,7 +937,6 @@ __global__ __launch_bounds__(K3_THREADS) void k_pair_bits(const K2Args P) {
                     __builtin_amdgcn_sched_barrier(0);
                 }
             }
-            }  // !MW
 
             // The next block's operands land during the LIF and the stores: its
             // bit rows (the next pair's first block after a pair's last one) and,
