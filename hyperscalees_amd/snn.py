@@ -185,7 +185,7 @@ class SnnEs:
         # from it, and the forward is x W_m^T (half the matrix work of the
         # factored product at 1024 rows per member); the readout, with fewer
         # rows per member, stays on the factored product.
-        can_mw = (self.ahead and (c.rows * c.T) % 256 == 0
+        can_mw = (self.ahead and L > 1 and (c.rows * c.T) % 256 == 0
                   and (self.split or min(c.dims[:-2]) > 64))
         self.mw = can_mw if member_weights is None else (bool(member_weights) and can_mw)
         self.wm = None
@@ -205,6 +205,13 @@ class SnnEs:
         self.overlap = can_overlap if overlap is None else (bool(overlap) and can_overlap)
         self.side = torch.cuda.Stream(device=device) if self.overlap else None
         self._drawn = {}  # layer -> (epoch, lo, event) of a draw issued on the side stream
+        # The next forward's first-layer draw, prefetched on the side stream
+        # during this one (its (epoch, lo) predicted: the next chunk, or the
+        # next epoch's first) into a second record buffer, so that a step
+        # starts with the Poisson encode alone; a forward for anything else
+        # draws inline as before.
+        self.rec0_next = torch.empty_like(self.rec[0]) if self.overlap else None
+        self._prefetched = None  # (epoch, lo, event) of the draw in rec0_next
         self.img = None
         if self.ahead and not self.split:
             self.img = []
@@ -337,15 +344,21 @@ class SnnEs:
         return K.member_fitness(self.logits, labels, c.chunk, c.rows, c.reward,
                                 out=self.raw[lo:lo + c.chunk], correct=self.correct)
 
-    def _draw_factors(self, l, epoch, lo):
-        """Layer l's factors of the chunk into its record (and, without member
-        weights, its operand image) on the current stream."""
+    def _draw_factors(self, l, epoch, lo, rec=None):
+        """Layer l's factors of the chunk into its record (or `rec`) and,
+        without member weights, its operand image, on the current stream."""
         c = self.cfg
         a, b = self.W[l].shape
         img = self.img_x if self.split else self.img
         mw = self.mw and l < self.L - 1
         K.pair_factors(c.keys[l], c.rank, c.sigma, epoch, c.noise_reuse, lo, c.chunk, a, b,
-                       self.rec[l], None if mw else img[l], split=self.split and not mw)
+                       self.rec[l] if rec is None else rec, None if mw else img[l],
+                       split=self.split and not mw)
+
+    def _next_forward(self, epoch, lo):
+        """The (epoch, lo) a training loop runs after this forward."""
+        c = self.cfg
+        return (epoch, lo + c.chunk) if lo + c.chunk < c.n else (epoch + 1, 0)
 
     def _issue_draws(self, epoch, lo, layers):
         """Layers' draws of the chunk on the side stream, after the work
@@ -384,6 +397,20 @@ class SnnEs:
         if self.overlap and l == 0 and drawn is not None:
             # the other layers' draws, beside the first layer's GEMM
             self._issue_draws(epoch, lo, range(1, self.L))
+        if self.overlap and self.mw and l == min(1, self.L - 2) and drawn is not None:
+            # the next forward's first-layer draw, beside the later layers'
+            # GEMMs (its buffer was last read by the previous step, which the
+            # side stream has waited for; with an operand image layer 0 has
+            # one image only, so only the record-only draw is prefetched)
+            ne, nl = self._next_forward(epoch, lo)
+            issued = torch.cuda.Event()
+            issued.record()
+            with torch.cuda.stream(self.side):
+                self.side.wait_event(issued)
+                self._draw_factors(0, ne, nl, rec=self.rec0_next)
+                done = torch.cuda.Event()
+                done.record(self.side)
+            self._prefetched = (ne, nl, done)
         return out
 
     def forward(self, epoch=0, lo=0, mark=None):
@@ -392,7 +419,13 @@ class SnnEs:
         record an event on the current stream)."""
         mark = mark or (lambda name: None)
         if self.overlap:
-            self._issue_draws(epoch, lo, [0])
+            pre, self._prefetched = self._prefetched, None
+            if pre is not None and pre[:2] == (epoch, lo):
+                # the prefetched draw: its buffer becomes layer 0's record
+                self.rec[0], self.rec0_next = self.rec0_next, self.rec[0]
+                self._drawn[0] = pre
+            else:
+                self._issue_draws(epoch, lo, [0])
         self.poisson(lo)
         mark("poisson")
         for l in range(self.L - 1):
