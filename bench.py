@@ -716,7 +716,7 @@ def main():
                      "readout_fitness": round(float(t_readout), 3),
                      "forward": round(float(t_fwd), 3), "es_update": round(float(t_upd), 3)},
         "fwd_tflops": round(fwd_flops / (t_fwd * 1e-3) / 1e12, 1),
-        "roofline": {"kernel": (("k_pair_bits<LIF, T=16, spikes, member weights"
+        "roofline": {"kernel": (("k_mw_bits<LIF, T=16, spikes"
                                  + (", split fp16 operands" if es.split else "")
                                  + "> (fc1: x W_m^T, T=16 x 524288 rows, LIF fused)")
                                 if es.mw else

@@ -684,13 +684,19 @@ int launch_linear_mw(LinParams& P, DeviceState* st, hipStream_t s, const LifOut*
     // two workgroups per CU, persistent over the pairs
     const int32_t slots = 2 * st->num_cus;
     int32_t grid = std::max(1, std::min(A.n_pairs, slots));
-    // pairs split over 4 workgroups of one XCD, as in launch_linear_pair: the
-    // member's weights are fetched about once and re-read from that XCD's L2
+    // pairs split over S workgroups of one XCD that work on them at the same
+    // time: one 256-row block each when the pair's rows allow (S = 8 at C3),
+    // so every block of a member streams the member's weights together and
+    // they are fetched from HBM about once and re-read from that XCD's L2;
+    // else 4, as in launch_linear_pair
     A.split = 1;
-    if (P.tid_lo % 2 == 0 && P.n % 2 == 0 && (2 * (int64_t)P.R) % (4 * MB_RB) == 0 &&
-        slots % 32 == 0 && (int64_t)A.n_pairs * 4 >= slots) {
-        A.split = 4;
-        grid = slots;
+    for (int32_t S : {8, 4}) {
+        if (P.tid_lo % 2 == 0 && P.n % 2 == 0 && (2 * (int64_t)P.R) % (S * MB_RB) == 0 &&
+            slots % (8 * S) == 0 && (int64_t)A.n_pairs * S >= slots) {
+            A.split = S;
+            grid = slots;
+            break;
+        }
     }
     A.group = 1;
     A.x = P.x;
