@@ -33,7 +33,10 @@ constexpr int MW_KC = 64;        // inputs (columns of W_m) per chunk
 constexpr int MW_BP = K2_NMAX + 8;  // LDS pitch of a staged B row (fp16; 272 B)
 
 // Elements of one member's weights: (a, kp) once (bf16) or twice (high then
-// low part, fp16).
+// low part, fp16), each chunk-major: input chunk c (inputs 64 c .. + 63) of
+// all a rows, [c][o][64], so that a 64-input chunk of a member is one
+// contiguous run for its writer (k_member_weights) and its reader's tiles
+// (k_mw_bits); chunk-strided rows spread writes over DRAM pages.
 static int64_t member_stride(int32_t a, int32_t b, bool split) {
     return (split ? 2 : 1) * (int64_t)a * ((b + 63) / 64 * 64);
 }
@@ -102,49 +105,75 @@ __global__ __launch_bounds__(MW_THREADS, 2) void k_member_weights(
         }
     }
 
-    // B staging: thread t loads rank row c = t / 2, inputs k0 + 32 (t % 2) +
-    // [0, 32) as 8 float4 (zero past b or past r)
-    const int32_t sc = tid >> 1, sk = (tid & 1) * 32;
+    // B staging: wave w stages rank rows 32w .. 32w + 31 of the chunk; its
+    // load q covers rows 32w + 2 (lane / 4) + q % 2, inputs 16 (q / 2) +
+    // 4 (lane % 4) .. + 3 (16 rows x 64 bytes per load, each 128-byte line
+    // whole over two loads), so a thread holds the same 16 inputs of two
+    // adjacent rank rows and stores their fp16 parts as pairs: 32-bit LDS
+    // writes, lane l on bank 16 (l % 4) + l / 4 (conflict-free)
+    const int32_t sc0 = 32 * wave + 2 * (lane >> 2), sk = 4 * (lane & 3);
     // 16-byte loads when every record row starts 16-byte aligned
     const bool vec = ((uintptr_t)rec % 16 == 0) && (ab % 4 == 0);
     float4 bv[8];
     auto bload = [&](int32_t k0) {
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
-            const int32_t k = k0 + sk + 4 * q;
-            if (vec && sc < r && k + 3 < b) {
-                bv[q] = *reinterpret_cast<const float4*>(rp + (size_t)sc * ab + k);
+            const int32_t c = sc0 + (q & 1), k = k0 + 16 * (q >> 1) + sk;
+            if (vec && c < r && k + 3 < b) {
+                bv[q] = *reinterpret_cast<const float4*>(rp + (size_t)c * ab + k);
             } else {
                 float e[4];
 #pragma unroll
-                for (int u = 0; u < 4; ++u) e[u] = (sc < r && k + u < b) ? rp[(size_t)sc * ab + k + u] : 0.0f;
+                for (int u = 0; u < 4; ++u) e[u] = (c < r && k + u < b) ? rp[(size_t)c * ab + k + u] : 0.0f;
                 bv[q] = make_float4(e[0], e[1], e[2], e[3]);
             }
         }
     };
     auto bstore = [&]() {
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const float e[4] = {bv[q].x, bv[q].y, bv[q].z, bv[q].w};
+        for (int kb = 0; kb < 4; ++kb) {
+            const float e0[4] = {bv[2 * kb].x, bv[2 * kb].y, bv[2 * kb].z, bv[2 * kb].w};
+            const float e1[4] = {bv[2 * kb + 1].x, bv[2 * kb + 1].y, bv[2 * kb + 1].z,
+                                 bv[2 * kb + 1].w};
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                uint16_t h, l;
-                split_f16(e[u], &h, &l);
-                const int32_t at = (sk + 4 * q + u) * MW_BP + sc;
-                Bh[at] = h;
-                Bl[at] = l;
+                uint16_t h0, l0, h1, l1;
+                split_f16(e0[u], &h0, &l0);
+                split_f16(e1[u], &h1, &l1);
+                const int32_t at = (16 * kb + sk + u) * MW_BP + sc0;  // even: 4-byte aligned
+                *reinterpret_cast<uint32_t*>(Bh + at) = (uint32_t)h0 | ((uint32_t)h1 << 16);
+                *reinterpret_cast<uint32_t*>(Bl + at) = (uint32_t)l0 | ((uint32_t)l1 << 16);
             }
         }
     };
     // W rows 16-byte aligned: 8 consecutive inputs as two float4
     const bool wvec = ((uintptr_t)W % 16 == 0) && (b % 4 == 0);
     const int32_t nch = kp / MW_KC;
+    // this lane's runs of W for the chunk at k0 (run lane + 64 q: row
+    // (lane + 64 q) / 8, inputs 8 (lane % 8) .. + 7), loaded before the
+    // chunk's products so that the loads land while they run
+    float wv[4][8];
+    auto wload = [&](int32_t k0) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int32_t run = lane + 64 * q, o = o0 + (run >> 3), k = k0 + (run & 7) * 8;
+            const float* wr = W + (size_t)min(o, a - 1) * b + k;
+            if (wvec && k + 7 < b) {
+                *reinterpret_cast<float4*>(wv[q]) = *reinterpret_cast<const float4*>(wr);
+                *reinterpret_cast<float4*>(wv[q] + 4) = *reinterpret_cast<const float4*>(wr + 4);
+            } else {
+#pragma unroll
+                for (int u = 0; u < 8; ++u) wv[q][u] = k + u < b ? wr[u] : 0.0f;
+            }
+        }
+    };
     bload(0);
     bstore();
     __syncthreads();
     for (int32_t ch = 0; ch < nch; ++ch) {
         const int32_t k0 = ch * MW_KC;
         if (ch + 1 < nch) bload(k0 + MW_KC);
+        if (wave_on) wload(k0);
         f32x16 acc[2] = {f32x16{}, f32x16{}};
         if (wave_on) {
 #pragma unroll
@@ -162,7 +191,6 @@ __global__ __launch_bounds__(MW_THREADS, 2) void k_member_weights(
             }
         }
         __syncthreads();  // every wave has read this chunk's B
-        if (ch + 1 < nch) bstore();
         if (wave_on) {
             // result -> the wave's scratch [row][input]
 #pragma unroll
@@ -177,21 +205,14 @@ __global__ __launch_bounds__(MW_THREADS, 2) void k_member_weights(
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int32_t run = lane + 64 * q, row = run >> 3, k8 = (run & 7) * 8;
-                const int32_t o = o0 + row, k = k0 + k8;
+                const int32_t o = o0 + row;
                 if (o >= a) continue;
-                float p[8], w[8];
+                float p[8];
+                const float* w = wv[q];
                 *reinterpret_cast<float4*>(p) = *reinterpret_cast<const float4*>(scr + row * MW_SP + k8);
                 *reinterpret_cast<float4*>(p + 4) =
                     *reinterpret_cast<const float4*>(scr + row * MW_SP + k8 + 4);
-                const float* wr = W + (size_t)o * b + k;
-                if (wvec && k + 7 < b) {
-                    *reinterpret_cast<float4*>(w) = *reinterpret_cast<const float4*>(wr);
-                    *reinterpret_cast<float4*>(w + 4) = *reinterpret_cast<const float4*>(wr + 4);
-                } else {
-#pragma unroll
-                    for (int u = 0; u < 8; ++u) w[u] = k + u < b ? wr[u] : 0.0f;
-                }
-                const int64_t at = (int64_t)o * kp + k;
+                const int64_t at = (int64_t)ch * a * MW_KC + o * MW_KC + k8;
                 if constexpr (X) {
                     u16x8 eh, el, oh, ol;
 #pragma unroll
@@ -226,6 +247,9 @@ __global__ __launch_bounds__(MW_THREADS, 2) void k_member_weights(
                 }
             }
         }
+        // the next chunk's B after this chunk's stores: its loads had the
+        // products and the stores' arithmetic to land
+        if (ch + 1 < nch) bstore();
         __syncthreads();  // the next chunk's B is in LDS
     }
 }
@@ -243,8 +267,9 @@ __global__ __launch_bounds__(MW_THREADS, 2) void k_member_weights(
 // k_pair_bits) stream by LDS DMA into NB buffers, each transfer issued right
 // after the barrier that frees its buffer, NB - 1 tiles ahead (NB = 3 when a
 // block has at least three stream tiles, so a transfer has two tiles of
-// MFMAs to land; else 2); with X each K tile streams twice (high, then low
-// part) on the same bit rows.  The epilogue runs the LIF (or
+// MFMAs to land; else 2); with X a stream tile holds 32 inputs of both
+// parts, its k-steps alternating high and low part, so each expanded x
+// operand feeds the MFMAs of two steps.  The epilogue runs the LIF (or
 // stores y) in registers as k_pair_bits does, per row tile.  Two workgroups
 // share a CU (58.6 KB of LDS each at b = 784).
 constexpr int MB_THREADS = 256, MB_RB = 256;
@@ -288,11 +313,17 @@ __global__ __launch_bounds__(MB_THREADS, 2) void k_mw_bits(const K2Args P) {
     for (int q = 0; q < 4; ++q) {
         const int32_t col = 32 * wave + 8 * q + (lane >> 3);
         const int32_t ch = (lane & 7) ^ (((8 * q + (lane >> 3)) >> 1) & 7);
-        dl_off[q] = min(col, a - 1) * kp + ch * 8;
+        // X: chunk ch holds part (ch / 2) % 2 of inputs 16 (ch / 4) + 8 (ch % 2)
+        // .. + 7 of the tile's 32, so k-steps 0-3 read high 0-15, low 0-15,
+        // high 16-31, low 16-31
+        dl_off[q] = min(col, a - 1) * K2_BK +
+                    (X ? (int32_t)(((ch >> 1) & 1) * part_off) + 16 * (ch >> 2) + 8 * (ch & 1) : ch * 8);
     }
+    // member weights are chunk-major (64-input chunks of a rows each), so a
+    // tile is one contiguous 16 KB run (X: two 8 KB runs, one per part)
     auto dl_issue = [&](const uint16_t* src, int32_t t, int32_t buf) {
         if (wave >= WT) return;  // W rows no output tile reads
-        const uint16_t* s = src + (X ? (t & 1) * part_off : 0) + (X ? t >> 1 : t) * K2_BK;
+        const uint16_t* s = src + (X ? (size_t)(t >> 1) * a * K2_BK + (t & 1) * 32 : (size_t)t * a * K2_BK);
         const uint32_t dst = __builtin_amdgcn_readfirstlane(lds_addr(WB + buf * MB_TILE + (4 * wave) * 512));
 #pragma unroll
         for (int q = 0; q < 4; ++q) lds_dma16(s + dl_off[q], dst + q * 1024);
@@ -455,9 +486,12 @@ __global__ __launch_bounds__(MB_THREADS, 2) void k_mw_bits(const K2Args P) {
             // one k-step: per column tile its two MFMAs and the read of its
             // fragment for the step at `nxt`; wn / ksn: the next step's words
             // and k-step
-            auto step = [&](auto zc, const uint16_t* nxt, const uint32_t (&wn)[2], int ksn) {
+            // ksn < 0: the next step runs on the same x operands (X: the low
+            // part's step after the high part's)
+            auto step = [&](auto zc, const uint16_t* nxt, const uint32_t (&wn)[2], auto kc) {
                 constexpr bool z = decltype(zc)::value;
-                u16x8 xn[2];
+                constexpr int ksn = decltype(kc)::value;
+                u16x8 xn[2] = {xa[0], xa[1]};
 #pragma unroll
                 for (int ct = 0; ct < WT; ++ct) {
 #pragma unroll
@@ -468,22 +502,34 @@ __global__ __launch_bounds__(MB_THREADS, 2) void k_mw_bits(const K2Args P) {
                             acc[rt][ct] = mfma32_bf16(xa[rt], fr[ct], z ? f32x16{} : acc[rt][ct]);
                     }
                     fr[ct] = lds_u16x8(nxt + 32 * ct * K2_BK);
-                    if (ct == 0) xn[0] = expand(wn[0], ksn);
-                    if (ct == (WT > 1 ? 1 : 0)) xn[1] = expand(wn[1], ksn);
+                    if constexpr (ksn >= 0) {
+                        if (ct == 0) xn[0] = expand(wn[0], ksn);
+                        if (ct == (WT > 1 ? 1 : 0)) xn[1] = expand(wn[1], ksn);
+                    }
                     __builtin_amdgcn_sched_barrier(0);
                 }
                 xa[0] = xn[0];
                 xa[1] = xn[1];
             };
+            using K0 = std::integral_constant<int, 0>;
+            using K1 = std::integral_constant<int, 1>;
+            using KS = std::integral_constant<int, -1>;
             auto tile = [&](int32_t kt, auto zc) {
                 const bool more = kt + 1 < ntb;
                 const int32_t kn = more ? kt + 1 : kt;
-                const int32_t kw = X ? kn >> 1 : kn;  // x word of tile kn
                 const int32_t cb = dl_cb, nb = next_buf(dl_cb);
                 const uint32_t wa[2] = {xw0[0], xw0[1]}, wb[2] = {xw1[0], xw1[1]};
-                step(zc, frag_ptr(cb, 1), wa, 1);
-                step(std::false_type{}, frag_ptr(cb, 2), wb, 2);
-                step(std::false_type{}, frag_ptr(cb, 3), wb, 3);
+                if constexpr (X) {
+                    // 32 inputs (32-bit x word kt): high and low steps share
+                    // the expanded x operands
+                    step(zc, frag_ptr(cb, 1), wa, KS{});
+                    step(std::false_type{}, frag_ptr(cb, 2), wa, K1{});
+                    step(std::false_type{}, frag_ptr(cb, 3), wa, KS{});
+                } else {
+                    step(zc, frag_ptr(cb, 1), wa, K1{});
+                    step(std::false_type{}, frag_ptr(cb, 2), wb, std::integral_constant<int, 2>{});
+                    step(std::false_type{}, frag_ptr(cb, 3), wb, std::integral_constant<int, 3>{});
+                }
                 if (more) {
                     dl_wait();  // tile kt + 1 has landed
                     lds_barrier();
@@ -491,11 +537,15 @@ __global__ __launch_bounds__(MB_THREADS, 2) void k_mw_bits(const K2Args P) {
                 }
 #pragma unroll
                 for (int rt = 0; rt < 2; ++rt) {
-                    xw0[rt] = xw[rt][2 * kw];
-                    xw1[rt] = xw[rt][2 * kw + 1];
+                    if constexpr (X) {
+                        xw0[rt] = xw[rt][kn];
+                    } else {
+                        xw0[rt] = xw[rt][2 * kn];
+                        xw1[rt] = xw[rt][2 * kn + 1];
+                    }
                 }
                 const uint32_t wn[2] = {xw0[0], xw0[1]};
-                step(std::false_type{}, frag_ptr(more ? nb : cb, 0), wn, 0);
+                step(std::false_type{}, frag_ptr(more ? nb : cb, 0), wn, K0{});
                 dl_cb = nb;
             };
             tile(0, std::true_type{});
@@ -671,7 +721,7 @@ int launch_linear_mw(LinParams& P, DeviceState* st, hipStream_t s, const LifOut*
     if (P.x_fmt != HSES_FMT_BITS || P.a > K2_NMAX || P.R % MB_RB || P.b > 64 * MB_XPF || P.tmm)
         return HSES_ERR_UNSUPPORTED;
     // the two-buffer stream needs two stream tiles per block: K of more than
-    // one tile, or the split form (each K tile streamed twice)
+    // one tile, or the split form (two stream tiles per 64 inputs)
     if (!xm && P.b <= 64) return HSES_ERR_UNSUPPORTED;
     if (lif && (P.n_time > 16 || (P.n_time & (P.n_time - 1)) != 0)) return HSES_ERR_UNSUPPORTED;
     // three tile buffers when a block streams at least three tiles

@@ -213,7 +213,8 @@ def pair_factors(key, rank, sigma, epoch, noise_reuse, tid_lo, n, a, b, rec, img
 def member_weights(W, rank, sigma, tid_lo, n, rec, math=MATH_F32X, out=None):
     """Every member's perturbed weights W + sign_m (sigma/sqrt(r)) A_m B_m^T from
     the factor record (hses_member_weights): int16 storage of bf16 (math BF16)
-    or of fp16 high and low parts of 1024 W_m (math F32X)."""
+    or of fp16 high and low parts of 1024 W_m (math F32X), chunk-major
+    ([part][input chunk of 64][a][64]) per member."""
     a, b = W.shape
     _dev(W, torch.float32, "W")
     nbytes = int(_lib.load().hses_member_weights_bytes(a, b, n, math))

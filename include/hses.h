@@ -422,8 +422,9 @@ int hses_perturbed_linear_lif_counts_pre_x(
  * hses_member_weights forms every member's W_m from the factor record (a
  * record written by hses_pair_factors with d_img = NULL, by either image
  * form, or by a *_rec forward): with math = HSES_MATH_BF16 W_m in bf16,
- * (a, ceil(b/64)*64) per member, zero past b; with HSES_MATH_F32X the fp16
- * high and low parts of 1024 W_m, each of that shape (the product A_m B_m^T
+ * a x ceil(b/64)*64 per member, zero past b, stored chunk-major
+ * ([b/64 chunk][a][64 inputs]); with HSES_MATH_F32X the fp16 high and low
+ * parts of 1024 W_m, each of that shape (the product A_m B_m^T
  * is taken on split operands in both, so only W_m's final rounding differs).
  * The forwards read them: bit-packed x, rows per member (n_time x
  * rows_per_member) a multiple of 256, a <= 128, b <= 1024 (b > 64 with

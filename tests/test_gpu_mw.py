@@ -64,14 +64,16 @@ def test_member_weights(hses_gpu, a, b, r, n, tid_lo):
     wb = K.member_weights(Wd, r, sigma, tid_lo, n, rec, math=MATH_BF16)
     torch.cuda.synchronize()
     Wm, S, _, _ = reference_weights(W, a, b, r, sigma, tid_lo, n)
-    hx = wx.view(n, 2, a, kp).cpu().numpy().view(np.float16).astype(np.float64)
+    # chunk-major storage: [part][input chunk of 64][a][64]
+    hx = wx.view(n, 2, kp // 64, a, 64).permute(0, 1, 3, 2, 4).reshape(n, 2, a, kp)
+    hx = hx.cpu().numpy().view(np.float16).astype(np.float64)
     got = (hx[:, 0] + hx[:, 1])[:, :, :b] / 1024.0
     assert not hx[:, :, :, b:].any(), "padding columns"
     # fp32 accumulation over r products and the split's 2^-22, within 2^-20
     # of the element's sum of |terms|
     err = np.abs(got - Wm)
     assert (err <= 2.0 ** -20 * S).all(), f"split weights err {(err / S).max():.3e} of sum|terms|"
-    gb = wb.view(n, a, kp).cpu().numpy()
+    gb = wb.view(n, kp // 64, a, 64).permute(0, 2, 1, 3).reshape(n, a, kp).cpu().numpy()
     gbf = (gb.astype(np.uint32) << 16).view(np.float32).astype(np.float64)[:, :, :b]
     assert not gb[:, :, b:].any(), "padding columns"
     # rounding to bf16 from an fp32-accurate value: within half a step plus
