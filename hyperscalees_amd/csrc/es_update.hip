@@ -345,7 +345,8 @@ __global__ __launch_bounds__(R_MAXT) void k_es_rows(UpdParams P, RowTiles G) {
         const float* src = P.rec + ((int64_t)(p - P.pair_lo) * r + ch * U_CW) * rstride + srow;
         const int32_t cn = min(U_CW, r - ch * U_CW);
 #pragma unroll
-        for (int c = 0; c < U_CW; ++c) pr[c] = c < cn ? src[c * rstride] : 0.0f;
+        for (int c = 0; c < U_CW; ++c)
+            pr[c] = c < cn ? __builtin_nontemporal_load(src + c * rstride) : 0.0f;  // read once
     };
     auto store_item = [&](const float (&pv)[U_CW], uint16_t* dst, int32_t cn, float w) {
 #pragma unroll

@@ -89,8 +89,11 @@ __global__ __launch_bounds__(KG_THREADS) void k_pair_gen(const K2Args P) {
     const NoiseCtx ctx{&t, P.log_exc, P.cos_exc};
     // no image (bimg NULL): the record alone
     const bool wimg = P.bimg != nullptr;
+    // the record is read back by later kernels, long after this one:
+    // non-temporal stores keep it from evicting the L2 lines of the kernels
+    // that run beside the draw
     auto one = [&](int32_t c, float v) {
-        rp[(size_t)c * rows] = v;
+        __builtin_nontemporal_store(v, rp + (size_t)c * rows);
         if (!wimg) return;
         const size_t at = sr.in_side ? (size_t)c * kp : (size_t)swap23(c);
         if constexpr (X) {
@@ -106,7 +109,7 @@ __global__ __launch_bounds__(KG_THREADS) void k_pair_gen(const K2Args P) {
         s, r, ctx,
         [&](int32_t c0, const float (&v)[4]) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) rp[(size_t)(c0 + q) * rows] = v[q];
+            for (int q = 0; q < 4; ++q) __builtin_nontemporal_store(v[q], rp + (size_t)(c0 + q) * rows);
             if (!wimg) return;
             if constexpr (X) {
                 uint16_t hi[4], lo[4];
