@@ -30,12 +30,17 @@ METRIC = "perturbed member-evals/sec + ES-update GB/s, SNN-MLP N=8192 r=128"
 PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
 PEAK_FP32_TFLOPS = 157.3      # MI355X dense fp32 MFMA
 PEAK_HBM_GBPS = 8000.0
-# HBM bytes per launch of fc1's GEMM on factors drawn ahead, from two rocprofv3 PMC runs
-# (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0, factors from a 1 GiB copy in the same process) of
-# `python3 -m hyperscalees_amd.profile_fc1`: 4.067 GB x 2 + 0.134 GB, measured on the kernel
-# source of commit 8b404b2; see profiles/fc1_c3_traffic.md.  Refreshed whenever the kernel
-# changes; the bench line names the source it was measured on.
-FC1_TRAFFIC = {}  # (math, member weights) -> (bytes per launch, source); filled once measured
+# HBM bytes per launch of fc1's GEMM on member weights (k_mw_bits), from two rocprofv3 PMC runs
+# of `python3 -m hyperscalees_amd.profile_fc1` (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0, factors
+# from a 1 GiB copy in the same process; profiles/fc1_c3_traffic.md), keyed by (math, member
+# weights).  Measured on the k_mw_bits source of commit 024c4e3 (unchanged since); refreshed
+# whenever the kernel changes, and the bench line names the source it was measured on.
+FC1_TRAFFIC = {
+    ("f32x", True): (4.528e9, "rocprofv3 PMC of profile_fc1, k_mw_bits of commit 024c4e3: "
+                              "4.393e9 B read + 0.134e9 B written"),
+    ("bf16", True): (2.760e9, "rocprofv3 PMC of profile_fc1 --math bf16, k_mw_bits of commit "
+                              "024c4e3: 2.626e9 B read + 0.134e9 B written"),
+}
 
 
 def layer_flops(cfg, l):
