@@ -597,9 +597,17 @@ __global__ __launch_bounds__(MB_THREADS, 2) void k_mw_bits(const K2Args P) {
                 // LIF (snn.rs:53-97) along each lane's rows, v = 0 at t = 0; the
                 // reset as in k_pair_bits (charged kept when no spike, else 0)
                 uint32_t wlo[2] = {0, 0}, whi[2] = {0, 0};  // lane u: spike words of wave row u
-                bool colok[WT];
+                // lanes of valid columns, as a ballot mask ANDed into each
+                // step's ballot (a scalar AND instead of a per-lane select)
+                uint64_t colmask[WT];
 #pragma unroll
-                for (int jo = 0; jo < WT; ++jo) colok[jo] = 32 * jo + lc < a;
+                for (int jo = 0; jo < WT; ++jo) colmask[jo] = __builtin_amdgcn_ballot_w64(32 * jo + lc < a);
+                // X: the LIF runs on the 2^10-scaled currents the MFMAs leave
+                // (membrane 2^10 v, threshold 2^10 v_th): scaling by a power of
+                // two commutes with every rounding of the update, so the spikes
+                // and resets are those of the unscaled recurrence
+                const float vth = X ? P.v_th * K3_XSCALE : P.v_th;
+                uint64_t dummy_carry;  // carry out of the count's add (unused)
                 static_for<0, 2>([&](auto rc) {
                     constexpr int rt = decltype(rc)::value;
                     float vm[WT];
@@ -616,12 +624,22 @@ __global__ __launch_bounds__(MB_THREADS, 2) void k_mw_bits(const K2Args P) {
                         uint64_t bal[WT];
 #pragma unroll
                         for (int jo = 0; jo < WT; ++jo) {
-                            const float c = X ? acc[rt][jo][qq] * (1.0f / K3_XSCALE) : acc[rt][jo][qq];
+                            const float c = acc[rt][jo][qq];
                             const float charged = __fadd_rn(vm[jo], __fmul_rn(__fadd_rn(-vm[jo], c), P.leak));
-                            const bool spike = charged >= P.v_th;
-                            vm[jo] = spike ? 0.0f : charged;
-                            if constexpr (RATE) cnt[jo] += spike ? 1 : 0;
-                            if constexpr (SPK) bal[jo] = __builtin_amdgcn_ballot_w64(spike && colok[jo]);
+                            // one compare: its lane mask selects the reset and
+                            // carries the count, and is the step's ballot
+                            const uint64_t sp = __builtin_amdgcn_ballot_w64(charged >= vth);
+                            float nv;
+                            asm("v_cndmask_b32 %0, %1, 0, %2" : "=v"(nv) : "v"(charged), "s"(sp));
+                            vm[jo] = nv;
+                            if constexpr (RATE) {
+                                int32_t nc;
+                                asm("v_addc_co_u32 %0, %1, %2, 0, %3"
+                                    : "=v"(nc), "=s"(dummy_carry)
+                                    : "v"(cnt[jo]), "s"(sp));
+                                cnt[jo] = nc;
+                            }
+                            if constexpr (SPK) bal[jo] = sp & colmask[jo];
                         }
                         if constexpr (RATE && qq % LT == LT - 1) {
                             const int32_t row = wrow0 + 32 * rt + 16 * hl + qq;
@@ -633,7 +651,7 @@ __global__ __launch_bounds__(MB_THREADS, 2) void k_mw_bits(const K2Args P) {
                                 for (int p = 0; p < NPL; ++p)
 #pragma unroll
                                     for (int jo = 0; jo < WT; ++jo)
-                                        pb[p][jo] = __builtin_amdgcn_ballot_w64(((cnt[jo] >> p) & 1) && colok[jo]);
+                                        pb[p][jo] = __builtin_amdgcn_ballot_w64((cnt[jo] >> p) & 1) & colmask[jo];
                                 if (lc == 0 && row < nvalid) {
                                     int32_t m, q;
                                     cur_rows.at(row, R, &m, &q);
@@ -656,7 +674,7 @@ __global__ __launch_bounds__(MB_THREADS, 2) void k_mw_bits(const K2Args P) {
                                 float* rp = P.rate + ((int64_t)m * P.rpm + q / LT) * P.rate_stride;
 #pragma unroll
                                 for (int jo = 0; jo < WT; ++jo)
-                                    if (colok[jo]) rp[32 * jo + lc] = (float)cnt[jo] * (1.0f / LT);
+                                    if (32 * jo + lc < a) rp[32 * jo + lc] = (float)cnt[jo] * (1.0f / LT);
                             }
                         }
                         if constexpr (SPK) {
