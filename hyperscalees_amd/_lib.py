@@ -82,6 +82,9 @@ PROTOTYPES = {
                                                     c_i32, c_i32, c_i32, c_i32, c_f32, c_f32,
                                                     c_i32, c_vp, c_size, c_vp, c_i64, c_i64, c_vp,
                                                     c_i64, c_vp, c_i64, c_vp]),
+    "hses_perturbed_readout_counts": (ctypes.c_int, [c_vp, c_i64, c_i32, c_vp, c_i32, c_i32,
+                                                     c_i32, c_f32, c_i32, c_i32, c_i32, c_vp,
+                                                     c_size, c_vp, c_i64, c_vp]),
     "hses_perturbed_linear_lif_counts_pre_x": (ctypes.c_int, [c_vp, c_i32, c_i64, c_i64, c_i32,
                                                               c_vp, c_i32, c_i32, c_i32, c_f32,
                                                               c_i32, c_i32, c_i32, c_f32, c_f32,

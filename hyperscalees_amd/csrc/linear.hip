@@ -937,6 +937,41 @@ extern "C" int hses_perturbed_linear_lif_mw(
     return rc;
 }
 
+extern "C" int hses_perturbed_readout_counts(const uint64_t* d_counts, int64_t counts_stride,
+                                             int32_t n_time, const float* d_W, int32_t a,
+                                             int32_t b, int32_t rank, float sigma, int32_t tid_lo,
+                                             int32_t n, int32_t rows_per_member,
+                                             const float* d_rec, size_t rec_bytes, float* d_y,
+                                             int64_t y_stride, void* stream) {
+    HSES_REQUIRE(a >= 1 && b >= 1 && n >= 0 && rank >= 1 && rows_per_member >= 1, "bad sizes");
+    HSES_REQUIRE(tid_lo >= 0 && (int64_t)tid_lo + n - 1 <= INT32_MAX, "thread id range");
+    HSES_REQUIRE(n_time >= 1 && n_time <= 16 && (n_time & (n_time - 1)) == 0,
+                 "hses_perturbed_readout_counts: n_time must be a power of two <= 16");
+    HSES_REQUIRE(a <= 32 && b <= 128 && rows_per_member <= 128,
+                 "hses_perturbed_readout_counts: a <= 32, b <= 128 and rows_per_member <= 128");
+    HSES_REQUIRE(readout_counts_lds(a, b, rank) <= 160 * 1024,
+                 "hses_perturbed_readout_counts: rank * (a + b) too large for LDS");
+    if (n == 0) return HSES_OK;
+    int rc = check_drawn(a, b, rank, sigma, tid_lo, n, d_rec, rec_bytes, nullptr, 0,
+                         "hses_perturbed_readout_counts", false, true);
+    if (rc) return rc;
+    HSES_REQUIRE(d_counts && d_W && d_y, "NULL pointer");
+    int32_t planes = 1;
+    while ((1 << (planes - 1)) < n_time) ++planes;
+    HSES_REQUIRE(counts_stride >= (int64_t)planes * ((b + 63) / 64),
+                 "counts_stride smaller than a row's count planes");
+    HSES_REQUIRE(y_stride >= a, "y_stride smaller than a row");
+    DeviceState* st;
+    rc = get_state(&st);
+    if (rc) return rc;
+    rc = launch_readout_counts(d_counts, counts_stride, n_time, d_W, a, b, rank,
+                               sigma / sqrtf((float)rank) /* eggroll.rs:433 */, tid_lo, n,
+                               rows_per_member, d_rec, d_y, y_stride, (hipStream_t)stream);
+    if (rc == HSES_ERR_UNSUPPORTED)
+        return set_error(HSES_ERR_UNSUPPORTED, "hses_perturbed_readout_counts: unsupported shape");
+    return rc;
+}
+
 extern "C" int hses_perturbed_linear_lif_counts_pre_x(
     const void* d_x, int32_t x_fmt, int64_t x_stride, int64_t x_plane, int32_t n_time,
     const float* d_W, int32_t a, int32_t b, int32_t rank, float sigma, int32_t tid_lo, int32_t n,

@@ -198,6 +198,13 @@ int launch_member_weights(const float* W, const float* rec, int32_t a, int32_t b
                           float bs, int32_t tid_lo, int32_t n, bool split, uint16_t* wm,
                           hipStream_t s);
 int launch_linear_mw(LinParams& P, DeviceState* st, hipStream_t s, const LifOut* lif);
+// The readout on count planes with member weights formed in LDS
+// (k_readout_counts): a <= 32, b <= 128, 2 rows per member <= 256, T <= 16.
+size_t readout_counts_lds(int32_t a, int32_t b, int32_t r);
+int launch_readout_counts(const uint64_t* cpl, int64_t cstride, int32_t T, const float* W,
+                          int32_t a, int32_t b, int32_t r, float bs, int32_t tid_lo, int32_t n,
+                          int32_t rpm, const float* rec, float* y, int64_t ystride,
+                          hipStream_t s);
 // The wide small-rank kernel: 0 when it does not apply to the shape, else its
 // workspace (W as bf16, (a, kp)).
 size_t linear_wide_workspace(int32_t a, int32_t b, int32_t r, int32_t n, int32_t rows_per_member,

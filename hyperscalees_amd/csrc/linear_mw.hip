@@ -841,4 +841,246 @@ int launch_linear_mw(LinParams& P, DeviceState* st, hipStream_t s, const LifOut*
     return nbuf == 3 ? by_math(std::false_type{}, nb3{}) : by_math(std::false_type{}, nb2{});
 }
 
+// ---- k_readout_counts: the readout on count planes, member weights in LDS ----
+//
+// The SNN readout (snn.rs:274-280: logits = rate W^T through do_mm,
+// eggroll.rs:419-446) for a layer with few outputs and rows per member: one
+// workgroup per pair copies the pair's factor record (r rank rows of a + b
+// values, one contiguous block) into LDS, forms
+//   W_m[k][n] = W[k][n] + sign_m sum_c A'[k][c] B[n][c],  A' = A (sigma/sqrt(r))
+// for both members (fp32 sums over c, one thread per (k, n) set), and then
+// for every sample row of the two members decodes its spike counts from the
+// P count planes (count = sum_p 2^p bit_p) and forms
+//   y[k] = (sum_n count[n] W_m[k][n]) / T,
+// the rate readout reassociated (the counts are exact, the 1/T a power of
+// two).  Thread t of the logits phase takes sample t / 2 of the pair and the
+// outputs k = t % 2, t % 2 + 2, ...
+constexpr int RO_THREADS = 256, RO_KMAX = 32, RO_BMAX = 128;
+// KQ: outputs in runs of 4 (a <= 4 KQ), so every output loop is unrolled
+template <int KQ>
+__global__ __launch_bounds__(RO_THREADS, 2) void k_readout_counts(
+    const uint64_t* __restrict__ cpl, int64_t cstride, int32_t T, int32_t P,
+    const float* __restrict__ W, int32_t a, int32_t b, int32_t r, float bs, int32_t tid_lo,
+    int32_t n, int32_t pair_lo, int32_t rpm, const float* __restrict__ rec,
+    float* __restrict__ y, int64_t ystride) {
+    extern __shared__ __align__(16) float ro_lds[];
+    const int32_t pi = blockIdx.x, tid = threadIdx.x;
+    const int32_t ab = a + b;
+    const float* rp = rec + (size_t)pi * r * ab;
+    const int32_t m_even = 2 * (pair_lo + pi) - tid_lo;  // -1: absent
+    // the count planes of this thread's first task (phase 3), loaded first so
+    // that they arrive during phases 1 and 2
+    const int32_t words = (b + 63) >> 6;
+    uint32_t plo0[5], phi0[5];
+    auto load_planes = [&](int32_t task, uint32_t (&plo)[5], uint32_t (&phi)[5]) {
+        const int32_t srow = task >> 1, wsel = task & 1;
+        const int32_t half = srow / rpm, sl = srow - half * rpm;
+        const int32_t m = m_even + half;
+        const bool ok = task < 4 * rpm && m >= 0 && m < n && wsel < words;
+        const uint64_t* pl = cpl + ((int64_t)(ok ? m : 0) * rpm + (ok ? sl : 0)) * cstride;
+#pragma unroll
+        for (int p = 0; p < 5; ++p) {
+            const uint64_t v = (ok && p < P) ? pl[p * words + wsel] : 0ull;
+            plo[p] = (uint32_t)v;
+            phi[p] = (uint32_t)(v >> 32);
+        }
+    };
+    load_planes(tid, plo0, phi0);
+    // 1. the pair's record block -> LDS ([c][j], row pitch a + b), in batches
+    // of loads that are all in flight before their stores
+    const int32_t total = r * ab;
+    if (((uintptr_t)rp % 16) == 0) {
+        const int32_t n4 = total / 4;
+        constexpr int CB = 9;
+        for (int32_t base = 0; base < n4; base += CB * RO_THREADS) {
+            f32x4 v[CB];
+#pragma unroll
+            for (int j = 0; j < CB; ++j) {
+                const int32_t i = base + j * RO_THREADS + tid;
+                if (i < n4) v[j] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(rp) + i);
+            }
+#pragma unroll
+            for (int j = 0; j < CB; ++j) {
+                const int32_t i = base + j * RO_THREADS + tid;
+                if (i < n4) *reinterpret_cast<f32x4*>(ro_lds + 4 * i) = v[j];
+            }
+        }
+        for (int32_t i = 4 * n4 + tid; i < total; i += RO_THREADS) ro_lds[i] = rp[i];
+    } else {
+        for (int32_t i = tid; i < total; i += RO_THREADS) ro_lds[i] = rp[i];
+    }
+    __syncthreads();
+    // 2. d[k][n] = sum_c A[k][c] B[n][c]: thread t takes input n = t % b, all
+    // outputs k < 4 KQ (those past a are dropped), and the ranks c = t / b,
+    // t / b + G, ... (G = 256 / b groups, summed through LDS afterwards); each
+    // rank row's values are read one row ahead of their products
+    constexpr int KP = 4 * KQ;
+    const int32_t G = RO_THREADS / b;  // >= 2 (b <= 128)
+    const int32_t nn = tid % b, cg = tid / b;
+    float d[KP];
+#pragma unroll
+    for (int k = 0; k < KP; ++k) d[k] = 0.0f;
+    if (cg < G) {
+        if (ab % 2 == 0 && b % 2 == 0) {
+            // A pairs (k, k + 1) 8-byte aligned; reads past a stay inside the
+            // block's slack
+            float bc = 0.0f, bn = 0.0f;
+            float2 ac[KP / 2], an[KP / 2];
+            auto ld = [&](int32_t c, float& bv, float2 (&av)[KP / 2]) {
+                const float* row = ro_lds + c * ab;
+                bv = row[nn];
+#pragma unroll
+                for (int q = 0; q < KP / 2; ++q) av[q] = *reinterpret_cast<const float2*>(row + b + 2 * q);
+            };
+            if (cg < r) ld(cg, bc, ac);
+            for (int32_t c = cg; c < r; c += G) {
+                if (c + G < r) ld(c + G, bn, an);
+#pragma unroll
+                for (int q = 0; q < KP / 2; ++q) {
+                    d[2 * q] = __builtin_fmaf(ac[q].x, bc, d[2 * q]);
+                    d[2 * q + 1] = __builtin_fmaf(ac[q].y, bc, d[2 * q + 1]);
+                }
+                bc = bn;
+#pragma unroll
+                for (int q = 0; q < KP / 2; ++q) ac[q] = an[q];
+            }
+        } else {
+            for (int32_t c = cg; c < r; c += G) {
+                const float* row = ro_lds + c * ab;
+                const float bv = row[nn];
+#pragma unroll
+                for (int k = 0; k < KP; ++k) d[k] = __builtin_fmaf(row[b + min(k, a - 1)], bv, d[k]);
+            }
+        }
+    }
+    __syncthreads();  // the record block is no longer read
+    float* part = ro_lds;  // [group][n][KP]
+    if (cg < G) {
+#pragma unroll
+        for (int k = 0; k < KP; ++k) part[(cg * b + nn) * KP + k] = d[k];
+    }
+    __syncthreads();
+    if (cg == 0) {
+        for (int32_t g = 1; g < G; ++g)
+#pragma unroll
+            for (int k = 0; k < KP; ++k) d[k] += part[(g * b + nn) * KP + k];
+    }
+    __syncthreads();  // the partials are no longer read
+    // both members' weights into LDS, transposed: Wm[(member b + n) KP + k],
+    // (sigma/sqrt(r)) applied to the sum (the forward scales A; the product
+    // is the same up to rounding)
+    const int32_t kp4 = KP;
+    float* Wm = ro_lds;
+    if (cg == 0) {
+#pragma unroll
+        for (int k = 0; k < KP; ++k) {
+            if (k < a) {
+                const float w = W[(size_t)k * b + nn], dd = d[k] * bs;
+                Wm[nn * KP + k] = w + dd;
+                Wm[(b + nn) * KP + k] = w - dd;
+            }
+        }
+    }
+    __syncthreads();
+    // 3. logits of the pair's 2 rpm sample rows: thread t takes sample t / 2
+    // and the inputs of its 64-bit word t % 2 (b <= 128: two words), all
+    // outputs; the two halves are added across the lane pair
+    const float inv_t = 1.0f / (float)T;  // a power of two: exact
+    for (int32_t task = tid; task < 4 * rpm; task += RO_THREADS) {
+        const int32_t srow = task >> 1, wsel = task & 1;
+        const int32_t half = srow / rpm, sl = srow - half * rpm;
+        const int32_t m = m_even + half;
+        const bool live = m >= 0 && m < n;
+        uint32_t plo[5], phi[5];
+        if (task == tid) {
+#pragma unroll
+            for (int p = 0; p < 5; ++p) {
+                plo[p] = plo0[p];
+                phi[p] = phi0[p];
+            }
+        } else {
+            load_planes(task, plo, phi);
+        }
+        float acc[4 * KQ];
+#pragma unroll
+        for (int k = 0; k < 4 * KQ; ++k) acc[k] = 0.0f;
+        const int32_t n0 = 64 * wsel, nend = min(b, n0 + 64);
+        const float* wbase = Wm + (size_t)(half * b) * kp4;
+        auto one = [&](int32_t nb, uint32_t cnt) {
+            const float cf = (float)cnt;
+            const float* wr = wbase + nb * kp4;
+#pragma unroll
+            for (int k4 = 0; k4 < 4 * KQ; k4 += 4) {
+                const float4 w4 = *reinterpret_cast<const float4*>(wr + k4);
+                acc[k4] = __builtin_fmaf(cf, w4.x, acc[k4]);
+                acc[k4 + 1] = __builtin_fmaf(cf, w4.y, acc[k4 + 1]);
+                acc[k4 + 2] = __builtin_fmaf(cf, w4.z, acc[k4 + 2]);
+                acc[k4 + 3] = __builtin_fmaf(cf, w4.w, acc[k4 + 3]);
+            }
+        };
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            const uint32_t(&src)[5] = hh ? phi : plo;
+            const int32_t nlo = n0 + 32 * hh, nhi = min(nend, nlo + 32);
+#pragma unroll 4
+            for (int32_t nb = nlo; nb < nhi; ++nb) {
+                const uint32_t sh = (uint32_t)(nb - nlo);
+                uint32_t cnt = 0;
+#pragma unroll
+                for (int p = 0; p < 5; ++p) cnt |= __builtin_amdgcn_ubfe(src[p], sh, 1) << p;
+                one(nb, cnt);
+            }
+        }
+        // the lane pair (tasks 2 s, 2 s + 1 are lanes l, l ^ 1) holds the two words
+#pragma unroll
+        for (int k = 0; k < 4 * KQ; ++k) acc[k] += __shfl_xor(acc[k], 1);
+        if (live && wsel == 0) {
+            float* yr = y + ((int64_t)m * rpm + sl) * ystride;
+#pragma unroll
+            for (int k = 0; k < 4 * KQ; ++k)
+                if (k < a) yr[k] = acc[k] * inv_t;
+        }
+    }
+}
+
+size_t readout_counts_lds(int32_t a, int32_t b, int32_t r) {
+    // the record block plus the slack its last row's A reads run into; the
+    // partials (G x b x 4 KQ) and member weights (2 x b x 4 KQ) reuse it
+    const size_t kp4 = (size_t)((a + 3) & ~3);
+    return std::max((size_t)r * (a + b) + kp4, (size_t)(RO_THREADS / b) * b * kp4) * 4;
+}
+
+int launch_readout_counts(const uint64_t* cpl, int64_t cstride, int32_t T, const float* W,
+                          int32_t a, int32_t b, int32_t r, float bs, int32_t tid_lo, int32_t n,
+                          int32_t rpm, const float* rec, float* y, int64_t ystride,
+                          hipStream_t s) {
+    if (a > RO_KMAX || b > RO_BMAX || 2 * rpm > RO_THREADS) return HSES_ERR_UNSUPPORTED;
+    const size_t lds = readout_counts_lds(a, b, r);
+    if (lds > 160 * 1024) return HSES_ERR_UNSUPPORTED;
+    int32_t P = 1;
+    while ((1 << (P - 1)) < T) ++P;
+    if (P > 5) return HSES_ERR_UNSUPPORTED;
+    int32_t lo, cnt;
+    pair_range(tid_lo, n, &lo, &cnt);
+    auto launch = [&](auto kern) -> int {
+        if (lds > 64 * 1024)
+            HSES_CHECK_HIP(hipFuncSetAttribute((const void*)kern,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        hipLaunchKernelGGL(kern, dim3((uint32_t)cnt), dim3(RO_THREADS), lds, s, cpl, cstride, T, P,
+                           W, a, b, r, bs, tid_lo, n, lo, rpm, rec, y, ystride);
+        HSES_CHECK_HIP(hipGetLastError());
+        return HSES_OK;
+    };
+    switch ((a + 3) / 4) {
+        case 1: return launch(k_readout_counts<1>);
+        case 2: return launch(k_readout_counts<2>);
+        case 3: return launch(k_readout_counts<3>);
+        case 4: return launch(k_readout_counts<4>);
+        case 5: return launch(k_readout_counts<5>);
+        case 6: return launch(k_readout_counts<6>);
+        case 7: return launch(k_readout_counts<7>);
+        default: return launch(k_readout_counts<8>);
+    }
+}
+
 }  // namespace hses

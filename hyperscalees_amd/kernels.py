@@ -438,6 +438,29 @@ def perturbed_linear_lif(x, W, key, rank, sigma, epoch, noise_reuse, tid_lo, n,
     return spikes, rate
 
 
+def readout_counts(counts, W, rank, sigma, tid_lo, n, rows_per_member, n_time, rec, out=None):
+    """The readout rate W_m^T on count planes (hses_perturbed_readout_counts):
+    counts (M, P', words(b)) int64 with P' >= count_planes(n_time), W (a, b),
+    the layer's factor record; returns y (M, a) fp32."""
+    a, b = W.shape
+    _dev(W, torch.float32, "W")
+    _dev(counts, torch.int64, "counts")
+    M = n * rows_per_member
+    wb = fmt_width(FMT_BITS, b)
+    if counts.dim() != 3 or counts.shape[0] != M or counts.shape[2] != wb or \
+            counts.shape[1] < count_planes(n_time) or not counts.is_contiguous():
+        raise ValueError(f"counts is (M, P' >= {count_planes(n_time)}, {wb}), contiguous")
+    if out is None:
+        out = torch.empty((M, a), dtype=torch.float32, device=W.device)
+    _dev(out, torch.float32, "out")
+    if out.numel() != M * a:
+        raise ValueError("out has the wrong size")
+    _lib.call("hses_perturbed_readout_counts", _p(counts), counts.shape[1] * wb, n_time, _p(W),
+              a, b, rank, sigma, tid_lo, n, rows_per_member, *_rec_arg(rec), _p(out), a,
+              _stream())
+    return out
+
+
 def count_planes(n_time):
     """Bit planes of a spike count over n_time steps (0..n_time)."""
     return int(n_time).bit_length()

@@ -188,6 +188,7 @@ class SnnEs:
         can_mw = (self.ahead and L > 1 and (c.rows * c.T) % 256 == 0
                   and (self.split or min(c.dims[:-2]) > 64))
         self.mw = can_mw if member_weights is None else (bool(member_weights) and can_mw)
+        self.ro_counts = False  # set with the split buffers
         self.wm = None
         if self.mw:
             n_odd = c.chunk if c.accumulate > 1 and c.chunk % 2 else 0
@@ -250,10 +251,17 @@ class SnnEs:
             self.npl = K.count_planes(c.T)
             self.cpl = torch.empty((M, self.npl, K.fmt_width(FMT_BITS, c.dims[-2])),
                                    dtype=torch.int64, device=device)
-            self.ylog = torch.empty((1, M * self.npl, c.dims[-1]), dtype=torch.float32,
-                                    device=device)
-            self.plane_w = torch.tensor([2.0 ** p / c.T for p in range(self.npl)],
-                                        dtype=torch.float32, device=device).view(1, -1, 1)
+            # a narrow readout reads the count planes directly, its member
+            # weights formed per pair in LDS (hses_perturbed_readout_counts);
+            # otherwise the factored split product on the planes' bit rows
+            self.ro_counts = c.dims[-1] <= 32 and c.dims[-2] <= 128 and c.rows <= 128
+            if self.ro_counts:
+                self.img_x[-1] = None  # the readout's draw is the record alone
+            else:
+                self.ylog = torch.empty((1, M * self.npl, c.dims[-1]), dtype=torch.float32,
+                                        device=device)
+                self.plane_w = torch.tensor([2.0 ** p / c.T for p in range(self.npl)],
+                                            dtype=torch.float32, device=device).view(1, -1, 1)
 
     # -- forward -------------------------------------------------------------
     def spikes_tm(self, l):
@@ -322,11 +330,17 @@ class SnnEs:
         c = self.cfg
         if self.split:
             img = self._draw(self.L - 1, epoch, lo)
-            x = self.cpl.view(1, self.M * self.npl, -1)
-            K.perturbed_linear(x, self.W[-1], c.keys[-1], c.rank, c.sigma, epoch, c.noise_reuse,
-                               lo, c.chunk, c.rows * self.npl, x_fmt=FMT_BITS, n_time=1,
-                               math=MATH_F32X, out=self.ylog, rec=self.rec[-1], img=img)
-            torch.sum(self.ylog.view(self.M, self.npl, -1) * self.plane_w, 1, out=self.logits)
+            if self.ro_counts:
+                K.readout_counts(self.cpl, self.W[-1], c.rank, c.sigma, lo, c.chunk, c.rows, c.T,
+                                 self.rec[-1], out=self.logits)
+            else:
+                x = self.cpl.view(1, self.M * self.npl, -1)
+                K.perturbed_linear(x, self.W[-1], c.keys[-1], c.rank, c.sigma, epoch,
+                                   c.noise_reuse, lo, c.chunk, c.rows * self.npl, x_fmt=FMT_BITS,
+                                   n_time=1, math=MATH_F32X, out=self.ylog, rec=self.rec[-1],
+                                   img=img)
+                torch.sum(self.ylog.view(self.M, self.npl, -1) * self.plane_w, 1,
+                          out=self.logits)
             self._rec_at[-1] = (epoch, lo)
             labels = self.labels[lo * c.rows:(lo + c.chunk) * c.rows]
             return K.member_fitness(self.logits, labels, c.chunk, c.rows, c.reward,
@@ -350,10 +364,11 @@ class SnnEs:
         c = self.cfg
         a, b = self.W[l].shape
         img = self.img_x if self.split else self.img
-        mw = self.mw and l < self.L - 1
+        # the record alone: member weights, or the readout on count planes
+        bare = (self.mw and l < self.L - 1) or (self.ro_counts and l == self.L - 1)
         K.pair_factors(c.keys[l], c.rank, c.sigma, epoch, c.noise_reuse, lo, c.chunk, a, b,
-                       self.rec[l] if rec is None else rec, None if mw else img[l],
-                       split=self.split and not mw)
+                       self.rec[l] if rec is None else rec, None if bare else img[l],
+                       split=self.split and not bare)
 
     def _next_forward(self, epoch, lo):
         """The (epoch, lo) a training loop runs after this forward."""

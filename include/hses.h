@@ -413,6 +413,26 @@ int hses_perturbed_linear_lif_counts_pre_x(
     void *d_work, size_t work_bytes, const float *d_rec, size_t rec_bytes, const uint16_t *d_img,
     size_t img_bytes, void *stream);
 
+/* The readout (snn.rs:274-280: logits = rate W^T through do_mm,
+ * eggroll.rs:419-446) on the count planes of
+ * hses_perturbed_linear_lif_counts_pre_x / hses_perturbed_linear_lif_mw: for
+ * every row of members [tid_lo, tid_lo + n), with rate = sum_p 2^p plane_p /
+ * n_time,
+ *     d_y row = rate (W + sign_m (sigma / sqrt(rank)) A_m B_m^T)^T,
+ * A_m, B_m read from the factor record of the (a, b) layer (written by
+ * hses_pair_factors or hses_pair_factors_x, with or without an image).  Each
+ * pair's member weights are formed in fp32 in LDS and the rows' counts are
+ * decoded from the planes, so nothing is materialised: the reference's
+ * factored product reassociated (a no-counterpart form for narrow readouts).
+ * a <= 32, b <= 128, rows_per_member <= 128, n_time a power of two <= 16,
+ * rank a multiple of 16 in [32, 128], sigma != 0; counts_stride (uint64
+ * words between rows) >= P * ceil(b/64), P = log2(n_time) + 1. */
+int hses_perturbed_readout_counts(const uint64_t *d_counts, int64_t counts_stride,
+                                  int32_t n_time, const float *d_W, int32_t a, int32_t b,
+                                  int32_t rank, float sigma, int32_t tid_lo, int32_t n,
+                                  int32_t rows_per_member, const float *d_rec, size_t rec_bytes,
+                                  float *d_y, int64_t y_stride, void *stream);
+
 /* ---- member weights ------------------------------------------------------
  * The same perturbed product formed per member instead of factored: with R
  * rows per member, y_m = x (W + sign_m (sigma / sqrt(r)) A_m B_m^T)^T costs

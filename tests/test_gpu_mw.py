@@ -241,3 +241,53 @@ def test_snn_steps_on_member_weights(hses_gpu, extra):
         for l in range(es_f.L):
             err = (es_m.grads[l] - es_f.grads[l]).abs().max().item()
             assert err <= 5e-2 * es_f.grads[l].abs().max().item(), f"layer {l} gradient"
+
+
+def pack_planes(counts, P, b, spare=0):
+    """(M, b) counts -> (M, P + spare, words) uint64 bit planes (bit n of plane p =
+    bit p of count n); spare plane rows filled with ones (must be ignored)."""
+    M, wb = counts.shape[0], (b + 63) // 64
+    out = np.zeros((M, P + spare, wb), np.uint64)
+    out[:, P:] = np.uint64(2**64 - 1)
+    for p in range(P):
+        bits = ((counts >> p) & 1).astype(np.uint64)
+        for c in range(b):
+            out[:, p, c // 64] |= bits[:, c] << np.uint64(c % 64)
+    return out
+
+
+@pytest.mark.parametrize("a,b,r,n,tid_lo,rows,T", [
+    (10, 128, 128, 6, 1, 64, 16),   # the C3 readout shape; half pairs at both ends
+    (10, 128, 128, 8, 0, 64, 16),
+    (32, 100, 48, 5, 2, 20, 8),     # ragged input width, odd count, rank 48
+    (3, 64, 32, 2, 0, 128, 1),      # one plane, the most rows per member
+])
+def test_readout_counts(hses_gpu, a, b, r, n, tid_lo, rows, T):
+    # hses_perturbed_readout_counts against float64: rate (W + A_m B_m^T)^T
+    # with rate = count / T decoded from the planes
+    rng = np.random.default_rng(a + b + r + n + rows)
+    sigma = 0.05
+    W = (rng.standard_normal((a, b)) / np.sqrt(b)).astype(np.float32)
+    Wd = torch.from_numpy(W).cuda()
+    rec = record(a, b, r, sigma, tid_lo, n)
+    M, P = n * rows, K.count_planes(T)
+    counts = rng.integers(0, T + 1, (M, b))
+    cpl = torch.from_numpy(pack_planes(counts, P, b, spare=1).view(np.int64)).cuda()
+    got = K.readout_counts(cpl, Wd, r, sigma, tid_lo, n, rows, T, rec).cpu().numpy()
+    Wm, S, _, _ = reference_weights(W, a, b, r, sigma, tid_lo, n)
+    rate = counts.astype(np.float64) / T
+    for m in range(n):
+        sl = slice(m * rows, (m + 1) * rows)
+        ref = rate[sl] @ Wm[m].T
+        scale = rate[sl] @ S[m].T + 1e-30
+        err = np.abs(got[sl] - ref) / scale
+        assert err.max() <= 4e-6, f"member {m}: err {err.max():.2e} of sum|terms|"
+
+
+def test_readout_counts_rejects(hses_gpu):
+    a, b, r, n = 40, 128, 32, 2  # a > 32
+    rec = record(a, b, r, 0.05, 0, n)
+    W = torch.zeros(a, b, device="cuda")
+    cpl = torch.zeros((n * 4, 5, 2), dtype=torch.int64, device="cuda")
+    with pytest.raises(HsesError, match="a <= 32"):
+        K.readout_counts(cpl, W, r, 0.05, 0, n, 4, 16, rec)
