@@ -33,13 +33,13 @@ PEAK_HBM_GBPS = 8000.0
 # HBM bytes per launch of fc1's GEMM on member weights (k_mw_bits), from two rocprofv3 PMC runs
 # of `python3 -m hyperscalees_amd.profile_fc1` (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0, factors
 # from a 1 GiB copy in the same process; profiles/fc1_c3_traffic.md), keyed by (math, member
-# weights).  Measured on the k_mw_bits source of commit 024c4e3 (unchanged since); refreshed
-# whenever the kernel changes, and the bench line names the source it was measured on.
+# weights).  Measured on the k_mw_bits source of commit 821b0d8; refreshed whenever the kernel
+# changes, and the bench line names the source it was measured on.
 FC1_TRAFFIC = {
-    ("f32x", True): (4.528e9, "rocprofv3 PMC of profile_fc1, k_mw_bits of commit 024c4e3: "
-                              "4.393e9 B read + 0.134e9 B written"),
-    ("bf16", True): (2.760e9, "rocprofv3 PMC of profile_fc1 --math bf16, k_mw_bits of commit "
-                              "024c4e3: 2.626e9 B read + 0.134e9 B written"),
+    ("f32x", True): (4.522e9, "rocprofv3 PMC of profile_fc1, k_mw_bits of commit 821b0d8: "
+                              "4.388e9 B read + 0.134e9 B written"),
+    ("bf16", True): (2.769e9, "rocprofv3 PMC of profile_fc1 --math bf16, k_mw_bits of commit "
+                              "821b0d8: 2.635e9 B read + 0.134e9 B written"),
 }
 
 
