@@ -243,7 +243,8 @@ __global__ __launch_bounds__(R_MAXT) void k_es_rows(UpdParams P, RowTiles G) {
     extern __shared__ __align__(16) unsigned char smem[];
     BmTables* tabs = reinterpret_cast<BmTables*>(smem);
     const int32_t at = G.at, bt = G.bt, rows = at + bt;
-    uint16_t* buf0 = reinterpret_cast<uint16_t*>(smem + align_up16(sizeof(BmTables)));
+    // the record form draws nothing: no generator tables in LDS
+    uint16_t* buf0 = reinterpret_cast<uint16_t*>(smem + (REC ? 0 : align_up16(sizeof(BmTables))));
     // halves per buffer: A rows, B rows, then one row shared by the idle
     // threads (written, never read)
     const int32_t bufsz = (rows + 1) * R_HP;
@@ -659,7 +660,8 @@ static int es_update_impl(const float* d_f, int32_t n, int32_t tid_lo, uint64_t 
                 if (cnt == 0) continue;
                 RowTiles G{at, bt, o0, g == 0 ? 0 : nfull * btm};
                 const int32_t threads = (at + bt + 63) / 64 * 64;
-                const size_t lds = align_up16(sizeof(BmTables)) + (size_t)2 * (at + bt + 1) * R_HP * 2;
+                const size_t lds = (rec ? 0 : align_up16(sizeof(BmTables))) +
+                                   (size_t)2 * (at + bt + 1) * R_HP * 2;
                 const int32_t nw = threads / 64, nct = (bt + 15) / 16;
                 const int32_t ct = (nct + nw - 1) / nw;
                 auto launch = [&](auto kern) -> int {
