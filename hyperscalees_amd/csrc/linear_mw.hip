@@ -845,8 +845,8 @@ int launch_linear_mw(LinParams& P, DeviceState* st, hipStream_t s, const LifOut*
 //
 // The SNN readout (snn.rs:274-280: logits = rate W^T through do_mm,
 // eggroll.rs:419-446) for a layer with few outputs and rows per member: one
-// workgroup per pair copies the pair's factor record (r rank rows of a + b
-// values, one contiguous block) into LDS, forms
+// workgroup per pair stages the pair's A rows (r x a) in LDS, streams its B
+// values from the factor record (coalesced over the inputs), forms
 //   W_m[k][n] = W[k][n] + sign_m sum_c A'[k][c] B[n][c],  A' = A (sigma/sqrt(r))
 // for both members (fp32 sums over c, one thread per (k, n) set), and then
 // for every sample row of the two members decodes its spike counts from the
@@ -858,7 +858,7 @@ int launch_linear_mw(LinParams& P, DeviceState* st, hipStream_t s, const LifOut*
 constexpr int RO_THREADS = 256, RO_KMAX = 32, RO_BMAX = 128;
 // KQ: outputs in runs of 4 (a <= 4 KQ), so every output loop is unrolled
 template <int KQ>
-__global__ __launch_bounds__(RO_THREADS, 2) void k_readout_counts(
+__global__ __launch_bounds__(RO_THREADS) void k_readout_counts(
     const uint64_t* __restrict__ cpl, int64_t cstride, int32_t T, int32_t P,
     const float* __restrict__ W, int32_t a, int32_t b, int32_t r, float bs, int32_t tid_lo,
     int32_t n, int32_t pair_lo, int32_t rpm, const float* __restrict__ rec,
@@ -886,75 +886,48 @@ __global__ __launch_bounds__(RO_THREADS, 2) void k_readout_counts(
         }
     };
     load_planes(tid, plo0, phi0);
-    // 1. the pair's record block -> LDS ([c][j], row pitch a + b), in batches
-    // of loads that are all in flight before their stores
-    const int32_t total = r * ab;
-    if (((uintptr_t)rp % 16) == 0) {
-        const int32_t n4 = total / 4;
-        constexpr int CB = 9;
-        for (int32_t base = 0; base < n4; base += CB * RO_THREADS) {
-            f32x4 v[CB];
-#pragma unroll
-            for (int j = 0; j < CB; ++j) {
-                const int32_t i = base + j * RO_THREADS + tid;
-                if (i < n4) v[j] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(rp) + i);
-            }
-#pragma unroll
-            for (int j = 0; j < CB; ++j) {
-                const int32_t i = base + j * RO_THREADS + tid;
-                if (i < n4) *reinterpret_cast<f32x4*>(ro_lds + 4 * i) = v[j];
-            }
-        }
-        for (int32_t i = 4 * n4 + tid; i < total; i += RO_THREADS) ro_lds[i] = rp[i];
-    } else {
-        for (int32_t i = tid; i < total; i += RO_THREADS) ro_lds[i] = rp[i];
+    // 1. the pair's A rows -> LDS as As[c][KP] (zero past a)
+    constexpr int KP = 4 * KQ;
+    float* As = ro_lds;
+    for (int32_t idx = tid; idx < r * KP; idx += RO_THREADS) {
+        const int32_t c = idx / KP, k = idx - c * KP;
+        As[idx] = k < a ? rp[(size_t)c * ab + b + k] : 0.0f;
     }
     __syncthreads();
     // 2. d[k][n] = sum_c A[k][c] B[n][c]: thread t takes input n = t % b, all
-    // outputs k < 4 KQ (those past a are dropped), and the ranks c = t / b,
-    // t / b + G, ... (G = 256 / b groups, summed through LDS afterwards); each
-    // rank row's values are read one row ahead of their products
-    constexpr int KP = 4 * KQ;
+    // outputs k < KP, and the ranks c = t / b, t / b + G, ... (G = 256 / b
+    // groups, summed through LDS afterwards); B values straight from the
+    // record (coalesced over n), a batch of ranks' loads in flight at once
     const int32_t G = RO_THREADS / b;  // >= 2 (b <= 128)
     const int32_t nn = tid % b, cg = tid / b;
     float d[KP];
 #pragma unroll
     for (int k = 0; k < KP; ++k) d[k] = 0.0f;
     if (cg < G) {
-        if (ab % 2 == 0 && b % 2 == 0) {
-            // A pairs (k, k + 1) 8-byte aligned; reads past a stay inside the
-            // block's slack
-            float bc = 0.0f, bn = 0.0f;
-            float2 ac[KP / 2], an[KP / 2];
-            auto ld = [&](int32_t c, float& bv, float2 (&av)[KP / 2]) {
-                const float* row = ro_lds + c * ab;
-                bv = row[nn];
+        constexpr int CB = 16;
+        for (int32_t c0 = cg; c0 < r; c0 += CB * G) {
+            float bv[CB];
 #pragma unroll
-                for (int q = 0; q < KP / 2; ++q) av[q] = *reinterpret_cast<const float2*>(row + b + 2 * q);
-            };
-            if (cg < r) ld(cg, bc, ac);
-            for (int32_t c = cg; c < r; c += G) {
-                if (c + G < r) ld(c + G, bn, an);
-#pragma unroll
-                for (int q = 0; q < KP / 2; ++q) {
-                    d[2 * q] = __builtin_fmaf(ac[q].x, bc, d[2 * q]);
-                    d[2 * q + 1] = __builtin_fmaf(ac[q].y, bc, d[2 * q + 1]);
-                }
-                bc = bn;
-#pragma unroll
-                for (int q = 0; q < KP / 2; ++q) ac[q] = an[q];
+            for (int q = 0; q < CB; ++q) {
+                const int32_t c = c0 + q * G;
+                bv[q] = c < r ? __builtin_nontemporal_load(rp + (size_t)c * ab + nn) : 0.0f;
             }
-        } else {
-            for (int32_t c = cg; c < r; c += G) {
-                const float* row = ro_lds + c * ab;
-                const float bv = row[nn];
 #pragma unroll
-                for (int k = 0; k < KP; ++k) d[k] = __builtin_fmaf(row[b + min(k, a - 1)], bv, d[k]);
+            for (int q = 0; q < CB; ++q) {
+                const int32_t c = min(c0 + q * G, r - 1);  // past r: bv = 0
+                const float* ar = As + c * KP;
+#pragma unroll
+                for (int k4 = 0; k4 < KP; k4 += 4) {
+                    const float4 a4 = *reinterpret_cast<const float4*>(ar + k4);
+                    d[k4] = __builtin_fmaf(a4.x, bv[q], d[k4]);
+                    d[k4 + 1] = __builtin_fmaf(a4.y, bv[q], d[k4 + 1]);
+                    d[k4 + 2] = __builtin_fmaf(a4.z, bv[q], d[k4 + 2]);
+                    d[k4 + 3] = __builtin_fmaf(a4.w, bv[q], d[k4 + 3]);
+                }
             }
         }
     }
-    __syncthreads();  // the record block is no longer read
-    float* part = ro_lds;  // [group][n][KP]
+    float* part = ro_lds + r * KP;  // [group][n][KP]
     if (cg < G) {
 #pragma unroll
         for (int k = 0; k < KP; ++k) part[(cg * b + nn) * KP + k] = d[k];
@@ -970,7 +943,7 @@ __global__ __launch_bounds__(RO_THREADS, 2) void k_readout_counts(
     // (sigma/sqrt(r)) applied to the sum (the forward scales A; the product
     // is the same up to rounding)
     const int32_t kp4 = KP;
-    float* Wm = ro_lds;
+    float* Wm = ro_lds + r * KP;
     if (cg == 0) {
 #pragma unroll
         for (int k = 0; k < KP; ++k) {
@@ -1044,10 +1017,10 @@ __global__ __launch_bounds__(RO_THREADS, 2) void k_readout_counts(
 }
 
 size_t readout_counts_lds(int32_t a, int32_t b, int32_t r) {
-    // the record block plus the slack its last row's A reads run into; the
-    // partials (G x b x 4 KQ) and member weights (2 x b x 4 KQ) reuse it
+    // A rows [r][4 KQ], then the partials [G][b][4 KQ] (G b <= 256), which the
+    // member weights [2][b][4 KQ] reuse
     const size_t kp4 = (size_t)((a + 3) & ~3);
-    return std::max((size_t)r * (a + b) + kp4, (size_t)(RO_THREADS / b) * b * kp4) * 4;
+    return ((size_t)r + RO_THREADS) * kp4 * 4;
 }
 
 int launch_readout_counts(const uint64_t* cpl, int64_t cstride, int32_t T, const float* W,
