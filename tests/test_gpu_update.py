@@ -94,3 +94,32 @@ def test_es_update_noise_reuse(hses_gpu):
     ref = oracle_grad(0.3, 4, fit, 9, 13, epoch=7, nreuse=3)
     g = gpu_grad(hses_gpu, 0.3, 4, fit, 9, 13, 1.0, epoch=7, nreuse=3).cpu().numpy()
     assert_close(g, ref)
+
+
+# Split-count sweep of the rank-128 contraction (the C3 layers' k_es_rows), as
+# the reference sweeps its fused einsum's K-chunk count against an f64 CPU
+# value (einsum_pair_fused_oxide.rs:758-795).  At the fc1 shape the split count
+# is min(512, pairs / 8): the member counts below give 1, 2, 3, 16, 128 and 511
+# splits (48 and 8190 members: pair ranges of unequal length); fc2 and the
+# readout at the benched population.  Both forms: the normals drawn in-kernel
+# and the factor record of a forward's draw.
+SWEEP = [(128, 784, 16), (128, 784, 32), (128, 784, 48), (128, 784, 256), (128, 784, 2048),
+         (128, 784, 8190), (128, 128, 8192), (10, 128, 8192)]
+
+
+@pytest.mark.parametrize("a,b,n", SWEEP)
+def test_es_update_split_sweep_rank128(hses_gpu, a, b, n):
+    r, sigma = 128, 0.02
+    fit = np.random.default_rng(n + a).standard_normal(n).astype(np.float32)
+    ref = O.lora_grad_f64(sigma, KEY, r, 0, fit, a, b, nthreads=16).astype(np.float64)
+    scale = np.float32(-math.sqrt(n) / n)
+    g = gpu_grad(hses_gpu, sigma, r, fit, a, b, scale).cpu().numpy()
+    assert_close(g, ref)
+    rec = hses_gpu.factor_record(a, b, r, 0, n)
+    hses_gpu.pair_factors(KEY, r, sigma, 0, 0, 0, n, a, b, rec, None)
+    ft = torch.from_numpy(fit).cuda()
+    gr = hses_gpu.es_update_rec(ft, 0, rec, r, sigma, a, b, scale).cpu().numpy()
+    torch.cuda.synchronize()
+    assert_close(gr, ref)
+    # the two forms run the same contraction on the same factors
+    assert np.array_equal(g, gr)
