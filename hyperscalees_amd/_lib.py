@@ -36,6 +36,11 @@ PROTOTYPES = {
     "hses_poisson_encode_planes": (ctypes.c_int, [c_vp, c_i64, c_vp, c_i64, c_i32, c_i64, c_i32,
                                                   c_u32, c_u32, c_u32, c_u32, c_vp, c_i32, c_i64,
                                                   c_i64, c_vp]),
+    "hses_poisson_pool_bytes": (c_size, [c_i64, c_i32]),
+    "hses_poisson_pool_prepare": (ctypes.c_int, [c_vp, c_i64, c_i32, c_i64, c_vp, c_size, c_vp]),
+    "hses_poisson_encode_pool": (ctypes.c_int, [c_vp, c_size, c_i64, c_i32, c_vp, c_i64, c_i32,
+                                                c_u32, c_u32, c_u32, c_u32, c_vp, c_i64, c_i64,
+                                                c_vp]),
     "hses_spike_rate": (ctypes.c_int, [c_vp, c_i32, c_i64, c_i32, c_i64, c_i32, c_vp, c_vp]),
     "hses_lif_scan": (ctypes.c_int, [c_vp, c_vp, c_i32, c_i64, c_i32, c_i64, c_f32, c_f32, c_vp,
                                      c_i32, c_i64, c_vp, c_vp]),

@@ -305,6 +305,158 @@ static size_t poisson_sparse_lds(int32_t in_dim) {
     return 4 * words * 96 * 4;  // 4 waves, each a u32 pattern and a u16 list entry per element
 }
 
+// ---- prepared pools ---------------------------------------------------------
+//
+// A training loop encodes batches gathered from one fixed pool of probability
+// rows (accumulate_train.rs:726-735: train_img.select(0, idx), then
+// poisson_encode_fused).  k_poisson_sparse classifies every element of every
+// gathered row again (its threshold, whether it can fire, the compaction):
+// about as many vector instructions as the streams themselves.  A prepared
+// pool holds that classification once per pool row:
+//   counts  int32 [pool_rows][2]: n_act, n_sat
+//   K       u32 [pool_rows][cap]: thresholds K(p) of the active elements
+//           (0 < K < 2^23), slots [0, n_act)
+//   col     u16 [pool_rows][cap]: their columns in slots [0, n_act); the
+//           saturated elements' (K(p) = 2^23: every step fires) in slots
+//           [cap - n_sat, cap)
+// Elements with K(p) = 0 (p <= 0, NaN, or too small for any u) never fire and
+// are left out.  cap = in_dim rounded up to 8 (16-byte aligned rows).
+__host__ __device__ constexpr size_t pool_align16(size_t x) { return (x + 15) & ~(size_t)15; }
+
+struct PoolLayout {
+    int32_t cap;
+    size_t off_k, off_col, bytes;
+    __host__ __device__ PoolLayout(int64_t pool_rows, int32_t in_dim) {
+        cap = (in_dim + 7) & ~7;
+        off_k = pool_align16((size_t)pool_rows * 8);
+        off_col = off_k + pool_align16((size_t)pool_rows * cap * 4);
+        bytes = off_col + pool_align16((size_t)pool_rows * cap * 2);
+    }
+};
+
+// One wave per pool row: the row's thresholds, compacted by ballot (active
+// from the front, saturated from the back, both in column order).
+__global__ __launch_bounds__(256) void k_poisson_pool_prepare(const float* __restrict__ p,
+                                                              int64_t pool_rows, int32_t in_dim,
+                                                              int64_t p_stride,
+                                                              unsigned char* __restrict__ pool) {
+    const PoolLayout lay(pool_rows, in_dim);
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= pool_rows) return;  // whole wave exits together
+    const float* pr = p + row * p_stride;
+    uint32_t* kr = reinterpret_cast<uint32_t*>(pool + lay.off_k) + row * lay.cap;
+    uint16_t* cr = reinterpret_cast<uint16_t*>(pool + lay.off_col) + row * lay.cap;
+    int32_t na = 0, ns = 0;
+    for (int32_t c0 = 0; c0 < in_dim; c0 += 64) {
+        const int32_t col = c0 + lane;
+        const uint32_t K = col < in_dim ? poisson_threshold(pr[col]) : 0u;
+        const bool sat = K >= 8388608u, act = K > 0u && !sat;
+        const uint64_t am = __ballot(act), sm = __ballot(sat);
+        const uint32_t below_a = __builtin_amdgcn_mbcnt_hi((uint32_t)(am >> 32),
+                                                           __builtin_amdgcn_mbcnt_lo((uint32_t)am, 0u));
+        const uint32_t below_s = __builtin_amdgcn_mbcnt_hi((uint32_t)(sm >> 32),
+                                                           __builtin_amdgcn_mbcnt_lo((uint32_t)sm, 0u));
+        if (act) {
+            kr[na + (int32_t)below_a] = K;
+            cr[na + (int32_t)below_a] = (uint16_t)col;
+        }
+        if (sat) cr[lay.cap - 1 - (ns + (int32_t)below_s)] = (uint16_t)col;
+        na += (int32_t)__popcll(am);
+        ns += (int32_t)__popcll(sm);
+    }
+    if (lane == 0) reinterpret_cast<int2*>(pool)[row] = make_int2(na, ns);
+}
+
+// Bit-packed Poisson of rows gathered from a prepared pool: one wave per
+// output row.  The row's pattern slots in LDS start at zero; the saturated
+// columns get the all-ones pattern; each active element runs its xorshift32
+// stream (the same stream, seed and compare as k_poisson_sparse's phase B)
+// with the next element's column and threshold already loaded; then the
+// 64 x 64 bit transposes of k_poisson_sparse's phase C store the words.
+template <int T>
+__global__ __launch_bounds__(256) void k_poisson_pool(const unsigned char* __restrict__ pool,
+                                                      int64_t pool_rows,
+                                                      const int32_t* __restrict__ prow,
+                                                      int64_t rows, int32_t in_dim, uint32_t mix,
+                                                      uint64_t* __restrict__ out,
+                                                      int64_t out_stride, int64_t plane) {
+    static_assert(T >= 1 && T <= 32 && (T & (T - 1)) == 0, "T must be a power of two <= 32");
+    constexpr int WPT = 64 / T;
+    constexpr uint32_t ALL = T == 32 ? 0xffffffffu : ((1u << T) - 1u);
+    extern __shared__ __align__(16) unsigned char psm[];
+    const PoolLayout lay(pool_rows, in_dim);
+    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int32_t words = (in_dim + 63) >> 6;
+    uint32_t* pat = reinterpret_cast<uint32_t*>(psm) + (size_t)wv * (words * 64);
+    const int64_t row = (int64_t)blockIdx.x * 4 + wv;
+    if (row >= rows) return;  // whole wave exits together
+    const int64_t src = prow ? (int64_t)prow[row] : row;
+    const bool src_ok = src >= 0 && src < pool_rows;
+    const int64_t sr = src_ok ? src : 0;
+    const int2 cnt = src_ok ? reinterpret_cast<const int2*>(pool)[sr] : make_int2(0, 0);
+    const uint32_t* kr = reinterpret_cast<const uint32_t*>(pool + lay.off_k) + sr * lay.cap;
+    const uint16_t* cr = reinterpret_cast<const uint16_t*>(pool + lay.off_col) + sr * lay.cap;
+    const uint32_t idx0 = (uint32_t)(row * in_dim);
+
+    for (int32_t i = lane; i < words * 16; i += 64) reinterpret_cast<uint4*>(pat)[i] = make_uint4(0, 0, 0, 0);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    for (int32_t e = lane; e < cnt.y; e += 64) pat[cr[lay.cap - 1 - e]] = ALL;
+    // streams of the active elements, the next element's loads in flight
+    int32_t e = lane;
+    uint32_t col = 0, K9 = 0;
+    if (e < cnt.x) {
+        col = cr[e];
+        K9 = kr[e] << 9;  // (x >> 9) < K  <=>  x < K * 2^9 for K < 2^23
+    }
+    for (; e < cnt.x; e += 64) {
+        const int32_t en = e + 64;
+        uint32_t coln = 0, K9n = 0;
+        if (en < cnt.x) {
+            coln = cr[en];
+            K9n = kr[en] << 9;
+        }
+        uint32_t x = 1000000007u * (idx0 + col) + mix + 0x9E3779B9u;
+        uint32_t pt = 0;
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            x ^= x << 13;
+            x ^= x >> 17;
+            x ^= x << 5;
+            asm("v_cmp_lt_u32 vcc, %1, %2\n\tv_addc_co_u32 %0, vcc, %0, %0, vcc"
+                : "+v"(pt)
+                : "v"(x), "v"(K9)
+                : "vcc");
+        }
+        pat[col] = __builtin_bitreverse32(pt) >> (32 - T);
+        col = coln;
+        K9 = K9n;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    const int32_t wi = lane / T, t = lane % T;
+    uint64_t* orow = out + (int64_t)t * plane + row * out_stride;
+    for (int32_t w0 = 0; w0 < words; w0 += WPT) {
+        uint32_t lo = 0, hi = 0;
+#pragma unroll
+        for (int i = 0; i < WPT; ++i) {
+            const int32_t wr = w0 + i < words ? w0 + i : words - 1;  // in bounds, masked below
+            const uint32_t v = w0 + i < words ? pat[wr * 64 + lane] : 0u;
+            if (i * T < 32)
+                lo |= v << (i * T);
+            else
+                hi |= v << (i * T - 32);
+        }
+        transpose64(lo, hi, lane);
+        if (w0 + wi < words) orow[w0 + wi] = ((uint64_t)hi << 32) | lo;
+    }
+}
+
 template <int FMT>
 __global__ __launch_bounds__(256) void k_lif(const float* __restrict__ cur,
                                              const float* __restrict__ v0, int32_t T, int64_t rows,
@@ -580,6 +732,72 @@ extern "C" int hses_poisson_encode(const float* d_p, int64_t p_rows, const int32
                                    int64_t out_stride, void* stream) {
     return hses_poisson_encode_planes(d_p, p_rows, d_rows, rows, in_dim, p_stride, T, s0, s1, s2, s3,
                                       d_out, fmt, out_stride, rows * out_stride, stream);
+}
+
+extern "C" size_t hses_poisson_pool_bytes(int64_t pool_rows, int32_t in_dim) {
+    if (pool_rows <= 0 || in_dim <= 0 || in_dim > 2048) return 0;
+    return PoolLayout(pool_rows, in_dim).bytes;
+}
+
+extern "C" int hses_poisson_pool_prepare(const float* d_p, int64_t pool_rows, int32_t in_dim,
+                                         int64_t p_stride, void* d_pool, size_t pool_bytes,
+                                         void* stream) {
+    HSES_REQUIRE(pool_rows >= 0 && in_dim >= 0, "negative size");
+    if (pool_rows == 0 || in_dim == 0) return HSES_OK;
+    HSES_REQUIRE(in_dim <= 2048, "in_dim > 2048");
+    HSES_REQUIRE(d_p && d_pool, "NULL pointer");
+    HSES_REQUIRE(p_stride >= in_dim, "p_stride < in_dim");
+    HSES_REQUIRE(reinterpret_cast<uintptr_t>(d_pool) % 16 == 0, "pool buffer not 16-byte aligned");
+    HSES_REQUIRE(pool_bytes >= PoolLayout(pool_rows, in_dim).bytes,
+                 "pool buffer smaller than hses_poisson_pool_bytes");
+    const int64_t blocks = (pool_rows + 3) / 4;
+    HSES_REQUIRE(blocks < (1ll << 31), "grid too large");
+    hipLaunchKernelGGL(k_poisson_pool_prepare, dim3((uint32_t)blocks), dim3(256), 0,
+                       (hipStream_t)stream, d_p, pool_rows, in_dim, p_stride,
+                       static_cast<unsigned char*>(d_pool));
+    HSES_CHECK_HIP(hipGetLastError());
+    return HSES_OK;
+}
+
+extern "C" int hses_poisson_encode_pool(const void* d_pool, size_t pool_bytes, int64_t pool_rows,
+                                        int32_t in_dim, const int32_t* d_rows, int64_t rows,
+                                        int32_t T, uint32_t s0, uint32_t s1, uint32_t s2,
+                                        uint32_t s3, uint64_t* d_out, int64_t out_stride,
+                                        int64_t out_plane, void* stream) {
+    HSES_REQUIRE(rows >= 0 && in_dim >= 0 && T >= 0 && pool_rows >= 0, "negative size");
+    if (rows == 0 || in_dim == 0 || T == 0) return HSES_OK;
+    HSES_REQUIRE(T <= 32 && (T & (T - 1)) == 0, "T must be a power of two <= 32");
+    HSES_REQUIRE(in_dim <= 2048, "in_dim > 2048");
+    HSES_REQUIRE(d_out && (d_pool || pool_rows == 0), "NULL pointer");
+    HSES_REQUIRE(pool_rows == 0 || pool_bytes >= PoolLayout(pool_rows, in_dim).bytes,
+                 "pool buffer smaller than hses_poisson_pool_bytes");
+    HSES_REQUIRE(reinterpret_cast<uintptr_t>(d_pool) % 16 == 0, "pool buffer not 16-byte aligned");
+    HSES_REQUIRE(d_rows || pool_rows >= rows, "pool_rows < rows without a row index");
+    HSES_REQUIRE(rows_layout_ok(fmt_row_units(HSES_FMT_BITS, in_dim), rows, T, out_stride, out_plane),
+                 "output rows overlap (out_stride too small, or time planes overlap)");
+    HSES_REQUIRE(rows * in_dim <= (int64_t)UINT32_MAX, "rows*in_dim exceeds the u32 index range");
+    const int64_t blocks = (rows + 3) / 4;
+    HSES_REQUIRE(blocks < (1ll << 31), "grid too large");
+    const uint32_t mix = s0 ^ s1 ^ s2 ^ s3;
+    const size_t lds = (size_t)4 * ((in_dim + 63) / 64) * 64 * 4;  // 4 waves, a u32 pattern per slot
+    const unsigned char* pl = static_cast<const unsigned char*>(d_pool);
+    hipStream_t s = (hipStream_t)stream;
+#define HSES_PPOOL(TV)                                                                          \
+    case TV:                                                                                    \
+        hipLaunchKernelGGL(k_poisson_pool<TV>, dim3((uint32_t)blocks), dim3(256), lds, s, pl,     \
+                           pool_rows, d_rows, rows, in_dim, mix, d_out, out_stride, out_plane); \
+        break;
+    switch (T) {
+        HSES_PPOOL(1)
+        HSES_PPOOL(2)
+        HSES_PPOOL(4)
+        HSES_PPOOL(8)
+        HSES_PPOOL(16)
+        HSES_PPOOL(32)
+    }
+#undef HSES_PPOOL
+    HSES_CHECK_HIP(hipGetLastError());
+    return HSES_OK;
 }
 
 extern "C" int hses_lif_scan(const float* d_cur, const float* d_v0, int32_t T, int64_t rows,

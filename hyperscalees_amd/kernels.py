@@ -128,6 +128,44 @@ def poisson_encode(p, T, seeds=(0, 0, 0, 0), fmt=FMT_F32, out=None, rows_index=N
     return out
 
 
+class PoissonPool:
+    """A pool of probability rows (pool_rows, in_dim) prepared once for
+    repeated bit-packed encodes of gathered rows (hses_poisson_pool_prepare):
+    per row the exact thresholds of the elements that can fire."""
+
+    def __init__(self, p):
+        _dev(p, torch.float32, "p")
+        self.rows, self.in_dim = p.shape
+        self.nbytes = int(_lib.load().hses_poisson_pool_bytes(self.rows, self.in_dim))
+        if self.nbytes == 0:
+            raise ValueError(f"no prepared pool for in_dim {self.in_dim} (at most 2048)")
+        self.buf = torch.empty(self.nbytes, dtype=torch.uint8, device=p.device)
+        _lib.call("hses_poisson_pool_prepare", _p(p), self.rows, self.in_dim, p.stride(0),
+                  _p(self.buf), self.nbytes, _stream())
+
+
+def poisson_encode_pool(pool, T, seeds=(0, 0, 0, 0), out=None, rows_index=None,
+                        time_inner=False):
+    """poisson_encode(p, T, seeds, FMT_BITS, out, rows_index, time_inner) on
+    the PoissonPool prepared from p: the same spikes."""
+    rows = pool.rows
+    if rows_index is not None:
+        _dev(rows_index, torch.int32, "rows_index")
+        rows = rows_index.numel()
+    units = fmt_width(FMT_BITS, pool.in_dim)
+    shape = (rows, T, units) if time_inner else (T, rows, units)
+    if out is None:
+        out = torch.empty(shape, dtype=_FMT_DTYPE[FMT_BITS], device=pool.buf.device)
+    _dev(out, _FMT_DTYPE[FMT_BITS], "out")
+    if tuple(out.shape) != shape:
+        raise ValueError(f"out has shape {tuple(out.shape)}, expected {shape}")
+    stride, plane = (T * units, units) if time_inner else (units, rows * units)
+    s0, s1, s2, s3 = (int(s) & 0xFFFFFFFF for s in seeds)
+    _lib.call("hses_poisson_encode_pool", _p(pool.buf), pool.nbytes, pool.rows, pool.in_dim,
+              _p(rows_index), rows, T, s0, s1, s2, s3, _p(out), stride, plane, _stream())
+    return out
+
+
 def spike_rate(spikes, fmt, h, out=None):
     """(T, rows, units) spikes in `fmt` -> (rows, h) fp32 mean over T."""
     _dev(spikes, _FMT_DTYPE[fmt], "spikes")

@@ -118,12 +118,20 @@ class SnnEs:
     """Device-resident SNN-MLP population evaluation and ES update."""
 
     def __init__(self, cfg, weights, pool, pool_labels, index, device="cuda", fused=None,
-                 record=None, ahead=None, member_weights=None, overlap=None):
+                 record=None, ahead=None, member_weights=None, overlap=None, prepared_pool=None):
         self.cfg = cfg
         c = cfg
         self.dev = device
         self.W = [torch.as_tensor(w, dtype=torch.float32).to(device).contiguous() for w in weights]
         self.pool = torch.as_tensor(pool, dtype=torch.float32).to(device).contiguous()
+        # The pool stays fixed across steps: the thresholds of its elements
+        # that can fire are prepared once (hses_poisson_pool_prepare), and each
+        # batch's encode reads those instead of classifying the gathered
+        # probabilities again (the same spikes).
+        can_pp = (str(device).startswith("cuda") and 1 <= c.T <= 32 and c.T & (c.T - 1) == 0
+                  and self.pool.shape[1] <= 2048)
+        use_pp = can_pp if prepared_pool is None else (bool(prepared_pool) and can_pp)
+        self.ppool = K.PoissonPool(self.pool) if use_pp else None
         idx = torch.as_tensor(index, dtype=torch.int32).to(device).contiguous()
         self.index = idx
         self.labels = torch.as_tensor(pool_labels, dtype=torch.int32).to(device)[idx.long()].contiguous()
@@ -281,6 +289,10 @@ class SnnEs:
     def poisson(self, lo=0):
         c = self.cfg
         rows = slice(lo * c.rows, (lo + c.chunk) * c.rows)
+        if self.ppool is not None:
+            K.poisson_encode_pool(self.ppool, c.T, self.chunk_seeds(lo), out=self.spk[0],
+                                  rows_index=self.index[rows], time_inner=self.time_inner)
+            return
         K.poisson_encode(self.pool, c.T, self.chunk_seeds(lo), FMT_BITS, out=self.spk[0],
                          rows_index=self.index[rows], time_inner=self.time_inner)
 

@@ -161,6 +161,27 @@ int hses_poisson_encode_planes(const float *d_p, int64_t p_rows, const int32_t *
                                uint32_t s0, uint32_t s1, uint32_t s2, uint32_t s3, void *d_out,
                                int32_t fmt, int64_t out_stride, int64_t out_plane, void *stream);
 
+/* Prepared pools: the batch gather + poisson_encode_fused of the training loop
+ * (accumulate_train.rs:726-735: train_img.select(0, idx), then
+ * poisson_encode_fused_oxide.rs:61-106) for a pool that stays fixed across
+ * steps.  hses_poisson_pool_prepare classifies each of the pool's pool_rows
+ * rows of in_dim probabilities (row stride p_stride floats) once: the exact
+ * threshold K(p) of every element that can fire, compacted per row, into
+ * d_pool (pool_bytes >= hses_poisson_pool_bytes(pool_rows, in_dim), 16-byte
+ * aligned; 0 for unsupported sizes: in_dim > 2048).
+ * hses_poisson_encode_pool then writes, for output row i, the bit-packed
+ * spikes of pool row d_rows[i] (or row i with d_rows NULL; an index outside
+ * [0, pool_rows) encodes as an all-zero row) at t*out_plane + i*out_stride
+ * words: the same streams, seeds and spikes as hses_poisson_encode_planes with
+ * HSES_FMT_BITS on the pool's probabilities, for T a power of two <= 32. */
+size_t hses_poisson_pool_bytes(int64_t pool_rows, int32_t in_dim);
+int hses_poisson_pool_prepare(const float *d_p, int64_t pool_rows, int32_t in_dim,
+                              int64_t p_stride, void *d_pool, size_t pool_bytes, void *stream);
+int hses_poisson_encode_pool(const void *d_pool, size_t pool_bytes, int64_t pool_rows,
+                             int32_t in_dim, const int32_t *d_rows, int64_t rows, int32_t T,
+                             uint32_t s0, uint32_t s1, uint32_t s2, uint32_t s3, uint64_t *d_out,
+                             int64_t out_stride, int64_t out_plane, void *stream);
+
 /* Mean firing rate over time (snn.rs:274, spikes.mean_dim(0)):
  * d_rate[row][c] = (number of spikes of (row, c) over T) / T, spikes in `fmt`
  * with row stride spk_stride (units) and time planes rows*spk_stride apart. */

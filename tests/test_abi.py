@@ -191,3 +191,23 @@ def test_empty_inputs_are_no_ops_without_a_gpu():
                                 NULL) == 0
     assert lib.hses_member_fitness(NULL, 10, NULL, 0, 4, 1, NULL, NULL, NULL) == 0
     assert lib.hses_combine_affine(NULL, NULL, NULL, 8, 0, NULL, NULL) == 0
+
+
+def test_poisson_pool_validation_without_a_gpu():
+    lib = _lib.load()
+    assert lib.hses_poisson_pool_bytes(10, 3000) == 0
+    assert lib.hses_poisson_pool_bytes(0, 784) == 0
+    # 10 rows of 784: counts (80 B), thresholds (10 x 784 x 4), columns (10 x 784 x 2)
+    assert lib.hses_poisson_pool_bytes(10, 784) == 80 + 31360 + 15680
+    v = ctypes.c_void_p(256)
+    nb = lib.hses_poisson_pool_bytes(10, 784)
+    _expect_invalid("hses_poisson_encode_pool", v, nb, 10, 784, NULL, 10, 12, 0, 0, 0, 0, v,
+                    13 * 12, 13, NULL)  # T not a power of two
+    _expect_invalid("hses_poisson_encode_pool", v, nb - 16, 10, 784, NULL, 10, 16, 0, 0, 0, 0, v,
+                    13 * 16, 13, NULL)  # pool buffer too small
+    _expect_invalid("hses_poisson_encode_pool", v, nb, 10, 784, NULL, 11, 16, 0, 0, 0, 0, v,
+                    13 * 16, 13, NULL)  # more rows than the pool without an index
+    _expect_invalid("hses_poisson_encode_pool", v, nb, 10, 784, NULL, 10, 16, 0, 0, 0, 0, v,
+                    13 * 16, 12, NULL)  # time planes overlap
+    _expect_invalid("hses_poisson_pool_prepare", v, 10, 784, 700, v, nb, NULL)  # p_stride
+    _expect_invalid("hses_poisson_pool_prepare", v, 10, 784, 784, ctypes.c_void_p(264), nb, NULL)

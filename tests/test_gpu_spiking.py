@@ -235,3 +235,80 @@ def test_solver_step(hses_gpu, kind):
         if kind != SGD:
             np.testing.assert_allclose(mt.cpu().numpy(), rm, rtol=1e-6, atol=1e-8)
         p, m, v = ref, rm, rv
+
+
+def special_pool(rng, rows, d):
+    """Sparse intensities with every class of element: exact zeros, negative,
+    NaN, too small to fire, exact and over-one saturation, just below one."""
+    p = sparse_intensities(rng, rows, d)
+    specials = np.array([0.0, -0.5, np.nan, 1e-9, 1e-7, 1.0, 2.0, np.inf,
+                         np.nextafter(np.float32(1.0), np.float32(0.0)), 0.5], np.float32)
+    mask = rng.random((rows, d)) < 0.1
+    p[mask] = rng.choice(specials, int(mask.sum()))
+    p[0, :] = 1.0        # a fully saturated row
+    if rows > 1:
+        p[1, :] = 0.0    # a silent row
+    return p
+
+
+@pytest.mark.parametrize("pool_rows,d,T,time_inner", [
+    (300, 784, 16, True),    # the C3 input: 784 = 12 words + 16 columns
+    (300, 784, 16, False),
+    (40, 100, 8, True),
+    (17, 64, 32, False),     # one word per row, T = 32
+    (9, 200, 1, True),
+    (25, 2048, 4, False),    # widest prepared row
+])
+def test_poisson_pool_equals_encode(hses_gpu, pool_rows, d, T, time_inner):
+    # the prepared pool's gathered encode == the direct gathered encode, bit
+    # for bit, and == the oracle's spikes
+    rng = np.random.default_rng(pool_rows + d + T)
+    p = special_pool(rng, pool_rows, d)
+    pt = torch.from_numpy(p).cuda()
+    pool = hses_gpu.PoissonPool(pt)
+    idx = rng.integers(0, pool_rows, 3 * pool_rows).astype(np.int32)
+    idx[:3] = [0, 1, pool_rows - 1]
+    idx[5] = -1             # outside the pool: all-zero rows
+    idx[7] = pool_rows
+    it = torch.from_numpy(idx).cuda()
+    seeds = (11, 22, 33, 44)
+    got = hses_gpu.poisson_encode_pool(pool, T, seeds, rows_index=it, time_inner=time_inner)
+    ref = hses_gpu.poisson_encode(pt, T, seeds, FMT_BITS, rows_index=it, time_inner=time_inner)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
+    bits = unpack_bits(got.transpose(0, 1) if time_inner else got, d)
+    safe = np.where((idx >= 0) & (idx < pool_rows), idx, 0)
+    want = O.poisson(p[safe], T, seeds)
+    want[:, (idx < 0) | (idx >= pool_rows), :] = 0.0
+    np.testing.assert_array_equal(bits, want)
+    # without a row index: output row i encodes pool row i
+    got = hses_gpu.poisson_encode_pool(pool, T, seeds, time_inner=time_inner)
+    ref = hses_gpu.poisson_encode(pt, T, seeds, FMT_BITS, time_inner=time_inner)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
+
+
+def test_poisson_pool_c3_batch(hses_gpu):
+    # the C3 batch: 8192 members x 64 rows from a 60000 x 784 pool, both
+    # encodes over all 524288 rows
+    from hyperscalees_amd import snn
+    pool, _ = snn.synthetic_pool(60000, 784, 10, seed=3)
+    idx = snn.sample_index(0, 8192, 64, 60000)
+    pt = torch.from_numpy(pool).cuda()
+    it = torch.as_tensor(idx, dtype=torch.int32).cuda()
+    pp = hses_gpu.PoissonPool(pt)
+    got = hses_gpu.poisson_encode_pool(pp, 16, (1, 2, 3, 4), rows_index=it, time_inner=True)
+    ref = hses_gpu.poisson_encode(pt, 16, (1, 2, 3, 4), FMT_BITS, rows_index=it, time_inner=True)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
+    assert int(ref.ne(0).sum()) > 0
+
+
+def test_poisson_pool_rejects(hses_gpu):
+    pt = torch.rand(4, 3000, device="cuda")
+    with pytest.raises(ValueError, match="2048"):
+        hses_gpu.PoissonPool(pt)
+    pool = hses_gpu.PoissonPool(torch.rand(4, 100, device="cuda"))
+    from hyperscalees_amd import _lib
+    with pytest.raises(_lib.HsesError, match="power of two"):
+        hses_gpu.poisson_encode_pool(pool, 12)
