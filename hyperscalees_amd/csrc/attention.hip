@@ -86,24 +86,32 @@ __global__ __launch_bounds__(256) void k_sa_encode(const float* __restrict__ cq,
 
 // One head of multihead_attention_once for one member per workgroup
 // (snn_self_attention_heads.py:54-70 with row_softmax_lif): K, V (and Q) of
-// the member's R tokens staged in LDS; each wave takes query rows, lane j is
-// key neuron j: h_j = beta (q_i . k_j), normalised by max |h| + 1e-6, n_iter
-// LIF steps with the inhibition g_inh * (sum of counts), p_j = count_j /
-// (sum count + 1e-6), then out_i = p @ V with lane c < hd summing over j.
+// the member's R tokens staged in LDS (dynamic, sized for R and hd, so that
+// several workgroups share a CU); each wave takes groups of RP = min(4, 64 /
+// hd) query rows.  Per row lane j is key neuron j: h_j = beta (q_i . k_j),
+// normalised by max |h| + 1e-6, n_iter LIF steps with the inhibition g_inh *
+// (sum of counts), p_j = count_j / (sum count + 1e-6) into the wave's LDS
+// rows; then out_i = p @ V for the group's RP rows at once, lane rr * hd + c
+// summing row rr's channel c over j in index order.
 constexpr int kSaWaves = 4;
-constexpr int kSaMaxR = 64, kSaMaxHd = 64;
+constexpr int kSaMaxR = 64, kSaMaxHd = 64, kSaMaxRP = 4;
+constexpr int kSaPP = kSaMaxR + 1;  // pitch of a wave's p rows (rows on distinct banks)
+static size_t sa_lds_bytes(int32_t R, int32_t hd) {
+    return (3 * (size_t)R * (hd + 1) + (size_t)kSaWaves * kSaMaxRP * kSaPP) * sizeof(float);
+}
 __global__ __launch_bounds__(kSaWaves * 64) void k_sa_attention(
         const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
         int32_t ld, int32_t R, int32_t H, int32_t hd, const float* __restrict__ beta,
         const float* __restrict__ vth, float g_inh, float leak, int32_t n_iter,
         float* __restrict__ out) {
-    __shared__ float qs[kSaMaxR * (kSaMaxHd + 1)];
-    __shared__ float ks[kSaMaxR * (kSaMaxHd + 1)];
-    __shared__ float vs[kSaMaxR * (kSaMaxHd + 1)];
-    __shared__ float ps[kSaWaves][kSaMaxR];
+    extern __shared__ float sa_lds[];
+    const int pitch = hd + 1;
+    float* qs = sa_lds;
+    float* ks = qs + R * pitch;
+    float* vs = ks + R * pitch;
     const int32_t m = blockIdx.x / H, h = blockIdx.x % H;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int pitch = hd + 1;
+    float* ps = vs + R * pitch + w * (kSaMaxRP * kSaPP);
     const int64_t row0 = (int64_t)m * R;
     for (int i = threadIdx.x; i < R * hd; i += kSaWaves * 64) {
         const int r = i / hd, c = i % hd;
@@ -115,32 +123,38 @@ __global__ __launch_bounds__(kSaWaves * 64) void k_sa_attention(
     __syncthreads();
     const float b = beta[m], th = vth[m];
     const bool key = lane < R;
-    for (int i = w; i < R; i += kSaWaves) {
-        float hj = 0.0f;
-        if (key) {
-            float s = 0.0f;
-            for (int c = 0; c < hd; ++c) s = __fadd_rn(s, __fmul_rn(qs[i * pitch + c], ks[lane * pitch + c]));
-            hj = __fmul_rn(b, s);
+    const int RP = min(kSaMaxRP, 64 / hd);
+    const int rr = lane / hd, cc = lane - rr * hd;  // p @ V: row rr of the group, channel cc
+    for (int i0 = w * RP; i0 < R; i0 += kSaWaves * RP) {
+        const int nr = min(RP, R - i0);
+        for (int q = 0; q < nr; ++q) {
+            const int i = i0 + q;
+            float hj = 0.0f;
+            if (key) {
+                float s = 0.0f;
+                for (int c = 0; c < hd; ++c) s = __fadd_rn(s, __fmul_rn(qs[i * pitch + c], ks[lane * pitch + c]));
+                hj = __fmul_rn(b, s);
+            }
+            const float den = __fadd_rn(wmax(key ? fabsf(hj) : 0.0f), 1e-6f);
+            const float hn = __fdiv_rn(hj, den);
+            float u = 0.0f, cnt = 0.0f;
+            for (int it = 0; it < n_iter; ++it) {
+                const float G = wsum(key ? cnt : 0.0f);  // integer counts: exact in any order
+                const float inh = __fmul_rn(g_inh, G);
+                float sp;
+                u = lif_upd(u, __fsub_rn(hn, inh), leak, th, &sp);
+                cnt = __fadd_rn(cnt, sp);
+            }
+            const float tot = wsum(key ? cnt : 0.0f);
+            if (key) ps[q * kSaPP + lane] = __fdiv_rn(cnt, __fadd_rn(tot, 1e-6f));
         }
-        const float den = __fadd_rn(wmax(key ? fabsf(hj) : 0.0f), 1e-6f);
-        const float hn = __fdiv_rn(hj, den);
-        float u = 0.0f, cnt = 0.0f;
-        for (int it = 0; it < n_iter; ++it) {
-            const float G = wsum(key ? cnt : 0.0f);  // integer counts: exact in any order
-            const float inh = __fmul_rn(g_inh, G);
-            float s;
-            u = lif_upd(u, __fsub_rn(hn, inh), leak, th, &s);
-            cnt = __fadd_rn(cnt, s);
-        }
-        const float tot = wsum(key ? cnt : 0.0f);
-        if (key) ps[w][lane] = __fdiv_rn(cnt, __fadd_rn(tot, 1e-6f));
-        // the row's weights are read by other lanes of this wave only
+        // the group's weights are read by other lanes of this wave only
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
         __builtin_amdgcn_wave_barrier();
-        if (lane < hd) {
+        if (rr < nr) {
             float s = 0.0f;
-            for (int j = 0; j < R; ++j) s = __fadd_rn(s, __fmul_rn(ps[w][j], vs[j * pitch + lane]));
-            out[(row0 + i) * ld + (int64_t)h * hd + lane] = s;
+            for (int j = 0; j < R; ++j) s = __fadd_rn(s, __fmul_rn(ps[rr * kSaPP + j], vs[j * pitch + cc]));
+            out[(row0 + i0 + rr) * ld + (int64_t)h * hd + cc] = s;
         }
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -240,7 +254,7 @@ extern "C" int hses_sa_attention(const float* d_q, const float* d_k, const float
     HSES_REQUIRE(d_q && d_k && d_v && d_beta && d_vth && d_out, "NULL pointer");
     HSES_REQUIRE(d_out != d_q && d_out != d_k && d_out != d_v, "out must not alias q, k or v");
     HSES_REQUIRE(n * H < (1ll << 31), "grid too large");
-    hipLaunchKernelGGL(k_sa_attention, dim3((uint32_t)(n * H)), dim3(kSaWaves * 64), 0,
+    hipLaunchKernelGGL(k_sa_attention, dim3((uint32_t)(n * H)), dim3(kSaWaves * 64), sa_lds_bytes(R, hd),
                        (hipStream_t)stream, d_q, d_k, d_v, ld, R, H, hd, d_beta, d_vth, g_inh,
                        1.0f / tau_m, n_iter, d_out);
     HSES_CHECK_HIP(hipGetLastError());
