@@ -17,16 +17,36 @@ namespace hses {
 
 namespace {
 
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+
+// Reduction over the 64 lanes of a wave, the result in every lane: within
+// rows of 16 lanes by DPP (quad swaps, then the half-row and row mirrors),
+// across rows by the permlane16 and permlane32 swaps (no LDS round trips).
+// Callers reduce values whose result does not depend on the order (integer
+// counts, maxima).
+template <class Op>
+__device__ __forceinline__ float wave_reduce(float v, Op op) {
+    v = op(v, dpp_mov<0xB1>(v));   // quad_perm 1,0,3,2
+    v = op(v, dpp_mov<0x4E>(v));   // quad_perm 2,3,0,1
+    v = op(v, dpp_mov<0x141>(v));  // row_half_mirror
+    v = op(v, dpp_mov<0x140>(v));  // row_mirror
+    const uint32_t u = __float_as_uint(v);
+    const auto p16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    v = op(__uint_as_float(p16[0]), __uint_as_float(p16[1]));
+    const uint32_t w = __float_as_uint(v);
+    const auto p32 = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+    return op(__uint_as_float(p32[0]), __uint_as_float(p32[1]));
+}
+
 __device__ __forceinline__ float wsum(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-    return v;
+    return wave_reduce(v, [](float x, float y) { return x + y; });
 }
 
 __device__ __forceinline__ float wmax(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
-    return v;
+    return wave_reduce(v, [](float x, float y) { return fmaxf(x, y); });
 }
 
 // snn_attention.py:41-49 (dt = 1): v + leak * (-v + cur); spike = v >= vth;
@@ -127,26 +147,44 @@ __global__ __launch_bounds__(kSaWaves * 64) void k_sa_attention(
     const int rr = lane / hd, cc = lane - rr * hd;  // p @ V: row rr of the group, channel cc
     for (int i0 = w * RP; i0 < R; i0 += kSaWaves * RP) {
         const int nr = min(RP, R - i0);
-        for (int q = 0; q < nr; ++q) {
-            const int i = i0 + q;
-            float hj = 0.0f;
+        // the group's rows side by side (rows past R repeat row R - 1 and are
+        // not stored): their wave reductions are independent chains
+        float hn[kSaMaxRP], u[kSaMaxRP], cnt[kSaMaxRP];
+        {
+            float sd[kSaMaxRP];
+#pragma unroll
+            for (int q = 0; q < kSaMaxRP; ++q) sd[q] = 0.0f;
             if (key) {
-                float s = 0.0f;
-                for (int c = 0; c < hd; ++c) s = __fadd_rn(s, __fmul_rn(qs[i * pitch + c], ks[lane * pitch + c]));
-                hj = __fmul_rn(b, s);
+                for (int c = 0; c < hd; ++c) {
+                    const float kv = ks[lane * pitch + c];
+#pragma unroll
+                    for (int q = 0; q < kSaMaxRP; ++q)
+                        sd[q] = __fadd_rn(sd[q], __fmul_rn(qs[min(i0 + q, R - 1) * pitch + c], kv));
+                }
             }
-            const float den = __fadd_rn(wmax(key ? fabsf(hj) : 0.0f), 1e-6f);
-            const float hn = __fdiv_rn(hj, den);
-            float u = 0.0f, cnt = 0.0f;
-            for (int it = 0; it < n_iter; ++it) {
-                const float G = wsum(key ? cnt : 0.0f);  // integer counts: exact in any order
+#pragma unroll
+            for (int q = 0; q < kSaMaxRP; ++q) {
+                const float hj = key ? __fmul_rn(b, sd[q]) : 0.0f;
+                const float den = __fadd_rn(wmax(key ? fabsf(hj) : 0.0f), 1e-6f);
+                hn[q] = __fdiv_rn(hj, den);
+                u[q] = 0.0f;
+                cnt[q] = 0.0f;
+            }
+        }
+        for (int it = 0; it < n_iter; ++it) {
+#pragma unroll
+            for (int q = 0; q < kSaMaxRP; ++q) {
+                const float G = wsum(key ? cnt[q] : 0.0f);  // integer counts: exact in any order
                 const float inh = __fmul_rn(g_inh, G);
                 float sp;
-                u = lif_upd(u, __fsub_rn(hn, inh), leak, th, &sp);
-                cnt = __fadd_rn(cnt, sp);
+                u[q] = lif_upd(u[q], __fsub_rn(hn[q], inh), leak, th, &sp);
+                cnt[q] = __fadd_rn(cnt[q], sp);
             }
-            const float tot = wsum(key ? cnt : 0.0f);
-            if (key) ps[q * kSaPP + lane] = __fdiv_rn(cnt, __fadd_rn(tot, 1e-6f));
+        }
+#pragma unroll
+        for (int q = 0; q < kSaMaxRP; ++q) {
+            const float tot = wsum(key ? cnt[q] : 0.0f);
+            if (key && q < nr) ps[q * kSaPP + lane] = __fdiv_rn(cnt[q], __fadd_rn(tot, 1e-6f));
         }
         // the group's weights are read by other lanes of this wave only
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
