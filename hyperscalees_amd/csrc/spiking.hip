@@ -369,13 +369,15 @@ __global__ __launch_bounds__(256) void k_poisson_pool_prepare(const float* __res
 }
 
 // Bit-packed Poisson of rows gathered from a prepared pool: one wave per
-// output row.  The row's pattern slots in LDS start at zero; the saturated
+// output row and workgroup (3.3 KB of LDS at in_dim 784; no workgroup
+// barrier, so a wave starts its next row as soon as it is done).  The row's
+// pattern slots in LDS start at zero; the saturated
 // columns get the all-ones pattern; each active element runs its xorshift32
 // stream (the same stream, seed and compare as k_poisson_sparse's phase B)
 // with the next element's column and threshold already loaded; then the
 // 64 x 64 bit transposes of k_poisson_sparse's phase C store the words.
 template <int T>
-__global__ __launch_bounds__(256) void k_poisson_pool(const unsigned char* __restrict__ pool,
+__global__ __launch_bounds__(64) void k_poisson_pool(const unsigned char* __restrict__ pool,
                                                       int64_t pool_rows,
                                                       const int32_t* __restrict__ prow,
                                                       int64_t rows, int32_t in_dim, uint32_t mix,
@@ -386,10 +388,10 @@ __global__ __launch_bounds__(256) void k_poisson_pool(const unsigned char* __res
     constexpr uint32_t ALL = T == 32 ? 0xffffffffu : ((1u << T) - 1u);
     extern __shared__ __align__(16) unsigned char psm[];
     const PoolLayout lay(pool_rows, in_dim);
-    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int lane = threadIdx.x;
     const int32_t words = (in_dim + 63) >> 6;
-    uint32_t* pat = reinterpret_cast<uint32_t*>(psm) + (size_t)wv * (words * 64);
-    const int64_t row = (int64_t)blockIdx.x * 4 + wv;
+    uint32_t* pat = reinterpret_cast<uint32_t*>(psm);
+    const int64_t row = (int64_t)blockIdx.x;
     if (row >= rows) return;  // whole wave exits together
     const int64_t src = prow ? (int64_t)prow[row] : row;
     const bool src_ok = src >= 0 && src < pool_rows;
@@ -776,15 +778,15 @@ extern "C" int hses_poisson_encode_pool(const void* d_pool, size_t pool_bytes, i
     HSES_REQUIRE(rows_layout_ok(fmt_row_units(HSES_FMT_BITS, in_dim), rows, T, out_stride, out_plane),
                  "output rows overlap (out_stride too small, or time planes overlap)");
     HSES_REQUIRE(rows * in_dim <= (int64_t)UINT32_MAX, "rows*in_dim exceeds the u32 index range");
-    const int64_t blocks = (rows + 3) / 4;
-    HSES_REQUIRE(blocks < (1ll << 31), "grid too large");
+    HSES_REQUIRE(rows < (1ll << 31), "grid too large");
+    const int64_t blocks = rows;
     const uint32_t mix = s0 ^ s1 ^ s2 ^ s3;
-    const size_t lds = (size_t)4 * ((in_dim + 63) / 64) * 64 * 4;  // 4 waves, a u32 pattern per slot
+    const size_t lds = (size_t)((in_dim + 63) / 64) * 64 * 4;  // a u32 pattern per slot
     const unsigned char* pl = static_cast<const unsigned char*>(d_pool);
     hipStream_t s = (hipStream_t)stream;
 #define HSES_PPOOL(TV)                                                                          \
     case TV:                                                                                    \
-        hipLaunchKernelGGL(k_poisson_pool<TV>, dim3((uint32_t)blocks), dim3(256), lds, s, pl,     \
+        hipLaunchKernelGGL(k_poisson_pool<TV>, dim3((uint32_t)blocks), dim3(64), lds, s, pl,      \
                            pool_rows, d_rows, rows, in_dim, mix, d_out, out_stride, out_plane); \
         break;
     switch (T) {
