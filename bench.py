@@ -527,6 +527,10 @@ def main():
     ap.add_argument("--math", choices=("bf16", "f32x"), default="f32x",
                     help="C3 forward arithmetic: fp32-accurate split fp16 operands (the "
                          "reference's fp32 results), or the faster bf16 MFMA")
+    ap.add_argument("--noise-cache", action="store_true",
+                    help="C3: keep the factor records across steps (the reference's "
+                         "LoraNoiseCache for noise_reuse = 0) instead of redrawing them every "
+                         "step as its training binary does; not the default measurement")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one GPU "
@@ -548,7 +552,7 @@ def main():
     idx = snn.sample_index(0, cfg.n, cfg.rows, pool_size)
     W = snn.init_weights(cfg.dims, 0, gain=snn.ACTIVE_GAIN)
     K.init(0)
-    es = snn.SnnEs(cfg, W, pool, labels, idx)
+    es = snn.SnnEs(cfg, W, pool, labels, idx, noise_cache=args.noise_cache)
     L = len(cfg.dims) - 1
 
     for i in range(args.warmup):
@@ -713,6 +717,9 @@ def main():
                          "full ES step (forward + fitness + z-score + ES update + AdamW)"),
             "population": cfg.n, "rank": cfg.rank, "T": cfg.T, "samples_per_member": cfg.rows,
             "parallelism": "single GPU",
+            **({"noise_cache": ("factor records kept across steps (LoraNoiseCache, "
+                                "noise_reuse = 0): the timed steps draw no factors")}
+               if args.noise_cache else {}),
         },
         "fwd_member_evals_per_s": round(cfg.n / (t_fwd * 1e-3), 1),
         "es_update_GBps": round(update_bytes(cfg) / (t_upd * 1e-3) / 1e9, 2),

@@ -118,7 +118,8 @@ class SnnEs:
     """Device-resident SNN-MLP population evaluation and ES update."""
 
     def __init__(self, cfg, weights, pool, pool_labels, index, device="cuda", fused=None,
-                 record=None, ahead=None, member_weights=None, overlap=None, prepared_pool=None):
+                 record=None, ahead=None, member_weights=None, overlap=None, prepared_pool=None,
+                 noise_cache=False):
         self.cfg = cfg
         c = cfg
         self.dev = device
@@ -210,7 +211,18 @@ class SnnEs:
         # the first layer's GEMM is issued, so that they share the CUs with
         # that matrix-core-bound kernel (one draw wave per SIMD fits beside
         # it); each layer's forward waits for its draw.
-        can_overlap = self.ahead and str(device).startswith("cuda")
+        # The noise cache (LoraNoiseCache, eggroll.rs:229-309; the hot path of
+        # accumulated_update_cached, eggroll.rs:627): with noise_reuse = 0 a
+        # member's factors depend on the layer key and its thread id only
+        # (true_epoch is 0, eggroll.rs:60-65), so the records drawn for the
+        # population stay valid across epochs and later steps skip the draws.
+        # Off by default: the reference's training binary regenerates the
+        # noise every step (accumulated_update passes no cache).
+        self.noise_cache = bool(noise_cache)
+        if self.noise_cache and not (self.ahead and c.noise_reuse == 0 and c.accumulate == 1):
+            raise ValueError("the noise cache needs factors drawn ahead, noise_reuse = 0 and "
+                             "accumulate = 1 (one record per layer for the whole population)")
+        can_overlap = self.ahead and str(device).startswith("cuda") and not self.noise_cache
         self.overlap = can_overlap if overlap is None else (bool(overlap) and can_overlap)
         self.side = torch.cuda.Stream(device=device) if self.overlap else None
         self._drawn = {}  # layer -> (epoch, lo, event) of a draw issued on the side stream
@@ -312,14 +324,14 @@ class SnnEs:
                                           spikes=None if last else self.spk[l + 1],
                                           rate=self.rate if last and not self.split else None,
                                           counts=counts, time_inner=self.time_inner)
-                self._rec_at[l] = (epoch, lo)
+                self._rec_at[l] = self._rec_key(epoch, lo)
                 return
             if last and self.split:
                 K.perturbed_linear_lif_counts_x(self.spk[l], self.W[l], c.rank, c.sigma, lo,
                                                 c.chunk, c.rows, c.T, c.tau_m, c.v_th,
                                                 self.rec[l], img, counts=self.cpl,
                                                 time_inner=self.time_inner)
-                self._rec_at[l] = (epoch, lo)
+                self._rec_at[l] = self._rec_key(epoch, lo)
                 return
             K.perturbed_linear_lif(self.spk[l], self.W[l], c.keys[l], c.rank, c.sigma, epoch,
                                    c.noise_reuse, lo, c.chunk, c.rows, c.T, c.tau_m, c.v_th,
@@ -329,7 +341,7 @@ class SnnEs:
                                    rec=self.rec[l] if self.rec else None, img=img,
                                    time_inner=self.time_inner, math=c.math)
             if self.rec:
-                self._rec_at[l] = (epoch, lo)
+                self._rec_at[l] = self._rec_key(epoch, lo)
             return
         cur = self.cur[:, :, :a] if a == self.cur.shape[2] else \
             self.cur.view(-1)[: c.T * self.M * a].view(c.T, self.M, a)
@@ -353,7 +365,7 @@ class SnnEs:
                                    img=img)
                 torch.sum(self.ylog.view(self.M, self.npl, -1) * self.plane_w, 1,
                           out=self.logits)
-            self._rec_at[-1] = (epoch, lo)
+            self._rec_at[-1] = self._rec_key(epoch, lo)
             labels = self.labels[lo * c.rows:(lo + c.chunk) * c.rows]
             return K.member_fitness(self.logits, labels, c.chunk, c.rows, c.reward,
                                     out=self.raw[lo:lo + c.chunk], correct=self.correct)
@@ -365,7 +377,7 @@ class SnnEs:
                            math=c.math, out=self.logits.view(1, self.M, -1),
                            rec=self.rec[-1] if self.rec else None, img=img)
         if self.rec:
-            self._rec_at[-1] = (epoch, lo)
+            self._rec_at[-1] = self._rec_key(epoch, lo)
         labels = self.labels[lo * c.rows:(lo + c.chunk) * c.rows]
         return K.member_fitness(self.logits, labels, c.chunk, c.rows, c.reward,
                                 out=self.raw[lo:lo + c.chunk], correct=self.correct)
@@ -401,16 +413,24 @@ class SnnEs:
                 done.record(self.side)
                 self._drawn[l] = (epoch, lo, done)
 
+    def _rec_key(self, epoch, lo):
+        """What a record holds: the (epoch, lo) of its draw, or with the noise
+        cache (lo) alone (the factors do not depend on the epoch)."""
+        return (0 if self.noise_cache else epoch, lo)
+
     def _draw(self, l, epoch, lo):
         """Layer l's operand of the chunk: with member weights every member's
         W_m formed from the record, else the operand image; None when the
         forward draws its factors itself.  The draw itself was issued on the
-        side stream (waited for here) or runs now."""
+        side stream (waited for here) or runs now; with the noise cache a
+        record that already holds the chunk is not drawn again."""
         img = self.img_x if self.split else self.img
         if not img:
             return None
         drawn = self._drawn.pop(l, None)
-        if drawn is not None and drawn[:2] == (epoch, lo):
+        if self.noise_cache and self._rec_at[l] == self._rec_key(epoch, lo):
+            pass  # the record (and operand image) of an earlier step still hold these factors
+        elif drawn is not None and drawn[:2] == (epoch, lo):
             torch.cuda.current_stream().wait_event(drawn[2])
         else:
             self._draw_factors(l, epoch, lo)
@@ -467,7 +487,8 @@ class SnnEs:
         from the factor records when they hold this epoch's chunk."""
         c = self.cfg
         a, b = self.W[l].shape
-        if self.rec is not None and self._rec_at[l] == (epoch, lo) and fit.numel() == c.chunk:
+        if (self.rec is not None and self._rec_at[l] == self._rec_key(epoch, lo)
+                and fit.numel() == c.chunk):
             K.es_update_rec(fit, lo, self.rec[l], c.rank, c.sigma, a, b, scale,
                             out=self.grads[l], accumulate=accumulate)
         else:

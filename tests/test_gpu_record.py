@@ -12,7 +12,7 @@ import torch
 
 from hyperscalees_amd import kernels as K
 from hyperscalees_amd import snn
-from hyperscalees_amd._lib import ADAMW, FMT_F32, MATH_BF16, SGD
+from hyperscalees_amd._lib import ADAMW, FMT_F32, MATH_BF16, MATH_F32X, SGD
 from tests import oracle_lib as O
 from tests.test_gpu_linear import pack_bits
 
@@ -145,3 +145,34 @@ def test_update_without_matching_forward_draws_the_normals(hses_gpu):
     torch.cuda.synchronize()
     for l in range(es_r.L):
         assert torch.equal(es_r.grads[l], es_g.grads[l])
+
+
+@pytest.mark.parametrize("math", [MATH_F32X, MATH_BF16])
+def test_noise_cache_steps_equal_redrawn(hses_gpu, math):
+    # noise_reuse = 0: the factors depend on the layer key and thread id only
+    # (eggroll.rs:60-65), so keeping the records across epochs (the reference's
+    # LoraNoiseCache, eggroll.rs:229-309, 627) gives the steps that redraw them
+    cfg = dict(C3_SMALL, math=math)
+    pool, labels = snn.synthetic_pool(3000, 784, 10, 0)
+    idx = snn.sample_index(0, cfg["n"], cfg["rows"], 3000)
+    W = snn.init_weights(snn.SnnConfig(**cfg).dims, 0, gain=snn.ACTIVE_GAIN)
+    es_d = snn.SnnEs(snn.SnnConfig(**cfg), W, pool, labels, idx)
+    es_c = snn.SnnEs(snn.SnnConfig(**cfg), W, pool, labels, idx, noise_cache=True)
+    assert es_c.noise_cache and es_c.mw and not es_c.overlap
+    for epoch in range(3):
+        f_d = es_d.step(epoch).clone()
+        f_c = es_c.step(epoch).clone()
+        torch.cuda.synchronize()
+        assert torch.equal(f_d, f_c), f"epoch {epoch}"
+        for l in range(es_d.L):
+            assert torch.equal(es_d.grads[l], es_c.grads[l]), f"layer {l} gradient, epoch {epoch}"
+            assert torch.equal(es_d.W[l], es_c.W[l])
+
+
+def test_noise_cache_rejects_epoch_dependent_noise(hses_gpu):
+    cfg = snn.SnnConfig(**dict(C3_SMALL, noise_reuse=2))
+    pool, labels = snn.synthetic_pool(100, 784, 10, 0)
+    idx = snn.sample_index(0, cfg.n, cfg.rows, 100)
+    W = snn.init_weights(cfg.dims, 0)
+    with pytest.raises(ValueError, match="noise_reuse = 0"):
+        snn.SnnEs(cfg, W, pool, labels, idx, noise_cache=True)
