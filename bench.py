@@ -668,11 +668,13 @@ def main():
     # algorithmic FLOPs of the kernel: x W_m^T on member weights, else the
     # factored product (layer_flops)
     fc1_flops = 2 * M1 * b1 * a1 if es.mw else layer_flops(cfg, 0)
-    # matrix-core FLOPs it issues: K padded to whole 64-k tiles, twice for the
+    # matrix-core FLOPs it issues: K padded to whole 64-k tiles (on member
+    # weights with split operands, 32-k tiles: 800 at b = 784), twice for the
     # split operands (and the factored form's 256 staged columns and rank
     # product)
     if es.mw:
-        mfma_flops = 2 * M1 * kp1 * a1 * (2 if es.split else 1)
+        kmw = (b1 + 31) // 32 * 32 if es.split else kp1
+        mfma_flops = 2 * M1 * kmw * a1 * (2 if es.split else 1)
     else:
         mfma_flops = (2 * M1 * kp1 * (a1 + cfg.rank) * (2 if es.split else 1)
                       + 2 * M1 * cfg.rank * a1 * (3 if es.split else 1))

@@ -303,7 +303,10 @@ __global__ __launch_bounds__(MB_THREADS, 2) void k_mw_bits(const K2Args P) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lc = lane & 31, hl = lane >> 5;
     const int32_t a = P.a, nkt = lay.words, kp = nkt * 64, R = P.R;
-    const int32_t ntb = X ? 2 * nkt : nkt;  // stream tiles per block
+    // stream tiles per block; with X a tile is 32 inputs, and a last 64-input
+    // chunk with 32 or fewer real inputs streams its first half only (C3's
+    // fc1: 25 tiles for 784 inputs, not 26); at least two (the stream primes two)
+    const int32_t ntb = X ? max(2, (P.b + 31) / 32) : nkt;
     const int32_t wrow0 = 64 * wave;
     // MFMA position p of a row tile -> its row: 8g + 4h + v -> 16h + 4g + v
     const int xrow = 16 * ((lc >> 2) & 1) + 4 * (lc >> 3) + (lc & 3);
@@ -747,7 +750,7 @@ int launch_linear_mw(LinParams& P, DeviceState* st, hipStream_t s, const LifOut*
     if (!xm && P.b <= 64) return HSES_ERR_UNSUPPORTED;
     if (lif && (P.n_time > 16 || (P.n_time & (P.n_time - 1)) != 0)) return HSES_ERR_UNSUPPORTED;
     // three tile buffers when a block streams at least three tiles
-    const int32_t ntb = (xm ? 2 : 1) * ((P.b + 63) / 64);
+    const int32_t ntb = xm ? std::max(2, (P.b + 31) / 32) : (P.b + 63) / 64;  // as k_mw_bits counts them
     const int nbuf = ntb >= 3 ? 3 : 2;
     const MbLayout lay(P.b, nbuf);
     if (lay.bytes > st->max_lds) return HSES_ERR_UNSUPPORTED;

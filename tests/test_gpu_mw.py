@@ -107,6 +107,8 @@ MW_CASES = [
     (128, 128, 64, 5, 3, 64, 4),       # odd start and count
     (10, 128, 128, 6, 1, 32, 8),       # narrow output (one output tile)
     (128, 784, 128, 128, 0, 32, 16),   # pairs split over 4 workgroups (512 rows each)
+    (64, 800, 32, 4, 0, 64, 4),        # last chunk 32 inputs: its first half streams alone
+    (64, 801, 32, 4, 0, 64, 4),        # last chunk 33 inputs: both halves
 ]
 
 
@@ -142,6 +144,7 @@ LIF_CASES = [
     (128, 784, 128, 6, 0, 16, 16, True, MATH_BF16),
     (128, 128, 64, 5, 3, 64, 4, False, MATH_F32X),
     (128, 784, 128, 128, 0, 32, 16, True, MATH_F32X),  # split over 4 workgroups
+    (32, 20, 32, 4, 0, 64, 4, True, MATH_F32X),        # one chunk of 20 inputs: two tiles
 ]
 
 
