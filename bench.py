@@ -36,10 +36,10 @@ PEAK_HBM_GBPS = 8000.0
 # weights).  Measured on the k_mw_bits source of commit 821b0d8; refreshed whenever the kernel
 # changes, and the bench line names the source it was measured on.
 FC1_TRAFFIC = {
-    ("f32x", True): (4.522e9, "rocprofv3 PMC of profile_fc1, k_mw_bits of commit 821b0d8: "
-                              "4.388e9 B read + 0.134e9 B written"),
-    ("bf16", True): (2.769e9, "rocprofv3 PMC of profile_fc1 --math bf16, k_mw_bits of commit "
-                              "821b0d8: 2.635e9 B read + 0.134e9 B written"),
+    ("f32x", True): (4.534e9, "rocprofv3 PMC of profile_fc1, k_mw_bits of commit 9357756: "
+                              "4.400e9 B read + 0.134e9 B written"),
+    ("bf16", True): (2.771e9, "rocprofv3 PMC of profile_fc1 --math bf16, k_mw_bits of commit "
+                              "9357756: 2.636e9 B read + 0.134e9 B written"),
 }
 
 
