@@ -4,6 +4,9 @@
     bit-packed spikes, and -> fp32 spikes;
   * Poisson encode (hses_poisson_encode): p (M=524288, 784) fp32 with 70% exact
     zeros -> bit-packed spikes (T=16), and -> fp32 spikes for T=4;
+  * the C3 step's encode (hses_poisson_encode_pool): the batch of 8192 members x
+    64 rows gathered from a prepared 60000 x 784 pool -> bit-packed spikes (T=16,
+    each row's 16 words adjacent);
   * torch's device copy of the LIF input (a reference point for the bandwidth
     a plain read + write stream reaches);
   * the exact normal generator (hses_lora_factors) over every pair's factors
@@ -83,6 +86,26 @@ def main():
     report("poisson_encode -> f32", ms, M * d * 4 + T4 * M * d * 4, shape=[T4, M, d],
            zero_frac=0.7)
     del p, bits, f32
+
+    import numpy as np
+    from . import snn
+    pool, _ = snn.synthetic_pool(60000, d, 10, seed=0)
+    idx = snn.sample_index(0, 8192, 64, 60000)
+    pp = K.PoissonPool(torch.from_numpy(pool).cuda())
+    it = torch.as_tensor(idx, dtype=torch.int32).cuda()
+    words = K.fmt_width(K.FMT_BITS, d)
+    ti = torch.empty((M, T, words), dtype=torch.int64, device="cuda")
+    ms = timed(lambda: K.poisson_encode_pool(pp, T, (1, 2, 3, 4), out=ti, rows_index=it,
+                                             time_inner=True), args.reps)
+    # bytes each gathered row reads: its counts, a u32 threshold and u16 column
+    # per active element, a u16 column per saturated one; plus the row index
+    act = ((pool > 0) & (pool < 1)).sum(axis=1)
+    sat = (pool >= 1).sum(axis=1)
+    per_row = 8 + 6 * act + 2 * sat
+    report("poisson_encode_pool -> bits (prepared pool, gathered rows)", ms,
+           int(per_row[idx].sum()) + 4 * M + T * M * words * 8, shape=[M, T, d],
+           pool_rows=60000, active_per_row=round(float(act[idx].mean()), 1))
+    del pp, ti
 
     pairs, a, b, r = 4096, 128, 784, 128
     ms = timed(lambda: K.lora_factors(0.01, 12345, r, 0, 0, (0, pairs), a, b), args.reps)
