@@ -123,3 +123,34 @@ def test_es_update_split_sweep_rank128(hses_gpu, a, b, n):
     assert_close(gr, ref)
     # the two forms run the same contraction on the same factors
     assert np.array_equal(g, gr)
+
+
+# The reference's own sweep of its fused ES contraction against an f64 CPU
+# value (einsum_pair_fused_oxide.rs:758-795): (pairs, rank, a, b), the
+# contraction length K = pairs x rank bisected over 1..64 chunks of 32, large K
+# against small outputs and the reverse, the a thresholds of its small-M path,
+# one K slice over many N blocks and the reverse, the fc3 (a = 10) and fc1
+# (b = 784) shapes, and the noise-bench shape.  (Its pitched variants have no
+# counterpart: the gradient here is a dense (a, b) array.)  Ranks that are a
+# multiple of 16 in [32, 128] also run the record form.
+REF_SWEEP = [(8, 3, 2, 3), (2, 16, 8, 8), (2, 32, 8, 8), (4, 32, 8, 8), (8, 64, 8, 8),
+             (16, 64, 8, 8), (32, 64, 8, 8), (50, 64, 8, 128), (50, 64, 64, 8), (2, 64, 12, 8),
+             (2, 64, 16, 8), (2, 64, 24, 8), (2, 64, 32, 8), (50, 64, 64, 128),
+             (100, 64, 64, 48), (100, 64, 64, 128), (64, 64, 10, 128), (200, 64, 128, 784),
+             (1000, 16, 32, 48), (2, 64, 32, 48)]
+
+
+@pytest.mark.parametrize("pairs,r,a,b", REF_SWEEP)
+def test_es_update_reference_sweep(hses_gpu, pairs, r, a, b):
+    n, sigma = 2 * pairs, 0.02
+    fit = np.random.default_rng(pairs * 7 + r + a + b).standard_normal(n).astype(np.float32)
+    ref = O.lora_grad_f64(sigma, KEY, r, 0, fit, a, b, nthreads=8).astype(np.float64)
+    scale = np.float32(-math.sqrt(n) / n)
+    g = gpu_grad(hses_gpu, sigma, r, fit, a, b, scale).cpu().numpy()
+    assert_close(g, ref)
+    if r % 16 == 0 and 32 <= r <= 128:
+        rec = hses_gpu.factor_record(a, b, r, 0, n)
+        hses_gpu.pair_factors(KEY, r, sigma, 0, 0, 0, n, a, b, rec, None)
+        gr = hses_gpu.es_update_rec(torch.from_numpy(fit).cuda(), 0, rec, r, sigma, a, b,
+                                    scale).cpu().numpy()
+        assert np.array_equal(g, gr)
