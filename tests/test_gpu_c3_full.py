@@ -79,6 +79,7 @@ def c3_run(hses_gpu):
     assert es.fused, "the full-size C3 step runs the fused forward + LIF kernel"
     assert es.record and es.ahead, "the full-size C3 step draws factors ahead into the record"
     assert es.mw, "the full-size C3 step runs on member weights"
+    assert es.ppool is not None, "the full-size C3 step encodes from the prepared pool"
     fit = es.forward(0)
     torch.cuda.synchronize()
     R = cfg.rows

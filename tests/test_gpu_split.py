@@ -253,6 +253,7 @@ def c3x_run(hses_gpu):
     W = snn.init_weights(cfg.dims, 0, gain=snn.ACTIVE_GAIN)
     es = snn.SnnEs(cfg, W, pool, labels, idx)
     assert es.fused and es.ahead and es.split
+    assert es.mw and es.ro_counts and es.ppool is not None, "the benched C3 path"
     fit = es.forward(0)
     torch.cuda.synchronize()
     R = cfg.rows
