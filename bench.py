@@ -534,7 +534,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one GPU "
-              "(the population shards by member across GPUs; see DESIGN.md)", file=sys.stderr)
+              "(across GPUs the population would shard by member, one slice of members per GPU)", file=sys.stderr)
         sys.exit(2)
     if args.workload in ("c1", "c2", "c4", "c5"):
         {"c1": bench_c1, "c2": bench_c2, "c4": bench_c4, "c5": bench_c5}[args.workload](args)
